@@ -1,0 +1,115 @@
+/*
+ * swarp_hip.h -- C ABI of libswarp_hip.so, the MI355X (gfx950) physics step of swarp.
+ *
+ * Every pointer is a caller-owned device pointer (HIP device memory) unless stated;
+ * nothing here allocates device memory.  All launches go to `stream` (a hipStream_t,
+ * NULL = the legacy default stream) and return without synchronising.  Functions
+ * return 0 on success and a negative code on a rejected argument; the message is in
+ * swarp_last_error() (thread-local).  No function keeps global mutable state.
+ *
+ * Layouts (row-major, contiguous, scalar type given by desc->dtype):
+ *   pos [E,A,2], theta [E,A], vel [E,A,2], speed [E,A], ang_vel [E,A],
+ *   z [E,A], vz [E,A], attitude [E,A,4] (x,y,z,w), body_rates [E,A,3]
+ *   -- the nine fields of the reference's TorchState (swarp/interop/autograd.py:29-45).
+ *   actions [T,E,A,act_dim]; params [A,22] in PARAM_FIELDS column order
+ *   (swarp/dynamics/base.py:114-145); model_tag / ctrl_mode [A] int32.
+ */
+#ifndef SWARP_HIP_H
+#define SWARP_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SWARP_ABI_VERSION 1
+
+#define SWARP_F32 0
+#define SWARP_F64 1
+
+/* Everything the step needs besides the state and the actions.
+ * Counterpart of the Stepper's configuration (swarp/core/stepper.py:87-137) plus
+ * WorldConfig's contact constants (swarp/core/config.py:181-322) and the obstacle
+ * arrays Stepper.set_obstacles installs (swarp/core/stepper.py:295-432). */
+typedef struct swarp_desc {
+    int32_t abi_version;     /* must equal SWARP_ABI_VERSION */
+    int32_t dtype;           /* SWARP_F32 or SWARP_F64 */
+    int32_t n_envs, n_agents, act_dim, substeps;
+    int32_t max_neighbors;   /* padded list width K (swarp/core/config.py max_neighbors) */
+    int32_t n_obstacles;
+    int32_t collisions;      /* agent-agent contacts on */
+    int32_t soft_walls;      /* bounds_mode == "soft" with bounds set */
+    int32_t clamp_bounds;    /* bounds_mode == "clamp" with bounds set (disc clamp) */
+    int32_t has_drone;       /* fleet holds a DRONE: all nine fields are stepped */
+    double dt;               /* env step; sub_dt = dt / substeps */
+    double k, c, margin, max_overlap;
+    double neighbor_radius;
+    double bounds_min[2], bounds_max[2];
+    const void *params;
+    const int32_t *model_tag, *ctrl_mode;
+    /* obstacles (NULL when n_obstacles == 0): pos [E,N,2], radius [N], angle [E,N],
+       half_extents [N,2], vel [E,N,2], ang_vel [E,N], type [N] int32 */
+    const void *obs_pos, *obs_radius, *obs_angle, *obs_half, *obs_vel, *obs_ang_vel;
+    const int32_t *obs_type;
+} swarp_desc_t;
+
+/* The nine state fields.  A NULL field means "not provided": an input adjoint that
+ * is NULL reads as zero, an output adjoint that is NULL is not written.  For a fleet
+ * without drones (desc->has_drone == 0) the last four fields are never touched. */
+typedef struct swarp_state {
+    void *pos, *theta, *vel, *speed, *ang_vel, *z, *vz, *attitude, *body_rates;
+} swarp_state_t;
+
+/* Library / ABI version (SWARP_ABI_VERSION). */
+int swarp_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *swarp_last_error(void);
+
+/* T-step forward rollout in one launch.
+ * Replaces T calls of Stepper.launch_substeps under _WarpStepFn.forward
+ * (swarp/interop/autograd.py:229-275, swarp/core/stepper.py:784-1011): each step runs
+ * `substeps` substeps of neighbour search (swarp/core/neighbors.py:76-97), contact
+ * forces (swarp/core/collisions.py:818-881) and integration
+ * (swarp/dynamics/kernels.py:812-971).
+ * `traj` receives the outputs of steps 0..T-2, each field strided by one state
+ * (field [T-1, E, A, ...]); it may be NULL when T == 1.  `final` receives the output
+ * of step T-1.  Inputs are never written. */
+int swarp_rollout_fwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                      const void *actions, const swarp_state_t *traj,
+                      const swarp_state_t *final_state, void *stream);
+
+/* Reverse of swarp_rollout_fwd in one launch (the adjoints the reference gets from
+ * wp.Tape.backward, swarp/interop/autograd.py:277-296).  Step inputs are recomputed
+ * from state0 and the checkpoints `traj` (the forward's own outputs); substep
+ * intermediates are recomputed in the kernel, never stored.  `adj_traj` (same
+ * layout as traj, fields may be NULL) and `adj_final` are the adjoints arriving at
+ * each step output.  Writes adj_state0 (fields may be NULL) and adj_actions
+ * [T,E,A,act_dim] (every element written). */
+int swarp_rollout_bwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                      const void *actions, const swarp_state_t *traj,
+                      const swarp_state_t *adj_traj, const swarp_state_t *adj_final,
+                      const swarp_state_t *adj_state0, void *adj_actions, void *stream);
+
+/* Padded radius-neighbour lists of one state: replaces NeighborGrid.query_into's
+ * brute-force kernel (swarp/core/neighbors.py:76-97, 465-492).  pos [E,A,2] of
+ * desc->dtype; idx [E,A,K] int32 (entries past cnt are zero-filled), cnt [E,A] int32,
+ * true_cnt [E,A] int32 (uncapped; NULL = not written).  Radius = desc->neighbor_radius,
+ * K = desc->max_neighbors. */
+int swarp_neighbors(const swarp_desc_t *desc, const void *pos, int32_t *idx, int32_t *cnt,
+                    int32_t *true_cnt, void *stream);
+
+/* COO radius graph from padded lists: replaces NeighborGrid.edge_index's torch mask ops
+ * (swarp/core/neighbors.py:716-733).  `offsets` [E*A] int64 must hold the exclusive
+ * prefix sum of cnt in (env, agent) order (n_edges = offsets[last] + cnt[last]);
+ * writes edge_index [2, n_edges] int64: row 0 = e*A + idx[e,a,s] (sender),
+ * row 1 = e*A + a (receiver), in (e, a, s) order. */
+int swarp_edge_index(int32_t n_envs, int32_t n_agents, int32_t max_neighbors,
+                     const int32_t *idx, const int32_t *cnt, const int64_t *offsets,
+                     int64_t n_edges, int64_t *edge_index, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SWARP_HIP_H */

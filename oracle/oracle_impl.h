@@ -1,0 +1,1150 @@
+/*
+ * oracle_impl.h -- body of the CPU restatement, included once per precision by
+ * swarp_oracle.c with REAL (float or double), FN(name) (name suffix) and the
+ * math macros SQRT/COS/SIN/TAN/ATAN/TANH/FABS defined.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is the parity checker for the HIP product
+ * (swarp_amd/csrc) and the CPU baseline timed by bench.py.  Nothing in the
+ * product may include, link or call it.
+ *
+ * Every function restates the reference algorithm from its source text, in the
+ * same operation order (no FMA contraction: the build uses -ffp-contract=off),
+ * so that a float32 run with no transcendental functions (holonomic agents,
+ * circle obstacles, walls) is bit-identical to any other IEEE implementation of
+ * the same op sequence.  Citations are relative to the reference checkout.
+ *
+ * The adjoint ("backward") functions are hand-derived reverse mode of the
+ * forward functions below; the reference gets the same from warp-lang's code
+ * generator.  Kink conventions follow warp-lang's documented builtins:
+ *   max(a, b):      a > b -> gradient to a, else to b
+ *   clamp(x, a, b): x < a -> a, x > b -> b, else x
+ *   length(v):      zero gradient at v == 0
+ * and a branch taken in the forward pass is taken again in the adjoint.
+ */
+
+typedef struct {
+    REAL px, py, th, vx, vy, s, w, z, vz, qx, qy, qz, qw, bx, by, bz;
+} FN(agent_t);
+
+typedef struct {
+    /* per-agent constants resolved from the [A, 22] parameter row */
+    REAL radius, mass, max_speed, max_accel, max_ang_vel, max_ang_accel;
+    REAL l_f, l_r, max_steer, thrust_max, arm, ixx, iyy, izz, kappa, gravity, min_speed;
+    int tag, mode;
+} FN(prm_t);
+
+typedef struct {
+    REAL k, c, margin, sub_dt, max_overlap, nbr_radius, eps2;
+    REAL bmin_x, bmin_y, bmax_x, bmax_y;
+    int n_envs, n_agents, act_dim, substeps, max_nbr;
+    int collisions, soft_walls, clamp_bounds, needs_forces, n_obs;
+    /* obstacles: pos [E,N,2], radius [N], type [N], angle [E,N], half [N,2],
+       vel [E,N,2], ang_vel [E,N] */
+    const REAL *o_pos, *o_rad, *o_ang, *o_half, *o_vel, *o_om;
+    const int32_t *o_type;
+} FN(ctx_t);
+
+/* ------------------------------------------------------------ small helpers */
+
+static inline REAL FN(rmax)(REAL a, REAL b) { return a > b ? a : b; }
+static inline REAL FN(rclamp)(REAL x, REAL a, REAL b)
+{
+    /* clamp(x, a, b) = min(max(a, x), b) */
+    REAL m = a > x ? a : x;
+    return m < b ? m : b;
+}
+/* gradient of clamp(x, a, b) with respect to x */
+static inline REAL FN(rclamp_gx)(REAL x, REAL a, REAL b, REAL g)
+{
+    if (x < a) return (REAL)0;
+    if (x > b) return (REAL)0;
+    return g;
+}
+
+/* clamp_norm (swarp/dynamics/kernels.py:68-71): v * (limit / max(length(v), limit)) */
+static inline void FN(clamp_norm)(REAL x, REAL y, REAL lim, REAL *ox, REAL *oy)
+{
+    REAL len = SQRT(x * x + y * y);
+    REAL m = FN(rmax)(len, lim);
+    REAL sc = lim / m;
+    *ox = x * sc;
+    *oy = y * sc;
+}
+
+static inline void FN(clamp_norm_adj)(REAL x, REAL y, REAL lim, REAL gx, REAL gy,
+                                      REAL *ax, REAL *ay)
+{
+    REAL len = SQRT(x * x + y * y);
+    REAL m = FN(rmax)(len, lim);
+    REAL sc = lim / m;
+    REAL adj_sc = gx * x + gy * y;
+    REAL rx = gx * sc, ry = gy * sc;
+    if (len > lim) {
+        /* sc = lim / m, d sc / d m = -lim / m^2 ; m = len */
+        REAL adj_m = -adj_sc * lim / (m * m);
+        if (len > (REAL)0) {
+            rx += adj_m * x / len;
+            ry += adj_m * y / len;
+        }
+    }
+    *ax += rx;
+    *ay += ry;
+}
+
+/* _normal_coeff (swarp/core/collisions.py:87-105) */
+static inline REAL FN(normal_coeff)(const FN(ctx_t) *C, REAL ov, REAL vn, REAL dd)
+{
+    REAL o = ov;
+    if (C->max_overlap > (REAL)0) o = C->max_overlap * TANH(ov / C->max_overlap);
+    return FN(rmax)((C->k * o - C->c * vn) / dd, (REAL)0);
+}
+
+static inline void FN(normal_coeff_adj)(const FN(ctx_t) *C, REAL ov, REAL vn, REAL dd,
+                                        REAL g, REAL *adj_ov, REAL *adj_vn)
+{
+    REAL o = ov, dodov = (REAL)1;
+    if (C->max_overlap > (REAL)0) {
+        REAL t = TANH(ov / C->max_overlap);
+        o = C->max_overlap * t;
+        dodov = (REAL)1 - t * t;
+    }
+    REAL x = (C->k * o - C->c * vn) / dd;
+    if (x > (REAL)0) {
+        REAL an = g / dd;
+        *adj_ov += C->k * an * dodov;
+        *adj_vn += -C->c * an;
+    }
+}
+
+/* pair_force (swarp/core/collisions.py:108-143) */
+static inline void FN(pair_force)(const FN(ctx_t) *C, REAL dx, REAL dy, REAL rvx, REAL rvy,
+                                  REAL md, REAL dd, REAL *fx, REAL *fy)
+{
+    REAL dist = SQRT(FN(rmax)(dx * dx + dy * dy, C->eps2));
+    REAL ov = md - dist;
+    *fx = (REAL)0;
+    *fy = (REAL)0;
+    if (ov > (REAL)0) {
+        REAL nx = dx / dist, ny = dy / dist;
+        REAL coef = FN(normal_coeff)(C, ov, rvx * nx + rvy * ny, dd);
+        *fx = coef * nx;
+        *fy = coef * ny;
+    }
+}
+
+/* reverse mode of pair_force: accumulates d/d(d) and d/d(rel_v) */
+static inline void FN(pair_force_adj)(const FN(ctx_t) *C, REAL dx, REAL dy, REAL rvx, REAL rvy,
+                                      REAL md, REAL dd, REAL gfx, REAL gfy,
+                                      REAL *adx, REAL *ady, REAL *arvx, REAL *arvy)
+{
+    REAL d2 = dx * dx + dy * dy;
+    REAL m = FN(rmax)(d2, C->eps2);
+    REAL dist = SQRT(m);
+    REAL ov = md - dist;
+    if (!(ov > (REAL)0)) return;
+    REAL nx = dx / dist, ny = dy / dist;
+    REAL vn = rvx * nx + rvy * ny;
+    REAL coef = FN(normal_coeff)(C, ov, vn, dd);
+    REAL adj_coef = gfx * nx + gfy * ny;
+    REAL anx = coef * gfx, any = coef * gfy;
+    REAL adj_ov = 0, adj_vn = 0;
+    FN(normal_coeff_adj)(C, ov, vn, dd, adj_coef, &adj_ov, &adj_vn);
+    *arvx += adj_vn * nx;
+    *arvy += adj_vn * ny;
+    anx += adj_vn * rvx;
+    any += adj_vn * rvy;
+    REAL gdx = anx / dist, gdy = any / dist;
+    REAL adj_dist = -(anx * nx + any * ny) / dist - adj_ov;
+    if (d2 > C->eps2) {
+        REAL adj_d2 = adj_dist * (REAL)0.5 / dist;
+        gdx += (REAL)2 * dx * adj_d2;
+        gdy += (REAL)2 * dy * adj_d2;
+    }
+    *adx += gdx;
+    *ady += gdy;
+}
+
+/* shape_bound / bounds_apart (swarp/core/collisions.py:61-84) */
+static inline REAL FN(shape_bound)(int st, REAL r, REAL hx, REAL hy)
+{
+    if (st == 1) return SQRT(hx * hx + hy * hy);
+    if (st == 2) return hx + r;
+    return r;
+}
+static inline int FN(bounds_apart)(REAL dx, REAL dy, REAL reach)
+{
+    REAL lim = reach * (REAL)1.0001 + (REAL)1.0e-6;
+    return dx * dx + dy * dy > lim * lim;
+}
+
+/* box_force (swarp/core/collisions.py:174-260); returns the force */
+static inline void FN(box_force)(const FN(ctx_t) *C, REAL px, REAL py, REAL vx, REAL vy,
+                                 REAL cx0, REAL cy0, REAL ang, REAL hx, REAL hy, REAL reach,
+                                 REAL dd, REAL vox, REAL voy, REAL om, REAL *fx, REAL *fy)
+{
+    REAL ca = COS(ang), sa = SIN(ang);
+    REAL dx = px - cx0, dy = py - cy0;
+    REAL lx = ca * dx + sa * dy;
+    REAL ly = -sa * dx + ca * dy;
+    REAL qx = FABS(lx) - hx, qy = FABS(ly) - hy;
+    REAL cx = FN(rclamp)(lx, -hx, hx), cy = FN(rclamp)(ly, -hy, hy);
+    REAL ox = lx - cx, oy = ly - cy;
+    REAL od2 = ox * ox + oy * oy;
+    REAL s, nlx, nly;
+    if (od2 > C->eps2) {
+        s = SQRT(od2);
+        nlx = ox / s;
+        nly = oy / s;
+    } else if (qx > qy) {
+        s = qx;
+        nlx = lx >= (REAL)0 ? (REAL)1 : (REAL)-1;
+        nly = (REAL)0;
+    } else {
+        s = qy;
+        nlx = (REAL)0;
+        nly = ly >= (REAL)0 ? (REAL)1 : (REAL)-1;
+    }
+    *fx = (REAL)0;
+    *fy = (REAL)0;
+    REAL ov = reach - s;
+    if (ov > (REAL)0) {
+        REAL nx = ca * nlx - sa * nly, ny = sa * nlx + ca * nly;
+        REAL spx = lx - s * nlx, spy = ly - s * nly;
+        REAL rx = ca * spx - sa * spy, ry = sa * spx + ca * spy;
+        REAL vsx = vox + -om * ry, vsy = voy + om * rx;
+        REAL rvx = vx - vsx, rvy = vy - vsy;
+        REAL coef = FN(normal_coeff)(C, ov, rvx * nx + rvy * ny, dd);
+        *fx = coef * nx;
+        *fy = coef * ny;
+    }
+}
+
+static inline void FN(box_force_adj)(const FN(ctx_t) *C, REAL px, REAL py, REAL vx, REAL vy,
+                                     REAL cx0, REAL cy0, REAL ang, REAL hx, REAL hy, REAL reach,
+                                     REAL dd, REAL vox, REAL voy, REAL om, REAL gfx, REAL gfy,
+                                     REAL *apx, REAL *apy, REAL *avx, REAL *avy)
+{
+    REAL ca = COS(ang), sa = SIN(ang);
+    REAL dx = px - cx0, dy = py - cy0;
+    REAL lx = ca * dx + sa * dy;
+    REAL ly = -sa * dx + ca * dy;
+    REAL qx = FABS(lx) - hx, qy = FABS(ly) - hy;
+    REAL cx = FN(rclamp)(lx, -hx, hx), cy = FN(rclamp)(ly, -hy, hy);
+    REAL ox = lx - cx, oy = ly - cy;
+    REAL od2 = ox * ox + oy * oy;
+    REAL s, nlx, nly;
+    int branch;
+    if (od2 > C->eps2) {
+        s = SQRT(od2);
+        nlx = ox / s;
+        nly = oy / s;
+        branch = 0;
+    } else if (qx > qy) {
+        s = qx;
+        nlx = lx >= (REAL)0 ? (REAL)1 : (REAL)-1;
+        nly = (REAL)0;
+        branch = 1;
+    } else {
+        s = qy;
+        nlx = (REAL)0;
+        nly = ly >= (REAL)0 ? (REAL)1 : (REAL)-1;
+        branch = 2;
+    }
+    REAL ov = reach - s;
+    if (!(ov > (REAL)0)) return;
+    REAL nx = ca * nlx - sa * nly, ny = sa * nlx + ca * nly;
+    REAL spx = lx - s * nlx, spy = ly - s * nly;
+    REAL rx = ca * spx - sa * spy, ry = sa * spx + ca * spy;
+    REAL vsx = vox + -om * ry, vsy = voy + om * rx;
+    REAL rvx = vx - vsx, rvy = vy - vsy;
+    REAL vn = rvx * nx + rvy * ny;
+    REAL coef = FN(normal_coeff)(C, ov, vn, dd);
+    /* f = coef * n */
+    REAL adj_coef = gfx * nx + gfy * ny;
+    REAL anx = coef * gfx, any = coef * gfy;
+    REAL adj_ov = 0, adj_vn = 0;
+    FN(normal_coeff_adj)(C, ov, vn, dd, adj_coef, &adj_ov, &adj_vn);
+    /* vn = rv . n */
+    REAL arvx = adj_vn * nx, arvy = adj_vn * ny;
+    anx += adj_vn * rvx;
+    any += adj_vn * rvy;
+    /* rv = v - vs ; vs = vo + (-om*ry, om*rx) */
+    *avx += arvx;
+    *avy += arvy;
+    REAL arx = -arvy * om;   /* d vsy / d rx = om, adj_vs = -adj_rv */
+    REAL ary = arvx * om;    /* d vsx / d ry = -om */
+    /* r = R sp */
+    REAL aspx = ca * arx + sa * ary, aspy = -sa * arx + ca * ary;
+    /* sp = l - s * nl */
+    REAL alx = aspx, aly = aspy;
+    REAL as = -(aspx * nlx + aspy * nly);
+    REAL anlx = -s * aspx, anly = -s * aspy;
+    /* n = R nl */
+    anlx += ca * anx + sa * any;
+    anly += -sa * anx + ca * any;
+    /* ov = reach - s */
+    as += -adj_ov;
+    if (branch == 0) {
+        /* nl = o / s ; s = sqrt(od2) */
+        REAL aox = anlx / s, aoy = anly / s;
+        as += -(anlx * nlx + anly * nly) / s;
+        REAL aod2 = as * (REAL)0.5 / s;
+        aox += (REAL)2 * ox * aod2;
+        aoy += (REAL)2 * oy * aod2;
+        /* o = l - clamp(l) */
+        alx += aox - FN(rclamp_gx)(lx, -hx, hx, aox);
+        aly += aoy - FN(rclamp_gx)(ly, -hy, hy, aoy);
+    } else if (branch == 1) {
+        /* s = |lx| - hx ; warp-lang adj_abs: x > 0 -> +g else -g */
+        alx += lx > (REAL)0 ? as : -as;
+    } else {
+        aly += ly > (REAL)0 ? as : -as;
+    }
+    /* l = R^T d */
+    REAL adx = ca * alx - sa * aly, ady = sa * alx + ca * aly;
+    *apx += adx;
+    *apy += ady;
+}
+
+/* closest_on_segment (swarp/core/collisions.py:156-171) */
+static inline void FN(closest_on_segment)(REAL px, REAL py, REAL cx, REAL cy, REAL ang, REAL hl,
+                                          REAL *ox, REAL *oy, REAL *t_out, REAL *tr_out)
+{
+    REAL dxu = COS(ang), dyu = SIN(ang);
+    REAL tr = (px - cx) * dxu + (py - cy) * dyu;
+    REAL t = FN(rclamp)(tr, -hl, hl);
+    *ox = cx + t * dxu;
+    *oy = cy + t * dyu;
+    if (t_out) *t_out = t;
+    if (tr_out) *tr_out = tr;
+}
+
+/* One obstacle's force on an agent; returns 0 if skipped by the broad phase. */
+static inline void FN(obstacle_force)(const FN(ctx_t) *C, int e, int o, REAL px, REAL py,
+                                      REAL vx, REAL vy, REAL ra, REAL dd, REAL *fx, REAL *fy)
+{
+    int N = C->n_obs;
+    REAL cx = C->o_pos[(e * N + o) * 2], cy = C->o_pos[(e * N + o) * 2 + 1];
+    int st = C->o_type[o];
+    REAL ro = C->o_rad[o], hx = C->o_half[o * 2], hy = C->o_half[o * 2 + 1];
+    *fx = (REAL)0;
+    *fy = (REAL)0;
+    if (FN(bounds_apart)(px - cx, py - cy, ra + C->margin + FN(shape_bound)(st, ro, hx, hy)))
+        return;
+    REAL vox = C->o_vel[(e * N + o) * 2], voy = C->o_vel[(e * N + o) * 2 + 1];
+    REAL om = C->o_om[e * N + o];
+    REAL ang = C->o_ang[e * N + o];
+    if (st == 1) {
+        FN(box_force)(C, px, py, vx, vy, cx, cy, ang, hx, hy, ra + C->margin, dd, vox, voy, om,
+                      fx, fy);
+    } else if (st == 2) {
+        REAL qx, qy;
+        FN(closest_on_segment)(px, py, cx, cy, ang, hx, &qx, &qy, 0, 0);
+        REAL rx = qx - cx, ry = qy - cy;
+        REAL vsx = vox + -om * ry, vsy = voy + om * rx;
+        FN(pair_force)(C, px - qx, py - qy, vx - vsx, vy - vsy, ra + ro + C->margin, dd, fx, fy);
+    } else {
+        FN(pair_force)(C, px - cx, py - cy, vx - vox, vy - voy, ra + ro + C->margin, dd, fx, fy);
+    }
+}
+
+static inline void FN(obstacle_force_adj)(const FN(ctx_t) *C, int e, int o, REAL px, REAL py,
+                                          REAL vx, REAL vy, REAL ra, REAL dd, REAL gfx, REAL gfy,
+                                          REAL *apx, REAL *apy, REAL *avx, REAL *avy)
+{
+    int N = C->n_obs;
+    REAL cx = C->o_pos[(e * N + o) * 2], cy = C->o_pos[(e * N + o) * 2 + 1];
+    int st = C->o_type[o];
+    REAL ro = C->o_rad[o], hx = C->o_half[o * 2], hy = C->o_half[o * 2 + 1];
+    if (FN(bounds_apart)(px - cx, py - cy, ra + C->margin + FN(shape_bound)(st, ro, hx, hy)))
+        return;
+    REAL vox = C->o_vel[(e * N + o) * 2], voy = C->o_vel[(e * N + o) * 2 + 1];
+    REAL om = C->o_om[e * N + o];
+    REAL ang = C->o_ang[e * N + o];
+    if (st == 1) {
+        FN(box_force_adj)(C, px, py, vx, vy, cx, cy, ang, hx, hy, ra + C->margin, dd, vox, voy,
+                          om, gfx, gfy, apx, apy, avx, avy);
+    } else if (st == 2) {
+        REAL qx, qy, t, tr;
+        FN(closest_on_segment)(px, py, cx, cy, ang, hx, &qx, &qy, &t, &tr);
+        REAL rx = qx - cx, ry = qy - cy;
+        REAL vsx = vox + -om * ry, vsy = voy + om * rx;
+        REAL adx = 0, ady = 0, arvx = 0, arvy = 0;
+        FN(pair_force_adj)(C, px - qx, py - qy, vx - vsx, vy - vsy, ra + ro + C->margin, dd,
+                           gfx, gfy, &adx, &ady, &arvx, &arvy);
+        /* d = p - q ; rv = v - vs ; vs = vo + (-om*ry, om*rx) ; r = q - c */
+        *apx += adx;
+        *apy += ady;
+        *avx += arvx;
+        *avy += arvy;
+        REAL aqx = -adx + (-arvy) * om;   /* through rx: vsy = voy + om*rx */
+        REAL aqy = -ady + arvx * om;      /* through ry: vsx = vox - om*ry */
+        /* q = c + t * u ; t = clamp(tr) ; tr = (p - c) . u */
+        REAL ux = COS(ang), uy = SIN(ang);
+        REAL at = aqx * ux + aqy * uy;
+        REAL atr = FN(rclamp_gx)(tr, -hx, hx, at);
+        *apx += atr * ux;
+        *apy += atr * uy;
+    } else {
+        REAL adx = 0, ady = 0, arvx = 0, arvy = 0;
+        FN(pair_force_adj)(C, px - cx, py - cy, vx - vox, vy - voy, ra + ro + C->margin, dd,
+                           gfx, gfy, &adx, &ady, &arvx, &arvy);
+        *apx += adx;
+        *apy += ady;
+        *avx += arvx;
+        *avy += arvy;
+    }
+}
+
+/* _wall_forces (swarp/core/collisions.py:746-778) */
+static inline void FN(wall_force)(const FN(ctx_t) *C, REAL px, REAL py, REAL vx, REAL vy,
+                                  REAL ra, REAL dd, REAL *fx_o, REAL *fy_o)
+{
+    REAL reach = ra + C->margin;
+    REAL fx = 0, fy = 0, pen;
+    pen = reach - (px - C->bmin_x);
+    if (pen > (REAL)0) fx += FN(normal_coeff)(C, pen, vx, dd);
+    pen = reach - (C->bmax_x - px);
+    if (pen > (REAL)0) fx += -FN(normal_coeff)(C, pen, -vx, dd);
+    pen = reach - (py - C->bmin_y);
+    if (pen > (REAL)0) fy += FN(normal_coeff)(C, pen, vy, dd);
+    pen = reach - (C->bmax_y - py);
+    if (pen > (REAL)0) fy += -FN(normal_coeff)(C, pen, -vy, dd);
+    *fx_o = fx;
+    *fy_o = fy;
+}
+
+static inline void FN(wall_force_adj)(const FN(ctx_t) *C, REAL px, REAL py, REAL vx, REAL vy,
+                                      REAL ra, REAL dd, REAL gfx, REAL gfy,
+                                      REAL *apx, REAL *apy, REAL *avx, REAL *avy)
+{
+    REAL reach = ra + C->margin, pen, aov, avn;
+    pen = reach - (px - C->bmin_x);
+    if (pen > (REAL)0) {
+        aov = 0; avn = 0;
+        FN(normal_coeff_adj)(C, pen, vx, dd, gfx, &aov, &avn);
+        *apx += -aov;
+        *avx += avn;
+    }
+    pen = reach - (C->bmax_x - px);
+    if (pen > (REAL)0) {
+        aov = 0; avn = 0;
+        FN(normal_coeff_adj)(C, pen, -vx, dd, -gfx, &aov, &avn);
+        *apx += aov;
+        *avx += -avn;
+    }
+    pen = reach - (py - C->bmin_y);
+    if (pen > (REAL)0) {
+        aov = 0; avn = 0;
+        FN(normal_coeff_adj)(C, pen, vy, dd, gfy, &aov, &avn);
+        *apy += -aov;
+        *avy += avn;
+    }
+    pen = reach - (C->bmax_y - py);
+    if (pen > (REAL)0) {
+        aov = 0; avn = 0;
+        FN(normal_coeff_adj)(C, pen, -vy, dd, -gfy, &aov, &avn);
+        *apy += aov;
+        *avy += -avn;
+    }
+}
+
+/* ------------------------------------------------------------------ neighbours */
+
+/* _brute_force (swarp/core/neighbors.py:76-97) for one env */
+static void FN(neighbors_env)(int A, int K, const FN(agent_t) *st, REAL radius,
+                              int32_t *idx, int32_t *cnt, int32_t *tru)
+{
+    for (int a = 0; a < A; ++a) {
+        REAL px = st[a].px, py = st[a].py;
+        int32_t count = 0, total = 0;
+        for (int b = 0; b < A; ++b) {
+            if (b == a) continue;
+            REAL dx = st[b].px - px, dy = st[b].py - py;
+            if (SQRT(dx * dx + dy * dy) <= radius) {
+                total += 1;
+                if (count < K) idx[a * K + count++] = b;
+            }
+        }
+        cnt[a] = count;
+        if (tru) tru[a] = total;
+    }
+}
+
+/* --------------------------------------------------------------- the force pass */
+
+/* collision_forces_kernel (swarp/core/collisions.py:818-881) for one env */
+static void FN(forces_env)(const FN(ctx_t) *C, int e, const FN(prm_t) *P, const FN(agent_t) *st,
+                           const int32_t *idx, const int32_t *cnt, REAL *F)
+{
+    int A = C->n_agents, K = C->max_nbr;
+    for (int a = 0; a < A; ++a) {
+        REAL px = st[a].px, py = st[a].py, vx = st[a].vx, vy = st[a].vy;
+        REAL ra = P[a].radius;
+        REAL fx = 0, fy = 0;
+        REAL dd = (REAL)1 + C->c * C->sub_dt / P[a].mass;
+        int n = C->collisions ? cnt[a] : 0;
+        for (int i = 0; i < n; ++i) {
+            int b = idx[a * K + i];
+            REAL gx, gy;
+            FN(pair_force)(C, px - st[b].px, py - st[b].py, vx - st[b].vx, vy - st[b].vy,
+                           ra + P[b].radius + C->margin, dd, &gx, &gy);
+            fx += gx;
+            fy += gy;
+        }
+        /* _static_forces: obstacles in index order, then the walls */
+        REAL sx = 0, sy = 0;
+        for (int o = 0; o < C->n_obs; ++o) {
+            REAL gx, gy;
+            FN(obstacle_force)(C, e, o, px, py, vx, vy, ra, dd, &gx, &gy);
+            sx += gx;
+            sy += gy;
+        }
+        if (C->soft_walls) {
+            REAL gx, gy;
+            FN(wall_force)(C, px, py, vx, vy, ra, dd, &gx, &gy);
+            sx += gx;
+            sy += gy;
+        }
+        F[a * 2] = fx + sx;
+        F[a * 2 + 1] = fy + sy;
+    }
+}
+
+static void FN(forces_env_adj)(const FN(ctx_t) *C, int e, const FN(prm_t) *P,
+                               const FN(agent_t) *st, const int32_t *idx, const int32_t *cnt,
+                               const REAL *aF, FN(agent_t) *adj)
+{
+    int A = C->n_agents, K = C->max_nbr;
+    for (int a = 0; a < A; ++a) {
+        REAL gfx = aF[a * 2], gfy = aF[a * 2 + 1];
+        if (gfx == (REAL)0 && gfy == (REAL)0) continue;
+        REAL px = st[a].px, py = st[a].py, vx = st[a].vx, vy = st[a].vy;
+        REAL ra = P[a].radius;
+        REAL dd = (REAL)1 + C->c * C->sub_dt / P[a].mass;
+        int n = C->collisions ? cnt[a] : 0;
+        for (int i = 0; i < n; ++i) {
+            int b = idx[a * K + i];
+            REAL adx = 0, ady = 0, arvx = 0, arvy = 0;
+            FN(pair_force_adj)(C, px - st[b].px, py - st[b].py, vx - st[b].vx, vy - st[b].vy,
+                               ra + P[b].radius + C->margin, dd, gfx, gfy,
+                               &adx, &ady, &arvx, &arvy);
+            adj[a].px += adx;
+            adj[a].py += ady;
+            adj[a].vx += arvx;
+            adj[a].vy += arvy;
+            adj[b].px -= adx;
+            adj[b].py -= ady;
+            adj[b].vx -= arvx;
+            adj[b].vy -= arvy;
+        }
+        for (int o = 0; o < C->n_obs; ++o)
+            FN(obstacle_force_adj)(C, e, o, px, py, vx, vy, ra, dd, gfx, gfy,
+                                   &adj[a].px, &adj[a].py, &adj[a].vx, &adj[a].vy);
+        if (C->soft_walls)
+            FN(wall_force_adj)(C, px, py, vx, vy, ra, dd, gfx, gfy,
+                               &adj[a].px, &adj[a].py, &adj[a].vx, &adj[a].vy);
+    }
+}
+
+/* ---------------------------------------------------------------- integration */
+
+/* _integrate_agent + _step_2d (swarp/dynamics/kernels.py:194-413), Euler */
+static void FN(integrate_agent)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *in,
+                                const REAL *act, REAL Fx, REAL Fy, FN(agent_t) *out)
+{
+    REAL dt = C->sub_dt;
+    REAL a0 = act[0], a1 = act[1];
+    REAL a2 = C->act_dim > 2 ? act[2] : (REAL)0;
+    REAL a3 = C->act_dim > 3 ? act[3] : (REAL)0;
+    *out = *in; /* drone fields (and unknown tags) pass through */
+    REAL pnx, pny;
+    if (P->tag == 3) {
+        /* DRONE branch (:349-369) with _drone_rates (:129-163) */
+        REAL dtm = dt / P->mass;
+        REAL dvx = Fx * dtm, dvy = Fy * dtm;
+        REAL zero = 0;
+        REAL f0 = FN(rclamp)(a0, zero, P->thrust_max), f1 = FN(rclamp)(a1, zero, P->thrust_max);
+        REAL f2 = FN(rclamp)(a2, zero, P->thrust_max), f3 = FN(rclamp)(a3, zero, P->thrust_max);
+        REAL thrust = f0 + f1 + f2 + f3;
+        REAL qx = in->qx, qy = in->qy, qz = in->qz, qw = in->qw;
+        REAL vx3 = 0, vy3 = 0, vz3 = thrust;
+        /* t = 2 * cross(u, v) */
+        REAL c1x = qy * vz3 - qz * vy3, c1y = qz * vx3 - qx * vz3, c1z = qx * vy3 - qy * vx3;
+        REAL tx_ = (REAL)2 * c1x, ty_ = (REAL)2 * c1y, tz_ = (REAL)2 * c1z;
+        REAL c2x = qy * tz_ - qz * ty_, c2y = qz * tx_ - qx * tz_, c2z = qx * ty_ - qy * tx_;
+        REAL fwx = vx3 + qw * tx_ + c2x, fwy = vy3 + qw * ty_ + c2y, fwz = vz3 + qw * tz_ + c2z;
+        REAL accx = fwx / P->mass - zero, accy = fwy / P->mass - zero;
+        REAL accz = fwz / P->mass - P->gravity;
+        REAL tqx = P->arm * (f1 - f3), tqy = P->arm * (f2 - f0);
+        REAL tqz = P->kappa * (f0 - f1 + f2 - f3);
+        REAL bx = in->bx, by = in->by, bz = in->bz;
+        REAL angx = (tqx - (P->izz - P->iyy) * by * bz) / P->ixx;
+        REAL angy = (tqy - (P->ixx - P->izz) * bz * bx) / P->iyy;
+        REAL angz = (tqz - (P->iyy - P->ixx) * bx * by) / P->izz;
+        REAL nbx = bx + angx * dt, nby = by + angy * dt, nbz = bz + angz * dt;
+        REAL nvz = in->vz + accz * dt;
+        REAL vxy_x = in->vx + accx * dt + dvx, vxy_y = in->vy + accy * dt + dvy;
+        /* _quat_deriv(q, br_new) (:117-126) */
+        REAL half = (REAL)0.5;
+        REAL dqx = half * (qw * nbx + qy * nbz - qz * nby);
+        REAL dqy = half * (qw * nby - qx * nbz + qz * nbx);
+        REAL dqz = half * (qw * nbz + qx * nby - qy * nbx);
+        REAL dqw = half * (-qx * nbx - qy * nby - qz * nbz);
+        REAL ux = qx + dqx * dt, uy = qy + dqy * dt, uz = qz + dqz * dt, uw = qw + dqw * dt;
+        REAL l = SQRT(ux * ux + uy * uy + uz * uz + uw * uw);
+        if (l > (REAL)0) {
+            out->qx = ux / l; out->qy = uy / l; out->qz = uz / l; out->qw = uw / l;
+        } else {
+            out->qx = 0; out->qy = 0; out->qz = 0; out->qw = 1;
+        }
+        pnx = in->px + vxy_x * dt;
+        pny = in->py + vxy_y * dt;
+        out->z = in->z + nvz * dt;
+        out->vz = nvz;
+        out->bx = nbx; out->by = nby; out->bz = nbz;
+        out->vx = vxy_x; out->vy = vxy_y;
+    } else {
+        REAL dtm = dt / P->mass;
+        REAL dvx = Fx * dtm, dvy = Fy * dtm;
+        REAL px = in->px, py = in->py, th = in->th;
+        if (P->tag == 0) {
+            REAL vnx, vny;
+            if (P->mode == 0) {
+                FN(clamp_norm)(a0, a1, P->max_speed, &vnx, &vny);
+            } else {
+                REAL accx, accy;
+                FN(clamp_norm)(a0, a1, P->max_accel, &accx, &accy);
+                FN(clamp_norm)(in->vx + accx * dt, in->vy + accy * dt, P->max_speed, &vnx, &vny);
+            }
+            vnx = vnx + dvx;
+            vny = vny + dvy;
+            pnx = px + vnx * dt;
+            pny = py + vny * dt;
+            out->th = th;
+            out->vx = vnx; out->vy = vny;
+            out->s = SQRT(vnx * vnx + vny * vny);
+            out->w = 0;
+        } else if (P->tag == 1) {
+            REAL sn, wn;
+            if (P->mode == 0) {
+                sn = FN(rclamp)(a0, -P->max_speed, P->max_speed);
+                wn = FN(rclamp)(a1, -P->max_ang_vel, P->max_ang_vel);
+            } else {
+                REAL acc = FN(rclamp)(a0, -P->max_accel, P->max_accel);
+                REAL alp = FN(rclamp)(a1, -P->max_ang_accel, P->max_ang_accel);
+                sn = FN(rclamp)(in->s + acc * dt, -P->max_speed, P->max_speed);
+                wn = FN(rclamp)(in->w + alp * dt, -P->max_ang_vel, P->max_ang_vel);
+            }
+            REAL vtx = sn * COS(th) + dvx, vty = sn * SIN(th) + dvy;
+            pnx = px + vtx * dt;
+            pny = py + vty * dt;
+            out->th = th + wn * dt;
+            out->vx = vtx; out->vy = vty;
+            out->s = sn;
+            out->w = wn;
+        } else if (P->tag == 2) {
+            REAL acc = FN(rclamp)(a0, -P->max_accel, P->max_accel);
+            REAL del = FN(rclamp)(a1, -P->max_steer, P->max_steer);
+            REAL sn = FN(rclamp)(in->s + acc * dt, P->min_speed, P->max_speed);
+            REAL wb = P->l_f + P->l_r;
+            REAL beta = ATAN(TAN(del) * P->l_r / wb);
+            REAL vtx = sn * COS(th + beta) + dvx, vty = sn * SIN(th + beta) + dvy;
+            REAL wn = sn / wb * COS(beta) * TAN(del);
+            pnx = px + vtx * dt;
+            pny = py + vty * dt;
+            out->th = th + wn * dt;
+            out->vx = vtx; out->vy = vty;
+            out->s = sn;
+            out->w = wn;
+        } else {
+            pnx = px;
+            pny = py;
+        }
+    }
+    if (C->clamp_bounds) {
+        REAL r = P->radius;
+        pnx = FN(rclamp)(pnx, C->bmin_x + r, C->bmax_x - r);
+        pny = FN(rclamp)(pny, C->bmin_y + r, C->bmax_y - r);
+    }
+    out->px = pnx;
+    out->py = pny;
+}
+
+/* Reverse mode of integrate_agent: g = adjoint of *out (all 16 fields);
+   accumulates into gin (adjoint of *in), gact and gF. */
+static void FN(integrate_agent_adj)(const FN(ctx_t) *C, const FN(prm_t) *P,
+                                    const FN(agent_t) *in, const REAL *act, REAL Fx, REAL Fy,
+                                    const FN(agent_t) *g, FN(agent_t) *gin, REAL *gact,
+                                    REAL *gFx, REAL *gFy)
+{
+    REAL dt = C->sub_dt;
+    REAL a0 = act[0], a1 = act[1];
+    REAL a2 = C->act_dim > 2 ? act[2] : (REAL)0;
+    REAL a3 = C->act_dim > 3 ? act[3] : (REAL)0;
+    FN(agent_t) fwd;
+    FN(integrate_agent)(C, P, in, act, Fx, Fy, &fwd);
+    /* position clamp: recompute the unclamped position */
+    REAL gpx = g->px, gpy = g->py;
+    if (C->clamp_bounds) {
+        FN(agent_t) raw;
+        FN(ctx_t) C2 = *C;
+        C2.clamp_bounds = 0;
+        FN(integrate_agent)(&C2, P, in, act, Fx, Fy, &raw);
+        REAL r = P->radius;
+        gpx = FN(rclamp_gx)(raw.px, C->bmin_x + r, C->bmax_x - r, gpx);
+        gpy = FN(rclamp_gx)(raw.py, C->bmin_y + r, C->bmax_y - r, gpy);
+    }
+    REAL dtm = dt / P->mass;
+    if (P->tag == 3) {
+        REAL zero = 0;
+        REAL f0 = FN(rclamp)(a0, zero, P->thrust_max), f1 = FN(rclamp)(a1, zero, P->thrust_max);
+        REAL f2 = FN(rclamp)(a2, zero, P->thrust_max), f3 = FN(rclamp)(a3, zero, P->thrust_max);
+        REAL thrust = f0 + f1 + f2 + f3;
+        REAL qx = in->qx, qy = in->qy, qz = in->qz, qw = in->qw;
+        REAL vx3 = 0, vy3 = 0, vz3 = thrust;
+        REAL c1x = qy * vz3 - qz * vy3, c1y = qz * vx3 - qx * vz3, c1z = qx * vy3 - qy * vx3;
+        REAL tx_ = (REAL)2 * c1x, ty_ = (REAL)2 * c1y, tz_ = (REAL)2 * c1z;
+        REAL bx = in->bx, by = in->by, bz = in->bz;
+        REAL angx = (P->arm * (f1 - f3) - (P->izz - P->iyy) * by * bz) / P->ixx;
+        REAL angy = (P->arm * (f2 - f0) - (P->ixx - P->izz) * bz * bx) / P->iyy;
+        REAL angz = (P->kappa * (f0 - f1 + f2 - f3) - (P->iyy - P->ixx) * bx * by) / P->izz;
+        REAL nbx = bx + angx * dt, nby = by + angy * dt, nbz = bz + angz * dt;
+        REAL half = (REAL)0.5;
+        REAL dqx = half * (qw * nbx + qy * nbz - qz * nby);
+        REAL dqy = half * (qw * nby - qx * nbz + qz * nbx);
+        REAL dqz = half * (qw * nbz + qx * nby - qy * nbx);
+        REAL dqw = half * (-qx * nbx - qy * nby - qz * nbz);
+        REAL ux = qx + dqx * dt, uy = qy + dqy * dt, uz = qz + dqz * dt, uw = qw + dqw * dt;
+        REAL l = SQRT(ux * ux + uy * uy + uz * uz + uw * uw);
+
+        /* outputs: p, z, v_xy, vz, q, br ; th, s, w pass through */
+        gin->th += g->th;
+        gin->s += g->s;
+        gin->w += g->w;
+        /* p_new = p + vxy*dt ; z_new = z + vz_new*dt */
+        gin->px += gpx;
+        gin->py += gpy;
+        REAL gvx = g->vx + gpx * dt, gvy = g->vy + gpy * dt;
+        gin->z += g->z;
+        REAL gnvz = g->vz + g->z * dt;
+        /* q_new = u / l */
+        REAL gux = 0, guy = 0, guz = 0, guw = 0;
+        if (l > (REAL)0) {
+            REAL nx = ux / l, ny = uy / l, nz = uz / l, nw = uw / l;
+            REAL dot = g->qx * nx + g->qy * ny + g->qz * nz + g->qw * nw;
+            gux = (g->qx - nx * dot) / l;
+            guy = (g->qy - ny * dot) / l;
+            guz = (g->qz - nz * dot) / l;
+            guw = (g->qw - nw * dot) / l;
+        }
+        /* u = q + dq*dt */
+        REAL gqx = gux, gqy = guy, gqz = guz, gqw = guw;
+        REAL gdqx = gux * dt, gdqy = guy * dt, gdqz = guz * dt, gdqw = guw * dt;
+        /* dq = 0.5 * quat_deriv(q, nb) */
+        gdqx *= half; gdqy *= half; gdqz *= half; gdqw *= half;
+        gqw += gdqx * nbx + gdqy * nby + gdqz * nbz;
+        gqy += gdqx * nbz - gdqz * nbx - gdqw * nby;
+        gqz += -gdqx * nby + gdqy * nbx - gdqw * nbz;
+        gqx += -gdqy * nbz + gdqz * nby - gdqw * nbx;
+        REAL gnbx = g->bx + gdqx * qw + gdqy * qz - gdqz * qy - gdqw * qx;
+        REAL gnby = g->by - gdqx * qz + gdqy * qw + gdqz * qx - gdqw * qy;
+        REAL gnbz = g->bz + gdqx * qy - gdqy * qx + gdqz * qw - gdqw * qz;
+        /* nb = b + ang*dt */
+        REAL gangx = gnbx * dt, gangy = gnby * dt, gangz = gnbz * dt;
+        REAL gbx = gnbx, gby = gnby, gbz = gnbz;
+        /* angx = (tqx - (izz-iyy)*by*bz)/ixx etc. */
+        REAL gtqx = gangx / P->ixx, gtqy = gangy / P->iyy, gtqz = gangz / P->izz;
+        gby += -(P->izz - P->iyy) * bz * gtqx;
+        gbz += -(P->izz - P->iyy) * by * gtqx;
+        gbz += -(P->ixx - P->izz) * bx * gtqy;
+        gbx += -(P->ixx - P->izz) * bz * gtqy;
+        gbx += -(P->iyy - P->ixx) * by * gtqz;
+        gby += -(P->iyy - P->ixx) * bx * gtqz;
+        REAL gf0 = -P->arm * gtqy + P->kappa * gtqz;
+        REAL gf1 = P->arm * gtqx - P->kappa * gtqz;
+        REAL gf2 = P->arm * gtqy + P->kappa * gtqz;
+        REAL gf3 = -P->arm * gtqx - P->kappa * gtqz;
+        /* nvz = vz + accz*dt ; vxy = v + acc_xy*dt + F*dtm */
+        gin->vz += gnvz;
+        REAL gaccz = gnvz * dt;
+        gin->vx += gvx;
+        gin->vy += gvy;
+        REAL gaccx = gvx * dt, gaccy = gvy * dt;
+        *gFx += gvx * dtm;
+        *gFy += gvy * dtm;
+        /* acc = fw / m - (0,0,g) */
+        REAL gfwx = gaccx / P->mass, gfwy = gaccy / P->mass, gfwz = gaccz / P->mass;
+        /* fw = v3 + qw*t + cross(u, t) */
+        REAL gv3x = gfwx, gv3y = gfwy, gv3z = gfwz;
+        gqw += gfwx * tx_ + gfwy * ty_ + gfwz * tz_;
+        REAL gtx = qw * gfwx, gty = qw * gfwy, gtz = qw * gfwz;
+        /* c2 = u x t : gu += t x gc2 ; gt += gc2 x u */
+        gqx += ty_ * gfwz - tz_ * gfwy;
+        gqy += tz_ * gfwx - tx_ * gfwz;
+        gqz += tx_ * gfwy - ty_ * gfwx;
+        gtx += gfwy * qz - gfwz * qy;
+        gty += gfwz * qx - gfwx * qz;
+        gtz += gfwx * qy - gfwy * qx;
+        /* t = 2 * (u x v3) */
+        REAL gc1x = (REAL)2 * gtx, gc1y = (REAL)2 * gty, gc1z = (REAL)2 * gtz;
+        gqx += vy3 * gc1z - vz3 * gc1y;
+        gqy += vz3 * gc1x - vx3 * gc1z;
+        gqz += vx3 * gc1y - vy3 * gc1x;
+        gv3x += gc1y * qz - gc1z * qy;
+        gv3y += gc1z * qx - gc1x * qz;
+        gv3z += gc1x * qy - gc1y * qx;
+        (void)gv3x; (void)gv3y;
+        REAL gthrust = gv3z;
+        gf0 += gthrust; gf1 += gthrust; gf2 += gthrust; gf3 += gthrust;
+        gact[0] += FN(rclamp_gx)(a0, zero, P->thrust_max, gf0);
+        gact[1] += FN(rclamp_gx)(a1, zero, P->thrust_max, gf1);
+        if (C->act_dim > 2) gact[2] += FN(rclamp_gx)(a2, zero, P->thrust_max, gf2);
+        if (C->act_dim > 3) gact[3] += FN(rclamp_gx)(a3, zero, P->thrust_max, gf3);
+        gin->qx += gqx; gin->qy += gqy; gin->qz += gqz; gin->qw += gqw;
+        gin->bx += gbx; gin->by += gby; gin->bz += gbz;
+        return;
+    }
+    /* 2-D models: drone fields pass through */
+    gin->z += g->z; gin->vz += g->vz;
+    gin->qx += g->qx; gin->qy += g->qy; gin->qz += g->qz; gin->qw += g->qw;
+    gin->bx += g->bx; gin->by += g->by; gin->bz += g->bz;
+    REAL th = in->th;
+    if (P->tag == 0) {
+        REAL vnx = fwd.vx, vny = fwd.vy, sp = fwd.s;
+        /* p_new = p + vn*dt ; s = length(vn) ; th passthrough ; w = 0 */
+        gin->px += gpx;
+        gin->py += gpy;
+        gin->th += g->th;
+        REAL gvx = g->vx + gpx * dt, gvy = g->vy + gpy * dt;
+        if (sp > (REAL)0) {
+            gvx += g->s * vnx / sp;
+            gvy += g->s * vny / sp;
+        }
+        *gFx += gvx * dtm;
+        *gFy += gvy * dtm;
+        if (P->mode == 0) {
+            FN(clamp_norm_adj)(a0, a1, P->max_speed, gvx, gvy, &gact[0], &gact[1]);
+        } else {
+            REAL accx, accy;
+            FN(clamp_norm)(a0, a1, P->max_accel, &accx, &accy);
+            REAL v0x = in->vx + accx * dt, v0y = in->vy + accy * dt;
+            REAL g0x = 0, g0y = 0;
+            FN(clamp_norm_adj)(v0x, v0y, P->max_speed, gvx, gvy, &g0x, &g0y);
+            gin->vx += g0x;
+            gin->vy += g0y;
+            FN(clamp_norm_adj)(a0, a1, P->max_accel, g0x * dt, g0y * dt, &gact[0], &gact[1]);
+        }
+    } else if (P->tag == 1) {
+        REAL sn = fwd.s;
+        REAL c = COS(th), sn_ = SIN(th);
+        gin->px += gpx;
+        gin->py += gpy;
+        REAL gvtx = g->vx + gpx * dt, gvty = g->vy + gpy * dt;
+        gin->th += g->th;
+        REAL gwn = g->w + g->th * dt;
+        *gFx += gvtx * dtm;
+        *gFy += gvty * dtm;
+        REAL gsn = g->s + gvtx * c + gvty * sn_;
+        gin->th += gvtx * sn * -sn_ + gvty * sn * c;
+        if (P->mode == 0) {
+            gact[0] += FN(rclamp_gx)(a0, -P->max_speed, P->max_speed, gsn);
+            gact[1] += FN(rclamp_gx)(a1, -P->max_ang_vel, P->max_ang_vel, gwn);
+        } else {
+            REAL acc = FN(rclamp)(a0, -P->max_accel, P->max_accel);
+            REAL alp = FN(rclamp)(a1, -P->max_ang_accel, P->max_ang_accel);
+            REAL gx = FN(rclamp_gx)(in->s + acc * dt, -P->max_speed, P->max_speed, gsn);
+            REAL gy = FN(rclamp_gx)(in->w + alp * dt, -P->max_ang_vel, P->max_ang_vel, gwn);
+            gin->s += gx;
+            gin->w += gy;
+            gact[0] += FN(rclamp_gx)(a0, -P->max_accel, P->max_accel, gx * dt);
+            gact[1] += FN(rclamp_gx)(a1, -P->max_ang_accel, P->max_ang_accel, gy * dt);
+        }
+    } else if (P->tag == 2) {
+        REAL acc = FN(rclamp)(a0, -P->max_accel, P->max_accel);
+        REAL del = FN(rclamp)(a1, -P->max_steer, P->max_steer);
+        REAL sn = fwd.s;
+        REAL wb = P->l_f + P->l_r;
+        REAL td = TAN(del);
+        REAL bu = td * P->l_r / wb;
+        REAL beta = ATAN(bu);
+        REAL ang = th + beta;
+        REAL ca = COS(ang), sa = SIN(ang), cb = COS(beta);
+        gin->px += gpx;
+        gin->py += gpy;
+        REAL gvtx = g->vx + gpx * dt, gvty = g->vy + gpy * dt;
+        gin->th += g->th;
+        REAL gwn = g->w + g->th * dt;
+        *gFx += gvtx * dtm;
+        *gFy += gvty * dtm;
+        /* vt = sn*(cos(ang), sin(ang)) + dv */
+        REAL gsn = g->s + gvtx * ca + gvty * sa;
+        REAL gang = -gvtx * sn * sa + gvty * sn * ca;
+        /* wn = sn / wb * cos(beta) * td */
+        gsn += gwn * cb * td / wb;
+        REAL gbeta = gang - gwn * (sn / wb) * SIN(beta) * td;
+        REAL gtd = gwn * (sn / wb) * cb;
+        gin->th += gang;
+        /* beta = atan(bu) ; bu = td * l_r / wb ; td = tan(del) */
+        REAL gbu = gbeta / ((REAL)1 + bu * bu);
+        gtd += gbu * P->l_r / wb;
+        REAL gdel = gtd * ((REAL)1 + td * td);
+        REAL gx = FN(rclamp_gx)(in->s + acc * dt, P->min_speed, P->max_speed, gsn);
+        gin->s += gx;
+        gact[0] += FN(rclamp_gx)(a0, -P->max_accel, P->max_accel, gx * dt);
+        gact[1] += FN(rclamp_gx)(a1, -P->max_steer, P->max_steer, gdel);
+    } else {
+        gin->px += gpx; gin->py += gpy; gin->th += g->th;
+        gin->vx += g->vx; gin->vy += g->vy; gin->s += g->s; gin->w += g->w;
+    }
+}
+
+/* ------------------------------------------------------------ one env, one step */
+
+typedef struct {
+    FN(agent_t) *st;    /* (S+1) * A states of the substep chain */
+    REAL *F;            /* S * A * 2 forces */
+    int32_t *idx, *cnt; /* S * A * K and S * A lists */
+} FN(chain_t);
+
+/* Stepper.launch_substeps (swarp/core/stepper.py:784-1011), taped ordering:
+   per substep neighbours on the substep input, forces, then integrate. */
+static void FN(step_env)(const FN(ctx_t) *C, int e, const FN(prm_t) *P, const FN(agent_t) *in,
+                         const REAL *act, FN(agent_t) *out, FN(chain_t) *ch)
+{
+    int A = C->n_agents, S = C->substeps, K = C->max_nbr, ad = C->act_dim;
+    FN(agent_t) *st = ch->st;
+    memcpy(st, in, sizeof(FN(agent_t)) * A);
+    for (int s = 0; s < S; ++s) {
+        FN(agent_t) *cur = st + s * A, *nxt = st + (s + 1) * A;
+        REAL *F = ch->F + s * A * 2;
+        int32_t *idx = ch->idx + s * A * K, *cnt = ch->cnt + s * A;
+        if (C->needs_forces) {
+            if (C->collisions)
+                FN(neighbors_env)(A, K, cur, C->nbr_radius, idx, cnt, NULL);
+            else
+                for (int a = 0; a < A; ++a) cnt[a] = 0;
+            FN(forces_env)(C, e, P, cur, idx, cnt, F);
+        } else {
+            for (int a = 0; a < 2 * A; ++a) F[a] = 0;
+        }
+        for (int a = 0; a < A; ++a)
+            FN(integrate_agent)(C, P + a, cur + a, act + a * ad, F[a * 2], F[a * 2 + 1], nxt + a);
+    }
+    memcpy(out, st + S * A, sizeof(FN(agent_t)) * A);
+}
+
+/* reverse of step_env: gout = adjoint of the step output; writes gin, accumulates gact */
+static void FN(step_env_adj)(const FN(ctx_t) *C, int e, const FN(prm_t) *P,
+                             const FN(agent_t) *in, const REAL *act, const FN(agent_t) *gout,
+                             FN(agent_t) *gin, REAL *gact, FN(chain_t) *ch, FN(agent_t) *tmp,
+                             REAL *gF)
+{
+    int A = C->n_agents, S = C->substeps, K = C->max_nbr, ad = C->act_dim;
+    /* tmp receives the (unused) step output; the chain keeps every substep input */
+    FN(step_env)(C, e, P, in, act, tmp, ch);
+    FN(agent_t) *g = gin;
+    memcpy(g, gout, sizeof(FN(agent_t)) * A);
+    for (int s = S - 1; s >= 0; --s) {
+        FN(agent_t) *cur = ch->st + s * A;
+        REAL *F = ch->F + s * A * 2;
+        int32_t *idx = ch->idx + s * A * K, *cnt = ch->cnt + s * A;
+        memset(tmp, 0, sizeof(FN(agent_t)) * A);
+        for (int a = 0; a < 2 * A; ++a) gF[a] = 0;
+        for (int a = 0; a < A; ++a)
+            FN(integrate_agent_adj)(C, P + a, cur + a, act + a * ad, F[a * 2], F[a * 2 + 1],
+                                    g + a, tmp + a, gact + a * ad, gF + a * 2, gF + a * 2 + 1);
+        if (C->needs_forces) FN(forces_env_adj)(C, e, P, cur, idx, cnt, gF, tmp);
+        memcpy(g, tmp, sizeof(FN(agent_t)) * A);
+    }
+}
+
+/* ------------------------------------------------------------------ entry points */
+
+static void FN(make_ctx)(const oracle_cfg_t *cfg, const oracle_obs_t *obs, FN(ctx_t) *C)
+{
+    memset(C, 0, sizeof(*C));
+    C->k = (REAL)cfg->k;
+    C->c = (REAL)cfg->c;
+    C->margin = (REAL)cfg->margin;
+    C->sub_dt = (REAL)(cfg->dt / cfg->substeps);
+    C->max_overlap = (REAL)cfg->max_overlap;
+    C->nbr_radius = (REAL)cfg->neighbor_radius;
+    C->eps2 = (REAL)1.0e-10;
+    C->bmin_x = (REAL)cfg->bmin_x;
+    C->bmin_y = (REAL)cfg->bmin_y;
+    C->bmax_x = (REAL)cfg->bmax_x;
+    C->bmax_y = (REAL)cfg->bmax_y;
+    C->n_envs = cfg->n_envs;
+    C->n_agents = cfg->n_agents;
+    C->act_dim = cfg->act_dim;
+    C->substeps = cfg->substeps;
+    C->max_nbr = cfg->max_neighbors > 0 ? cfg->max_neighbors : 1;
+    C->collisions = cfg->collisions;
+    C->soft_walls = cfg->soft_walls;
+    C->clamp_bounds = cfg->clamp_bounds;
+    C->n_obs = obs ? obs->n_obstacles : 0;
+    C->needs_forces = C->collisions || C->soft_walls || C->n_obs > 0;
+    if (C->n_obs > 0) {
+        C->o_pos = (const REAL *)obs->pos;
+        C->o_rad = (const REAL *)obs->radius;
+        C->o_type = obs->type;
+        C->o_ang = (const REAL *)obs->angle;
+        C->o_half = (const REAL *)obs->half;
+        C->o_vel = (const REAL *)obs->vel;
+        C->o_om = (const REAL *)obs->ang_vel;
+    }
+}
+
+static void FN(make_prm)(const REAL *params, const int32_t *tags, const int32_t *modes, int A,
+                         FN(prm_t) *P)
+{
+    for (int a = 0; a < A; ++a) {
+        const REAL *r = params + a * 22;
+        P[a].radius = r[0]; P[a].mass = r[1]; P[a].max_speed = r[2]; P[a].max_accel = r[3];
+        P[a].max_ang_vel = r[4]; P[a].max_ang_accel = r[5]; P[a].l_f = r[6]; P[a].l_r = r[7];
+        P[a].max_steer = r[8]; P[a].thrust_max = r[9]; P[a].arm = r[10]; P[a].ixx = r[11];
+        P[a].iyy = r[12]; P[a].izz = r[13]; P[a].kappa = r[14]; P[a].gravity = r[15];
+        P[a].min_speed = r[16];
+        P[a].tag = tags[a];
+        P[a].mode = modes[a];
+    }
+}
+
+int FN(oracle_neighbors)(int E, int A, int K, const REAL *pos, double radius, int32_t *idx,
+                         int32_t *cnt, int32_t *tru)
+{
+    FN(agent_t) *st = (FN(agent_t) *)calloc((size_t)A, sizeof(FN(agent_t)));
+    if (!st) return -1;
+    for (int e = 0; e < E; ++e) {
+        for (int a = 0; a < A; ++a) {
+            st[a].px = pos[(e * A + a) * 2];
+            st[a].py = pos[(e * A + a) * 2 + 1];
+        }
+        FN(neighbors_env)(A, K, st, (REAL)radius, idx + (size_t)e * A * K, cnt + (size_t)e * A,
+                          tru + (size_t)e * A);
+    }
+    free(st);
+    return 0;
+}
+
+/* T-step rollout.  state0 [E,A,16], actions [T,E,A,ad], states out [T,E,A,16]. */
+int FN(oracle_rollout)(const oracle_cfg_t *cfg, const REAL *params, const int32_t *tags,
+                       const int32_t *modes, const oracle_obs_t *obs, int T, const REAL *state0,
+                       const REAL *actions, REAL *states)
+{
+    FN(ctx_t) C;
+    FN(make_ctx)(cfg, obs, &C);
+    int E = C.n_envs, A = C.n_agents, S = C.substeps, K = C.max_nbr, ad = C.act_dim;
+    FN(prm_t) *P = (FN(prm_t) *)calloc((size_t)A, sizeof(FN(prm_t)));
+    FN(make_prm)(params, tags, modes, A, P);
+    int nth = cfg->n_threads > 0 ? cfg->n_threads : 1;
+    int err = 0;
+#pragma omp parallel num_threads(nth)
+    {
+        FN(chain_t) ch;
+        ch.st = (FN(agent_t) *)malloc(sizeof(FN(agent_t)) * (size_t)(S + 1) * A);
+        ch.F = (REAL *)malloc(sizeof(REAL) * (size_t)S * A * 2);
+        ch.idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)S * A * K);
+        ch.cnt = (int32_t *)malloc(sizeof(int32_t) * (size_t)S * A);
+        if (!ch.st || !ch.F || !ch.idx || !ch.cnt) err = 1;
+#pragma omp for schedule(static)
+        for (int e = 0; e < E; ++e) {
+            if (err) continue;
+            const FN(agent_t) *cur = (const FN(agent_t) *)(state0 + (size_t)e * A * 16);
+            for (int t = 0; t < T; ++t) {
+                FN(agent_t) *out = (FN(agent_t) *)(states + ((size_t)t * E + e) * A * 16);
+                FN(step_env)(&C, e, P, cur, actions + ((size_t)t * E + e) * A * ad, out, &ch);
+                cur = out;
+            }
+        }
+        free(ch.st); free(ch.F); free(ch.idx); free(ch.cnt);
+    }
+    free(P);
+    return err ? -1 : 0;
+}
+
+/* Reverse of oracle_rollout.  `states` are the forward outputs (the per-step
+   checkpoints); adj_states [T,E,A,16] is the adjoint injected at every step
+   output (NULL = zero except adj_final), adj_final [E,A,16] the adjoint of the
+   last state (NULL = zero).  Writes adj_state0 [E,A,16] and adj_actions. */
+int FN(oracle_rollout_adj)(const oracle_cfg_t *cfg, const REAL *params, const int32_t *tags,
+                           const int32_t *modes, const oracle_obs_t *obs, int T,
+                           const REAL *state0, const REAL *actions, const REAL *states,
+                           const REAL *adj_states, const REAL *adj_final, REAL *adj_state0,
+                           REAL *adj_actions)
+{
+    FN(ctx_t) C;
+    FN(make_ctx)(cfg, obs, &C);
+    int E = C.n_envs, A = C.n_agents, S = C.substeps, K = C.max_nbr, ad = C.act_dim;
+    FN(prm_t) *P = (FN(prm_t) *)calloc((size_t)A, sizeof(FN(prm_t)));
+    FN(make_prm)(params, tags, modes, A, P);
+    int nth = cfg->n_threads > 0 ? cfg->n_threads : 1;
+    int err = 0;
+    memset(adj_actions, 0, sizeof(REAL) * (size_t)T * E * A * ad);
+#pragma omp parallel num_threads(nth)
+    {
+        FN(chain_t) ch;
+        ch.st = (FN(agent_t) *)malloc(sizeof(FN(agent_t)) * (size_t)(S + 1) * A);
+        ch.F = (REAL *)malloc(sizeof(REAL) * (size_t)S * A * 2);
+        ch.idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)S * A * K);
+        ch.cnt = (int32_t *)malloc(sizeof(int32_t) * (size_t)S * A);
+        FN(agent_t) *g = (FN(agent_t) *)malloc(sizeof(FN(agent_t)) * (size_t)A);
+        FN(agent_t) *gn = (FN(agent_t) *)malloc(sizeof(FN(agent_t)) * (size_t)A);
+        FN(agent_t) *tmp = (FN(agent_t) *)malloc(sizeof(FN(agent_t)) * (size_t)A);
+        REAL *gF = (REAL *)malloc(sizeof(REAL) * (size_t)A * 2);
+        if (!ch.st || !ch.F || !ch.idx || !ch.cnt || !g || !gn || !tmp || !gF) err = 1;
+#pragma omp for schedule(static)
+        for (int e = 0; e < E; ++e) {
+            if (err) continue;
+            memset(g, 0, sizeof(FN(agent_t)) * A);
+            for (int t = T - 1; t >= 0; --t) {
+                if (adj_states) {
+                    const REAL *src = adj_states + ((size_t)t * E + e) * A * 16;
+                    REAL *gd = (REAL *)g;
+                    for (int i = 0; i < A * 16; ++i) gd[i] += src[i];
+                }
+                if (t == T - 1 && adj_final) {
+                    const REAL *src = adj_final + (size_t)e * A * 16;
+                    REAL *gd = (REAL *)g;
+                    for (int i = 0; i < A * 16; ++i) gd[i] += src[i];
+                }
+                const FN(agent_t) *in =
+                    t == 0 ? (const FN(agent_t) *)(state0 + (size_t)e * A * 16)
+                           : (const FN(agent_t) *)(states + ((size_t)(t - 1) * E + e) * A * 16);
+                FN(step_env_adj)(&C, e, P, in, actions + ((size_t)t * E + e) * A * ad, g, gn,
+                                 adj_actions + ((size_t)t * E + e) * A * ad, &ch, tmp, gF);
+                memcpy(g, gn, sizeof(FN(agent_t)) * A);
+            }
+            memcpy(adj_state0 + (size_t)e * A * 16, g, sizeof(FN(agent_t)) * A);
+        }
+        free(ch.st); free(ch.F); free(ch.idx); free(ch.cnt);
+        free(g); free(gn); free(tmp); free(gF);
+    }
+    free(P);
+    return err ? -1 : 0;
+}
+
+/* The force pass alone on one state (for the closed-form pins). F out [E,A,2]. */
+int FN(oracle_forces)(const oracle_cfg_t *cfg, const REAL *params, const int32_t *tags,
+                      const int32_t *modes, const oracle_obs_t *obs, const REAL *state,
+                      REAL *F)
+{
+    FN(ctx_t) C;
+    FN(make_ctx)(cfg, obs, &C);
+    int E = C.n_envs, A = C.n_agents, K = C.max_nbr;
+    FN(prm_t) *P = (FN(prm_t) *)calloc((size_t)A, sizeof(FN(prm_t)));
+    int32_t *idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)A * K);
+    int32_t *cnt = (int32_t *)malloc(sizeof(int32_t) * (size_t)A);
+    FN(make_prm)(params, tags, modes, A, P);
+    for (int e = 0; e < E; ++e) {
+        const FN(agent_t) *st = (const FN(agent_t) *)(state + (size_t)e * A * 16);
+        if (C.collisions)
+            FN(neighbors_env)(A, K, st, C.nbr_radius, idx, cnt, NULL);
+        else
+            for (int a = 0; a < A; ++a) cnt[a] = 0;
+        FN(forces_env)(&C, e, P, st, idx, cnt, F + (size_t)e * A * 2);
+    }
+    free(P); free(idx); free(cnt);
+    return 0;
+}

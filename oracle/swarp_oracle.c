@@ -1,0 +1,66 @@
+/*
+ * swarp_oracle.c -- CPU restatement of swarp's differentiable physics step.
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker of the HIP product and the CPU
+ * baseline timed by bench.py.  Only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline leg may load it (through oracle/oracle.py).
+ *
+ * Restates, from the reference's source text:
+ *   neighbours     swarp/core/neighbors.py:76-97 (_brute_force)
+ *   contact forces swarp/core/collisions.py:48-260, 690-881
+ *   integration    swarp/dynamics/kernels.py:68-413 (Euler, all four models)
+ *   step ordering  swarp/core/stepper.py:784-1011 (taped path)
+ * and the reverse mode warp-lang generates for them (swarp/interop/autograd.py:277-296).
+ *
+ * Built with -ffp-contract=off so every a*b+c rounds twice, as written.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+typedef struct {
+    int n_envs, n_agents, act_dim, substeps, max_neighbors;
+    int collisions, soft_walls, clamp_bounds, n_threads;
+    double dt, k, c, margin, max_overlap, neighbor_radius;
+    double bmin_x, bmin_y, bmax_x, bmax_y;
+} oracle_cfg_t;
+
+typedef struct {
+    int n_obstacles;
+    const void *pos, *radius, *angle, *half, *vel, *ang_vel;
+    const int32_t *type;
+} oracle_obs_t;
+
+int oracle_abi_version(void) { return 1; }
+
+#define REAL double
+#define FN(x) x##_f64
+#define SQRT sqrt
+#define COS cos
+#define SIN sin
+#define TAN tan
+#define ATAN atan
+#define TANH tanh
+#define FABS fabs
+#include "oracle_impl.h"
+#undef REAL
+#undef FN
+#undef SQRT
+#undef COS
+#undef SIN
+#undef TAN
+#undef ATAN
+#undef TANH
+#undef FABS
+
+#define REAL float
+#define FN(x) x##_f32
+#define SQRT sqrtf
+#define COS cosf
+#define SIN sinf
+#define TAN tanf
+#define ATAN atanf
+#define TANH tanhf
+#define FABS fabsf
+#include "oracle_impl.h"

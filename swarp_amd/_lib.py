@@ -1,0 +1,127 @@
+"""ctypes binding of libswarp_hip.so (the C ABI declared in include/swarp_hip.h).
+
+The library is built in-tree (``python -m swarp_amd.build``) and loaded from this
+package directory.  There is no fallback: if the library is missing or was built
+for another ABI, every step raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+ABI_VERSION = 1
+F32, F64 = 0, 1
+
+_PKG = Path(__file__).resolve().parent
+LIB_PATH = Path(os.environ.get("SWARP_HIP_LIB", _PKG / "libswarp_hip.so"))
+
+
+class SwarpDesc(ctypes.Structure):
+    """Mirror of ``swarp_desc_t``."""
+
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
+        ("n_envs", ctypes.c_int32),
+        ("n_agents", ctypes.c_int32),
+        ("act_dim", ctypes.c_int32),
+        ("substeps", ctypes.c_int32),
+        ("max_neighbors", ctypes.c_int32),
+        ("n_obstacles", ctypes.c_int32),
+        ("collisions", ctypes.c_int32),
+        ("soft_walls", ctypes.c_int32),
+        ("clamp_bounds", ctypes.c_int32),
+        ("has_drone", ctypes.c_int32),
+        ("dt", ctypes.c_double),
+        ("k", ctypes.c_double),
+        ("c", ctypes.c_double),
+        ("margin", ctypes.c_double),
+        ("max_overlap", ctypes.c_double),
+        ("neighbor_radius", ctypes.c_double),
+        ("bounds_min", ctypes.c_double * 2),
+        ("bounds_max", ctypes.c_double * 2),
+        ("params", ctypes.c_void_p),
+        ("model_tag", ctypes.c_void_p),
+        ("ctrl_mode", ctypes.c_void_p),
+        ("obs_pos", ctypes.c_void_p),
+        ("obs_radius", ctypes.c_void_p),
+        ("obs_angle", ctypes.c_void_p),
+        ("obs_half", ctypes.c_void_p),
+        ("obs_vel", ctypes.c_void_p),
+        ("obs_ang_vel", ctypes.c_void_p),
+        ("obs_type", ctypes.c_void_p),
+    ]
+
+
+class SwarpState(ctypes.Structure):
+    """Mirror of ``swarp_state_t`` (nine nullable field pointers)."""
+
+    _fields_ = [
+        (name, ctypes.c_void_p)
+        for name in ("pos", "theta", "vel", "speed", "ang_vel", "z", "vz", "attitude", "body_rates")
+    ]
+
+
+#: Exported entry points and their ctypes signatures.
+SIGNATURES = {
+    "swarp_abi_version": ([], ctypes.c_int),
+    "swarp_last_error": ([], ctypes.c_char_p),
+    "swarp_rollout_fwd": (
+        [ctypes.POINTER(SwarpDesc), ctypes.c_int32, ctypes.POINTER(SwarpState), ctypes.c_void_p,
+         ctypes.POINTER(SwarpState), ctypes.POINTER(SwarpState), ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "swarp_rollout_bwd": (
+        [ctypes.POINTER(SwarpDesc), ctypes.c_int32, ctypes.POINTER(SwarpState), ctypes.c_void_p,
+         ctypes.POINTER(SwarpState), ctypes.POINTER(SwarpState), ctypes.POINTER(SwarpState),
+         ctypes.POINTER(SwarpState), ctypes.c_void_p, ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "swarp_neighbors": (
+        [ctypes.POINTER(SwarpDesc), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+         ctypes.c_void_p, ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "swarp_edge_index": (
+        [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
+         ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+}
+
+_lib = None
+
+
+class SwarpLibraryError(RuntimeError):
+    """The HIP library is missing, stale, or rejected a call."""
+
+
+def load() -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raises if it is absent or mismatched."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise SwarpLibraryError(
+            f"{LIB_PATH} is missing: build it with `python -m swarp_amd.build` "
+            "(hipcc, gfx950). swarp_amd has no CPU fallback."
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (args, res) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    ver = lib.swarp_abi_version()
+    if ver != ABI_VERSION:
+        raise SwarpLibraryError(f"{LIB_PATH} has ABI {ver}, expected {ABI_VERSION}: rebuild it")
+    _lib = lib
+    return lib
+
+
+def check(rc: int) -> None:
+    """Raise the library's own message when a call returned non-zero."""
+    if rc != 0:
+        msg = load().swarp_last_error().decode(errors="replace")
+        raise SwarpLibraryError(f"libswarp_hip: {msg}")

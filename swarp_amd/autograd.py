@@ -1,0 +1,317 @@
+"""PyTorch autograd boundary of the step: ``TorchState``, ``warp_step``, ``rollout``,
+``GradRing`` -- the drop-in surface of ``swarp/interop/autograd.py:29-369``.
+
+The reference records every substep launch on a ``wp.Tape`` and replays Warp's
+generated adjoints per step.  Here a rollout of T steps is one autograd node over two
+HIP launches:
+
+* forward: ``swarp_rollout_fwd`` runs all T steps, writing each step's output state
+  (the trajectory, which doubles as the backward's checkpoints);
+* backward: ``swarp_rollout_bwd`` walks the steps in reverse, recomputing each step's
+  substeps from its checkpoint, and returns d(loss)/d(actions_seq) and d(loss)/d(state0).
+
+``warp_step`` is the T = 1 case.  The per-step semantics are the reference's: grads flow
+to the initial state and every action, every trajectory state can feed the loss, a
+repeated backward (``retain_graph``) gives the same result, and returned grads are fresh
+tensors.  Under ``torch.no_grad()`` (or when nothing requires grad) no graph is built
+and ``warp_step`` writes into the stepper's two recycled output slots
+(``swarp/core/stepper.py:688-710``).
+
+For a fleet without drones the four drone fields (``z, vz, attitude, body_rates``) are
+not stepped: every output state carries the input's drone tensors, whose values the
+reference would have copied unchanged (``swarp/dynamics/kernels.py:1856-1864``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import NamedTuple
+
+import torch
+
+from . import _lib
+from .stepper import Stepper, state_struct
+
+FIELDS = ("pos", "theta", "vel", "speed", "ang_vel", "z", "vz", "attitude", "body_rates")
+_TAIL = ((2,), (), (2,), (), (), (), (), (4,), (3,))
+
+
+class TorchState(NamedTuple):
+    """Torch view of the world state (``swarp/interop/autograd.py:29-45``)."""
+
+    pos: torch.Tensor  # [n_envs, n_agents, 2]
+    theta: torch.Tensor  # [n_envs, n_agents]
+    vel: torch.Tensor  # [n_envs, n_agents, 2]
+    speed: torch.Tensor  # [n_envs, n_agents]
+    ang_vel: torch.Tensor  # [n_envs, n_agents]
+    z: torch.Tensor | None = None  # [n_envs, n_agents]
+    vz: torch.Tensor | None = None  # [n_envs, n_agents]
+    attitude: torch.Tensor | None = None  # [n_envs, n_agents, 4] (x, y, z, w)
+    body_rates: torch.Tensor | None = None  # [n_envs, n_agents, 3]
+
+
+def fill_state_defaults(state: TorchState) -> TorchState:
+    """Materialise ``None`` drone fields as zeros / identity attitude
+    (``swarp/interop/autograd.py:48-68``)."""
+    if all(t is not None for t in state):
+        return state
+    ref = state.pos
+    e, a = ref.shape[0], ref.shape[1]
+    opts = {"device": ref.device, "dtype": ref.dtype}
+    z = state.z if state.z is not None else torch.zeros(e, a, **opts)
+    vz = state.vz if state.vz is not None else torch.zeros(e, a, **opts)
+    if state.attitude is not None:
+        att = state.attitude
+    else:
+        att = torch.zeros(e, a, 4, **opts)
+        att[..., 3] = 1.0
+    br = state.body_rates if state.body_rates is not None else torch.zeros(e, a, 3, **opts)
+    return state._replace(z=z, vz=vz, attitude=att, body_rates=br)
+
+
+def _nfields(stepper: Stepper) -> int:
+    return 9 if stepper.has_drone else 5
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _validate(stepper: Stepper, state: TorchState, actions_seq: torch.Tensor) -> tuple[int, int, int]:
+    if actions_seq.dim() != 4:
+        raise ValueError(
+            f"actions must be [T, n_envs, n_agents, act_dim]; got {tuple(actions_seq.shape)}"
+        )
+    T, E, A, ad = actions_seq.shape
+    if A != stepper.n_agents:
+        raise ValueError(f"actions carry {A} agents, the stepper has {stepper.n_agents}")
+    if ad < 1:
+        raise ValueError("act_dim must be >= 1")
+    if actions_seq.dtype != stepper.dtype:
+        raise TypeError(f"actions dtype {actions_seq.dtype} does not match the stepper's {stepper.dtype}")
+    if not actions_seq.is_cuda:
+        raise RuntimeError(
+            "swarp_amd steps on the HIP device only (no CPU fallback); got tensors on "
+            f"{actions_seq.device}"
+        )
+    for name, t, tail in zip(FIELDS, state, _TAIL):
+        if t is None:
+            continue
+        if tuple(t.shape) != (E, A, *tail):
+            raise ValueError(f"state.{name} must be {[E, A, *tail]}; got {list(t.shape)}")
+        if t.dtype != stepper.dtype:
+            raise TypeError(f"state.{name} dtype {t.dtype} does not match the stepper's {stepper.dtype}")
+        if t.device != actions_seq.device:
+            raise ValueError(f"state.{name} is on {t.device}, actions on {actions_seq.device}")
+    return T, E, ad
+
+
+def _launch_fwd(stepper: Stepper, state0, actions_seq: torch.Tensor, traj, final) -> None:
+    """One forward launch; ``traj``/``final`` are field lists (``traj`` stacked [T-1,...])."""
+    T, E, _, ad = actions_seq.shape
+    nf = _nfields(stepper)
+    lib = _lib.load()
+    desc = stepper.desc(E, ad)
+    s0 = state_struct(list(state0)[:nf])
+    fin = state_struct(list(final)[:nf])
+    tr = state_struct(list(traj)[:nf]) if traj is not None and T > 1 else None
+    _lib.check(lib.swarp_rollout_fwd(
+        ctypes.byref(desc), T, ctypes.byref(s0), actions_seq.data_ptr(),
+        ctypes.byref(tr) if tr is not None else None, ctypes.byref(fin), _stream(actions_seq),
+    ))
+
+
+def _empty_like_fields(stepper: Stepper, lead: tuple[int, ...], E: int, dev) -> list[torch.Tensor]:
+    nf = _nfields(stepper)
+    A = stepper.n_agents
+    return [torch.empty(*lead, E, A, *_TAIL[k], device=dev, dtype=stepper.dtype) for k in range(nf)]
+
+
+class _RolloutFn(torch.autograd.Function):
+    """T steps as one autograd node; outputs = final state fields, then the stacked
+    trajectory fields of steps 0..T-2."""
+
+    @staticmethod
+    def forward(ctx, stepper: Stepper, bufs, actions_seq: torch.Tensor, *state0: torch.Tensor):
+        ctx.set_materialize_grads(False)
+        T, E = actions_seq.shape[0], actions_seq.shape[1]
+        dev = actions_seq.device
+        actions_seq = actions_seq.contiguous()
+        state0 = tuple(t.contiguous() for t in state0)
+        if bufs is None:
+            final = _empty_like_fields(stepper, (), E, dev)
+            traj = _empty_like_fields(stepper, (max(T - 1, 0),), E, dev)
+        else:
+            final, traj = bufs
+        _launch_fwd(stepper, state0, actions_seq, traj, final)
+        ctx.stepper = stepper
+        ctx.nf = len(state0)
+        ctx.T = T
+        ctx.save_for_backward(actions_seq, *state0, *traj)
+        return (*final, *traj)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        stepper: Stepper = ctx.stepper
+        nf, T = ctx.nf, ctx.T
+        saved = ctx.saved_tensors
+        actions_seq = saved[0]
+        state0 = saved[1:1 + nf]
+        traj = saved[1 + nf:1 + 2 * nf]
+        g_final = [None if g is None else g.contiguous() for g in grads[:nf]]
+        g_traj = [None if g is None else g.contiguous() for g in grads[nf:2 * nf]]
+        need = ctx.needs_input_grad
+        adj_act = torch.empty_like(actions_seq)
+        adj0 = [torch.empty_like(s) if need[3 + k] else None for k, s in enumerate(state0)]
+        E, ad = actions_seq.shape[1], actions_seq.shape[3]
+        lib = _lib.load()
+        desc = stepper.desc(E, ad)
+        s0 = state_struct(state0)
+        tr = state_struct(traj) if T > 1 else None
+        gtr = state_struct(g_traj) if T > 1 and any(g is not None for g in g_traj) else None
+        gfin = state_struct(g_final) if any(g is not None for g in g_final) else None
+        a0 = state_struct(adj0)
+        _lib.check(lib.swarp_rollout_bwd(
+            ctypes.byref(desc), T, ctypes.byref(s0), actions_seq.data_ptr(),
+            ctypes.byref(tr) if tr is not None else None,
+            ctypes.byref(gtr) if gtr is not None else None,
+            ctypes.byref(gfin) if gfin is not None else None,
+            ctypes.byref(a0), adj_act.data_ptr(), _stream(actions_seq),
+        ))
+        return (None, None, adj_act if need[2] else None, *adj0)
+
+
+def _grad_mode(state: TorchState, actions: torch.Tensor) -> bool:
+    return torch.is_grad_enabled() and (
+        actions.requires_grad or any(t is not None and t.requires_grad for t in state)
+    )
+
+
+def _assemble(stepper: Stepper, state: TorchState, outs, T: int):
+    """(final TorchState, trajectory list) from the Function's outputs."""
+    nf = _nfields(stepper)
+    final_f = outs[:nf]
+    traj_f = outs[nf:2 * nf]
+    tail = tuple(state[nf:]) if nf == 5 else ()
+    traj = [TorchState(*(f[t] for f in traj_f), *tail) for t in range(T - 1)]
+    final = TorchState(*final_f, *tail)
+    traj.append(final)
+    return final, traj
+
+
+@dataclass
+class StepGradSlot:
+    """One step's pre-allocated outputs inside a :class:`GradRing`."""
+
+    ring: "GradRing"
+    index: int
+
+    @property
+    def out(self) -> list[torch.Tensor]:
+        return [b[self.index] for b in self.ring.bufs]
+
+
+class GradRing:
+    """Reusable output buffers for BPTT rollouts (``swarp/interop/autograd.py:184-226``).
+
+    Holds ``capacity`` step outputs.  ``rollout(..., ring=ring)`` writes a T-step
+    trajectory (T <= capacity) into it with no allocation; ``warp_step(..., slot=...)``
+    writes one step into the slot ``acquire`` hands out.  Reusing the ring overwrites
+    the previous rollout's outputs (the returned grads are always fresh tensors).
+    """
+
+    def __init__(self, stepper: Stepper, n_envs: int, act_dim: int, capacity: int) -> None:
+        if capacity < 1:
+            raise ValueError("GradRing capacity must be >= 1")
+        self.stepper = stepper
+        self.capacity = capacity
+        self.n_envs = n_envs
+        self.act_dim = act_dim
+        self._idx = 0
+        self.bufs = _empty_like_fields(stepper, (capacity,), n_envs, torch.device(stepper.device))
+        self.slots = [StepGradSlot(self, i) for i in range(capacity)]
+
+    def reset(self) -> None:
+        self._idx = 0
+
+    def acquire(self) -> StepGradSlot:
+        if self._idx >= self.capacity:
+            raise RuntimeError(
+                f"GradRing capacity {self.capacity} exhausted; size it to the rollout length T"
+            )
+        slot = self.slots[self._idx]
+        self._idx += 1
+        return slot
+
+    def rollout_buffers(self, T: int):
+        if T > self.capacity:
+            raise RuntimeError(
+                f"GradRing capacity {self.capacity} exhausted; size it to the rollout length T"
+            )
+        self._idx = T
+        final = [b[T - 1] for b in self.bufs]
+        traj = [b[: T - 1] for b in self.bufs]
+        return final, traj
+
+
+def warp_step(
+    stepper: Stepper,
+    state: TorchState,
+    actions: torch.Tensor,
+    slot: StepGradSlot | None = None,
+) -> TorchState:
+    """Differentiable env step ``state, actions -> next state``
+    (``swarp/interop/autograd.py:299-338``)."""
+    state = fill_state_defaults(state)
+    if actions.dim() != 3:
+        raise ValueError(f"actions must be [n_envs, n_agents, act_dim]; got {tuple(actions.shape)}")
+    seq = actions.unsqueeze(0)
+    _validate(stepper, state, seq)
+    nf = _nfields(stepper)
+    if _grad_mode(state, actions):
+        bufs = None
+        if slot is not None:
+            bufs = (slot.out, [b[:0] for b in slot.ring.bufs])
+        outs = _RolloutFn.apply(stepper, bufs, seq, *state[:nf])
+        final, _ = _assemble(stepper, state, outs, 1)
+        return final
+    out = stepper.output_state(actions.shape[0])
+    final = list(out[:nf])
+    _launch_fwd(stepper, [t.contiguous() for t in state[:nf]], seq.contiguous(), None, final)
+    tail = tuple(state[nf:]) if nf == 5 else ()
+    return TorchState(*final, *tail)
+
+
+def rollout(
+    stepper: Stepper,
+    state: TorchState,
+    actions_seq: torch.Tensor,
+    ring: GradRing | None = None,
+) -> tuple[TorchState, list[TorchState]]:
+    """Backprop-through-time rollout (``swarp/interop/autograd.py:341-369``).
+
+    ``actions_seq [T, n_envs, n_agents, act_dim]``.  Returns ``(final_state,
+    trajectory)`` with the state after each of the T steps; gradients flow to
+    ``state`` and ``actions_seq``.
+    """
+    state = fill_state_defaults(state)
+    T, E, _ = _validate(stepper, state, actions_seq)
+    if T < 1:
+        raise ValueError("actions_seq must hold at least one step")
+    nf = _nfields(stepper)
+    bufs = None
+    if ring is not None:
+        ring.reset()
+        bufs = ring.rollout_buffers(T)
+    if _grad_mode(state, actions_seq):
+        outs = _RolloutFn.apply(stepper, bufs, actions_seq, *state[:nf])
+    else:
+        if bufs is None:
+            final = _empty_like_fields(stepper, (), E, actions_seq.device)
+            traj = _empty_like_fields(stepper, (T - 1,), E, actions_seq.device)
+        else:
+            final, traj = bufs
+        _launch_fwd(stepper, [t.contiguous() for t in state[:nf]], actions_seq.contiguous(), traj, final)
+        outs = (*final, *traj)
+    return _assemble(stepper, state, outs, T)

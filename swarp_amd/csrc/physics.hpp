@@ -1,0 +1,747 @@
+// physics.hpp -- per-agent device physics of the swarp step for gfx950: contact
+// forces, walls, obstacles and the Euler integrator of the four dynamics models, plus
+// their hand-written reverse mode.  Included by swarp_hip.hip only.
+//
+// Operation order follows the reference source text so that float32 results with no
+// transcendental functions are bit-identical to any IEEE restatement of it; the build
+// disables FMA contraction and keeps divide/sqrt correctly rounded.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace swarp {
+
+__device__ __forceinline__ float m_sqrt(float x) { return sqrtf(x); }
+__device__ __forceinline__ double m_sqrt(double x) { return sqrt(x); }
+__device__ __forceinline__ float m_cos(float x) { return cosf(x); }
+__device__ __forceinline__ double m_cos(double x) { return cos(x); }
+__device__ __forceinline__ float m_sin(float x) { return sinf(x); }
+__device__ __forceinline__ double m_sin(double x) { return sin(x); }
+__device__ __forceinline__ float m_tan(float x) { return tanf(x); }
+__device__ __forceinline__ double m_tan(double x) { return tan(x); }
+__device__ __forceinline__ float m_atan(float x) { return atanf(x); }
+__device__ __forceinline__ double m_atan(double x) { return atan(x); }
+__device__ __forceinline__ float m_tanh(float x) { return tanhf(x); }
+__device__ __forceinline__ double m_tanh(double x) { return tanh(x); }
+__device__ __forceinline__ float m_abs(float x) { return fabsf(x); }
+__device__ __forceinline__ double m_abs(double x) { return fabs(x); }
+
+// warp-lang semantics: max(a,b) = a > b ? a : b ; clamp(x,a,b) = min(max(a,x),b)
+template <typename T> __device__ __forceinline__ T wmax(T a, T b) { return a > b ? a : b; }
+template <typename T> __device__ __forceinline__ T wclamp(T x, T a, T b)
+{
+    T m = a > x ? a : x;
+    return m < b ? m : b;
+}
+// gradient of clamp(x, a, b) w.r.t. x (x < a -> a, x > b -> b, else x)
+template <typename T> __device__ __forceinline__ T wclamp_g(T x, T a, T b, T g)
+{
+    return (x < a || x > b) ? T(0) : g;
+}
+
+// One agent's full state: the nine TorchState fields flattened (16 scalars).
+template <typename T> struct St {
+    T px, py, th, vx, vy, s, w, z, vz, qx, qy, qz, qw, bx, by, bz;
+};
+
+template <typename T> __device__ __forceinline__ void st_zero(St<T> &g)
+{
+    g.px = g.py = g.th = g.vx = g.vy = g.s = g.w = g.z = g.vz = T(0);
+    g.qx = g.qy = g.qz = g.qw = g.bx = g.by = g.bz = T(0);
+}
+
+// Per-agent constants of one parameter row (PARAM_FIELDS column order).
+template <typename T> struct Prm {
+    T radius, mass, max_speed, max_accel, max_ang_vel, max_ang_accel, l_f, l_r, max_steer;
+    T thrust_max, arm, ixx, iyy, izz, kappa, gravity, min_speed;
+    int tag, mode;
+};
+
+// Step-wide constants, already rounded to T on the host exactly as the reference's
+// `dtype(x)` conversions do.
+template <typename T> struct Cst {
+    T k, c, margin, sub_dt, max_overlap, eps2;
+    T t_nbr;        // largest T with sqrt(t_nbr) <= neighbor_radius (exact membership test)
+    T t_skin;       // candidate threshold of the per-step skin list (>= t_nbr)
+    T half_margin;  // per-agent displacement budget that keeps the skin list exact
+    T bmin_x, bmin_y, bmax_x, bmax_y;
+    int E, A, ad, S, K, N;
+    int collisions, soft_walls, clamp, needs_forces, use_skin;
+};
+
+// Obstacle arrays (device); shared extents [N], per-env poses [E,N].
+template <typename T> struct Obs {
+    const T *pos, *rad, *ang, *half, *vel, *om;
+    const int32_t *type;
+};
+
+// ------------------------------------------------------------- contact law
+
+// _normal_coeff (swarp/core/collisions.py:87-105)
+template <typename T>
+__device__ __forceinline__ T normal_coeff(const Cst<T> &C, T ov, T vn, T dd)
+{
+    T o = ov;
+    if (C.max_overlap > T(0)) o = C.max_overlap * m_tanh(ov / C.max_overlap);
+    return wmax((C.k * o - C.c * vn) / dd, T(0));
+}
+
+template <typename T>
+__device__ __forceinline__ void normal_coeff_adj(const Cst<T> &C, T ov, T vn, T dd, T g,
+                                                 T &a_ov, T &a_vn)
+{
+    T o = ov, slope = T(1);
+    if (C.max_overlap > T(0)) {
+        T th = m_tanh(ov / C.max_overlap);
+        o = C.max_overlap * th;
+        slope = T(1) - th * th;
+    }
+    if ((C.k * o - C.c * vn) / dd > T(0)) {
+        T q = g / dd;
+        a_ov += C.k * q * slope;
+        a_vn -= C.c * q;
+    }
+}
+
+// pair_force (swarp/core/collisions.py:108-143): force on self, d = self - other
+template <typename T>
+__device__ __forceinline__ void pair_force(const Cst<T> &C, T dx, T dy, T rvx, T rvy, T md,
+                                           T dd, T &fx, T &fy)
+{
+    T dist = m_sqrt(wmax(dx * dx + dy * dy, C.eps2));
+    T ov = md - dist;
+    fx = T(0);
+    fy = T(0);
+    if (ov > T(0)) {
+        T nx = dx / dist, ny = dy / dist;
+        T coef = normal_coeff(C, ov, rvx * nx + rvy * ny, dd);
+        fx = coef * nx;
+        fy = coef * ny;
+    }
+}
+
+// reverse of pair_force: accumulates the adjoints of d and rel_v
+template <typename T>
+__device__ __forceinline__ void pair_force_adj(const Cst<T> &C, T dx, T dy, T rvx, T rvy, T md,
+                                               T dd, T gx, T gy, T &adx, T &ady, T &arx,
+                                               T &ary)
+{
+    T d2 = dx * dx + dy * dy;
+    T dist = m_sqrt(wmax(d2, C.eps2));
+    T ov = md - dist;
+    if (!(ov > T(0))) return;
+    T nx = dx / dist, ny = dy / dist;
+    T vn = rvx * nx + rvy * ny;
+    T coef = normal_coeff(C, ov, vn, dd);
+    T a_ov = T(0), a_vn = T(0);
+    normal_coeff_adj(C, ov, vn, dd, gx * nx + gy * ny, a_ov, a_vn);
+    T anx = coef * gx + a_vn * rvx;
+    T any = coef * gy + a_vn * rvy;
+    arx += a_vn * nx;
+    ary += a_vn * ny;
+    T a_dist = -(anx * nx + any * ny) / dist - a_ov;
+    T ex = anx / dist, ey = any / dist;
+    if (d2 > C.eps2) {
+        T h = a_dist * T(0.5) / dist;
+        ex += T(2) * dx * h;
+        ey += T(2) * dy * h;
+    }
+    adx += ex;
+    ady += ey;
+}
+
+// ------------------------------------------------------------------- walls
+
+// _wall_forces (swarp/core/collisions.py:746-778)
+template <typename T>
+__device__ __forceinline__ void wall_force(const Cst<T> &C, T px, T py, T vx, T vy, T ra, T dd,
+                                           T &fx, T &fy)
+{
+    T reach = ra + C.margin;
+    T ax = T(0), ay = T(0), pen;
+    pen = reach - (px - C.bmin_x);
+    if (pen > T(0)) ax += normal_coeff(C, pen, vx, dd);
+    pen = reach - (C.bmax_x - px);
+    if (pen > T(0)) ax += -normal_coeff(C, pen, -vx, dd);
+    pen = reach - (py - C.bmin_y);
+    if (pen > T(0)) ay += normal_coeff(C, pen, vy, dd);
+    pen = reach - (C.bmax_y - py);
+    if (pen > T(0)) ay += -normal_coeff(C, pen, -vy, dd);
+    fx = ax;
+    fy = ay;
+}
+
+template <typename T>
+__device__ __forceinline__ void wall_force_adj(const Cst<T> &C, T px, T py, T vx, T vy, T ra,
+                                               T dd, T gx, T gy, St<T> &a)
+{
+    T reach = ra + C.margin, pen;
+    pen = reach - (px - C.bmin_x);
+    if (pen > T(0)) {
+        T o = T(0), v = T(0);
+        normal_coeff_adj(C, pen, vx, dd, gx, o, v);
+        a.px -= o;
+        a.vx += v;
+    }
+    pen = reach - (C.bmax_x - px);
+    if (pen > T(0)) {
+        T o = T(0), v = T(0);
+        normal_coeff_adj(C, pen, -vx, dd, -gx, o, v);
+        a.px += o;
+        a.vx -= v;
+    }
+    pen = reach - (py - C.bmin_y);
+    if (pen > T(0)) {
+        T o = T(0), v = T(0);
+        normal_coeff_adj(C, pen, vy, dd, gy, o, v);
+        a.py -= o;
+        a.vy += v;
+    }
+    pen = reach - (C.bmax_y - py);
+    if (pen > T(0)) {
+        T o = T(0), v = T(0);
+        normal_coeff_adj(C, pen, -vy, dd, -gy, o, v);
+        a.py += o;
+        a.vy -= v;
+    }
+}
+
+// --------------------------------------------------------------- obstacles
+
+// box_force (swarp/core/collisions.py:174-260); reach = agent radius + margin
+template <typename T>
+__device__ __forceinline__ void box_force(const Cst<T> &C, T px, T py, T vx, T vy, T cx0, T cy0,
+                                          T ang, T hx, T hy, T reach, T dd, T vox, T voy, T om,
+                                          T &fx, T &fy)
+{
+    T ca = m_cos(ang), sa = m_sin(ang);
+    T dx = px - cx0, dy = py - cy0;
+    T lx = ca * dx + sa * dy;
+    T ly = -sa * dx + ca * dy;
+    T qx = m_abs(lx) - hx, qy = m_abs(ly) - hy;
+    T ox = lx - wclamp(lx, -hx, hx), oy = ly - wclamp(ly, -hy, hy);
+    T od2 = ox * ox + oy * oy;
+    T s, nlx, nly;
+    if (od2 > C.eps2) {
+        s = m_sqrt(od2);
+        nlx = ox / s;
+        nly = oy / s;
+    } else if (qx > qy) {
+        s = qx;
+        nlx = lx >= T(0) ? T(1) : T(-1);
+        nly = T(0);
+    } else {
+        s = qy;
+        nlx = T(0);
+        nly = ly >= T(0) ? T(1) : T(-1);
+    }
+    fx = T(0);
+    fy = T(0);
+    T ov = reach - s;
+    if (ov > T(0)) {
+        T nx = ca * nlx - sa * nly, ny = sa * nlx + ca * nly;
+        T spx = lx - s * nlx, spy = ly - s * nly;
+        T rx = ca * spx - sa * spy, ry = sa * spx + ca * spy;
+        T rvx = vx - (vox + -om * ry), rvy = vy - (voy + om * rx);
+        T coef = normal_coeff(C, ov, rvx * nx + rvy * ny, dd);
+        fx = coef * nx;
+        fy = coef * ny;
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void box_force_adj(const Cst<T> &C, T px, T py, T vx, T vy, T cx0,
+                                              T cy0, T ang, T hx, T hy, T reach, T dd, T vox,
+                                              T voy, T om, T gx, T gy, St<T> &a)
+{
+    T ca = m_cos(ang), sa = m_sin(ang);
+    T dx = px - cx0, dy = py - cy0;
+    T lx = ca * dx + sa * dy;
+    T ly = -sa * dx + ca * dy;
+    T qx = m_abs(lx) - hx, qy = m_abs(ly) - hy;
+    T ox = lx - wclamp(lx, -hx, hx), oy = ly - wclamp(ly, -hy, hy);
+    T od2 = ox * ox + oy * oy;
+    T s, nlx, nly;
+    int face;
+    if (od2 > C.eps2) {
+        s = m_sqrt(od2);
+        nlx = ox / s;
+        nly = oy / s;
+        face = 0;
+    } else if (qx > qy) {
+        s = qx;
+        nlx = lx >= T(0) ? T(1) : T(-1);
+        nly = T(0);
+        face = 1;
+    } else {
+        s = qy;
+        nlx = T(0);
+        nly = ly >= T(0) ? T(1) : T(-1);
+        face = 2;
+    }
+    T ov = reach - s;
+    if (!(ov > T(0))) return;
+    T nx = ca * nlx - sa * nly, ny = sa * nlx + ca * nly;
+    T spx = lx - s * nlx, spy = ly - s * nly;
+    T rx = ca * spx - sa * spy, ry = sa * spx + ca * spy;
+    T rvx = vx - (vox + -om * ry), rvy = vy - (voy + om * rx);
+    T vn = rvx * nx + rvy * ny;
+    T coef = normal_coeff(C, ov, vn, dd);
+    T a_ov = T(0), a_vn = T(0);
+    normal_coeff_adj(C, ov, vn, dd, gx * nx + gy * ny, a_ov, a_vn);
+    T anx = coef * gx + a_vn * rvx, any = coef * gy + a_vn * rvy;
+    T arvx = a_vn * nx, arvy = a_vn * ny;
+    a.vx += arvx;
+    a.vy += arvy;
+    // surface velocity: vs = vo + (-om*ry, om*rx), rel_v = v - vs
+    T arx = -om * arvy, ary = om * arvx;
+    T aspx = ca * arx + sa * ary, aspy = -sa * arx + ca * ary;
+    T alx = aspx, aly = aspy;
+    T as = -(aspx * nlx + aspy * nly) - a_ov;
+    T anlx = -s * aspx + (ca * anx + sa * any);
+    T anly = -s * aspy + (-sa * anx + ca * any);
+    if (face == 0) {
+        T aox = anlx / s, aoy = anly / s;
+        as += -(anlx * nlx + anly * nly) / s;
+        T h = as * T(0.5) / s;
+        aox += T(2) * ox * h;
+        aoy += T(2) * oy * h;
+        alx += aox - wclamp_g(lx, -hx, hx, aox);
+        aly += aoy - wclamp_g(ly, -hy, hy, aoy);
+    } else if (face == 1) {
+        alx += lx > T(0) ? as : -as;
+    } else {
+        aly += ly > T(0) ? as : -as;
+    }
+    a.px += ca * alx - sa * aly;
+    a.py += sa * alx + ca * aly;
+}
+
+// One obstacle on one agent (_obstacle_forces body, swarp/core/collisions.py:690-743).
+template <typename T>
+__device__ __forceinline__ void obstacle_force(const Cst<T> &C, const Obs<T> &O, size_t eN, int o,
+                                               T px, T py, T vx, T vy, T ra, T dd, T &fx, T &fy)
+{
+    fx = T(0);
+    fy = T(0);
+    const size_t j = eN + o;
+    const T cx = O.pos[2 * j], cy = O.pos[2 * j + 1];
+    const int st = O.type[o];
+    const T ro = O.rad[o], hx = O.half[2 * o], hy = O.half[2 * o + 1];
+    T bound = st == 1 ? m_sqrt(hx * hx + hy * hy) : (st == 2 ? hx + ro : ro);
+    T lim = (ra + C.margin + bound) * T(1.0001) + T(1.0e-6);
+    T ddx = px - cx, ddy = py - cy;
+    if (ddx * ddx + ddy * ddy > lim * lim) return;
+    const T vox = O.vel[2 * j], voy = O.vel[2 * j + 1], om = O.om[j], ang = O.ang[j];
+    if (st == 1) {
+        box_force(C, px, py, vx, vy, cx, cy, ang, hx, hy, ra + C.margin, dd, vox, voy, om, fx,
+                  fy);
+    } else if (st == 2) {
+        T ux = m_cos(ang), uy = m_sin(ang);
+        T t = wclamp((px - cx) * ux + (py - cy) * uy, -hx, hx);
+        T qx = cx + t * ux, qy = cy + t * uy;
+        T rx = qx - cx, ry = qy - cy;
+        pair_force(C, px - qx, py - qy, vx - (vox + -om * ry), vy - (voy + om * rx),
+                   ra + ro + C.margin, dd, fx, fy);
+    } else {
+        pair_force(C, px - cx, py - cy, vx - vox, vy - voy, ra + ro + C.margin, dd, fx, fy);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void obstacle_force_adj(const Cst<T> &C, const Obs<T> &O, size_t eN,
+                                                   int o, T px, T py, T vx, T vy, T ra, T dd,
+                                                   T gx, T gy, St<T> &a)
+{
+    const size_t j = eN + o;
+    const T cx = O.pos[2 * j], cy = O.pos[2 * j + 1];
+    const int st = O.type[o];
+    const T ro = O.rad[o], hx = O.half[2 * o], hy = O.half[2 * o + 1];
+    T bound = st == 1 ? m_sqrt(hx * hx + hy * hy) : (st == 2 ? hx + ro : ro);
+    T lim = (ra + C.margin + bound) * T(1.0001) + T(1.0e-6);
+    T ddx = px - cx, ddy = py - cy;
+    if (ddx * ddx + ddy * ddy > lim * lim) return;
+    const T vox = O.vel[2 * j], voy = O.vel[2 * j + 1], om = O.om[j], ang = O.ang[j];
+    if (st == 1) {
+        box_force_adj(C, px, py, vx, vy, cx, cy, ang, hx, hy, ra + C.margin, dd, vox, voy, om,
+                      gx, gy, a);
+    } else if (st == 2) {
+        T ux = m_cos(ang), uy = m_sin(ang);
+        T tr = (px - cx) * ux + (py - cy) * uy;
+        T t = wclamp(tr, -hx, hx);
+        T qx = cx + t * ux, qy = cy + t * uy;
+        T rx = qx - cx, ry = qy - cy;
+        T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
+        pair_force_adj(C, px - qx, py - qy, vx - (vox + -om * ry), vy - (voy + om * rx),
+                       ra + ro + C.margin, dd, gx, gy, adx, ady, arx, ary);
+        a.px += adx;
+        a.py += ady;
+        a.vx += arx;
+        a.vy += ary;
+        // closest point q(p): d = p - q, rel_v through the lever r = q - c
+        T aqx = -adx - om * ary;
+        T aqy = -ady + om * arx;
+        T atr = wclamp_g(tr, -hx, hx, aqx * ux + aqy * uy);
+        a.px += atr * ux;
+        a.py += atr * uy;
+    } else {
+        T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
+        pair_force_adj(C, px - cx, py - cy, vx - vox, vy - voy, ra + ro + C.margin, dd, gx, gy,
+                       adx, ady, arx, ary);
+        a.px += adx;
+        a.py += ady;
+        a.vx += arx;
+        a.vy += ary;
+    }
+}
+
+// ------------------------------------------------------------- integration
+
+// clamp_norm (swarp/dynamics/kernels.py:68-71)
+template <typename T>
+__device__ __forceinline__ void clamp_norm(T x, T y, T lim, T &ox, T &oy)
+{
+    T sc = lim / wmax(m_sqrt(x * x + y * y), lim);
+    ox = x * sc;
+    oy = y * sc;
+}
+
+template <typename T>
+__device__ __forceinline__ void clamp_norm_adj(T x, T y, T lim, T gx, T gy, T &ax, T &ay)
+{
+    T len = m_sqrt(x * x + y * y);
+    T m = wmax(len, lim);
+    T sc = lim / m;
+    T rx = gx * sc, ry = gy * sc;
+    if (len > lim) {
+        T am = -(gx * x + gy * y) * lim / (m * m);
+        rx += am * x / len;
+        ry += am * y / len;
+    }
+    ax += rx;
+    ay += ry;
+}
+
+// Semi-implicit Euler substep of one agent: _integrate_agent + _step_2d
+// (swarp/dynamics/kernels.py:194-413).  `o` receives the new state.
+template <typename T, bool DRONE>
+__device__ __forceinline__ void integrate(const Cst<T> &C, const Prm<T> &P, const St<T> &in,
+                                          const T (&a)[4], T Fx, T Fy, St<T> &o)
+{
+    const T dt = C.sub_dt;
+    const T dtm = dt / P.mass;
+    const T dvx = Fx * dtm, dvy = Fy * dtm;
+    o = in;
+    T pnx = in.px, pny = in.py;
+    if (DRONE && P.tag == 3) {
+        const T z0 = T(0);
+        T f0 = wclamp(a[0], z0, P.thrust_max), f1 = wclamp(a[1], z0, P.thrust_max);
+        T f2 = wclamp(a[2], z0, P.thrust_max), f3 = wclamp(a[3], z0, P.thrust_max);
+        T thr = f0 + f1 + f2 + f3;
+        // _quat_rotate_vec(q, (0,0,thrust)) written generically (kernels.py:108-114)
+        T vx3 = T(0), vy3 = T(0), vz3 = thr;
+        T c1x = in.qy * vz3 - in.qz * vy3, c1y = in.qz * vx3 - in.qx * vz3;
+        T c1z = in.qx * vy3 - in.qy * vx3;
+        T tx = T(2) * c1x, ty = T(2) * c1y, tz = T(2) * c1z;
+        T c2x = in.qy * tz - in.qz * ty, c2y = in.qz * tx - in.qx * tz, c2z = in.qx * ty - in.qy * tx;
+        T fwx = vx3 + in.qw * tx + c2x, fwy = vy3 + in.qw * ty + c2y, fwz = vz3 + in.qw * tz + c2z;
+        T accx = fwx / P.mass - z0, accy = fwy / P.mass - z0, accz = fwz / P.mass - P.gravity;
+        T tqx = P.arm * (f1 - f3), tqy = P.arm * (f2 - f0), tqz = P.kappa * (f0 - f1 + f2 - f3);
+        T nbx = in.bx + (tqx - (P.izz - P.iyy) * in.by * in.bz) / P.ixx * dt;
+        T nby = in.by + (tqy - (P.ixx - P.izz) * in.bz * in.bx) / P.iyy * dt;
+        T nbz = in.bz + (tqz - (P.iyy - P.ixx) * in.bx * in.by) / P.izz * dt;
+        T nvz = in.vz + accz * dt;
+        T vxx = in.vx + accx * dt + dvx, vxy = in.vy + accy * dt + dvy;
+        const T h = T(0.5);
+        T dqx = h * (in.qw * nbx + in.qy * nbz - in.qz * nby);
+        T dqy = h * (in.qw * nby - in.qx * nbz + in.qz * nbx);
+        T dqz = h * (in.qw * nbz + in.qx * nby - in.qy * nbx);
+        T dqw = h * (-in.qx * nbx - in.qy * nby - in.qz * nbz);
+        T ux = in.qx + dqx * dt, uy = in.qy + dqy * dt, uz = in.qz + dqz * dt, uw = in.qw + dqw * dt;
+        T l = m_sqrt(ux * ux + uy * uy + uz * uz + uw * uw);
+        if (l > T(0)) {
+            o.qx = ux / l; o.qy = uy / l; o.qz = uz / l; o.qw = uw / l;
+        } else {
+            o.qx = T(0); o.qy = T(0); o.qz = T(0); o.qw = T(1);
+        }
+        pnx = in.px + vxx * dt;
+        pny = in.py + vxy * dt;
+        o.z = in.z + nvz * dt;
+        o.vz = nvz;
+        o.bx = nbx; o.by = nby; o.bz = nbz;
+        o.vx = vxx; o.vy = vxy;
+    } else if (P.tag == 0) {
+        T vnx, vny;
+        if (P.mode == 0) {
+            clamp_norm(a[0], a[1], P.max_speed, vnx, vny);
+        } else {
+            T acx, acy;
+            clamp_norm(a[0], a[1], P.max_accel, acx, acy);
+            clamp_norm(in.vx + acx * dt, in.vy + acy * dt, P.max_speed, vnx, vny);
+        }
+        vnx = vnx + dvx;
+        vny = vny + dvy;
+        pnx = in.px + vnx * dt;
+        pny = in.py + vny * dt;
+        o.vx = vnx; o.vy = vny;
+        o.s = m_sqrt(vnx * vnx + vny * vny);
+        o.w = T(0);
+    } else if (P.tag == 1) {
+        T sn, wn;
+        if (P.mode == 0) {
+            sn = wclamp(a[0], -P.max_speed, P.max_speed);
+            wn = wclamp(a[1], -P.max_ang_vel, P.max_ang_vel);
+        } else {
+            T acc = wclamp(a[0], -P.max_accel, P.max_accel);
+            T alp = wclamp(a[1], -P.max_ang_accel, P.max_ang_accel);
+            sn = wclamp(in.s + acc * dt, -P.max_speed, P.max_speed);
+            wn = wclamp(in.w + alp * dt, -P.max_ang_vel, P.max_ang_vel);
+        }
+        T vtx = sn * m_cos(in.th) + dvx, vty = sn * m_sin(in.th) + dvy;
+        pnx = in.px + vtx * dt;
+        pny = in.py + vty * dt;
+        o.th = in.th + wn * dt;
+        o.vx = vtx; o.vy = vty;
+        o.s = sn;
+        o.w = wn;
+    } else if (P.tag == 2) {
+        T acc = wclamp(a[0], -P.max_accel, P.max_accel);
+        T del = wclamp(a[1], -P.max_steer, P.max_steer);
+        T sn = wclamp(in.s + acc * dt, P.min_speed, P.max_speed);
+        T wb = P.l_f + P.l_r;
+        T beta = m_atan(m_tan(del) * P.l_r / wb);
+        T vtx = sn * m_cos(in.th + beta) + dvx, vty = sn * m_sin(in.th + beta) + dvy;
+        T wn = sn / wb * m_cos(beta) * m_tan(del);
+        pnx = in.px + vtx * dt;
+        pny = in.py + vty * dt;
+        o.th = in.th + wn * dt;
+        o.vx = vtx; o.vy = vty;
+        o.s = sn;
+        o.w = wn;
+    }
+    if (C.clamp) {
+        pnx = wclamp(pnx, C.bmin_x + P.radius, C.bmax_x - P.radius);
+        pny = wclamp(pny, C.bmin_y + P.radius, C.bmax_y - P.radius);
+    }
+    o.px = pnx;
+    o.py = pny;
+}
+
+// Reverse of integrate.  g = adjoint of the substep output.  Overwrites gi with the
+// adjoint of the substep input, accumulates ga (actions) and returns gF (force).
+template <typename T, bool DRONE>
+__device__ __forceinline__ void integrate_adj(const Cst<T> &C, const Prm<T> &P, const St<T> &in,
+                                              const T (&a)[4], T Fx, T Fy, const St<T> &g,
+                                              St<T> &gi, T (&ga)[4], T &gFx, T &gFy)
+{
+    const T dt = C.sub_dt;
+    const T dtm = dt / P.mass;
+    const T dvx = Fx * dtm, dvy = Fy * dtm;
+    gi = g;  // default: every field passes through
+    T gpx = g.px, gpy = g.py;
+    gFx = T(0);
+    gFy = T(0);
+    if (DRONE && P.tag == 3) {
+        const T z0 = T(0);
+        T f0 = wclamp(a[0], z0, P.thrust_max), f1 = wclamp(a[1], z0, P.thrust_max);
+        T f2 = wclamp(a[2], z0, P.thrust_max), f3 = wclamp(a[3], z0, P.thrust_max);
+        T thr = f0 + f1 + f2 + f3;
+        T vx3 = T(0), vy3 = T(0), vz3 = thr;
+        T qx = in.qx, qy = in.qy, qz = in.qz, qw = in.qw;
+        T c1x = qy * vz3 - qz * vy3, c1y = qz * vx3 - qx * vz3, c1z = qx * vy3 - qy * vx3;
+        T tx = T(2) * c1x, ty = T(2) * c1y, tz = T(2) * c1z;
+        T accx = (vx3 + qw * tx + (qy * tz - qz * ty)) / P.mass;
+        T accy = (vy3 + qw * ty + (qz * tx - qx * tz)) / P.mass;
+        T accz = (vz3 + qw * tz + (qx * ty - qy * tx)) / P.mass - P.gravity;
+        T nbx = in.bx + (P.arm * (f1 - f3) - (P.izz - P.iyy) * in.by * in.bz) / P.ixx * dt;
+        T nby = in.by + (P.arm * (f2 - f0) - (P.ixx - P.izz) * in.bz * in.bx) / P.iyy * dt;
+        T nbz = in.bz + (P.kappa * (f0 - f1 + f2 - f3) - (P.iyy - P.ixx) * in.bx * in.by) / P.izz * dt;
+        const T h = T(0.5);
+        T ux = qx + h * (qw * nbx + qy * nbz - qz * nby) * dt;
+        T uy = qy + h * (qw * nby - qx * nbz + qz * nbx) * dt;
+        T uz = qz + h * (qw * nbz + qx * nby - qy * nbx) * dt;
+        T uw = qw + h * (-qx * nbx - qy * nby - qz * nbz) * dt;
+        T l = m_sqrt(ux * ux + uy * uy + uz * uz + uw * uw);
+        (void)accx; (void)accy; (void)accz;
+        if (C.clamp) {
+            T vxx = in.vx + accx * dt + dvx, vxy = in.vy + accy * dt + dvy;
+            gpx = wclamp_g(in.px + vxx * dt, C.bmin_x + P.radius, C.bmax_x - P.radius, gpx);
+            gpy = wclamp_g(in.py + vxy * dt, C.bmin_y + P.radius, C.bmax_y - P.radius, gpy);
+        }
+        gi.px = gpx;
+        gi.py = gpy;
+        T gvx = g.vx + gpx * dt, gvy = g.vy + gpy * dt;
+        gi.z = g.z;
+        T gnvz = g.vz + g.z * dt;
+        T gux = T(0), guy = T(0), guz = T(0), guw = T(0);
+        if (l > T(0)) {
+            T nx = ux / l, ny = uy / l, nz = uz / l, nw = uw / l;
+            T dq = g.qx * nx + g.qy * ny + g.qz * nz + g.qw * nw;
+            gux = (g.qx - nx * dq) / l;
+            guy = (g.qy - ny * dq) / l;
+            guz = (g.qz - nz * dq) / l;
+            guw = (g.qw - nw * dq) / l;
+        }
+        T gqx = gux, gqy = guy, gqz = guz, gqw = guw;
+        T Dx = h * gux * dt, Dy = h * guy * dt, Dz = h * guz * dt, Dw = h * guw * dt;
+        gqw += Dx * nbx + Dy * nby + Dz * nbz;
+        gqx += -Dy * nbz + Dz * nby - Dw * nbx;
+        gqy += Dx * nbz - Dz * nbx - Dw * nby;
+        gqz += -Dx * nby + Dy * nbx - Dw * nbz;
+        T gnbx = g.bx + Dx * qw + Dy * qz - Dz * qy - Dw * qx;
+        T gnby = g.by - Dx * qz + Dy * qw + Dz * qx - Dw * qy;
+        T gnbz = g.bz + Dx * qy - Dy * qx + Dz * qw - Dw * qz;
+        T gbx = gnbx, gby = gnby, gbz = gnbz;
+        T gtx = gnbx * dt / P.ixx, gty = gnby * dt / P.iyy, gtz = gnbz * dt / P.izz;
+        gby -= (P.izz - P.iyy) * in.bz * gtx;
+        gbz -= (P.izz - P.iyy) * in.by * gtx;
+        gbz -= (P.ixx - P.izz) * in.bx * gty;
+        gbx -= (P.ixx - P.izz) * in.bz * gty;
+        gbx -= (P.iyy - P.ixx) * in.by * gtz;
+        gby -= (P.iyy - P.ixx) * in.bx * gtz;
+        T gf0 = -P.arm * gty + P.kappa * gtz;
+        T gf1 = P.arm * gtx - P.kappa * gtz;
+        T gf2 = P.arm * gty + P.kappa * gtz;
+        T gf3 = -P.arm * gtx - P.kappa * gtz;
+        gi.vz = gnvz;
+        gi.vx = gvx;
+        gi.vy = gvy;
+        gFx = gvx * dtm;
+        gFy = gvy * dtm;
+        T gfx = gvx * dt / P.mass, gfy = gvy * dt / P.mass, gfz = gnvz * dt / P.mass;
+        gqw += gfx * tx + gfy * ty + gfz * tz;
+        T gtx2 = qw * gfx + (gfy * qz - gfz * qy);
+        T gty2 = qw * gfy + (gfz * qx - gfx * qz);
+        T gtz2 = qw * gfz + (gfx * qy - gfy * qx);
+        gqx += ty * gfz - tz * gfy;
+        gqy += tz * gfx - tx * gfz;
+        gqz += tx * gfy - ty * gfx;
+        T g1x = T(2) * gtx2, g1y = T(2) * gty2, g1z = T(2) * gtz2;
+        gqx += vy3 * g1z - vz3 * g1y;
+        gqy += vz3 * g1x - vx3 * g1z;
+        gqz += vx3 * g1y - vy3 * g1x;
+        T gthr = gfz + (g1x * qy - g1y * qx);
+        gf0 += gthr; gf1 += gthr; gf2 += gthr; gf3 += gthr;
+        ga[0] += wclamp_g(a[0], z0, P.thrust_max, gf0);
+        ga[1] += wclamp_g(a[1], z0, P.thrust_max, gf1);
+        ga[2] += wclamp_g(a[2], z0, P.thrust_max, gf2);
+        ga[3] += wclamp_g(a[3], z0, P.thrust_max, gf3);
+        gi.qx = gqx; gi.qy = gqy; gi.qz = gqz; gi.qw = gqw;
+        gi.bx = gbx; gi.by = gby; gi.bz = gbz;
+        return;
+    }
+    if (P.tag == 0) {
+        T vnx, vny, acx = T(0), acy = T(0), v0x = T(0), v0y = T(0);
+        if (P.mode == 0) {
+            clamp_norm(a[0], a[1], P.max_speed, vnx, vny);
+        } else {
+            clamp_norm(a[0], a[1], P.max_accel, acx, acy);
+            v0x = in.vx + acx * dt;
+            v0y = in.vy + acy * dt;
+            clamp_norm(v0x, v0y, P.max_speed, vnx, vny);
+        }
+        vnx = vnx + dvx;
+        vny = vny + dvy;
+        if (C.clamp) {
+            gpx = wclamp_g(in.px + vnx * dt, C.bmin_x + P.radius, C.bmax_x - P.radius, gpx);
+            gpy = wclamp_g(in.py + vny * dt, C.bmin_y + P.radius, C.bmax_y - P.radius, gpy);
+        }
+        T sp = m_sqrt(vnx * vnx + vny * vny);
+        gi.px = gpx;
+        gi.py = gpy;
+        gi.th = g.th;
+        gi.vx = T(0);
+        gi.vy = T(0);
+        gi.s = T(0);
+        gi.w = T(0);
+        T gvx = g.vx + gpx * dt, gvy = g.vy + gpy * dt;
+        if (sp > T(0)) {
+            gvx += g.s * vnx / sp;
+            gvy += g.s * vny / sp;
+        }
+        gFx = gvx * dtm;
+        gFy = gvy * dtm;
+        if (P.mode == 0) {
+            clamp_norm_adj(a[0], a[1], P.max_speed, gvx, gvy, ga[0], ga[1]);
+        } else {
+            T g0x = T(0), g0y = T(0);
+            clamp_norm_adj(v0x, v0y, P.max_speed, gvx, gvy, g0x, g0y);
+            gi.vx = g0x;
+            gi.vy = g0y;
+            clamp_norm_adj(a[0], a[1], P.max_accel, g0x * dt, g0y * dt, ga[0], ga[1]);
+        }
+    } else if (P.tag == 1) {
+        T sn, wn, acc = T(0), alp = T(0);
+        if (P.mode == 0) {
+            sn = wclamp(a[0], -P.max_speed, P.max_speed);
+            wn = wclamp(a[1], -P.max_ang_vel, P.max_ang_vel);
+        } else {
+            acc = wclamp(a[0], -P.max_accel, P.max_accel);
+            alp = wclamp(a[1], -P.max_ang_accel, P.max_ang_accel);
+            sn = wclamp(in.s + acc * dt, -P.max_speed, P.max_speed);
+            wn = wclamp(in.w + alp * dt, -P.max_ang_vel, P.max_ang_vel);
+        }
+        T c = m_cos(in.th), sg = m_sin(in.th);
+        if (C.clamp) {
+            gpx = wclamp_g(in.px + (sn * c + dvx) * dt, C.bmin_x + P.radius, C.bmax_x - P.radius, gpx);
+            gpy = wclamp_g(in.py + (sn * sg + dvy) * dt, C.bmin_y + P.radius, C.bmax_y - P.radius, gpy);
+        }
+        gi.px = gpx;
+        gi.py = gpy;
+        T gvx = g.vx + gpx * dt, gvy = g.vy + gpy * dt;
+        T gwn = g.w + g.th * dt;
+        gFx = gvx * dtm;
+        gFy = gvy * dtm;
+        T gsn = g.s + gvx * c + gvy * sg;
+        gi.th = g.th + (gvx * sn * -sg + gvy * sn * c);
+        gi.vx = T(0);
+        gi.vy = T(0);
+        gi.s = T(0);
+        gi.w = T(0);
+        if (P.mode == 0) {
+            ga[0] += wclamp_g(a[0], -P.max_speed, P.max_speed, gsn);
+            ga[1] += wclamp_g(a[1], -P.max_ang_vel, P.max_ang_vel, gwn);
+        } else {
+            T gx = wclamp_g(in.s + acc * dt, -P.max_speed, P.max_speed, gsn);
+            T gy = wclamp_g(in.w + alp * dt, -P.max_ang_vel, P.max_ang_vel, gwn);
+            gi.s = gx;
+            gi.w = gy;
+            ga[0] += wclamp_g(a[0], -P.max_accel, P.max_accel, gx * dt);
+            ga[1] += wclamp_g(a[1], -P.max_ang_accel, P.max_ang_accel, gy * dt);
+        }
+    } else if (P.tag == 2) {
+        T acc = wclamp(a[0], -P.max_accel, P.max_accel);
+        T del = wclamp(a[1], -P.max_steer, P.max_steer);
+        T sn = wclamp(in.s + acc * dt, P.min_speed, P.max_speed);
+        T wb = P.l_f + P.l_r;
+        T td = m_tan(del);
+        T bu = td * P.l_r / wb;
+        T beta = m_atan(bu);
+        T ang = in.th + beta;
+        T ca = m_cos(ang), sa = m_sin(ang), cb = m_cos(beta);
+        if (C.clamp) {
+            gpx = wclamp_g(in.px + (sn * ca + dvx) * dt, C.bmin_x + P.radius, C.bmax_x - P.radius, gpx);
+            gpy = wclamp_g(in.py + (sn * sa + dvy) * dt, C.bmin_y + P.radius, C.bmax_y - P.radius, gpy);
+        }
+        gi.px = gpx;
+        gi.py = gpy;
+        T gvx = g.vx + gpx * dt, gvy = g.vy + gpy * dt;
+        T gwn = g.w + g.th * dt;
+        gFx = gvx * dtm;
+        gFy = gvy * dtm;
+        T gsn = g.s + gvx * ca + gvy * sa + gwn * cb * td / wb;
+        T gang = -gvx * sn * sa + gvy * sn * ca;
+        T gbeta = gang - gwn * (sn / wb) * m_sin(beta) * td;
+        T gtd = gwn * (sn / wb) * cb + gbeta / (T(1) + bu * bu) * P.l_r / wb;
+        gi.th = g.th + gang;
+        gi.vx = T(0);
+        gi.vy = T(0);
+        gi.w = T(0);
+        T gx = wclamp_g(in.s + acc * dt, P.min_speed, P.max_speed, gsn);
+        gi.s = gx;
+        ga[0] += wclamp_g(a[0], -P.max_accel, P.max_accel, gx * dt);
+        ga[1] += wclamp_g(a[1], -P.max_steer, P.max_steer, gtd * (T(1) + td * td));
+    }
+}
+
+}  // namespace swarp

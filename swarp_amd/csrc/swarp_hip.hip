@@ -1,0 +1,876 @@
+// swarp_hip.hip -- gfx950 kernels and C ABI of the swarp physics step (include/swarp_hip.h).
+//
+// Execution model
+//   * One lane per (env, agent).  An env occupies PA consecutive lanes of a wave64
+//     (PA = next power of two >= n_agents, <= 64), so an env never spans waves and
+//     every exchange between its agents stays inside one wave: positions, velocities,
+//     neighbour masks and force adjoints go through a small LDS staging area.
+//   * Workgroup = one wave (64 lanes), so the workgroup barrier costs nothing and
+//     envs are spread over the whole chip at wave granularity.
+//   * One launch runs a whole T-step rollout: the state stays in registers between
+//     steps; HBM sees the actions in and each step's output state (the checkpoint).
+//   * The backward launch walks t = T-1..0, reloads each step's input checkpoint,
+//     recomputes that step's substeps into LDS, then runs the reverse pass.  The force
+//     adjoint of a pair is gathered by both agents from the same recomputed pair, in
+//     ascending neighbour order: deterministic, no atomics.
+//   * Neighbour membership uses the exact threshold test d2 <= t_nbr, where t_nbr is
+//     the largest value whose correctly rounded square root is <= the radius, which
+//     is bit-identical to the reference's sqrt(d2) <= radius (neighbors.py:91).
+//     Within a step, substeps after the first scan only a skin list built at substep 0;
+//     a per-env displacement bound proves the skin list complete, and an env whose
+//     agents moved too far rescans all pairs.  Both give the same lists.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "physics.hpp"
+#include "swarp_hip.h"
+
+namespace swarp {
+
+template <int PA> struct MaskT { typedef uint32_t type; };
+template <> struct MaskT<64> { typedef uint64_t type; };
+
+__device__ __forceinline__ int m_ctz(uint32_t m) { return __builtin_ctz(m); }
+__device__ __forceinline__ int m_ctz(uint64_t m) { return __builtin_ctzll(m); }
+__device__ __forceinline__ int m_popc(uint32_t m) { return __builtin_popcount(m); }
+__device__ __forceinline__ int m_popc(uint64_t m) { return __builtin_popcountll(m); }
+
+// Field pointers of one state; strides (in scalars) 2,1,2,1,1,1,1,4,3.
+template <typename T> struct Fields {
+    T *f[9];
+};
+template <typename T> struct CFields {
+    const T *f[9];
+};
+
+template <typename T> struct Args {
+    const T *params;
+    const int32_t *tag, *mode;
+    Obs<T> obs;
+    CFields<T> s0;       // rollout input state
+    const T *act;        // [T,E,A,ad]
+    Fields<T> traj;      // outputs of steps 0..T-2 (stride E*A per step)
+    Fields<T> fin;       // output of step T-1
+    CFields<T> atraj;    // adjoints arriving at traj (nullable per field)
+    CFields<T> afin;     // adjoint arriving at fin (nullable per field)
+    Fields<T> a0;        // adjoint of s0 (nullable per field)
+    T *aact;             // adjoint of actions
+    int nsteps;
+};
+
+__device__ __forceinline__ int fstride(int k)
+{
+    // pos theta vel speed ang_vel z vz attitude body_rates
+    return k == 0 || k == 2 ? 2 : (k == 7 ? 4 : (k == 8 ? 3 : 1));
+}
+
+template <typename T, bool DRONE>
+__device__ __forceinline__ void load_state(const T *const *f, size_t i, size_t off, St<T> &s)
+{
+    // `off` = element offset of the state in the trajectory (step * E * A)
+    const size_t j = i + off;
+    s.px = f[0][2 * j]; s.py = f[0][2 * j + 1];
+    s.th = f[1][j];
+    s.vx = f[2][2 * j]; s.vy = f[2][2 * j + 1];
+    s.s = f[3][j];
+    s.w = f[4][j];
+    if (DRONE) {
+        s.z = f[5][j]; s.vz = f[6][j];
+        s.qx = f[7][4 * j]; s.qy = f[7][4 * j + 1]; s.qz = f[7][4 * j + 2]; s.qw = f[7][4 * j + 3];
+        s.bx = f[8][3 * j]; s.by = f[8][3 * j + 1]; s.bz = f[8][3 * j + 2];
+    } else {
+        s.z = s.vz = s.qx = s.qy = s.qz = s.bx = s.by = s.bz = T(0);
+        s.qw = T(1);
+    }
+}
+
+template <typename T, bool DRONE>
+__device__ __forceinline__ void store_state(T *const *f, size_t j, const St<T> &s)
+{
+    f[0][2 * j] = s.px; f[0][2 * j + 1] = s.py;
+    f[1][j] = s.th;
+    f[2][2 * j] = s.vx; f[2][2 * j + 1] = s.vy;
+    f[3][j] = s.s;
+    f[4][j] = s.w;
+    if (DRONE) {
+        f[5][j] = s.z; f[6][j] = s.vz;
+        f[7][4 * j] = s.qx; f[7][4 * j + 1] = s.qy; f[7][4 * j + 2] = s.qz; f[7][4 * j + 3] = s.qw;
+        f[8][3 * j] = s.bx; f[8][3 * j + 1] = s.by; f[8][3 * j + 2] = s.bz;
+    }
+}
+
+// Adds a nullable adjoint state (fields may be NULL) at element j.
+template <typename T, bool DRONE>
+__device__ __forceinline__ void add_adj(const T *const *f, size_t j, St<T> &g)
+{
+    if (f[0]) { g.px += f[0][2 * j]; g.py += f[0][2 * j + 1]; }
+    if (f[1]) g.th += f[1][j];
+    if (f[2]) { g.vx += f[2][2 * j]; g.vy += f[2][2 * j + 1]; }
+    if (f[3]) g.s += f[3][j];
+    if (f[4]) g.w += f[4][j];
+    if (DRONE) {
+        if (f[5]) g.z += f[5][j];
+        if (f[6]) g.vz += f[6][j];
+        if (f[7]) { g.qx += f[7][4 * j]; g.qy += f[7][4 * j + 1]; g.qz += f[7][4 * j + 2]; g.qw += f[7][4 * j + 3]; }
+        if (f[8]) { g.bx += f[8][3 * j]; g.by += f[8][3 * j + 1]; g.bz += f[8][3 * j + 2]; }
+    }
+}
+
+template <typename T, bool DRONE>
+__device__ __forceinline__ void store_adj(T *const *f, size_t j, const St<T> &g)
+{
+    if (f[0]) { f[0][2 * j] = g.px; f[0][2 * j + 1] = g.py; }
+    if (f[1]) f[1][j] = g.th;
+    if (f[2]) { f[2][2 * j] = g.vx; f[2][2 * j + 1] = g.vy; }
+    if (f[3]) f[3][j] = g.s;
+    if (f[4]) f[4][j] = g.w;
+    if (DRONE) {
+        if (f[5]) f[5][j] = g.z;
+        if (f[6]) f[6][j] = g.vz;
+        if (f[7]) { f[7][4 * j] = g.qx; f[7][4 * j + 1] = g.qy; f[7][4 * j + 2] = g.qz; f[7][4 * j + 3] = g.qw; }
+        if (f[8]) { f[8][3 * j] = g.bx; f[8][3 * j + 1] = g.by; f[8][3 * j + 2] = g.bz; }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void load_prm(const Args<T> &g, int a, Prm<T> &p)
+{
+    const T *r = g.params + a * 22;
+    p.radius = r[0]; p.mass = r[1]; p.max_speed = r[2]; p.max_accel = r[3];
+    p.max_ang_vel = r[4]; p.max_ang_accel = r[5]; p.l_f = r[6]; p.l_r = r[7];
+    p.max_steer = r[8]; p.thrust_max = r[9]; p.arm = r[10]; p.ixx = r[11];
+    p.iyy = r[12]; p.izz = r[13]; p.kappa = r[14]; p.gravity = r[15]; p.min_speed = r[16];
+    p.tag = g.tag[a];
+    p.mode = g.mode[a];
+}
+
+template <typename T>
+__device__ __forceinline__ void load_act(const T *act, size_t j, int ad, T (&a)[4])
+{
+    const T *p = act + j * ad;
+    a[0] = p[0];
+    a[1] = ad > 1 ? p[1] : T(0);
+    a[2] = ad > 2 ? p[2] : T(0);
+    a[3] = ad > 3 ? p[3] : T(0);
+}
+
+// LDS staging of one substep.  Fields: 0 px, 1 py, 2 vx, 3 vy, 4 th, 5 s, 6 w, 7 Fx, 8 Fy,
+// then (drone) 9 z, 10 vz, 11..14 q, 15..17 br.  Each field is 64 consecutive scalars.
+constexpr int F_PX = 0, F_PY = 1, F_VX = 2, F_VY = 3, F_TH = 4, F_S = 5, F_W = 6, F_FX = 7,
+              F_FY = 8, NF_2D = 9, NF_DRONE = 18;
+
+// Neighbour lists of one agent as a bitmask over the env's agents, ascending bit =
+// ascending list order (neighbors.py:90-96).  Full scan over every pair of the env.
+template <typename T, int PA>
+__device__ __forceinline__ typename MaskT<PA>::type scan_all(const T *lx, const T *ly, int base,
+                                                             int A, int me, T px, T py, T t_nbr,
+                                                             T t_skin,
+                                                             typename MaskT<PA>::type &cand)
+{
+    typedef typename MaskT<PA>::type M;
+    M incl = 0, cd = 0;
+#pragma unroll
+    for (int b = 0; b < PA; ++b) {
+        if (b < A) {
+            T dx = lx[base + b] - px, dy = ly[base + b] - py;
+            T d2 = dx * dx + dy * dy;
+            incl |= d2 <= t_nbr ? (M(1) << b) : M(0);
+            cd |= d2 <= t_skin ? (M(1) << b) : M(0);
+        }
+    }
+    const M self = ~(M(1) << me);
+    cand = cd & self;
+    return incl & self;
+}
+
+// Same membership, evaluated only on the skin candidates.
+template <typename T, int PA>
+__device__ __forceinline__ typename MaskT<PA>::type scan_cand(const T *lx, const T *ly, int base,
+                                                              T px, T py, T t_nbr,
+                                                              typename MaskT<PA>::type cand)
+{
+    typedef typename MaskT<PA>::type M;
+    M incl = 0;
+    while (cand) {
+        const int b = m_ctz(cand);
+        cand &= cand - 1;
+        T dx = lx[base + b] - px, dy = ly[base + b] - py;
+        T d2 = dx * dx + dy * dy;
+        incl |= d2 <= t_nbr ? (M(1) << b) : M(0);
+    }
+    return incl;
+}
+
+// First K members of an inclusion mask (the padded list of length K).
+template <typename M> __device__ __forceinline__ M cap_list(M incl, int K)
+{
+    if (m_popc(incl) <= K) return incl;
+    M rest = incl;
+    for (int i = 0; i < K; ++i) rest &= rest - 1;
+    return incl ^ rest;
+}
+
+// Per-lane context shared by the forward and backward kernels.
+template <typename T, int PA> struct Lane {
+    int lane, agent, base, env;
+    bool real;     // agent < A (lane holds a real agent slot of its env)
+    bool active;   // real and env < E
+    size_t idx;    // env * A + agent (clamped to a valid element for inactive lanes)
+    Prm<T> pr;
+    T dd;          // implicit damping denominator 1 + c*sub_dt/m (collisions.py:845)
+};
+
+template <typename T, int PA>
+__device__ __forceinline__ void lane_init(const Cst<T> &C, const Args<T> &g, Lane<T, PA> &L)
+{
+    constexpr int EPW = 64 / PA;
+    L.lane = threadIdx.x;
+    L.agent = L.lane % PA;
+    L.base = L.lane - L.agent;
+    L.env = blockIdx.x * EPW + L.lane / PA;
+    L.real = L.agent < C.A;
+    L.active = L.real && L.env < C.E;
+    const int ag = L.real ? L.agent : 0;
+    const int ev = L.env < C.E ? L.env : 0;
+    L.idx = (size_t)ev * C.A + ag;
+    load_prm(g, ag, L.pr);
+    L.dd = T(1) + C.c * C.sub_dt / L.pr.mass;
+}
+
+// Whether every real agent of this lane's env stayed within the skin budget.
+template <int PA> __device__ __forceinline__ bool env_all(bool ok, int base)
+{
+    const uint64_t bal = __ballot(ok);
+    const uint64_t full = PA == 64 ? ~0ull : ((1ull << PA) - 1ull);
+    return ((bal >> base) & full) == full;
+}
+
+// Contact + static forces of one substep, reading the env's positions/velocities from
+// the LDS slot `sl`.  Returns the uncapped inclusion mask (for the true count).
+template <typename T, int PA>
+__device__ __forceinline__ typename MaskT<PA>::type forces(
+    const Cst<T> &C, const Args<T> &g, const Lane<T, PA> &L, const T *sl, const T *lr,
+    const St<T> &st, int s, bool full, typename MaskT<PA>::type &cand, T &Fx, T &Fy)
+{
+    typedef typename MaskT<PA>::type M;
+    const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64, *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
+    M incl = 0;
+    T fx = T(0), fy = T(0);
+    if (C.collisions) {
+        if (full) {
+            M cd;
+            incl = scan_all<T, PA>(lx, ly, L.base, C.A, L.agent, st.px, st.py, C.t_nbr, C.t_skin, cd);
+            if (s == 0) cand = cd;
+        } else {
+            incl = scan_cand<T, PA>(lx, ly, L.base, st.px, st.py, C.t_nbr, cand);
+        }
+        M m = cap_list(incl, C.K);
+        const T ra = L.pr.radius;
+        while (m) {
+            const int b = m_ctz(m);
+            m &= m - 1;
+            const int j = L.base + b;
+            T gx, gy;
+            pair_force(C, st.px - lx[j], st.py - ly[j], st.vx - lvx[j], st.vy - lvy[j],
+                       ra + lr[j] + C.margin, L.dd, gx, gy);
+            fx += gx;
+            fy += gy;
+        }
+    }
+    T sx = T(0), sy = T(0);
+    if (C.N > 0) {
+        const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
+        for (int o = 0; o < C.N; ++o) {
+            T gx, gy;
+            obstacle_force(C, g.obs, eN, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.dd, gx, gy);
+            sx += gx;
+            sy += gy;
+        }
+    }
+    if (C.soft_walls) {
+        T gx, gy;
+        wall_force(C, st.px, st.py, st.vx, st.vy, L.pr.radius, L.dd, gx, gy);
+        sx += gx;
+        sy += gy;
+    }
+    Fx = fx + sx;
+    Fy = fy + sy;
+    return incl;
+}
+
+// ------------------------------------------------------------------ forward rollout
+
+template <typename T, int PA, bool DRONE>
+__global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> C, const Args<T> g)
+{
+    typedef typename MaskT<PA>::type M;
+    __shared__ T sl[4 * 64];  // px py vx vy of the current substep
+    __shared__ T lr[64];      // agent radius per lane
+    Lane<T, PA> L;
+    lane_init<T, PA>(C, g, L);
+    lr[L.lane] = L.pr.radius;
+    St<T> st;
+    load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
+    const size_t EA = (size_t)C.E * C.A;
+    for (int t = 0; t < g.nsteps; ++t) {
+        T a[4];
+        load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
+        M cand = 0;
+        T D = T(0);
+        bool ok = false;
+        for (int s = 0; s < C.S; ++s) {
+            T Fx = T(0), Fy = T(0);
+            if (C.needs_forces) {
+                if (C.collisions) {
+                    __syncthreads();
+                    sl[F_PX * 64 + L.lane] = st.px;
+                    sl[F_PY * 64 + L.lane] = st.py;
+                    sl[F_VX * 64 + L.lane] = st.vx;
+                    sl[F_VY * 64 + L.lane] = st.vy;
+                    __syncthreads();
+                }
+                forces<T, PA>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy);
+            }
+            St<T> nx;
+            integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
+            if (C.use_skin) {
+                D += (m_abs(nx.px - st.px) + m_abs(nx.py - st.py)) * T(1.0001);
+                ok = env_all<PA>(!L.real || D <= C.half_margin, L.base);
+            }
+            st = nx;
+        }
+        if (L.active) {
+            if (t + 1 < g.nsteps)
+                store_state<T, DRONE>(g.traj.f, (size_t)t * EA + L.idx, st);
+            else
+                store_state<T, DRONE>(g.fin.f, L.idx, st);
+        }
+    }
+}
+
+// ----------------------------------------------------------------- backward rollout
+
+template <typename T, bool DRONE>
+__device__ __forceinline__ void slot_put(T *sl, int lane, const St<T> &s)
+{
+    sl[F_PX * 64 + lane] = s.px; sl[F_PY * 64 + lane] = s.py;
+    sl[F_VX * 64 + lane] = s.vx; sl[F_VY * 64 + lane] = s.vy;
+    sl[F_TH * 64 + lane] = s.th; sl[F_S * 64 + lane] = s.s; sl[F_W * 64 + lane] = s.w;
+    if (DRONE) {
+        sl[9 * 64 + lane] = s.z; sl[10 * 64 + lane] = s.vz;
+        sl[11 * 64 + lane] = s.qx; sl[12 * 64 + lane] = s.qy;
+        sl[13 * 64 + lane] = s.qz; sl[14 * 64 + lane] = s.qw;
+        sl[15 * 64 + lane] = s.bx; sl[16 * 64 + lane] = s.by; sl[17 * 64 + lane] = s.bz;
+    }
+}
+
+template <typename T, bool DRONE>
+__device__ __forceinline__ void slot_get(const T *sl, int lane, St<T> &s)
+{
+    s.px = sl[F_PX * 64 + lane]; s.py = sl[F_PY * 64 + lane];
+    s.vx = sl[F_VX * 64 + lane]; s.vy = sl[F_VY * 64 + lane];
+    s.th = sl[F_TH * 64 + lane]; s.s = sl[F_S * 64 + lane]; s.w = sl[F_W * 64 + lane];
+    if (DRONE) {
+        s.z = sl[9 * 64 + lane]; s.vz = sl[10 * 64 + lane];
+        s.qx = sl[11 * 64 + lane]; s.qy = sl[12 * 64 + lane];
+        s.qz = sl[13 * 64 + lane]; s.qw = sl[14 * 64 + lane];
+        s.bx = sl[15 * 64 + lane]; s.by = sl[16 * 64 + lane]; s.bz = sl[17 * 64 + lane];
+    } else {
+        s.z = s.vz = s.qx = s.qy = s.qz = s.bx = s.by = s.bz = T(0);
+        s.qw = T(1);
+    }
+}
+
+// Whether agent `me` is among the first K members of inclusion mask `incl`.
+template <typename M> __device__ __forceinline__ bool in_list(M incl, int me, int K)
+{
+    return ((incl >> me) & M(1)) && m_popc(incl & ((M(1) << me) - M(1))) < K;
+}
+
+template <typename T, int PA, bool DRONE>
+__global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T> g)
+{
+    typedef typename MaskT<PA>::type M;
+    constexpr int NF = DRONE ? NF_DRONE : NF_2D;
+    extern __shared__ __align__(16) unsigned char smem[];
+    T *lr = (T *)smem;          // radius per lane
+    T *ldd = lr + 64;           // damping denominator per lane
+    T *slots = ldd + 64;        // S slots of NF fields
+    M *lmask = (M *)(slots + (size_t)C.S * NF * 64);  // S inclusion masks per lane
+    Lane<T, PA> L;
+    lane_init<T, PA>(C, g, L);
+    lr[L.lane] = L.pr.radius;
+    ldd[L.lane] = L.dd;
+    const size_t EA = (size_t)C.E * C.A;
+    St<T> gs;  // adjoint of the current step's output
+    st_zero(gs);
+    for (int t = g.nsteps - 1; t >= 0; --t) {
+        if (t == g.nsteps - 1)
+            add_adj<T, DRONE>(g.afin.f, L.idx, gs);
+        else
+            add_adj<T, DRONE>(g.atraj.f, (size_t)t * EA + L.idx, gs);
+        St<T> st;
+        if (t == 0)
+            load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
+        else
+            load_state<T, DRONE>(g.traj.f, L.idx, (size_t)(t - 1) * EA, st);
+        T a[4];
+        load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
+
+        // ---- recompute the substep chain of this step into LDS
+        M cand = 0;
+        T D = T(0);
+        bool ok = false;
+        for (int s = 0; s < C.S; ++s) {
+            T *sl = slots + (size_t)s * NF * 64;
+            __syncthreads();
+            slot_put<T, DRONE>(sl, L.lane, st);
+            __syncthreads();
+            T Fx = T(0), Fy = T(0);
+            M incl = 0;
+            if (C.needs_forces)
+                incl = forces<T, PA>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy);
+            sl[F_FX * 64 + L.lane] = Fx;
+            sl[F_FY * 64 + L.lane] = Fy;
+            lmask[s * 64 + L.lane] = incl;
+            St<T> nx;
+            integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
+            if (C.use_skin) {
+                D += (m_abs(nx.px - st.px) + m_abs(nx.py - st.py)) * T(1.0001);
+                ok = env_all<PA>(!L.real || D <= C.half_margin, L.base);
+            }
+            st = nx;
+        }
+
+        // ---- reverse pass
+        T ga[4] = {T(0), T(0), T(0), T(0)};
+        for (int s = C.S - 1; s >= 0; --s) {
+            T *sl = slots + (size_t)s * NF * 64;
+            __syncthreads();
+            St<T> in;
+            slot_get<T, DRONE>(sl, L.lane, in);
+            const T Fx = sl[F_FX * 64 + L.lane], Fy = sl[F_FY * 64 + L.lane];
+            St<T> gi;
+            T gFx, gFy;
+            integrate_adj<T, DRONE>(C, L.pr, in, a, Fx, Fy, gs, gi, ga, gFx, gFy);
+            if (C.needs_forces) {
+                __syncthreads();
+                sl[F_FX * 64 + L.lane] = gFx;  // the slot now carries the force adjoint
+                sl[F_FY * 64 + L.lane] = gFy;
+                __syncthreads();
+                if (C.collisions) {
+                    const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64;
+                    const T *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
+                    const T *lgx = sl + F_FX * 64, *lgy = sl + F_FY * 64;
+                    const M mine = lmask[s * 64 + L.lane];
+                    M m = mine;
+                    while (m) {
+                        const int b = m_ctz(m);
+                        m &= m - 1;
+                        const int j = L.base + b;
+                        const T md = L.pr.radius + lr[j] + C.margin;
+                        if (in_list(mine, b, C.K)) {  // b in my list: d = me - b
+                            T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
+                            pair_force_adj(C, in.px - lx[j], in.py - ly[j], in.vx - lvx[j],
+                                           in.vy - lvy[j], md, L.dd, gFx, gFy, adx, ady, arx, ary);
+                            gi.px += adx; gi.py += ady; gi.vx += arx; gi.vy += ary;
+                        }
+                        if (in_list(lmask[s * 64 + j], L.agent, C.K)) {  // me in b's list
+                            T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
+                            pair_force_adj(C, lx[j] - in.px, ly[j] - in.py, lvx[j] - in.vx,
+                                           lvy[j] - in.vy, lr[j] + L.pr.radius + C.margin, ldd[j],
+                                           lgx[j], lgy[j], adx, ady, arx, ary);
+                            gi.px -= adx; gi.py -= ady; gi.vx -= arx; gi.vy -= ary;
+                        }
+                    }
+                }
+                if (C.N > 0) {
+                    const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
+                    for (int o = 0; o < C.N; ++o)
+                        obstacle_force_adj(C, g.obs, eN, o, in.px, in.py, in.vx, in.vy,
+                                           L.pr.radius, L.dd, gFx, gFy, gi);
+                }
+                if (C.soft_walls)
+                    wall_force_adj(C, in.px, in.py, in.vx, in.vy, L.pr.radius, L.dd, gFx, gFy, gi);
+            }
+            gs = gi;
+        }
+        if (L.active) {
+            T *pa = g.aact + ((size_t)t * EA + L.idx) * C.ad;
+            for (int k = 0; k < C.ad; ++k) pa[k] = k < 4 ? ga[k] : T(0);
+        }
+    }
+    if (L.active) store_adj<T, DRONE>(g.a0.f, L.idx, gs);
+}
+
+// --------------------------------------------------------------- neighbour lists
+
+template <typename T, int PA>
+__global__ __launch_bounds__(64) void k_neighbors(const Cst<T> C, const T *pos, int32_t *idx,
+                                                  int32_t *cnt, int32_t *tru)
+{
+    typedef typename MaskT<PA>::type M;
+    constexpr int EPW = 64 / PA;
+    __shared__ T lx[64], ly[64];
+    const int lane = threadIdx.x, agent = lane % PA, base = lane - agent;
+    const int env = blockIdx.x * EPW + lane / PA;
+    const bool active = agent < C.A && env < C.E;
+    const size_t i = active ? (size_t)env * C.A + agent : 0;
+    const T px = pos[2 * i], py = pos[2 * i + 1];
+    lx[lane] = px;
+    ly[lane] = py;
+    __syncthreads();
+    M cd;
+    const M incl = scan_all<T, PA>(lx, ly, base, C.A, agent, px, py, C.t_nbr, C.t_nbr, cd);
+    if (!active) return;
+    M m = cap_list(incl, C.K);
+    const int n = m_popc(m);
+    int32_t *row = idx + i * C.K;
+    for (int k = 0; k < C.K; ++k) {
+        int v = 0;
+        if (k < n) {
+            v = m_ctz(m);
+            m &= m - 1;
+        }
+        row[k] = v;
+    }
+    cnt[i] = n;
+    if (tru) tru[i] = m_popc(incl);
+}
+
+__global__ void k_edge_index(int E, int A, int K, const int32_t *idx, const int32_t *cnt,
+                             const int64_t *off, int64_t n_edges, int64_t *out)
+{
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)E * A) return;
+    const int64_t e = (int64_t)(i / A);
+    const int64_t n = cnt[i];
+    const int64_t o = off[i];
+    for (int64_t s = 0; s < n && o + s < n_edges; ++s) {
+        out[o + s] = e * A + idx[i * K + s];
+        out[n_edges + o + s] = (int64_t)i;
+    }
+}
+
+}  // namespace swarp
+
+// ====================================================================== host side
+
+using namespace swarp;
+
+static thread_local char g_err[512];
+
+static int fail(const char *msg)
+{
+    snprintf(g_err, sizeof g_err, "%s", msg);
+    return -1;
+}
+
+static float h_sqrt(float x) { return sqrtf(x); }
+static double h_sqrt(double x) { return sqrt(x); }
+static float h_next(float x, float to) { return nextafterf(x, to); }
+static double h_next(double x, double to) { return nextafter(x, to); }
+
+// Largest x with fl(sqrt(x)) <= r: the exact replacement of sqrt(d2) <= r.  The host's
+// sqrt is IEEE correctly rounded, like the device's, so the two tests agree bit for bit.
+template <typename T> static T exact_threshold(double radius)
+{
+    const T r = (T)radius;
+    if (r != r || r < T(0)) return (T)-INFINITY;
+    if (isinf(r)) return (T)INFINITY;
+    T t = r * r;
+    for (;;) {
+        T nx = h_next(t, (T)INFINITY);
+        if (isinf(nx) || !(h_sqrt(nx) <= r)) break;
+        t = nx;
+    }
+    while (t > T(0) && h_sqrt(t) > r) t = h_next(t, (T)-INFINITY);
+    return t;
+}
+
+template <typename T> static int fill_cst(const swarp_desc_t *d, double skin, Cst<T> &C)
+{
+    memset(&C, 0, sizeof C);
+    C.k = (T)d->k;
+    C.c = (T)d->c;
+    C.margin = (T)d->margin;
+    C.sub_dt = (T)(d->dt / d->substeps);
+    C.max_overlap = (T)d->max_overlap;
+    C.eps2 = (T)1.0e-10;
+    C.t_nbr = exact_threshold<T>(d->neighbor_radius);
+    const double r = (double)(T)d->neighbor_radius;
+    const double rs = r + (skin > 0.0 ? skin : 0.0);
+    T ts = (T)(rs * rs);
+    if (ts < C.t_nbr) ts = C.t_nbr;
+    C.t_skin = ts;
+    C.half_margin = (T)(0.5 * (sqrt((double)ts) - sqrt((double)C.t_nbr)) * (1.0 - 1e-3));
+    if (C.half_margin < T(0)) C.half_margin = T(0);
+    C.bmin_x = (T)d->bounds_min[0];
+    C.bmin_y = (T)d->bounds_min[1];
+    C.bmax_x = (T)d->bounds_max[0];
+    C.bmax_y = (T)d->bounds_max[1];
+    C.E = d->n_envs;
+    C.A = d->n_agents;
+    C.ad = d->act_dim;
+    C.S = d->substeps;
+    C.K = d->max_neighbors;
+    C.N = d->n_obstacles;
+    C.collisions = d->collisions;
+    C.soft_walls = d->soft_walls;
+    C.clamp = d->clamp_bounds;
+    C.needs_forces = (d->collisions || d->soft_walls || d->n_obstacles > 0) ? 1 : 0;
+    C.use_skin = (d->collisions && d->substeps > 1 && skin > 0.0) ? 1 : 0;
+    return 0;
+}
+
+static int check_desc(const swarp_desc_t *d, bool need_params = true)
+{
+    if (!d) return fail("desc is NULL");
+    if (d->abi_version != SWARP_ABI_VERSION) return fail("desc->abi_version mismatch");
+    if (d->dtype != SWARP_F32 && d->dtype != SWARP_F64) return fail("desc->dtype must be SWARP_F32 or SWARP_F64");
+    if (d->n_envs < 1) return fail("n_envs must be >= 1");
+    if (d->n_agents < 1 || d->n_agents > 64) return fail("n_agents must lie in [1, 64] in this build");
+    if (d->act_dim < 1) return fail("act_dim must be >= 1");
+    if (d->substeps < 1) return fail("substeps must be >= 1");
+    if (d->collisions && d->max_neighbors < 1) return fail("max_neighbors must be >= 1");
+    if (d->n_obstacles < 0) return fail("n_obstacles must be >= 0");
+    if (need_params && (!d->params || !d->model_tag || !d->ctrl_mode))
+        return fail("params/model_tag/ctrl_mode must be set");
+    if (d->n_obstacles > 0 && (!d->obs_pos || !d->obs_radius || !d->obs_angle || !d->obs_half ||
+                               !d->obs_vel || !d->obs_ang_vel || !d->obs_type))
+        return fail("obstacle arrays must be set when n_obstacles > 0");
+    return 0;
+}
+
+static int pad_agents(int A)
+{
+    int p = 4;
+    while (p < A) p <<= 1;
+    return p;
+}
+
+static double skin_of(const swarp_desc_t *d)
+{
+    // Candidate-list skin: room for (S-1) substeps of motion of both agents of a pair
+    // at about 1.5x the fleet's top speed.  Only speed depends on it; exactness does not.
+    if (d->substeps < 2) return 0.0;
+    double vmax = 1.0;
+    if (getenv("SWARP_SKIN_VMAX")) vmax = atof(getenv("SWARP_SKIN_VMAX"));
+    return 2.0 * 1.5 * vmax * (d->substeps - 1) * (d->dt / d->substeps);
+}
+
+template <typename T> static void fill_args(const swarp_desc_t *d, Args<T> &a)
+{
+    memset(&a, 0, sizeof a);
+    a.params = (const T *)d->params;
+    a.tag = d->model_tag;
+    a.mode = d->ctrl_mode;
+    a.obs.pos = (const T *)d->obs_pos;
+    a.obs.rad = (const T *)d->obs_radius;
+    a.obs.ang = (const T *)d->obs_angle;
+    a.obs.half = (const T *)d->obs_half;
+    a.obs.vel = (const T *)d->obs_vel;
+    a.obs.om = (const T *)d->obs_ang_vel;
+    a.obs.type = d->obs_type;
+}
+
+template <typename T> static void copy_fields(const swarp_state_t *s, T **f)
+{
+    void *const src[9] = {s->pos, s->theta, s->vel, s->speed, s->ang_vel,
+                          s->z, s->vz, s->attitude, s->body_rates};
+    for (int k = 0; k < 9; ++k) f[k] = (T *)src[k];
+}
+
+static bool fields_ok(const swarp_state_t *s, int n)
+{
+    if (!s) return false;
+    void *const src[9] = {s->pos, s->theta, s->vel, s->speed, s->ang_vel,
+                          s->z, s->vz, s->attitude, s->body_rates};
+    for (int k = 0; k < n; ++k)
+        if (!src[k]) return false;
+    return true;
+}
+
+#define SWARP_DISPATCH_PA(PA_, KERNEL, ...)                                        \
+    switch (PA_) {                                                                 \
+    case 4: hipLaunchKernelGGL((KERNEL<T, 4, __VA_ARGS__>), grid4, dim3(64), shm, st, C, a); break; \
+    case 8: hipLaunchKernelGGL((KERNEL<T, 8, __VA_ARGS__>), grid8, dim3(64), shm, st, C, a); break; \
+    case 16: hipLaunchKernelGGL((KERNEL<T, 16, __VA_ARGS__>), grid16, dim3(64), shm, st, C, a); break; \
+    case 32: hipLaunchKernelGGL((KERNEL<T, 32, __VA_ARGS__>), grid32, dim3(64), shm, st, C, a); break; \
+    default: hipLaunchKernelGGL((KERNEL<T, 64, __VA_ARGS__>), grid64, dim3(64), shm, st, C, a); break; \
+    }
+
+template <typename T, bool DRONE>
+static void launch_fwd(int PA, const Cst<T> &C, const Args<T> &a, hipStream_t st)
+{
+    const size_t shm = 0;
+    const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
+        grid32((C.E + 1) / 2), grid64(C.E);
+    SWARP_DISPATCH_PA(PA, k_rollout_fwd, DRONE)
+}
+
+template <typename T, bool DRONE>
+static void launch_bwd(int PA, const Cst<T> &C, const Args<T> &a, size_t shm, hipStream_t st)
+{
+    const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
+        grid32((C.E + 1) / 2), grid64(C.E);
+    SWARP_DISPATCH_PA(PA, k_rollout_bwd, DRONE)
+}
+
+template <typename T>
+static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s0,
+                       const void *act, const swarp_state_t *traj, const swarp_state_t *fin,
+                       hipStream_t st)
+{
+    Cst<T> C;
+    fill_cst<T>(d, skin_of(d), C);
+    Args<T> a;
+    fill_args<T>(d, a);
+    const int nf = d->has_drone ? 9 : 5;
+    if (!fields_ok(s0, nf)) return fail("state0 is missing a field");
+    if (!fields_ok(fin, nf)) return fail("final_state is missing a field");
+    if (nT > 1 && !fields_ok(traj, nf)) return fail("traj is missing a field (T > 1)");
+    if (!act) return fail("actions is NULL");
+    copy_fields<T>(s0, (T **)a.s0.f);
+    copy_fields<T>(fin, a.fin.f);
+    if (nT > 1) copy_fields<T>(traj, a.traj.f);
+    a.act = (const T *)act;
+    a.nsteps = nT;
+    const int PA = pad_agents(d->n_agents);
+    if (d->has_drone)
+        launch_fwd<T, true>(PA, C, a, st);
+    else
+        launch_fwd<T, false>(PA, C, a, st);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(hipGetErrorString(e));
+    return 0;
+}
+
+template <typename T>
+static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s0,
+                       const void *act, const swarp_state_t *traj, const swarp_state_t *atraj,
+                       const swarp_state_t *afin, const swarp_state_t *a0, void *aact,
+                       hipStream_t st)
+{
+    Cst<T> C;
+    fill_cst<T>(d, skin_of(d), C);
+    Args<T> a;
+    fill_args<T>(d, a);
+    const int nf = d->has_drone ? 9 : 5;
+    if (!fields_ok(s0, nf)) return fail("state0 is missing a field");
+    if (nT > 1 && !fields_ok(traj, nf)) return fail("traj is missing a field (T > 1)");
+    if (!act || !aact) return fail("actions / adj_actions is NULL");
+    copy_fields<T>(s0, (T **)a.s0.f);
+    if (nT > 1) copy_fields<T>(traj, a.traj.f);
+    if (atraj) copy_fields<T>(atraj, (T **)a.atraj.f);
+    if (afin) copy_fields<T>(afin, (T **)a.afin.f);
+    if (a0) copy_fields<T>(a0, a.a0.f);
+    a.act = (const T *)act;
+    a.aact = (T *)aact;
+    a.nsteps = nT;
+    const int PA = pad_agents(d->n_agents);
+    const int NF = d->has_drone ? NF_DRONE : NF_2D;
+    const size_t msz = PA == 64 ? 8 : 4;
+    const size_t shm = 2 * 64 * sizeof(T) + (size_t)d->substeps * NF * 64 * sizeof(T) +
+                       (size_t)d->substeps * 64 * msz;
+    if (shm > 65536) return fail("substeps too large for the backward LDS staging (limit 64 KiB per wave)");
+    if (d->has_drone)
+        launch_bwd<T, true>(PA, C, a, shm, st);
+    else
+        launch_bwd<T, false>(PA, C, a, shm, st);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(hipGetErrorString(e));
+    return 0;
+}
+
+extern "C" {
+
+int swarp_abi_version(void) { return SWARP_ABI_VERSION; }
+
+const char *swarp_last_error(void) { return g_err; }
+
+int swarp_rollout_fwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                      const void *actions, const swarp_state_t *traj,
+                      const swarp_state_t *final_state, void *stream)
+{
+    g_err[0] = 0;
+    if (check_desc(desc)) return -1;
+    if (T < 1) return fail("T must be >= 1");
+    hipStream_t st = (hipStream_t)stream;
+    if (desc->dtype == SWARP_F32)
+        return rollout_fwd<float>(desc, T, state0, actions, traj, final_state, st);
+    return rollout_fwd<double>(desc, T, state0, actions, traj, final_state, st);
+}
+
+int swarp_rollout_bwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                      const void *actions, const swarp_state_t *traj,
+                      const swarp_state_t *adj_traj, const swarp_state_t *adj_final,
+                      const swarp_state_t *adj_state0, void *adj_actions, void *stream)
+{
+    g_err[0] = 0;
+    if (check_desc(desc)) return -1;
+    if (T < 1) return fail("T must be >= 1");
+    hipStream_t st = (hipStream_t)stream;
+    if (desc->dtype == SWARP_F32)
+        return rollout_bwd<float>(desc, T, state0, actions, traj, adj_traj, adj_final, adj_state0,
+                                  adj_actions, st);
+    return rollout_bwd<double>(desc, T, state0, actions, traj, adj_traj, adj_final, adj_state0,
+                               adj_actions, st);
+}
+
+int swarp_neighbors(const swarp_desc_t *desc, const void *pos, int32_t *idx, int32_t *cnt,
+                    int32_t *true_cnt, void *stream)
+{
+    g_err[0] = 0;
+    if (check_desc(desc, false)) return -1;
+    if (desc->max_neighbors < 1) return fail("max_neighbors must be >= 1");
+    if (!pos || !idx || !cnt) return fail("pos/idx/cnt must be set");
+    hipStream_t st = (hipStream_t)stream;
+    const int PA = pad_agents(desc->n_agents);
+    const int E = desc->n_envs;
+    const dim3 grid((E + (64 / PA) - 1) / (64 / PA));
+#define SWARP_NB(TT)                                                                          \
+    {                                                                                         \
+        Cst<TT> C;                                                                            \
+        fill_cst<TT>(desc, 0.0, C);                                                           \
+        const TT *p = (const TT *)pos;                                                        \
+        switch (PA) {                                                                         \
+        case 4: hipLaunchKernelGGL((k_neighbors<TT, 4>), grid, dim3(64), 0, st, C, p, idx, cnt, true_cnt); break; \
+        case 8: hipLaunchKernelGGL((k_neighbors<TT, 8>), grid, dim3(64), 0, st, C, p, idx, cnt, true_cnt); break; \
+        case 16: hipLaunchKernelGGL((k_neighbors<TT, 16>), grid, dim3(64), 0, st, C, p, idx, cnt, true_cnt); break; \
+        case 32: hipLaunchKernelGGL((k_neighbors<TT, 32>), grid, dim3(64), 0, st, C, p, idx, cnt, true_cnt); break; \
+        default: hipLaunchKernelGGL((k_neighbors<TT, 64>), grid, dim3(64), 0, st, C, p, idx, cnt, true_cnt); break; \
+        }                                                                                     \
+    }
+    if (desc->dtype == SWARP_F32)
+        SWARP_NB(float)
+    else
+        SWARP_NB(double)
+#undef SWARP_NB
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(hipGetErrorString(e));
+    return 0;
+}
+
+int swarp_edge_index(int32_t n_envs, int32_t n_agents, int32_t max_neighbors, const int32_t *idx,
+                     const int32_t *cnt, const int64_t *offsets, int64_t n_edges,
+                     int64_t *edge_index, void *stream)
+{
+    g_err[0] = 0;
+    if (n_envs < 1 || n_agents < 1 || max_neighbors < 1) return fail("bad sizes");
+    if (n_edges < 0) return fail("n_edges must be >= 0");
+    if (n_edges == 0) return 0;
+    if (!idx || !cnt || !offsets || !edge_index) return fail("pointer arguments must be set");
+    const size_t n = (size_t)n_envs * n_agents;
+    hipLaunchKernelGGL(k_edge_index, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, n_envs, n_agents, max_neighbors, idx, cnt, offsets,
+                       n_edges, edge_index);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(hipGetErrorString(e));
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,312 @@
+"""Host side of the step: per-agent parameters, world constants, obstacles, and the
+descriptor handed to the HIP library.
+
+Counterpart of ``Stepper`` (``swarp/core/stepper.py:66-239, 295-432, 581-710``): the
+same constructor, validation and error types, the same derived constants
+(``sub_dt = dt / substeps``, the contact reach check, soft-wall / clamp flags), and
+``set_obstacles`` with the same defaults.  The substep pipeline itself lives in one
+HIP launch per rollout (``swarp_amd/csrc``), so there are no per-substep buffers
+here; the no-grad path keeps the reference's two-slot ping-pong outputs.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import NamedTuple
+
+import torch
+
+from . import _lib
+from .config import (
+    AgentConfig,
+    AgentShape,
+    ControlMode,
+    DynamicsModel,
+    Integrator,
+    ObstacleKind,
+    Obstacles,
+    WorldConfig,
+    action_dim,
+)
+from .neighbors import NeighborGrid
+
+
+class AgentParams(NamedTuple):
+    """Device-resident per-agent parameters (``swarp/dynamics/base.py:334-349``)."""
+
+    floats: torch.Tensor     # [n_agents, NUM_PARAMS]
+    model_tag: torch.Tensor  # [n_agents] int32
+    ctrl_mode: torch.Tensor  # [n_agents] int32
+
+
+def build_agent_params(configs: list[AgentConfig], device, dtype) -> AgentParams:
+    """Pack AgentConfig rows into device tensors (``swarp/dynamics/base.py:352-366``)."""
+    rows = torch.tensor([c.to_row() for c in configs], dtype=torch.float64).to(dtype)
+    tags = torch.tensor([int(c.model) for c in configs], dtype=torch.int32)
+    modes = torch.tensor([int(c.ctrl_mode) for c in configs], dtype=torch.int32)
+    return AgentParams(rows.to(device).contiguous(), tags.to(device), modes.to(device))
+
+
+_DTYPES = {
+    torch.float32: torch.float32,
+    torch.float64: torch.float64,
+    "float32": torch.float32,
+    "float64": torch.float64,
+    "fp32": torch.float32,
+    "fp64": torch.float64,
+}
+
+
+def resolve_dtype(dtype) -> torch.dtype:
+    """torch dtype of a Stepper precision given as a torch dtype or its name."""
+    if isinstance(dtype, str):
+        dtype = dtype.replace("torch.", "")
+    try:
+        return _DTYPES[dtype]
+    except (KeyError, TypeError):
+        raise TypeError(f"unsupported dtype {dtype!r}; use torch.float32 or torch.float64") from None
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+class Stepper:
+    """Owns per-agent parameters, interaction config and obstacles of one world.
+
+    ``dtype`` is a torch dtype (``torch.float32`` / ``torch.float64``) or its name; the
+    reference takes the matching Warp dtype.  Unlike the reference, a bare Stepper
+    refuses model features this build does not implement instead of running them.
+    """
+
+    def __init__(
+        self,
+        configs: list[AgentConfig],
+        dt: float = 0.1,
+        substeps: int = 1,
+        device: str = "cuda:0",
+        dtype=torch.float32,
+        world: WorldConfig | None = None,
+    ) -> None:
+        world = world if world is not None else WorldConfig(collisions=False)
+        if substeps < 1:
+            raise ValueError("substeps must be >= 1")
+        if len(configs) < 1:
+            raise ValueError("a Stepper needs at least one AgentConfig")
+        self.configs = configs
+        self.n_agents = len(configs)
+        self.dt = dt
+        self.substeps = substeps
+        self.sub_dt = dt / substeps
+        self.device = str(device)
+        self.dtype = resolve_dtype(dtype)
+        self.torch_dtype = self.dtype
+        self.world = world
+        self._check_supported()
+        self.params = build_agent_params(configs, self.device, self.dtype)
+        self.act_dim = max(action_dim(c.model) for c in configs)
+        self.has_drone = any(c.model == DynamicsModel.DRONE for c in configs)
+
+        self.collisions = world.collisions
+        self.max_agent_radius = max(c.radius for c in configs)
+        self.neighbor_radius = 0.0
+        if self.collisions:
+            reach = 2.0 * self.max_agent_radius + world.collision_margin
+            self.neighbor_radius = world.neighbor_radius or reach
+            if self.neighbor_radius < reach:
+                raise ValueError(
+                    f"neighbor_radius={self.neighbor_radius} is smaller than the collision "
+                    f"reach {reach} (= 2 * max radius + margin); collisions would be missed."
+                )
+        self._soft_walls = world.bounds is not None and world.bounds_mode == "soft"
+        self._clamp = world.bounds is not None and world.bounds_mode == "clamp"
+        if world.bounds is not None:
+            x_min, x_max, y_min, y_max = world.bounds
+            self._bounds = (x_min, y_min, x_max, y_max)
+        else:
+            self._bounds = (0.0, 0.0, 0.0, 0.0)
+
+        self.n_obstacles = 0
+        self.obstacles: Obstacles | None = None
+        self._obs: dict[str, torch.Tensor] = {}
+        self.any_movable = False
+        self._descs: dict[tuple[int, int], _lib.SwarpDesc] = {}
+        self._grids: dict[int, NeighborGrid] = {}
+        self._out_states: dict[int, list] = {}
+        self._out_idx: dict[int, int] = {}
+        self.mutation_version = 0
+
+    # ------------------------------------------------------------------ checks
+
+    def _check_supported(self) -> None:
+        if self.n_agents > 64:
+            raise NotImplementedError("this build steps at most 64 agents per env")
+        w = self.world
+        if w.integrator != Integrator.EULER:
+            raise NotImplementedError("only Integrator.EULER is implemented on the HIP path")
+        if w.wheel_contacts:
+            raise NotImplementedError("WorldConfig.wheel_contacts is not implemented")
+        if w.neighbor_method not in ("auto", "brute"):
+            raise NotImplementedError(
+                f"neighbor_method={w.neighbor_method!r}: this build implements the brute-force "
+                "lists only (the reference's own choice at <= 512 agents)"
+            )
+        for c in self.configs:
+            if c.shape == AgentShape.BOX:
+                raise NotImplementedError("box agents are not implemented")
+            if c.ctrl_mode == ControlMode.SERVO:
+                raise NotImplementedError("ControlMode.SERVO is not implemented")
+
+    # --------------------------------------------------------------- obstacles
+
+    def set_obstacles(self, obstacles: Obstacles) -> None:
+        """Install the obstacle set (``swarp/core/stepper.py:295-432``); absent fields
+        take their documented defaults."""
+        obs = obstacles.resolve(self.device, self.dtype)
+        if obs.any_movable:
+            raise NotImplementedError("MOVABLE obstacles (compound bodies) are not implemented yet")
+        n_envs, n = obs.n_envs, obs.n_obstacles
+        z = {"device": self.device, "dtype": self.dtype}
+        self._obs = {
+            "pos": obs.pos,
+            "radius": obs.radius,
+            "type": obs.shape if obs.shape is not None else torch.zeros(n, device=self.device, dtype=torch.int32),
+            "angle": obs.angle if obs.angle is not None else torch.zeros(n_envs, n, **z),
+            "half": obs.half_extents if obs.half_extents is not None else torch.zeros(n, 2, **z),
+            "vel": obs.vel if obs.vel is not None else torch.zeros(n_envs, n, 2, **z),
+            "ang_vel": obs.ang_vel if obs.ang_vel is not None else torch.zeros(n_envs, n, **z),
+        }
+        self.obstacles = obstacles
+        self.n_obstacles = n
+        self._obs_envs = n_envs
+        self.any_movable = False
+        self._descs.clear()
+        self.mutation_version += 1
+
+    @property
+    def _needs_forces(self) -> bool:
+        return self.collisions or self._soft_walls or self.n_obstacles > 0
+
+    # --------------------------------------------------------------- descriptor
+
+    def desc(self, n_envs: int, act_dim: int) -> _lib.SwarpDesc:
+        """The (cached) C descriptor of this world for a batch of ``n_envs``."""
+        key = (n_envs, act_dim)
+        d = self._descs.get(key)
+        if d is not None:
+            return d
+        if self.n_obstacles > 0 and self._obs_envs != n_envs:
+            raise ValueError(
+                f"obstacles were installed for {self._obs_envs} envs, stepping {n_envs}"
+            )
+        d = _lib.SwarpDesc()
+        d.abi_version = _lib.ABI_VERSION
+        d.dtype = _lib.F64 if self.dtype == torch.float64 else _lib.F32
+        d.n_envs = n_envs
+        d.n_agents = self.n_agents
+        d.act_dim = act_dim
+        d.substeps = self.substeps
+        d.max_neighbors = self.world.max_neighbors if self.collisions else 0
+        d.n_obstacles = self.n_obstacles
+        d.collisions = int(self.collisions)
+        d.soft_walls = int(self._soft_walls)
+        d.clamp_bounds = int(self._clamp)
+        d.has_drone = int(self.has_drone)
+        d.dt = float(self.dt)
+        d.k = float(self.world.collision_k)
+        d.c = float(self.world.collision_c)
+        d.margin = float(self.world.collision_margin)
+        d.max_overlap = float(self.world.contact_max_overlap)
+        d.neighbor_radius = float(self.neighbor_radius)
+        bx0, by0, bx1, by1 = self._bounds
+        d.bounds_min[0], d.bounds_min[1] = bx0, by0
+        d.bounds_max[0], d.bounds_max[1] = bx1, by1
+        d.params = self.params.floats.data_ptr()
+        d.model_tag = self.params.model_tag.data_ptr()
+        d.ctrl_mode = self.params.ctrl_mode.data_ptr()
+        if self.n_obstacles > 0:
+            o = self._obs
+            d.obs_pos = o["pos"].data_ptr()
+            d.obs_radius = o["radius"].data_ptr()
+            d.obs_angle = o["angle"].data_ptr()
+            d.obs_half = o["half"].data_ptr()
+            d.obs_vel = o["vel"].data_ptr()
+            d.obs_ang_vel = o["ang_vel"].data_ptr()
+            d.obs_type = o["type"].data_ptr()
+        self._descs[key] = d
+        return d
+
+    # --------------------------------------------------------------- neighbours
+
+    def grid(self, n_envs: int) -> NeighborGrid:
+        g = self._grids.get(n_envs)
+        if g is None:
+            g = NeighborGrid(
+                n_envs,
+                self.n_agents,
+                radius=self.neighbor_radius if self.collisions else 2.0 * self.max_agent_radius
+                + self.world.collision_margin,
+                max_neighbors=self.world.max_neighbors,
+                device=self.device,
+                dtype=self.dtype,
+                grid_dim=self.world.grid_dim,
+                method=self.world.neighbor_method,
+                uniform_bins=self.world.uniform_bins,
+                bounds=self.world.bounds,
+            )
+            self._grids[n_envs] = g
+        return g
+
+    # --------------------------------------------------------------- allocation
+
+    def alloc_state(self, n_envs: int, requires_grad: bool = False):
+        from .autograd import TorchState
+
+        z = {"device": self.device, "dtype": self.dtype}
+        att = torch.zeros(n_envs, self.n_agents, 4, **z)
+        att[..., 3] = 1.0
+        st = TorchState(
+            pos=torch.zeros(n_envs, self.n_agents, 2, **z),
+            theta=torch.zeros(n_envs, self.n_agents, **z),
+            vel=torch.zeros(n_envs, self.n_agents, 2, **z),
+            speed=torch.zeros(n_envs, self.n_agents, **z),
+            ang_vel=torch.zeros(n_envs, self.n_agents, **z),
+            z=torch.zeros(n_envs, self.n_agents, **z),
+            vz=torch.zeros(n_envs, self.n_agents, **z),
+            attitude=att,
+            body_rates=torch.zeros(n_envs, self.n_agents, 3, **z),
+        )
+        if requires_grad:
+            st = type(st)(*(t.requires_grad_(True) for t in st))
+        return st
+
+    def output_state(self, n_envs: int):
+        """Ping-pong output slot of the no-grad path (``swarp/core/stepper.py:688-710``):
+        valid until this batch size is stepped twice more."""
+        states = self._out_states.get(n_envs)
+        if states is None:
+            states = [self.alloc_state(n_envs), self.alloc_state(n_envs)]
+            self._out_states[n_envs] = states
+            self._out_idx[n_envs] = 0
+        i = self._out_idx[n_envs]
+        self._out_idx[n_envs] = 1 - i
+        return states[i]
+
+    def launch_substeps(self, state_in, actions: torch.Tensor, state_out) -> None:
+        """Advance one env step from ``state_in`` into ``state_out`` (no autograd)."""
+        from .autograd import _launch_fwd
+
+        _launch_fwd(self, state_in, actions.unsqueeze(0), None, state_out)
+
+
+def state_struct(fields) -> _lib.SwarpState:
+    """SwarpState of up to nine tensors (None = NULL)."""
+    s = _lib.SwarpState()
+    names = ("pos", "theta", "vel", "speed", "ang_vel", "z", "vz", "attitude", "body_rates")
+    for name, t in zip(names, fields):
+        setattr(s, name, _ptr(t))
+    return s
+
+
+def byref(x):
+    return ctypes.byref(x)
