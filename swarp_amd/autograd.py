@@ -34,6 +34,18 @@ from . import _lib
 from .stepper import Stepper, state_struct
 
 FIELDS = ("pos", "theta", "vel", "speed", "ang_vel", "z", "vz", "attitude", "body_rates")
+
+#: Optional kernel timing sink: when a list, every rollout launch appends
+#: (kind, start_event, end_event) recorded on the launch stream ("fwd" / "bwd").
+KERNEL_EVENTS: list | None = None
+
+
+def _event(stream_tensor: torch.Tensor):
+    ev = torch.cuda.Event(enable_timing=True)
+    ev.record(torch.cuda.current_stream(stream_tensor.device))
+    return ev
+
+
 _TAIL = ((2,), (), (2,), (), (), (), (), (4,), (3,))
 
 
@@ -144,7 +156,12 @@ class _RolloutFn(torch.autograd.Function):
             traj = _empty_like_fields(stepper, (max(T - 1, 0),), E, dev)
         else:
             final, traj = bufs
+        sink = KERNEL_EVENTS
+        if sink is not None:
+            e0 = _event(actions_seq)
         _launch_fwd(stepper, state0, actions_seq, traj, final)
+        if sink is not None:
+            sink.append(("fwd", e0, _event(actions_seq)))
         ctx.stepper = stepper
         ctx.nf = len(state0)
         ctx.T = T
@@ -172,6 +189,9 @@ class _RolloutFn(torch.autograd.Function):
         gtr = state_struct(g_traj) if T > 1 and any(g is not None for g in g_traj) else None
         gfin = state_struct(g_final) if any(g is not None for g in g_final) else None
         a0 = state_struct(adj0)
+        sink = KERNEL_EVENTS
+        if sink is not None:
+            e0 = _event(actions_seq)
         _lib.check(lib.swarp_rollout_bwd(
             ctypes.byref(desc), T, ctypes.byref(s0), actions_seq.data_ptr(),
             ctypes.byref(tr) if tr is not None else None,
@@ -179,6 +199,8 @@ class _RolloutFn(torch.autograd.Function):
             ctypes.byref(gfin) if gfin is not None else None,
             ctypes.byref(a0), adj_act.data_ptr(), _stream(actions_seq),
         ))
+        if sink is not None:
+            sink.append(("bwd", e0, _event(actions_seq)))
         return (None, None, adj_act if need[2] else None, *adj0)
 
 

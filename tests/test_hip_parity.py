@@ -1,0 +1,153 @@
+"""HIP path vs the CPU oracle on identical seeded inputs (the parity tests proper).
+
+Bars (written per test):
+* holonomic / drone worlds compute with +, -, *, / and sqrt only, so float32 states are
+  compared BIT-EXACT with the float32 oracle (both keep the reference's op order with no
+  FMA contraction and correctly rounded divide / sqrt);
+* worlds with transcendental functions (diff-drive, bicycle, box / segment obstacles,
+  tanh-saturated contacts) are compared at 1e-5 relative: device and host libm differ by
+  an ulp;
+* gradients are compared at 1e-5 relative (max-norm) against the float32 oracle, and at
+  the reference's own cross-precision bar (rtol 1e-3, tests/unit/test_gradients.py:257)
+  against the float64 oracle.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from cases import nav_agents, nav_inputs, nav_world
+from hip_helpers import hip_run, make_stepper, oracle_run, rel
+from oracle.oracle import pack_state
+from swarp_amd.config import AgentConfig, ControlMode, DynamicsModel, ObstacleShape, WorldConfig
+
+pytestmark = pytest.mark.gpu
+
+
+def _nav_case(E, A, T, S, extent, seed=0, dtype=np.float32):
+    pos, goals, acts = nav_inputs(E, A, T, extent=extent, seed=seed, dtype=torch.float64)
+    s0 = pack_state({"pos": pos.numpy()}, dtype=np.float64).astype(dtype)
+    acts = acts.numpy().astype(dtype)
+    # loss = sum ||p_T - g||^2  ->  adjoint 2 (p_T - g) on the final position only;
+    # plus a random cotangent on every trajectory state so every adjoint path is used
+    return s0, acts, goals.numpy()
+
+
+def _cotangent(T, E, A, seed, nf=5, scale=1.0):
+    rng = np.random.default_rng(seed)
+    w = rng.normal(size=(T, E, A, 16)) * scale
+    if nf == 5:
+        w[..., 7:] = 0.0
+    return w
+
+
+def _check(name, hip, orc, state_exact, g_tol=1e-5, nf=5):
+    hs, hg0, hga = hip
+    os_, og0, oga = orc
+    cols = slice(0, 7) if nf == 5 else slice(0, 16)
+    if state_exact:
+        assert np.array_equal(hs[..., cols], os_[..., cols]), (
+            f"{name}: states not bit-exact, max rel {rel(hs[..., cols], os_[..., cols]):.3e}")
+    else:
+        assert rel(hs[..., cols], os_[..., cols]) <= 1e-5, f"{name}: states rel {rel(hs[..., cols], os_[..., cols]):.3e}"
+    assert rel(hga, oga) <= g_tol, f"{name}: d/d actions rel {rel(hga, oga):.3e}"
+    assert rel(hg0[..., cols], og0[..., cols]) <= g_tol, f"{name}: d/d state0 rel {rel(hg0[..., cols], og0[..., cols]):.3e}"
+
+
+def test_config1_navigation_bitexact():
+    """Config 1: 64 envs x 4 holonomic agents, dt 0.05, 1 substep, 10 steps."""
+    E, A, T = 64, 4, 10
+    s0, acts, goals = _nav_case(E, A, T, 1, extent=1.0)
+    w = _cotangent(T, E, A, 1)
+    cfgs, world = nav_agents(A), nav_world(A, world_size=1.0)
+    st = make_stepper(cfgs, world, 0.05, 1, torch.float32)
+    hip = hip_run(st, s0, acts, w, np.float32)
+    orc = oracle_run(cfgs, world, 0.05, 1, s0, acts, w, np.float32)
+    _check("c1", hip, orc, state_exact=True)
+    o64 = oracle_run(cfgs, world, 0.05, 1, s0.astype(np.float64), acts.astype(np.float64), w, np.float64)
+    np.testing.assert_allclose(hip[2], o64[2], rtol=1e-3, atol=1e-4)
+
+
+def test_config2_shape_reduced():
+    """Config 2 shape: 16 agents in a 4x4 arena, 4 substeps, 32 steps (1000 envs)."""
+    E, A, T, S = 1000, 16, 32, 4
+    s0, acts, _ = _nav_case(E, A, T, S, extent=2.0, seed=3)
+    w = _cotangent(T, E, A, 2)
+    cfgs, world = nav_agents(A), nav_world(A, world_size=2.0)
+    st = make_stepper(cfgs, world, 0.05, S, torch.float32)
+    hip = hip_run(st, s0, acts, w, np.float32)
+    orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float32)
+    _check("c2-reduced", hip, orc, state_exact=True)
+
+
+def test_crowded_contacts_truncated_lists():
+    """Dense envs with truncated lists (K < A - 1), velocity damping, walls, 3 substeps."""
+    E, A, T, S = 128, 12, 6, 3
+    rng = np.random.default_rng(5)
+    s0 = pack_state({"pos": rng.uniform(-0.3, 0.3, size=(E, A, 2)),
+                     "vel": 0.3 * rng.normal(size=(E, A, 2))}).astype(np.float32)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
+    cfgs = nav_agents(A, agent_radius=0.08, mode=ControlMode.ACCELERATION)
+    world = WorldConfig(collision_k=50.0, collision_c=2.0, collision_margin=0.03, max_neighbors=4,
+                        neighbor_radius=0.3, bounds=(-0.4, 0.4, -0.4, 0.4))
+    w = _cotangent(T, E, A, 3)
+    st = make_stepper(cfgs, world, 0.05, S, torch.float32)
+    hip = hip_run(st, s0, acts, w, np.float32)
+    orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float32)
+    _check("crowded", hip, orc, state_exact=True)
+
+
+def test_mixed_fleet_obstacles():
+    """Config 3 shape (reduced): diff-drive + bicycle, 8 obstacles per env, 4 substeps."""
+    E, A, T, S = 64, 32, 20, 4
+    rng = np.random.default_rng(7)
+    cfgs = [AgentConfig(model=DynamicsModel.DIFF_DRIVE, radius=0.05) for _ in range(A // 2)] + [
+        AgentConfig(model=DynamicsModel.KINEMATIC_BICYCLE, radius=0.05) for _ in range(A // 2)]
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.025,
+                        bounds=(-2.0, 2.0, -2.0, 2.0), max_neighbors=32)
+    n = 8
+    obs = {"pos": rng.uniform(-2, 2, size=(E, n, 2)),
+           "radius": np.r_[rng.uniform(0.05, 0.2, 4), np.zeros(2), np.full(2, 0.05)],
+           "type": np.r_[np.zeros(4), np.ones(2), np.full(2, 2)].astype(np.int32),
+           "angle": rng.uniform(-np.pi, np.pi, size=(E, n)),
+           "half": np.r_[np.zeros((4, 2)), rng.uniform(0.05, 0.3, size=(2, 2)),
+                         np.c_[rng.uniform(0.1, 0.4, 2), np.zeros(2)]]}
+    s0 = pack_state({"pos": rng.uniform(-2, 2, size=(E, A, 2)),
+                     "theta": rng.uniform(-np.pi, np.pi, size=(E, A))}).astype(np.float32)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
+    w = _cotangent(T, E, A, 4, scale=0.1)
+    st = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
+    hip = hip_run(st, s0, acts, w, np.float32)
+    orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float32, obs=obs)
+    _check("mixed", hip, orc, state_exact=False, g_tol=1e-4)
+
+
+def test_drones_bitexact():
+    """Config 4 shape (reduced): quadrotors with planar contacts, 16 steps."""
+    E, A, T, S = 64, 8, 16, 2
+    rng = np.random.default_rng(9)
+    cfgs = [AgentConfig(model=DynamicsModel.DRONE, radius=0.1, thrust_max=10.0) for _ in range(A)]
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02)
+    ax = rng.normal(size=(E, A, 3))
+    ax /= np.linalg.norm(ax, axis=-1, keepdims=True)
+    ang = rng.uniform(0, 0.1, size=(E, A, 1))
+    q = np.concatenate([ax * np.sin(ang / 2), np.cos(ang / 2)], -1)
+    s0 = pack_state({"pos": rng.uniform(-0.5, 0.5, size=(E, A, 2)), "z": np.ones((E, A)),
+                     "attitude": q}).astype(np.float32)
+    acts = (rng.uniform(0, 1, size=(T, E, A, 4)) * 10.0 * 0.5).astype(np.float32)
+    w = _cotangent(T, E, A, 5, nf=9, scale=0.01)
+    st = make_stepper(cfgs, world, 0.02, S, torch.float32)
+    hip = hip_run(st, s0, acts, w, np.float32)
+    orc = oracle_run(cfgs, world, 0.02, S, s0, acts, w, np.float32)
+    _check("drones", hip, orc, state_exact=True, nf=9, g_tol=1e-4)
+
+
+def test_float64_matches_float64_oracle():
+    E, A, T, S = 32, 8, 8, 2
+    s0, acts, _ = _nav_case(E, A, T, S, extent=0.4, seed=11, dtype=np.float64)
+    cfgs, world = nav_agents(A), nav_world(A, world_size=0.5)
+    w = _cotangent(T, E, A, 6)
+    st = make_stepper(cfgs, world, 0.05, S, torch.float64)
+    hip = hip_run(st, s0, acts, w, np.float64)
+    orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float64)
+    _check("f64", hip, orc, state_exact=True, g_tol=1e-12)
