@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--substeps", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target duration of the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--copy-mb", type=int, default=0,
+                    help="after the benchmark, run 3 plain device copies of this many MiB "
+                         "(calibrates rocprof byte counters against a known traffic)")
     return ap.parse_args()
 
 
@@ -113,13 +116,17 @@ def cpu_baseline(E_full, A, T, S, seconds, cfgs, world):
     dt_probe = run(probe)
     E = int(min(E_full, max(probe, probe * seconds / max(dt_probe, 1e-6))))
     el = run(E) if E != probe else dt_probe
+    reps, total = 1, el
+    while total < seconds and reps < 50:
+        total += run(E)
+        reps += 1
     return {
-        "value": E * T / el,
+        "value": E * T * reps / total,
         "unit": "env-steps/s",
         "cores": n,
         "kind": "port",
-        "sample": f"{E} of {E_full} envs x {A} agents, {S} substeps, {T}-step BPTT fwd+bwd, "
-                  f"float32 C oracle with OpenMP over envs ({el:.1f} s)",
+        "sample": f"{reps} x {E} of {E_full} envs x {A} agents, {S} substeps, {T}-step BPTT "
+                  f"fwd+bwd, float32 C oracle, OpenMP over envs ({total:.1f} s)",
     }
 
 
@@ -225,6 +232,14 @@ def main():
     }
     if args.cpu_seconds > 0:
         out["cpu_baseline"] = cpu_baseline(E, A, T, S, args.cpu_seconds, cfgs, world)
+    if args.copy_mb > 0:
+        n = args.copy_mb * (1 << 20) // 4
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        out["copy_calibration_bytes"] = {"read": 4 * n, "write": 4 * n}
     print(json.dumps(out), flush=True)
 
 

@@ -42,6 +42,8 @@ typedef struct swarp_desc {
     int32_t soft_walls;      /* bounds_mode == "soft" with bounds set */
     int32_t clamp_bounds;    /* bounds_mode == "clamp" with bounds set (disc clamp) */
     int32_t has_drone;       /* fleet holds a DRONE: all nine fields are stepped */
+    int32_t holo_velocity_only; /* every agent is HOLONOMIC in VELOCITY mode: selects the
+                                   specialised kernels (must describe params truthfully) */
     double dt;               /* env step; sub_dt = dt / substeps */
     double k, c, margin, max_overlap;
     double neighbor_radius;

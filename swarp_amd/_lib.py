@@ -34,6 +34,7 @@ class SwarpDesc(ctypes.Structure):
         ("soft_walls", ctypes.c_int32),
         ("clamp_bounds", ctypes.c_int32),
         ("has_drone", ctypes.c_int32),
+        ("holo_velocity_only", ctypes.c_int32),
         ("dt", ctypes.c_double),
         ("k", ctypes.c_double),
         ("c", ctypes.c_double),

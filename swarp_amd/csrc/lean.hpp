@@ -1,0 +1,345 @@
+// lean.hpp -- specialised rollout kernels for fleets of holonomic agents in velocity
+// mode without obstacles (the reference's NavigationScenario default, BASELINE config 1/2).
+// Included by swarp_hip.hip; uses its Lane/mask helpers.
+//
+// Same arithmetic, in the same order, as the generic kernels (so the results are
+// bit-identical), with what this fleet does not need removed:
+//   * clamp_norm(action) is computed once per step (the action is constant over the
+//     substeps) instead of once per substep;
+//   * only pos / vel are carried through the substeps; theta passes through, speed is
+//     the length of the last substep's velocity, ang_vel is zero;
+//   * the neighbour scan has a compile-time trip count: pad lanes of a partially filled
+//     env slot hold NaN positions, which fail every membership test, so the LDS reads of
+//     a scan are issued back to back and waited on once;
+//   * the next step's inputs are loaded one step ahead.
+#pragma once
+
+namespace swarp {
+
+template <typename T> struct alignas(2 * sizeof(T)) P2 {
+    T x, y;
+};
+
+template <typename T> __device__ __forceinline__ P2<T> ld2(const T *p, size_t j)
+{
+    return *reinterpret_cast<const P2<T> *>(p + 2 * j);
+}
+template <typename T> __device__ __forceinline__ void st2(T *p, size_t j, T x, T y)
+{
+    P2<T> v;
+    v.x = x;
+    v.y = y;
+    *reinterpret_cast<P2<T> *>(p + 2 * j) = v;
+}
+
+// Full scan of the env's PA slots: inclusion (radius) and skin-candidate masks.
+template <typename T, int PA>
+__device__ __forceinline__ void lean_scan(const P2<T> *lp, int base, int me, T px, T py,
+                                          const Cst<T> &C, typename MaskT<PA>::type &incl,
+                                          typename MaskT<PA>::type &cand)
+{
+    typedef typename MaskT<PA>::type M;
+    M in = 0, cd = 0;
+    constexpr int CH = PA < 16 ? PA : 16;  // LDS reads batched per chunk, one wait each
+#pragma unroll
+    for (int b0 = 0; b0 < PA; b0 += CH) {
+        P2<T> q[CH];
+#pragma unroll
+        for (int k = 0; k < CH; ++k) q[k] = lp[base + b0 + k];
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+            const T dx = q[k].x - px, dy = q[k].y - py;
+            const T d2 = dx * dx + dy * dy;
+            in |= d2 <= C.t_nbr ? (M(1) << (b0 + k)) : M(0);
+            cd |= d2 <= C.t_skin ? (M(1) << (b0 + k)) : M(0);
+        }
+    }
+    const M self = ~(M(1) << me);
+    incl = in & self;
+    cand = cd & self;
+}
+
+template <typename T, int PA>
+__device__ __forceinline__ typename MaskT<PA>::type lean_cand(const P2<T> *lp, int base, T px,
+                                                              T py, T t_nbr,
+                                                              typename MaskT<PA>::type cand)
+{
+    typedef typename MaskT<PA>::type M;
+    M in = 0;
+    while (cand) {
+        const int b = m_ctz(cand);
+        cand &= cand - 1;
+        const P2<T> q = lp[base + b];
+        const T dx = q.x - px, dy = q.y - py;
+        const T d2 = dx * dx + dy * dy;
+        in |= d2 <= t_nbr ? (M(1) << b) : M(0);
+    }
+    return in;
+}
+
+// One substep of the force pass: neighbour lists (into `incl`) and the total force.
+template <typename T, int PA>
+__device__ __forceinline__ void lean_forces(const Cst<T> &C, const P2<T> *lp, const P2<T> *lv,
+                                            const T *lr, int base, int me, T ra, T dd, T px,
+                                            T py, T vx, T vy, bool full, bool first,
+                                            typename MaskT<PA>::type &cand,
+                                            typename MaskT<PA>::type &incl, T &Fx, T &Fy)
+{
+    typedef typename MaskT<PA>::type M;
+    T fx = T(0), fy = T(0);
+    incl = 0;
+    if (C.collisions) {
+        if (full) {
+            M cd;
+            lean_scan<T, PA>(lp, base, me, px, py, C, incl, cd);
+            if (first) cand = cd;
+        } else {
+            incl = lean_cand<T, PA>(lp, base, px, py, C.t_nbr, cand);
+        }
+        M m = cap_list(incl, C.K);
+        while (m) {
+            const int b = m_ctz(m);
+            m &= m - 1;
+            const int j = base + b;
+            const P2<T> q = lp[j], w = lv[j];
+            T gx, gy;
+            pair_force(C, px - q.x, py - q.y, vx - w.x, vy - w.y, ra + lr[j] + C.margin, dd, gx, gy);
+            fx += gx;
+            fy += gy;
+        }
+    }
+    T sx = T(0), sy = T(0);
+    if (C.soft_walls) wall_force(C, px, py, vx, vy, ra, dd, sx, sy);
+    Fx = fx + sx;
+    Fy = fy + sy;
+}
+
+template <typename T, int PA>
+__global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g)
+{
+    typedef typename MaskT<PA>::type M;
+    __shared__ P2<T> lp[64], lv[64];
+    __shared__ T lr[64];
+    const int lane = threadIdx.x, me = lane % PA, base = lane - me;
+    const int env = blockIdx.x * (64 / PA) + lane / PA;
+    const bool real = me < C.A;
+    const bool active = real && env < C.E;
+    const size_t i = (size_t)(env < C.E ? env : 0) * C.A + (real ? me : 0);
+    const T *prow = g.params + (real ? me : 0) * 22;
+    const T ra = prow[0], mass = prow[1], vmax = prow[2];
+    const T dt = C.sub_dt, dtm = dt / mass, dd = T(1) + C.c * C.sub_dt / mass;
+    lr[lane] = ra;
+    const T qnan = __builtin_nan("");
+    P2<T> p = ld2(g.s0.f[0], i), v = ld2(g.s0.f[2], i);
+    if (!real) p.x = p.y = qnan;  // pad slot: never within any radius
+    const T th = g.s0.f[1][i];
+    const size_t EA = (size_t)C.E * C.A;
+    P2<T> a = ld2(g.act, i);
+    for (int t = 0; t < g.nsteps; ++t) {
+        P2<T> an = a;
+        if (t + 1 < g.nsteps) an = ld2(g.act, (size_t)(t + 1) * EA + i);
+        T cnx, cny;
+        clamp_norm(a.x, a.y, vmax, cnx, cny);
+        M cand = 0, incl;
+        T D = T(0);
+        bool ok = false;
+        for (int s = 0; s < C.S; ++s) {
+            T Fx = T(0), Fy = T(0);
+            if (C.needs_forces) {
+                if (C.collisions) {
+                    __syncthreads();
+                    lp[lane] = p;
+                    lv[lane] = v;
+                    __syncthreads();
+                }
+                lean_forces<T, PA>(C, lp, lv, lr, base, me, ra, dd, p.x, p.y, v.x, v.y,
+                                   s == 0 || !ok, s == 0, cand, incl, Fx, Fy);
+            }
+            const T vnx = cnx + Fx * dtm, vny = cny + Fy * dtm;
+            const T pnx = p.x + vnx * dt, pny = p.y + vny * dt;
+            if (C.use_skin) {
+                D += (m_abs(pnx - p.x) + m_abs(pny - p.y)) * T(1.0001);
+                ok = env_all<PA>(!real || D <= C.half_margin, base);
+            }
+            p.x = pnx;
+            p.y = pny;
+            v.x = vnx;
+            v.y = vny;
+        }
+        if (active) {
+            const bool last = t + 1 == g.nsteps;
+            T *const *f = last ? g.fin.f : g.traj.f;
+            const size_t j = last ? i : (size_t)t * EA + i;
+            st2(f[0], j, p.x, p.y);
+            f[1][j] = th;
+            st2(f[2], j, v.x, v.y);
+            f[3][j] = m_sqrt(v.x * v.x + v.y * v.y);
+            f[4][j] = T(0);
+        }
+        a = an;
+    }
+}
+
+template <typename T, int PA>
+__global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g)
+{
+    typedef typename MaskT<PA>::type M;
+    extern __shared__ __align__(16) unsigned char smem[];
+    // per substep slot: P2 pos[64], P2 vel[64]; then masks [S][64]; then gF[64], r[64], dd[64]
+    P2<T> *slot = (P2<T> *)smem;
+    M *lm = (M *)(slot + (size_t)C.S * 128);
+    P2<T> *lg = (P2<T> *)(lm + (size_t)C.S * 64);
+    T *lr = (T *)(lg + 64);
+    T *ldd = lr + 64;
+    const int lane = threadIdx.x, me = lane % PA, base = lane - me;
+    const int env = blockIdx.x * (64 / PA) + lane / PA;
+    const bool real = me < C.A;
+    const bool active = real && env < C.E;
+    const size_t i = (size_t)(env < C.E ? env : 0) * C.A + (real ? me : 0);
+    const T *prow = g.params + (real ? me : 0) * 22;
+    const T ra = prow[0], mass = prow[1], vmax = prow[2];
+    const T dt = C.sub_dt, dtm = dt / mass, dd = T(1) + C.c * C.sub_dt / mass;
+    lr[lane] = ra;
+    ldd[lane] = dd;
+    const T qnan = __builtin_nan("");
+    const size_t EA = (size_t)C.E * C.A;
+    // adjoint of the current step's output: pos, theta, vel (speed enters per step)
+    T gpx = T(0), gpy = T(0), gth = T(0), gvx = T(0), gvy = T(0);
+    int t = g.nsteps - 1;
+    // step inputs: checkpoint t-1 (or state0), action t
+    P2<T> p = t == 0 ? ld2(g.s0.f[0], i) : ld2(g.traj.f[0], (size_t)(t - 1) * EA + i);
+    P2<T> v = t == 0 ? ld2(g.s0.f[2], i) : ld2(g.traj.f[2], (size_t)(t - 1) * EA + i);
+    P2<T> a = ld2(g.act, (size_t)t * EA + i);
+    for (; t >= 0; --t) {
+        // adjoint arriving at this step's output
+        {
+            const T *const *f = t == g.nsteps - 1 ? g.afin.f : g.atraj.f;
+            const size_t j = t == g.nsteps - 1 ? i : (size_t)t * EA + i;
+            if (f[0]) { P2<T> q = ld2(f[0], j); gpx += q.x; gpy += q.y; }
+            if (f[1]) gth += f[1][j];
+            if (f[2]) { P2<T> q = ld2(f[2], j); gvx += q.x; gvy += q.y; }
+        }
+        const T *gsp = t == g.nsteps - 1 ? g.afin.f[3] : g.atraj.f[3];
+        const T gs = gsp ? gsp[t == g.nsteps - 1 ? i : (size_t)t * EA + i] : T(0);
+        // prefetch the previous step's inputs
+        P2<T> pn = p, vn = v, an = a;
+        if (t > 0) {
+            pn = t - 1 == 0 ? ld2(g.s0.f[0], i) : ld2(g.traj.f[0], (size_t)(t - 2) * EA + i);
+            vn = t - 1 == 0 ? ld2(g.s0.f[2], i) : ld2(g.traj.f[2], (size_t)(t - 2) * EA + i);
+            an = ld2(g.act, (size_t)(t - 1) * EA + i);
+        }
+        if (!real) p.x = p.y = qnan;
+        T cnx, cny;
+        clamp_norm(a.x, a.y, vmax, cnx, cny);
+
+        // ---- recompute the substeps of step t into LDS
+        M cand = 0, incl;
+        T D = T(0);
+        bool ok = false;
+        for (int s = 0; s < C.S; ++s) {
+            P2<T> *sp = slot + s * 128;
+            __syncthreads();
+            sp[lane] = p;
+            sp[64 + lane] = v;
+            __syncthreads();
+            T Fx = T(0), Fy = T(0);
+            if (C.needs_forces)
+                lean_forces<T, PA>(C, sp, sp + 64, lr, base, me, ra, dd, p.x, p.y, v.x, v.y,
+                                   s == 0 || !ok, s == 0, cand, incl, Fx, Fy);
+            else
+                incl = 0;
+            lm[s * 64 + lane] = incl;
+            const T vnx = cnx + Fx * dtm, vny = cny + Fy * dtm;
+            const T pnx = p.x + vnx * dt, pny = p.y + vny * dt;
+            if (C.use_skin) {
+                D += (m_abs(pnx - p.x) + m_abs(pny - p.y)) * T(1.0001);
+                ok = env_all<PA>(!real || D <= C.half_margin, base);
+            }
+            p.x = pnx;
+            p.y = pny;
+            v.x = vnx;
+            v.y = vny;
+        }
+        // speed output = |v| of the last substep (zero gradient at v = 0)
+        const T spd = m_sqrt(v.x * v.x + v.y * v.y);
+        if (spd > T(0)) {
+            gvx += gs * v.x / spd;
+            gvy += gs * v.y / spd;
+        }
+
+        // ---- reverse pass over the substeps
+        T gcx = T(0), gcy = T(0);
+        for (int s = C.S - 1; s >= 0; --s) {
+            const T gtx = gvx + gpx * dt, gty = gvy + gpy * dt;  // adjoint of v_new
+            gcx += gtx;
+            gcy += gty;
+            const T gFx = gtx * dtm, gFy = gty * dtm;
+            T ipx = gpx, ipy = gpy, ivx = T(0), ivy = T(0);
+            if (C.needs_forces) {
+                const P2<T> *sp = slot + s * 128;
+                const P2<T> q0 = sp[lane], w0 = sp[64 + lane];
+                if (C.collisions) {
+                    __syncthreads();
+                    P2<T> gg;
+                    gg.x = gFx;
+                    gg.y = gFy;
+                    lg[lane] = gg;
+                    __syncthreads();
+                    const M mine = lm[s * 64 + lane];
+                    M m = mine;
+                    while (m) {
+                        const int b = m_ctz(m);
+                        m &= m - 1;
+                        const int j = base + b;
+                        const P2<T> q = sp[j], w = sp[64 + j];
+                        if (in_list(mine, b, C.K)) {
+                            T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
+                            pair_force_adj(C, q0.x - q.x, q0.y - q.y, w0.x - w.x, w0.y - w.y,
+                                           ra + lr[j] + C.margin, dd, gFx, gFy, adx, ady, arx, ary);
+                            ipx += adx; ipy += ady; ivx += arx; ivy += ary;
+                        }
+                        if (in_list(lm[s * 64 + j], me, C.K)) {
+                            const P2<T> gb = lg[j];
+                            T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
+                            pair_force_adj(C, q.x - q0.x, q.y - q0.y, w.x - w0.x, w.y - w0.y,
+                                           lr[j] + ra + C.margin, ldd[j], gb.x, gb.y, adx, ady,
+                                           arx, ary);
+                            ipx -= adx; ipy -= ady; ivx -= arx; ivy -= ary;
+                        }
+                    }
+                }
+                if (C.soft_walls) {
+                    St<T> ga;
+                    ga.px = ipx; ga.py = ipy; ga.vx = ivx; ga.vy = ivy;
+                    wall_force_adj(C, q0.x, q0.y, w0.x, w0.y, ra, dd, gFx, gFy, ga);
+                    ipx = ga.px; ipy = ga.py; ivx = ga.vx; ivy = ga.vy;
+                }
+            }
+            gpx = ipx;
+            gpy = ipy;
+            gvx = ivx;
+            gvy = ivy;
+        }
+        if (active) {
+            T ax = T(0), ay = T(0);
+            clamp_norm_adj(a.x, a.y, vmax, gcx, gcy, ax, ay);
+            T *pa = g.aact + ((size_t)t * EA + i) * C.ad;
+            pa[0] = ax;
+            if (C.ad > 1) pa[1] = ay;
+            for (int k = 2; k < C.ad; ++k) pa[k] = T(0);
+        }
+        p = pn;
+        v = vn;
+        a = an;
+    }
+    if (active) {
+        T *const *f = g.a0.f;
+        if (f[0]) st2(f[0], i, gpx, gpy);
+        if (f[1]) f[1][i] = gth;
+        if (f[2]) st2(f[2], i, gvx, gvy);
+        if (f[3]) f[3][i] = T(0);
+        if (f[4]) f[4][i] = T(0);
+    }
+}
+
+}  // namespace swarp

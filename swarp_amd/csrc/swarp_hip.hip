@@ -172,14 +172,13 @@ __device__ __forceinline__ typename MaskT<PA>::type scan_all(const T *lx, const 
 {
     typedef typename MaskT<PA>::type M;
     M incl = 0, cd = 0;
+    (void)A;  // pad slots (b >= A) hold NaN positions and never pass the test
 #pragma unroll
     for (int b = 0; b < PA; ++b) {
-        if (b < A) {
-            T dx = lx[base + b] - px, dy = ly[base + b] - py;
-            T d2 = dx * dx + dy * dy;
-            incl |= d2 <= t_nbr ? (M(1) << b) : M(0);
-            cd |= d2 <= t_skin ? (M(1) << b) : M(0);
-        }
+        T dx = lx[base + b] - px, dy = ly[base + b] - py;
+        T d2 = dx * dx + dy * dy;
+        incl |= d2 <= t_nbr ? (M(1) << b) : M(0);
+        cd |= d2 <= t_skin ? (M(1) << b) : M(0);
     }
     const M self = ~(M(1) << me);
     cand = cd & self;
@@ -314,6 +313,7 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> C, const Args<T
     lr[L.lane] = L.pr.radius;
     St<T> st;
     load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
+    if (!L.real) st.px = st.py = __builtin_nan("");
     const size_t EA = (size_t)C.E * C.A;
     for (int t = 0; t < g.nsteps; ++t) {
         T a[4];
@@ -417,6 +417,7 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
             load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
         else
             load_state<T, DRONE>(g.traj.f, L.idx, (size_t)(t - 1) * EA, st);
+        if (!L.real) st.px = st.py = __builtin_nan("");
         T a[4];
         load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
 
@@ -506,6 +507,10 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
     if (L.active) store_adj<T, DRONE>(g.a0.f, L.idx, gs);
 }
 
+}  // namespace swarp
+#include "lean.hpp"
+namespace swarp {
+
 // --------------------------------------------------------------- neighbour lists
 
 template <typename T, int PA>
@@ -519,7 +524,8 @@ __global__ __launch_bounds__(64) void k_neighbors(const Cst<T> C, const T *pos, 
     const int env = blockIdx.x * EPW + lane / PA;
     const bool active = agent < C.A && env < C.E;
     const size_t i = active ? (size_t)env * C.A + agent : 0;
-    const T px = pos[2 * i], py = pos[2 * i + 1];
+    const bool real = agent < C.A;
+    const T px = real ? pos[2 * i] : (T)__builtin_nan(""), py = real ? pos[2 * i + 1] : (T)__builtin_nan("");
     lx[lane] = px;
     ly[lane] = py;
     __syncthreads();
@@ -720,6 +726,39 @@ static void launch_bwd(int PA, const Cst<T> &C, const Args<T> &a, size_t shm, hi
     SWARP_DISPATCH_PA(PA, k_rollout_bwd, DRONE)
 }
 
+static bool lean_ok(const swarp_desc_t *d)
+{
+    return d->holo_velocity_only && !d->has_drone && d->n_obstacles == 0 && !d->clamp_bounds;
+}
+
+template <typename T> static void launch_holo_fwd(int PA, const Cst<T> &C, const Args<T> &a, hipStream_t st)
+{
+    const size_t shm = 0;
+    const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
+        grid32((C.E + 1) / 2), grid64(C.E);
+    switch (PA) {
+    case 4: hipLaunchKernelGGL((k_holo_fwd<T, 4>), grid4, dim3(64), shm, st, C, a); break;
+    case 8: hipLaunchKernelGGL((k_holo_fwd<T, 8>), grid8, dim3(64), shm, st, C, a); break;
+    case 16: hipLaunchKernelGGL((k_holo_fwd<T, 16>), grid16, dim3(64), shm, st, C, a); break;
+    case 32: hipLaunchKernelGGL((k_holo_fwd<T, 32>), grid32, dim3(64), shm, st, C, a); break;
+    default: hipLaunchKernelGGL((k_holo_fwd<T, 64>), grid64, dim3(64), shm, st, C, a); break;
+    }
+}
+
+template <typename T>
+static void launch_holo_bwd(int PA, const Cst<T> &C, const Args<T> &a, size_t shm, hipStream_t st)
+{
+    const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
+        grid32((C.E + 1) / 2), grid64(C.E);
+    switch (PA) {
+    case 4: hipLaunchKernelGGL((k_holo_bwd<T, 4>), grid4, dim3(64), shm, st, C, a); break;
+    case 8: hipLaunchKernelGGL((k_holo_bwd<T, 8>), grid8, dim3(64), shm, st, C, a); break;
+    case 16: hipLaunchKernelGGL((k_holo_bwd<T, 16>), grid16, dim3(64), shm, st, C, a); break;
+    case 32: hipLaunchKernelGGL((k_holo_bwd<T, 32>), grid32, dim3(64), shm, st, C, a); break;
+    default: hipLaunchKernelGGL((k_holo_bwd<T, 64>), grid64, dim3(64), shm, st, C, a); break;
+    }
+}
+
 template <typename T>
 static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s0,
                        const void *act, const swarp_state_t *traj, const swarp_state_t *fin,
@@ -740,7 +779,9 @@ static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     a.act = (const T *)act;
     a.nsteps = nT;
     const int PA = pad_agents(d->n_agents);
-    if (d->has_drone)
+    if (lean_ok(d))
+        launch_holo_fwd<T>(PA, C, a, st);
+    else if (d->has_drone)
         launch_fwd<T, true>(PA, C, a, st);
     else
         launch_fwd<T, false>(PA, C, a, st);
@@ -772,6 +813,16 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     a.aact = (T *)aact;
     a.nsteps = nT;
     const int PA = pad_agents(d->n_agents);
+    if (lean_ok(d)) {
+        const size_t msz = PA == 64 ? 8 : 4;
+        const size_t lshm = (size_t)d->substeps * 128 * 2 * sizeof(T) +
+                            (size_t)d->substeps * 64 * msz + 64 * 2 * sizeof(T) + 2 * 64 * sizeof(T);
+        if (lshm > 65536) return fail("substeps too large for the backward LDS staging (limit 64 KiB per wave)");
+        launch_holo_bwd<T>(PA, C, a, lshm, st);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fail(hipGetErrorString(e));
+        return 0;
+    }
     const int NF = d->has_drone ? NF_DRONE : NF_2D;
     const size_t msz = PA == 64 ? 8 : 4;
     const size_t shm = 2 * 64 * sizeof(T) + (size_t)d->substeps * NF * 64 * sizeof(T) +

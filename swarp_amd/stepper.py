@@ -106,6 +106,13 @@ class Stepper:
         self.params = build_agent_params(configs, self.device, self.dtype)
         self.act_dim = max(action_dim(c.model) for c in configs)
         self.has_drone = any(c.model == DynamicsModel.DRONE for c in configs)
+        self.holo_velocity_only = all(
+            c.model == DynamicsModel.HOLONOMIC and c.ctrl_mode == ControlMode.VELOCITY
+            for c in configs
+        )
+        #: route eligible fleets to the specialised kernels (set False to force the
+        #: generic ones; both give bit-identical results)
+        self.use_specialised = True
 
         self.collisions = world.collisions
         self.max_agent_radius = max(c.radius for c in configs)
@@ -212,6 +219,8 @@ class Stepper:
         d.soft_walls = int(self._soft_walls)
         d.clamp_bounds = int(self._clamp)
         d.has_drone = int(self.has_drone)
+        d.holo_velocity_only = int(self.use_specialised and self.holo_velocity_only
+                                   and self.n_obstacles == 0 and not self._clamp)
         d.dt = float(self.dt)
         d.k = float(self.world.collision_k)
         d.c = float(self.world.collision_c)

@@ -151,3 +151,38 @@ def test_float64_matches_float64_oracle():
     hip = hip_run(st, s0, acts, w, np.float64)
     orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float64)
     _check("f64", hip, orc, state_exact=True, g_tol=1e-12)
+
+
+def test_specialised_matches_generic_kernels():
+    """The holonomic-velocity kernels and the generic kernels: identical forward bits,
+    gradients equal to rounding (the adjoint sums in a different order)."""
+    E, A, T, S = 400, 16, 12, 4
+    s0, acts, _ = _nav_case(E, A, T, S, extent=0.6, seed=21)
+    cfgs, world = nav_agents(A), nav_world(A, world_size=0.7)
+    w = _cotangent(T, E, A, 7)
+    lean = make_stepper(cfgs, world, 0.05, S, torch.float32)
+    gen = make_stepper(cfgs, world, 0.05, S, torch.float32)
+    gen.use_specialised = False
+    a = hip_run(lean, s0, acts, w, np.float32)
+    b = hip_run(gen, s0, acts, w, np.float32)
+    assert np.array_equal(a[0][..., :7], b[0][..., :7])
+    assert rel(a[2], b[2]) <= 1e-6 and rel(a[1][..., :7], b[1][..., :7]) <= 1e-6
+
+
+def test_padded_agent_slots():
+    """n_agents not a power of two (pad lanes in every env slot): 5, 12 and 20 agents."""
+    for A, K in ((5, 4), (12, 12), (20, 8)):
+        E, T, S = 96, 6, 2
+        rng = np.random.default_rng(A)
+        s0 = pack_state({"pos": rng.uniform(-0.4, 0.4, size=(E, A, 2))}).astype(np.float32)
+        acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
+        cfgs = nav_agents(A)
+        world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.025,
+                            bounds=(-0.5, 0.5, -0.5, 0.5), max_neighbors=K, neighbor_radius=0.2)
+        w = _cotangent(T, E, A, A)
+        for spec in (True, False):
+            st = make_stepper(cfgs, world, 0.05, S, torch.float32)
+            st.use_specialised = spec
+            hip = hip_run(st, s0, acts, w, np.float32)
+            orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float32)
+            _check(f"pad A={A} spec={spec}", hip, orc, state_exact=True)
