@@ -199,6 +199,7 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
     const T *prow = g.params + (real ? me : 0) * 22;
     const T ra = prow[0], mass = prow[1], vmax = prow[2];
     const T dt = C.sub_dt, dtm = dt / mass, dd = T(1) + C.c * C.sub_dt / mass;
+    const T inv_dd = T(1) / dd;
     lr[lane] = ra;
     ldd[lane] = dd;
     const T qnan = __builtin_nan("");
@@ -279,10 +280,11 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
                 const P2<T> *sp = slot + s * 128;
                 const P2<T> q0 = sp[lane], w0 = sp[64 + lane];
                 if (C.collisions) {
+                    // publish the force adjoint pre-divided by the damping denominator
                     __syncthreads();
                     P2<T> gg;
-                    gg.x = gFx;
-                    gg.y = gFy;
+                    gg.x = gFx * inv_dd;
+                    gg.y = gFy * inv_dd;
                     lg[lane] = gg;
                     __syncthreads();
                     const M mine = lm[s * 64 + lane];
@@ -291,21 +293,15 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
                         const int b = m_ctz(m);
                         m &= m - 1;
                         const int j = base + b;
+                        const bool own = in_list(mine, b, C.K);
+                        const bool rev = in_list(lm[s * 64 + j], me, C.K);
+                        if (!own && !rev) continue;
                         const P2<T> q = sp[j], w = sp[64 + j];
-                        if (in_list(mine, b, C.K)) {
-                            T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
-                            pair_force_adj(C, q0.x - q.x, q0.y - q.y, w0.x - w.x, w0.y - w.y,
-                                           ra + lr[j] + C.margin, dd, gFx, gFy, adx, ady, arx, ary);
-                            ipx += adx; ipy += ady; ivx += arx; ivy += ary;
-                        }
-                        if (in_list(lm[s * 64 + j], me, C.K)) {
-                            const P2<T> gb = lg[j];
-                            T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
-                            pair_force_adj(C, q.x - q0.x, q.y - q0.y, w.x - w0.x, w.y - w0.y,
-                                           lr[j] + ra + C.margin, ldd[j], gb.x, gb.y, adx, ady,
-                                           arx, ary);
-                            ipx -= adx; ipy -= ady; ivx -= arx; ivy -= ary;
-                        }
+                        const P2<T> gb = lg[j];
+                        const T wx = (own ? gg.x : T(0)) - (rev ? gb.x : T(0));
+                        const T wy = (own ? gg.y : T(0)) - (rev ? gb.y : T(0));
+                        pair_adj_combined(C, q0.x - q.x, q0.y - q.y, w0.x - w.x, w0.y - w.y,
+                                          ra + lr[j] + C.margin, wx, wy, ipx, ipy, ivx, ivy);
                     }
                 }
                 if (C.soft_walls) {

@@ -150,6 +150,52 @@ __device__ __forceinline__ void pair_force_adj(const Cst<T> &C, T dx, T dy, T rv
     ady += ey;
 }
 
+// Reverse of the contact pair (a, b) seen from agent a, for both forces the pair exerts.
+// With d = p_a - p_b and rv = v_a - v_b, a's force is G(d, rv) / dd_a and b's force is
+// -G(d, rv) / dd_b, where G = max(num, 0) * n, n = d / |d|, num = k*ov' - c*(rv.n) (the
+// contact law is symmetric under (d, rv) -> (-d, -rv)).  So the adjoint of both is one
+// evaluation of G's adjoint with the cotangent w = [b in a's list] g_a/dd_a
+// - [a in b's list] g_b/dd_b (the caller passes w).  The distance, the normal and num are
+// recomputed exactly as in the forward pass so every branch is taken as it was there; the
+// arithmetic after the branches uses one reciprocal of the distance.
+template <typename T>
+__device__ __forceinline__ void pair_adj_combined(const Cst<T> &C, T dx, T dy, T rvx, T rvy, T md,
+                                                  T wx, T wy, T &adx, T &ady, T &arx, T &ary)
+{
+    const T d2 = dx * dx + dy * dy;
+    const T dist = m_sqrt(wmax(d2, C.eps2));
+    const T ov = md - dist;
+    if (!(ov > T(0))) return;
+    const T nx = dx / dist, ny = dy / dist;
+    const T vn = rvx * nx + rvy * ny;
+    T o = ov, slope = T(1);
+    if (C.max_overlap > T(0)) {
+        const T th = m_tanh(ov / C.max_overlap);
+        o = C.max_overlap * th;
+        slope = T(1) - th * th;
+    }
+    const T num = C.k * o - C.c * vn;
+    if (!(num > T(0))) return;  // clamped repulsive: no gradient (dd >= 1 keeps the sign)
+    const T a_num = wx * nx + wy * ny;
+    T anx = num * wx, any = num * wy;
+    const T a_ov = C.k * a_num * slope;
+    const T a_vn = -C.c * a_num;
+    arx += a_vn * nx;
+    ary += a_vn * ny;
+    anx += a_vn * rvx;
+    any += a_vn * rvy;
+    const T inv = T(1) / dist;
+    const T a_dist = -(anx * nx + any * ny) * inv - a_ov;
+    T ex = anx * inv, ey = any * inv;
+    if (d2 > C.eps2) {
+        const T h = a_dist * T(0.5) * inv;
+        ex += T(2) * dx * h;
+        ey += T(2) * dy * h;
+    }
+    adx += ex;
+    ady += ey;
+}
+
 // ------------------------------------------------------------------- walls
 
 // _wall_forces (swarp/core/collisions.py:746-778)

@@ -220,6 +220,7 @@ template <typename T, int PA> struct Lane {
     size_t idx;    // env * A + agent (clamped to a valid element for inactive lanes)
     Prm<T> pr;
     T dd;          // implicit damping denominator 1 + c*sub_dt/m (collisions.py:845)
+    T inv_dd;      // 1 / dd (adjoint arithmetic only)
 };
 
 template <typename T, int PA>
@@ -237,6 +238,7 @@ __device__ __forceinline__ void lane_init(const Cst<T> &C, const Args<T> &g, Lan
     L.idx = (size_t)ev * C.A + ag;
     load_prm(g, ag, L.pr);
     L.dd = T(1) + C.c * C.sub_dt / L.pr.mass;
+    L.inv_dd = T(1) / L.dd;
 }
 
 // Whether every real agent of this lane's env stayed within the skin budget.
@@ -458,9 +460,11 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
             T gFx, gFy;
             integrate_adj<T, DRONE>(C, L.pr, in, a, Fx, Fy, gs, gi, ga, gFx, gFy);
             if (C.needs_forces) {
+                // the slot now carries the force adjoint divided by the damping denominator
+                const T wFx = gFx * L.inv_dd, wFy = gFy * L.inv_dd;
                 __syncthreads();
-                sl[F_FX * 64 + L.lane] = gFx;  // the slot now carries the force adjoint
-                sl[F_FY * 64 + L.lane] = gFy;
+                sl[F_FX * 64 + L.lane] = wFx;
+                sl[F_FY * 64 + L.lane] = wFy;
                 __syncthreads();
                 if (C.collisions) {
                     const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64;
@@ -472,20 +476,14 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
                         const int b = m_ctz(m);
                         m &= m - 1;
                         const int j = L.base + b;
-                        const T md = L.pr.radius + lr[j] + C.margin;
-                        if (in_list(mine, b, C.K)) {  // b in my list: d = me - b
-                            T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
-                            pair_force_adj(C, in.px - lx[j], in.py - ly[j], in.vx - lvx[j],
-                                           in.vy - lvy[j], md, L.dd, gFx, gFy, adx, ady, arx, ary);
-                            gi.px += adx; gi.py += ady; gi.vx += arx; gi.vy += ary;
-                        }
-                        if (in_list(lmask[s * 64 + j], L.agent, C.K)) {  // me in b's list
-                            T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
-                            pair_force_adj(C, lx[j] - in.px, ly[j] - in.py, lvx[j] - in.vx,
-                                           lvy[j] - in.vy, lr[j] + L.pr.radius + C.margin, ldd[j],
-                                           lgx[j], lgy[j], adx, ady, arx, ary);
-                            gi.px -= adx; gi.py -= ady; gi.vx -= arx; gi.vy -= ary;
-                        }
+                        const bool own = in_list(mine, b, C.K);
+                        const bool rev = in_list(lmask[s * 64 + j], L.agent, C.K);
+                        if (!own && !rev) continue;
+                        const T wx = (own ? wFx : T(0)) - (rev ? lgx[j] : T(0));
+                        const T wy = (own ? wFy : T(0)) - (rev ? lgy[j] : T(0));
+                        pair_adj_combined(C, in.px - lx[j], in.py - ly[j], in.vx - lvx[j],
+                                          in.vy - lvy[j], L.pr.radius + lr[j] + C.margin, wx, wy,
+                                          gi.px, gi.py, gi.vx, gi.vy);
                     }
                 }
                 if (C.N > 0) {
