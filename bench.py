@@ -196,6 +196,14 @@ def main():
         }
     dom = max(kernels, key=lambda k: kernels[k]["avg_ms"])
     kd = kernels[dom]
+    traffic = None
+    prof = ROOT / "profiles" / "traffic_c2.json"
+    if prof.exists() and (E, A, T, S) == (16000, 16, 32, 4):
+        # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+        # of this same workload, scaled by the copy-kernel calibration they record
+        tr = json.loads(prof.read_text())
+        k = tr["kernels"][dom]
+        traffic = 1024 * (k["fetch_kib"] * tr["fetch_scale"] + k["write_kib"] * tr["write_scale"])
     fused_frac = (fwd_bytes(A) + bwd_bytes(A)) * E * T / (
         (kernels["fwd"]["avg_ms"] + kernels["bwd"]["avg_ms"]) * 1e-3) / HBM_PEAK
 
@@ -224,7 +232,7 @@ def main():
             "peak": HBM_PEAK / 1e9,
             "unit": "GB/s",
             "frac": kd["frac"],
-            "traffic": None,
+            "traffic": traffic,
         },
         "fwd_bwd_kernel_roofline_frac": fused_frac,
         "fwd_only_env_steps_per_s": fwd_only,

@@ -1,0 +1,162 @@
+"""Host-side tests (no GPU): the C-ABI library loads and exports every function the header
+declares, the ctypes struct layouts equal the C header's, and the host logic keeps the
+reference's validation and error types."""
+
+import ctypes
+import math
+import re
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from swarp_amd import (AgentConfig, ControlMode, DynamicsModel, GradRing, Integrator, Obstacles,
+                       Stepper, TorchState, WorldConfig, action_bounds, action_dim, drone_config,
+                       rollout, warp_step)
+from swarp_amd import _lib
+from swarp_amd.config import PARAM_FIELDS, AgentShape
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "swarp_hip.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(swarp_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_function():
+    lib = _lib.load()
+    names = _declared_functions()
+    assert names == sorted(_lib.SIGNATURES), names
+    for n in names:
+        assert hasattr(lib, n), n
+    assert lib.swarp_abi_version() == _lib.ABI_VERSION
+    assert lib.swarp_last_error() == b""
+
+
+def test_struct_layout_matches_header(tmp_path):
+    prog = tmp_path / "layout.c"
+    desc_fields = [f for f, _ in _lib.SwarpDesc._fields_]
+    state_fields = [f for f, _ in _lib.SwarpState._fields_]
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){",
+             'printf("%zu\\n", sizeof(swarp_desc_t));', 'printf("%zu\\n", sizeof(swarp_state_t));']
+    lines += [f'printf("%zu\\n", offsetof(swarp_desc_t, {f}));' for f in desc_fields]
+    lines += [f'printf("%zu\\n", offsetof(swarp_state_t, {f}));' for f in state_fields]
+    lines.append("return 0;}")
+    prog.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", str(prog), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [ctypes.sizeof(_lib.SwarpDesc), ctypes.sizeof(_lib.SwarpState)]
+    want += [getattr(_lib.SwarpDesc, f).offset for f in desc_fields]
+    want += [getattr(_lib.SwarpState, f).offset for f in state_fields]
+    assert got == want
+
+
+def test_library_rejects_bad_descriptor_without_gpu():
+    """Argument checks run on the host before any launch and report through the error
+    channel (no device call is made for a rejected descriptor)."""
+    lib = _lib.load()
+    d = _lib.SwarpDesc()
+    d.abi_version = 999
+    s = _lib.SwarpState()
+    rc = lib.swarp_rollout_fwd(ctypes.byref(d), 1, ctypes.byref(s), None, None, ctypes.byref(s), None)
+    assert rc != 0 and b"abi_version" in lib.swarp_last_error()
+    d.abi_version = _lib.ABI_VERSION
+    d.dtype = 0
+    d.n_envs, d.n_agents, d.act_dim, d.substeps = 1, 65, 2, 1
+    rc = lib.swarp_rollout_fwd(ctypes.byref(d), 1, ctypes.byref(s), None, None, ctypes.byref(s), None)
+    assert rc != 0 and b"n_agents" in lib.swarp_last_error()
+
+
+# ------------------------------------------------------------------ config surface
+
+def test_param_fields_layout():
+    # column order of swarp/dynamics/base.py:114-145
+    assert PARAM_FIELDS == (
+        "radius", "mass", "max_speed", "max_accel", "max_ang_vel", "max_ang_accel", "l_f", "l_r",
+        "max_steer", "thrust_max", "arm_length", "inertia_xx", "inertia_yy", "inertia_zz",
+        "torque_coeff", "gravity", "min_speed", "shape", "half_x", "half_y", "cmd_gain_v",
+        "cmd_gain_w")
+    row = AgentConfig(max_speed=2.0).to_row()
+    assert row[PARAM_FIELDS.index("min_speed")] == -2.0
+    assert row[0] == 0.05 and len(row) == 22
+
+
+def test_agent_config_validation_and_coercion():
+    assert AgentConfig(model="diff-drive").model == DynamicsModel.DIFF_DRIVE
+    assert AgentConfig(model="drone").model == DynamicsModel.DRONE
+    with pytest.raises(ValueError, match="unknown model"):
+        AgentConfig(model="tank")
+    with pytest.raises(ValueError, match="SERVO"):
+        AgentConfig(model=DynamicsModel.HOLONOMIC, ctrl_mode=ControlMode.SERVO)
+    with pytest.raises(ValueError, match="positive"):
+        AgentConfig(mass=0.0)
+    box = AgentConfig(shape=AgentShape.BOX, half_extents=(0.3, 0.4))
+    assert math.isclose(box.radius, 0.5)
+    assert action_dim("drone") == 4 and action_dim(DynamicsModel.HOLONOMIC) == 2
+    lo, hi = action_bounds(AgentConfig(model="diff_drive", max_speed=2.0, max_ang_vel=1.5))
+    assert lo == [-2.0, -1.5] and hi == [2.0, 1.5]
+    assert drone_config().radius == 0.15
+
+
+def test_world_config_validation_and_override():
+    with pytest.raises(ValueError):
+        WorldConfig(bounds_mode="sticky")
+    with pytest.raises(ValueError):
+        WorldConfig(bounds=(1.0, -1.0, 0.0, 1.0))
+    with pytest.raises(ValueError):
+        WorldConfig(collision_k=-1.0)
+    base = WorldConfig(collision_k=100.0, bounds=(-2.0, 2.0, -2.0, 2.0), max_neighbors=16)
+    merged = base.override_with(WorldConfig(collision_c=3.0))
+    assert merged.collision_c == 3.0 and merged.bounds == (-2.0, 2.0, -2.0, 2.0)
+    assert base.override_with(None) is base
+
+
+def test_stepper_reach_check_and_unsupported_features():
+    cfgs = [AgentConfig(radius=0.2) for _ in range(2)]
+    with pytest.raises(ValueError, match="neighbor_radius"):
+        Stepper(cfgs, device="cpu", world=WorldConfig(neighbor_radius=0.1))
+    with pytest.raises(ValueError, match="substeps"):
+        Stepper(cfgs, substeps=0, device="cpu")
+    with pytest.raises(NotImplementedError):
+        Stepper(cfgs, device="cpu", world=WorldConfig(integrator=Integrator.RK4))
+    with pytest.raises(NotImplementedError):
+        Stepper([AgentConfig(shape="box", half_extents=(0.1, 0.1))], device="cpu")
+    st = Stepper(cfgs, dt=0.1, substeps=4, device="cpu", world=WorldConfig())
+    assert math.isclose(st.sub_dt, 0.025)
+    assert math.isclose(st.neighbor_radius, 2 * 0.2 + 0.02)
+    assert st.holo_velocity_only and not st.has_drone
+    with pytest.raises(NotImplementedError, match="MOVABLE"):
+        st.set_obstacles(Obstacles(pos=torch.zeros(1, 1, 2), radius=torch.ones(1),
+                                   kind=torch.ones(1, dtype=torch.int32)))
+
+
+def test_step_refuses_cpu_tensors():
+    """No CPU fallback: stepping host tensors raises instead of computing."""
+    st = Stepper([AgentConfig()], device="cpu", world=WorldConfig(collisions=False))
+    z = torch.zeros(1, 1)
+    s = TorchState(torch.zeros(1, 1, 2), z, torch.zeros(1, 1, 2), z, z)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        warp_step(st, s, torch.zeros(1, 1, 2))
+    with pytest.raises(ValueError, match="act_dim"):
+        rollout(st, s, torch.zeros(3, 1, 1))
+    with pytest.raises(TypeError):
+        warp_step(st, s, torch.zeros(1, 1, 2, dtype=torch.float64))
+
+
+def test_grad_ring_overrun():
+    st = Stepper([AgentConfig()], device="cpu", world=WorldConfig(collisions=False))
+    ring = GradRing(st, n_envs=2, act_dim=2, capacity=2)
+    ring.acquire()
+    ring.acquire()
+    with pytest.raises(RuntimeError, match="capacity"):
+        ring.acquire()
+    ring.reset()
+    ring.acquire()
+    with pytest.raises(RuntimeError, match="capacity"):
+        ring.rollout_buffers(3)
