@@ -78,16 +78,22 @@ __device__ __forceinline__ typename MaskT<PA>::type lean_cand(const P2<T> *lp, i
 }
 
 // One substep of the force pass: neighbour lists (into `incl`) and the total force.
+// Also records which listed contacts are active (`act`) and the wall contact bits, the
+// branches the reverse pass follows.
 template <typename T, int PA>
 __device__ __forceinline__ void lean_forces(const Cst<T> &C, const P2<T> *lp, const P2<T> *lv,
                                             const T *lr, int base, int me, T ra, T dd, T px,
                                             T py, T vx, T vy, bool full, bool first,
                                             typename MaskT<PA>::type &cand,
-                                            typename MaskT<PA>::type &incl, T &Fx, T &Fy)
+                                            typename MaskT<PA>::type &incl,
+                                            typename MaskT<PA>::type &act, unsigned &wbits,
+                                            T &Fx, T &Fy)
 {
     typedef typename MaskT<PA>::type M;
     T fx = T(0), fy = T(0);
     incl = 0;
+    act = 0;
+    wbits = 0u;
     if (C.collisions) {
         if (full) {
             M cd;
@@ -103,13 +109,15 @@ __device__ __forceinline__ void lean_forces(const Cst<T> &C, const P2<T> *lp, co
             const int j = base + b;
             const P2<T> q = lp[j], w = lv[j];
             T gx, gy;
-            pair_force(C, px - q.x, py - q.y, vx - w.x, vy - w.y, ra + lr[j] + C.margin, dd, gx, gy);
+            const bool on = pair_force_rec(C, px - q.x, py - q.y, vx - w.x, vy - w.y,
+                                           ra + lr[j] + C.margin, dd, gx, gy);
+            act |= on ? (M(1) << b) : M(0);
             fx += gx;
             fy += gy;
         }
     }
     T sx = T(0), sy = T(0);
-    if (C.soft_walls) wall_force(C, px, py, vx, vy, ra, dd, sx, sy);
+    if (C.soft_walls) wall_force_axes(C, px, py, vx, vy, ra, dd, sx, sy, wbits);
     Fx = fx + sx;
     Fy = fy + sy;
 }
@@ -140,7 +148,8 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
         if (t + 1 < g.nsteps) an = ld2(g.act, (size_t)(t + 1) * EA + i);
         T cnx, cny;
         clamp_norm(a.x, a.y, vmax, cnx, cny);
-        M cand = 0, incl;
+        M cand = 0, incl, act;
+        unsigned wb;
         T D = T(0);
         bool ok = false;
         for (int s = 0; s < C.S; ++s) {
@@ -153,7 +162,7 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
                     __syncthreads();
                 }
                 lean_forces<T, PA>(C, lp, lv, lr, base, me, ra, dd, p.x, p.y, v.x, v.y,
-                                   s == 0 || !ok, s == 0, cand, incl, Fx, Fy);
+                                   s == 0 || !ok, s == 0, cand, incl, act, wb, Fx, Fy);
             }
             const T vnx = cnx + Fx * dtm, vny = cny + Fy * dtm;
             const T pnx = p.x + vnx * dt, pny = p.y + vny * dt;
@@ -185,12 +194,15 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
 {
     typedef typename MaskT<PA>::type M;
     extern __shared__ __align__(16) unsigned char smem[];
-    // per substep slot: P2 pos[64], P2 vel[64]; then masks [S][64]; then gF[64], r[64], dd[64]
+    // per substep slot: P2 pos[64], P2 vel[64]; then inclusion masks [S][64], active-contact
+    // masks [S][64]; then gF[64], r[64], dd[64]; then wall bits [S][64] (bytes)
     P2<T> *slot = (P2<T> *)smem;
     M *lm = (M *)(slot + (size_t)C.S * 128);
-    P2<T> *lg = (P2<T> *)(lm + (size_t)C.S * 64);
+    M *la = lm + (size_t)C.S * 64;
+    P2<T> *lg = (P2<T> *)(la + (size_t)C.S * 64);
     T *lr = (T *)(lg + 64);
     T *ldd = lr + 64;
+    unsigned char *lw = (unsigned char *)(ldd + 64);
     const int lane = threadIdx.x, me = lane % PA, base = lane - me;
     const int env = blockIdx.x * (64 / PA) + lane / PA;
     const bool real = me < C.A;
@@ -234,7 +246,8 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
         clamp_norm(a.x, a.y, vmax, cnx, cny);
 
         // ---- recompute the substeps of step t into LDS
-        M cand = 0, incl;
+        M cand = 0, incl, act;
+        unsigned wb;
         T D = T(0);
         bool ok = false;
         for (int s = 0; s < C.S; ++s) {
@@ -244,12 +257,17 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
             sp[64 + lane] = v;
             __syncthreads();
             T Fx = T(0), Fy = T(0);
-            if (C.needs_forces)
+            if (C.needs_forces) {
                 lean_forces<T, PA>(C, sp, sp + 64, lr, base, me, ra, dd, p.x, p.y, v.x, v.y,
-                                   s == 0 || !ok, s == 0, cand, incl, Fx, Fy);
-            else
+                                   s == 0 || !ok, s == 0, cand, incl, act, wb, Fx, Fy);
+            } else {
                 incl = 0;
+                act = 0;
+                wb = 0u;
+            }
             lm[s * 64 + lane] = incl;
+            la[s * 64 + lane] = act;
+            lw[s * 64 + lane] = (unsigned char)wb;
             const T vnx = cnx + Fx * dtm, vny = cny + Fy * dtm;
             const T pnx = p.x + vnx * dt, pny = p.y + vny * dt;
             if (C.use_skin) {
@@ -287,29 +305,26 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
                     gg.y = gFy * inv_dd;
                     lg[lane] = gg;
                     __syncthreads();
-                    const M mine = lm[s * 64 + lane];
-                    M m = mine;
+                    const M mact = la[s * 64 + lane];
+                    M m = lm[s * 64 + lane];
                     while (m) {
                         const int b = m_ctz(m);
                         m &= m - 1;
                         const int j = base + b;
-                        const bool own = in_list(mine, b, C.K);
-                        const bool rev = in_list(lm[s * 64 + j], me, C.K);
+                        const bool own = (mact >> b) & M(1);
+                        const bool rev = (la[s * 64 + j] >> me) & M(1);
                         if (!own && !rev) continue;
                         const P2<T> q = sp[j], w = sp[64 + j];
                         const P2<T> gb = lg[j];
                         const T wx = (own ? gg.x : T(0)) - (rev ? gb.x : T(0));
                         const T wy = (own ? gg.y : T(0)) - (rev ? gb.y : T(0));
-                        pair_adj_combined(C, q0.x - q.x, q0.y - q.y, w0.x - w.x, w0.y - w.y,
-                                          ra + lr[j] + C.margin, wx, wy, ipx, ipy, ivx, ivy);
+                        pair_adj_active(C, q0.x - q.x, q0.y - q.y, w0.x - w.x, w0.y - w.y,
+                                        ra + lr[j] + C.margin, wx, wy, ipx, ipy, ivx, ivy);
                     }
                 }
-                if (C.soft_walls) {
-                    St<T> ga;
-                    ga.px = ipx; ga.py = ipy; ga.vx = ivx; ga.vy = ivy;
-                    wall_force_adj(C, q0.x, q0.y, w0.x, w0.y, ra, dd, gFx, gFy, ga);
-                    ipx = ga.px; ipy = ga.py; ivx = ga.vx; ivy = ga.vy;
-                }
+                if (C.soft_walls)
+                    wall_axes_adj(C, q0.x, q0.y, w0.x, w0.y, ra, dd, inv_dd, gFx, gFy,
+                                  (unsigned)lw[s * 64 + lane], ipx, ipy, ivx, ivy);
             }
             gpx = ipx;
             gpy = ipy;

@@ -120,6 +120,70 @@ __device__ __forceinline__ void pair_force(const Cst<T> &C, T dx, T dy, T rvx, T
     }
 }
 
+// pair_force that also reports whether the contact is active (overlap and a positive
+// coefficient), the branch the reverse pass must follow.
+template <typename T>
+__device__ __forceinline__ bool pair_force_rec(const Cst<T> &C, T dx, T dy, T rvx, T rvy, T md,
+                                               T dd, T &fx, T &fy)
+{
+    T dist = m_sqrt(wmax(dx * dx + dy * dy, C.eps2));
+    T ov = md - dist;
+    fx = T(0);
+    fy = T(0);
+    bool on = false;
+    if (ov > T(0)) {
+        T nx = dx / dist, ny = dy / dist;
+        T coef = normal_coeff(C, ov, rvx * nx + rvy * ny, dd);
+        fx = coef * nx;
+        fy = coef * ny;
+        on = coef > T(0);
+    }
+    return on;
+}
+
+__device__ __forceinline__ float m_rsqrt(float x) { return rsqrtf(x); }
+__device__ __forceinline__ double m_rsqrt(double x) { return rsqrt(x); }
+
+// Adjoint of one active contact pair, both forces at once (see pair_adj_combined), with
+// the branch already known from the recomputed forward pass: the arithmetic only has to
+// be accurate, so the distance comes from one reciprocal square root.
+template <typename T>
+__device__ __forceinline__ void pair_adj_active(const Cst<T> &C, T dx, T dy, T rvx, T rvy, T md,
+                                                T wx, T wy, T &adx, T &ady, T &arx, T &ary)
+{
+    const T d2 = dx * dx + dy * dy;
+    const T m2 = wmax(d2, C.eps2);
+    const T inv = m_rsqrt(m2);
+    const T dist = m2 * inv;
+    const T nx = dx * inv, ny = dy * inv;
+    const T vn = rvx * nx + rvy * ny;
+    const T ov = md - dist;
+    T o = ov, slope = T(1);
+    if (C.max_overlap > T(0)) {
+        const T th = m_tanh(ov / C.max_overlap);
+        o = C.max_overlap * th;
+        slope = T(1) - th * th;
+    }
+    const T num = C.k * o - C.c * vn;
+    const T a_num = wx * nx + wy * ny;
+    T anx = num * wx, any = num * wy;
+    const T a_ov = C.k * a_num * slope;
+    const T a_vn = -C.c * a_num;
+    arx += a_vn * nx;
+    ary += a_vn * ny;
+    anx += a_vn * rvx;
+    any += a_vn * rvy;
+    const T a_dist = -(anx * nx + any * ny) * inv - a_ov;
+    T ex = anx * inv, ey = any * inv;
+    if (d2 > C.eps2) {
+        const T h = a_dist * T(0.5) * inv;
+        ex += T(2) * dx * h;
+        ey += T(2) * dy * h;
+    }
+    adx += ex;
+    ady += ey;
+}
+
 // reverse of pair_force: accumulates the adjoints of d and rel_v
 template <typename T>
 __device__ __forceinline__ void pair_force_adj(const Cst<T> &C, T dx, T dy, T rvx, T rvy, T md,
@@ -215,6 +279,83 @@ __device__ __forceinline__ void wall_force(const Cst<T> &C, T px, T py, T vx, T 
     if (pen > T(0)) ay += -normal_coeff(C, pen, -vy, dd);
     fx = ax;
     fy = ay;
+}
+
+// _wall_forces with one contact evaluation per axis.  When the bounds are at least two
+// reaches wide an agent cannot touch both walls of an axis, so at most one of the two
+// `fx +=` terms of the reference is non-zero and the sum is that term alone (0 + x).
+// Falls back to the four-term form otherwise.  `bits` records which axes are in
+// contact with a positive coefficient (bit 0: x, bit 1: y) for the reverse pass.
+template <typename T>
+__device__ __forceinline__ void wall_force_axes(const Cst<T> &C, T px, T py, T vx, T vy, T ra,
+                                                T dd, T &fx, T &fy, unsigned &bits)
+{
+    const T reach = ra + C.margin;
+    const T w2 = T(2) * reach * T(1.00001);
+    bits = 0u;
+    if (!(C.bmax_x - C.bmin_x >= w2) || !(C.bmax_y - C.bmin_y >= w2)) {
+        wall_force(C, px, py, vx, vy, ra, dd, fx, fy);
+        bits = 3u;  // reverse pass re-derives every side
+        return;
+    }
+    const T pl = reach - (px - C.bmin_x), pr = reach - (C.bmax_x - px);
+    const T pb = reach - (py - C.bmin_y), pt = reach - (C.bmax_y - py);
+    T ax = T(0), ay = T(0);
+    if (pl > T(0) || pr > T(0)) {
+        const bool lo = pl > T(0);
+        const T cf = normal_coeff(C, lo ? pl : pr, lo ? vx : -vx, dd);
+        ax += lo ? cf : -cf;
+        bits |= cf > T(0) ? 1u : 0u;
+    }
+    if (pb > T(0) || pt > T(0)) {
+        const bool lo = pb > T(0);
+        const T cf = normal_coeff(C, lo ? pb : pt, lo ? vy : -vy, dd);
+        ay += lo ? cf : -cf;
+        bits |= cf > T(0) ? 2u : 0u;
+    }
+    fx = ax;
+    fy = ay;
+}
+
+// Reverse of wall_force_axes given its recorded contact bits; g * inv_dd = cotangent / dd.
+// For either wall of an axis d(coef)/d(p) = -k*slope/dd along the inward normal and
+// d(coef)/d(v) = -c/dd, so the side only enters through the overlap of the slope.
+template <typename T>
+__device__ __forceinline__ void wall_axes_adj(const Cst<T> &C, T px, T py, T vx, T vy, T ra,
+                                              T dd, T inv_dd, T gx, T gy, unsigned bits,
+                                              T &apx, T &apy, T &avx, T &avy)
+{
+    const T reach = ra + C.margin;
+    const T w2 = T(2) * reach * T(1.00001);
+    if (!(C.bmax_x - C.bmin_x >= w2) || !(C.bmax_y - C.bmin_y >= w2)) {
+        St<T> a;
+        a.px = apx; a.py = apy; a.vx = avx; a.vy = avy;
+        wall_force_adj(C, px, py, vx, vy, ra, dd, gx, gy, a);
+        apx = a.px; apy = a.py; avx = a.vx; avy = a.vy;
+        return;
+    }
+    if (bits & 1u) {
+        const T pl = reach - (px - C.bmin_x), pr = reach - (C.bmax_x - px);
+        T slope = T(1);
+        if (C.max_overlap > T(0)) {
+            const T th = m_tanh((pl > T(0) ? pl : pr) / C.max_overlap);
+            slope = T(1) - th * th;
+        }
+        const T q = gx * inv_dd;
+        apx -= C.k * slope * q;
+        avx -= C.c * q;
+    }
+    if (bits & 2u) {
+        const T pb = reach - (py - C.bmin_y), pt = reach - (C.bmax_y - py);
+        T slope = T(1);
+        if (C.max_overlap > T(0)) {
+            const T th = m_tanh((pb > T(0) ? pb : pt) / C.max_overlap);
+            slope = T(1) - th * th;
+        }
+        const T q = gy * inv_dd;
+        apy -= C.k * slope * q;
+        avy -= C.c * q;
+    }
 }
 
 template <typename T>

@@ -293,7 +293,8 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
     }
     if (C.soft_walls) {
         T gx, gy;
-        wall_force(C, st.px, st.py, st.vx, st.vy, L.pr.radius, L.dd, gx, gy);
+        unsigned wb;
+        wall_force_axes(C, st.px, st.py, st.vx, st.vy, L.pr.radius, L.dd, gx, gy, wb);
         sx += gx;
         sy += gy;
     }
@@ -814,7 +815,8 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     if (lean_ok(d)) {
         const size_t msz = PA == 64 ? 8 : 4;
         const size_t lshm = (size_t)d->substeps * 128 * 2 * sizeof(T) +
-                            (size_t)d->substeps * 64 * msz + 64 * 2 * sizeof(T) + 2 * 64 * sizeof(T);
+                            (size_t)d->substeps * 64 * msz * 2 + 64 * 2 * sizeof(T) +
+                            2 * 64 * sizeof(T) + (size_t)d->substeps * 64;
         if (lshm > 65536) return fail("substeps too large for the backward LDS staging (limit 64 KiB per wave)");
         launch_holo_bwd<T>(PA, C, a, lshm, st);
         hipError_t e = hipGetLastError();
