@@ -143,11 +143,14 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
     const T th = g.s0.f[1][i];
     const size_t EA = (size_t)C.E * C.A;
     P2<T> a = ld2(g.act, i);
+    // resolve the initial loads here: a load still in flight at the loop entry makes every
+    // iteration wait for all outstanding memory operations, prefetch and stores included
+    __builtin_amdgcn_s_waitcnt(0);
+    T cnx, cny;  // the step's clamped velocity command
+    clamp_norm(a.x, a.y, vmax, cnx, cny);
     for (int t = 0; t < g.nsteps; ++t) {
         P2<T> an = a;
         if (t + 1 < g.nsteps) an = ld2(g.act, (size_t)(t + 1) * EA + i);
-        T cnx, cny;
-        clamp_norm(a.x, a.y, vmax, cnx, cny);
         M cand = 0, incl, act;
         unsigned wb;
         T D = T(0);
@@ -175,6 +178,10 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
             v.x = vnx;
             v.y = vny;
         }
+        // use the prefetched action before issuing this step's stores: memory operations
+        // complete in order, so waiting for it afterwards would also wait for the stores
+        clamp_norm(an.x, an.y, vmax, cnx, cny);
+        asm volatile("" ::"v"(cnx), "v"(cny));  // keeps the use ahead of the stores
         if (active) {
             const bool last = t + 1 == g.nsteps;
             T *const *f = last ? g.fin.f : g.traj.f;
@@ -185,7 +192,6 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
             f[3][j] = m_sqrt(v.x * v.x + v.y * v.y);
             f[4][j] = T(0);
         }
-        a = an;
     }
 }
 
@@ -223,23 +229,41 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
     P2<T> p = t == 0 ? ld2(g.s0.f[0], i) : ld2(g.traj.f[0], (size_t)(t - 1) * EA + i);
     P2<T> v = t == 0 ? ld2(g.s0.f[2], i) : ld2(g.traj.f[2], (size_t)(t - 1) * EA + i);
     P2<T> a = ld2(g.act, (size_t)t * EA + i);
+    // adjoint arriving at step t's outputs (pos, theta, vel, speed); null fields carry none
+    struct Arr {
+        P2<T> p, v;
+        T th, s;
+    };
+    auto arrival = [&](int tt) {
+        Arr r;
+        const T *const *f = tt == g.nsteps - 1 ? g.afin.f : g.atraj.f;
+        const size_t j = tt == g.nsteps - 1 ? i : (size_t)tt * EA + i;
+        const P2<T> z = {T(0), T(0)};
+        r.p = f[0] ? ld2(f[0], j) : z;
+        r.th = f[1] ? f[1][j] : T(0);
+        r.v = f[2] ? ld2(f[2], j) : z;
+        r.s = f[3] ? f[3][j] : T(0);
+        return r;
+    };
+    Arr arr = arrival(t);
+    // resolve the initial loads here: a load still in flight at the loop entry makes every
+    // iteration wait for all outstanding memory operations, prefetch and stores included
+    __builtin_amdgcn_s_waitcnt(0);
     for (; t >= 0; --t) {
-        // adjoint arriving at this step's output
-        {
-            const T *const *f = t == g.nsteps - 1 ? g.afin.f : g.atraj.f;
-            const size_t j = t == g.nsteps - 1 ? i : (size_t)t * EA + i;
-            if (f[0]) { P2<T> q = ld2(f[0], j); gpx += q.x; gpy += q.y; }
-            if (f[1]) gth += f[1][j];
-            if (f[2]) { P2<T> q = ld2(f[2], j); gvx += q.x; gvy += q.y; }
-        }
-        const T *gsp = t == g.nsteps - 1 ? g.afin.f[3] : g.atraj.f[3];
-        const T gs = gsp ? gsp[t == g.nsteps - 1 ? i : (size_t)t * EA + i] : T(0);
-        // prefetch the previous step's inputs
+        gpx += arr.p.x;
+        gpy += arr.p.y;
+        gth += arr.th;
+        gvx += arr.v.x;
+        gvy += arr.v.y;
+        const T gs = arr.s;
+        // prefetch the previous step's inputs and arriving adjoint
         P2<T> pn = p, vn = v, an = a;
+        Arr arn = arr;
         if (t > 0) {
             pn = t - 1 == 0 ? ld2(g.s0.f[0], i) : ld2(g.traj.f[0], (size_t)(t - 2) * EA + i);
             vn = t - 1 == 0 ? ld2(g.s0.f[2], i) : ld2(g.traj.f[2], (size_t)(t - 2) * EA + i);
             an = ld2(g.act, (size_t)(t - 1) * EA + i);
+            arn = arrival(t - 1);
         }
         if (!real) p.x = p.y = qnan;
         T cnx, cny;
@@ -331,6 +355,11 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
             gvx = ivx;
             gvy = ivy;
         }
+        // use the prefetched values before issuing this step's stores: memory operations
+        // complete in order, so waiting for them afterwards would also wait for the stores
+        asm volatile("" ::"v"(pn.x), "v"(pn.y), "v"(vn.x), "v"(vn.y), "v"(an.x), "v"(an.y),
+                     "v"(arn.p.x), "v"(arn.p.y), "v"(arn.v.x), "v"(arn.v.y), "v"(arn.th),
+                     "v"(arn.s));
         if (active) {
             T ax = T(0), ay = T(0);
             clamp_norm_adj(a.x, a.y, vmax, gcx, gcy, ax, ay);
@@ -342,6 +371,7 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
         p = pn;
         v = vn;
         a = an;
+        arr = arn;
     }
     if (active) {
         T *const *f = g.a0.f;
