@@ -82,8 +82,9 @@ __device__ __forceinline__ typename MaskT<PA>::type lean_cand(const P2<T> *lp, i
 // branches the reverse pass follows.
 template <typename T, int PA>
 __device__ __forceinline__ void lean_forces(const Cst<T> &C, const P2<T> *lp, const P2<T> *lv,
-                                            const T *lr, int base, int me, T ra, T dd, T px,
-                                            T py, T vx, T vy, bool full, bool first,
+                                            const T *lr, int base, int me, T ra,
+                                            const Dv<T> &dd, T px, T py, T vx, T vy, bool full,
+                                            bool first,
                                             typename MaskT<PA>::type &cand,
                                             typename MaskT<PA>::type &incl,
                                             typename MaskT<PA>::type &act, unsigned &wbits,
@@ -109,8 +110,8 @@ __device__ __forceinline__ void lean_forces(const Cst<T> &C, const P2<T> *lp, co
             const int j = base + b;
             const P2<T> q = lp[j], w = lv[j];
             T gx, gy;
-            const bool on = pair_force_rec(C, px - q.x, py - q.y, vx - w.x, vy - w.y,
-                                           ra + lr[j] + C.margin, dd, gx, gy);
+            const bool on = pair_force_rec_r(C, px - q.x, py - q.y, vx - w.x, vy - w.y,
+                                             ra + lr[j] + C.margin, dd, gx, gy);
             act |= on ? (M(1) << b) : M(0);
             fx += gx;
             fy += gy;
@@ -136,6 +137,7 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
     const T *prow = g.params + (real ? me : 0) * 22;
     const T ra = prow[0], mass = prow[1], vmax = prow[2];
     const T dt = C.sub_dt, dtm = dt / mass, dd = T(1) + C.c * C.sub_dt / mass;
+    const Dv<T> ddv = divisor(dd, true);
     lr[lane] = ra;
     const T qnan = __builtin_nan("");
     P2<T> p = ld2(g.s0.f[0], i), v = ld2(g.s0.f[2], i);
@@ -164,7 +166,7 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
                     lv[lane] = v;
                     __syncthreads();
                 }
-                lean_forces<T, PA>(C, lp, lv, lr, base, me, ra, dd, p.x, p.y, v.x, v.y,
+                lean_forces<T, PA>(C, lp, lv, lr, base, me, ra, ddv, p.x, p.y, v.x, v.y,
                                    s == 0 || !ok, s == 0, cand, incl, act, wb, Fx, Fy);
             }
             const T vnx = cnx + Fx * dtm, vny = cny + Fy * dtm;
@@ -217,6 +219,7 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
     const T *prow = g.params + (real ? me : 0) * 22;
     const T ra = prow[0], mass = prow[1], vmax = prow[2];
     const T dt = C.sub_dt, dtm = dt / mass, dd = T(1) + C.c * C.sub_dt / mass;
+    const Dv<T> ddv = divisor(dd, true);
     const T inv_dd = T(1) / dd;
     lr[lane] = ra;
     ldd[lane] = dd;
@@ -282,7 +285,7 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
             __syncthreads();
             T Fx = T(0), Fy = T(0);
             if (C.needs_forces) {
-                lean_forces<T, PA>(C, sp, sp + 64, lr, base, me, ra, dd, p.x, p.y, v.x, v.y,
+                lean_forces<T, PA>(C, sp, sp + 64, lr, base, me, ra, ddv, p.x, p.y, v.x, v.y,
                                    s == 0 || !ok, s == 0, cand, incl, act, wb, Fx, Fy);
             } else {
                 incl = 0;

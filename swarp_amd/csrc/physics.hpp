@@ -67,6 +67,7 @@ template <typename T> struct Cst {
     T bmin_x, bmin_y, bmax_x, bmax_y;
     int E, A, ad, S, K, N;
     int collisions, soft_walls, clamp, needs_forces, use_skin;
+    int fast_div;  // neighbour radius <= 2^20: contact distances are short-division divisors
 };
 
 // Obstacle arrays (device); shared extents [N], per-env poses [E,N].
@@ -74,6 +75,83 @@ template <typename T> struct Obs {
     const T *pos, *rad, *ang, *half, *vel, *om;
     const int32_t *type;
 };
+
+// ---------------------------------------------- exact fp32 arithmetic, restricted ranges
+//
+// The build keeps fp32 division and sqrt correctly rounded; the compiler's general
+// sequences also scale tiny or huge operands and fix up special values.  Where the
+// operands are known to lie in a range in which those steps are identities, the
+// remaining steps are spelled out below, in the compiler's order, so the results are the
+// same bits with fewer instructions, and a division by a per-lane constant reuses one
+// refined reciprocal.  fp64 keeps the plain operators.
+
+// Correctly rounded sqrt(x) for finite x >= 2^-96: hardware estimate, then the two
+// one-ulp residual corrections.
+__device__ __forceinline__ float sqrt_rn_big(float x)
+{
+    const float s = __builtin_amdgcn_sqrtf(x);
+    const float sm = __int_as_float(__float_as_int(s) - 1);
+    const float sp = __int_as_float(__float_as_int(s) + 1);
+    const float rm = __builtin_fmaf(-sm, s, x);
+    const float rp = __builtin_fmaf(-sp, s, x);
+    const float s1 = rm <= 0.0f ? sm : s;
+    return rp > 0.0f ? sp : s1;
+}
+__device__ __forceinline__ double sqrt_rn_big(double x) { return sqrt(x); }
+
+// Refined reciprocal of a divisor d in [2^-60, 2^20] (one Newton step on the estimate).
+__device__ __forceinline__ float rcp_refined(float d)
+{
+    const float r0 = __builtin_amdgcn_rcpf(d);
+    const float e = __builtin_fmaf(-d, r0, 1.0f);
+    return __builtin_fmaf(e, r0, r0);
+}
+__device__ __forceinline__ double rcp_refined(double) { return 0.0; }
+
+// n / d correctly rounded given r = rcp_refined(d), for d in [2^-60, 2^20] and
+// 2^-100 <= |n| <= 2^30: two residual corrections of the quotient estimate.
+__device__ __forceinline__ float div_rn_core(float n, float d, float r)
+{
+    float q = n * r;
+    float e = __builtin_fmaf(-d, q, n);
+    q = __builtin_fmaf(e, r, q);
+    e = __builtin_fmaf(-d, q, n);
+    return __builtin_fmaf(e, r, q);
+}
+
+// A divisor with its refined reciprocal.  `hi` bounds the numerators the short sequence
+// takes: 2^30 when d is in [2^-60, 2^20], else -1 (every division takes the general path).
+template <typename T> struct Dv {
+    T d, r, hi;
+};
+template <typename T> __device__ __forceinline__ Dv<T> divisor(T d, bool ok)
+{
+    Dv<T> v;
+    v.d = d;
+    v.r = rcp_refined(d);
+    v.hi = (ok && d >= T(0x1p-60) && d <= T(0x1p20)) ? T(0x1p30) : T(-1);
+    return v;
+}
+
+// A divisor known to lie in [2^-60, 2^20] whenever `ok` holds.
+template <typename T> __device__ __forceinline__ Dv<T> divisor_in_range(T d, bool ok)
+{
+    Dv<T> v;
+    v.d = d;
+    v.r = rcp_refined(d);
+    v.hi = ok ? T(0x1p30) : T(-1);
+    return v;
+}
+
+// n / d, correctly rounded; zero, tiny, huge or NaN numerators take the general division.
+template <typename T> __device__ __forceinline__ T div_rn(T n, const Dv<T> &v) { return n / v.d; }
+__device__ __forceinline__ float div_rn(float n, const Dv<float> &v)
+{
+    const float a = fabsf(n);
+    float q = div_rn_core(n, v.d, v.r);
+    if (__builtin_expect(!(a >= 0x1p-100f && a <= v.hi), 0)) q = n / v.d;
+    return q;
+}
 
 // ------------------------------------------------------------- contact law
 
@@ -84,6 +162,15 @@ __device__ __forceinline__ T normal_coeff(const Cst<T> &C, T ov, T vn, T dd)
     T o = ov;
     if (C.max_overlap > T(0)) o = C.max_overlap * m_tanh(ov / C.max_overlap);
     return wmax((C.k * o - C.c * vn) / dd, T(0));
+}
+
+// normal_coeff with the damping denominator as a prepared divisor (same result)
+template <typename T>
+__device__ __forceinline__ T normal_coeff_r(const Cst<T> &C, T ov, T vn, const Dv<T> &dd)
+{
+    T o = ov;
+    if (C.max_overlap > T(0)) o = C.max_overlap * m_tanh(ov / C.max_overlap);
+    return wmax(div_rn(C.k * o - C.c * vn, dd), T(0));
 }
 
 template <typename T>
@@ -134,6 +221,28 @@ __device__ __forceinline__ bool pair_force_rec(const Cst<T> &C, T dx, T dy, T rv
     if (ov > T(0)) {
         T nx = dx / dist, ny = dy / dist;
         T coef = normal_coeff(C, ov, rvx * nx + rvy * ny, dd);
+        fx = coef * nx;
+        fy = coef * ny;
+        on = coef > T(0);
+    }
+    return on;
+}
+
+// pair_force_rec with the range-restricted exact arithmetic: the distance is at least
+// sqrt(eps2) and at most the neighbour radius, |d| <= distance; rdd = rcp_refined(dd).
+template <typename T>
+__device__ __forceinline__ bool pair_force_rec_r(const Cst<T> &C, T dx, T dy, T rvx, T rvy,
+                                                 T md, const Dv<T> &dd, T &fx, T &fy)
+{
+    T dist = sqrt_rn_big(wmax(dx * dx + dy * dy, C.eps2));
+    T ov = md - dist;
+    fx = T(0);
+    fy = T(0);
+    bool on = false;
+    if (ov > T(0)) {
+        const Dv<T> ds = divisor_in_range(dist, C.fast_div != 0);  // sqrt(eps2) <= dist
+        T nx = div_rn(dx, ds), ny = div_rn(dy, ds);
+        T coef = normal_coeff_r(C, ov, rvx * nx + rvy * ny, dd);
         fx = coef * nx;
         fy = coef * ny;
         on = coef > T(0);
@@ -288,8 +397,9 @@ __device__ __forceinline__ void wall_force(const Cst<T> &C, T px, T py, T vx, T 
 // contact with a positive coefficient (bit 0: x, bit 1: y) for the reverse pass.
 template <typename T>
 __device__ __forceinline__ void wall_force_axes(const Cst<T> &C, T px, T py, T vx, T vy, T ra,
-                                                T dd, T &fx, T &fy, unsigned &bits)
+                                                const Dv<T> &dv, T &fx, T &fy, unsigned &bits)
 {
+    const T dd = dv.d;
     const T reach = ra + C.margin;
     const T w2 = T(2) * reach * T(1.00001);
     bits = 0u;
@@ -303,13 +413,13 @@ __device__ __forceinline__ void wall_force_axes(const Cst<T> &C, T px, T py, T v
     T ax = T(0), ay = T(0);
     if (pl > T(0) || pr > T(0)) {
         const bool lo = pl > T(0);
-        const T cf = normal_coeff(C, lo ? pl : pr, lo ? vx : -vx, dd);
+        const T cf = normal_coeff_r(C, lo ? pl : pr, lo ? vx : -vx, dv);
         ax += lo ? cf : -cf;
         bits |= cf > T(0) ? 1u : 0u;
     }
     if (pb > T(0) || pt > T(0)) {
         const bool lo = pb > T(0);
-        const T cf = normal_coeff(C, lo ? pb : pt, lo ? vy : -vy, dd);
+        const T cf = normal_coeff_r(C, lo ? pb : pt, lo ? vy : -vy, dv);
         ay += lo ? cf : -cf;
         bits |= cf > T(0) ? 2u : 0u;
     }

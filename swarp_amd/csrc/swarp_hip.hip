@@ -221,6 +221,7 @@ template <typename T, int PA> struct Lane {
     Prm<T> pr;
     T dd;          // implicit damping denominator 1 + c*sub_dt/m (collisions.py:845)
     T inv_dd;      // 1 / dd (adjoint arithmetic only)
+    Dv<T> ddv;     // dd as a prepared divisor (exact fp32 division by dd)
 };
 
 template <typename T, int PA>
@@ -239,6 +240,7 @@ __device__ __forceinline__ void lane_init(const Cst<T> &C, const Args<T> &g, Lan
     load_prm(g, ag, L.pr);
     L.dd = T(1) + C.c * C.sub_dt / L.pr.mass;
     L.inv_dd = T(1) / L.dd;
+    L.ddv = divisor(L.dd, true);
 }
 
 // Whether every real agent of this lane's env stayed within the skin budget.
@@ -294,7 +296,7 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
     if (C.soft_walls) {
         T gx, gy;
         unsigned wb;
-        wall_force_axes(C, st.px, st.py, st.vx, st.vy, L.pr.radius, L.dd, gx, gy, wb);
+        wall_force_axes(C, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv, gx, gy, wb);
         sx += gx;
         sy += gy;
     }
@@ -628,6 +630,9 @@ template <typename T> static int fill_cst(const swarp_desc_t *d, double skin, Cs
     C.clamp = d->clamp_bounds;
     C.needs_forces = (d->collisions || d->soft_walls || d->n_obstacles > 0) ? 1 : 0;
     C.use_skin = (d->collisions && d->substeps > 1 && skin > 0.0) ? 1 : 0;
+    // contact distances lie in [sqrt(eps2), neighbour radius]: within the range of the
+    // short exact division when the radius is at most 2^20
+    C.fast_div = d->neighbor_radius <= 0x1p20 ? 1 : 0;
     return 0;
 }
 
