@@ -306,11 +306,14 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
             v.x = vnx;
             v.y = vny;
         }
-        // speed output = |v| of the last substep (zero gradient at v = 0)
-        const T spd = m_sqrt(v.x * v.x + v.y * v.y);
-        if (spd > T(0)) {
-            gvx += gs * v.x / spd;
-            gvy += gs * v.y / spd;
+        // speed output = |v| of the last substep (zero gradient at v = 0); skipped where no
+        // adjoint arrives at it, since it would add exactly zero
+        if (gs != T(0)) {
+            const T spd = m_sqrt(v.x * v.x + v.y * v.y);
+            if (spd > T(0)) {
+                gvx += gs * v.x / spd;
+                gvy += gs * v.y / spd;
+            }
         }
 
         // ---- reverse pass over the substeps
@@ -365,7 +368,7 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
                      "v"(arn.s));
         if (active) {
             T ax = T(0), ay = T(0);
-            clamp_norm_adj(a.x, a.y, vmax, gcx, gcy, ax, ay);
+            clamp_norm_adj_rcp(a.x, a.y, vmax, gcx, gcy, ax, ay);
             T *pa = g.aact + ((size_t)t * EA + i) * C.ad;
             pa[0] = ax;
             if (C.ad > 1) pa[1] = ay;

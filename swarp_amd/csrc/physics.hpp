@@ -719,6 +719,28 @@ __device__ __forceinline__ void clamp_norm_adj(T x, T y, T lim, T gx, T gy, T &a
     ay += ry;
 }
 
+__device__ __forceinline__ float m_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ double m_rcp(double x) { return 1.0 / x; }
+
+// clamp_norm_adj with reciprocal estimates in place of the correctly rounded divisions:
+// the branch (len > lim) is decided on the exact length, as the forward pass decided it;
+// the adjoint values only need to be accurate (a few ulp in float32, exact in float64).
+template <typename T>
+__device__ __forceinline__ void clamp_norm_adj_rcp(T x, T y, T lim, T gx, T gy, T &ax, T &ay)
+{
+    const T len = m_sqrt(x * x + y * y);
+    if (len > lim) {
+        const T il = m_rcp(len);
+        const T sc = lim * il;
+        const T am = -(gx * x + gy * y) * sc * il;
+        ax += gx * sc + am * x * il;
+        ay += gy * sc + am * y * il;
+    } else {
+        ax += gx;
+        ay += gy;
+    }
+}
+
 // Semi-implicit Euler substep of one agent: _integrate_agent + _step_2d
 // (swarp/dynamics/kernels.py:194-413).  `o` receives the new state.
 template <typename T, bool DRONE>

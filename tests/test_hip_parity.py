@@ -169,6 +169,25 @@ def test_specialised_matches_generic_kernels():
     assert rel(a[2], b[2]) <= 1e-6 and rel(a[1][..., :7], b[1][..., :7]) <= 1e-6
 
 
+def test_partial_last_wave():
+    """n_envs that leave the last wave partly empty: the specialised kernels hold two envs
+    per lane (2 * 64 / PA envs per wave), so an env count that is not a multiple of that
+    leaves slot-1 envs, or whole rows, past n_envs."""
+    for A, E in ((4, 45), (16, 37), (16, 3), (64, 3)):
+        T, S = 5, 2
+        rng = np.random.default_rng(100 + A + E)
+        s0 = pack_state({"pos": rng.uniform(-0.5, 0.5, size=(E, A, 2))}).astype(np.float32)
+        acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
+        cfgs = nav_agents(A)
+        world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.025,
+                            bounds=(-0.6, 0.6, -0.6, 0.6), max_neighbors=min(32, max(4, A)))
+        w = _cotangent(T, E, A, 9)
+        st = make_stepper(cfgs, world, 0.05, S, torch.float32)
+        hip = hip_run(st, s0, acts, w, np.float32)
+        orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float32)
+        _check(f"partial A={A} E={E}", hip, orc, state_exact=True)
+
+
 def test_padded_agent_slots():
     """n_agents not a power of two (pad lanes in every env slot): 5, 12 and 20 agents."""
     for A, K in ((5, 4), (12, 12), (20, 8)):
