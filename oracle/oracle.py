@@ -35,6 +35,7 @@ class OracleCfg(ctypes.Structure):
         ("neighbor_radius", ctypes.c_double),
         ("bmin_x", ctypes.c_double), ("bmin_y", ctypes.c_double),
         ("bmax_x", ctypes.c_double), ("bmax_y", ctypes.c_double),
+        ("lin_damping", ctypes.c_double), ("ang_damping", ctypes.c_double),
     ]
 
 
@@ -44,6 +45,8 @@ class OracleObs(ctypes.Structure):
         ("pos", ctypes.c_void_p), ("radius", ctypes.c_void_p), ("angle", ctypes.c_void_p),
         ("half", ctypes.c_void_p), ("vel", ctypes.c_void_p), ("ang_vel", ctypes.c_void_p),
         ("type", ctypes.c_void_p),
+        ("kind", ctypes.c_void_p), ("body", ctypes.c_void_p),
+        ("mass", ctypes.c_void_p), ("inertia", ctypes.c_void_p), ("body_off", ctypes.c_void_p),
     ]
 
 
@@ -120,6 +123,16 @@ class Oracle:
         for k in ("pos", "radius", "angle", "half", "vel", "ang_vel"):
             arrs[k] = np.ascontiguousarray(obs[k], dtype=self.dtype)
         arrs["type"] = np.ascontiguousarray(obs["type"], dtype=np.int32)
+        if obs.get("kind") is not None:
+            n = arrs["radius"].shape[0]
+            arrs["kind"] = np.ascontiguousarray(obs["kind"], dtype=np.int32)
+            body = obs.get("body")
+            arrs["body"] = np.ascontiguousarray(np.arange(n) if body is None else body, dtype=np.int32)
+            arrs["mass"] = np.ascontiguousarray(obs.get("mass", np.ones(n)), dtype=self.dtype)
+            arrs["inertia"] = np.ascontiguousarray(obs.get("inertia", np.ones(n)), dtype=self.dtype)
+            off = obs.get("body_off")
+            arrs["body_off"] = np.ascontiguousarray(np.zeros((n, 2)) if off is None else off,
+                                                    dtype=self.dtype)
         keep.append(arrs)
         o.n_obstacles = int(arrs["radius"].shape[0])
         for k, v in arrs.items():
@@ -171,6 +184,50 @@ class Oracle:
         if rc != 0:
             raise RuntimeError("oracle_rollout_adj failed")
         return a0, aact
+
+    def rollout_ob(self, cfg, params, tags, modes, obs, state0, ob0, actions):
+        """Rollout with the obstacle state (``[E, 12 N]`` per step: shape pos, angle, vel,
+        ang_vel, then the body state of each root) carried along; returns (states, ob)."""
+        keep = []
+        c = self._cfg(cfg)
+        p, t, m = self._prm(params, tags, modes, keep)
+        o = self._obs(obs, keep)
+        s0 = np.ascontiguousarray(state0, dtype=self.dtype)
+        b0 = None if ob0 is None else np.ascontiguousarray(ob0, dtype=self.dtype)
+        act = np.ascontiguousarray(actions, dtype=self.dtype)
+        T = act.shape[0]
+        E = s0.shape[0]
+        out = np.zeros((T,) + s0.shape, dtype=self.dtype)
+        obo = np.zeros((T, E, 12 * o.n_obstacles), dtype=self.dtype)
+        fn = self._fn("rollout_ob")
+        fn.restype = ctypes.c_int
+        rc = fn(ctypes.byref(c), _p(p), _p(t), _p(m), ctypes.byref(o), ctypes.c_int(T), _p(s0),
+                _p(b0), _p(act), _p(out), _p(obo))
+        if rc != 0:
+            raise RuntimeError("oracle_rollout_ob failed")
+        return out, obo
+
+    def rollout_adj_ob(self, cfg, params, tags, modes, obs, state0, ob0, actions, states, ob_states,
+                       adj_states=None, adj_final=None, adj_ob_states=None, adj_ob_final=None):
+        keep = []
+        c = self._cfg(cfg)
+        p, t, m = self._prm(params, tags, modes, keep)
+        o = self._obs(obs, keep)
+        cast = lambda a: None if a is None else np.ascontiguousarray(a, dtype=self.dtype)  # noqa: E731
+        s0, b0, act, st, obst = cast(state0), cast(ob0), cast(actions), cast(states), cast(ob_states)
+        ast, afin, aob, aobf = cast(adj_states), cast(adj_final), cast(adj_ob_states), cast(adj_ob_final)
+        T = act.shape[0]
+        a0 = np.zeros_like(s0)
+        aob0 = np.zeros((s0.shape[0], 12 * o.n_obstacles), dtype=self.dtype)
+        aact = np.zeros_like(act)
+        fn = self._fn("rollout_adj_ob")
+        fn.restype = ctypes.c_int
+        rc = fn(ctypes.byref(c), _p(p), _p(t), _p(m), ctypes.byref(o), ctypes.c_int(T), _p(s0),
+                _p(b0), _p(act), _p(st), _p(obst), _p(ast), _p(afin), _p(aob), _p(aobf), _p(a0),
+                _p(aob0), _p(aact))
+        if rc != 0:
+            raise RuntimeError("oracle_rollout_adj_ob failed")
+        return a0, aob0, aact
 
     def neighbors(self, pos, radius, K):
         pos = np.ascontiguousarray(pos, dtype=self.dtype)

@@ -42,7 +42,19 @@ typedef struct {
        vel [E,N,2], ang_vel [E,N] */
     const REAL *o_pos, *o_rad, *o_ang, *o_half, *o_vel, *o_om;
     const int32_t *o_type;
+    /* movable compound bodies (swarp/core/config.py:70-78): kind [N] (1 = MOVABLE),
+       mass [N], inertia [N], body [N] (root shape of each shape), body_off [N,2] */
+    const int32_t *o_kind, *o_body;
+    const REAL *o_mass, *o_inertia, *o_off;
+    REAL lin_damping, ang_damping;
+    int any_movable;
 } FN(ctx_t);
+
+/* Per-env obstacle state, 12 reals per obstacle index o:
+     [6*o .. 6*o+5]        shape o:  pos x, pos y, angle, vel x, vel y, ang_vel
+     [6*N+6*o .. 6*N+6*o+5] body rooted at o: pos x, pos y, angle, vel x, vel y, ang_vel
+   (the reference's obs_* and body_* arrays, swarp/core/stepper.py:418-431). */
+#define OB_W 12
 
 /* ------------------------------------------------------------ small helpers */
 
@@ -59,6 +71,43 @@ static inline REAL FN(rclamp_gx)(REAL x, REAL a, REAL b, REAL g)
     if (x < a) return (REAL)0;
     if (x > b) return (REAL)0;
     return g;
+}
+
+/* sin and cos of a body angle, identical on every IEEE platform: Cody-Waite reduction
+   by pi/2 (pi/2 split in a 33-bit head and a tail, so k * head is exact for |k| < 2^20)
+   and the Taylor series of sin and cos on |r| <= pi/4 to r^17 / r^18, all in double
+   precision, then rounded to REAL.  The device build evaluates the same operations in
+   the same order (swarp_amd/csrc/physics.hpp, sincos_portable), which makes body poses
+   bit-identical between the two. */
+static inline void FN(psincos)(REAL xr, REAL *so, REAL *co)
+{
+    const double x = (double)xr;
+    const double k = rint(x * 0x1.45f306dc9c883p-1);
+    const double r = (x - k * 0x1.921fb544p+0) - k * 0x1.0b4611a626331p-34;
+    const double z = r * r;
+    double ps = 0x1.952c77030ad4ap-49;
+    ps = ps * z - 0x1.ae7f3e733b81fp-41;
+    ps = ps * z + 0x1.6124613a86d09p-33;
+    ps = ps * z - 0x1.ae64567f544e4p-26;
+    ps = ps * z + 0x1.71de3a556c734p-19;
+    ps = ps * z - 0x1.a01a01a01a01ap-13;
+    ps = ps * z + 0x1.1111111111111p-7;
+    ps = ps * z - 0x1.5555555555555p-3;
+    const double sn = r + r * (z * ps);
+    double pc = -0x1.6827863b97d97p-53;
+    pc = pc * z + 0x1.ae7f3e733b81fp-45;
+    pc = pc * z - 0x1.93974a8c07c9dp-37;
+    pc = pc * z + 0x1.1eed8eff8d898p-29;
+    pc = pc * z - 0x1.27e4fb7789f5cp-22;
+    pc = pc * z + 0x1.a01a01a01a01ap-16;
+    pc = pc * z - 0x1.6c16c16c16c17p-10;
+    pc = pc * z + 0x1.5555555555555p-5;
+    const double cn = (1.0 - z * 0.5) + (z * z) * pc;
+    const long long q = (long long)k & 3;
+    const double s_ = q == 0 ? sn : (q == 1 ? cn : (q == 2 ? -sn : -cn));
+    const double c_ = q == 0 ? cn : (q == 1 ? -sn : (q == 2 ? -cn : sn));
+    *so = (REAL)s_;
+    *co = (REAL)c_;
 }
 
 /* clamp_norm (swarp/dynamics/kernels.py:68-71): v * (limit / max(length(v), limit)) */
@@ -162,6 +211,14 @@ static inline void FN(pair_force_adj)(const FN(ctx_t) *C, REAL dx, REAL dy, REAL
     }
     *adx += gdx;
     *ady += gdy;
+}
+
+/* Whether the body pass re-installs shape s (it belongs to a movable body). */
+static inline int FN(shape_moves)(const FN(ctx_t) *C, int s)
+{
+    if (!C->any_movable) return 0;
+    int r = C->o_body[s];
+    return C->o_body[r] == r && C->o_kind[r] == 1;
 }
 
 /* shape_bound / bounds_apart (swarp/core/collisions.py:61-84) */
@@ -320,20 +377,21 @@ static inline void FN(closest_on_segment)(REAL px, REAL py, REAL cx, REAL cy, RE
 }
 
 /* One obstacle's force on an agent; returns 0 if skipped by the broad phase. */
-static inline void FN(obstacle_force)(const FN(ctx_t) *C, int e, int o, REAL px, REAL py,
-                                      REAL vx, REAL vy, REAL ra, REAL dd, REAL *fx, REAL *fy)
+static inline void FN(obstacle_force)(const FN(ctx_t) *C, const REAL *od, int o, REAL px,
+                                      REAL py, REAL vx, REAL vy, REAL ra, REAL dd, REAL *fx,
+                                      REAL *fy)
 {
-    int N = C->n_obs;
-    REAL cx = C->o_pos[(e * N + o) * 2], cy = C->o_pos[(e * N + o) * 2 + 1];
+    const REAL *sh = od + 6 * o;  /* this env's shape state: pos, angle, vel, ang_vel */
+    REAL cx = sh[0], cy = sh[1];
     int st = C->o_type[o];
     REAL ro = C->o_rad[o], hx = C->o_half[o * 2], hy = C->o_half[o * 2 + 1];
     *fx = (REAL)0;
     *fy = (REAL)0;
     if (FN(bounds_apart)(px - cx, py - cy, ra + C->margin + FN(shape_bound)(st, ro, hx, hy)))
         return;
-    REAL vox = C->o_vel[(e * N + o) * 2], voy = C->o_vel[(e * N + o) * 2 + 1];
-    REAL om = C->o_om[e * N + o];
-    REAL ang = C->o_ang[e * N + o];
+    REAL vox = sh[3], voy = sh[4];
+    REAL om = sh[5];
+    REAL ang = sh[2];
     if (st == 1) {
         FN(box_force)(C, px, py, vx, vy, cx, cy, ang, hx, hy, ra + C->margin, dd, vox, voy, om,
                       fx, fy);
@@ -348,19 +406,22 @@ static inline void FN(obstacle_force)(const FN(ctx_t) *C, int e, int o, REAL px,
     }
 }
 
-static inline void FN(obstacle_force_adj)(const FN(ctx_t) *C, int e, int o, REAL px, REAL py,
-                                          REAL vx, REAL vy, REAL ra, REAL dd, REAL gfx, REAL gfy,
-                                          REAL *apx, REAL *apy, REAL *avx, REAL *avy)
+/* Reverse of obstacle_force.  `god` (nullable) receives the adjoint of a MOVABLE (circle)
+   shape's state; static obstacles are constants of the step. */
+static inline void FN(obstacle_force_adj)(const FN(ctx_t) *C, const REAL *od, int o, REAL px,
+                                          REAL py, REAL vx, REAL vy, REAL ra, REAL dd, REAL gfx,
+                                          REAL gfy, REAL *apx, REAL *apy, REAL *avx, REAL *avy,
+                                          REAL *god)
 {
-    int N = C->n_obs;
-    REAL cx = C->o_pos[(e * N + o) * 2], cy = C->o_pos[(e * N + o) * 2 + 1];
+    const REAL *sh = od + 6 * o;
+    REAL cx = sh[0], cy = sh[1];
     int st = C->o_type[o];
     REAL ro = C->o_rad[o], hx = C->o_half[o * 2], hy = C->o_half[o * 2 + 1];
     if (FN(bounds_apart)(px - cx, py - cy, ra + C->margin + FN(shape_bound)(st, ro, hx, hy)))
         return;
-    REAL vox = C->o_vel[(e * N + o) * 2], voy = C->o_vel[(e * N + o) * 2 + 1];
-    REAL om = C->o_om[e * N + o];
-    REAL ang = C->o_ang[e * N + o];
+    REAL vox = sh[3], voy = sh[4];
+    REAL om = sh[5];
+    REAL ang = sh[2];
     if (st == 1) {
         FN(box_force_adj)(C, px, py, vx, vy, cx, cy, ang, hx, hy, ra + C->margin, dd, vox, voy,
                           om, gfx, gfy, apx, apy, avx, avy);
@@ -393,6 +454,13 @@ static inline void FN(obstacle_force_adj)(const FN(ctx_t) *C, int e, int o, REAL
         *apy += ady;
         *avx += arvx;
         *avy += arvy;
+        if (god && FN(shape_moves)(C, o)) {
+            REAL *g = god + 6 * o;
+            g[0] -= adx;
+            g[1] -= ady;
+            g[3] -= arvx;
+            g[4] -= arvy;
+        }
     }
 }
 
@@ -474,8 +542,8 @@ static void FN(neighbors_env)(int A, int K, const FN(agent_t) *st, REAL radius,
 /* --------------------------------------------------------------- the force pass */
 
 /* collision_forces_kernel (swarp/core/collisions.py:818-881) for one env */
-static void FN(forces_env)(const FN(ctx_t) *C, int e, const FN(prm_t) *P, const FN(agent_t) *st,
-                           const int32_t *idx, const int32_t *cnt, REAL *F)
+static void FN(forces_env)(const FN(ctx_t) *C, const REAL *od, const FN(prm_t) *P,
+                           const FN(agent_t) *st, const int32_t *idx, const int32_t *cnt, REAL *F)
 {
     int A = C->n_agents, K = C->max_nbr;
     for (int a = 0; a < A; ++a) {
@@ -496,7 +564,7 @@ static void FN(forces_env)(const FN(ctx_t) *C, int e, const FN(prm_t) *P, const 
         REAL sx = 0, sy = 0;
         for (int o = 0; o < C->n_obs; ++o) {
             REAL gx, gy;
-            FN(obstacle_force)(C, e, o, px, py, vx, vy, ra, dd, &gx, &gy);
+            FN(obstacle_force)(C, od, o, px, py, vx, vy, ra, dd, &gx, &gy);
             sx += gx;
             sy += gy;
         }
@@ -511,9 +579,9 @@ static void FN(forces_env)(const FN(ctx_t) *C, int e, const FN(prm_t) *P, const 
     }
 }
 
-static void FN(forces_env_adj)(const FN(ctx_t) *C, int e, const FN(prm_t) *P,
+static void FN(forces_env_adj)(const FN(ctx_t) *C, const REAL *od, const FN(prm_t) *P,
                                const FN(agent_t) *st, const int32_t *idx, const int32_t *cnt,
-                               const REAL *aF, FN(agent_t) *adj)
+                               const REAL *aF, FN(agent_t) *adj, REAL *god)
 {
     int A = C->n_agents, K = C->max_nbr;
     for (int a = 0; a < A; ++a) {
@@ -539,8 +607,8 @@ static void FN(forces_env_adj)(const FN(ctx_t) *C, int e, const FN(prm_t) *P,
             adj[b].vy -= arvy;
         }
         for (int o = 0; o < C->n_obs; ++o)
-            FN(obstacle_force_adj)(C, e, o, px, py, vx, vy, ra, dd, gfx, gfy,
-                                   &adj[a].px, &adj[a].py, &adj[a].vx, &adj[a].vy);
+            FN(obstacle_force_adj)(C, od, o, px, py, vx, vy, ra, dd, gfx, gfy,
+                                   &adj[a].px, &adj[a].py, &adj[a].vx, &adj[a].vy, god);
         if (C->soft_walls)
             FN(wall_force_adj)(C, px, py, vx, vy, ra, dd, gfx, gfy,
                                &adj[a].px, &adj[a].py, &adj[a].vx, &adj[a].vy);
@@ -899,24 +967,298 @@ static void FN(integrate_agent_adj)(const FN(ctx_t) *C, const FN(prm_t) *P,
     }
 }
 
+/* ------------------------------------------------------------- movable bodies */
+
+/* One movable body's contact sum, for the forward pass and its reverse.  Body rooted at
+   o; every shape of it is a circle (the build's scope).  Per shape s of the body (index
+   order) the reaction of every agent not bounds_apart from it, in agent order, then the
+   contacts with the circles of other bodies and of the scenery (index order), exactly
+   the loops of obstacle_dynamics_kernel (swarp/core/bodies.py:423-501). */
+typedef struct {
+    REAL qx, qy, th, tvx, tvy, om, ca, sa;
+    REAL fx, fy, tau, ext;
+} FN(bodysum_t);
+
+
+static void FN(body_sum)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *st,
+                         const REAL *od, const REAL *bd, int o, FN(bodysum_t) *B)
+{
+    int N = C->n_obs, A = C->n_agents;
+    const REAL *b = bd + 6 * N + 6 * o;
+    B->qx = b[0]; B->qy = b[1]; B->th = b[2]; B->tvx = b[3]; B->tvy = b[4]; B->om = b[5];
+    FN(psincos)(B->th, &B->sa, &B->ca);
+    REAL fx = 0, fy = 0, tau = 0, ext = 0;
+    REAL denom_self = (REAL)1 + C->c * C->sub_dt / C->o_mass[o];
+    for (int s = 0; s < N; ++s) {
+        if (C->o_body[s] != o) continue;
+        REAL offx = C->o_off[2 * s], offy = C->o_off[2 * s + 1];
+        REAL owx = B->ca * offx - B->sa * offy;
+        REAL owy = B->sa * offx + B->ca * offy;
+        REAL csx = B->qx + owx, csy = B->qy + owy;
+        REAL vsx = B->tvx - B->om * owy, vsy = B->tvy + B->om * owx;
+        REAL ro = C->o_rad[s];
+        REAL ax = FABS(offx), ay = FABS(offy);
+        REAL reach = SQRT(ax * ax + ay * ay) + ro;
+        ext = FN(rmax)(ext, reach);
+        REAL bound = ro;
+        for (int a = 0; a < A; ++a) {
+            REAL ra = P[a].radius;
+            if (FN(bounds_apart)(st[a].px - csx, st[a].py - csy, ra + bound + C->margin)) continue;
+            REAL dd = (REAL)1 + C->c * C->sub_dt / P[a].mass;
+            REAL gx, gy;
+            FN(pair_force)(C, st[a].px - csx, st[a].py - csy, st[a].vx - vsx, st[a].vy - vsy,
+                           ra + ro + C->margin, dd, &gx, &gy);
+            REAL f0 = -gx, f1 = -gy;
+            REAL lx = owx + (REAL)0, ly = owy + (REAL)0;
+            fx += f0;
+            fy += f1;
+            tau += lx * f1 - ly * f0;
+        }
+        for (int o2 = 0; o2 < N; ++o2) {
+            if (C->o_body[o2] == o) continue;
+            const REAL *d2 = od + 6 * o2;
+            REAL r2 = C->o_rad[o2];
+            if (FN(bounds_apart)(d2[0] - csx, d2[1] - csy, bound + r2 + C->margin)) continue;
+            REAL gx, gy;
+            FN(pair_force)(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4],
+                           ro + r2 + C->margin, denom_self, &gx, &gy);
+            REAL lx = owx + (REAL)0, ly = owy + (REAL)0;
+            fx += gx;
+            fy += gy;
+            tau += lx * gy - ly * gx;
+        }
+    }
+    B->fx = fx; B->fy = fy; B->tau = tau; B->ext = ext;
+}
+
+/* The body pass of one env (obstacle_dynamics_kernel, disc variant,
+   swarp/core/bodies.py:367-568): every movable body integrated from the reactions of the
+   agents of the substep's input state `st`, reading the shape state `ob` of the substep
+   input; writes the step's new obstacle state `ob_out` (static shapes copied, each
+   movable shape re-installed at its body's new pose).  Other bodies' shapes are read
+   from the input snapshot. */
+static void FN(bodies_env)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *st,
+                           const REAL *ob, REAL *ob_out)
+{
+    int N = C->n_obs;
+    memcpy(ob_out, ob, sizeof(REAL) * OB_W * N);
+    for (int o = 0; o < N; ++o) {
+        if (C->o_body[o] != o || C->o_kind[o] != 1) continue;
+        FN(bodysum_t) B;
+        FN(body_sum)(C, P, st, ob, ob, o, &B);
+        REAL sdt = C->sub_dt, one = 1;
+        REAL lin_decay = one - C->lin_damping * sdt;
+        REAL ang_decay = one - C->ang_damping * sdt;
+        REAL m = C->o_mass[o], I = C->o_inertia[o];
+        REAL nvx = (B.tvx + B.fx / m * sdt) * lin_decay;
+        REAL nvy = (B.tvy + B.fy / m * sdt) * lin_decay;
+        REAL nom = (B.om + B.tau / I * sdt) * ang_decay;
+        REAL nx = B.qx + nvx * sdt;
+        REAL ny = B.qy + nvy * sdt;
+        if (C->clamp_bounds) {
+            REAL half = (REAL)0.5;
+            REAL lo_x = C->bmin_x + B.ext, mid_x = (C->bmin_x + C->bmax_x) * half;
+            lo_x = lo_x < mid_x ? lo_x : mid_x;
+            REAL hi_x = FN(rmax)(C->bmax_x - B.ext, lo_x);
+            REAL lo_y = C->bmin_y + B.ext, mid_y = (C->bmin_y + C->bmax_y) * half;
+            lo_y = lo_y < mid_y ? lo_y : mid_y;
+            REAL hi_y = FN(rmax)(C->bmax_y - B.ext, lo_y);
+            REAL cx = FN(rclamp)(nx, lo_x, hi_x), cy = FN(rclamp)(ny, lo_y, hi_y);
+            if (cx != nx) nvx = 0;
+            if (cy != ny) nvy = 0;
+            nx = cx;
+            ny = cy;
+        }
+        REAL nth = B.th + nom * sdt;
+        REAL *bo = ob_out + 6 * N + 6 * o;
+        bo[0] = nx; bo[1] = ny; bo[2] = nth; bo[3] = nvx; bo[4] = nvy; bo[5] = nom;
+        REAL nsa, nca;
+        FN(psincos)(nth, &nsa, &nca);
+        for (int s = 0; s < N; ++s) {
+            if (C->o_body[s] != o) continue;
+            REAL offx = C->o_off[2 * s], offy = C->o_off[2 * s + 1];
+            REAL owx = nca * offx - nsa * offy;
+            REAL owy = nsa * offx + nca * offy;
+            REAL *so = ob_out + 6 * s;
+            so[0] = nx + owx; so[1] = ny + owy; so[2] = nth;
+            so[3] = nvx - nom * owy; so[4] = nvy + nom * owx; so[5] = nom;
+        }
+    }
+}
+
+/* Reverse of bodies_env (this build's own adjoint: the reference never tapes the body
+   pass).  gout = adjoint of ob_out; accumulates the agents' adjoint into gst and writes
+   the adjoint of the input obstacle state into gob (overwritten). */
+static void FN(bodies_env_adj)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *st,
+                               const REAL *ob, const REAL *gout, FN(agent_t) *gst, REAL *gob)
+{
+    int N = C->n_obs, A = C->n_agents;
+    /* pass-through of everything the pass does not rewrite */
+    memcpy(gob, gout, sizeof(REAL) * OB_W * N);
+    for (int s = 0; s < N; ++s)
+        if (FN(shape_moves)(C, s)) memset(gob + 6 * s, 0, sizeof(REAL) * 6);
+    for (int o = 0; o < N; ++o) {
+        if (C->o_body[o] != o || C->o_kind[o] != 1) continue;
+        FN(bodysum_t) B;
+        FN(body_sum)(C, P, st, ob, ob, o, &B);
+        REAL sdt = C->sub_dt, one = 1;
+        REAL lin_decay = one - C->lin_damping * sdt;
+        REAL ang_decay = one - C->ang_damping * sdt;
+        REAL m = C->o_mass[o], I = C->o_inertia[o];
+        REAL nvx = (B.tvx + B.fx / m * sdt) * lin_decay;
+        REAL nvy = (B.tvy + B.fy / m * sdt) * lin_decay;
+        REAL nom = (B.om + B.tau / I * sdt) * ang_decay;
+        REAL nx = B.qx + nvx * sdt, ny = B.qy + nvy * sdt;
+        int clx = 0, cly = 0;
+        if (C->clamp_bounds) {
+            REAL half = (REAL)0.5;
+            REAL lo_x = C->bmin_x + B.ext, mid_x = (C->bmin_x + C->bmax_x) * half;
+            lo_x = lo_x < mid_x ? lo_x : mid_x;
+            REAL hi_x = FN(rmax)(C->bmax_x - B.ext, lo_x);
+            REAL lo_y = C->bmin_y + B.ext, mid_y = (C->bmin_y + C->bmax_y) * half;
+            lo_y = lo_y < mid_y ? lo_y : mid_y;
+            REAL hi_y = FN(rmax)(C->bmax_y - B.ext, lo_y);
+            clx = FN(rclamp)(nx, lo_x, hi_x) != nx;
+            cly = FN(rclamp)(ny, lo_y, hi_y) != ny;
+            if (clx) nvx = 0;
+            if (cly) nvy = 0;
+        }
+        REAL nth = B.th + nom * sdt;
+        REAL nsa, nca;
+        FN(psincos)(nth, &nsa, &nca);
+        /* adjoint of the new body state: its own entry plus every re-installed shape */
+        const REAL *gb = gout + 6 * N + 6 * o;
+        REAL g_nx = gb[0], g_ny = gb[1], g_nth = gb[2], g_nvx = gb[3], g_nvy = gb[4];
+        REAL g_nom = gb[5];
+        for (int s = 0; s < N; ++s) {
+            if (C->o_body[s] != o) continue;
+            REAL offx = C->o_off[2 * s], offy = C->o_off[2 * s + 1];
+            REAL owx = nca * offx - nsa * offy;
+            REAL owy = nsa * offx + nca * offy;
+            const REAL *g = gout + 6 * s;
+            g_nx += g[0];
+            g_ny += g[1];
+            g_nth += g[2];
+            g_nvx += g[3];
+            g_nvy += g[4];
+            g_nom += g[5] - g[3] * owy + g[4] * owx;
+            REAL g_owx = g[0] + g[4] * nom, g_owy = g[1] - g[3] * nom;
+            g_nth += -g_owx * owy + g_owy * owx;
+        }
+        /* nth = th + nom * sdt */
+        REAL g_th = g_nth;
+        g_nom += g_nth * sdt;
+        /* nx = qx + nvx * sdt (a clamped axis is a constant with zero velocity) */
+        REAL g_qx = clx ? (REAL)0 : g_nx, g_qy = cly ? (REAL)0 : g_ny;
+        if (clx) g_nvx = 0; else g_nvx += g_nx * sdt;
+        if (cly) g_nvy = 0; else g_nvy += g_ny * sdt;
+        REAL g_tvx = g_nvx * lin_decay, g_tvy = g_nvy * lin_decay;
+        REAL g_fx = g_nvx * lin_decay * sdt / m, g_fy = g_nvy * lin_decay * sdt / m;
+        REAL g_om = g_nom * ang_decay;
+        REAL g_tau = g_nom * ang_decay * sdt / I;
+        /* the contact sum, term by term */
+        REAL denom_self = (REAL)1 + C->c * C->sub_dt / m;
+        for (int s = 0; s < N; ++s) {
+            if (C->o_body[s] != o) continue;
+            REAL offx = C->o_off[2 * s], offy = C->o_off[2 * s + 1];
+            REAL owx = B.ca * offx - B.sa * offy;
+            REAL owy = B.sa * offx + B.ca * offy;
+            REAL csx = B.qx + owx, csy = B.qy + owy;
+            REAL vsx = B.tvx - B.om * owy, vsy = B.tvy + B.om * owx;
+            REAL ro = C->o_rad[s];
+            REAL g_owx = 0, g_owy = 0, g_csx = 0, g_csy = 0, g_vsx = 0, g_vsy = 0;
+            for (int a = 0; a < A; ++a) {
+                REAL ra = P[a].radius;
+                if (FN(bounds_apart)(st[a].px - csx, st[a].py - csy, ra + ro + C->margin)) continue;
+                REAL dd = (REAL)1 + C->c * C->sub_dt / P[a].mass;
+                REAL gx, gy;
+                FN(pair_force)(C, st[a].px - csx, st[a].py - csy, st[a].vx - vsx, st[a].vy - vsy,
+                               ra + ro + C->margin, dd, &gx, &gy);
+                REAL f0 = -gx, f1 = -gy;
+                /* tau += lx f1 - ly f0, lever (lx, ly) = (owx, owy) */
+                REAL g_f0 = g_fx - g_tau * owy, g_f1 = g_fy + g_tau * owx;
+                g_owx += g_tau * f1;
+                g_owy -= g_tau * f0;
+                REAL adx = 0, ady = 0, arx = 0, ary = 0;
+                FN(pair_force_adj)(C, st[a].px - csx, st[a].py - csy, st[a].vx - vsx,
+                                   st[a].vy - vsy, ra + ro + C->margin, dd, -g_f0, -g_f1,
+                                   &adx, &ady, &arx, &ary);
+                gst[a].px += adx;
+                gst[a].py += ady;
+                gst[a].vx += arx;
+                gst[a].vy += ary;
+                g_csx -= adx;
+                g_csy -= ady;
+                g_vsx -= arx;
+                g_vsy -= ary;
+            }
+            for (int o2 = 0; o2 < N; ++o2) {
+                if (C->o_body[o2] == o) continue;
+                const REAL *d2 = ob + 6 * o2;
+                REAL r2 = C->o_rad[o2];
+                if (FN(bounds_apart)(d2[0] - csx, d2[1] - csy, ro + r2 + C->margin)) continue;
+                REAL gx, gy;
+                FN(pair_force)(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4],
+                               ro + r2 + C->margin, denom_self, &gx, &gy);
+                REAL g_f0 = g_fx - g_tau * owy, g_f1 = g_fy + g_tau * owx;
+                g_owx += g_tau * gy;
+                g_owy -= g_tau * gx;
+                REAL adx = 0, ady = 0, arx = 0, ary = 0;
+                FN(pair_force_adj)(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4],
+                                   ro + r2 + C->margin, denom_self, g_f0, g_f1, &adx, &ady, &arx,
+                                   &ary);
+                g_csx += adx;
+                g_csy += ady;
+                g_vsx += arx;
+                g_vsy += ary;
+                if (FN(shape_moves)(C, o2)) {
+                    REAL *g2 = gob + 6 * o2;
+                    g2[0] -= adx;
+                    g2[1] -= ady;
+                    g2[3] -= arx;
+                    g2[4] -= ary;
+                }
+            }
+            /* cs = q + ow ; vs = tv + om x ow ; ow = R(th) off */
+            g_qx += g_csx;
+            g_qy += g_csy;
+            g_owx += g_csx + g_vsy * B.om;
+            g_owy += g_csy - g_vsx * B.om;
+            g_tvx += g_vsx;
+            g_tvy += g_vsy;
+            g_om += -g_vsx * owy + g_vsy * owx;
+            g_th += -g_owx * owy + g_owy * owx;
+        }
+        REAL *gi = gob + 6 * N + 6 * o;
+        gi[0] = g_qx; gi[1] = g_qy; gi[2] = g_th; gi[3] = g_tvx; gi[4] = g_tvy; gi[5] = g_om;
+    }
+}
+
 /* ------------------------------------------------------------ one env, one step */
 
 typedef struct {
     FN(agent_t) *st;    /* (S+1) * A states of the substep chain */
     REAL *F;            /* S * A * 2 forces */
     int32_t *idx, *cnt; /* S * A * K and S * A lists */
+    REAL *ob;           /* (S+1) * OB_W * N obstacle states (NULL without obstacles) */
 } FN(chain_t);
 
-/* Stepper.launch_substeps (swarp/core/stepper.py:784-1011), taped ordering:
-   per substep neighbours on the substep input, forces, then integrate. */
-static void FN(step_env)(const FN(ctx_t) *C, int e, const FN(prm_t) *P, const FN(agent_t) *in,
-                         const REAL *act, FN(agent_t) *out, FN(chain_t) *ch)
+/* Stepper.launch_substeps (swarp/core/stepper.py:784-1011): per substep neighbours on
+   the substep input, forces, then the body pass (swarp/core/stepper.py:952-991), then
+   integrate.  Movable bodies are integrated on every step here, taped or not. */
+static void FN(step_env)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *in,
+                         const REAL *ob_in, const REAL *act, FN(agent_t) *out, REAL *ob_out,
+                         FN(chain_t) *ch)
 {
-    int A = C->n_agents, S = C->substeps, K = C->max_nbr, ad = C->act_dim;
+    int A = C->n_agents, S = C->substeps, K = C->max_nbr, ad = C->act_dim, N = C->n_obs;
+    size_t nob = (size_t)OB_W * N;
     FN(agent_t) *st = ch->st;
     memcpy(st, in, sizeof(FN(agent_t)) * A);
+    if (N) memcpy(ch->ob, ob_in, sizeof(REAL) * nob);
     for (int s = 0; s < S; ++s) {
         FN(agent_t) *cur = st + s * A, *nxt = st + (s + 1) * A;
+        const REAL *obc = N ? ch->ob + s * nob : NULL;
+        REAL *obn = N ? ch->ob + (s + 1) * nob : NULL;
         REAL *F = ch->F + s * A * 2;
         int32_t *idx = ch->idx + s * A * K, *cnt = ch->cnt + s * A;
         if (C->needs_forces) {
@@ -924,29 +1266,44 @@ static void FN(step_env)(const FN(ctx_t) *C, int e, const FN(prm_t) *P, const FN
                 FN(neighbors_env)(A, K, cur, C->nbr_radius, idx, cnt, NULL);
             else
                 for (int a = 0; a < A; ++a) cnt[a] = 0;
-            FN(forces_env)(C, e, P, cur, idx, cnt, F);
+            FN(forces_env)(C, obc, P, cur, idx, cnt, F);
         } else {
             for (int a = 0; a < 2 * A; ++a) F[a] = 0;
         }
+        if (C->any_movable)
+            FN(bodies_env)(C, P, cur, obc, obn);
+        else if (N)
+            memcpy(obn, obc, sizeof(REAL) * nob);
         for (int a = 0; a < A; ++a)
             FN(integrate_agent)(C, P + a, cur + a, act + a * ad, F[a * 2], F[a * 2 + 1], nxt + a);
     }
     memcpy(out, st + S * A, sizeof(FN(agent_t)) * A);
+    if (N && ob_out) memcpy(ob_out, ch->ob + S * nob, sizeof(REAL) * nob);
 }
 
-/* reverse of step_env: gout = adjoint of the step output; writes gin, accumulates gact */
-static void FN(step_env_adj)(const FN(ctx_t) *C, int e, const FN(prm_t) *P,
-                             const FN(agent_t) *in, const REAL *act, const FN(agent_t) *gout,
-                             FN(agent_t) *gin, REAL *gact, FN(chain_t) *ch, FN(agent_t) *tmp,
-                             REAL *gF)
+/* reverse of step_env: gout / gob_out = adjoint of the step output; writes gin / gob_in,
+   accumulates gact.  tmp: A agents; gF: 2A; obw: 2 * OB_W * N scratch. */
+static void FN(step_env_adj)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *in,
+                             const REAL *ob_in, const REAL *act, const FN(agent_t) *gout,
+                             const REAL *gob_out, FN(agent_t) *gin, REAL *gob_in, REAL *gact,
+                             FN(chain_t) *ch, FN(agent_t) *tmp, REAL *gF, REAL *obw)
 {
-    int A = C->n_agents, S = C->substeps, K = C->max_nbr, ad = C->act_dim;
-    /* tmp receives the (unused) step output; the chain keeps every substep input */
-    FN(step_env)(C, e, P, in, act, tmp, ch);
+    int A = C->n_agents, S = C->substeps, K = C->max_nbr, ad = C->act_dim, N = C->n_obs;
+    size_t nob = (size_t)OB_W * N;
+    /* tmp / obw receive the (unused) step output; the chain keeps every substep input */
+    FN(step_env)(C, P, in, ob_in, act, tmp, obw, ch);
     FN(agent_t) *g = gin;
     memcpy(g, gout, sizeof(FN(agent_t)) * A);
+    REAL *gob = obw, *gprev = obw + nob;
+    if (N) {
+        if (gob_out)
+            memcpy(gob, gob_out, sizeof(REAL) * nob);
+        else
+            memset(gob, 0, sizeof(REAL) * nob);
+    }
     for (int s = S - 1; s >= 0; --s) {
         FN(agent_t) *cur = ch->st + s * A;
+        const REAL *obc = N ? ch->ob + s * nob : NULL;
         REAL *F = ch->F + s * A * 2;
         int32_t *idx = ch->idx + s * A * K, *cnt = ch->cnt + s * A;
         memset(tmp, 0, sizeof(FN(agent_t)) * A);
@@ -954,9 +1311,19 @@ static void FN(step_env_adj)(const FN(ctx_t) *C, int e, const FN(prm_t) *P,
         for (int a = 0; a < A; ++a)
             FN(integrate_agent_adj)(C, P + a, cur + a, act + a * ad, F[a * 2], F[a * 2 + 1],
                                     g + a, tmp + a, gact + a * ad, gF + a * 2, gF + a * 2 + 1);
-        if (C->needs_forces) FN(forces_env_adj)(C, e, P, cur, idx, cnt, gF, tmp);
+        if (C->any_movable)
+            FN(bodies_env_adj)(C, P, cur, obc, gob, tmp, gprev);
+        else if (N)
+            memcpy(gprev, gob, sizeof(REAL) * nob);
+        if (C->needs_forces) FN(forces_env_adj)(C, obc, P, cur, idx, cnt, gF, tmp, N ? gprev : NULL);
         memcpy(g, tmp, sizeof(FN(agent_t)) * A);
+        if (N) {
+            REAL *t = gob;
+            gob = gprev;
+            gprev = t;
+        }
     }
+    if (N && gob_in) memcpy(gob_in, gob, sizeof(REAL) * nob);
 }
 
 /* ------------------------------------------------------------------ entry points */
@@ -983,6 +1350,8 @@ static void FN(make_ctx)(const oracle_cfg_t *cfg, const oracle_obs_t *obs, FN(ct
     C->collisions = cfg->collisions;
     C->soft_walls = cfg->soft_walls;
     C->clamp_bounds = cfg->clamp_bounds;
+    C->lin_damping = (REAL)cfg->lin_damping;
+    C->ang_damping = (REAL)cfg->ang_damping;
     C->n_obs = obs ? obs->n_obstacles : 0;
     C->needs_forces = C->collisions || C->soft_walls || C->n_obs > 0;
     if (C->n_obs > 0) {
@@ -993,6 +1362,30 @@ static void FN(make_ctx)(const oracle_cfg_t *cfg, const oracle_obs_t *obs, FN(ct
         C->o_half = (const REAL *)obs->half;
         C->o_vel = (const REAL *)obs->vel;
         C->o_om = (const REAL *)obs->ang_vel;
+        C->o_kind = obs->kind;
+        C->o_body = obs->body;
+        C->o_mass = (const REAL *)obs->mass;
+        C->o_inertia = (const REAL *)obs->inertia;
+        C->o_off = (const REAL *)obs->body_off;
+        if (C->o_kind && C->o_body && C->o_mass && C->o_inertia && C->o_off)
+            for (int o = 0; o < C->n_obs; ++o)
+                if (C->o_body[o] == o && C->o_kind[o] == 1) C->any_movable = 1;
+    }
+}
+
+/* The obstacle state of env e as installed (shapes from the obstacle arrays, bodies 0). */
+static void FN(static_ob)(const FN(ctx_t) *C, int e, REAL *ob)
+{
+    int N = C->n_obs;
+    memset(ob, 0, sizeof(REAL) * OB_W * N);
+    for (int o = 0; o < N; ++o) {
+        REAL *sh = ob + 6 * o;
+        sh[0] = C->o_pos[(e * N + o) * 2];
+        sh[1] = C->o_pos[(e * N + o) * 2 + 1];
+        sh[2] = C->o_ang[e * N + o];
+        sh[3] = C->o_vel[(e * N + o) * 2];
+        sh[4] = C->o_vel[(e * N + o) * 2 + 1];
+        sh[5] = C->o_om[e * N + o];
     }
 }
 
@@ -1028,14 +1421,33 @@ int FN(oracle_neighbors)(int E, int A, int K, const REAL *pos, double radius, in
     return 0;
 }
 
-/* T-step rollout.  state0 [E,A,16], actions [T,E,A,ad], states out [T,E,A,16]. */
-int FN(oracle_rollout)(const oracle_cfg_t *cfg, const REAL *params, const int32_t *tags,
-                       const int32_t *modes, const oracle_obs_t *obs, int T, const REAL *state0,
-                       const REAL *actions, REAL *states)
+static int FN(chain_alloc)(FN(chain_t) *ch, int A, int S, int K, int N)
+{
+    ch->st = (FN(agent_t) *)malloc(sizeof(FN(agent_t)) * (size_t)(S + 1) * A);
+    ch->F = (REAL *)malloc(sizeof(REAL) * (size_t)S * A * 2);
+    ch->idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)S * A * K);
+    ch->cnt = (int32_t *)malloc(sizeof(int32_t) * (size_t)S * A);
+    ch->ob = N ? (REAL *)malloc(sizeof(REAL) * (size_t)(S + 1) * OB_W * N) : NULL;
+    return !ch->st || !ch->F || !ch->idx || !ch->cnt || (N && !ch->ob);
+}
+
+static void FN(chain_free)(FN(chain_t) *ch)
+{
+    free(ch->st); free(ch->F); free(ch->idx); free(ch->cnt); free(ch->ob);
+}
+
+/* T-step rollout.  state0 [E,A,16], actions [T,E,A,ad], states out [T,E,A,16].
+   ob0 [E, 12N] is the initial obstacle state (NULL = as installed); ob_states
+   [T, E, 12N] (nullable) receives each step's obstacle state. */
+int FN(oracle_rollout_ob)(const oracle_cfg_t *cfg, const REAL *params, const int32_t *tags,
+                          const int32_t *modes, const oracle_obs_t *obs, int T,
+                          const REAL *state0, const REAL *ob0, const REAL *actions, REAL *states,
+                          REAL *ob_states)
 {
     FN(ctx_t) C;
     FN(make_ctx)(cfg, obs, &C);
-    int E = C.n_envs, A = C.n_agents, S = C.substeps, K = C.max_nbr, ad = C.act_dim;
+    int E = C.n_envs, A = C.n_agents, S = C.substeps, K = C.max_nbr, ad = C.act_dim, N = C.n_obs;
+    size_t nob = (size_t)OB_W * N;
     FN(prm_t) *P = (FN(prm_t) *)calloc((size_t)A, sizeof(FN(prm_t)));
     FN(make_prm)(params, tags, modes, A, P);
     int nth = cfg->n_threads > 0 ? cfg->n_threads : 1;
@@ -1043,40 +1455,64 @@ int FN(oracle_rollout)(const oracle_cfg_t *cfg, const REAL *params, const int32_
 #pragma omp parallel num_threads(nth)
     {
         FN(chain_t) ch;
-        ch.st = (FN(agent_t) *)malloc(sizeof(FN(agent_t)) * (size_t)(S + 1) * A);
-        ch.F = (REAL *)malloc(sizeof(REAL) * (size_t)S * A * 2);
-        ch.idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)S * A * K);
-        ch.cnt = (int32_t *)malloc(sizeof(int32_t) * (size_t)S * A);
-        if (!ch.st || !ch.F || !ch.idx || !ch.cnt) err = 1;
+        REAL *obw = N ? (REAL *)malloc(sizeof(REAL) * 2 * nob) : NULL;
+        if (FN(chain_alloc)(&ch, A, S, K, N) || (N && !obw)) err = 1;
 #pragma omp for schedule(static)
         for (int e = 0; e < E; ++e) {
             if (err) continue;
             const FN(agent_t) *cur = (const FN(agent_t) *)(state0 + (size_t)e * A * 16);
+            REAL *obc = obw, *obn = N ? obw + nob : NULL;
+            if (N) {
+                if (ob0)
+                    memcpy(obc, ob0 + (size_t)e * nob, sizeof(REAL) * nob);
+                else
+                    FN(static_ob)(&C, e, obc);
+            }
             for (int t = 0; t < T; ++t) {
                 FN(agent_t) *out = (FN(agent_t) *)(states + ((size_t)t * E + e) * A * 16);
-                FN(step_env)(&C, e, P, cur, actions + ((size_t)t * E + e) * A * ad, out, &ch);
+                FN(step_env)(&C, P, cur, obc, actions + ((size_t)t * E + e) * A * ad, out, obn,
+                             &ch);
                 cur = out;
+                if (N) {
+                    if (ob_states) memcpy(ob_states + ((size_t)t * E + e) * nob, obn, sizeof(REAL) * nob);
+                    REAL *x = obc;
+                    obc = obn;
+                    obn = x;
+                }
             }
         }
-        free(ch.st); free(ch.F); free(ch.idx); free(ch.cnt);
+        FN(chain_free)(&ch);
+        free(obw);
     }
     free(P);
     return err ? -1 : 0;
 }
 
-/* Reverse of oracle_rollout.  `states` are the forward outputs (the per-step
-   checkpoints); adj_states [T,E,A,16] is the adjoint injected at every step
-   output (NULL = zero except adj_final), adj_final [E,A,16] the adjoint of the
-   last state (NULL = zero).  Writes adj_state0 [E,A,16] and adj_actions. */
-int FN(oracle_rollout_adj)(const oracle_cfg_t *cfg, const REAL *params, const int32_t *tags,
-                           const int32_t *modes, const oracle_obs_t *obs, int T,
-                           const REAL *state0, const REAL *actions, const REAL *states,
-                           const REAL *adj_states, const REAL *adj_final, REAL *adj_state0,
-                           REAL *adj_actions)
+int FN(oracle_rollout)(const oracle_cfg_t *cfg, const REAL *params, const int32_t *tags,
+                       const int32_t *modes, const oracle_obs_t *obs, int T, const REAL *state0,
+                       const REAL *actions, REAL *states)
+{
+    return FN(oracle_rollout_ob)(cfg, params, tags, modes, obs, T, state0, NULL, actions, states,
+                                 NULL);
+}
+
+/* Reverse of oracle_rollout_ob.  `states` / `ob_states` are the forward outputs (the
+   per-step checkpoints); adj_states [T,E,A,16] / adj_ob_states [T,E,12N] are the adjoints
+   injected at every step output (NULL = zero), adj_final [E,A,16] / adj_ob_final [E,12N]
+   the adjoints of the last state (NULL = zero).  Writes adj_state0 [E,A,16], adj_ob0
+   [E,12N] (nullable) and adj_actions. */
+int FN(oracle_rollout_adj_ob)(const oracle_cfg_t *cfg, const REAL *params, const int32_t *tags,
+                              const int32_t *modes, const oracle_obs_t *obs, int T,
+                              const REAL *state0, const REAL *ob0, const REAL *actions,
+                              const REAL *states, const REAL *ob_states, const REAL *adj_states,
+                              const REAL *adj_final, const REAL *adj_ob_states,
+                              const REAL *adj_ob_final, REAL *adj_state0, REAL *adj_ob0,
+                              REAL *adj_actions)
 {
     FN(ctx_t) C;
     FN(make_ctx)(cfg, obs, &C);
-    int E = C.n_envs, A = C.n_agents, S = C.substeps, K = C.max_nbr, ad = C.act_dim;
+    int E = C.n_envs, A = C.n_agents, S = C.substeps, K = C.max_nbr, ad = C.act_dim, N = C.n_obs;
+    size_t nob = (size_t)OB_W * N;
     FN(prm_t) *P = (FN(prm_t) *)calloc((size_t)A, sizeof(FN(prm_t)));
     FN(make_prm)(params, tags, modes, A, P);
     int nth = cfg->n_threads > 0 ? cfg->n_threads : 1;
@@ -1085,19 +1521,18 @@ int FN(oracle_rollout_adj)(const oracle_cfg_t *cfg, const REAL *params, const in
 #pragma omp parallel num_threads(nth)
     {
         FN(chain_t) ch;
-        ch.st = (FN(agent_t) *)malloc(sizeof(FN(agent_t)) * (size_t)(S + 1) * A);
-        ch.F = (REAL *)malloc(sizeof(REAL) * (size_t)S * A * 2);
-        ch.idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)S * A * K);
-        ch.cnt = (int32_t *)malloc(sizeof(int32_t) * (size_t)S * A);
         FN(agent_t) *g = (FN(agent_t) *)malloc(sizeof(FN(agent_t)) * (size_t)A);
         FN(agent_t) *gn = (FN(agent_t) *)malloc(sizeof(FN(agent_t)) * (size_t)A);
         FN(agent_t) *tmp = (FN(agent_t) *)malloc(sizeof(FN(agent_t)) * (size_t)A);
         REAL *gF = (REAL *)malloc(sizeof(REAL) * (size_t)A * 2);
-        if (!ch.st || !ch.F || !ch.idx || !ch.cnt || !g || !gn || !tmp || !gF) err = 1;
+        REAL *ow = (REAL *)malloc(sizeof(REAL) * (4 * nob + 1));
+        if (FN(chain_alloc)(&ch, A, S, K, N) || !g || !gn || !tmp || !gF || !ow) err = 1;
 #pragma omp for schedule(static)
         for (int e = 0; e < E; ++e) {
             if (err) continue;
+            REAL *gob = ow, *gobn = ow + nob, *obw = ow + 2 * nob, *obin = ow + 3 * nob;
             memset(g, 0, sizeof(FN(agent_t)) * A);
+            if (N) memset(gob, 0, sizeof(REAL) * nob);
             for (int t = T - 1; t >= 0; --t) {
                 if (adj_states) {
                     const REAL *src = adj_states + ((size_t)t * E + e) * A * 16;
@@ -1109,20 +1544,66 @@ int FN(oracle_rollout_adj)(const oracle_cfg_t *cfg, const REAL *params, const in
                     REAL *gd = (REAL *)g;
                     for (int i = 0; i < A * 16; ++i) gd[i] += src[i];
                 }
+                if (N && adj_ob_states) {
+                    const REAL *src = adj_ob_states + ((size_t)t * E + e) * nob;
+                    for (size_t i = 0; i < nob; ++i) gob[i] += src[i];
+                }
+                if (N && t == T - 1 && adj_ob_final) {
+                    const REAL *src = adj_ob_final + (size_t)e * nob;
+                    for (size_t i = 0; i < nob; ++i) gob[i] += src[i];
+                }
                 const FN(agent_t) *in =
                     t == 0 ? (const FN(agent_t) *)(state0 + (size_t)e * A * 16)
                            : (const FN(agent_t) *)(states + ((size_t)(t - 1) * E + e) * A * 16);
-                FN(step_env_adj)(&C, e, P, in, actions + ((size_t)t * E + e) * A * ad, g, gn,
-                                 adj_actions + ((size_t)t * E + e) * A * ad, &ch, tmp, gF);
+                if (N) {
+                    if (t > 0)
+                        memcpy(obin, ob_states + ((size_t)(t - 1) * E + e) * nob, sizeof(REAL) * nob);
+                    else if (ob0)
+                        memcpy(obin, ob0 + (size_t)e * nob, sizeof(REAL) * nob);
+                    else
+                        FN(static_ob)(&C, e, obin);
+                }
+                FN(step_env_adj)(&C, P, in, N ? obin : NULL,
+                                 actions + ((size_t)t * E + e) * A * ad, g, N ? gob : NULL, gn,
+                                 N ? gobn : NULL, adj_actions + ((size_t)t * E + e) * A * ad,
+                                 &ch, tmp, gF, obw);
                 memcpy(g, gn, sizeof(FN(agent_t)) * A);
+                if (N) memcpy(gob, gobn, sizeof(REAL) * nob);
             }
             memcpy(adj_state0 + (size_t)e * A * 16, g, sizeof(FN(agent_t)) * A);
+            if (N && adj_ob0) memcpy(adj_ob0 + (size_t)e * nob, gob, sizeof(REAL) * nob);
         }
-        free(ch.st); free(ch.F); free(ch.idx); free(ch.cnt);
-        free(g); free(gn); free(tmp); free(gF);
+        FN(chain_free)(&ch);
+        free(g); free(gn); free(tmp); free(gF); free(ow);
     }
     free(P);
     return err ? -1 : 0;
+}
+
+int FN(oracle_rollout_adj)(const oracle_cfg_t *cfg, const REAL *params, const int32_t *tags,
+                           const int32_t *modes, const oracle_obs_t *obs, int T,
+                           const REAL *state0, const REAL *actions, const REAL *states,
+                           const REAL *adj_states, const REAL *adj_final, REAL *adj_state0,
+                           REAL *adj_actions)
+{
+    FN(ctx_t) C;
+    FN(make_ctx)(cfg, obs, &C);
+    if (C.any_movable) return -2; /* bodies need the obstacle-state entry point */
+    /* without movable bodies the obstacle state is constant: its checkpoints are the
+       installed arrays, rebuilt per step by the _ob entry point from ob0 = NULL */
+    int E = C.n_envs, N = C.n_obs;
+    REAL *obs_st = NULL;
+    if (N) {
+        obs_st = (REAL *)malloc(sizeof(REAL) * (size_t)T * E * OB_W * N);
+        if (!obs_st) return -1;
+        for (int t = 0; t < T; ++t)
+            for (int e = 0; e < E; ++e) FN(static_ob)(&C, e, obs_st + ((size_t)t * E + e) * OB_W * N);
+    }
+    int rc = FN(oracle_rollout_adj_ob)(cfg, params, tags, modes, obs, T, state0, NULL, actions,
+                                       states, obs_st, adj_states, adj_final, NULL, NULL,
+                                       adj_state0, NULL, adj_actions);
+    free(obs_st);
+    return rc;
 }
 
 /* The force pass alone on one state (for the closed-form pins). F out [E,A,2]. */
@@ -1137,14 +1618,16 @@ int FN(oracle_forces)(const oracle_cfg_t *cfg, const REAL *params, const int32_t
     int32_t *idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)A * K);
     int32_t *cnt = (int32_t *)malloc(sizeof(int32_t) * (size_t)A);
     FN(make_prm)(params, tags, modes, A, P);
+    REAL *od = C.n_obs ? (REAL *)malloc(sizeof(REAL) * OB_W * C.n_obs) : NULL;
     for (int e = 0; e < E; ++e) {
         const FN(agent_t) *st = (const FN(agent_t) *)(state + (size_t)e * A * 16);
         if (C.collisions)
             FN(neighbors_env)(A, K, st, C.nbr_radius, idx, cnt, NULL);
         else
             for (int a = 0; a < A; ++a) cnt[a] = 0;
-        FN(forces_env)(&C, e, P, st, idx, cnt, F + (size_t)e * A * 2);
+        if (od) FN(static_ob)(&C, e, od);
+        FN(forces_env)(&C, od, P, st, idx, cnt, F + (size_t)e * A * 2);
     }
-    free(P); free(idx); free(cnt);
+    free(P); free(idx); free(cnt); free(od);
     return 0;
 }

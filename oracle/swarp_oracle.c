@@ -24,12 +24,17 @@ typedef struct {
     int collisions, soft_walls, clamp_bounds, n_threads;
     double dt, k, c, margin, max_overlap, neighbor_radius;
     double bmin_x, bmin_y, bmax_x, bmax_y;
+    double lin_damping, ang_damping; /* movable bodies' viscous decay rates */
 } oracle_cfg_t;
 
 typedef struct {
     int n_obstacles;
     const void *pos, *radius, *angle, *half, *vel, *ang_vel;
     const int32_t *type;
+    /* movable compound bodies (NULL = every obstacle immovable): kind [N] (1 = MOVABLE),
+       body [N] (root shape), mass [N], inertia [N], body_off [N,2] */
+    const int32_t *kind, *body;
+    const void *mass, *inertia, *body_off;
 } oracle_obs_t;
 
 int oracle_abi_version(void) { return 1; }

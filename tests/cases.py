@@ -43,6 +43,8 @@ def oracle_cfg(configs, world: WorldConfig, dt, substeps, n_envs, act_dim, n_thr
         bmax_x=b[1] if b else 0.0,
         bmin_y=b[2] if b else 0.0,
         bmax_y=b[3] if b else 0.0,
+        lin_damping=world.obstacle_linear_damping,
+        ang_damping=world.obstacle_angular_damping,
     )
 
 
@@ -71,6 +73,41 @@ def obstacles_np(obs: dict | None, n_envs: int):
     if ang.ndim == 1:
         ang = np.broadcast_to(ang, (n_envs, n)).copy()
     out["angle"] = ang
+    if obs.get("kind") is not None:
+        out["kind"] = np.asarray(obs["kind"], dtype=np.int32)
+        out["body"] = np.asarray(obs.get("body", np.arange(n)), dtype=np.int32)
+        out["mass"] = np.asarray(obs.get("mass", np.ones(n)), dtype=np.float64)
+        out["inertia"] = np.asarray(obs.get("inertia", np.ones(n)), dtype=np.float64)
+        out["body_off"] = np.asarray(obs.get("body_off", np.zeros((n, 2))), dtype=np.float64)
+    return out
+
+
+def body_seed_np(ob: dict) -> np.ndarray:
+    """Initial obstacle state [E, 12 N] of a filled obstacle dict: each shape's installed
+    pose and velocity, then per index the body state of its root, derived as
+    Stepper._body_seed does (swarp/core/stepper.py:434-476): origin = root pos - R(root
+    angle) root offset, heading / velocity / spin = the root's."""
+    pos, ang, vel, om = ob["pos"], ob["angle"], ob["vel"], ob["ang_vel"]
+    E, n = pos.shape[:2]
+    out = np.zeros((E, 12 * n))
+    sh = out[:, :6 * n].reshape(E, n, 6)
+    sh[..., 0:2] = pos
+    sh[..., 2] = ang
+    sh[..., 3:5] = vel
+    sh[..., 5] = om
+    body = ob.get("body", np.arange(n))
+    off = ob.get("body_off", np.zeros((n, 2)))
+    bd = out[:, 6 * n:].reshape(E, n, 6)
+    for o in range(n):
+        r = int(body[o])
+        ca, sa = np.cos(ang[:, r]), np.sin(ang[:, r])
+        wx = ca * off[r, 0] - sa * off[r, 1]
+        wy = sa * off[r, 0] + ca * off[r, 1]
+        bd[:, o, 0] = pos[:, r, 0] - wx
+        bd[:, o, 1] = pos[:, r, 1] - wy
+        bd[:, o, 2] = ang[:, r]
+        bd[:, o, 3:5] = vel[:, r]
+        bd[:, o, 5] = om[:, r]
     return out
 
 
