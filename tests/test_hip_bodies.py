@@ -1,0 +1,207 @@
+"""Movable compound bodies on the HIP path (swarp/core/bodies.py:367-568) vs the CPU
+oracle, and this build's body adjoint vs finite differences.
+
+Bars: the body pass computes with +, -, *, /, sqrt and a portable sin / cos evaluated
+identically on host and device, so float32 agent states AND obstacle states are compared
+BIT-EXACT with the float32 oracle; gradients within 1e-5 relative (max-norm) of the
+oracle's.  The reference has no gradient through bodies (it skips the body pass on taped
+steps, swarp/core/stepper.py:952), so the adjoint is also checked by fp64 gradcheck.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from cases import nav_agents, obstacles_np, oracle_cfg, params_of
+from hip_helpers import make_stepper, rel, state_to16, to_torch_state
+from oracle.oracle import Oracle, pack_state
+from swarp_amd import rollout
+from swarp_amd.config import WorldConfig
+
+pytestmark = [
+    pytest.mark.gpu,
+    pytest.mark.skip(reason=(
+        "the HIP body path is switched off (set_obstacles raises NotImplementedError for "
+        "MOVABLE obstacles): after these kernels had run on the GPU, a later fp32 drone "
+        "parity test in the same process hit an illegal memory access whose cause has not "
+        "been shown; these tests stay skipped until it is")),
+]
+MOVABLE = 1
+TDT = {np.float32: torch.float32, np.float64: torch.float64}
+
+
+def cross_obs(E, center, d=0.2, r=0.1, mass=1.0, extra=()):
+    """Config 5's body (5 circles in a rigid cross, centre circle as root) plus `extra`
+    circles given as (centre, radius, movable)."""
+    offs = [[0, 0], [d, 0], [-d, 0], [0, d], [0, -d]]
+    inertia = sum(0.5 * (mass / 5) * r * r + (mass / 5) * (o[0] ** 2 + o[1] ** 2) for o in offs)
+    centers = [[center[0] + o[0], center[1] + o[1]] for o in offs]
+    radius, kind, body = [r] * 5, [MOVABLE] * 5, [0] * 5
+    m, inert = [mass] * 5, [inertia] * 5
+    for i, (c, rr, mov) in enumerate(extra):
+        centers.append(list(c))
+        radius.append(rr)
+        kind.append(MOVABLE if mov else 0)
+        body.append(5 + i)
+        offs.append([0.0, 0.0])
+        m.append(0.5)
+        inert.append(0.5 * 0.5 * rr * rr)
+    pos = np.broadcast_to(np.asarray(centers, dtype=np.float64), (E, len(centers), 2)).copy()
+    return {"pos": pos, "radius": np.asarray(radius), "kind": np.asarray(kind, np.int32),
+            "body": np.asarray(body, np.int32), "body_off": np.asarray(offs, np.float64),
+            "mass": np.asarray(m), "inertia": np.asarray(inert)}
+
+
+def run_pair(cfgs, world, dt, S, s0, acts, obs, np_dtype, seed=0):
+    """HIP and oracle rollouts + backward of a random linear loss on the agent trajectory
+    and the obstacle-state trajectory; returns both (states, ob, g_state0, g_ob0, g_act)."""
+    E, A = s0.shape[:2]
+    T = acts.shape[0]
+    td = TDT[np_dtype]
+    st = make_stepper(cfgs, world, dt, S, td, obs=obs, n_envs=E)
+    ob0 = st.ob_state.detach().clone().requires_grad_(True)
+    st.ob_state = ob0
+    rng = np.random.default_rng(seed)
+    w_st = rng.normal(size=(T, E, A, 16))
+    w_st[..., 5:] = 0.0
+    w_ob = rng.normal(size=(T,) + tuple(ob0.shape))
+    s0t = to_torch_state(s0, td, True, 5)
+    a = torch.tensor(acts, dtype=td, device="cuda", requires_grad=True)
+    final, traj = rollout(st, s0t, a)
+    obtr = st.ob_trajectory
+    loss = (torch.tensor(w_ob, dtype=td, device="cuda") * obtr).sum()
+    wt = torch.tensor(w_st, dtype=td, device="cuda")
+    for t in range(T):
+        loss = loss + (wt[t, ..., 0:2] * traj[t].pos).sum() + (wt[t, ..., 2] * traj[t].theta).sum() \
+            + (wt[t, ..., 3:5] * traj[t].vel).sum()
+    loss.backward()
+    hip = (np.stack([state_to16(x) for x in traj]), obtr.detach().double().cpu().numpy(),
+           s0t.pos.grad.double().cpu().numpy(), ob0.grad.double().cpu().numpy(),
+           a.grad.double().cpu().numpy())
+    O = Oracle(np_dtype)
+    cfg = oracle_cfg(cfgs, world, dt, S, E, acts.shape[-1], n_threads=8)
+    p, t_, m = params_of(cfgs)
+    ob = obstacles_np(obs, E)
+    ob0n = ob0.detach().cpu().numpy().astype(np_dtype)
+    s0n, actn = s0.astype(np_dtype), acts.astype(np_dtype)
+    ost, oob = O.rollout_ob(cfg, p, t_, m, ob, s0n, ob0n, actn)
+    g0, gob0, ga = O.rollout_adj_ob(cfg, p, t_, m, ob, s0n, ob0n, actn, ost, oob, w_st, None,
+                                    w_ob, None)
+    orc = (ost.astype(np.float64), oob.astype(np.float64), g0[..., 0:2].astype(np.float64),
+           gob0.astype(np.float64), ga.astype(np.float64))
+    return hip, orc
+
+
+def check(name, hip, orc, exact=True, g_tol=1e-5):
+    hs, hob, hg0, hgob, hga = hip
+    os_, oob, og0, ogob, oga = orc
+    if exact:
+        assert np.array_equal(hs[..., :7], os_[..., :7]), (
+            f"{name}: agent states not bit-exact (rel {rel(hs[..., :7], os_[..., :7]):.2e})")
+        assert np.array_equal(hob, oob), f"{name}: obstacle states not bit-exact (rel {rel(hob, oob):.2e})"
+    else:
+        assert rel(hs[..., :7], os_[..., :7]) <= 1e-12 and rel(hob, oob) <= 1e-12, name
+    assert rel(hga, oga) <= g_tol, f"{name}: d/d actions rel {rel(hga, oga):.3e}"
+    assert rel(hg0, og0) <= g_tol, f"{name}: d/d pos0 rel {rel(hg0, og0):.3e}"
+    assert rel(hgob, ogob) <= g_tol, f"{name}: d/d ob0 rel {rel(hgob, ogob):.3e}"
+
+
+def _world(bounds=1.5, mode="soft", **kw):
+    base = dict(collisions=True, collision_k=100.0, collision_c=1.0, collision_margin=0.025,
+                bounds=None if bounds is None else (-bounds, bounds, -bounds, bounds),
+                bounds_mode=mode, max_neighbors=16, neighbor_radius=0.3)
+    base.update(kw)
+    return WorldConfig(**base)
+
+
+def _pushers(E, A, seed, spread=0.6):
+    rng = np.random.default_rng(seed)
+    pos = rng.uniform(-spread, spread, size=(E, A, 2))
+    acts = rng.uniform(-1, 1, size=(8, E, A, 2))
+    # half the agents drive towards the body at the origin
+    acts[..., : A // 2, :] = -pos[None, :, : A // 2, :] / np.linalg.norm(pos[None, :, : A // 2, :],
+                                                                         axis=-1, keepdims=True)
+    return pack_state({"pos": pos}), acts
+
+
+def test_bodies_match_oracle_multi_env_waves():
+    """12 agents per env (4 envs per wave, last wave partial): a cross body, a second
+    movable circle and a static circle; soft walls."""
+    E, A = 37, 12
+    s0, acts = _pushers(E, A, 1)
+    obs = cross_obs(E, (0.0, 0.0), extra=(((0.55, 0.1), 0.12, True), ((-0.5, -0.45), 0.1, False)))
+    hip, orc = run_pair(nav_agents(A), _world(), 0.05, 4, s0, acts, obs, np.float32)
+    check("multi-env", hip, orc)
+    assert np.abs(orc[1][-1, :, 6 * 7 + 5]).max() > 1e-3, "the cross never turned"
+
+
+def test_bodies_match_oracle_config5_shape():
+    """Config 5's shape at reduced E: 64 agents per env (one env per wave), radius-0.3
+    lists capped at K=16."""
+    E, A = 6, 64
+    s0, acts = _pushers(E, A, 2, spread=1.2)
+    obs = cross_obs(E, (0.0, 0.0))
+    hip, orc = run_pair(nav_agents(A), _world(bounds=3.0), 0.05, 4, s0, acts, obs, np.float32)
+    check("config5", hip, orc)
+
+
+def test_bodies_clamp_bounds():
+    E, A = 8, 8
+    s0, acts = _pushers(E, A, 3, spread=0.4)
+    acts[...] = np.array([1.0, 0.0])
+    obs = cross_obs(E, (0.15, 0.0))
+    hip, orc = run_pair(nav_agents(A), _world(bounds=0.55, mode="clamp"), 0.05, 4, s0, acts, obs,
+                        np.float32)
+    check("clamp", hip, orc)
+
+
+def test_bodies_float64_matches_float64_oracle():
+    E, A = 5, 6
+    s0, acts = _pushers(E, A, 4, spread=0.4)
+    obs = cross_obs(E, (0.0, 0.0), extra=(((0.4, 0.0), 0.1, True),))
+    hip, orc = run_pair(nav_agents(A), _world(), 0.05, 2, s0, acts, obs, np.float64)
+    check("f64", hip, orc, exact=True, g_tol=1e-12)
+
+
+def test_body_gradcheck_fp64():
+    """torch.autograd.gradcheck through rollout with a movable body: d(final body state,
+    final agent positions)/d(actions, initial obstacle state)."""
+    E, A, T = 2, 3, 3
+    cfgs = nav_agents(A, max_speed=100.0)
+    world = _world(collision_k=40.0, collision_c=0.5, bounds=None)
+    obs = cross_obs(E, (0.0, 0.0), d=0.15, r=0.08, extra=(((0.33, 0.05), 0.09, True),))
+    st = make_stepper(cfgs, world, 0.05, 2, torch.float64, obs=obs, n_envs=E)
+    base_ob = st.ob_state.detach().clone()
+    pos = torch.tensor([[[-0.2, 0.03], [0.1, -0.19], [0.05, 0.24]],
+                        [[-0.21, -0.02], [0.12, 0.2], [0.42, 0.1]]], dtype=torch.float64,
+                       device="cuda")
+    z = torch.zeros(E, A, dtype=torch.float64, device="cuda")
+    acts0 = torch.tensor(np.random.default_rng(5).normal(size=(T, E, A, 2)) * 0.5,
+                         dtype=torch.float64, device="cuda")
+
+    def f(acts, ob0):
+        st.ob_state = ob0
+        from swarp_amd import TorchState
+        s = TorchState(pos, z, torch.zeros(E, A, 2, dtype=torch.float64, device="cuda"), z, z)
+        final, _ = rollout(st, s, acts)
+        return final.pos, st.ob_state
+
+    assert torch.autograd.gradcheck(f, (acts0.clone().requires_grad_(True),
+                                        base_ob.clone().requires_grad_(True)),
+                                    eps=1e-6, atol=1e-5, rtol=1e-4)
+
+
+def test_grad_and_nograd_forward_agree_and_state_advances():
+    E, A = 4, 8
+    s0, acts = _pushers(E, A, 6, spread=0.5)
+    obs = cross_obs(E, (0.0, 0.0))
+    st = make_stepper(nav_agents(A), _world(), 0.05, 4, torch.float32, obs=obs, n_envs=E)
+    ob0 = st.ob_state.clone()
+    a = torch.tensor(acts, dtype=torch.float32, device="cuda")
+    with torch.no_grad():
+        f1, _ = rollout(st, to_torch_state(s0, torch.float32, False, 5), a)
+    ob1 = st.ob_state.clone()
+    st.ob_state = ob0.clone()
+    f2, _ = rollout(st, to_torch_state(s0, torch.float32, True, 5), a.clone().requires_grad_(True))
+    assert torch.equal(f1.pos, f2.pos.detach()) and torch.equal(ob1, st.ob_state.detach())
+    assert not torch.equal(ob1, ob0), "the obstacle state did not advance"
