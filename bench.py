@@ -183,12 +183,15 @@ def main():
         el_f = time.perf_counter() - t1
     fwd_only = E * T * args.steps / el_f
 
+    # the library launches the specialised holonomic-velocity kernels when the desc allows
+    fam = "k_holo" if stepper.desc(E, 2).holo_velocity_only else "k_rollout"
+    pa = 1 << max(2, (A - 1).bit_length())
     kernels = {}
     for kind, per in (("fwd", fwd_bytes(A)), ("bwd", bwd_bytes(A))):
         d = sum(dur[kind]) / max(len(dur[kind]), 1)
         alg = per * E * T
         kernels[kind] = {
-            "name": f"k_rollout_{kind}<float,16>",
+            "name": f"{fam}_{kind}<float, {pa}>",
             "avg_ms": d * 1e3,
             "alg_bytes_per_launch": alg,
             "achieved_GBps": alg / d / 1e9 if d > 0 else None,
