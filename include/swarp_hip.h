@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 1
+#define SWARP_ABI_VERSION 2
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -93,6 +93,33 @@ int swarp_rollout_bwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *
                       const void *actions, const swarp_state_t *traj,
                       const swarp_state_t *adj_traj, const swarp_state_t *adj_final,
                       const swarp_state_t *adj_state0, void *adj_actions, void *stream);
+
+/* Rollout tape: what the backward's reverse pass reads besides the checkpoints (the
+ * input velocity of substeps 1..S-1, each substep's uncapped neighbour mask and
+ * active-contact mask, the wall-contact bits, the last step's output velocity), written
+ * by the forward so that the backward does not recompute the substeps.  Counterpart of
+ * the taped substep buffers the reference keeps alive for wp.Tape.backward
+ * (StepBuffers / make_buffers, swarp/core/stepper.py:55-63, 642-678).
+ * Writes in *bytes the tape size of a T-step rollout of this configuration; 0 when the
+ * configuration keeps no tape (only fleets on the specialised holonomic-velocity kernels
+ * with substeps <= 4 and contacts or walls do), in which case the _tape entry points
+ * behave as the plain ones. */
+int swarp_tape_bytes(const swarp_desc_t *desc, int32_t T, uint64_t *bytes);
+
+/* swarp_rollout_fwd that also writes the tape (`tape_bytes` must be
+ * swarp_tape_bytes(desc, T); the tape is device memory owned by the caller). */
+int swarp_rollout_fwd_tape(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                           const void *actions, const swarp_state_t *traj,
+                           const swarp_state_t *final_state, void *tape, uint64_t tape_bytes,
+                           void *stream);
+
+/* swarp_rollout_bwd reading the substep intermediates from the tape written by
+ * swarp_rollout_fwd_tape on the same inputs (same results, bit for bit). */
+int swarp_rollout_bwd_tape(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                           const void *actions, const swarp_state_t *traj,
+                           const swarp_state_t *adj_traj, const swarp_state_t *adj_final,
+                           const swarp_state_t *adj_state0, void *adj_actions,
+                           const void *tape, uint64_t tape_bytes, void *stream);
 
 /* Padded radius-neighbour lists of one state: replaces NeighborGrid.query_into's
  * brute-force kernel (swarp/core/neighbors.py:76-97, 465-492).  pos [E,A,2] of

@@ -11,7 +11,7 @@ import ctypes
 import os
 from pathlib import Path
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 F32, F64 = 0, 1
 
 _PKG = Path(__file__).resolve().parent
@@ -78,6 +78,23 @@ SIGNATURES = {
         [ctypes.POINTER(SwarpDesc), ctypes.c_int32, ctypes.POINTER(SwarpState), ctypes.c_void_p,
          ctypes.POINTER(SwarpState), ctypes.POINTER(SwarpState), ctypes.POINTER(SwarpState),
          ctypes.POINTER(SwarpState), ctypes.c_void_p, ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "swarp_tape_bytes": (
+        [ctypes.POINTER(SwarpDesc), ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64)],
+        ctypes.c_int,
+    ),
+    "swarp_rollout_fwd_tape": (
+        [ctypes.POINTER(SwarpDesc), ctypes.c_int32, ctypes.POINTER(SwarpState), ctypes.c_void_p,
+         ctypes.POINTER(SwarpState), ctypes.POINTER(SwarpState), ctypes.c_void_p, ctypes.c_uint64,
+         ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "swarp_rollout_bwd_tape": (
+        [ctypes.POINTER(SwarpDesc), ctypes.c_int32, ctypes.POINTER(SwarpState), ctypes.c_void_p,
+         ctypes.POINTER(SwarpState), ctypes.POINTER(SwarpState), ctypes.POINTER(SwarpState),
+         ctypes.POINTER(SwarpState), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
+         ctypes.c_void_p],
         ctypes.c_int,
     ),
     "swarp_neighbors": (

@@ -119,8 +119,10 @@ def _validate(stepper: Stepper, state: TorchState, actions_seq: torch.Tensor) ->
     return T, E, ad
 
 
-def _launch_fwd(stepper: Stepper, state0, actions_seq: torch.Tensor, traj, final) -> None:
-    """One forward launch; ``traj``/``final`` are field lists (``traj`` stacked [T-1,...])."""
+def _launch_fwd(stepper: Stepper, state0, actions_seq: torch.Tensor, traj, final,
+                tape: torch.Tensor | None = None) -> None:
+    """One forward launch; ``traj``/``final`` are field lists (``traj`` stacked [T-1,...]).
+    ``tape`` (uint8, ``Stepper.tape_bytes`` long) also receives the rollout tape."""
     T, E, _, ad = actions_seq.shape
     nf = _nfields(stepper)
     lib = _lib.load()
@@ -128,9 +130,16 @@ def _launch_fwd(stepper: Stepper, state0, actions_seq: torch.Tensor, traj, final
     s0 = state_struct(list(state0)[:nf])
     fin = state_struct(list(final)[:nf])
     tr = state_struct(list(traj)[:nf]) if traj is not None and T > 1 else None
-    _lib.check(lib.swarp_rollout_fwd(
+    if tape is None:
+        _lib.check(lib.swarp_rollout_fwd(
+            ctypes.byref(desc), T, ctypes.byref(s0), actions_seq.data_ptr(),
+            ctypes.byref(tr) if tr is not None else None, ctypes.byref(fin), _stream(actions_seq),
+        ))
+        return
+    _lib.check(lib.swarp_rollout_fwd_tape(
         ctypes.byref(desc), T, ctypes.byref(s0), actions_seq.data_ptr(),
-        ctypes.byref(tr) if tr is not None else None, ctypes.byref(fin), _stream(actions_seq),
+        ctypes.byref(tr) if tr is not None else None, ctypes.byref(fin), tape.data_ptr(),
+        tape.numel(), _stream(actions_seq),
     ))
 
 
@@ -156,15 +165,19 @@ class _RolloutFn(torch.autograd.Function):
             traj = _empty_like_fields(stepper, (max(T - 1, 0),), E, dev)
         else:
             final, traj = bufs
+        # the rollout tape lets the backward skip recomputing the substeps
+        nb = stepper.tape_bytes(E, actions_seq.shape[3], T)
+        tape = torch.empty(nb, device=dev, dtype=torch.uint8) if nb else None
         sink = KERNEL_EVENTS
         if sink is not None:
             e0 = _event(actions_seq)
-        _launch_fwd(stepper, state0, actions_seq, traj, final)
+        _launch_fwd(stepper, state0, actions_seq, traj, final, tape)
         if sink is not None:
             sink.append(("fwd", e0, _event(actions_seq)))
         ctx.stepper = stepper
         ctx.nf = len(state0)
         ctx.T = T
+        ctx.tape = tape
         ctx.save_for_backward(actions_seq, *state0, *traj)
         return (*final, *traj)
 
@@ -192,13 +205,24 @@ class _RolloutFn(torch.autograd.Function):
         sink = KERNEL_EVENTS
         if sink is not None:
             e0 = _event(actions_seq)
-        _lib.check(lib.swarp_rollout_bwd(
-            ctypes.byref(desc), T, ctypes.byref(s0), actions_seq.data_ptr(),
-            ctypes.byref(tr) if tr is not None else None,
-            ctypes.byref(gtr) if gtr is not None else None,
-            ctypes.byref(gfin) if gfin is not None else None,
-            ctypes.byref(a0), adj_act.data_ptr(), _stream(actions_seq),
-        ))
+        tape = ctx.tape
+        if tape is None:
+            _lib.check(lib.swarp_rollout_bwd(
+                ctypes.byref(desc), T, ctypes.byref(s0), actions_seq.data_ptr(),
+                ctypes.byref(tr) if tr is not None else None,
+                ctypes.byref(gtr) if gtr is not None else None,
+                ctypes.byref(gfin) if gfin is not None else None,
+                ctypes.byref(a0), adj_act.data_ptr(), _stream(actions_seq),
+            ))
+        else:
+            _lib.check(lib.swarp_rollout_bwd_tape(
+                ctypes.byref(desc), T, ctypes.byref(s0), actions_seq.data_ptr(),
+                ctypes.byref(tr) if tr is not None else None,
+                ctypes.byref(gtr) if gtr is not None else None,
+                ctypes.byref(gfin) if gfin is not None else None,
+                ctypes.byref(a0), adj_act.data_ptr(), tape.data_ptr(), tape.numel(),
+                _stream(actions_seq),
+            ))
         if sink is not None:
             sink.append(("bwd", e0, _event(actions_seq)))
         return (None, None, adj_act if need[2] else None, *adj0)

@@ -123,12 +123,101 @@ __device__ __forceinline__ void lean_forces(const Cst<T> &C, const P2<T> *lp, co
     Fy = fy + sy;
 }
 
-template <typename T, int PA>
-__global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g)
+// ------------------------------------------------------------------ rollout tape
+//
+// What the reverse pass of a step reads besides the step's input checkpoint, written by
+// the forward so that the backward does not recompute the step (substep count <= 4):
+//   rec [T][workgroup][chunk][lane] 16-byte chunks: per step and lane one record of
+//       TapeRec::R bytes (NC = R / 16 chunks) holding
+//       TAPE_MAX_S mask words   per substep the inclusion mask (uncapped lists) and the
+//                               active-contact mask, packed as one TapeW word
+//       TAPE_MAX_S - 1 pairs    input velocity of substeps 1..S-1 (positions follow exactly
+//                               as p_{s+1} = p_s + v_{s+1} * sub_dt, the forward's own update)
+//       one 32-bit word         wall-contact bits, 2 per substep
+//   vl  [workgroup][lane] pairs output velocity of the last step (the backward takes no
+//                               final state; every other step's output velocity is a
+//                               checkpoint)
+// Slots past the configuration's substep count are left unwritten.  The tape is private
+// to the two kernels, so it is indexed by lane rather than by agent: each 16-byte chunk
+// store of the forward and load of the backward moves 1 KB of contiguous memory per wave.
+// Lanes without an agent write records the backward never reads.
+constexpr int TAPE_MAX_S = 4;
+
+template <typename T> struct Tape {
+    void *rec;
+    T *vl;
+};
+
+// Mask word of one agent and substep: inclusion bits, then active-contact bits.
+template <int PA> struct TapeW {
+    typedef uint32_t type;  // PA <= 16: incl | act << 16
+    static __device__ __forceinline__ type pack(uint32_t in, uint32_t ac) { return in | ac << 16; }
+    static __device__ __forceinline__ uint32_t incl(type w) { return w & 0xffffu; }
+    static __device__ __forceinline__ uint32_t act(type w) { return w >> 16; }
+};
+template <> struct TapeW<32> {
+    typedef uint64_t type;
+    static __device__ __forceinline__ type pack(uint32_t in, uint32_t ac)
+    {
+        return (uint64_t)in | (uint64_t)ac << 32;
+    }
+    static __device__ __forceinline__ uint32_t incl(type w) { return (uint32_t)w; }
+    static __device__ __forceinline__ uint32_t act(type w) { return (uint32_t)(w >> 32); }
+};
+struct alignas(16) MaskPair64 {
+    uint64_t in, ac;
+};
+template <> struct TapeW<64> {
+    typedef MaskPair64 type;
+    static __device__ __forceinline__ type pack(uint64_t in, uint64_t ac) { return {in, ac}; }
+    static __device__ __forceinline__ uint64_t incl(type w) { return w.in; }
+    static __device__ __forceinline__ uint64_t act(type w) { return w.ac; }
+};
+
+// Byte layout of one tape record.
+template <typename T, int PA> struct TapeRec {
+    typedef typename TapeW<PA>::type W;
+    static constexpr int OM = 0;
+    static constexpr int OV = TAPE_MAX_S * (int)sizeof(W);
+    static constexpr int OW = OV + (TAPE_MAX_S - 1) * (int)sizeof(P2<T>);
+    static constexpr int R = (OW + 4 + 15) / 16 * 16;
+    static constexpr int NC = R / 16;
+};
+
+struct alignas(16) Chunk16 {
+    uint32_t d[4];
+};
+
+// Write `v` at byte `off` of this lane's record staged in LDS as [chunk][lane] 16-byte
+// cells (every field lies inside one chunk).
+template <typename X>
+__device__ __forceinline__ void stage_put(unsigned char *st, int lane, int off, const X &v)
+{
+    __builtin_memcpy(st + (((off >> 4) * 64 + lane) << 4) + (off & 15), &v, sizeof(X));
+}
+
+// Read the field of type X at byte `off` of a record held in registers.
+template <typename X, int NC>
+__device__ __forceinline__ X rec_get(const Chunk16 (&r)[NC], int off)
+{
+    X x;
+    __builtin_memcpy(&x, (const unsigned char *)r + off, sizeof(X));
+    return x;
+}
+
+template <typename T, int PA, bool TAPE>
+__global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g,
+                                                 const Tape<T> tp)
 {
     typedef typename MaskT<PA>::type M;
+    typedef TapeW<PA> TW;
+    typedef TapeRec<T, PA> TR;
     __shared__ P2<T> lp[64], lv[64];
     __shared__ T lr[64];
+    // tape staging: each lane writes and reads back only its own record, so the step's
+    // tape goes to memory with the state stores, after the prefetched action is used
+    __shared__ Chunk16 tst[TAPE ? TR::NC * 64 : 1];
+    unsigned char *const tsb = (unsigned char *)tst;
     const int lane = threadIdx.x, me = lane % PA, base = lane - me;
     const int env = blockIdx.x * (64 / PA) + lane / PA;
     const bool real = me < C.A;
@@ -153,8 +242,8 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
     for (int t = 0; t < g.nsteps; ++t) {
         P2<T> an = a;
         if (t + 1 < g.nsteps) an = ld2(g.act, (size_t)(t + 1) * EA + i);
-        M cand = 0, incl, act;
-        unsigned wb;
+        M cand = 0, incl = 0, act = 0;
+        unsigned wb = 0u, wbits = 0u;
         T D = T(0);
         bool ok = false;
         for (int s = 0; s < C.S; ++s) {
@@ -171,6 +260,11 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
             }
             const T vnx = cnx + Fx * dtm, vny = cny + Fy * dtm;
             const T pnx = p.x + vnx * dt, pny = p.y + vny * dt;
+            if (TAPE) {
+                stage_put(tsb, lane, TR::OM + s * (int)sizeof(typename TW::type), TW::pack(incl, act));
+                wbits |= wb << (2 * s);
+                if (s + 1 < C.S) stage_put(tsb, lane, TR::OV + s * (int)sizeof(P2<T>), P2<T>{vnx, vny});
+            }
             if (C.use_skin) {
                 D += (m_abs(pnx - p.x) + m_abs(pny - p.y)) * T(1.0001);
                 ok = env_all<PA>(!real || D <= C.half_margin, base);
@@ -194,13 +288,27 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
             f[3][j] = m_sqrt(v.x * v.x + v.y * v.y);
             f[4][j] = T(0);
         }
+        if (TAPE) {
+            stage_put(tsb, lane, TR::OW, (uint32_t)wbits);
+            Chunk16 c[TR::NC];
+#pragma unroll
+            for (int k = 0; k < TR::NC; ++k) c[k] = tst[k * 64 + lane];
+            Chunk16 *dst = (Chunk16 *)tp.rec + ((size_t)t * gridDim.x + blockIdx.x) * TR::NC * 64 + lane;
+#pragma unroll
+            for (int k = 0; k < TR::NC; ++k) dst[k * 64] = c[k];
+            if (t + 1 == g.nsteps) st2(tp.vl, (size_t)blockIdx.x * 64 + lane, v.x, v.y);
+        }
     }
 }
 
-template <typename T, int PA>
-__global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g)
+template <typename T, int PA, bool TAPE>
+__global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g,
+                                                 const Tape<T> tp)
 {
     typedef typename MaskT<PA>::type M;
+    typedef TapeW<PA> TW;
+    typedef typename TW::type W;
+    typedef TapeRec<T, PA> TR;
     extern __shared__ __align__(16) unsigned char smem[];
     // per substep slot: P2 pos[64], P2 vel[64]; then inclusion masks [S][64], active-contact
     // masks [S][64]; then gF[64], r[64], dd[64]; then wall bits [S][64] (bytes)
@@ -249,6 +357,24 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
         return r;
     };
     Arr arr = arrival(t);
+    // tape record of step tt (TAPE), one step ahead like the checkpoint
+    struct Tp {
+        Chunk16 c[TR::NC];
+    };
+    auto tape_of = [&](int tt) {
+        Tp r;
+        const Chunk16 *src =
+            (const Chunk16 *)tp.rec + ((size_t)tt * gridDim.x + blockIdx.x) * TR::NC * 64 + lane;
+#pragma unroll
+        for (int k = 0; k < TR::NC; ++k) r.c[k] = src[k * 64];
+        return r;
+    };
+    Tp tc;
+    P2<T> vout = {T(0), T(0)};  // output velocity of step t (TAPE)
+    if (TAPE) {
+        tc = tape_of(t);
+        vout = ld2(tp.vl, (size_t)blockIdx.x * 64 + lane);
+    }
     // resolve the initial loads here: a load still in flight at the loop entry makes every
     // iteration wait for all outstanding memory operations, prefetch and stores included
     __builtin_amdgcn_s_waitcnt(0);
@@ -268,16 +394,46 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
             an = ld2(g.act, (size_t)(t - 1) * EA + i);
             arn = arrival(t - 1);
         }
+        Tp tn;
+        if (TAPE) {
+            tn = tc;
+            if (t > 0) tn = tape_of(t - 1);
+        }
         if (!real) p.x = p.y = qnan;
         T cnx, cny;
         clamp_norm(a.x, a.y, vmax, cnx, cny);
+        const P2<T> vin = v;
 
-        // ---- recompute the substeps of step t into LDS
+        // ---- the substeps of step t into LDS: from the tape, or recomputed
+        if (TAPE) {
+            __syncthreads();  // the previous step's reverse pass is done with the slots
+            P2<T> pp = p, vv = v;
+            const unsigned wall = active ? rec_get<uint32_t>(tc.c, TR::OW) : 0u;
+#pragma unroll
+            for (int s = 0; s < TAPE_MAX_S; ++s) {
+                if (s < C.S) {
+                    P2<T> *sp = slot + s * 128;
+                    sp[lane] = pp;
+                    sp[64 + lane] = vv;
+                    const W w = rec_get<W>(tc.c, TR::OM + s * (int)sizeof(W));
+                    lm[s * 64 + lane] = active ? (M)TW::incl(w) : M(0);
+                    la[s * 64 + lane] = active ? (M)TW::act(w) : M(0);
+                    lw[s * 64 + lane] = (unsigned char)((wall >> (2 * s)) & 3u);
+                    if (s + 1 < TAPE_MAX_S && s + 1 < C.S) {
+                        vv = rec_get<P2<T>>(tc.c, TR::OV + s * (int)sizeof(P2<T>));
+                        pp.x = pp.x + vv.x * dt;
+                        pp.y = pp.y + vv.y * dt;
+                    }
+                }
+            }
+            __syncthreads();
+            v = vout;
+        }
         M cand = 0, incl, act;
         unsigned wb;
         T D = T(0);
         bool ok = false;
-        for (int s = 0; s < C.S; ++s) {
+        for (int s = 0; s < (TAPE ? 0 : C.S); ++s) {
             P2<T> *sp = slot + s * 128;
             __syncthreads();
             sp[lane] = p;
@@ -378,6 +534,10 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
         v = vn;
         a = an;
         arr = arn;
+        if (TAPE) {
+            vout = vin;
+            tc = tn;
+        }
     }
     if (active) {
         T *const *f = g.a0.f;

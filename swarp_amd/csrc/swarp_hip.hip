@@ -735,39 +735,88 @@ static bool lean_ok(const swarp_desc_t *d)
     return d->holo_velocity_only && !d->has_drone && d->n_obstacles == 0 && !d->clamp_bounds;
 }
 
-template <typename T> static void launch_holo_fwd(int PA, const Cst<T> &C, const Args<T> &a, hipStream_t st)
+// Byte offsets of the tape regions (see lean.hpp); total == 0: no tape.
+struct TapeLayout {
+    uint64_t rec, vl, total;
+};
+
+static uint64_t align256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
+
+template <typename T> static uint64_t tape_rec_bytes(int PA)
+{
+    switch (PA) {
+    case 4: return TapeRec<T, 4>::R;
+    case 8: return TapeRec<T, 8>::R;
+    case 16: return TapeRec<T, 16>::R;
+    case 32: return TapeRec<T, 32>::R;
+    default: return TapeRec<T, 64>::R;
+    }
+}
+
+static TapeLayout tape_layout(const swarp_desc_t *d, int32_t nT)
+{
+    TapeLayout L = {0, 0, 0};
+    const bool forces = d->collisions || d->soft_walls;
+    if (!lean_ok(d) || !forces || d->substeps > TAPE_MAX_S || nT < 1) return L;
+    const bool f32 = d->dtype == SWARP_F32;
+    const int PA = pad_agents(d->n_agents);
+    const uint64_t R = f32 ? tape_rec_bytes<float>(PA) : tape_rec_bytes<double>(PA);
+    // one record per step and lane of every workgroup (64 / PA envs each)
+    const uint64_t lanes = (uint64_t)((d->n_envs + 64 / PA - 1) / (64 / PA)) * 64;
+    L.rec = 0;
+    L.vl = align256((uint64_t)nT * lanes * R);
+    L.total = align256(L.vl + lanes * 2 * (f32 ? 4 : 8));
+    return L;
+}
+
+template <typename T> static Tape<T> tape_ptrs(const TapeLayout &L, void *base)
+{
+    Tape<T> tp = {nullptr, nullptr};
+    if (!base || L.total == 0) return tp;
+    unsigned char *b = (unsigned char *)base;
+    tp.rec = (void *)(b + L.rec);
+    tp.vl = (T *)(b + L.vl);
+    return tp;
+}
+
+template <typename T, bool TAPE>
+static void launch_holo_fwd(int PA, const Cst<T> &C, const Args<T> &a, const Tape<T> &tp,
+                            hipStream_t st)
 {
     const size_t shm = 0;
     const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
         grid32((C.E + 1) / 2), grid64(C.E);
     switch (PA) {
-    case 4: hipLaunchKernelGGL((k_holo_fwd<T, 4>), grid4, dim3(64), shm, st, C, a); break;
-    case 8: hipLaunchKernelGGL((k_holo_fwd<T, 8>), grid8, dim3(64), shm, st, C, a); break;
-    case 16: hipLaunchKernelGGL((k_holo_fwd<T, 16>), grid16, dim3(64), shm, st, C, a); break;
-    case 32: hipLaunchKernelGGL((k_holo_fwd<T, 32>), grid32, dim3(64), shm, st, C, a); break;
-    default: hipLaunchKernelGGL((k_holo_fwd<T, 64>), grid64, dim3(64), shm, st, C, a); break;
+    case 4: hipLaunchKernelGGL((k_holo_fwd<T, 4, TAPE>), grid4, dim3(64), shm, st, C, a, tp); break;
+    case 8: hipLaunchKernelGGL((k_holo_fwd<T, 8, TAPE>), grid8, dim3(64), shm, st, C, a, tp); break;
+    case 16: hipLaunchKernelGGL((k_holo_fwd<T, 16, TAPE>), grid16, dim3(64), shm, st, C, a, tp); break;
+    case 32: hipLaunchKernelGGL((k_holo_fwd<T, 32, TAPE>), grid32, dim3(64), shm, st, C, a, tp); break;
+    default: hipLaunchKernelGGL((k_holo_fwd<T, 64, TAPE>), grid64, dim3(64), shm, st, C, a, tp); break;
     }
 }
 
-template <typename T>
-static void launch_holo_bwd(int PA, const Cst<T> &C, const Args<T> &a, size_t shm, hipStream_t st)
+template <typename T, bool TAPE>
+static void launch_holo_bwd(int PA, const Cst<T> &C, const Args<T> &a, const Tape<T> &tp,
+                            size_t shm, hipStream_t st)
 {
     const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
         grid32((C.E + 1) / 2), grid64(C.E);
     switch (PA) {
-    case 4: hipLaunchKernelGGL((k_holo_bwd<T, 4>), grid4, dim3(64), shm, st, C, a); break;
-    case 8: hipLaunchKernelGGL((k_holo_bwd<T, 8>), grid8, dim3(64), shm, st, C, a); break;
-    case 16: hipLaunchKernelGGL((k_holo_bwd<T, 16>), grid16, dim3(64), shm, st, C, a); break;
-    case 32: hipLaunchKernelGGL((k_holo_bwd<T, 32>), grid32, dim3(64), shm, st, C, a); break;
-    default: hipLaunchKernelGGL((k_holo_bwd<T, 64>), grid64, dim3(64), shm, st, C, a); break;
+    case 4: hipLaunchKernelGGL((k_holo_bwd<T, 4, TAPE>), grid4, dim3(64), shm, st, C, a, tp); break;
+    case 8: hipLaunchKernelGGL((k_holo_bwd<T, 8, TAPE>), grid8, dim3(64), shm, st, C, a, tp); break;
+    case 16: hipLaunchKernelGGL((k_holo_bwd<T, 16, TAPE>), grid16, dim3(64), shm, st, C, a, tp); break;
+    case 32: hipLaunchKernelGGL((k_holo_bwd<T, 32, TAPE>), grid32, dim3(64), shm, st, C, a, tp); break;
+    default: hipLaunchKernelGGL((k_holo_bwd<T, 64, TAPE>), grid64, dim3(64), shm, st, C, a, tp); break;
     }
 }
 
 template <typename T>
 static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s0,
                        const void *act, const swarp_state_t *traj, const swarp_state_t *fin,
-                       hipStream_t st)
+                       void *tape, uint64_t tape_bytes, hipStream_t st)
 {
+    const TapeLayout TL = tape_layout(d, nT);
+    if (tape && tape_bytes != TL.total) return fail("tape_bytes does not match swarp_tape_bytes");
     Cst<T> C;
     fill_cst<T>(d, skin_of(d), C);
     Args<T> a;
@@ -784,7 +833,10 @@ static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     a.nsteps = nT;
     const int PA = pad_agents(d->n_agents);
     if (lean_ok(d))
-        launch_holo_fwd<T>(PA, C, a, st);
+        if (tape && TL.total)
+            launch_holo_fwd<T, true>(PA, C, a, tape_ptrs<T>(TL, tape), st);
+        else
+            launch_holo_fwd<T, false>(PA, C, a, tape_ptrs<T>(TL, nullptr), st);
     else if (d->has_drone)
         launch_fwd<T, true>(PA, C, a, st);
     else
@@ -798,8 +850,10 @@ template <typename T>
 static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s0,
                        const void *act, const swarp_state_t *traj, const swarp_state_t *atraj,
                        const swarp_state_t *afin, const swarp_state_t *a0, void *aact,
-                       hipStream_t st)
+                       const void *tape, uint64_t tape_bytes, hipStream_t st)
 {
+    const TapeLayout TL = tape_layout(d, nT);
+    if (tape && tape_bytes != TL.total) return fail("tape_bytes does not match swarp_tape_bytes");
     Cst<T> C;
     fill_cst<T>(d, skin_of(d), C);
     Args<T> a;
@@ -823,7 +877,10 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
                             (size_t)d->substeps * 64 * msz * 2 + 64 * 2 * sizeof(T) +
                             2 * 64 * sizeof(T) + (size_t)d->substeps * 64;
         if (lshm > 65536) return fail("substeps too large for the backward LDS staging (limit 64 KiB per wave)");
-        launch_holo_bwd<T>(PA, C, a, lshm, st);
+        if (tape && TL.total)
+            launch_holo_bwd<T, true>(PA, C, a, tape_ptrs<T>(TL, (void *)tape), lshm, st);
+        else
+            launch_holo_bwd<T, false>(PA, C, a, tape_ptrs<T>(TL, nullptr), lshm, st);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return fail(hipGetErrorString(e));
         return 0;
@@ -857,8 +914,33 @@ int swarp_rollout_fwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *
     if (T < 1) return fail("T must be >= 1");
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
-        return rollout_fwd<float>(desc, T, state0, actions, traj, final_state, st);
-    return rollout_fwd<double>(desc, T, state0, actions, traj, final_state, st);
+        return rollout_fwd<float>(desc, T, state0, actions, traj, final_state, nullptr, 0, st);
+    return rollout_fwd<double>(desc, T, state0, actions, traj, final_state, nullptr, 0, st);
+}
+
+int swarp_tape_bytes(const swarp_desc_t *desc, int32_t T, uint64_t *bytes)
+{
+    g_err[0] = 0;
+    if (check_desc(desc)) return -1;
+    if (T < 1) return fail("T must be >= 1");
+    if (!bytes) return fail("bytes is NULL");
+    *bytes = tape_layout(desc, T).total;
+    return 0;
+}
+
+int swarp_rollout_fwd_tape(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                           const void *actions, const swarp_state_t *traj,
+                           const swarp_state_t *final_state, void *tape, uint64_t tape_bytes,
+                           void *stream)
+{
+    g_err[0] = 0;
+    if (check_desc(desc)) return -1;
+    if (T < 1) return fail("T must be >= 1");
+    if (!tape && tape_bytes) return fail("tape is NULL");
+    hipStream_t st = (hipStream_t)stream;
+    if (desc->dtype == SWARP_F32)
+        return rollout_fwd<float>(desc, T, state0, actions, traj, final_state, tape, tape_bytes, st);
+    return rollout_fwd<double>(desc, T, state0, actions, traj, final_state, tape, tape_bytes, st);
 }
 
 int swarp_rollout_bwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
@@ -872,9 +954,27 @@ int swarp_rollout_bwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
         return rollout_bwd<float>(desc, T, state0, actions, traj, adj_traj, adj_final, adj_state0,
-                                  adj_actions, st);
+                                  adj_actions, nullptr, 0, st);
     return rollout_bwd<double>(desc, T, state0, actions, traj, adj_traj, adj_final, adj_state0,
-                               adj_actions, st);
+                               adj_actions, nullptr, 0, st);
+}
+
+int swarp_rollout_bwd_tape(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                           const void *actions, const swarp_state_t *traj,
+                           const swarp_state_t *adj_traj, const swarp_state_t *adj_final,
+                           const swarp_state_t *adj_state0, void *adj_actions,
+                           const void *tape, uint64_t tape_bytes, void *stream)
+{
+    g_err[0] = 0;
+    if (check_desc(desc)) return -1;
+    if (T < 1) return fail("T must be >= 1");
+    if (!tape && tape_bytes) return fail("tape is NULL");
+    hipStream_t st = (hipStream_t)stream;
+    if (desc->dtype == SWARP_F32)
+        return rollout_bwd<float>(desc, T, state0, actions, traj, adj_traj, adj_final, adj_state0,
+                                  adj_actions, tape, tape_bytes, st);
+    return rollout_bwd<double>(desc, T, state0, actions, traj, adj_traj, adj_final, adj_state0,
+                               adj_actions, tape, tape_bytes, st);
 }
 
 int swarp_neighbors(const swarp_desc_t *desc, const void *pos, int32_t *idx, int32_t *cnt,

@@ -113,6 +113,10 @@ class Stepper:
         #: route eligible fleets to the specialised kernels (set False to force the
         #: generic ones; both give bit-identical results)
         self.use_specialised = True
+        #: grad rollouts on the specialised kernels keep a tape of the substep
+        #: intermediates so that the backward does not recompute them (set False to
+        #: recompute; both give bit-identical results)
+        self.use_tape = True
 
         self.collisions = world.collisions
         self.max_agent_radius = max(c.radius for c in configs)
@@ -246,6 +250,15 @@ class Stepper:
         return d
 
     # --------------------------------------------------------------- neighbours
+
+    def tape_bytes(self, n_envs: int, act_dim: int, T: int) -> int:
+        """Size of the rollout tape of a T-step grad rollout (0: no tape is kept)."""
+        if not self.use_tape:
+            return 0
+        d = self.desc(n_envs, act_dim)
+        n = ctypes.c_uint64(0)
+        _lib.check(_lib.load().swarp_tape_bytes(ctypes.byref(d), T, ctypes.byref(n)))
+        return int(n.value)
 
     def grid(self, n_envs: int) -> NeighborGrid:
         g = self._grids.get(n_envs)

@@ -170,9 +170,8 @@ def test_specialised_matches_generic_kernels():
 
 
 def test_partial_last_wave():
-    """n_envs that leave the last wave partly empty: the specialised kernels hold two envs
-    per lane (2 * 64 / PA envs per wave), so an env count that is not a multiple of that
-    leaves slot-1 envs, or whole rows, past n_envs."""
+    """n_envs that leave the last wave partly empty: a wave holds 64 / PA envs, so an env
+    count that is not a multiple of that leaves env slots of the last wave past n_envs."""
     for A, E in ((4, 45), (16, 37), (16, 3), (64, 3)):
         T, S = 5, 2
         rng = np.random.default_rng(100 + A + E)

@@ -1,0 +1,103 @@
+"""Rollout tape on the GPU: the backward that reads the substep intermediates from the
+forward's tape against the backward that recomputes them.
+
+Bar: BIT-IDENTICAL.  The reverse pass runs the same arithmetic in the same order on the
+same values either way (positions of substeps 1..S-1 are re-derived with the forward's own
+update), so forward states and both gradients must be equal bit for bit.  The tape path is
+also the default one, so every specialised-kernel parity test against the oracle runs
+through it.
+"""
+
+import dataclasses
+
+import numpy as np
+import pytest
+import torch
+
+from cases import nav_agents, nav_world
+from hip_helpers import hip_run, make_stepper
+from oracle.oracle import pack_state
+from swarp_amd.config import WorldConfig
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(E, A, T, extent, seed, dtype=np.float32):
+    rng = np.random.default_rng(seed)
+    s0 = pack_state({"pos": rng.uniform(-extent, extent, size=(E, A, 2)),
+                     "vel": rng.uniform(-0.3, 0.3, size=(E, A, 2))}).astype(dtype)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(dtype)
+    w = rng.normal(size=(T, E, A, 16))
+    w[..., 7:] = 0.0
+    return s0, acts, w
+
+
+def _pair(cfgs, world, S, dtype=torch.float32):
+    on = make_stepper(cfgs, world, 0.05, S, dtype)
+    off = make_stepper(cfgs, world, 0.05, S, dtype)
+    off.use_tape = False
+    return on, off
+
+
+CASES = [
+    # (E, A, T, S, extent, world kwargs) -- contacts + soft walls unless stated
+    (400, 16, 12, 4, 0.6, dict(world_size=0.7)),          # config-2 shape, dense
+    (37, 16, 6, 3, 0.5, dict(world_size=0.55)),           # partial last wave, S = 3
+    (45, 4, 5, 1, 0.4, dict(world_size=0.45)),            # S = 1: no velocity entries
+    (20, 12, 7, 2, 0.15, dict(world_size=0.3, max_neighbors=3)),  # truncated lists
+    (9, 32, 4, 4, 0.4, dict(world_size=0.45)),            # 8-byte mask words
+    (3, 64, 4, 2, 0.5, dict(world_size=0.55)),            # 16-byte mask words
+]
+
+
+@pytest.mark.parametrize("E,A,T,S,extent,kw", CASES)
+def test_tape_matches_recompute(E, A, T, S, extent, kw):
+    kw = dict(kw)
+    ws = kw.pop("world_size")
+    mk = kw.pop("max_neighbors", None)
+    world = nav_world(A, world_size=ws)
+    if mk is not None:
+        world = dataclasses.replace(world, max_neighbors=mk)
+    cfgs = nav_agents(A)
+    on, off = _pair(cfgs, world, S)
+    assert on.tape_bytes(E, 2, T) > 0 and off.tape_bytes(E, 2, T) == 0
+    s0, acts, w = _case(E, A, T, extent, seed=E + A + S)
+    a = hip_run(on, s0, acts, w, np.float32)
+    b = hip_run(off, s0, acts, w, np.float32)
+    assert np.array_equal(a[0][..., :7], b[0][..., :7]), "forward states differ"
+    assert np.array_equal(a[2], b[2]), "d/d actions differ"
+    assert np.array_equal(a[1][..., :7], b[1][..., :7]), "d/d state0 differ"
+
+
+def test_tape_walls_only_and_contacts_only():
+    E, A, T, S = 30, 8, 6, 4
+    s0, acts, w = _case(E, A, T, 0.5, seed=5)
+    walls = WorldConfig(collisions=False, bounds=(-0.5, 0.5, -0.5, 0.5), bounds_mode="soft")
+    contacts = WorldConfig(collisions=True, collision_margin=0.025, max_neighbors=8)
+    for world in (walls, contacts):
+        on, off = _pair(nav_agents(A), world, S)
+        assert on.tape_bytes(E, 2, T) > 0
+        a = hip_run(on, s0, acts, w, np.float32)
+        b = hip_run(off, s0, acts, w, np.float32)
+        for x, y in zip(a, b):
+            assert np.array_equal(x[..., :7], y[..., :7])
+
+
+def test_tape_float64():
+    E, A, T, S = 32, 8, 6, 4
+    s0, acts, w = _case(E, A, T, 0.3, seed=8, dtype=np.float64)
+    on, off = _pair(nav_agents(A), nav_world(A, world_size=0.35), S, torch.float64)
+    a = hip_run(on, s0, acts, w, np.float64)
+    b = hip_run(off, s0, acts, w, np.float64)
+    for x, y in zip(a, b):
+        assert np.array_equal(x[..., :7], y[..., :7])
+
+
+def test_no_tape_beyond_four_substeps():
+    """Five substeps keep no tape; the rollout recomputes and still runs."""
+    E, A, T, S = 10, 8, 3, 5
+    s0, acts, w = _case(E, A, T, 0.4, seed=3)
+    st = make_stepper(nav_agents(A), nav_world(A, world_size=0.45), 0.05, S, torch.float32)
+    assert st.tape_bytes(E, 2, T) == 0
+    states, g0, ga = hip_run(st, s0, acts, w, np.float32)
+    assert np.isfinite(ga).all() and np.isfinite(g0).all()

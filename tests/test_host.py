@@ -73,6 +73,48 @@ def test_library_rejects_bad_descriptor_without_gpu():
     assert rc != 0 and b"n_agents" in lib.swarp_last_error()
 
 
+def test_tape_size_without_gpu():
+    """Rollout tape size (a host computation): one record per step and lane of every
+    workgroup (64 / PA envs each, PA = agents padded to a power of two) -- 4 mask words
+    (4 B up to 16 agents, 8 B up to 32, 16 B up to 64), 3 velocity pairs, a 32-bit wall
+    word, padded to 16 B -- then the last step's velocities, each region 256-byte aligned.
+    No tape where the backward recomputes (generic kernels, more than 4 substeps, nothing
+    to record)."""
+    from cases import nav_agents, nav_world
+
+    def al(x):
+        return (x + 255) // 256 * 256
+
+    def stepper(A, S, dtype=torch.float32, **kw):
+        return Stepper(nav_agents(A), dt=0.05, substeps=S, device="cpu", dtype=dtype,
+                       world=nav_world(A, **kw))
+
+    E, T = 1000, 32
+    for A, PA, S, dtype, rec, pair in ((16, 16, 4, torch.float32, 48, 8),    # 16 + 24 + 4 -> 48
+                                       (8, 8, 1, torch.float32, 48, 8),
+                                       (20, 32, 4, torch.float64, 96, 16),   # 32 + 48 + 4 -> 96
+                                       (40, 64, 2, torch.float32, 96, 8),    # 64 + 24 + 4 -> 96
+                                       (64, 64, 3, torch.float64, 128, 16)):  # 64 + 48 + 4 -> 128
+        lanes = -(-E // (64 // PA)) * 64
+        assert stepper(A, S, dtype).tape_bytes(E, 2, T) == al(T * lanes * rec) + al(lanes * pair), (A, S)
+    # contacts without walls keep the same records; 10 envs of 8 agents fill 2 workgroups
+    st = Stepper(nav_agents(8), dt=0.05, substeps=2, device="cpu", dtype=torch.float32,
+                 world=WorldConfig(collisions=True, collision_margin=0.025))
+    assert st.tape_bytes(10, 2, 3) == al(3 * 128 * 48) + al(128 * 8)
+    assert stepper(16, 5).tape_bytes(E, 2, T) == 0
+    st = stepper(16, 4)
+    st.use_tape = False
+    assert st.tape_bytes(E, 2, T) == 0
+    dd = Stepper(nav_agents(4, model=DynamicsModel.DIFF_DRIVE), dt=0.05, device="cpu",
+                 world=nav_world(4))
+    assert dd.tape_bytes(E, 2, T) == 0
+    free = Stepper(nav_agents(4), dt=0.05, device="cpu", world=WorldConfig(collisions=False))
+    assert free.tape_bytes(E, 2, T) == 0
+    lib = _lib.load()
+    n = ctypes.c_uint64(7)
+    assert lib.swarp_tape_bytes(ctypes.byref(st.desc(E, 2)), 0, ctypes.byref(n)) != 0
+
+
 # ------------------------------------------------------------------ config surface
 
 def test_param_fields_layout():
