@@ -4,7 +4,8 @@ The step (neighbour search, soft contacts, integration of holonomic / diff-drive
 bicycle / quadrotor agents) and its adjoint run as hand-written HIP kernels in
 ``libswarp_hip.so`` behind a C ABI (``include/swarp_hip.h``); this package is the
 PyTorch-facing host side with the reference's API (``Stepper``, ``TorchState``,
-``warp_step``, ``rollout``, ``GradRing``, ``NeighborGrid`` and the config classes).
+``warp_step``, ``rollout``, ``GradRing``, ``NeighborGrid``, the config classes, and the
+``World`` / ``Environment`` / ``make("navigation", ...)`` surface that calls the step).
 """
 
 from .autograd import GradRing, StepGradSlot, TorchState, fill_state_defaults, rollout, warp_step
@@ -25,13 +26,17 @@ from .config import (
     action_dim,
     drone_config,
 )
+from .environment import Environment, make
 from .neighbors import NeighborGrid
+from .scenarios import SCENARIOS, NavigationScenario, Scenario, make_scenario
 from .stepper import AgentParams, Stepper, build_agent_params
+from .world import World
 
 __all__ = [
-    "AgentConfig", "AgentParams", "AgentShape", "ControlMode", "DynamicsModel", "GradRing",
-    "Integrator", "MODEL_ACTION_DIM", "NUM_PARAMS", "NeighborGrid", "ObstacleKind",
-    "ObstacleShape", "Obstacles", "PARAM_FIELDS", "StepGradSlot", "Stepper", "TorchState",
-    "WorldConfig", "action_bounds", "action_dim", "build_agent_params", "drone_config",
-    "fill_state_defaults", "rollout", "warp_step",
+    "AgentConfig", "AgentParams", "AgentShape", "ControlMode", "DynamicsModel", "Environment",
+    "GradRing", "Integrator", "MODEL_ACTION_DIM", "NUM_PARAMS", "NavigationScenario",
+    "NeighborGrid", "ObstacleKind", "ObstacleShape", "Obstacles", "PARAM_FIELDS", "SCENARIOS",
+    "Scenario", "StepGradSlot", "Stepper", "TorchState", "World", "WorldConfig",
+    "action_bounds", "action_dim", "build_agent_params", "drone_config", "fill_state_defaults",
+    "make", "make_scenario", "rollout", "warp_step",
 ]

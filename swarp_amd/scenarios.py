@@ -1,0 +1,376 @@
+"""Scenarios that build a ``World`` for ``Environment``: the ``Scenario`` interface
+(``swarp/scenarios/base.py:29-228``) and ``NavigationScenario``
+(``swarp/scenarios/navigation.py:38-839``), the step's caller in every benchmark of the
+reference.
+
+Observations and rewards are torch ops on the step's outputs -- the reference's own
+differentiable path (``_refresh_step_cache`` / ``observations`` / ``rewards``,
+``swarp/scenarios/navigation.py:671-839``); the reference's fused Warp obs/reward/reset
+kernels are a no-grad speed path of the scenario, not of the physics step, and are not
+rebuilt here.  Resets draw spawns and goals with the stratified separated sampler the
+reference keeps as its torch reference (``_sample_separated``, ``:222-272``) on the
+world's generator, so they are reproducible per seed but are not the reference's Warp
+RNG stream.
+"""
+
+from __future__ import annotations
+
+import math
+from abc import ABC, abstractmethod
+from typing import Any
+
+import torch
+
+from .config import AgentConfig, AgentShape, ControlMode, DynamicsModel, Obstacles, WorldConfig
+from .config import _coerce
+from .world import World
+
+
+class Scenario(ABC):
+    """A task on top of a World: ``make_world``, ``reset_world``, ``observations``,
+    ``rewards``, ``done``, ``info`` and the ``post_step`` hook."""
+
+    world: World
+
+    @property
+    @abstractmethod
+    def obs_dim(self) -> int:
+        """Per-agent observation width."""
+
+    @property
+    def state_dim(self) -> int:
+        return 0
+
+    @property
+    def n_roles(self) -> int:
+        return 1
+
+    @property
+    def role_counts(self) -> tuple[int, ...]:
+        return ()
+
+    @property
+    def aux_dim(self) -> int:
+        return 0
+
+    def critic_state(self) -> torch.Tensor | None:
+        return None
+
+    def agent_roles(self) -> torch.Tensor | None:
+        return None
+
+    def aux_targets(self) -> torch.Tensor | None:
+        return None
+
+    def comm_mask(self) -> torch.Tensor | None:
+        return None
+
+    @abstractmethod
+    def make_world(self, n_envs: int, device: str, dt: float, substeps: int,
+                   dtype: torch.dtype, world_config: WorldConfig | None = None) -> World:
+        """Build the World; the scenario's own WorldConfig ends with
+        ``.override_with(world_config)``."""
+
+    @abstractmethod
+    def reset_world(self, env_mask: torch.Tensor | None = None, *, obs_only: bool = False) -> None:
+        """(Re)randomise every env (``env_mask=None``) or the ``True`` envs of a bool
+        ``[n_envs]`` mask, without a host sync."""
+
+    @abstractmethod
+    def observations(self) -> torch.Tensor:
+        """``[n_envs, n_agents, obs_dim]``."""
+
+    def observation(self, agent_idx: int) -> torch.Tensor:
+        return self.observations()[:, agent_idx]
+
+    def agent_reward(self, agent_idx: int) -> torch.Tensor:
+        w = self.world
+        return torch.zeros(w.n_envs, device=w.device, dtype=w.dtype)
+
+    def global_reward(self) -> torch.Tensor:
+        w = self.world
+        return torch.zeros(w.n_envs, device=w.device, dtype=w.dtype)
+
+    def rewards(self) -> torch.Tensor:
+        per_agent = torch.stack([self.agent_reward(i) for i in range(self.world.n_agents)], 1)
+        return per_agent + self.global_reward().unsqueeze(1)
+
+    def done(self) -> torch.Tensor:
+        w = self.world
+        return torch.zeros(w.n_envs, device=w.device, dtype=torch.bool)
+
+    def info(self) -> dict[str, Any]:
+        return {}
+
+    def post_step(self) -> None:  # noqa: B027 (optional hook)
+        """Called right after the physics step, before observations and rewards."""
+
+
+class NavigationScenario(Scenario):
+    """Agents navigate to per-agent goals with soft collision avoidance
+    (``swarp/scenarios/navigation.py:1-11``).
+
+    Reward per agent: position shaping ``(prev_dist - dist) * pos_shaping_factor``
+    (summed over the env's agents when ``shared_reward``), ``collision_penalty`` per
+    touching listed neighbour, and ``final_reward`` to every agent of an env whose agents
+    are all within ``goal_tolerance`` of their goals (which also ends the episode).
+    Observation per agent (``9 + 5 * neighbor_obs``): pos, vel, cos/sin heading, angular
+    velocity, goal - pos, then the first ``neighbor_obs`` listed neighbours' relative
+    positions, relative velocities and validity flags.
+    """
+
+    def __init__(
+        self,
+        n_agents: int = 4,
+        agent_radius: float = 0.05,
+        model: DynamicsModel = DynamicsModel.HOLONOMIC,
+        ctrl_mode: ControlMode = ControlMode.VELOCITY,
+        max_speed: float = 1.0,
+        world_size: float = 1.0,
+        n_obstacles: int = 0,
+        obstacle_radius: float = 0.1,
+        neighbor_obs: int = 2,
+        neighbor_radius: float | None = None,
+        shared_reward: bool = False,
+        pos_shaping_factor: float = 1.0,
+        collision_penalty: float = -1.0,
+        final_reward: float = 5.0,
+        goal_tolerance: float | None = None,
+        min_spawn_separation: float | None = None,
+        neighbor_method: str = "auto",
+        agent_shape: AgentShape | str = AgentShape.DISC,
+        agent_half_extents: tuple[float, float] | None = None,
+    ) -> None:
+        shape = _coerce(AgentShape, agent_shape, "agent_shape")
+        if shape == AgentShape.BOX:
+            raise NotImplementedError("box agents are not part of this build's step")
+        footprint = AgentConfig(radius=agent_radius, half_extents=agent_half_extents or (0.0, 0.0))
+        self.agent_shape = footprint.shape
+        self.agent_half_extents = footprint.half_extents
+        self.n_agents = n_agents
+        self.agent_radius = footprint.radius
+        self.model = model
+        self.ctrl_mode = ctrl_mode
+        self.max_speed = max_speed
+        self.world_size = world_size
+        self.n_obstacles = n_obstacles
+        self.obstacle_radius = obstacle_radius
+        self.neighbor_obs = neighbor_obs
+        self.neighbor_radius = neighbor_radius
+        self.shared_reward = shared_reward
+        self.pos_shaping_factor = pos_shaping_factor
+        self.collision_penalty = collision_penalty
+        self.final_reward = final_reward
+        self.goal_tolerance = goal_tolerance if goal_tolerance is not None else self.agent_radius
+        self.min_spawn_separation = (min_spawn_separation if min_spawn_separation is not None
+                                     else 3.0 * self.agent_radius)
+        self.neighbor_method = neighbor_method
+        # provisional until make_world resolves max_neighbors (navigation.py:100-103)
+        self._k_obs = min(self.neighbor_obs, min(32, max(4, self.n_agents)))
+        self._cache: dict[str, torch.Tensor] | None = None
+        self._prev_dist: torch.Tensor | None = None
+
+    # ------------------------------------------------------------------ world
+
+    def _agent_configs(self) -> list[AgentConfig]:
+        return [
+            AgentConfig(model=self.model, ctrl_mode=self.ctrl_mode, radius=self.agent_radius,
+                        max_speed=self.max_speed, max_accel=2.0 * self.max_speed,
+                        shape=self.agent_shape, half_extents=self.agent_half_extents)
+            for _ in range(self.n_agents)
+        ]
+
+    def make_world(self, n_envs, device, dt, substeps, dtype, world_config=None) -> World:
+        """World constants of ``swarp/scenarios/navigation.py:127-141``: k = 100, c = 1,
+        margin = r / 2, soft walls at +-world_size, neighbour radius = max(user, 2r +
+        margin), K = min(32, max(4, n_agents))."""
+        margin = 0.5 * self.agent_radius
+        reach = 2.0 * self.agent_radius + margin
+        cfg = WorldConfig(
+            collisions=True,
+            collision_k=100.0,
+            collision_c=1.0,
+            collision_margin=margin,
+            bounds=(-self.world_size, self.world_size, -self.world_size, self.world_size),
+            bounds_mode="soft",
+            neighbor_radius=max(self.neighbor_radius or 0.0, reach),
+            max_neighbors=min(32, max(4, self.n_agents)),
+            neighbor_method=self.neighbor_method,
+        ).override_with(world_config)
+        self.world = World(self._agent_configs(), cfg, n_envs=n_envs, device=device, dt=dt,
+                           substeps=substeps, dtype=dtype)
+        self.world.goals = torch.zeros(n_envs, self.n_agents, 2, device=device, dtype=dtype)
+        self._k_obs = min(self.neighbor_obs, cfg.max_neighbors)
+        self._cache = None
+        self._prev_dist = None
+        if self.n_obstacles > 0:
+            tt = {"device": device, "dtype": dtype}
+            self.world.set_obstacles(Obstacles(
+                torch.zeros(n_envs, self.n_obstacles, 2, **tt),
+                torch.full((self.n_obstacles,), self.obstacle_radius, **tt),
+            ))
+        return self.world
+
+    @property
+    def obs_dim(self) -> int:
+        return 9 + 5 * self._k_obs
+
+    _SPAWN_CELL_OVERSAMPLE = 8
+
+    def _sample_separated(self, n_envs: int, n_points: int, min_dist: float) -> torch.Tensor:
+        """Points at least ``min_dist`` apart by construction: each env takes
+        ``n_points`` distinct cells of a g x g grid over the spawn square and jitters each
+        point inside its cell's centred sub-square of side ``cell - min_dist``; plain
+        uniform when no grid leaves jitter room (``navigation.py:222-272``)."""
+        w = self.world
+        lim = self.world_size - 2.0 * self.agent_radius
+        shape = (n_envs, n_points, 2)
+        if n_points == 1 or min_dist <= 0.0:
+            return w.sample_uniform(shape, -lim, lim)
+        side = 2.0 * lim
+        g = math.ceil(math.sqrt(n_points * self._SPAWN_CELL_OVERSAMPLE))
+        g = min(g, int(side // (2.0 * min_dist)))
+        g = max(g, math.ceil(math.sqrt(n_points)))
+        if side / g <= min_dist:
+            return w.sample_uniform(shape, -lim, lim)
+        s = side / g
+        jitter = s - min_dist
+        cell = w.sample_uniform((n_envs, g * g), 0.0, 1.0).argsort(dim=-1)[:, :n_points]
+        col = (cell % g).to(w.dtype)
+        row = torch.div(cell, g, rounding_mode="floor").to(w.dtype)
+        centers = torch.stack([col, row], dim=-1) * s + (0.5 * s - lim)
+        return centers + (w.sample_uniform(shape, 0.0, 1.0) - 0.5) * jitter
+
+    def reset_world(self, env_mask: torch.Tensor | None = None, *, obs_only: bool = False) -> None:
+        """Spawns, goals, headings U[-pi, pi] and zero velocities for the selected envs
+        (``navigation.py:439-473``); obstacles uniform inside the walls."""
+        w = self.world
+        n = w.n_envs
+        pos = self._sample_separated(n, self.n_agents, self.min_spawn_separation)
+        goals = self._sample_separated(n, self.n_agents, self.min_spawn_separation)
+        theta = w.sample_uniform((n, self.n_agents), -math.pi, math.pi)
+        w.write_state(env_mask, pos=pos, theta=theta, vel=0.0, speed=0.0, ang_vel=0.0)
+        if env_mask is None:
+            w.goals.copy_(goals)
+        else:
+            w.goals.copy_(torch.where(env_mask.view(-1, 1, 1), goals, w.goals))
+        if self.n_obstacles > 0:
+            lim = self.world_size - self.obstacle_radius
+            opos = w.sample_uniform((n, self.n_obstacles, 2), -lim, lim)
+            if env_mask is None:
+                w.obstacle_pos.copy_(opos)
+            else:
+                w.obstacle_pos.copy_(torch.where(env_mask.view(-1, 1, 1), opos, w.obstacle_pos))
+            w.set_obstacles(w.obstacles)
+        # a full reset rebases every env's shaping baseline
+        self._refresh(reset_mask=env_mask if env_mask is not None else
+                      torch.ones(n, dtype=torch.bool, device=w.device))
+
+    # ------------------------------------------------------------ obs / rewards
+
+    def post_step(self) -> None:
+        self._refresh()
+
+    def _refresh(self, reset_mask: torch.Tensor | None = None) -> None:
+        """Neighbour features, goal distances and reward terms of the current state
+        (``navigation.py:671-761``).  ``reset_mask`` marks envs just reset: their shaping
+        baseline restarts at the spawn distance and their shaping term is zero."""
+        w = self.world
+        pos, vel = w.state.pos, w.state.vel
+        idx, cnt = w.neighbors()
+        k_all = idx.shape[-1]
+        k = min(self.neighbor_obs, k_all)
+        idx_long = idx.long()
+        valid = torch.arange(k_all, device=w.device).view(1, 1, -1) < cnt.long().unsqueeze(-1)
+        flat = idx_long.reshape(w.n_envs, -1)
+        npos = torch.gather(pos, 1, flat.unsqueeze(-1).expand(-1, -1, 2))
+        npos = npos.view(w.n_envs, w.n_agents, k_all, 2)
+        rel_pos_all = npos - pos.unsqueeze(2)
+        # touching listed pairs (|d| < r_i + r_j) per agent: a count, not differentiated
+        ndist = rel_pos_all.norm(dim=-1)
+        r = w.agent_radius
+        touching = ((ndist < r.view(1, -1, 1) + r[idx_long]) & valid).sum(dim=-1).to(w.dtype)
+        rel_pos = rel_pos_all[:, :, :k] * valid[:, :, :k].unsqueeze(-1)
+        flat_k = idx_long[:, :, :k].reshape(w.n_envs, -1)
+        nvel = torch.gather(vel, 1, flat_k.unsqueeze(-1).expand(-1, -1, 2))
+        nvel = nvel.view(w.n_envs, w.n_agents, k, 2)
+        rel_vel = (nvel - vel.unsqueeze(2)) * valid[:, :, :k].unsqueeze(-1)
+        dist = (pos - w.goals).norm(dim=-1)
+        if self._prev_dist is None:
+            self._prev_dist = dist.detach().clone()
+        shaping = (self._prev_dist - dist) * self.pos_shaping_factor
+        if reset_mask is None:
+            self._prev_dist = dist.detach().clone()
+        else:
+            m = reset_mask.unsqueeze(-1)
+            shaping = torch.where(m, torch.zeros_like(shaping), shaping)
+            self._prev_dist = torch.where(m, dist.detach(), self._prev_dist)
+        self._cache = {
+            "rel_pos": rel_pos,
+            "rel_vel": rel_vel,
+            "valid": valid,
+            "touching": touching,
+            "dist_to_goal": dist,
+            "on_goal": dist < self.goal_tolerance,
+            "pos_shaping": shaping,
+            "neighbor_overflow": w.neighbor_overflow(),
+        }
+
+    def observations(self) -> torch.Tensor:
+        w = self.world
+        s = w.state
+        c = self._cache
+        feats = [s.pos, s.vel, torch.cos(s.theta).unsqueeze(-1), torch.sin(s.theta).unsqueeze(-1),
+                 s.ang_vel.unsqueeze(-1), w.goals - s.pos]
+        k = min(self.neighbor_obs, c["rel_pos"].shape[2])
+        if k > 0:
+            e, a = w.n_envs, w.n_agents
+            feats += [c["rel_pos"][:, :, :k].reshape(e, a, -1),
+                      c["rel_vel"][:, :, :k].reshape(e, a, -1),
+                      c["valid"][:, :, :k].to(w.dtype)]
+        return torch.cat(feats, dim=-1)
+
+    def rewards(self) -> torch.Tensor:
+        c = self._cache
+        rew = self.collision_penalty * c["touching"]
+        if self.shared_reward:
+            rew = rew + c["pos_shaping"].sum(dim=-1, keepdim=True)
+        else:
+            rew = rew + c["pos_shaping"]
+        final = self.final_reward * c["on_goal"].all(dim=-1).to(self.world.dtype)
+        return rew + final.unsqueeze(-1)
+
+    def agent_reward(self, agent_idx: int) -> torch.Tensor:
+        c = self._cache
+        rew = self.collision_penalty * c["touching"][:, agent_idx]
+        if not self.shared_reward:
+            rew = rew + c["pos_shaping"][:, agent_idx]
+        return rew
+
+    def global_reward(self) -> torch.Tensor:
+        c = self._cache
+        rew = self.final_reward * c["on_goal"].all(dim=-1).to(self.world.dtype)
+        if self.shared_reward:
+            rew = rew + c["pos_shaping"].sum(dim=-1)
+        return rew
+
+    def done(self) -> torch.Tensor:
+        return self._cache["on_goal"].all(dim=-1)
+
+    def info(self) -> dict[str, Any]:
+        c = self._cache
+        return {"dist_to_goal": c["dist_to_goal"], "on_goal": c["on_goal"],
+                "collisions": c["touching"], "neighbor_overflow": c["neighbor_overflow"]}
+
+
+#: Registered scenarios of this build (``swarp/scenarios/__init__.py`` registers twelve;
+#: the physics step's caller in every benchmark is navigation).
+SCENARIOS: dict[str, type[Scenario]] = {"navigation": NavigationScenario}
+
+
+def make_scenario(name: str, **kwargs) -> Scenario:
+    try:
+        cls = SCENARIOS[name]
+    except KeyError:
+        raise ValueError(f"unknown scenario {name!r}; valid names: {sorted(SCENARIOS)}") from None
+    return cls(**kwargs)
