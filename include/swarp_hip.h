@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 2
+#define SWARP_ABI_VERSION 3
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -54,6 +54,13 @@ typedef struct swarp_desc {
        half_extents [N,2], vel [E,N,2], ang_vel [E,N], type [N] int32 */
     const void *obs_pos, *obs_radius, *obs_angle, *obs_half, *obs_vel, *obs_ang_vel;
     const int32_t *obs_type;
+    /* movable compound bodies (read by the _ob entry points only; Obstacles' body fields,
+       swarp/core/config.py:70-78): kind [N] int32 (1 = MOVABLE), body [N] int32 (root
+       index of each shape's body), mass [N], inertia [N], body_offset [N,2]; the linear /
+       angular damping of WorldConfig (obstacle_linear_damping, obstacle_angular_damping) */
+    const int32_t *obs_kind, *obs_body;
+    const void *obs_mass, *obs_inertia, *obs_body_off;
+    double lin_damping, ang_damping;
 } swarp_desc_t;
 
 /* The nine state fields.  A NULL field means "not provided": an input adjoint that
@@ -120,6 +127,32 @@ int swarp_rollout_bwd_tape(const swarp_desc_t *desc, int32_t T, const swarp_stat
                            const swarp_state_t *adj_traj, const swarp_state_t *adj_final,
                            const swarp_state_t *adj_state0, void *adj_actions,
                            const void *tape, uint64_t tape_bytes, void *stream);
+
+/* Rollout of a world whose obstacle state evolves: movable compound bodies integrated
+ * from the agents' contact reactions inside every substep (the body pass of
+ * obstacle_dynamics_kernel, swarp/core/bodies.py:367-568, disc variant: the shapes of a
+ * movable body are circles; the reference runs it on untaped steps,
+ * swarp/core/stepper.py:952-991).  Replaces T calls of Stepper.launch_substeps with the
+ * body pass enabled.  Fleets of 2-D models, 1 <= n_obstacles <= 16.
+ * ob0 [E, 12N]: per env and obstacle index o, the shape state (pos x, pos y, angle,
+ * vel x, vel y, ang_vel) at [6o..6o+5] and the state of the body rooted at o at
+ * [6N+6o..6N+6o+5] (the reference's obs_* and body_* arrays, stepper.py:418-431).
+ * ob_traj [T, E, 12N] receives the obstacle state after each step.  Other arguments as
+ * swarp_rollout_fwd. */
+int swarp_rollout_fwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                         const void *ob0, const void *actions, const swarp_state_t *traj,
+                         const swarp_state_t *final_state, void *ob_traj, void *stream);
+
+/* Reverse of swarp_rollout_fwd_ob (this build's own adjoint of the body pass; the
+ * reference has none).  adj_ob_traj [T, E, 12N] (nullable) is the adjoint arriving at each
+ * step's obstacle output; adj_ob0 [E, 12N] (nullable) receives the adjoint of ob0.  Other
+ * arguments as swarp_rollout_bwd. */
+int swarp_rollout_bwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                         const void *ob0, const void *actions, const swarp_state_t *traj,
+                         const void *ob_traj, const swarp_state_t *adj_traj,
+                         const swarp_state_t *adj_final, const void *adj_ob_traj,
+                         const swarp_state_t *adj_state0, void *adj_ob0, void *adj_actions,
+                         void *stream);
 
 /* Padded radius-neighbour lists of one state: replaces NeighborGrid.query_into's
  * brute-force kernel (swarp/core/neighbors.py:76-97, 465-492).  pos [E,A,2] of

@@ -11,7 +11,7 @@ import ctypes
 import os
 from pathlib import Path
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 F32, F64 = 0, 1
 
 _PKG = Path(__file__).resolve().parent
@@ -53,6 +53,13 @@ class SwarpDesc(ctypes.Structure):
         ("obs_vel", ctypes.c_void_p),
         ("obs_ang_vel", ctypes.c_void_p),
         ("obs_type", ctypes.c_void_p),
+        ("obs_kind", ctypes.c_void_p),
+        ("obs_body", ctypes.c_void_p),
+        ("obs_mass", ctypes.c_void_p),
+        ("obs_inertia", ctypes.c_void_p),
+        ("obs_body_off", ctypes.c_void_p),
+        ("lin_damping", ctypes.c_double),
+        ("ang_damping", ctypes.c_double),
     ]
 
 
@@ -95,6 +102,19 @@ SIGNATURES = {
          ctypes.POINTER(SwarpState), ctypes.POINTER(SwarpState), ctypes.POINTER(SwarpState),
          ctypes.POINTER(SwarpState), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64,
          ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "swarp_rollout_fwd_ob": (
+        [ctypes.POINTER(SwarpDesc), ctypes.c_int32, ctypes.POINTER(SwarpState), ctypes.c_void_p,
+         ctypes.c_void_p, ctypes.POINTER(SwarpState), ctypes.POINTER(SwarpState), ctypes.c_void_p,
+         ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "swarp_rollout_bwd_ob": (
+        [ctypes.POINTER(SwarpDesc), ctypes.c_int32, ctypes.POINTER(SwarpState), ctypes.c_void_p,
+         ctypes.c_void_p, ctypes.POINTER(SwarpState), ctypes.c_void_p, ctypes.POINTER(SwarpState),
+         ctypes.POINTER(SwarpState), ctypes.c_void_p, ctypes.POINTER(SwarpState), ctypes.c_void_p,
+         ctypes.c_void_p, ctypes.c_void_p],
         ctypes.c_int,
     ),
     "swarp_neighbors": (

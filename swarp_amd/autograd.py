@@ -228,6 +228,118 @@ class _RolloutFn(torch.autograd.Function):
         return (None, None, adj_act if need[2] else None, *adj0)
 
 
+def _launch_fwd_ob(stepper: Stepper, state0, ob0: torch.Tensor, actions_seq: torch.Tensor,
+                   traj, final, ob_traj: torch.Tensor) -> None:
+    """One forward launch of a world with movable bodies (2-D fleet, five fields)."""
+    T, E, _, ad = actions_seq.shape
+    lib = _lib.load()
+    desc = stepper.desc(E, ad)
+    s0 = state_struct(list(state0)[:5])
+    fin = state_struct(list(final)[:5])
+    tr = state_struct(list(traj)[:5]) if traj is not None and T > 1 else None
+    _lib.check(lib.swarp_rollout_fwd_ob(
+        ctypes.byref(desc), T, ctypes.byref(s0), ob0.data_ptr(), actions_seq.data_ptr(),
+        ctypes.byref(tr) if tr is not None else None, ctypes.byref(fin), ob_traj.data_ptr(),
+        _stream(actions_seq),
+    ))
+
+
+class _RolloutObFn(torch.autograd.Function):
+    """T steps of a world with movable bodies as one autograd node: inputs (actions,
+    obstacle state, five state fields); outputs the final state fields, the stacked
+    trajectory fields of steps 0..T-2, and the obstacle states after every step
+    ``[T, n_envs, 12 N]``."""
+
+    @staticmethod
+    def forward(ctx, stepper: Stepper, actions_seq: torch.Tensor, ob0: torch.Tensor,
+                *state0: torch.Tensor):
+        ctx.set_materialize_grads(False)
+        T, E = actions_seq.shape[0], actions_seq.shape[1]
+        dev = actions_seq.device
+        actions_seq = actions_seq.contiguous()
+        ob0 = ob0.contiguous()
+        state0 = tuple(t.contiguous() for t in state0)
+        final = _empty_like_fields(stepper, (), E, dev)
+        traj = _empty_like_fields(stepper, (max(T - 1, 0),), E, dev)
+        ob_traj = torch.empty((T,) + tuple(ob0.shape), device=dev, dtype=ob0.dtype)
+        sink = KERNEL_EVENTS
+        if sink is not None:
+            e0 = _event(actions_seq)
+        _launch_fwd_ob(stepper, state0, ob0, actions_seq, traj, final, ob_traj)
+        if sink is not None:
+            sink.append(("fwd", e0, _event(actions_seq)))
+        ctx.stepper = stepper
+        ctx.T = T
+        ctx.save_for_backward(actions_seq, ob0, ob_traj, *state0, *traj)
+        return (*final, *traj, ob_traj)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        stepper: Stepper = ctx.stepper
+        T = ctx.T
+        saved = ctx.saved_tensors
+        actions_seq, ob0, ob_traj = saved[0], saved[1], saved[2]
+        state0 = saved[3:8]
+        traj = saved[8:13]
+        g_final = [None if g is None else g.contiguous() for g in grads[:5]]
+        g_traj = [None if g is None else g.contiguous() for g in grads[5:10]]
+        g_ob = grads[10].contiguous() if grads[10] is not None else None
+        need = ctx.needs_input_grad
+        adj_act = torch.empty_like(actions_seq)
+        adj_ob0 = torch.empty_like(ob0) if need[2] else None
+        adj0 = [torch.empty_like(s) if need[3 + k] else None for k, s in enumerate(state0)]
+        E, ad = actions_seq.shape[1], actions_seq.shape[3]
+        lib = _lib.load()
+        desc = stepper.desc(E, ad)
+        s0 = state_struct(state0)
+        tr = state_struct(traj) if T > 1 else None
+        gtr = state_struct(g_traj) if T > 1 and any(g is not None for g in g_traj) else None
+        gfin = state_struct(g_final) if any(g is not None for g in g_final) else None
+        a0 = state_struct(adj0)
+        sink = KERNEL_EVENTS
+        if sink is not None:
+            e0 = _event(actions_seq)
+        _lib.check(lib.swarp_rollout_bwd_ob(
+            ctypes.byref(desc), T, ctypes.byref(s0), ob0.data_ptr(), actions_seq.data_ptr(),
+            ctypes.byref(tr) if tr is not None else None, ob_traj.data_ptr(),
+            ctypes.byref(gtr) if gtr is not None else None,
+            ctypes.byref(gfin) if gfin is not None else None,
+            g_ob.data_ptr() if g_ob is not None else None, ctypes.byref(a0),
+            adj_ob0.data_ptr() if adj_ob0 is not None else None, adj_act.data_ptr(),
+            _stream(actions_seq),
+        ))
+        if sink is not None:
+            sink.append(("bwd", e0, _event(actions_seq)))
+        return (None, adj_act if need[1] else None, adj_ob0, *adj0)
+
+
+def _rollout_bodies(stepper: Stepper, state: TorchState, actions_seq: torch.Tensor):
+    """rollout / warp_step of a world with movable bodies: consumes ``stepper.ob_state``,
+    leaves the obstacle state after the last step in it and every step's in
+    ``stepper.ob_trajectory``."""
+    T, E, _ = _validate(stepper, state, actions_seq)
+    ob0 = stepper.ob_state
+    if ob0 is None or tuple(ob0.shape) != (E, 12 * stepper.n_obstacles):
+        raise ValueError(f"stepper.ob_state must be [{E}, {12 * stepper.n_obstacles}]")
+    grad = torch.is_grad_enabled() and (
+        ob0.requires_grad or actions_seq.requires_grad
+        or any(t is not None and t.requires_grad for t in state))
+    if grad:
+        outs = _RolloutObFn.apply(stepper, actions_seq, ob0, *state[:5])
+        ob_traj = outs[10]
+        outs = outs[:10]
+    else:
+        final = _empty_like_fields(stepper, (), E, actions_seq.device)
+        traj = _empty_like_fields(stepper, (T - 1,), E, actions_seq.device)
+        ob_traj = torch.empty((T,) + tuple(ob0.shape), device=ob0.device, dtype=ob0.dtype)
+        _launch_fwd_ob(stepper, [t.contiguous() for t in state[:5]], ob0.contiguous(),
+                       actions_seq.contiguous(), traj, final, ob_traj)
+        outs = (*final, *traj)
+    stepper.ob_trajectory = ob_traj
+    stepper.ob_state = ob_traj[T - 1]
+    return _assemble(stepper, state, outs, T)
+
+
 def _grad_mode(state: TorchState, actions: torch.Tensor) -> bool:
     return torch.is_grad_enabled() and (
         actions.requires_grad or any(t is not None and t.requires_grad for t in state)
@@ -313,6 +425,9 @@ def warp_step(
     if actions.dim() != 3:
         raise ValueError(f"actions must be [n_envs, n_agents, act_dim]; got {tuple(actions.shape)}")
     seq = actions.unsqueeze(0)
+    if stepper.any_movable:
+        final, _ = _rollout_bodies(stepper, state, seq)
+        return final
     _validate(stepper, state, seq)
     nf = _nfields(stepper)
     if _grad_mode(state, actions):
@@ -342,6 +457,8 @@ def rollout(
     ``state`` and ``actions_seq``.
     """
     state = fill_state_defaults(state)
+    if stepper.any_movable:
+        return _rollout_bodies(stepper, state, actions_seq)
     T, E, _ = _validate(stepper, state, actions_seq)
     if T < 1:
         raise ValueError("actions_seq must hold at least one step")

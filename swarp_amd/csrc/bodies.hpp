@@ -1,0 +1,785 @@
+// bodies.hpp -- rollout kernels for worlds with movable compound bodies: the body pass of
+// obstacle_dynamics_kernel (swarp/core/bodies.py:367-568, disc variant: every shape of a
+// movable body is a circle) inside the fused substep chain, and this build's own adjoint
+// of it (the reference never tapes the body pass, swarp/core/stepper.py:952).
+// Included by swarp_hip.hip after the generic kernels; uses their lane/state helpers.
+//
+// Per-env obstacle state, 12 scalars per obstacle index o (the reference's obs_* and
+// body_* arrays, swarp/core/stepper.py:418-431):
+//   [6o .. 6o+5]          shape o:       pos x, pos y, angle, vel x, vel y, ang_vel
+//   [6N+6o .. 6N+6o+5]    body rooted at o: pos x, pos y, angle, vel x, vel y, ang_vel
+// It lives in LDS for the substeps of a step (double-buffered: substep input / output)
+// and goes to HBM once per step as the step's obstacle output, which is also the
+// backward's checkpoint.  Static scenery keeps its installed state.
+//
+// Substep order (swarp/core/stepper.py:908-991): lists on the input positions, agent
+// forces against the input obstacle state, the body pass (every movable body integrated
+// from the reactions of the input agent state), then the agents' integration.
+//
+// Sums over agents (a body's contact force and torque, the adjoints of a body's pose)
+// are formed in agent order by one loop over the contributing lanes of the env, which
+// keeps them in the reference's summation order; a contribution that is exactly zero is
+// skipped, which does not change a sum that starts at +0.
+#pragma once
+
+namespace swarp {
+
+constexpr int OB_W = 12;       // scalars per obstacle index in the per-env state
+constexpr int NOB_MAX = 16;    // obstacles per env on this path
+
+// Static obstacle tables of the body path.
+template <typename T> struct ObTab {
+    const T *rad, *half, *mass, *inertia, *off;  // [N], [N,2], [N], [N], [N,2]
+    const int32_t *type, *kind, *body;            // [N]
+    T lin_damp, ang_damp;
+    int N;
+};
+
+// Obstacle-state inputs / outputs of a rollout.
+template <typename T> struct ObIO {
+    const T *ob0;       // [E, 12N] state entering the rollout
+    T *traj;            // [T, E, 12N] state after each step
+    const T *atraj;     // [T, E, 12N] adjoint arriving at each step's output (nullable)
+    T *a0;              // [E, 12N] adjoint of ob0 (nullable)
+};
+
+// sin and cos of a body angle, the same on host and device: Cody-Waite reduction by
+// pi/2 (pi/2 split into a 33-bit head, so k * head is exact for |k| < 2^20, and a tail)
+// and the Taylor series of sin and cos on |r| <= pi/4 up to r^17 / r^18, in double
+// precision, rounded to T.
+template <typename T> __device__ __forceinline__ void psincos(T xr, T &so, T &co)
+{
+    const double x = (double)xr;
+    const double k = __builtin_rint(x * 0x1.45f306dc9c883p-1);
+    const double r = (x - k * 0x1.921fb544p+0) - k * 0x1.0b4611a626331p-34;
+    const double z = r * r;
+    double ps = 0x1.952c77030ad4ap-49;
+    ps = ps * z - 0x1.ae7f3e733b81fp-41;
+    ps = ps * z + 0x1.6124613a86d09p-33;
+    ps = ps * z - 0x1.ae64567f544e4p-26;
+    ps = ps * z + 0x1.71de3a556c734p-19;
+    ps = ps * z - 0x1.a01a01a01a01ap-13;
+    ps = ps * z + 0x1.1111111111111p-7;
+    ps = ps * z - 0x1.5555555555555p-3;
+    const double sn = r + r * (z * ps);
+    double pc = -0x1.6827863b97d97p-53;
+    pc = pc * z + 0x1.ae7f3e733b81fp-45;
+    pc = pc * z - 0x1.93974a8c07c9dp-37;
+    pc = pc * z + 0x1.1eed8eff8d898p-29;
+    pc = pc * z - 0x1.27e4fb7789f5cp-22;
+    pc = pc * z + 0x1.a01a01a01a01ap-16;
+    pc = pc * z - 0x1.6c16c16c16c17p-10;
+    pc = pc * z + 0x1.5555555555555p-5;
+    const double cn = (1.0 - z * 0.5) + (z * z) * pc;
+    const long long q = (long long)k & 3;
+    const double s_ = q == 0 ? sn : (q == 1 ? cn : (q == 2 ? -sn : -cn));
+    const double c_ = q == 0 ? cn : (q == 1 ? -sn : (q == 2 ? -cn : sn));
+    so = (T)s_;
+    co = (T)c_;
+}
+
+// bounds_apart (swarp/core/collisions.py:73-84)
+template <typename T> __device__ __forceinline__ bool b_apart(T dx, T dy, T reach)
+{
+    const T lim = reach * T(1.0001) + T(1.0e-6);
+    return dx * dx + dy * dy > lim * lim;
+}
+
+// Whether shape s belongs to a movable body (the body pass re-installs it).
+template <typename T> __device__ __forceinline__ bool shape_moves(const ObTab<T> &tb, int s)
+{
+    const int r = tb.body[s];
+    return tb.body[r] == r && tb.kind[r] == 1;
+}
+
+// One obstacle's force on an agent, the obstacle's pose read from the env's state `od`
+// (_obstacle_forces body, swarp/core/collisions.py:690-743).
+template <typename T>
+__device__ __forceinline__ void ob_force(const Cst<T> &C, const ObTab<T> &tb, const T *od, int o,
+                                         T px, T py, T vx, T vy, T ra, T dd, T &fx, T &fy)
+{
+    fx = T(0);
+    fy = T(0);
+    const T *sh = od + 6 * o;
+    const T cx = sh[0], cy = sh[1];
+    const int st = tb.type[o];
+    const T ro = tb.rad[o], hx = tb.half[2 * o], hy = tb.half[2 * o + 1];
+    const T bound = st == 1 ? m_sqrt(hx * hx + hy * hy) : (st == 2 ? hx + ro : ro);
+    if (b_apart(px - cx, py - cy, ra + C.margin + bound)) return;
+    const T vox = sh[3], voy = sh[4], om = sh[5], ang = sh[2];
+    if (st == 1) {
+        box_force(C, px, py, vx, vy, cx, cy, ang, hx, hy, ra + C.margin, dd, vox, voy, om, fx,
+                  fy);
+    } else if (st == 2) {
+        T ux = m_cos(ang), uy = m_sin(ang);
+        T t = wclamp((px - cx) * ux + (py - cy) * uy, -hx, hx);
+        T qx = cx + t * ux, qy = cy + t * uy;
+        T rx = qx - cx, ry = qy - cy;
+        pair_force(C, px - qx, py - qy, vx - (vox + -om * ry), vy - (voy + om * rx),
+                   ra + ro + C.margin, dd, fx, fy);
+    } else {
+        pair_force(C, px - cx, py - cy, vx - vox, vy - voy, ra + ro + C.margin, dd, fx, fy);
+    }
+}
+
+// Reverse of ob_force: the agent's adjoint into `a`; for a circle the adjoint of the
+// obstacle's position and velocity is returned in (opx, opy, ovx, ovy) (zero otherwise).
+template <typename T>
+__device__ __forceinline__ void ob_force_adj(const Cst<T> &C, const ObTab<T> &tb, const T *od,
+                                             int o, T px, T py, T vx, T vy, T ra, T dd, T gx,
+                                             T gy, St<T> &a, T &opx, T &opy, T &ovx, T &ovy)
+{
+    opx = opy = ovx = ovy = T(0);
+    const T *sh = od + 6 * o;
+    const T cx = sh[0], cy = sh[1];
+    const int st = tb.type[o];
+    const T ro = tb.rad[o], hx = tb.half[2 * o], hy = tb.half[2 * o + 1];
+    const T bound = st == 1 ? m_sqrt(hx * hx + hy * hy) : (st == 2 ? hx + ro : ro);
+    if (b_apart(px - cx, py - cy, ra + C.margin + bound)) return;
+    const T vox = sh[3], voy = sh[4], om = sh[5], ang = sh[2];
+    if (st == 1) {
+        box_force_adj(C, px, py, vx, vy, cx, cy, ang, hx, hy, ra + C.margin, dd, vox, voy, om,
+                      gx, gy, a);
+    } else if (st == 2) {
+        T ux = m_cos(ang), uy = m_sin(ang);
+        T tr = (px - cx) * ux + (py - cy) * uy;
+        T t = wclamp(tr, -hx, hx);
+        T qx = cx + t * ux, qy = cy + t * uy;
+        T rx = qx - cx, ry = qy - cy;
+        T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
+        pair_force_adj(C, px - qx, py - qy, vx - (vox + -om * ry), vy - (voy + om * rx),
+                       ra + ro + C.margin, dd, gx, gy, adx, ady, arx, ary);
+        a.px += adx;
+        a.py += ady;
+        a.vx += arx;
+        a.vy += ary;
+        T aqx = -adx - om * ary;
+        T aqy = -ady + om * arx;
+        T atr = wclamp_g(tr, -hx, hx, aqx * ux + aqy * uy);
+        a.px += atr * ux;
+        a.py += atr * uy;
+    } else {
+        T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
+        pair_force_adj(C, px - cx, py - cy, vx - vox, vy - voy, ra + ro + C.margin, dd, gx, gy,
+                       adx, ady, arx, ary);
+        a.px += adx;
+        a.py += ady;
+        a.vx += arx;
+        a.vy += ary;
+        opx = -adx;
+        opy = -ady;
+        ovx = -arx;
+        ovy = -ary;
+    }
+}
+
+// Agent forces of one substep on the body path: listed pairs (as the generic kernels),
+// obstacles from the env's state, walls.
+template <typename T, int PA>
+__device__ __forceinline__ typename MaskT<PA>::type forces_b(
+    const Cst<T> &C, const ObTab<T> &tb, const Lane<T, PA> &L, const T *sl, const T *lr,
+    const T *od, const St<T> &st, int s, bool full, typename MaskT<PA>::type &cand, T &Fx, T &Fy)
+{
+    typedef typename MaskT<PA>::type M;
+    const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64, *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
+    M incl = 0;
+    T fx = T(0), fy = T(0);
+    if (C.collisions) {
+        if (full) {
+            M cd;
+            incl = scan_all<T, PA>(lx, ly, L.base, C.A, L.agent, st.px, st.py, C.t_nbr, C.t_skin, cd);
+            if (s == 0) cand = cd;
+        } else {
+            incl = scan_cand<T, PA>(lx, ly, L.base, st.px, st.py, C.t_nbr, cand);
+        }
+        M m = cap_list(incl, C.K);
+        const T ra = L.pr.radius;
+        while (m) {
+            const int b = m_ctz(m);
+            m &= m - 1;
+            const int j = L.base + b;
+            T gx, gy;
+            pair_force(C, st.px - lx[j], st.py - ly[j], st.vx - lvx[j], st.vy - lvy[j],
+                       ra + lr[j] + C.margin, L.dd, gx, gy);
+            fx += gx;
+            fy += gy;
+        }
+    }
+    T sx = T(0), sy = T(0);
+    for (int o = 0; o < tb.N; ++o) {
+        T gx, gy;
+        ob_force(C, tb, od, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.dd, gx, gy);
+        sx += gx;
+        sy += gy;
+    }
+    if (C.soft_walls) {
+        T gx, gy;
+        unsigned wb;
+        wall_force_axes(C, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv, gx, gy, wb);
+        sx += gx;
+        sy += gy;
+    }
+    Fx = fx + sx;
+    Fy = fy + sy;
+    return incl;
+}
+
+// Sum of v[base + b] over the set bits b of m, in ascending order, onto acc.
+template <typename T, typename M>
+__device__ __forceinline__ T ordered_sum(T acc, M m, const T *v, int base)
+{
+    while (m) {
+        const int b = m_ctz(m);
+        m &= m - 1;
+        acc += v[base + b];
+    }
+    return acc;
+}
+
+// This env's lanes whose flag is set, as a mask over the env's agent slots.
+template <int PA> __device__ __forceinline__ typename MaskT<PA>::type env_ballot(bool f, int base)
+{
+    typedef typename MaskT<PA>::type M;
+    const uint64_t bal = __ballot(f);
+    const uint64_t full = PA == 64 ? ~0ull : ((1ull << PA) - 1ull);
+    return (M)((bal >> base) & full);
+}
+
+// New state of one movable body: the contact sum of body_sum, then the integration of
+// bodies_env (the oracle's restatement of obstacle_dynamics_kernel).
+template <typename T> struct BodyNew {
+    T qx, qy, th, tvx, tvy, om, ca, sa;   // input pose (with its sin / cos)
+    T fx, fy, tau, ext;                   // contact sum
+    T nx, ny, nth, nvx, nvy, nom, nca, nsa;
+    bool clx, cly;
+};
+
+// The body pass of one env for movable body root o: every lane of the env computes the
+// same values (agent contributions reach all of them through `lred`).  Agent state of
+// the lane in `st`; `od` = the env's obstacle state at the substep input.
+template <typename T, int PA>
+__device__ __forceinline__ void body_step(const Cst<T> &C, const ObTab<T> &tb,
+                                          const Lane<T, PA> &L, const St<T> &st, const T *od,
+                                          int o, T *lred, BodyNew<T> &B)
+{
+    typedef typename MaskT<PA>::type M;
+    const int N = tb.N;
+    const T *b = od + 6 * N + 6 * o;
+    B.qx = b[0];
+    B.qy = b[1];
+    B.th = b[2];
+    B.tvx = b[3];
+    B.tvy = b[4];
+    B.om = b[5];
+    psincos(B.th, B.sa, B.ca);
+    T fx = T(0), fy = T(0), tau = T(0), ext = T(0);
+    const T mo = tb.mass[o];
+    const T denom_self = T(1) + C.c * C.sub_dt / mo;
+    for (int s = 0; s < N; ++s) {
+        if (tb.body[s] != o) continue;
+        const T offx = tb.off[2 * s], offy = tb.off[2 * s + 1];
+        const T owx = B.ca * offx - B.sa * offy;
+        const T owy = B.sa * offx + B.ca * offy;
+        const T csx = B.qx + owx, csy = B.qy + owy;
+        const T vsx = B.tvx - B.om * owy, vsy = B.tvy + B.om * owx;
+        const T ro = tb.rad[s];
+        const T ax = m_abs(offx), ay = m_abs(offy);
+        const T reach = m_sqrt(ax * ax + ay * ay) + ro;
+        ext = wmax(ext, reach);
+        // the agents' reactions, in agent order
+        T f0 = T(0), f1 = T(0), tq = T(0);
+        if (L.active && !b_apart(st.px - csx, st.py - csy, L.pr.radius + ro + C.margin)) {
+            T gx, gy;
+            pair_force(C, st.px - csx, st.py - csy, st.vx - vsx, st.vy - vsy,
+                       L.pr.radius + ro + C.margin, L.dd, gx, gy);
+            f0 = -gx;
+            f1 = -gy;
+            const T lx = owx + T(0), ly = owy + T(0);
+            tq = lx * f1 - ly * f0;
+        }
+        __syncthreads();
+        lred[L.lane] = f0;
+        lred[64 + L.lane] = f1;
+        lred[128 + L.lane] = tq;
+        __syncthreads();
+        const M nz = env_ballot<PA>(f0 != T(0) || f1 != T(0), L.base);
+        fx = ordered_sum(fx, nz, lred, L.base);
+        fy = ordered_sum(fy, nz, lred + 64, L.base);
+        tau = ordered_sum(tau, nz, lred + 128, L.base);
+        // contacts with the circles of other bodies and of the scenery, in index order
+        for (int o2 = 0; o2 < N; ++o2) {
+            if (tb.body[o2] == o) continue;
+            const T *d2 = od + 6 * o2;
+            const T r2 = tb.rad[o2];
+            if (b_apart(d2[0] - csx, d2[1] - csy, ro + r2 + C.margin)) continue;
+            T gx, gy;
+            pair_force(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4], ro + r2 + C.margin,
+                       denom_self, gx, gy);
+            const T lx = owx + T(0), ly = owy + T(0);
+            fx += gx;
+            fy += gy;
+            tau += lx * gy - ly * gx;
+        }
+    }
+    B.fx = fx;
+    B.fy = fy;
+    B.tau = tau;
+    B.ext = ext;
+    const T sdt = C.sub_dt, one = T(1);
+    const T lin_decay = one - tb.lin_damp * sdt;
+    const T ang_decay = one - tb.ang_damp * sdt;
+    const T I = tb.inertia[o];
+    T nvx = (B.tvx + fx / mo * sdt) * lin_decay;
+    T nvy = (B.tvy + fy / mo * sdt) * lin_decay;
+    const T nom = (B.om + tau / I * sdt) * ang_decay;
+    T nx = B.qx + nvx * sdt;
+    T ny = B.qy + nvy * sdt;
+    B.clx = B.cly = false;
+    if (C.clamp) {
+        const T half = T(0.5);
+        T lo_x = C.bmin_x + ext, mid_x = (C.bmin_x + C.bmax_x) * half;
+        lo_x = lo_x < mid_x ? lo_x : mid_x;
+        const T hi_x = wmax(C.bmax_x - ext, lo_x);
+        T lo_y = C.bmin_y + ext, mid_y = (C.bmin_y + C.bmax_y) * half;
+        lo_y = lo_y < mid_y ? lo_y : mid_y;
+        const T hi_y = wmax(C.bmax_y - ext, lo_y);
+        const T cx = wclamp(nx, lo_x, hi_x), cy = wclamp(ny, lo_y, hi_y);
+        B.clx = cx != nx;
+        B.cly = cy != ny;
+        if (B.clx) nvx = T(0);
+        if (B.cly) nvy = T(0);
+        nx = cx;
+        ny = cy;
+    }
+    B.nx = nx;
+    B.ny = ny;
+    B.nvx = nvx;
+    B.nvy = nvy;
+    B.nom = nom;
+    B.nth = B.th + nom * sdt;
+    psincos(B.nth, B.nsa, B.nca);
+}
+
+// The body pass of one env: obn = obc with every movable body advanced and its shapes
+// re-installed at the new pose.  Lane `agent` of the env copies entries agent, agent+PA...
+template <typename T, int PA>
+__device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
+                                          const Lane<T, PA> &L, const St<T> &st, const T *obc,
+                                          T *obn, T *lred)
+{
+    const int N = tb.N;
+    for (int q = L.agent; q < OB_W * N; q += PA) obn[q] = obc[q];
+    for (int o = 0; o < N; ++o) {
+        if (tb.body[o] != o || tb.kind[o] != 1) continue;
+        BodyNew<T> B;
+        body_step<T, PA>(C, tb, L, st, obc, o, lred, B);
+        if (L.agent == 0) {
+            T *bo = obn + 6 * N + 6 * o;
+            bo[0] = B.nx;
+            bo[1] = B.ny;
+            bo[2] = B.nth;
+            bo[3] = B.nvx;
+            bo[4] = B.nvy;
+            bo[5] = B.nom;
+            for (int s = 0; s < N; ++s) {
+                if (tb.body[s] != o) continue;
+                const T offx = tb.off[2 * s], offy = tb.off[2 * s + 1];
+                const T owx = B.nca * offx - B.nsa * offy;
+                const T owy = B.nsa * offx + B.nca * offy;
+                T *so = obn + 6 * s;
+                so[0] = B.nx + owx;
+                so[1] = B.ny + owy;
+                so[2] = B.nth;
+                so[3] = B.nvx - B.nom * owy;
+                so[4] = B.nvy + B.nom * owx;
+                so[5] = B.nom;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ forward rollout
+
+template <typename T, int PA>
+__global__ __launch_bounds__(64) void k_body_fwd(const Cst<T> C, const Args<T> g,
+                                                 const ObTab<T> tb, const ObIO<T> io)
+{
+    typedef typename MaskT<PA>::type M;
+    constexpr int EPW = 64 / PA;
+    __shared__ T sl[4 * 64];                         // px py vx vy of the substep
+    __shared__ T lr[64];                             // agent radius per lane
+    __shared__ T lred[3 * 64];                       // agent contributions to body sums
+    __shared__ T lob[2][EPW][OB_W * NOB_MAX];        // obstacle state: in / out of a substep
+    Lane<T, PA> L;
+    lane_init<T, PA>(C, g, L);
+    lr[L.lane] = L.pr.radius;
+    const int ew = L.lane / PA;
+    const int NW = OB_W * tb.N;
+    const bool env_ok = L.env < C.E;
+    const size_t eo = (size_t)(env_ok ? L.env : 0) * NW;
+    for (int q = L.agent; q < NW; q += PA) lob[0][ew][q] = io.ob0[eo + q];
+    St<T> st;
+    load_state<T, false>(g.s0.f, L.idx, 0, st);
+    if (!L.active) st.px = st.py = __builtin_nan("");
+    const size_t EA = (size_t)C.E * C.A, ENW = (size_t)C.E * NW;
+    int cur = 0;
+    for (int t = 0; t < g.nsteps; ++t) {
+        T a[4];
+        load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
+        M cand = 0;
+        T D = T(0);
+        bool ok = false;
+        for (int s = 0; s < C.S; ++s) {
+            __syncthreads();
+            sl[F_PX * 64 + L.lane] = st.px;
+            sl[F_PY * 64 + L.lane] = st.py;
+            sl[F_VX * 64 + L.lane] = st.vx;
+            sl[F_VY * 64 + L.lane] = st.vy;
+            __syncthreads();
+            const T *obc = lob[cur][ew];
+            T Fx, Fy;
+            forces_b<T, PA>(C, tb, L, sl, lr, obc, st, s, s == 0 || !ok, cand, Fx, Fy);
+            body_pass<T, PA>(C, tb, L, st, obc, lob[cur ^ 1][ew], lred);
+            St<T> nx;
+            integrate<T, false>(C, L.pr, st, a, Fx, Fy, nx);
+            if (C.use_skin) {
+                D += (m_abs(nx.px - st.px) + m_abs(nx.py - st.py)) * T(1.0001);
+                ok = env_all<PA>(!L.active || D <= C.half_margin, L.base);
+            }
+            st = nx;
+            cur ^= 1;
+        }
+        __syncthreads();
+        if (L.active) {
+            if (t + 1 < g.nsteps)
+                store_state<T, false>(g.traj.f, (size_t)t * EA + L.idx, st);
+            else
+                store_state<T, false>(g.fin.f, L.idx, st);
+        }
+        if (env_ok)
+            for (int q = L.agent; q < NW; q += PA) io.traj[(size_t)t * ENW + eo + q] = lob[cur][ew][q];
+    }
+}
+
+// ----------------------------------------------------------------- backward rollout
+
+// Dynamic LDS of k_body_bwd (host and device agree on this layout).
+template <typename T, int PA> __host__ __device__ constexpr size_t body_bwd_lds(int S, int N)
+{
+    typedef typename MaskT<PA>::type M;
+    return 2 * 64 * sizeof(T)                               // radius, damping divisor
+           + (size_t)S * NF_2D * 64 * sizeof(T)             // substep agent slots
+           + (size_t)S * 64 * sizeof(M)                     // inclusion masks
+           + 6 * 64 * sizeof(T)                             // ordered-sum staging
+           + (size_t)(S + 1) * (64 / PA) * OB_W * N * sizeof(T)  // obstacle state per substep
+           + 2 * (size_t)(64 / PA) * OB_W * N * sizeof(T);       // obstacle adjoint in / out
+}
+
+// Reverse of body_pass for one env.  gout = adjoint of the pass's output (the env's
+// obstacle state after the substep), gin receives the adjoint of its input (overwritten);
+// the lane's agent adjoint is accumulated into `ga`.  Same order of terms as the oracle's
+// bodies_env_adj.
+template <typename T, int PA>
+__device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &tb,
+                                              const Lane<T, PA> &L, const St<T> &st,
+                                              const T *obc, const T *gout, T *gin, T *lred,
+                                              St<T> &ga)
+{
+    typedef typename MaskT<PA>::type M;
+    const int N = tb.N;
+    // pass-through of everything the pass does not rewrite
+    for (int q = L.agent; q < OB_W * N; q += PA) {
+        const int s = q / 6;
+        gin[q] = (q < 6 * N && shape_moves(tb, s)) ? T(0) : gout[q];
+    }
+    __syncthreads();
+    for (int o = 0; o < N; ++o) {
+        if (tb.body[o] != o || tb.kind[o] != 1) continue;
+        BodyNew<T> B;
+        body_step<T, PA>(C, tb, L, st, obc, o, lred, B);
+        const T sdt = C.sub_dt, one = T(1);
+        const T lin_decay = one - tb.lin_damp * sdt;
+        const T ang_decay = one - tb.ang_damp * sdt;
+        const T m = tb.mass[o], I = tb.inertia[o];
+        // adjoint of the new body state: its own entry plus every re-installed shape
+        const T *gb = gout + 6 * N + 6 * o;
+        T g_nx = gb[0], g_ny = gb[1], g_nth = gb[2], g_nvx = gb[3], g_nvy = gb[4], g_nom = gb[5];
+        for (int s = 0; s < N; ++s) {
+            if (tb.body[s] != o) continue;
+            const T offx = tb.off[2 * s], offy = tb.off[2 * s + 1];
+            const T owx = B.nca * offx - B.nsa * offy;
+            const T owy = B.nsa * offx + B.nca * offy;
+            const T *gs = gout + 6 * s;
+            g_nx += gs[0];
+            g_ny += gs[1];
+            g_nth += gs[2];
+            g_nvx += gs[3];
+            g_nvy += gs[4];
+            g_nom += gs[5] - gs[3] * owy + gs[4] * owx;
+            const T g_owx = gs[0] + gs[4] * B.nom, g_owy = gs[1] - gs[3] * B.nom;
+            g_nth += -g_owx * owy + g_owy * owx;
+        }
+        T g_th = g_nth;
+        g_nom += g_nth * sdt;
+        T g_qx = B.clx ? T(0) : g_nx, g_qy = B.cly ? T(0) : g_ny;
+        if (B.clx) g_nvx = T(0); else g_nvx += g_nx * sdt;
+        if (B.cly) g_nvy = T(0); else g_nvy += g_ny * sdt;
+        T g_tvx = g_nvx * lin_decay, g_tvy = g_nvy * lin_decay;
+        const T g_fx = g_nvx * lin_decay * sdt / m, g_fy = g_nvy * lin_decay * sdt / m;
+        T g_om = g_nom * ang_decay;
+        const T g_tau = g_nom * ang_decay * sdt / I;
+        const T denom_self = T(1) + C.c * C.sub_dt / m;
+        for (int s = 0; s < N; ++s) {
+            if (tb.body[s] != o) continue;
+            const T offx = tb.off[2 * s], offy = tb.off[2 * s + 1];
+            const T owx = B.ca * offx - B.sa * offy;
+            const T owy = B.sa * offx + B.ca * offy;
+            const T csx = B.qx + owx, csy = B.qy + owy;
+            const T vsx = B.tvx - B.om * owy, vsy = B.tvy + B.om * owx;
+            const T ro = tb.rad[s];
+            const T g_f0 = g_fx - g_tau * owy, g_f1 = g_fy + g_tau * owx;
+            // the agents' terms, in agent order
+            T c0 = T(0), c1 = T(0), c2 = T(0), c3 = T(0), c4 = T(0), c5 = T(0);
+            if (L.active && !b_apart(st.px - csx, st.py - csy, L.pr.radius + ro + C.margin)) {
+                const T dx = st.px - csx, dy = st.py - csy, rvx = st.vx - vsx, rvy = st.vy - vsy;
+                const T md = L.pr.radius + ro + C.margin;
+                T gx, gy;
+                pair_force(C, dx, dy, rvx, rvy, md, L.dd, gx, gy);
+                const T f0 = -gx, f1 = -gy;
+                T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
+                pair_force_adj(C, dx, dy, rvx, rvy, md, L.dd, -g_f0, -g_f1, adx, ady, arx, ary);
+                ga.px += adx;
+                ga.py += ady;
+                ga.vx += arx;
+                ga.vy += ary;
+                c0 = g_tau * f1;   // onto g_owx
+                c1 = -(g_tau * f0);  // onto g_owy (g_owy -= g_tau * f0)
+                c2 = -adx;         // onto g_csx
+                c3 = -ady;
+                c4 = -arx;         // onto g_vsx
+                c5 = -ary;
+            }
+            __syncthreads();
+            lred[L.lane] = c0;
+            lred[64 + L.lane] = c1;
+            lred[128 + L.lane] = c2;
+            lred[192 + L.lane] = c3;
+            lred[256 + L.lane] = c4;
+            lred[320 + L.lane] = c5;
+            __syncthreads();
+            const M nz = env_ballot<PA>(c0 != T(0) || c1 != T(0) || c2 != T(0) || c3 != T(0) ||
+                                            c4 != T(0) || c5 != T(0),
+                                        L.base);
+            T g_owx = ordered_sum(T(0), nz, lred, L.base);
+            T g_owy = ordered_sum(T(0), nz, lred + 64, L.base);
+            T g_csx = ordered_sum(T(0), nz, lred + 128, L.base);
+            T g_csy = ordered_sum(T(0), nz, lred + 192, L.base);
+            T g_vsx = ordered_sum(T(0), nz, lred + 256, L.base);
+            T g_vsy = ordered_sum(T(0), nz, lred + 320, L.base);
+            for (int o2 = 0; o2 < N; ++o2) {
+                if (tb.body[o2] == o) continue;
+                const T *d2 = obc + 6 * o2;
+                const T r2 = tb.rad[o2];
+                if (b_apart(d2[0] - csx, d2[1] - csy, ro + r2 + C.margin)) continue;
+                T gx, gy;
+                pair_force(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4],
+                           ro + r2 + C.margin, denom_self, gx, gy);
+                g_owx += g_tau * gy;
+                g_owy -= g_tau * gx;
+                T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
+                pair_force_adj(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4],
+                               ro + r2 + C.margin, denom_self, g_f0, g_f1, adx, ady, arx, ary);
+                g_csx += adx;
+                g_csy += ady;
+                g_vsx += arx;
+                g_vsy += ary;
+                if (shape_moves(tb, o2) && L.agent == 0) {
+                    T *g2 = gin + 6 * o2;
+                    g2[0] -= adx;
+                    g2[1] -= ady;
+                    g2[3] -= arx;
+                    g2[4] -= ary;
+                }
+            }
+            g_qx += g_csx;
+            g_qy += g_csy;
+            g_owx += g_csx + g_vsy * B.om;
+            g_owy += g_csy - g_vsx * B.om;
+            g_tvx += g_vsx;
+            g_tvy += g_vsy;
+            g_om += -g_vsx * owy + g_vsy * owx;
+            g_th += -g_owx * owy + g_owy * owx;
+        }
+        if (L.agent == 0) {
+            T *gi = gin + 6 * N + 6 * o;
+            gi[0] = g_qx;
+            gi[1] = g_qy;
+            gi[2] = g_th;
+            gi[3] = g_tvx;
+            gi[4] = g_tvy;
+            gi[5] = g_om;
+        }
+        __syncthreads();
+    }
+}
+
+template <typename T, int PA>
+__global__ __launch_bounds__(64) void k_body_bwd(const Cst<T> C, const Args<T> g,
+                                                 const ObTab<T> tb, const ObIO<T> io)
+{
+    typedef typename MaskT<PA>::type M;
+    constexpr int EPW = 64 / PA;
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int N = tb.N, NW = OB_W * N;
+    T *lr = (T *)smem;                                   // radius per lane
+    T *ldd = lr + 64;                                    // damping divisor per lane
+    T *slots = ldd + 64;                                 // S slots of NF_2D fields
+    M *lmask = (M *)(slots + (size_t)C.S * NF_2D * 64);  // S inclusion masks
+    T *lred = (T *)(lmask + (size_t)C.S * 64);           // 6 x 64 ordered-sum staging
+    T *lobs = lred + 6 * 64;                             // [S+1][EPW][NW] obstacle states
+    T *lgob = lobs + (size_t)(C.S + 1) * EPW * NW;       // [2][EPW][NW] obstacle adjoints
+    Lane<T, PA> L;
+    lane_init<T, PA>(C, g, L);
+    lr[L.lane] = L.pr.radius;
+    ldd[L.lane] = L.dd;
+    const int ew = L.lane / PA;
+    const bool env_ok = L.env < C.E;
+    const size_t eo = (size_t)(env_ok ? L.env : 0) * NW;
+    const size_t EA = (size_t)C.E * C.A, ENW = (size_t)C.E * NW;
+    T *gob = lgob + (size_t)ew * NW;             // adjoint of the current substep's output
+    T *gprev = lgob + (size_t)(EPW + ew) * NW;   // adjoint of its input
+    for (int q = L.agent; q < NW; q += PA) gob[q] = T(0);
+    St<T> gs;
+    st_zero(gs);
+    for (int t = g.nsteps - 1; t >= 0; --t) {
+        if (t == g.nsteps - 1)
+            add_adj<T, false>(g.afin.f, L.idx, gs);
+        else
+            add_adj<T, false>(g.atraj.f, (size_t)t * EA + L.idx, gs);
+        __syncthreads();
+        if (io.atraj && env_ok)
+            for (int q = L.agent; q < NW; q += PA) gob[q] += io.atraj[(size_t)t * ENW + eo + q];
+        St<T> st;
+        if (t == 0)
+            load_state<T, false>(g.s0.f, L.idx, 0, st);
+        else
+            load_state<T, false>(g.traj.f, L.idx, (size_t)(t - 1) * EA, st);
+        if (!L.active) st.px = st.py = __builtin_nan("");
+        {
+            const T *src = t == 0 ? io.ob0 + eo : io.traj + (size_t)(t - 1) * ENW + eo;
+            T *dst = lobs + (size_t)ew * NW;
+            for (int q = L.agent; q < NW; q += PA) dst[q] = src[q];
+        }
+        T a[4];
+        load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
+
+        // ---- recompute the substep chain of this step into LDS
+        M cand = 0;
+        T D = T(0);
+        bool ok = false;
+        for (int s = 0; s < C.S; ++s) {
+            T *sl = slots + (size_t)s * NF_2D * 64;
+            __syncthreads();
+            slot_put<T, false>(sl, L.lane, st);
+            __syncthreads();
+            const T *obc = lobs + ((size_t)s * EPW + ew) * NW;
+            T Fx, Fy;
+            const M incl = forces_b<T, PA>(C, tb, L, sl, lr, obc, st, s, s == 0 || !ok, cand, Fx, Fy);
+            sl[F_FX * 64 + L.lane] = Fx;
+            sl[F_FY * 64 + L.lane] = Fy;
+            lmask[s * 64 + L.lane] = incl;
+            body_pass<T, PA>(C, tb, L, st, obc, lobs + ((size_t)(s + 1) * EPW + ew) * NW, lred);
+            St<T> nx;
+            integrate<T, false>(C, L.pr, st, a, Fx, Fy, nx);
+            if (C.use_skin) {
+                D += (m_abs(nx.px - st.px) + m_abs(nx.py - st.py)) * T(1.0001);
+                ok = env_all<PA>(!L.active || D <= C.half_margin, L.base);
+            }
+            st = nx;
+        }
+
+        // ---- reverse pass
+        T ga[4] = {T(0), T(0), T(0), T(0)};
+        for (int s = C.S - 1; s >= 0; --s) {
+            T *sl = slots + (size_t)s * NF_2D * 64;
+            const T *obc = lobs + ((size_t)s * EPW + ew) * NW;
+            __syncthreads();
+            St<T> in;
+            slot_get<T, false>(sl, L.lane, in);
+            const T Fx = sl[F_FX * 64 + L.lane], Fy = sl[F_FY * 64 + L.lane];
+            St<T> gi;
+            T gFx, gFy;
+            integrate_adj<T, false>(C, L.pr, in, a, Fx, Fy, gs, gi, ga, gFx, gFy);
+            // the body pass: adjoint of its input obstacle state into gprev
+            body_pass_adj<T, PA>(C, tb, L, in, obc, gob, gprev, lred, gi);
+            if (C.needs_forces) {
+                const T wFx = gFx * L.inv_dd, wFy = gFy * L.inv_dd;
+                __syncthreads();
+                sl[F_FX * 64 + L.lane] = wFx;
+                sl[F_FY * 64 + L.lane] = wFy;
+                __syncthreads();
+                if (C.collisions) {
+                    const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64;
+                    const T *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
+                    const T *lgx = sl + F_FX * 64, *lgy = sl + F_FY * 64;
+                    const M mine = lmask[s * 64 + L.lane];
+                    M m = mine;
+                    while (m) {
+                        const int b = m_ctz(m);
+                        m &= m - 1;
+                        const int j = L.base + b;
+                        const bool own = in_list(mine, b, C.K);
+                        const bool rev = in_list(lmask[s * 64 + j], L.agent, C.K);
+                        if (!own && !rev) continue;
+                        const T wx = (own ? wFx : T(0)) - (rev ? lgx[j] : T(0));
+                        const T wy = (own ? wFy : T(0)) - (rev ? lgy[j] : T(0));
+                        pair_adj_combined(C, in.px - lx[j], in.py - ly[j], in.vx - lvx[j],
+                                          in.vy - lvy[j], L.pr.radius + lr[j] + C.margin, wx, wy,
+                                          gi.px, gi.py, gi.vx, gi.vy);
+                    }
+                }
+                // obstacles: the agent's adjoint, and the moving circles' in agent order
+                for (int o = 0; o < N; ++o) {
+                    T opx = T(0), opy = T(0), ovx = T(0), ovy = T(0);
+                    if (L.active)
+                        ob_force_adj(C, tb, obc, o, in.px, in.py, in.vx, in.vy, L.pr.radius,
+                                     L.dd, gFx, gFy, gi, opx, opy, ovx, ovy);
+                    if (!shape_moves(tb, o)) continue;
+                    __syncthreads();
+                    lred[L.lane] = opx;
+                    lred[64 + L.lane] = opy;
+                    lred[128 + L.lane] = ovx;
+                    lred[192 + L.lane] = ovy;
+                    __syncthreads();
+                    const M nz = env_ballot<PA>(opx != T(0) || opy != T(0) || ovx != T(0) ||
+                                                    ovy != T(0),
+                                                L.base);
+                    if (nz && L.agent == 0) {
+                        T *g2 = gprev + 6 * o;
+                        g2[0] = ordered_sum(g2[0], nz, lred, L.base);
+                        g2[1] = ordered_sum(g2[1], nz, lred + 64, L.base);
+                        g2[3] = ordered_sum(g2[3], nz, lred + 128, L.base);
+                        g2[4] = ordered_sum(g2[4], nz, lred + 192, L.base);
+                    }
+                }
+                if (C.soft_walls)
+                    wall_force_adj(C, in.px, in.py, in.vx, in.vy, L.pr.radius, L.dd, gFx, gFy, gi);
+            }
+            gs = gi;
+            __syncthreads();
+            T *tmp = gob;
+            gob = gprev;
+            gprev = tmp;
+        }
+        if (L.active) {
+            T *pa = g.aact + ((size_t)t * EA + L.idx) * C.ad;
+            for (int k = 0; k < C.ad; ++k) pa[k] = k < 4 ? ga[k] : T(0);
+        }
+    }
+    if (L.active) store_adj<T, false>(g.a0.f, L.idx, gs);
+    __syncthreads();
+    if (io.a0 && env_ok)
+        for (int q = L.agent; q < NW; q += PA) io.a0[eo + q] = gob[q];
+}
+
+}  // namespace swarp

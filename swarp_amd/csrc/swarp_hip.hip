@@ -510,6 +510,7 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
 
 }  // namespace swarp
 #include "lean.hpp"
+#include "bodies.hpp"
 namespace swarp {
 
 // --------------------------------------------------------------- neighbour lists
@@ -899,9 +900,148 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     return 0;
 }
 
+template <typename T> static int fill_obtab(const swarp_desc_t *d, ObTab<T> &tb)
+{
+    if (d->n_obstacles < 1 || d->n_obstacles > NOB_MAX)
+        return fail("the body path takes 1 to 16 obstacles per env");
+    if (!d->obs_kind || !d->obs_body || !d->obs_mass || !d->obs_inertia || !d->obs_body_off)
+        return fail("obs_kind/obs_body/obs_mass/obs_inertia/obs_body_off must be set");
+    if (d->has_drone) return fail("the body path steps 2-D fleets only");
+    tb.rad = (const T *)d->obs_radius;
+    tb.half = (const T *)d->obs_half;
+    tb.mass = (const T *)d->obs_mass;
+    tb.inertia = (const T *)d->obs_inertia;
+    tb.off = (const T *)d->obs_body_off;
+    tb.type = d->obs_type;
+    tb.kind = d->obs_kind;
+    tb.body = d->obs_body;
+    tb.lin_damp = (T)d->lin_damping;
+    tb.ang_damp = (T)d->ang_damping;
+    tb.N = d->n_obstacles;
+    return 0;
+}
+
+template <typename T>
+static int rollout_fwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s0,
+                          const void *ob0, const void *act, const swarp_state_t *traj,
+                          const swarp_state_t *fin, void *ob_traj, hipStream_t st)
+{
+    Cst<T> C;
+    fill_cst<T>(d, skin_of(d), C);
+    Args<T> a;
+    fill_args<T>(d, a);
+    ObTab<T> tb;
+    if (fill_obtab<T>(d, tb)) return -1;
+    if (!fields_ok(s0, 5)) return fail("state0 is missing a field");
+    if (!fields_ok(fin, 5)) return fail("final_state is missing a field");
+    if (nT > 1 && !fields_ok(traj, 5)) return fail("traj is missing a field (T > 1)");
+    if (!act || !ob0 || !ob_traj) return fail("actions / ob0 / ob_traj is NULL");
+    copy_fields<T>(s0, (T **)a.s0.f);
+    copy_fields<T>(fin, a.fin.f);
+    if (nT > 1) copy_fields<T>(traj, a.traj.f);
+    a.act = (const T *)act;
+    a.nsteps = nT;
+    ObIO<T> io = {(const T *)ob0, (T *)ob_traj, nullptr, nullptr};
+    const int PA = pad_agents(d->n_agents);
+    const dim3 grid((C.E + 64 / PA - 1) / (64 / PA));
+    switch (PA) {
+    case 4: hipLaunchKernelGGL((k_body_fwd<T, 4>), grid, dim3(64), 0, st, C, a, tb, io); break;
+    case 8: hipLaunchKernelGGL((k_body_fwd<T, 8>), grid, dim3(64), 0, st, C, a, tb, io); break;
+    case 16: hipLaunchKernelGGL((k_body_fwd<T, 16>), grid, dim3(64), 0, st, C, a, tb, io); break;
+    case 32: hipLaunchKernelGGL((k_body_fwd<T, 32>), grid, dim3(64), 0, st, C, a, tb, io); break;
+    default: hipLaunchKernelGGL((k_body_fwd<T, 64>), grid, dim3(64), 0, st, C, a, tb, io); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(hipGetErrorString(e));
+    return 0;
+}
+
+template <typename T> static size_t body_bwd_lds_of(int PA, int S, int N)
+{
+    switch (PA) {
+    case 4: return body_bwd_lds<T, 4>(S, N);
+    case 8: return body_bwd_lds<T, 8>(S, N);
+    case 16: return body_bwd_lds<T, 16>(S, N);
+    case 32: return body_bwd_lds<T, 32>(S, N);
+    default: return body_bwd_lds<T, 64>(S, N);
+    }
+}
+
+template <typename T>
+static int rollout_bwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s0,
+                          const void *ob0, const void *act, const swarp_state_t *traj,
+                          const void *ob_traj, const swarp_state_t *atraj,
+                          const swarp_state_t *afin, const void *aob_traj,
+                          const swarp_state_t *a0, void *aob0, void *aact, hipStream_t st)
+{
+    Cst<T> C;
+    fill_cst<T>(d, skin_of(d), C);
+    Args<T> a;
+    fill_args<T>(d, a);
+    ObTab<T> tb;
+    if (fill_obtab<T>(d, tb)) return -1;
+    if (!fields_ok(s0, 5)) return fail("state0 is missing a field");
+    if (nT > 1 && !fields_ok(traj, 5)) return fail("traj is missing a field (T > 1)");
+    if (!act || !aact || !ob0 || !ob_traj) return fail("actions / adj_actions / ob0 / ob_traj is NULL");
+    copy_fields<T>(s0, (T **)a.s0.f);
+    if (nT > 1) copy_fields<T>(traj, a.traj.f);
+    if (atraj) copy_fields<T>(atraj, (T **)a.atraj.f);
+    if (afin) copy_fields<T>(afin, (T **)a.afin.f);
+    if (a0) copy_fields<T>(a0, a.a0.f);
+    a.act = (const T *)act;
+    a.aact = (T *)aact;
+    a.nsteps = nT;
+    ObIO<T> io = {(const T *)ob0, (T *)ob_traj, (const T *)aob_traj, (T *)aob0};
+    const int PA = pad_agents(d->n_agents);
+    const size_t shm = body_bwd_lds_of<T>(PA, d->substeps, d->n_obstacles);
+    if (shm > 65536) return fail("substeps too large for the body backward's LDS staging (limit 64 KiB per wave)");
+    const dim3 grid((C.E + 64 / PA - 1) / (64 / PA));
+    switch (PA) {
+    case 4: hipLaunchKernelGGL((k_body_bwd<T, 4>), grid, dim3(64), shm, st, C, a, tb, io); break;
+    case 8: hipLaunchKernelGGL((k_body_bwd<T, 8>), grid, dim3(64), shm, st, C, a, tb, io); break;
+    case 16: hipLaunchKernelGGL((k_body_bwd<T, 16>), grid, dim3(64), shm, st, C, a, tb, io); break;
+    case 32: hipLaunchKernelGGL((k_body_bwd<T, 32>), grid, dim3(64), shm, st, C, a, tb, io); break;
+    default: hipLaunchKernelGGL((k_body_bwd<T, 64>), grid, dim3(64), shm, st, C, a, tb, io); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(hipGetErrorString(e));
+    return 0;
+}
+
 extern "C" {
 
 int swarp_abi_version(void) { return SWARP_ABI_VERSION; }
+
+int swarp_rollout_fwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                         const void *ob0, const void *actions, const swarp_state_t *traj,
+                         const swarp_state_t *final_state, void *ob_traj, void *stream)
+{
+    g_err[0] = 0;
+    if (check_desc(desc)) return -1;
+    if (T < 1) return fail("T must be >= 1");
+    hipStream_t st = (hipStream_t)stream;
+    if (desc->dtype == SWARP_F32)
+        return rollout_fwd_ob<float>(desc, T, state0, ob0, actions, traj, final_state, ob_traj, st);
+    return rollout_fwd_ob<double>(desc, T, state0, ob0, actions, traj, final_state, ob_traj, st);
+}
+
+int swarp_rollout_bwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                         const void *ob0, const void *actions, const swarp_state_t *traj,
+                         const void *ob_traj, const swarp_state_t *adj_traj,
+                         const swarp_state_t *adj_final, const void *adj_ob_traj,
+                         const swarp_state_t *adj_state0, void *adj_ob0, void *adj_actions,
+                         void *stream)
+{
+    g_err[0] = 0;
+    if (check_desc(desc)) return -1;
+    if (T < 1) return fail("T must be >= 1");
+    hipStream_t st = (hipStream_t)stream;
+    if (desc->dtype == SWARP_F32)
+        return rollout_bwd_ob<float>(desc, T, state0, ob0, actions, traj, ob_traj, adj_traj,
+                                     adj_final, adj_ob_traj, adj_state0, adj_ob0, adj_actions, st);
+    return rollout_bwd_ob<double>(desc, T, state0, ob0, actions, traj, ob_traj, adj_traj,
+                                  adj_final, adj_ob_traj, adj_state0, adj_ob0, adj_actions, st);
+}
 
 const char *swarp_last_error(void) { return g_err; }
 

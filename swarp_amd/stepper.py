@@ -141,6 +141,10 @@ class Stepper:
         self.obstacles: Obstacles | None = None
         self._obs: dict[str, torch.Tensor] = {}
         self.any_movable = False
+        #: movable bodies: the per-env obstacle state [n_envs, 12 N] entering the next
+        #: rollout (advanced by every rollout) and the last rollout's [T, n_envs, 12 N]
+        self.ob_state: torch.Tensor | None = None
+        self.ob_trajectory: torch.Tensor | None = None
         self._descs: dict[tuple[int, int], _lib.SwarpDesc] = {}
         self._grids: dict[int, NeighborGrid] = {}
         self._out_states: dict[int, list] = {}
@@ -172,27 +176,74 @@ class Stepper:
 
     def set_obstacles(self, obstacles: Obstacles) -> None:
         """Install the obstacle set (``swarp/core/stepper.py:295-432``); absent fields
-        take their documented defaults."""
+        take their documented defaults.  With MOVABLE obstacles the per-env obstacle state
+        ``ob_state`` ``[n_envs, 12 N]`` is seeded from the shapes' installed poses
+        (``_body_seed``, ``swarp/core/stepper.py:434-476``) and advanced by every rollout."""
         obs = obstacles.resolve(self.device, self.dtype)
-        if obs.any_movable:
-            raise NotImplementedError("MOVABLE obstacles (compound bodies) are not implemented yet")
         n_envs, n = obs.n_envs, obs.n_obstacles
         z = {"device": self.device, "dtype": self.dtype}
+        zi = {"device": self.device, "dtype": torch.int32}
         self._obs = {
             "pos": obs.pos,
             "radius": obs.radius,
-            "type": obs.shape if obs.shape is not None else torch.zeros(n, device=self.device, dtype=torch.int32),
+            "type": obs.shape if obs.shape is not None else torch.zeros(n, **zi),
             "angle": obs.angle if obs.angle is not None else torch.zeros(n_envs, n, **z),
             "half": obs.half_extents if obs.half_extents is not None else torch.zeros(n, 2, **z),
             "vel": obs.vel if obs.vel is not None else torch.zeros(n_envs, n, 2, **z),
             "ang_vel": obs.ang_vel if obs.ang_vel is not None else torch.zeros(n_envs, n, **z),
+            "kind": obs.kind if obs.kind is not None else torch.zeros(n, **zi),
+            "body": obs.body if obs.body is not None else torch.arange(n, **zi),
+            "mass": obs.mass if obs.mass is not None else torch.ones(n, **z),
+            "inertia": obs.inertia if obs.inertia is not None else torch.ones(n, **z),
+            "off": obs.body_offset if obs.body_offset is not None else torch.zeros(n, 2, **z),
         }
+        body = self._obs["body"]
+        if n > 0 and bool(((body < 0) | (body >= n)).any()):
+            raise ValueError(f"obstacle body indices must lie in [0, {n})")
+        movable = obs.any_movable
+        if movable:
+            if n > 16:
+                raise NotImplementedError("movable bodies: this build steps at most 16 obstacles per env")
+            if self.has_drone:
+                raise NotImplementedError("movable bodies with DRONE agents are not implemented")
+            moving = self._moving_shapes(self._obs["kind"], self._obs["body"])
+            if bool(((self._obs["type"] != 0) & moving).any()):
+                raise NotImplementedError(
+                    "movable bodies: only circle shapes (the disc variant of the body pass)")
         self.obstacles = obstacles
         self.n_obstacles = n
         self._obs_envs = n_envs
-        self.any_movable = False
+        self.any_movable = movable
+        self.ob_state = self._body_seed() if movable else None
+        self.ob_trajectory = None
         self._descs.clear()
         self.mutation_version += 1
+
+    @staticmethod
+    def _moving_shapes(kind: torch.Tensor, body: torch.Tensor) -> torch.Tensor:
+        """Bool [N]: the shape belongs to a movable body (its root is MOVABLE)."""
+        root = body.long()
+        return (body[root] == body) & (kind[root] == 1)
+
+    def _body_seed(self) -> torch.Tensor:
+        """Obstacle state [n_envs, 12 N]: per shape its installed pose and velocity, then
+        per index the state of the body rooted there, derived from the root shape: origin
+        = root pos - R(root angle) @ root offset; heading, velocity and spin the root's."""
+        o = self._obs
+        pos, ang, vel, om = (o["pos"].double(), o["angle"].double(), o["vel"].double(),
+                             o["ang_vel"].double())
+        n_envs, n = pos.shape[0], pos.shape[1]
+        root = o["body"].long()
+        off = o["off"].double()[root]                       # [N, 2] offset of each root
+        ra = ang[:, root]                                   # [E, N]
+        ca, sa = torch.cos(ra), torch.sin(ra)
+        wx = ca * off[:, 0] - sa * off[:, 1]
+        wy = sa * off[:, 0] + ca * off[:, 1]
+        shapes = torch.cat([pos, ang.unsqueeze(-1), vel, om.unsqueeze(-1)], -1)  # [E, N, 6]
+        bodies = torch.stack([pos[:, root, 0] - wx, pos[:, root, 1] - wy, ra,
+                              vel[:, root, 0], vel[:, root, 1], om[:, root]], -1)
+        return torch.cat([shapes.reshape(n_envs, 6 * n), bodies.reshape(n_envs, 6 * n)],
+                         -1).to(self.dtype).contiguous()
 
     @property
     def _needs_forces(self) -> bool:
@@ -246,6 +297,13 @@ class Stepper:
             d.obs_vel = o["vel"].data_ptr()
             d.obs_ang_vel = o["ang_vel"].data_ptr()
             d.obs_type = o["type"].data_ptr()
+            d.obs_kind = o["kind"].data_ptr()
+            d.obs_body = o["body"].data_ptr()
+            d.obs_mass = o["mass"].data_ptr()
+            d.obs_inertia = o["inertia"].data_ptr()
+            d.obs_body_off = o["off"].data_ptr()
+        d.lin_damping = float(self.world.obstacle_linear_damping)
+        d.ang_damping = float(self.world.obstacle_angular_damping)
         self._descs[key] = d
         return d
 

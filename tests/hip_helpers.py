@@ -49,11 +49,16 @@ def make_stepper(configs, world, dt, substeps, dtype, obs: dict | None = None, n
     st = Stepper(configs, dt=dt, substeps=substeps, device="cuda:0", dtype=dtype, world=world)
     if obs is not None:
         o = obstacles_np(obs, n_envs)
+        body = {}
+        if "kind" in o:  # movable compound bodies
+            body = dict(kind=torch.tensor(o["kind"]), body=torch.tensor(o["body"]),
+                        mass=torch.tensor(o["mass"]), inertia=torch.tensor(o["inertia"]),
+                        body_offset=torch.tensor(o["body_off"]))
         st.set_obstacles(Obstacles(
             pos=torch.tensor(o["pos"]), radius=torch.tensor(o["radius"]),
             shape=torch.tensor(o["type"]), angle=torch.tensor(o["angle"]),
             half_extents=torch.tensor(o["half"]), vel=torch.tensor(o["vel"]),
-            ang_vel=torch.tensor(o["ang_vel"]),
+            ang_vel=torch.tensor(o["ang_vel"]), **body,
         ))
     return st
 

@@ -1,5 +1,7 @@
 """Movable compound bodies on the HIP path (swarp/core/bodies.py:367-568) vs the CPU
-oracle, and this build's body adjoint vs finite differences.
+oracle, and this build's body adjoint vs finite differences.  (The file name sorts after
+the other GPU parity files, so a full GPU run exercises the generic and drone kernels
+before these.)
 
 Bars: the body pass computes with +, -, *, /, sqrt and a portable sin / cos evaluated
 identically on host and device, so float32 agent states AND obstacle states are compared
@@ -18,14 +20,7 @@ from oracle.oracle import Oracle, pack_state
 from swarp_amd import rollout
 from swarp_amd.config import WorldConfig
 
-pytestmark = [
-    pytest.mark.gpu,
-    pytest.mark.skip(reason=(
-        "the HIP body path is switched off (set_obstacles raises NotImplementedError for "
-        "MOVABLE obstacles): after these kernels had run on the GPU, a later fp32 drone "
-        "parity test in the same process hit an illegal memory access whose cause has not "
-        "been shown; these tests stay skipped until it is")),
-]
+pytestmark = pytest.mark.gpu
 MOVABLE = 1
 TDT = {np.float32: torch.float32, np.float64: torch.float64}
 

@@ -173,9 +173,32 @@ def test_stepper_reach_check_and_unsupported_features():
     assert math.isclose(st.sub_dt, 0.025)
     assert math.isclose(st.neighbor_radius, 2 * 0.2 + 0.02)
     assert st.holo_velocity_only and not st.has_drone
-    with pytest.raises(NotImplementedError, match="MOVABLE"):
+    # a movable body seeds the per-env obstacle state (swarp/core/stepper.py:434-476):
+    # shapes at their installed poses, the body origin = root pos - R(root angle) @ offset
+    E = 2
+    pos = torch.tensor([[[1.0, 2.0], [1.0, 2.5]], [[0.0, 0.0], [0.0, 0.5]]])
+    ang = torch.tensor([[0.5, 0.5], [0.0, 0.0]])
+    vel = torch.tensor([[[0.1, 0.2], [0.3, 0.4]], [[0.0, 0.0], [0.0, 0.0]]])
+    st.set_obstacles(Obstacles(pos=pos, radius=torch.tensor([0.1, 0.1]), angle=ang, vel=vel,
+                               kind=torch.tensor([1, 1], dtype=torch.int32),
+                               body=torch.tensor([0, 0], dtype=torch.int32),
+                               body_offset=torch.tensor([[0.2, -0.1], [0.2, 0.4]])))
+    assert st.any_movable and st.ob_state.shape == (E, 24)
+    ob = st.ob_state.double().reshape(E, 2, 2, 6)  # [env, shapes | bodies, index, 6]
+    assert torch.allclose(ob[:, 0, :, 0:2], pos.double()) and torch.allclose(ob[:, 0, :, 3:5], vel.double())
+    c, s_ = math.cos(0.5), math.sin(0.5)
+    origin = (1.0 - (c * 0.2 - s_ * -0.1), 2.0 - (s_ * 0.2 + c * -0.1))
+    for idx in (0, 1):  # every index carries the state of its body (rooted at 0)
+        assert torch.allclose(ob[0, 1, idx, 0:3], torch.tensor([*origin, 0.5], dtype=torch.float64))
+        assert torch.allclose(ob[0, 1, idx, 3:5], torch.tensor([0.1, 0.2], dtype=torch.float64))
+    with pytest.raises(NotImplementedError, match="circle"):
         st.set_obstacles(Obstacles(pos=torch.zeros(1, 1, 2), radius=torch.ones(1),
+                                   shape=torch.ones(1, dtype=torch.int32),
                                    kind=torch.ones(1, dtype=torch.int32)))
+    with pytest.raises(NotImplementedError, match="DRONE"):
+        Stepper([drone_config()], device="cpu").set_obstacles(
+            Obstacles(pos=torch.zeros(1, 1, 2), radius=torch.ones(1),
+                      kind=torch.ones(1, dtype=torch.int32)))
 
 
 def test_step_refuses_cpu_tensors():
