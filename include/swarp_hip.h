@@ -23,10 +23,14 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 3
+#define SWARP_ABI_VERSION 4
 
 #define SWARP_F32 0
 #define SWARP_F64 1
+
+/* desc->integrator (the reference's Integrator, swarp/dynamics/base.py:97-101) */
+#define SWARP_EULER 0
+#define SWARP_RK4 1
 
 /* Everything the step needs besides the state and the actions.
  * Counterpart of the Stepper's configuration (swarp/core/stepper.py:87-137) plus
@@ -61,6 +65,9 @@ typedef struct swarp_desc {
     const int32_t *obs_kind, *obs_body;
     const void *obs_mass, *obs_inertia, *obs_body_off;
     double lin_damping, ang_damping;
+    /* SWARP_EULER: semi-implicit Euler (_integrate_agent, swarp/dynamics/kernels.py:278-413);
+       SWARP_RK4: classic RK4 on each substep (_integrate_rk4, :520-793), every model */
+    int32_t integrator;
 } swarp_desc_t;
 
 /* The nine state fields.  A NULL field means "not provided": an input adjoint that

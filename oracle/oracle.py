@@ -36,6 +36,7 @@ class OracleCfg(ctypes.Structure):
         ("bmin_x", ctypes.c_double), ("bmin_y", ctypes.c_double),
         ("bmax_x", ctypes.c_double), ("bmax_y", ctypes.c_double),
         ("lin_damping", ctypes.c_double), ("ang_damping", ctypes.c_double),
+        ("rk4", ctypes.c_int),
     ]
 
 

@@ -48,6 +48,7 @@ typedef struct {
     const REAL *o_mass, *o_inertia, *o_off;
     REAL lin_damping, ang_damping;
     int any_movable;
+    int rk4;  /* Integrator.RK4 for the 2-D models */
 } FN(ctx_t);
 
 /* Per-env obstacle state, 12 reals per obstacle index o:
@@ -617,14 +618,405 @@ static void FN(forces_env_adj)(const FN(ctx_t) *C, const REAL *od, const FN(prm_
 
 /* ---------------------------------------------------------------- integration */
 
+/* ------------------------------------------------------------------------- RK4 */
+
+/* The 16 agent fields a - b * h, componentwise: o = x + k * h */
+static void FN(ag_axpy)(const FN(agent_t) *x, const FN(agent_t) *k, REAL h, FN(agent_t) *o)
+{
+    o->px = x->px + k->px * h; o->py = x->py + k->py * h; o->th = x->th + k->th * h;
+    o->vx = x->vx + k->vx * h; o->vy = x->vy + k->vy * h;
+    o->s = x->s + k->s * h; o->w = x->w + k->w * h;
+    o->z = x->z + k->z * h; o->vz = x->vz + k->vz * h;
+    o->qx = x->qx + k->qx * h; o->qy = x->qy + k->qy * h;
+    o->qz = x->qz + k->qz * h; o->qw = x->qw + k->qw * h;
+    o->bx = x->bx + k->bx * h; o->by = x->by + k->by * h; o->bz = x->bz + k->bz * h;
+}
+
+/* _deriv (swarp/dynamics/kernels.py:416-517): the state derivative with the actions held
+   constant.  Holonomic integrates (pos, vel), diff-drive (pos, theta, speed, ang_vel),
+   the bicycle (pos, theta, speed), the drone (pos, vel, z, vz, attitude, body_rates,
+   with _drone_rates :129-163 and _quat_deriv :117-126); every other field has rate 0. */
+static void FN(rk_deriv)(const FN(prm_t) *P, const FN(agent_t) *x, const REAL *a,
+                         FN(agent_t) *k)
+{
+    memset(k, 0, sizeof *k);
+    if (P->tag == 0) {
+        k->px = x->vx;
+        k->py = x->vy;
+        if (P->mode != 0) FN(clamp_norm)(a[0], a[1], P->max_accel, &k->vx, &k->vy);
+    } else if (P->tag == 1) {
+        k->px = x->s * COS(x->th);
+        k->py = x->s * SIN(x->th);
+        k->th = x->w;
+        if (P->mode != 0) {
+            k->s = FN(rclamp)(a[0], -P->max_accel, P->max_accel);
+            k->w = FN(rclamp)(a[1], -P->max_ang_accel, P->max_ang_accel);
+        }
+    } else if (P->tag == 2) {
+        REAL wb = P->l_f + P->l_r;
+        REAL del = FN(rclamp)(a[1], -P->max_steer, P->max_steer);
+        REAL beta = ATAN(TAN(del) * P->l_r / wb);
+        k->px = x->s * COS(x->th + beta);
+        k->py = x->s * SIN(x->th + beta);
+        k->th = x->s / wb * COS(beta) * TAN(del);
+        k->s = FN(rclamp)(a[0], -P->max_accel, P->max_accel);
+    } else if (P->tag == 3) {
+        REAL zero = 0, half = (REAL)0.5;
+        REAL f0 = FN(rclamp)(a[0], zero, P->thrust_max), f1 = FN(rclamp)(a[1], zero, P->thrust_max);
+        REAL f2 = FN(rclamp)(a[2], zero, P->thrust_max), f3 = FN(rclamp)(a[3], zero, P->thrust_max);
+        REAL thr = f0 + f1 + f2 + f3;
+        REAL qx = x->qx, qy = x->qy, qz = x->qz, qw = x->qw;
+        REAL vx3 = 0, vy3 = 0, vz3 = thr;
+        REAL c1x = qy * vz3 - qz * vy3, c1y = qz * vx3 - qx * vz3, c1z = qx * vy3 - qy * vx3;
+        REAL tx = (REAL)2 * c1x, ty = (REAL)2 * c1y, tz = (REAL)2 * c1z;
+        REAL c2x = qy * tz - qz * ty, c2y = qz * tx - qx * tz, c2z = qx * ty - qy * tx;
+        REAL fwx = vx3 + qw * tx + c2x, fwy = vy3 + qw * ty + c2y, fwz = vz3 + qw * tz + c2z;
+        REAL bx = x->bx, by = x->by, bz = x->bz;
+        k->px = x->vx;
+        k->py = x->vy;
+        k->vx = fwx / P->mass - zero;
+        k->vy = fwy / P->mass - zero;
+        k->vz = fwz / P->mass - P->gravity;
+        k->z = x->vz;
+        k->bx = (P->arm * (f1 - f3) - (P->izz - P->iyy) * by * bz) / P->ixx;
+        k->by = (P->arm * (f2 - f0) - (P->ixx - P->izz) * bz * bx) / P->iyy;
+        k->bz = (P->kappa * (f0 - f1 + f2 - f3) - (P->iyy - P->ixx) * bx * by) / P->izz;
+        k->qx = half * (qw * bx + qy * bz - qz * by);
+        k->qy = half * (qw * by - qx * bz + qz * bx);
+        k->qz = half * (qw * bz + qx * by - qy * bx);
+        k->qw = half * (-qx * bx - qy * by - qz * bz);
+    }
+}
+
+/* Reverse of rk_deriv: gk = adjoint of k; accumulates into gx and ga[0..3]. */
+static void FN(rk_deriv_adj)(const FN(prm_t) *P, const FN(agent_t) *x, const REAL *a,
+                             const FN(agent_t) *gk, FN(agent_t) *gx, REAL *ga)
+{
+    if (P->tag == 0) {
+        gx->vx += gk->px;
+        gx->vy += gk->py;
+        if (P->mode != 0) FN(clamp_norm_adj)(a[0], a[1], P->max_accel, gk->vx, gk->vy, &ga[0], &ga[1]);
+    } else if (P->tag == 1) {
+        REAL c = COS(x->th), sn = SIN(x->th);
+        gx->s += gk->px * c + gk->py * sn;
+        gx->th += -gk->px * x->s * sn + gk->py * x->s * c;
+        gx->w += gk->th;
+        if (P->mode != 0) {
+            ga[0] += FN(rclamp_gx)(a[0], -P->max_accel, P->max_accel, gk->s);
+            ga[1] += FN(rclamp_gx)(a[1], -P->max_ang_accel, P->max_ang_accel, gk->w);
+        }
+    } else if (P->tag == 2) {
+        REAL wb = P->l_f + P->l_r;
+        REAL del = FN(rclamp)(a[1], -P->max_steer, P->max_steer);
+        REAL td = TAN(del);
+        REAL u = td * P->l_r / wb;
+        REAL beta = ATAN(u);
+        REAL cb = COS(beta), sb = SIN(beta);
+        REAL c = COS(x->th + beta), sn = SIN(x->th + beta);
+        gx->s += gk->px * c + gk->py * sn + gk->th * (cb * td / wb);
+        REAL gang = -gk->px * x->s * sn + gk->py * x->s * c;   /* d / d(th + beta) */
+        gx->th += gang;
+        REAL gbeta = gang + gk->th * (x->s / wb * (-sb) * td);
+        REAL gdel = gk->th * (x->s / wb * cb * ((REAL)1 + td * td))
+                    + gbeta / ((REAL)1 + u * u) * ((REAL)1 + td * td) * P->l_r / wb;
+        ga[1] += FN(rclamp_gx)(a[1], -P->max_steer, P->max_steer, gdel);
+        ga[0] += FN(rclamp_gx)(a[0], -P->max_accel, P->max_accel, gk->s);
+    } else if (P->tag == 3) {
+        REAL zero = 0, half = (REAL)0.5;
+        REAL f0 = FN(rclamp)(a[0], zero, P->thrust_max), f1 = FN(rclamp)(a[1], zero, P->thrust_max);
+        REAL f2 = FN(rclamp)(a[2], zero, P->thrust_max), f3 = FN(rclamp)(a[3], zero, P->thrust_max);
+        REAL thr = f0 + f1 + f2 + f3;
+        REAL qx = x->qx, qy = x->qy, qz = x->qz, qw = x->qw;
+        REAL bx = x->bx, by = x->by, bz = x->bz;
+        REAL vx3 = 0, vy3 = 0, vz3 = thr;
+        REAL tx = (REAL)2 * (qy * vz3 - qz * vy3), ty = (REAL)2 * (qz * vx3 - qx * vz3);
+        REAL tz = (REAL)2 * (qx * vy3 - qy * vx3);
+        gx->vx += gk->px;
+        gx->vy += gk->py;
+        gx->vz += gk->z;
+        /* fw = v3 + qw t + u x t ; acc = fw / m */
+        REAL gfx = gk->vx / P->mass, gfy = gk->vy / P->mass, gfz = gk->vz / P->mass;
+        REAL gqx = 0, gqy = 0, gqz = 0, gqw = 0;
+        gqw += gfx * tx + gfy * ty + gfz * tz;
+        REAL gtx = qw * gfx + (gfy * qz - gfz * qy);
+        REAL gty = qw * gfy + (gfz * qx - gfx * qz);
+        REAL gtz = qw * gfz + (gfx * qy - gfy * qx);
+        gqx += ty * gfz - tz * gfy;
+        gqy += tz * gfx - tx * gfz;
+        gqz += tx * gfy - ty * gfx;
+        /* t = 2 (u x v3) */
+        REAL g1x = (REAL)2 * gtx, g1y = (REAL)2 * gty, g1z = (REAL)2 * gtz;
+        gqx += vy3 * g1z - vz3 * g1y;
+        gqy += vz3 * g1x - vx3 * g1z;
+        gqz += vx3 * g1y - vy3 * g1x;
+        REAL gthr = gfz + (g1x * qy - g1y * qx);
+        /* body-rate derivative (Euler's equation) */
+        REAL gax = gk->bx / P->ixx, gay = gk->by / P->iyy, gaz = gk->bz / P->izz;
+        REAL gbx = 0, gby = 0, gbz = 0;
+        gby -= (P->izz - P->iyy) * bz * gax;
+        gbz -= (P->izz - P->iyy) * by * gax;
+        gbz -= (P->ixx - P->izz) * bx * gay;
+        gbx -= (P->ixx - P->izz) * bz * gay;
+        gbx -= (P->iyy - P->ixx) * by * gaz;
+        gby -= (P->iyy - P->ixx) * bx * gaz;
+        REAL gf0 = gthr - P->arm * gay + P->kappa * gaz;
+        REAL gf1 = gthr + P->arm * gax - P->kappa * gaz;
+        REAL gf2 = gthr + P->arm * gay + P->kappa * gaz;
+        REAL gf3 = gthr - P->arm * gax - P->kappa * gaz;
+        /* quaternion derivative 0.5 q (x) (b, 0) */
+        REAL Dx = half * gk->qx, Dy = half * gk->qy, Dz = half * gk->qz, Dw = half * gk->qw;
+        gqw += Dx * bx + Dy * by + Dz * bz;
+        gqx += -Dy * bz + Dz * by - Dw * bx;
+        gqy += Dx * bz - Dz * bx - Dw * by;
+        gqz += -Dx * by + Dy * bx - Dw * bz;
+        gbx += Dx * qw + Dy * qz - Dz * qy - Dw * qx;
+        gby += -Dx * qz + Dy * qw + Dz * qx - Dw * qy;
+        gbz += Dx * qy - Dy * qx + Dz * qw - Dw * qz;
+        gx->qx += gqx; gx->qy += gqy; gx->qz += gqz; gx->qw += gqw;
+        gx->bx += gbx; gx->by += gby; gx->bz += gbz;
+        ga[0] += FN(rclamp_gx)(a[0], zero, P->thrust_max, gf0);
+        ga[1] += FN(rclamp_gx)(a[1], zero, P->thrust_max, gf1);
+        ga[2] += FN(rclamp_gx)(a[2], zero, P->thrust_max, gf2);
+        ga[3] += FN(rclamp_gx)(a[3], zero, P->thrust_max, gf3);
+    }
+}
+
+/* The RK4 stage states (x1 = the start), their derivatives and the combine
+   x + (k1 + 2 k2 + 2 k3 + k4) dt / 6 (swarp/dynamics/kernels.py:584-738). */
+typedef struct {
+    FN(agent_t) x1, x2, x3, x4, k1, k2, k3, k4, xi;
+} FN(rk_t);
+
+static void FN(rk_stages)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *in,
+                          const REAL *a, FN(rk_t) *R)
+{
+    REAL dt = C->sub_dt, half = (REAL)0.5, two = (REAL)2;
+    REAL dt2 = dt * half, sixth = dt / (REAL)6;
+    FN(agent_t) x = *in;
+    /* velocity control sets the velocity-level state from the command (:588-595) */
+    if (P->mode == 0) {
+        if (P->tag == 0) {
+            FN(clamp_norm)(a[0], a[1], P->max_speed, &x.vx, &x.vy);
+        } else if (P->tag == 1) {
+            x.s = FN(rclamp)(a[0], -P->max_speed, P->max_speed);
+            x.w = FN(rclamp)(a[1], -P->max_ang_vel, P->max_ang_vel);
+        }
+    }
+    R->x1 = x;
+    FN(rk_deriv)(P, &R->x1, a, &R->k1);
+    FN(ag_axpy)(&x, &R->k1, dt2, &R->x2);
+    FN(rk_deriv)(P, &R->x2, a, &R->k2);
+    FN(ag_axpy)(&x, &R->k2, dt2, &R->x3);
+    FN(rk_deriv)(P, &R->x3, a, &R->k3);
+    FN(ag_axpy)(&x, &R->k3, dt, &R->x4);
+    FN(rk_deriv)(P, &R->x4, a, &R->k4);
+#define RK_COMB(f) R->xi.f = x.f + (R->k1.f + R->k2.f * two + R->k3.f * two + R->k4.f) * sixth
+    RK_COMB(px); RK_COMB(py); RK_COMB(th); RK_COMB(vx); RK_COMB(vy); RK_COMB(s); RK_COMB(w);
+    RK_COMB(z); RK_COMB(vz); RK_COMB(qx); RK_COMB(qy); RK_COMB(qz); RK_COMB(qw);
+    RK_COMB(bx); RK_COMB(by); RK_COMB(bz);
+#undef RK_COMB
+}
+
+/* _integrate_rk4 (swarp/dynamics/kernels.py:520-793): limits on the combined result,
+   the contact force as dv = F * (dt / m) after the combine, the attitude renormalised. */
+static void FN(rk4_agent)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *in,
+                          const REAL *a, REAL Fx, REAL Fy, FN(agent_t) *out)
+{
+    REAL dt = C->sub_dt;
+    FN(rk_t) R;
+    FN(rk_stages)(C, P, in, a, &R);
+    REAL dfx = Fx * (dt / P->mass), dfy = Fy * (dt / P->mass);
+    *out = *in;
+    REAL pnx = R.xi.px + dfx * dt, pny = R.xi.py + dfy * dt;
+    if (P->tag == 0) {
+        REAL vx, vy;
+        FN(clamp_norm)(R.xi.vx, R.xi.vy, P->max_speed, &vx, &vy);
+        vx = vx + dfx;
+        vy = vy + dfy;
+        out->vx = vx; out->vy = vy;
+        out->s = SQRT(vx * vx + vy * vy);
+        out->w = 0;
+    } else if (P->tag == 1) {
+        REAL so = FN(rclamp)(R.xi.s, -P->max_speed, P->max_speed);
+        REAL th = R.xi.th;
+        out->th = th;
+        out->vx = so * COS(th) + dfx;
+        out->vy = so * SIN(th) + dfy;
+        out->s = so;
+        out->w = FN(rclamp)(R.xi.w, -P->max_ang_vel, P->max_ang_vel);
+    } else if (P->tag == 2) {
+        REAL so = FN(rclamp)(R.xi.s, P->min_speed, P->max_speed);
+        REAL th = R.xi.th;
+        REAL del = FN(rclamp)(a[1], -P->max_steer, P->max_steer);
+        REAL wb = P->l_f + P->l_r;
+        REAL beta = ATAN(TAN(del) * P->l_r / wb);
+        out->w = so / wb * COS(beta) * TAN(del);
+        out->th = th;
+        out->vx = so * COS(th + beta) + dfx;
+        out->vy = so * SIN(th + beta) + dfy;
+        out->s = so;
+    } else if (P->tag == 3) {
+        out->vx = R.xi.vx + dfx;
+        out->vy = R.xi.vy + dfy;
+        out->z = R.xi.z;
+        out->vz = R.xi.vz;
+        REAL l = SQRT(R.xi.qx * R.xi.qx + R.xi.qy * R.xi.qy + R.xi.qz * R.xi.qz + R.xi.qw * R.xi.qw);
+        if (l > (REAL)0) {
+            out->qx = R.xi.qx / l; out->qy = R.xi.qy / l; out->qz = R.xi.qz / l; out->qw = R.xi.qw / l;
+        } else {
+            out->qx = 0; out->qy = 0; out->qz = 0; out->qw = 1;
+        }
+        out->bx = R.xi.bx; out->by = R.xi.by; out->bz = R.xi.bz;
+    } else {
+        return; /* unknown tag: the state passes through */
+    }
+    if (C->clamp_bounds) {
+        REAL r = P->radius;
+        pnx = FN(rclamp)(pnx, C->bmin_x + r, C->bmax_x - r);
+        pny = FN(rclamp)(pny, C->bmin_y + r, C->bmax_y - r);
+    }
+    out->px = pnx;
+    out->py = pny;
+}
+
+/* Reverse of rk4_agent: g = adjoint of *out; accumulates into gin, gact[0..3], gF. */
+static void FN(rk4_agent_adj)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *in,
+                              const REAL *a, REAL Fx, REAL Fy, const FN(agent_t) *g,
+                              FN(agent_t) *gin, REAL *gact, REAL *gFx, REAL *gFy)
+{
+    REAL dt = C->sub_dt, half = (REAL)0.5, two = (REAL)2;
+    REAL dt2 = dt * half, sixth = dt / (REAL)6;
+    if (P->tag > 3) {
+        FN(ag_axpy)(gin, g, (REAL)1, gin);
+        return;
+    }
+    FN(rk_t) R;
+    FN(rk_stages)(C, P, in, a, &R);
+    REAL dfx = Fx * (dt / P->mass), dfy = Fy * (dt / P->mass);
+    REAL gpx = g->px, gpy = g->py;
+    if (C->clamp_bounds) {
+        REAL r = P->radius;
+        gpx = FN(rclamp_gx)(R.xi.px + dfx * dt, C->bmin_x + r, C->bmax_x - r, gpx);
+        gpy = FN(rclamp_gx)(R.xi.py + dfy * dt, C->bmin_y + r, C->bmax_y - r, gpy);
+    }
+    FN(agent_t) gxi;
+    memset(&gxi, 0, sizeof gxi);
+    gxi.px = gpx;
+    gxi.py = gpy;
+    REAL gdfx = gpx * dt + g->vx, gdfy = gpy * dt + g->vy;
+    if (P->tag == 0) {
+        REAL vx, vy;
+        FN(clamp_norm)(R.xi.vx, R.xi.vy, P->max_speed, &vx, &vy);
+        vx = vx + dfx;
+        vy = vy + dfy;
+        REAL gvx = g->vx, gvy = g->vy;
+        REAL sp = SQRT(vx * vx + vy * vy);
+        if (sp > (REAL)0) {
+            gvx += g->s * vx / sp;
+            gvy += g->s * vy / sp;
+            gdfx += g->s * vx / sp;
+            gdfy += g->s * vy / sp;
+        }
+        FN(clamp_norm_adj)(R.xi.vx, R.xi.vy, P->max_speed, gvx, gvy, &gxi.vx, &gxi.vy);
+        gin->th += g->th;
+    } else if (P->tag == 1) {
+        REAL so = FN(rclamp)(R.xi.s, -P->max_speed, P->max_speed);
+        REAL th = R.xi.th, c = COS(th), sn = SIN(th);
+        REAL gso = g->s + g->vx * c + g->vy * sn;
+        gxi.th = g->th - g->vx * so * sn + g->vy * so * c;
+        gxi.s = FN(rclamp_gx)(R.xi.s, -P->max_speed, P->max_speed, gso);
+        gxi.w = FN(rclamp_gx)(R.xi.w, -P->max_ang_vel, P->max_ang_vel, g->w);
+    } else if (P->tag == 2) {
+        REAL so = FN(rclamp)(R.xi.s, P->min_speed, P->max_speed);
+        REAL th = R.xi.th;
+        REAL del = FN(rclamp)(a[1], -P->max_steer, P->max_steer);
+        REAL wb = P->l_f + P->l_r;
+        REAL td = TAN(del), u = td * P->l_r / wb;
+        REAL beta = ATAN(u), cb = COS(beta), sb = SIN(beta);
+        REAL c = COS(th + beta), sn = SIN(th + beta);
+        REAL gso = g->s + g->w * (cb * td / wb) + g->vx * c + g->vy * sn;
+        REAL gang = -g->vx * so * sn + g->vy * so * c;
+        gxi.th = g->th + gang;
+        REAL gbeta = gang + g->w * (so / wb * (-sb) * td);
+        REAL gdel = g->w * (so / wb * cb * ((REAL)1 + td * td))
+                    + gbeta / ((REAL)1 + u * u) * ((REAL)1 + td * td) * P->l_r / wb;
+        gact[1] += FN(rclamp_gx)(a[1], -P->max_steer, P->max_steer, gdel);
+        gxi.s = FN(rclamp_gx)(R.xi.s, P->min_speed, P->max_speed, gso);
+    } else {
+        gxi.vx = g->vx;
+        gxi.vy = g->vy;
+        gxi.z = g->z;
+        gxi.vz = g->vz;
+        gxi.bx = g->bx; gxi.by = g->by; gxi.bz = g->bz;
+        REAL l = SQRT(R.xi.qx * R.xi.qx + R.xi.qy * R.xi.qy + R.xi.qz * R.xi.qz + R.xi.qw * R.xi.qw);
+        if (l > (REAL)0) {
+            REAL nx = R.xi.qx / l, ny = R.xi.qy / l, nz = R.xi.qz / l, nw = R.xi.qw / l;
+            REAL dq = g->qx * nx + g->qy * ny + g->qz * nz + g->qw * nw;
+            gxi.qx = (g->qx - nx * dq) / l;
+            gxi.qy = (g->qy - ny * dq) / l;
+            gxi.qz = (g->qz - nz * dq) / l;
+            gxi.qw = (g->qw - nw * dq) / l;
+        }
+        gin->th += g->th;
+        gin->s += g->s;
+        gin->w += g->w;
+    }
+    *gFx += gdfx * (dt / P->mass);
+    *gFy += gdfy * (dt / P->mass);
+    /* the combine and the stages, in reverse */
+    FN(agent_t) gx = gxi, gk1, gk2, gk3, gk4, gs;
+    memset(&gk1, 0, sizeof gk1);
+    FN(ag_axpy)(&gk1, &gxi, sixth, &gk1);
+    memset(&gk2, 0, sizeof gk2);
+    FN(ag_axpy)(&gk2, &gxi, two * sixth, &gk2);
+    gk3 = gk2;
+    gk4 = gk1;
+    memset(&gs, 0, sizeof gs);
+    FN(rk_deriv_adj)(P, &R.x4, a, &gk4, &gs, gact);
+    FN(ag_axpy)(&gx, &gs, (REAL)1, &gx);
+    FN(ag_axpy)(&gk3, &gs, dt, &gk3);
+    memset(&gs, 0, sizeof gs);
+    FN(rk_deriv_adj)(P, &R.x3, a, &gk3, &gs, gact);
+    FN(ag_axpy)(&gx, &gs, (REAL)1, &gx);
+    FN(ag_axpy)(&gk2, &gs, dt2, &gk2);
+    memset(&gs, 0, sizeof gs);
+    FN(rk_deriv_adj)(P, &R.x2, a, &gk2, &gs, gact);
+    FN(ag_axpy)(&gx, &gs, (REAL)1, &gx);
+    FN(ag_axpy)(&gk1, &gs, dt2, &gk1);
+    memset(&gs, 0, sizeof gs);
+    FN(rk_deriv_adj)(P, &R.x1, a, &gk1, &gs, gact);
+    FN(ag_axpy)(&gx, &gs, (REAL)1, &gx);
+    /* velocity control: the commanded velocity-level state replaces the input's */
+    if (P->mode == 0 && P->tag == 0) {
+        FN(clamp_norm_adj)(a[0], a[1], P->max_speed, gx.vx, gx.vy, &gact[0], &gact[1]);
+        gx.vx = gx.vy = 0;
+    } else if (P->mode == 0 && P->tag == 1) {
+        gact[0] += FN(rclamp_gx)(a[0], -P->max_speed, P->max_speed, gx.s);
+        gact[1] += FN(rclamp_gx)(a[1], -P->max_ang_vel, P->max_ang_vel, gx.w);
+        gx.s = gx.w = 0;
+    }
+    /* fields no model integrates pass their adjoint through */
+    if (P->tag != 3) {
+        gx.z += g->z; gx.vz += g->vz;
+        gx.qx += g->qx; gx.qy += g->qy; gx.qz += g->qz; gx.qw += g->qw;
+        gx.bx += g->bx; gx.by += g->by; gx.bz += g->bz;
+    }
+    FN(ag_axpy)(gin, &gx, (REAL)1, gin);
+}
+
 /* _integrate_agent + _step_2d (swarp/dynamics/kernels.py:194-413), Euler */
 static void FN(integrate_agent)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *in,
                                 const REAL *act, REAL Fx, REAL Fy, FN(agent_t) *out)
 {
     REAL dt = C->sub_dt;
-    REAL a0 = act[0], a1 = act[1];
+    REAL a0 = act[0], a1 = C->act_dim > 1 ? act[1] : (REAL)0;
     REAL a2 = C->act_dim > 2 ? act[2] : (REAL)0;
     REAL a3 = C->act_dim > 3 ? act[3] : (REAL)0;
+    if (C->rk4) {
+        REAL a[4] = {a0, a1, a2, a3};
+        FN(rk4_agent)(C, P, in, a, Fx, Fy, out);
+        return;
+    }
     *out = *in; /* drone fields (and unknown tags) pass through */
     REAL pnx, pny;
     if (P->tag == 3) {
@@ -747,9 +1139,15 @@ static void FN(integrate_agent_adj)(const FN(ctx_t) *C, const FN(prm_t) *P,
                                     REAL *gFx, REAL *gFy)
 {
     REAL dt = C->sub_dt;
-    REAL a0 = act[0], a1 = act[1];
+    REAL a0 = act[0], a1 = C->act_dim > 1 ? act[1] : (REAL)0;
     REAL a2 = C->act_dim > 2 ? act[2] : (REAL)0;
     REAL a3 = C->act_dim > 3 ? act[3] : (REAL)0;
+    if (C->rk4) {
+        REAL a[4] = {a0, a1, a2, a3}, ga[4] = {0, 0, 0, 0};
+        FN(rk4_agent_adj)(C, P, in, a, Fx, Fy, g, gin, ga, gFx, gFy);
+        for (int j = 0; j < C->act_dim && j < 4; ++j) gact[j] += ga[j];
+        return;
+    }
     FN(agent_t) fwd;
     FN(integrate_agent)(C, P, in, act, Fx, Fy, &fwd);
     /* position clamp: recompute the unclamped position */
@@ -1352,6 +1750,7 @@ static void FN(make_ctx)(const oracle_cfg_t *cfg, const oracle_obs_t *obs, FN(ct
     C->clamp_bounds = cfg->clamp_bounds;
     C->lin_damping = (REAL)cfg->lin_damping;
     C->ang_damping = (REAL)cfg->ang_damping;
+    C->rk4 = cfg->rk4;
     C->n_obs = obs ? obs->n_obstacles : 0;
     C->needs_forces = C->collisions || C->soft_walls || C->n_obs > 0;
     if (C->n_obs > 0) {

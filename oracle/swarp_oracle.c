@@ -8,7 +8,8 @@
  * Restates, from the reference's source text:
  *   neighbours     swarp/core/neighbors.py:76-97 (_brute_force)
  *   contact forces swarp/core/collisions.py:48-260, 690-881
- *   integration    swarp/dynamics/kernels.py:68-413 (Euler, all four models)
+ *   integration    swarp/dynamics/kernels.py:68-413 (Euler, all four models),
+                  :416-793 (RK4, the three 2-D models)
  *   step ordering  swarp/core/stepper.py:784-1011 (taped path)
  * and the reverse mode warp-lang generates for them (swarp/interop/autograd.py:277-296).
  *
@@ -25,6 +26,7 @@ typedef struct {
     double dt, k, c, margin, max_overlap, neighbor_radius;
     double bmin_x, bmin_y, bmax_x, bmax_y;
     double lin_damping, ang_damping; /* movable bodies' viscous decay rates */
+    int rk4;                         /* Integrator.RK4 (2-D models) instead of Euler */
 } oracle_cfg_t;
 
 typedef struct {

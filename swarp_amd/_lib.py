@@ -11,8 +11,9 @@ import ctypes
 import os
 from pathlib import Path
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 F32, F64 = 0, 1
+EULER, RK4 = 0, 1
 
 _PKG = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("SWARP_HIP_LIB", _PKG / "libswarp_hip.so"))
@@ -60,6 +61,7 @@ class SwarpDesc(ctypes.Structure):
         ("obs_body_off", ctypes.c_void_p),
         ("lin_damping", ctypes.c_double),
         ("ang_damping", ctypes.c_double),
+        ("integrator", ctypes.c_int32),
     ]
 
 

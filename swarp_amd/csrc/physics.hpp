@@ -68,6 +68,7 @@ template <typename T> struct Cst {
     int E, A, ad, S, K, N;
     int collisions, soft_walls, clamp, needs_forces, use_skin;
     int fast_div;  // neighbour radius <= 2^20: contact distances are short-division divisors
+    int rk4;       // Integrator.RK4 instead of semi-implicit Euler
 };
 
 // Obstacle arrays (device); shared extents [N], per-env poses [E,N].
@@ -741,12 +742,408 @@ __device__ __forceinline__ void clamp_norm_adj_rcp(T x, T y, T lim, T gx, T gy, 
     }
 }
 
+// ------------------------------------------------------------------------------ RK4
+
+// o = x + k * h over the 16 state fields.
+template <typename T>
+__device__ __forceinline__ void st_axpy(const St<T> &x, const St<T> &k, T h, St<T> &o)
+{
+    o.px = x.px + k.px * h; o.py = x.py + k.py * h; o.th = x.th + k.th * h;
+    o.vx = x.vx + k.vx * h; o.vy = x.vy + k.vy * h; o.s = x.s + k.s * h; o.w = x.w + k.w * h;
+    o.z = x.z + k.z * h; o.vz = x.vz + k.vz * h;
+    o.qx = x.qx + k.qx * h; o.qy = x.qy + k.qy * h; o.qz = x.qz + k.qz * h; o.qw = x.qw + k.qw * h;
+    o.bx = x.bx + k.bx * h; o.by = x.by + k.by * h; o.bz = x.bz + k.bz * h;
+}
+
+// _deriv (swarp/dynamics/kernels.py:416-517): the state derivative with the actions held
+// constant.  Holonomic integrates (pos, vel), diff-drive (pos, theta, speed, ang_vel), the
+// bicycle (pos, theta, speed), the drone (pos, vel, z, vz, attitude, body_rates; _drone_rates
+// :129-163, _quat_deriv :117-126); every other field has rate 0.
+template <typename T, bool DRONE>
+__device__ __forceinline__ void rk_deriv(const Prm<T> &P, const St<T> &x, const T (&a)[4], St<T> &k)
+{
+    st_zero(k);
+    if (DRONE && P.tag == 3) {
+        const T z0 = T(0), h = T(0.5);
+        T f0 = wclamp(a[0], z0, P.thrust_max), f1 = wclamp(a[1], z0, P.thrust_max);
+        T f2 = wclamp(a[2], z0, P.thrust_max), f3 = wclamp(a[3], z0, P.thrust_max);
+        T thr = f0 + f1 + f2 + f3;
+        T vx3 = T(0), vy3 = T(0), vz3 = thr;
+        T c1x = x.qy * vz3 - x.qz * vy3, c1y = x.qz * vx3 - x.qx * vz3, c1z = x.qx * vy3 - x.qy * vx3;
+        T tx = T(2) * c1x, ty = T(2) * c1y, tz = T(2) * c1z;
+        T c2x = x.qy * tz - x.qz * ty, c2y = x.qz * tx - x.qx * tz, c2z = x.qx * ty - x.qy * tx;
+        T fwx = vx3 + x.qw * tx + c2x, fwy = vy3 + x.qw * ty + c2y, fwz = vz3 + x.qw * tz + c2z;
+        k.px = x.vx;
+        k.py = x.vy;
+        k.vx = fwx / P.mass - z0;
+        k.vy = fwy / P.mass - z0;
+        k.vz = fwz / P.mass - P.gravity;
+        k.z = x.vz;
+        k.bx = (P.arm * (f1 - f3) - (P.izz - P.iyy) * x.by * x.bz) / P.ixx;
+        k.by = (P.arm * (f2 - f0) - (P.ixx - P.izz) * x.bz * x.bx) / P.iyy;
+        k.bz = (P.kappa * (f0 - f1 + f2 - f3) - (P.iyy - P.ixx) * x.bx * x.by) / P.izz;
+        k.qx = h * (x.qw * x.bx + x.qy * x.bz - x.qz * x.by);
+        k.qy = h * (x.qw * x.by - x.qx * x.bz + x.qz * x.bx);
+        k.qz = h * (x.qw * x.bz + x.qx * x.by - x.qy * x.bx);
+        k.qw = h * (-x.qx * x.bx - x.qy * x.by - x.qz * x.bz);
+    } else if (P.tag == 0) {
+        k.px = x.vx;
+        k.py = x.vy;
+        if (P.mode != 0) clamp_norm(a[0], a[1], P.max_accel, k.vx, k.vy);
+    } else if (P.tag == 1) {
+        k.px = x.s * m_cos(x.th);
+        k.py = x.s * m_sin(x.th);
+        k.th = x.w;
+        if (P.mode != 0) {
+            k.s = wclamp(a[0], -P.max_accel, P.max_accel);
+            k.w = wclamp(a[1], -P.max_ang_accel, P.max_ang_accel);
+        }
+    } else if (P.tag == 2) {
+        T wb = P.l_f + P.l_r;
+        T del = wclamp(a[1], -P.max_steer, P.max_steer);
+        T beta = m_atan(m_tan(del) * P.l_r / wb);
+        k.px = x.s * m_cos(x.th + beta);
+        k.py = x.s * m_sin(x.th + beta);
+        k.th = x.s / wb * m_cos(beta) * m_tan(del);
+        k.s = wclamp(a[0], -P.max_accel, P.max_accel);
+    }
+}
+
+// Reverse of rk_deriv: gk = adjoint of k; accumulates into gx and ga.
+template <typename T, bool DRONE>
+__device__ __forceinline__ void rk_deriv_adj(const Prm<T> &P, const St<T> &x, const T (&a)[4],
+                                             const St<T> &gk, St<T> &gx, T (&ga)[4])
+{
+    if (DRONE && P.tag == 3) {
+        const T z0 = T(0), h = T(0.5);
+        T f0 = wclamp(a[0], z0, P.thrust_max), f1 = wclamp(a[1], z0, P.thrust_max);
+        T f2 = wclamp(a[2], z0, P.thrust_max), f3 = wclamp(a[3], z0, P.thrust_max);
+        T thr = f0 + f1 + f2 + f3;
+        T qx = x.qx, qy = x.qy, qz = x.qz, qw = x.qw, bx = x.bx, by = x.by, bz = x.bz;
+        T vx3 = T(0), vy3 = T(0), vz3 = thr;
+        T tx = T(2) * (qy * vz3 - qz * vy3), ty = T(2) * (qz * vx3 - qx * vz3);
+        T tz = T(2) * (qx * vy3 - qy * vx3);
+        gx.vx += gk.px;
+        gx.vy += gk.py;
+        gx.vz += gk.z;
+        // fw = v3 + qw t + u x t ; acc = fw / m
+        T gfx = gk.vx / P.mass, gfy = gk.vy / P.mass, gfz = gk.vz / P.mass;
+        T gqx = T(0), gqy = T(0), gqz = T(0), gqw = T(0);
+        gqw += gfx * tx + gfy * ty + gfz * tz;
+        T gtx = qw * gfx + (gfy * qz - gfz * qy);
+        T gty = qw * gfy + (gfz * qx - gfx * qz);
+        T gtz = qw * gfz + (gfx * qy - gfy * qx);
+        gqx += ty * gfz - tz * gfy;
+        gqy += tz * gfx - tx * gfz;
+        gqz += tx * gfy - ty * gfx;
+        // t = 2 (u x v3)
+        T g1x = T(2) * gtx, g1y = T(2) * gty, g1z = T(2) * gtz;
+        gqx += vy3 * g1z - vz3 * g1y;
+        gqy += vz3 * g1x - vx3 * g1z;
+        gqz += vx3 * g1y - vy3 * g1x;
+        T gthr = gfz + (g1x * qy - g1y * qx);
+        // body-rate derivative (Euler's equation)
+        T gax = gk.bx / P.ixx, gay = gk.by / P.iyy, gaz = gk.bz / P.izz;
+        T gbx = T(0), gby = T(0), gbz = T(0);
+        gby -= (P.izz - P.iyy) * bz * gax;
+        gbz -= (P.izz - P.iyy) * by * gax;
+        gbz -= (P.ixx - P.izz) * bx * gay;
+        gbx -= (P.ixx - P.izz) * bz * gay;
+        gbx -= (P.iyy - P.ixx) * by * gaz;
+        gby -= (P.iyy - P.ixx) * bx * gaz;
+        T gf0 = gthr - P.arm * gay + P.kappa * gaz;
+        T gf1 = gthr + P.arm * gax - P.kappa * gaz;
+        T gf2 = gthr + P.arm * gay + P.kappa * gaz;
+        T gf3 = gthr - P.arm * gax - P.kappa * gaz;
+        // quaternion derivative 0.5 q (x) (b, 0)
+        T Dx = h * gk.qx, Dy = h * gk.qy, Dz = h * gk.qz, Dw = h * gk.qw;
+        gqw += Dx * bx + Dy * by + Dz * bz;
+        gqx += -Dy * bz + Dz * by - Dw * bx;
+        gqy += Dx * bz - Dz * bx - Dw * by;
+        gqz += -Dx * by + Dy * bx - Dw * bz;
+        gbx += Dx * qw + Dy * qz - Dz * qy - Dw * qx;
+        gby += -Dx * qz + Dy * qw + Dz * qx - Dw * qy;
+        gbz += Dx * qy - Dy * qx + Dz * qw - Dw * qz;
+        gx.qx += gqx; gx.qy += gqy; gx.qz += gqz; gx.qw += gqw;
+        gx.bx += gbx; gx.by += gby; gx.bz += gbz;
+        ga[0] += wclamp_g(a[0], z0, P.thrust_max, gf0);
+        ga[1] += wclamp_g(a[1], z0, P.thrust_max, gf1);
+        ga[2] += wclamp_g(a[2], z0, P.thrust_max, gf2);
+        ga[3] += wclamp_g(a[3], z0, P.thrust_max, gf3);
+    } else if (P.tag == 0) {
+        gx.vx += gk.px;
+        gx.vy += gk.py;
+        if (P.mode != 0) clamp_norm_adj(a[0], a[1], P.max_accel, gk.vx, gk.vy, ga[0], ga[1]);
+    } else if (P.tag == 1) {
+        T c = m_cos(x.th), sn = m_sin(x.th);
+        gx.s += gk.px * c + gk.py * sn;
+        gx.th += -gk.px * x.s * sn + gk.py * x.s * c;
+        gx.w += gk.th;
+        if (P.mode != 0) {
+            ga[0] += wclamp_g(a[0], -P.max_accel, P.max_accel, gk.s);
+            ga[1] += wclamp_g(a[1], -P.max_ang_accel, P.max_ang_accel, gk.w);
+        }
+    } else if (P.tag == 2) {
+        T wb = P.l_f + P.l_r;
+        T del = wclamp(a[1], -P.max_steer, P.max_steer);
+        T td = m_tan(del);
+        T u = td * P.l_r / wb;
+        T beta = m_atan(u);
+        T cb = m_cos(beta), sb = m_sin(beta);
+        T c = m_cos(x.th + beta), sn = m_sin(x.th + beta);
+        gx.s += gk.px * c + gk.py * sn + gk.th * (cb * td / wb);
+        T gang = -gk.px * x.s * sn + gk.py * x.s * c;  // d / d(th + beta)
+        gx.th += gang;
+        T gbeta = gang + gk.th * (x.s / wb * (-sb) * td);
+        T gdel = gk.th * (x.s / wb * cb * (T(1) + td * td))
+                 + gbeta / (T(1) + u * u) * (T(1) + td * td) * P.l_r / wb;
+        ga[1] += wclamp_g(a[1], -P.max_steer, P.max_steer, gdel);
+        ga[0] += wclamp_g(a[0], -P.max_accel, P.max_accel, gk.s);
+    }
+}
+
+// The stage states x2..x4 (x1 = x0) and the combine x0 + (k1 + 2 k2 + 2 k3 + k4) dt / 6
+// (swarp/dynamics/kernels.py:584-738).  x0 is the input with the velocity-control command
+// written into the velocity-level state (:588-595).
+template <typename T> struct RkSt {
+    St<T> x0, x2, x3, x4, xi;
+};
+
+template <typename T, bool DRONE>
+__device__ __forceinline__ void rk_stages(const Cst<T> &C, const Prm<T> &P, const St<T> &in,
+                                          const T (&a)[4], RkSt<T> &R)
+{
+    const T dt = C.sub_dt, two = T(2);
+    const T dt2 = dt * T(0.5), sixth = dt / T(6);
+    R.x0 = in;
+    if (P.mode == 0) {
+        if (P.tag == 0) {
+            clamp_norm(a[0], a[1], P.max_speed, R.x0.vx, R.x0.vy);
+        } else if (P.tag == 1) {
+            R.x0.s = wclamp(a[0], -P.max_speed, P.max_speed);
+            R.x0.w = wclamp(a[1], -P.max_ang_vel, P.max_ang_vel);
+        }
+    }
+    St<T> k1, k2, k3, k4;
+    rk_deriv<T, DRONE>(P, R.x0, a, k1);
+    st_axpy(R.x0, k1, dt2, R.x2);
+    rk_deriv<T, DRONE>(P, R.x2, a, k2);
+    st_axpy(R.x0, k2, dt2, R.x3);
+    rk_deriv<T, DRONE>(P, R.x3, a, k3);
+    st_axpy(R.x0, k3, dt, R.x4);
+    rk_deriv<T, DRONE>(P, R.x4, a, k4);
+#define SWARP_RK_COMB(f) R.xi.f = R.x0.f + (k1.f + k2.f * two + k3.f * two + k4.f) * sixth
+    SWARP_RK_COMB(px); SWARP_RK_COMB(py); SWARP_RK_COMB(th); SWARP_RK_COMB(vx);
+    SWARP_RK_COMB(vy); SWARP_RK_COMB(s); SWARP_RK_COMB(w); SWARP_RK_COMB(z);
+    SWARP_RK_COMB(vz); SWARP_RK_COMB(qx); SWARP_RK_COMB(qy); SWARP_RK_COMB(qz);
+    SWARP_RK_COMB(qw); SWARP_RK_COMB(bx); SWARP_RK_COMB(by); SWARP_RK_COMB(bz);
+#undef SWARP_RK_COMB
+}
+
+// RK4 substep of one agent: _integrate_rk4 (swarp/dynamics/kernels.py:520-793).  Limits on
+// the combined result only, the contact force as dv = F * (dt / m) after the combine, the
+// attitude renormalised.
+template <typename T, bool DRONE>
+__device__ __forceinline__ void integrate_rk4(const Cst<T> &C, const Prm<T> &P, const St<T> &in,
+                                              const T (&a)[4], T Fx, T Fy, St<T> &o)
+{
+    const T dt = C.sub_dt;
+    RkSt<T> R;
+    rk_stages<T, DRONE>(C, P, in, a, R);
+    const T dfx = Fx * (dt / P.mass), dfy = Fy * (dt / P.mass);
+    o = in;
+    T pnx = R.xi.px + dfx * dt, pny = R.xi.py + dfy * dt;
+    if (DRONE && P.tag == 3) {
+        o.vx = R.xi.vx + dfx;
+        o.vy = R.xi.vy + dfy;
+        o.z = R.xi.z;
+        o.vz = R.xi.vz;
+        T l = m_sqrt(R.xi.qx * R.xi.qx + R.xi.qy * R.xi.qy + R.xi.qz * R.xi.qz + R.xi.qw * R.xi.qw);
+        if (l > T(0)) {
+            o.qx = R.xi.qx / l; o.qy = R.xi.qy / l; o.qz = R.xi.qz / l; o.qw = R.xi.qw / l;
+        } else {
+            o.qx = T(0); o.qy = T(0); o.qz = T(0); o.qw = T(1);
+        }
+        o.bx = R.xi.bx; o.by = R.xi.by; o.bz = R.xi.bz;
+    } else if (P.tag == 0) {
+        T vx, vy;
+        clamp_norm(R.xi.vx, R.xi.vy, P.max_speed, vx, vy);
+        vx = vx + dfx;
+        vy = vy + dfy;
+        o.vx = vx; o.vy = vy;
+        o.s = m_sqrt(vx * vx + vy * vy);
+        o.w = T(0);
+    } else if (P.tag == 1) {
+        T so = wclamp(R.xi.s, -P.max_speed, P.max_speed);
+        T th = R.xi.th;
+        o.th = th;
+        o.vx = so * m_cos(th) + dfx;
+        o.vy = so * m_sin(th) + dfy;
+        o.s = so;
+        o.w = wclamp(R.xi.w, -P.max_ang_vel, P.max_ang_vel);
+    } else if (P.tag == 2) {
+        T so = wclamp(R.xi.s, P.min_speed, P.max_speed);
+        T th = R.xi.th;
+        T del = wclamp(a[1], -P.max_steer, P.max_steer);
+        T wb = P.l_f + P.l_r;
+        T beta = m_atan(m_tan(del) * P.l_r / wb);
+        o.w = so / wb * m_cos(beta) * m_tan(del);
+        o.th = th;
+        o.vx = so * m_cos(th + beta) + dfx;
+        o.vy = so * m_sin(th + beta) + dfy;
+        o.s = so;
+    } else {
+        return;
+    }
+    if (C.clamp) {
+        pnx = wclamp(pnx, C.bmin_x + P.radius, C.bmax_x - P.radius);
+        pny = wclamp(pny, C.bmin_y + P.radius, C.bmax_y - P.radius);
+    }
+    o.px = pnx;
+    o.py = pny;
+}
+
+// Reverse of integrate_rk4 with integrate_adj's contract: overwrites gi (adjoint of the
+// input) and gF, accumulates ga.  The stages are recomputed from the input.
+template <typename T, bool DRONE>
+__device__ __forceinline__ void integrate_rk4_adj(const Cst<T> &C, const Prm<T> &P,
+                                                  const St<T> &in, const T (&a)[4], T Fx, T Fy,
+                                                  const St<T> &g, St<T> &gi, T (&ga)[4], T &gFx,
+                                                  T &gFy)
+{
+    const T dt = C.sub_dt, two = T(2);
+    const T dt2 = dt * T(0.5), sixth = dt / T(6);
+    gFx = T(0);
+    gFy = T(0);
+    if (P.tag > 3 || (!DRONE && P.tag == 3)) {
+        gi = g;
+        return;
+    }
+    RkSt<T> R;
+    rk_stages<T, DRONE>(C, P, in, a, R);
+    const T dfx = Fx * (dt / P.mass), dfy = Fy * (dt / P.mass);
+    T gpx = g.px, gpy = g.py;
+    if (C.clamp) {
+        gpx = wclamp_g(R.xi.px + dfx * dt, C.bmin_x + P.radius, C.bmax_x - P.radius, gpx);
+        gpy = wclamp_g(R.xi.py + dfy * dt, C.bmin_y + P.radius, C.bmax_y - P.radius, gpy);
+    }
+    St<T> gxi;
+    st_zero(gxi);
+    gxi.px = gpx;
+    gxi.py = gpy;
+    T gdfx = gpx * dt + g.vx, gdfy = gpy * dt + g.vy;
+    T pass_th = T(0), pass_s = T(0), pass_w = T(0);
+    if (DRONE && P.tag == 3) {
+        gxi.vx = g.vx;
+        gxi.vy = g.vy;
+        gxi.z = g.z;
+        gxi.vz = g.vz;
+        gxi.bx = g.bx; gxi.by = g.by; gxi.bz = g.bz;
+        T l = m_sqrt(R.xi.qx * R.xi.qx + R.xi.qy * R.xi.qy + R.xi.qz * R.xi.qz + R.xi.qw * R.xi.qw);
+        if (l > T(0)) {
+            T nx = R.xi.qx / l, ny = R.xi.qy / l, nz = R.xi.qz / l, nw = R.xi.qw / l;
+            T dq = g.qx * nx + g.qy * ny + g.qz * nz + g.qw * nw;
+            gxi.qx = (g.qx - nx * dq) / l;
+            gxi.qy = (g.qy - ny * dq) / l;
+            gxi.qz = (g.qz - nz * dq) / l;
+            gxi.qw = (g.qw - nw * dq) / l;
+        }
+        pass_th = g.th;
+        pass_s = g.s;
+        pass_w = g.w;
+    } else if (P.tag == 0) {
+        T vx, vy;
+        clamp_norm(R.xi.vx, R.xi.vy, P.max_speed, vx, vy);
+        vx = vx + dfx;
+        vy = vy + dfy;
+        T gvx = g.vx, gvy = g.vy;
+        T sp = m_sqrt(vx * vx + vy * vy);
+        if (sp > T(0)) {
+            gvx += g.s * vx / sp;
+            gvy += g.s * vy / sp;
+            gdfx += g.s * vx / sp;
+            gdfy += g.s * vy / sp;
+        }
+        clamp_norm_adj(R.xi.vx, R.xi.vy, P.max_speed, gvx, gvy, gxi.vx, gxi.vy);
+        pass_th = g.th;
+    } else if (P.tag == 1) {
+        T so = wclamp(R.xi.s, -P.max_speed, P.max_speed);
+        T th = R.xi.th, c = m_cos(th), sn = m_sin(th);
+        T gso = g.s + g.vx * c + g.vy * sn;
+        gxi.th = g.th - g.vx * so * sn + g.vy * so * c;
+        gxi.s = wclamp_g(R.xi.s, -P.max_speed, P.max_speed, gso);
+        gxi.w = wclamp_g(R.xi.w, -P.max_ang_vel, P.max_ang_vel, g.w);
+    } else {
+        T so = wclamp(R.xi.s, P.min_speed, P.max_speed);
+        T th = R.xi.th;
+        T del = wclamp(a[1], -P.max_steer, P.max_steer);
+        T wb = P.l_f + P.l_r;
+        T td = m_tan(del), u = td * P.l_r / wb;
+        T beta = m_atan(u), cb = m_cos(beta), sb = m_sin(beta);
+        T c = m_cos(th + beta), sn = m_sin(th + beta);
+        T gso = g.s + g.w * (cb * td / wb) + g.vx * c + g.vy * sn;
+        T gang = -g.vx * so * sn + g.vy * so * c;
+        gxi.th = g.th + gang;
+        T gbeta = gang + g.w * (so / wb * (-sb) * td);
+        T gdel = g.w * (so / wb * cb * (T(1) + td * td))
+                 + gbeta / (T(1) + u * u) * (T(1) + td * td) * P.l_r / wb;
+        ga[1] += wclamp_g(a[1], -P.max_steer, P.max_steer, gdel);
+        gxi.s = wclamp_g(R.xi.s, P.min_speed, P.max_speed, gso);
+    }
+    gFx = gdfx * (dt / P.mass);
+    gFy = gdfy * (dt / P.mass);
+    // the combine and the stages, in reverse
+    St<T> gx = gxi, gk1, gk2, gk3, gs, z;
+    st_zero(z);
+    st_axpy(z, gxi, sixth, gk1);
+    st_axpy(z, gxi, two * sixth, gk2);
+    gk3 = gk2;
+    st_zero(gs);
+    rk_deriv_adj<T, DRONE>(P, R.x4, a, gk1, gs, ga);  // k4 carries gk1's weight
+    st_axpy(gx, gs, T(1), gx);
+    st_axpy(gk3, gs, dt, gk3);
+    st_zero(gs);
+    rk_deriv_adj<T, DRONE>(P, R.x3, a, gk3, gs, ga);
+    st_axpy(gx, gs, T(1), gx);
+    st_axpy(gk2, gs, dt2, gk2);
+    st_zero(gs);
+    rk_deriv_adj<T, DRONE>(P, R.x2, a, gk2, gs, ga);
+    st_axpy(gx, gs, T(1), gx);
+    st_axpy(gk1, gs, dt2, gk1);
+    st_zero(gs);
+    rk_deriv_adj<T, DRONE>(P, R.x0, a, gk1, gs, ga);
+    st_axpy(gx, gs, T(1), gx);
+    // velocity control: the commanded velocity-level state replaces the input's
+    if (P.mode == 0 && P.tag == 0) {
+        clamp_norm_adj(a[0], a[1], P.max_speed, gx.vx, gx.vy, ga[0], ga[1]);
+        gx.vx = gx.vy = T(0);
+    } else if (P.mode == 0 && P.tag == 1) {
+        ga[0] += wclamp_g(a[0], -P.max_speed, P.max_speed, gx.s);
+        ga[1] += wclamp_g(a[1], -P.max_ang_vel, P.max_ang_vel, gx.w);
+        gx.s = gx.w = T(0);
+    }
+    gi = gx;
+    gi.th += pass_th;
+    gi.s += pass_s;
+    gi.w += pass_w;
+    // fields no 2-D model integrates pass their adjoint through
+    if (!(DRONE && P.tag == 3)) {
+        gi.z += g.z; gi.vz += g.vz;
+        gi.qx += g.qx; gi.qy += g.qy; gi.qz += g.qz; gi.qw += g.qw;
+        gi.bx += g.bx; gi.by += g.by; gi.bz += g.bz;
+    }
+}
+
 // Semi-implicit Euler substep of one agent: _integrate_agent + _step_2d
 // (swarp/dynamics/kernels.py:194-413).  `o` receives the new state.
 template <typename T, bool DRONE>
 __device__ __forceinline__ void integrate(const Cst<T> &C, const Prm<T> &P, const St<T> &in,
                                           const T (&a)[4], T Fx, T Fy, St<T> &o)
 {
+    if (C.rk4) {
+        integrate_rk4<T, DRONE>(C, P, in, a, Fx, Fy, o);
+        return;
+    }
     const T dt = C.sub_dt;
     const T dtm = dt / P.mass;
     const T dvx = Fx * dtm, dvy = Fy * dtm;
@@ -853,6 +1250,10 @@ __device__ __forceinline__ void integrate_adj(const Cst<T> &C, const Prm<T> &P, 
                                               const T (&a)[4], T Fx, T Fy, const St<T> &g,
                                               St<T> &gi, T (&ga)[4], T &gFx, T &gFy)
 {
+    if (C.rk4) {
+        integrate_rk4_adj<T, DRONE>(C, P, in, a, Fx, Fy, g, gi, ga, gFx, gFy);
+        return;
+    }
     const T dt = C.sub_dt;
     const T dtm = dt / P.mass;
     const T dvx = Fx * dtm, dvy = Fy * dtm;

@@ -634,6 +634,7 @@ template <typename T> static int fill_cst(const swarp_desc_t *d, double skin, Cs
     // contact distances lie in [sqrt(eps2), neighbour radius]: within the range of the
     // short exact division when the radius is at most 2^20
     C.fast_div = d->neighbor_radius <= 0x1p20 ? 1 : 0;
+    C.rk4 = d->integrator == SWARP_RK4 ? 1 : 0;
     return 0;
 }
 
@@ -648,6 +649,8 @@ static int check_desc(const swarp_desc_t *d, bool need_params = true)
     if (d->substeps < 1) return fail("substeps must be >= 1");
     if (d->collisions && d->max_neighbors < 1) return fail("max_neighbors must be >= 1");
     if (d->n_obstacles < 0) return fail("n_obstacles must be >= 0");
+    if (d->integrator != SWARP_EULER && d->integrator != SWARP_RK4)
+        return fail("desc->integrator must be SWARP_EULER or SWARP_RK4");
     if (need_params && (!d->params || !d->model_tag || !d->ctrl_mode))
         return fail("params/model_tag/ctrl_mode must be set");
     if (d->n_obstacles > 0 && (!d->obs_pos || !d->obs_radius || !d->obs_angle || !d->obs_half ||
@@ -733,7 +736,8 @@ static void launch_bwd(int PA, const Cst<T> &C, const Args<T> &a, size_t shm, hi
 
 static bool lean_ok(const swarp_desc_t *d)
 {
-    return d->holo_velocity_only && !d->has_drone && d->n_obstacles == 0 && !d->clamp_bounds;
+    return d->holo_velocity_only && !d->has_drone && d->n_obstacles == 0 && !d->clamp_bounds &&
+           d->integrator == SWARP_EULER;
 }
 
 // Byte offsets of the tape regions (see lean.hpp); total == 0: no tape.

@@ -157,8 +157,6 @@ class Stepper:
         if self.n_agents > 64:
             raise NotImplementedError("this build steps at most 64 agents per env")
         w = self.world
-        if w.integrator != Integrator.EULER:
-            raise NotImplementedError("only Integrator.EULER is implemented on the HIP path")
         if w.wheel_contacts:
             raise NotImplementedError("WorldConfig.wheel_contacts is not implemented")
         if w.neighbor_method not in ("auto", "brute"):
@@ -304,6 +302,7 @@ class Stepper:
             d.obs_body_off = o["off"].data_ptr()
         d.lin_damping = float(self.world.obstacle_linear_damping)
         d.ang_damping = float(self.world.obstacle_angular_damping)
+        d.integrator = _lib.RK4 if self.world.integrator == Integrator.RK4 else _lib.EULER
         self._descs[key] = d
         return d
 

@@ -45,6 +45,7 @@ def oracle_cfg(configs, world: WorldConfig, dt, substeps, n_envs, act_dim, n_thr
         bmax_y=b[3] if b else 0.0,
         lin_damping=world.obstacle_linear_damping,
         ang_damping=world.obstacle_angular_damping,
+        rk4=int(world.integrator.value == "rk4"),
     )
 
 

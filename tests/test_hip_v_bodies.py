@@ -18,7 +18,7 @@ from cases import nav_agents, obstacles_np, oracle_cfg, params_of
 from hip_helpers import make_stepper, rel, state_to16, to_torch_state
 from oracle.oracle import Oracle, pack_state
 from swarp_amd import rollout
-from swarp_amd.config import WorldConfig
+from swarp_amd.config import Integrator, WorldConfig
 
 pytestmark = pytest.mark.gpu
 MOVABLE = 1
@@ -156,6 +156,16 @@ def test_bodies_float64_matches_float64_oracle():
     obs = cross_obs(E, (0.0, 0.0), extra=(((0.4, 0.0), 0.1, True),))
     hip, orc = run_pair(nav_agents(A), _world(), 0.05, 2, s0, acts, obs, np.float64)
     check("f64", hip, orc, exact=True, g_tol=1e-12)
+
+
+def test_bodies_with_rk4_agents():
+    """Integrator.RK4 inside the body kernels' substeps: bit-exact agent and body states."""
+    E, A = 16, 8
+    s0, acts = _pushers(E, A, 5, spread=0.5)
+    obs = cross_obs(E, (0.0, 0.0), extra=(((0.45, 0.1), 0.1, True),))
+    hip, orc = run_pair(nav_agents(A), _world(integrator=Integrator.RK4), 0.05, 4, s0, acts, obs,
+                        np.float32)
+    check("rk4", hip, orc)
 
 
 def test_body_gradcheck_fp64():

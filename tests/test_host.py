@@ -165,8 +165,8 @@ def test_stepper_reach_check_and_unsupported_features():
         Stepper(cfgs, device="cpu", world=WorldConfig(neighbor_radius=0.1))
     with pytest.raises(ValueError, match="substeps"):
         Stepper(cfgs, substeps=0, device="cpu")
-    with pytest.raises(NotImplementedError):
-        Stepper(cfgs, device="cpu", world=WorldConfig(integrator=Integrator.RK4))
+    rk = Stepper(cfgs, device="cpu", world=WorldConfig(integrator=Integrator.RK4))
+    assert rk.desc(2, 2).integrator == 1 and Stepper(cfgs, device="cpu").desc(2, 2).integrator == 0
     with pytest.raises(NotImplementedError):
         Stepper([AgentConfig(shape="box", half_extents=(0.1, 0.1))], device="cpu")
     st = Stepper(cfgs, dt=0.1, substeps=4, device="cpu", world=WorldConfig())
