@@ -169,6 +169,39 @@ int swarp_rollout_bwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
 int swarp_neighbors(const swarp_desc_t *desc, const void *pos, int32_t *idx, int32_t *cnt,
                     int32_t *true_cnt, void *stream);
 
+/* Inputs and outputs of the navigation scenario's fused per-step pass (swarp_nav_obs).
+ * Scalars are in desc->dtype; E = desc->n_envs, A = desc->n_agents, K =
+ * desc->max_neighbors, W = 9 + 5 * k_obs (the observation width). */
+typedef struct swarp_nav {
+    const void *pos, *vel, *theta, *ang_vel; /* state [E,A,2], [E,A,2], [E,A], [E,A] */
+    const void *goals;                       /* [E,A,2] */
+    const uint8_t *reset_mask;               /* [E]: envs just reset (NULL = none) */
+    void *prev_dist;                         /* [E,A] shaping baseline, read and updated */
+    int32_t *nbr_idx, *nbr_cnt, *nbr_true;   /* lists of pos: [E,A,K], [E,A], [E,A] (true
+                                                may be NULL) */
+    void *obs;                               /* [E,A,W] */
+    void *touching, *dist, *shaping;         /* [E,A] */
+    uint8_t *on_goal, *overflow;             /* [E,A] */
+    void *reward;                            /* [E,A] (full passes only) */
+    uint8_t *done;                           /* [E]   (full passes only) */
+    int32_t k_obs;                           /* neighbour slots in the observation */
+    int32_t advance_prev;                    /* 1: the baseline advances to the current
+                                                distance (a step pass) */
+    int32_t full_pass;                       /* 0: obs-only pass over the envs of
+                                                reset_mask (auto-reset); 1: every env,
+                                                reward and done included */
+    int32_t shared_reward;
+    double pos_shaping_factor, goal_tolerance, collision_penalty, final_reward;
+} swarp_nav_t;
+
+/* The navigation scenario's per-step pass in one launch: radius lists of `pos`
+ * (as swarp_neighbors), observation rows, touching count, goal distance, position
+ * shaping, on-goal / overflow flags, reward and done.  Replaces the reference's no-grad
+ * fast path: the NeighborGrid build + nav_obs_kernel + nav_reward_kernel
+ * (swarp/scenarios/navigation.py:539-650, swarp/scenarios/navigation_kernels.py:41-243).
+ * Radii for the touching test are column P_RADIUS of desc->params. */
+int swarp_nav_obs(const swarp_desc_t *desc, const swarp_nav_t *nav, void *stream);
+
 /* COO radius graph from padded lists: replaces NeighborGrid.edge_index's torch mask ops
  * (swarp/core/neighbors.py:716-733).  `offsets` [E*A] int64 must hold the exclusive
  * prefix sum of cnt in (env, agent) order (n_edges = offsets[last] + cnt[last]);

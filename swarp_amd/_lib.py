@@ -74,6 +74,24 @@ class SwarpState(ctypes.Structure):
     ]
 
 
+class SwarpNav(ctypes.Structure):
+    """Mirror of ``swarp_nav_t`` (the navigation pass's buffers and constants)."""
+
+    _fields_ = [
+        ("pos", ctypes.c_void_p), ("vel", ctypes.c_void_p), ("theta", ctypes.c_void_p),
+        ("ang_vel", ctypes.c_void_p), ("goals", ctypes.c_void_p),
+        ("reset_mask", ctypes.c_void_p), ("prev_dist", ctypes.c_void_p),
+        ("nbr_idx", ctypes.c_void_p), ("nbr_cnt", ctypes.c_void_p), ("nbr_true", ctypes.c_void_p),
+        ("obs", ctypes.c_void_p), ("touching", ctypes.c_void_p), ("dist", ctypes.c_void_p),
+        ("shaping", ctypes.c_void_p), ("on_goal", ctypes.c_void_p),
+        ("overflow", ctypes.c_void_p), ("reward", ctypes.c_void_p), ("done", ctypes.c_void_p),
+        ("k_obs", ctypes.c_int32), ("advance_prev", ctypes.c_int32),
+        ("full_pass", ctypes.c_int32), ("shared_reward", ctypes.c_int32),
+        ("pos_shaping_factor", ctypes.c_double), ("goal_tolerance", ctypes.c_double),
+        ("collision_penalty", ctypes.c_double), ("final_reward", ctypes.c_double),
+    ]
+
+
 #: Exported entry points and their ctypes signatures.
 SIGNATURES = {
     "swarp_abi_version": ([], ctypes.c_int),
@@ -122,6 +140,10 @@ SIGNATURES = {
     "swarp_neighbors": (
         [ctypes.POINTER(SwarpDesc), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
          ctypes.c_void_p, ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "swarp_nav_obs": (
+        [ctypes.POINTER(SwarpDesc), ctypes.POINTER(SwarpNav), ctypes.c_void_p],
         ctypes.c_int,
     ),
     "swarp_edge_index": (

@@ -511,6 +511,7 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
 }  // namespace swarp
 #include "lean.hpp"
 #include "bodies.hpp"
+#include "nav.hpp"
 namespace swarp {
 
 // --------------------------------------------------------------- neighbour lists
@@ -1012,6 +1013,57 @@ static int rollout_bwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     return 0;
 }
 
+template <typename T> static int nav_obs(const swarp_desc_t *d, const swarp_nav_t *v, hipStream_t st)
+{
+    Cst<T> C;
+    fill_cst<T>(d, 0.0, C);
+    NavArgs<T> g;
+    memset(&g, 0, sizeof g);
+    g.pos = (const T *)v->pos;
+    g.vel = (const T *)v->vel;
+    g.th = (const T *)v->theta;
+    g.om = (const T *)v->ang_vel;
+    g.goal = (const T *)v->goals;
+    g.params = (const T *)d->params;
+    g.rmask = v->reset_mask;
+    g.prev = (T *)v->prev_dist;
+    g.obs = (T *)v->obs;
+    g.touch = (T *)v->touching;
+    g.dist = (T *)v->dist;
+    g.shaping = (T *)v->shaping;
+    g.reward = (T *)v->reward;
+    g.idx = v->nbr_idx;
+    g.cnt = v->nbr_cnt;
+    g.tru = v->nbr_true;
+    g.ongoal = v->on_goal;
+    g.overflow = v->overflow;
+    g.done = v->done;
+    g.shaping_factor = (T)v->pos_shaping_factor;
+    g.goal_tol = (T)v->goal_tolerance;
+    g.coll_pen = (T)v->collision_penalty;
+    g.final_rew = (T)v->final_reward;
+    g.k_obs = v->k_obs;
+    g.W = 9 + 5 * v->k_obs;
+    g.advance_prev = v->advance_prev ? 1 : 0;
+    g.full_pass = v->full_pass ? 1 : 0;
+    g.shared = v->shared_reward ? 1 : 0;
+    const size_t lds = (size_t)64 * g.W * sizeof(T);
+    g.stage = lds <= 48 * 1024 ? 1 : 0;  // rows leave through LDS when they fit
+    const unsigned dyn = g.stage ? (unsigned)lds : 0u;
+    const int PA = pad_agents(d->n_agents);
+    const dim3 grid((d->n_envs + (64 / PA) - 1) / (64 / PA));
+    switch (PA) {
+    case 4: hipLaunchKernelGGL((k_nav<T, 4>), grid, dim3(64), dyn, st, C, g); break;
+    case 8: hipLaunchKernelGGL((k_nav<T, 8>), grid, dim3(64), dyn, st, C, g); break;
+    case 16: hipLaunchKernelGGL((k_nav<T, 16>), grid, dim3(64), dyn, st, C, g); break;
+    case 32: hipLaunchKernelGGL((k_nav<T, 32>), grid, dim3(64), dyn, st, C, g); break;
+    default: hipLaunchKernelGGL((k_nav<T, 64>), grid, dim3(64), dyn, st, C, g); break;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(hipGetErrorString(e));
+    return 0;
+}
+
 extern "C" {
 
 int swarp_abi_version(void) { return SWARP_ABI_VERSION; }
@@ -1153,6 +1205,25 @@ int swarp_neighbors(const swarp_desc_t *desc, const void *pos, int32_t *idx, int
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
     return 0;
+}
+
+int swarp_nav_obs(const swarp_desc_t *desc, const swarp_nav_t *nav, void *stream)
+{
+    g_err[0] = 0;
+    if (check_desc(desc)) return -1;
+    if (!nav) return fail("nav is NULL");
+    if (desc->max_neighbors < 1) return fail("max_neighbors must be >= 1");
+    if (nav->k_obs < 0 || nav->k_obs > desc->max_neighbors)
+        return fail("k_obs must lie in [0, max_neighbors]");
+    if (!nav->pos || !nav->vel || !nav->theta || !nav->ang_vel || !nav->goals || !nav->prev_dist ||
+        !nav->nbr_idx || !nav->nbr_cnt || !nav->obs || !nav->touching || !nav->dist ||
+        !nav->shaping || !nav->on_goal || !nav->overflow || !nav->reward || !nav->done)
+        return fail("every swarp_nav_t pointer except reset_mask and nbr_true must be set");
+    if (!nav->full_pass && !nav->reset_mask)
+        return fail("an obs-only pass (full_pass == 0) needs reset_mask");
+    hipStream_t st = (hipStream_t)stream;
+    if (desc->dtype == SWARP_F32) return nav_obs<float>(desc, nav, st);
+    return nav_obs<double>(desc, nav, st);
 }
 
 int swarp_edge_index(int32_t n_envs, int32_t n_agents, int32_t max_neighbors, const int32_t *idx,

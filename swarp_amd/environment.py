@@ -63,6 +63,8 @@ class Environment:
                                          substeps=substeps, dtype=dtype,
                                          world_config=world_config)
         self.n_agents = self.world.n_agents
+        # the scenario's fused no-grad obs/reward pass (environment.py:155)
+        self._fused = scenario.fused_available if fused == "auto" else bool(fused)
         self._seed(seed)
         self._step_count = torch.zeros(n_envs, device=self.device, dtype=torch.int32)
         self._never_truncated = torch.zeros(n_envs, device=self.device, dtype=torch.bool)
@@ -139,6 +141,21 @@ class Environment:
             high[i, : len(hi)] = torch.tensor(hi, device=self.device, dtype=self.dtype)
         return low, high
 
+    # ------------------------------------------------------------ path choice
+
+    def _taped_step(self, actions: torch.Tensor | None = None) -> bool:
+        """Whether the coming step is differentiated: grad mode on and something
+        requires grad (``swarp/core/environment.py:403-417``)."""
+        if not torch.is_grad_enabled():
+            return False
+        if actions is not None and actions.requires_grad:
+            return True
+        return any(t is not None and t.requires_grad for t in self.world.state)
+
+    def _set_fused_active(self, actions: torch.Tensor | None = None) -> None:
+        """The fused pass serves untaped steps; a differentiated step takes torch."""
+        self.scenario.set_fused_active(self._fused and not self._taped_step(actions))
+
     # ------------------------------------------------------------------ episodes
 
     def reset(self, seed: int | None = None) -> torch.Tensor:
@@ -146,6 +163,7 @@ class Environment:
         if seed is not None:
             self._seed(seed)
         self.world.action = None
+        self._set_fused_active()
         with torch.no_grad():
             self.world.reset_state()
             self.scenario.reset_world(None)
@@ -154,6 +172,7 @@ class Environment:
 
     def reset_at(self, env_mask: torch.Tensor) -> torch.Tensor:
         """Reset the envs where ``env_mask`` (bool ``[n_envs]``) is True."""
+        self._set_fused_active()
         with torch.no_grad():
             self.scenario.reset_world(env_mask)
         self._step_count.masked_fill_(env_mask, 0)
@@ -175,6 +194,7 @@ class Environment:
             )
         if actions.dtype != self.dtype:
             raise TypeError(f"actions dtype {actions.dtype} != env dtype {self.dtype}")
+        self._set_fused_active(actions)
         self.world.action = actions
         self.world.step(actions)
         self.scenario.post_step()

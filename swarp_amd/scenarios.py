@@ -3,14 +3,17 @@
 (``swarp/scenarios/navigation.py:38-839``), the step's caller in every benchmark of the
 reference.
 
-Observations and rewards are torch ops on the step's outputs -- the reference's own
-differentiable path (``_refresh_step_cache`` / ``observations`` / ``rewards``,
-``swarp/scenarios/navigation.py:671-839``); the reference's fused Warp obs/reward/reset
-kernels are a no-grad speed path of the scenario, not of the physics step, and are not
-rebuilt here.  Resets draw spawns and goals with the stratified separated sampler the
-reference keeps as its torch reference (``_sample_separated``, ``:222-272``) on the
-world's generator, so they are reproducible per seed but are not the reference's Warp
-RNG stream.
+Observations and rewards have two paths, as in the reference:
+* torch ops on the step's outputs -- the reference's own differentiable path
+  (``_refresh_step_cache`` / ``observations`` / ``rewards``,
+  ``swarp/scenarios/navigation.py:671-839``), taken when the step is differentiated;
+* the fused no-grad pass: one HIP launch (``swarp_nav_obs``) builds the lists and writes
+  the observation, reward, done and info buffers in place -- the counterpart of the
+  reference's fused Warp kernels (``swarp/scenarios/navigation.py:508-650``,
+  ``navigation_kernels.py``).  ``Environment`` switches it on for untaped steps.
+Resets draw spawns and goals with the stratified separated sampler the reference keeps
+as its torch reference (``_sample_separated``, ``:222-272``) on the world's generator,
+so they are reproducible per seed but are not the reference's Warp RNG stream.
 """
 
 from __future__ import annotations
@@ -19,8 +22,11 @@ import math
 from abc import ABC, abstractmethod
 from typing import Any
 
+import ctypes
+
 import torch
 
+from . import _lib
 from .config import AgentConfig, AgentShape, ControlMode, DynamicsModel, Obstacles, WorldConfig
 from .config import _coerce
 from .world import World
@@ -105,6 +111,15 @@ class Scenario(ABC):
     def post_step(self) -> None:  # noqa: B027 (optional hook)
         """Called right after the physics step, before observations and rewards."""
 
+    #: whether the scenario has a fused no-grad obs/reward pass
+    #: (``swarp/scenarios/base.py`` ``fused_available``)
+    fused_available: bool = False
+    fused_active: bool = False
+
+    def set_fused_active(self, on: bool) -> None:
+        """Route the next passes through the fused kernels (``on``) or torch."""
+        self.fused_active = bool(on) and self.fused_available
+
 
 class NavigationScenario(Scenario):
     """Agents navigate to per-agent goals with soft collision avoidance
@@ -169,6 +184,8 @@ class NavigationScenario(Scenario):
         self._k_obs = min(self.neighbor_obs, min(32, max(4, self.n_agents)))
         self._cache: dict[str, torch.Tensor] | None = None
         self._prev_dist: torch.Tensor | None = None
+        self._fb: dict[str, torch.Tensor] | None = None   # fused-pass buffers
+        self._fresh = "torch"   # which path wrote the current obs / reward
 
     # ------------------------------------------------------------------ world
 
@@ -203,6 +220,8 @@ class NavigationScenario(Scenario):
         self._k_obs = min(self.neighbor_obs, cfg.max_neighbors)
         self._cache = None
         self._prev_dist = None
+        self._fb = None
+        self._fresh = "torch"
         if self.n_obstacles > 0:
             tt = {"device": device, "dtype": dtype}
             self.world.set_obstacles(Obstacles(
@@ -263,13 +282,94 @@ class NavigationScenario(Scenario):
                 w.obstacle_pos.copy_(torch.where(env_mask.view(-1, 1, 1), opos, w.obstacle_pos))
             w.set_obstacles(w.obstacles)
         # a full reset rebases every env's shaping baseline
-        self._refresh(reset_mask=env_mask if env_mask is not None else
-                      torch.ones(n, dtype=torch.bool, device=w.device))
+        mask = env_mask if env_mask is not None else torch.ones(n, dtype=torch.bool,
+                                                                device=w.device)
+        if self.fused_active:
+            # an auto-reset pass leaves the returned reward / done alone (full_pass 0)
+            self.launch_fused(advance_prev=0, full_pass=0 if obs_only else 1, reset_mask=mask)
+        else:
+            self._refresh(reset_mask=mask)
 
     # ------------------------------------------------------------ obs / rewards
 
     def post_step(self) -> None:
-        self._refresh()
+        if self.fused_active:
+            self.launch_fused(advance_prev=1, full_pass=1)
+        else:
+            self._refresh()
+
+    # ------------------------------------------------------ fused pass (HIP)
+
+    fused_available = True
+
+    def ensure_fused(self) -> dict[str, torch.Tensor]:
+        """The fused pass's persistent buffers (``fused_spec``,
+        ``swarp/scenarios/navigation.py:508-522``), allocated once per world."""
+        w = self.world
+        if self._fb is None:
+            e, a = w.n_envs, w.n_agents
+            f = {"device": w.device, "dtype": w.dtype}
+            u8 = {"device": w.device, "dtype": torch.uint8}
+            self._fb = {
+                "obs": torch.zeros(e, a, self.obs_dim, **f),
+                "touch": torch.zeros(e, a, **f), "dist": torch.zeros(e, a, **f),
+                "shaping": torch.zeros(e, a, **f), "reward": torch.zeros(e, a, **f),
+                "ongoal": torch.zeros(e, a, **u8), "overflow": torch.zeros(e, a, **u8),
+                "done": torch.zeros(e, **u8), "resetmask": torch.zeros(e, **u8),
+            }
+        if self._prev_dist is None:
+            self._prev_dist = torch.zeros(w.n_envs, w.n_agents, device=w.device, dtype=w.dtype)
+        return self._fb
+
+    def fused_nav(self, state, advance_prev: int, full_pass: int, reset_mask) -> _lib.SwarpNav:
+        """The ``swarp_nav_t`` of one pass over ``state`` (pointers only; no launch)."""
+        w = self.world
+        fb = self.ensure_fused()
+        grid = w.stepper.grid(w.n_envs)
+        p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+        nav = _lib.SwarpNav()
+        nav.pos, nav.vel = p(state.pos), p(state.vel)
+        nav.theta, nav.ang_vel = p(state.theta), p(state.ang_vel)
+        nav.goals = p(w.goals)
+        nav.reset_mask = None if reset_mask is None else p(reset_mask)
+        nav.prev_dist = p(self._prev_dist)
+        nav.nbr_idx, nav.nbr_cnt = p(grid.neighbor_idx), p(grid.neighbor_count)
+        nav.nbr_true = p(grid.neighbor_true_count)
+        nav.obs, nav.touching, nav.dist = p(fb["obs"]), p(fb["touch"]), p(fb["dist"])
+        nav.shaping, nav.reward = p(fb["shaping"]), p(fb["reward"])
+        nav.on_goal, nav.overflow, nav.done = p(fb["ongoal"]), p(fb["overflow"]), p(fb["done"])
+        nav.k_obs = self._k_obs
+        nav.advance_prev, nav.full_pass = int(advance_prev), int(full_pass)
+        nav.shared_reward = int(self.shared_reward)
+        nav.pos_shaping_factor = float(self.pos_shaping_factor)
+        nav.goal_tolerance = float(self.goal_tolerance)
+        nav.collision_penalty = float(self.collision_penalty)
+        nav.final_reward = float(self.final_reward)
+        return nav
+
+    def launch_fused(self, advance_prev: int, full_pass: int,
+                     reset_mask: torch.Tensor | None = None) -> None:
+        """One fused pass on the current state: lists, observations, shaping and flags,
+        and (``full_pass``) reward and done (``launch_fused``,
+        ``swarp/scenarios/navigation.py:524-537``)."""
+        w = self.world
+        fb = self.ensure_fused()
+        rm = None
+        if reset_mask is not None:
+            rm = fb["resetmask"]
+            rm.copy_(reset_mask)
+        st = w.state
+        for t in (st.pos, st.vel, st.theta, st.ang_vel):
+            if not t.is_contiguous():
+                raise ValueError("world state fields must be contiguous")
+        nav = self.fused_nav(st, advance_prev, full_pass, rm)
+        desc = w.stepper.desc(w.n_envs, w.act_dim)
+        lib = _lib.load()
+        stream = torch.cuda.current_stream(st.pos.device).cuda_stream
+        _lib.check(lib.swarp_nav_obs(ctypes.byref(desc), ctypes.byref(nav),
+                                     ctypes.c_void_p(stream)))
+        w.lists_built_on(st.pos)
+        self._fresh = "fused"
 
     def _refresh(self, reset_mask: torch.Tensor | None = None) -> None:
         """Neighbour features, goal distances and reward terms of the current state
@@ -299,12 +399,13 @@ class NavigationScenario(Scenario):
         if self._prev_dist is None:
             self._prev_dist = dist.detach().clone()
         shaping = (self._prev_dist - dist) * self.pos_shaping_factor
+        # the baseline is one persistent buffer shared with the fused pass
         if reset_mask is None:
-            self._prev_dist = dist.detach().clone()
+            self._prev_dist.copy_(dist.detach())
         else:
             m = reset_mask.unsqueeze(-1)
             shaping = torch.where(m, torch.zeros_like(shaping), shaping)
-            self._prev_dist = torch.where(m, dist.detach(), self._prev_dist)
+            self._prev_dist.copy_(torch.where(m, dist.detach(), self._prev_dist))
         self._cache = {
             "rel_pos": rel_pos,
             "rel_vel": rel_vel,
@@ -315,8 +416,11 @@ class NavigationScenario(Scenario):
             "pos_shaping": shaping,
             "neighbor_overflow": w.neighbor_overflow(),
         }
+        self._fresh = "torch"
 
     def observations(self) -> torch.Tensor:
+        if self._fresh == "fused":
+            return self._fb["obs"]
         w = self.world
         s = w.state
         c = self._cache
@@ -331,6 +435,8 @@ class NavigationScenario(Scenario):
         return torch.cat(feats, dim=-1)
 
     def rewards(self) -> torch.Tensor:
+        if self._fresh == "fused":
+            return self._fb["reward"]
         c = self._cache
         rew = self.collision_penalty * c["touching"]
         if self.shared_reward:
@@ -340,24 +446,38 @@ class NavigationScenario(Scenario):
         final = self.final_reward * c["on_goal"].all(dim=-1).to(self.world.dtype)
         return rew + final.unsqueeze(-1)
 
+    def _terms(self) -> dict[str, torch.Tensor]:
+        """touching / pos_shaping / on_goal of whichever path ran last."""
+        if self._fresh == "fused":
+            fb = self._fb
+            return {"touching": fb["touch"], "pos_shaping": fb["shaping"],
+                    "on_goal": fb["ongoal"].view(torch.bool)}
+        return self._cache
+
     def agent_reward(self, agent_idx: int) -> torch.Tensor:
-        c = self._cache
+        c = self._terms()
         rew = self.collision_penalty * c["touching"][:, agent_idx]
         if not self.shared_reward:
             rew = rew + c["pos_shaping"][:, agent_idx]
         return rew
 
     def global_reward(self) -> torch.Tensor:
-        c = self._cache
+        c = self._terms()
         rew = self.final_reward * c["on_goal"].all(dim=-1).to(self.world.dtype)
         if self.shared_reward:
             rew = rew + c["pos_shaping"].sum(dim=-1)
         return rew
 
     def done(self) -> torch.Tensor:
+        if self._fresh == "fused":
+            return self._fb["done"].view(torch.bool)
         return self._cache["on_goal"].all(dim=-1)
 
     def info(self) -> dict[str, Any]:
+        if self._fresh == "fused":
+            fb = self._fb
+            return {"dist_to_goal": fb["dist"], "on_goal": fb["ongoal"].view(torch.bool),
+                    "collisions": fb["touch"], "neighbor_overflow": fb["overflow"].view(torch.bool)}
         c = self._cache
         return {"dist_to_goal": c["dist_to_goal"], "on_goal": c["on_goal"],
                 "collisions": c["touching"], "neighbor_overflow": c["neighbor_overflow"]}

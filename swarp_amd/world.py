@@ -158,6 +158,11 @@ class World:
         self.build_neighbors()
         return self.stepper.grid(self.n_envs).torch_views()
 
+    def lists_built_on(self, pos: torch.Tensor) -> None:
+        """Record that the grid's lists were just built on ``pos`` by another launch
+        (the scenario's fused pass builds them with its observations)."""
+        self._lists_of = pos
+
     def mark_pos_dirty(self) -> None:
         """Invalidate the lists after positions were written out of band."""
         self._lists_of = None
