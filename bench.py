@@ -55,6 +55,9 @@ def parse():
     ap.add_argument("--substeps", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target duration of the CPU-baseline sample (0 = skip)")
+    ap.add_argument("--env-steps", type=int, default=100,
+                    help="timed Environment.step calls of the no-grad navigation leg "
+                         "(16000 x 16, graph on and off); 0 skips it")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="after the benchmark, run 3 plain device copies of this many MiB "
                          "(calibrates rocprof byte counters against a known traffic)")
@@ -241,6 +244,19 @@ def main():
         "fwd_only_env_steps_per_s": fwd_only,
         "kernels": kernels,
     }
+    if args.env_steps > 0:
+        # the reference's own published benchmark: no-grad Environment.step of the
+        # navigation scenario (step + lists + obs/reward), 1 substep, graph on and off
+        from swarp_amd.throughput import bench_one
+
+        rows = {}
+        for g in (True, False):
+            r = bench_one(16000, 16, steps=args.env_steps, use_graph=g)
+            rows["graph" if g else "eager"] = {
+                "env_steps_s": r["env_steps_s"], "ms_per_step": r["ms_per_step"],
+                "reference_rtx3070_env_steps_s": r["reference_rtx3070_env_steps_s"],
+            }
+        out["env_step_nograd_16000x16"] = rows
     if args.cpu_seconds > 0:
         out["cpu_baseline"] = cpu_baseline(E, A, T, S, args.cpu_seconds, cfgs, world)
     if args.copy_mb > 0:

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 4
+#define SWARP_ABI_VERSION 5
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -192,6 +192,12 @@ typedef struct swarp_nav {
                                                 reward and done included */
     int32_t shared_reward;
     double pos_shaping_factor, goal_tolerance, collision_penalty, final_reward;
+    int32_t *step_count;                     /* [E] episode step counter, incremented on
+                                                step passes (advance_prev = 1, full_pass =
+                                                1); NULL = not counted here */
+    uint8_t *truncated;                      /* [E] step_count >= max_steps after the
+                                                increment (NULL = not written) */
+    int32_t max_steps;                       /* <= 0: no time limit */
 } swarp_nav_t;
 
 /* The navigation scenario's per-step pass in one launch: radius lists of `pos`

@@ -11,7 +11,9 @@ import ctypes
 import os
 from pathlib import Path
 
-ABI_VERSION = 4
+import torch
+
+ABI_VERSION = 5
 F32, F64 = 0, 1
 EULER, RK4 = 0, 1
 
@@ -89,6 +91,8 @@ class SwarpNav(ctypes.Structure):
         ("full_pass", ctypes.c_int32), ("shared_reward", ctypes.c_int32),
         ("pos_shaping_factor", ctypes.c_double), ("goal_tolerance", ctypes.c_double),
         ("collision_penalty", ctypes.c_double), ("final_reward", ctypes.c_double),
+        ("step_count", ctypes.c_void_p), ("truncated", ctypes.c_void_p),
+        ("max_steps", ctypes.c_int32),
     ]
 
 
@@ -180,6 +184,13 @@ def load() -> ctypes.CDLL:
         raise SwarpLibraryError(f"{LIB_PATH} has ABI {ver}, expected {ABI_VERSION}: rebuild it")
     _lib = lib
     return lib
+
+
+def stream_of(device: torch.device) -> int:
+    """Raw handle of torch's current stream on ``device`` (the stream every launch of
+    this package goes to; inside a graph capture it is the capture stream)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
 
 
 def check(rc: int) -> None:

@@ -87,7 +87,7 @@ def _nfields(stepper: Stepper) -> int:
 
 
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return _lib.stream_of(t.device)
 
 
 def _validate(stepper: Stepper, state: TorchState, actions_seq: torch.Tensor) -> tuple[int, int, int]:

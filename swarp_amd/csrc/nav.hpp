@@ -22,9 +22,27 @@ template <typename T> struct NavArgs {
     T *prev, *obs, *touch, *dist, *shaping, *reward;
     int32_t *idx, *cnt, *tru;
     uint8_t *ongoal, *overflow, *done;
+    int32_t *step_count;   // [E] (NULL: not counted here)
+    uint8_t *truncated;    // [E] (NULL: not written)
     T shaping_factor, goal_tol, coll_pen, final_rew;
-    int k_obs, W, advance_prev, full_pass, shared, stage;
+    int k_obs, W, advance_prev, full_pass, shared, stage, max_steps;
 };
+
+// Copy `n` elements of type X from LDS to global memory with the wave's 64 lanes, in
+// 16-byte pieces when both ends and the length allow it.
+template <typename X>
+__device__ __forceinline__ void wave_copy(X *dst, const X *src, int n, int lane)
+{
+    const size_t bytes = (size_t)n * sizeof(X);
+    if (((uintptr_t)dst & 15) == 0 && ((uintptr_t)src & 15) == 0 && (bytes & 15) == 0) {
+        uint4 *d = reinterpret_cast<uint4 *>(dst);
+        const uint4 *q = reinterpret_cast<const uint4 *>(src);
+        const int n4 = (int)(bytes >> 4);
+        for (int k = lane; k < n4; k += 64) d[k] = q[k];
+    } else {
+        for (int k = lane; k < n; k += 64) dst[k] = src[k];
+    }
+}
 
 template <typename T, int PA>
 __global__ __launch_bounds__(64) void k_nav(const Cst<T> C, const NavArgs<T> g)
@@ -32,8 +50,10 @@ __global__ __launch_bounds__(64) void k_nav(const Cst<T> C, const NavArgs<T> g)
     typedef typename MaskT<PA>::type M;
     __shared__ T lx[64], ly[64], lvx[64], lvy[64], lra[64], lsh[64];
     __shared__ int log_[64];
-    extern __shared__ unsigned char nav_dyn[];
+    extern __shared__ __align__(16) unsigned char nav_dyn[];
+    // staged output rows: observation rows [64][W], then list rows [64][K]
     T *row_lds = reinterpret_cast<T *>(nav_dyn);
+    int32_t *idx_lds = reinterpret_cast<int32_t *>(nav_dyn + (size_t)64 * g.W * sizeof(T));
 
     const int lane = threadIdx.x, agent = lane % PA, base = lane - agent;
     const int env = blockIdx.x * (64 / PA) + lane / PA;
@@ -67,8 +87,8 @@ __global__ __launch_bounds__(64) void k_nav(const Cst<T> C, const NavArgs<T> g)
     const M incl = scan_all<T, PA>(lx, ly, base, C.A, agent, px, py, C.t_nbr, C.t_nbr, cd);
     const M m = cap_list(incl, C.K);
     const int n = m_popc(m);
-    if (work) {
-        int32_t *irow = g.idx + i * C.K;
+    if (g.stage || work) {
+        int32_t *irow = g.stage ? idx_lds + (size_t)lane * C.K : g.idx + i * C.K;
         M mm = m;
         for (int k = 0; k < C.K; ++k) {
             int v = 0;
@@ -78,6 +98,8 @@ __global__ __launch_bounds__(64) void k_nav(const Cst<T> C, const NavArgs<T> g)
             }
             irow[k] = v;
         }
+    }
+    if (work) {
         g.cnt[i] = n;
         if (g.tru) g.tru[i] = m_popc(incl);
     }
@@ -167,20 +189,23 @@ __global__ __launch_bounds__(64) void k_nav(const Cst<T> C, const NavArgs<T> g)
     }
 
     if (g.stage) {
-        // the env rows of this wave are contiguous in obs: envs [blockIdx.x * EPW, ...)
+        // an env's rows are A consecutive rows both in LDS (lanes e*PA .. e*PA+A-1) and in
+        // memory, so each env leaves as one contiguous block; with no pad slots (A == PA)
+        // and every env written, the whole wave's rows are one block
         __syncthreads();
         const int env0 = blockIdx.x * (64 / PA);
         const int n_env = min(64 / PA, C.E - env0);
-        const size_t first = (size_t)env0 * C.A;
-        // rows of a partially filled env slot (agents >= A) are skipped: walk the valid
-        // (env, agent) rows in order, W values each
-        const int rows = n_env * C.A;
-        const int total = rows * W;
-        for (int k = lane; k < total; k += 64) {
-            const int r = k / W, c = k - r * W;
-            const int e_loc = r / C.A, a = r - e_loc * C.A;
-            const bool ew = g.full_pass != 0 || (g.rmask != nullptr && g.rmask[env0 + e_loc] != 0);
-            if (ew) g.obs[(first + r) * W + c] = row_lds[(size_t)(e_loc * PA + a) * W + c];
+        if (g.full_pass != 0 && PA == C.A) {
+            const size_t first = (size_t)env0 * C.A;
+            wave_copy(g.obs + first * W, row_lds, n_env * C.A * W, lane);
+            wave_copy(g.idx + first * C.K, idx_lds, n_env * C.A * C.K, lane);
+        } else {
+            for (int e = 0; e < n_env; ++e) {
+                if (g.full_pass == 0 && !(g.rmask != nullptr && g.rmask[env0 + e] != 0)) continue;
+                const size_t first = (size_t)(env0 + e) * C.A;
+                wave_copy(g.obs + first * W, row_lds + (size_t)e * PA * W, C.A * W, lane);
+                wave_copy(g.idx + first * C.K, idx_lds + (size_t)e * PA * C.K, C.A * C.K, lane);
+            }
         }
     }
 
@@ -201,7 +226,15 @@ __global__ __launch_bounds__(64) void k_nav(const Cst<T> C, const NavArgs<T> g)
             r += g.shared ? sum : shp;
             const T fin = all_og ? g.final_rew : T(0);
             g.reward[i] = r + fin;
-            if (agent == 0) g.done[env] = all_og ? 1 : 0;
+            if (agent == 0) {
+                g.done[env] = all_og ? 1 : 0;
+                // the env's step counter and time limit (a step pass)
+                if (g.step_count != nullptr && g.advance_prev) {
+                    const int sc = g.step_count[env] + 1;
+                    g.step_count[env] = sc;
+                    if (g.truncated) g.truncated[env] = (g.max_steps > 0 && sc >= g.max_steps) ? 1 : 0;
+                }
+            }
         }
     }
 }

@@ -1047,7 +1047,10 @@ template <typename T> static int nav_obs(const swarp_desc_t *d, const swarp_nav_
     g.advance_prev = v->advance_prev ? 1 : 0;
     g.full_pass = v->full_pass ? 1 : 0;
     g.shared = v->shared_reward ? 1 : 0;
-    const size_t lds = (size_t)64 * g.W * sizeof(T);
+    g.step_count = v->step_count;
+    g.truncated = v->truncated;
+    g.max_steps = v->max_steps;
+    const size_t lds = (size_t)64 * g.W * sizeof(T) + (size_t)64 * d->max_neighbors * 4;
     g.stage = lds <= 48 * 1024 ? 1 : 0;  // rows leave through LDS when they fit
     const unsigned dyn = g.stage ? (unsigned)lds : 0u;
     const int PA = pad_agents(d->n_agents);

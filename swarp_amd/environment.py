@@ -1,14 +1,21 @@
 """``Environment`` and ``make``: the vectorised multi-agent environment over a Scenario
 (``swarp/core/environment.py:17-749``, ``swarp/__init__.py:95-121``).
 
-``step`` advances the world through the HIP step (differentiable end to end when
-something requires grad: dynamics through the hand-written adjoint, observations and
-rewards through torch autograd) and returns the Gymnasium 5-tuple ``(obs, reward,
-terminated, truncated, info)``.  ``auto_reset=True`` resets finished envs in place with
-a masked, host-sync-free reset.  The reference's whole-step CUDA-graph runtime and fused
-obs/reward kernels are not part of this build: ``use_graph`` and ``fused`` are accepted
-and every step takes the functional path (``graph_mode`` is always False; an explicit
-``use_graph=True`` warns, as the reference does when capture is unavailable).
+``step`` advances the world through the HIP step and returns the Gymnasium 5-tuple
+``(obs, reward, terminated, truncated, info)``.  Three paths, chosen per step as the
+reference chooses them (``swarp/core/environment.py:155-182, 395-421``):
+* a differentiated step (grad mode on and something requires grad): the functional
+  step with its hand-written adjoint, observations and rewards through torch autograd;
+* an untaped step with ``fused``: the step, then the scenario's fused HIP pass;
+* an untaped step with ``use_graph=True``: the step and the fused pass (which also
+  advances the step counter) replayed as one HIP graph (``swarp_amd.persistent.StepGraph``).
+  ``"auto"`` leaves the graph off: on MI355X a replay of the two-node graph costs more
+  host time than the two eager launches it replaces (measured with the reference's
+  throughput grid, ``swarp_amd.throughput``), unlike the many-launch step the reference
+  captures on CUDA.
+``auto_reset=True`` resets finished envs in place with a masked, host-sync-free reset,
+run eagerly after the step (the reference folds it into its graph for scenarios whose
+reset kernels are capturable; here the reset's sampler is torch on the world generator).
 """
 
 from __future__ import annotations
@@ -20,6 +27,7 @@ from typing import Any
 import torch
 
 from .config import WorldConfig, action_bounds
+from .persistent import StepGraph
 from .scenarios import SCENARIOS, Scenario, make_scenario
 
 
@@ -52,9 +60,6 @@ class Environment:
                 f"device {self.device!r} requested but no HIP device is visible; pass "
                 "device='cpu' to build and reset on the host (stepping needs the GPU)"
             )
-        if use_graph is True:
-            warnings.warn("use_graph=True: this build has no whole-step graph runtime; "
-                          "stepping on the functional path", RuntimeWarning, stacklevel=2)
         self.dtype = dtype
         self.max_steps = max_steps
         self.auto_reset = auto_reset
@@ -70,6 +75,22 @@ class Environment:
         self._never_truncated = torch.zeros(n_envs, device=self.device, dtype=torch.bool)
         self._truncated_buf = torch.zeros(n_envs, device=self.device, dtype=torch.bool)
         self._episode_end_buf = torch.zeros(n_envs, device=self.device, dtype=torch.bool)
+        # whole-step graph (environment.py:166-170); "auto" keeps it off: the eager step is
+        # two launches, which replay no faster as a graph on this platform
+        st = self.world.stepper
+        coverable = (self._fused and self.device.startswith("cuda") and not st.has_drone
+                     and not st.any_movable)
+        want = False if use_graph == "auto" else bool(use_graph)
+        if want and not coverable:
+            warnings.warn("use_graph=True: this world cannot be captured (needs the fused "
+                          "pass on a HIP device, 2-D agents, no movable bodies); stepping "
+                          "eagerly", RuntimeWarning, stacklevel=2)
+            want = False
+        self._graph = StepGraph(self.world, hook=self._graph_hook,
+                                token=self._graph_token) if want else None
+        if self._fused and hasattr(scenario, "attach_counter"):
+            # the fused step pass advances the step counter and writes the time limit
+            scenario.attach_counter(self._step_count, self._truncated_buf, self.max_steps)
 
     # ------------------------------------------------------------------ seeding
 
@@ -90,7 +111,30 @@ class Environment:
 
     @property
     def graph_mode(self) -> bool:
-        return False
+        """Whether untaped steps replay the whole-step graph."""
+        return self._graph is not None
+
+    def _graph_hook(self, state_out, stream: int, warm: bool) -> None:
+        """Post-physics work of a graph step: the fused pass, whose step variant also
+        advances the shaping baseline, the step counter and the time limit
+        (``step_count_kernel``); the warm-up launch before a capture does none of those."""
+        import ctypes
+
+        from . import _lib
+
+        sc = self.scenario
+        nav = sc.fused_nav(state_out, advance_prev=0 if warm else 1, full_pass=1, reset_mask=None)
+        desc = self.world.stepper.desc(self.n_envs, self.world.act_dim)
+        _lib.check(_lib.load().swarp_nav_obs(ctypes.byref(desc), ctypes.byref(nav),
+                                             ctypes.c_void_p(stream)))
+
+    def _graph_token(self) -> tuple:
+        """Pointers the captured pass bakes in besides the step's (recapture on a move)."""
+        sc, w = self.scenario, self.world
+        fb = sc.ensure_fused()
+        grid = w.stepper.grid(self.n_envs)
+        return (w.goals.data_ptr(), sc._prev_dist.data_ptr(), fb["obs"].data_ptr(),
+                grid.neighbor_idx.data_ptr(), sc._k_obs)
 
     @property
     def obs_dim(self) -> int:
@@ -196,13 +240,22 @@ class Environment:
             raise TypeError(f"actions dtype {actions.dtype} != env dtype {self.dtype}")
         self._set_fused_active(actions)
         self.world.action = actions
-        self.world.step(actions)
-        self.scenario.post_step()
-        reward = self.scenario.rewards()
-        self._step_count += 1
-        terminated = self.scenario.done()
+        sc = self.scenario
+        counted = getattr(sc, "counts_steps", False)
+        if self._graph is not None and sc.fused_active:
+            # step + fused pass (incl. step counter / time limit): one replay
+            self._graph.step(actions)
+            sc._fresh = "fused"
+        else:
+            self.world.step(actions)
+            sc.post_step()
+            if not counted:
+                self._step_count += 1
+        reward = sc.rewards()
+        terminated = sc.done()
         if self.max_steps is not None:
-            truncated = torch.ge(self._step_count, self.max_steps, out=self._truncated_buf)
+            truncated = (self._truncated_buf if counted else
+                         torch.ge(self._step_count, self.max_steps, out=self._truncated_buf))
         else:
             truncated = self._never_truncated
         info = self.scenario.info()

@@ -96,7 +96,7 @@ class NeighborGrid:
                 raise TypeError("neighbour buffers must be contiguous int32")
         pos = pos.contiguous()
         lib = _lib.load()
-        stream = torch.cuda.current_stream(pos.device).cuda_stream
+        stream = _lib.stream_of(pos.device)
         _lib.check(lib.swarp_neighbors(
             ctypes.byref(self._desc), pos.data_ptr(), neighbor_idx.data_ptr(),
             neighbor_count.data_ptr(), self.neighbor_true_count.data_ptr(), stream,
@@ -124,7 +124,7 @@ class NeighborGrid:
             return out
         offsets = (incl - cnt).contiguous()
         lib = _lib.load()
-        stream = torch.cuda.current_stream(out.device).cuda_stream
+        stream = _lib.stream_of(out.device)
         _lib.check(lib.swarp_edge_index(
             self.n_envs, self.n_agents, self.max_neighbors, self.neighbor_idx.data_ptr(),
             self.neighbor_count.data_ptr(), offsets.data_ptr(), n_edges, out.data_ptr(), stream,

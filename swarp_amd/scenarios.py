@@ -186,6 +186,10 @@ class NavigationScenario(Scenario):
         self._prev_dist: torch.Tensor | None = None
         self._fb: dict[str, torch.Tensor] | None = None   # fused-pass buffers
         self._fresh = "torch"   # which path wrote the current obs / reward
+        self._navs: dict[tuple, _lib.SwarpNav] = {}      # swarp_nav_t per pointer set
+        # (step_count int32 [E], truncated bool [E] or None, max_steps): the episode
+        # counter the fused step pass advances (attached by Environment)
+        self._counter: tuple | None = None
 
     # ------------------------------------------------------------------ world
 
@@ -222,6 +226,7 @@ class NavigationScenario(Scenario):
         self._prev_dist = None
         self._fb = None
         self._fresh = "torch"
+        self._navs = {}
         if self.n_obstacles > 0:
             tt = {"device": device, "dtype": dtype}
             self.world.set_obstacles(Obstacles(
@@ -276,11 +281,11 @@ class NavigationScenario(Scenario):
         if self.n_obstacles > 0:
             lim = self.world_size - self.obstacle_radius
             opos = w.sample_uniform((n, self.n_obstacles, 2), -lim, lim)
+            # in place: the stepper reads this very tensor (static circles, nothing to seed)
             if env_mask is None:
                 w.obstacle_pos.copy_(opos)
             else:
                 w.obstacle_pos.copy_(torch.where(env_mask.view(-1, 1, 1), opos, w.obstacle_pos))
-            w.set_obstacles(w.obstacles)
         # a full reset rebases every env's shaping baseline
         mask = env_mask if env_mask is not None else torch.ones(n, dtype=torch.bool,
                                                                 device=w.device)
@@ -321,8 +326,33 @@ class NavigationScenario(Scenario):
             self._prev_dist = torch.zeros(w.n_envs, w.n_agents, device=w.device, dtype=w.dtype)
         return self._fb
 
+    def attach_counter(self, step_count: torch.Tensor, truncated: torch.Tensor | None,
+                       max_steps: int | None) -> None:
+        """Let the fused step pass advance ``step_count`` and write ``truncated``
+        (``step_count >= max_steps``) in the same launch."""
+        self._counter = (step_count, truncated, max_steps)
+        self._navs = {}
+
+    @property
+    def counts_steps(self) -> bool:
+        """Whether a fused step pass advances the attached episode counter."""
+        return self.fused_active and self._counter is not None
+
     def fused_nav(self, state, advance_prev: int, full_pass: int, reset_mask) -> _lib.SwarpNav:
-        """The ``swarp_nav_t`` of one pass over ``state`` (pointers only; no launch)."""
+        """The ``swarp_nav_t`` of one pass over ``state`` (pointers only; no launch).
+        Cached per pointer set: a step alternates between two output buffers."""
+        key = (state.pos.data_ptr(), state.vel.data_ptr(), state.theta.data_ptr(),
+               state.ang_vel.data_ptr(), int(advance_prev), int(full_pass),
+               None if reset_mask is None else reset_mask.data_ptr())
+        nav = self._navs.get(key)
+        if nav is None:
+            nav = self._make_nav(state, advance_prev, full_pass, reset_mask)
+            if len(self._navs) > 16:
+                self._navs.clear()
+            self._navs[key] = nav
+        return nav
+
+    def _make_nav(self, state, advance_prev: int, full_pass: int, reset_mask) -> _lib.SwarpNav:
         w = self.world
         fb = self.ensure_fused()
         grid = w.stepper.grid(w.n_envs)
@@ -345,6 +375,11 @@ class NavigationScenario(Scenario):
         nav.goal_tolerance = float(self.goal_tolerance)
         nav.collision_penalty = float(self.collision_penalty)
         nav.final_reward = float(self.final_reward)
+        if self._counter is not None and advance_prev and full_pass:
+            sc, tr, ms = self._counter
+            nav.step_count = p(sc)
+            nav.truncated = None if (tr is None or ms is None) else p(tr)
+            nav.max_steps = 0 if ms is None else int(ms)
         return nav
 
     def launch_fused(self, advance_prev: int, full_pass: int,
@@ -365,9 +400,8 @@ class NavigationScenario(Scenario):
         nav = self.fused_nav(st, advance_prev, full_pass, rm)
         desc = w.stepper.desc(w.n_envs, w.act_dim)
         lib = _lib.load()
-        stream = torch.cuda.current_stream(st.pos.device).cuda_stream
         _lib.check(lib.swarp_nav_obs(ctypes.byref(desc), ctypes.byref(nav),
-                                     ctypes.c_void_p(stream)))
+                                     ctypes.c_void_p(_lib.stream_of(st.pos.device))))
         w.lists_built_on(st.pos)
         self._fresh = "fused"
 
