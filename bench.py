@@ -58,6 +58,9 @@ def parse():
     ap.add_argument("--env-steps", type=int, default=100,
                     help="timed Environment.step calls of the no-grad navigation leg "
                          "(16000 x 16, graph on and off); 0 skips it")
+    ap.add_argument("--workload", default="c2", choices=("c2", "c3", "c4", "c5"),
+                    help="BASELINE.json config to time: c2 (the headline, default), c3 mixed "
+                         "fleet + obstacles, c4 drones, c5 movable body + per-step lists/COO")
     ap.add_argument("--copy-mb", type=int, default=0,
                     help="after the benchmark, run 3 plain device copies of this many MiB "
                          "(calibrates rocprof byte counters against a known traffic)")
@@ -133,6 +136,183 @@ def cpu_baseline(E_full, A, T, S, seconds, cfgs, world):
     }
 
 
+def _c3(seed=0):
+    """4096 x 32 mixed fleet (16 diff-drive velocity control, 16
+    kinematic bicycles), headings U[-pi, pi], per-env static obstacles (4 circles r
+    U[0.05, 0.2], 2 axis-aligned boxes half-extent U[0.05, 0.3], 2 segments length
+    U[0.2, 0.8]) uniform in [-2, 2]^2, 4 substeps, 20-step BPTT."""
+    import torch
+
+    from swarp_amd import (AgentConfig, DynamicsModel, Obstacles, ObstacleShape, Stepper,
+                           TorchState, WorldConfig)
+
+    E, A, T, S, r = 4096, 32, 20, 4, 0.05
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    u = lambda *sh, lo=0.0, hi=1.0: torch.rand(*sh, generator=g) * (hi - lo) + lo  # noqa: E731
+    cfgs = ([AgentConfig(model=DynamicsModel.DIFF_DRIVE, radius=r) for _ in range(16)]
+            + [AgentConfig(model=DynamicsModel.KINEMATIC_BICYCLE, radius=r) for _ in range(16)])
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.5 * r,
+                        bounds=(-2.0, 2.0, -2.0, 2.0), bounds_mode="soft", max_neighbors=32)
+    st = Stepper(cfgs, dt=0.05, substeps=S, device="cuda:0", dtype=torch.float32, world=world)
+    seg_len = u(2, lo=0.2, hi=0.8)
+    st.set_obstacles(Obstacles(
+        pos=u(E, 8, 2, lo=-2.0, hi=2.0),
+        radius=torch.cat([u(4, lo=0.05, hi=0.2), torch.zeros(2), torch.full((2,), 0.02)]),
+        shape=torch.tensor([int(ObstacleShape.CIRCLE)] * 4 + [int(ObstacleShape.BOX)] * 2
+                           + [int(ObstacleShape.SEGMENT)] * 2, dtype=torch.int32),
+        angle=torch.cat([torch.zeros(E, 6), u(E, 2, lo=-3.14159, hi=3.14159)], 1),
+        half_extents=torch.cat([torch.zeros(4, 2), u(2, 2, lo=0.05, hi=0.3),
+                                torch.stack([0.5 * seg_len, torch.zeros(2)], 1)]),
+    ))
+    c = lambda t: t.cuda()  # noqa: E731
+    z = torch.zeros(E, A)
+    state = TorchState(c(u(E, A, 2, lo=-2.0, hi=2.0)), c(u(E, A, lo=-3.14159, hi=3.14159)),
+                       c(torch.zeros(E, A, 2)), c(z.clone()), c(z.clone()))
+    acts = c(u(T, E, A, 2, lo=-1.0, hi=1.0))
+    goals = c(u(E, A, 2, lo=-2.0, hi=2.0))
+    fwd = 4 * A * (2 * 7 + 2) + 8 * 6 * 4
+    bwd = 4 * A * (3 * 7 + 2 * 2) + 8 * 6 * 4
+    desc = "mixed fleet 4096 envs x 32 agents (diff-drive + bicycle), 8 obstacles, 4 substeps, 20-step BPTT (BASELINE configs[2])"
+    return st, state, acts, goals, fwd, bwd, desc, None
+
+
+def _c4(seed=0):
+    """8192 x 8 quadrotors, rotor thrusts U[0, 1] x thrust_max,
+    attitude axis uniform on the sphere with angle U[0, 0.1], planar contacts r = 0.1,
+    64-step BPTT (dt 0.02, 1 substep)."""
+    import math
+
+    import torch
+
+    from swarp_amd import AgentConfig, DynamicsModel, Stepper, TorchState, WorldConfig
+
+    E, A, T, S = 8192, 8, 64, 1
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    cfgs = [AgentConfig(model=DynamicsModel.DRONE, radius=0.1) for _ in range(A)]
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02)
+    st = Stepper(cfgs, dt=0.02, substeps=S, device="cuda:0", dtype=torch.float32, world=world)
+    ax = torch.randn(E, A, 3, generator=g)
+    ax = ax / ax.norm(dim=-1, keepdim=True)
+    ang = torch.rand(E, A, 1, generator=g) * 0.1
+    q = torch.cat([ax * torch.sin(ang / 2), torch.cos(ang / 2)], -1)
+    c = lambda t: t.contiguous().cuda()  # noqa: E731
+    z = torch.zeros(E, A)
+    state = TorchState(c((torch.rand(E, A, 2, generator=g) * 2 - 1) * math.sqrt(A) * 0.25),
+                       c(z), c(torch.zeros(E, A, 2)), c(z), c(z), c(torch.ones(E, A)), c(z), c(q),
+                       c(torch.zeros(E, A, 3)))
+    acts = c(torch.rand(T, E, A, 4, generator=g) * cfgs[0].thrust_max)
+    goals = c(torch.rand(E, A, 2, generator=g) * 2 - 1)
+    fwd, bwd = 4 * A * (2 * 16 + 4), 4 * A * (3 * 16 + 2 * 4)
+    desc = "drones 8192 envs x 8 quadrotors, 64-step BPTT, dt 0.02 (BASELINE configs[3])"
+    return st, state, acts, goals, fwd, bwd, desc, None
+
+
+def _c5(seed=0):
+    """16000 x 64 agents pushing a movable cross (5 circles r 0.1,
+    mass 1, inertia from the geometry), lists of radius 0.3 capped at K = 16 with the
+    overflow flag and the COO radius graph emitted every step, positions U[-3, 3]^2,
+    16-step BPTT, loss = squared body distance to a uniform-random goal."""
+    import torch
+
+    from swarp_amd import AgentConfig, Obstacles, Stepper, TorchState, WorldConfig
+
+    E, A, T, S, r = 16000, 64, 16, 4, 0.05
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    cfgs = [AgentConfig(radius=r, max_speed=1.0, max_accel=2.0) for _ in range(A)]
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.5 * r,
+                        bounds=(-3.0, 3.0, -3.0, 3.0), bounds_mode="soft", neighbor_radius=0.3,
+                        max_neighbors=16)
+    st = Stepper(cfgs, dt=0.05, substeps=S, device="cuda:0", dtype=torch.float32, world=world)
+    d, rb, m = 0.2, 0.1, 1.0
+    offs = torch.tensor([[0.0, 0.0], [d, 0.0], [-d, 0.0], [0.0, d], [0.0, -d]])
+    inertia = float(sum(0.5 * (m / 5) * rb * rb + (m / 5) * float(o @ o) for o in offs))
+    st.set_obstacles(Obstacles(
+        pos=offs.unsqueeze(0).expand(E, 5, 2).contiguous(), radius=torch.full((5,), rb),
+        kind=torch.ones(5, dtype=torch.int32), body=torch.zeros(5, dtype=torch.int32),
+        mass=torch.full((5,), m), inertia=torch.full((5,), inertia), body_offset=offs))
+    c = lambda t: t.contiguous().cuda()  # noqa: E731
+    z = torch.zeros(E, A)
+    state = TorchState(c((torch.rand(E, A, 2, generator=g) * 2 - 1) * 3.0), c(z),
+                       c(torch.zeros(E, A, 2)), c(z), c(z))
+    acts = c(torch.rand(T, E, A, 2, generator=g) * 2 - 1)
+    goals = c((torch.rand(E, 2, generator=g) * 2 - 1) * 2.0)
+    fwd = 4 * A * (2 * 7 + 2) + 48 + 4 * A * (16 + 2)
+    bwd = 4 * A * (3 * 7 + 2 * 2) + 72
+    desc = ("movable cross body, 16000 envs x 64 agents, r_nbr 0.3 / K 16 lists + overflow "
+            "+ COO every step, 4 substeps, 16-step BPTT (BASELINE configs[4])")
+    return st, state, acts, goals, fwd, bwd, desc, "body"
+
+
+def run_other(args):
+    """Time one BPTT iteration of BASELINE configs[2..4] through the public API and print
+    the same JSON line as the headline run (no CPU baseline, no Environment leg)."""
+    import torch
+
+    import swarp_amd.autograd as ag
+    from swarp_amd import TorchState, rollout
+
+    st, state, acts, goals, fwd_b, bwd_b, desc, kind = {"c3": _c3, "c4": _c4, "c5": _c5}[args.workload]()
+    T, E, A = acts.shape[:3]
+    a = acts.clone().requires_grad_(True)
+    s0 = TorchState(state.pos.clone().requires_grad_(True), *state[1:])
+    ob0 = st.ob_state.clone() if kind == "body" else None
+    grid = st.grid(E) if kind == "body" else None
+
+    def step():
+        a.grad = None
+        s0.pos.grad = None
+        if kind == "body":
+            st.ob_state = ob0.clone().requires_grad_(True)
+        final, traj = rollout(st, s0, a)
+        if kind == "body":
+            body = st.ob_trajectory[-1][:, 30:32]   # the body rooted at shape 0: position
+            loss = ((body - goals) ** 2).sum()
+            with torch.no_grad():                  # lists, overflow and COO of every step
+                for x in traj:
+                    grid.build(x.pos)
+                    grid.overflow_view()
+                    grid.edge_index()
+        else:
+            loss = ((final.pos - goals) ** 2).sum()
+        loss.backward()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ag.KERNEL_EVENTS = []
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    events, ag.KERNEL_EVENTS = ag.KERNEL_EVENTS, None
+    dur = {"fwd": [], "bwd": []}
+    for k, e0, e1 in events:
+        dur[k].append(e0.elapsed_time(e1) * 1e-3)
+    kernels = {}
+    for k, per in (("fwd", fwd_b), ("bwd", bwd_b)):
+        d = sum(dur[k]) / max(len(dur[k]), 1)
+        alg = per * E * T
+        kernels[k] = {"avg_ms": d * 1e3, "alg_bytes_per_launch": alg,
+                      "achieved_GBps": alg / d / 1e9 if d > 0 else None,
+                      "frac": alg / d / HBM_PEAK if d > 0 else None}
+    dom = max(kernels, key=lambda k: kernels[k]["avg_ms"])
+    out = {
+        "metric": "fwd+bwd BPTT env-steps/s", "value": E * T * args.steps / el,
+        "unit": "env-steps/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": el / args.steps * 1e3, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": desc, "n_envs": E, "n_agents": A, "horizon": T},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": kernels[dom]["achieved_GBps"],
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": kernels[dom]["frac"],
+                     "traffic": None},
+        "fwd_bwd_kernel_roofline_frac": (fwd_b + bwd_b) * E * T / (
+            (kernels["fwd"]["avg_ms"] + kernels["bwd"]["avg_ms"]) * 1e-3) / HBM_PEAK,
+        "kernels": kernels,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -140,6 +320,9 @@ def main():
               "is not supported: the step shards over envs with no exchange, see DESIGN.md.",
               file=sys.stderr)
         sys.exit(2)
+    if args.workload != "c2":
+        run_other(args)
+        return
     import torch
 
     import swarp_amd.autograd as ag
