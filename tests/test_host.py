@@ -267,3 +267,23 @@ def test_environment_validates_actions_before_any_launch():
         env.step(torch.zeros(3, 2, 3))
     with pytest.raises(TypeError, match="dtype"):
         env.step(torch.zeros(3, 2, 2, dtype=torch.float64))
+
+
+def test_compile_registry_does_not_keep_the_stepper_alive():
+    """The custom op's handle registry holds steppers weakly (swarp/interop/compile.py:45-90;
+    the reference's tests/interop/test_compile.py:91-113)."""
+    import gc
+    import weakref
+
+    from swarp_amd import compile as compile_mod
+
+    st = Stepper([AgentConfig() for _ in range(2)], device="cpu")
+    handle = compile_mod.register_stepper(st)
+    assert compile_mod.register_stepper(st) == handle
+    ref = weakref.ref(st)
+    del st
+    gc.collect()
+    assert ref() is None and handle not in compile_mod._STEPPERS
+    with pytest.raises(RuntimeError, match="garbage-collected"):
+        compile_mod._stepper(handle)
+    assert hasattr(torch.ops.swarp_amd, "step")
