@@ -130,13 +130,21 @@ __device__ __forceinline__ void lean_forces(const Cst<T> &C, const P2<T> *lp, co
 //   rec [T][workgroup][chunk][lane] 16-byte chunks: per step and lane one record of
 //       TapeRec::R bytes (NC = R / 16 chunks) holding
 //       TAPE_MAX_S mask words   per substep the inclusion mask (uncapped lists) and the
-//                               active-contact mask, packed as one TapeW word
+//                               active-contact mask, packed as one TapeW word; an agent is
+//                               never its own neighbour, so its own bit carries the
+//                               substep's wall-contact bits (x in the inclusion mask, y in
+//                               the active mask)
 //       TAPE_MAX_S - 1 pairs    input velocity of substeps 1..S-1 (positions follow exactly
 //                               as p_{s+1} = p_s + v_{s+1} * sub_dt, the forward's own update)
-//       one 32-bit word         wall-contact bits, 2 per substep
 //   vl  [workgroup][lane] pairs output velocity of the last step (the backward takes no
 //                               final state; every other step's output velocity is a
 //                               checkpoint)
+// The velocity after substep s is the step's clamped command plus F_s dt / m, and F_s is
+// exactly +0 when substep s has no active contact and no wall bit (every term is +-0 and
+// the sum starts at +0).  Such velocities are not stored: the forward writes a velocity
+// chunk only for the lanes whose masks say a force acted, the backward loads it only
+// for those lanes and otherwise rebuilds the velocity as command + 0 -- the same bits.
+// Most lanes feel no force in most steps, so most velocity cache lines are never moved.
 // Slots past the configuration's substep count are left unwritten.  The tape is private
 // to the two kernels, so it is indexed by lane rather than by agent: each 16-byte chunk
 // store of the forward and load of the backward moves 1 KB of contiguous memory per wave.
@@ -178,11 +186,24 @@ template <> struct TapeW<64> {
 template <typename T, int PA> struct TapeRec {
     typedef typename TapeW<PA>::type W;
     static constexpr int OM = 0;
-    static constexpr int OV = TAPE_MAX_S * (int)sizeof(W);
-    static constexpr int OW = OV + (TAPE_MAX_S - 1) * (int)sizeof(P2<T>);
-    static constexpr int R = (OW + 4 + 15) / 16 * 16;
+    static constexpr int OV = TAPE_MAX_S * (int)sizeof(W);  // a multiple of 16
+    static constexpr int R = (OV + (TAPE_MAX_S - 1) * (int)sizeof(P2<T>) + 15) / 16 * 16;
     static constexpr int NC = R / 16;
+    static constexpr int NM = OV / 16;  // chunks of mask words, always stored and loaded
+    // chunk holding the velocity of substep j + 1
+    static constexpr __device__ __forceinline__ int vchunk(int j)
+    {
+        return (OV + j * (int)sizeof(P2<T>)) / 16;
+    }
 };
+
+// Whether the velocity after substep s was stored: a force may have acted (an active
+// contact or a wall bit; the record's own-bit convention above).
+template <int PA, typename W>
+__device__ __forceinline__ bool vel_stored(const W &w, int me)
+{
+    return TapeW<PA>::act(w) != 0 || ((TapeW<PA>::incl(w) >> me) & 1) != 0;
+}
 
 struct alignas(16) Chunk16 {
     uint32_t d[4];
@@ -243,7 +264,7 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
         P2<T> an = a;
         if (t + 1 < g.nsteps) an = ld2(g.act, (size_t)(t + 1) * EA + i);
         M cand = 0, incl = 0, act = 0;
-        unsigned wb = 0u, wbits = 0u;
+        unsigned wb = 0u, vneed = 0u;
         T D = T(0);
         bool ok = false;
         for (int s = 0; s < C.S; ++s) {
@@ -261,9 +282,13 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
             const T vnx = cnx + Fx * dtm, vny = cny + Fy * dtm;
             const T pnx = p.x + vnx * dt, pny = p.y + vny * dt;
             if (TAPE) {
-                stage_put(tsb, lane, TR::OM + s * (int)sizeof(typename TW::type), TW::pack(incl, act));
-                wbits |= wb << (2 * s);
-                if (s + 1 < C.S) stage_put(tsb, lane, TR::OV + s * (int)sizeof(P2<T>), P2<T>{vnx, vny});
+                const M own = M(1) << me;
+                stage_put(tsb, lane, TR::OM + s * (int)sizeof(typename TW::type),
+                          TW::pack(incl | ((wb & 1u) ? own : M(0)), act | ((wb & 2u) ? own : M(0))));
+                if (s + 1 < C.S) {
+                    stage_put(tsb, lane, TR::OV + s * (int)sizeof(P2<T>), P2<T>{vnx, vny});
+                    vneed |= (act != 0 || wb != 0u) ? 1u << TR::vchunk(s) : 0u;
+                }
             }
             if (C.use_skin) {
                 D += (m_abs(pnx - p.x) + m_abs(pny - p.y)) * T(1.0001);
@@ -289,13 +314,13 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
             f[4][j] = T(0);
         }
         if (TAPE) {
-            stage_put(tsb, lane, TR::OW, (uint32_t)wbits);
             Chunk16 c[TR::NC];
 #pragma unroll
             for (int k = 0; k < TR::NC; ++k) c[k] = tst[k * 64 + lane];
             Chunk16 *dst = (Chunk16 *)tp.rec + ((size_t)t * gridDim.x + blockIdx.x) * TR::NC * 64 + lane;
 #pragma unroll
-            for (int k = 0; k < TR::NC; ++k) dst[k * 64] = c[k];
+            for (int k = 0; k < TR::NC; ++k)
+                if (k < TR::NM || ((vneed >> k) & 1u)) dst[k * 64] = c[k];
             if (t + 1 == g.nsteps) st2(tp.vl, (size_t)blockIdx.x * 64 + lane, v.x, v.y);
         }
     }
@@ -361,18 +386,36 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
     struct Tp {
         Chunk16 c[TR::NC];
     };
-    auto tape_of = [&](int tt) {
-        Tp r;
-        const Chunk16 *src =
-            (const Chunk16 *)tp.rec + ((size_t)tt * gridDim.x + blockIdx.x) * TR::NC * 64 + lane;
-#pragma unroll
-        for (int k = 0; k < TR::NC; ++k) r.c[k] = src[k * 64];
-        return r;
+    auto rec_of = [&](int tt) {
+        return (const Chunk16 *)tp.rec + ((size_t)tt * gridDim.x + blockIdx.x) * TR::NC * 64 + lane;
     };
-    Tp tc;
+    // the mask chunks of step tt (issued two steps ahead of use)
+    auto masks_into = [&](int tt, Tp &r) {
+        const Chunk16 *src = rec_of(tt);
+#pragma unroll
+        for (int k = 0; k < TR::NM; ++k) r.c[k] = src[k * 64];
+    };
+    // the velocity chunks of step tt that the forward stored (issued one step ahead)
+    auto vels_into = [&](int tt, Tp &r) {
+        const Chunk16 *src = rec_of(tt);
+        unsigned need = 0u;
+#pragma unroll
+        for (int j = 0; j + 1 < TAPE_MAX_S; ++j)
+            if (j + 1 < C.S && vel_stored<PA>(rec_get<W>(r.c, TR::OM + j * (int)sizeof(W)), me))
+                need |= 1u << TR::vchunk(j);
+#pragma unroll
+        for (int k = TR::NM; k < TR::NC; ++k) {
+            Chunk16 x = {};
+            if (((need >> k) & 1u) && active) x = src[k * 64];
+            r.c[k] = x;
+        }
+    };
+    Tp tc, tn;
     P2<T> vout = {T(0), T(0)};  // output velocity of step t (TAPE)
     if (TAPE) {
-        tc = tape_of(t);
+        masks_into(t, tc);
+        vels_into(t, tc);
+        if (t > 0) masks_into(t - 1, tn);
         vout = ld2(tp.vl, (size_t)blockIdx.x * 64 + lane);
     }
     // resolve the initial loads here: a load still in flight at the loop entry makes every
@@ -394,10 +437,10 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
             an = ld2(g.act, (size_t)(t - 1) * EA + i);
             arn = arrival(t - 1);
         }
-        Tp tn;
-        if (TAPE) {
-            tn = tc;
-            if (t > 0) tn = tape_of(t - 1);
+        Tp tnn;
+        if (TAPE && t > 0) {
+            vels_into(t - 1, tn);
+            if (t > 1) masks_into(t - 2, tnn);
         }
         if (!real) p.x = p.y = qnan;
         T cnx, cny;
@@ -408,7 +451,6 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
         if (TAPE) {
             __syncthreads();  // the previous step's reverse pass is done with the slots
             P2<T> pp = p, vv = v;
-            const unsigned wall = active ? rec_get<uint32_t>(tc.c, TR::OW) : 0u;
 #pragma unroll
             for (int s = 0; s < TAPE_MAX_S; ++s) {
                 if (s < C.S) {
@@ -416,11 +458,18 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
                     sp[lane] = pp;
                     sp[64 + lane] = vv;
                     const W w = rec_get<W>(tc.c, TR::OM + s * (int)sizeof(W));
-                    lm[s * 64 + lane] = active ? (M)TW::incl(w) : M(0);
-                    la[s * 64 + lane] = active ? (M)TW::act(w) : M(0);
-                    lw[s * 64 + lane] = (unsigned char)((wall >> (2 * s)) & 3u);
+                    const M own = M(1) << me;
+                    const M in = (M)TW::incl(w), ac = (M)TW::act(w);
+                    lm[s * 64 + lane] = active ? (in & ~own) : M(0);
+                    la[s * 64 + lane] = active ? (ac & ~own) : M(0);
+                    lw[s * 64 + lane] = active ? (unsigned char)(((in & own) ? 1u : 0u) |
+                                                                 ((ac & own) ? 2u : 0u))
+                                               : (unsigned char)0;
                     if (s + 1 < TAPE_MAX_S && s + 1 < C.S) {
-                        vv = rec_get<P2<T>>(tc.c, TR::OV + s * (int)sizeof(P2<T>));
+                        // a stored velocity, or the command plus the exactly-zero force term
+                        vv = (active && vel_stored<PA>(w, me))
+                                 ? rec_get<P2<T>>(tc.c, TR::OV + s * (int)sizeof(P2<T>))
+                                 : P2<T>{cnx + T(0), cny + T(0)};
                         pp.x = pp.x + vv.x * dt;
                         pp.y = pp.y + vv.y * dt;
                     }
@@ -537,6 +586,7 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
         if (TAPE) {
             vout = vin;
             tc = tn;
+            tn = tnn;
         }
     }
     if (active) {

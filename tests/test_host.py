@@ -76,8 +76,9 @@ def test_library_rejects_bad_descriptor_without_gpu():
 def test_tape_size_without_gpu():
     """Rollout tape size (a host computation): one record per step and lane of every
     workgroup (64 / PA envs each, PA = agents padded to a power of two) -- 4 mask words
-    (4 B up to 16 agents, 8 B up to 32, 16 B up to 64), 3 velocity pairs, a 32-bit wall
-    word, padded to 16 B -- then the last step's velocities, each region 256-byte aligned.
+    (4 B up to 16 agents, 8 B up to 32, 16 B up to 64; the wall bits ride in the agent's
+    own bits), 3 velocity pairs, padded to 16 B -- then the last step's velocities, each
+    region 256-byte aligned.
     No tape where the backward recomputes (generic kernels, more than 4 substeps, nothing
     to record)."""
     from cases import nav_agents, nav_world
@@ -90,11 +91,11 @@ def test_tape_size_without_gpu():
                        world=nav_world(A, **kw))
 
     E, T = 1000, 32
-    for A, PA, S, dtype, rec, pair in ((16, 16, 4, torch.float32, 48, 8),    # 16 + 24 + 4 -> 48
+    for A, PA, S, dtype, rec, pair in ((16, 16, 4, torch.float32, 48, 8),    # 16 + 24 -> 48
                                        (8, 8, 1, torch.float32, 48, 8),
-                                       (20, 32, 4, torch.float64, 96, 16),   # 32 + 48 + 4 -> 96
-                                       (40, 64, 2, torch.float32, 96, 8),    # 64 + 24 + 4 -> 96
-                                       (64, 64, 3, torch.float64, 128, 16)):  # 64 + 48 + 4 -> 128
+                                       (20, 32, 4, torch.float64, 80, 16),   # 32 + 48 -> 80
+                                       (40, 64, 2, torch.float32, 96, 8),    # 64 + 24 -> 96
+                                       (64, 64, 3, torch.float64, 112, 16)):  # 64 + 48 -> 112
         lanes = -(-E // (64 // PA)) * 64
         assert stepper(A, S, dtype).tape_bytes(E, 2, T) == al(T * lanes * rec) + al(lanes * pair), (A, S)
     # contacts without walls keep the same records; 10 envs of 8 agents fill 2 workgroups
