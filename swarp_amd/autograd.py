@@ -70,15 +70,17 @@ def fill_state_defaults(state: TorchState) -> TorchState:
         return state
     ref = state.pos
     e, a = ref.shape[0], ref.shape[1]
-    opts = {"device": ref.device, "dtype": ref.dtype}
-    z = state.z if state.z is not None else torch.zeros(e, a, **opts)
-    vz = state.vz if state.vz is not None else torch.zeros(e, a, **opts)
+    # the missing fields are disjoint views of one zeroed allocation (one fill, not four)
+    buf = torch.zeros(9 * e * a, device=ref.device, dtype=ref.dtype)
+    n = e * a
+    z = state.z if state.z is not None else buf[:n].view(e, a)
+    vz = state.vz if state.vz is not None else buf[n:2 * n].view(e, a)
     if state.attitude is not None:
         att = state.attitude
     else:
-        att = torch.zeros(e, a, 4, **opts)
+        att = buf[2 * n:6 * n].view(e, a, 4)
         att[..., 3] = 1.0
-    br = state.body_rates if state.body_rates is not None else torch.zeros(e, a, 3, **opts)
+    br = state.body_rates if state.body_rates is not None else buf[6 * n:].view(e, a, 3)
     return state._replace(z=z, vz=vz, attitude=att, body_rates=br)
 
 
@@ -352,7 +354,9 @@ def _assemble(stepper: Stepper, state: TorchState, outs, T: int):
     final_f = outs[:nf]
     traj_f = outs[nf:2 * nf]
     tail = tuple(state[nf:]) if nf == 5 else ()
-    traj = [TorchState(*(f[t] for f in traj_f), *tail) for t in range(T - 1)]
+    # one unbind per field (a single autograd node) instead of T - 1 selects per field
+    per_step = [f.unbind(0) for f in traj_f] if T > 1 else []
+    traj = [TorchState(*(u[t] for u in per_step), *tail) for t in range(T - 1)]
     final = TorchState(*final_f, *tail)
     traj.append(final)
     return final, traj
