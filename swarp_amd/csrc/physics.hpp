@@ -507,12 +507,12 @@ __device__ __forceinline__ void wall_force_adj(const Cst<T> &C, T px, T py, T vx
 // --------------------------------------------------------------- obstacles
 
 // box_force (swarp/core/collisions.py:174-260); reach = agent radius + margin
+// (ca, sa) = cos / sin of the box angle
 template <typename T>
-__device__ __forceinline__ void box_force(const Cst<T> &C, T px, T py, T vx, T vy, T cx0, T cy0,
-                                          T ang, T hx, T hy, T reach, T dd, T vox, T voy, T om,
-                                          T &fx, T &fy)
+__device__ __forceinline__ void box_force_cs(const Cst<T> &C, T px, T py, T vx, T vy, T cx0,
+                                             T cy0, T ca, T sa, T hx, T hy, T reach, T dd,
+                                             T vox, T voy, T om, T &fx, T &fy)
 {
-    T ca = m_cos(ang), sa = m_sin(ang);
     T dx = px - cx0, dy = py - cy0;
     T lx = ca * dx + sa * dy;
     T ly = -sa * dx + ca * dy;
@@ -548,11 +548,19 @@ __device__ __forceinline__ void box_force(const Cst<T> &C, T px, T py, T vx, T v
 }
 
 template <typename T>
-__device__ __forceinline__ void box_force_adj(const Cst<T> &C, T px, T py, T vx, T vy, T cx0,
-                                              T cy0, T ang, T hx, T hy, T reach, T dd, T vox,
-                                              T voy, T om, T gx, T gy, St<T> &a)
+__device__ __forceinline__ void box_force(const Cst<T> &C, T px, T py, T vx, T vy, T cx0, T cy0,
+                                          T ang, T hx, T hy, T reach, T dd, T vox, T voy, T om,
+                                          T &fx, T &fy)
 {
-    T ca = m_cos(ang), sa = m_sin(ang);
+    box_force_cs(C, px, py, vx, vy, cx0, cy0, m_cos(ang), m_sin(ang), hx, hy, reach, dd, vox,
+                 voy, om, fx, fy);
+}
+
+template <typename T>
+__device__ __forceinline__ void box_force_adj_cs(const Cst<T> &C, T px, T py, T vx, T vy, T cx0,
+                                                 T cy0, T ca, T sa, T hx, T hy, T reach, T dd,
+                                                 T vox, T voy, T om, T gx, T gy, St<T> &a)
+{
     T dx = px - cx0, dy = py - cy0;
     T lx = ca * dx + sa * dy;
     T ly = -sa * dx + ca * dy;
@@ -615,10 +623,36 @@ __device__ __forceinline__ void box_force_adj(const Cst<T> &C, T px, T py, T vx,
     a.py += sa * alx + ca * aly;
 }
 
+template <typename T>
+__device__ __forceinline__ void box_force_adj(const Cst<T> &C, T px, T py, T vx, T vy, T cx0,
+                                              T cy0, T ang, T hx, T hy, T reach, T dd, T vox,
+                                              T voy, T om, T gx, T gy, St<T> &a)
+{
+    box_force_adj_cs(C, px, py, vx, vy, cx0, cy0, m_cos(ang), m_sin(ang), hx, hy, reach, dd, vox,
+                     voy, om, gx, gy, a);
+}
+
+// cos / sin of obstacle j's angle: from the per-launch table when there is one.
+template <typename T>
+__device__ __forceinline__ void ob_trig(const Obs<T> &O, size_t j, int o, const T *cs, T &c, T &s)
+{
+    if (cs != nullptr) {
+        c = cs[2 * o];
+        s = cs[2 * o + 1];
+    } else {
+        const T ang = O.ang[j];
+        c = m_cos(ang);
+        s = m_sin(ang);
+    }
+}
+
 // One obstacle on one agent (_obstacle_forces body, swarp/core/collisions.py:690-743).
+// `cs`: this env's obstacle angles as (cos, sin) pairs [N][2], computed once per launch
+// (the angles do not change within one), or NULL to evaluate them here.
 template <typename T>
 __device__ __forceinline__ void obstacle_force(const Cst<T> &C, const Obs<T> &O, size_t eN, int o,
-                                               T px, T py, T vx, T vy, T ra, T dd, T &fx, T &fy)
+                                               T px, T py, T vx, T vy, T ra, T dd, T &fx, T &fy,
+                                               const T *cs = nullptr)
 {
     fx = T(0);
     fy = T(0);
@@ -630,12 +664,15 @@ __device__ __forceinline__ void obstacle_force(const Cst<T> &C, const Obs<T> &O,
     T lim = (ra + C.margin + bound) * T(1.0001) + T(1.0e-6);
     T ddx = px - cx, ddy = py - cy;
     if (ddx * ddx + ddy * ddy > lim * lim) return;
-    const T vox = O.vel[2 * j], voy = O.vel[2 * j + 1], om = O.om[j], ang = O.ang[j];
+    const T vox = O.vel[2 * j], voy = O.vel[2 * j + 1], om = O.om[j];
     if (st == 1) {
-        box_force(C, px, py, vx, vy, cx, cy, ang, hx, hy, ra + C.margin, dd, vox, voy, om, fx,
-                  fy);
+        T ca, sa;
+        ob_trig(O, j, o, cs, ca, sa);
+        box_force_cs(C, px, py, vx, vy, cx, cy, ca, sa, hx, hy, ra + C.margin, dd, vox, voy, om,
+                     fx, fy);
     } else if (st == 2) {
-        T ux = m_cos(ang), uy = m_sin(ang);
+        T ux, uy;
+        ob_trig(O, j, o, cs, ux, uy);
         T t = wclamp((px - cx) * ux + (py - cy) * uy, -hx, hx);
         T qx = cx + t * ux, qy = cy + t * uy;
         T rx = qx - cx, ry = qy - cy;
@@ -649,7 +686,7 @@ __device__ __forceinline__ void obstacle_force(const Cst<T> &C, const Obs<T> &O,
 template <typename T>
 __device__ __forceinline__ void obstacle_force_adj(const Cst<T> &C, const Obs<T> &O, size_t eN,
                                                    int o, T px, T py, T vx, T vy, T ra, T dd,
-                                                   T gx, T gy, St<T> &a)
+                                                   T gx, T gy, St<T> &a, const T *cs = nullptr)
 {
     const size_t j = eN + o;
     const T cx = O.pos[2 * j], cy = O.pos[2 * j + 1];
@@ -659,12 +696,15 @@ __device__ __forceinline__ void obstacle_force_adj(const Cst<T> &C, const Obs<T>
     T lim = (ra + C.margin + bound) * T(1.0001) + T(1.0e-6);
     T ddx = px - cx, ddy = py - cy;
     if (ddx * ddx + ddy * ddy > lim * lim) return;
-    const T vox = O.vel[2 * j], voy = O.vel[2 * j + 1], om = O.om[j], ang = O.ang[j];
+    const T vox = O.vel[2 * j], voy = O.vel[2 * j + 1], om = O.om[j];
     if (st == 1) {
-        box_force_adj(C, px, py, vx, vy, cx, cy, ang, hx, hy, ra + C.margin, dd, vox, voy, om,
-                      gx, gy, a);
+        T ca, sa;
+        ob_trig(O, j, o, cs, ca, sa);
+        box_force_adj_cs(C, px, py, vx, vy, cx, cy, ca, sa, hx, hy, ra + C.margin, dd, vox, voy,
+                         om, gx, gy, a);
     } else if (st == 2) {
-        T ux = m_cos(ang), uy = m_sin(ang);
+        T ux, uy;
+        ob_trig(O, j, o, cs, ux, uy);
         T tr = (px - cx) * ux + (py - cy) * uy;
         T t = wclamp(tr, -hx, hx);
         T qx = cx + t * ux, qy = cy + t * uy;

@@ -253,10 +253,31 @@ template <int PA> __device__ __forceinline__ bool env_all(bool ok, int base)
 
 // Contact + static forces of one substep, reading the env's positions/velocities from
 // the LDS slot `sl`.  Returns the uncapped inclusion mask (for the true count).
+// Obstacle angles as (cos, sin) per env slot of the wave, filled once per launch when
+// 64/PA envs x N obstacles fit (OCS_MAX pairs); NULL table otherwise.
+constexpr int OCS_MAX = 256;
+
+template <typename T, int PA>
+__device__ __forceinline__ const T *ob_trig_table(const Cst<T> &C, const Args<T> &g,
+                                                  const Lane<T, PA> &L, T *ocs)
+{
+    if (C.N <= 0 || (64 / PA) * C.N > OCS_MAX) return nullptr;
+    const int ew = L.lane / PA;
+    const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
+    for (int q = L.agent; q < C.N; q += PA) {
+        const T ang = g.obs.ang[eN + q];
+        ocs[2 * (ew * C.N + q)] = m_cos(ang);
+        ocs[2 * (ew * C.N + q) + 1] = m_sin(ang);
+    }
+    __syncthreads();
+    return ocs + 2 * ew * C.N;
+}
+
 template <typename T, int PA>
 __device__ __forceinline__ typename MaskT<PA>::type forces(
     const Cst<T> &C, const Args<T> &g, const Lane<T, PA> &L, const T *sl, const T *lr,
-    const St<T> &st, int s, bool full, typename MaskT<PA>::type &cand, T &Fx, T &Fy)
+    const St<T> &st, int s, bool full, typename MaskT<PA>::type &cand, T &Fx, T &Fy,
+    const T *ocs = nullptr)
 {
     typedef typename MaskT<PA>::type M;
     const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64, *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
@@ -288,7 +309,8 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
         for (int o = 0; o < C.N; ++o) {
             T gx, gy;
-            obstacle_force(C, g.obs, eN, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.dd, gx, gy);
+            obstacle_force(C, g.obs, eN, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.dd, gx, gy,
+                           ocs);
             sx += gx;
             sy += gy;
         }
@@ -313,9 +335,11 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> C, const Args<T
     typedef typename MaskT<PA>::type M;
     __shared__ T sl[4 * 64];  // px py vx vy of the current substep
     __shared__ T lr[64];      // agent radius per lane
+    __shared__ T ocs_lds[2 * OCS_MAX];
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
     lr[L.lane] = L.pr.radius;
+    const T *ocs = ob_trig_table<T, PA>(C, g, L, ocs_lds);
     St<T> st;
     load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
     if (!L.real) st.px = st.py = __builtin_nan("");
@@ -337,7 +361,7 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> C, const Args<T
                     sl[F_VY * 64 + L.lane] = st.vy;
                     __syncthreads();
                 }
-                forces<T, PA>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy);
+                forces<T, PA>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy, ocs);
             }
             St<T> nx;
             integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
@@ -405,10 +429,12 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
     T *ldd = lr + 64;           // damping denominator per lane
     T *slots = ldd + 64;        // S slots of NF fields
     M *lmask = (M *)(slots + (size_t)C.S * NF * 64);  // S inclusion masks per lane
+    __shared__ T ocs_lds[2 * OCS_MAX];
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
     lr[L.lane] = L.pr.radius;
     ldd[L.lane] = L.dd;
+    const T *ocs = ob_trig_table<T, PA>(C, g, L, ocs_lds);
     const size_t EA = (size_t)C.E * C.A;
     St<T> gs;  // adjoint of the current step's output
     st_zero(gs);
@@ -438,7 +464,7 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
             T Fx = T(0), Fy = T(0);
             M incl = 0;
             if (C.needs_forces)
-                incl = forces<T, PA>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy);
+                incl = forces<T, PA>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy, ocs);
             sl[F_FX * 64 + L.lane] = Fx;
             sl[F_FY * 64 + L.lane] = Fy;
             lmask[s * 64 + L.lane] = incl;
@@ -493,7 +519,7 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
                     const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
                     for (int o = 0; o < C.N; ++o)
                         obstacle_force_adj(C, g.obs, eN, o, in.px, in.py, in.vx, in.vy,
-                                           L.pr.radius, L.dd, gFx, gFy, gi);
+                                           L.pr.radius, L.dd, gFx, gFy, gi, ocs);
                 }
                 if (C.soft_walls)
                     wall_force_adj(C, in.px, in.py, in.vx, in.vy, L.pr.radius, L.dd, gFx, gFy, gi);
