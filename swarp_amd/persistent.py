@@ -11,11 +11,21 @@ current set before the next replay.  The graphs are captured lazily and recaptur
 a pointer they baked in moves (obstacles, buffers) -- the reference's recapture token.
 
 Differentiated steps never come here: a graph replay records nothing for autograd.
+
+Lifetime: bound-method hooks are held weakly, so an owner (an ``Environment``) and its
+StepGraph form no reference cycle and the captured graphs die by reference counting when
+the owner does.  A graph left to the cyclic collector could be destroyed in the middle of
+another capture -- a collection can start at any Python allocation -- and destroying a
+graph while a stream is capturing aborts the process.  For the same reason the collector
+is paused while a capture is open.
 """
 
 from __future__ import annotations
 
 import ctypes
+import gc
+import inspect
+import weakref
 from typing import Callable
 
 import torch
@@ -29,6 +39,16 @@ from .stepper import state_struct
 Hook = Callable[[TorchState, int, bool], None]
 
 
+def _held(fn):
+    """A zero-argument getter for ``fn``: weak for a bound method (no cycle through its
+    owner), strong otherwise."""
+    if fn is None:
+        return lambda: None
+    if inspect.ismethod(fn):
+        return weakref.WeakMethod(fn)
+    return lambda: fn
+
+
 class StepGraph:
     """Ping-pong state buffers and the two captured whole-step graphs of one World."""
 
@@ -37,8 +57,8 @@ class StepGraph:
             raise NotImplementedError(
                 "whole-step graphs cover 2-D fleets without movable bodies in this build")
         self.world = world
-        self.hook = hook
-        self._extra_token = token
+        self._hook = _held(hook)
+        self._extra_token = _held(token)
         E, A = world.n_envs, world.n_agents
         self.bufs = [world.zero_state(), world.zero_state()]
         self.act = torch.zeros(E, A, world.act_dim, device=world.device, dtype=world.dtype)
@@ -51,7 +71,8 @@ class StepGraph:
         w = self.world
         d = w.stepper.desc(w.n_envs, w.act_dim)
         base = (w.stepper.mutation_version, ctypes.addressof(d), w.stepper.params.floats.data_ptr())
-        return base + (self._extra_token() if self._extra_token else ())
+        extra = self._extra_token()
+        return base + (extra() if extra is not None else ())
 
     def adopt_state(self) -> None:
         """Make ``world.state`` the current persistent set (copying a replaced state in)."""
@@ -80,17 +101,24 @@ class StepGraph:
         # eager warm-up of the same launches (first-launch set-up stays out of the
         # capture); the hook's warm launch leaves carried state (the baseline) alone,
         # and the replay below overwrites everything it wrote
+        hook = self._hook()
         stream = _lib.stream_of(self.act.device)
         self._launch_step(src, dst, stream)
-        if self.hook is not None:
-            self.hook(dst, stream, True)
+        if hook is not None:
+            hook(dst, stream, True)
         torch.cuda.current_stream(self.act.device).synchronize()
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            cap = _lib.stream_of(self.act.device)
-            self._launch_step(src, dst, cap)
-            if self.hook is not None:
-                self.hook(dst, cap, False)
+        collecting = gc.isenabled()
+        gc.disable()  # no collection (and no graph destructor) inside the capture
+        try:
+            with torch.cuda.graph(g):
+                cap = _lib.stream_of(self.act.device)
+                self._launch_step(src, dst, cap)
+                if hook is not None:
+                    hook(dst, cap, False)
+        finally:
+            if collecting:
+                gc.enable()
         self.captures += 1
         return g
 

@@ -79,8 +79,13 @@ class World:
         def z(*shape):
             return torch.zeros(*shape, device=self.device, dtype=self.dtype)
 
+        # every field materialised once (identity attitude), so a step never has to
+        # allocate the defaults of the fields a 2-D fleet passes through
+        att = z(e, a, 4)
+        att[..., 3] = 1.0
         return TorchState(pos=z(e, a, 2), theta=z(e, a), vel=z(e, a, 2), speed=z(e, a),
-                          ang_vel=z(e, a))
+                          ang_vel=z(e, a), z=z(e, a), vz=z(e, a), attitude=att,
+                          body_rates=z(e, a, 3))
 
     def step(self, actions: torch.Tensor) -> None:
         """Advance the world one step (differentiable when grads are enabled)."""
@@ -106,7 +111,10 @@ class World:
                 continue
             dst = getattr(self.state, name).data
             if mask is None:
-                dst.copy_(value.expand_as(dst) if torch.is_tensor(value) else value)
+                if torch.is_tensor(value):
+                    dst.copy_(value.expand_as(dst))
+                else:  # a number: a fill, not a copy from a host tensor (no sync)
+                    dst.fill_(value)
             else:
                 m = mask.view(-1, *([1] * (dst.dim() - 1)))
                 dst.copy_(torch.where(m, value, dst))

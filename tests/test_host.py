@@ -288,3 +288,24 @@ def test_compile_registry_does_not_keep_the_stepper_alive():
     with pytest.raises(RuntimeError, match="garbage-collected"):
         compile_mod._stepper(handle)
     assert hasattr(torch.ops.swarp_amd, "step")
+
+
+def test_step_graph_forms_no_cycle_with_its_owner():
+    """A StepGraph holds its owner's bound-method hooks weakly: the owner (and the graphs
+    it captured) die by reference counting, never inside the cyclic collector, which may
+    run in the middle of another capture."""
+    import gc
+    import weakref
+
+    from swarp_amd import make
+    from swarp_amd.persistent import StepGraph
+
+    env = make("navigation", 3, device="cpu", n_agents=2)
+    env._graph = StepGraph(env.world, hook=env._graph_hook, token=env._graph_token)
+    ref, gref = weakref.ref(env), weakref.ref(env._graph)
+    gc.disable()
+    try:
+        del env
+        assert ref() is None and gref() is None
+    finally:
+        gc.enable()
