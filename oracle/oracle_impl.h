@@ -30,6 +30,7 @@ typedef struct {
     /* per-agent constants resolved from the [A, 22] parameter row */
     REAL radius, mass, max_speed, max_accel, max_ang_vel, max_ang_accel;
     REAL l_f, l_r, max_steer, thrust_max, arm, ixx, iyy, izz, kappa, gravity, min_speed;
+    REAL shape, hx, hy; /* footprint: 0 disc, 1 box of half-extents (hx, hy) */
     int tag, mode;
 } FN(prm_t);
 
@@ -37,7 +38,9 @@ typedef struct {
     REAL k, c, margin, sub_dt, max_overlap, nbr_radius, eps2;
     REAL bmin_x, bmin_y, bmax_x, bmax_y;
     int n_envs, n_agents, act_dim, substeps, max_nbr;
-    int collisions, soft_walls, clamp_bounds, needs_forces, n_obs;
+    int collisions, soft_walls, needs_forces, n_obs;
+    int clamp_bounds; /* 0 off, 1 disc clamp, 2 footprint clamp (a world holding boxes) */
+    int boxes;        /* some agent is a box: the box-aware contact pass */
     /* obstacles: pos [E,N,2], radius [N], type [N], angle [E,N], half [N,2],
        vel [E,N,2], ang_vel [E,N] */
     const REAL *o_pos, *o_rad, *o_ang, *o_half, *o_vel, *o_om;
@@ -518,6 +521,8 @@ static inline void FN(wall_force_adj)(const FN(ctx_t) *C, REAL px, REAL py, REAL
     }
 }
 
+#include "oracle_boxes.h"
+
 /* ------------------------------------------------------------------ neighbours */
 
 /* _brute_force (swarp/core/neighbors.py:76-97) for one env */
@@ -546,6 +551,10 @@ static void FN(neighbors_env)(int A, int K, const FN(agent_t) *st, REAL radius,
 static void FN(forces_env)(const FN(ctx_t) *C, const REAL *od, const FN(prm_t) *P,
                            const FN(agent_t) *st, const int32_t *idx, const int32_t *cnt, REAL *F)
 {
+    if (C->boxes) {
+        FN(forces_env_box)(C, od, P, st, idx, cnt, F);
+        return;
+    }
     int A = C->n_agents, K = C->max_nbr;
     for (int a = 0; a < A; ++a) {
         REAL px = st[a].px, py = st[a].py, vx = st[a].vx, vy = st[a].vy;
@@ -584,6 +593,10 @@ static void FN(forces_env_adj)(const FN(ctx_t) *C, const REAL *od, const FN(prm_
                                const FN(agent_t) *st, const int32_t *idx, const int32_t *cnt,
                                const REAL *aF, FN(agent_t) *adj, REAL *god)
 {
+    if (C->boxes) {
+        FN(forces_env_box_adj)(C, od, P, st, idx, cnt, aF, adj);
+        return;
+    }
     int A = C->n_agents, K = C->max_nbr;
     for (int a = 0; a < A; ++a) {
         REAL gfx = aF[a * 2], gfy = aF[a * 2 + 1];
@@ -870,11 +883,7 @@ static void FN(rk4_agent)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent
     } else {
         return; /* unknown tag: the state passes through */
     }
-    if (C->clamp_bounds) {
-        REAL r = P->radius;
-        pnx = FN(rclamp)(pnx, C->bmin_x + r, C->bmax_x - r);
-        pny = FN(rclamp)(pny, C->bmin_y + r, C->bmax_y - r);
-    }
+    if (C->clamp_bounds) FN(clamp_position)(C, P, out->th, &pnx, &pny);
     out->px = pnx;
     out->py = pny;
 }
@@ -893,12 +902,7 @@ static void FN(rk4_agent_adj)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(a
     FN(rk_t) R;
     FN(rk_stages)(C, P, in, a, &R);
     REAL dfx = Fx * (dt / P->mass), dfy = Fy * (dt / P->mass);
-    REAL gpx = g->px, gpy = g->py;
-    if (C->clamp_bounds) {
-        REAL r = P->radius;
-        gpx = FN(rclamp_gx)(R.xi.px + dfx * dt, C->bmin_x + r, C->bmax_x - r, gpx);
-        gpy = FN(rclamp_gx)(R.xi.py + dfy * dt, C->bmin_y + r, C->bmax_y - r, gpy);
-    }
+    REAL gpx = g->px, gpy = g->py; /* the clamp is reversed by integrate_agent_adj */
     FN(agent_t) gxi;
     memset(&gxi, 0, sizeof gxi);
     gxi.px = gpx;
@@ -1122,11 +1126,7 @@ static void FN(integrate_agent)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN
             pny = py;
         }
     }
-    if (C->clamp_bounds) {
-        REAL r = P->radius;
-        pnx = FN(rclamp)(pnx, C->bmin_x + r, C->bmax_x - r);
-        pny = FN(rclamp)(pny, C->bmin_y + r, C->bmax_y - r);
-    }
+    if (C->clamp_bounds) FN(clamp_position)(C, P, out->th, &pnx, &pny);
     out->px = pnx;
     out->py = pny;
 }
@@ -1142,6 +1142,17 @@ static void FN(integrate_agent_adj)(const FN(ctx_t) *C, const FN(prm_t) *P,
     REAL a0 = act[0], a1 = C->act_dim > 1 ? act[1] : (REAL)0;
     REAL a2 = C->act_dim > 2 ? act[2] : (REAL)0;
     REAL a3 = C->act_dim > 3 ? act[3] : (REAL)0;
+    if (C->clamp_bounds) {
+        /* the position clamp, reversed at the unclamped output (its bounds move with the
+           heading under the footprint clamp); the rest is differentiated without it */
+        FN(ctx_t) C2 = *C;
+        C2.clamp_bounds = 0;
+        FN(agent_t) raw, g2 = *g;
+        FN(integrate_agent)(&C2, P, in, act, Fx, Fy, &raw);
+        FN(clamp_position_adj)(C, P, raw.px, raw.py, raw.th, &g2.px, &g2.py, &g2.th);
+        FN(integrate_agent_adj)(&C2, P, in, act, Fx, Fy, &g2, gin, gact, gFx, gFy);
+        return;
+    }
     if (C->rk4) {
         REAL a[4] = {a0, a1, a2, a3}, ga[4] = {0, 0, 0, 0};
         FN(rk4_agent_adj)(C, P, in, a, Fx, Fy, g, gin, ga, gFx, gFy);
@@ -1150,17 +1161,7 @@ static void FN(integrate_agent_adj)(const FN(ctx_t) *C, const FN(prm_t) *P,
     }
     FN(agent_t) fwd;
     FN(integrate_agent)(C, P, in, act, Fx, Fy, &fwd);
-    /* position clamp: recompute the unclamped position */
     REAL gpx = g->px, gpy = g->py;
-    if (C->clamp_bounds) {
-        FN(agent_t) raw;
-        FN(ctx_t) C2 = *C;
-        C2.clamp_bounds = 0;
-        FN(integrate_agent)(&C2, P, in, act, Fx, Fy, &raw);
-        REAL r = P->radius;
-        gpx = FN(rclamp_gx)(raw.px, C->bmin_x + r, C->bmax_x - r, gpx);
-        gpy = FN(rclamp_gx)(raw.py, C->bmin_y + r, C->bmax_y - r, gpy);
-    }
     REAL dtm = dt / P->mass;
     if (P->tag == 3) {
         REAL zero = 0;
@@ -1789,8 +1790,9 @@ static void FN(static_ob)(const FN(ctx_t) *C, int e, REAL *ob)
 }
 
 static void FN(make_prm)(const REAL *params, const int32_t *tags, const int32_t *modes, int A,
-                         FN(prm_t) *P)
+                         FN(prm_t) *P, FN(ctx_t) *C)
 {
+    C->boxes = 0;
     for (int a = 0; a < A; ++a) {
         const REAL *r = params + a * 22;
         P[a].radius = r[0]; P[a].mass = r[1]; P[a].max_speed = r[2]; P[a].max_accel = r[3];
@@ -1798,6 +1800,8 @@ static void FN(make_prm)(const REAL *params, const int32_t *tags, const int32_t 
         P[a].max_steer = r[8]; P[a].thrust_max = r[9]; P[a].arm = r[10]; P[a].ixx = r[11];
         P[a].iyy = r[12]; P[a].izz = r[13]; P[a].kappa = r[14]; P[a].gravity = r[15];
         P[a].min_speed = r[16];
+        P[a].shape = r[17]; P[a].hx = r[18]; P[a].hy = r[19];
+        if (P[a].shape > (REAL)0.5) C->boxes = 1;
         P[a].tag = tags[a];
         P[a].mode = modes[a];
     }
@@ -1848,7 +1852,7 @@ int FN(oracle_rollout_ob)(const oracle_cfg_t *cfg, const REAL *params, const int
     int E = C.n_envs, A = C.n_agents, S = C.substeps, K = C.max_nbr, ad = C.act_dim, N = C.n_obs;
     size_t nob = (size_t)OB_W * N;
     FN(prm_t) *P = (FN(prm_t) *)calloc((size_t)A, sizeof(FN(prm_t)));
-    FN(make_prm)(params, tags, modes, A, P);
+    FN(make_prm)(params, tags, modes, A, P, &C);
     int nth = cfg->n_threads > 0 ? cfg->n_threads : 1;
     int err = 0;
 #pragma omp parallel num_threads(nth)
@@ -1913,7 +1917,7 @@ int FN(oracle_rollout_adj_ob)(const oracle_cfg_t *cfg, const REAL *params, const
     int E = C.n_envs, A = C.n_agents, S = C.substeps, K = C.max_nbr, ad = C.act_dim, N = C.n_obs;
     size_t nob = (size_t)OB_W * N;
     FN(prm_t) *P = (FN(prm_t) *)calloc((size_t)A, sizeof(FN(prm_t)));
-    FN(make_prm)(params, tags, modes, A, P);
+    FN(make_prm)(params, tags, modes, A, P, &C);
     int nth = cfg->n_threads > 0 ? cfg->n_threads : 1;
     int err = 0;
     memset(adj_actions, 0, sizeof(REAL) * (size_t)T * E * A * ad);
@@ -2016,7 +2020,7 @@ int FN(oracle_forces)(const oracle_cfg_t *cfg, const REAL *params, const int32_t
     FN(prm_t) *P = (FN(prm_t) *)calloc((size_t)A, sizeof(FN(prm_t)));
     int32_t *idx = (int32_t *)malloc(sizeof(int32_t) * (size_t)A * K);
     int32_t *cnt = (int32_t *)malloc(sizeof(int32_t) * (size_t)A);
-    FN(make_prm)(params, tags, modes, A, P);
+    FN(make_prm)(params, tags, modes, A, P, &C);
     REAL *od = C.n_obs ? (REAL *)malloc(sizeof(REAL) * OB_W * C.n_obs) : NULL;
     for (int e = 0; e < E; ++e) {
         const FN(agent_t) *st = (const FN(agent_t) *)(state + (size_t)e * A * 16);

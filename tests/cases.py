@@ -31,7 +31,9 @@ def oracle_cfg(configs, world: WorldConfig, dt, substeps, n_envs, act_dim, n_thr
         max_neighbors=world.max_neighbors,
         collisions=int(collisions),
         soft_walls=int(b is not None and world.bounds_mode == "soft"),
-        clamp_bounds=int(b is not None and world.bounds_mode == "clamp"),
+        # 2: the footprint clamp a world holding box agents uses (kernels.py:74-99)
+        clamp_bounds=(0 if b is None or world.bounds_mode != "clamp" else
+                      2 if any(int(c.shape) == 1 for c in configs) else 1),
         n_threads=n_threads,
         dt=dt,
         k=world.collision_k,

@@ -1,0 +1,278 @@
+"""Pins of the oracle's box-agent restatement (oriented-rectangle footprints).
+
+Forward: closed forms the geometry fixes (face overlap of two boxes, a box corner at a
+small gap from a face, a box against a circle / box / capsule obstacle, the support
+extent of a rotated box against a soft wall, the footprint clamp of a rotated box) and
+the pair law's action = reaction, bit for bit, that the reference's lower-index-as-A rule
+guarantees (swarp/core/collisions.py:489-541).  Reverse: the oracle's dual-number
+Jacobians against central finite differences of its own forward in fp64, across the
+regimes of obb_contact (overlap, vertex distance), every shape pairing, obstacles,
+walls and the footprint clamp.  Geometry follows swarp/core/collisions.py:266-688 and
+swarp/dynamics/kernels.py:79-99; the reference's own tests of it are
+tests/unit/test_box_agents.py (not runnable here: they need warp-lang).
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from cases import obstacles_np, oracle_cfg, params_of
+from oracle.oracle import Oracle, pack_state
+from swarp_amd.config import AgentConfig, AgentShape, ControlMode, DynamicsModel, WorldConfig
+from test_oracle_gradcheck import _fd_check
+
+O = Oracle(np.float64)
+K = 100.0
+M = 0.025
+
+
+def _box(hx, hy, model=DynamicsModel.HOLONOMIC, **kw):
+    return AgentConfig(model=model, shape=AgentShape.BOX, half_extents=(hx, hy), radius=None, **kw)
+
+
+def _disc(r, model=DynamicsModel.HOLONOMIC, **kw):
+    return AgentConfig(model=model, radius=r, **kw)
+
+
+def _forces(configs, world, state, obs=None, dtype=np.float64):
+    o = Oracle(dtype)
+    E = state.shape[0]
+    cfg = oracle_cfg(configs, world, 0.05, 1, E, 2)
+    p, t, m = params_of(configs)
+    return o.forces(cfg, p, t, m, obstacles_np(obs, E), state.astype(dtype))
+
+
+def _world(**kw):
+    base = dict(collision_k=K, collision_c=0.0, collision_margin=M, max_neighbors=8)
+    base.update(kw)
+    return WorldConfig(**base)
+
+
+def test_face_overlap_of_two_boxes():
+    """Aligned boxes overlapping by 0.05 along x: the least-overlap axis is A's x face,
+    the normal points from B to A, overlap = margin + 0.05 (collisions.py:400-447)."""
+    cfgs = [_box(0.2, 0.1), _box(0.2, 0.1)]
+    s = pack_state({"pos": [[[0.0, 0.0], [0.35, 0.02]]]})
+    F = _forces(cfgs, _world(), s)
+    want = K * (M + 0.05)
+    assert F[0, 0, 0] == pytest.approx(-want, rel=1e-12) and F[0, 0, 1] == 0.0
+    assert np.array_equal(F[0, 1], -F[0, 0])
+
+
+def test_face_overlap_damper_reads_the_contact_point():
+    """The damper of the face overlap above reads the material-point velocities at the
+    contact point: on A's right face (x = 0.2), midway along the overlap of the two
+    boxes' extents across it (y in [-0.08, 0.1] -> 0.01).  A spins at wa, B moves and
+    spins; the closing speed along n = (-1, 0) follows from v + w x (x - c)."""
+    cfgs = [_box(0.2, 0.1), _box(0.2, 0.1)]
+    c, wa, wb, vb = 2.0, 3.0, -1.5, np.array([0.4, 0.7])
+    s = pack_state({"pos": [[[0.0, 0.0], [0.35, 0.02]]], "vel": [[[0.0, 0.0], vb]],
+                    "ang_vel": [[wa, wb]]})
+    F = _forces(cfgs, _world(collision_c=c), s)
+    x = np.array([0.2, 0.01])
+    ra, rb = x - np.array([0.0, 0.0]), x - np.array([0.35, 0.02])
+    vpa = np.array([-wa * ra[1], wa * ra[0]])
+    vpb = vb + np.array([-wb * rb[1], wb * rb[0]])
+    vn = float((vpa - vpb) @ np.array([-1.0, 0.0]))
+    coef = (K * (M + 0.05) - c * vn) / (1.0 + c * 0.05 / 1.0)
+    assert F[0, 0, 0] == pytest.approx(-coef, rel=1e-12)
+
+
+def test_disc_box_damper_reads_the_box_surface():
+    """A disc over a spinning box's top face: the closing velocity is taken against the
+    box's surface point under the disc, v_b + w_b x (q - c_b) with q = (0.15, 0.1)."""
+    cfgs = [_disc(0.05), _box(0.2, 0.1)]
+    c, vd, vb, wb = 1.0, np.array([0.2, -0.3]), np.array([0.1, 0.25]), 2.0
+    s = pack_state({"pos": [[[0.15, 0.16], [0.0, 0.0]]], "vel": [[vd, vb]], "ang_vel": [[0.0, wb]]})
+    F = _forces(cfgs, _world(collision_c=c), s)
+    q = np.array([0.15, 0.1])
+    vs = vb + np.array([-wb * q[1], wb * q[0]])
+    vn = float((vd - vs) @ np.array([0.0, 1.0]))
+    coef = (K * (0.05 + M - 0.06) - c * vn) / (1.0 + c * 0.05 / 1.0)
+    assert F[0, 0, 1] == pytest.approx(coef, rel=1e-12) and F[0, 0, 0] == 0.0
+    assert np.array_equal(F[0, 1], -F[0, 0])
+
+
+def test_corner_at_a_small_gap():
+    """A box turned 45 degrees points a corner at an aligned box's face from 0.01 away
+    (inside the margin): SAT reports a positive gap, the vertex pass finds the exact
+    distance, and the force is k (margin - 0.01) along the face normal (:384-398)."""
+    h = 0.1
+    c = h * math.sqrt(2.0)
+    cfgs = [_box(h, h), _box(0.2, 0.2)]
+    s = pack_state({"pos": [[[0.0, 0.0], [c + 0.01 + 0.2, 0.0]]], "theta": [[math.pi / 4, 0.0]]})
+    F = _forces(cfgs, _world(), s)
+    assert F[0, 0, 0] == pytest.approx(-K * (M - 0.01), rel=1e-9)
+    assert abs(F[0, 0, 1]) < 1e-9
+    assert np.array_equal(F[0, 1], -F[0, 0])
+
+
+def test_disc_against_a_box_agent():
+    """A disc centre 0.06 from a box's long face: box_force with the disc as the point on
+    the disc, its negation on the box (:515-527)."""
+    cfgs = [_disc(0.05), _box(0.2, 0.1)]
+    s = pack_state({"pos": [[[0.0, 0.16], [0.0, 0.0]]]})
+    F = _forces(cfgs, _world(), s)
+    want = K * (0.05 + M - 0.06)
+    assert F[0, 0, 1] == pytest.approx(want, rel=1e-12) and F[0, 0, 0] == 0.0
+    assert np.array_equal(F[0, 1], -F[0, 0])
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_pair_forces_cancel_exactly(seed):
+    """Both threads of a pair evaluate one contact with the lower index as box A (or the
+    disc as the point): with equal masses the two forces are exact negatives, in both
+    precisions, whatever the poses (:489-541)."""
+    rng = np.random.default_rng(seed)
+    for a_box, b_box in ((True, True), (True, False), (False, True)):
+        cfgs = [_box(0.15, 0.08) if a_box else _disc(0.07),
+                _box(0.12, 0.1) if b_box else _disc(0.06)]
+        pos = rng.uniform(-0.12, 0.12, size=(8, 2, 2))
+        s = pack_state({"pos": pos, "theta": rng.uniform(-np.pi, np.pi, size=(8, 2)),
+                        "vel": rng.normal(size=(8, 2, 2)), "ang_vel": rng.normal(size=(8, 2))})
+        for dt in (np.float64, np.float32):
+            F = _forces(cfgs, _world(collision_c=2.0), s, dtype=dt)
+            assert np.array_equal(F[:, 1], -F[:, 0])
+            assert np.count_nonzero(F) > 0
+
+
+def test_box_agent_against_obstacles():
+    """A box agent (0.2 x 0.1 half extents, heading 0) against one obstacle of each kind:
+    a circle whose centre is 0.1 above its top face, a box overlapping its right face by
+    0.02, a capsule whose core is 0.06 below its bottom face (:543-626)."""
+    cfgs = [_box(0.2, 0.1)]
+    w = _world(collisions=False)
+    s = pack_state({"pos": [[[0.0, 0.0]]]})
+    circle = {"pos": [[[0.0, 0.2]]], "radius": [0.1], "type": [0]}
+    F = _forces(cfgs, w, s, circle)
+    assert F[0, 0, 0] == 0.0 and F[0, 0, 1] == pytest.approx(-K * (0.1 + M - 0.1), rel=1e-12)
+    box = {"pos": [[[0.38, 0.0]]], "radius": [0.0], "type": [1], "half": [[0.2, 0.3]]}
+    F = _forces(cfgs, w, s, box)
+    assert F[0, 0, 0] == pytest.approx(-K * (M + 0.02), rel=1e-12) and F[0, 0, 1] == 0.0
+    seg = {"pos": [[[0.05, -0.16]]], "radius": [0.05], "type": [2], "half": [[0.3, 0.0]]}
+    F = _forces(cfgs, w, s, seg)
+    assert abs(F[0, 0, 0]) < 1e-12
+    assert F[0, 0, 1] == pytest.approx(K * (0.05 + M - 0.06), rel=1e-9)
+
+
+def test_rotated_box_against_a_soft_wall():
+    """The wall sees the support extent ex = hx |cos| + hy |sin| (:641-688)."""
+    cfgs = [_box(0.2, 0.1)]
+    w = _world(collisions=False, bounds=(-1.0, 1.0, -1.0, 1.0))
+    th = 0.7
+    s = pack_state({"pos": [[[-0.8, 0.0]]], "theta": [[th]]})
+    F = _forces(cfgs, w, s)
+    ex = 0.2 * abs(math.cos(th)) + 0.1 * abs(math.sin(th))
+    assert F[0, 0, 0] == pytest.approx(K * (ex + M - 0.2), rel=1e-12) and F[0, 0, 1] == 0.0
+    # damped and spinning: the wall's damper reads the velocity of the vertex touching it
+    c, v, w_ = 1.5, np.array([-0.3, 0.2]), 2.5
+    s = pack_state({"pos": [[[-0.8, 0.0]]], "theta": [[th]], "vel": [[v]], "ang_vel": [[w_]]})
+    F = _forces(cfgs, _world(collisions=False, collision_c=c, bounds=(-1.0, 1.0, -1.0, 1.0)), s)
+    e0 = 0.2 * np.array([math.cos(th), math.sin(th)])
+    e1 = 0.1 * np.array([-math.sin(th), math.cos(th)])
+    verts = [e0 + e1, -e0 + e1, -e0 - e1, e0 - e1]
+    r = min(verts, key=lambda q: q[0])  # the vertex reaching furthest toward -x
+    vn = v[0] - w_ * r[1]
+    coef = (K * (-r[0] + M - 0.2) - c * vn) / (1.0 + c * 0.05)
+    assert F[0, 0, 0] == pytest.approx(coef, rel=1e-12)
+
+
+def test_footprint_clamp():
+    """A box turned to 1.2 rad driven into the right wall stops with its support extent
+    against it (kernels.py:79-99); a disc in the same world keeps the radius inset."""
+    cfgs = [_box(0.2, 0.1, max_speed=10.0), _disc(0.05, max_speed=10.0)]
+    w = WorldConfig(collisions=False, bounds=(-0.5, 0.5, -0.5, 0.5), bounds_mode="clamp")
+    cfg = oracle_cfg(cfgs, w, 0.1, 1, 1, 2)
+    assert cfg["clamp_bounds"] == 2
+    p, t, m = params_of(cfgs)
+    s0 = pack_state({"pos": [[[0.3, 0.0], [0.4, 0.2]]], "theta": [[1.2, 0.0]]})
+    tr = O.rollout(cfg, p, t, m, None, s0, np.array([[[[2.0, 0.0], [2.0, 0.0]]]]))
+    ex = 0.2 * abs(math.cos(1.2)) + 0.1 * abs(math.sin(1.2))
+    assert tr[0, 0, 0, 0] == 0.5 - ex
+    assert tr[0, 0, 1, 0] == 0.5 - 0.05
+
+
+# ------------------------------------------------------------------ finite differences
+
+def _rs(E, A, seed, spread, ang=True):
+    rng = np.random.default_rng(seed)
+    return pack_state({
+        "pos": rng.uniform(-spread, spread, size=(E, A, 2)),
+        "theta": rng.uniform(-np.pi, np.pi, size=(E, A)) if ang else np.zeros((E, A)),
+        "vel": rng.normal(size=(E, A, 2)) * 0.3,
+        "speed": rng.normal(size=(E, A)) * 0.3,
+        "ang_vel": rng.normal(size=(E, A)) * 0.5,
+    }), rng
+
+
+def _dd(n, **kw):
+    return [_box(0.12, 0.07, model=DynamicsModel.DIFF_DRIVE, ctrl_mode=ControlMode.ACCELERATION,
+                 max_speed=5.0, max_accel=5.0, max_ang_vel=8.0, max_ang_accel=8.0, **kw)
+            for _ in range(n)]
+
+
+def test_fd_box_pairs_overlapping():
+    """Crowded diff-drive boxes: SAT overlap contacts, damped, two substeps."""
+    s0, rng = _rs(2, 3, 1, 0.1)
+    acts = rng.uniform(-1, 1, size=(2, 2, 3, 2))
+    _fd_check(_dd(3), _world(collision_c=1.5), 0.05, 2, s0, acts, fields=(0, 1, 2, 3, 4, 5, 6))
+
+
+def test_fd_box_pairs_within_margin():
+    """Boxes a few millimetres apart: the vertex-distance regime of obb_contact."""
+    cfgs = _dd(2)
+    rng = np.random.default_rng(5)
+    # B turned 45 degrees, its leftmost corner 6 mm from A's right face (A at heading 0)
+    c, sn = math.cos(math.pi / 4), math.sin(math.pi / 4)
+    corner = (-0.12 * c + 0.07 * sn, -0.12 * sn - 0.07 * c)  # -e0 + e1
+    b = (0.12 + 0.006 - corner[0], 0.02 - corner[1])
+    s0 = pack_state({"pos": [[[0.0, 0.0], list(b)]],
+                     "theta": [[0.0, math.pi / 4]], "vel": rng.normal(size=(1, 2, 2)) * 0.1,
+                     "speed": [[0.1, -0.1]], "ang_vel": [[0.2, -0.4]]})
+    acts = rng.uniform(-0.5, 0.5, size=(2, 1, 2, 2))
+    _fd_check(cfgs, _world(collision_margin=0.04, collision_c=1.0), 0.05, 2, s0, acts,
+              fields=(0, 1, 2, 3, 4, 5, 6))
+
+
+def test_fd_mixed_discs_and_boxes():
+    """Discs (holonomic), diff-drive boxes and a bicycle box in one crowded env."""
+    cfgs = [_disc(0.06, max_speed=5.0, max_accel=5.0, ctrl_mode=ControlMode.ACCELERATION),
+            _disc(0.05, max_speed=5.0)] + _dd(2) + [
+        _box(0.1, 0.05, model=DynamicsModel.KINEMATIC_BICYCLE, max_speed=5.0, max_accel=5.0,
+             max_steer=1.0, l_f=0.16, l_r=0.14)]
+    s0, rng = _rs(2, 5, 3, 0.15)
+    acts = rng.uniform(-1, 1, size=(2, 2, 5, 2))
+    _fd_check(cfgs, _world(collision_c=1.0, contact_max_overlap=0.05), 0.05, 2, s0, acts,
+              fields=(0, 1, 2, 3, 4, 5, 6))
+
+
+def test_fd_box_agents_obstacles_and_walls():
+    """Boxes against a circle, a rotated box and a capsule, inside soft walls."""
+    cfgs = _dd(3)
+    obs = {"pos": [[[0.15, 0.0], [-0.2, 0.1], [0.0, -0.25]], [[0.1, 0.1], [-0.15, -0.1], [0.2, -0.2]]],
+           "radius": [0.08, 0.0, 0.03], "type": [0, 1, 2],
+           "angle": [0.0, 0.4, -0.3], "half": [[0.0, 0.0], [0.1, 0.06], [0.2, 0.0]],
+           "vel": [[[0.0, 0.0], [0.1, -0.2], [0.0, 0.0]]] * 2, "ang_vel": [[0.0, 0.5, -0.3]] * 2}
+    s0, rng = _rs(2, 3, 7, 0.22)
+    acts = rng.uniform(-1, 1, size=(2, 2, 3, 2))
+    w = _world(collision_c=1.0, bounds=(-0.32, 0.32, -0.32, 0.32))
+    _fd_check(cfgs, w, 0.05, 2, s0, acts, obs=obs, fields=(0, 1, 2, 3, 4, 5, 6))
+
+
+def test_fd_footprint_clamp():
+    """Diff-drive boxes driven into the clamp: the position gradient stops and the heading
+    picks up the footprint's dependence on it."""
+    cfgs = [_box(0.15, 0.05, model=DynamicsModel.DIFF_DRIVE, max_speed=5.0, max_ang_vel=5.0)
+            for _ in range(2)]
+    w = WorldConfig(collisions=False, bounds=(-0.4, 0.4, -0.4, 0.4), bounds_mode="clamp")
+    s0 = pack_state({"pos": [[[0.2, 0.0], [-0.1, -0.3]]], "theta": [[0.3, -1.9]]})
+    acts = np.array([[[[3.0, 0.7], [2.5, -0.4]]], [[[3.0, 0.5], [2.5, 0.3]]]])
+    _fd_check(cfgs, w, 0.1, 2, s0, acts, fields=(0, 1, 2, 3, 4, 5, 6))
+    # the clamp is active in this case (otherwise the test would not pin it)
+    cfg = oracle_cfg(cfgs, w, 0.1, 2, 1, 2)
+    p, t, m = params_of(cfgs)
+    tr = O.rollout(cfg, p, t, m, None, s0, acts)
+    th = tr[-1, 0, 0, 2]
+    ex = 0.15 * abs(math.cos(th)) + 0.05 * abs(math.sin(th))
+    assert tr[-1, 0, 0, 0] == pytest.approx(0.4 - ex, abs=1e-15)
