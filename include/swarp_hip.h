@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 5
+#define SWARP_ABI_VERSION 6
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -44,7 +44,9 @@ typedef struct swarp_desc {
     int32_t n_obstacles;
     int32_t collisions;      /* agent-agent contacts on */
     int32_t soft_walls;      /* bounds_mode == "soft" with bounds set */
-    int32_t clamp_bounds;    /* bounds_mode == "clamp" with bounds set (disc clamp) */
+    int32_t clamp_bounds;    /* bounds_mode == "clamp" with bounds set: 1 the disc clamp,
+                                2 the footprint clamp of a world holding box agents
+                                (clamp_footprint, swarp/dynamics/kernels.py:74-99) */
     int32_t has_drone;       /* fleet holds a DRONE: all nine fields are stepped */
     int32_t holo_velocity_only; /* every agent is HOLONOMIC in VELOCITY mode: selects the
                                    specialised kernels (must describe params truthfully) */
@@ -68,6 +70,10 @@ typedef struct swarp_desc {
     /* SWARP_EULER: semi-implicit Euler (_integrate_agent, swarp/dynamics/kernels.py:278-413);
        SWARP_RK4: classic RK4 on each substep (_integrate_rk4, :520-793), every model */
     int32_t integrator;
+    /* some agent is a BOX (params' shape column, swarp/dynamics/base.py:83-95): the
+       box-aware contact pass (collision_forces_box_kernel, swarp/core/collisions.py:
+       999-1059) -- oriented-rectangle contacts against discs, boxes, obstacles and walls */
+    int32_t has_boxes;
 } swarp_desc_t;
 
 /* The nine state fields.  A NULL field means "not provided": an input adjoint that

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 F32, F64 = 0, 1
 EULER, RK4 = 0, 1
 
@@ -64,6 +64,7 @@ class SwarpDesc(ctypes.Structure):
         ("lin_damping", ctypes.c_double),
         ("ang_damping", ctypes.c_double),
         ("integrator", ctypes.c_int32),
+        ("has_boxes", ctypes.c_int32),
     ]
 
 

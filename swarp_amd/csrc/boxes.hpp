@@ -1,0 +1,532 @@
+// boxes.hpp -- box agents: oriented-rectangle footprints in the contact pass.
+//
+// Counterpart of the reference's box-agent kernel (collision_forces_box_kernel,
+// swarp/core/collisions.py:999-1059) and the functions it calls: obb_contact / obb_force
+// (:312-487), _agent_pair_force (:489-541), _box_obstacle_force / _obstacle_forces_box
+// (:543-626), _wall_forces_box (:641-688), _static_forces_shaped (:950-996).
+//
+// Every function here is written once over a value type V: V = T in the forward pass,
+// V = Dual<T, 3> in the reverse pass, where three forward-mode tangents seeded on three
+// fields of the lane's own state (position and heading, then velocity and spin) give
+// the force's Jacobian columns for those fields.  Dual comparisons read the value part,
+// so the reverse pass takes the branches the forward pass took, and the value part is
+// the forward arithmetic itself (same operations, same order).  The derivative rules
+// are those of the generated adjoint the reference differentiates with: max/min/clamp
+// pass the tangent of the operand they return, abs(x) has slope sign(x) (+1 at 0).
+//
+// Included by swarp_hip.hip after physics.hpp.
+
+namespace swarp {
+
+template <typename T, int N> struct Dual {
+    T v;
+    T d[N];
+    __device__ __forceinline__ Dual() {}
+    __device__ __forceinline__ Dual(T x) : v(x)
+    {
+#pragma unroll
+        for (int i = 0; i < N; ++i) d[i] = T(0);
+    }
+};
+
+template <typename T> __device__ __forceinline__ T val(T x) { return x; }
+template <typename T, int N> __device__ __forceinline__ T val(const Dual<T, N> &x) { return x.v; }
+
+#define SWARP_DUAL_LOOP _Pragma("unroll") for (int i = 0; i < N; ++i)
+
+template <typename T, int N>
+__device__ __forceinline__ Dual<T, N> operator+(const Dual<T, N> &a, const Dual<T, N> &b)
+{
+    Dual<T, N> r;
+    r.v = a.v + b.v;
+    SWARP_DUAL_LOOP r.d[i] = a.d[i] + b.d[i];
+    return r;
+}
+template <typename T, int N>
+__device__ __forceinline__ Dual<T, N> operator-(const Dual<T, N> &a, const Dual<T, N> &b)
+{
+    Dual<T, N> r;
+    r.v = a.v - b.v;
+    SWARP_DUAL_LOOP r.d[i] = a.d[i] - b.d[i];
+    return r;
+}
+template <typename T, int N>
+__device__ __forceinline__ Dual<T, N> operator-(const Dual<T, N> &a)
+{
+    Dual<T, N> r;
+    r.v = -a.v;
+    SWARP_DUAL_LOOP r.d[i] = -a.d[i];
+    return r;
+}
+template <typename T, int N>
+__device__ __forceinline__ Dual<T, N> operator*(const Dual<T, N> &a, const Dual<T, N> &b)
+{
+    Dual<T, N> r;
+    r.v = a.v * b.v;
+    SWARP_DUAL_LOOP r.d[i] = a.d[i] * b.v + a.v * b.d[i];
+    return r;
+}
+template <typename T, int N>
+__device__ __forceinline__ Dual<T, N> operator*(const Dual<T, N> &a, T k)
+{
+    Dual<T, N> r;
+    r.v = a.v * k;
+    SWARP_DUAL_LOOP r.d[i] = a.d[i] * k;
+    return r;
+}
+template <typename T, int N>
+__device__ __forceinline__ Dual<T, N> operator/(const Dual<T, N> &a, const Dual<T, N> &b)
+{
+    Dual<T, N> r;
+    r.v = a.v / b.v;
+    SWARP_DUAL_LOOP r.d[i] = (a.d[i] - r.v * b.d[i]) / b.v;
+    return r;
+}
+template <typename T, int N>
+__device__ __forceinline__ Dual<T, N> operator/(const Dual<T, N> &a, T k)
+{
+    Dual<T, N> r;
+    r.v = a.v / k;
+    SWARP_DUAL_LOOP r.d[i] = a.d[i] / k;
+    return r;
+}
+template <typename T, int N>
+__device__ __forceinline__ bool operator>(const Dual<T, N> &a, const Dual<T, N> &b)
+{
+    return a.v > b.v;
+}
+template <typename T, int N>
+__device__ __forceinline__ bool operator<(const Dual<T, N> &a, const Dual<T, N> &b)
+{
+    return a.v < b.v;
+}
+template <typename T, int N> __device__ __forceinline__ Dual<T, N> m_sqrt(const Dual<T, N> &a)
+{
+    Dual<T, N> r;
+    r.v = m_sqrt(a.v);
+    const T h = r.v > T(0) ? T(0.5) / r.v : T(0);
+    SWARP_DUAL_LOOP r.d[i] = a.d[i] * h;
+    return r;
+}
+template <typename T, int N> __device__ __forceinline__ Dual<T, N> m_abs(const Dual<T, N> &a)
+{
+    return a.v < T(0) ? -a : a;
+}
+template <typename T, int N> __device__ __forceinline__ Dual<T, N> m_cos(const Dual<T, N> &a)
+{
+    Dual<T, N> r;
+    r.v = m_cos(a.v);
+    const T s = -m_sin(a.v);
+    SWARP_DUAL_LOOP r.d[i] = s * a.d[i];
+    return r;
+}
+template <typename T, int N> __device__ __forceinline__ Dual<T, N> m_sin(const Dual<T, N> &a)
+{
+    Dual<T, N> r;
+    r.v = m_sin(a.v);
+    const T c = m_cos(a.v);
+    SWARP_DUAL_LOOP r.d[i] = c * a.d[i];
+    return r;
+}
+template <typename T, int N> __device__ __forceinline__ Dual<T, N> m_tanh(const Dual<T, N> &a)
+{
+    Dual<T, N> r;
+    r.v = m_tanh(a.v);
+    const T s = T(1) - r.v * r.v;
+    SWARP_DUAL_LOOP r.d[i] = s * a.d[i];
+    return r;
+}
+#undef SWARP_DUAL_LOOP
+
+// Lane state as the contact pass sees it.
+enum { BX_PX = 0, BX_PY, BX_TH, BX_VX, BX_VY, BX_W };
+
+template <typename T> __device__ __forceinline__ T wmin(T a, T b) { return a < b ? a : b; }
+
+// _normal_coeff (collisions.py:87-105) over V; the same arithmetic as normal_coeff.
+template <typename T, typename V>
+__device__ __forceinline__ V normal_coeff_v(const Cst<T> &C, V ov, V vn, T dd)
+{
+    V o = ov;
+    if (C.max_overlap > T(0)) o = m_tanh(ov / C.max_overlap) * C.max_overlap;
+    return wmax((o * C.k - vn * C.c) / dd, V(T(0)));
+}
+
+// box_force (collisions.py:174-260): the point (p, v) against the box (c, angle given as
+// ca = cos, sa = sin, half-extents h) moving with (vo, om); reach = point radius + margin.
+template <typename T, typename V>
+__device__ __forceinline__ void box_force_v(const Cst<T> &C, V px, V py, V vx, V vy, V cx0, V cy0,
+                                            V ca, V sa, T hx, T hy, T reach, T dd, V vox, V voy,
+                                            V om, V &fx, V &fy)
+{
+    const V dx = px - cx0, dy = py - cy0;
+    const V lx = ca * dx + sa * dy;
+    const V ly = (-sa) * dx + ca * dy;
+    const V qx = m_abs(lx) - V(hx), qy = m_abs(ly) - V(hy);
+    const V ox = lx - wclamp(lx, V(-hx), V(hx)), oy = ly - wclamp(ly, V(-hy), V(hy));
+    const V od2 = ox * ox + oy * oy;
+    V s, nlx, nly;
+    if (val(od2) > C.eps2) {
+        s = m_sqrt(od2);
+        nlx = ox / s;
+        nly = oy / s;
+    } else if (val(qx) > val(qy)) {
+        s = qx;
+        nlx = V(val(lx) >= T(0) ? T(1) : T(-1));
+        nly = V(T(0));
+    } else {
+        s = qy;
+        nlx = V(T(0));
+        nly = V(val(ly) >= T(0) ? T(1) : T(-1));
+    }
+    fx = V(T(0));
+    fy = V(T(0));
+    const V ov = V(reach) - s;
+    if (val(ov) > T(0)) {
+        const V nx = ca * nlx - sa * nly, ny = sa * nlx + ca * nly;
+        const V spx = lx - s * nlx, spy = ly - s * nly;
+        const V rx = ca * spx - sa * spy, ry = sa * spx + ca * spy;
+        const V rvx = vx - (vox + (-om) * ry), rvy = vy - (voy + om * rx);
+        const V coef = normal_coeff_v(C, ov, rvx * nx + rvy * ny, dd);
+        fx = coef * nx;
+        fy = coef * ny;
+    }
+}
+
+// _point_box + _vertex_vs_box (collisions.py:273-310): vertex v against a box; keeps or
+// replaces (best distance, normal, contact point).  flip = +1 for a vertex of box A.
+template <typename T, typename V>
+__device__ __forceinline__ void vertex_vs_box(const Cst<T> &C, V vx, V vy, V cx, V cy, V ca, V sa,
+                                              T hx, T hy, T flip, V &best, V &nx, V &ny, V &xx,
+                                              V &xy)
+{
+    const V dx = vx - cx, dy = vy - cy;
+    const V lx = ca * dx + sa * dy;
+    const V ly = (-sa) * dx + ca * dy;
+    const V kx = wclamp(lx, V(-hx), V(hx)), ky = wclamp(ly, V(-hy), V(hy));
+    const V ox = lx - kx, oy = ly - ky;
+    const V dist = m_sqrt(wmax(ox * ox + oy * oy, V(C.eps2)));
+    if (val(dist) < val(best)) {
+        const V qx = cx + (ca * kx - sa * ky), qy = cy + (sa * kx + ca * ky);
+        const V sc = V(flip) / dist;
+        best = dist;
+        nx = (vx - qx) * sc;
+        ny = (vy - qy) * sc;
+        xx = (vx + qx) * T(0.5);
+        xy = (vy + qy) * T(0.5);
+    }
+}
+
+// obb_contact (collisions.py:312-447): signed distance s, unit normal n (from B to A) and
+// contact point x of box A (centre cA, heading cos/sin caA/saA, half-extents hA) and box B.
+template <typename T, typename V>
+__device__ __forceinline__ void obb_contact(const Cst<T> &C, V cAx, V cAy, V caA, V saA, T hA0,
+                                            T hA1, V cBx, V cBy, V caB, V saB, T hB0, T hB1,
+                                            T reach, V &s, V &nx, V &ny, V &xx, V &xy)
+{
+    const V uA0x = caA, uA0y = saA, uA1x = -saA, uA1y = caA;
+    const V uB0x = caB, uB0y = saB, uB1x = -saB, uB1y = caB;
+    const V dx = cAx - cBx, dy = cAy - cBy;
+    const V a00 = m_abs(uA0x * uB0x + uA0y * uB0y);
+    const V a01 = m_abs(uA0x * uB1x + uA0y * uB1y);
+    const V a10 = m_abs(uA1x * uB0x + uA1y * uB0y);
+    const V a11 = m_abs(uA1x * uB1x + uA1y * uB1y);
+    const V dA0 = dx * uA0x + dy * uA0y, dA1 = dx * uA1x + dy * uA1y;
+    const V dB0 = dx * uB0x + dy * uB0y, dB1 = dx * uB1x + dy * uB1y;
+
+    // projection gap along each face normal; the largest one is the SAT separation
+    s = (m_abs(dA0) - V(hA0)) - (a00 * hB0 + a01 * hB1);
+    int axis = 0;
+    V t = (m_abs(dA1) - V(hA1)) - (a10 * hB0 + a11 * hB1);
+    if (val(t) > val(s)) {
+        s = t;
+        axis = 1;
+    }
+    t = (m_abs(dB0) - V(hB0)) - (a00 * hA0 + a10 * hA1);
+    if (val(t) > val(s)) {
+        s = t;
+        axis = 2;
+    }
+    t = (m_abs(dB1) - V(hB1)) - (a01 * hA0 + a11 * hA1);
+    if (val(t) > val(s)) {
+        s = t;
+        axis = 3;
+    }
+
+    nx = V(T(0));
+    ny = V(T(0));
+    xx = cAx;
+    xy = cAy;
+    if (val(s) > reach) {
+        // no contact; s is a lower bound on the gap
+    } else if (val(s) > T(0)) {
+        // disjoint: the exact distance, attained at a vertex of one box against the other
+        const V eA0x = uA0x * hA0, eA0y = uA0y * hA0, eA1x = uA1x * hA1, eA1y = uA1y * hA1;
+        const V eB0x = uB0x * hB0, eB0y = uB0y * hB0, eB1x = uB1x * hB1, eB1y = uB1y * hB1;
+        V best = V(T(1.0e30));
+        const T one = T(1);
+        vertex_vs_box(C, (cAx + eA0x) + eA1x, (cAy + eA0y) + eA1y, cBx, cBy, caB, saB, hB0, hB1,
+                      one, best, nx, ny, xx, xy);
+        vertex_vs_box(C, (cAx - eA0x) + eA1x, (cAy - eA0y) + eA1y, cBx, cBy, caB, saB, hB0, hB1,
+                      one, best, nx, ny, xx, xy);
+        vertex_vs_box(C, (cAx - eA0x) - eA1x, (cAy - eA0y) - eA1y, cBx, cBy, caB, saB, hB0, hB1,
+                      one, best, nx, ny, xx, xy);
+        vertex_vs_box(C, (cAx + eA0x) - eA1x, (cAy + eA0y) - eA1y, cBx, cBy, caB, saB, hB0, hB1,
+                      one, best, nx, ny, xx, xy);
+        vertex_vs_box(C, (cBx + eB0x) + eB1x, (cBy + eB0y) + eB1y, cAx, cAy, caA, saA, hA0, hA1,
+                      -one, best, nx, ny, xx, xy);
+        vertex_vs_box(C, (cBx - eB0x) + eB1x, (cBy - eB0y) + eB1y, cAx, cAy, caA, saA, hA0, hA1,
+                      -one, best, nx, ny, xx, xy);
+        vertex_vs_box(C, (cBx - eB0x) - eB1x, (cBy - eB0y) - eB1y, cAx, cAy, caA, saA, hA0, hA1,
+                      -one, best, nx, ny, xx, xy);
+        vertex_vs_box(C, (cBx + eB0x) - eB1x, (cBy + eB0y) - eB1y, cAx, cAy, caA, saA, hA0, hA1,
+                      -one, best, nx, ny, xx, xy);
+        s = best;
+    } else {
+        // overlapping: the axis of least overlap, oriented B -> A, and its reference face
+        V ux = uA0x, uy = uA0y, tx = uA1x, ty = uA1y, dn = dA0;
+        T h_n = hA0, h_t = hA1;
+        V r_t = a10 * hB0 + a11 * hB1;  // the incident box's reach along tdir
+        if (axis == 1) {
+            ux = uA1x; uy = uA1y; tx = uA0x; ty = uA0y; dn = dA1;
+            h_n = hA1; h_t = hA0;
+            r_t = a00 * hB0 + a01 * hB1;
+        } else if (axis == 2) {
+            ux = uB0x; uy = uB0y; tx = uB1x; ty = uB1y; dn = dB0;
+            h_n = hB0; h_t = hB1;
+            r_t = a01 * hA0 + a11 * hA1;
+        } else if (axis == 3) {
+            ux = uB1x; uy = uB1y; tx = uB0x; ty = uB0y; dn = dB1;
+            h_n = hB1; h_t = hB0;
+            r_t = a00 * hA0 + a10 * hA1;
+        }
+        const T sgn = val(dn) < T(0) ? T(-1) : T(1);
+        nx = ux * sgn;
+        ny = uy * sgn;
+        // reference face: A's face toward B for an A axis, B's face toward A for a B axis
+        V crx = cAx, cry = cAy, cix = cBx, ciy = cBy;
+        V xn = (cAx * nx + cAy * ny) - V(h_n);
+        if (axis >= 2) {
+            crx = cBx; cry = cBy; cix = cAx; ciy = cAy;
+            xn = (cBx * nx + cBy * ny) + V(h_n);
+        }
+        const V ct_ref = crx * tx + cry * ty, ct_inc = cix * tx + ciy * ty;
+        const V lo = wmax(ct_ref - V(h_t), ct_inc - r_t);
+        const V hi = wmin(ct_ref + V(h_t), ct_inc + r_t);
+        const V mid = V(T(0.5)) * (lo + hi);
+        xx = nx * xn + tx * mid;
+        xy = ny * xn + ty * mid;
+    }
+}
+
+// obb_force (collisions.py:449-487): force on box A from box B; the damper reads the
+// closing velocity of the two material points at the contact point.
+template <typename T, typename V>
+__device__ __forceinline__ void obb_force(const Cst<T> &C, V cAx, V cAy, V caA, V saA, T hA0,
+                                          T hA1, V vAx, V vAy, V wA, V cBx, V cBy, V caB, V saB,
+                                          T hB0, T hB1, V vBx, V vBy, V wB, T reach, T dd, V &fx,
+                                          V &fy)
+{
+    V s, nx, ny, xx, xy;
+    obb_contact(C, cAx, cAy, caA, saA, hA0, hA1, cBx, cBy, caB, saB, hB0, hB1, reach, s, nx, ny,
+                xx, xy);
+    fx = V(T(0));
+    fy = V(T(0));
+    const V ov = V(reach) - s;
+    if (val(ov) > T(0)) {
+        const V rAx = xx - cAx, rAy = xy - cAy, rBx = xx - cBx, rBy = xy - cBy;
+        const V pax = vAx + (-wA) * rAy, pay = vAy + wA * rAx;
+        const V pbx = vBx + (-wB) * rBy, pby = vBy + wB * rBx;
+        const V rvx = pax - pbx, rvy = pay - pby;
+        const V coef = normal_coeff_v(C, ov, rvx * nx + rvy * ny, dd);
+        fx = coef * nx;
+        fy = coef * ny;
+    }
+}
+
+// Footprint of one agent as the contact pass needs it.
+template <typename T> struct Foot {
+    T shape, radius, hx, hy;
+};
+
+// _agent_pair_force (collisions.py:489-541) for a pair with at least one box: the force
+// on agent a (state sa, heading cos/sin ca/sn_a) from agent b.  Box-box evaluates the one
+// contact with the lower index as box A on both sides.
+template <typename T, typename V>
+__device__ __forceinline__ void agent_pair_force_box(const Cst<T> &C, int a, int b,
+                                                     const Foot<T> &Fa, const V (&sa)[6], V caa,
+                                                     V saa, const Foot<T> &Fb, const V (&sb)[6],
+                                                     V cab, V sab, T dd, V &fx, V &fy)
+{
+    const T half = T(0.5);
+    if (Fa.shape < half) {
+        box_force_v(C, sa[BX_PX], sa[BX_PY], sa[BX_VX], sa[BX_VY], sb[BX_PX], sb[BX_PY], cab, sab,
+                    Fb.hx, Fb.hy, Fa.radius + C.margin, dd, sb[BX_VX], sb[BX_VY], sb[BX_W], fx, fy);
+    } else if (Fb.shape < half) {
+        V gx, gy;
+        box_force_v(C, sb[BX_PX], sb[BX_PY], sb[BX_VX], sb[BX_VY], sa[BX_PX], sa[BX_PY], caa, saa,
+                    Fa.hx, Fa.hy, Fb.radius + C.margin, dd, sa[BX_VX], sa[BX_VY], sa[BX_W], gx, gy);
+        fx = -gx;
+        fy = -gy;
+    } else if (a < b) {
+        obb_force(C, sa[BX_PX], sa[BX_PY], caa, saa, Fa.hx, Fa.hy, sa[BX_VX], sa[BX_VY], sa[BX_W],
+                  sb[BX_PX], sb[BX_PY], cab, sab, Fb.hx, Fb.hy, sb[BX_VX], sb[BX_VY], sb[BX_W],
+                  C.margin, dd, fx, fy);
+    } else {
+        V gx, gy;
+        obb_force(C, sb[BX_PX], sb[BX_PY], cab, sab, Fb.hx, Fb.hy, sb[BX_VX], sb[BX_VY], sb[BX_W],
+                  sa[BX_PX], sa[BX_PY], caa, saa, Fa.hx, Fa.hy, sa[BX_VX], sa[BX_VY], sa[BX_W],
+                  C.margin, dd, gx, gy);
+        fx = -gx;
+        fy = -gy;
+    }
+}
+
+// Static forces on a box agent (state s, heading cos/sin ca/sa): obstacles in index order
+// (_obstacle_forces_box + _box_obstacle_force, :543-626), then the soft walls
+// (_wall_forces_box, :641-688).  `ocs`: this env's obstacle angles as (cos, sin) pairs,
+// or NULL.
+template <typename T, typename V>
+__device__ __forceinline__ void box_static_forces(const Cst<T> &C, const Obs<T> &O, size_t eN,
+                                                  const T *ocs, T hx, T hy, const V (&s)[6], V ca,
+                                                  V sa, T dd, V &fx_o, V &fy_o)
+{
+    V fx = V(T(0)), fy = V(T(0));
+    const T ra = m_sqrt(hx * hx + hy * hy);
+    for (int o = 0; o < C.N; ++o) {
+        const size_t j = eN + o;
+        const T cx = O.pos[2 * j], cy = O.pos[2 * j + 1];
+        const int st = O.type[o];
+        const T ro = O.rad[o], ohx = O.half[2 * o], ohy = O.half[2 * o + 1];
+        const T bound = st == 1 ? m_sqrt(ohx * ohx + ohy * ohy) : (st == 2 ? ohx + ro : ro);
+        const T lim = (ra + C.margin + bound) * T(1.0001) + T(1.0e-6);
+        const T ddx = val(s[BX_PX]) - cx, ddy = val(s[BX_PY]) - cy;
+        if (ddx * ddx + ddy * ddy > lim * lim) continue;
+        T oc, os;
+        ob_trig(O, j, o, ocs, oc, os);
+        const V vox = V(O.vel[2 * j]), voy = V(O.vel[2 * j + 1]), om = V(O.om[j]);
+        V gx, gy;
+        if (st == 1) {
+            obb_force(C, s[BX_PX], s[BX_PY], ca, sa, hx, hy, s[BX_VX], s[BX_VY], s[BX_W], V(cx),
+                      V(cy), V(oc), V(os), ohx, ohy, vox, voy, om, C.margin, dd, gx, gy);
+        } else if (st == 2) {
+            // a capsule: the degenerate box (half_len, 0) with the reach grown by its radius
+            obb_force(C, s[BX_PX], s[BX_PY], ca, sa, hx, hy, s[BX_VX], s[BX_VY], s[BX_W], V(cx),
+                      V(cy), V(oc), V(os), ohx, T(0), vox, voy, om, ro + C.margin, dd, gx, gy);
+        } else {
+            // a circle: minus box_force with the circle's centre as the point
+            V hxv, hyv;
+            box_force_v(C, V(cx), V(cy), vox, voy, s[BX_PX], s[BX_PY], ca, sa, hx, hy,
+                        ro + C.margin, dd, s[BX_VX], s[BX_VY], s[BX_W], hxv, hyv);
+            gx = -hxv;
+            gy = -hyv;
+        }
+        fx = fx + gx;
+        fy = fy + gy;
+    }
+    if (C.soft_walls) {
+        // the walls see the support extents; the damper reads the touching vertex's velocity
+        const V ex = m_abs(ca) * hx + m_abs(sa) * hy;
+        const V ey = m_abs(sa) * hx + m_abs(ca) * hy;
+        const T vc = val(ca), vs = val(sa);
+        const T sc = vc > T(0) ? T(1) : (vc < T(0) ? T(-1) : T(0));
+        const T ss = vs > T(0) ? T(1) : (vs < T(0) ? T(-1) : T(0));
+        const V rl_y = sa * (-sc * hx) + ca * (ss * hy);
+        const V rb_x = ca * (-ss * hx) + sa * (sc * hy);
+        const V em = ex + V(C.margin), eym = ey + V(C.margin);
+        V wx = V(T(0)), wy = V(T(0));
+        V pen = em - (s[BX_PX] - V(C.bmin_x));
+        if (val(pen) > T(0)) wx = wx + normal_coeff_v(C, pen, s[BX_VX] - s[BX_W] * rl_y, dd);
+        pen = em - (V(C.bmax_x) - s[BX_PX]);
+        if (val(pen) > T(0))
+            wx = wx + (-normal_coeff_v(C, pen, -(s[BX_VX] + s[BX_W] * rl_y), dd));
+        pen = eym - (s[BX_PY] - V(C.bmin_y));
+        if (val(pen) > T(0)) wy = wy + normal_coeff_v(C, pen, s[BX_VY] + s[BX_W] * rb_x, dd);
+        pen = eym - (V(C.bmax_y) - s[BX_PY]);
+        if (val(pen) > T(0))
+            wy = wy + (-normal_coeff_v(C, pen, -(s[BX_VY] - s[BX_W] * rb_x), dd));
+        fx = fx + wx;
+        fy = fy + wy;
+    }
+    fx_o = fx;
+    fy_o = fy;
+}
+
+// ------------------------------------------------------------------ reverse helpers
+
+// Adds J^T w to the lane's adjoint, where J holds the Jacobian columns of (fx, fy) with
+// respect to the seeded fields k0, k0+1, k0+2 of the lane's state.
+template <typename T>
+__device__ __forceinline__ void add_cols(const Dual<T, 3> &fx, const Dual<T, 3> &fy, T wx, T wy,
+                                         int k0, St<T> &g)
+{
+    const T c0 = wx * fx.d[0] + wy * fy.d[0];
+    const T c1 = wx * fx.d[1] + wy * fy.d[1];
+    const T c2 = wx * fx.d[2] + wy * fy.d[2];
+    if (k0 == BX_PX) {
+        g.px += c0;
+        g.py += c1;
+        g.th += c2;
+    } else {
+        g.vx += c0;
+        g.vy += c1;
+        g.w += c2;
+    }
+}
+
+// The lane's state as duals with fields k0..k0+2 seeded (one tangent each).
+template <typename T>
+__device__ __forceinline__ void seed_state(const St<T> &s, int k0, Dual<T, 3> (&o)[6])
+{
+    const T f[6] = {s.px, s.py, s.th, s.vx, s.vy, s.w};
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        o[k] = Dual<T, 3>(f[k]);
+        if (k >= k0 && k < k0 + 3) o[k].d[k - k0] = T(1);
+    }
+}
+
+// Reverse of a pair with a box, seen from agent a (state `in`) against agent b (`sb`,
+// cos/sin of its heading cb/sb_): adds J_a(f)^T w, with f the pair function evaluated
+// with a unit damping denominator and w the caller's combined cotangent (own force
+// adjoint / dd_a minus, where a is in b's list, b's / dd_b).
+template <typename T>
+__device__ __forceinline__ void box_pair_adj(const Cst<T> &C, int a, int b, const Foot<T> &Fa,
+                                             const St<T> &in, const Foot<T> &Fb, const T (&sb)[6],
+                                             T wx, T wy, St<T> &g)
+{
+    typedef Dual<T, 3> D3;
+    D3 ob[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) ob[k] = D3(sb[k]);
+    const D3 cbv = m_cos(D3(sb[BX_TH])), sbv = m_sin(D3(sb[BX_TH]));
+#pragma unroll 1
+    for (int k0 = 0; k0 < 6; k0 += 3) {
+        D3 me[6];
+        seed_state(in, k0, me);
+        const D3 ca = m_cos(me[BX_TH]), sa = m_sin(me[BX_TH]);
+        D3 fx, fy;
+        agent_pair_force_box<T, D3>(C, a, b, Fa, me, ca, sa, Fb, ob, cbv, sbv, T(1), fx, fy);
+        add_cols(fx, fy, wx, wy, k0, g);
+    }
+}
+
+// Reverse of a box agent's static forces: adds J(f)^T g_F.
+template <typename T>
+__device__ __forceinline__ void box_static_adj(const Cst<T> &C, const Obs<T> &O, size_t eN,
+                                               const T *ocs, const Foot<T> &Fa, const St<T> &in,
+                                               T dd, T gx, T gy, St<T> &g)
+{
+    typedef Dual<T, 3> D3;
+#pragma unroll 1
+    for (int k0 = 0; k0 < 6; k0 += 3) {
+        D3 me[6];
+        seed_state(in, k0, me);
+        const D3 ca = m_cos(me[BX_TH]), sa = m_sin(me[BX_TH]);
+        D3 fx, fy;
+        box_static_forces<T, D3>(C, O, eN, ocs, Fa.hx, Fa.hy, me, ca, sa, dd, fx, fy);
+        add_cols(fx, fy, gx, gy, k0, g);
+    }
+}
+
+}  // namespace swarp

@@ -54,6 +54,7 @@ template <typename T> __device__ __forceinline__ void st_zero(St<T> &g)
 template <typename T> struct Prm {
     T radius, mass, max_speed, max_accel, max_ang_vel, max_ang_accel, l_f, l_r, max_steer;
     T thrust_max, arm, ixx, iyy, izz, kappa, gravity, min_speed;
+    T shape, hx, hy;  // footprint: 0 disc, 1 box of half-extents (hx, hy)
     int tag, mode;
 };
 
@@ -66,7 +67,9 @@ template <typename T> struct Cst {
     T half_margin;  // per-agent displacement budget that keeps the skin list exact
     T bmin_x, bmin_y, bmax_x, bmax_y;
     int E, A, ad, S, K, N;
-    int collisions, soft_walls, clamp, needs_forces, use_skin;
+    int collisions, soft_walls, needs_forces, use_skin;
+    int clamp;     // 0 off, 1 disc clamp, 2 footprint clamp (a world holding box agents)
+    int boxes;     // some agent is a box: the box-aware contact pass
     int fast_div;  // neighbour radius <= 2^20: contact distances are short-division divisors
     int rk4;       // Integrator.RK4 instead of semi-implicit Euler
 };
@@ -735,6 +738,56 @@ __device__ __forceinline__ void obstacle_force_adj(const Cst<T> &C, const Obs<T>
 
 // ------------------------------------------------------------- integration
 
+// Inset of the position clamp along x and y (clamp_footprint, swarp/dynamics/kernels.py:
+// 79-99): a disc by its radius; under the footprint clamp a box at heading th by its
+// support extents hx |cos| + hy |sin| and hx |sin| + hy |cos|.
+template <typename T>
+__device__ __forceinline__ void clamp_insets(const Cst<T> &C, const Prm<T> &P, T th, T &ex, T &ey)
+{
+    ex = P.radius;
+    ey = P.radius;
+    if (C.clamp == 2 && P.shape > T(0.5)) {
+        const T ca = m_abs(m_cos(th)), sa = m_abs(m_sin(th));
+        ex = P.hx * ca + P.hy * sa;
+        ey = P.hx * sa + P.hy * ca;
+    }
+}
+
+// The position clamp of a substep's output (kernels.py:395-403).
+template <typename T>
+__device__ __forceinline__ void clamp_position(const Cst<T> &C, const Prm<T> &P, T th, T &px, T &py)
+{
+    T ex, ey;
+    clamp_insets(C, P, th, ex, ey);
+    px = wclamp(px, C.bmin_x + ex, C.bmax_x - ex);
+    py = wclamp(py, C.bmin_y + ey, C.bmax_y - ey);
+}
+
+// Reverse of clamp_position at the unclamped output (px, py, th): rewrites the position
+// adjoint (clamp(x, a, b): x < a -> a, x > b -> b, else x) and adds the heading's share,
+// through the footprint's bounds, to gth.
+template <typename T>
+__device__ __forceinline__ void clamp_position_adj(const Cst<T> &C, const Prm<T> &P, T px, T py,
+                                                   T th, T &gpx, T &gpy, T &gth)
+{
+    T ex, ey;
+    clamp_insets(C, P, th, ex, ey);
+    const T lox = C.bmin_x + ex, hix = C.bmax_x - ex, loy = C.bmin_y + ey, hiy = C.bmax_y - ey;
+    T aex = T(0), aey = T(0);
+    if (px < lox) aex += gpx;
+    else if (px > hix) aex -= gpx;
+    if (py < loy) aey += gpy;
+    else if (py > hiy) aey -= gpy;
+    gpx = wclamp_g(px, lox, hix, gpx);
+    gpy = wclamp_g(py, loy, hiy, gpy);
+    if (C.clamp == 2 && P.shape > T(0.5) && (aex != T(0) || aey != T(0))) {
+        const T c = m_cos(th), s = m_sin(th);
+        const T dca = c < T(0) ? s : -s;  // d|cos th| / dth
+        const T dsa = s < T(0) ? -c : c;  // d|sin th| / dth
+        gth += aex * (P.hx * dca + P.hy * dsa) + aey * (P.hx * dsa + P.hy * dca);
+    }
+}
+
 // clamp_norm (swarp/dynamics/kernels.py:68-71)
 template <typename T>
 __device__ __forceinline__ void clamp_norm(T x, T y, T lim, T &ox, T &oy)
@@ -1035,10 +1088,7 @@ __device__ __forceinline__ void integrate_rk4(const Cst<T> &C, const Prm<T> &P, 
     } else {
         return;
     }
-    if (C.clamp) {
-        pnx = wclamp(pnx, C.bmin_x + P.radius, C.bmax_x - P.radius);
-        pny = wclamp(pny, C.bmin_y + P.radius, C.bmax_y - P.radius);
-    }
+    if (C.clamp) clamp_position(C, P, o.th, pnx, pny);
     o.px = pnx;
     o.py = pny;
 }
@@ -1063,10 +1113,6 @@ __device__ __forceinline__ void integrate_rk4_adj(const Cst<T> &C, const Prm<T> 
     rk_stages<T, DRONE>(C, P, in, a, R);
     const T dfx = Fx * (dt / P.mass), dfy = Fy * (dt / P.mass);
     T gpx = g.px, gpy = g.py;
-    if (C.clamp) {
-        gpx = wclamp_g(R.xi.px + dfx * dt, C.bmin_x + P.radius, C.bmax_x - P.radius, gpx);
-        gpy = wclamp_g(R.xi.py + dfy * dt, C.bmin_y + P.radius, C.bmax_y - P.radius, gpy);
-    }
     St<T> gxi;
     st_zero(gxi);
     gxi.px = gpx;
@@ -1275,20 +1321,19 @@ __device__ __forceinline__ void integrate(const Cst<T> &C, const Prm<T> &P, cons
         o.s = sn;
         o.w = wn;
     }
-    if (C.clamp) {
-        pnx = wclamp(pnx, C.bmin_x + P.radius, C.bmax_x - P.radius);
-        pny = wclamp(pny, C.bmin_y + P.radius, C.bmax_y - P.radius);
-    }
+    if (C.clamp) clamp_position(C, P, o.th, pnx, pny);
     o.px = pnx;
     o.py = pny;
 }
 
-// Reverse of integrate.  g = adjoint of the substep output.  Overwrites gi with the
-// adjoint of the substep input, accumulates ga (actions) and returns gF (force).
+// Reverse of integrate without its position clamp (integrate_adj reverses that first).
+// g = adjoint of the substep output.  Overwrites gi with the adjoint of the substep
+// input, accumulates ga (actions) and returns gF (force).
 template <typename T, bool DRONE>
-__device__ __forceinline__ void integrate_adj(const Cst<T> &C, const Prm<T> &P, const St<T> &in,
-                                              const T (&a)[4], T Fx, T Fy, const St<T> &g,
-                                              St<T> &gi, T (&ga)[4], T &gFx, T &gFy)
+__device__ __forceinline__ void integrate_adj_core(const Cst<T> &C, const Prm<T> &P,
+                                                   const St<T> &in, const T (&a)[4], T Fx, T Fy,
+                                                   const St<T> &g, St<T> &gi, T (&ga)[4], T &gFx,
+                                                   T &gFy)
 {
     if (C.rk4) {
         integrate_rk4_adj<T, DRONE>(C, P, in, a, Fx, Fy, g, gi, ga, gFx, gFy);
@@ -1323,11 +1368,6 @@ __device__ __forceinline__ void integrate_adj(const Cst<T> &C, const Prm<T> &P, 
         T uw = qw + h * (-qx * nbx - qy * nby - qz * nbz) * dt;
         T l = m_sqrt(ux * ux + uy * uy + uz * uz + uw * uw);
         (void)accx; (void)accy; (void)accz;
-        if (C.clamp) {
-            T vxx = in.vx + accx * dt + dvx, vxy = in.vy + accy * dt + dvy;
-            gpx = wclamp_g(in.px + vxx * dt, C.bmin_x + P.radius, C.bmax_x - P.radius, gpx);
-            gpy = wclamp_g(in.py + vxy * dt, C.bmin_y + P.radius, C.bmax_y - P.radius, gpy);
-        }
         gi.px = gpx;
         gi.py = gpy;
         T gvx = g.vx + gpx * dt, gvy = g.vy + gpy * dt;
@@ -1402,10 +1442,6 @@ __device__ __forceinline__ void integrate_adj(const Cst<T> &C, const Prm<T> &P, 
         }
         vnx = vnx + dvx;
         vny = vny + dvy;
-        if (C.clamp) {
-            gpx = wclamp_g(in.px + vnx * dt, C.bmin_x + P.radius, C.bmax_x - P.radius, gpx);
-            gpy = wclamp_g(in.py + vny * dt, C.bmin_y + P.radius, C.bmax_y - P.radius, gpy);
-        }
         T sp = m_sqrt(vnx * vnx + vny * vny);
         gi.px = gpx;
         gi.py = gpy;
@@ -1442,10 +1478,6 @@ __device__ __forceinline__ void integrate_adj(const Cst<T> &C, const Prm<T> &P, 
             wn = wclamp(in.w + alp * dt, -P.max_ang_vel, P.max_ang_vel);
         }
         T c = m_cos(in.th), sg = m_sin(in.th);
-        if (C.clamp) {
-            gpx = wclamp_g(in.px + (sn * c + dvx) * dt, C.bmin_x + P.radius, C.bmax_x - P.radius, gpx);
-            gpy = wclamp_g(in.py + (sn * sg + dvy) * dt, C.bmin_y + P.radius, C.bmax_y - P.radius, gpy);
-        }
         gi.px = gpx;
         gi.py = gpy;
         T gvx = g.vx + gpx * dt, gvy = g.vy + gpy * dt;
@@ -1479,10 +1511,6 @@ __device__ __forceinline__ void integrate_adj(const Cst<T> &C, const Prm<T> &P, 
         T beta = m_atan(bu);
         T ang = in.th + beta;
         T ca = m_cos(ang), sa = m_sin(ang), cb = m_cos(beta);
-        if (C.clamp) {
-            gpx = wclamp_g(in.px + (sn * ca + dvx) * dt, C.bmin_x + P.radius, C.bmax_x - P.radius, gpx);
-            gpy = wclamp_g(in.py + (sn * sa + dvy) * dt, C.bmin_y + P.radius, C.bmax_y - P.radius, gpy);
-        }
         gi.px = gpx;
         gi.py = gpy;
         T gvx = g.vx + gpx * dt, gvy = g.vy + gpy * dt;
@@ -1502,6 +1530,24 @@ __device__ __forceinline__ void integrate_adj(const Cst<T> &C, const Prm<T> &P, 
         ga[0] += wclamp_g(a[0], -P.max_accel, P.max_accel, gx * dt);
         ga[1] += wclamp_g(a[1], -P.max_steer, P.max_steer, gtd * (T(1) + td * td));
     }
+}
+
+// Reverse of integrate: the position clamp, reversed at the unclamped output (its
+// bounds move with the heading under the footprint clamp), then the rest of the step.
+template <typename T, bool DRONE>
+__device__ __forceinline__ void integrate_adj(const Cst<T> &C, const Prm<T> &P, const St<T> &in,
+                                              const T (&a)[4], T Fx, T Fy, const St<T> &g,
+                                              St<T> &gi, T (&ga)[4], T &gFx, T &gFy)
+{
+    Cst<T> C0 = C;
+    C0.clamp = 0;
+    St<T> g2 = g;
+    if (C.clamp) {
+        St<T> raw;
+        integrate<T, DRONE>(C0, P, in, a, Fx, Fy, raw);
+        clamp_position_adj(C, P, raw.px, raw.py, raw.th, g2.px, g2.py, g2.th);
+    }
+    integrate_adj_core<T, DRONE>(C0, P, in, a, Fx, Fy, g2, gi, ga, gFx, gFy);
 }
 
 }  // namespace swarp

@@ -26,6 +26,7 @@
 #include <string.h>
 
 #include "physics.hpp"
+#include "boxes.hpp"
 #include "swarp_hip.h"
 
 namespace swarp {
@@ -143,6 +144,7 @@ __device__ __forceinline__ void load_prm(const Args<T> &g, int a, Prm<T> &p)
     p.max_ang_vel = r[4]; p.max_ang_accel = r[5]; p.l_f = r[6]; p.l_r = r[7];
     p.max_steer = r[8]; p.thrust_max = r[9]; p.arm = r[10]; p.ixx = r[11];
     p.iyy = r[12]; p.izz = r[13]; p.kappa = r[14]; p.gravity = r[15]; p.min_speed = r[16];
+    p.shape = r[17]; p.hx = r[18]; p.hy = r[19];
     p.tag = g.tag[a];
     p.mode = g.mode[a];
 }
@@ -273,12 +275,23 @@ __device__ __forceinline__ const T *ob_trig_table(const Cst<T> &C, const Args<T>
     return ocs + 2 * ew * C.N;
 }
 
-template <typename T, int PA>
+// Box worlds: `lbx` holds per lane the footprint (shape, hx, hy rows of 64) and the slot
+// `sl` also carries the headings and spins (F_TH, F_W rows).  BOXES = false compiles the
+// box paths out (fleets with drones, which are never boxes).
+template <typename T, int PA, bool BOXES>
 __device__ __forceinline__ typename MaskT<PA>::type forces(
     const Cst<T> &C, const Args<T> &g, const Lane<T, PA> &L, const T *sl, const T *lr,
     const St<T> &st, int s, bool full, typename MaskT<PA>::type &cand, T &Fx, T &Fy,
-    const T *ocs = nullptr)
+    const T *ocs = nullptr, const T *lbx = nullptr)
 {
+    const bool boxes = BOXES && C.boxes;
+    const bool box_me = boxes && L.pr.shape > T(0.5);
+    T me[6] = {st.px, st.py, st.th, st.vx, st.vy, st.w};
+    T cme = T(1), sme = T(0);
+    if (boxes) {
+        cme = m_cos(st.th);
+        sme = m_sin(st.th);
+    }
     typedef typename MaskT<PA>::type M;
     const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64, *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
     M incl = 0;
@@ -293,19 +306,33 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
         }
         M m = cap_list(incl, C.K);
         const T ra = L.pr.radius;
+        const Foot<T> fa = {L.pr.shape, ra, L.pr.hx, L.pr.hy};
+        const T *lth = sl + F_TH * 64, *lw = sl + F_W * 64;
         while (m) {
             const int b = m_ctz(m);
             m &= m - 1;
             const int j = L.base + b;
             T gx, gy;
-            pair_force(C, st.px - lx[j], st.py - ly[j], st.vx - lvx[j], st.vy - lvy[j],
-                       ra + lr[j] + C.margin, L.dd, gx, gy);
+            if (boxes && (box_me || lbx[j] > T(0.5))) {
+                // a pair with a box (collision_forces_box_kernel, collisions.py:1044-1052)
+                const Foot<T> fb = {lbx[j], lr[j], lbx[64 + j], lbx[128 + j]};
+                const T ob[6] = {lx[j], ly[j], lth[j], lvx[j], lvy[j], lw[j]};
+                agent_pair_force_box<T, T>(C, L.agent, b, fa, me, cme, sme, fb, ob,
+                                           m_cos(lth[j]), m_sin(lth[j]), L.dd, gx, gy);
+            } else {
+                pair_force(C, st.px - lx[j], st.py - ly[j], st.vx - lvx[j], st.vy - lvy[j],
+                           ra + lr[j] + C.margin, L.dd, gx, gy);
+            }
             fx += gx;
             fy += gy;
         }
     }
     T sx = T(0), sy = T(0);
-    if (C.N > 0) {
+    if (box_me) {
+        // a box agent's obstacles and walls (_static_forces_shaped, collisions.py:950-996)
+        const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
+        box_static_forces<T, T>(C, g.obs, eN, ocs, L.pr.hx, L.pr.hy, me, cme, sme, L.dd, sx, sy);
+    } else if (C.N > 0) {
         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
         for (int o = 0; o < C.N; ++o) {
             T gx, gy;
@@ -315,7 +342,7 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
             sy += gy;
         }
     }
-    if (C.soft_walls) {
+    if (C.soft_walls && !box_me) {
         T gx, gy;
         unsigned wb;
         wall_force_axes(C, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv, gx, gy, wb);
@@ -333,12 +360,16 @@ template <typename T, int PA, bool DRONE>
 __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> C, const Args<T> g)
 {
     typedef typename MaskT<PA>::type M;
-    __shared__ T sl[4 * 64];  // px py vx vy of the current substep
+    __shared__ T sl[7 * 64];  // px py vx vy th (s) w of the current substep
     __shared__ T lr[64];      // agent radius per lane
+    __shared__ T lbx[3 * 64]; // footprint per lane: shape, hx, hy (box worlds)
     __shared__ T ocs_lds[2 * OCS_MAX];
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
     lr[L.lane] = L.pr.radius;
+    lbx[L.lane] = L.pr.shape;
+    lbx[64 + L.lane] = L.pr.hx;
+    lbx[128 + L.lane] = L.pr.hy;
     const T *ocs = ob_trig_table<T, PA>(C, g, L, ocs_lds);
     St<T> st;
     load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
@@ -359,9 +390,13 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> C, const Args<T
                     sl[F_PY * 64 + L.lane] = st.py;
                     sl[F_VX * 64 + L.lane] = st.vx;
                     sl[F_VY * 64 + L.lane] = st.vy;
+                    if (C.boxes) {
+                        sl[F_TH * 64 + L.lane] = st.th;
+                        sl[F_W * 64 + L.lane] = st.w;
+                    }
                     __syncthreads();
                 }
-                forces<T, PA>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy, ocs);
+                forces<T, PA, !DRONE>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy, ocs, lbx);
             }
             St<T> nx;
             integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
@@ -430,9 +465,13 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
     T *slots = ldd + 64;        // S slots of NF fields
     M *lmask = (M *)(slots + (size_t)C.S * NF * 64);  // S inclusion masks per lane
     __shared__ T ocs_lds[2 * OCS_MAX];
+    __shared__ T lbx[3 * 64];  // footprint per lane: shape, hx, hy (box worlds)
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
     lr[L.lane] = L.pr.radius;
+    lbx[L.lane] = L.pr.shape;
+    lbx[64 + L.lane] = L.pr.hx;
+    lbx[128 + L.lane] = L.pr.hy;
     ldd[L.lane] = L.dd;
     const T *ocs = ob_trig_table<T, PA>(C, g, L, ocs_lds);
     const size_t EA = (size_t)C.E * C.A;
@@ -464,7 +503,8 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
             T Fx = T(0), Fy = T(0);
             M incl = 0;
             if (C.needs_forces)
-                incl = forces<T, PA>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy, ocs);
+                incl = forces<T, PA, !DRONE>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy,
+                                             ocs, lbx);
             sl[F_FX * 64 + L.lane] = Fx;
             sl[F_FY * 64 + L.lane] = Fy;
             lmask[s * 64 + L.lane] = incl;
@@ -510,19 +550,36 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
                         if (!own && !rev) continue;
                         const T wx = (own ? wFx : T(0)) - (rev ? lgx[j] : T(0));
                         const T wy = (own ? wFy : T(0)) - (rev ? lgy[j] : T(0));
-                        pair_adj_combined(C, in.px - lx[j], in.py - ly[j], in.vx - lvx[j],
-                                          in.vy - lvy[j], L.pr.radius + lr[j] + C.margin, wx, wy,
-                                          gi.px, gi.py, gi.vx, gi.vy);
+                        if (!DRONE && C.boxes && (L.pr.shape > T(0.5) || lbx[j] > T(0.5))) {
+                            const Foot<T> fa = {L.pr.shape, L.pr.radius, L.pr.hx, L.pr.hy};
+                            const Foot<T> fb = {lbx[j], lr[j], lbx[64 + j], lbx[128 + j]};
+                            const T ob[6] = {lx[j], ly[j], sl[F_TH * 64 + j], lvx[j], lvy[j],
+                                             sl[F_W * 64 + j]};
+                            box_pair_adj(C, L.agent, b, fa, in, fb, ob, wx, wy, gi);
+                        } else {
+                            pair_adj_combined(C, in.px - lx[j], in.py - ly[j], in.vx - lvx[j],
+                                              in.vy - lvy[j], L.pr.radius + lr[j] + C.margin, wx,
+                                              wy, gi.px, gi.py, gi.vx, gi.vy);
+                        }
                     }
                 }
-                if (C.N > 0) {
-                    const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
-                    for (int o = 0; o < C.N; ++o)
-                        obstacle_force_adj(C, g.obs, eN, o, in.px, in.py, in.vx, in.vy,
-                                           L.pr.radius, L.dd, gFx, gFy, gi, ocs);
+                if (!DRONE && C.boxes && L.pr.shape > T(0.5)) {
+                    if (C.N > 0 || C.soft_walls) {
+                        const Foot<T> fa = {L.pr.shape, L.pr.radius, L.pr.hx, L.pr.hy};
+                        const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
+                        box_static_adj(C, g.obs, eN, ocs, fa, in, L.dd, gFx, gFy, gi);
+                    }
+                } else {
+                    if (C.N > 0) {
+                        const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
+                        for (int o = 0; o < C.N; ++o)
+                            obstacle_force_adj(C, g.obs, eN, o, in.px, in.py, in.vx, in.vy,
+                                               L.pr.radius, L.dd, gFx, gFy, gi, ocs);
+                    }
+                    if (C.soft_walls)
+                        wall_force_adj(C, in.px, in.py, in.vx, in.vy, L.pr.radius, L.dd, gFx,
+                                       gFy, gi);
                 }
-                if (C.soft_walls)
-                    wall_force_adj(C, in.px, in.py, in.vx, in.vy, L.pr.radius, L.dd, gFx, gFy, gi);
             }
             gs = gi;
         }
@@ -656,6 +713,7 @@ template <typename T> static int fill_cst(const swarp_desc_t *d, double skin, Cs
     C.collisions = d->collisions;
     C.soft_walls = d->soft_walls;
     C.clamp = d->clamp_bounds;
+    C.boxes = d->has_boxes ? 1 : 0;
     C.needs_forces = (d->collisions || d->soft_walls || d->n_obstacles > 0) ? 1 : 0;
     C.use_skin = (d->collisions && d->substeps > 1 && skin > 0.0) ? 1 : 0;
     // contact distances lie in [sqrt(eps2), neighbour radius]: within the range of the
@@ -678,6 +736,10 @@ static int check_desc(const swarp_desc_t *d, bool need_params = true)
     if (d->n_obstacles < 0) return fail("n_obstacles must be >= 0");
     if (d->integrator != SWARP_EULER && d->integrator != SWARP_RK4)
         return fail("desc->integrator must be SWARP_EULER or SWARP_RK4");
+    if (d->clamp_bounds < 0 || d->clamp_bounds > 2) return fail("desc->clamp_bounds must be 0, 1 or 2");
+    if (d->clamp_bounds == 2 && !d->has_boxes)
+        return fail("the footprint clamp (clamp_bounds 2) is for worlds holding box agents");
+    if (d->has_boxes && d->has_drone) return fail("a drone cannot be a box agent");
     if (need_params && (!d->params || !d->model_tag || !d->ctrl_mode))
         return fail("params/model_tag/ctrl_mode must be set");
     if (d->n_obstacles > 0 && (!d->obs_pos || !d->obs_radius || !d->obs_angle || !d->obs_half ||
@@ -764,7 +826,7 @@ static void launch_bwd(int PA, const Cst<T> &C, const Args<T> &a, size_t shm, hi
 static bool lean_ok(const swarp_desc_t *d)
 {
     return d->holo_velocity_only && !d->has_drone && d->n_obstacles == 0 && !d->clamp_bounds &&
-           d->integrator == SWARP_EULER;
+           d->integrator == SWARP_EULER && !d->has_boxes;
 }
 
 // Byte offsets of the tape regions (see lean.hpp); total == 0: no tape.
@@ -1104,6 +1166,7 @@ int swarp_rollout_fwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
     g_err[0] = 0;
     if (check_desc(desc)) return -1;
     if (T < 1) return fail("T must be >= 1");
+    if (desc->has_boxes) return fail("box agents with movable bodies are not supported in this build");
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
         return rollout_fwd_ob<float>(desc, T, state0, ob0, actions, traj, final_state, ob_traj, st);
@@ -1120,6 +1183,7 @@ int swarp_rollout_bwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
     g_err[0] = 0;
     if (check_desc(desc)) return -1;
     if (T < 1) return fail("T must be >= 1");
+    if (desc->has_boxes) return fail("box agents with movable bodies are not supported in this build");
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
         return rollout_bwd_ob<float>(desc, T, state0, ob0, actions, traj, ob_traj, adj_traj,

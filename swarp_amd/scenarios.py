@@ -156,10 +156,17 @@ class NavigationScenario(Scenario):
         agent_shape: AgentShape | str = AgentShape.DISC,
         agent_half_extents: tuple[float, float] | None = None,
     ) -> None:
+        # agent_shape="box": every agent a box of agent_half_extents (default
+        # (agent_radius, agent_radius / 2)); its circumscribed radius then replaces
+        # agent_radius everywhere the scenario reads it (navigation.py:61-79)
         shape = _coerce(AgentShape, agent_shape, "agent_shape")
         if shape == AgentShape.BOX:
-            raise NotImplementedError("box agents are not part of this build's step")
-        footprint = AgentConfig(radius=agent_radius, half_extents=agent_half_extents or (0.0, 0.0))
+            if agent_half_extents is None:
+                agent_half_extents = (agent_radius, 0.5 * agent_radius)
+            footprint = AgentConfig(shape=shape, half_extents=agent_half_extents)
+        else:
+            footprint = AgentConfig(radius=agent_radius,
+                                    half_extents=agent_half_extents or (0.0, 0.0))
         self.agent_shape = footprint.shape
         self.agent_half_extents = footprint.half_extents
         self.n_agents = n_agents
@@ -195,7 +202,8 @@ class NavigationScenario(Scenario):
 
     def _agent_configs(self) -> list[AgentConfig]:
         return [
-            AgentConfig(model=self.model, ctrl_mode=self.ctrl_mode, radius=self.agent_radius,
+            AgentConfig(model=self.model, ctrl_mode=self.ctrl_mode,
+                        radius=None if self.agent_shape == AgentShape.BOX else self.agent_radius,
                         max_speed=self.max_speed, max_accel=2.0 * self.max_speed,
                         shape=self.agent_shape, half_extents=self.agent_half_extents)
             for _ in range(self.n_agents)

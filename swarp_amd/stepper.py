@@ -106,6 +106,9 @@ class Stepper:
         self.params = build_agent_params(configs, self.device, self.dtype)
         self.act_dim = max(action_dim(c.model) for c in configs)
         self.has_drone = any(c.model == DynamicsModel.DRONE for c in configs)
+        #: a box agent selects the box-aware contact pass and the footprint clamp
+        #: (swarp/core/stepper.py:211-215)
+        self.has_boxes = any(c.shape == AgentShape.BOX for c in configs)
         self.holo_velocity_only = all(
             c.model == DynamicsModel.HOLONOMIC and c.ctrl_mode == ControlMode.VELOCITY
             for c in configs
@@ -165,8 +168,6 @@ class Stepper:
                 "lists only (the reference's own choice at <= 512 agents)"
             )
         for c in self.configs:
-            if c.shape == AgentShape.BOX:
-                raise NotImplementedError("box agents are not implemented")
             if c.ctrl_mode == ControlMode.SERVO:
                 raise NotImplementedError("ControlMode.SERVO is not implemented")
 
@@ -204,6 +205,8 @@ class Stepper:
                 raise NotImplementedError("movable bodies: this build steps at most 16 obstacles per env")
             if self.has_drone:
                 raise NotImplementedError("movable bodies with DRONE agents are not implemented")
+            if self.has_boxes:
+                raise NotImplementedError("movable bodies with box agents are not implemented")
             moving = self._moving_shapes(self._obs["kind"], self._obs["body"])
             if bool(((self._obs["type"] != 0) & moving).any()):
                 raise NotImplementedError(
@@ -270,10 +273,13 @@ class Stepper:
         d.n_obstacles = self.n_obstacles
         d.collisions = int(self.collisions)
         d.soft_walls = int(self._soft_walls)
-        d.clamp_bounds = int(self._clamp)
+        # a world holding box agents clamps every agent's footprint (kernels.py:74-99)
+        d.clamp_bounds = (2 if self.has_boxes else 1) if self._clamp else 0
         d.has_drone = int(self.has_drone)
+        d.has_boxes = int(self.has_boxes)
         d.holo_velocity_only = int(self.use_specialised and self.holo_velocity_only
-                                   and self.n_obstacles == 0 and not self._clamp)
+                                   and self.n_obstacles == 0 and not self._clamp
+                                   and not self.has_boxes)
         d.dt = float(self.dt)
         d.k = float(self.world.collision_k)
         d.c = float(self.world.collision_c)

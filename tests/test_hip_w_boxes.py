@@ -1,0 +1,139 @@
+"""Box agents on the HIP path vs the CPU oracle (collision_forces_box_kernel and the
+footprint clamp, swarp/core/collisions.py:999-1059, swarp/dynamics/kernels.py:79-99).
+
+Bars:
+* float64, every case at full length: states at 1e-10 and gradients at 1e-8 relative
+  (max-norm) -- the pin of the box adjoint;
+* float32 states at 1e-5 relative over the full rollout (box geometry runs through
+  cos / sin, whose device and host results differ by an ulp);
+* float32 gradients: at least as accurate as the float32 oracle's.  Both are measured
+  against the float64 oracle run on the same (float32-rounded) inputs, and the HIP
+  error may be at most twice the oracle's (floor 1e-5).  A fixed float32-vs-float32
+  tolerance does not fit box contacts: a point sunk just inside a box's surface (the
+  exterior distance |o| barely above its floor, o the short difference of two nearly
+  equal coordinates) has a normal o / |o| whose derivative scales with 1 / |o|, so
+  one-ulp differences of cos / sin become relative gradient differences of 1e-4 to a
+  few 1e-3 between any two float32 evaluations of the same formula (both sit equally
+  far from the float64 result).
+The HIP reverse pass differentiates the box contacts with forward-mode tangents per lane
+(gathering each pair's cotangents), the oracle with seeded one-tangent duals per pair
+(scattering to both agents): the comparison checks two assemblies of the same
+Jacobians.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from hip_helpers import hip_run, make_stepper, oracle_run, rel
+from oracle.oracle import pack_state
+from swarp_amd.config import AgentConfig, AgentShape, ControlMode, DynamicsModel, Integrator, WorldConfig
+from test_hip_parity import _cotangent
+
+pytestmark = pytest.mark.gpu
+
+
+def _box(hx, hy, model, **kw):
+    return AgentConfig(model=model, shape=AgentShape.BOX, half_extents=(hx, hy), radius=None,
+                       max_speed=2.0, max_accel=4.0, **kw)
+
+
+def _fleet(A):
+    q = A // 3
+    cfgs = [AgentConfig(radius=0.05, max_speed=2.0, max_accel=4.0,
+                        ctrl_mode=ControlMode.ACCELERATION) for _ in range(q)]
+    cfgs += [_box(0.07, 0.04, DynamicsModel.DIFF_DRIVE, ctrl_mode=ControlMode.ACCELERATION)
+             for _ in range(q)]
+    cfgs += [_box(0.06, 0.035, DynamicsModel.KINEMATIC_BICYCLE, l_f=0.05, l_r=0.05,
+                  max_steer=0.6) for _ in range(A - 2 * q)]
+    return cfgs
+
+
+def _state(E, A, rng, extent, dtype):
+    return pack_state({
+        "pos": rng.uniform(-extent, extent, size=(E, A, 2)),
+        "theta": rng.uniform(-np.pi, np.pi, size=(E, A)),
+        "vel": rng.normal(size=(E, A, 2)) * 0.2,
+        "speed": rng.normal(size=(E, A)) * 0.2,
+        "ang_vel": rng.normal(size=(E, A)) * 0.5,
+    }).astype(dtype)
+
+
+def _obstacles(E, rng):
+    n = 6
+    return {"pos": rng.uniform(-0.5, 0.5, size=(E, n, 2)),
+            "radius": np.r_[rng.uniform(0.04, 0.1, 2), np.zeros(2), np.full(2, 0.03)],
+            "type": np.r_[np.zeros(2), np.ones(2), np.full(2, 2)].astype(np.int32),
+            "angle": rng.uniform(-np.pi, np.pi, size=(E, n)),
+            "half": np.r_[np.zeros((2, 2)), rng.uniform(0.04, 0.12, size=(2, 2)),
+                          np.c_[rng.uniform(0.05, 0.15, 2), np.zeros(2)]]}
+
+
+def _run(cfgs, world, S, s0, acts, w, dtype, obs=None, E=None):
+    td = torch.float32 if dtype == np.float32 else torch.float64
+    st = make_stepper(cfgs, world, 0.05, S, td, obs=obs, n_envs=E)
+    assert st.has_boxes
+    hip = hip_run(st, s0, acts, w, dtype)
+    orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, dtype, obs=obs)
+    return hip, orc
+
+
+def _check_box(name, cfgs, world, S, s0, acts, w, obs=None, E=None):
+    hip, orc = _run(cfgs, world, S, s0.astype(np.float64), acts.astype(np.float64), w,
+                    np.float64, obs=obs, E=E)
+    hs, hg0, hga = hip
+    os_, og0, oga = orc
+    assert rel(hs[..., :7], os_[..., :7]) <= 1e-10, f"{name} f64 states"
+    assert rel(hga, oga) <= 1e-8, f"{name} f64 d/d actions {rel(hga, oga):.3e}"
+    assert rel(hg0[..., :7], og0[..., :7]) <= 1e-8, f"{name} f64 d/d state0"
+    s32, a32 = s0.astype(np.float32), acts.astype(np.float32)
+    _, truth = _run(cfgs, world, S, s32.astype(np.float64), a32.astype(np.float64), w,
+                    np.float64, obs=obs, E=E)
+    hip, orc = _run(cfgs, world, S, s32, a32, w, np.float32, obs=obs, E=E)
+    assert rel(hip[0][..., :7], orc[0][..., :7]) <= 1e-5, f"{name} f32 states"
+    for k, what in ((2, "d/d actions"), (1, "d/d state0")):
+        h, o, t = (x[k][..., :7] if k == 1 else x[k] for x in (hip, orc, truth))
+        e_hip, e_orc = rel(h, t), rel(o, t)
+        assert e_hip <= max(2.0 * e_orc, 1e-5), (
+            f"{name} f32 {what}: error vs f64 {e_hip:.3e}, the f32 oracle's {e_orc:.3e}")
+
+
+def test_box_fleet_with_obstacles_and_walls():
+    """Discs, diff-drive boxes and bicycle boxes in crowded envs with circle, box and
+    capsule obstacles inside soft walls, four substeps (12 agents: padded lanes)."""
+    E, A, T, S = 48, 12, 8, 4
+    rng = np.random.default_rng(31)
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02,
+                        bounds=(-0.6, 0.6, -0.6, 0.6), max_neighbors=8,
+                        contact_max_overlap=0.05)
+    s0 = _state(E, A, rng, 0.45, np.float64)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2))
+    w = _cotangent(T, E, A, 3, scale=0.1)
+    _check_box("box fleet", _fleet(A), world, S, s0, acts, w, obs=_obstacles(E, rng), E=E)
+
+
+@pytest.mark.parametrize("integ", [Integrator.EULER, Integrator.RK4], ids=["euler", "rk4"])
+def test_box_footprint_clamp(integ):
+    """Box and disc agents against the footprint clamp."""
+    E, A, T, S = 40, 8, 8, 2
+    rng = np.random.default_rng(32)
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02,
+                        bounds=(-0.3, 0.3, -0.3, 0.3), bounds_mode="clamp", max_neighbors=7,
+                        integrator=integ)
+    s0 = _state(E, A, rng, 0.25, np.float64)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2))
+    w = _cotangent(T, E, A, 4, scale=0.1)
+    _check_box(f"box clamp {integ.name}", _fleet(A), world, S, s0, acts, w)
+
+
+def test_sixty_four_box_agents():
+    """A full wave per env (64 agents, 64-bit list masks), all boxes."""
+    E, A, T, S = 6, 64, 4, 2
+    rng = np.random.default_rng(34)
+    cfgs = [_box(0.05, 0.03, DynamicsModel.DIFF_DRIVE) for _ in range(A)]
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02,
+                        bounds=(-0.7, 0.7, -0.7, 0.7), max_neighbors=12)
+    s0 = _state(E, A, rng, 0.6, np.float64)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2))
+    w = _cotangent(T, E, A, 6, scale=0.1)
+    _check_box("64 boxes", cfgs, world, S, s0, acts, w)

@@ -168,8 +168,15 @@ def test_stepper_reach_check_and_unsupported_features():
         Stepper(cfgs, substeps=0, device="cpu")
     rk = Stepper(cfgs, device="cpu", world=WorldConfig(integrator=Integrator.RK4))
     assert rk.desc(2, 2).integrator == 1 and Stepper(cfgs, device="cpu").desc(2, 2).integrator == 0
-    with pytest.raises(NotImplementedError):
-        Stepper([AgentConfig(shape="box", half_extents=(0.1, 0.1))], device="cpu")
+    # box agents: the box-aware pass and, under bounds_mode="clamp", the footprint clamp
+    bx = Stepper([AgentConfig(shape="box", half_extents=(0.1, 0.1)), AgentConfig(radius=0.05)],
+                 device="cpu", world=WorldConfig(bounds=(-1, 1, -1, 1), bounds_mode="clamp"))
+    d = bx.desc(2, 2)
+    assert bx.has_boxes and d.has_boxes == 1 and d.clamp_bounds == 2 and d.holo_velocity_only == 0
+    assert Stepper(cfgs, device="cpu", world=WorldConfig(bounds=(-1, 1, -1, 1),
+                                                         bounds_mode="clamp")).desc(2, 2).clamp_bounds == 1
+    with pytest.raises(NotImplementedError, match="wheel_contacts"):
+        Stepper(cfgs, device="cpu", world=WorldConfig(wheel_contacts=True))
     st = Stepper(cfgs, dt=0.1, substeps=4, device="cpu", world=WorldConfig())
     assert math.isclose(st.sub_dt, 0.025)
     assert math.isclose(st.neighbor_radius, 2 * 0.2 + 0.02)
@@ -253,8 +260,10 @@ def test_make_routes_keywords_and_rejects_unknown_ones():
         make("navigation", 2, device="cpu", n_agent=3)
     with pytest.raises(ValueError):
         make("navigation", 0, device="cpu")
-    with pytest.raises(NotImplementedError):
-        make("navigation", 2, device="cpu", agent_shape="box")
+    # box agents: the circumscribed radius replaces agent_radius (navigation.py:61-79)
+    benv = make("navigation", 2, device="cpu", agent_shape="box", agent_radius=0.04)
+    assert benv.world.stepper.has_boxes
+    assert math.isclose(benv.scenario.agent_radius, math.hypot(0.04, 0.02))
     # a world_config override reaches the engine (WorldConfig.override_with)
     env = make("navigation", 2, device="cpu", world_config=WorldConfig(max_neighbors=2))
     assert env.world.stepper.world.max_neighbors == 2 and env.obs_dim == 9 + 5 * 2

@@ -193,6 +193,71 @@ def test_footprint_clamp():
     assert tr[0, 0, 1, 0] == 0.5 - 0.05
 
 
+def test_disc_past_a_box_corner():
+    """A disc beyond a box's corner: the normal is the corner-to-centre diagonal and the
+    depth uses the corner distance (the exterior SDF of box_force)."""
+    cfgs = [_disc(0.08), _box(0.2, 0.1)]
+    s = pack_state({"pos": [[[0.24, 0.14], [0.0, 0.0]]]})
+    F = _forces(cfgs, _world(), s)
+    d = 0.04 * math.sqrt(2.0)
+    mag = K * (0.08 + M - d)
+    assert F[0, 0] == pytest.approx([mag / math.sqrt(2.0)] * 2, rel=1e-9)
+    assert np.array_equal(F[0, 1], -F[0, 0])
+
+
+@pytest.mark.parametrize("phi", [0.3, 0.9, 1.4])
+def test_capsule_end_cap_is_round(phi):
+    """A box corner 0.04 from a capsule core's end, at angle phi: the end cap is a circle,
+    so the push is radial with the same depth at every phi (obb_contact with the
+    degenerate box (half_len, 0))."""
+    seg = {"pos": [[[0.0, 0.0]]], "radius": [0.05], "type": [2], "half": [[0.25, 0.0]]}
+    end = np.array([0.25, 0.0])
+    u = np.array([math.cos(phi), math.sin(phi)])
+    # an aligned 0.06-square whose lower-left corner sits at end + 0.04 u
+    centre = end + 0.04 * u + 0.06
+    F = _forces([_box(0.06, 0.06)], _world(collisions=False), pack_state({"pos": [[centre]]}), seg)
+    assert F[0, 0] == pytest.approx(K * (0.05 + M - 0.04) * u, rel=1e-9, abs=1e-12)
+
+
+def test_plus_crossing_is_detected():
+    """Two thin boxes crossing in a '+': no corner of either lies inside the other, so
+    only the separating-axis test sees the overlap; the push is along a face normal."""
+    cfgs = [_box(0.25, 0.015), _box(0.25, 0.015)]
+    s = pack_state({"pos": [[[0.0, 0.0], [0.02, 0.01]]], "theta": [[0.0, math.pi / 2]]})
+    F = _forces(cfgs, _world(), s)
+    assert np.linalg.norm(F[0, 0]) > 1.0
+    assert np.array_equal(F[0, 1], -F[0, 0])
+    assert min(abs(F[0, 0, 0]), abs(F[0, 0, 1])) < 1e-9
+
+
+def test_rotation_and_translation_invariance():
+    """Rotating and shifting a whole mixed scene (agents, obstacles, velocities) rotates
+    every force with it."""
+    cfgs = [_box(0.18, 0.09), _box(0.12, 0.07), _box(0.09, 0.09), _disc(0.07)]
+    pos = np.array([[0.0, 0.0], [0.24, 0.1], [0.03, 0.19], [-0.22, -0.05]])
+    th = np.array([0.25, -0.35, 1.0, 0.0])
+    vel = np.array([[0.2, -0.1], [-0.3, 0.05], [0.1, 0.2], [0.4, 0.0]])
+    om = np.array([0.6, -1.1, 1.8, 0.0])
+    obs = {"pos": np.array([[[0.18, -0.19], [-0.28, 0.18], [0.4, 0.28]]]),
+           "radius": [0.0, 0.03, 0.09], "type": [1, 2, 0],
+           "half": [[0.14, 0.05], [0.18, 0.0], [0.0, 0.0]], "angle": np.array([[0.2, -0.5, 0.0]]),
+           "vel": np.array([[[0.1, 0.0], [0.0, -0.2], [0.0, 0.1]]]),
+           "ang_vel": np.array([[0.3, -0.4, 1.0]])}
+    w = _world(collision_c=1.0, bounds=(-0.6, 0.6, -0.6, 0.6), collision_margin=0.02)
+    w_free = _world(collision_c=1.0, collision_margin=0.02)
+    s = pack_state({"pos": pos[None], "theta": th[None], "vel": vel[None], "ang_vel": om[None]})
+    f0 = _forces(cfgs, w_free, s, obs)[0]
+    assert (np.linalg.norm(f0, axis=-1) > 1e-3).sum() >= 3
+    a, shift = 0.8, np.array([0.25, -0.4])
+    r = np.array([[math.cos(a), -math.sin(a)], [math.sin(a), math.cos(a)]])
+    obs1 = dict(obs, pos=obs["pos"] @ r.T + shift, angle=obs["angle"] + a, vel=obs["vel"] @ r.T)
+    s1 = pack_state({"pos": (pos @ r.T + shift)[None], "theta": (th + a)[None],
+                     "vel": (vel @ r.T)[None], "ang_vel": om[None]})
+    f1 = _forces(cfgs, w_free, s1, obs1)[0]
+    np.testing.assert_allclose(f1, f0 @ r.T, atol=1e-9, rtol=0)
+    assert np.count_nonzero(_forces(cfgs, w, s, obs)) > 0
+
+
 # ------------------------------------------------------------------ finite differences
 
 def _rs(E, A, seed, spread, ang=True):
