@@ -58,7 +58,7 @@ def parse():
     ap.add_argument("--env-steps", type=int, default=100,
                     help="timed Environment.step calls of the no-grad navigation leg "
                          "(16000 x 16, graph on and off); 0 skips it")
-    ap.add_argument("--workload", default="c2", choices=("c2", "c3", "c4", "c5"),
+    ap.add_argument("--workload", default="c2", choices=("c2", "c3", "c3box", "c4", "c5"),
                     help="BASELINE.json config to time: c2 (the headline, default), c3 mixed "
                          "fleet + obstacles, c4 drones, c5 movable body + per-step lists/COO")
     ap.add_argument("--copy-mb", type=int, default=0,
@@ -136,21 +136,25 @@ def cpu_baseline(E_full, A, T, S, seconds, cfgs, world):
     }
 
 
-def _c3(seed=0):
+def _c3(seed=0, boxes=False):
     """4096 x 32 mixed fleet (16 diff-drive velocity control, 16
     kinematic bicycles), headings U[-pi, pi], per-env static obstacles (4 circles r
     U[0.05, 0.2], 2 axis-aligned boxes half-extent U[0.05, 0.3], 2 segments length
-    U[0.2, 0.8]) uniform in [-2, 2]^2, 4 substeps, 20-step BPTT."""
+    U[0.2, 0.8]) uniform in [-2, 2]^2, 4 substeps, 20-step BPTT.  ``boxes``: the same
+    fleet with box footprints of half-extents (r, r / 2) (the navigation scenario's
+    default box, swarp/scenarios/navigation.py:70-73) -- the box-agent contact pass."""
     import torch
 
-    from swarp_amd import (AgentConfig, DynamicsModel, Obstacles, ObstacleShape, Stepper,
-                           TorchState, WorldConfig)
+    from swarp_amd import (AgentConfig, AgentShape, DynamicsModel, Obstacles, ObstacleShape,
+                           Stepper, TorchState, WorldConfig)
 
     E, A, T, S, r = 4096, 32, 20, 4, 0.05
     g = torch.Generator(device="cpu").manual_seed(seed)
     u = lambda *sh, lo=0.0, hi=1.0: torch.rand(*sh, generator=g) * (hi - lo) + lo  # noqa: E731
-    cfgs = ([AgentConfig(model=DynamicsModel.DIFF_DRIVE, radius=r) for _ in range(16)]
-            + [AgentConfig(model=DynamicsModel.KINEMATIC_BICYCLE, radius=r) for _ in range(16)])
+    foot = (dict(shape=AgentShape.BOX, half_extents=(r, 0.5 * r), radius=None) if boxes
+            else dict(radius=r))
+    cfgs = ([AgentConfig(model=DynamicsModel.DIFF_DRIVE, **foot) for _ in range(16)]
+            + [AgentConfig(model=DynamicsModel.KINEMATIC_BICYCLE, **foot) for _ in range(16)])
     world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.5 * r,
                         bounds=(-2.0, 2.0, -2.0, 2.0), bounds_mode="soft", max_neighbors=32)
     st = Stepper(cfgs, dt=0.05, substeps=S, device="cuda:0", dtype=torch.float32, world=world)
@@ -173,6 +177,8 @@ def _c3(seed=0):
     fwd = 4 * A * (2 * 7 + 2) + 8 * 6 * 4
     bwd = 4 * A * (3 * 7 + 2 * 2) + 8 * 6 * 4
     desc = "mixed fleet 4096 envs x 32 agents (diff-drive + bicycle), 8 obstacles, 4 substeps, 20-step BPTT (BASELINE configs[2])"
+    if boxes:
+        desc = desc.replace("agents (", "box agents (half-extents 0.05 x 0.025, ")
     return st, state, acts, goals, fwd, bwd, desc, None
 
 
@@ -251,7 +257,8 @@ def run_other(args):
     import swarp_amd.autograd as ag
     from swarp_amd import TorchState, rollout
 
-    st, state, acts, goals, fwd_b, bwd_b, desc, kind = {"c3": _c3, "c4": _c4, "c5": _c5}[args.workload]()
+    st, state, acts, goals, fwd_b, bwd_b, desc, kind = {
+        "c3": _c3, "c3box": lambda: _c3(boxes=True), "c4": _c4, "c5": _c5}[args.workload]()
     T, E, A = acts.shape[:3]
     a = acts.clone().requires_grad_(True)
     s0 = TorchState(state.pos.clone().requires_grad_(True), *state[1:])

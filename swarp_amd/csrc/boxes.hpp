@@ -6,9 +6,9 @@
 // (:543-626), _wall_forces_box (:641-688), _static_forces_shaped (:950-996).
 //
 // Every function here is written once over a value type V: V = T in the forward pass,
-// V = Dual<T, 3> in the reverse pass, where three forward-mode tangents seeded on three
-// fields of the lane's own state (position and heading, then velocity and spin) give
-// the force's Jacobian columns for those fields.  Dual comparisons read the value part,
+// V = Dual<T, N> in the reverse pass, where N forward-mode tangents seeded on N of the
+// six fields of the lane's own state the contact reads give the force's Jacobian
+// columns for those fields (6 / N evaluations per contact).  Dual comparisons read the value part,
 // so the reverse pass takes the branches the forward pass took, and the value part is
 // the forward arithmetic itself (same operations, same order).  The derivative rules
 // are those of the generated adjoint the reference differentiates with: max/min/clamp
@@ -386,11 +386,15 @@ __device__ __forceinline__ void agent_pair_force_box(const Cst<T> &C, int a, int
 // (_obstacle_forces_box + _box_obstacle_force, :543-626), then the soft walls
 // (_wall_forces_box, :641-688).  `ocs`: this env's obstacle angles as (cos, sin) pairs,
 // or NULL.
+// `active` (nullable): set when some obstacle or wall exerts a nonzero force -- with none,
+// every derivative of the static force is zero too.
 template <typename T, typename V>
 __device__ __forceinline__ void box_static_forces(const Cst<T> &C, const Obs<T> &O, size_t eN,
                                                   const T *ocs, T hx, T hy, const V (&s)[6], V ca,
-                                                  V sa, T dd, V &fx_o, V &fy_o)
+                                                  V sa, T dd, V &fx_o, V &fy_o,
+                                                  bool *active = nullptr)
 {
+    bool act = false;
     V fx = V(T(0)), fy = V(T(0));
     const T ra = m_sqrt(hx * hx + hy * hy);
     for (int o = 0; o < C.N; ++o) {
@@ -421,6 +425,7 @@ __device__ __forceinline__ void box_static_forces(const Cst<T> &C, const Obs<T> 
             gx = -hxv;
             gy = -hyv;
         }
+        act |= val(gx) != T(0) || val(gy) != T(0);
         fx = fx + gx;
         fy = fy + gy;
     }
@@ -436,95 +441,128 @@ __device__ __forceinline__ void box_static_forces(const Cst<T> &C, const Obs<T> 
         const V em = ex + V(C.margin), eym = ey + V(C.margin);
         V wx = V(T(0)), wy = V(T(0));
         V pen = em - (s[BX_PX] - V(C.bmin_x));
-        if (val(pen) > T(0)) wx = wx + normal_coeff_v(C, pen, s[BX_VX] - s[BX_W] * rl_y, dd);
+        if (val(pen) > T(0)) {
+            const V q = normal_coeff_v(C, pen, s[BX_VX] - s[BX_W] * rl_y, dd);
+            act |= val(q) != T(0);
+            wx = wx + q;
+        }
         pen = em - (V(C.bmax_x) - s[BX_PX]);
-        if (val(pen) > T(0))
-            wx = wx + (-normal_coeff_v(C, pen, -(s[BX_VX] + s[BX_W] * rl_y), dd));
+        if (val(pen) > T(0)) {
+            const V q = normal_coeff_v(C, pen, -(s[BX_VX] + s[BX_W] * rl_y), dd);
+            act |= val(q) != T(0);
+            wx = wx + (-q);
+        }
         pen = eym - (s[BX_PY] - V(C.bmin_y));
-        if (val(pen) > T(0)) wy = wy + normal_coeff_v(C, pen, s[BX_VY] + s[BX_W] * rb_x, dd);
+        if (val(pen) > T(0)) {
+            const V q = normal_coeff_v(C, pen, s[BX_VY] + s[BX_W] * rb_x, dd);
+            act |= val(q) != T(0);
+            wy = wy + q;
+        }
         pen = eym - (V(C.bmax_y) - s[BX_PY]);
-        if (val(pen) > T(0))
-            wy = wy + (-normal_coeff_v(C, pen, -(s[BX_VY] - s[BX_W] * rb_x), dd));
+        if (val(pen) > T(0)) {
+            const V q = normal_coeff_v(C, pen, -(s[BX_VY] - s[BX_W] * rb_x), dd);
+            act |= val(q) != T(0);
+            wy = wy + (-q);
+        }
         fx = fx + wx;
         fy = fy + wy;
     }
     fx_o = fx;
     fy_o = fy;
+    if (active) *active = act;
 }
 
 // ------------------------------------------------------------------ reverse helpers
 
+// Tangents carried per reverse evaluation: the six state fields a contact reads (px py th
+// vx vy w) are seeded SWARP_BOX_TANGENTS at a time, 6 / SWARP_BOX_TANGENTS evaluations.
+// All six in one evaluation measured fastest (the value arithmetic is shared; config-3
+// box fleet backward 6.7 ms against 11.1 ms with two and 16.6 ms with one).
+#ifndef SWARP_BOX_TANGENTS
+#define SWARP_BOX_TANGENTS 6
+#endif
+constexpr int BOX_NT = SWARP_BOX_TANGENTS;
+static_assert(6 % BOX_NT == 0, "the box tangent count must divide 6");
+
 // Adds J^T w to the lane's adjoint, where J holds the Jacobian columns of (fx, fy) with
-// respect to the seeded fields k0, k0+1, k0+2 of the lane's state.
-template <typename T>
-__device__ __forceinline__ void add_cols(const Dual<T, 3> &fx, const Dual<T, 3> &fy, T wx, T wy,
+// respect to the seeded fields k0 .. k0 + N - 1 of the lane's state.
+template <typename T, int N>
+__device__ __forceinline__ void add_cols(const Dual<T, N> &fx, const Dual<T, N> &fy, T wx, T wy,
                                          int k0, St<T> &g)
 {
-    const T c0 = wx * fx.d[0] + wy * fy.d[0];
-    const T c1 = wx * fx.d[1] + wy * fy.d[1];
-    const T c2 = wx * fx.d[2] + wy * fy.d[2];
-    if (k0 == BX_PX) {
-        g.px += c0;
-        g.py += c1;
-        g.th += c2;
-    } else {
-        g.vx += c0;
-        g.vy += c1;
-        g.w += c2;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const T c = wx * fx.d[i] + wy * fy.d[i];
+        switch (k0 + i) {
+        case BX_PX: g.px += c; break;
+        case BX_PY: g.py += c; break;
+        case BX_TH: g.th += c; break;
+        case BX_VX: g.vx += c; break;
+        case BX_VY: g.vy += c; break;
+        default: g.w += c; break;
+        }
     }
 }
 
-// The lane's state as duals with fields k0..k0+2 seeded (one tangent each).
-template <typename T>
-__device__ __forceinline__ void seed_state(const St<T> &s, int k0, Dual<T, 3> (&o)[6])
+// The lane's state as duals with fields k0 .. k0 + N - 1 seeded (one tangent each).
+template <typename T, int N>
+__device__ __forceinline__ void seed_state(const St<T> &s, int k0, Dual<T, N> (&o)[6])
 {
     const T f[6] = {s.px, s.py, s.th, s.vx, s.vy, s.w};
 #pragma unroll
     for (int k = 0; k < 6; ++k) {
-        o[k] = Dual<T, 3>(f[k]);
-        if (k >= k0 && k < k0 + 3) o[k].d[k - k0] = T(1);
+        o[k] = Dual<T, N>(f[k]);
+#pragma unroll
+        for (int i = 0; i < N; ++i)
+            if (k == k0 + i) o[k].d[i] = T(1);
     }
 }
 
+// The reverse evaluations are out-of-line calls when SWARP_BOX_NOINLINE is defined.
+#ifdef SWARP_BOX_NOINLINE
+#define SWARP_BOX_ADJ __device__ __noinline__
+#else
+#define SWARP_BOX_ADJ __device__ __forceinline__
+#endif
+
 // Reverse of a pair with a box, seen from agent a (state `in`) against agent b (`sb`,
-// cos/sin of its heading cb/sb_): adds J_a(f)^T w, with f the pair function evaluated
+// cos / sin of its heading cb, snb): adds J_a(f)^T w, with f the pair function evaluated
 // with a unit damping denominator and w the caller's combined cotangent (own force
 // adjoint / dd_a minus, where a is in b's list, b's / dd_b).
 template <typename T>
-__device__ __forceinline__ void box_pair_adj(const Cst<T> &C, int a, int b, const Foot<T> &Fa,
+SWARP_BOX_ADJ void box_pair_adj(const Cst<T> &C, int a, int b, const Foot<T> &Fa,
                                              const St<T> &in, const Foot<T> &Fb, const T (&sb)[6],
-                                             T wx, T wy, St<T> &g)
+                                             T cb, T snb, T wx, T wy, St<T> &g)
 {
-    typedef Dual<T, 3> D3;
-    D3 ob[6];
-#pragma unroll
-    for (int k = 0; k < 6; ++k) ob[k] = D3(sb[k]);
-    const D3 cbv = m_cos(D3(sb[BX_TH])), sbv = m_sin(D3(sb[BX_TH]));
+    typedef Dual<T, BOX_NT> DN;
 #pragma unroll 1
-    for (int k0 = 0; k0 < 6; k0 += 3) {
-        D3 me[6];
+    for (int k0 = 0; k0 < 6; k0 += BOX_NT) {
+        DN ob[6];
+#pragma unroll
+        for (int k = 0; k < 6; ++k) ob[k] = DN(sb[k]);
+        DN me[6];
         seed_state(in, k0, me);
-        const D3 ca = m_cos(me[BX_TH]), sa = m_sin(me[BX_TH]);
-        D3 fx, fy;
-        agent_pair_force_box<T, D3>(C, a, b, Fa, me, ca, sa, Fb, ob, cbv, sbv, T(1), fx, fy);
+        const DN ca = m_cos(me[BX_TH]), sa = m_sin(me[BX_TH]);
+        DN fx, fy;
+        agent_pair_force_box<T, DN>(C, a, b, Fa, me, ca, sa, Fb, ob, DN(cb), DN(snb), T(1), fx, fy);
         add_cols(fx, fy, wx, wy, k0, g);
     }
 }
 
 // Reverse of a box agent's static forces: adds J(f)^T g_F.
 template <typename T>
-__device__ __forceinline__ void box_static_adj(const Cst<T> &C, const Obs<T> &O, size_t eN,
+SWARP_BOX_ADJ void box_static_adj(const Cst<T> &C, const Obs<T> &O, size_t eN,
                                                const T *ocs, const Foot<T> &Fa, const St<T> &in,
                                                T dd, T gx, T gy, St<T> &g)
 {
-    typedef Dual<T, 3> D3;
+    typedef Dual<T, BOX_NT> DN;
 #pragma unroll 1
-    for (int k0 = 0; k0 < 6; k0 += 3) {
-        D3 me[6];
+    for (int k0 = 0; k0 < 6; k0 += BOX_NT) {
+        DN me[6];
         seed_state(in, k0, me);
-        const D3 ca = m_cos(me[BX_TH]), sa = m_sin(me[BX_TH]);
-        D3 fx, fy;
-        box_static_forces<T, D3>(C, O, eN, ocs, Fa.hx, Fa.hy, me, ca, sa, dd, fx, fy);
+        const DN ca = m_cos(me[BX_TH]), sa = m_sin(me[BX_TH]);
+        DN fx, fy;
+        box_static_forces<T, DN>(C, O, eN, ocs, Fa.hx, Fa.hy, me, ca, sa, dd, fx, fy);
         add_cols(fx, fy, gx, gy, k0, g);
     }
 }

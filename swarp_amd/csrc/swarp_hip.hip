@@ -275,23 +275,27 @@ __device__ __forceinline__ const T *ob_trig_table(const Cst<T> &C, const Args<T>
     return ocs + 2 * ew * C.N;
 }
 
-// Box worlds: `lbx` holds per lane the footprint (shape, hx, hy rows of 64) and the slot
-// `sl` also carries the headings and spins (F_TH, F_W rows).  BOXES = false compiles the
-// box paths out (fleets with drones, which are never boxes).
+// Box worlds (BOXES; false compiles the box paths out): `lbx` holds per lane the
+// footprint (shape, hx, hy rows of 64), `lcs` the cos and sin of every lane's heading
+// (rows of 64), and the slot `sl` also carries the headings and spins (F_TH, F_W rows).
+// `act` (nullable) receives the mask of listed neighbours whose box contact exerts a
+// force and `stat` whether any static contact of a box agent does: without them every
+// derivative of those forces is zero.
 template <typename T, int PA, bool BOXES>
 __device__ __forceinline__ typename MaskT<PA>::type forces(
     const Cst<T> &C, const Args<T> &g, const Lane<T, PA> &L, const T *sl, const T *lr,
     const St<T> &st, int s, bool full, typename MaskT<PA>::type &cand, T &Fx, T &Fy,
-    const T *ocs = nullptr, const T *lbx = nullptr)
+    const T *ocs = nullptr, const T *lbx = nullptr, const T *lcs = nullptr,
+    typename MaskT<PA>::type *act = nullptr, bool *stat = nullptr)
 {
-    const bool boxes = BOXES && C.boxes;
-    const bool box_me = boxes && L.pr.shape > T(0.5);
+    const bool box_me = BOXES && L.pr.shape > T(0.5);
     T me[6] = {st.px, st.py, st.th, st.vx, st.vy, st.w};
     T cme = T(1), sme = T(0);
-    if (boxes) {
-        cme = m_cos(st.th);
-        sme = m_sin(st.th);
+    if (BOXES) {
+        cme = lcs[L.lane];
+        sme = lcs[64 + L.lane];
     }
+    typename MaskT<PA>::type am = 0;
     typedef typename MaskT<PA>::type M;
     const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64, *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
     M incl = 0;
@@ -313,12 +317,13 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
             m &= m - 1;
             const int j = L.base + b;
             T gx, gy;
-            if (boxes && (box_me || lbx[j] > T(0.5))) {
+            if (BOXES && (box_me || lbx[j] > T(0.5))) {
                 // a pair with a box (collision_forces_box_kernel, collisions.py:1044-1052)
                 const Foot<T> fb = {lbx[j], lr[j], lbx[64 + j], lbx[128 + j]};
                 const T ob[6] = {lx[j], ly[j], lth[j], lvx[j], lvy[j], lw[j]};
-                agent_pair_force_box<T, T>(C, L.agent, b, fa, me, cme, sme, fb, ob,
-                                           m_cos(lth[j]), m_sin(lth[j]), L.dd, gx, gy);
+                agent_pair_force_box<T, T>(C, L.agent, b, fa, me, cme, sme, fb, ob, lcs[j],
+                                           lcs[64 + j], L.dd, gx, gy);
+                if (gx != T(0) || gy != T(0)) am |= typename MaskT<PA>::type(1) << b;
             } else {
                 pair_force(C, st.px - lx[j], st.py - ly[j], st.vx - lvx[j], st.vy - lvy[j],
                            ra + lr[j] + C.margin, L.dd, gx, gy);
@@ -331,7 +336,8 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
     if (box_me) {
         // a box agent's obstacles and walls (_static_forces_shaped, collisions.py:950-996)
         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
-        box_static_forces<T, T>(C, g.obs, eN, ocs, L.pr.hx, L.pr.hy, me, cme, sme, L.dd, sx, sy);
+        box_static_forces<T, T>(C, g.obs, eN, ocs, L.pr.hx, L.pr.hy, me, cme, sme, L.dd, sx, sy,
+                                stat);
     } else if (C.N > 0) {
         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
         for (int o = 0; o < C.N; ++o) {
@@ -351,18 +357,22 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
     }
     Fx = fx + sx;
     Fy = fy + sy;
+    if (act) *act = am;
     return incl;
 }
 
 // ------------------------------------------------------------------ forward rollout
 
-template <typename T, int PA, bool DRONE>
+// BOXES: the box-aware contact pass is compiled in (a world holding box agents); the
+// disc-only instances keep the register budget of the disc contact law.
+template <typename T, int PA, bool DRONE, bool BOXES>
 __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> C, const Args<T> g)
 {
     typedef typename MaskT<PA>::type M;
     __shared__ T sl[7 * 64];  // px py vx vy th (s) w of the current substep
     __shared__ T lr[64];      // agent radius per lane
     __shared__ T lbx[3 * 64]; // footprint per lane: shape, hx, hy (box worlds)
+    __shared__ T lcs[2 * 64]; // cos, sin of each lane's heading this substep (box worlds)
     __shared__ T ocs_lds[2 * OCS_MAX];
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
@@ -390,13 +400,19 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> C, const Args<T
                     sl[F_PY * 64 + L.lane] = st.py;
                     sl[F_VX * 64 + L.lane] = st.vx;
                     sl[F_VY * 64 + L.lane] = st.vy;
-                    if (C.boxes) {
+                    if (BOXES) {
                         sl[F_TH * 64 + L.lane] = st.th;
                         sl[F_W * 64 + L.lane] = st.w;
                     }
-                    __syncthreads();
                 }
-                forces<T, PA, !DRONE>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy, ocs, lbx);
+                if (BOXES) {
+                    if (!C.collisions) __syncthreads();
+                    lcs[L.lane] = m_cos(st.th);
+                    lcs[64 + L.lane] = m_sin(st.th);
+                }
+                if (C.collisions || BOXES) __syncthreads();
+                forces<T, PA, BOXES>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy, ocs, lbx,
+                                     lcs);
             }
             St<T> nx;
             integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
@@ -454,7 +470,7 @@ template <typename M> __device__ __forceinline__ bool in_list(M incl, int me, in
     return ((incl >> me) & M(1)) && m_popc(incl & ((M(1) << me) - M(1))) < K;
 }
 
-template <typename T, int PA, bool DRONE>
+template <typename T, int PA, bool DRONE, bool BOXES>
 __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T> g)
 {
     typedef typename MaskT<PA>::type M;
@@ -464,6 +480,11 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
     T *ldd = lr + 64;           // damping denominator per lane
     T *slots = ldd + 64;        // S slots of NF fields
     M *lmask = (M *)(slots + (size_t)C.S * NF * 64);  // S inclusion masks per lane
+    // box worlds: per substep the masks of force-exerting box contacts, the cos / sin of
+    // every lane's heading, and whether a box agent's static contacts exert a force
+    M *lact = lmask + (size_t)C.S * 64;
+    T *lcsb = (T *)(lact + (size_t)C.S * 64);
+    unsigned char *lst = (unsigned char *)(lcsb + (size_t)C.S * 128);
     __shared__ T ocs_lds[2 * OCS_MAX];
     __shared__ T lbx[3 * 64];  // footprint per lane: shape, hx, hy (box worlds)
     Lane<T, PA> L;
@@ -499,12 +520,23 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
             T *sl = slots + (size_t)s * NF * 64;
             __syncthreads();
             slot_put<T, DRONE>(sl, L.lane, st);
+            if (BOXES) {
+                lcsb[s * 128 + L.lane] = m_cos(st.th);
+                lcsb[s * 128 + 64 + L.lane] = m_sin(st.th);
+            }
             __syncthreads();
             T Fx = T(0), Fy = T(0);
             M incl = 0;
-            if (C.needs_forces)
-                incl = forces<T, PA, !DRONE>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy,
-                                             ocs, lbx);
+            if (C.needs_forces) {
+                M am = 0;
+                bool stf = false;
+                incl = forces<T, PA, BOXES>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy,
+                                            ocs, lbx, lcsb + s * 128, &am, &stf);
+                if (BOXES) {
+                    lact[s * 64 + L.lane] = am;
+                    lst[s * 64 + L.lane] = stf ? 1 : 0;
+                }
+            }
             sl[F_FX * 64 + L.lane] = Fx;
             sl[F_FY * 64 + L.lane] = Fy;
             lmask[s * 64 + L.lane] = incl;
@@ -550,12 +582,18 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
                         if (!own && !rev) continue;
                         const T wx = (own ? wFx : T(0)) - (rev ? lgx[j] : T(0));
                         const T wy = (own ? wFy : T(0)) - (rev ? lgy[j] : T(0));
-                        if (!DRONE && C.boxes && (L.pr.shape > T(0.5) || lbx[j] > T(0.5))) {
+                        if (BOXES && (L.pr.shape > T(0.5) || lbx[j] > T(0.5))) {
+                            // one contact seen from both sides: it exerts a force, or
+                            // every derivative of it is zero
+                            const bool on = own ? ((lact[s * 64 + L.lane] >> b) & M(1)) != 0
+                                                : ((lact[s * 64 + j] >> L.agent) & M(1)) != 0;
+                            if (!on) continue;
                             const Foot<T> fa = {L.pr.shape, L.pr.radius, L.pr.hx, L.pr.hy};
                             const Foot<T> fb = {lbx[j], lr[j], lbx[64 + j], lbx[128 + j]};
                             const T ob[6] = {lx[j], ly[j], sl[F_TH * 64 + j], lvx[j], lvy[j],
                                              sl[F_W * 64 + j]};
-                            box_pair_adj(C, L.agent, b, fa, in, fb, ob, wx, wy, gi);
+                            box_pair_adj(C, L.agent, b, fa, in, fb, ob, lcsb[s * 128 + j],
+                                         lcsb[s * 128 + 64 + j], wx, wy, gi);
                         } else {
                             pair_adj_combined(C, in.px - lx[j], in.py - ly[j], in.vx - lvx[j],
                                               in.vy - lvy[j], L.pr.radius + lr[j] + C.margin, wx,
@@ -563,8 +601,8 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
                         }
                     }
                 }
-                if (!DRONE && C.boxes && L.pr.shape > T(0.5)) {
-                    if (C.N > 0 || C.soft_walls) {
+                if (BOXES && L.pr.shape > T(0.5)) {
+                    if ((C.N > 0 || C.soft_walls) && lst[s * 64 + L.lane]) {
                         const Foot<T> fa = {L.pr.shape, L.pr.radius, L.pr.hx, L.pr.hy};
                         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
                         box_static_adj(C, g.obs, eN, ocs, fa, in, L.dd, gFx, gFy, gi);
@@ -806,21 +844,21 @@ static bool fields_ok(const swarp_state_t *s, int n)
     default: hipLaunchKernelGGL((KERNEL<T, 64, __VA_ARGS__>), grid64, dim3(64), shm, st, C, a); break; \
     }
 
-template <typename T, bool DRONE>
+template <typename T, bool DRONE, bool BOXES>
 static void launch_fwd(int PA, const Cst<T> &C, const Args<T> &a, hipStream_t st)
 {
     const size_t shm = 0;
     const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
         grid32((C.E + 1) / 2), grid64(C.E);
-    SWARP_DISPATCH_PA(PA, k_rollout_fwd, DRONE)
+    SWARP_DISPATCH_PA(PA, k_rollout_fwd, DRONE, BOXES)
 }
 
-template <typename T, bool DRONE>
+template <typename T, bool DRONE, bool BOXES>
 static void launch_bwd(int PA, const Cst<T> &C, const Args<T> &a, size_t shm, hipStream_t st)
 {
     const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
         grid32((C.E + 1) / 2), grid64(C.E);
-    SWARP_DISPATCH_PA(PA, k_rollout_bwd, DRONE)
+    SWARP_DISPATCH_PA(PA, k_rollout_bwd, DRONE, BOXES)
 }
 
 static bool lean_ok(const swarp_desc_t *d)
@@ -932,9 +970,11 @@ static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
         else
             launch_holo_fwd<T, false>(PA, C, a, tape_ptrs<T>(TL, nullptr), st);
     else if (d->has_drone)
-        launch_fwd<T, true>(PA, C, a, st);
+        launch_fwd<T, true, false>(PA, C, a, st);
+    else if (d->has_boxes)
+        launch_fwd<T, false, true>(PA, C, a, st);
     else
-        launch_fwd<T, false>(PA, C, a, st);
+        launch_fwd<T, false, false>(PA, C, a, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
     return 0;
@@ -981,13 +1021,17 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     }
     const int NF = d->has_drone ? NF_DRONE : NF_2D;
     const size_t msz = PA == 64 ? 8 : 4;
-    const size_t shm = 2 * 64 * sizeof(T) + (size_t)d->substeps * NF * 64 * sizeof(T) +
-                       (size_t)d->substeps * 64 * msz;
+    size_t shm = 2 * 64 * sizeof(T) + (size_t)d->substeps * NF * 64 * sizeof(T) +
+                 (size_t)d->substeps * 64 * msz;
+    if (d->has_boxes)  // contact masks, heading cos / sin, static-contact flags per substep
+        shm += (size_t)d->substeps * 64 * (msz + 2 * sizeof(T) + 1);
     if (shm > 65536) return fail("substeps too large for the backward LDS staging (limit 64 KiB per wave)");
     if (d->has_drone)
-        launch_bwd<T, true>(PA, C, a, shm, st);
+        launch_bwd<T, true, false>(PA, C, a, shm, st);
+    else if (d->has_boxes)
+        launch_bwd<T, false, true>(PA, C, a, shm, st);
     else
-        launch_bwd<T, false>(PA, C, a, shm, st);
+        launch_bwd<T, false, false>(PA, C, a, shm, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
     return 0;
