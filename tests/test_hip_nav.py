@@ -121,10 +121,14 @@ def test_fused_pass_matches_oracle_fp64_direct_rows():
     _compare(env, o, trig_tol=4e-16)
 
 
+@pytest.mark.parametrize("shape", ["disc", "box"])
 @pytest.mark.parametrize("auto_reset", [False, True])
-def test_environment_fused_equals_torch_path(auto_reset):
+def test_environment_fused_equals_torch_path(auto_reset, shape):
+    """The fused pass and the torch path give the same episode, with disc agents and with
+    box agents (agent_shape="box": the box contact pass steps the world and the
+    circumscribed radius is the scenario's agent radius, navigation.py:61-79)."""
     E, A, T = 64, 16, 12
-    kw = dict(max_steps=5, auto_reset=auto_reset, goal_tolerance=0.2)
+    kw = dict(max_steps=5, auto_reset=auto_reset, goal_tolerance=0.2, agent_shape=shape)
     ef, et = _env(E, A, fused=True, **kw), _env(E, A, fused=False, **kw)
     of, ot = ef.reset(), et.reset()
     assert ef.scenario._fresh == "fused" and et.scenario._fresh == "torch"
@@ -146,6 +150,7 @@ def test_environment_fused_equals_torch_path(auto_reset):
             else:
                 torch.testing.assert_close(v1, v2, rtol=0, atol=1e-6)
     assert ef.scenario._fresh == "fused"
+    assert ef.world.stepper.has_boxes == (shape == "box")
 
 
 def test_grad_step_takes_the_torch_path():
