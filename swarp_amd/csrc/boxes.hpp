@@ -74,12 +74,16 @@ __device__ __forceinline__ Dual<T, N> operator*(const Dual<T, N> &a, T k)
     SWARP_DUAL_LOOP r.d[i] = a.d[i] * k;
     return r;
 }
+// The value part divides exactly (it is the forward arithmetic); the tangents scale by one
+// hardware reciprocal (1 ulp in fp32, exact in fp64), accurate far beyond what a
+// gradient needs.
 template <typename T, int N>
 __device__ __forceinline__ Dual<T, N> operator/(const Dual<T, N> &a, const Dual<T, N> &b)
 {
     Dual<T, N> r;
     r.v = a.v / b.v;
-    SWARP_DUAL_LOOP r.d[i] = (a.d[i] - r.v * b.d[i]) / b.v;
+    const T inv = m_rcp(b.v);
+    SWARP_DUAL_LOOP r.d[i] = (a.d[i] - r.v * b.d[i]) * inv;
     return r;
 }
 template <typename T, int N>
@@ -87,7 +91,8 @@ __device__ __forceinline__ Dual<T, N> operator/(const Dual<T, N> &a, T k)
 {
     Dual<T, N> r;
     r.v = a.v / k;
-    SWARP_DUAL_LOOP r.d[i] = a.d[i] / k;
+    const T inv = m_rcp(k);
+    SWARP_DUAL_LOOP r.d[i] = a.d[i] * inv;
     return r;
 }
 template <typename T, int N>
@@ -104,7 +109,7 @@ template <typename T, int N> __device__ __forceinline__ Dual<T, N> m_sqrt(const 
 {
     Dual<T, N> r;
     r.v = m_sqrt(a.v);
-    const T h = r.v > T(0) ? T(0.5) / r.v : T(0);
+    const T h = r.v > T(0) ? T(0.5) * m_rcp(r.v) : T(0);
     SWARP_DUAL_LOOP r.d[i] = a.d[i] * h;
     return r;
 }
@@ -382,94 +387,133 @@ __device__ __forceinline__ void agent_pair_force_box(const Cst<T> &C, int a, int
     }
 }
 
+// One obstacle's force on a box agent (state s, heading cos / sin ca / sa), the body of
+// _box_obstacle_force (:543-586): a BOX obstacle is obb_force with reach = margin, a
+// SEGMENT the degenerate box (half_len, 0) with reach = radius + margin (the exact
+// capsule), a CIRCLE minus box_force with the circle's centre as the point.
+template <typename T, typename V>
+__device__ __forceinline__ void box_obstacle_v(const Cst<T> &C, const Obs<T> &O, size_t j, int o,
+                                               const T *ocs, T hx, T hy, const V (&s)[6], V ca,
+                                               V sa, T dd, V &gx, V &gy)
+{
+    const T cx = O.pos[2 * j], cy = O.pos[2 * j + 1];
+    const int st = O.type[o];
+    const T ro = O.rad[o], ohx = O.half[2 * o], ohy = O.half[2 * o + 1];
+    T oc, os;
+    ob_trig(O, j, o, ocs, oc, os);
+    const V vox = V(O.vel[2 * j]), voy = V(O.vel[2 * j + 1]), om = V(O.om[j]);
+    if (st == 1 || st == 2) {
+        obb_force(C, s[BX_PX], s[BX_PY], ca, sa, hx, hy, s[BX_VX], s[BX_VY], s[BX_W], V(cx), V(cy),
+                  V(oc), V(os), ohx, st == 1 ? ohy : T(0), vox, voy, om,
+                  st == 1 ? C.margin : ro + C.margin, dd, gx, gy);
+    } else {
+        V hxv, hyv;
+        box_force_v(C, V(cx), V(cy), vox, voy, s[BX_PX], s[BX_PY], ca, sa, hx, hy, ro + C.margin,
+                    dd, s[BX_VX], s[BX_VY], s[BX_W], hxv, hyv);
+        gx = -hxv;
+        gy = -hyv;
+    }
+}
+
+// Whether obstacle o can touch a box agent of circumradius ra at (px, py): the reference's
+// broad phase (bounds_apart with shape_bound, collisions.py:61-84).
+template <typename T>
+__device__ __forceinline__ bool box_obstacle_near(const Cst<T> &C, const Obs<T> &O, size_t j,
+                                                  int o, T ra, T px, T py)
+{
+    const int st = O.type[o];
+    const T ro = O.rad[o], ohx = O.half[2 * o], ohy = O.half[2 * o + 1];
+    const T bound = st == 1 ? m_sqrt(ohx * ohx + ohy * ohy) : (st == 2 ? ohx + ro : ro);
+    const T lim = (ra + C.margin + bound) * T(1.0001) + T(1.0e-6);
+    const T ddx = px - O.pos[2 * j], ddy = py - O.pos[2 * j + 1];
+    return !(ddx * ddx + ddy * ddy > lim * lim);
+}
+
+// The soft walls on a box agent (_wall_forces_box, :641-688): the support extents replace
+// the radius, the damper reads the velocity of the vertex touching each wall.  `active`
+// (nullable) is set when a wall exerts a force.
+template <typename T, typename V>
+__device__ __forceinline__ void box_walls_v(const Cst<T> &C, T hx, T hy, const V (&s)[6], V ca,
+                                            V sa, T dd, V &wx, V &wy, bool *active = nullptr)
+{
+    const V ex = m_abs(ca) * hx + m_abs(sa) * hy;
+    const V ey = m_abs(sa) * hx + m_abs(ca) * hy;
+    const T vc = val(ca), vs = val(sa);
+    const T sc = vc > T(0) ? T(1) : (vc < T(0) ? T(-1) : T(0));
+    const T ss = vs > T(0) ? T(1) : (vs < T(0) ? T(-1) : T(0));
+    const V rl_y = sa * (-sc * hx) + ca * (ss * hy);
+    const V rb_x = ca * (-ss * hx) + sa * (sc * hy);
+    const V em = ex + V(C.margin), eym = ey + V(C.margin);
+    bool act = false;
+    wx = V(T(0));
+    wy = V(T(0));
+    V pen = em - (s[BX_PX] - V(C.bmin_x));
+    if (val(pen) > T(0)) {
+        const V q = normal_coeff_v(C, pen, s[BX_VX] - s[BX_W] * rl_y, dd);
+        act |= val(q) != T(0);
+        wx = wx + q;
+    }
+    pen = em - (V(C.bmax_x) - s[BX_PX]);
+    if (val(pen) > T(0)) {
+        const V q = normal_coeff_v(C, pen, -(s[BX_VX] + s[BX_W] * rl_y), dd);
+        act |= val(q) != T(0);
+        wx = wx + (-q);
+    }
+    pen = eym - (s[BX_PY] - V(C.bmin_y));
+    if (val(pen) > T(0)) {
+        const V q = normal_coeff_v(C, pen, s[BX_VY] + s[BX_W] * rb_x, dd);
+        act |= val(q) != T(0);
+        wy = wy + q;
+    }
+    pen = eym - (V(C.bmax_y) - s[BX_PY]);
+    if (val(pen) > T(0)) {
+        const V q = normal_coeff_v(C, pen, -(s[BX_VY] - s[BX_W] * rb_x), dd);
+        act |= val(q) != T(0);
+        wy = wy + (-q);
+    }
+    if (active) *active = act;
+}
+
 // Static forces on a box agent (state s, heading cos/sin ca/sa): obstacles in index order
-// (_obstacle_forces_box + _box_obstacle_force, :543-626), then the soft walls
-// (_wall_forces_box, :641-688).  `ocs`: this env's obstacle angles as (cos, sin) pairs,
-// or NULL.
-// `active` (nullable): set when some obstacle or wall exerts a nonzero force -- with none,
-// every derivative of the static force is zero too.
+// (_obstacle_forces_box, :589-626), then the soft walls (_static_forces_shaped,
+// :950-996).  `ocs`: this env's obstacle angles as (cos, sin) pairs, or NULL.  Recording
+// (all nullable): `omask` gets bit o for each of the first 64 obstacles exerting a force,
+// `wall` whether a wall does, `beyond` whether an obstacle past the 64th does.
 template <typename T, typename V>
 __device__ __forceinline__ void box_static_forces(const Cst<T> &C, const Obs<T> &O, size_t eN,
                                                   const T *ocs, T hx, T hy, const V (&s)[6], V ca,
                                                   V sa, T dd, V &fx_o, V &fy_o,
-                                                  bool *active = nullptr)
+                                                  uint64_t *omask = nullptr, bool *wall = nullptr,
+                                                  bool *beyond = nullptr)
 {
-    bool act = false;
     V fx = V(T(0)), fy = V(T(0));
     const T ra = m_sqrt(hx * hx + hy * hy);
+    uint64_t om = 0;
+    bool far = false;
     for (int o = 0; o < C.N; ++o) {
         const size_t j = eN + o;
-        const T cx = O.pos[2 * j], cy = O.pos[2 * j + 1];
-        const int st = O.type[o];
-        const T ro = O.rad[o], ohx = O.half[2 * o], ohy = O.half[2 * o + 1];
-        const T bound = st == 1 ? m_sqrt(ohx * ohx + ohy * ohy) : (st == 2 ? ohx + ro : ro);
-        const T lim = (ra + C.margin + bound) * T(1.0001) + T(1.0e-6);
-        const T ddx = val(s[BX_PX]) - cx, ddy = val(s[BX_PY]) - cy;
-        if (ddx * ddx + ddy * ddy > lim * lim) continue;
-        T oc, os;
-        ob_trig(O, j, o, ocs, oc, os);
-        const V vox = V(O.vel[2 * j]), voy = V(O.vel[2 * j + 1]), om = V(O.om[j]);
+        if (!box_obstacle_near(C, O, j, o, ra, val(s[BX_PX]), val(s[BX_PY]))) continue;
         V gx, gy;
-        if (st == 1) {
-            obb_force(C, s[BX_PX], s[BX_PY], ca, sa, hx, hy, s[BX_VX], s[BX_VY], s[BX_W], V(cx),
-                      V(cy), V(oc), V(os), ohx, ohy, vox, voy, om, C.margin, dd, gx, gy);
-        } else if (st == 2) {
-            // a capsule: the degenerate box (half_len, 0) with the reach grown by its radius
-            obb_force(C, s[BX_PX], s[BX_PY], ca, sa, hx, hy, s[BX_VX], s[BX_VY], s[BX_W], V(cx),
-                      V(cy), V(oc), V(os), ohx, T(0), vox, voy, om, ro + C.margin, dd, gx, gy);
-        } else {
-            // a circle: minus box_force with the circle's centre as the point
-            V hxv, hyv;
-            box_force_v(C, V(cx), V(cy), vox, voy, s[BX_PX], s[BX_PY], ca, sa, hx, hy,
-                        ro + C.margin, dd, s[BX_VX], s[BX_VY], s[BX_W], hxv, hyv);
-            gx = -hxv;
-            gy = -hyv;
+        box_obstacle_v(C, O, j, o, ocs, hx, hy, s, ca, sa, dd, gx, gy);
+        if (val(gx) != T(0) || val(gy) != T(0)) {
+            if (o < 64) om |= 1ull << o;
+            else far = true;
         }
-        act |= val(gx) != T(0) || val(gy) != T(0);
         fx = fx + gx;
         fy = fy + gy;
     }
+    bool won = false;
     if (C.soft_walls) {
-        // the walls see the support extents; the damper reads the touching vertex's velocity
-        const V ex = m_abs(ca) * hx + m_abs(sa) * hy;
-        const V ey = m_abs(sa) * hx + m_abs(ca) * hy;
-        const T vc = val(ca), vs = val(sa);
-        const T sc = vc > T(0) ? T(1) : (vc < T(0) ? T(-1) : T(0));
-        const T ss = vs > T(0) ? T(1) : (vs < T(0) ? T(-1) : T(0));
-        const V rl_y = sa * (-sc * hx) + ca * (ss * hy);
-        const V rb_x = ca * (-ss * hx) + sa * (sc * hy);
-        const V em = ex + V(C.margin), eym = ey + V(C.margin);
-        V wx = V(T(0)), wy = V(T(0));
-        V pen = em - (s[BX_PX] - V(C.bmin_x));
-        if (val(pen) > T(0)) {
-            const V q = normal_coeff_v(C, pen, s[BX_VX] - s[BX_W] * rl_y, dd);
-            act |= val(q) != T(0);
-            wx = wx + q;
-        }
-        pen = em - (V(C.bmax_x) - s[BX_PX]);
-        if (val(pen) > T(0)) {
-            const V q = normal_coeff_v(C, pen, -(s[BX_VX] + s[BX_W] * rl_y), dd);
-            act |= val(q) != T(0);
-            wx = wx + (-q);
-        }
-        pen = eym - (s[BX_PY] - V(C.bmin_y));
-        if (val(pen) > T(0)) {
-            const V q = normal_coeff_v(C, pen, s[BX_VY] + s[BX_W] * rb_x, dd);
-            act |= val(q) != T(0);
-            wy = wy + q;
-        }
-        pen = eym - (V(C.bmax_y) - s[BX_PY]);
-        if (val(pen) > T(0)) {
-            const V q = normal_coeff_v(C, pen, -(s[BX_VY] - s[BX_W] * rb_x), dd);
-            act |= val(q) != T(0);
-            wy = wy + (-q);
-        }
+        V wx, wy;
+        box_walls_v(C, hx, hy, s, ca, sa, dd, wx, wy, &won);
         fx = fx + wx;
         fy = fy + wy;
     }
     fx_o = fx;
     fy_o = fy;
-    if (active) *active = act;
+    if (omask) *omask = om;
+    if (wall) *wall = won;
+    if (beyond) *beyond = far;
 }
 
 // ------------------------------------------------------------------ reverse helpers
@@ -525,27 +569,102 @@ __device__ __forceinline__ void seed_state(const St<T> &s, int k0, Dual<T, N> (&
 #define SWARP_BOX_ADJ __device__ __forceinline__
 #endif
 
-// Reverse of a pair with a box, seen from agent a (state `in`) against agent b (`sb`,
-// cos / sin of its heading cb, snb): adds J_a(f)^T w, with f the pair function evaluated
-// with a unit damping denominator and w the caller's combined cotangent (own force
-// adjoint / dd_a minus, where a is in b's list, b's / dd_b).
+// Kinds of work item of the box reverse pass (see box_item_adj).
+enum { BI_PAIR = 0, BI_OBST = 1, BI_WALL = 2, BI_FULL = 3 };
+
+// Reverse of one box contact of agent a (state `in`): adds J_a(f)^T w.  The contact is
+//   BI_PAIR  a pair with neighbour b (`sb`, cos / sin cb, snb of its heading), f the pair
+//            function with a unit damping denominator, w the caller's combined cotangent
+//            (a's force adjoint / dd_a minus, where a is in b's list, b's / dd_b);
+//   BI_OBST  obstacle o (index j = env * N + o) on box agent a, dd = a's, w = a's force
+//            adjoint; likewise BI_WALL (the walls) and BI_FULL (every static contact).
+// Pairs and obstacles are routed to one of two evaluation sites -- the box-box law
+// (obb_force, box A / box B) or the point-box law (box_force, point / box) -- with the
+// seeded agent as either operand, so the lanes of a wave evaluating different kinds of
+// contact share those two sites.
 template <typename T>
-SWARP_BOX_ADJ void box_pair_adj(const Cst<T> &C, int a, int b, const Foot<T> &Fa,
-                                             const St<T> &in, const Foot<T> &Fb, const T (&sb)[6],
-                                             T cb, T snb, T wx, T wy, St<T> &g)
+SWARP_BOX_ADJ void box_item_adj(const Cst<T> &C, const Obs<T> &O, size_t eN, const T *ocs,
+                                int kind, int ag, const Foot<T> &Fa, const St<T> &in, int b,
+                                const Foot<T> &Fb, const T (&sb)[6], T cb, T snb, int o, T dd,
+                                T wx, T wy, St<T> &g)
 {
     typedef Dual<T, BOX_NT> DN;
+    const T half = T(0.5);
+    // operands as plain values: X = the other agent or the obstacle
+    T xs[6] = {T(0), T(0), T(0), T(0), T(0), T(0)}, xc = T(1), xsn = T(0), xh0 = T(0), xh1 = T(0);
+    T reach = C.margin, sgn = T(1);
+    bool obb = false, me_first = true;  // obb: box-box law; me_first: a is box A / the point
+    if (kind == BI_PAIR) {
+#pragma unroll
+        for (int k = 0; k < 6; ++k) xs[k] = sb[k];
+        xc = cb;
+        xsn = snb;
+        xh0 = Fb.hx;
+        xh1 = Fb.hy;
+        if (Fa.shape > half && Fb.shape > half) {  // the lower index is box A
+            obb = true;
+            me_first = ag < b;
+            sgn = me_first ? T(1) : T(-1);
+        } else if (Fa.shape < half) {               // disc a: the point of box b
+            reach = Fa.radius + C.margin;
+        } else {                                    // box a against disc b
+            me_first = false;
+            sgn = T(-1);
+            reach = Fb.radius + C.margin;
+        }
+    } else if (kind == BI_OBST) {
+        const size_t j = eN + o;
+        const int st = O.type[o];
+        const T ro = O.rad[o];
+        xs[BX_PX] = O.pos[2 * j];
+        xs[BX_PY] = O.pos[2 * j + 1];
+        xs[BX_VX] = O.vel[2 * j];
+        xs[BX_VY] = O.vel[2 * j + 1];
+        xs[BX_W] = O.om[j];
+        ob_trig(O, j, o, ocs, xc, xsn);
+        xh0 = O.half[2 * o];
+        xh1 = st == 1 ? O.half[2 * o + 1] : T(0);
+        if (st == 1 || st == 2) {
+            obb = true;
+            reach = st == 1 ? C.margin : ro + C.margin;
+        } else {                                    // circle: minus box_force, its centre the point
+            me_first = false;
+            sgn = T(-1);
+            reach = ro + C.margin;
+        }
+    }
+    const T vx = sgn * wx, vy = sgn * wy;
 #pragma unroll 1
     for (int k0 = 0; k0 < 6; k0 += BOX_NT) {
-        DN ob[6];
-#pragma unroll
-        for (int k = 0; k < 6; ++k) ob[k] = DN(sb[k]);
         DN me[6];
         seed_state(in, k0, me);
         const DN ca = m_cos(me[BX_TH]), sa = m_sin(me[BX_TH]);
         DN fx, fy;
-        agent_pair_force_box<T, DN>(C, a, b, Fa, me, ca, sa, Fb, ob, DN(cb), DN(snb), T(1), fx, fy);
-        add_cols(fx, fy, wx, wy, k0, g);
+        if (kind == BI_WALL) {
+            box_walls_v<T, DN>(C, Fa.hx, Fa.hy, me, ca, sa, dd, fx, fy);
+        } else if (kind == BI_FULL) {
+            box_static_forces<T, DN>(C, O, eN, ocs, Fa.hx, Fa.hy, me, ca, sa, dd, fx, fy);
+        } else {
+            // operand 1 (box A / the point) and operand 2 (box B / the box)
+            DN p1[6], p2[6];
+#pragma unroll
+            for (int k = 0; k < 6; ++k) {
+                p1[k] = me_first ? me[k] : DN(xs[k]);
+                p2[k] = me_first ? DN(xs[k]) : me[k];
+            }
+            const DN c1 = me_first ? ca : DN(xc), s1 = me_first ? sa : DN(xsn);
+            const DN c2 = me_first ? DN(xc) : ca, s2 = me_first ? DN(xsn) : sa;
+            const T h10 = me_first ? Fa.hx : xh0, h11 = me_first ? Fa.hy : xh1;
+            const T h20 = me_first ? xh0 : Fa.hx, h21 = me_first ? xh1 : Fa.hy;
+            if (obb)
+                obb_force(C, p1[BX_PX], p1[BX_PY], c1, s1, h10, h11, p1[BX_VX], p1[BX_VY],
+                          p1[BX_W], p2[BX_PX], p2[BX_PY], c2, s2, h20, h21, p2[BX_VX], p2[BX_VY],
+                          p2[BX_W], reach, dd, fx, fy);
+            else
+                box_force_v(C, p1[BX_PX], p1[BX_PY], p1[BX_VX], p1[BX_VY], p2[BX_PX], p2[BX_PY],
+                            c2, s2, h20, h21, reach, dd, p2[BX_VX], p2[BX_VY], p2[BX_W], fx, fy);
+        }
+        add_cols(fx, fy, vx, vy, k0, g);
     }
 }
 

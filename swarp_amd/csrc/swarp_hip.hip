@@ -279,14 +279,15 @@ __device__ __forceinline__ const T *ob_trig_table(const Cst<T> &C, const Args<T>
 // footprint (shape, hx, hy rows of 64), `lcs` the cos and sin of every lane's heading
 // (rows of 64), and the slot `sl` also carries the headings and spins (F_TH, F_W rows).
 // `act` (nullable) receives the mask of listed neighbours whose box contact exerts a
-// force and `stat` whether any static contact of a box agent does: without them every
-// derivative of those forces is zero.
+// force; for a box agent `om` / `wall` / `beyond` which of its first 64 obstacles, its
+// walls, and any later obstacle do: the contacts without force have zero derivatives.
 template <typename T, int PA, bool BOXES>
 __device__ __forceinline__ typename MaskT<PA>::type forces(
     const Cst<T> &C, const Args<T> &g, const Lane<T, PA> &L, const T *sl, const T *lr,
     const St<T> &st, int s, bool full, typename MaskT<PA>::type &cand, T &Fx, T &Fy,
     const T *ocs = nullptr, const T *lbx = nullptr, const T *lcs = nullptr,
-    typename MaskT<PA>::type *act = nullptr, bool *stat = nullptr)
+    typename MaskT<PA>::type *act = nullptr, uint64_t *om = nullptr, bool *wall = nullptr,
+    bool *beyond = nullptr)
 {
     const bool box_me = BOXES && L.pr.shape > T(0.5);
     T me[6] = {st.px, st.py, st.th, st.vx, st.vy, st.w};
@@ -337,7 +338,7 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
         // a box agent's obstacles and walls (_static_forces_shaped, collisions.py:950-996)
         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
         box_static_forces<T, T>(C, g.obs, eN, ocs, L.pr.hx, L.pr.hy, me, cme, sme, L.dd, sx, sy,
-                                stat);
+                                om, wall, beyond);
     } else if (C.N > 0) {
         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
         for (int o = 0; o < C.N; ++o) {
@@ -470,6 +471,124 @@ template <typename M> __device__ __forceinline__ bool in_list(M incl, int me, in
     return ((incl >> me) & M(1)) && m_popc(incl & ((M(1) << me) - M(1))) < K;
 }
 
+// Reverse pass of one substep's box contacts, as one wave-wide work list.  Lane a's items
+// are its force-exerting box pairs (ascending neighbour), then for a box agent its
+// force-exerting obstacles (ascending index) and walls -- or, when an obstacle past the
+// 64th exerts a force, one item for all its static contacts.  The wave evaluates the
+// items one per lane, 64 at a time (the owner of item q found by binary search over the
+// item offsets), and each lane adds its own items' results in item order.  A per-lane
+// loop would run one dual evaluation for the whole wave per list position, obstacle and
+// wall that any lane needs.
+// `sl`: the substep's slot (force rows holding force adjoint / damping denominator),
+// `lcs`: its heading cos / sin rows, `lmask_s` its list masks; this lane's force-exerting
+// box pairs `imask`, obstacles `om` and flags `wf` (1 walls, 2 a later obstacle).
+template <typename T, int PA>
+__device__ __forceinline__ void box_rounds(const Cst<T> &C, const Args<T> &g,
+                                           const Lane<T, PA> &L, const T *sl, const T *lr,
+                                           const T *ldd, const T *lbx, const T *lcs,
+                                           const typename MaskT<PA>::type *lmask_s,
+                                           const T *ocs_base, typename MaskT<PA>::type imask,
+                                           uint64_t om, unsigned wf, T gFx, T gFy, St<T> &gi)
+{
+    typedef typename MaskT<PA>::type M;
+    __shared__ int pre[64];
+    __shared__ M imk[64];
+    __shared__ uint64_t iom[64];
+    __shared__ unsigned char iwf[64];
+    __shared__ T gfr[2 * 64];
+    __shared__ T res[6 * 64];
+    const int lane = L.lane;
+    if (wf & 2u) om = 0;  // one item for every static contact
+    const int n = m_popc(imask) + __builtin_popcountll(om) + ((wf & 3u) ? 1 : 0);
+    int x = n;  // inclusive prefix sum of the item counts over the wave
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+    }
+    const int start = x - n;
+    const int total = __shfl(x, 63, 64);
+    if (total == 0) return;
+    pre[lane] = start;
+    imk[lane] = imask;
+    iom[lane] = om;
+    iwf[lane] = (unsigned char)wf;
+    gfr[lane] = gFx;
+    gfr[64 + lane] = gFy;
+    __syncthreads();
+    for (int r = 0; r < total; r += 64) {
+        const int q = r + lane;
+        if (q < total) {
+            int lo = 0, hi = 63;  // the last lane whose first item is <= q owns it
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (pre[mid] <= q) lo = mid;
+                else hi = mid - 1;
+            }
+            const int a = lo, ag = a % PA, base = a - ag;
+            int k = q - pre[a];
+            St<T> ins;
+            slot_get<T, false>(sl, a, ins);
+            const Foot<T> fa = {lbx[a], lr[a], lbx[64 + a], lbx[128 + a]};
+            const int env = blockIdx.x * (64 / PA) + a / PA;
+            const size_t eN = (size_t)(env < C.E ? env : 0) * C.N;
+            const T *ocs_a = ocs_base ? ocs_base + 2 * (a / PA) * C.N : nullptr;
+            M mk = imk[a];
+            uint64_t mo = iom[a];
+            const int np = m_popc(mk), no = __builtin_popcountll(mo);
+            int kind, b = 0, o = 0, j = base;
+            T wx, wy, dd;
+            if (k < np) {
+                kind = BI_PAIR;
+                for (; k > 0; --k) mk &= mk - 1;
+                b = m_ctz(mk);
+                j = base + b;
+                const bool own = in_list(lmask_s[a], b, C.K);
+                const bool rev = in_list(lmask_s[j], ag, C.K);
+                wx = (own ? sl[F_FX * 64 + a] : T(0)) - (rev ? sl[F_FX * 64 + j] : T(0));
+                wy = (own ? sl[F_FY * 64 + a] : T(0)) - (rev ? sl[F_FY * 64 + j] : T(0));
+                dd = T(1);
+            } else {
+                k -= np;
+                if (k < no) {
+                    kind = BI_OBST;
+                    for (; k > 0; --k) mo &= mo - 1;
+                    o = __builtin_ctzll(mo);
+                } else {
+                    kind = (iwf[a] & 2u) ? BI_FULL : BI_WALL;
+                }
+                wx = gfr[a];
+                wy = gfr[64 + a];
+                dd = ldd[a];
+            }
+            const Foot<T> fb = {lbx[j], lr[j], lbx[64 + j], lbx[128 + j]};
+            const T ob[6] = {sl[F_PX * 64 + j], sl[F_PY * 64 + j], sl[F_TH * 64 + j],
+                             sl[F_VX * 64 + j], sl[F_VY * 64 + j], sl[F_W * 64 + j]};
+            St<T> acc;
+            st_zero(acc);
+            box_item_adj(C, g.obs, eN, ocs_a, kind, ag, fa, ins, b, fb, ob, lcs[j], lcs[64 + j], o,
+                         dd, wx, wy, acc);
+            res[lane] = acc.px;
+            res[64 + lane] = acc.py;
+            res[128 + lane] = acc.th;
+            res[192 + lane] = acc.vx;
+            res[256 + lane] = acc.vy;
+            res[320 + lane] = acc.w;
+        }
+        __syncthreads();
+        const int q0 = start > r ? start : r, q1 = min(start + n, r + 64);
+        for (int c = q0 - r; c < q1 - r; ++c) {
+            gi.px += res[c];
+            gi.py += res[64 + c];
+            gi.th += res[128 + c];
+            gi.vx += res[192 + c];
+            gi.vy += res[256 + c];
+            gi.w += res[320 + c];
+        }
+        __syncthreads();
+    }
+}
+
 template <typename T, int PA, bool DRONE, bool BOXES>
 __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T> g)
 {
@@ -480,11 +599,13 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
     T *ldd = lr + 64;           // damping denominator per lane
     T *slots = ldd + 64;        // S slots of NF fields
     M *lmask = (M *)(slots + (size_t)C.S * NF * 64);  // S inclusion masks per lane
-    // box worlds: per substep the masks of force-exerting box contacts, the cos / sin of
-    // every lane's heading, and whether a box agent's static contacts exert a force
+    // box worlds, per substep: the masks of force-exerting box pairs, the cos / sin of
+    // every lane's heading, a box agent's force-exerting obstacles (first 64) and flags
+    // (1: a wall exerts a force, 2: a later obstacle does)
     M *lact = lmask + (size_t)C.S * 64;
     T *lcsb = (T *)(lact + (size_t)C.S * 64);
-    unsigned char *lst = (unsigned char *)(lcsb + (size_t)C.S * 128);
+    uint64_t *lom = (uint64_t *)(lcsb + (size_t)C.S * 128);
+    unsigned char *lwf = (unsigned char *)(lom + (size_t)C.S * 64);
     __shared__ T ocs_lds[2 * OCS_MAX];
     __shared__ T lbx[3 * 64];  // footprint per lane: shape, hx, hy (box worlds)
     Lane<T, PA> L;
@@ -529,12 +650,14 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
             M incl = 0;
             if (C.needs_forces) {
                 M am = 0;
-                bool stf = false;
+                uint64_t om = 0;
+                bool wl = false, far = false;
                 incl = forces<T, PA, BOXES>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy,
-                                            ocs, lbx, lcsb + s * 128, &am, &stf);
+                                            ocs, lbx, lcsb + s * 128, &am, &om, &wl, &far);
                 if (BOXES) {
                     lact[s * 64 + L.lane] = am;
-                    lst[s * 64 + L.lane] = stf ? 1 : 0;
+                    lom[s * 64 + L.lane] = om;
+                    lwf[s * 64 + L.lane] = (wl ? 1 : 0) | (far ? 2 : 0);
                 }
             }
             sl[F_FX * 64 + L.lane] = Fx;
@@ -567,6 +690,7 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
                 sl[F_FX * 64 + L.lane] = wFx;
                 sl[F_FY * 64 + L.lane] = wFy;
                 __syncthreads();
+                M imask = 0;  // force-exerting box pairs, reversed in box_rounds
                 if (C.collisions) {
                     const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64;
                     const T *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
@@ -580,33 +704,30 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
                         const bool own = in_list(mine, b, C.K);
                         const bool rev = in_list(lmask[s * 64 + j], L.agent, C.K);
                         if (!own && !rev) continue;
-                        const T wx = (own ? wFx : T(0)) - (rev ? lgx[j] : T(0));
-                        const T wy = (own ? wFy : T(0)) - (rev ? lgy[j] : T(0));
                         if (BOXES && (L.pr.shape > T(0.5) || lbx[j] > T(0.5))) {
                             // one contact seen from both sides: it exerts a force, or
                             // every derivative of it is zero
                             const bool on = own ? ((lact[s * 64 + L.lane] >> b) & M(1)) != 0
                                                 : ((lact[s * 64 + j] >> L.agent) & M(1)) != 0;
-                            if (!on) continue;
-                            const Foot<T> fa = {L.pr.shape, L.pr.radius, L.pr.hx, L.pr.hy};
-                            const Foot<T> fb = {lbx[j], lr[j], lbx[64 + j], lbx[128 + j]};
-                            const T ob[6] = {lx[j], ly[j], sl[F_TH * 64 + j], lvx[j], lvy[j],
-                                             sl[F_W * 64 + j]};
-                            box_pair_adj(C, L.agent, b, fa, in, fb, ob, lcsb[s * 128 + j],
-                                         lcsb[s * 128 + 64 + j], wx, wy, gi);
-                        } else {
-                            pair_adj_combined(C, in.px - lx[j], in.py - ly[j], in.vx - lvx[j],
-                                              in.vy - lvy[j], L.pr.radius + lr[j] + C.margin, wx,
-                                              wy, gi.px, gi.py, gi.vx, gi.vy);
+                            if (on) imask |= M(1) << b;
+                            continue;
                         }
+                        const T wx = (own ? wFx : T(0)) - (rev ? lgx[j] : T(0));
+                        const T wy = (own ? wFy : T(0)) - (rev ? lgy[j] : T(0));
+                        pair_adj_combined(C, in.px - lx[j], in.py - ly[j], in.vx - lvx[j],
+                                          in.vy - lvy[j], L.pr.radius + lr[j] + C.margin, wx, wy,
+                                          gi.px, gi.py, gi.vx, gi.vy);
                     }
                 }
+                if (BOXES) {
+                    const bool bx = L.pr.shape > T(0.5);
+                    box_rounds<T, PA>(C, g, L, sl, lr, ldd, lbx, lcsb + s * 128, lmask + s * 64,
+                                      ocs ? ocs_lds : nullptr, imask,
+                                      bx ? lom[s * 64 + L.lane] : 0ull,
+                                      bx ? lwf[s * 64 + L.lane] : 0, gFx, gFy, gi);
+                }
                 if (BOXES && L.pr.shape > T(0.5)) {
-                    if ((C.N > 0 || C.soft_walls) && lst[s * 64 + L.lane]) {
-                        const Foot<T> fa = {L.pr.shape, L.pr.radius, L.pr.hx, L.pr.hy};
-                        const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
-                        box_static_adj(C, g.obs, eN, ocs, fa, in, L.dd, gFx, gFy, gi);
-                    }
+                    // a box agent's static contacts were reversed in box_rounds
                 } else {
                     if (C.N > 0) {
                         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
@@ -1024,7 +1145,7 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     size_t shm = 2 * 64 * sizeof(T) + (size_t)d->substeps * NF * 64 * sizeof(T) +
                  (size_t)d->substeps * 64 * msz;
     if (d->has_boxes)  // contact masks, heading cos / sin, static-contact flags per substep
-        shm += (size_t)d->substeps * 64 * (msz + 2 * sizeof(T) + 1);
+        shm += (size_t)d->substeps * 64 * (msz + 2 * sizeof(T) + 8 + 1);
     if (shm > 65536) return fail("substeps too large for the backward LDS staging (limit 64 KiB per wave)");
     if (d->has_drone)
         launch_bwd<T, true, false>(PA, C, a, shm, st);
