@@ -12,9 +12,10 @@ types so a caller's configuration code carries over unchanged:
 * ``Obstacles`` follows ``swarp/core/config.py:39-178``.
 * ``drone_config`` follows ``swarp/dynamics/drone.py:24-53``.
 
-What the MI355X build does not run is rejected here, loudly, rather than silently
-approximated: box agents, ``ControlMode.SERVO``, RK4, wheel contacts and per-env
-parameter tables raise ``NotImplementedError`` when a ``Stepper`` is built with them.
+What the MI355X build does not run is rejected loudly rather than silently
+approximated: ``ControlMode.SERVO``, wheel contacts, per-env parameter tables, box
+agents together with movable bodies and more than 64 agents per env raise
+``NotImplementedError`` when a ``Stepper`` is built with them (or the bodies installed).
 """
 
 from __future__ import annotations
