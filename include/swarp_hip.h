@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 6
+#define SWARP_ABI_VERSION 7
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -74,6 +74,14 @@ typedef struct swarp_desc {
        box-aware contact pass (collision_forces_box_kernel, swarp/core/collisions.py:
        999-1059) -- oriented-rectangle contacts against discs, boxes, obstacles and walls */
     int32_t has_boxes;
+    /* WorldConfig.wheel_contacts (forward only, Euler, no drones; swarp/core/stepper.py:
+       851-858): the force pass also computes each agent's contact torque
+       (collision_forces_wheel_kernel, swarp/core/collisions.py:1343-1403) and a diff-drive
+       agent's step is reworked by wheel_contact (swarp/dynamics/kernels.py:1328-1387);
+       lat_grip = wheel_lateral_friction * gravity, turn_cap = wheel_turn_torque.
+       swarp_rollout_bwd rejects it. */
+    int32_t wheel_contacts;
+    double lat_grip, turn_cap;
 } swarp_desc_t;
 
 /* The nine state fields.  A NULL field means "not provided": an input adjoint that

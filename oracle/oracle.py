@@ -36,7 +36,8 @@ class OracleCfg(ctypes.Structure):
         ("bmin_x", ctypes.c_double), ("bmin_y", ctypes.c_double),
         ("bmax_x", ctypes.c_double), ("bmax_y", ctypes.c_double),
         ("lin_damping", ctypes.c_double), ("ang_damping", ctypes.c_double),
-        ("rk4", ctypes.c_int),
+        ("rk4", ctypes.c_int), ("wheel", ctypes.c_int),
+        ("lat_grip", ctypes.c_double), ("turn_cap", ctypes.c_double),
     ]
 
 

@@ -343,7 +343,7 @@ static void FN(d_obb_contact)(const FN(ctx_t) *C, D cAx, D cAy, D thA, REAL hA0,
 /* obb_force (collisions.py:449-487): force on box A from box B */
 static void FN(d_obb_force)(const FN(ctx_t) *C, D cAx, D cAy, D thA, REAL hA0, REAL hA1, D vAx,
                             D vAy, D wA, D cBx, D cBy, D thB, REAL hB0, REAL hB1, D vBx, D vBy,
-                            D wB, REAL reach, REAL dd, D *fx, D *fy)
+                            D wB, REAL reach, REAL dd, D *fx, D *fy, D *xo, D *yo)
 {
     D s, nx, ny, xx, xy;
     FN(d_obb_contact)(C, cAx, cAy, thA, hA0, hA1, cBx, cBy, thB, hB0, hB1, reach, &s, &nx, &ny,
@@ -362,6 +362,8 @@ static void FN(d_obb_force)(const FN(ctx_t) *C, D cAx, D cAy, D thA, REAL hA0, R
         *fx = FN(dmul)(coef, nx);
         *fy = FN(dmul)(coef, ny);
     }
+    if (xo) *xo = xx;
+    if (yo) *yo = xy;
 }
 
 /* _agent_pair_force (collisions.py:489-541): force on agent a (state sa) from agent b
@@ -387,13 +389,13 @@ static void FN(d_agent_pair_force)(const FN(ctx_t) *C, int a, int b, const FN(pr
     } else if (a < b) {
         FN(d_obb_force)(C, sa[BX_PX], sa[BX_PY], sa[BX_TH], Pa->hx, Pa->hy, sa[BX_VX], sa[BX_VY],
                         sa[BX_W], sb[BX_PX], sb[BX_PY], sb[BX_TH], Pb->hx, Pb->hy, sb[BX_VX],
-                        sb[BX_VY], sb[BX_W], C->margin, dd, fx, fy);
+                        sb[BX_VY], sb[BX_W], C->margin, dd, fx, fy, NULL, NULL);
     } else {
         /* the lower index is box A on both threads: one contact, opposite signs */
         D gx, gy;
         FN(d_obb_force)(C, sb[BX_PX], sb[BX_PY], sb[BX_TH], Pb->hx, Pb->hy, sb[BX_VX], sb[BX_VY],
                         sb[BX_W], sa[BX_PX], sa[BX_PY], sa[BX_TH], Pa->hx, Pa->hy, sa[BX_VX],
-                        sa[BX_VY], sa[BX_W], C->margin, dd, &gx, &gy);
+                        sa[BX_VY], sa[BX_W], C->margin, dd, &gx, &gy, NULL, NULL);
         *fx = FN(dneg)(gx);
         *fy = FN(dneg)(gy);
     }
@@ -421,12 +423,12 @@ static void FN(d_box_static_forces)(const FN(ctx_t) *C, const REAL *od, const FN
         D gx, gy;
         if (st == 1) {
             FN(d_obb_force)(C, s[BX_PX], s[BX_PY], s[BX_TH], hx, hy, s[BX_VX], s[BX_VY], s[BX_W],
-                            cx, cy, ang, ohx, ohy, vox, voy, om, C->margin, dd, &gx, &gy);
+                            cx, cy, ang, ohx, ohy, vox, voy, om, C->margin, dd, &gx, &gy, NULL, NULL);
         } else if (st == 2) {
             /* a capsule: the degenerate box (half_len, 0), reach grown by its radius */
             FN(d_obb_force)(C, s[BX_PX], s[BX_PY], s[BX_TH], hx, hy, s[BX_VX], s[BX_VY], s[BX_W],
                             cx, cy, ang, ohx, (REAL)0, vox, voy, om, ro + C->margin, dd, &gx,
-                            &gy);
+                            &gy, NULL, NULL);
         } else {
             /* a circle: minus box_force with the circle centre as the point */
             D hxv, hyv;
@@ -593,6 +595,244 @@ static void FN(forces_env_box_adj)(const FN(ctx_t) *C, const REAL *od, const FN(
             }
         }
     }
+}
+
+/* ------------------------------------------------------------- wheel contacts */
+/* WorldConfig.wheel_contacts (no-grad Euler 2-D path only): the force pass also returns
+   each agent's contact torque about its centre (collision_forces_wheel_kernel,
+   swarp/core/collisions.py:1128-1403) and a diff-drive agent's step is reworked by
+   wheel_contact (swarp/dynamics/kernels.py:1328-1387). */
+
+static inline REAL FN(cross2)(REAL rx, REAL ry, REAL fx, REAL fy) { return rx * fy - ry * fx; }
+
+/* _box_sd (collisions.py:1133-1141): signed distance from a point to an oriented box */
+static REAL FN(box_sd)(REAL vx, REAL vy, REAL cx, REAL cy, REAL ca, REAL sa, REAL h0, REAL h1)
+{
+    REAL dx = vx - cx, dy = vy - cy;
+    REAL lx = FABS(ca * dx + sa * dy) - h0;
+    REAL ly = FABS(-sa * dx + ca * dy) - h1;
+    REAL ox = FN(rmax)(lx, (REAL)0), oy = FN(rmax)(ly, (REAL)0);
+    REAL m = FN(rmax)(lx, ly);
+    m = m < (REAL)0 ? m : (REAL)0;
+    return SQRT(ox * ox + oy * oy) + m;
+}
+
+/* _manifold_point (collisions.py:1144-1185): the in-reach vertices of either box averaged
+   with their depths as weights; (x, y) when none is in reach */
+static void FN(manifold_point)(REAL cAx, REAL cAy, REAL thA, REAL hA0, REAL hA1, REAL cBx,
+                               REAL cBy, REAL thB, REAL hB0, REAL hB1, REAL reach, REAL *x,
+                               REAL *y)
+{
+    REAL caA = COS(thA), saA = SIN(thA), caB = COS(thB), saB = SIN(thB);
+    REAL eA0x = caA * hA0, eA0y = saA * hA0, eA1x = -saA * hA1, eA1y = caA * hA1;
+    REAL eB0x = caB * hB0, eB0y = saB * hB0, eB1x = -saB * hB1, eB1y = caB * hB1;
+    REAL ax = 0, ay = 0, ws = 0;
+    for (int i = 0; i < 4; ++i) {
+        REAL sx = (i == 1 || i == 2) ? (REAL)-1 : (REAL)1, sy = i >= 2 ? (REAL)-1 : (REAL)1;
+        REAL vax = (cAx + eA0x * sx) + eA1x * sy, vay = (cAy + eA0y * sx) + eA1y * sy;
+        REAL da = FN(rmax)(reach - FN(box_sd)(vax, vay, cBx, cBy, caB, saB, hB0, hB1), (REAL)0);
+        ax += vax * da;
+        ay += vay * da;
+        ws += da;
+        REAL vbx = (cBx + eB0x * sx) + eB1x * sy, vby = (cBy + eB0y * sx) + eB1y * sy;
+        REAL db = FN(rmax)(reach - FN(box_sd)(vbx, vby, cAx, cAy, caA, saA, hA0, hA1), (REAL)0);
+        ax += vbx * db;
+        ay += vby * db;
+        ws += db;
+    }
+    if (ws > (REAL)0) {
+        *x = ax / ws;
+        *y = ay / ws;
+    }
+}
+
+/* _agent_pair_force_torque (collisions.py:1188-1243): the pair force on a and its torque
+   about a's centre (0 for a disc a) */
+static void FN(pair_force_torque)(const FN(ctx_t) *C, int a, int b, const FN(prm_t) *Pa,
+                                  const FN(prm_t) *Pb, const FN(agent_t) *A,
+                                  const FN(agent_t) *B, REAL dd, REAL *fx, REAL *fy, REAL *tau)
+{
+    const REAL half = (REAL)0.5;
+    *tau = 0;
+    if (Pa->shape < half && Pb->shape < half) {
+        FN(pair_force)(C, A->px - B->px, A->py - B->py, A->vx - B->vx, A->vy - B->vy,
+                       Pa->radius + Pb->radius + C->margin, dd, fx, fy);
+        return;
+    }
+    FN(dn) sa[BX_N], sb[BX_N], gx, gy, xx, xy;
+    FN(dstate)(A, -1, sa);
+    FN(dstate)(B, -1, sb);
+    if (Pa->shape < half) {
+        FN(d_agent_pair_force)(C, a, b, Pa, Pb, sa, sb, dd, &gx, &gy);
+        *fx = gx.v;
+        *fy = gy.v;
+    } else if (Pb->shape < half) {
+        FN(d_agent_pair_force)(C, a, b, Pa, Pb, sa, sb, dd, &gx, &gy);
+        *fx = gx.v;
+        *fy = gy.v;
+        REAL fn = SQRT(*fx * *fx + *fy * *fy);
+        if (fn > (REAL)0) {  /* at the disc's point nearest to a */
+            REAL k = Pb->radius / fn;
+            *tau = FN(cross2)((B->px + *fx * k) - A->px, (B->py + *fy * k) - A->py, *fx, *fy);
+        }
+    } else {
+        if (a < b) {
+            FN(d_obb_force)(C, sa[BX_PX], sa[BX_PY], sa[BX_TH], Pa->hx, Pa->hy, sa[BX_VX],
+                            sa[BX_VY], sa[BX_W], sb[BX_PX], sb[BX_PY], sb[BX_TH], Pb->hx, Pb->hy,
+                            sb[BX_VX], sb[BX_VY], sb[BX_W], C->margin, dd, &gx, &gy, &xx, &xy);
+            *fx = gx.v;
+            *fy = gy.v;
+        } else {
+            FN(d_obb_force)(C, sb[BX_PX], sb[BX_PY], sb[BX_TH], Pb->hx, Pb->hy, sb[BX_VX],
+                            sb[BX_VY], sb[BX_W], sa[BX_PX], sa[BX_PY], sa[BX_TH], Pa->hx, Pa->hy,
+                            sa[BX_VX], sa[BX_VY], sa[BX_W], C->margin, dd, &gx, &gy, &xx, &xy);
+            *fx = -gx.v;
+            *fy = -gy.v;
+        }
+        if (*fx * *fx + *fy * *fy > (REAL)0) {
+            REAL x = xx.v, y = xy.v;
+            FN(manifold_point)(A->px, A->py, A->th, Pa->hx, Pa->hy, B->px, B->py, B->th, Pb->hx,
+                               Pb->hy, C->margin, &x, &y);
+            *tau = FN(cross2)(x - A->px, y - A->py, *fx, *fy);
+        }
+    }
+}
+
+/* _static_forces_torque (collisions.py:1246-1340) for a box agent: obstacles (each force
+   at its contact point: a circle's point nearest the box, a box's or capsule core's
+   manifold point) and the walls one by one at their support vertices */
+static void FN(box_static_torque)(const FN(ctx_t) *C, const REAL *od, const FN(prm_t) *P,
+                                  const FN(agent_t) *A, REAL dd, REAL *fx_o, REAL *fy_o,
+                                  REAL *tau_o)
+{
+    const REAL hx = P->hx, hy = P->hy, rb = SQRT(hx * hx + hy * hy);
+    REAL fx = 0, fy = 0, tau = 0;
+    FN(dn) s[BX_N];
+    FN(dstate)(A, -1, s);
+    for (int o = 0; o < C->n_obs; ++o) {
+        const REAL *sh = od + 6 * o;
+        int st = C->o_type[o];
+        REAL ro = C->o_rad[o], ohx = C->o_half[o * 2], ohy = C->o_half[o * 2 + 1];
+        if (FN(bounds_apart)(A->px - sh[0], A->py - sh[1], rb + C->margin + FN(shape_bound)(st, ro, ohx, ohy)))
+            continue;
+        FN(dn) cx = FN(dk)(sh[0]), cy = FN(dk)(sh[1]), ang = FN(dk)(sh[2]);
+        FN(dn) vox = FN(dk)(sh[3]), voy = FN(dk)(sh[4]), om = FN(dk)(sh[5]);
+        FN(dn) gx, gy, xx = cx, xy = cy;
+        if (st == 1 || st == 2) {
+            FN(d_obb_force)(C, s[BX_PX], s[BX_PY], s[BX_TH], hx, hy, s[BX_VX], s[BX_VY], s[BX_W],
+                            cx, cy, ang, ohx, st == 1 ? ohy : (REAL)0, vox, voy, om,
+                            st == 1 ? C->margin : ro + C->margin, dd, &gx, &gy, &xx, &xy);
+        } else {
+            FN(dn) hxv, hyv;
+            FN(d_box_force)(C, cx, cy, vox, voy, s[BX_PX], s[BX_PY], s[BX_TH], hx, hy,
+                            ro + C->margin, dd, s[BX_VX], s[BX_VY], s[BX_W], &hxv, &hyv);
+            gx = FN(dneg)(hxv);
+            gy = FN(dneg)(hyv);
+        }
+        REAL fox = gx.v, foy = gy.v, x = xx.v, y = xy.v;
+        if (fox * fox + foy * foy > (REAL)0) {
+            if (st == 0) {
+                REAL k = ro / SQRT(fox * fox + foy * foy);
+                x = x + fox * k;
+                y = y + foy * k;
+            } else {
+                FN(manifold_point)(A->px, A->py, A->th, hx, hy, sh[0], sh[1], sh[2], ohx,
+                                   st == 1 ? ohy : (REAL)0, st == 1 ? C->margin : ro + C->margin,
+                                   &x, &y);
+            }
+        }
+        fx += fox;
+        fy += foy;
+        tau += FN(cross2)(x - A->px, y - A->py, fox, foy);
+    }
+    if (C->soft_walls) {
+        REAL ca = COS(A->th), sa = SIN(A->th);
+        REAL ex = hx * FABS(ca) + hy * FABS(sa), ey = hx * FABS(sa) + hy * FABS(ca);
+        REAL sc = ca > 0 ? (REAL)1 : (ca < 0 ? (REAL)-1 : (REAL)0);
+        REAL ss = sa > 0 ? (REAL)1 : (sa < 0 ? (REAL)-1 : (REAL)0);
+        REAL rl_y = -sc * hx * sa + ss * hy * ca, rb_x = -ss * hx * ca + sc * hy * sa;
+        REAL wx = 0, wy = 0, pen;
+        pen = ex + C->margin - (A->px - C->bmin_x);
+        if (pen > 0) {
+            REAL fl = FN(normal_coeff)(C, pen, A->vx - A->w * rl_y, dd);
+            wx += fl;
+            tau += -rl_y * fl;
+        }
+        pen = ex + C->margin - (C->bmax_x - A->px);
+        if (pen > 0) {
+            REAL fr = -FN(normal_coeff)(C, pen, -(A->vx + A->w * rl_y), dd);
+            wx += fr;
+            tau += rl_y * fr;
+        }
+        pen = ey + C->margin - (A->py - C->bmin_y);
+        if (pen > 0) {
+            REAL fb = FN(normal_coeff)(C, pen, A->vy + A->w * rb_x, dd);
+            wy += fb;
+            tau += rb_x * fb;
+        }
+        pen = ey + C->margin - (C->bmax_y - A->py);
+        if (pen > 0) {
+            REAL ft = -FN(normal_coeff)(C, pen, -(A->vy - A->w * rb_x), dd);
+            wy += ft;
+            tau += -rb_x * ft;
+        }
+        fx += wx;
+        fy += wy;
+    }
+    *fx_o = fx;
+    *fy_o = fy;
+    *tau_o = tau;
+}
+
+/* Torques of the wheel-contact force pass (the forces are forces_env_box's) */
+static void FN(torques_env)(const FN(ctx_t) *C, const REAL *od, const FN(prm_t) *P,
+                            const FN(agent_t) *st, const int32_t *idx, const int32_t *cnt,
+                            REAL *tq)
+{
+    int A = C->n_agents, K = C->max_nbr;
+    for (int a = 0; a < A; ++a) {
+        REAL dd = (REAL)1 + C->c * C->sub_dt / P[a].mass;
+        REAL tau = 0;
+        int n = C->collisions ? cnt[a] : 0;
+        for (int i = 0; i < n; ++i) {
+            int b = idx[a * K + i];
+            REAL fx, fy, tb;
+            FN(pair_force_torque)(C, a, b, P + a, P + b, st + a, st + b, dd, &fx, &fy, &tb);
+            tau += tb;
+        }
+        REAL ts = 0;
+        if (P[a].shape > (REAL)0.5) {
+            REAL fx, fy;
+            FN(box_static_torque)(C, od, P + a, st + a, dd, &fx, &fy, &ts);
+        }
+        tq[a] = tau + ts;
+    }
+}
+
+/* wheel_contact (swarp/dynamics/kernels.py:1328-1387): a diff-drive agent's step output
+   (*out, unclamped) reworked: sideways force only beyond the wheels' grip, the contact
+   torque turning it only beyond turn_cap; other models pass through */
+static void FN(wheel_contact)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *in,
+                              REAL Fx, REAL Fy, REAL torque, FN(agent_t) *out)
+{
+    if (P->tag != 1) return;
+    REAL dt = C->sub_dt, zero = 0;
+    REAL ca = COS(in->th), sa = SIN(in->th);
+    REAL f_lat = -Fx * sa + Fy * ca;
+    REAL slip = FN(rmax)(FABS(f_lat) - C->lat_grip * P->mass, zero);
+    if (f_lat < zero) slip = -slip;
+    REAL dv = (slip - f_lat) * (dt / P->mass);
+    REAL cx = -sa * dv, cy = ca * dv;
+    out->vx = out->vx + cx;
+    out->vy = out->vy + cy;
+    out->px = out->px + cx * dt;
+    out->py = out->py + cy * dt;
+    REAL inertia = P->mass * (P->hx * P->hx + P->hy * P->hy) / (REAL)3;
+    REAL excess = FN(rmax)(FABS(torque) - C->turn_cap, zero);
+    if (torque < zero) excess = -excess;
+    REAL w_drive = out->w;
+    if (torque * out->w < zero && FABS(torque) > C->turn_cap) w_drive = zero;
+    out->th = in->th + (w_drive + excess * (dt / inertia)) * dt;
 }
 
 /* ------------------------------------------------------------ the footprint clamp */

@@ -41,6 +41,8 @@ typedef struct {
     int collisions, soft_walls, needs_forces, n_obs;
     int clamp_bounds; /* 0 off, 1 disc clamp, 2 footprint clamp (a world holding boxes) */
     int boxes;        /* some agent is a box: the box-aware contact pass */
+    int wheel;        /* WorldConfig.wheel_contacts (no-grad Euler 2-D only) */
+    REAL lat_grip, turn_cap;
     /* obstacles: pos [E,N,2], radius [N], type [N], angle [E,N], half [N,2],
        vel [E,N,2], ang_vel [E,N] */
     const REAL *o_pos, *o_rad, *o_ang, *o_half, *o_vel, *o_om;
@@ -551,7 +553,7 @@ static void FN(neighbors_env)(int A, int K, const FN(agent_t) *st, REAL radius,
 static void FN(forces_env)(const FN(ctx_t) *C, const REAL *od, const FN(prm_t) *P,
                            const FN(agent_t) *st, const int32_t *idx, const int32_t *cnt, REAL *F)
 {
-    if (C->boxes) {
+    if (C->boxes || C->wheel) {
         FN(forces_env_box)(C, od, P, st, idx, cnt, F);
         return;
     }
@@ -1673,8 +1675,24 @@ static void FN(step_env)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_
             FN(bodies_env)(C, P, cur, obc, obn);
         else if (N)
             memcpy(obn, obc, sizeof(REAL) * nob);
-        for (int a = 0; a < A; ++a)
-            FN(integrate_agent)(C, P + a, cur + a, act + a * ad, F[a * 2], F[a * 2 + 1], nxt + a);
+        if (C->wheel) {
+            /* contact torques, the unclamped step, wheel_contact, then the clamp */
+            REAL tq[64];
+            FN(ctx_t) C2 = *C;
+            C2.clamp_bounds = 0;
+            if (C->needs_forces && C->collisions + C->n_obs + C->soft_walls > 0)
+                FN(torques_env)(C, obc, P, cur, idx, cnt, tq);
+            else
+                for (int a = 0; a < A; ++a) tq[a] = 0;
+            for (int a = 0; a < A; ++a) {
+                FN(integrate_agent)(&C2, P + a, cur + a, act + a * ad, F[a * 2], F[a * 2 + 1], nxt + a);
+                FN(wheel_contact)(C, P + a, cur + a, F[a * 2], F[a * 2 + 1], tq[a], nxt + a);
+                if (C->clamp_bounds) FN(clamp_position)(C, P + a, nxt[a].th, &nxt[a].px, &nxt[a].py);
+            }
+        } else {
+            for (int a = 0; a < A; ++a)
+                FN(integrate_agent)(C, P + a, cur + a, act + a * ad, F[a * 2], F[a * 2 + 1], nxt + a);
+        }
     }
     memcpy(out, st + S * A, sizeof(FN(agent_t)) * A);
     if (N && ob_out) memcpy(ob_out, ch->ob + S * nob, sizeof(REAL) * nob);
@@ -1752,6 +1770,9 @@ static void FN(make_ctx)(const oracle_cfg_t *cfg, const oracle_obs_t *obs, FN(ct
     C->lin_damping = (REAL)cfg->lin_damping;
     C->ang_damping = (REAL)cfg->ang_damping;
     C->rk4 = cfg->rk4;
+    C->wheel = cfg->wheel;
+    C->lat_grip = (REAL)cfg->lat_grip;
+    C->turn_cap = (REAL)cfg->turn_cap;
     C->n_obs = obs ? obs->n_obstacles : 0;
     C->needs_forces = C->collisions || C->soft_walls || C->n_obs > 0;
     if (C->n_obs > 0) {
@@ -1914,6 +1935,7 @@ int FN(oracle_rollout_adj_ob)(const oracle_cfg_t *cfg, const REAL *params, const
 {
     FN(ctx_t) C;
     FN(make_ctx)(cfg, obs, &C);
+    if (C.wheel) return -3; /* wheel contacts have no reverse mode (the reference's too) */
     int E = C.n_envs, A = C.n_agents, S = C.substeps, K = C.max_nbr, ad = C.act_dim, N = C.n_obs;
     size_t nob = (size_t)OB_W * N;
     FN(prm_t) *P = (FN(prm_t) *)calloc((size_t)A, sizeof(FN(prm_t)));

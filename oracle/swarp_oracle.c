@@ -27,6 +27,8 @@ typedef struct {
     double bmin_x, bmin_y, bmax_x, bmax_y;
     double lin_damping, ang_damping; /* movable bodies' viscous decay rates */
     int rk4;                         /* Integrator.RK4 (2-D models) instead of Euler */
+    int wheel;                       /* WorldConfig.wheel_contacts (forward only) */
+    double lat_grip, turn_cap;       /* wheel_lateral_friction * gravity, wheel_turn_torque */
 } oracle_cfg_t;
 
 typedef struct {

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 F32, F64 = 0, 1
 EULER, RK4 = 0, 1
 
@@ -65,6 +65,9 @@ class SwarpDesc(ctypes.Structure):
         ("ang_damping", ctypes.c_double),
         ("integrator", ctypes.c_int32),
         ("has_boxes", ctypes.c_int32),
+        ("wheel_contacts", ctypes.c_int32),
+        ("lat_grip", ctypes.c_double),
+        ("turn_cap", ctypes.c_double),
     ]
 
 

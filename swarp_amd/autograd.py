@@ -157,6 +157,10 @@ class _RolloutFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, stepper: Stepper, bufs, actions_seq: torch.Tensor, *state0: torch.Tensor):
+        if stepper.world.wheel_contacts:  # swarp/core/stepper.py:852-857
+            raise ValueError(
+                "WorldConfig.wheel_contacts runs on the slim Euler 2D path only (no drone "
+                "agents, untaped, Integrator.EULER)")
         ctx.set_materialize_grads(False)
         T, E = actions_seq.shape[0], actions_seq.shape[1]
         dev = actions_seq.device

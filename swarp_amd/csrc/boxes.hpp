@@ -330,11 +330,13 @@ template <typename T, typename V>
 __device__ __forceinline__ void obb_force(const Cst<T> &C, V cAx, V cAy, V caA, V saA, T hA0,
                                           T hA1, V vAx, V vAy, V wA, V cBx, V cBy, V caB, V saB,
                                           T hB0, T hB1, V vBx, V vBy, V wB, T reach, T dd, V &fx,
-                                          V &fy)
+                                          V &fy, V *xo = nullptr, V *yo = nullptr)
 {
     V s, nx, ny, xx, xy;
     obb_contact(C, cAx, cAy, caA, saA, hA0, hA1, cBx, cBy, caB, saB, hB0, hB1, reach, s, nx, ny,
                 xx, xy);
+    if (xo) *xo = xx;
+    if (yo) *yo = xy;
     fx = V(T(0));
     fy = V(T(0));
     const V ov = V(reach) - s;
@@ -514,6 +516,172 @@ __device__ __forceinline__ void box_static_forces(const Cst<T> &C, const Obs<T> 
     if (omask) *omask = om;
     if (wall) *wall = won;
     if (beyond) *beyond = far;
+}
+
+// ------------------------------------------------------------------ wheel contacts
+// WorldConfig.wheel_contacts (no-grad Euler 2-D path only): the force pass also returns
+// each agent's contact torque about its centre (collision_forces_wheel_kernel,
+// swarp/core/collisions.py:1128-1403), which wheel_contact (swarp/dynamics/kernels.py:
+// 1328-1387) turns into heading change beyond the drive's turn_cap.
+
+template <typename T> __device__ __forceinline__ T cross2(T rx, T ry, T fx, T fy)
+{
+    return rx * fy - ry * fx;
+}
+
+// _box_sd (:1133-1141): signed distance from a point to an oriented box.
+template <typename T>
+__device__ __forceinline__ T box_sd(T vx, T vy, T cx, T cy, T ca, T sa, T h0, T h1)
+{
+    const T dx = vx - cx, dy = vy - cy;
+    const T lx = m_abs(ca * dx + sa * dy) - h0;
+    const T ly = m_abs((-sa) * dx + ca * dy) - h1;
+    const T ox = wmax(lx, T(0)), oy = wmax(ly, T(0));
+    return m_sqrt(ox * ox + oy * oy) + wmin(wmax(lx, ly), T(0));
+}
+
+// _manifold_point (:1144-1185): the in-reach vertices of either box, averaged with their
+// depths as weights; (x, y) is kept when none is in reach.
+template <typename T>
+__device__ __forceinline__ void manifold_point(T cAx, T cAy, T caA, T saA, T hA0, T hA1, T cBx,
+                                               T cBy, T caB, T saB, T hB0, T hB1, T reach, T &x,
+                                               T &y)
+{
+    const T eA0x = caA * hA0, eA0y = saA * hA0, eA1x = (-saA) * hA1, eA1y = caA * hA1;
+    const T eB0x = caB * hB0, eB0y = saB * hB0, eB1x = (-saB) * hB1, eB1y = caB * hB1;
+    T ax = T(0), ay = T(0), ws = T(0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const T sx = (i == 1 || i == 2) ? T(-1) : T(1), sy = i >= 2 ? T(-1) : T(1);
+        const T vax = (cAx + eA0x * sx) + eA1x * sy, vay = (cAy + eA0y * sx) + eA1y * sy;
+        const T da = wmax(reach - box_sd(vax, vay, cBx, cBy, caB, saB, hB0, hB1), T(0));
+        ax += vax * da;
+        ay += vay * da;
+        ws += da;
+        const T vbx = (cBx + eB0x * sx) + eB1x * sy, vby = (cBy + eB0y * sx) + eB1y * sy;
+        const T db = wmax(reach - box_sd(vbx, vby, cAx, cAy, caA, saA, hA0, hA1), T(0));
+        ax += vbx * db;
+        ay += vby * db;
+        ws += db;
+    }
+    if (ws > T(0)) {
+        x = ax / ws;
+        y = ay / ws;
+    }
+}
+
+// Torque about agent a's centre of the pair force (fx, fy) on a (_agent_pair_force_torque,
+// :1188-1243): 0 for a disc a; a box against a disc b at the disc's point nearest to a; a
+// box against a box at the contact's manifold point.
+template <typename T>
+__device__ __forceinline__ T pair_torque(const Cst<T> &C, int a, int b, const Foot<T> &Fa,
+                                         const T (&sa)[6], T caa, T saa, const Foot<T> &Fb,
+                                         const T (&sb)[6], T cab, T sab, T fx, T fy)
+{
+    const T half = T(0.5);
+    if (Fa.shape < half) return T(0);
+    if (Fb.shape < half) {
+        const T fn = m_sqrt(fx * fx + fy * fy);
+        if (!(fn > T(0))) return T(0);
+        const T k = Fb.radius / fn;
+        return cross2((sb[BX_PX] + fx * k) - sa[BX_PX], (sb[BX_PY] + fy * k) - sa[BX_PY], fx, fy);
+    }
+    if (!(fx * fx + fy * fy > T(0))) return T(0);
+    // the contact point obb_force computed (the lower index is box A)
+    T gx, gy, x, y;
+    if (a < b)
+        obb_force(C, sa[BX_PX], sa[BX_PY], caa, saa, Fa.hx, Fa.hy, sa[BX_VX], sa[BX_VY], sa[BX_W],
+                  sb[BX_PX], sb[BX_PY], cab, sab, Fb.hx, Fb.hy, sb[BX_VX], sb[BX_VY], sb[BX_W],
+                  C.margin, T(1), gx, gy, &x, &y);
+    else
+        obb_force(C, sb[BX_PX], sb[BX_PY], cab, sab, Fb.hx, Fb.hy, sb[BX_VX], sb[BX_VY], sb[BX_W],
+                  sa[BX_PX], sa[BX_PY], caa, saa, Fa.hx, Fa.hy, sa[BX_VX], sa[BX_VY], sa[BX_W],
+                  C.margin, T(1), gx, gy, &x, &y);
+    manifold_point(sa[BX_PX], sa[BX_PY], caa, saa, Fa.hx, Fa.hy, sb[BX_PX], sb[BX_PY], cab, sab,
+                   Fb.hx, Fb.hy, C.margin, x, y);
+    return cross2(x - sa[BX_PX], y - sa[BX_PY], fx, fy);
+}
+
+// Torque of a box agent's static contacts about its centre (_static_forces_torque,
+// :1246-1340): each obstacle's force at its point (a circle's point nearest the box, a
+// box's or capsule core's manifold point), each wall's at its support vertex.
+template <typename T>
+__device__ __forceinline__ T box_static_torque(const Cst<T> &C, const Obs<T> &O, size_t eN,
+                                               const T *ocs, T hx, T hy, const T (&s)[6], T ca,
+                                               T sa, T dd)
+{
+    const T ra = m_sqrt(hx * hx + hy * hy);
+    T tau = T(0);
+    for (int o = 0; o < C.N; ++o) {
+        const size_t j = eN + o;
+        if (!box_obstacle_near(C, O, j, o, ra, s[BX_PX], s[BX_PY])) continue;
+        const int st = O.type[o];
+        const T cx = O.pos[2 * j], cy = O.pos[2 * j + 1];
+        const T ro = O.rad[o], ohx = O.half[2 * o], ohy = st == 1 ? O.half[2 * o + 1] : T(0);
+        T oc, os;
+        ob_trig(O, j, o, ocs, oc, os);
+        T fx, fy, x = cx, y = cy;
+        if (st == 1 || st == 2) {
+            obb_force(C, s[BX_PX], s[BX_PY], ca, sa, hx, hy, s[BX_VX], s[BX_VY], s[BX_W], cx, cy,
+                      oc, os, ohx, ohy, O.vel[2 * j], O.vel[2 * j + 1], O.om[j],
+                      st == 1 ? C.margin : ro + C.margin, dd, fx, fy, &x, &y);
+        } else {
+            box_obstacle_v(C, O, j, o, ocs, hx, hy, s, ca, sa, dd, fx, fy);
+        }
+        if (fx * fx + fy * fy > T(0)) {
+            if (st == 0) {
+                const T k = ro / m_sqrt(fx * fx + fy * fy);
+                x = x + fx * k;
+                y = y + fy * k;
+            } else {
+                manifold_point(s[BX_PX], s[BX_PY], ca, sa, hx, hy, cx, cy, oc, os, ohx, ohy,
+                               st == 1 ? C.margin : ro + C.margin, x, y);
+            }
+        }
+        tau += cross2(x - s[BX_PX], y - s[BX_PY], fx, fy);
+    }
+    if (C.soft_walls) {
+        const T ex = hx * m_abs(ca) + hy * m_abs(sa), ey = hx * m_abs(sa) + hy * m_abs(ca);
+        const T sc = ca > T(0) ? T(1) : (ca < T(0) ? T(-1) : T(0));
+        const T ss = sa > T(0) ? T(1) : (sa < T(0) ? T(-1) : T(0));
+        const T rl_y = (-sc * hx) * sa + (ss * hy) * ca, rb_x = (-ss * hx) * ca + (sc * hy) * sa;
+        T pen = (ex + C.margin) - (s[BX_PX] - C.bmin_x);
+        if (pen > T(0)) tau += (-rl_y) * normal_coeff(C, pen, s[BX_VX] - s[BX_W] * rl_y, dd);
+        pen = (ex + C.margin) - (C.bmax_x - s[BX_PX]);
+        if (pen > T(0)) tau += rl_y * (-normal_coeff(C, pen, -(s[BX_VX] + s[BX_W] * rl_y), dd));
+        pen = (ey + C.margin) - (s[BX_PY] - C.bmin_y);
+        if (pen > T(0)) tau += rb_x * normal_coeff(C, pen, s[BX_VY] + s[BX_W] * rb_x, dd);
+        pen = (ey + C.margin) - (C.bmax_y - s[BX_PY]);
+        if (pen > T(0)) tau += (-rb_x) * (-normal_coeff(C, pen, -(s[BX_VY] - s[BX_W] * rb_x), dd));
+    }
+    return tau;
+}
+
+// wheel_contact (swarp/dynamics/kernels.py:1328-1387): a diff-drive agent's unclamped step
+// output `o` from input `in` reworked -- sideways force only beyond the wheels' grip, the
+// contact torque turning it only beyond turn_cap; other models pass through.
+template <typename T>
+__device__ __forceinline__ void wheel_contact(const Cst<T> &C, const Prm<T> &P, const St<T> &in,
+                                              T Fx, T Fy, T torque, St<T> &o)
+{
+    if (P.tag != 1) return;
+    const T dt = C.sub_dt, zero = T(0);
+    const T ca = m_cos(in.th), sa = m_sin(in.th);
+    const T f_lat = (-Fx) * sa + Fy * ca;
+    T slip = wmax(m_abs(f_lat) - C.lat_grip * P.mass, zero);
+    if (f_lat < zero) slip = -slip;
+    const T dv = (slip - f_lat) * (dt / P.mass);
+    const T cx = (-sa) * dv, cy = ca * dv;
+    o.vx = o.vx + cx;
+    o.vy = o.vy + cy;
+    o.px = o.px + cx * dt;
+    o.py = o.py + cy * dt;
+    const T inertia = P.mass * (P.hx * P.hx + P.hy * P.hy) / T(3);
+    T excess = wmax(m_abs(torque) - C.turn_cap, zero);
+    if (torque < zero) excess = -excess;
+    T w_drive = o.w;
+    if (torque * o.w < zero && m_abs(torque) > C.turn_cap) w_drive = zero;
+    o.th = in.th + (w_drive + excess * (dt / inertia)) * dt;
 }
 
 // ------------------------------------------------------------------ reverse helpers

@@ -70,6 +70,8 @@ template <typename T> struct Cst {
     int collisions, soft_walls, needs_forces, use_skin;
     int clamp;     // 0 off, 1 disc clamp, 2 footprint clamp (a world holding box agents)
     int boxes;     // some agent is a box: the box-aware contact pass
+    int wheel;     // WorldConfig.wheel_contacts: contact torques + wheel_contact (no grad)
+    T lat_grip, turn_cap;
     int fast_div;  // neighbour radius <= 2^20: contact distances are short-division divisors
     int rk4;       // Integrator.RK4 instead of semi-implicit Euler
 };

@@ -287,7 +287,7 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
     const St<T> &st, int s, bool full, typename MaskT<PA>::type &cand, T &Fx, T &Fy,
     const T *ocs = nullptr, const T *lbx = nullptr, const T *lcs = nullptr,
     typename MaskT<PA>::type *act = nullptr, uint64_t *om = nullptr, bool *wall = nullptr,
-    bool *beyond = nullptr)
+    bool *beyond = nullptr, T *tq = nullptr)
 {
     const bool box_me = BOXES && L.pr.shape > T(0.5);
     T me[6] = {st.px, st.py, st.th, st.vx, st.vy, st.w};
@@ -297,6 +297,8 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
         sme = lcs[64 + L.lane];
     }
     typename MaskT<PA>::type am = 0;
+    const bool wheel = BOXES && tq != nullptr;  // contact torques (wheel contacts)
+    T tau = T(0);
     typedef typename MaskT<PA>::type M;
     const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64, *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
     M incl = 0;
@@ -325,6 +327,9 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
                 agent_pair_force_box<T, T>(C, L.agent, b, fa, me, cme, sme, fb, ob, lcs[j],
                                            lcs[64 + j], L.dd, gx, gy);
                 if (gx != T(0) || gy != T(0)) am |= typename MaskT<PA>::type(1) << b;
+                if (wheel)
+                    tau += pair_torque(C, L.agent, b, fa, me, cme, sme, fb, ob, lcs[j], lcs[64 + j],
+                                       gx, gy);
             } else {
                 pair_force(C, st.px - lx[j], st.py - ly[j], st.vx - lvx[j], st.vy - lvy[j],
                            ra + lr[j] + C.margin, L.dd, gx, gy);
@@ -339,6 +344,8 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
         box_static_forces<T, T>(C, g.obs, eN, ocs, L.pr.hx, L.pr.hy, me, cme, sme, L.dd, sx, sy,
                                 om, wall, beyond);
+        if (wheel)
+            tau = tau + box_static_torque(C, g.obs, eN, ocs, L.pr.hx, L.pr.hy, me, cme, sme, L.dd);
     } else if (C.N > 0) {
         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
         for (int o = 0; o < C.N; ++o) {
@@ -359,6 +366,7 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
     Fx = fx + sx;
     Fy = fy + sy;
     if (act) *act = am;
+    if (wheel) *tq = tau;
     return incl;
 }
 
@@ -393,7 +401,7 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> C, const Args<T
         T D = T(0);
         bool ok = false;
         for (int s = 0; s < C.S; ++s) {
-            T Fx = T(0), Fy = T(0);
+            T Fx = T(0), Fy = T(0), Tq = T(0);
             if (C.needs_forces) {
                 if (C.collisions) {
                     __syncthreads();
@@ -413,10 +421,21 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> C, const Args<T
                 }
                 if (C.collisions || BOXES) __syncthreads();
                 forces<T, PA, BOXES>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy, ocs, lbx,
-                                     lcs);
+                                     lcs, nullptr, nullptr, nullptr, nullptr,
+                                     BOXES && C.wheel ? &Tq : nullptr);
             }
             St<T> nx;
-            integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
+            if (BOXES && C.wheel) {
+                // the unclamped step, wheel_contact, then the clamp (integrate2d_wheel_kernel,
+                // swarp/dynamics/kernels.py:1389-1478)
+                Cst<T> C0 = C;
+                C0.clamp = 0;
+                integrate<T, DRONE>(C0, L.pr, st, a, Fx, Fy, nx);
+                wheel_contact(C, L.pr, st, Fx, Fy, Tq, nx);
+                if (C.clamp) clamp_position(C, L.pr, nx.th, nx.px, nx.py);
+            } else {
+                integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
+            }
             if (C.use_skin) {
                 D += (m_abs(nx.px - st.px) + m_abs(nx.py - st.py)) * T(1.0001);
                 ok = env_all<PA>(!L.real || D <= C.half_margin, L.base);
@@ -873,6 +892,9 @@ template <typename T> static int fill_cst(const swarp_desc_t *d, double skin, Cs
     C.soft_walls = d->soft_walls;
     C.clamp = d->clamp_bounds;
     C.boxes = d->has_boxes ? 1 : 0;
+    C.wheel = d->wheel_contacts ? 1 : 0;
+    C.lat_grip = (T)d->lat_grip;
+    C.turn_cap = (T)d->turn_cap;
     C.needs_forces = (d->collisions || d->soft_walls || d->n_obstacles > 0) ? 1 : 0;
     C.use_skin = (d->collisions && d->substeps > 1 && skin > 0.0) ? 1 : 0;
     // contact distances lie in [sqrt(eps2), neighbour radius]: within the range of the
@@ -899,6 +921,8 @@ static int check_desc(const swarp_desc_t *d, bool need_params = true)
     if (d->clamp_bounds == 2 && !d->has_boxes)
         return fail("the footprint clamp (clamp_bounds 2) is for worlds holding box agents");
     if (d->has_boxes && d->has_drone) return fail("a drone cannot be a box agent");
+    if (d->wheel_contacts && (d->has_drone || d->integrator != SWARP_EULER))
+        return fail("wheel contacts run on the Euler 2-D path only (no drones, no RK4)");
     if (need_params && (!d->params || !d->model_tag || !d->ctrl_mode))
         return fail("params/model_tag/ctrl_mode must be set");
     if (d->n_obstacles > 0 && (!d->obs_pos || !d->obs_radius || !d->obs_angle || !d->obs_half ||
@@ -985,7 +1009,7 @@ static void launch_bwd(int PA, const Cst<T> &C, const Args<T> &a, size_t shm, hi
 static bool lean_ok(const swarp_desc_t *d)
 {
     return d->holo_velocity_only && !d->has_drone && d->n_obstacles == 0 && !d->clamp_bounds &&
-           d->integrator == SWARP_EULER && !d->has_boxes;
+           d->integrator == SWARP_EULER && !d->has_boxes && !d->wheel_contacts;
 }
 
 // Byte offsets of the tape regions (see lean.hpp); total == 0: no tape.
@@ -1092,7 +1116,7 @@ static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
             launch_holo_fwd<T, false>(PA, C, a, tape_ptrs<T>(TL, nullptr), st);
     else if (d->has_drone)
         launch_fwd<T, true, false>(PA, C, a, st);
-    else if (d->has_boxes)
+    else if (d->has_boxes || d->wheel_contacts)
         launch_fwd<T, false, true>(PA, C, a, st);
     else
         launch_fwd<T, false, false>(PA, C, a, st);
@@ -1331,7 +1355,8 @@ int swarp_rollout_fwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
     g_err[0] = 0;
     if (check_desc(desc)) return -1;
     if (T < 1) return fail("T must be >= 1");
-    if (desc->has_boxes) return fail("box agents with movable bodies are not supported in this build");
+    if (desc->has_boxes || desc->wheel_contacts)
+        return fail("box agents and wheel contacts with movable bodies are not supported in this build");
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
         return rollout_fwd_ob<float>(desc, T, state0, ob0, actions, traj, final_state, ob_traj, st);
@@ -1348,7 +1373,8 @@ int swarp_rollout_bwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
     g_err[0] = 0;
     if (check_desc(desc)) return -1;
     if (T < 1) return fail("T must be >= 1");
-    if (desc->has_boxes) return fail("box agents with movable bodies are not supported in this build");
+    if (desc->has_boxes || desc->wheel_contacts)
+        return fail("box agents and wheel contacts with movable bodies are not supported in this build");
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
         return rollout_bwd_ob<float>(desc, T, state0, ob0, actions, traj, ob_traj, adj_traj,
@@ -1405,6 +1431,8 @@ int swarp_rollout_bwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *
     g_err[0] = 0;
     if (check_desc(desc)) return -1;
     if (T < 1) return fail("T must be >= 1");
+    if (desc->wheel_contacts)
+        return fail("wheel contacts have no reverse pass (the reference runs them untaped only)");
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
         return rollout_bwd<float>(desc, T, state0, actions, traj, adj_traj, adj_final, adj_state0,
@@ -1423,6 +1451,8 @@ int swarp_rollout_bwd_tape(const swarp_desc_t *desc, int32_t T, const swarp_stat
     if (check_desc(desc)) return -1;
     if (T < 1) return fail("T must be >= 1");
     if (!tape && tape_bytes) return fail("tape is NULL");
+    if (desc->wheel_contacts)
+        return fail("wheel contacts have no reverse pass (the reference runs them untaped only)");
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
         return rollout_bwd<float>(desc, T, state0, actions, traj, adj_traj, adj_final, adj_state0,

@@ -160,8 +160,12 @@ class Stepper:
         if self.n_agents > 64:
             raise NotImplementedError("this build steps at most 64 agents per env")
         w = self.world
-        if w.wheel_contacts:
-            raise NotImplementedError("WorldConfig.wheel_contacts is not implemented")
+        drone = any(c.model == DynamicsModel.DRONE for c in self.configs)
+        if w.wheel_contacts and (drone or w.integrator.value != "euler"):
+            # swarp/core/stepper.py:852-857
+            raise ValueError(
+                "WorldConfig.wheel_contacts runs on the slim Euler 2D path only (no drone "
+                "agents, untaped, Integrator.EULER)")
         if w.neighbor_method not in ("auto", "brute"):
             raise NotImplementedError(
                 f"neighbor_method={w.neighbor_method!r}: this build implements the brute-force "
@@ -277,9 +281,12 @@ class Stepper:
         d.clamp_bounds = (2 if self.has_boxes else 1) if self._clamp else 0
         d.has_drone = int(self.has_drone)
         d.has_boxes = int(self.has_boxes)
+        d.wheel_contacts = int(self.world.wheel_contacts)
+        d.lat_grip = float(self.world.wheel_lateral_friction * self.world.gravity)
+        d.turn_cap = float(self.world.wheel_turn_torque)
         d.holo_velocity_only = int(self.use_specialised and self.holo_velocity_only
                                    and self.n_obstacles == 0 and not self._clamp
-                                   and not self.has_boxes)
+                                   and not self.has_boxes and not self.world.wheel_contacts)
         d.dt = float(self.dt)
         d.k = float(self.world.collision_k)
         d.c = float(self.world.collision_c)

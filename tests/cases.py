@@ -48,6 +48,9 @@ def oracle_cfg(configs, world: WorldConfig, dt, substeps, n_envs, act_dim, n_thr
         lin_damping=world.obstacle_linear_damping,
         ang_damping=world.obstacle_angular_damping,
         rk4=int(world.integrator.value == "rk4"),
+        wheel=int(world.wheel_contacts),
+        lat_grip=world.wheel_lateral_friction * world.gravity,
+        turn_cap=world.wheel_turn_torque,
     )
 
 

@@ -137,3 +137,50 @@ def test_sixty_four_box_agents():
     acts = rng.uniform(-1, 1, size=(T, E, A, 2))
     w = _cotangent(T, E, A, 6, scale=0.1)
     _check_box("64 boxes", cfgs, world, S, s0, acts, w)
+
+
+def test_wheel_contacts_forward_and_no_reverse():
+    """WorldConfig.wheel_contacts: contact torques (pair torques at the manifold point or
+    the disc's nearest point, obstacle and wall torques) and wheel_contact's rework of the
+    diff-drive step, forward only (collisions.py:1128-1403, kernels.py:1328-1478): states
+    within 1e-10 of the fp64 oracle, 1e-5 of the fp32 one; a differentiated rollout raises
+    as the reference's taped path does (swarp/core/stepper.py:852-857)."""
+    from hip_helpers import state_to16, to_torch_state
+    from oracle.oracle import Oracle
+    from cases import obstacles_np, oracle_cfg, params_of
+    from swarp_amd import rollout
+
+    E, A, T, S = 40, 9, 8, 2
+    rng = np.random.default_rng(35)
+    cfgs = ([AgentConfig(radius=0.05, max_speed=2.0, max_accel=4.0) for _ in range(3)]
+            + [_box(0.07, 0.04, DynamicsModel.DIFF_DRIVE, ctrl_mode=ControlMode.ACCELERATION)
+               for _ in range(6)])
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02,
+                        bounds=(-0.5, 0.5, -0.5, 0.5), max_neighbors=8, wheel_contacts=True,
+                        wheel_lateral_friction=0.3, wheel_turn_torque=0.02)
+    obs = _obstacles(E, rng)
+    s0 = _state(E, A, rng, 0.4, np.float64)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2))
+    for dt_np, td, tol in ((np.float64, torch.float64, 1e-10), (np.float32, torch.float32, 1e-5)):
+        st = make_stepper(cfgs, world, 0.05, S, td, obs=obs, n_envs=E)
+        state = to_torch_state(s0.astype(dt_np), td, False, 5)
+        a = torch.tensor(acts.astype(dt_np), dtype=td, device="cuda")
+        with torch.no_grad():
+            _, traj = rollout(st, state, a)
+        hs = np.stack([state_to16(x) for x in traj])
+        cfg = oracle_cfg(cfgs, world, 0.05, S, E, 2)
+        p, t, m = params_of(cfgs)
+        os_ = Oracle(dt_np).rollout(cfg, p, t, m, obstacles_np(obs, E), s0.astype(dt_np),
+                                    acts.astype(dt_np))
+        assert np.isfinite(hs).all()
+        assert rel(hs[..., :7], os_[..., :7]) <= tol, f"{np.dtype(dt_np).name} states"
+    # the wheel rework changes the trajectory (the parity above is not vacuous)
+    plain = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02,
+                        bounds=(-0.5, 0.5, -0.5, 0.5), max_neighbors=8)
+    cfg = oracle_cfg(cfgs, plain, 0.05, S, E, 2)
+    ref = Oracle(np.float64).rollout(cfg, p, t, m, obstacles_np(obs, E), s0, acts)
+    assert rel(ref[..., :7], os_[..., :7].astype(np.float64)) > 1e-3
+    st = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
+    state = to_torch_state(s0.astype(np.float32), torch.float32, True, 5)
+    with pytest.raises(ValueError, match="wheel_contacts"):
+        rollout(st, state, torch.zeros(T, E, A, 2, device="cuda", requires_grad=True))

@@ -175,8 +175,16 @@ def test_stepper_reach_check_and_unsupported_features():
     assert bx.has_boxes and d.has_boxes == 1 and d.clamp_bounds == 2 and d.holo_velocity_only == 0
     assert Stepper(cfgs, device="cpu", world=WorldConfig(bounds=(-1, 1, -1, 1),
                                                          bounds_mode="clamp")).desc(2, 2).clamp_bounds == 1
-    with pytest.raises(NotImplementedError, match="wheel_contacts"):
-        Stepper(cfgs, device="cpu", world=WorldConfig(wheel_contacts=True))
+    # wheel contacts: Euler 2-D fleets only (swarp/core/stepper.py:852-857)
+    wd = Stepper(cfgs, device="cpu", world=WorldConfig(wheel_contacts=True, wheel_turn_torque=0.1,
+                                                       wheel_lateral_friction=0.5)).desc(2, 2)
+    assert wd.wheel_contacts == 1 and wd.holo_velocity_only == 0
+    assert math.isclose(wd.lat_grip, 0.5 * 9.81) and math.isclose(wd.turn_cap, 0.1)
+    with pytest.raises(ValueError, match="wheel_contacts"):
+        Stepper(cfgs, device="cpu", world=WorldConfig(wheel_contacts=True, integrator=Integrator.RK4))
+    with pytest.raises(ValueError, match="wheel_contacts"):
+        Stepper([AgentConfig(model=DynamicsModel.DRONE)], device="cpu",
+                world=WorldConfig(wheel_contacts=True))
     st = Stepper(cfgs, dt=0.1, substeps=4, device="cpu", world=WorldConfig())
     assert math.isclose(st.sub_dt, 0.025)
     assert math.isclose(st.neighbor_radius, 2 * 0.2 + 0.02)

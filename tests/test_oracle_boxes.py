@@ -341,3 +341,61 @@ def test_fd_footprint_clamp():
     th = tr[-1, 0, 0, 2]
     ex = 0.15 * abs(math.cos(th)) + 0.05 * abs(math.sin(th))
     assert tr[-1, 0, 0, 0] == pytest.approx(0.4 - ex, abs=1e-15)
+
+
+# ------------------------------------------------------------------ wheel contacts
+
+def _wheel_step(cfgs, world, s0, acts, dt=0.1, obs=None):
+    cfg = oracle_cfg(cfgs, world, dt, 1, s0.shape[0], 2)
+    p, t, m = params_of(cfgs)
+    return O.rollout(cfg, p, t, m, obstacles_np(obs, s0.shape[0]), s0, acts)
+
+
+def test_wheel_contacts_grip_and_turn():
+    """wheel_contact (swarp/dynamics/kernels.py:1328-1387) on a diff-drive box at heading 0
+    under a circle obstacle pressing down on the right end of its top face: the force is
+    (0, -f) with f = k * depth, applied at the circle's point nearest the box (0.15, 0.09),
+    so the torque about the centre is -0.15 f.  Sideways the box moves only by what
+    exceeds the grip mu g m; the heading turns by (|tau| - turn_cap)+ dt / I with
+    I = m (hx^2 + hy^2) / 3."""
+    cfgs = [_box(0.2, 0.1, model=DynamicsModel.DIFF_DRIVE)]
+    circle = {"pos": [[[0.15, 0.19]]], "radius": [0.1], "type": [0]}
+    s0 = pack_state({"pos": [[[0.0, 0.0]]]})
+    acts = np.zeros((1, 1, 1, 2))
+    dt = 0.1
+    f = K * (0.1 + M - 0.09)
+    for mu, cap in ((0.2, 0.0), (10.0, 0.0), (0.2, 0.2)):
+        w = _world(collisions=False, wheel_contacts=True, wheel_lateral_friction=mu,
+                   wheel_turn_torque=cap)
+        tr = _wheel_step(cfgs, w, s0, acts, dt, circle)[0, 0, 0]
+        grip = mu * 9.81
+        vy = -max(f - grip, 0.0) * dt   # the slip beyond the grip (mass 1)
+        assert tr[4] == pytest.approx(vy, abs=1e-12) and tr[1] == pytest.approx(vy * dt, abs=1e-13)
+        tau, inertia = -0.15 * f, (0.2 ** 2 + 0.1 ** 2) / 3.0
+        excess = -max(abs(tau) - cap, 0.0)
+        assert tr[2] == pytest.approx(excess * dt / inertia * dt, rel=1e-12, abs=1e-15)
+    # without wheel contacts the same push moves it sideways by the whole force, no turn
+    tr = _wheel_step(cfgs, _world(collisions=False), s0, acts, dt, circle)[0, 0, 0]
+    assert tr[4] == pytest.approx(-f * dt, rel=1e-12) and tr[2] == 0.0
+
+
+def test_wheel_contacts_symmetric_push_has_no_torque():
+    """Two aligned boxes face to face on one axis: the manifold point lies on the centre
+    line, so the contact torque and the heading change are zero."""
+    cfgs = [_box(0.2, 0.1, model=DynamicsModel.DIFF_DRIVE) for _ in range(2)]
+    w = _world(wheel_contacts=True)
+    s0 = pack_state({"pos": [[[0.0, 0.0], [0.38, 0.0]]]})
+    tr = _wheel_step(cfgs, w, s0, np.zeros((1, 1, 2, 2)))[0, 0]
+    assert tr[0, 2] == 0.0 and tr[1, 2] == 0.0 and tr[0, 0] < 0.0 < tr[1, 0]
+
+
+def test_wheel_contacts_have_no_reverse_mode():
+    cfgs = [_box(0.2, 0.1, model=DynamicsModel.DIFF_DRIVE)]
+    w = _world(collisions=False, wheel_contacts=True)
+    cfg = oracle_cfg(cfgs, w, 0.1, 1, 1, 2)
+    p, t, m = params_of(cfgs)
+    s0 = pack_state({"pos": [[[0.0, 0.0]]]})
+    acts = np.zeros((1, 1, 1, 2))
+    tr = O.rollout(cfg, p, t, m, None, s0, acts)
+    with pytest.raises(RuntimeError):
+        O.rollout_adj(cfg, p, t, m, None, s0, acts, tr, np.ones_like(tr), None)
