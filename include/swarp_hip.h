@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 7
+#define SWARP_ABI_VERSION 8
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -82,6 +82,11 @@ typedef struct swarp_desc {
        swarp_rollout_bwd rejects it. */
     int32_t wheel_contacts;
     double lat_grip, turn_cap;
+    /* 1: `params` is [n_envs, n_agents, 22], one row per (env, agent) -- the per-env
+       override of Stepper.set_agent_params_per_env (swarp/core/stepper.py:493-575,
+       the reference's *_per_env kernel variants); 0: [n_agents, 22] shared by every env.
+       The _ob (movable-body) entry points reject it. */
+    int32_t params_per_env;
 } swarp_desc_t;
 
 /* The nine state fields.  A NULL field means "not provided": an input adjoint that

@@ -25,6 +25,7 @@ from .config import (
     action_bounds,
     action_dim,
     drone_config,
+    per_env_float_template,
 )
 from .environment import Environment, make
 from .neighbors import NeighborGrid
@@ -35,7 +36,7 @@ from .world import World
 __all__ = [
     "AgentConfig", "AgentParams", "AgentShape", "ControlMode", "DynamicsModel", "Environment",
     "GradRing", "Integrator", "MODEL_ACTION_DIM", "NUM_PARAMS", "NavigationScenario",
-    "NeighborGrid", "ObstacleKind", "ObstacleShape", "Obstacles", "PARAM_FIELDS", "SCENARIOS",
+    "NeighborGrid", "ObstacleKind", "per_env_float_template", "ObstacleShape", "Obstacles", "PARAM_FIELDS", "SCENARIOS",
     "Scenario", "StepGradSlot", "Stepper", "TorchState", "World", "WorldConfig",
     "action_bounds", "action_dim", "build_agent_params", "drone_config", "fill_state_defaults",
     "make", "make_scenario", "rollout", "warp_step",

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 F32, F64 = 0, 1
 EULER, RK4 = 0, 1
 
@@ -68,6 +68,7 @@ class SwarpDesc(ctypes.Structure):
         ("wheel_contacts", ctypes.c_int32),
         ("lat_grip", ctypes.c_double),
         ("turn_cap", ctypes.c_double),
+        ("params_per_env", ctypes.c_int32),
     ]
 
 

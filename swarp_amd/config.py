@@ -13,8 +13,8 @@ types so a caller's configuration code carries over unchanged:
 * ``drone_config`` follows ``swarp/dynamics/drone.py:24-53``.
 
 What the MI355X build does not run is rejected loudly rather than silently
-approximated: ``ControlMode.SERVO``, wheel contacts, per-env parameter tables, box
-agents together with movable bodies and more than 64 agents per env raise
+approximated: ``ControlMode.SERVO``, box agents / wheel contacts / per-env parameter
+tables together with movable bodies and more than 64 agents per env raise
 ``NotImplementedError`` when a ``Stepper`` is built with them (or the bodies installed).
 """
 
@@ -231,6 +231,17 @@ class AgentConfig:
         if row["min_speed"] is None:
             row["min_speed"] = -self.max_speed
         return [float(row[name]) for name in PARAM_FIELDS]
+
+
+def per_env_float_template(configs: list[AgentConfig], n_envs: int):
+    """A ``[n_envs, n_agents, NUM_PARAMS]`` float64 array pre-filled from ``configs``
+    (``swarp/dynamics/base.py:369-377``): every env starts as a copy of the shared rows;
+    edit columns (e.g. ``[..., P_MASS]``) to randomize, then hand the result to
+    ``Stepper.set_agent_params_per_env``."""
+    import numpy as np
+
+    rows = np.array([c.to_row() for c in configs], dtype=np.float64)
+    return np.broadcast_to(rows, (n_envs, *rows.shape)).copy()
 
 
 #: Per-slot action limits each model clamps against (``swarp/dynamics/base.py:294-331``).

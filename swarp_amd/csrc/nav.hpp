@@ -73,7 +73,9 @@ __global__ __launch_bounds__(64) void k_nav(const Cst<T> C, const NavArgs<T> g)
         vx = g.vel[2 * i];
         vy = g.vel[2 * i + 1];
     }
-    const T ra = g.params[(real ? agent : 0) * 22];  // P_RADIUS, the static radius
+    // P_RADIUS, the static radius (per env with per-env parameter tables)
+    const T ra = g.params[((C.per_env ? (size_t)(env < C.E ? env : 0) * C.A : 0) +
+                           (real ? agent : 0)) * 22];
     lx[lane] = px;
     ly[lane] = py;
     lvx[lane] = vx;

@@ -137,9 +137,9 @@ __device__ __forceinline__ void store_adj(T *const *f, size_t j, const St<T> &g)
 }
 
 template <typename T>
-__device__ __forceinline__ void load_prm(const Args<T> &g, int a, Prm<T> &p)
+__device__ __forceinline__ void load_prm(const Args<T> &g, size_t row, int a, Prm<T> &p)
 {
-    const T *r = g.params + a * 22;
+    const T *r = g.params + row * 22;
     p.radius = r[0]; p.mass = r[1]; p.max_speed = r[2]; p.max_accel = r[3];
     p.max_ang_vel = r[4]; p.max_ang_accel = r[5]; p.l_f = r[6]; p.l_r = r[7];
     p.max_steer = r[8]; p.thrust_max = r[9]; p.arm = r[10]; p.ixx = r[11];
@@ -239,7 +239,8 @@ __device__ __forceinline__ void lane_init(const Cst<T> &C, const Args<T> &g, Lan
     const int ag = L.real ? L.agent : 0;
     const int ev = L.env < C.E ? L.env : 0;
     L.idx = (size_t)ev * C.A + ag;
-    load_prm(g, ag, L.pr);
+    // per-env parameter tables (Stepper.set_agent_params_per_env) index [env, agent]
+    load_prm(g, C.per_env ? (size_t)ev * C.A + ag : (size_t)ag, ag, L.pr);
     L.dd = T(1) + C.c * C.sub_dt / L.pr.mass;
     L.inv_dd = T(1) / L.dd;
     L.ddv = divisor(L.dd, true);
@@ -892,6 +893,7 @@ template <typename T> static int fill_cst(const swarp_desc_t *d, double skin, Cs
     C.soft_walls = d->soft_walls;
     C.clamp = d->clamp_bounds;
     C.boxes = d->has_boxes ? 1 : 0;
+    C.per_env = d->params_per_env ? 1 : 0;
     C.wheel = d->wheel_contacts ? 1 : 0;
     C.lat_grip = (T)d->lat_grip;
     C.turn_cap = (T)d->turn_cap;
@@ -1009,7 +1011,8 @@ static void launch_bwd(int PA, const Cst<T> &C, const Args<T> &a, size_t shm, hi
 static bool lean_ok(const swarp_desc_t *d)
 {
     return d->holo_velocity_only && !d->has_drone && d->n_obstacles == 0 && !d->clamp_bounds &&
-           d->integrator == SWARP_EULER && !d->has_boxes && !d->wheel_contacts;
+           d->integrator == SWARP_EULER && !d->has_boxes && !d->wheel_contacts &&
+           !d->params_per_env;
 }
 
 // Byte offsets of the tape regions (see lean.hpp); total == 0: no tape.
@@ -1355,8 +1358,9 @@ int swarp_rollout_fwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
     g_err[0] = 0;
     if (check_desc(desc)) return -1;
     if (T < 1) return fail("T must be >= 1");
-    if (desc->has_boxes || desc->wheel_contacts)
-        return fail("box agents and wheel contacts with movable bodies are not supported in this build");
+    if (desc->has_boxes || desc->wheel_contacts || desc->params_per_env)
+        return fail("box agents, wheel contacts and per-env parameters with movable bodies are "
+                    "not supported in this build");
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
         return rollout_fwd_ob<float>(desc, T, state0, ob0, actions, traj, final_state, ob_traj, st);
@@ -1373,8 +1377,9 @@ int swarp_rollout_bwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
     g_err[0] = 0;
     if (check_desc(desc)) return -1;
     if (T < 1) return fail("T must be >= 1");
-    if (desc->has_boxes || desc->wheel_contacts)
-        return fail("box agents and wheel contacts with movable bodies are not supported in this build");
+    if (desc->has_boxes || desc->wheel_contacts || desc->params_per_env)
+        return fail("box agents, wheel contacts and per-env parameters with movable bodies are "
+                    "not supported in this build");
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
         return rollout_bwd_ob<float>(desc, T, state0, ob0, actions, traj, ob_traj, adj_traj,

@@ -22,6 +22,9 @@ from .config import (
     AgentShape,
     ControlMode,
     DynamicsModel,
+    NUM_PARAMS,
+    P_RADIUS,
+    P_SHAPE,
     Integrator,
     ObstacleKind,
     Obstacles,
@@ -104,6 +107,8 @@ class Stepper:
         self.world = world
         self._check_supported()
         self.params = build_agent_params(configs, self.device, self.dtype)
+        #: per-env parameter override [n_envs, n_agents, NUM_PARAMS] (None: shared rows)
+        self.params_per_env: torch.Tensor | None = None
         self.act_dim = max(action_dim(c.model) for c in configs)
         self.has_drone = any(c.model == DynamicsModel.DRONE for c in configs)
         #: a box agent selects the box-aware contact pass and the footprint clamp
@@ -174,6 +179,48 @@ class Stepper:
         for c in self.configs:
             if c.ctrl_mode == ControlMode.SERVO:
                 raise NotImplementedError("ControlMode.SERVO is not implemented")
+
+    # ------------------------------------------------------- per-env parameters
+
+    def set_agent_params_per_env(self, floats) -> None:
+        """Install a per-env parameter table ``[n_envs, n_agents, NUM_PARAMS]`` (domain
+        randomization; columns in ``AgentConfig.to_row()`` order, see
+        ``per_env_float_template``).  Counterpart of
+        ``swarp/core/stepper.py:493-575``: the shape is checked, the ``P_SHAPE`` column
+        must equal the configs' (a footprint is structural), and with collisions the
+        largest per-env radius must fit the neighbour radius; those two host reads run
+        only on a first install or a reallocation.  Refreshing an installed table with a
+        device tensor of the same shape and dtype is an in-place copy with no host read
+        (the per-reset re-randomization path), trusted against the bound checked then."""
+        is_torch = torch.is_tensor(floats)
+        shape = tuple(floats.shape)
+        if len(shape) != 3 or shape[1:] != (self.n_agents, NUM_PARAMS):
+            raise ValueError(
+                f"per-env params must have shape [n_envs, n_agents={self.n_agents}, "
+                f"NUM_PARAMS={NUM_PARAMS}]; got {shape}")
+        cur = self.params_per_env
+        if (is_torch and cur is not None and tuple(cur.shape) == shape
+                and floats.dtype == self.dtype and floats.device == cur.device):
+            cur.copy_(floats)
+            return
+        t = torch.as_tensor(floats, dtype=torch.float64).to("cpu")
+        shared = torch.tensor([float(c.shape) for c in self.configs], dtype=torch.float64)
+        if not torch.equal(t[..., P_SHAPE], shared.expand(shape[0], -1)):
+            raise ValueError("per-env params must not change the P_SHAPE column: an agent's "
+                             "AgentShape is structural and fixed by its AgentConfig.")
+        if self.collisions:
+            max_r = float(t[..., P_RADIUS].max())
+            reach = 2.0 * max_r + self.world.collision_margin
+            if self.neighbor_radius < reach:
+                raise ValueError(
+                    f"per-env radius up to {max_r} needs neighbor_radius >= {reach} "
+                    f"(= 2 * max per-env radius + margin), but neighbor_radius="
+                    f"{self.neighbor_radius}; set WorldConfig.neighbor_radius accordingly.")
+        first = cur is None
+        self.params_per_env = t.to(device=self.device, dtype=self.dtype).contiguous()
+        self._descs.clear()
+        if first:
+            self.mutation_version += 1
 
     # --------------------------------------------------------------- obstacles
 
@@ -296,7 +343,15 @@ class Stepper:
         bx0, by0, bx1, by1 = self._bounds
         d.bounds_min[0], d.bounds_min[1] = bx0, by0
         d.bounds_max[0], d.bounds_max[1] = bx1, by1
-        d.params = self.params.floats.data_ptr()
+        if self.params_per_env is not None:
+            if self.params_per_env.shape[0] != n_envs:
+                raise ValueError(
+                    f"per-env params were installed for {self.params_per_env.shape[0]} envs, "
+                    f"stepping {n_envs}")
+            d.params = self.params_per_env.data_ptr()
+            d.params_per_env = 1
+        else:
+            d.params = self.params.floats.data_ptr()
         d.model_tag = self.params.model_tag.data_ptr()
         d.ctrl_mode = self.params.ctrl_mode.data_ptr()
         if self.n_obstacles > 0:

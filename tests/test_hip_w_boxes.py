@@ -184,3 +184,49 @@ def test_wheel_contacts_forward_and_no_reverse():
     state = to_torch_state(s0.astype(np.float32), torch.float32, True, 5)
     with pytest.raises(ValueError, match="wheel_contacts"):
         rollout(st, state, torch.zeros(T, E, A, 2, device="cuda", requires_grad=True))
+
+
+def test_per_env_parameter_tables():
+    """Stepper.set_agent_params_per_env (swarp/core/stepper.py:493-575; the *_per_env
+    kernels): masses, radii, speed and turn limits randomized per env.  Each env of the HIP
+    rollout equals an independent oracle rollout with that env's rows (states and
+    gradients, fp64 1e-10 / 1e-8), with box and disc agents, obstacles and walls."""
+    from swarp_amd import per_env_float_template
+    from swarp_amd.config import P_MASS, P_MAX_ANG_VEL, P_MAX_SPEED, P_RADIUS
+
+    E, A, T, S = 12, 6, 5, 2
+    rng = np.random.default_rng(36)
+    cfgs = ([AgentConfig(radius=0.05, max_speed=2.0, max_accel=4.0) for _ in range(3)]
+            + [_box(0.07, 0.04, DynamicsModel.DIFF_DRIVE) for _ in range(3)])
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02,
+                        bounds=(-0.4, 0.4, -0.4, 0.4), max_neighbors=6, neighbor_radius=0.3)
+    obs = _obstacles(E, rng)
+    tab = per_env_float_template(cfgs, E)
+    tab[..., P_MASS] *= rng.uniform(0.5, 2.0, size=(E, A))
+    tab[:, :3, P_RADIUS] *= rng.uniform(0.7, 1.3, size=(E, 3))
+    tab[..., P_MAX_SPEED] *= rng.uniform(0.5, 1.5, size=(E, A))
+    tab[..., P_MAX_ANG_VEL] *= rng.uniform(0.5, 1.5, size=(E, A))
+    s0 = _state(E, A, rng, 0.3, np.float64)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2))
+    w = _cotangent(T, E, A, 7, scale=0.1)
+    st = make_stepper(cfgs, world, 0.05, S, torch.float64, obs=obs, n_envs=E)
+    st.set_agent_params_per_env(tab)
+    hs, hg0, hga = hip_run(st, s0, acts, w, np.float64)
+    for e in range(E):
+        ce = [AgentConfig(**{**c.__dict__}) for c in cfgs]
+        ob_e = {k: (np.asarray(v)[e:e + 1] if np.ndim(v) == 3 or k in ("angle",) and np.ndim(v) == 2
+                    else v) for k, v in obs.items()}
+        from cases import oracle_cfg
+        from oracle.oracle import Oracle
+        cfg = oracle_cfg(ce, world, 0.05, S, 1, 2)
+        O = Oracle(np.float64)
+        tags = np.array([int(c.model) for c in cfgs], dtype=np.int32)
+        modes = np.array([int(c.ctrl_mode) for c in cfgs], dtype=np.int32)
+        from cases import obstacles_np
+        obn = obstacles_np(ob_e, 1)
+        tr = O.rollout(cfg, tab[e], tags, modes, obn, s0[e:e + 1], acts[:, e:e + 1])
+        g0, ga = O.rollout_adj(cfg, tab[e], tags, modes, obn, s0[e:e + 1], acts[:, e:e + 1], tr,
+                               w[:, e:e + 1], None)
+        assert rel(hs[:, e:e + 1, :, :7], tr[..., :7]) <= 1e-10, f"env {e} states"
+        assert rel(hga[:, e:e + 1], ga) <= 1e-8, f"env {e} d/d actions"
+        assert rel(hg0[e:e + 1, :, :7], g0[..., :7]) <= 1e-8, f"env {e} d/d state0"

@@ -326,3 +326,34 @@ def test_step_graph_forms_no_cycle_with_its_owner():
         assert ref() is None and gref() is None
     finally:
         gc.enable()
+
+
+def test_per_env_params_validation():
+    """Stepper.set_agent_params_per_env checks (swarp/core/stepper.py:493-575)."""
+    from swarp_amd import per_env_float_template
+    from swarp_amd.config import P_MASS, P_RADIUS, P_SHAPE
+
+    cfgs = [AgentConfig(radius=0.05), AgentConfig(radius=0.05)]
+    st = Stepper(cfgs, device="cpu", world=WorldConfig(neighbor_radius=0.3))
+    tab = per_env_float_template(cfgs, 3)
+    assert tab.shape == (3, 2, len(PARAM_FIELDS))
+    tab[..., P_MASS] = [[1.0, 2.0], [0.5, 1.5], [3.0, 1.0]]
+    st.set_agent_params_per_env(tab)
+    d = st.desc(3, 2)
+    assert d.params_per_env == 1 and d.params == st.params_per_env.data_ptr()
+    with pytest.raises(ValueError, match="installed for 3 envs"):
+        st.desc(4, 2)
+    with pytest.raises(ValueError, match="shape"):
+        st.set_agent_params_per_env(tab[:, :1])
+    bad = tab.copy()
+    bad[0, 0, P_SHAPE] = 1.0
+    with pytest.raises(ValueError, match="P_SHAPE"):
+        st.set_agent_params_per_env(bad)
+    big = tab.copy()
+    big[..., P_RADIUS] = 0.2
+    with pytest.raises(ValueError, match="neighbor_radius"):
+        st.set_agent_params_per_env(big)
+    # a same-shape device tensor refreshes in place (no reallocation)
+    ptr = st.params_per_env.data_ptr()
+    st.set_agent_params_per_env(torch.as_tensor(tab, dtype=torch.float32))
+    assert st.params_per_env.data_ptr() == ptr
