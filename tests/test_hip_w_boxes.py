@@ -212,17 +212,17 @@ def test_per_env_parameter_tables():
     st = make_stepper(cfgs, world, 0.05, S, torch.float64, obs=obs, n_envs=E)
     st.set_agent_params_per_env(tab)
     hs, hg0, hga = hip_run(st, s0, acts, w, np.float64)
+    from cases import obstacles_np, oracle_cfg
+    from oracle.oracle import Oracle
+
+    O = Oracle(np.float64)
+    cfg = oracle_cfg(cfgs, world, 0.05, S, 1, 2)
+    tags = np.array([int(c.model) for c in cfgs], dtype=np.int32)
+    modes = np.array([int(c.ctrl_mode) for c in cfgs], dtype=np.int32)
     for e in range(E):
-        ce = [AgentConfig(**{**c.__dict__}) for c in cfgs]
-        ob_e = {k: (np.asarray(v)[e:e + 1] if np.ndim(v) == 3 or k in ("angle",) and np.ndim(v) == 2
-                    else v) for k, v in obs.items()}
-        from cases import oracle_cfg
-        from oracle.oracle import Oracle
-        cfg = oracle_cfg(ce, world, 0.05, S, 1, 2)
-        O = Oracle(np.float64)
-        tags = np.array([int(c.model) for c in cfgs], dtype=np.int32)
-        modes = np.array([int(c.ctrl_mode) for c in cfgs], dtype=np.int32)
-        from cases import obstacles_np
+        # env e's obstacles: the per-env arrays (poses, angles) sliced, the shared kept
+        ob_e = {k: (np.asarray(v)[e:e + 1] if k in ("pos", "angle") else v)
+                for k, v in obs.items()}
         obn = obstacles_np(ob_e, 1)
         tr = O.rollout(cfg, tab[e], tags, modes, obn, s0[e:e + 1], acts[:, e:e + 1])
         g0, ga = O.rollout_adj(cfg, tab[e], tags, modes, obn, s0[e:e + 1], acts[:, e:e + 1], tr,
