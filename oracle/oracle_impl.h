@@ -31,6 +31,7 @@ typedef struct {
     REAL radius, mass, max_speed, max_accel, max_ang_vel, max_ang_accel;
     REAL l_f, l_r, max_steer, thrust_max, arm, ixx, iyy, izz, kappa, gravity, min_speed;
     REAL shape, hx, hy; /* footprint: 0 disc, 1 box of half-extents (hx, hy) */
+    REAL gain_v, gain_w; /* ControlMode.SERVO command gains */
     int tag, mode;
 } FN(prm_t);
 
@@ -1011,9 +1012,31 @@ static void FN(rk4_agent_adj)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(a
 }
 
 /* _integrate_agent + _step_2d (swarp/dynamics/kernels.py:194-413), Euler */
+/* servo_command (swarp/dynamics/kernels.py:165-191): a SERVO agent's command as the
+   VELOCITY command it amounts to this substep (the integrate kernels' :849-863) */
+static void FN(servo_command)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *in,
+                              const REAL *act, REAL *as)
+{
+    REAL dt = C->sub_dt;
+    REAL tv = FN(rclamp)(act[0], -P->max_speed, P->max_speed) * P->gain_v;
+    REAL tw = FN(rclamp)(act[1], -P->max_ang_vel, P->max_ang_vel) * P->gain_w;
+    REAL dv = P->max_accel * dt, dw = P->max_ang_accel * dt;
+    as[0] = in->s + FN(rclamp)(tv - in->s, -dv, dv);
+    as[1] = in->w + FN(rclamp)(tw - in->w, -dw, dw);
+    for (int k = 2; k < 4; ++k) as[k] = C->act_dim > k ? act[k] : (REAL)0;
+}
+
 static void FN(integrate_agent)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *in,
                                 const REAL *act, REAL Fx, REAL Fy, FN(agent_t) *out)
 {
+    if (P->mode == 2) {
+        FN(prm_t) Pv = *P;
+        Pv.mode = 0;
+        REAL as[4];
+        FN(servo_command)(C, P, in, act, as);
+        FN(integrate_agent)(C, &Pv, in, as, Fx, Fy, out);
+        return;
+    }
     REAL dt = C->sub_dt;
     REAL a0 = act[0], a1 = C->act_dim > 1 ? act[1] : (REAL)0;
     REAL a2 = C->act_dim > 2 ? act[2] : (REAL)0;
@@ -1140,6 +1163,26 @@ static void FN(integrate_agent_adj)(const FN(ctx_t) *C, const FN(prm_t) *P,
                                     const FN(agent_t) *g, FN(agent_t) *gin, REAL *gact,
                                     REAL *gFx, REAL *gFy)
 {
+    if (P->mode == 2) {
+        /* as0 = s + clamp(tv - s, -dv, dv), tv = clamp(a0, +-max_speed) gain_v; likewise w */
+        FN(prm_t) Pv = *P;
+        Pv.mode = 0;
+        REAL as[4], gs[4] = {0, 0, 0, 0};
+        FN(servo_command)(C, P, in, act, as);
+        FN(integrate_agent_adj)(C, &Pv, in, as, Fx, Fy, g, gin, gs, gFx, gFy);
+        REAL dt = C->sub_dt;
+        REAL tv = FN(rclamp)(act[0], -P->max_speed, P->max_speed) * P->gain_v;
+        REAL tw = FN(rclamp)(act[1], -P->max_ang_vel, P->max_ang_vel) * P->gain_w;
+        REAL dv = P->max_accel * dt, dw = P->max_ang_accel * dt;
+        REAL xv = tv - in->s, xw = tw - in->w;
+        int iv = !(xv < -dv) && !(xv > dv), iw = !(xw < -dw) && !(xw > dw);
+        if (!iv) gin->s += gs[0];
+        if (!iw) gin->w += gs[1];
+        if (iv) gact[0] += FN(rclamp_gx)(act[0], -P->max_speed, P->max_speed, gs[0] * P->gain_v);
+        if (iw) gact[1] += FN(rclamp_gx)(act[1], -P->max_ang_vel, P->max_ang_vel, gs[1] * P->gain_w);
+        for (int k = 2; k < C->act_dim && k < 4; ++k) gact[k] += gs[k];
+        return;
+    }
     REAL dt = C->sub_dt;
     REAL a0 = act[0], a1 = C->act_dim > 1 ? act[1] : (REAL)0;
     REAL a2 = C->act_dim > 2 ? act[2] : (REAL)0;
@@ -1822,6 +1865,7 @@ static void FN(make_prm)(const REAL *params, const int32_t *tags, const int32_t 
         P[a].iyy = r[12]; P[a].izz = r[13]; P[a].kappa = r[14]; P[a].gravity = r[15];
         P[a].min_speed = r[16];
         P[a].shape = r[17]; P[a].hx = r[18]; P[a].hy = r[19];
+        P[a].gain_v = r[20]; P[a].gain_w = r[21];
         if (P[a].shape > (REAL)0.5) C->boxes = 1;
         P[a].tag = tags[a];
         P[a].mode = modes[a];

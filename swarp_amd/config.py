@@ -13,8 +13,8 @@ types so a caller's configuration code carries over unchanged:
 * ``drone_config`` follows ``swarp/dynamics/drone.py:24-53``.
 
 What the MI355X build does not run is rejected loudly rather than silently
-approximated: ``ControlMode.SERVO``, box agents / wheel contacts / per-env parameter
-tables together with movable bodies and more than 64 agents per env raise
+approximated: box agents / wheel contacts / per-env parameter tables together with
+movable bodies and more than 64 agents per env raise
 ``NotImplementedError`` when a ``Stepper`` is built with them (or the bodies installed).
 """
 

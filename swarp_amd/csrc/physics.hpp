@@ -55,6 +55,7 @@ template <typename T> struct Prm {
     T radius, mass, max_speed, max_accel, max_ang_vel, max_ang_accel, l_f, l_r, max_steer;
     T thrust_max, arm, ixx, iyy, izz, kappa, gravity, min_speed;
     T shape, hx, hy;  // footprint: 0 disc, 1 box of half-extents (hx, hy)
+    T gain_v, gain_w; // ControlMode.SERVO command gains
     int tag, mode;
 };
 
@@ -1226,8 +1227,8 @@ __device__ __forceinline__ void integrate_rk4_adj(const Cst<T> &C, const Prm<T> 
 // Semi-implicit Euler substep of one agent: _integrate_agent + _step_2d
 // (swarp/dynamics/kernels.py:194-413).  `o` receives the new state.
 template <typename T, bool DRONE>
-__device__ __forceinline__ void integrate(const Cst<T> &C, const Prm<T> &P, const St<T> &in,
-                                          const T (&a)[4], T Fx, T Fy, St<T> &o)
+__device__ __forceinline__ void integrate_core(const Cst<T> &C, const Prm<T> &P, const St<T> &in,
+                                               const T (&a)[4], T Fx, T Fy, St<T> &o)
 {
     if (C.rk4) {
         integrate_rk4<T, DRONE>(C, P, in, a, Fx, Fy, o);
@@ -1327,6 +1328,38 @@ __device__ __forceinline__ void integrate(const Cst<T> &C, const Prm<T> &P, cons
     if (C.clamp) clamp_position(C, P, o.th, pnx, pny);
     o.px = pnx;
     o.py = pny;
+}
+
+// servo_command (swarp/dynamics/kernels.py:165-191): ControlMode.SERVO as the VELOCITY
+// command it amounts to this substep -- the drive's speed and turn rate move toward the
+// gained command by at most max_accel dt and max_ang_accel dt.
+template <typename T>
+__device__ __forceinline__ void servo_command(const Cst<T> &C, const Prm<T> &P, const St<T> &in,
+                                              const T (&a)[4], T (&as)[4])
+{
+    const T dt = C.sub_dt;
+    const T tv = wclamp(a[0], -P.max_speed, P.max_speed) * P.gain_v;
+    const T tw = wclamp(a[1], -P.max_ang_vel, P.max_ang_vel) * P.gain_w;
+    const T dv = P.max_accel * dt, dw = P.max_ang_accel * dt;
+    as[0] = in.s + wclamp(tv - in.s, -dv, dv);
+    as[1] = in.w + wclamp(tw - in.w, -dw, dw);
+    as[2] = a[2];
+    as[3] = a[3];
+}
+
+// One substep of integration (integrate_kernel, swarp/dynamics/kernels.py:812-971): a
+// SERVO agent's command turned into the VELOCITY command first (:849-863).
+template <typename T, bool DRONE>
+__device__ __forceinline__ void integrate(const Cst<T> &C, const Prm<T> &P, const St<T> &in,
+                                          const T (&a)[4], T Fx, T Fy, St<T> &o)
+{
+    T as[4] = {a[0], a[1], a[2], a[3]};
+    Prm<T> Pv = P;
+    if (P.mode == 2) {
+        servo_command(C, P, in, a, as);
+        Pv.mode = 0;
+    }
+    integrate_core<T, DRONE>(C, Pv, in, as, Fx, Fy, o);
 }
 
 // Reverse of integrate without its position clamp (integrate_adj reverses that first).
@@ -1535,22 +1568,49 @@ __device__ __forceinline__ void integrate_adj_core(const Cst<T> &C, const Prm<T>
     }
 }
 
-// Reverse of integrate: the position clamp, reversed at the unclamped output (its
-// bounds move with the heading under the footprint clamp), then the rest of the step.
+// Reverse of integrate: a SERVO agent's command conversion around the rest; the position
+// clamp, reversed at the unclamped output (its bounds move with the heading under the
+// footprint clamp); then the step itself.
 template <typename T, bool DRONE>
 __device__ __forceinline__ void integrate_adj(const Cst<T> &C, const Prm<T> &P, const St<T> &in,
                                               const T (&a)[4], T Fx, T Fy, const St<T> &g,
                                               St<T> &gi, T (&ga)[4], T &gFx, T &gFy)
 {
+    const bool servo = P.mode == 2;
+    T as[4] = {a[0], a[1], a[2], a[3]};
+    Prm<T> Pv = P;
+    if (servo) {
+        servo_command(C, P, in, a, as);
+        Pv.mode = 0;
+    }
     Cst<T> C0 = C;
     C0.clamp = 0;
     St<T> g2 = g;
     if (C.clamp) {
         St<T> raw;
-        integrate<T, DRONE>(C0, P, in, a, Fx, Fy, raw);
-        clamp_position_adj(C, P, raw.px, raw.py, raw.th, g2.px, g2.py, g2.th);
+        integrate_core<T, DRONE>(C0, Pv, in, as, Fx, Fy, raw);
+        clamp_position_adj(C, Pv, raw.px, raw.py, raw.th, g2.px, g2.py, g2.th);
     }
-    integrate_adj_core<T, DRONE>(C0, P, in, a, Fx, Fy, g2, gi, ga, gFx, gFy);
+    T gs[4] = {T(0), T(0), T(0), T(0)};
+    integrate_adj_core<T, DRONE>(C0, Pv, in, as, Fx, Fy, g2, gi, gs, gFx, gFy);
+    if (servo) {
+        // as0 = s + clamp(tv - s, -dv, dv), tv = clamp(a0, +-max_speed) gain_v; likewise w
+        const T dt = C.sub_dt;
+        const T tv = wclamp(a[0], -P.max_speed, P.max_speed) * P.gain_v;
+        const T tw = wclamp(a[1], -P.max_ang_vel, P.max_ang_vel) * P.gain_w;
+        const T dv = P.max_accel * dt, dw = P.max_ang_accel * dt;
+        const T xv = tv - in.s, xw = tw - in.w;
+        const bool iv = !(xv < -dv) && !(xv > dv), iw = !(xw < -dw) && !(xw > dw);
+        gi.s += iv ? T(0) : gs[0];
+        gi.w += iw ? T(0) : gs[1];
+        ga[0] += iv ? wclamp_g(a[0], -P.max_speed, P.max_speed, gs[0] * P.gain_v) : T(0);
+        ga[1] += iw ? wclamp_g(a[1], -P.max_ang_vel, P.max_ang_vel, gs[1] * P.gain_w) : T(0);
+    } else {
+        ga[0] += gs[0];
+        ga[1] += gs[1];
+    }
+    ga[2] += gs[2];
+    ga[3] += gs[3];
 }
 
 }  // namespace swarp

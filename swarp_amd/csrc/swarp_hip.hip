@@ -145,6 +145,7 @@ __device__ __forceinline__ void load_prm(const Args<T> &g, size_t row, int a, Pr
     p.max_steer = r[8]; p.thrust_max = r[9]; p.arm = r[10]; p.ixx = r[11];
     p.iyy = r[12]; p.izz = r[13]; p.kappa = r[14]; p.gravity = r[15]; p.min_speed = r[16];
     p.shape = r[17]; p.hx = r[18]; p.hy = r[19];
+    p.gain_v = r[20]; p.gain_w = r[21];
     p.tag = g.tag[a];
     p.mode = g.mode[a];
 }

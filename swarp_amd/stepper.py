@@ -176,9 +176,6 @@ class Stepper:
                 f"neighbor_method={w.neighbor_method!r}: this build implements the brute-force "
                 "lists only (the reference's own choice at <= 512 agents)"
             )
-        for c in self.configs:
-            if c.ctrl_mode == ControlMode.SERVO:
-                raise NotImplementedError("ControlMode.SERVO is not implemented")
 
     # ------------------------------------------------------- per-env parameters
 

@@ -230,3 +230,29 @@ def test_per_env_parameter_tables():
         assert rel(hs[:, e:e + 1, :, :7], tr[..., :7]) <= 1e-10, f"env {e} states"
         assert rel(hga[:, e:e + 1], ga) <= 1e-8, f"env {e} d/d actions"
         assert rel(hg0[e:e + 1, :, :7], g0[..., :7]) <= 1e-8, f"env {e} d/d state0"
+
+
+def test_servo_control_mode():
+    """ControlMode.SERVO (servo_command, swarp/dynamics/kernels.py:165-191, applied before
+    Euler or RK4): diff-drive servo agents (discs and boxes) with contacts and walls,
+    states and gradients against the oracle (fp64 1e-10 / 1e-8, fp32 states 1e-5)."""
+    from swarp_amd.config import ControlMode as CM
+
+    E, A, T, S = 24, 6, 6, 2
+    rng = np.random.default_rng(37)
+    cfgs = ([AgentConfig(model=DynamicsModel.DIFF_DRIVE, ctrl_mode=CM.SERVO, radius=0.05,
+                         max_speed=1.5, max_accel=2.0, cmd_gain_v=0.8, cmd_gain_w=1.2)
+             for _ in range(3)]
+            + [_box(0.07, 0.04, DynamicsModel.DIFF_DRIVE, ctrl_mode=CM.SERVO) for _ in range(3)])
+    for integ in (Integrator.EULER, Integrator.RK4):
+        world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02,
+                            bounds=(-0.35, 0.35, -0.35, 0.35), max_neighbors=6, integrator=integ)
+        s0 = _state(E, A, rng, 0.3, np.float64)
+        acts = rng.uniform(-2, 2, size=(T, E, A, 2))
+        w = _cotangent(T, E, A, 8, scale=0.1)
+        hip, orc = _run(cfgs, world, S, s0, acts, w, np.float64)
+        assert rel(hip[0][..., :7], orc[0][..., :7]) <= 1e-10, integ
+        assert rel(hip[2], orc[2]) <= 1e-8 and rel(hip[1][..., :7], orc[1][..., :7]) <= 1e-8, integ
+        hip, orc = _run(cfgs, world, S, s0.astype(np.float32), acts.astype(np.float32), w,
+                        np.float32)
+        assert rel(hip[0][..., :7], orc[0][..., :7]) <= 1e-5, integ

@@ -399,3 +399,38 @@ def test_wheel_contacts_have_no_reverse_mode():
     tr = O.rollout(cfg, p, t, m, None, s0, acts)
     with pytest.raises(RuntimeError):
         O.rollout_adj(cfg, p, t, m, None, s0, acts, tr, np.ones_like(tr), None)
+
+
+# ------------------------------------------------------------------ ControlMode.SERVO
+
+def _servo(n=2, **kw):
+    from swarp_amd.config import ControlMode as CM
+    return [AgentConfig(model=DynamicsModel.DIFF_DRIVE, ctrl_mode=CM.SERVO, max_speed=1.5,
+                        max_accel=2.0, max_ang_vel=3.0, max_ang_accel=4.0, cmd_gain_v=0.8,
+                        cmd_gain_w=1.2, **kw) for _ in range(n)]
+
+
+def test_servo_closed_form():
+    """servo_command (swarp/dynamics/kernels.py:165-191): speed and turn rate move toward
+    the gained, clamped command by at most max_accel dt / max_ang_accel dt, then the
+    VELOCITY branch runs on the result."""
+    cfgs = _servo(1)
+    w = WorldConfig(collisions=False)
+    dt = 0.1
+    s0 = pack_state({"pos": [[[0.0, 0.0]]], "speed": [[0.3]], "ang_vel": [[-0.2]]})
+    tr = _wheel_step(cfgs, w, s0, np.array([[[[5.0, 0.5]]]]), dt)[0, 0, 0]
+    s = 0.3 + min(max(1.5 * 0.8 - 0.3, -0.2), 0.2)        # clamped command 1.5, step <= 0.2
+    om = -0.2 + min(max(0.5 * 1.2 + 0.2, -0.4), 0.4)      # step <= 0.4
+    assert tr[5] == pytest.approx(s, rel=1e-14) and tr[6] == pytest.approx(om, rel=1e-14)
+    assert tr[2] == pytest.approx(om * dt, rel=1e-14)
+    assert tr[0] == pytest.approx(s * dt, rel=1e-14)
+
+
+def test_fd_servo():
+    """Finite differences through the servo conversion (saturated and unsaturated steps),
+    with contacts, walls and substeps."""
+    cfgs = _servo(3)
+    s0, rng = _rs(2, 3, 9, 0.15)
+    acts = rng.uniform(-2, 2, size=(3, 2, 3, 2))
+    _fd_check(cfgs, _world(collision_c=1.0, bounds=(-0.3, 0.3, -0.3, 0.3)), 0.05, 2, s0, acts,
+              fields=(0, 1, 2, 3, 4, 5, 6))
