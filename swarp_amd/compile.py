@@ -8,8 +8,11 @@ environment loop sees the step as one opaque, differentiable operator.
 
 The op is functional: the forward writes freshly allocated outputs (the four drone
 fields of a 2-D fleet are copied through, never aliased) and mutates no input; the
-backward launches the step's adjoint (``swarp_rollout_bwd``, T = 1) on the saved inputs,
-recomputing the substeps inside the kernel, so nothing survives between the two calls.
+backward is a second opaque op, ``swarp_amd::step_bwd``, which launches the step's
+adjoint (``swarp_rollout_bwd``, T = 1) on the saved inputs, recomputing the substeps
+inside the kernel, so nothing survives between the two calls.  Both ops have fake
+implementations: AOTAutograd traces the backward graph with fake tensors, so the
+autograd rule itself must not touch device memory.
 Steppers cross the op boundary as integer handles from a weak registry: a handle does not
 keep its stepper (and its device buffers) alive.  Worlds with movable bodies carry an
 obstacle state the op's signature has no room for; they raise ``NotImplementedError``.
@@ -81,16 +84,19 @@ def _step_op_fake(stepper_id, actions, pos, theta, vel, speed, ang_vel, z, vz, a
             for t in (pos, theta, vel, speed, ang_vel, z, vz, attitude, body_rates)]
 
 
-def _setup_context(ctx, inputs, output):
-    stepper_id, actions, *state = inputs
-    ctx.stepper_id = stepper_id
-    ctx.save_for_backward(actions, *state)
-
-
-def _backward(ctx, *grad_outputs):
-    grads = grad_outputs[0] if len(grad_outputs) == 1 else grad_outputs
-    stepper = _stepper(ctx.stepper_id)
-    actions, *state = ctx.saved_tensors
+@torch.library.custom_op("swarp_amd::step_bwd", mutates_args=())
+def _step_bwd_op(stepper_id: int, actions: torch.Tensor, pos: torch.Tensor, theta: torch.Tensor,
+                 vel: torch.Tensor, speed: torch.Tensor, ang_vel: torch.Tensor, z: torch.Tensor,
+                 vz: torch.Tensor, attitude: torch.Tensor, body_rates: torch.Tensor,
+                 g_pos: torch.Tensor | None, g_theta: torch.Tensor | None,
+                 g_vel: torch.Tensor | None, g_speed: torch.Tensor | None,
+                 g_ang_vel: torch.Tensor | None, g_z: torch.Tensor | None,
+                 g_vz: torch.Tensor | None, g_attitude: torch.Tensor | None,
+                 g_body_rates: torch.Tensor | None) -> list[torch.Tensor]:
+    """Adjoint of one step: [d actions, d pos, ..., d body_rates] (fresh tensors)."""
+    stepper = _stepper(stepper_id)
+    state = (pos, theta, vel, speed, ang_vel, z, vz, attitude, body_rates)
+    grads = (g_pos, g_theta, g_vel, g_speed, g_ang_vel, g_z, g_vz, g_attitude, g_body_rates)
     nf = _nfields(stepper)
     E, ad = actions.shape[0], actions.shape[2]
     seq = actions.unsqueeze(0).contiguous()
@@ -106,9 +112,31 @@ def _backward(ctx, *grad_outputs):
         ctypes.byref(desc), 1, ctypes.byref(st0), seq.data_ptr(), None, None,
         ctypes.byref(gfin) if gfin is not None else None, ctypes.byref(a0), adj_act.data_ptr(),
         _stream(seq)))
-    # the fields a 2-D fleet does not step pass through: their adjoint too
-    tail = [None if g is None else g.clone() for g in grads[nf:]]
-    return (None, adj_act[0], *adj0, *tail)
+    # the fields a 2-D fleet does not step pass through: so does their adjoint
+    tail = [torch.zeros_like(state[k]) if grads[k] is None else grads[k].clone()
+            for k in range(nf, 9)]
+    return [adj_act[0], *adj0, *tail]
+
+
+@_step_bwd_op.register_fake
+def _step_bwd_op_fake(stepper_id, actions, pos, theta, vel, speed, ang_vel, z, vz, attitude,
+                      body_rates, g_pos, g_theta, g_vel, g_speed, g_ang_vel, g_z, g_vz,
+                      g_attitude, g_body_rates):
+    return [torch.empty(t.shape, dtype=t.dtype, device=t.device)
+            for t in (actions, pos, theta, vel, speed, ang_vel, z, vz, attitude, body_rates)]
+
+
+def _setup_context(ctx, inputs, output):
+    stepper_id, actions, *state = inputs
+    ctx.stepper_id = stepper_id
+    ctx.save_for_backward(actions, *state)
+
+
+def _backward(ctx, *grad_outputs):
+    grads = grad_outputs[0] if len(grad_outputs) == 1 else grad_outputs
+    actions, *state = ctx.saved_tensors
+    outs = torch.ops.swarp_amd.step_bwd(ctx.stepper_id, actions, *state, *grads)
+    return (None, *outs)
 
 
 _step_op.register_autograd(_backward, setup_context=_setup_context)
