@@ -261,3 +261,19 @@ def cores() -> int:
         return len(os.sched_getaffinity(0))
     except AttributeError:  # pragma: no cover
         return os.cpu_count() or 1
+
+
+PMATH = {"sin": 0, "cos": 1, "tan": 2, "atan": 3, "tanh": 4}
+
+
+def pmath(name: str, x: np.ndarray) -> np.ndarray:
+    """The portable transcendental ``name`` (include/swarp_pmath.h) over ``x`` (float32:
+    evaluated in double and rounded once, as the kernels do; float64: as is)."""
+    x = np.ascontiguousarray(x)
+    y = np.empty_like(x)
+    L = lib()
+    fn = L.oracle_pmath_f32 if x.dtype == np.float32 else L.oracle_pmath_f64
+    fn.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_long]
+    fn.restype = None
+    fn(PMATH[name], _p(x), _p(y), x.size)
+    return y

@@ -80,41 +80,13 @@ static inline REAL FN(rclamp_gx)(REAL x, REAL a, REAL b, REAL g)
     return g;
 }
 
-/* sin and cos of a body angle, identical on every IEEE platform: Cody-Waite reduction
-   by pi/2 (pi/2 split in a 33-bit head and a tail, so k * head is exact for |k| < 2^20)
-   and the Taylor series of sin and cos on |r| <= pi/4 to r^17 / r^18, all in double
-   precision, then rounded to REAL.  The device build evaluates the same operations in
-   the same order (swarp_amd/csrc/physics.hpp, sincos_portable), which makes body poses
-   bit-identical between the two. */
+/* sin and cos of a body angle: the portable evaluation (swarp_pmath.h) */
 static inline void FN(psincos)(REAL xr, REAL *so, REAL *co)
 {
-    const double x = (double)xr;
-    const double k = rint(x * 0x1.45f306dc9c883p-1);
-    const double r = (x - k * 0x1.921fb544p+0) - k * 0x1.0b4611a626331p-34;
-    const double z = r * r;
-    double ps = 0x1.952c77030ad4ap-49;
-    ps = ps * z - 0x1.ae7f3e733b81fp-41;
-    ps = ps * z + 0x1.6124613a86d09p-33;
-    ps = ps * z - 0x1.ae64567f544e4p-26;
-    ps = ps * z + 0x1.71de3a556c734p-19;
-    ps = ps * z - 0x1.a01a01a01a01ap-13;
-    ps = ps * z + 0x1.1111111111111p-7;
-    ps = ps * z - 0x1.5555555555555p-3;
-    const double sn = r + r * (z * ps);
-    double pc = -0x1.6827863b97d97p-53;
-    pc = pc * z + 0x1.ae7f3e733b81fp-45;
-    pc = pc * z - 0x1.93974a8c07c9dp-37;
-    pc = pc * z + 0x1.1eed8eff8d898p-29;
-    pc = pc * z - 0x1.27e4fb7789f5cp-22;
-    pc = pc * z + 0x1.a01a01a01a01ap-16;
-    pc = pc * z - 0x1.6c16c16c16c17p-10;
-    pc = pc * z + 0x1.5555555555555p-5;
-    const double cn = (1.0 - z * 0.5) + (z * z) * pc;
-    const long long q = (long long)k & 3;
-    const double s_ = q == 0 ? sn : (q == 1 ? cn : (q == 2 ? -sn : -cn));
-    const double c_ = q == 0 ? cn : (q == 1 ? -sn : (q == 2 ? -cn : sn));
-    *so = (REAL)s_;
-    *co = (REAL)c_;
+    double s, c;
+    swarp_psincos((double)xr, &s, &c);
+    *so = (REAL)s;
+    *co = (REAL)c;
 }
 
 /* clamp_norm (swarp/dynamics/kernels.py:68-71): v * (limit / max(length(v), limit)) */

@@ -20,6 +20,11 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* sin, cos, tan, atan, tanh: the portable double-precision evaluations shared with the
+   HIP kernels (include/swarp_pmath.h, pinned against libm by tests/test_pmath.py), so a
+   float32 restatement computes the same transcendental values as the device. */
+#include "swarp_pmath.h"
+
 typedef struct {
     int n_envs, n_agents, act_dim, substeps, max_neighbors;
     int collisions, soft_walls, clamp_bounds, n_threads;
@@ -46,11 +51,11 @@ int oracle_abi_version(void) { return 1; }
 #define REAL double
 #define FN(x) x##_f64
 #define SQRT sqrt
-#define COS cos
-#define SIN sin
-#define TAN tan
-#define ATAN atan
-#define TANH tanh
+#define COS swarp_pcos
+#define SIN swarp_psin
+#define TAN swarp_ptan
+#define ATAN swarp_patan
+#define TANH swarp_ptanh
 #define FABS fabs
 #include "oracle_impl.h"
 #undef REAL
@@ -66,10 +71,33 @@ int oracle_abi_version(void) { return 1; }
 #define REAL float
 #define FN(x) x##_f32
 #define SQRT sqrtf
-#define COS cosf
-#define SIN sinf
-#define TAN tanf
-#define ATAN atanf
-#define TANH tanhf
+#define COS(x) ((float)swarp_pcos((double)(x)))
+#define SIN(x) ((float)swarp_psin((double)(x)))
+#define TAN(x) ((float)swarp_ptan((double)(x)))
+#define ATAN(x) ((float)swarp_patan((double)(x)))
+#define TANH(x) ((float)swarp_ptanh((double)(x)))
 #define FABS fabsf
 #include "oracle_impl.h"
+
+/* The portable transcendental functions over arrays (fn: 0 sin, 1 cos, 2 tan, 3 atan,
+   4 tanh), for their accuracy tests. */
+static double pm_eval(int fn, double x)
+{
+    switch (fn) {
+    case 0: return swarp_psin(x);
+    case 1: return swarp_pcos(x);
+    case 2: return swarp_ptan(x);
+    case 3: return swarp_patan(x);
+    default: return swarp_ptanh(x);
+    }
+}
+
+void oracle_pmath_f64(int fn, const double *x, double *y, long n)
+{
+    for (long i = 0; i < n; ++i) y[i] = pm_eval(fn, x[i]);
+}
+
+void oracle_pmath_f32(int fn, const float *x, float *y, long n)
+{
+    for (long i = 0; i < n; ++i) y[i] = (float)pm_eval(fn, (double)x[i]);
+}

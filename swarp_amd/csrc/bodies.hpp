@@ -2,7 +2,7 @@
 // obstacle_dynamics_kernel (swarp/core/bodies.py:367-568, disc variant: every shape of a
 // movable body is a circle) inside the fused substep chain, and this build's own adjoint
 // of it (the reference never tapes the body pass, swarp/core/stepper.py:952).
-// Included by swarp_hip.hip after the generic kernels; uses their lane/state helpers.
+// Instantiated by k_bodies.hip.
 //
 // Per-env obstacle state, 12 scalars per obstacle index o (the reference's obs_* and
 // body_* arrays, swarp/core/stepper.py:418-431):
@@ -21,6 +21,7 @@
 // keeps them in the reference's summation order; a contribution that is exactly zero is
 // skipped, which does not change a sum that starts at +0.
 #pragma once
+#include "common.hpp"
 
 namespace swarp {
 
@@ -43,39 +44,13 @@ template <typename T> struct ObIO {
     T *a0;              // [E, 12N] adjoint of ob0 (nullable)
 };
 
-// sin and cos of a body angle, the same on host and device: Cody-Waite reduction by
-// pi/2 (pi/2 split into a 33-bit head, so k * head is exact for |k| < 2^20, and a tail)
-// and the Taylor series of sin and cos on |r| <= pi/4 up to r^17 / r^18, in double
-// precision, rounded to T.
+// sin and cos of a body angle (the portable evaluation of swarp_pmath.h, as the oracle's)
 template <typename T> __device__ __forceinline__ void psincos(T xr, T &so, T &co)
 {
-    const double x = (double)xr;
-    const double k = __builtin_rint(x * 0x1.45f306dc9c883p-1);
-    const double r = (x - k * 0x1.921fb544p+0) - k * 0x1.0b4611a626331p-34;
-    const double z = r * r;
-    double ps = 0x1.952c77030ad4ap-49;
-    ps = ps * z - 0x1.ae7f3e733b81fp-41;
-    ps = ps * z + 0x1.6124613a86d09p-33;
-    ps = ps * z - 0x1.ae64567f544e4p-26;
-    ps = ps * z + 0x1.71de3a556c734p-19;
-    ps = ps * z - 0x1.a01a01a01a01ap-13;
-    ps = ps * z + 0x1.1111111111111p-7;
-    ps = ps * z - 0x1.5555555555555p-3;
-    const double sn = r + r * (z * ps);
-    double pc = -0x1.6827863b97d97p-53;
-    pc = pc * z + 0x1.ae7f3e733b81fp-45;
-    pc = pc * z - 0x1.93974a8c07c9dp-37;
-    pc = pc * z + 0x1.1eed8eff8d898p-29;
-    pc = pc * z - 0x1.27e4fb7789f5cp-22;
-    pc = pc * z + 0x1.a01a01a01a01ap-16;
-    pc = pc * z - 0x1.6c16c16c16c17p-10;
-    pc = pc * z + 0x1.5555555555555p-5;
-    const double cn = (1.0 - z * 0.5) + (z * z) * pc;
-    const long long q = (long long)k & 3;
-    const double s_ = q == 0 ? sn : (q == 1 ? cn : (q == 2 ? -sn : -cn));
-    const double c_ = q == 0 ? cn : (q == 1 ? -sn : (q == 2 ? -cn : sn));
-    so = (T)s_;
-    co = (T)c_;
+    double s, c;
+    swarp_psincos((double)xr, &s, &c);
+    so = (T)s;
+    co = (T)c;
 }
 
 // bounds_apart (swarp/core/collisions.py:73-84)
@@ -780,6 +755,47 @@ __global__ __launch_bounds__(64) void k_body_bwd(const Cst<T> C, const Args<T> g
     __syncthreads();
     if (io.a0 && env_ok)
         for (int q = L.agent; q < NW; q += PA) io.a0[eo + q] = gob[q];
+}
+
+// ---------------------------------------------------------------------- launchers
+
+template <typename T> size_t body_bwd_lds_of(int PA, int S, int N)
+{
+    switch (PA) {
+    case 4: return body_bwd_lds<T, 4>(S, N);
+    case 8: return body_bwd_lds<T, 8>(S, N);
+    case 16: return body_bwd_lds<T, 16>(S, N);
+    case 32: return body_bwd_lds<T, 32>(S, N);
+    default: return body_bwd_lds<T, 64>(S, N);
+    }
+}
+
+template <typename T>
+void launch_body_fwd(int PA, const Cst<T> &C, const Args<T> &a, const ObTab<T> &tb,
+                     const ObIO<T> &io, hipStream_t st)
+{
+    const dim3 grid((C.E + 64 / PA - 1) / (64 / PA));
+    switch (PA) {
+    case 4: hipLaunchKernelGGL((k_body_fwd<T, 4>), grid, dim3(64), 0, st, C, a, tb, io); break;
+    case 8: hipLaunchKernelGGL((k_body_fwd<T, 8>), grid, dim3(64), 0, st, C, a, tb, io); break;
+    case 16: hipLaunchKernelGGL((k_body_fwd<T, 16>), grid, dim3(64), 0, st, C, a, tb, io); break;
+    case 32: hipLaunchKernelGGL((k_body_fwd<T, 32>), grid, dim3(64), 0, st, C, a, tb, io); break;
+    default: hipLaunchKernelGGL((k_body_fwd<T, 64>), grid, dim3(64), 0, st, C, a, tb, io); break;
+    }
+}
+
+template <typename T>
+void launch_body_bwd(int PA, const Cst<T> &C, const Args<T> &a, const ObTab<T> &tb,
+                     const ObIO<T> &io, size_t shm, hipStream_t st)
+{
+    const dim3 grid((C.E + 64 / PA - 1) / (64 / PA));
+    switch (PA) {
+    case 4: hipLaunchKernelGGL((k_body_bwd<T, 4>), grid, dim3(64), shm, st, C, a, tb, io); break;
+    case 8: hipLaunchKernelGGL((k_body_bwd<T, 8>), grid, dim3(64), shm, st, C, a, tb, io); break;
+    case 16: hipLaunchKernelGGL((k_body_bwd<T, 16>), grid, dim3(64), shm, st, C, a, tb, io); break;
+    case 32: hipLaunchKernelGGL((k_body_bwd<T, 32>), grid, dim3(64), shm, st, C, a, tb, io); break;
+    default: hipLaunchKernelGGL((k_body_bwd<T, 64>), grid, dim3(64), shm, st, C, a, tb, io); break;
+    }
 }
 
 }  // namespace swarp

@@ -1,0 +1,414 @@
+// common.hpp -- lane layout, state I/O and the contact pass shared by every rollout kernel
+// family (generic, holonomic, bodies, navigation).
+//
+// Execution model
+//   * One lane per (env, agent).  An env occupies PA consecutive lanes of a wave64
+//     (PA = next power of two >= n_agents, <= 64), so an env never spans waves and
+//     every exchange between its agents stays inside one wave: positions, velocities,
+//     neighbour masks and force adjoints go through a small LDS staging area.
+//   * Workgroup = one wave (64 lanes), so the workgroup barrier costs nothing and
+//     envs are spread over the whole chip at wave granularity.
+//   * One launch runs a whole T-step rollout: the state stays in registers between
+//     steps; HBM sees the actions in and each step's output state (the checkpoint).
+//   * The backward launch walks t = T-1..0, reloads each step's input checkpoint,
+//     recomputes that step's substeps into LDS, then runs the reverse pass.  The force
+//     adjoint of a pair is gathered by both agents from the same recomputed pair, in
+//     ascending neighbour order: deterministic, no atomics.
+//   * Neighbour membership uses the exact threshold test d2 <= t_nbr, where t_nbr is
+//     the largest value whose correctly rounded square root is <= the radius, which
+//     is bit-identical to the reference's sqrt(d2) <= radius (neighbors.py:91).
+//     Within a step, substeps after the first scan only a skin list built at substep 0;
+//     a per-env displacement bound proves the skin list complete, and an env whose
+//     agents moved too far rescans all pairs.  Both give the same lists.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "physics.hpp"
+#include "boxes.hpp"
+#include "swarp_hip.h"
+
+namespace swarp {
+
+template <int PA> struct MaskT { typedef uint32_t type; };
+template <> struct MaskT<64> { typedef uint64_t type; };
+
+__device__ __forceinline__ int m_ctz(uint32_t m) { return __builtin_ctz(m); }
+__device__ __forceinline__ int m_ctz(uint64_t m) { return __builtin_ctzll(m); }
+__device__ __forceinline__ int m_popc(uint32_t m) { return __builtin_popcount(m); }
+__device__ __forceinline__ int m_popc(uint64_t m) { return __builtin_popcountll(m); }
+
+// Field pointers of one state; strides (in scalars) 2,1,2,1,1,1,1,4,3.
+template <typename T> struct Fields {
+    T *f[9];
+};
+template <typename T> struct CFields {
+    const T *f[9];
+};
+
+template <typename T> struct Args {
+    const T *params;
+    const int32_t *tag, *mode;
+    Obs<T> obs;
+    CFields<T> s0;       // rollout input state
+    const T *act;        // [T,E,A,ad]
+    Fields<T> traj;      // outputs of steps 0..T-2 (stride E*A per step)
+    Fields<T> fin;       // output of step T-1
+    CFields<T> atraj;    // adjoints arriving at traj (nullable per field)
+    CFields<T> afin;     // adjoint arriving at fin (nullable per field)
+    Fields<T> a0;        // adjoint of s0 (nullable per field)
+    T *aact;             // adjoint of actions
+    int nsteps;
+};
+
+__device__ __forceinline__ int fstride(int k)
+{
+    // pos theta vel speed ang_vel z vz attitude body_rates
+    return k == 0 || k == 2 ? 2 : (k == 7 ? 4 : (k == 8 ? 3 : 1));
+}
+
+template <typename T, bool DRONE>
+__device__ __forceinline__ void load_state(const T *const *f, size_t i, size_t off, St<T> &s)
+{
+    // `off` = element offset of the state in the trajectory (step * E * A)
+    const size_t j = i + off;
+    s.px = f[0][2 * j]; s.py = f[0][2 * j + 1];
+    s.th = f[1][j];
+    s.vx = f[2][2 * j]; s.vy = f[2][2 * j + 1];
+    s.s = f[3][j];
+    s.w = f[4][j];
+    if (DRONE) {
+        s.z = f[5][j]; s.vz = f[6][j];
+        s.qx = f[7][4 * j]; s.qy = f[7][4 * j + 1]; s.qz = f[7][4 * j + 2]; s.qw = f[7][4 * j + 3];
+        s.bx = f[8][3 * j]; s.by = f[8][3 * j + 1]; s.bz = f[8][3 * j + 2];
+    } else {
+        s.z = s.vz = s.qx = s.qy = s.qz = s.bx = s.by = s.bz = T(0);
+        s.qw = T(1);
+    }
+}
+
+template <typename T, bool DRONE>
+__device__ __forceinline__ void store_state(T *const *f, size_t j, const St<T> &s)
+{
+    f[0][2 * j] = s.px; f[0][2 * j + 1] = s.py;
+    f[1][j] = s.th;
+    f[2][2 * j] = s.vx; f[2][2 * j + 1] = s.vy;
+    f[3][j] = s.s;
+    f[4][j] = s.w;
+    if (DRONE) {
+        f[5][j] = s.z; f[6][j] = s.vz;
+        f[7][4 * j] = s.qx; f[7][4 * j + 1] = s.qy; f[7][4 * j + 2] = s.qz; f[7][4 * j + 3] = s.qw;
+        f[8][3 * j] = s.bx; f[8][3 * j + 1] = s.by; f[8][3 * j + 2] = s.bz;
+    }
+}
+
+// Adds a nullable adjoint state (fields may be NULL) at element j.
+template <typename T, bool DRONE>
+__device__ __forceinline__ void add_adj(const T *const *f, size_t j, St<T> &g)
+{
+    if (f[0]) { g.px += f[0][2 * j]; g.py += f[0][2 * j + 1]; }
+    if (f[1]) g.th += f[1][j];
+    if (f[2]) { g.vx += f[2][2 * j]; g.vy += f[2][2 * j + 1]; }
+    if (f[3]) g.s += f[3][j];
+    if (f[4]) g.w += f[4][j];
+    if (DRONE) {
+        if (f[5]) g.z += f[5][j];
+        if (f[6]) g.vz += f[6][j];
+        if (f[7]) { g.qx += f[7][4 * j]; g.qy += f[7][4 * j + 1]; g.qz += f[7][4 * j + 2]; g.qw += f[7][4 * j + 3]; }
+        if (f[8]) { g.bx += f[8][3 * j]; g.by += f[8][3 * j + 1]; g.bz += f[8][3 * j + 2]; }
+    }
+}
+
+template <typename T, bool DRONE>
+__device__ __forceinline__ void store_adj(T *const *f, size_t j, const St<T> &g)
+{
+    if (f[0]) { f[0][2 * j] = g.px; f[0][2 * j + 1] = g.py; }
+    if (f[1]) f[1][j] = g.th;
+    if (f[2]) { f[2][2 * j] = g.vx; f[2][2 * j + 1] = g.vy; }
+    if (f[3]) f[3][j] = g.s;
+    if (f[4]) f[4][j] = g.w;
+    if (DRONE) {
+        if (f[5]) f[5][j] = g.z;
+        if (f[6]) f[6][j] = g.vz;
+        if (f[7]) { f[7][4 * j] = g.qx; f[7][4 * j + 1] = g.qy; f[7][4 * j + 2] = g.qz; f[7][4 * j + 3] = g.qw; }
+        if (f[8]) { f[8][3 * j] = g.bx; f[8][3 * j + 1] = g.by; f[8][3 * j + 2] = g.bz; }
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ void load_prm(const Args<T> &g, size_t row, int a, Prm<T> &p)
+{
+    const T *r = g.params + row * 22;
+    p.radius = r[0]; p.mass = r[1]; p.max_speed = r[2]; p.max_accel = r[3];
+    p.max_ang_vel = r[4]; p.max_ang_accel = r[5]; p.l_f = r[6]; p.l_r = r[7];
+    p.max_steer = r[8]; p.thrust_max = r[9]; p.arm = r[10]; p.ixx = r[11];
+    p.iyy = r[12]; p.izz = r[13]; p.kappa = r[14]; p.gravity = r[15]; p.min_speed = r[16];
+    p.shape = r[17]; p.hx = r[18]; p.hy = r[19];
+    p.gain_v = r[20]; p.gain_w = r[21];
+    p.tag = g.tag[a];
+    p.mode = g.mode[a];
+}
+
+template <typename T>
+__device__ __forceinline__ void load_act(const T *act, size_t j, int ad, T (&a)[4])
+{
+    const T *p = act + j * ad;
+    a[0] = p[0];
+    a[1] = ad > 1 ? p[1] : T(0);
+    a[2] = ad > 2 ? p[2] : T(0);
+    a[3] = ad > 3 ? p[3] : T(0);
+}
+
+// LDS staging of one substep.  Fields: 0 px, 1 py, 2 vx, 3 vy, 4 th, 5 s, 6 w, 7 Fx, 8 Fy,
+// then (drone) 9 z, 10 vz, 11..14 q, 15..17 br.  Each field is 64 consecutive scalars.
+constexpr int F_PX = 0, F_PY = 1, F_VX = 2, F_VY = 3, F_TH = 4, F_S = 5, F_W = 6, F_FX = 7,
+              F_FY = 8, NF_2D = 9, NF_DRONE = 18;
+
+// Neighbour lists of one agent as a bitmask over the env's agents, ascending bit =
+// ascending list order (neighbors.py:90-96).  Full scan over every pair of the env.
+template <typename T, int PA>
+__device__ __forceinline__ typename MaskT<PA>::type scan_all(const T *lx, const T *ly, int base,
+                                                             int A, int me, T px, T py, T t_nbr,
+                                                             T t_skin,
+                                                             typename MaskT<PA>::type &cand)
+{
+    typedef typename MaskT<PA>::type M;
+    M incl = 0, cd = 0;
+    (void)A;  // pad slots (b >= A) hold NaN positions and never pass the test
+#pragma unroll
+    for (int b = 0; b < PA; ++b) {
+        T dx = lx[base + b] - px, dy = ly[base + b] - py;
+        T d2 = dx * dx + dy * dy;
+        incl |= d2 <= t_nbr ? (M(1) << b) : M(0);
+        cd |= d2 <= t_skin ? (M(1) << b) : M(0);
+    }
+    const M self = ~(M(1) << me);
+    cand = cd & self;
+    return incl & self;
+}
+
+// Same membership, evaluated only on the skin candidates.
+template <typename T, int PA>
+__device__ __forceinline__ typename MaskT<PA>::type scan_cand(const T *lx, const T *ly, int base,
+                                                              T px, T py, T t_nbr,
+                                                              typename MaskT<PA>::type cand)
+{
+    typedef typename MaskT<PA>::type M;
+    M incl = 0;
+    while (cand) {
+        const int b = m_ctz(cand);
+        cand &= cand - 1;
+        T dx = lx[base + b] - px, dy = ly[base + b] - py;
+        T d2 = dx * dx + dy * dy;
+        incl |= d2 <= t_nbr ? (M(1) << b) : M(0);
+    }
+    return incl;
+}
+
+// First K members of an inclusion mask (the padded list of length K).
+template <typename M> __device__ __forceinline__ M cap_list(M incl, int K)
+{
+    if (m_popc(incl) <= K) return incl;
+    M rest = incl;
+    for (int i = 0; i < K; ++i) rest &= rest - 1;
+    return incl ^ rest;
+}
+
+// Per-lane context shared by the forward and backward kernels.
+template <typename T, int PA> struct Lane {
+    int lane, agent, base, env;
+    bool real;     // agent < A (lane holds a real agent slot of its env)
+    bool active;   // real and env < E
+    size_t idx;    // env * A + agent (clamped to a valid element for inactive lanes)
+    Prm<T> pr;
+    T dd;          // implicit damping denominator 1 + c*sub_dt/m (collisions.py:845)
+    T inv_dd;      // 1 / dd (adjoint arithmetic only)
+    Dv<T> ddv;     // dd as a prepared divisor (exact fp32 division by dd)
+};
+
+template <typename T, int PA>
+__device__ __forceinline__ void lane_init(const Cst<T> &C, const Args<T> &g, Lane<T, PA> &L)
+{
+    constexpr int EPW = 64 / PA;
+    L.lane = threadIdx.x;
+    L.agent = L.lane % PA;
+    L.base = L.lane - L.agent;
+    L.env = blockIdx.x * EPW + L.lane / PA;
+    L.real = L.agent < C.A;
+    L.active = L.real && L.env < C.E;
+    const int ag = L.real ? L.agent : 0;
+    const int ev = L.env < C.E ? L.env : 0;
+    L.idx = (size_t)ev * C.A + ag;
+    // per-env parameter tables (Stepper.set_agent_params_per_env) index [env, agent]
+    load_prm(g, C.per_env ? (size_t)ev * C.A + ag : (size_t)ag, ag, L.pr);
+    L.dd = T(1) + C.c * C.sub_dt / L.pr.mass;
+    L.inv_dd = T(1) / L.dd;
+    L.ddv = divisor(L.dd, true);
+}
+
+// Whether every real agent of this lane's env stayed within the skin budget.
+template <int PA> __device__ __forceinline__ bool env_all(bool ok, int base)
+{
+    const uint64_t bal = __ballot(ok);
+    const uint64_t full = PA == 64 ? ~0ull : ((1ull << PA) - 1ull);
+    return ((bal >> base) & full) == full;
+}
+
+// Contact + static forces of one substep, reading the env's positions/velocities from
+// the LDS slot `sl`.  Returns the uncapped inclusion mask (for the true count).
+// Obstacle angles as (cos, sin) per env slot of the wave, filled once per launch when
+// 64/PA envs x N obstacles fit (OCS_MAX pairs); NULL table otherwise.
+constexpr int OCS_MAX = 256;
+
+template <typename T, int PA>
+__device__ __forceinline__ const T *ob_trig_table(const Cst<T> &C, const Args<T> &g,
+                                                  const Lane<T, PA> &L, T *ocs)
+{
+    if (C.N <= 0 || (64 / PA) * C.N > OCS_MAX) return nullptr;
+    const int ew = L.lane / PA;
+    const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
+    for (int q = L.agent; q < C.N; q += PA) {
+        const T ang = g.obs.ang[eN + q];
+        ocs[2 * (ew * C.N + q)] = m_cos(ang);
+        ocs[2 * (ew * C.N + q) + 1] = m_sin(ang);
+    }
+    __syncthreads();
+    return ocs + 2 * ew * C.N;
+}
+
+// Box worlds (BOXES; false compiles the box paths out): `lbx` holds per lane the
+// footprint (shape, hx, hy rows of 64), `lcs` the cos and sin of every lane's heading
+// (rows of 64), and the slot `sl` also carries the headings and spins (F_TH, F_W rows).
+// `act` (nullable) receives the mask of listed neighbours whose box contact exerts a
+// force; for a box agent `om` / `wall` / `beyond` which of its first 64 obstacles, its
+// walls, and any later obstacle do: the contacts without force have zero derivatives.
+template <typename T, int PA, bool BOXES>
+__device__ __forceinline__ typename MaskT<PA>::type forces(
+    const Cst<T> &C, const Args<T> &g, const Lane<T, PA> &L, const T *sl, const T *lr,
+    const St<T> &st, int s, bool full, typename MaskT<PA>::type &cand, T &Fx, T &Fy,
+    const T *ocs = nullptr, const T *lbx = nullptr, const T *lcs = nullptr,
+    typename MaskT<PA>::type *act = nullptr, uint64_t *om = nullptr, bool *wall = nullptr,
+    bool *beyond = nullptr, T *tq = nullptr)
+{
+    const bool box_me = BOXES && L.pr.shape > T(0.5);
+    T me[6] = {st.px, st.py, st.th, st.vx, st.vy, st.w};
+    T cme = T(1), sme = T(0);
+    if (BOXES) {
+        cme = lcs[L.lane];
+        sme = lcs[64 + L.lane];
+    }
+    typename MaskT<PA>::type am = 0;
+    const bool wheel = BOXES && tq != nullptr;  // contact torques (wheel contacts)
+    T tau = T(0);
+    typedef typename MaskT<PA>::type M;
+    const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64, *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
+    M incl = 0;
+    T fx = T(0), fy = T(0);
+    if (C.collisions) {
+        if (full) {
+            M cd;
+            incl = scan_all<T, PA>(lx, ly, L.base, C.A, L.agent, st.px, st.py, C.t_nbr, C.t_skin, cd);
+            if (s == 0) cand = cd;
+        } else {
+            incl = scan_cand<T, PA>(lx, ly, L.base, st.px, st.py, C.t_nbr, cand);
+        }
+        M m = cap_list(incl, C.K);
+        const T ra = L.pr.radius;
+        const Foot<T> fa = {L.pr.shape, ra, L.pr.hx, L.pr.hy};
+        const T *lth = sl + F_TH * 64, *lw = sl + F_W * 64;
+        while (m) {
+            const int b = m_ctz(m);
+            m &= m - 1;
+            const int j = L.base + b;
+            T gx, gy;
+            if (BOXES && (box_me || lbx[j] > T(0.5))) {
+                // a pair with a box (collision_forces_box_kernel, collisions.py:1044-1052)
+                const Foot<T> fb = {lbx[j], lr[j], lbx[64 + j], lbx[128 + j]};
+                const T ob[6] = {lx[j], ly[j], lth[j], lvx[j], lvy[j], lw[j]};
+                agent_pair_force_box<T, T>(C, L.agent, b, fa, me, cme, sme, fb, ob, lcs[j],
+                                           lcs[64 + j], L.dd, gx, gy);
+                if (gx != T(0) || gy != T(0)) am |= typename MaskT<PA>::type(1) << b;
+                if (wheel)
+                    tau += pair_torque(C, L.agent, b, fa, me, cme, sme, fb, ob, lcs[j], lcs[64 + j],
+                                       gx, gy);
+            } else {
+                pair_force(C, st.px - lx[j], st.py - ly[j], st.vx - lvx[j], st.vy - lvy[j],
+                           ra + lr[j] + C.margin, L.dd, gx, gy);
+            }
+            fx += gx;
+            fy += gy;
+        }
+    }
+    T sx = T(0), sy = T(0);
+    if (box_me) {
+        // a box agent's obstacles and walls (_static_forces_shaped, collisions.py:950-996)
+        const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
+        box_static_forces<T, T>(C, g.obs, eN, ocs, L.pr.hx, L.pr.hy, me, cme, sme, L.dd, sx, sy,
+                                om, wall, beyond);
+        if (wheel)
+            tau = tau + box_static_torque(C, g.obs, eN, ocs, L.pr.hx, L.pr.hy, me, cme, sme, L.dd);
+    } else if (C.N > 0) {
+        const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
+        for (int o = 0; o < C.N; ++o) {
+            T gx, gy;
+            obstacle_force(C, g.obs, eN, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.dd, gx, gy,
+                           ocs);
+            sx += gx;
+            sy += gy;
+        }
+    }
+    if (C.soft_walls && !box_me) {
+        T gx, gy;
+        unsigned wb;
+        wall_force_axes(C, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv, gx, gy, wb);
+        sx += gx;
+        sy += gy;
+    }
+    Fx = fx + sx;
+    Fy = fy + sy;
+    if (act) *act = am;
+    if (wheel) *tq = tau;
+    return incl;
+}
+
+// ----------------------------------------------------------------- backward rollout
+
+template <typename T, bool DRONE>
+__device__ __forceinline__ void slot_put(T *sl, int lane, const St<T> &s)
+{
+    sl[F_PX * 64 + lane] = s.px; sl[F_PY * 64 + lane] = s.py;
+    sl[F_VX * 64 + lane] = s.vx; sl[F_VY * 64 + lane] = s.vy;
+    sl[F_TH * 64 + lane] = s.th; sl[F_S * 64 + lane] = s.s; sl[F_W * 64 + lane] = s.w;
+    if (DRONE) {
+        sl[9 * 64 + lane] = s.z; sl[10 * 64 + lane] = s.vz;
+        sl[11 * 64 + lane] = s.qx; sl[12 * 64 + lane] = s.qy;
+        sl[13 * 64 + lane] = s.qz; sl[14 * 64 + lane] = s.qw;
+        sl[15 * 64 + lane] = s.bx; sl[16 * 64 + lane] = s.by; sl[17 * 64 + lane] = s.bz;
+    }
+}
+
+template <typename T, bool DRONE>
+__device__ __forceinline__ void slot_get(const T *sl, int lane, St<T> &s)
+{
+    s.px = sl[F_PX * 64 + lane]; s.py = sl[F_PY * 64 + lane];
+    s.vx = sl[F_VX * 64 + lane]; s.vy = sl[F_VY * 64 + lane];
+    s.th = sl[F_TH * 64 + lane]; s.s = sl[F_S * 64 + lane]; s.w = sl[F_W * 64 + lane];
+    if (DRONE) {
+        s.z = sl[9 * 64 + lane]; s.vz = sl[10 * 64 + lane];
+        s.qx = sl[11 * 64 + lane]; s.qy = sl[12 * 64 + lane];
+        s.qz = sl[13 * 64 + lane]; s.qw = sl[14 * 64 + lane];
+        s.bx = sl[15 * 64 + lane]; s.by = sl[16 * 64 + lane]; s.bz = sl[17 * 64 + lane];
+    } else {
+        s.z = s.vz = s.qx = s.qy = s.qz = s.bx = s.by = s.bz = T(0);
+        s.qw = T(1);
+    }
+}
+
+// Whether agent `me` is among the first K members of inclusion mask `incl`.
+template <typename M> __device__ __forceinline__ bool in_list(M incl, int me, int K)
+{
+    return ((incl >> me) & M(1)) && m_popc(incl & ((M(1) << me) - M(1))) < K;
+}
+
+}  // namespace swarp

@@ -1,0 +1,10 @@
+// k_boxes.hip -- instantiates the generic rollout kernels with (DRONE, BOXES) = (false, true)
+// for the scalar type SWARP_T (the build compiles this unit once per dtype).
+#include "generic.hpp"
+
+namespace swarp {
+template void launch_fwd<SWARP_T, false, true>(int, const Cst<SWARP_T> &, const Args<SWARP_T> &,
+                                         hipStream_t);
+template void launch_bwd<SWARP_T, false, true>(int, const Cst<SWARP_T> &, const Args<SWARP_T> &,
+                                         size_t, hipStream_t);
+}  // namespace swarp

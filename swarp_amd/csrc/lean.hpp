@@ -1,6 +1,6 @@
 // lean.hpp -- specialised rollout kernels for fleets of holonomic agents in velocity
 // mode without obstacles (the reference's NavigationScenario default, BASELINE config 1/2).
-// Included by swarp_hip.hip; uses its Lane/mask helpers.
+// Instantiated by k_holo.hip; the host side sizes the tape with TapeRec.
 //
 // Same arithmetic, in the same order, as the generic kernels (so the results are
 // bit-identical), with what this fleet does not need removed:
@@ -13,6 +13,7 @@
 //     a scan are issued back to back and waited on once;
 //   * the next step's inputs are loaded one step ahead.
 #pragma once
+#include "common.hpp"
 
 namespace swarp {
 
@@ -596,6 +597,38 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
         if (f[2]) st2(f[2], i, gvx, gvy);
         if (f[3]) f[3][i] = T(0);
         if (f[4]) f[4][i] = T(0);
+    }
+}
+
+// ---------------------------------------------------------------------- launchers
+
+template <typename T, bool TAPE>
+void launch_holo_fwd(int PA, const Cst<T> &C, const Args<T> &a, const Tape<T> &tp, hipStream_t st)
+{
+    const size_t shm = 0;
+    const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
+        grid32((C.E + 1) / 2), grid64(C.E);
+    switch (PA) {
+    case 4: hipLaunchKernelGGL((k_holo_fwd<T, 4, TAPE>), grid4, dim3(64), shm, st, C, a, tp); break;
+    case 8: hipLaunchKernelGGL((k_holo_fwd<T, 8, TAPE>), grid8, dim3(64), shm, st, C, a, tp); break;
+    case 16: hipLaunchKernelGGL((k_holo_fwd<T, 16, TAPE>), grid16, dim3(64), shm, st, C, a, tp); break;
+    case 32: hipLaunchKernelGGL((k_holo_fwd<T, 32, TAPE>), grid32, dim3(64), shm, st, C, a, tp); break;
+    default: hipLaunchKernelGGL((k_holo_fwd<T, 64, TAPE>), grid64, dim3(64), shm, st, C, a, tp); break;
+    }
+}
+
+template <typename T, bool TAPE>
+void launch_holo_bwd(int PA, const Cst<T> &C, const Args<T> &a, const Tape<T> &tp, size_t shm,
+                     hipStream_t st)
+{
+    const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
+        grid32((C.E + 1) / 2), grid64(C.E);
+    switch (PA) {
+    case 4: hipLaunchKernelGGL((k_holo_bwd<T, 4, TAPE>), grid4, dim3(64), shm, st, C, a, tp); break;
+    case 8: hipLaunchKernelGGL((k_holo_bwd<T, 8, TAPE>), grid8, dim3(64), shm, st, C, a, tp); break;
+    case 16: hipLaunchKernelGGL((k_holo_bwd<T, 16, TAPE>), grid16, dim3(64), shm, st, C, a, tp); break;
+    case 32: hipLaunchKernelGGL((k_holo_bwd<T, 32, TAPE>), grid32, dim3(64), shm, st, C, a, tp); break;
+    default: hipLaunchKernelGGL((k_holo_bwd<T, 64, TAPE>), grid64, dim3(64), shm, st, C, a, tp); break;
     }
 }
 

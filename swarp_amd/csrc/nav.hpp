@@ -12,7 +12,9 @@
 // lanes of a wave64, so the env's lists and its reward reduction stay inside the wave
 // (positions and per-agent terms in LDS, no global atomics).  Observation rows are
 // assembled in LDS and leave as contiguous, coalesced stores when they fit.
-// Included by swarp_hip.hip (uses MaskT, scan_all, cap_list, Cst).
+// Instantiated by k_nav.hip.
+#pragma once
+#include "common.hpp"
 
 namespace swarp {
 
@@ -238,6 +240,19 @@ __global__ __launch_bounds__(64) void k_nav(const Cst<T> C, const NavArgs<T> g)
                 }
             }
         }
+    }
+}
+
+template <typename T>
+void launch_nav(int PA, const Cst<T> &C, const NavArgs<T> &g, unsigned dyn, hipStream_t st)
+{
+    const dim3 grid((C.E + (64 / PA) - 1) / (64 / PA));
+    switch (PA) {
+    case 4: hipLaunchKernelGGL((k_nav<T, 4>), grid, dim3(64), dyn, st, C, g); break;
+    case 8: hipLaunchKernelGGL((k_nav<T, 8>), grid, dim3(64), dyn, st, C, g); break;
+    case 16: hipLaunchKernelGGL((k_nav<T, 16>), grid, dim3(64), dyn, st, C, g); break;
+    case 32: hipLaunchKernelGGL((k_nav<T, 32>), grid, dim3(64), dyn, st, C, g); break;
+    default: hipLaunchKernelGGL((k_nav<T, 64>), grid, dim3(64), dyn, st, C, g); break;
     }
 }
 

@@ -9,20 +9,24 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "swarp_pmath.h"
+
 namespace swarp {
 
 __device__ __forceinline__ float m_sqrt(float x) { return sqrtf(x); }
 __device__ __forceinline__ double m_sqrt(double x) { return sqrt(x); }
-__device__ __forceinline__ float m_cos(float x) { return cosf(x); }
-__device__ __forceinline__ double m_cos(double x) { return cos(x); }
-__device__ __forceinline__ float m_sin(float x) { return sinf(x); }
-__device__ __forceinline__ double m_sin(double x) { return sin(x); }
-__device__ __forceinline__ float m_tan(float x) { return tanf(x); }
-__device__ __forceinline__ double m_tan(double x) { return tan(x); }
-__device__ __forceinline__ float m_atan(float x) { return atanf(x); }
-__device__ __forceinline__ double m_atan(double x) { return atan(x); }
-__device__ __forceinline__ float m_tanh(float x) { return tanhf(x); }
-__device__ __forceinline__ double m_tanh(double x) { return tanh(x); }
+// Transcendental functions: the portable double-precision evaluations of swarp_pmath.h
+// (float results rounded once), bit-identical to the CPU oracle's.
+__device__ __forceinline__ float m_cos(float x) { return (float)swarp_pcos((double)x); }
+__device__ __forceinline__ double m_cos(double x) { return swarp_pcos(x); }
+__device__ __forceinline__ float m_sin(float x) { return (float)swarp_psin((double)x); }
+__device__ __forceinline__ double m_sin(double x) { return swarp_psin(x); }
+__device__ __forceinline__ float m_tan(float x) { return (float)swarp_ptan((double)x); }
+__device__ __forceinline__ double m_tan(double x) { return swarp_ptan(x); }
+__device__ __forceinline__ float m_atan(float x) { return (float)swarp_patan((double)x); }
+__device__ __forceinline__ double m_atan(double x) { return swarp_patan(x); }
+__device__ __forceinline__ float m_tanh(float x) { return (float)swarp_ptanh((double)x); }
+__device__ __forceinline__ double m_tanh(double x) { return swarp_ptanh(x); }
 __device__ __forceinline__ float m_abs(float x) { return fabsf(x); }
 __device__ __forceinline__ double m_abs(double x) { return fabs(x); }
 

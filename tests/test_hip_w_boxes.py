@@ -83,6 +83,8 @@ def _check_box(name, cfgs, world, S, s0, acts, w, obs=None, E=None):
                     np.float64, obs=obs, E=E)
     hs, hg0, hga = hip
     os_, og0, oga = orc
+    print(f"\n{name} f64: states rel {rel(hs[..., :7], os_[..., :7]):.3e}, d/d actions rel "
+          f"{rel(hga, oga):.3e}, d/d state0 rel {rel(hg0[..., :7], og0[..., :7]):.3e}")
     assert rel(hs[..., :7], os_[..., :7]) <= 1e-10, f"{name} f64 states"
     assert rel(hga, oga) <= 1e-8, f"{name} f64 d/d actions {rel(hga, oga):.3e}"
     assert rel(hg0[..., :7], og0[..., :7]) <= 1e-8, f"{name} f64 d/d state0"
@@ -90,10 +92,13 @@ def _check_box(name, cfgs, world, S, s0, acts, w, obs=None, E=None):
     _, truth = _run(cfgs, world, S, s32.astype(np.float64), a32.astype(np.float64), w,
                     np.float64, obs=obs, E=E)
     hip, orc = _run(cfgs, world, S, s32, a32, w, np.float32, obs=obs, E=E)
+    print(f"{name} f32: states rel {rel(hip[0][..., :7], orc[0][..., :7]):.3e}")
     assert rel(hip[0][..., :7], orc[0][..., :7]) <= 1e-5, f"{name} f32 states"
     for k, what in ((2, "d/d actions"), (1, "d/d state0")):
         h, o, t = (x[k][..., :7] if k == 1 else x[k] for x in (hip, orc, truth))
         e_hip, e_orc = rel(h, t), rel(o, t)
+        print(f"{name} f32 {what}: HIP vs f32 oracle {rel(h, o):.3e}; vs f64: HIP {e_hip:.3e}, "
+              f"f32 oracle {e_orc:.3e}")
         assert e_hip <= max(2.0 * e_orc, 1e-5), (
             f"{name} f32 {what}: error vs f64 {e_hip:.3e}, the f32 oracle's {e_orc:.3e}")
 
