@@ -236,6 +236,22 @@ int swarp_edge_index(int32_t n_envs, int32_t n_agents, int32_t max_neighbors,
                      const int32_t *idx, const int32_t *cnt, const int64_t *offsets,
                      int64_t n_edges, int64_t *edge_index, void *stream);
 
+/* The COO radius graph without any allocation.  No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same edges in the same order as
+ * swarp_edge_index, but the prefix sums of cnt are computed inside -- their per-block
+ * partial sums live in a file-scope device array of 65536 int64 (512 KiB per GPU, held
+ * until the process ends), so n_envs * n_agents must be <= 16777216 (larger sizes are
+ * rejected) -- and the edge count is written to the device scalar *n_edges instead of
+ * being passed in.  edge_index is [2, capacity] int64: senders at edge_index[0 .. m),
+ * receivers at edge_index[capacity .. capacity + m), m = min(*n_edges, capacity); edges
+ * past capacity are dropped (compare *n_edges with capacity).  Counts are read as
+ * min(max(cnt, 0), max_neighbors).  Calls that overlap on one GPU share its array and
+ * race: serialise them (one stream, or events). */
+int swarp_edge_index_noalloc(int32_t n_envs, int32_t n_agents, int32_t max_neighbors,
+                             const int32_t *idx, const int32_t *cnt, int64_t capacity,
+                             int64_t *edge_index, int64_t *n_edges, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -160,6 +160,11 @@ SIGNATURES = {
          ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p],
         ctypes.c_int,
     ),
+    "swarp_edge_index_noalloc": (
+        [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
+         ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p],
+        ctypes.c_int,
+    ),
 }
 
 _lib = None

@@ -38,7 +38,8 @@ DTYPES = (("f32", "float", "1"), ("f64", "double", "0"))
 
 
 def units() -> list[tuple[str, Path, list[str]]]:
-    out = [("swarp_hip", CSRC / "swarp_hip.hip", [])]
+    out = [("swarp_hip", CSRC / "swarp_hip.hip", []),
+           ("coo_noalloc", CSRC / "coo_noalloc.hip", [])]
     for fam in FAMILIES:
         for tag, ctype, is32 in DTYPES:
             out.append((f"{fam}.{tag}", CSRC / f"{fam}.hip",

@@ -44,6 +44,11 @@ static int fail(const char *msg)
     return -1;
 }
 
+namespace swarp {
+// The error channel of the entry points defined in other units (coo_noalloc.hip).
+int set_error(const char *msg) { return msg[0] ? fail(msg) : (g_err[0] = 0, 0); }
+}  // namespace swarp
+
 static float h_sqrt(float x) { return sqrtf(x); }
 static double h_sqrt(double x) { return sqrt(x); }
 static float h_next(float x, float to) { return nextafterf(x, to); }
