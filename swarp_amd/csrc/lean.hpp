@@ -78,10 +78,61 @@ __device__ __forceinline__ typename MaskT<PA>::type lean_cand(const P2<T> *lp, i
     return in;
 }
 
+// ---------------------------------------------- skin scan of 16-agent envs by row rotation
+//
+// An env of PA = 16 agents is one DPP row of 16 lanes, and row_ror:k hands lane a the
+// value of lane (a - k) mod 16 without touching LDS.  The distance of a pair is the same
+// bits seen from either end (the subtraction only changes sign), so each lane evaluates 8
+// of its 15 pairs: offsets k = 1..8 towards (a - k), whose result is its bit for
+// neighbour a - k; lanes a + k (k = 1..7) evaluated the pairs towards a, and their compare
+// bits come back by row_ror:(16 - k).  Bits are collected relative to the lane (bit j =
+// neighbour (a + j) mod 16) and rotated into agent order at the end.
+// (bound_ctrl set: every source lane of a row rotation exists, and the flag lets the
+// compiler fold the move into its user as a DPP operand)
+template <int K> __device__ __forceinline__ float ror16(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                 0x120 + K, 0xf, 0xf, true));
+}
+template <int K> __device__ __forceinline__ uint32_t ror16u(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x120 + K, 0xf, 0xf, true);
+}
+
+template <int K>
+__device__ __forceinline__ void skin_offset(float px, float py, float t, uint32_t &own,
+                                            uint32_t &got)
+{
+    const float dx = ror16<K>(px) - px, dy = ror16<K>(py) - py;  // neighbour (a - K)
+    const float d2 = dx * dx + dy * dy;
+    const bool in = d2 <= t;
+    own |= in ? (1u << (16 - K)) : 0u;
+    if (K < 8) got |= ror16u<16 - K>(in ? (1u << K) : 0u);  // lane a + K's pair with a
+}
+
+// Mask (agent order, self excluded) of the env's agents within squared distance t, for
+// PA = 16 float lanes; `rot` = 16 - (agent index of this lane).
+__device__ __forceinline__ uint32_t skin_dpp16(float px, float py, float t, uint32_t rot)
+{
+    uint32_t own = 0u, got = 0u;
+    skin_offset<1>(px, py, t, own, got);
+    skin_offset<2>(px, py, t, own, got);
+    skin_offset<3>(px, py, t, own, got);
+    skin_offset<4>(px, py, t, own, got);
+    skin_offset<5>(px, py, t, own, got);
+    skin_offset<6>(px, py, t, own, got);
+    skin_offset<7>(px, py, t, own, got);
+    skin_offset<8>(px, py, t, own, got);
+    const uint32_t r = own | got;  // bit j: neighbour (a + j) mod 16
+    return __builtin_amdgcn_ubfe(r | (r << 16), rot, 16u);
+}
+
 // One substep of the force pass: neighbour lists (into `incl`) and the total force.
 // Also records which listed contacts are active (`act`) and the wall contact bits, the
-// branches the reverse pass follows.
-template <typename T, int PA>
+// branches the reverse pass follows.  SAT: contact_max_overlap > 0 (the tanh law).
+// For 16-agent float envs a full scan builds only the skin mask (skin_dpp16) and the
+// lists come from the candidate check, as on the other substeps.
+template <typename T, int PA, bool SAT>
 __device__ __forceinline__ void lean_forces(const Cst<T> &C, const P2<T> *lp, const P2<T> *lv,
                                             const T *lr, int base, int me, T ra,
                                             const Dv<T> &dd, T px, T py, T vx, T vy, bool full,
@@ -92,12 +143,17 @@ __device__ __forceinline__ void lean_forces(const Cst<T> &C, const P2<T> *lp, co
                                             T &Fx, T &Fy)
 {
     typedef typename MaskT<PA>::type M;
+    constexpr bool DPP16 = PA == 16 && sizeof(T) == 4;
     T fx = T(0), fy = T(0);
     incl = 0;
     act = 0;
     wbits = 0u;
     if (C.collisions) {
-        if (full) {
+        if (DPP16 && full) {
+            const M cd = (M)skin_dpp16((float)px, (float)py, (float)C.t_skin, 16u - (uint32_t)me);
+            if (first) cand = cd;
+            incl = lean_cand<T, PA>(lp, base, px, py, C.t_nbr, cd);
+        } else if (full) {
             M cd;
             lean_scan<T, PA>(lp, base, me, px, py, C, incl, cd);
             if (first) cand = cd;
@@ -111,7 +167,7 @@ __device__ __forceinline__ void lean_forces(const Cst<T> &C, const P2<T> *lp, co
             const int j = base + b;
             const P2<T> q = lp[j], w = lv[j];
             T gx, gy;
-            const bool on = pair_force_rec_r(C, px - q.x, py - q.y, vx - w.x, vy - w.y,
+            const bool on = pair_force_rec_r<T, SAT>(C, px - q.x, py - q.y, vx - w.x, vy - w.y,
                                              ra + lr[j] + C.margin, dd, gx, gy);
             act |= on ? (M(1) << b) : M(0);
             fx += gx;
@@ -119,7 +175,7 @@ __device__ __forceinline__ void lean_forces(const Cst<T> &C, const P2<T> *lp, co
         }
     }
     T sx = T(0), sy = T(0);
-    if (C.soft_walls) wall_force_axes(C, px, py, vx, vy, ra, dd, sx, sy, wbits);
+    if (C.soft_walls) wall_force_axes<T, SAT>(C, px, py, vx, vy, ra, dd, sx, sy, wbits);
     Fx = fx + sx;
     Fy = fy + sy;
 }
@@ -227,10 +283,12 @@ __device__ __forceinline__ X rec_get(const Chunk16 (&r)[NC], int off)
     return x;
 }
 
-template <typename T, int PA, bool TAPE>
+// SC: the substep count when fixed at compile time (the substep loops unroll), 0: C.S.
+template <typename T, int PA, bool TAPE, bool SAT, int SC>
 __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g,
                                                  const Tape<T> tp)
 {
+    const int S = SC > 0 ? SC : C.S;
     typedef typename MaskT<PA>::type M;
     typedef TapeW<PA> TW;
     typedef TapeRec<T, PA> TR;
@@ -268,7 +326,8 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
         unsigned wb = 0u, vneed = 0u;
         T D = T(0);
         bool ok = false;
-        for (int s = 0; s < C.S; ++s) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
             T Fx = T(0), Fy = T(0);
             if (C.needs_forces) {
                 if (C.collisions) {
@@ -277,8 +336,8 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
                     lv[lane] = v;
                     __syncthreads();
                 }
-                lean_forces<T, PA>(C, lp, lv, lr, base, me, ra, ddv, p.x, p.y, v.x, v.y,
-                                   s == 0 || !ok, s == 0, cand, incl, act, wb, Fx, Fy);
+                lean_forces<T, PA, SAT>(C, lp, lv, lr, base, me, ra, ddv, p.x, p.y, v.x, v.y,
+                                        s == 0 || !ok, s == 0, cand, incl, act, wb, Fx, Fy);
             }
             const T vnx = cnx + Fx * dtm, vny = cny + Fy * dtm;
             const T pnx = p.x + vnx * dt, pny = p.y + vny * dt;
@@ -286,7 +345,7 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
                 const M own = M(1) << me;
                 stage_put(tsb, lane, TR::OM + s * (int)sizeof(typename TW::type),
                           TW::pack(incl | ((wb & 1u) ? own : M(0)), act | ((wb & 2u) ? own : M(0))));
-                if (s + 1 < C.S) {
+                if (s + 1 < S) {
                     stage_put(tsb, lane, TR::OV + s * (int)sizeof(P2<T>), P2<T>{vnx, vny});
                     vneed |= (act != 0 || wb != 0u) ? 1u << TR::vchunk(s) : 0u;
                 }
@@ -327,10 +386,11 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
     }
 }
 
-template <typename T, int PA, bool TAPE>
+template <typename T, int PA, bool TAPE, bool SAT, int SC>
 __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g,
                                                  const Tape<T> tp)
 {
+    const int S = SC > 0 ? SC : C.S;
     typedef typename MaskT<PA>::type M;
     typedef TapeW<PA> TW;
     typedef typename TW::type W;
@@ -339,9 +399,9 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
     // per substep slot: P2 pos[64], P2 vel[64]; then inclusion masks [S][64], active-contact
     // masks [S][64]; then gF[64], r[64], dd[64]; then wall bits [S][64] (bytes)
     P2<T> *slot = (P2<T> *)smem;
-    M *lm = (M *)(slot + (size_t)C.S * 128);
-    M *la = lm + (size_t)C.S * 64;
-    P2<T> *lg = (P2<T> *)(la + (size_t)C.S * 64);
+    M *lm = (M *)(slot + (size_t)S * 128);
+    M *la = lm + (size_t)S * 64;
+    P2<T> *lg = (P2<T> *)(la + (size_t)S * 64);
     T *lr = (T *)(lg + 64);
     T *ldd = lr + 64;
     unsigned char *lw = (unsigned char *)(ldd + 64);
@@ -402,7 +462,7 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
         unsigned need = 0u;
 #pragma unroll
         for (int j = 0; j + 1 < TAPE_MAX_S; ++j)
-            if (j + 1 < C.S && vel_stored<PA>(rec_get<W>(r.c, TR::OM + j * (int)sizeof(W)), me))
+            if (j + 1 < S && vel_stored<PA>(rec_get<W>(r.c, TR::OM + j * (int)sizeof(W)), me))
                 need |= 1u << TR::vchunk(j);
 #pragma unroll
         for (int k = TR::NM; k < TR::NC; ++k) {
@@ -454,7 +514,7 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
             P2<T> pp = p, vv = v;
 #pragma unroll
             for (int s = 0; s < TAPE_MAX_S; ++s) {
-                if (s < C.S) {
+                if (s < S) {
                     P2<T> *sp = slot + s * 128;
                     sp[lane] = pp;
                     sp[64 + lane] = vv;
@@ -466,7 +526,7 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
                     lw[s * 64 + lane] = active ? (unsigned char)(((in & own) ? 1u : 0u) |
                                                                  ((ac & own) ? 2u : 0u))
                                                : (unsigned char)0;
-                    if (s + 1 < TAPE_MAX_S && s + 1 < C.S) {
+                    if (s + 1 < TAPE_MAX_S && s + 1 < S) {
                         // a stored velocity, or the command plus the exactly-zero force term
                         vv = (active && vel_stored<PA>(w, me))
                                  ? rec_get<P2<T>>(tc.c, TR::OV + s * (int)sizeof(P2<T>))
@@ -483,7 +543,7 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
         unsigned wb;
         T D = T(0);
         bool ok = false;
-        for (int s = 0; s < (TAPE ? 0 : C.S); ++s) {
+        for (int s = 0; s < (TAPE ? 0 : S); ++s) {
             P2<T> *sp = slot + s * 128;
             __syncthreads();
             sp[lane] = p;
@@ -491,8 +551,8 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
             __syncthreads();
             T Fx = T(0), Fy = T(0);
             if (C.needs_forces) {
-                lean_forces<T, PA>(C, sp, sp + 64, lr, base, me, ra, ddv, p.x, p.y, v.x, v.y,
-                                   s == 0 || !ok, s == 0, cand, incl, act, wb, Fx, Fy);
+                lean_forces<T, PA, SAT>(C, sp, sp + 64, lr, base, me, ra, ddv, p.x, p.y, v.x,
+                                        v.y, s == 0 || !ok, s == 0, cand, incl, act, wb, Fx, Fy);
             } else {
                 incl = 0;
                 act = 0;
@@ -524,7 +584,8 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
 
         // ---- reverse pass over the substeps
         T gcx = T(0), gcy = T(0);
-        for (int s = C.S - 1; s >= 0; --s) {
+#pragma unroll
+        for (int s = S - 1; s >= 0; --s) {
             const T gtx = gvx + gpx * dt, gty = gvy + gpy * dt;  // adjoint of v_new
             gcx += gtx;
             gcy += gty;
@@ -554,12 +615,12 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
                         const P2<T> gb = lg[j];
                         const T wx = (own ? gg.x : T(0)) - (rev ? gb.x : T(0));
                         const T wy = (own ? gg.y : T(0)) - (rev ? gb.y : T(0));
-                        pair_adj_active(C, q0.x - q.x, q0.y - q.y, w0.x - w.x, w0.y - w.y,
+                        pair_adj_active<T, SAT>(C, q0.x - q.x, q0.y - q.y, w0.x - w.x, w0.y - w.y,
                                         ra + lr[j] + C.margin, wx, wy, ipx, ipy, ivx, ivy);
                     }
                 }
                 if (C.soft_walls)
-                    wall_axes_adj(C, q0.x, q0.y, w0.x, w0.y, ra, dd, inv_dd, gFx, gFy,
+                    wall_axes_adj<T, SAT>(C, q0.x, q0.y, w0.x, w0.y, ra, dd, inv_dd, gFx, gFy,
                                   (unsigned)lw[s * 64 + lane], ipx, ipy, ivx, ivy);
             }
             gpx = ipx;
@@ -602,19 +663,35 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
 
 // ---------------------------------------------------------------------- launchers
 
+#define SWARP_HOLO_PA(KERNEL, SATV, SCV, SHM)                                                     \
+    switch (PA) {                                                                                 \
+    case 4: hipLaunchKernelGGL((KERNEL<T, 4, TAPE, SATV, SCV>), grid4, dim3(64), SHM, st, C, a, tp); break;   \
+    case 8: hipLaunchKernelGGL((KERNEL<T, 8, TAPE, SATV, SCV>), grid8, dim3(64), SHM, st, C, a, tp); break;   \
+    case 16: hipLaunchKernelGGL((KERNEL<T, 16, TAPE, SATV, SCV>), grid16, dim3(64), SHM, st, C, a, tp); break; \
+    case 32: hipLaunchKernelGGL((KERNEL<T, 32, TAPE, SATV, SCV>), grid32, dim3(64), SHM, st, C, a, tp); break; \
+    default: hipLaunchKernelGGL((KERNEL<T, 64, TAPE, SATV, SCV>), grid64, dim3(64), SHM, st, C, a, tp); break; \
+    }
+
+// The saturated contact law (contact_max_overlap > 0) selects the SAT instances; the others
+// carry no tanh code at all.  Without saturation, 1 and 4 substeps have instances with the
+// count fixed at compile time (the navigation configurations); other counts loop at run time.
+#define SWARP_HOLO_DISPATCH(KERNEL, SHM)                                                           \
+    if (C.max_overlap > T(0)) {                                                                   \
+        SWARP_HOLO_PA(KERNEL, true, 0, SHM)                                                       \
+    } else if (C.S == 4) {                                                                        \
+        SWARP_HOLO_PA(KERNEL, false, 4, SHM)                                                      \
+    } else if (C.S == 1) {                                                                        \
+        SWARP_HOLO_PA(KERNEL, false, 1, SHM)                                                      \
+    } else {                                                                                      \
+        SWARP_HOLO_PA(KERNEL, false, 0, SHM)                                                      \
+    }
+
 template <typename T, bool TAPE>
 void launch_holo_fwd(int PA, const Cst<T> &C, const Args<T> &a, const Tape<T> &tp, hipStream_t st)
 {
-    const size_t shm = 0;
     const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
         grid32((C.E + 1) / 2), grid64(C.E);
-    switch (PA) {
-    case 4: hipLaunchKernelGGL((k_holo_fwd<T, 4, TAPE>), grid4, dim3(64), shm, st, C, a, tp); break;
-    case 8: hipLaunchKernelGGL((k_holo_fwd<T, 8, TAPE>), grid8, dim3(64), shm, st, C, a, tp); break;
-    case 16: hipLaunchKernelGGL((k_holo_fwd<T, 16, TAPE>), grid16, dim3(64), shm, st, C, a, tp); break;
-    case 32: hipLaunchKernelGGL((k_holo_fwd<T, 32, TAPE>), grid32, dim3(64), shm, st, C, a, tp); break;
-    default: hipLaunchKernelGGL((k_holo_fwd<T, 64, TAPE>), grid64, dim3(64), shm, st, C, a, tp); break;
-    }
+    SWARP_HOLO_DISPATCH(k_holo_fwd, 0)
 }
 
 template <typename T, bool TAPE>
@@ -623,13 +700,11 @@ void launch_holo_bwd(int PA, const Cst<T> &C, const Args<T> &a, const Tape<T> &t
 {
     const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
         grid32((C.E + 1) / 2), grid64(C.E);
-    switch (PA) {
-    case 4: hipLaunchKernelGGL((k_holo_bwd<T, 4, TAPE>), grid4, dim3(64), shm, st, C, a, tp); break;
-    case 8: hipLaunchKernelGGL((k_holo_bwd<T, 8, TAPE>), grid8, dim3(64), shm, st, C, a, tp); break;
-    case 16: hipLaunchKernelGGL((k_holo_bwd<T, 16, TAPE>), grid16, dim3(64), shm, st, C, a, tp); break;
-    case 32: hipLaunchKernelGGL((k_holo_bwd<T, 32, TAPE>), grid32, dim3(64), shm, st, C, a, tp); break;
-    default: hipLaunchKernelGGL((k_holo_bwd<T, 64, TAPE>), grid64, dim3(64), shm, st, C, a, tp); break;
-    }
+    SWARP_HOLO_DISPATCH(k_holo_bwd, shm)
 }
+
+#undef SWARP_HOLO_DISPATCH
+
+#undef SWARP_HOLO_PA
 
 }  // namespace swarp

@@ -92,10 +92,9 @@ template <typename T> struct Obs {
 //
 // The build keeps fp32 division and sqrt correctly rounded; the compiler's general
 // sequences also scale tiny or huge operands and fix up special values.  Where the
-// operands are known to lie in a range in which those steps are identities, the
-// remaining steps are spelled out below, in the compiler's order, so the results are the
-// same bits with fewer instructions, and a division by a per-lane constant reuses one
-// refined reciprocal.  fp64 keeps the plain operators.
+// operands are known to lie in a range in which those steps are identities, shorter
+// sequences below give the same bits, and a division by a per-lane constant reuses one
+// prepared reciprocal.  fp64 keeps the plain operators.
 
 // Correctly rounded sqrt(x) for finite x >= 2^-96: hardware estimate, then the two
 // one-ulp residual corrections.
@@ -111,86 +110,102 @@ __device__ __forceinline__ float sqrt_rn_big(float x)
 }
 __device__ __forceinline__ double sqrt_rn_big(double x) { return sqrt(x); }
 
-// Refined reciprocal of a divisor d in [2^-60, 2^20] (one Newton step on the estimate).
-__device__ __forceinline__ float rcp_refined(float d)
+// Reciprocal of a float32 divisor in double precision: the hardware estimate (relative
+// error about 2^-24) and two Newton steps, which bring the relative error to the
+// rounding limit of double precision (2^-53; 2^-51 suffices below).
+__device__ __forceinline__ double rcp_d(float d)
 {
-    const float r0 = __builtin_amdgcn_rcpf(d);
-    const float e = __builtin_fmaf(-d, r0, 1.0f);
-    return __builtin_fmaf(e, r0, r0);
-}
-__device__ __forceinline__ double rcp_refined(double) { return 0.0; }
-
-// n / d correctly rounded given r = rcp_refined(d), for d in [2^-60, 2^20] and
-// 2^-100 <= |n| <= 2^30: two residual corrections of the quotient estimate.
-__device__ __forceinline__ float div_rn_core(float n, float d, float r)
-{
-    float q = n * r;
-    float e = __builtin_fmaf(-d, q, n);
-    q = __builtin_fmaf(e, r, q);
-    e = __builtin_fmaf(-d, q, n);
-    return __builtin_fmaf(e, r, q);
+    const double x = (double)d;
+    double y = __builtin_amdgcn_rcp(x);
+    double e = __builtin_fma(-x, y, 1.0);
+    y = __builtin_fma(y, e, y);
+    e = __builtin_fma(-x, y, 1.0);
+    return __builtin_fma(y, e, y);
 }
 
-// A divisor with its refined reciprocal.  `hi` bounds the numerators the short sequence
-// takes: 2^30 when d is in [2^-60, 2^20], else -1 (every division takes the general path).
+// A prepared divisor.  float: n / d = RN(n * y) evaluated in double precision with
+// y = rcp_d(d) is the correctly rounded float quotient whenever the quotient is not
+// subnormal.  Proof: with n = N 2^a, d = D 2^b (N, D < 2^24) and a float rounding
+// boundary m = M 2^c next to x = n / d (M odd, M < 2^25), x - m = (n - m d) / d where
+// n - m d is a non-zero multiple of 2^(b + c) >= n / (M D) (1 - 2^-23), so
+// |x - m| > 2^-49.01 |x|; the double product is within (2^-51 + 2^-53) |x| of x, hence on
+// the same side of every boundary (x itself is a boundary only for d a power of two, where
+// y and the product are exact).  Subnormal quotients (a coarser grid) are excluded by
+// sending |n| < 2^-100 (and NaN) to the general division when d <= 2^20; a divisor outside
+// [2^-60, 2^20] sends every numerator there.
 template <typename T> struct Dv {
-    T d, r, hi;
+    T d, lo;
+};
+template <> struct Dv<float> {
+    float d, lo;
+    double y;
 };
 template <typename T> __device__ __forceinline__ Dv<T> divisor(T d, bool ok)
 {
     Dv<T> v;
     v.d = d;
-    v.r = rcp_refined(d);
-    v.hi = (ok && d >= T(0x1p-60) && d <= T(0x1p20)) ? T(0x1p30) : T(-1);
+    v.lo = T(0);
+    return v;
+}
+__device__ __forceinline__ Dv<float> divisor(float d, bool ok)
+{
+    Dv<float> v;
+    v.d = d;
+    v.y = rcp_d(d);
+    v.lo = (ok && d >= 0x1p-60f && d <= 0x1p20f) ? 0x1p-100f : __builtin_inff();
     return v;
 }
 
 // A divisor known to lie in [2^-60, 2^20] whenever `ok` holds.
 template <typename T> __device__ __forceinline__ Dv<T> divisor_in_range(T d, bool ok)
 {
-    Dv<T> v;
+    return divisor(d, ok);
+}
+__device__ __forceinline__ Dv<float> divisor_in_range(float d, bool ok)
+{
+    Dv<float> v;
     v.d = d;
-    v.r = rcp_refined(d);
-    v.hi = ok ? T(0x1p30) : T(-1);
+    v.y = rcp_d(d);
+    v.lo = ok ? 0x1p-100f : __builtin_inff();
     return v;
 }
 
-// n / d, correctly rounded; zero, tiny, huge or NaN numerators take the general division.
+// n / d, correctly rounded; tiny or NaN numerators take the general division.
 template <typename T> __device__ __forceinline__ T div_rn(T n, const Dv<T> &v) { return n / v.d; }
 __device__ __forceinline__ float div_rn(float n, const Dv<float> &v)
 {
-    const float a = fabsf(n);
-    float q = div_rn_core(n, v.d, v.r);
-    if (__builtin_expect(!(a >= 0x1p-100f && a <= v.hi), 0)) q = n / v.d;
+    float q = (float)((double)n * v.y);
+    if (__builtin_expect(!(fabsf(n) >= v.lo), 0)) q = n / v.d;
     return q;
 }
 
 // ------------------------------------------------------------- contact law
 
-// _normal_coeff (swarp/core/collisions.py:87-105)
-template <typename T>
+// _normal_coeff (swarp/core/collisions.py:87-105).  SAT = false compiles the tanh
+// saturation out (callers that know contact_max_overlap == 0).
+template <typename T, bool SAT = true>
 __device__ __forceinline__ T normal_coeff(const Cst<T> &C, T ov, T vn, T dd)
 {
     T o = ov;
-    if (C.max_overlap > T(0)) o = C.max_overlap * m_tanh(ov / C.max_overlap);
+    if (SAT && C.max_overlap > T(0)) o = C.max_overlap * m_tanh(ov / C.max_overlap);
     return wmax((C.k * o - C.c * vn) / dd, T(0));
 }
 
 // normal_coeff with the damping denominator as a prepared divisor (same result)
-template <typename T>
+template <typename T, bool SAT = true>
 __device__ __forceinline__ T normal_coeff_r(const Cst<T> &C, T ov, T vn, const Dv<T> &dd)
 {
     T o = ov;
-    if (C.max_overlap > T(0)) o = C.max_overlap * m_tanh(ov / C.max_overlap);
+    if (SAT && C.max_overlap > T(0)) o = C.max_overlap * m_tanh(ov / C.max_overlap);
     return wmax(div_rn(C.k * o - C.c * vn, dd), T(0));
 }
 
-template <typename T>
+template <typename T, bool SAT = true>
 __device__ __forceinline__ void normal_coeff_adj(const Cst<T> &C, T ov, T vn, T dd, T g,
                                                  T &a_ov, T &a_vn)
 {
     T o = ov, slope = T(1);
-    if (C.max_overlap > T(0)) {
+    if (SAT && C.max_overlap > T(0)) {
         T th = m_tanh(ov / C.max_overlap);
         o = C.max_overlap * th;
         slope = T(1) - th * th;
@@ -241,8 +256,8 @@ __device__ __forceinline__ bool pair_force_rec(const Cst<T> &C, T dx, T dy, T rv
 }
 
 // pair_force_rec with the range-restricted exact arithmetic: the distance is at least
-// sqrt(eps2) and at most the neighbour radius, |d| <= distance; rdd = rcp_refined(dd).
-template <typename T>
+// sqrt(eps2) and at most the neighbour radius, |d| <= distance; dd is a prepared divisor.
+template <typename T, bool SAT = true>
 __device__ __forceinline__ bool pair_force_rec_r(const Cst<T> &C, T dx, T dy, T rvx, T rvy,
                                                  T md, const Dv<T> &dd, T &fx, T &fy)
 {
@@ -254,7 +269,7 @@ __device__ __forceinline__ bool pair_force_rec_r(const Cst<T> &C, T dx, T dy, T 
     if (ov > T(0)) {
         const Dv<T> ds = divisor_in_range(dist, C.fast_div != 0);  // sqrt(eps2) <= dist
         T nx = div_rn(dx, ds), ny = div_rn(dy, ds);
-        T coef = normal_coeff_r(C, ov, rvx * nx + rvy * ny, dd);
+        T coef = normal_coeff_r<T, SAT>(C, ov, rvx * nx + rvy * ny, dd);
         fx = coef * nx;
         fy = coef * ny;
         on = coef > T(0);
@@ -268,7 +283,7 @@ __device__ __forceinline__ double m_rsqrt(double x) { return rsqrt(x); }
 // Adjoint of one active contact pair, both forces at once (see pair_adj_combined), with
 // the branch already known from the recomputed forward pass: the arithmetic only has to
 // be accurate, so the distance comes from one reciprocal square root.
-template <typename T>
+template <typename T, bool SAT = true>
 __device__ __forceinline__ void pair_adj_active(const Cst<T> &C, T dx, T dy, T rvx, T rvy, T md,
                                                 T wx, T wy, T &adx, T &ady, T &arx, T &ary)
 {
@@ -280,7 +295,7 @@ __device__ __forceinline__ void pair_adj_active(const Cst<T> &C, T dx, T dy, T r
     const T vn = rvx * nx + rvy * ny;
     const T ov = md - dist;
     T o = ov, slope = T(1);
-    if (C.max_overlap > T(0)) {
+    if (SAT && C.max_overlap > T(0)) {
         const T th = m_tanh(ov / C.max_overlap);
         o = C.max_overlap * th;
         slope = T(1) - th * th;
@@ -384,20 +399,20 @@ __device__ __forceinline__ void pair_adj_combined(const Cst<T> &C, T dx, T dy, T
 // ------------------------------------------------------------------- walls
 
 // _wall_forces (swarp/core/collisions.py:746-778)
-template <typename T>
+template <typename T, bool SAT = true>
 __device__ __forceinline__ void wall_force(const Cst<T> &C, T px, T py, T vx, T vy, T ra, T dd,
                                            T &fx, T &fy)
 {
     T reach = ra + C.margin;
     T ax = T(0), ay = T(0), pen;
     pen = reach - (px - C.bmin_x);
-    if (pen > T(0)) ax += normal_coeff(C, pen, vx, dd);
+    if (pen > T(0)) ax += normal_coeff<T, SAT>(C, pen, vx, dd);
     pen = reach - (C.bmax_x - px);
-    if (pen > T(0)) ax += -normal_coeff(C, pen, -vx, dd);
+    if (pen > T(0)) ax += -normal_coeff<T, SAT>(C, pen, -vx, dd);
     pen = reach - (py - C.bmin_y);
-    if (pen > T(0)) ay += normal_coeff(C, pen, vy, dd);
+    if (pen > T(0)) ay += normal_coeff<T, SAT>(C, pen, vy, dd);
     pen = reach - (C.bmax_y - py);
-    if (pen > T(0)) ay += -normal_coeff(C, pen, -vy, dd);
+    if (pen > T(0)) ay += -normal_coeff<T, SAT>(C, pen, -vy, dd);
     fx = ax;
     fy = ay;
 }
@@ -407,7 +422,7 @@ __device__ __forceinline__ void wall_force(const Cst<T> &C, T px, T py, T vx, T 
 // `fx +=` terms of the reference is non-zero and the sum is that term alone (0 + x).
 // Falls back to the four-term form otherwise.  `bits` records which axes are in
 // contact with a positive coefficient (bit 0: x, bit 1: y) for the reverse pass.
-template <typename T>
+template <typename T, bool SAT = true>
 __device__ __forceinline__ void wall_force_axes(const Cst<T> &C, T px, T py, T vx, T vy, T ra,
                                                 const Dv<T> &dv, T &fx, T &fy, unsigned &bits)
 {
@@ -416,7 +431,7 @@ __device__ __forceinline__ void wall_force_axes(const Cst<T> &C, T px, T py, T v
     const T w2 = T(2) * reach * T(1.00001);
     bits = 0u;
     if (!(C.bmax_x - C.bmin_x >= w2) || !(C.bmax_y - C.bmin_y >= w2)) {
-        wall_force(C, px, py, vx, vy, ra, dd, fx, fy);
+        wall_force<T, SAT>(C, px, py, vx, vy, ra, dd, fx, fy);
         bits = 3u;  // reverse pass re-derives every side
         return;
     }
@@ -425,13 +440,13 @@ __device__ __forceinline__ void wall_force_axes(const Cst<T> &C, T px, T py, T v
     T ax = T(0), ay = T(0);
     if (pl > T(0) || pr > T(0)) {
         const bool lo = pl > T(0);
-        const T cf = normal_coeff_r(C, lo ? pl : pr, lo ? vx : -vx, dv);
+        const T cf = normal_coeff_r<T, SAT>(C, lo ? pl : pr, lo ? vx : -vx, dv);
         ax += lo ? cf : -cf;
         bits |= cf > T(0) ? 1u : 0u;
     }
     if (pb > T(0) || pt > T(0)) {
         const bool lo = pb > T(0);
-        const T cf = normal_coeff_r(C, lo ? pb : pt, lo ? vy : -vy, dv);
+        const T cf = normal_coeff_r<T, SAT>(C, lo ? pb : pt, lo ? vy : -vy, dv);
         ay += lo ? cf : -cf;
         bits |= cf > T(0) ? 2u : 0u;
     }
@@ -439,10 +454,14 @@ __device__ __forceinline__ void wall_force_axes(const Cst<T> &C, T px, T py, T v
     fy = ay;
 }
 
+template <typename T, bool SAT = true>
+__device__ __forceinline__ void wall_force_adj(const Cst<T> &C, T px, T py, T vx, T vy, T ra,
+                                               T dd, T gx, T gy, St<T> &a);
+
 // Reverse of wall_force_axes given its recorded contact bits; g * inv_dd = cotangent / dd.
 // For either wall of an axis d(coef)/d(p) = -k*slope/dd along the inward normal and
 // d(coef)/d(v) = -c/dd, so the side only enters through the overlap of the slope.
-template <typename T>
+template <typename T, bool SAT = true>
 __device__ __forceinline__ void wall_axes_adj(const Cst<T> &C, T px, T py, T vx, T vy, T ra,
                                               T dd, T inv_dd, T gx, T gy, unsigned bits,
                                               T &apx, T &apy, T &avx, T &avy)
@@ -452,14 +471,14 @@ __device__ __forceinline__ void wall_axes_adj(const Cst<T> &C, T px, T py, T vx,
     if (!(C.bmax_x - C.bmin_x >= w2) || !(C.bmax_y - C.bmin_y >= w2)) {
         St<T> a;
         a.px = apx; a.py = apy; a.vx = avx; a.vy = avy;
-        wall_force_adj(C, px, py, vx, vy, ra, dd, gx, gy, a);
+        wall_force_adj<T, SAT>(C, px, py, vx, vy, ra, dd, gx, gy, a);
         apx = a.px; apy = a.py; avx = a.vx; avy = a.vy;
         return;
     }
     if (bits & 1u) {
         const T pl = reach - (px - C.bmin_x), pr = reach - (C.bmax_x - px);
         T slope = T(1);
-        if (C.max_overlap > T(0)) {
+        if (SAT && C.max_overlap > T(0)) {
             const T th = m_tanh((pl > T(0) ? pl : pr) / C.max_overlap);
             slope = T(1) - th * th;
         }
@@ -470,7 +489,7 @@ __device__ __forceinline__ void wall_axes_adj(const Cst<T> &C, T px, T py, T vx,
     if (bits & 2u) {
         const T pb = reach - (py - C.bmin_y), pt = reach - (C.bmax_y - py);
         T slope = T(1);
-        if (C.max_overlap > T(0)) {
+        if (SAT && C.max_overlap > T(0)) {
             const T th = m_tanh((pb > T(0) ? pb : pt) / C.max_overlap);
             slope = T(1) - th * th;
         }
@@ -480,7 +499,7 @@ __device__ __forceinline__ void wall_axes_adj(const Cst<T> &C, T px, T py, T vx,
     }
 }
 
-template <typename T>
+template <typename T, bool SAT>
 __device__ __forceinline__ void wall_force_adj(const Cst<T> &C, T px, T py, T vx, T vy, T ra,
                                                T dd, T gx, T gy, St<T> &a)
 {
@@ -488,28 +507,28 @@ __device__ __forceinline__ void wall_force_adj(const Cst<T> &C, T px, T py, T vx
     pen = reach - (px - C.bmin_x);
     if (pen > T(0)) {
         T o = T(0), v = T(0);
-        normal_coeff_adj(C, pen, vx, dd, gx, o, v);
+        normal_coeff_adj<T, SAT>(C, pen, vx, dd, gx, o, v);
         a.px -= o;
         a.vx += v;
     }
     pen = reach - (C.bmax_x - px);
     if (pen > T(0)) {
         T o = T(0), v = T(0);
-        normal_coeff_adj(C, pen, -vx, dd, -gx, o, v);
+        normal_coeff_adj<T, SAT>(C, pen, -vx, dd, -gx, o, v);
         a.px += o;
         a.vx -= v;
     }
     pen = reach - (py - C.bmin_y);
     if (pen > T(0)) {
         T o = T(0), v = T(0);
-        normal_coeff_adj(C, pen, vy, dd, gy, o, v);
+        normal_coeff_adj<T, SAT>(C, pen, vy, dd, gy, o, v);
         a.py -= o;
         a.vy += v;
     }
     pen = reach - (C.bmax_y - py);
     if (pen > T(0)) {
         T o = T(0), v = T(0);
-        normal_coeff_adj(C, pen, -vy, dd, -gy, o, v);
+        normal_coeff_adj<T, SAT>(C, pen, -vy, dd, -gy, o, v);
         a.py += o;
         a.vy -= v;
     }
