@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 8
+#define SWARP_ABI_VERSION 9
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -87,6 +87,10 @@ typedef struct swarp_desc {
        the reference's *_per_env kernel variants); 0: [n_agents, 22] shared by every env.
        The _ob (movable-body) entry points reject it. */
     int32_t params_per_env;
+    /* The fleet's top speed (the largest max_speed of its parameter rows; <= 0 reads as
+       1).  Sizes the per-step skin of the neighbour search, which only affects speed:
+       the lists stay exact whatever the agents do. */
+    double skin_speed;
 } swarp_desc_t;
 
 /* The nine state fields.  A NULL field means "not provided": an input adjoint that
@@ -217,6 +221,12 @@ typedef struct swarp_nav {
     uint8_t *truncated;                      /* [E] step_count >= max_steps after the
                                                 increment (NULL = not written) */
     int32_t max_steps;                       /* <= 0: no time limit */
+    const void *radius;                      /* [A] radii of the touching test: the
+                                                scenario's static agent radius, which
+                                                the reference hands its navigation
+                                                kernels even when parameters are
+                                                randomized per env (navigation.py:556-557);
+                                                NULL: column P_RADIUS of desc->params */
 } swarp_nav_t;
 
 /* The navigation scenario's per-step pass in one launch: radius lists of `pos`
@@ -224,7 +234,7 @@ typedef struct swarp_nav {
  * shaping, on-goal / overflow flags, reward and done.  Replaces the reference's no-grad
  * fast path: the NeighborGrid build + nav_obs_kernel + nav_reward_kernel
  * (swarp/scenarios/navigation.py:539-650, swarp/scenarios/navigation_kernels.py:41-243).
- * Radii for the touching test are column P_RADIUS of desc->params. */
+ * Radii for the touching test: nav->radius (else column P_RADIUS of desc->params). */
 int swarp_nav_obs(const swarp_desc_t *desc, const swarp_nav_t *nav, void *stream);
 
 /* COO radius graph from padded lists: replaces NeighborGrid.edge_index's torch mask ops

@@ -832,7 +832,10 @@ static void FN(wheel_contact)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(a
     if (torque < zero) excess = -excess;
     REAL w_drive = out->w;
     if (torque * out->w < zero && FABS(torque) > C->turn_cap) w_drive = zero;
-    out->th = in->th + (w_drive + excess * (dt / inertia)) * dt;
+    /* a disc has no footprint inertia: the torque term is skipped when there is no
+       excess (the reference's 0 * (dt / 0) = NaN), keeping the signed zero */
+    REAL turn = excess != zero ? excess * (dt / inertia) : excess;
+    out->th = in->th + (w_drive + turn) * dt;
 }
 
 /* ------------------------------------------------------------ the footprint clamp */

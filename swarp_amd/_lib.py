@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 F32, F64 = 0, 1
 EULER, RK4 = 0, 1
 
@@ -69,6 +69,7 @@ class SwarpDesc(ctypes.Structure):
         ("lat_grip", ctypes.c_double),
         ("turn_cap", ctypes.c_double),
         ("params_per_env", ctypes.c_int32),
+        ("skin_speed", ctypes.c_double),
     ]
 
 
@@ -98,6 +99,7 @@ class SwarpNav(ctypes.Structure):
         ("collision_penalty", ctypes.c_double), ("final_reward", ctypes.c_double),
         ("step_count", ctypes.c_void_p), ("truncated", ctypes.c_void_p),
         ("max_steps", ctypes.c_int32),
+        ("radius", ctypes.c_void_p),
     ]
 
 

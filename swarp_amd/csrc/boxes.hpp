@@ -681,7 +681,11 @@ __device__ __forceinline__ void wheel_contact(const Cst<T> &C, const Prm<T> &P, 
     if (torque < zero) excess = -excess;
     T w_drive = o.w;
     if (torque * o.w < zero && m_abs(torque) > C.turn_cap) w_drive = zero;
-    o.th = in.th + (w_drive + excess * (dt / inertia)) * dt;
+    // a disc has no footprint inertia (0): skip the torque term when there is no excess
+    // torque -- the reference's 0 * (dt / 0) -- keeping the signed zero, so the bits equal
+    // the reference's wherever it is finite
+    const T turn = excess != zero ? excess * (dt / inertia) : excess;
+    o.th = in.th + (w_drive + turn) * dt;
 }
 
 // ------------------------------------------------------------------ reverse helpers

@@ -20,6 +20,7 @@ namespace swarp {
 
 template <typename T> struct NavArgs {
     const T *pos, *vel, *th, *om, *goal, *params;
+    const T *radius;       // [A] static radii of the touching test (NULL: params column)
     const uint8_t *rmask;  // [E] just-reset envs (NULL: none)
     T *prev, *obs, *touch, *dist, *shaping, *reward;
     int32_t *idx, *cnt, *tru;
@@ -75,9 +76,11 @@ __global__ __launch_bounds__(64) void k_nav(const Cst<T> C, const NavArgs<T> g)
         vx = g.vel[2 * i];
         vy = g.vel[2 * i + 1];
     }
-    // P_RADIUS, the static radius (per env with per-env parameter tables)
-    const T ra = g.params[((C.per_env ? (size_t)(env < C.E ? env : 0) * C.A : 0) +
-                           (real ? agent : 0)) * 22];
+    // the static radius: the scenario's per-agent radius (the reference's navigation
+    // kernels take it even under per-env randomization), else column P_RADIUS
+    const T ra = g.radius ? g.radius[real ? agent : 0]
+                          : g.params[((C.per_env ? (size_t)(env < C.E ? env : 0) * C.A : 0) +
+                                      (real ? agent : 0)) * 22];
     lx[lane] = px;
     ly[lane] = py;
     lvx[lane] = vx;

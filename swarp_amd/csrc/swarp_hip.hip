@@ -154,8 +154,7 @@ static double skin_of(const swarp_desc_t *d)
     // Candidate-list skin: room for (S-1) substeps of motion of both agents of a pair
     // at about 1.5x the fleet's top speed.  Only speed depends on it; exactness does not.
     if (d->substeps < 2) return 0.0;
-    double vmax = 1.0;
-    if (getenv("SWARP_SKIN_VMAX")) vmax = atof(getenv("SWARP_SKIN_VMAX"));
+    const double vmax = d->skin_speed > 0.0 ? d->skin_speed : 1.0;
     return 2.0 * 1.5 * vmax * (d->substeps - 1) * (d->dt / d->substeps);
 }
 
@@ -432,6 +431,7 @@ template <typename T> static int nav_obs(const swarp_desc_t *d, const swarp_nav_
     g.om = (const T *)v->ang_vel;
     g.goal = (const T *)v->goals;
     g.params = (const T *)d->params;
+    g.radius = (const T *)v->radius;
     g.rmask = v->reset_mask;
     g.prev = (T *)v->prev_dist;
     g.obs = (T *)v->obs;

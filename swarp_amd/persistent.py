@@ -70,7 +70,11 @@ class StepGraph:
     def _token(self) -> tuple:
         w = self.world
         d = w.stepper.desc(w.n_envs, w.act_dim)
-        base = (w.stepper.mutation_version, ctypes.addressof(d), w.stepper.params.floats.data_ptr())
+        pe = w.stepper.params_per_env
+        # every device address the captured kernels bake in: the descriptor, the shared
+        # parameter rows and the per-env table (a re-randomization may reallocate it)
+        base = (w.stepper.mutation_version, ctypes.addressof(d), w.stepper.params.floats.data_ptr(),
+                pe.data_ptr() if pe is not None else 0)
         extra = self._extra_token()
         return base + (extra() if extra is not None else ())
 

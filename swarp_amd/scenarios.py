@@ -369,6 +369,9 @@ class NavigationScenario(Scenario):
         nav.pos, nav.vel = p(state.pos), p(state.vel)
         nav.theta, nav.ang_vel = p(state.theta), p(state.ang_vel)
         nav.goals = p(w.goals)
+        # the touching test uses the static radius, as the torch path and the
+        # reference's navigation kernels do (navigation.py:556-557)
+        nav.radius = p(w.agent_radius)
         nav.reset_mask = None if reset_mask is None else p(reset_mask)
         nav.prev_dist = p(self._prev_dist)
         nav.nbr_idx, nav.nbr_cnt = p(grid.neighbor_idx), p(grid.neighbor_count)

@@ -23,6 +23,7 @@ from .config import (
     ControlMode,
     DynamicsModel,
     NUM_PARAMS,
+    P_MAX_SPEED,
     P_RADIUS,
     P_SHAPE,
     Integrator,
@@ -213,11 +214,12 @@ class Stepper:
                     f"per-env radius up to {max_r} needs neighbor_radius >= {reach} "
                     f"(= 2 * max per-env radius + margin), but neighbor_radius="
                     f"{self.neighbor_radius}; set WorldConfig.neighbor_radius accordingly.")
-        first = cur is None
         self.params_per_env = t.to(device=self.device, dtype=self.dtype).contiguous()
+        self._pe_skin_speed = float(t[..., P_MAX_SPEED].max())
         self._descs.clear()
-        if first:
-            self.mutation_version += 1
+        # a new table is a new device address: descriptors and captured graphs that baked
+        # the old one must be rebuilt
+        self.mutation_version += 1
 
     # --------------------------------------------------------------- obstacles
 
@@ -368,8 +370,16 @@ class Stepper:
         d.lin_damping = float(self.world.obstacle_linear_damping)
         d.ang_damping = float(self.world.obstacle_angular_damping)
         d.integrator = _lib.RK4 if self.world.integrator == Integrator.RK4 else _lib.EULER
+        d.skin_speed = self._skin_speed()
         self._descs[key] = d
         return d
+
+    def _skin_speed(self) -> float:
+        """The fleet's top speed (largest max_speed of the rows in use): sizes the
+        neighbour search's per-step skin (speed only; the lists are exact regardless)."""
+        if self.params_per_env is not None:
+            return self._pe_skin_speed  # recorded at install (no device read here)
+        return float(max(c.max_speed for c in self.configs))
 
     # --------------------------------------------------------------- neighbours
 

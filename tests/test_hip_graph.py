@@ -101,3 +101,30 @@ def test_graph_recaptures_when_obstacles_move_pointers():
         with torch.no_grad():
             _same(ge.step(_acts(E, A, t)), ee.step(_acts(E, A, t)), f"step {t}")
     assert ge._graph.captures == n0 + 2
+
+
+def test_graph_follows_a_reinstalled_per_env_table():
+    """Re-randomizing per-env parameters with a host (numpy) table reallocates the device
+    table: the next replay recaptures instead of replaying the freed address, and every
+    step equals the eager environment's."""
+    import numpy as np
+
+    from swarp_amd import per_env_float_template
+    from swarp_amd.config import P_MAX_SPEED, P_RADIUS
+
+    E, A = 64, 8
+    ge, ee = _pair(E, A, max_steps=100, neighbor_radius=0.2)
+    rng = np.random.default_rng(4)
+    ge.reset()
+    ee.reset()
+    for t in range(9):
+        if t % 3 == 0:
+            table = per_env_float_template(ge.world.agent_configs, E)
+            table[..., P_RADIUS] = rng.uniform(0.03, 0.06, size=(E, A))
+            table[..., P_MAX_SPEED] = rng.uniform(0.5, 1.5, size=(E, A))
+            for env in (ge, ee):
+                env.world.stepper.set_agent_params_per_env(table)
+        with torch.no_grad():
+            _same(ge.step(_acts(E, A, t)), ee.step(_acts(E, A, t)), f"step {t}")
+        assert torch.equal(ge.world.state.pos, ee.world.state.pos), t
+    assert ge._graph.captures >= 2 + 2 * 3 - 2  # recaptured after each reallocation

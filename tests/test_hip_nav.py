@@ -164,3 +164,41 @@ def test_grad_step_takes_the_torch_path():
     with torch.no_grad():
         env.step(torch.zeros(16, 4, 2, device="cuda"))
     assert env.scenario._fresh == "fused"
+
+
+def test_fused_pass_uses_static_radius_under_per_env_tables():
+    """With radii randomized per env (Stepper.set_agent_params_per_env) the touching count
+    still uses the scenario's static radius, as the reference's navigation kernels receive
+    it (swarp/scenarios/navigation.py:556-557) and as the torch path computes it: fused ==
+    torch path == oracle/nav.py with the static radius."""
+    from swarp_amd import per_env_float_template
+    from swarp_amd.config import P_RADIUS
+
+    E, A = 48, 16
+    ef = _env(E, A, fused=True, neighbor_radius=0.4)
+    et = _env(E, A, fused=False, neighbor_radius=0.4)
+    rng = np.random.default_rng(12)
+    table = per_env_float_template(ef.world.agent_configs, E)
+    table[..., P_RADIUS] = rng.uniform(0.02, 0.15, size=(E, A))
+    for env in (ef, et):
+        env.world.stepper.set_agent_params_per_env(table)
+    ef.reset()
+    et.reset()
+    g = torch.Generator(device="cuda").manual_seed(2)
+    for t in range(4):
+        a = torch.rand(E, A, 2, device="cuda", generator=g) * 2 - 1
+        with torch.no_grad():
+            rf = ef.step(a)
+            rt = et.step(a)
+        assert torch.equal(ef.world.state.pos, et.world.state.pos), t
+        assert torch.equal(rf[4]["collisions"], rt[4]["collisions"]), t
+        torch.testing.assert_close(rf[1], rt[1], rtol=0, atol=2e-6)
+        s = ef.world.state
+        o = nav_pass(_np(s.pos), _np(s.vel), _np(s.theta), _np(s.ang_vel), _np(ef.world.goals),
+                     _np(ef.world.agent_radius), float(ef.world.stepper.neighbor_radius),
+                     ef.world.stepper.world.max_neighbors, ef.scenario._k_obs,
+                     np.zeros((E, A), np.float32), None, 0, 1, ef.scenario.pos_shaping_factor,
+                     ef.scenario.goal_tolerance, ef.scenario.collision_penalty,
+                     ef.scenario.final_reward, ef.scenario.shared_reward)
+        assert np.array_equal(_np(rf[4]["collisions"]), o["touching"]), t
+    assert rf[4]["collisions"].sum() > 0  # contacts happened (the check is not vacuous)

@@ -191,6 +191,39 @@ def test_wheel_contacts_forward_and_no_reverse():
         rollout(st, state, torch.zeros(T, E, A, 2, device="cuda", requires_grad=True))
 
 
+def test_wheel_contacts_disc_diff_drive():
+    """Disc diff-drive agents (velocity and servo control) under wheel_contacts: no
+    footprint inertia, so the reference's torque term would be 0 * inf = NaN
+    (swarp/dynamics/kernels.py:1379-1386); here it is skipped when there is no excess
+    torque, headings stay finite, and HIP equals the oracle (fp64 1e-10, fp32 1e-5)."""
+    from hip_helpers import state_to16, to_torch_state
+    from oracle.oracle import Oracle
+    from cases import oracle_cfg, params_of
+    from swarp_amd import rollout
+
+    E, A, T, S = 32, 6, 8, 2
+    rng = np.random.default_rng(41)
+    cfgs = ([AgentConfig(model=DynamicsModel.DIFF_DRIVE, radius=0.05) for _ in range(3)]
+            + [AgentConfig(model=DynamicsModel.DIFF_DRIVE, ctrl_mode=ControlMode.SERVO,
+                           radius=0.05, max_speed=1.5, max_accel=2.0) for _ in range(3)])
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02,
+                        bounds=(-0.3, 0.3, -0.3, 0.3), max_neighbors=6, wheel_contacts=True,
+                        wheel_lateral_friction=0.3, wheel_turn_torque=0.02)
+    s0 = _state(E, A, rng, 0.25, np.float64)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2))
+    for dt_np, td, tol in ((np.float64, torch.float64, 1e-10), (np.float32, torch.float32, 1e-5)):
+        st = make_stepper(cfgs, world, 0.05, S, td)
+        state = to_torch_state(s0.astype(dt_np), td, False, 5)
+        with torch.no_grad():
+            _, traj = rollout(st, state, torch.tensor(acts.astype(dt_np), dtype=td, device="cuda"))
+        hs = np.stack([state_to16(x) for x in traj])
+        cfg = oracle_cfg(cfgs, world, 0.05, S, E, 2)
+        p, t, m = params_of(cfgs)
+        os_ = Oracle(dt_np).rollout(cfg, p, t, m, None, s0.astype(dt_np), acts.astype(dt_np))
+        assert np.isfinite(hs).all() and np.isfinite(os_).all()
+        assert rel(hs[..., :7], os_[..., :7]) <= tol, f"{np.dtype(dt_np).name} states"
+
+
 def test_per_env_parameter_tables():
     """Stepper.set_agent_params_per_env (swarp/core/stepper.py:493-575; the *_per_env
     kernels): masses, radii, speed and turn limits randomized per env.  Each env of the HIP

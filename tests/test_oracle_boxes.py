@@ -434,3 +434,29 @@ def test_fd_servo():
     acts = rng.uniform(-2, 2, size=(3, 2, 3, 2))
     _fd_check(cfgs, _world(collision_c=1.0, bounds=(-0.3, 0.3, -0.3, 0.3)), 0.05, 2, s0, acts,
               fields=(0, 1, 2, 3, 4, 5, 6))
+
+
+def test_wheel_contacts_disc_diff_drive_stays_finite():
+    """A disc diff-drive agent has no footprint inertia (half extents 0).  Under
+    wheel_contacts the reference evaluates excess * (dt / inertia), which is 0 * inf = NaN
+    whenever the contact torque stays below turn_cap (swarp/dynamics/kernels.py:1379-1386);
+    the restatement skips the term when there is no excess, so headings stay finite and
+    equal the plain step's heading update."""
+    E, A, T, S = 6, 4, 5, 2
+    cfgs = [AgentConfig(model=DynamicsModel.DIFF_DRIVE, radius=0.05) for _ in range(A)]
+    world = _world(bounds=(-0.4, 0.4, -0.4, 0.4), max_neighbors=4, wheel_contacts=True,
+                   wheel_lateral_friction=0.3, wheel_turn_torque=0.02)
+    rng = np.random.default_rng(3)
+    s0 = pack_state({"pos": rng.uniform(-0.12, 0.12, size=(E, A, 2)),
+                     "theta": rng.uniform(-3, 3, size=(E, A))})
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2))
+    cfg = oracle_cfg(cfgs, world, 0.05, S, E, 2)
+    p, t, m = params_of(cfgs)
+    st = Oracle(np.float64).rollout(cfg, p, t, m, None, s0, acts)
+    assert np.isfinite(st).all()
+    # discs feel no contact torque, so the heading advances by the commanded turn rate
+    # exactly as without wheel contacts
+    plain = oracle_cfg(cfgs, _world(bounds=(-0.4, 0.4, -0.4, 0.4), max_neighbors=4), 0.05, S,
+                       E, 2)
+    ref = Oracle(np.float64).rollout(plain, p, t, m, None, s0, acts)
+    np.testing.assert_array_equal(st[..., 2], ref[..., 2])
