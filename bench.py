@@ -18,6 +18,7 @@ bounded sample of the same workload on this host's cores.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -286,6 +287,7 @@ def run_other(args):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    gc.collect()  # the set-up's garbage: a full collection would land in the timed steps
     ag.KERNEL_EVENTS = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -350,6 +352,7 @@ def main():
     for _ in range(args.warmup):
         bptt_step()
     torch.cuda.synchronize()
+    gc.collect()  # the set-up's garbage: a full collection would land in the timed steps
     ag.KERNEL_EVENTS = []
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -369,6 +372,7 @@ def main():
         for _ in range(args.warmup):
             rollout(stepper, state, acts)
         torch.cuda.synchronize()
+        gc.collect()
         t1 = time.perf_counter()
         for _ in range(args.steps):
             rollout(stepper, state, acts)

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 9
+#define SWARP_ABI_VERSION 10
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -91,6 +91,13 @@ typedef struct swarp_desc {
        1).  Sizes the per-step skin of the neighbour search, which only affects speed:
        the lists stay exact whatever the agents do. */
     double skin_speed;
+    /* The fleet's dynamics models and control modes as bit sets: bit m of fleet_models
+       set when some agent's model_tag is m (DynamicsModel, swarp/dynamics/base.py:12-19),
+       bit c of fleet_modes when some agent's ctrl_mode is c (ControlMode, :57-78).  They
+       select kernel instances compiled without the absent models and modes, so they must
+       describe model_tag / ctrl_mode truthfully; 0 reads as "any" (the general
+       instances). */
+    int32_t fleet_models, fleet_modes;
 } swarp_desc_t;
 
 /* The nine state fields.  A NULL field means "not provided": an input adjoint that

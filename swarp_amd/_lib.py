@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 F32, F64 = 0, 1
 EULER, RK4 = 0, 1
 
@@ -70,6 +70,8 @@ class SwarpDesc(ctypes.Structure):
         ("turn_cap", ctypes.c_double),
         ("params_per_env", ctypes.c_int32),
         ("skin_speed", ctypes.c_double),
+        ("fleet_models", ctypes.c_int32),
+        ("fleet_modes", ctypes.c_int32),
     ]
 
 

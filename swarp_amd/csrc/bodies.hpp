@@ -375,11 +375,12 @@ __device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
 
 // ------------------------------------------------------------------ forward rollout
 
-template <typename T, int PA>
-__global__ __launch_bounds__(64) void k_body_fwd(const Cst<T> C, const Args<T> g,
+template <typename T, int PA, unsigned F>
+__global__ __launch_bounds__(64) void k_body_fwd(const Cst<T> Cin, const Args<T> g,
                                                  const ObTab<T> tb, const ObIO<T> io)
 {
     typedef typename MaskT<PA>::type M;
+    const Cst<T> C = fold_cst<F>(Cin);
     constexpr int EPW = 64 / PA;
     __shared__ T sl[4 * 64];                         // px py vx vy of the substep
     __shared__ T lr[64];                             // agent radius per lane
@@ -387,6 +388,7 @@ __global__ __launch_bounds__(64) void k_body_fwd(const Cst<T> C, const Args<T> g
     __shared__ T lob[2][EPW][OB_W * NOB_MAX];        // obstacle state: in / out of a substep
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
+    fold_prm<F>(L.pr);
     lr[L.lane] = L.pr.radius;
     const int ew = L.lane / PA;
     const int NW = OB_W * tb.N;
@@ -598,10 +600,11 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
     }
 }
 
-template <typename T, int PA>
-__global__ __launch_bounds__(64) void k_body_bwd(const Cst<T> C, const Args<T> g,
+template <typename T, int PA, unsigned F>
+__global__ __launch_bounds__(64) void k_body_bwd(const Cst<T> Cin, const Args<T> g,
                                                  const ObTab<T> tb, const ObIO<T> io)
 {
+    const Cst<T> C = fold_cst<F>(Cin);
     typedef typename MaskT<PA>::type M;
     constexpr int EPW = 64 / PA;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -615,6 +618,7 @@ __global__ __launch_bounds__(64) void k_body_bwd(const Cst<T> C, const Args<T> g
     T *lgob = lobs + (size_t)(C.S + 1) * EPW * NW;       // [2][EPW][NW] obstacle adjoints
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
+    fold_prm<F>(L.pr);
     lr[L.lane] = L.pr.radius;
     ldd[L.lane] = L.dd;
     const int ew = L.lane / PA;
@@ -770,32 +774,47 @@ template <typename T> size_t body_bwd_lds_of(int PA, int S, int N)
     }
 }
 
+#define SWARP_BODY_DISPATCH(KERNEL, FP, SHM)                                          \
+    switch (PA) {                                                                      \
+    case 4: hipLaunchKernelGGL((KERNEL<T, 4, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
+    case 8: hipLaunchKernelGGL((KERNEL<T, 8, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
+    case 16: hipLaunchKernelGGL((KERNEL<T, 16, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
+    case 32: hipLaunchKernelGGL((KERNEL<T, 32, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
+    default: hipLaunchKernelGGL((KERNEL<T, 64, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
+    }
+
+// The profile besides FT_ALL the body kernels compile for float32 (0: none).
+template <typename T> constexpr unsigned body_profile()
+{
+    return sizeof(T) == 4 ? FT_PROF_BODY : 0u;
+}
+
+// feat: the FT_* paths the world uses; the profile runs when it covers them.
 template <typename T>
 void launch_body_fwd(int PA, const Cst<T> &C, const Args<T> &a, const ObTab<T> &tb,
-                     const ObIO<T> &io, hipStream_t st)
+                     const ObIO<T> &io, unsigned feat, hipStream_t st)
 {
     const dim3 grid((C.E + 64 / PA - 1) / (64 / PA));
-    switch (PA) {
-    case 4: hipLaunchKernelGGL((k_body_fwd<T, 4>), grid, dim3(64), 0, st, C, a, tb, io); break;
-    case 8: hipLaunchKernelGGL((k_body_fwd<T, 8>), grid, dim3(64), 0, st, C, a, tb, io); break;
-    case 16: hipLaunchKernelGGL((k_body_fwd<T, 16>), grid, dim3(64), 0, st, C, a, tb, io); break;
-    case 32: hipLaunchKernelGGL((k_body_fwd<T, 32>), grid, dim3(64), 0, st, C, a, tb, io); break;
-    default: hipLaunchKernelGGL((k_body_fwd<T, 64>), grid, dim3(64), 0, st, C, a, tb, io); break;
+    constexpr unsigned P = body_profile<T>();
+    if (P != 0u && (feat & ~P) == 0u) {
+        SWARP_BODY_DISPATCH(k_body_fwd, (P ? P : FT_ALL), 0)
+    } else {
+        SWARP_BODY_DISPATCH(k_body_fwd, FT_ALL, 0)
     }
 }
 
 template <typename T>
 void launch_body_bwd(int PA, const Cst<T> &C, const Args<T> &a, const ObTab<T> &tb,
-                     const ObIO<T> &io, size_t shm, hipStream_t st)
+                     const ObIO<T> &io, unsigned feat, size_t shm, hipStream_t st)
 {
     const dim3 grid((C.E + 64 / PA - 1) / (64 / PA));
-    switch (PA) {
-    case 4: hipLaunchKernelGGL((k_body_bwd<T, 4>), grid, dim3(64), shm, st, C, a, tb, io); break;
-    case 8: hipLaunchKernelGGL((k_body_bwd<T, 8>), grid, dim3(64), shm, st, C, a, tb, io); break;
-    case 16: hipLaunchKernelGGL((k_body_bwd<T, 16>), grid, dim3(64), shm, st, C, a, tb, io); break;
-    case 32: hipLaunchKernelGGL((k_body_bwd<T, 32>), grid, dim3(64), shm, st, C, a, tb, io); break;
-    default: hipLaunchKernelGGL((k_body_bwd<T, 64>), grid, dim3(64), shm, st, C, a, tb, io); break;
+    constexpr unsigned P = body_profile<T>();
+    if (P != 0u && (feat & ~P) == 0u) {
+        SWARP_BODY_DISPATCH(k_body_bwd, (P ? P : FT_ALL), shm)
+    } else {
+        SWARP_BODY_DISPATCH(k_body_bwd, FT_ALL, shm)
     }
 }
+#undef SWARP_BODY_DISPATCH
 
 }  // namespace swarp

@@ -215,6 +215,58 @@ template <typename M> __device__ __forceinline__ M cap_list(M incl, int K)
     return incl ^ rest;
 }
 
+// ------------------------------------------------------------- feature profiles
+//
+// The generic and body kernels are instantiated per feature profile F: a bit set of the
+// optional paths an instance compiles.  fold_cst / fold_prm overwrite, in a kernel's own
+// copy of the constants and of each lane's parameter row, every field an absent feature
+// reads with the compile-time value that switches it off, so constant propagation removes
+// those paths (FT_ALL keeps them all).  The host picks an instance whose profile covers
+// the world's features (swarp_desc_t fleet_models / fleet_modes and the constants).
+enum : unsigned {
+    FT_RK4 = 1u << 0,    // Integrator.RK4
+    FT_SAT = 1u << 1,    // contact_max_overlap > 0 (tanh law)
+    FT_OBST = 1u << 2,   // static obstacles
+    FT_WALL = 1u << 3,   // soft walls
+    FT_CLAMP = 1u << 4,  // position clamp
+    FT_MODES = 1u << 5,  // ACCELERATION / SERVO control of a holonomic or diff-drive agent
+    FT_HOLO = 1u << 6,   // model tags present: holonomic, diff-drive, bicycle, drone
+    FT_DIFF = 1u << 7,
+    FT_BICY = 1u << 8,
+    FT_DRONE = 1u << 9,
+    FT_ALL = 0x3ffu,
+};
+// Profiles compiled besides FT_ALL (float32): 2-D fleets with obstacles and walls under
+// Euler, drone fleets (config 4), holonomic fleets with movable bodies
+// (config 5).
+constexpr unsigned FT_PROF_2D = FT_OBST | FT_WALL | FT_HOLO | FT_DIFF | FT_BICY;
+constexpr unsigned FT_PROF_DRONE = FT_WALL | FT_DRONE;
+constexpr unsigned FT_PROF_BODY = FT_WALL | FT_HOLO;
+
+template <unsigned F, typename T> __device__ __forceinline__ Cst<T> fold_cst(Cst<T> C)
+{
+    if (!(F & FT_RK4)) C.rk4 = 0;
+    if (!(F & FT_SAT)) C.max_overlap = T(0);
+    if (!(F & FT_OBST)) C.N = 0;
+    if (!(F & FT_WALL)) C.soft_walls = 0;
+    if (!(F & FT_CLAMP)) C.clamp = 0;
+    return C;
+}
+
+template <unsigned F, typename T> __device__ __forceinline__ void fold_prm(Prm<T> &P)
+{
+    constexpr unsigned tags = F & (FT_HOLO | FT_DIFF | FT_BICY | FT_DRONE);
+    if (tags == FT_HOLO) P.tag = 0;
+    if (tags == FT_DIFF) P.tag = 1;
+    if (tags == FT_BICY) P.tag = 2;
+    if (tags == FT_DRONE) P.tag = 3;
+    if (!(F & FT_HOLO)) __builtin_assume(P.tag != 0);
+    if (!(F & FT_DIFF)) __builtin_assume(P.tag != 1);
+    if (!(F & FT_BICY)) __builtin_assume(P.tag != 2);
+    if (!(F & FT_DRONE)) __builtin_assume(P.tag != 3);
+    if (!(F & FT_MODES)) P.mode = 0;
+}
+
 // Per-lane context shared by the forward and backward kernels.
 template <typename T, int PA> struct Lane {
     int lane, agent, base, env;

@@ -10,10 +10,11 @@ namespace swarp {
 
 // BOXES: the box-aware contact pass is compiled in (a world holding box agents); the
 // disc-only instances keep the register budget of the disc contact law.
-template <typename T, int PA, bool DRONE, bool BOXES>
-__global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> C, const Args<T> g)
+template <typename T, int PA, bool DRONE, bool BOXES, unsigned F>
+__global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> Cin, const Args<T> g)
 {
     typedef typename MaskT<PA>::type M;
+    const Cst<T> C = fold_cst<F>(Cin);
     __shared__ T sl[7 * 64];  // px py vx vy th (s) w of the current substep
     __shared__ T lr[64];      // agent radius per lane
     __shared__ T lbx[3 * 64]; // footprint per lane: shape, hx, hy (box worlds)
@@ -21,6 +22,7 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> C, const Args<T
     __shared__ T ocs_lds[2 * OCS_MAX];
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
+    fold_prm<F>(L.pr);
     lr[L.lane] = L.pr.radius;
     lbx[L.lane] = L.pr.shape;
     lbx[64 + L.lane] = L.pr.hx;
@@ -206,9 +208,10 @@ __device__ __forceinline__ void box_rounds(const Cst<T> &C, const Args<T> &g,
     }
 }
 
-template <typename T, int PA, bool DRONE, bool BOXES>
-__global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T> g)
+template <typename T, int PA, bool DRONE, bool BOXES, unsigned F>
+__global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> Cin, const Args<T> g)
 {
+    const Cst<T> C = fold_cst<F>(Cin);
     typedef typename MaskT<PA>::type M;
     constexpr int NF = DRONE ? NF_DRONE : NF_2D;
     extern __shared__ __align__(16) unsigned char smem[];
@@ -227,6 +230,7 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
     __shared__ T lbx[3 * 64];  // footprint per lane: shape, hx, hy (box worlds)
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
+    fold_prm<F>(L.pr);
     lr[L.lane] = L.pr.radius;
     lbx[L.lane] = L.pr.shape;
     lbx[64 + L.lane] = L.pr.hx;
@@ -378,21 +382,39 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> C, const Args<T
     default: hipLaunchKernelGGL((KERNEL<T, 64, __VA_ARGS__>), grid64, dim3(64), shm, st, C, a); break; \
     }
 
+// The profile besides FT_ALL each (DRONE, BOXES) family compiles for float32 (0: none).
+template <typename T, bool DRONE, bool BOXES> constexpr unsigned family_profile()
+{
+    return sizeof(T) != 4 || BOXES ? 0u : (DRONE ? FT_PROF_DRONE : FT_PROF_2D);
+}
+
+// feat: the FT_* paths the world uses; the family's profile runs when it covers them.
 template <typename T, bool DRONE, bool BOXES>
-void launch_fwd(int PA, const Cst<T> &C, const Args<T> &a, hipStream_t st)
+void launch_fwd(int PA, const Cst<T> &C, const Args<T> &a, unsigned feat, hipStream_t st)
 {
     const size_t shm = 0;
     const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
         grid32((C.E + 1) / 2), grid64(C.E);
-    SWARP_DISPATCH_PA(PA, k_rollout_fwd, DRONE, BOXES)
+    constexpr unsigned P = family_profile<T, DRONE, BOXES>();
+    if (P != 0u && (feat & ~P) == 0u) {
+        SWARP_DISPATCH_PA(PA, k_rollout_fwd, DRONE, BOXES, P ? P : FT_ALL)
+    } else {
+        SWARP_DISPATCH_PA(PA, k_rollout_fwd, DRONE, BOXES, FT_ALL)
+    }
 }
 
 template <typename T, bool DRONE, bool BOXES>
-void launch_bwd(int PA, const Cst<T> &C, const Args<T> &a, size_t shm, hipStream_t st)
+void launch_bwd(int PA, const Cst<T> &C, const Args<T> &a, unsigned feat, size_t shm,
+                hipStream_t st)
 {
     const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
         grid32((C.E + 1) / 2), grid64(C.E);
-    SWARP_DISPATCH_PA(PA, k_rollout_bwd, DRONE, BOXES)
+    constexpr unsigned P = family_profile<T, DRONE, BOXES>();
+    if (P != 0u && (feat & ~P) == 0u) {
+        SWARP_DISPATCH_PA(PA, k_rollout_bwd, DRONE, BOXES, P ? P : FT_ALL)
+    } else {
+        SWARP_DISPATCH_PA(PA, k_rollout_bwd, DRONE, BOXES, FT_ALL)
+    }
 }
 
 #undef SWARP_DISPATCH_PA

@@ -4,7 +4,7 @@
 
 namespace swarp {
 template void launch_fwd<SWARP_T, true, false>(int, const Cst<SWARP_T> &, const Args<SWARP_T> &,
-                                         hipStream_t);
+                                         unsigned, hipStream_t);
 template void launch_bwd<SWARP_T, true, false>(int, const Cst<SWARP_T> &, const Args<SWARP_T> &,
-                                         size_t, hipStream_t);
+                                         unsigned, size_t, hipStream_t);
 }  // namespace swarp

@@ -9,32 +9,34 @@
 
 #define SWARP_EXTERN_LAUNCHERS(T)                                                            \
     extern template void launch_fwd<T, false, false>(int, const Cst<T> &, const Args<T> &,   \
-                                                     hipStream_t);                          \
+                                                     unsigned, hipStream_t);                 \
     extern template void launch_fwd<T, true, false>(int, const Cst<T> &, const Args<T> &,    \
-                                                    hipStream_t);                           \
+                                                    unsigned, hipStream_t);                  \
     extern template void launch_fwd<T, false, true>(int, const Cst<T> &, const Args<T> &,    \
-                                                    hipStream_t);                           \
+                                                    unsigned, hipStream_t);                  \
     extern template void launch_bwd<T, false, false>(int, const Cst<T> &, const Args<T> &,   \
-                                                     size_t, hipStream_t);                  \
+                                                     unsigned, size_t, hipStream_t);         \
     extern template void launch_bwd<T, true, false>(int, const Cst<T> &, const Args<T> &,    \
-                                                    size_t, hipStream_t);                   \
+                                                    unsigned, size_t, hipStream_t);          \
     extern template void launch_bwd<T, false, true>(int, const Cst<T> &, const Args<T> &,    \
-                                                    size_t, hipStream_t);                   \
+                                                    unsigned, size_t, hipStream_t);          \
     extern template void launch_holo_fwd<T, true>(int, const Cst<T> &, const Args<T> &,      \
-                                                  const Tape<T> &, hipStream_t);            \
+                                                  const Tape<T> &, hipStream_t);             \
     extern template void launch_holo_fwd<T, false>(int, const Cst<T> &, const Args<T> &,     \
-                                                   const Tape<T> &, hipStream_t);           \
+                                                   const Tape<T> &, hipStream_t);            \
     extern template void launch_holo_bwd<T, true>(int, const Cst<T> &, const Args<T> &,      \
-                                                  const Tape<T> &, size_t, hipStream_t);    \
+                                                  const Tape<T> &, size_t, hipStream_t);     \
     extern template void launch_holo_bwd<T, false>(int, const Cst<T> &, const Args<T> &,     \
-                                                   const Tape<T> &, size_t, hipStream_t);   \
+                                                   const Tape<T> &, size_t, hipStream_t);    \
     extern template void launch_body_fwd<T>(int, const Cst<T> &, const Args<T> &,            \
-                                            const ObTab<T> &, const ObIO<T> &, hipStream_t);\
+                                            const ObTab<T> &, const ObIO<T> &, unsigned,     \
+                                            hipStream_t);                                    \
     extern template void launch_body_bwd<T>(int, const Cst<T> &, const Args<T> &,            \
-                                            const ObTab<T> &, const ObIO<T> &, size_t,      \
-                                            hipStream_t);                                   \
+                                            const ObTab<T> &, const ObIO<T> &, unsigned,     \
+                                            size_t,                                          \
+                                            hipStream_t);                                    \
     extern template void launch_nav<T>(int, const Cst<T> &, const NavArgs<T> &, unsigned,    \
-                                       hipStream_t);                                        \
+                                       hipStream_t);                                         \
     extern template void launch_neighbors<T>(int, const Cst<T> &, const T *, int32_t *,      \
                                              int32_t *, int32_t *, hipStream_t);
 

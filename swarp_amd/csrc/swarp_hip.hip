@@ -190,6 +190,29 @@ static bool fields_ok(const swarp_state_t *s, int n)
     return true;
 }
 
+// The optional kernel paths (FT_* bits) the world uses, which select the kernel instance.
+// body: the obstacles are the movable bodies of the body kernels, not static obstacles.
+static unsigned world_features(const swarp_desc_t *d, bool body)
+{
+    unsigned f = 0;
+    if (d->integrator == SWARP_RK4) f |= FT_RK4;
+    if (d->max_overlap > 0.0) f |= FT_SAT;
+    if (!body && d->n_obstacles > 0) f |= FT_OBST;
+    if (d->soft_walls) f |= FT_WALL;
+    if (d->clamp_bounds) f |= FT_CLAMP;
+    const unsigned models = d->fleet_models ? (unsigned)d->fleet_models : ~0u;
+    const unsigned modes = d->fleet_modes ? (unsigned)d->fleet_modes : ~0u;
+    if (models & ~0xfu) return FT_ALL;
+    // the control mode only changes holonomic and diff-drive agents (bicycles and drones
+    // read their actions one way)
+    if ((modes & ~1u) && (models & 3u)) f |= FT_MODES;
+    if (models & 1u) f |= FT_HOLO;
+    if (models & 2u) f |= FT_DIFF;
+    if (models & 4u) f |= FT_BICY;
+    if (models & 8u) f |= FT_DRONE;
+    return f;
+}
+
 static bool lean_ok(const swarp_desc_t *d)
 {
     return d->holo_velocity_only && !d->has_drone && d->n_obstacles == 0 && !d->clamp_bounds &&
@@ -269,11 +292,11 @@ static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
         else
             launch_holo_fwd<T, false>(PA, C, a, tape_ptrs<T>(TL, nullptr), st);
     else if (d->has_drone)
-        launch_fwd<T, true, false>(PA, C, a, st);
+        launch_fwd<T, true, false>(PA, C, a, world_features(d, false), st);
     else if (d->has_boxes || d->wheel_contacts)
-        launch_fwd<T, false, true>(PA, C, a, st);
+        launch_fwd<T, false, true>(PA, C, a, world_features(d, false), st);
     else
-        launch_fwd<T, false, false>(PA, C, a, st);
+        launch_fwd<T, false, false>(PA, C, a, world_features(d, false), st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
     return 0;
@@ -326,11 +349,11 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
         shm += (size_t)d->substeps * 64 * (msz + 2 * sizeof(T) + 8 + 1);
     if (shm > 65536) return fail("substeps too large for the backward LDS staging (limit 64 KiB per wave)");
     if (d->has_drone)
-        launch_bwd<T, true, false>(PA, C, a, shm, st);
+        launch_bwd<T, true, false>(PA, C, a, world_features(d, false), shm, st);
     else if (d->has_boxes)
-        launch_bwd<T, false, true>(PA, C, a, shm, st);
+        launch_bwd<T, false, true>(PA, C, a, world_features(d, false), shm, st);
     else
-        launch_bwd<T, false, false>(PA, C, a, shm, st);
+        launch_bwd<T, false, false>(PA, C, a, world_features(d, false), shm, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
     return 0;
@@ -379,7 +402,7 @@ static int rollout_fwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     a.nsteps = nT;
     ObIO<T> io = {(const T *)ob0, (T *)ob_traj, nullptr, nullptr};
     const int PA = pad_agents(d->n_agents);
-    launch_body_fwd<T>(PA, C, a, tb, io, st);
+    launch_body_fwd<T>(PA, C, a, tb, io, world_features(d, true), st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
     return 0;
@@ -413,7 +436,7 @@ static int rollout_bwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     const int PA = pad_agents(d->n_agents);
     const size_t shm = body_bwd_lds_of<T>(PA, d->substeps, d->n_obstacles);
     if (shm > 65536) return fail("substeps too large for the body backward's LDS staging (limit 64 KiB per wave)");
-    launch_body_bwd<T>(PA, C, a, tb, io, shm, st);
+    launch_body_bwd<T>(PA, C, a, tb, io, world_features(d, true), shm, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
     return 0;

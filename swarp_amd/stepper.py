@@ -126,6 +126,11 @@ class Stepper:
         #: intermediates so that the backward does not recompute them (set False to
         #: recompute; both give bit-identical results)
         self.use_tape = True
+        #: route fleets whose features a compiled profile covers (2-D fleets with
+        #: obstacles and walls under Euler, drone fleets, holonomic fleets pushing movable
+        #: bodies) to the kernel instances compiled without the absent paths (set False
+        #: for the general instances; both give bit-identical results)
+        self.use_profiles = True
 
         self.collisions = world.collisions
         self.max_agent_radius = max(c.radius for c in configs)
@@ -371,6 +376,9 @@ class Stepper:
         d.ang_damping = float(self.world.obstacle_angular_damping)
         d.integrator = _lib.RK4 if self.world.integrator == Integrator.RK4 else _lib.EULER
         d.skin_speed = self._skin_speed()
+        if self.use_profiles:  # 0 (unset) selects the general instances
+            d.fleet_models = sum(1 << m for m in {int(c.model) for c in self.configs})
+            d.fleet_modes = sum(1 << m for m in {int(c.ctrl_mode) for c in self.configs})
         self._descs[key] = d
         return d
 

@@ -217,6 +217,23 @@ def test_stepper_reach_check_and_unsupported_features():
                       kind=torch.ones(1, dtype=torch.int32)))
 
 
+def test_desc_fleet_models_and_modes():
+    """The descriptor's fleet bit sets describe the configs (they select the kernel
+    instance: a profile compiled without the absent models and modes); use_profiles=False
+    leaves them 0, the general instances."""
+    cfgs = [AgentConfig(model=DynamicsModel.DIFF_DRIVE, ctrl_mode=ControlMode.SERVO),
+            AgentConfig(model=DynamicsModel.KINEMATIC_BICYCLE),
+            AgentConfig(model=DynamicsModel.DIFF_DRIVE, ctrl_mode=ControlMode.ACCELERATION)]
+    d = Stepper(cfgs, device="cpu").desc(3, 2)
+    assert d.fleet_models == (1 << 1) | (1 << 2) and d.fleet_modes == 0b111
+    d = Stepper([drone_config()], device="cpu").desc(3, 4)
+    assert d.fleet_models == 1 << 3 and d.fleet_modes == 1 << int(drone_config().ctrl_mode)
+    st = Stepper([AgentConfig()], device="cpu")
+    st.use_profiles = False
+    d = st.desc(1, 2)
+    assert d.fleet_models == 0 and d.fleet_modes == 0
+
+
 def test_step_refuses_cpu_tensors():
     """No CPU fallback: stepping host tensors raises instead of computing."""
     st = Stepper([AgentConfig()], device="cpu", world=WorldConfig(collisions=False))
