@@ -30,8 +30,8 @@ constexpr int NOB_MAX = 16;    // obstacles per env on this path
 
 // Static obstacle tables of the body path.
 template <typename T> struct ObTab {
-    const T *rad, *half, *mass, *inertia, *off;  // [N], [N,2], [N], [N], [N,2]
-    const int32_t *type, *kind, *body;            // [N]
+    const SWARP_RO T *rad, *half, *mass, *inertia, *off;  // [N], [N,2], [N], [N], [N,2]
+    const SWARP_RO int32_t *type, *kind, *body;            // [N]
     T lin_damp, ang_damp;
     int N;
 };
@@ -373,10 +373,24 @@ __device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
     }
 }
 
+// Waves per SIMD the float32 profile instances of the body kernels are compiled for
+// (register budget 512 / waves per lane): a 16000-env launch is latency-bound, so more
+// resident waves beat the spills the tighter budget costs (measured on the config-5
+// workload).  Fewer for 4 and 8 agents per env, where the obstacle-state LDS of 16 and 8
+// env slots bounds residency anyway; the general instances keep the compiler's choice.
+constexpr int body_fwd_waves(int PA, size_t tsize, unsigned F)
+{
+    return (tsize != 4 || F == FT_ALL) ? 1 : (PA >= 16 ? 4 : (PA == 8 ? 3 : 2));
+}
+constexpr int body_bwd_waves(int PA, size_t tsize, unsigned F)
+{
+    return (tsize != 4 || F == FT_ALL) ? 1 : (PA >= 8 ? 3 : 2);
+}
+
 // ------------------------------------------------------------------ forward rollout
 
 template <typename T, int PA, unsigned F>
-__global__ __launch_bounds__(64) void k_body_fwd(const Cst<T> Cin, const Args<T> g,
+__global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_fwd(const Cst<T> Cin, const Args<T> g,
                                                  const ObTab<T> tb, const ObIO<T> io)
 {
     typedef typename MaskT<PA>::type M;
@@ -601,7 +615,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
 }
 
 template <typename T, int PA, unsigned F>
-__global__ __launch_bounds__(64) void k_body_bwd(const Cst<T> Cin, const Args<T> g,
+__global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_bwd(const Cst<T> Cin, const Args<T> g,
                                                  const ObTab<T> tb, const ObIO<T> io)
 {
     const Cst<T> C = fold_cst<F>(Cin);

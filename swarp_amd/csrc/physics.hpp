@@ -82,10 +82,20 @@ template <typename T> struct Cst {
     int rk4;       // Integrator.RK4 instead of semi-implicit Euler
 };
 
+// Read-only tables that no launch writes, read through the constant address space in
+// device code: a load at a wave-uniform index (the loops over obstacles and shapes) then
+// becomes a scalar load through the scalar cache instead of a vector load per lane.  The
+// host sees plain pointers of the same size.
+#if defined(__HIP_DEVICE_COMPILE__)
+#define SWARP_RO __attribute__((address_space(4)))
+#else
+#define SWARP_RO
+#endif
+
 // Obstacle arrays (device); shared extents [N], per-env poses [E,N].
 template <typename T> struct Obs {
-    const T *pos, *rad, *ang, *half, *vel, *om;
-    const int32_t *type;
+    const SWARP_RO T *pos, *rad, *ang, *half, *vel, *om;
+    const SWARP_RO int32_t *type;
 };
 
 // ---------------------------------------------- exact fp32 arithmetic, restricted ranges

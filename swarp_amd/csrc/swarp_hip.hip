@@ -164,13 +164,13 @@ template <typename T> static void fill_args(const swarp_desc_t *d, Args<T> &a)
     a.params = (const T *)d->params;
     a.tag = d->model_tag;
     a.mode = d->ctrl_mode;
-    a.obs.pos = (const T *)d->obs_pos;
-    a.obs.rad = (const T *)d->obs_radius;
-    a.obs.ang = (const T *)d->obs_angle;
-    a.obs.half = (const T *)d->obs_half;
-    a.obs.vel = (const T *)d->obs_vel;
-    a.obs.om = (const T *)d->obs_ang_vel;
-    a.obs.type = d->obs_type;
+    a.obs.pos = (decltype(a.obs.pos))d->obs_pos;
+    a.obs.rad = (decltype(a.obs.rad))d->obs_radius;
+    a.obs.ang = (decltype(a.obs.ang))d->obs_angle;
+    a.obs.half = (decltype(a.obs.half))d->obs_half;
+    a.obs.vel = (decltype(a.obs.vel))d->obs_vel;
+    a.obs.om = (decltype(a.obs.om))d->obs_ang_vel;
+    a.obs.type = (decltype(a.obs.type))d->obs_type;
 }
 
 template <typename T> static void copy_fields(const swarp_state_t *s, T **f)
@@ -366,14 +366,14 @@ template <typename T> static int fill_obtab(const swarp_desc_t *d, ObTab<T> &tb)
     if (!d->obs_kind || !d->obs_body || !d->obs_mass || !d->obs_inertia || !d->obs_body_off)
         return fail("obs_kind/obs_body/obs_mass/obs_inertia/obs_body_off must be set");
     if (d->has_drone) return fail("the body path steps 2-D fleets only");
-    tb.rad = (const T *)d->obs_radius;
-    tb.half = (const T *)d->obs_half;
-    tb.mass = (const T *)d->obs_mass;
-    tb.inertia = (const T *)d->obs_inertia;
-    tb.off = (const T *)d->obs_body_off;
-    tb.type = d->obs_type;
-    tb.kind = d->obs_kind;
-    tb.body = d->obs_body;
+    tb.rad = (decltype(tb.rad))d->obs_radius;
+    tb.half = (decltype(tb.half))d->obs_half;
+    tb.mass = (decltype(tb.mass))d->obs_mass;
+    tb.inertia = (decltype(tb.inertia))d->obs_inertia;
+    tb.off = (decltype(tb.off))d->obs_body_off;
+    tb.type = (decltype(tb.type))d->obs_type;
+    tb.kind = (decltype(tb.kind))d->obs_kind;
+    tb.body = (decltype(tb.body))d->obs_body;
     tb.lin_damp = (T)d->lin_damping;
     tb.ang_damp = (T)d->ang_damping;
     tb.N = d->n_obstacles;
