@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 10
+#define SWARP_ABI_VERSION 11
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -98,7 +98,26 @@ typedef struct swarp_desc {
        describe model_tag / ctrl_mode truthfully; 0 reads as "any" (the general
        instances). */
     int32_t fleet_models, fleet_modes;
+    /* Neighbour-list order (NeighborGrid's method, swarp/core/neighbors.py:387-389):
+       SWARP_LISTS_BRUTE ascending agent index (_brute_force, :76-97); SWARP_LISTS_GRID the
+       uniform grid's (_query_uniform, :214-251) over grid_bins x grid_bins cells (at most
+       64 x 64).  grid_pinned = 1: the frame is grid_origin / grid_cell (the world
+       rectangle's, NeighborGrid._fill_static_grid :476-490, as the reference computes
+       them in float64; rounded to dtype here); 0: swarp_neighbors reduces it over the
+       batch (:149-181) into grid_frame, a caller-owned device buffer of 3 scalars of
+       dtype.  Stepping with grid lists takes a pinned frame. */
+    int32_t neighbor_method, grid_bins, grid_pinned;
+    double grid_origin[2], grid_cell;
+    void *grid_frame;
 } swarp_desc_t;
+
+#define SWARP_LISTS_BRUTE 0
+#define SWARP_LISTS_GRID 1
+/* Agents per env: up to 64 on every path; up to SWARP_WIDE_MAX_AGENTS on the wide-env
+   path (one workgroup per env), which steps 2-D and drone fleets with any model,
+   control mode, obstacles, walls, clamp and integrator, but no box agents, wheel
+   contacts or movable bodies, and serves every fleet with grid-ordered lists. */
+#define SWARP_WIDE_MAX_AGENTS 1024
 
 /* The nine state fields.  A NULL field means "not provided": an input adjoint that
  * is NULL reads as zero, an output adjoint that is NULL is not written.  For a fleet

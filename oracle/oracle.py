@@ -38,6 +38,8 @@ class OracleCfg(ctypes.Structure):
         ("lin_damping", ctypes.c_double), ("ang_damping", ctypes.c_double),
         ("rk4", ctypes.c_int), ("wheel", ctypes.c_int),
         ("lat_grip", ctypes.c_double), ("turn_cap", ctypes.c_double),
+        ("grid_bins", ctypes.c_int), ("grid_ox", ctypes.c_double), ("grid_oy", ctypes.c_double),
+        ("grid_cell", ctypes.c_double),
     ]
 
 
@@ -242,6 +244,27 @@ class Oracle:
         fn(ctypes.c_int(E), ctypes.c_int(A), ctypes.c_int(K), _p(pos), ctypes.c_double(radius),
            _p(idx), _p(cnt), _p(tru))
         return idx, cnt, tru
+
+    def neighbors_grid(self, pos, radius, K, bins, frame=None):
+        """Lists in the uniform grid's order; ``frame`` = (ox, oy, cell) pins the frame (as
+        float64, rounded to the oracle's precision), None reduces it over the batch.
+        Returns idx, cnt, tru and the frame used."""
+        pos = np.ascontiguousarray(pos, dtype=self.dtype)
+        E, A = pos.shape[:2]
+        idx = np.zeros((E, A, K), dtype=np.int32)
+        cnt = np.zeros((E, A), dtype=np.int32)
+        tru = np.zeros((E, A), dtype=np.int32)
+        fr = np.zeros(3, dtype=self.dtype)
+        ox, oy, cs = frame if frame is not None else (0.0, 0.0, 0.0)
+        fn = self._fn("neighbors_grid")
+        fn.restype = ctypes.c_int
+        rc = fn(ctypes.c_int(E), ctypes.c_int(A), ctypes.c_int(K), _p(pos),
+                ctypes.c_double(radius), ctypes.c_int(bins), ctypes.c_int(frame is not None),
+                ctypes.c_double(ox), ctypes.c_double(oy), ctypes.c_double(cs), _p(idx), _p(cnt),
+                _p(tru), _p(fr))
+        if rc != 0:
+            raise RuntimeError("oracle_neighbors_grid failed")
+        return idx, cnt, tru, fr
 
     def forces(self, cfg, params, tags, modes, obs, state):
         keep = []

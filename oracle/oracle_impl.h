@@ -55,6 +55,8 @@ typedef struct {
     REAL lin_damping, ang_damping;
     int any_movable;
     int rk4;  /* Integrator.RK4 for the 2-D models */
+    int grid_bins;          /* lists in uniform-grid order (0: index order) */
+    REAL g_ox, g_oy, g_cs;  /* the grid's frame: origin, cell size */
 } FN(ctx_t);
 
 /* Per-env obstacle state, 12 reals per obstacle index o:
@@ -518,6 +520,63 @@ static void FN(neighbors_env)(int A, int K, const FN(agent_t) *st, REAL radius,
         cnt[a] = count;
         if (tru) tru[a] = total;
     }
+}
+
+/* One axis of a uniform-grid cell (_compute_keys / _query_uniform, swarp/core/neighbors.py:
+   188-193, 230-232): truncation toward zero of (p - o) / cs, clamped to [0, bins). */
+static int FN(grid_axis)(REAL p, REAL o, REAL cs, int bins)
+{
+    REAL q = (p - o) / cs;
+    int c = q == q ? (int)q : 0;
+    return c < 0 ? 0 : (c > bins - 1 ? bins - 1 : c);
+}
+
+/* _query_uniform (swarp/core/neighbors.py:214-251) for one env with the frame (ox, oy,
+   cs): the cells of the 3x3 block around the agent's cell row by row (dy outer, dx
+   inner), the agents of a cell in ascending index -- the order of the stable sort of the
+   (env, cell) keys (:184-211, :663-666) -- tested with |p_b - p| <= radius. */
+static void FN(neighbors_env_grid)(int A, int K, const FN(agent_t) *st, REAL radius, int bins,
+                                   REAL ox, REAL oy, REAL cs, int32_t *idx, int32_t *cnt,
+                                   int32_t *tru)
+{
+    int *cx = (int *)malloc(sizeof(int) * 2 * (size_t)A), *cy = cx + A;
+    for (int a = 0; a < A; ++a) {
+        cx[a] = FN(grid_axis)(st[a].px, ox, cs, bins);
+        cy[a] = FN(grid_axis)(st[a].py, oy, cs, bins);
+    }
+    for (int a = 0; a < A; ++a) {
+        REAL px = st[a].px, py = st[a].py;
+        int32_t count = 0, total = 0;
+        for (int dy = -1; dy <= 1; ++dy) {
+            int ny = cy[a] + dy;
+            if (ny < 0 || ny >= bins) continue;
+            for (int dx = -1; dx <= 1; ++dx) {
+                int nx = cx[a] + dx;
+                if (nx < 0 || nx >= bins) continue;
+                for (int b = 0; b < A; ++b) {
+                    if (cx[b] != nx || cy[b] != ny || b == a) continue;
+                    REAL ex = st[b].px - px, ey = st[b].py - py;
+                    if (SQRT(ex * ex + ey * ey) <= radius) {
+                        total += 1;
+                        if (count < K) idx[a * K + count++] = b;
+                    }
+                }
+            }
+        }
+        cnt[a] = count;
+        if (tru) tru[a] = total;
+    }
+    free(cx);
+}
+
+/* The lists of one env in the world's order. */
+static void FN(lists_env)(const FN(ctx_t) *C, const FN(agent_t) *st, int32_t *idx, int32_t *cnt)
+{
+    if (C->grid_bins > 0)
+        FN(neighbors_env_grid)(C->n_agents, C->max_nbr, st, C->nbr_radius, C->grid_bins, C->g_ox,
+                               C->g_oy, C->g_cs, idx, cnt, NULL);
+    else
+        FN(neighbors_env)(C->n_agents, C->max_nbr, st, C->nbr_radius, idx, cnt, NULL);
 }
 
 /* --------------------------------------------------------------- the force pass */
@@ -1679,7 +1738,7 @@ static void FN(step_env)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_
         int32_t *idx = ch->idx + s * A * K, *cnt = ch->cnt + s * A;
         if (C->needs_forces) {
             if (C->collisions)
-                FN(neighbors_env)(A, K, cur, C->nbr_radius, idx, cnt, NULL);
+                FN(lists_env)(C, cur, idx, cnt);
             else
                 for (int a = 0; a < A; ++a) cnt[a] = 0;
             FN(forces_env)(C, obc, P, cur, idx, cnt, F);
@@ -1788,6 +1847,10 @@ static void FN(make_ctx)(const oracle_cfg_t *cfg, const oracle_obs_t *obs, FN(ct
     C->wheel = cfg->wheel;
     C->lat_grip = (REAL)cfg->lat_grip;
     C->turn_cap = (REAL)cfg->turn_cap;
+    C->grid_bins = cfg->grid_bins;
+    C->g_ox = (REAL)cfg->grid_ox;
+    C->g_oy = (REAL)cfg->grid_oy;
+    C->g_cs = (REAL)cfg->grid_cell;
     C->n_obs = obs ? obs->n_obstacles : 0;
     C->needs_forces = C->collisions || C->soft_walls || C->n_obs > 0;
     if (C->n_obs > 0) {
@@ -1856,6 +1919,56 @@ int FN(oracle_neighbors)(int E, int A, int K, const REAL *pos, double radius, in
         }
         FN(neighbors_env)(A, K, st, (REAL)radius, idx + (size_t)e * A * K, cnt + (size_t)e * A,
                           tru + (size_t)e * A);
+    }
+    free(st);
+    return 0;
+}
+
+/* Lists in the uniform grid's order.  pinned: the frame is (ox, oy, cs) rounded to REAL
+   (NeighborGrid._fill_static_grid, swarp/core/neighbors.py:476-490); else it is reduced
+   over the batch in REAL (_bounds_init / _bounds_reduce / _finalize_grid, :149-181):
+   origin = the min corner, cell size = max(radius, max(extent x, extent y) / bins).
+   frame_out (nullable) receives the frame used. */
+int FN(oracle_neighbors_grid)(int E, int A, int K, const REAL *pos, double radius, int bins,
+                              int pinned, double ox, double oy, double cs, int32_t *idx,
+                              int32_t *cnt, int32_t *tru, REAL *frame_out)
+{
+    REAL fo_x, fo_y, fcs;
+    REAL r = (REAL)radius;
+    if (pinned) {
+        fo_x = (REAL)ox;
+        fo_y = (REAL)oy;
+        fcs = (REAL)cs;
+    } else {
+        REAL big = (REAL)1e30, mnx = big, mny = big, mxx = -big, mxy = -big;
+        for (size_t q = 0; q < (size_t)E * A; ++q) {
+            REAL x = pos[2 * q], y = pos[2 * q + 1];
+            mnx = x < mnx ? x : mnx;
+            mny = y < mny ? y : mny;
+            mxx = x > mxx ? x : mxx;
+            mxy = y > mxy ? y : mxy;
+        }
+        REAL ex = mxx - mnx, ey = mxy - mny;
+        REAL ext = ex > ey ? ex : ey;
+        REAL qd = ext / (REAL)bins;
+        fo_x = mnx;
+        fo_y = mny;
+        fcs = r > qd ? r : qd;
+    }
+    if (frame_out) {
+        frame_out[0] = fo_x;
+        frame_out[1] = fo_y;
+        frame_out[2] = fcs;
+    }
+    FN(agent_t) *st = (FN(agent_t) *)calloc((size_t)A, sizeof(FN(agent_t)));
+    if (!st) return -1;
+    for (int e = 0; e < E; ++e) {
+        for (int a = 0; a < A; ++a) {
+            st[a].px = pos[(e * A + a) * 2];
+            st[a].py = pos[(e * A + a) * 2 + 1];
+        }
+        FN(neighbors_env_grid)(A, K, st, r, bins, fo_x, fo_y, fcs, idx + (size_t)e * A * K,
+                               cnt + (size_t)e * A, tru + (size_t)e * A);
     }
     free(st);
     return 0;
@@ -2063,7 +2176,7 @@ int FN(oracle_forces)(const oracle_cfg_t *cfg, const REAL *params, const int32_t
     for (int e = 0; e < E; ++e) {
         const FN(agent_t) *st = (const FN(agent_t) *)(state + (size_t)e * A * 16);
         if (C.collisions)
-            FN(neighbors_env)(A, K, st, C.nbr_radius, idx, cnt, NULL);
+            FN(lists_env)(&C, st, idx, cnt);
         else
             for (int a = 0; a < A; ++a) cnt[a] = 0;
         if (od) FN(static_ob)(&C, e, od);

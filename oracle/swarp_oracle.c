@@ -34,6 +34,11 @@ typedef struct {
     int rk4;                         /* Integrator.RK4 (2-D models) instead of Euler */
     int wheel;                       /* WorldConfig.wheel_contacts (forward only) */
     double lat_grip, turn_cap;       /* wheel_lateral_friction * gravity, wheel_turn_torque */
+    /* list order: grid_bins = 0 ascending index (_brute_force); > 0 the uniform grid's
+       (_query_uniform) over grid_bins^2 cells with the pinned frame (origin, cell size)
+       grid_ox, grid_oy, grid_cell, rounded to REAL */
+    int grid_bins;
+    double grid_ox, grid_oy, grid_cell;
 } oracle_cfg_t;
 
 typedef struct {

@@ -13,9 +13,11 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 F32, F64 = 0, 1
 EULER, RK4 = 0, 1
+LISTS_BRUTE, LISTS_GRID = 0, 1
+WIDE_MAX_AGENTS = 1024
 
 _PKG = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("SWARP_HIP_LIB", _PKG / "libswarp_hip.so"))
@@ -72,6 +74,12 @@ class SwarpDesc(ctypes.Structure):
         ("skin_speed", ctypes.c_double),
         ("fleet_models", ctypes.c_int32),
         ("fleet_modes", ctypes.c_int32),
+        ("neighbor_method", ctypes.c_int32),
+        ("grid_bins", ctypes.c_int32),
+        ("grid_pinned", ctypes.c_int32),
+        ("grid_origin", ctypes.c_double * 2),
+        ("grid_cell", ctypes.c_double),
+        ("grid_frame", ctypes.c_void_p),
     ]
 
 

@@ -13,9 +13,11 @@ types so a caller's configuration code carries over unchanged:
 * ``drone_config`` follows ``swarp/dynamics/drone.py:24-53``.
 
 What the MI355X build does not run is rejected loudly rather than silently
-approximated: box agents / wheel contacts / per-env parameter tables together with
-movable bodies and more than 64 agents per env raise
-``NotImplementedError`` when a ``Stepper`` is built with them (or the bodies installed).
+approximated, with ``NotImplementedError`` when a ``Stepper`` is built with it (or the
+bodies installed): movable bodies together with per-env parameter tables, box agents or
+drones; box agents, wheel contacts or movable bodies in envs of more than 64 agents (or
+with grid-ordered lists); more than 1024 agents per env; the hash-grid list order; and
+stepping with grid-ordered lists without world bounds.
 """
 
 from __future__ import annotations

@@ -6,6 +6,7 @@
 #include "bodies.hpp"
 #include "nav.hpp"
 #include "neighbors.hpp"
+#include "wide.hpp"
 
 #define SWARP_EXTERN_LAUNCHERS(T)                                                            \
     extern template void launch_fwd<T, false, false>(int, const Cst<T> &, const Args<T> &,   \
@@ -38,7 +39,14 @@
     extern template void launch_nav<T>(int, const Cst<T> &, const NavArgs<T> &, unsigned,    \
                                        hipStream_t);                                         \
     extern template void launch_neighbors<T>(int, const Cst<T> &, const T *, int32_t *,      \
-                                             int32_t *, int32_t *, hipStream_t);
+                                             int32_t *, int32_t *, hipStream_t);             \
+    extern template void launch_wide_lists<T>(const Cst<T> &, const T *, const T *, int32_t *,\
+                                              int32_t *, int32_t *, hipStream_t);            \
+    extern template void launch_grid_frame<T>(const T *, int64_t, T, int, T *, hipStream_t);  \
+    extern template void launch_wide_fwd<T>(bool, const Cst<T> &, const Args<T> &,            \
+                                            hipStream_t);                                    \
+    extern template void launch_wide_bwd<T>(bool, const Cst<T> &, const Args<T> &,            \
+                                            hipStream_t);
 
 namespace swarp {
 SWARP_EXTERN_LAUNCHERS(float)

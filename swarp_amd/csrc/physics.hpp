@@ -80,6 +80,8 @@ template <typename T> struct Cst {
     T lat_grip, turn_cap;
     int fast_div;  // neighbour radius <= 2^20: contact distances are short-division divisors
     int rk4;       // Integrator.RK4 instead of semi-implicit Euler
+    int grid_bins;          // lists in uniform-grid order over bins x bins cells (0: index order)
+    T grid_ox, grid_oy, grid_cs;  // the grid's pinned frame: origin and cell size
 };
 
 // Read-only tables that no launch writes, read through the constant address space in

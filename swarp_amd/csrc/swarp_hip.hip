@@ -112,6 +112,10 @@ template <typename T> static int fill_cst(const swarp_desc_t *d, double skin, Cs
     // short exact division when the radius is at most 2^20
     C.fast_div = d->neighbor_radius <= 0x1p20 ? 1 : 0;
     C.rk4 = d->integrator == SWARP_RK4 ? 1 : 0;
+    C.grid_bins = d->neighbor_method == SWARP_LISTS_GRID ? d->grid_bins : 0;
+    C.grid_ox = (T)d->grid_origin[0];
+    C.grid_oy = (T)d->grid_origin[1];
+    C.grid_cs = (T)d->grid_cell;
     return 0;
 }
 
@@ -121,7 +125,14 @@ static int check_desc(const swarp_desc_t *d, bool need_params = true)
     if (d->abi_version != SWARP_ABI_VERSION) return fail("desc->abi_version mismatch");
     if (d->dtype != SWARP_F32 && d->dtype != SWARP_F64) return fail("desc->dtype must be SWARP_F32 or SWARP_F64");
     if (d->n_envs < 1) return fail("n_envs must be >= 1");
-    if (d->n_agents < 1 || d->n_agents > 64) return fail("n_agents must lie in [1, 64] in this build");
+    if (d->n_agents < 1 || d->n_agents > SWARP_WIDE_MAX_AGENTS)
+        return fail("n_agents must lie in [1, 1024]");
+    if (d->neighbor_method != SWARP_LISTS_BRUTE && d->neighbor_method != SWARP_LISTS_GRID)
+        return fail("desc->neighbor_method must be SWARP_LISTS_BRUTE or SWARP_LISTS_GRID");
+    if (d->neighbor_method == SWARP_LISTS_GRID) {
+        if (d->grid_bins < 1 || d->grid_bins > 64) return fail("grid_bins must lie in [1, 64]");
+        if (d->grid_pinned && !(d->grid_cell > 0.0)) return fail("grid_cell must be positive");
+    }
     if (d->act_dim < 1) return fail("act_dim must be >= 1");
     if (d->substeps < 1) return fail("substeps must be >= 1");
     if (d->collisions && d->max_neighbors < 1) return fail("max_neighbors must be >= 1");
@@ -213,9 +224,34 @@ static unsigned world_features(const swarp_desc_t *d, bool body)
     return f;
 }
 
+// The wide-env kernels (one workgroup per env): more than 64 agents, or grid-ordered lists.
+static bool wide_path(const swarp_desc_t *d)
+{
+    return d->n_agents > 64 || d->neighbor_method == SWARP_LISTS_GRID;
+}
+
+// What the wide-env kernels do not step, as an error message (NULL: they step it).
+static const char *wide_unsupported(const swarp_desc_t *d)
+{
+    if (d->has_boxes) return "box agents step with at most 64 agents per env and index-ordered lists";
+    if (d->wheel_contacts) return "wheel contacts step with at most 64 agents per env and index-ordered lists";
+    if (d->neighbor_method == SWARP_LISTS_GRID && d->collisions && !d->grid_pinned)
+        return "stepping with uniform-grid lists needs the grid frame pinned by the world bounds "
+               "(an adaptive frame reduces over every env at every substep)";
+    return nullptr;
+}
+
+template <typename T> static int wide_lds_check(const swarp_desc_t *d)
+{
+    const int NC = d->neighbor_method == SWARP_LISTS_GRID ? d->grid_bins * d->grid_bins : 0;
+    if (wide_lds_bytes<T>(((d->n_agents + 63) / 64) * 64, NC) > 65536)
+        return fail("n_agents too large for the wide-env LDS staging at this dtype (limit 64 KiB)");
+    return 0;
+}
+
 static bool lean_ok(const swarp_desc_t *d)
 {
-    return d->holo_velocity_only && !d->has_drone && d->n_obstacles == 0 && !d->clamp_bounds &&
+    return !wide_path(d) && d->holo_velocity_only && !d->has_drone && d->n_obstacles == 0 && !d->clamp_bounds &&
            d->integrator == SWARP_EULER && !d->has_boxes && !d->wheel_contacts &&
            !d->params_per_env;
 }
@@ -286,17 +322,23 @@ static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     a.act = (const T *)act;
     a.nsteps = nT;
     const int PA = pad_agents(d->n_agents);
-    if (lean_ok(d))
+    const unsigned feat = world_features(d, false);
+    if (wide_path(d)) {
+        if (const char *why = wide_unsupported(d)) return fail(why);
+        if (wide_lds_check<T>(d)) return -1;
+        launch_wide_fwd<T>(d->has_drone != 0, C, a, st);
+    } else if (lean_ok(d)) {
         if (tape && TL.total)
             launch_holo_fwd<T, true>(PA, C, a, tape_ptrs<T>(TL, tape), st);
         else
             launch_holo_fwd<T, false>(PA, C, a, tape_ptrs<T>(TL, nullptr), st);
-    else if (d->has_drone)
-        launch_fwd<T, true, false>(PA, C, a, world_features(d, false), st);
-    else if (d->has_boxes || d->wheel_contacts)
-        launch_fwd<T, false, true>(PA, C, a, world_features(d, false), st);
-    else
-        launch_fwd<T, false, false>(PA, C, a, world_features(d, false), st);
+    } else if (d->has_drone) {
+        launch_fwd<T, true, false>(PA, C, a, feat, st);
+    } else if (d->has_boxes || d->wheel_contacts) {
+        launch_fwd<T, false, true>(PA, C, a, feat, st);
+    } else {
+        launch_fwd<T, false, false>(PA, C, a, feat, st);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
     return 0;
@@ -327,6 +369,14 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     a.aact = (T *)aact;
     a.nsteps = nT;
     const int PA = pad_agents(d->n_agents);
+    if (wide_path(d)) {
+        if (const char *why = wide_unsupported(d)) return fail(why);
+        if (wide_lds_check<T>(d)) return -1;
+        launch_wide_bwd<T>(d->has_drone != 0, C, a, st);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fail(hipGetErrorString(e));
+        return 0;
+    }
     if (lean_ok(d)) {
         const size_t msz = PA == 64 ? 8 : 4;
         const size_t lshm = (size_t)d->substeps * 128 * 2 * sizeof(T) +
@@ -366,6 +416,8 @@ template <typename T> static int fill_obtab(const swarp_desc_t *d, ObTab<T> &tb)
     if (!d->obs_kind || !d->obs_body || !d->obs_mass || !d->obs_inertia || !d->obs_body_off)
         return fail("obs_kind/obs_body/obs_mass/obs_inertia/obs_body_off must be set");
     if (d->has_drone) return fail("the body path steps 2-D fleets only");
+    if (wide_path(d))
+        return fail("the body path steps at most 64 agents per env with index-ordered lists");
     tb.rad = (decltype(tb.rad))d->obs_radius;
     tb.half = (decltype(tb.half))d->obs_half;
     tb.mass = (decltype(tb.mass))d->obs_mass;
@@ -618,14 +670,34 @@ int swarp_neighbors(const swarp_desc_t *desc, const void *pos, int32_t *idx, int
     if (!pos || !idx || !cnt) return fail("pos/idx/cnt must be set");
     hipStream_t st = (hipStream_t)stream;
     const int PA = pad_agents(desc->n_agents);
+    const bool adaptive = desc->neighbor_method == SWARP_LISTS_GRID && !desc->grid_pinned;
+    if (adaptive && !desc->grid_frame) return fail("grid_frame must be set for an adaptive grid frame");
     if (desc->dtype == SWARP_F32) {
+        if (wide_path(desc) && wide_lds_check<float>(desc)) return -1;
         Cst<float> C;
         fill_cst<float>(desc, 0.0, C);
-        launch_neighbors<float>(PA, C, (const float *)pos, idx, cnt, true_cnt, st);
+        if (wide_path(desc)) {
+            float *fr = adaptive ? (float *)desc->grid_frame : nullptr;
+            if (adaptive)
+                launch_grid_frame<float>((const float *)pos, (int64_t)C.E * C.A,
+                                         (float)desc->neighbor_radius, C.grid_bins, fr, st);
+            launch_wide_lists<float>(C, (const float *)pos, fr, idx, cnt, true_cnt, st);
+        } else {
+            launch_neighbors<float>(PA, C, (const float *)pos, idx, cnt, true_cnt, st);
+        }
     } else {
+        if (wide_path(desc) && wide_lds_check<double>(desc)) return -1;
         Cst<double> C;
         fill_cst<double>(desc, 0.0, C);
-        launch_neighbors<double>(PA, C, (const double *)pos, idx, cnt, true_cnt, st);
+        if (wide_path(desc)) {
+            double *fr = adaptive ? (double *)desc->grid_frame : nullptr;
+            if (adaptive)
+                launch_grid_frame<double>((const double *)pos, (int64_t)C.E * C.A,
+                                          desc->neighbor_radius, C.grid_bins, fr, st);
+            launch_wide_lists<double>(C, (const double *)pos, fr, idx, cnt, true_cnt, st);
+        } else {
+            launch_neighbors<double>(PA, C, (const double *)pos, idx, cnt, true_cnt, st);
+        }
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
@@ -636,6 +708,8 @@ int swarp_nav_obs(const swarp_desc_t *desc, const swarp_nav_t *nav, void *stream
 {
     g_err[0] = 0;
     if (check_desc(desc)) return -1;
+    if (wide_path(desc))
+        return fail("the fused navigation pass takes at most 64 agents per env with index-ordered lists");
     if (!nav) return fail("nav is NULL");
     if (desc->max_neighbors < 1) return fail("max_neighbors must be >= 1");
     if (nav->k_obs < 0 || nav->k_obs > desc->max_neighbors)

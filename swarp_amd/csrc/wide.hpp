@@ -1,0 +1,577 @@
+// wide.hpp -- envs of up to 1024 agents, and the uniform-grid list order.
+//
+// The generic and specialised kernels put a whole env into one wave (at most 64 agents,
+// the lists as 64-bit masks).  These kernels give each env one workgroup of ceil(A/64)
+// waves, one lane per agent, with the env's positions, velocities and radii in LDS.  They
+// serve every 2-D or drone fleet (any model, control mode, obstacles, walls, clamp,
+// integrator) of more than 64 agents per env, and every fleet whose lists follow the
+// uniform grid.
+//
+// List order (which K in-radius neighbours a capped list keeps, and the order the pair
+// forces are summed in):
+//   brute  ascending agent index (_brute_force, swarp/core/neighbors.py:76-97);
+//   grid   the uniform grid's (_query_uniform, swarp/core/neighbors.py:214-251): the cells
+//          of the 3x3 block around the agent's cell row by row (dy outer, dx inner), the
+//          agents of a cell in ascending index (the stable sort of the (env, cell) keys,
+//          :184-211, 663-666).  A cell is (int)((p - origin) / cell_size) per axis,
+//          clamped to [0, bins); the frame (origin, cell size) is pinned by the world
+//          bounds or, for list builds, reduced over the batch (:149-181).
+// Every list position has a traversal key -- the agent index (brute), or slot * 1024 +
+// rank in its cell with slot = 3 (dy + 1) + (dx + 1) (grid) -- increasing along the
+// traversal, so "j is in i's capped list" is "j within radius of i and key_i(j) <=
+// cut_i", where cut_i is the key of i's K-th listed neighbour (INT_MAX when fewer).  The
+// backward gathers each pair's two sides with that test, as the generic kernels do with
+// their masks.
+//
+// The backward recomputes, for each substep in reverse, the substeps before it from the
+// step's checkpoint (S (S + 1) / 2 forward substeps per step): no per-substep state of
+// the env has to fit in LDS.
+#pragma once
+#include "common.hpp"
+
+namespace swarp {
+
+constexpr int WIDE_MAX_AGENTS = 1024;
+constexpr int GRID_MAX_CELLS = 4096;   // bins^2 cell offsets in LDS
+constexpr int32_t CUT_ALL = 0x7fffffff;
+
+// Uniform-grid frame of one launch: origin and cell size (from Cst for a pinned frame,
+// from `frame` [3] on the device for a batch-reduced one).
+template <typename T> struct GridFrame {
+    T ox, oy, cs;
+    int bins;
+};
+
+// One axis of a cell index (_compute_keys / _query_uniform, swarp/core/neighbors.py:
+// 188-193, 230-232): truncation toward zero of (p - o) / cs, clamped to [0, bins).
+template <typename T> __device__ __forceinline__ int grid_axis(T p, T o, T cs, int bins)
+{
+    const T q = (p - o) / cs;
+    int c = (int)q;
+    if (!(q == q)) c = 0;
+    return c < 0 ? 0 : (c > bins - 1 ? bins - 1 : c);
+}
+
+// LDS of one wide workgroup (AP = waves * 64 agent slots, NC = cells or 0).
+template <typename T> struct WideLds {
+    T *px, *py, *vx, *vy, *rad, *wfx, *wfy;
+    int32_t *cut, *key, *rank, *sorted, *cstart;
+};
+
+template <typename T> __host__ __device__ inline size_t wide_lds_bytes(int AP, int NC)
+{
+    return (size_t)AP * (7 * sizeof(T) + 4 * sizeof(int32_t)) + (size_t)(NC + 1) * sizeof(int32_t);
+}
+
+template <typename T> __device__ __forceinline__ WideLds<T> wide_lds(unsigned char *smem, int AP)
+{
+    WideLds<T> W;
+    T *t = (T *)smem;
+    W.px = t;
+    W.py = t + AP;
+    W.vx = t + 2 * AP;
+    W.vy = t + 3 * AP;
+    W.rad = t + 4 * AP;
+    W.wfx = t + 5 * AP;
+    W.wfy = t + 6 * AP;
+    int32_t *q = (int32_t *)(t + 7 * AP);
+    W.cut = q;
+    W.key = q + AP;
+    W.rank = q + 2 * AP;
+    W.sorted = q + 3 * AP;
+    W.cstart = q + 4 * AP;
+    return W;
+}
+
+// Exclusive prefix sum of v[0 .. n) in place over the workgroup; v[n] = the total.
+__device__ inline void block_exclusive_scan(int32_t *v, int n, int32_t *wsum)
+{
+    const int nt = blockDim.x, tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int per = (n + nt - 1) / nt;
+    const int lo = tid * per, hi = min(n, lo + per);
+    int32_t s = 0;
+    for (int c = lo; c < hi; ++c) s += v[c];
+    int32_t x = s;  // inclusive scan of the per-thread sums
+    for (int d = 1; d < 64; d <<= 1) {
+        const int32_t y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) wsum[wv] = x;
+    __syncthreads();
+    int32_t before = 0;
+    for (int w = 0; w < wv; ++w) before += wsum[w];
+    int32_t run = before + x - s;
+    __syncthreads();
+    for (int c = lo; c < hi; ++c) {
+        const int32_t t = v[c];
+        v[c] = run;
+        run += t;
+    }
+    if (tid == nt - 1) v[n] = before + x;
+    __syncthreads();
+}
+
+// Cells of the env's agents: key[i] (cell id), rank[i] (agents of the same cell with a
+// smaller index), cstart[c] (first sorted slot of cell c, cstart[NC] = A), sorted[]
+// (agent indices cell by cell, ascending within a cell).  The
+// positions are in W.px / W.py.  Every thread of the workgroup calls it.
+template <typename T>
+__device__ inline void grid_build(const WideLds<T> &W, int A, const GridFrame<T> &G,
+                                  int32_t *wsum)
+{
+    const int tid = threadIdx.x, nt = blockDim.x, NC = G.bins * G.bins;
+    for (int c = tid; c < NC; c += nt) W.cstart[c] = 0;
+    __syncthreads();
+    int k = 0;
+    if (tid < A) {
+        const int cx = grid_axis(W.px[tid], G.ox, G.cs, G.bins);
+        const int cy = grid_axis(W.py[tid], G.oy, G.cs, G.bins);
+        k = cy * G.bins + cx;
+        W.key[tid] = k;
+        atomicAdd(&W.cstart[k], 1);
+    }
+    __syncthreads();
+    block_exclusive_scan(W.cstart, NC, wsum);
+    if (tid < A) {
+        int r = 0;  // agents of the same cell with a smaller index
+        for (int j = 0; j < tid; ++j) r += W.key[j] == k ? 1 : 0;
+        W.rank[tid] = r;
+        W.sorted[W.cstart[k] + r] = tid;
+    }
+    __syncthreads();
+}
+
+// Visits agent i's in-radius neighbours in list order: f(j, traversal key) for each of the
+// first `limit` of them.  Returns the number of in-radius neighbours visited (all of them
+// when count_all, else at most limit).  Positions from W.
+template <typename T, bool GRID, typename Fn>
+__device__ __forceinline__ int visit_list(const WideLds<T> &W, int A, const GridFrame<T> &G,
+                                          int i, T px, T py, T t_nbr, int limit, bool count_all,
+                                          Fn &&f)
+{
+    int n = 0;
+    if (!GRID) {
+        for (int j0 = 0; j0 < A; j0 += 64) {
+            uint64_t m = 0;
+            const int jn = min(64, A - j0);
+            for (int b = 0; b < jn; ++b) {
+                const int j = j0 + b;
+                const T dx = W.px[j] - px, dy = W.py[j] - py;
+                const T d2 = dx * dx + dy * dy;
+                m |= (d2 <= t_nbr && j != i) ? (1ull << b) : 0ull;
+            }
+            while (m && n < limit) {
+                const int b = __builtin_ctzll(m);
+                m &= m - 1;
+                f(j0 + b, j0 + b);
+                ++n;
+            }
+            if (count_all) n += __builtin_popcountll(m);
+            if (!count_all && n >= limit) break;
+        }
+        return n;
+    }
+    const int k = W.key[i], cx = k % G.bins, cy = k / G.bins;
+    for (int sy = 0; sy < 3; ++sy) {
+        const int ny = cy + sy - 1;
+        if (ny < 0 || ny >= G.bins) continue;
+        for (int sx = 0; sx < 3; ++sx) {
+            const int nx = cx + sx - 1;
+            if (nx < 0 || nx >= G.bins) continue;
+            const int c = ny * G.bins + nx, c0 = W.cstart[c], c1 = W.cstart[c + 1];
+            for (int si = c0; si < c1; ++si) {
+                const int j = W.sorted[si];
+                const T dx = W.px[j] - px, dy = W.py[j] - py;
+                const T d2 = dx * dx + dy * dy;
+                if (!(d2 <= t_nbr) || j == i) continue;
+                if (n < limit) f(j, (3 * sy + sx) * 1024 + (si - c0));
+                ++n;
+                if (!count_all && n >= limit) return n;
+            }
+        }
+    }
+    return n;
+}
+
+// Traversal key of agent i's position in agent j's grid list (i within radius of j, so
+// i's cell lies in the 3x3 block around j's).
+template <typename T>
+__device__ __forceinline__ int32_t grid_key_in(const WideLds<T> &W, int bins, int i, int j)
+{
+    const int ki = W.key[i], kj = W.key[j];
+    const int sx = ki % bins - kj % bins + 1, sy = ki / bins - kj / bins + 1;
+    return (3 * sy + sx) * 1024 + W.rank[i];
+}
+
+// Frame of this launch.
+template <typename T>
+__device__ __forceinline__ GridFrame<T> grid_frame(const Cst<T> &C, const T *frame)
+{
+    GridFrame<T> G;
+    G.bins = C.grid_bins;
+    if (frame) {
+        G.ox = frame[0];
+        G.oy = frame[1];
+        G.cs = frame[2];
+    } else {
+        G.ox = C.grid_ox;
+        G.oy = C.grid_oy;
+        G.cs = C.grid_cs;
+    }
+    return G;
+}
+
+// ------------------------------------------------------------------ frame reduction
+
+// _bounds_init / _bounds_reduce / _finalize_grid (swarp/core/neighbors.py:149-181): the
+// batch's min corner, extent max(dx, dy), cell size max(radius, extent / bins), in T.
+template <typename T>
+__global__ __launch_bounds__(1024) void k_grid_frame(const T *pos, int64_t n, T radius, int bins,
+                                                     T *frame)
+{
+    __shared__ T red[4][16];
+    const T big = T(1e30);
+    T mnx = big, mny = big, mxx = -big, mxy = -big;
+    for (int64_t q = threadIdx.x; q < n; q += 1024) {
+        const T x = pos[2 * q], y = pos[2 * q + 1];
+        mnx = x < mnx ? x : mnx;
+        mny = y < mny ? y : mny;
+        mxx = x > mxx ? x : mxx;
+        mxy = y > mxy ? y : mxy;
+    }
+    for (int d = 32; d > 0; d >>= 1) {
+        const T a = __shfl_down(mnx, d, 64), b = __shfl_down(mny, d, 64);
+        const T c = __shfl_down(mxx, d, 64), e = __shfl_down(mxy, d, 64);
+        mnx = a < mnx ? a : mnx;
+        mny = b < mny ? b : mny;
+        mxx = c > mxx ? c : mxx;
+        mxy = e > mxy ? e : mxy;
+    }
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    if (lane == 0) {
+        red[0][wv] = mnx;
+        red[1][wv] = mny;
+        red[2][wv] = mxx;
+        red[3][wv] = mxy;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 16; ++w) {
+            mnx = red[0][w] < mnx ? red[0][w] : mnx;
+            mny = red[1][w] < mny ? red[1][w] : mny;
+            mxx = red[2][w] > mxx ? red[2][w] : mxx;
+            mxy = red[3][w] > mxy ? red[3][w] : mxy;
+        }
+        const T ex = mxx - mnx, ey = mxy - mny;
+        const T ext = ex > ey ? ex : ey;
+        const T q = ext / T(bins);
+        frame[0] = mnx;
+        frame[1] = mny;
+        frame[2] = radius > q ? radius : q;
+    }
+}
+
+// ------------------------------------------------------------------ neighbour lists
+
+// Padded lists, counts and true counts of one env per workgroup (brute or grid order).
+template <typename T, bool GRID>
+__global__ __launch_bounds__(1024) void k_wide_lists(const Cst<T> C, const T *pos, const T *frame,
+                                                     int32_t *idx, int32_t *cnt, int32_t *tru)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int32_t wsum[16];
+    const int AP = blockDim.x, i = threadIdx.x, A = C.A, env = blockIdx.x;
+    const WideLds<T> W = wide_lds<T>(smem, AP);
+    const GridFrame<T> G = grid_frame(C, frame);
+    const size_t row = (size_t)env * A + (i < A ? i : 0);
+    const T px = i < A ? pos[2 * row] : T(0), py = i < A ? pos[2 * row + 1] : T(0);
+    W.px[i] = px;
+    W.py[i] = py;
+    __syncthreads();
+    if (GRID) grid_build(W, A, G, wsum);
+    if (i >= A) return;
+    int32_t *out = idx + row * C.K;
+    const int n = visit_list<T, GRID>(W, A, G, i, px, py, C.t_nbr, C.K, true,
+                                      [&](int j, int32_t) { *out++ = j; });
+    const int c = n < C.K ? n : C.K;
+    for (int q = c; q < C.K; ++q) idx[row * C.K + q] = 0;
+    cnt[row] = c;
+    if (tru) tru[row] = n;
+}
+
+// ------------------------------------------------------------------ rollout kernels
+
+template <typename T> struct WLane {
+    int i, env;
+    bool active;
+    size_t idx;
+    Prm<T> pr;
+    T dd, inv_dd;
+    Dv<T> ddv;
+};
+
+template <typename T, unsigned F>
+__device__ __forceinline__ void wide_init(const Cst<T> &C, const Args<T> &g, WLane<T> &L)
+{
+    L.i = threadIdx.x;
+    L.env = blockIdx.x;
+    L.active = L.i < C.A;
+    const int ag = L.active ? L.i : 0;
+    L.idx = (size_t)L.env * C.A + ag;
+    load_prm(g, C.per_env ? L.idx : (size_t)ag, ag, L.pr);
+    fold_prm<F>(L.pr);
+    L.dd = T(1) + C.c * C.sub_dt / L.pr.mass;
+    L.inv_dd = T(1) / L.dd;
+    L.ddv = divisor(L.dd, true);
+}
+
+// Publishes the substep's positions and velocities (and the grid) -- every thread.
+template <typename T, bool GRID>
+__device__ __forceinline__ void wide_publish(const Cst<T> &C, const WideLds<T> &W,
+                                             const GridFrame<T> &G, const WLane<T> &L,
+                                             const St<T> &st, int32_t *wsum)
+{
+    __syncthreads();
+    W.px[L.i] = st.px;
+    W.py[L.i] = st.py;
+    W.vx[L.i] = st.vx;
+    W.vy[L.i] = st.vy;
+    __syncthreads();
+    if (GRID && C.collisions) grid_build(W, C.A, G, wsum);
+}
+
+// Contact and static forces of the lane's agent (collision_forces_kernel, swarp/core/
+// collisions.py:818-881: listed pairs in list order, then obstacles, then walls); `cut`
+// receives the key of the K-th listed neighbour (CUT_ALL when the list is not full).
+template <typename T, bool GRID>
+__device__ __forceinline__ void wide_forces(const Cst<T> &C, const Args<T> &g,
+                                            const WideLds<T> &W, const GridFrame<T> &G,
+                                            const WLane<T> &L, const St<T> &st, T &Fx, T &Fy,
+                                            int32_t &cut)
+{
+    T fx = T(0), fy = T(0);
+    cut = CUT_ALL;
+    if (C.collisions && L.active) {
+        const T ra = L.pr.radius;
+        int n = 0;
+        int32_t last = CUT_ALL;
+        visit_list<T, GRID>(W, C.A, G, L.i, st.px, st.py, C.t_nbr, C.K, false,
+                            [&](int j, int32_t key) {
+                                T gx, gy;
+                                pair_force(C, st.px - W.px[j], st.py - W.py[j], st.vx - W.vx[j],
+                                           st.vy - W.vy[j], ra + W.rad[j] + C.margin, L.dd, gx, gy);
+                                fx += gx;
+                                fy += gy;
+                                last = key;
+                                ++n;
+                            });
+        if (n >= C.K) cut = last;
+    }
+    T sx = T(0), sy = T(0);
+    if (C.N > 0 && L.active) {
+        const size_t eN = (size_t)L.env * C.N;
+        for (int o = 0; o < C.N; ++o) {
+            T gx, gy;
+            obstacle_force(C, g.obs, eN, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.dd, gx, gy);
+            sx += gx;
+            sy += gy;
+        }
+    }
+    if (C.soft_walls) {
+        T gx, gy;
+        unsigned wb;
+        wall_force_axes(C, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv, gx, gy, wb);
+        sx += gx;
+        sy += gy;
+    }
+    Fx = fx + sx;
+    Fy = fy + sy;
+}
+
+template <typename T, bool DRONE, bool GRID>
+__device__ __forceinline__ void wide_substep(const Cst<T> &C, const Args<T> &g,
+                                             const WideLds<T> &W, const GridFrame<T> &G,
+                                             const WLane<T> &L, const T (&a)[4], St<T> &st,
+                                             int32_t *wsum)
+{
+    T Fx = T(0), Fy = T(0);
+    if (C.needs_forces) {
+        if (C.collisions) wide_publish<T, GRID>(C, W, G, L, st, wsum);
+        int32_t cut;
+        wide_forces<T, GRID>(C, g, W, G, L, st, Fx, Fy, cut);
+    }
+    St<T> nx;
+    integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
+    st = nx;
+}
+
+template <typename T, bool DRONE, bool GRID, unsigned F>
+__global__ __launch_bounds__(1024) void k_wide_fwd(const Cst<T> Cin, const Args<T> g)
+{
+    const Cst<T> C = fold_cst<F>(Cin);
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int32_t wsum[16];
+    const WideLds<T> W = wide_lds<T>(smem, blockDim.x);
+    const GridFrame<T> G = grid_frame(C, (const T *)nullptr);
+    WLane<T> L;
+    wide_init<T, F>(C, g, L);
+    W.rad[L.i] = L.pr.radius;
+    St<T> st;
+    load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
+    const size_t EA = (size_t)C.E * C.A;
+    for (int t = 0; t < g.nsteps; ++t) {
+        T a[4];
+        load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
+        for (int s = 0; s < C.S; ++s) wide_substep<T, DRONE, GRID>(C, g, W, G, L, a, st, wsum);
+        if (L.active) {
+            if (t + 1 < g.nsteps)
+                store_state<T, DRONE>(g.traj.f, (size_t)t * EA + L.idx, st);
+            else
+                store_state<T, DRONE>(g.fin.f, L.idx, st);
+        }
+    }
+}
+
+template <typename T, bool DRONE, bool GRID, unsigned F>
+__global__ __launch_bounds__(1024) void k_wide_bwd(const Cst<T> Cin, const Args<T> g)
+{
+    const Cst<T> C = fold_cst<F>(Cin);
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ int32_t wsum[16];
+    const WideLds<T> W = wide_lds<T>(smem, blockDim.x);
+    const GridFrame<T> G = grid_frame(C, (const T *)nullptr);
+    WLane<T> L;
+    wide_init<T, F>(C, g, L);
+    W.rad[L.i] = L.pr.radius;
+    const size_t EA = (size_t)C.E * C.A;
+    St<T> gs;
+    st_zero(gs);
+    for (int t = g.nsteps - 1; t >= 0; --t) {
+        if (L.active) {
+            if (t == g.nsteps - 1)
+                add_adj<T, DRONE>(g.afin.f, L.idx, gs);
+            else
+                add_adj<T, DRONE>(g.atraj.f, (size_t)t * EA + L.idx, gs);
+        }
+        St<T> st0;
+        if (t == 0)
+            load_state<T, DRONE>(g.s0.f, L.idx, 0, st0);
+        else
+            load_state<T, DRONE>(g.traj.f, L.idx, (size_t)(t - 1) * EA, st0);
+        T a[4];
+        load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
+        T ga[4] = {T(0), T(0), T(0), T(0)};
+        for (int s = C.S - 1; s >= 0; --s) {
+            // the substep's input, recomputed from the step's checkpoint
+            St<T> in = st0;
+            for (int q = 0; q < s; ++q) wide_substep<T, DRONE, GRID>(C, g, W, G, L, a, in, wsum);
+            T Fx = T(0), Fy = T(0);
+            int32_t cut = CUT_ALL;
+            if (C.needs_forces) {
+                if (C.collisions) wide_publish<T, GRID>(C, W, G, L, in, wsum);
+                wide_forces<T, GRID>(C, g, W, G, L, in, Fx, Fy, cut);
+            }
+            St<T> gi;
+            T gFx, gFy;
+            integrate_adj<T, DRONE>(C, L.pr, in, a, Fx, Fy, gs, gi, ga, gFx, gFy);
+            if (C.needs_forces) {
+                if (C.collisions) {
+                    const T wFx = gFx * L.inv_dd, wFy = gFy * L.inv_dd;
+                    W.wfx[L.i] = wFx;
+                    W.wfy[L.i] = wFy;
+                    W.cut[L.i] = cut;
+                    __syncthreads();
+                    if (L.active) {
+                        // every in-radius pair, both sides: own (j in i's list), rev (i in j's)
+                        visit_list<T, GRID>(
+                            W, C.A, G, L.i, in.px, in.py, C.t_nbr, C.A, false,
+                            [&](int j, int32_t key) {
+                                const bool own = key <= cut;
+                                const int32_t kin = GRID ? grid_key_in(W, G.bins, L.i, j) : L.i;
+                                const bool rev = kin <= W.cut[j];
+                                if (!own && !rev) return;
+                                const T wx = (own ? wFx : T(0)) - (rev ? W.wfx[j] : T(0));
+                                const T wy = (own ? wFy : T(0)) - (rev ? W.wfy[j] : T(0));
+                                pair_adj_combined(C, in.px - W.px[j], in.py - W.py[j],
+                                                  in.vx - W.vx[j], in.vy - W.vy[j],
+                                                  L.pr.radius + W.rad[j] + C.margin, wx, wy,
+                                                  gi.px, gi.py, gi.vx, gi.vy);
+                            });
+                    }
+                }
+                if (L.active) {
+                    if (C.N > 0) {
+                        const size_t eN = (size_t)L.env * C.N;
+                        for (int o = 0; o < C.N; ++o)
+                            obstacle_force_adj(C, g.obs, eN, o, in.px, in.py, in.vx, in.vy,
+                                               L.pr.radius, L.dd, gFx, gFy, gi);
+                    }
+                    if (C.soft_walls)
+                        wall_force_adj(C, in.px, in.py, in.vx, in.vy, L.pr.radius, L.dd, gFx,
+                                       gFy, gi);
+                }
+            }
+            gs = gi;
+        }
+        if (L.active) {
+            T *pa = g.aact + ((size_t)t * EA + L.idx) * C.ad;
+            for (int k = 0; k < C.ad; ++k) pa[k] = k < 4 ? ga[k] : T(0);
+        }
+    }
+    if (L.active) store_adj<T, DRONE>(g.a0.f, L.idx, gs);
+}
+
+// ---------------------------------------------------------------------- launchers
+
+template <typename T> inline int wide_threads(int A) { return ((A + 63) / 64) * 64; }
+
+template <typename T> size_t wide_shm(const Cst<T> &C)
+{
+    return wide_lds_bytes<T>(wide_threads<T>(C.A), C.grid_bins > 0 ? C.grid_bins * C.grid_bins : 0);
+}
+
+template <typename T>
+void launch_wide_lists(const Cst<T> &C, const T *pos, const T *frame, int32_t *idx, int32_t *cnt,
+                       int32_t *tru, hipStream_t st)
+{
+    const dim3 grid(C.E), block(wide_threads<T>(C.A));
+    const size_t shm = wide_shm<T>(C);
+    if (C.grid_bins > 0)
+        hipLaunchKernelGGL((k_wide_lists<T, true>), grid, block, shm, st, C, pos, frame, idx, cnt, tru);
+    else
+        hipLaunchKernelGGL((k_wide_lists<T, false>), grid, block, shm, st, C, pos, frame, idx, cnt, tru);
+}
+
+template <typename T>
+void launch_grid_frame(const T *pos, int64_t n, T radius, int bins, T *frame, hipStream_t st)
+{
+    hipLaunchKernelGGL((k_grid_frame<T>), dim3(1), dim3(1024), 0, st, pos, n, radius, bins, frame);
+}
+
+#define SWARP_WIDE_DISPATCH(KERNEL)                                                            \
+    if (drone) {                                                                               \
+        if (grid) hipLaunchKernelGGL((KERNEL<T, true, true, FT_ALL>), g, b, shm, st, C, a);    \
+        else hipLaunchKernelGGL((KERNEL<T, true, false, FT_ALL>), g, b, shm, st, C, a);        \
+    } else {                                                                                   \
+        if (grid) hipLaunchKernelGGL((KERNEL<T, false, true, FT_ALL>), g, b, shm, st, C, a);   \
+        else hipLaunchKernelGGL((KERNEL<T, false, false, FT_ALL>), g, b, shm, st, C, a);       \
+    }
+
+template <typename T> void launch_wide_fwd(bool drone, const Cst<T> &C, const Args<T> &a, hipStream_t st)
+{
+    const dim3 g(C.E), b(wide_threads<T>(C.A));
+    const size_t shm = wide_shm<T>(C);
+    const bool grid = C.grid_bins > 0;
+    SWARP_WIDE_DISPATCH(k_wide_fwd)
+}
+
+template <typename T> void launch_wide_bwd(bool drone, const Cst<T> &C, const Args<T> &a, hipStream_t st)
+{
+    const dim3 g(C.E), b(wide_threads<T>(C.A));
+    const size_t shm = wide_shm<T>(C);
+    const bool grid = C.grid_bins > 0;
+    SWARP_WIDE_DISPATCH(k_wide_bwd)
+}
+#undef SWARP_WIDE_DISPATCH
+
+}  // namespace swarp

@@ -1,21 +1,100 @@
 """Padded radius-neighbour lists, overflow flag and COO radius graph.
 
-Counterpart of ``NeighborGrid`` (``swarp/core/neighbors.py:334-733``) for the brute
-method, which the reference itself selects for <= 512 agents per env
-(``:388-389``): ``build`` / ``query_into`` fill ``neighbor_idx [E,A,K]``,
-``neighbor_count [E,A]`` and ``neighbor_true_count [E,A]`` on the HIP device;
-``overflow_view`` and ``edge_index`` keep the reference's semantics (including the
-one host sync ``edge_index`` needs for the edge count).  Entries of ``neighbor_idx``
-past the count are zero.
+Counterpart of ``NeighborGrid`` (``swarp/core/neighbors.py:334-733``):
+``build`` / ``query_into`` fill ``neighbor_idx [E,A,K]``, ``neighbor_count [E,A]`` and
+``neighbor_true_count [E,A]`` on the HIP device in the order of the resolved method --
+``"brute"`` (ascending agent index, ``:76-97``) or ``"uniform_grid"`` (the 3x3 cell block
+row by row, ascending index within a cell, ``:149-254, 622-687``), ``"auto"`` picking the
+grid above 512 agents as the reference does (``:388-389``).  The grid frame is pinned by
+``bounds`` or reduced over the batch on every build.  ``overflow_view`` and
+``edge_index`` keep the reference's semantics (including the one host sync
+``edge_index`` needs for the edge count).  Entries of ``neighbor_idx`` past the count are
+zero.  The hash-grid method (``"grid"``, Warp's ``HashGrid``, whose query order is
+Warp's) is not built.
 """
 
 from __future__ import annotations
 
 import ctypes
+import math
+import warnings
 
 import torch
 
 from . import _lib
+
+
+def resolve_method(method: str, n_agents: int) -> str:
+    """NeighborGrid's choice of list order (``swarp/core/neighbors.py:387-389``)."""
+    if method == "auto":
+        return "uniform_grid" if n_agents > 512 else "brute"
+    return method
+
+
+def grid_bins(n_agents: int, uniform_bins: int | None) -> int:
+    """Cells per axis of the uniform grid (``swarp/core/neighbors.py:390-393``)."""
+    return uniform_bins or max(4, min(128, int(math.ceil(math.sqrt(n_agents)))))
+
+
+def pinned_frame(bounds, radius: float, bins: int) -> tuple[float, float, float]:
+    """The frame a world rectangle pins, in float64 as the reference computes it
+    (``NeighborGrid._fill_static_grid``, ``swarp/core/neighbors.py:476-490``):
+    origin (x_min, y_min), cell size max(radius, extent / bins)."""
+    x_min, x_max, y_min, y_max = bounds
+    extent = max(x_max - x_min, y_max - y_min)
+    return float(x_min), float(y_min), float(max(radius, extent / bins))
+
+
+def fill_list_order(d, method: str, n_agents: int, uniform_bins: int | None, bounds,
+                    radius: float) -> None:
+    """The descriptor's list-order fields for a resolved method."""
+    if method == "uniform_grid":
+        bins = grid_bins(n_agents, uniform_bins)
+        d.neighbor_method = _lib.LISTS_GRID
+        d.grid_bins = bins
+        if bounds is not None:
+            ox, oy, cs = pinned_frame(bounds, radius, bins)
+            d.grid_pinned = 1
+            d.grid_origin[0], d.grid_origin[1] = ox, oy
+            d.grid_cell = cs
+    else:
+        d.neighbor_method = _lib.LISTS_BRUTE
+
+
+def _check_bins(bins: int) -> None:
+    if bins > 64:
+        raise NotImplementedError(
+            f"uniform_bins={bins}: this build keeps at most 64 x 64 cells per env in LDS")
+
+
+def check_list_method(method: str, n_agents: int, uniform_bins: int | None,
+                      stepping: bool = False) -> str:
+    """Validates a NeighborGrid / WorldConfig method for this build; returns the resolved
+    method.  ``stepping``: the lists also order the step's contact sums, so the cell
+    limit of the wide-env kernels applies now rather than at the first build."""
+    if method not in ("auto", "grid", "brute", "uniform_grid"):
+        raise ValueError('method must be "auto", "grid", "brute", or "uniform_grid"')
+    if method == "grid":
+        raise NotImplementedError(
+            'method="grid" (Warp\'s HashGrid, whose query order is Warp\'s own) is not built; '
+            'use "brute" or "uniform_grid"')
+    if uniform_bins is not None and uniform_bins < 1:
+        raise ValueError("uniform_bins must be >= 1")
+    if n_agents > _lib.WIDE_MAX_AGENTS:
+        raise NotImplementedError(
+            f"this build lists at most {_lib.WIDE_MAX_AGENTS} agents per env (one workgroup "
+            "per env)")
+    m = resolve_method(method, n_agents)
+    if m == "uniform_grid":
+        bins = grid_bins(n_agents, uniform_bins)
+        if stepping:
+            _check_bins(bins)
+        if bins * bins > 16 * max(1, n_agents):
+            warnings.warn(
+                f"uniform_bins={bins} gives {bins * bins} cells per env for {n_agents} agents; "
+                "the default heuristic (~sqrt(n_agents)) keeps occupancy near one agent per "
+                "cell.", RuntimeWarning, stacklevel=3)
+    return m
 
 
 class NeighborGrid:
@@ -34,14 +113,9 @@ class NeighborGrid:
     ) -> None:
         if radius <= 0.0:
             raise ValueError("radius must be positive")
-        if method not in ("auto", "grid", "brute", "uniform_grid"):
-            raise ValueError('method must be "auto", "grid", "brute", or "uniform_grid"')
-        if method in ("grid", "uniform_grid"):
-            raise NotImplementedError(f"method={method!r}: only the brute-force lists are built")
         if max_neighbors < 1:
             raise ValueError("max_neighbors must be >= 1")
-        if n_agents > 64:
-            raise NotImplementedError("this build lists at most 64 agents per env")
+        method = check_list_method(method, n_agents, uniform_bins)
         from .stepper import resolve_dtype
 
         self.n_envs = n_envs
@@ -50,9 +124,9 @@ class NeighborGrid:
         self.max_neighbors = max_neighbors
         self.device = str(device)
         self.dtype = resolve_dtype(dtype)
-        self.method = "brute"
+        self.method = method
         self.grid_dim = grid_dim
-        self.uniform_bins = uniform_bins
+        self.uniform_bins = grid_bins(n_agents, uniform_bins)
         self._bounds = bounds
         z = {"device": self.device, "dtype": torch.int32}
         self.neighbor_idx = torch.zeros(n_envs, n_agents, max_neighbors, **z)
@@ -60,29 +134,55 @@ class NeighborGrid:
         self.neighbor_true_count = torch.zeros(n_envs, n_agents, **z)
         self.build_count = 0
         self.built_version = -1
+        # the batch-reduced grid frame (origin x, y, cell size) of the last build
+        self._frame = torch.zeros(3, device=self.device, dtype=self.dtype)
+        self._descs = {m: self._make_desc(m) for m in ("brute", "uniform_grid")}
+
+    def _make_desc(self, method: str):
         d = _lib.SwarpDesc()
         d.abi_version = _lib.ABI_VERSION
         d.dtype = _lib.F64 if self.dtype == torch.float64 else _lib.F32
-        d.n_envs = n_envs
-        d.n_agents = n_agents
+        d.n_envs = self.n_envs
+        d.n_agents = self.n_agents
         d.act_dim = 2
         d.substeps = 1
-        d.max_neighbors = max_neighbors
+        d.max_neighbors = self.max_neighbors
         d.collisions = 1
-        d.neighbor_radius = float(radius)
+        d.neighbor_radius = float(self.radius)
         d.dt = 1.0
-        self._desc = d
+        fill_list_order(d, method, self.n_agents, self.uniform_bins, self._bounds, self.radius)
+        if method == "uniform_grid" and not d.grid_pinned:
+            d.grid_frame = self._frame.data_ptr()
+        return d
 
     def build(self, pos: torch.Tensor, reset_mask=None) -> None:
         """Refresh the internal lists from positions ``[n_envs, n_agents, 2]``."""
         self.query_into(pos, self.neighbor_idx, self.neighbor_count)
 
     def build_brute_force(self, pos: torch.Tensor) -> None:
-        self.query_into(pos, self.neighbor_idx, self.neighbor_count)
+        """Force the index-ordered lists into the internal buffers."""
+        self._query(pos, self.neighbor_idx, self.neighbor_count, "brute")
+
+    def build_uniform(self, pos: torch.Tensor) -> None:
+        """Force the uniform-grid lists into the internal buffers."""
+        self._query(pos, self.neighbor_idx, self.neighbor_count, "uniform_grid")
+
+    def build_grid(self, pos: torch.Tensor) -> None:
+        raise NotImplementedError("the hash-grid lists (Warp's HashGrid order) are not built")
+
+    def grid_frame(self) -> torch.Tensor:
+        """The batch-reduced frame of the last uniform-grid build: origin x, origin y,
+        cell size (a pinned frame is not written here)."""
+        return self._frame
 
     def query_into(self, pos: torch.Tensor, neighbor_idx: torch.Tensor,
                    neighbor_count: torch.Tensor, reset_mask=None) -> None:
         """Write padded lists into caller-owned int32 buffers (true count into the grid's)."""
+        self._query(pos, neighbor_idx, neighbor_count, self.method)
+
+    def _query(self, pos, neighbor_idx, neighbor_count, method: str) -> None:
+        if method == "uniform_grid":
+            _check_bins(self.uniform_bins)
         if pos.shape != (self.n_envs, self.n_agents, 2):
             raise ValueError(
                 f"pos must be [{self.n_envs}, {self.n_agents}, 2]; got {tuple(pos.shape)}"
@@ -98,7 +198,7 @@ class NeighborGrid:
         lib = _lib.load()
         stream = _lib.stream_of(pos.device)
         _lib.check(lib.swarp_neighbors(
-            ctypes.byref(self._desc), pos.data_ptr(), neighbor_idx.data_ptr(),
+            ctypes.byref(self._descs[method]), pos.data_ptr(), neighbor_idx.data_ptr(),
             neighbor_count.data_ptr(), self.neighbor_true_count.data_ptr(), stream,
         ))
         self.build_count += 1

@@ -117,8 +117,12 @@ class Scenario(ABC):
     fused_active: bool = False
 
     def set_fused_active(self, on: bool) -> None:
-        """Route the next passes through the fused kernels (``on``) or torch."""
-        self.fused_active = bool(on) and self.fused_available
+        """Route the next passes through the fused kernels (``on``) or torch.  The fused
+        pass lists at most 64 agents per env in index order; wider worlds (and grid-ordered
+        lists) take the torch pass over the library's lists."""
+        st = getattr(getattr(self, "world", None), "stepper", None)
+        wide = bool(getattr(st, "wide", False))
+        self.fused_active = bool(on) and self.fused_available and not wide
 
 
 class NavigationScenario(Scenario):

@@ -32,7 +32,7 @@ from .config import (
     WorldConfig,
     action_dim,
 )
-from .neighbors import NeighborGrid
+from .neighbors import NeighborGrid, check_list_method, fill_list_order
 
 
 class AgentParams(NamedTuple):
@@ -168,20 +168,29 @@ class Stepper:
     # ------------------------------------------------------------------ checks
 
     def _check_supported(self) -> None:
-        if self.n_agents > 64:
-            raise NotImplementedError("this build steps at most 64 agents per env")
         w = self.world
+        #: the resolved neighbour-list order ("brute" or "uniform_grid")
+        self.list_method = check_list_method(w.neighbor_method, self.n_agents, w.uniform_bins,
+                                             stepping=True)
+        # envs over 64 agents, or grid-ordered lists, step on the wide-env kernels
+        self.wide = self.n_agents > 64 or self.list_method == "uniform_grid"
+        if self.wide:
+            if any(c.shape == AgentShape.BOX for c in self.configs):
+                raise NotImplementedError(
+                    "box agents step with at most 64 agents per env and index-ordered lists")
+            if w.wheel_contacts:
+                raise NotImplementedError(
+                    "wheel contacts step with at most 64 agents per env and index-ordered lists")
+            if self.list_method == "uniform_grid" and w.collisions and w.bounds is None:
+                raise NotImplementedError(
+                    "stepping with uniform-grid lists needs WorldConfig.bounds: the adaptive "
+                    "grid frame is a reduction over every env at every substep")
         drone = any(c.model == DynamicsModel.DRONE for c in self.configs)
         if w.wheel_contacts and (drone or w.integrator.value != "euler"):
             # swarp/core/stepper.py:852-857
             raise ValueError(
                 "WorldConfig.wheel_contacts runs on the slim Euler 2D path only (no drone "
                 "agents, untaped, Integrator.EULER)")
-        if w.neighbor_method not in ("auto", "brute"):
-            raise NotImplementedError(
-                f"neighbor_method={w.neighbor_method!r}: this build implements the brute-force "
-                "lists only (the reference's own choice at <= 512 agents)"
-            )
 
     # ------------------------------------------------------- per-env parameters
 
@@ -262,6 +271,10 @@ class Stepper:
                 raise NotImplementedError("movable bodies with DRONE agents are not implemented")
             if self.has_boxes:
                 raise NotImplementedError("movable bodies with box agents are not implemented")
+            if self.wide:
+                raise NotImplementedError(
+                    "movable bodies: this build steps them with at most 64 agents per env and "
+                    "index-ordered lists")
             moving = self._moving_shapes(self._obs["kind"], self._obs["body"])
             if bool(((self._obs["type"] != 0) & moving).any()):
                 raise NotImplementedError(
@@ -376,6 +389,8 @@ class Stepper:
         d.ang_damping = float(self.world.obstacle_angular_damping)
         d.integrator = _lib.RK4 if self.world.integrator == Integrator.RK4 else _lib.EULER
         d.skin_speed = self._skin_speed()
+        fill_list_order(d, self.list_method, self.n_agents, self.world.uniform_bins,
+                        self.world.bounds, float(self.neighbor_radius))
         if self.use_profiles:  # 0 (unset) selects the general instances
             d.fleet_models = sum(1 << m for m in {int(c.model) for c in self.configs})
             d.fleet_modes = sum(1 << m for m in {int(c.ctrl_mode) for c in self.configs})

@@ -23,7 +23,18 @@ def oracle_cfg(configs, world: WorldConfig, dt, substeps, n_envs, act_dim, n_thr
     reach = 2.0 * max_r + world.collision_margin
     nbr = (world.neighbor_radius or reach) if collisions else 0.0
     b = world.bounds
+    # list order: NeighborGrid's method choice (swarp/core/neighbors.py:387-393) and the
+    # frame a world rectangle pins (:476-490), in float64
+    method = world.neighbor_method
+    if method == "auto":
+        method = "uniform_grid" if len(configs) > 512 else "brute"
+    grid = {}
+    if method == "uniform_grid" and b is not None:
+        bins = world.uniform_bins or max(4, min(128, int(math.ceil(math.sqrt(len(configs))))))
+        extent = max(b[1] - b[0], b[3] - b[2])
+        grid = dict(grid_bins=bins, grid_ox=b[0], grid_oy=b[2], grid_cell=max(nbr, extent / bins))
     return dict(
+        **grid,
         n_envs=n_envs,
         n_agents=len(configs),
         act_dim=act_dim,

@@ -68,7 +68,7 @@ def test_library_rejects_bad_descriptor_without_gpu():
     assert rc != 0 and b"abi_version" in lib.swarp_last_error()
     d.abi_version = _lib.ABI_VERSION
     d.dtype = 0
-    d.n_envs, d.n_agents, d.act_dim, d.substeps = 1, 65, 2, 1
+    d.n_envs, d.n_agents, d.act_dim, d.substeps = 1, 1025, 2, 1
     rc = lib.swarp_rollout_fwd(ctypes.byref(d), 1, ctypes.byref(s), None, None, ctypes.byref(s), None)
     assert rc != 0 and b"n_agents" in lib.swarp_last_error()
 
@@ -232,6 +232,51 @@ def test_desc_fleet_models_and_modes():
     st.use_profiles = False
     d = st.desc(1, 2)
     assert d.fleet_models == 0 and d.fleet_modes == 0
+
+
+def test_list_method_resolution_and_grid_frame():
+    """NeighborGrid's method choice (swarp/core/neighbors.py:387-393) and the frame a world
+    rectangle pins (:476-490), as the reference's tests pin them
+    (tests/unit/test_neighbors.py:139-163, 201-209, 348-365)."""
+    from swarp_amd import NeighborGrid
+
+    assert NeighborGrid(4, 600, radius=0.1, method="auto", device="cpu").method == "uniform_grid"
+    assert NeighborGrid(4, 512, radius=0.1, method="auto", device="cpu").method == "brute"
+    kw = dict(device="cpu", method="uniform_grid")
+    adaptive = NeighborGrid(4, 600, radius=0.2, **kw)._descs["uniform_grid"]
+    assert adaptive.neighbor_method == _lib.LISTS_GRID and adaptive.grid_pinned == 0
+    assert adaptive.grid_bins == 25 and adaptive.grid_frame
+    # bounds is (x_min, x_max, y_min, y_max): origin = the min corner, cell = the larger
+    # side / bins (4.0 / 25 beats the 0.1 radius), the radius a floor on the cell
+    pinned = NeighborGrid(4, 600, radius=0.1, bounds=(-1.0, 1.0, -2.0, 2.0), **kw)._descs["uniform_grid"]
+    assert pinned.grid_pinned == 1 and list(pinned.grid_origin) == [-1.0, -2.0]
+    assert pinned.grid_cell == pytest.approx(4.0 / 25)
+    coarse = NeighborGrid(4, 600, radius=0.5, bounds=(-1.0, 1.0, -2.0, 2.0), **kw)._descs["uniform_grid"]
+    assert coarse.grid_cell == pytest.approx(0.5)
+    assert NeighborGrid(4, 8, radius=0.2, device="cpu", method="brute")._descs["brute"].neighbor_method == 0
+    with pytest.warns(RuntimeWarning, match="cells per env"):
+        NeighborGrid(2, 8, radius=0.5, device="cpu", method="uniform_grid", uniform_bins=128)
+    import warnings
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        NeighborGrid(2, 8, radius=0.5, device="cpu", method="uniform_grid")
+    with pytest.raises(ValueError, match="uniform_bins"):
+        NeighborGrid(2, 8, radius=0.5, device="cpu", method="uniform_grid", uniform_bins=0)
+    with pytest.raises(NotImplementedError, match="HashGrid"):
+        NeighborGrid(2, 8, radius=0.5, device="cpu", method="grid")
+    with pytest.raises(NotImplementedError, match="1024"):
+        NeighborGrid(2, 1025, radius=0.5, device="cpu")
+    # stepping: more than 64 agents or grid lists take the wide-env kernels
+    big = Stepper([AgentConfig(radius=0.02) for _ in range(600)], device="cpu",
+                  world=WorldConfig(bounds=(-2.0, 2.0, -2.0, 2.0)))
+    d = big.desc(2, 2)
+    assert big.wide and d.neighbor_method == _lib.LISTS_GRID and d.grid_pinned == 1
+    assert list(d.grid_origin) == [-2.0, -2.0] and d.grid_cell == pytest.approx(max(big.neighbor_radius, 4.0 / 25))
+    assert Stepper([AgentConfig() for _ in range(100)], device="cpu").desc(2, 2).neighbor_method == 0
+    with pytest.raises(NotImplementedError, match="bounds"):
+        Stepper([AgentConfig(radius=0.02) for _ in range(600)], device="cpu", world=WorldConfig())
+    with pytest.raises(NotImplementedError, match="box agents"):
+        Stepper([AgentConfig(shape="box", half_extents=(0.02, 0.02)) for _ in range(70)], device="cpu")
 
 
 def test_step_refuses_cpu_tensors():
