@@ -381,14 +381,20 @@ def main():
     fwd_only = E * T * args.steps / el_f
 
     # the library launches the specialised holonomic-velocity kernels when the desc allows
-    fam = "k_holo" if stepper.desc(E, 2).holo_velocity_only else "k_rollout"
+    desc = stepper.desc(E, 2)
     pa = 1 << max(2, (A - 1).bit_length())
+    if desc.holo_velocity_only:  # k_holo_*<T, PA, TAPE, SAT, compile-time substeps>
+        sc = S if S in (1, 4) and not desc.max_overlap > 0 else 0
+        targs = f"float, {pa}, true, {'true' if desc.max_overlap > 0 else 'false'}, {sc}"
+        fam = "k_holo"
+    else:
+        targs, fam = f"float, {pa}", "k_rollout"
     kernels = {}
     for kind, per in (("fwd", fwd_bytes(A)), ("bwd", bwd_bytes(A))):
         d = sum(dur[kind]) / max(len(dur[kind]), 1)
         alg = per * E * T
         kernels[kind] = {
-            "name": f"{fam}_{kind}<float, {pa}>",
+            "name": f"{fam}_{kind}<{targs}>",
             "avg_ms": d * 1e3,
             "alg_bytes_per_launch": alg,
             "achieved_GBps": alg / d / 1e9 if d > 0 else None,
@@ -396,14 +402,19 @@ def main():
         }
     dom = max(kernels, key=lambda k: kernels[k]["avg_ms"])
     kd = kernels[dom]
-    traffic = None
+    traffic = traffic_source = None
     prof = ROOT / "profiles" / "traffic_c2.json"
     if prof.exists() and (E, A, T, S) == (16000, 16, 32, 4):
-        # HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
-        # of this same workload, scaled by the copy-kernel calibration they record
+        # HBM bytes per launch are not measured in this run (counters need rocprofv3):
+        # they come from the committed FETCH_SIZE / WRITE_SIZE passes of this workload,
+        # scaled by the copy-kernel calibration recorded with them, and only while the
+        # kernel instance those passes profiled is the one timed here
         tr = json.loads(prof.read_text())
         k = tr["kernels"][dom]
-        traffic = 1024 * (k["fetch_kib"] * tr["fetch_scale"] + k["write_kib"] * tr["write_scale"])
+        if k["name"] == kd["name"]:
+            traffic = 1024 * (k["fetch_kib"] * tr["fetch_scale"] + k["write_kib"] * tr["write_scale"])
+            traffic_source = (f"{tr['source']}: rocprofv3 FETCH_SIZE / WRITE_SIZE of {k['name']}"
+                              " (committed profile, not measured in this run)")
     fused_frac = (fwd_bytes(A) + bwd_bytes(A)) * E * T / (
         (kernels["fwd"]["avg_ms"] + kernels["bwd"]["avg_ms"]) * 1e-3) / HBM_PEAK
 
@@ -433,6 +444,7 @@ def main():
             "unit": "GB/s",
             "frac": kd["frac"],
             "traffic": traffic,
+            "traffic_source": traffic_source,
         },
         "fwd_bwd_kernel_roofline_frac": fused_frac,
         "fwd_only_env_steps_per_s": fwd_only,
