@@ -199,16 +199,41 @@ __device__ __forceinline__ typename MaskT<PA>::type forces_b(
     return incl;
 }
 
-// Sum of v[base + b] over the set bits b of m, in ascending order, onto acc.
-template <typename T, typename M>
-__device__ __forceinline__ T ordered_sum(T acc, M m, const T *v, int base)
+// The value x of lane l (l wave-uniform).
+__device__ __forceinline__ float read_lane(float x, int l)
 {
-    while (m) {
-        const int b = m_ctz(m);
-        m &= m - 1;
-        acc += v[base + b];
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+__device__ __forceinline__ double read_lane(double x, int l)
+{
+    const long long b = __double_as_longlong(x);
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(b & 0xffffffffll), l);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(b >> 32), l);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// acc[q] += v[q] of every flagged lane of this lane's env, in ascending agent order: the
+// additions, in their order, of a loop over the env's agents that skips the unflagged
+// ones (skipping a zero contribution leaves a sum that starts at +0 unchanged).  The
+// values travel by readlane, their lane indices taken in order from the wave's ballot,
+// so the loop runs once per flagged lane of the wave with no LDS round trip; lanes of
+// the wave's other envs leave acc alone.
+template <int PA, int NV, typename T>
+__device__ __forceinline__ void env_ordered_sums(T (&acc)[NV], const T (&v)[NV], bool flag,
+                                                 int lane)
+{
+    uint64_t bal = __ballot(flag);
+    const int slot = lane / PA;
+    while (bal) {
+        const int l = __builtin_ctzll(bal);
+        bal &= bal - 1;
+        const bool mine = PA == 64 || l / PA == slot;
+#pragma unroll
+        for (int q = 0; q < NV; ++q) {
+            const T x = read_lane(v[q], l);
+            if (mine) acc[q] += x;
+        }
     }
-    return acc;
 }
 
 // This env's lanes whose flag is set, as a mask over the env's agent slots.
@@ -230,12 +255,12 @@ template <typename T> struct BodyNew {
 };
 
 // The body pass of one env for movable body root o: every lane of the env computes the
-// same values (agent contributions reach all of them through `lred`).  Agent state of
+// same values (agent contributions reach all of them by readlane, env_ordered_sums).  Agent state of
 // the lane in `st`; `od` = the env's obstacle state at the substep input.
 template <typename T, int PA>
 __device__ __forceinline__ void body_step(const Cst<T> &C, const ObTab<T> &tb,
                                           const Lane<T, PA> &L, const St<T> &st, const T *od,
-                                          int o, T *lred, BodyNew<T> &B)
+                                          int o, BodyNew<T> &B)
 {
     typedef typename MaskT<PA>::type M;
     const int N = tb.N;
@@ -272,15 +297,14 @@ __device__ __forceinline__ void body_step(const Cst<T> &C, const ObTab<T> &tb,
             const T lx = owx + T(0), ly = owy + T(0);
             tq = lx * f1 - ly * f0;
         }
-        __syncthreads();
-        lred[L.lane] = f0;
-        lred[64 + L.lane] = f1;
-        lred[128 + L.lane] = tq;
-        __syncthreads();
-        const M nz = env_ballot<PA>(f0 != T(0) || f1 != T(0), L.base);
-        fx = ordered_sum(fx, nz, lred, L.base);
-        fy = ordered_sum(fy, nz, lred + 64, L.base);
-        tau = ordered_sum(tau, nz, lred + 128, L.base);
+        {
+            T acc[3] = {fx, fy, tau};
+            const T val[3] = {f0, f1, tq};
+            env_ordered_sums<PA, 3>(acc, val, f0 != T(0) || f1 != T(0), L.lane);
+            fx = acc[0];
+            fy = acc[1];
+            tau = acc[2];
+        }
         // contacts with the circles of other bodies and of the scenery, in index order
         for (int o2 = 0; o2 < N; ++o2) {
             if (tb.body[o2] == o) continue;
@@ -340,14 +364,14 @@ __device__ __forceinline__ void body_step(const Cst<T> &C, const ObTab<T> &tb,
 template <typename T, int PA>
 __device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
                                           const Lane<T, PA> &L, const St<T> &st, const T *obc,
-                                          T *obn, T *lred)
+                                          T *obn)
 {
     const int N = tb.N;
     for (int q = L.agent; q < OB_W * N; q += PA) obn[q] = obc[q];
     for (int o = 0; o < N; ++o) {
         if (tb.body[o] != o || tb.kind[o] != 1) continue;
         BodyNew<T> B;
-        body_step<T, PA>(C, tb, L, st, obc, o, lred, B);
+        body_step<T, PA>(C, tb, L, st, obc, o, B);
         if (L.agent == 0) {
             T *bo = obn + 6 * N + 6 * o;
             bo[0] = B.nx;
@@ -398,7 +422,6 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
     constexpr int EPW = 64 / PA;
     __shared__ T sl[4 * 64];                         // px py vx vy of the substep
     __shared__ T lr[64];                             // agent radius per lane
-    __shared__ T lred[3 * 64];                       // agent contributions to body sums
     __shared__ T lob[2][EPW][OB_W * NOB_MAX];        // obstacle state: in / out of a substep
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
@@ -430,7 +453,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
             const T *obc = lob[cur][ew];
             T Fx, Fy;
             forces_b<T, PA>(C, tb, L, sl, lr, obc, st, s, s == 0 || !ok, cand, Fx, Fy);
-            body_pass<T, PA>(C, tb, L, st, obc, lob[cur ^ 1][ew], lred);
+            body_pass<T, PA>(C, tb, L, st, obc, lob[cur ^ 1][ew]);
             St<T> nx;
             integrate<T, false>(C, L.pr, st, a, Fx, Fy, nx);
             if (C.use_skin) {
@@ -461,7 +484,6 @@ template <typename T, int PA> __host__ __device__ constexpr size_t body_bwd_lds(
     return 2 * 64 * sizeof(T)                               // radius, damping divisor
            + (size_t)S * NF_2D * 64 * sizeof(T)             // substep agent slots
            + (size_t)S * 64 * sizeof(M)                     // inclusion masks
-           + 6 * 64 * sizeof(T)                             // ordered-sum staging
            + (size_t)(S + 1) * (64 / PA) * OB_W * N * sizeof(T)  // obstacle state per substep
            + 2 * (size_t)(64 / PA) * OB_W * N * sizeof(T);       // obstacle adjoint in / out
 }
@@ -473,7 +495,7 @@ template <typename T, int PA> __host__ __device__ constexpr size_t body_bwd_lds(
 template <typename T, int PA>
 __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &tb,
                                               const Lane<T, PA> &L, const St<T> &st,
-                                              const T *obc, const T *gout, T *gin, T *lred,
+                                              const T *obc, const T *gout, T *gin,
                                               St<T> &ga)
 {
     typedef typename MaskT<PA>::type M;
@@ -487,7 +509,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
     for (int o = 0; o < N; ++o) {
         if (tb.body[o] != o || tb.kind[o] != 1) continue;
         BodyNew<T> B;
-        body_step<T, PA>(C, tb, L, st, obc, o, lred, B);
+        body_step<T, PA>(C, tb, L, st, obc, o, B);
         const T sdt = C.sub_dt, one = T(1);
         const T lin_decay = one - tb.lin_damp * sdt;
         const T ang_decay = one - tb.ang_damp * sdt;
@@ -550,23 +572,16 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
                 c4 = -arx;         // onto g_vsx
                 c5 = -ary;
             }
-            __syncthreads();
-            lred[L.lane] = c0;
-            lred[64 + L.lane] = c1;
-            lred[128 + L.lane] = c2;
-            lred[192 + L.lane] = c3;
-            lred[256 + L.lane] = c4;
-            lred[320 + L.lane] = c5;
-            __syncthreads();
-            const M nz = env_ballot<PA>(c0 != T(0) || c1 != T(0) || c2 != T(0) || c3 != T(0) ||
+            T acc[6] = {T(0), T(0), T(0), T(0), T(0), T(0)};
+            {
+                const T val[6] = {c0, c1, c2, c3, c4, c5};
+                env_ordered_sums<PA, 6>(acc, val,
+                                        c0 != T(0) || c1 != T(0) || c2 != T(0) || c3 != T(0) ||
                                             c4 != T(0) || c5 != T(0),
-                                        L.base);
-            T g_owx = ordered_sum(T(0), nz, lred, L.base);
-            T g_owy = ordered_sum(T(0), nz, lred + 64, L.base);
-            T g_csx = ordered_sum(T(0), nz, lred + 128, L.base);
-            T g_csy = ordered_sum(T(0), nz, lred + 192, L.base);
-            T g_vsx = ordered_sum(T(0), nz, lred + 256, L.base);
-            T g_vsy = ordered_sum(T(0), nz, lred + 320, L.base);
+                                        L.lane);
+            }
+            T g_owx = acc[0], g_owy = acc[1], g_csx = acc[2], g_csy = acc[3], g_vsx = acc[4],
+              g_vsy = acc[5];
             for (int o2 = 0; o2 < N; ++o2) {
                 if (tb.body[o2] == o) continue;
                 const T *d2 = obc + 6 * o2;
@@ -627,8 +642,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
     T *ldd = lr + 64;                                    // damping divisor per lane
     T *slots = ldd + 64;                                 // S slots of NF_2D fields
     M *lmask = (M *)(slots + (size_t)C.S * NF_2D * 64);  // S inclusion masks
-    T *lred = (T *)(lmask + (size_t)C.S * 64);           // 6 x 64 ordered-sum staging
-    T *lobs = lred + 6 * 64;                             // [S+1][EPW][NW] obstacle states
+    T *lobs = (T *)(lmask + (size_t)C.S * 64);           // [S+1][EPW][NW] obstacle states
     T *lgob = lobs + (size_t)(C.S + 1) * EPW * NW;       // [2][EPW][NW] obstacle adjoints
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
@@ -681,7 +695,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             sl[F_FX * 64 + L.lane] = Fx;
             sl[F_FY * 64 + L.lane] = Fy;
             lmask[s * 64 + L.lane] = incl;
-            body_pass<T, PA>(C, tb, L, st, obc, lobs + ((size_t)(s + 1) * EPW + ew) * NW, lred);
+            body_pass<T, PA>(C, tb, L, st, obc, lobs + ((size_t)(s + 1) * EPW + ew) * NW);
             St<T> nx;
             integrate<T, false>(C, L.pr, st, a, Fx, Fy, nx);
             if (C.use_skin) {
@@ -704,7 +718,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             T gFx, gFy;
             integrate_adj<T, false>(C, L.pr, in, a, Fx, Fy, gs, gi, ga, gFx, gFy);
             // the body pass: adjoint of its input obstacle state into gprev
-            body_pass_adj<T, PA>(C, tb, L, in, obc, gob, gprev, lred, gi);
+            body_pass_adj<T, PA>(C, tb, L, in, obc, gob, gprev, gi);
             if (C.needs_forces) {
                 const T wFx = gFx * L.inv_dd, wFy = gFy * L.inv_dd;
                 __syncthreads();
@@ -738,21 +752,20 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
                         ob_force_adj(C, tb, obc, o, in.px, in.py, in.vx, in.vy, L.pr.radius,
                                      L.dd, gFx, gFy, gi, opx, opy, ovx, ovy);
                     if (!shape_moves(tb, o)) continue;
-                    __syncthreads();
-                    lred[L.lane] = opx;
-                    lred[64 + L.lane] = opy;
-                    lred[128 + L.lane] = ovx;
-                    lred[192 + L.lane] = ovy;
-                    __syncthreads();
-                    const M nz = env_ballot<PA>(opx != T(0) || opy != T(0) || ovx != T(0) ||
-                                                    ovy != T(0),
-                                                L.base);
-                    if (nz && L.agent == 0) {
-                        T *g2 = gprev + 6 * o;
-                        g2[0] = ordered_sum(g2[0], nz, lred, L.base);
-                        g2[1] = ordered_sum(g2[1], nz, lred + 64, L.base);
-                        g2[3] = ordered_sum(g2[3], nz, lred + 128, L.base);
-                        g2[4] = ordered_sum(g2[4], nz, lred + 192, L.base);
+                    // the env's agent-0 lane keeps the shape's adjoint; the other lanes'
+                    // copies of the sums are not used
+                    T *g2 = gprev + 6 * o;
+                    T acc[4] = {g2[0], g2[1], g2[3], g2[4]};
+                    const T val[4] = {opx, opy, ovx, ovy};
+                    env_ordered_sums<PA, 4>(acc, val,
+                                            opx != T(0) || opy != T(0) || ovx != T(0) ||
+                                                ovy != T(0),
+                                            L.lane);
+                    if (L.agent == 0) {
+                        g2[0] = acc[0];
+                        g2[1] = acc[1];
+                        g2[3] = acc[2];
+                        g2[4] = acc[3];
                     }
                 }
                 if (C.soft_walls)
