@@ -31,7 +31,7 @@ from typing import NamedTuple
 import torch
 
 from . import _lib
-from .stepper import Stepper, state_struct
+from .stepper import Stepper, check_extent, state_struct
 
 FIELDS = ("pos", "theta", "vel", "speed", "ang_vel", "z", "vz", "attitude", "body_rates")
 
@@ -129,9 +129,13 @@ def _launch_fwd(stepper: Stepper, state0, actions_seq: torch.Tensor, traj, final
     nf = _nfields(stepper)
     lib = _lib.load()
     desc = stepper.desc(E, ad)
-    s0 = state_struct(list(state0)[:nf])
-    fin = state_struct(list(final)[:nf])
-    tr = state_struct(list(traj)[:nf]) if traj is not None and T > 1 else None
+    EA, dt = E * stepper.n_agents, stepper.dtype
+    check_extent(actions_seq, T * EA * ad, "actions", dt)
+    s0 = state_struct(list(state0)[:nf], EA, dt, "state0")
+    fin = state_struct(list(final)[:nf], EA, dt, "final")
+    tr = state_struct(list(traj)[:nf], (T - 1) * EA, dt, "traj") if traj is not None and T > 1 else None
+    if tape is not None:
+        check_extent(tape, stepper.tape_bytes(E, ad, T), "tape", torch.uint8)
     if tape is None:
         _lib.check(lib.swarp_rollout_fwd(
             ctypes.byref(desc), T, ctypes.byref(s0), actions_seq.data_ptr(),
@@ -203,15 +207,22 @@ class _RolloutFn(torch.autograd.Function):
         E, ad = actions_seq.shape[1], actions_seq.shape[3]
         lib = _lib.load()
         desc = stepper.desc(E, ad)
-        s0 = state_struct(state0)
-        tr = state_struct(traj) if T > 1 else None
-        gtr = state_struct(g_traj) if T > 1 and any(g is not None for g in g_traj) else None
-        gfin = state_struct(g_final) if any(g is not None for g in g_final) else None
-        a0 = state_struct(adj0)
+        EA, dt = E * stepper.n_agents, stepper.dtype
+        check_extent(actions_seq, T * EA * ad, "actions", dt)
+        check_extent(adj_act, T * EA * ad, "adj_actions", dt)
+        s0 = state_struct(state0, EA, dt, "state0")
+        tr = state_struct(traj, (T - 1) * EA, dt, "traj") if T > 1 else None
+        gtr = (state_struct(g_traj, (T - 1) * EA, dt, "adj_traj")
+               if T > 1 and any(g is not None for g in g_traj) else None)
+        gfin = (state_struct(g_final, EA, dt, "adj_final")
+                if any(g is not None for g in g_final) else None)
+        a0 = state_struct(adj0, EA, dt, "adj_state0")
         sink = KERNEL_EVENTS
         if sink is not None:
             e0 = _event(actions_seq)
         tape = ctx.tape
+        if tape is not None:
+            check_extent(tape, stepper.tape_bytes(E, ad, T), "tape", torch.uint8)
         if tape is None:
             _lib.check(lib.swarp_rollout_bwd(
                 ctypes.byref(desc), T, ctypes.byref(s0), actions_seq.data_ptr(),
@@ -240,9 +251,13 @@ def _launch_fwd_ob(stepper: Stepper, state0, ob0: torch.Tensor, actions_seq: tor
     T, E, _, ad = actions_seq.shape
     lib = _lib.load()
     desc = stepper.desc(E, ad)
-    s0 = state_struct(list(state0)[:5])
-    fin = state_struct(list(final)[:5])
-    tr = state_struct(list(traj)[:5]) if traj is not None and T > 1 else None
+    EA, dt, NW = E * stepper.n_agents, stepper.dtype, 12 * stepper.n_obstacles
+    check_extent(actions_seq, T * EA * ad, "actions", dt)
+    check_extent(ob0, E * NW, "ob_state", dt)
+    check_extent(ob_traj, T * E * NW, "ob_trajectory", dt)
+    s0 = state_struct(list(state0)[:5], EA, dt, "state0")
+    fin = state_struct(list(final)[:5], EA, dt, "final")
+    tr = state_struct(list(traj)[:5], (T - 1) * EA, dt, "traj") if traj is not None and T > 1 else None
     _lib.check(lib.swarp_rollout_fwd_ob(
         ctypes.byref(desc), T, ctypes.byref(s0), ob0.data_ptr(), actions_seq.data_ptr(),
         ctypes.byref(tr) if tr is not None else None, ctypes.byref(fin), ob_traj.data_ptr(),
@@ -297,11 +312,20 @@ class _RolloutObFn(torch.autograd.Function):
         E, ad = actions_seq.shape[1], actions_seq.shape[3]
         lib = _lib.load()
         desc = stepper.desc(E, ad)
-        s0 = state_struct(state0)
-        tr = state_struct(traj) if T > 1 else None
-        gtr = state_struct(g_traj) if T > 1 and any(g is not None for g in g_traj) else None
-        gfin = state_struct(g_final) if any(g is not None for g in g_final) else None
-        a0 = state_struct(adj0)
+        EA, dt, NW = E * stepper.n_agents, stepper.dtype, 12 * stepper.n_obstacles
+        check_extent(actions_seq, T * EA * ad, "actions", dt)
+        check_extent(adj_act, T * EA * ad, "adj_actions", dt)
+        check_extent(ob0, E * NW, "ob_state", dt)
+        check_extent(ob_traj, T * E * NW, "ob_trajectory", dt)
+        check_extent(g_ob, T * E * NW, "adj_ob_trajectory", dt)
+        check_extent(adj_ob0, E * NW, "adj_ob_state", dt)
+        s0 = state_struct(state0, EA, dt, "state0")
+        tr = state_struct(traj, (T - 1) * EA, dt, "traj") if T > 1 else None
+        gtr = (state_struct(g_traj, (T - 1) * EA, dt, "adj_traj")
+               if T > 1 and any(g is not None for g in g_traj) else None)
+        gfin = (state_struct(g_final, EA, dt, "adj_final")
+                if any(g is not None for g in g_final) else None)
+        a0 = state_struct(adj0, EA, dt, "adj_state0")
         sink = KERNEL_EVENTS
         if sink is not None:
             e0 = _event(actions_seq)

@@ -28,7 +28,7 @@ import torch
 from . import _lib
 from .autograd import (TorchState, _empty_like_fields, _launch_fwd, _nfields, _stream,
                        fill_state_defaults, warp_step)
-from .stepper import Stepper, state_struct
+from .stepper import Stepper, check_extent, state_struct
 
 _STEPPERS: "weakref.WeakValueDictionary[int, Stepper]" = weakref.WeakValueDictionary()
 _HANDLES: dict[int, int] = {}  # id(stepper) -> handle
@@ -106,8 +106,10 @@ def _step_bwd_op(stepper_id: int, actions: torch.Tensor, pos: torch.Tensor, thet
     adj_act = torch.empty_like(seq)
     lib = _lib.load()
     desc = stepper.desc(E, ad)
-    gfin = state_struct(g_final) if any(g is not None for g in g_final) else None
-    st0, a0 = state_struct(s0), state_struct(adj0)
+    EA, dt = E * stepper.n_agents, stepper.dtype
+    check_extent(seq, EA * ad, "actions", dt)
+    gfin = state_struct(g_final, EA, dt, "adj_final") if any(g is not None for g in g_final) else None
+    st0, a0 = state_struct(s0, EA, dt, "state0"), state_struct(adj0, EA, dt, "adj_state0")
     _lib.check(lib.swarp_rollout_bwd(
         ctypes.byref(desc), 1, ctypes.byref(st0), seq.data_ptr(), None, None,
         ctypes.byref(gfin) if gfin is not None else None, ctypes.byref(a0), adj_act.data_ptr(),

@@ -194,6 +194,11 @@ class NeighborGrid:
         for t in (neighbor_idx, neighbor_count):
             if t.dtype != torch.int32 or not t.is_contiguous():
                 raise TypeError("neighbour buffers must be contiguous int32")
+        EA = self.n_envs * self.n_agents
+        for t, n, name in ((neighbor_idx, EA * self.max_neighbors, "neighbor_idx"),
+                           (neighbor_count, EA, "neighbor_count")):
+            if t.numel() != n:  # the reach the list kernels write
+                raise ValueError(f"{name}: {t.numel()} elements {tuple(t.shape)}, the build writes {n}")
         pos = pos.contiguous()
         lib = _lib.load()
         stream = _lib.stream_of(pos.device)

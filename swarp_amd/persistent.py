@@ -32,7 +32,7 @@ import torch
 
 from . import _lib
 from .autograd import FIELDS, TorchState
-from .stepper import state_struct
+from .stepper import check_extent, state_struct
 
 #: hook(state_out, stream, warm): launches the post-step work on ``state_out``; ``warm``
 #: marks the eager warm-up launch before a capture, which must leave carried state alone
@@ -94,8 +94,10 @@ class StepGraph:
         w = self.world
         lib = _lib.load()
         desc = w.stepper.desc(w.n_envs, w.act_dim)
-        s_in = state_struct(list(src)[:5])
-        s_out = state_struct(list(dst)[:5])
+        EA, dt = w.n_envs * w.n_agents, w.stepper.dtype
+        check_extent(self.act, EA * w.act_dim, "actions", dt)
+        s_in = state_struct(list(src)[:5], EA, dt, "state")
+        s_out = state_struct(list(dst)[:5], EA, dt, "next state")
         _lib.check(lib.swarp_rollout_fwd(ctypes.byref(desc), 1, ctypes.byref(s_in),
                                          self.act.data_ptr(), None, ctypes.byref(s_out),
                                          ctypes.c_void_p(stream)))

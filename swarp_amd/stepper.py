@@ -476,11 +476,31 @@ class Stepper:
         _launch_fwd(self, state_in, actions.unsqueeze(0), None, state_out)
 
 
-def state_struct(fields) -> _lib.SwarpState:
-    """SwarpState of up to nine tensors (None = NULL)."""
+_FIELD_NAMES = ("pos", "theta", "vel", "speed", "ang_vel", "z", "vz", "attitude", "body_rates")
+_FIELD_WIDTH = (2, 1, 2, 1, 1, 1, 1, 4, 3)
+
+
+def check_extent(t, n: int, name: str, dtype=None) -> None:
+    """Host-side extent check of a tensor handed to the library: contiguous, of `dtype`,
+    with exactly `n` elements -- the reach the kernels index it with.  Raises before any
+    launch instead of letting a kernel read or write past the tensor."""
+    if t is None:
+        return
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: the library takes contiguous tensors")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name}: dtype {t.dtype}, the launch needs {dtype}")
+    if t.numel() != n:
+        raise ValueError(f"{name}: {t.numel()} elements {tuple(t.shape)}, the launch indexes {n}")
+
+
+def state_struct(fields, n: int | None = None, dtype=None, what: str = "state") -> _lib.SwarpState:
+    """SwarpState of up to nine tensors (None = NULL).  With `n` (the lead dimensions times
+    n_envs * n_agents), each field is checked to hold exactly n * its width elements."""
     s = _lib.SwarpState()
-    names = ("pos", "theta", "vel", "speed", "ang_vel", "z", "vz", "attitude", "body_rates")
-    for name, t in zip(names, fields):
+    for k, (name, t) in enumerate(zip(_FIELD_NAMES, fields)):
+        if n is not None:
+            check_extent(t, n * _FIELD_WIDTH[k], f"{what}.{name}", dtype)
         setattr(s, name, _ptr(t))
     return s
 

@@ -419,3 +419,27 @@ def test_per_env_params_validation():
     ptr = st.params_per_env.data_ptr()
     st.set_agent_params_per_env(torch.as_tensor(tab, dtype=torch.float32))
     assert st.params_per_env.data_ptr() == ptr
+
+
+def test_extent_checks_before_launch():
+    """Every tensor handed to the library is checked, on the host, to hold exactly the
+    elements the kernels index (contiguous, of the stepper's dtype) -- before any launch."""
+    from swarp_amd.stepper import check_extent, state_struct
+
+    t = torch.zeros(4, 3, 2)
+    check_extent(t, 24, "x", torch.float32)
+    with pytest.raises(ValueError, match="indexes 25"):
+        check_extent(t, 25, "x", torch.float32)
+    with pytest.raises(TypeError, match="dtype"):
+        check_extent(t, 24, "x", torch.float64)
+    with pytest.raises(ValueError, match="contiguous"):
+        check_extent(t.transpose(0, 1), 24, "x")
+    E, A = 4, 3
+    ok = [torch.zeros(E, A, 2), torch.zeros(E, A), torch.zeros(E, A, 2), torch.zeros(E, A),
+          torch.zeros(E, A)]
+    state_struct(ok, E * A, torch.float32, "s")
+    bad = list(ok)
+    bad[2] = torch.zeros(E, A)  # vel missing its pair
+    with pytest.raises(ValueError, match="s.vel"):
+        state_struct(bad, E * A, torch.float32, "s")
+    state_struct([None] * 5, E * A, torch.float32, "s")  # NULL fields are not read
