@@ -343,7 +343,8 @@ class _RolloutObFn(torch.autograd.Function):
         return (None, adj_act if need[1] else None, adj_ob0, *adj0)
 
 
-def _rollout_bodies(stepper: Stepper, state: TorchState, actions_seq: torch.Tensor):
+def _rollout_bodies(stepper: Stepper, state: TorchState, actions_seq: torch.Tensor,
+                    given=(True,) * 9):
     """rollout / warp_step of a world with movable bodies: consumes ``stepper.ob_state``,
     leaves the obstacle state after the last step in it and every step's in
     ``stepper.ob_trajectory``."""
@@ -367,7 +368,7 @@ def _rollout_bodies(stepper: Stepper, state: TorchState, actions_seq: torch.Tens
         outs = (*final, *traj)
     stepper.ob_trajectory = ob_traj
     stepper.ob_state = ob_traj[T - 1]
-    return _assemble(stepper, state, outs, T)
+    return _assemble(stepper, state, outs, T, given)
 
 
 def _grad_mode(state: TorchState, actions: torch.Tensor) -> bool:
@@ -376,18 +377,81 @@ def _grad_mode(state: TorchState, actions: torch.Tensor) -> bool:
     )
 
 
-def _assemble(stepper: Stepper, state: TorchState, outs, T: int):
-    """(final TorchState, trajectory list) from the Function's outputs."""
+class Trajectory(list):
+    """The states after each step of a rollout: a ``list`` of :class:`TorchState` whose
+    per-step states are built on first use.  A BPTT loop that only reads the final state
+    never pays for the T - 1 per-step views (one unbind per field and a TorchState per
+    step); any read, iteration or change of the list builds them all first, after which
+    it behaves as a plain list.  ``len`` needs no build."""
+
+    def __init__(self, n: int, build):
+        super().__init__()
+        self._n = n
+        self._build = build
+
+    def _fill(self) -> None:
+        if self._build is not None:
+            build, self._build = self._build, None
+            list.extend(self, build())
+
+    def __len__(self) -> int:
+        return self._n if self._build is not None else list.__len__(self)
+
+    def __bool__(self) -> bool:
+        return len(self) > 0
+
+    def __reduce_ex__(self, protocol):
+        self._fill()
+        return (list, (list(self),))
+
+
+def _list_method(name):
+    base = getattr(list, name)
+
+    def method(self, *args, **kwargs):
+        self._fill()
+        return base(self, *args, **kwargs)
+
+    method.__name__ = name
+    return method
+
+
+for _name in ("__getitem__", "__setitem__", "__delitem__", "__iter__", "__reversed__",
+              "__contains__", "__eq__", "__ne__", "__lt__", "__le__", "__gt__", "__ge__",
+              "__add__", "__iadd__", "__mul__", "__rmul__", "__imul__", "__repr__",
+              "append", "extend", "insert", "pop", "remove", "index", "count",
+              "clear", "copy", "sort", "reverse"):
+    setattr(Trajectory, _name, _list_method(_name))
+Trajectory.__hash__ = None
+
+
+def _with_defaults(state: TorchState) -> tuple[TorchState, tuple[bool, ...]]:
+    """fill_state_defaults, and which fields the caller provided."""
+    given = tuple(t is not None for t in state)
+    return fill_state_defaults(state), given
+
+
+def _assemble(stepper: Stepper, state: TorchState, outs, T: int, given=(True,) * 9):
+    """(final TorchState, trajectory) from the Function's outputs.  Every returned state
+    owns its tensors, as the reference's per-step outputs do: for a 2-D fleet the four
+    drone fields it does not step are passed through as copies of the input's (the
+    defaults this call made are handed to the final state as they are)."""
     nf = _nfields(stepper)
     final_f = outs[:nf]
     traj_f = outs[nf:2 * nf]
     tail = tuple(state[nf:]) if nf == 5 else ()
-    # one unbind per field (a single autograd node) instead of T - 1 selects per field
-    per_step = [f.unbind(0) for f in traj_f] if T > 1 else []
-    traj = [TorchState(*(u[t] for u in per_step), *tail) for t in range(T - 1)]
-    final = TorchState(*final_f, *tail)
-    traj.append(final)
-    return final, traj
+    final_tail = tuple(t.clone() if given[nf + k] else t for k, t in enumerate(tail))
+    final = TorchState(*final_f, *final_tail)
+
+    def build():
+        # one unbind per field (a single autograd node) instead of T - 1 selects per field
+        per_step = [f.unbind(0) for f in traj_f] if T > 1 else []
+        steps = [TorchState(*(u[t] for u in per_step), *(x.clone() for x in tail))
+                 for t in range(T - 1)]
+        steps.append(final)
+        return steps
+
+    return final, Trajectory(T, build)
 
 
 @dataclass
@@ -453,12 +517,12 @@ def warp_step(
 ) -> TorchState:
     """Differentiable env step ``state, actions -> next state``
     (``swarp/interop/autograd.py:299-338``)."""
-    state = fill_state_defaults(state)
+    state, given = _with_defaults(state)
     if actions.dim() != 3:
         raise ValueError(f"actions must be [n_envs, n_agents, act_dim]; got {tuple(actions.shape)}")
     seq = actions.unsqueeze(0)
     if stepper.any_movable:
-        final, _ = _rollout_bodies(stepper, state, seq)
+        final, _ = _rollout_bodies(stepper, state, seq, given)
         return final
     _validate(stepper, state, seq)
     nf = _nfields(stepper)
@@ -467,7 +531,7 @@ def warp_step(
         if slot is not None:
             bufs = (slot.out, [b[:0] for b in slot.ring.bufs])
         outs = _RolloutFn.apply(stepper, bufs, seq, *state[:nf])
-        final, _ = _assemble(stepper, state, outs, 1)
+        final, _ = _assemble(stepper, state, outs, 1, given)
         return final
     out = stepper.output_state(actions.shape[0])
     final = list(out[:nf])
@@ -485,12 +549,12 @@ def rollout(
     """Backprop-through-time rollout (``swarp/interop/autograd.py:341-369``).
 
     ``actions_seq [T, n_envs, n_agents, act_dim]``.  Returns ``(final_state,
-    trajectory)`` with the state after each of the T steps; gradients flow to
-    ``state`` and ``actions_seq``.
+    trajectory)`` with the state after each of the T steps (a :class:`Trajectory`, a
+    list built on first use); gradients flow to ``state`` and ``actions_seq``.
     """
-    state = fill_state_defaults(state)
+    state, given = _with_defaults(state)
     if stepper.any_movable:
-        return _rollout_bodies(stepper, state, actions_seq)
+        return _rollout_bodies(stepper, state, actions_seq, given)
     T, E, _ = _validate(stepper, state, actions_seq)
     if T < 1:
         raise ValueError("actions_seq must hold at least one step")
@@ -509,4 +573,4 @@ def rollout(
             final, traj = bufs
         _launch_fwd(stepper, [t.contiguous() for t in state[:nf]], actions_seq.contiguous(), traj, final)
         outs = (*final, *traj)
-    return _assemble(stepper, state, outs, T)
+    return _assemble(stepper, state, outs, T, given)

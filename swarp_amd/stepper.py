@@ -160,6 +160,7 @@ class Stepper:
         self.ob_state: torch.Tensor | None = None
         self.ob_trajectory: torch.Tensor | None = None
         self._descs: dict[tuple[int, int], _lib.SwarpDesc] = {}
+        self._tape_sizes: dict[tuple[int, int], int] = {}
         self._grids: dict[int, NeighborGrid] = {}
         self._out_states: dict[int, list] = {}
         self._out_idx: dict[int, int] = {}
@@ -231,6 +232,7 @@ class Stepper:
         self.params_per_env = t.to(device=self.device, dtype=self.dtype).contiguous()
         self._pe_skin_speed = float(t[..., P_MAX_SPEED].max())
         self._descs.clear()
+        self._tape_sizes.clear()
         # a new table is a new device address: descriptors and captured graphs that baked
         # the old one must be rebuilt
         self.mutation_version += 1
@@ -286,6 +288,7 @@ class Stepper:
         self.ob_state = self._body_seed() if movable else None
         self.ob_trajectory = None
         self._descs.clear()
+        self._tape_sizes.clear()
         self.mutation_version += 1
 
     @staticmethod
@@ -411,9 +414,13 @@ class Stepper:
         if not self.use_tape:
             return 0
         d = self.desc(n_envs, act_dim)
-        n = ctypes.c_uint64(0)
-        _lib.check(_lib.load().swarp_tape_bytes(ctypes.byref(d), T, ctypes.byref(n)))
-        return int(n.value)
+        key = (ctypes.addressof(d), T)  # a descriptor lives until the world changes
+        n = self._tape_sizes.get(key)
+        if n is None:
+            c = ctypes.c_uint64(0)
+            _lib.check(_lib.load().swarp_tape_bytes(ctypes.byref(d), T, ctypes.byref(c)))
+            n = self._tape_sizes[key] = int(c.value)
+        return n
 
     def grid(self, n_envs: int) -> NeighborGrid:
         g = self._grids.get(n_envs)

@@ -443,3 +443,25 @@ def test_extent_checks_before_launch():
     with pytest.raises(ValueError, match="s.vel"):
         state_struct(bad, E * A, torch.float32, "s")
     state_struct([None] * 5, E * A, torch.float32, "s")  # NULL fields are not read
+
+
+def test_trajectory_is_a_list_built_on_first_use():
+    """rollout's trajectory: a list whose per-step states are built on first use (a loop
+    that reads only the final state never builds them); len needs no build."""
+    from swarp_amd.autograd import Trajectory
+
+    built = []
+
+    def build():
+        built.append(1)
+        return ["s0", "s1", "s2"]
+
+    t = Trajectory(3, build)
+    assert isinstance(t, list) and len(t) == 3 and bool(t) and not built
+    assert t[-1] == "s2" and built == [1]
+    assert list(t) == ["s0", "s1", "s2"] and t == ["s0", "s1", "s2"] and "s1" in t
+    assert [x for x in reversed(t)] == ["s2", "s1", "s0"] and t[1:] == ["s1", "s2"]
+    t.append("s3")
+    assert len(t) == 4 and t.index("s3") == 3 and built == [1]
+    e = Trajectory(0, list)
+    assert len(e) == 0 and not e and list(e) == []
