@@ -147,8 +147,9 @@ int swarp_rollout_fwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *
 
 /* Reverse of swarp_rollout_fwd in one launch (the adjoints the reference gets from
  * wp.Tape.backward, swarp/interop/autograd.py:277-296).  Step inputs are recomputed
- * from state0 and the checkpoints `traj` (the forward's own outputs); substep
- * intermediates are recomputed in the kernel, never stored.  `adj_traj` (same
+ * from state0 and the checkpoints `traj` (the forward's own outputs); this entry point
+ * recomputes each step's substep intermediates in the kernel from its checkpoint
+ * (swarp_rollout_bwd_tape reads them from the forward's tape instead).  `adj_traj` (same
  * layout as traj, fields may be NULL) and `adj_final` are the adjoints arriving at
  * each step output.  Writes adj_state0 (fields may be NULL) and adj_actions
  * [T,E,A,act_dim] (every element written). */

@@ -11,11 +11,13 @@ reference's published figures (RTX 3070 Laptop GPU, ``docs/benchmarks.md:27-59``
 printed beside each row for comparison.
 
 Run:  python -m swarp_amd.throughput [--steps 100] [--no-graph] [--json] [--rows 16000x16,...]
+      python -m swarp_amd.throughput --launch-cost   # host cost of a graph replay vs eager
 """
 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import time
 
@@ -69,6 +71,54 @@ def bench_one(n_envs: int, n_agents: int, device: str = "cuda:0", steps: int = 1
     }
 
 
+def launch_cost(device: str = "cuda:0", calls: int = 2000) -> dict:
+    """Host time per call, in microseconds, of issuing a two-kernel step three ways: two
+    eager launches, ``torch.cuda.CUDAGraph.replay()`` of the same two kernels captured in a
+    graph, and ``hipGraphLaunch`` on that graph's executable called directly through
+    ctypes.  The two kernels are tiny element-wise updates of a 16000 x 16 float buffer, so
+    the figures are launch costs, not kernel times; "total" adds the drain of the queue."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipGraphLaunch.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipGraphLaunch.restype = ctypes.c_int
+    x = torch.zeros(16000 * 16, device=device)
+    y = torch.zeros_like(x)
+    stream = torch.cuda.Stream(device=device)
+
+    def work():
+        x.add_(1.0)
+        y.mul_(0.5)
+
+    def timed(fn):
+        for _ in range(50):
+            fn()
+        torch.cuda.synchronize(device)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize(device)
+        t2 = time.perf_counter()
+        return {"host_us": (t1 - t0) / calls * 1e6, "total_us": (t2 - t0) / calls * 1e6}
+
+    with torch.cuda.stream(stream):
+        work()
+        torch.cuda.synchronize(device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            work()
+        torch.cuda.synchronize(device)
+        exe = ctypes.c_void_p(graph.raw_cuda_graph_exec())
+        raw_stream = ctypes.c_void_p(stream.cuda_stream)
+
+        def raw():
+            rc = hip.hipGraphLaunch(exe, raw_stream)
+            if rc:
+                raise RuntimeError(f"hipGraphLaunch returned {rc}")
+
+        return {"eager_two_launches": timed(work), "graph_replay": timed(graph.replay),
+                "hipGraphLaunch": timed(raw)}
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--device", default="cuda:0")
@@ -77,7 +127,14 @@ def main() -> None:
     ap.add_argument("--json", action="store_true", help="one JSON line per row")
     ap.add_argument("--rows", default=None,
                     help="comma-separated EnvsxAgents rows to run (default: the whole grid)")
+    ap.add_argument("--launch-cost", action="store_true",
+                    help="print the host cost of a graph replay against two eager launches")
     args = ap.parse_args()
+    if args.launch_cost:
+        for name, r in launch_cost(args.device).items():
+            print(f"{name:>20}: host {r['host_us']:6.1f} us/call, total {r['total_us']:6.1f} us/call",
+                  flush=True)
+        return
     rows = [(e, a) for e in ENV_COUNTS for a in AGENT_COUNTS]
     if args.rows:
         rows = [tuple(int(x) for x in r.split("x")) for r in args.rows.split(",")]
