@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 11
+#define SWARP_ABI_VERSION 12
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -84,8 +84,7 @@ typedef struct swarp_desc {
     double lat_grip, turn_cap;
     /* 1: `params` is [n_envs, n_agents, 22], one row per (env, agent) -- the per-env
        override of Stepper.set_agent_params_per_env (swarp/core/stepper.py:493-575,
-       the reference's *_per_env kernel variants); 0: [n_agents, 22] shared by every env.
-       The _ob (movable-body) entry points reject it. */
+       the reference's *_per_env kernel variants); 0: [n_agents, 22] shared by every env. */
     int32_t params_per_env;
     /* The fleet's top speed (the largest max_speed of its parameter rows; <= 0 reads as
        1).  Sizes the per-step skin of the neighbour search, which only affects speed:
@@ -109,6 +108,12 @@ typedef struct swarp_desc {
     int32_t neighbor_method, grid_bins, grid_pinned;
     double grid_origin[2], grid_cell;
     void *grid_frame;
+    /* The shared [n_agents, 22] table (Stepper.params.floats) when params_per_env = 1: the
+       body pass of the _ob entry points reads the agents' radius and mass from it, as the
+       reference's launch_obstacle_dynamics does whatever table the agent side uses
+       (swarp/core/stepper.py:961-964); the agents' own forces and integration read
+       `params`.  Ignored when params_per_env = 0. */
+    const void *body_params;
 } swarp_desc_t;
 
 #define SWARP_LISTS_BRUTE 0
@@ -190,7 +195,9 @@ int swarp_rollout_bwd_tape(const swarp_desc_t *desc, int32_t T, const swarp_stat
  * obstacle_dynamics_kernel, swarp/core/bodies.py:367-568, disc variant: the shapes of a
  * movable body are circles; the reference runs it on untaped steps,
  * swarp/core/stepper.py:952-991).  Replaces T calls of Stepper.launch_substeps with the
- * body pass enabled.  Fleets of 2-D models, 1 <= n_obstacles <= 16.
+ * body pass enabled.  Fleets of any dynamics models including drones, shared or per-env
+ * parameter rows (then desc->body_params), disc agents, at most 64 agents per env,
+ * 1 <= n_obstacles <= 16.
  * ob0 [E, 12N]: per env and obstacle index o, the shape state (pos x, pos y, angle,
  * vel x, vel y, ang_vel) at [6o..6o+5] and the state of the body rooted at o at
  * [6N+6o..6N+6o+5] (the reference's obs_* and body_* arrays, stepper.py:418-431).

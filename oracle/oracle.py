@@ -51,6 +51,7 @@ class OracleObs(ctypes.Structure):
         ("type", ctypes.c_void_p),
         ("kind", ctypes.c_void_p), ("body", ctypes.c_void_p),
         ("mass", ctypes.c_void_p), ("inertia", ctypes.c_void_p), ("body_off", ctypes.c_void_p),
+        ("body_params", ctypes.c_void_p),
     ]
 
 
@@ -137,6 +138,9 @@ class Oracle:
             off = obs.get("body_off")
             arrs["body_off"] = np.ascontiguousarray(np.zeros((n, 2)) if off is None else off,
                                                     dtype=self.dtype)
+        if obs.get("body_params") is not None:
+            # [A, 22] rows the body pass reads (the shared table under per-env rows)
+            arrs["body_params"] = np.ascontiguousarray(obs["body_params"], dtype=self.dtype)
         keep.append(arrs)
         o.n_obstacles = int(arrs["radius"].shape[0])
         for k, v in arrs.items():

@@ -57,6 +57,10 @@ typedef struct {
     int rk4;  /* Integrator.RK4 for the 2-D models */
     int grid_bins;          /* lists in uniform-grid order (0: index order) */
     REAL g_ox, g_oy, g_cs;  /* the grid's frame: origin, cell size */
+    /* agent rows the body pass reads, when they differ from the agents' own (NULL): the
+       reference's launch_obstacle_dynamics takes the shared table even where the agent
+       side runs per-env rows (swarp/core/stepper.py:961-964) */
+    const FN(prm_t) *PB;
 } FN(ctx_t);
 
 /* Per-env obstacle state, 12 reals per obstacle index o:
@@ -1746,7 +1750,7 @@ static void FN(step_env)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_
             for (int a = 0; a < 2 * A; ++a) F[a] = 0;
         }
         if (C->any_movable)
-            FN(bodies_env)(C, P, cur, obc, obn);
+            FN(bodies_env)(C, C->PB ? C->PB : P, cur, obc, obn);
         else if (N)
             memcpy(obn, obc, sizeof(REAL) * nob);
         if (C->wheel) {
@@ -1803,7 +1807,7 @@ static void FN(step_env_adj)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(ag
             FN(integrate_agent_adj)(C, P + a, cur + a, act + a * ad, F[a * 2], F[a * 2 + 1],
                                     g + a, tmp + a, gact + a * ad, gF + a * 2, gF + a * 2 + 1);
         if (C->any_movable)
-            FN(bodies_env_adj)(C, P, cur, obc, gob, tmp, gprev);
+            FN(bodies_env_adj)(C, C->PB ? C->PB : P, cur, obc, gob, tmp, gprev);
         else if (N)
             memcpy(gprev, gob, sizeof(REAL) * nob);
         if (C->needs_forces) FN(forces_env_adj)(C, obc, P, cur, idx, cnt, gF, tmp, N ? gprev : NULL);
@@ -1974,6 +1978,19 @@ int FN(oracle_neighbors_grid)(int E, int A, int K, const REAL *pos, double radiu
     return 0;
 }
 
+/* The rows the body pass reads when obs->body_params is set (installed in C->PB; free
+   the result), else NULL. */
+static FN(prm_t) *FN(body_rows)(const oracle_obs_t *obs, const int32_t *tags,
+                                const int32_t *modes, int A, FN(ctx_t) *C)
+{
+    if (!obs || !obs->body_params) return NULL;
+    FN(prm_t) *PB = (FN(prm_t) *)calloc((size_t)A, sizeof(FN(prm_t)));
+    FN(ctx_t) scratch = *C;
+    FN(make_prm)((const REAL *)obs->body_params, tags, modes, A, PB, &scratch);
+    C->PB = PB;
+    return PB;
+}
+
 static int FN(chain_alloc)(FN(chain_t) *ch, int A, int S, int K, int N)
 {
     ch->st = (FN(agent_t) *)malloc(sizeof(FN(agent_t)) * (size_t)(S + 1) * A);
@@ -2003,6 +2020,7 @@ int FN(oracle_rollout_ob)(const oracle_cfg_t *cfg, const REAL *params, const int
     size_t nob = (size_t)OB_W * N;
     FN(prm_t) *P = (FN(prm_t) *)calloc((size_t)A, sizeof(FN(prm_t)));
     FN(make_prm)(params, tags, modes, A, P, &C);
+    FN(prm_t) *PB = FN(body_rows)(obs, tags, modes, A, &C);
     int nth = cfg->n_threads > 0 ? cfg->n_threads : 1;
     int err = 0;
 #pragma omp parallel num_threads(nth)
@@ -2038,6 +2056,7 @@ int FN(oracle_rollout_ob)(const oracle_cfg_t *cfg, const REAL *params, const int
         free(obw);
     }
     free(P);
+    free(PB);
     return err ? -1 : 0;
 }
 
@@ -2069,6 +2088,7 @@ int FN(oracle_rollout_adj_ob)(const oracle_cfg_t *cfg, const REAL *params, const
     size_t nob = (size_t)OB_W * N;
     FN(prm_t) *P = (FN(prm_t) *)calloc((size_t)A, sizeof(FN(prm_t)));
     FN(make_prm)(params, tags, modes, A, P, &C);
+    FN(prm_t) *PB = FN(body_rows)(obs, tags, modes, A, &C);
     int nth = cfg->n_threads > 0 ? cfg->n_threads : 1;
     int err = 0;
     memset(adj_actions, 0, sizeof(REAL) * (size_t)T * E * A * ad);
@@ -2131,6 +2151,7 @@ int FN(oracle_rollout_adj_ob)(const oracle_cfg_t *cfg, const REAL *params, const
         free(g); free(gn); free(tmp); free(gF); free(ow);
     }
     free(P);
+    free(PB);
     return err ? -1 : 0;
 }
 

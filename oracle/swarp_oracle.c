@@ -49,6 +49,9 @@ typedef struct {
        body [N] (root shape), mass [N], inertia [N], body_off [N,2] */
     const int32_t *kind, *body;
     const void *mass, *inertia, *body_off;
+    /* [A, 22] agent rows the body pass reads (NULL: the agents' own rows): the shared
+       table when the agents' rows are per env (swarp/core/stepper.py:961-964) */
+    const void *body_params;
 } oracle_obs_t;
 
 int oracle_abi_version(void) { return 1; }

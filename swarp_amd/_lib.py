@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 F32, F64 = 0, 1
 EULER, RK4 = 0, 1
 LISTS_BRUTE, LISTS_GRID = 0, 1
@@ -80,6 +80,7 @@ class SwarpDesc(ctypes.Structure):
         ("grid_origin", ctypes.c_double * 2),
         ("grid_cell", ctypes.c_double),
         ("grid_frame", ctypes.c_void_p),
+        ("body_params", ctypes.c_void_p),
     ]
 
 

@@ -247,17 +247,19 @@ class _RolloutFn(torch.autograd.Function):
 
 def _launch_fwd_ob(stepper: Stepper, state0, ob0: torch.Tensor, actions_seq: torch.Tensor,
                    traj, final, ob_traj: torch.Tensor) -> None:
-    """One forward launch of a world with movable bodies (2-D fleet, five fields)."""
+    """One forward launch of a world with movable bodies (five state fields, nine with
+    drones)."""
     T, E, _, ad = actions_seq.shape
+    nf = _nfields(stepper)
     lib = _lib.load()
     desc = stepper.desc(E, ad)
     EA, dt, NW = E * stepper.n_agents, stepper.dtype, 12 * stepper.n_obstacles
     check_extent(actions_seq, T * EA * ad, "actions", dt)
     check_extent(ob0, E * NW, "ob_state", dt)
     check_extent(ob_traj, T * E * NW, "ob_trajectory", dt)
-    s0 = state_struct(list(state0)[:5], EA, dt, "state0")
-    fin = state_struct(list(final)[:5], EA, dt, "final")
-    tr = state_struct(list(traj)[:5], (T - 1) * EA, dt, "traj") if traj is not None and T > 1 else None
+    s0 = state_struct(list(state0)[:nf], EA, dt, "state0")
+    fin = state_struct(list(final)[:nf], EA, dt, "final")
+    tr = state_struct(list(traj)[:nf], (T - 1) * EA, dt, "traj") if traj is not None and T > 1 else None
     _lib.check(lib.swarp_rollout_fwd_ob(
         ctypes.byref(desc), T, ctypes.byref(s0), ob0.data_ptr(), actions_seq.data_ptr(),
         ctypes.byref(tr) if tr is not None else None, ctypes.byref(fin), ob_traj.data_ptr(),
@@ -267,9 +269,9 @@ def _launch_fwd_ob(stepper: Stepper, state0, ob0: torch.Tensor, actions_seq: tor
 
 class _RolloutObFn(torch.autograd.Function):
     """T steps of a world with movable bodies as one autograd node: inputs (actions,
-    obstacle state, five state fields); outputs the final state fields, the stacked
-    trajectory fields of steps 0..T-2, and the obstacle states after every step
-    ``[T, n_envs, 12 N]``."""
+    obstacle state, the five state fields, nine with drones); outputs the final state
+    fields, the stacked trajectory fields of steps 0..T-2, and the obstacle states after
+    every step ``[T, n_envs, 12 N]``."""
 
     @staticmethod
     def forward(ctx, stepper: Stepper, actions_seq: torch.Tensor, ob0: torch.Tensor,
@@ -291,20 +293,21 @@ class _RolloutObFn(torch.autograd.Function):
             sink.append(("fwd", e0, _event(actions_seq)))
         ctx.stepper = stepper
         ctx.T = T
+        ctx.nf = len(state0)
         ctx.save_for_backward(actions_seq, ob0, ob_traj, *state0, *traj)
         return (*final, *traj, ob_traj)
 
     @staticmethod
     def backward(ctx, *grads):
         stepper: Stepper = ctx.stepper
-        T = ctx.T
+        T, nf = ctx.T, ctx.nf
         saved = ctx.saved_tensors
         actions_seq, ob0, ob_traj = saved[0], saved[1], saved[2]
-        state0 = saved[3:8]
-        traj = saved[8:13]
-        g_final = [None if g is None else g.contiguous() for g in grads[:5]]
-        g_traj = [None if g is None else g.contiguous() for g in grads[5:10]]
-        g_ob = grads[10].contiguous() if grads[10] is not None else None
+        state0 = saved[3:3 + nf]
+        traj = saved[3 + nf:3 + 2 * nf]
+        g_final = [None if g is None else g.contiguous() for g in grads[:nf]]
+        g_traj = [None if g is None else g.contiguous() for g in grads[nf:2 * nf]]
+        g_ob = grads[2 * nf].contiguous() if grads[2 * nf] is not None else None
         need = ctx.needs_input_grad
         adj_act = torch.empty_like(actions_seq)
         adj_ob0 = torch.empty_like(ob0) if need[2] else None
@@ -355,15 +358,16 @@ def _rollout_bodies(stepper: Stepper, state: TorchState, actions_seq: torch.Tens
     grad = torch.is_grad_enabled() and (
         ob0.requires_grad or actions_seq.requires_grad
         or any(t is not None and t.requires_grad for t in state))
+    nf = _nfields(stepper)
     if grad:
-        outs = _RolloutObFn.apply(stepper, actions_seq, ob0, *state[:5])
-        ob_traj = outs[10]
-        outs = outs[:10]
+        outs = _RolloutObFn.apply(stepper, actions_seq, ob0, *state[:nf])
+        ob_traj = outs[2 * nf]
+        outs = outs[:2 * nf]
     else:
         final = _empty_like_fields(stepper, (), E, actions_seq.device)
         traj = _empty_like_fields(stepper, (T - 1,), E, actions_seq.device)
         ob_traj = torch.empty((T,) + tuple(ob0.shape), device=ob0.device, dtype=ob0.dtype)
-        _launch_fwd_ob(stepper, [t.contiguous() for t in state[:5]], ob0.contiguous(),
+        _launch_fwd_ob(stepper, [t.contiguous() for t in state[:nf]], ob0.contiguous(),
                        actions_seq.contiguous(), traj, final, ob_traj)
         outs = (*final, *traj)
     stepper.ob_trajectory = ob_traj

@@ -32,6 +32,10 @@ constexpr int NOB_MAX = 16;    // obstacles per env on this path
 template <typename T> struct ObTab {
     const SWARP_RO T *rad, *half, *mass, *inertia, *off;  // [N], [N,2], [N], [N], [N,2]
     const SWARP_RO int32_t *type, *kind, *body;            // [N]
+    // [A, 22] parameter rows the body pass reads for the agents' reactions when the
+    // agents' own rows are per env (NULL: the agents' rows).  The reference's body pass
+    // takes the shared table whatever the agent side uses (swarp/core/stepper.py:961-964).
+    const SWARP_RO T *bprm;
     T lin_damp, ang_damp;
     int N;
 };
@@ -43,6 +47,22 @@ template <typename T> struct ObIO {
     const T *atraj;     // [T, E, 12N] adjoint arriving at each step's output (nullable)
     T *a0;              // [E, 12N] adjoint of ob0 (nullable)
 };
+
+// An agent as the body pass sees it: the radius and the implicit damping denominator
+// 1 + c sub_dt / m of its parameter row in the table the pass reads.
+template <typename T> struct BodyRow {
+    T r, dd;
+};
+
+template <typename T, int PA>
+__device__ __forceinline__ BodyRow<T> body_row(const Cst<T> &C, const ObTab<T> &tb,
+                                               const Lane<T, PA> &L)
+{
+    if (!tb.bprm) return BodyRow<T>{L.pr.radius, L.dd};
+    const int ag = L.real ? L.agent : 0;
+    const T m = tb.bprm[(size_t)ag * 22 + 1];
+    return BodyRow<T>{tb.bprm[(size_t)ag * 22], T(1) + C.c * C.sub_dt / m};
+}
 
 // sin and cos of a body angle (the portable evaluation of swarp_pmath.h, as the oracle's)
 template <typename T> __device__ __forceinline__ void psincos(T xr, T &so, T &co)
@@ -259,8 +279,8 @@ template <typename T> struct BodyNew {
 // the lane in `st`; `od` = the env's obstacle state at the substep input.
 template <typename T, int PA>
 __device__ __forceinline__ void body_step(const Cst<T> &C, const ObTab<T> &tb,
-                                          const Lane<T, PA> &L, const St<T> &st, const T *od,
-                                          int o, BodyNew<T> &B)
+                                          const Lane<T, PA> &L, const BodyRow<T> &br,
+                                          const St<T> &st, const T *od, int o, BodyNew<T> &B)
 {
     typedef typename MaskT<PA>::type M;
     const int N = tb.N;
@@ -288,10 +308,10 @@ __device__ __forceinline__ void body_step(const Cst<T> &C, const ObTab<T> &tb,
         ext = wmax(ext, reach);
         // the agents' reactions, in agent order
         T f0 = T(0), f1 = T(0), tq = T(0);
-        if (L.active && !b_apart(st.px - csx, st.py - csy, L.pr.radius + ro + C.margin)) {
+        if (L.active && !b_apart(st.px - csx, st.py - csy, br.r + ro + C.margin)) {
             T gx, gy;
             pair_force(C, st.px - csx, st.py - csy, st.vx - vsx, st.vy - vsy,
-                       L.pr.radius + ro + C.margin, L.dd, gx, gy);
+                       br.r + ro + C.margin, br.dd, gx, gy);
             f0 = -gx;
             f1 = -gy;
             const T lx = owx + T(0), ly = owy + T(0);
@@ -363,15 +383,15 @@ __device__ __forceinline__ void body_step(const Cst<T> &C, const ObTab<T> &tb,
 // re-installed at the new pose.  Lane `agent` of the env copies entries agent, agent+PA...
 template <typename T, int PA>
 __device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
-                                          const Lane<T, PA> &L, const St<T> &st, const T *obc,
-                                          T *obn)
+                                          const Lane<T, PA> &L, const BodyRow<T> &br,
+                                          const St<T> &st, const T *obc, T *obn)
 {
     const int N = tb.N;
     for (int q = L.agent; q < OB_W * N; q += PA) obn[q] = obc[q];
     for (int o = 0; o < N; ++o) {
         if (tb.body[o] != o || tb.kind[o] != 1) continue;
         BodyNew<T> B;
-        body_step<T, PA>(C, tb, L, st, obc, o, B);
+        body_step<T, PA>(C, tb, L, br, st, obc, o, B);
         if (L.agent == 0) {
             T *bo = obn + 6 * N + 6 * o;
             bo[0] = B.nx;
@@ -413,7 +433,7 @@ constexpr int body_bwd_waves(int PA, size_t tsize, unsigned F)
 
 // ------------------------------------------------------------------ forward rollout
 
-template <typename T, int PA, unsigned F>
+template <typename T, int PA, bool DRONE, unsigned F>
 __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_fwd(const Cst<T> Cin, const Args<T> g,
                                                  const ObTab<T> tb, const ObIO<T> io)
 {
@@ -426,6 +446,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
     fold_prm<F>(L.pr);
+    const BodyRow<T> br = body_row<T, PA>(C, tb, L);
     lr[L.lane] = L.pr.radius;
     const int ew = L.lane / PA;
     const int NW = OB_W * tb.N;
@@ -433,7 +454,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
     const size_t eo = (size_t)(env_ok ? L.env : 0) * NW;
     for (int q = L.agent; q < NW; q += PA) lob[0][ew][q] = io.ob0[eo + q];
     St<T> st;
-    load_state<T, false>(g.s0.f, L.idx, 0, st);
+    load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
     if (!L.active) st.px = st.py = __builtin_nan("");
     const size_t EA = (size_t)C.E * C.A, ENW = (size_t)C.E * NW;
     int cur = 0;
@@ -453,9 +474,9 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
             const T *obc = lob[cur][ew];
             T Fx, Fy;
             forces_b<T, PA>(C, tb, L, sl, lr, obc, st, s, s == 0 || !ok, cand, Fx, Fy);
-            body_pass<T, PA>(C, tb, L, st, obc, lob[cur ^ 1][ew]);
+            body_pass<T, PA>(C, tb, L, br, st, obc, lob[cur ^ 1][ew]);
             St<T> nx;
-            integrate<T, false>(C, L.pr, st, a, Fx, Fy, nx);
+            integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
             if (C.use_skin) {
                 D += (m_abs(nx.px - st.px) + m_abs(nx.py - st.py)) * T(1.0001);
                 ok = env_all<PA>(!L.active || D <= C.half_margin, L.base);
@@ -466,9 +487,9 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
         __syncthreads();
         if (L.active) {
             if (t + 1 < g.nsteps)
-                store_state<T, false>(g.traj.f, (size_t)t * EA + L.idx, st);
+                store_state<T, DRONE>(g.traj.f, (size_t)t * EA + L.idx, st);
             else
-                store_state<T, false>(g.fin.f, L.idx, st);
+                store_state<T, DRONE>(g.fin.f, L.idx, st);
         }
         if (env_ok)
             for (int q = L.agent; q < NW; q += PA) io.traj[(size_t)t * ENW + eo + q] = lob[cur][ew][q];
@@ -478,11 +499,12 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
 // ----------------------------------------------------------------- backward rollout
 
 // Dynamic LDS of k_body_bwd (host and device agree on this layout).
-template <typename T, int PA> __host__ __device__ constexpr size_t body_bwd_lds(int S, int N)
+template <typename T, int PA, bool DRONE>
+__host__ __device__ constexpr size_t body_bwd_lds(int S, int N)
 {
     typedef typename MaskT<PA>::type M;
     return 2 * 64 * sizeof(T)                               // radius, damping divisor
-           + (size_t)S * NF_2D * 64 * sizeof(T)             // substep agent slots
+           + (size_t)S * (DRONE ? NF_DRONE : NF_2D) * 64 * sizeof(T)  // substep agent slots
            + (size_t)S * 64 * sizeof(M)                     // inclusion masks
            + (size_t)(S + 1) * (64 / PA) * OB_W * N * sizeof(T)  // obstacle state per substep
            + 2 * (size_t)(64 / PA) * OB_W * N * sizeof(T);       // obstacle adjoint in / out
@@ -494,9 +516,9 @@ template <typename T, int PA> __host__ __device__ constexpr size_t body_bwd_lds(
 // bodies_env_adj.
 template <typename T, int PA>
 __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &tb,
-                                              const Lane<T, PA> &L, const St<T> &st,
-                                              const T *obc, const T *gout, T *gin,
-                                              St<T> &ga)
+                                              const Lane<T, PA> &L, const BodyRow<T> &br,
+                                              const St<T> &st, const T *obc, const T *gout,
+                                              T *gin, St<T> &ga)
 {
     typedef typename MaskT<PA>::type M;
     const int N = tb.N;
@@ -509,7 +531,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
     for (int o = 0; o < N; ++o) {
         if (tb.body[o] != o || tb.kind[o] != 1) continue;
         BodyNew<T> B;
-        body_step<T, PA>(C, tb, L, st, obc, o, B);
+        body_step<T, PA>(C, tb, L, br, st, obc, o, B);
         const T sdt = C.sub_dt, one = T(1);
         const T lin_decay = one - tb.lin_damp * sdt;
         const T ang_decay = one - tb.ang_damp * sdt;
@@ -553,14 +575,14 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
             const T g_f0 = g_fx - g_tau * owy, g_f1 = g_fy + g_tau * owx;
             // the agents' terms, in agent order
             T c0 = T(0), c1 = T(0), c2 = T(0), c3 = T(0), c4 = T(0), c5 = T(0);
-            if (L.active && !b_apart(st.px - csx, st.py - csy, L.pr.radius + ro + C.margin)) {
+            if (L.active && !b_apart(st.px - csx, st.py - csy, br.r + ro + C.margin)) {
                 const T dx = st.px - csx, dy = st.py - csy, rvx = st.vx - vsx, rvy = st.vy - vsy;
-                const T md = L.pr.radius + ro + C.margin;
+                const T md = br.r + ro + C.margin;
                 T gx, gy;
-                pair_force(C, dx, dy, rvx, rvy, md, L.dd, gx, gy);
+                pair_force(C, dx, dy, rvx, rvy, md, br.dd, gx, gy);
                 const T f0 = -gx, f1 = -gy;
                 T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
-                pair_force_adj(C, dx, dy, rvx, rvy, md, L.dd, -g_f0, -g_f1, adx, ady, arx, ary);
+                pair_force_adj(C, dx, dy, rvx, rvy, md, br.dd, -g_f0, -g_f1, adx, ady, arx, ary);
                 ga.px += adx;
                 ga.py += ady;
                 ga.vx += arx;
@@ -629,24 +651,26 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
     }
 }
 
-template <typename T, int PA, unsigned F>
+template <typename T, int PA, bool DRONE, unsigned F>
 __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_bwd(const Cst<T> Cin, const Args<T> g,
                                                  const ObTab<T> tb, const ObIO<T> io)
 {
     const Cst<T> C = fold_cst<F>(Cin);
     typedef typename MaskT<PA>::type M;
     constexpr int EPW = 64 / PA;
+    constexpr int NF = DRONE ? NF_DRONE : NF_2D;
     extern __shared__ __align__(16) unsigned char smem[];
     const int N = tb.N, NW = OB_W * N;
     T *lr = (T *)smem;                                   // radius per lane
     T *ldd = lr + 64;                                    // damping divisor per lane
-    T *slots = ldd + 64;                                 // S slots of NF_2D fields
-    M *lmask = (M *)(slots + (size_t)C.S * NF_2D * 64);  // S inclusion masks
+    T *slots = ldd + 64;                                 // S slots of NF fields
+    M *lmask = (M *)(slots + (size_t)C.S * NF * 64);     // S inclusion masks
     T *lobs = (T *)(lmask + (size_t)C.S * 64);           // [S+1][EPW][NW] obstacle states
     T *lgob = lobs + (size_t)(C.S + 1) * EPW * NW;       // [2][EPW][NW] obstacle adjoints
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
     fold_prm<F>(L.pr);
+    const BodyRow<T> br = body_row<T, PA>(C, tb, L);
     lr[L.lane] = L.pr.radius;
     ldd[L.lane] = L.dd;
     const int ew = L.lane / PA;
@@ -660,17 +684,17 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
     st_zero(gs);
     for (int t = g.nsteps - 1; t >= 0; --t) {
         if (t == g.nsteps - 1)
-            add_adj<T, false>(g.afin.f, L.idx, gs);
+            add_adj<T, DRONE>(g.afin.f, L.idx, gs);
         else
-            add_adj<T, false>(g.atraj.f, (size_t)t * EA + L.idx, gs);
+            add_adj<T, DRONE>(g.atraj.f, (size_t)t * EA + L.idx, gs);
         __syncthreads();
         if (io.atraj && env_ok)
             for (int q = L.agent; q < NW; q += PA) gob[q] += io.atraj[(size_t)t * ENW + eo + q];
         St<T> st;
         if (t == 0)
-            load_state<T, false>(g.s0.f, L.idx, 0, st);
+            load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
         else
-            load_state<T, false>(g.traj.f, L.idx, (size_t)(t - 1) * EA, st);
+            load_state<T, DRONE>(g.traj.f, L.idx, (size_t)(t - 1) * EA, st);
         if (!L.active) st.px = st.py = __builtin_nan("");
         {
             const T *src = t == 0 ? io.ob0 + eo : io.traj + (size_t)(t - 1) * ENW + eo;
@@ -685,9 +709,9 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
         T D = T(0);
         bool ok = false;
         for (int s = 0; s < C.S; ++s) {
-            T *sl = slots + (size_t)s * NF_2D * 64;
+            T *sl = slots + (size_t)s * NF * 64;
             __syncthreads();
-            slot_put<T, false>(sl, L.lane, st);
+            slot_put<T, DRONE>(sl, L.lane, st);
             __syncthreads();
             const T *obc = lobs + ((size_t)s * EPW + ew) * NW;
             T Fx, Fy;
@@ -695,9 +719,9 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             sl[F_FX * 64 + L.lane] = Fx;
             sl[F_FY * 64 + L.lane] = Fy;
             lmask[s * 64 + L.lane] = incl;
-            body_pass<T, PA>(C, tb, L, st, obc, lobs + ((size_t)(s + 1) * EPW + ew) * NW);
+            body_pass<T, PA>(C, tb, L, br, st, obc, lobs + ((size_t)(s + 1) * EPW + ew) * NW);
             St<T> nx;
-            integrate<T, false>(C, L.pr, st, a, Fx, Fy, nx);
+            integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
             if (C.use_skin) {
                 D += (m_abs(nx.px - st.px) + m_abs(nx.py - st.py)) * T(1.0001);
                 ok = env_all<PA>(!L.active || D <= C.half_margin, L.base);
@@ -708,17 +732,17 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
         // ---- reverse pass
         T ga[4] = {T(0), T(0), T(0), T(0)};
         for (int s = C.S - 1; s >= 0; --s) {
-            T *sl = slots + (size_t)s * NF_2D * 64;
+            T *sl = slots + (size_t)s * NF * 64;
             const T *obc = lobs + ((size_t)s * EPW + ew) * NW;
             __syncthreads();
             St<T> in;
-            slot_get<T, false>(sl, L.lane, in);
+            slot_get<T, DRONE>(sl, L.lane, in);
             const T Fx = sl[F_FX * 64 + L.lane], Fy = sl[F_FY * 64 + L.lane];
             St<T> gi;
             T gFx, gFy;
-            integrate_adj<T, false>(C, L.pr, in, a, Fx, Fy, gs, gi, ga, gFx, gFy);
+            integrate_adj<T, DRONE>(C, L.pr, in, a, Fx, Fy, gs, gi, ga, gFx, gFy);
             // the body pass: adjoint of its input obstacle state into gprev
-            body_pass_adj<T, PA>(C, tb, L, in, obc, gob, gprev, gi);
+            body_pass_adj<T, PA>(C, tb, L, br, in, obc, gob, gprev, gi);
             if (C.needs_forces) {
                 const T wFx = gFx * L.inv_dd, wFy = gFy * L.inv_dd;
                 __syncthreads();
@@ -782,7 +806,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             for (int k = 0; k < C.ad; ++k) pa[k] = k < 4 ? ga[k] : T(0);
         }
     }
-    if (L.active) store_adj<T, false>(g.a0.f, L.idx, gs);
+    if (L.active) store_adj<T, DRONE>(g.a0.f, L.idx, gs);
     __syncthreads();
     if (io.a0 && env_ok)
         for (int q = L.agent; q < NW; q += PA) io.a0[eo + q] = gob[q];
@@ -790,24 +814,29 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
 
 // ---------------------------------------------------------------------- launchers
 
-template <typename T> size_t body_bwd_lds_of(int PA, int S, int N)
+template <typename T, bool DRONE> size_t body_bwd_lds_pa(int PA, int S, int N)
 {
     switch (PA) {
-    case 4: return body_bwd_lds<T, 4>(S, N);
-    case 8: return body_bwd_lds<T, 8>(S, N);
-    case 16: return body_bwd_lds<T, 16>(S, N);
-    case 32: return body_bwd_lds<T, 32>(S, N);
-    default: return body_bwd_lds<T, 64>(S, N);
+    case 4: return body_bwd_lds<T, 4, DRONE>(S, N);
+    case 8: return body_bwd_lds<T, 8, DRONE>(S, N);
+    case 16: return body_bwd_lds<T, 16, DRONE>(S, N);
+    case 32: return body_bwd_lds<T, 32, DRONE>(S, N);
+    default: return body_bwd_lds<T, 64, DRONE>(S, N);
     }
 }
 
-#define SWARP_BODY_DISPATCH(KERNEL, FP, SHM)                                          \
+template <typename T> size_t body_bwd_lds_of(int PA, int S, int N, bool drone)
+{
+    return drone ? body_bwd_lds_pa<T, true>(PA, S, N) : body_bwd_lds_pa<T, false>(PA, S, N);
+}
+
+#define SWARP_BODY_DISPATCH(KERNEL, DR, FP, SHM)                                       \
     switch (PA) {                                                                      \
-    case 4: hipLaunchKernelGGL((KERNEL<T, 4, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
-    case 8: hipLaunchKernelGGL((KERNEL<T, 8, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
-    case 16: hipLaunchKernelGGL((KERNEL<T, 16, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
-    case 32: hipLaunchKernelGGL((KERNEL<T, 32, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
-    default: hipLaunchKernelGGL((KERNEL<T, 64, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
+    case 4: hipLaunchKernelGGL((KERNEL<T, 4, DR, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
+    case 8: hipLaunchKernelGGL((KERNEL<T, 8, DR, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
+    case 16: hipLaunchKernelGGL((KERNEL<T, 16, DR, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
+    case 32: hipLaunchKernelGGL((KERNEL<T, 32, DR, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
+    default: hipLaunchKernelGGL((KERNEL<T, 64, DR, FP>), grid, dim3(64), SHM, st, C, a, tb, io); break; \
     }
 
 // The profile besides FT_ALL the body kernels compile for float32 (0: none).
@@ -816,30 +845,35 @@ template <typename T> constexpr unsigned body_profile()
     return sizeof(T) == 4 ? FT_PROF_BODY : 0u;
 }
 
-// feat: the FT_* paths the world uses; the profile runs when it covers them.
+// feat: the FT_* paths the world uses; the profile runs when it covers them.  A fleet
+// holding a drone (all nine state fields stepped) runs the general DRONE instances.
 template <typename T>
 void launch_body_fwd(int PA, const Cst<T> &C, const Args<T> &a, const ObTab<T> &tb,
-                     const ObIO<T> &io, unsigned feat, hipStream_t st)
+                     const ObIO<T> &io, unsigned feat, bool drone, hipStream_t st)
 {
     const dim3 grid((C.E + 64 / PA - 1) / (64 / PA));
     constexpr unsigned P = body_profile<T>();
-    if (P != 0u && (feat & ~P) == 0u) {
-        SWARP_BODY_DISPATCH(k_body_fwd, (P ? P : FT_ALL), 0)
+    if (drone) {
+        SWARP_BODY_DISPATCH(k_body_fwd, true, FT_ALL, 0)
+    } else if (P != 0u && (feat & ~P) == 0u) {
+        SWARP_BODY_DISPATCH(k_body_fwd, false, (P ? P : FT_ALL), 0)
     } else {
-        SWARP_BODY_DISPATCH(k_body_fwd, FT_ALL, 0)
+        SWARP_BODY_DISPATCH(k_body_fwd, false, FT_ALL, 0)
     }
 }
 
 template <typename T>
 void launch_body_bwd(int PA, const Cst<T> &C, const Args<T> &a, const ObTab<T> &tb,
-                     const ObIO<T> &io, unsigned feat, size_t shm, hipStream_t st)
+                     const ObIO<T> &io, unsigned feat, bool drone, size_t shm, hipStream_t st)
 {
     const dim3 grid((C.E + 64 / PA - 1) / (64 / PA));
     constexpr unsigned P = body_profile<T>();
-    if (P != 0u && (feat & ~P) == 0u) {
-        SWARP_BODY_DISPATCH(k_body_bwd, (P ? P : FT_ALL), shm)
+    if (drone) {
+        SWARP_BODY_DISPATCH(k_body_bwd, true, FT_ALL, shm)
+    } else if (P != 0u && (feat & ~P) == 0u) {
+        SWARP_BODY_DISPATCH(k_body_bwd, false, (P ? P : FT_ALL), shm)
     } else {
-        SWARP_BODY_DISPATCH(k_body_bwd, FT_ALL, shm)
+        SWARP_BODY_DISPATCH(k_body_bwd, false, FT_ALL, shm)
     }
 }
 #undef SWARP_BODY_DISPATCH

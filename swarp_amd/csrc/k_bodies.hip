@@ -4,8 +4,9 @@
 namespace swarp {
 template void launch_body_fwd<SWARP_T>(int, const Cst<SWARP_T> &, const Args<SWARP_T> &,
                                        const ObTab<SWARP_T> &, const ObIO<SWARP_T> &, unsigned,
-                                       hipStream_t);
+                                       bool, hipStream_t);
 template void launch_body_bwd<SWARP_T>(int, const Cst<SWARP_T> &, const Args<SWARP_T> &,
                                        const ObTab<SWARP_T> &, const ObIO<SWARP_T> &, unsigned,
-                                       size_t, hipStream_t);
+                                       bool, size_t, hipStream_t);
+template size_t body_bwd_lds_of<SWARP_T>(int, int, int, bool);
 }  // namespace swarp

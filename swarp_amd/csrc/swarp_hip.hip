@@ -415,7 +415,6 @@ template <typename T> static int fill_obtab(const swarp_desc_t *d, ObTab<T> &tb)
         return fail("the body path takes 1 to 16 obstacles per env");
     if (!d->obs_kind || !d->obs_body || !d->obs_mass || !d->obs_inertia || !d->obs_body_off)
         return fail("obs_kind/obs_body/obs_mass/obs_inertia/obs_body_off must be set");
-    if (d->has_drone) return fail("the body path steps 2-D fleets only");
     if (wide_path(d))
         return fail("the body path steps at most 64 agents per env with index-ordered lists");
     tb.rad = (decltype(tb.rad))d->obs_radius;
@@ -426,6 +425,10 @@ template <typename T> static int fill_obtab(const swarp_desc_t *d, ObTab<T> &tb)
     tb.type = (decltype(tb.type))d->obs_type;
     tb.kind = (decltype(tb.kind))d->obs_kind;
     tb.body = (decltype(tb.body))d->obs_body;
+    // per-env rows: the body pass reads the shared table (body_params)
+    if (d->params_per_env && !d->body_params)
+        return fail("body_params must be set when params_per_env = 1 and bodies move");
+    tb.bprm = d->params_per_env ? (decltype(tb.bprm))d->body_params : nullptr;
     tb.lin_damp = (T)d->lin_damping;
     tb.ang_damp = (T)d->ang_damping;
     tb.N = d->n_obstacles;
@@ -443,9 +446,10 @@ static int rollout_fwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     fill_args<T>(d, a);
     ObTab<T> tb;
     if (fill_obtab<T>(d, tb)) return -1;
-    if (!fields_ok(s0, 5)) return fail("state0 is missing a field");
-    if (!fields_ok(fin, 5)) return fail("final_state is missing a field");
-    if (nT > 1 && !fields_ok(traj, 5)) return fail("traj is missing a field (T > 1)");
+    const int nf = d->has_drone ? 9 : 5;
+    if (!fields_ok(s0, nf)) return fail("state0 is missing a field");
+    if (!fields_ok(fin, nf)) return fail("final_state is missing a field");
+    if (nT > 1 && !fields_ok(traj, nf)) return fail("traj is missing a field (T > 1)");
     if (!act || !ob0 || !ob_traj) return fail("actions / ob0 / ob_traj is NULL");
     copy_fields<T>(s0, (T **)a.s0.f);
     copy_fields<T>(fin, a.fin.f);
@@ -454,7 +458,7 @@ static int rollout_fwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     a.nsteps = nT;
     ObIO<T> io = {(const T *)ob0, (T *)ob_traj, nullptr, nullptr};
     const int PA = pad_agents(d->n_agents);
-    launch_body_fwd<T>(PA, C, a, tb, io, world_features(d, true), st);
+    launch_body_fwd<T>(PA, C, a, tb, io, world_features(d, true), d->has_drone != 0, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
     return 0;
@@ -473,8 +477,9 @@ static int rollout_bwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     fill_args<T>(d, a);
     ObTab<T> tb;
     if (fill_obtab<T>(d, tb)) return -1;
-    if (!fields_ok(s0, 5)) return fail("state0 is missing a field");
-    if (nT > 1 && !fields_ok(traj, 5)) return fail("traj is missing a field (T > 1)");
+    const int nf = d->has_drone ? 9 : 5;
+    if (!fields_ok(s0, nf)) return fail("state0 is missing a field");
+    if (nT > 1 && !fields_ok(traj, nf)) return fail("traj is missing a field (T > 1)");
     if (!act || !aact || !ob0 || !ob_traj) return fail("actions / adj_actions / ob0 / ob_traj is NULL");
     copy_fields<T>(s0, (T **)a.s0.f);
     if (nT > 1) copy_fields<T>(traj, a.traj.f);
@@ -486,9 +491,9 @@ static int rollout_bwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     a.nsteps = nT;
     ObIO<T> io = {(const T *)ob0, (T *)ob_traj, (const T *)aob_traj, (T *)aob0};
     const int PA = pad_agents(d->n_agents);
-    const size_t shm = body_bwd_lds_of<T>(PA, d->substeps, d->n_obstacles);
+    const size_t shm = body_bwd_lds_of<T>(PA, d->substeps, d->n_obstacles, d->has_drone != 0);
     if (shm > 65536) return fail("substeps too large for the body backward's LDS staging (limit 64 KiB per wave)");
-    launch_body_bwd<T>(PA, C, a, tb, io, world_features(d, true), shm, st);
+    launch_body_bwd<T>(PA, C, a, tb, io, world_features(d, true), d->has_drone != 0, shm, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
     return 0;
@@ -553,9 +558,9 @@ int swarp_rollout_fwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
     g_err[0] = 0;
     if (check_desc(desc)) return -1;
     if (T < 1) return fail("T must be >= 1");
-    if (desc->has_boxes || desc->wheel_contacts || desc->params_per_env)
-        return fail("box agents, wheel contacts and per-env parameters with movable bodies are "
-                    "not supported in this build");
+    if (desc->has_boxes || desc->wheel_contacts)
+        return fail("box agents and wheel contacts with movable bodies are not supported in "
+                    "this build");
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
         return rollout_fwd_ob<float>(desc, T, state0, ob0, actions, traj, final_state, ob_traj, st);
@@ -572,9 +577,9 @@ int swarp_rollout_bwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
     g_err[0] = 0;
     if (check_desc(desc)) return -1;
     if (T < 1) return fail("T must be >= 1");
-    if (desc->has_boxes || desc->wheel_contacts || desc->params_per_env)
-        return fail("box agents, wheel contacts and per-env parameters with movable bodies are "
-                    "not supported in this build");
+    if (desc->has_boxes || desc->wheel_contacts)
+        return fail("box agents and wheel contacts with movable bodies are not supported in "
+                    "this build");
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
         return rollout_bwd_ob<float>(desc, T, state0, ob0, actions, traj, ob_traj, adj_traj,

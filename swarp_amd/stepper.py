@@ -269,8 +269,6 @@ class Stepper:
         if movable:
             if n > 16:
                 raise NotImplementedError("movable bodies: this build steps at most 16 obstacles per env")
-            if self.has_drone:
-                raise NotImplementedError("movable bodies with DRONE agents are not implemented")
             if self.has_boxes:
                 raise NotImplementedError("movable bodies with box agents are not implemented")
             if self.wide:
@@ -370,6 +368,8 @@ class Stepper:
                     f"stepping {n_envs}")
             d.params = self.params_per_env.data_ptr()
             d.params_per_env = 1
+            # the body pass reads the shared rows (swarp/core/stepper.py:961-964)
+            d.body_params = self.params.floats.data_ptr()
         else:
             d.params = self.params.floats.data_ptr()
         d.model_tag = self.params.model_tag.data_ptr()

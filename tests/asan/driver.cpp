@@ -49,6 +49,7 @@ struct Case {
     int E, A, T, S, K, ad, nobs;
     bool drone, boxes, walls, bodies, rk4, grid;
     int models;  // 0 holonomic, 1 diff/bicycle mix, 3 drone
+    bool per_env = false;  // per-env parameter rows (the body pass then reads the shared)
 };
 
 template <typename T>
@@ -102,6 +103,17 @@ int run_case(const Case &c)
         mode[a] = 0;
     }
     d.params = params;
+    if (c.per_env) {
+        T *rows = make<T>(EA * 22, own);
+        for (size_t q = 0; q < EA; ++q) {
+            memcpy(rows + q * 22, params + (q % A) * 22, sizeof(T) * 22);
+            rows[q * 22] = T(0.04 + 0.01 * (double)(q % 3));     // radius
+            rows[q * 22 + 1] = T(1.0 + 0.5 * (double)(q % 2));  // mass
+        }
+        d.params = rows;
+        d.params_per_env = 1;
+        d.body_params = params;
+    }
     d.model_tag = tag;
     d.ctrl_mode = mode;
     const int N = c.nobs;
@@ -225,6 +237,8 @@ int main(int argc, char **argv)
         // name                 E   A   T  S  K  ad N  drone  boxes  walls  bodies rk4   grid   models
         {"bodies f32 A=12",      5, 12, 4, 2, 8, 2, 5, false, false, true,  true,  false, false, 0},
         {"bodies f32 A=64",      2, 64, 3, 2, 16, 2, 5, false, false, true,  true,  false, false, 0},
+        {"bodies drones f32 A=8", 9, 8, 3, 2, 8, 4, 5, true,  false, true,  true,  false, false, 3},
+        {"bodies per-env f32",   6, 12, 3, 2, 8, 2, 5, false, false, true,  true,  false, false, 0, true},
         {"drones f32 64x8",     16, 8, 6, 2, 8, 4, 0, true,  false, false, false, false, false, 3},
         {"drones f64 A=3",       4, 3, 5, 1, 4, 4, 0, true,  false, false, false, false, false, 3},
         {"mixed f32 obstacles",  9, 32, 4, 2, 16, 2, 6, false, false, true,  false, false, false, 1},

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from cases import nav_agents, obstacles_np, oracle_cfg, params_of
+from cases import body_seed_np, nav_agents, obstacles_np, oracle_cfg, params_of
 from hip_helpers import make_stepper, rel, state_to16, to_torch_state
 from oracle.oracle import Oracle, pack_state
 from swarp_amd import rollout
@@ -210,3 +210,141 @@ def test_grad_and_nograd_forward_agree_and_state_advances():
     f2, _ = rollout(st, to_torch_state(s0, torch.float32, True, 5), a.clone().requires_grad_(True))
     assert torch.equal(f1.pos, f2.pos.detach()) and torch.equal(ob1, st.ob_state.detach())
     assert not torch.equal(ob1, ob0), "the obstacle state did not advance"
+
+
+def _run_fields(cfgs, world, dt, S, s0, acts, obs, np_dtype, seed=0, per_env=None):
+    """run_pair for any fleet: every stepped field (nine with drones) enters the loss and
+    the comparison; `per_env` ([E, A, 22]) installs per-env agent rows, and the oracle then
+    runs each env on its own rows with the shared table as the body pass's rows."""
+    from hip_helpers import FIELDS
+    from oracle.oracle import OFFSET, WIDTH
+    E, A = s0.shape[:2]
+    T = acts.shape[0]
+    td = TDT[np_dtype]
+    nf = 9 if any(int(c.model) == 3 for c in cfgs) else 5
+    st = make_stepper(cfgs, world, dt, S, td, obs=obs, n_envs=E)
+    if per_env is not None:
+        st.set_agent_params_per_env(torch.tensor(per_env, dtype=td))
+    ob0 = st.ob_state.detach().clone().requires_grad_(True)
+    st.ob_state = ob0
+    rng = np.random.default_rng(seed)
+    w_st = rng.normal(size=(T, E, A, 16))
+    if nf == 5:
+        w_st[..., 7:] = 0.0
+    w_ob = rng.normal(size=(T,) + tuple(ob0.shape))
+    s0t = to_torch_state(s0, td, True, nf)
+    a = torch.tensor(acts, dtype=td, device="cuda", requires_grad=True)
+    final, traj = rollout(st, s0t, a)
+    obtr = st.ob_trajectory
+    loss = (torch.tensor(w_ob, dtype=td, device="cuda") * obtr).sum()
+    wt = torch.tensor(w_st, dtype=td, device="cuda")
+    for t in range(T):
+        for k, (name, w, o) in enumerate(zip(FIELDS, WIDTH, OFFSET)):
+            if k >= nf:
+                continue
+            ww = wt[t, ..., o:o + w]
+            loss = loss + ((ww[..., 0] if w == 1 else ww) * getattr(traj[t], name)).sum()
+    loss.backward()
+    g0 = np.zeros((E, A, 16))
+    for k, (name, w, o) in enumerate(zip(FIELDS, WIDTH, OFFSET)):
+        if k < nf and getattr(s0t, name).grad is not None:
+            g0[..., o:o + w] = getattr(s0t, name).grad.double().cpu().numpy().reshape(E, A, w)
+    hip = (np.stack([state_to16(x) for x in traj]), obtr.detach().double().cpu().numpy(), g0,
+           ob0.grad.double().cpu().numpy(), a.grad.double().cpu().numpy())
+    O = Oracle(np_dtype)
+    p, t_, m = params_of(cfgs)
+    ob = obstacles_np(obs, E)
+    ob0n = ob0.detach().cpu().numpy().astype(np_dtype)
+    s0n, actn = s0.astype(np_dtype), acts.astype(np_dtype)
+    if per_env is None:
+        groups = [(slice(0, E), p, ob)]
+    else:
+        groups = []
+        for e in range(E):
+            obe = {k: (v[e:e + 1] if k in ("pos", "angle", "vel", "ang_vel") else v)
+                   for k, v in ob.items()}
+            obe["body_params"] = p
+            groups.append((slice(e, e + 1), per_env[e], obe))
+    ost = np.zeros((T, E, A, 16))
+    oob = np.zeros((T,) + tuple(ob0.shape))
+    og0, ogob, oga = np.zeros((E, A, 16)), np.zeros(tuple(ob0.shape)), np.zeros(acts.shape)
+    for sl, pe, obe in groups:
+        n = sl.stop - sl.start
+        cfg = oracle_cfg(cfgs, world, dt, S, n, acts.shape[-1], n_threads=8)
+        s_, o_ = O.rollout_ob(cfg, pe, t_, m, obe, s0n[sl], ob0n[sl], actn[:, sl])
+        g0_, gob_, ga_ = O.rollout_adj_ob(cfg, pe, t_, m, obe, s0n[sl], ob0n[sl], actn[:, sl],
+                                          s_, o_, w_st[:, sl], None, w_ob[:, sl], None)
+        ost[:, sl], oob[:, sl], og0[sl], ogob[sl], oga[:, sl] = s_, o_, g0_, gob_, ga_
+    cols = slice(0, 16) if nf == 9 else slice(0, 7)
+    return hip, (ost, oob, og0, ogob, oga), cols
+
+
+def _check_fields(name, hip, orc, cols, exact=True, g_tol=1e-5):
+    hs, hob, hg0, hgob, hga = hip
+    os_, oob, og0, ogob, oga = orc
+    print(f"\n{name}: states rel {rel(hs[..., cols], os_[..., cols]):.2e}, ob rel {rel(hob, oob):.2e}, "
+          f"d/d actions {rel(hga, oga):.2e}, d/d state0 {rel(hg0[..., cols], og0[..., cols]):.2e}, "
+          f"d/d ob0 {rel(hgob, ogob):.2e}")
+    if exact:
+        assert np.array_equal(hs[..., cols], os_[..., cols]), (
+            f"{name}: agent states not bit-exact (rel {rel(hs[..., cols], os_[..., cols]):.2e})")
+        assert np.array_equal(hob, oob), f"{name}: obstacle states not bit-exact (rel {rel(hob, oob):.2e})"
+    else:
+        assert rel(hs[..., cols], os_[..., cols]) <= 1e-12 and rel(hob, oob) <= 1e-12, name
+    assert rel(hga, oga) <= g_tol, f"{name}: d/d actions rel {rel(hga, oga):.3e}"
+    assert rel(hg0[..., cols], og0[..., cols]) <= g_tol, f"{name}: d/d state0 rel {rel(hg0, og0):.3e}"
+    assert rel(hgob, ogob) <= g_tol, f"{name}: d/d ob0 rel {rel(hgob, ogob):.3e}"
+
+
+@pytest.mark.parametrize("np_dtype", [np.float32, np.float64])
+def test_bodies_with_drones(np_dtype):
+    """A drone fleet (config 4's quadrotors) flying into the cross body and a second
+    movable circle: every one of the nine state fields and the obstacle states bit-exact,
+    gradients 1e-5 (fp32) / 1e-12 (fp64) of the oracle."""
+    from swarp_amd.config import AgentConfig, DynamicsModel
+    E, A, T = 24, 8, 10
+    rng = np.random.default_rng(11)
+    cfgs = [AgentConfig(model=DynamicsModel.DRONE, radius=0.1, thrust_max=10.0) for _ in range(A)]
+    pos = rng.uniform(-0.7, 0.7, size=(E, A, 2))
+    vel = -0.6 * pos / np.linalg.norm(pos, axis=-1, keepdims=True)
+    ax = rng.normal(size=(E, A, 3))
+    ax /= np.linalg.norm(ax, axis=-1, keepdims=True)
+    ang = rng.uniform(0, 0.1, size=(E, A, 1))
+    q = np.concatenate([ax * np.sin(ang / 2), np.cos(ang / 2)], -1)
+    s0 = pack_state({"pos": pos, "vel": vel, "z": np.ones((E, A)), "attitude": q})
+    acts = rng.uniform(0, 1, size=(T, E, A, 4)) * 10.0
+    obs = cross_obs(E, (0.0, 0.0), extra=(((0.5, 0.2), 0.12, True),))
+    hip, orc, cols = _run_fields(cfgs, _world(), 0.02, 2, s0, acts, obs, np_dtype, seed=3)
+    _check_fields("drones", hip, orc, cols, exact=True, g_tol=1e-5 if np_dtype == np.float32 else 1e-12)
+    assert np.abs(orc[1][-1, :, 6 * 5 + 3:6 * 5 + 5]).max() > 1e-3, "the drones never pushed the cross"
+
+
+def test_bodies_with_per_env_parameter_rows():
+    """Per-env agent rows (Stepper.set_agent_params_per_env) with a movable body: the
+    agents step on their env's rows and the body pass reads the shared table, as the
+    reference's launch_obstacle_dynamics does (swarp/core/stepper.py:961-964).  Each env
+    equals an independent oracle rollout with its rows; the body states would differ if
+    the body pass read the per-env rows."""
+    from swarp_amd import per_env_float_template
+    E, A = 12, 8
+    s0, acts = _pushers(E, A, 12, spread=0.5)
+    cfgs = nav_agents(A)
+    rows = np.array(per_env_float_template(cfgs, E), dtype=np.float64)
+    rng = np.random.default_rng(13)
+    rows[..., 0] = rng.uniform(0.04, 0.08, size=(E, A))   # radius
+    rows[..., 1] = rng.uniform(0.5, 2.0, size=(E, A))     # mass
+    obs = cross_obs(E, (0.0, 0.0))
+    hip, orc, cols = _run_fields(cfgs, _world(), 0.05, 4, s0, acts, obs, np.float32, seed=4,
+                                 per_env=rows)
+    _check_fields("per-env", hip, orc, cols)
+    # the same rollout with the body pass on the per-env rows moves the body differently
+    O = Oracle(np.float32)
+    ob = obstacles_np(obs, E)
+    e = 0
+    obe = {k: (v[e:e + 1] if k in ("pos", "angle", "vel", "ang_vel") else v) for k, v in ob.items()}
+    p, t_, m = params_of(cfgs)
+    cfg = oracle_cfg(cfgs, _world(), 0.05, 4, 1, 2, n_threads=1)
+    _, o_own = O.rollout_ob(cfg, rows[e].astype(np.float32), t_, m, obe,
+                            s0[e:e + 1].astype(np.float32), body_seed_np(obe).astype(np.float32),
+                            acts[:, e:e + 1].astype(np.float32))
+    assert not np.array_equal(o_own, orc[1][:, e:e + 1]), "the test cannot tell the tables apart"

@@ -71,6 +71,21 @@ def test_library_rejects_bad_descriptor_without_gpu():
     d.n_envs, d.n_agents, d.act_dim, d.substeps = 1, 1025, 2, 1
     rc = lib.swarp_rollout_fwd(ctypes.byref(d), 1, ctypes.byref(s), None, None, ctypes.byref(s), None)
     assert rc != 0 and b"n_agents" in lib.swarp_last_error()
+    # per-env agent rows with moving bodies need the shared table for the body pass
+    from swarp_amd import per_env_float_template
+    cfgs = [AgentConfig(radius=0.05)]
+    st = Stepper(cfgs, device="cpu", world=WorldConfig(neighbor_radius=0.3))
+    st.set_obstacles(Obstacles(pos=torch.zeros(1, 1, 2), radius=torch.ones(1),
+                               kind=torch.ones(1, dtype=torch.int32)))
+    st.set_agent_params_per_env(per_env_float_template(cfgs, 1))
+    d = st.desc(1, 2)
+    d.body_params = None
+    rc = lib.swarp_rollout_fwd_ob(ctypes.byref(d), 1, ctypes.byref(s), None, None, None,
+                                  ctypes.byref(s), None, None)
+    assert rc != 0
+    rc = lib.swarp_rollout_fwd_ob(ctypes.byref(d), 1, ctypes.byref(s), 1, 1, None,
+                                  ctypes.byref(s), 1, None)
+    assert rc != 0 and b"body_params" in lib.swarp_last_error()
 
 
 def test_tape_size_without_gpu():
@@ -211,10 +226,11 @@ def test_stepper_reach_check_and_unsupported_features():
         st.set_obstacles(Obstacles(pos=torch.zeros(1, 1, 2), radius=torch.ones(1),
                                    shape=torch.ones(1, dtype=torch.int32),
                                    kind=torch.ones(1, dtype=torch.int32)))
-    with pytest.raises(NotImplementedError, match="DRONE"):
-        Stepper([drone_config()], device="cpu").set_obstacles(
-            Obstacles(pos=torch.zeros(1, 1, 2), radius=torch.ones(1),
-                      kind=torch.ones(1, dtype=torch.int32)))
+    # drone fleets push bodies by their planar state (the body kernels' DRONE instances)
+    dr = Stepper([drone_config()], device="cpu")
+    dr.set_obstacles(Obstacles(pos=torch.zeros(1, 1, 2), radius=torch.ones(1),
+                               kind=torch.ones(1, dtype=torch.int32)))
+    assert dr.any_movable and dr.ob_state.shape == (1, 12)
 
 
 def test_desc_fleet_models_and_modes():
@@ -403,6 +419,8 @@ def test_per_env_params_validation():
     st.set_agent_params_per_env(tab)
     d = st.desc(3, 2)
     assert d.params_per_env == 1 and d.params == st.params_per_env.data_ptr()
+    # the body pass reads the shared rows (swarp/core/stepper.py:961-964)
+    assert d.body_params == st.params.floats.data_ptr()
     with pytest.raises(ValueError, match="installed for 3 envs"):
         st.desc(4, 2)
     with pytest.raises(ValueError, match="shape"):

@@ -246,3 +246,63 @@ def test_body_adjoint_matches_finite_differences():
     acts = 0.5 * rng.normal(size=(3, 1, 3, 2))
     st, obo = _fd_bodies(cfgs, world, 0.05, 2, s0, acts, ob)
     assert np.abs(obo[-1, 0, 30 + 5]) > 1e-4, "the compound body never turned"
+
+
+def test_body_pass_reads_its_own_parameter_rows():
+    """With per-env agent rows the reference's body pass still reads the shared table
+    (swarp/core/stepper.py:961-964): the body's reaction uses that table's radius and mass,
+    while the agent's own force (and so its step) uses the agent's row."""
+    world = _world(collision_k=100.0, collision_c=1.0, collision_margin=0.02)
+    cfgs = _agents(1, radius=0.1)
+    ob = _circles(1, [[0.15, 0.0]], 0.1, [MOVABLE], mass=[2.0], inertia=[0.3])
+    s0 = pack_state({"pos": [[[0.0, 0.0]]], "vel": [[[0.3, 0.0]]]})
+    acts = np.array([[[[0.3, 0.0]]]])
+    dt = 0.01
+    cfg = oracle_cfg(cfgs, world, dt, 1, 1, 2)
+    p, t, m = params_of(cfgs)
+    shared = p.copy()
+    shared[0, 0], shared[0, 1] = 0.12, 3.0  # the body pass's radius and mass
+    ob_b = dict(ob, body_params=shared)
+    st_a, obo_a = O.rollout_ob(cfg, p, t, m, ob, s0, body_seed_np(ob), acts)
+    st_b, obo_b = O.rollout_ob(cfg, p, t, m, ob_b, s0, body_seed_np(ob), acts)
+    np.testing.assert_array_equal(st_a, st_b)  # the agent side reads its own row
+    dd = 1.0 + 1.0 * dt / 3.0
+    R = -_pair_force(np.array([-0.15, 0.0]), np.array([0.3, 0.0]), 0.24, 100.0, 1.0, dd)
+    v = (R / 2.0 * dt) * (1.0 - 10.0 * dt)
+    assert obo_b[0, 0, 6 + 3] == pytest.approx(v[0], rel=1e-14)
+    assert obo_b[0, 0, 6 + 3] != obo_a[0, 0, 6 + 3]
+    # the same table as the agents' rows changes nothing
+    _, obo_c = O.rollout_ob(cfg, p, t, m, dict(ob, body_params=p), s0, body_seed_np(ob), acts)
+    np.testing.assert_array_equal(obo_c, obo_a)
+
+
+def test_drone_fleet_pushes_a_body():
+    """Drones take part in the body pass by their planar position and velocity (the disc
+    variant reads pos / vel only, swarp/core/bodies.py:384-393): a drone flying into a
+    circle body pushes it, and the body's adjoint matches finite differences."""
+    world = _world(collision_k=100.0, collision_c=1.0, collision_margin=0.02)
+    cfgs = [AgentConfig(model=DynamicsModel.DRONE, radius=0.1, thrust_max=10.0)]
+    ob = _circles(1, [[0.17, 0.0]], 0.1, [MOVABLE], mass=[2.0], inertia=[0.3])
+    s0 = pack_state({"pos": [[[0.0, 0.0]]], "vel": [[[0.5, 0.05]]], "z": [[1.0]]})
+    acts = np.full((6, 1, 1, 4), 2.5)
+    st, obo = _run(cfgs, world, 0.02, 2, s0, acts, ob)
+    assert obo[-1, 0, 6 + 3] > 1e-3, "the drone never pushed the body"
+    cfg = oracle_cfg(cfgs, world, 0.02, 2, 1, 4)
+    p, t, m = params_of(cfgs)
+    b0 = body_seed_np(ob)
+    rng = np.random.default_rng(3)
+    w_st = rng.normal(size=st.shape)
+    w_ob = rng.normal(size=obo.shape)
+    _, _, ga = O.rollout_adj_ob(cfg, p, t, m, ob, s0, b0, acts, st, obo, w_st, None, w_ob, None)
+
+    def loss(a):
+        s, o = O.rollout_ob(cfg, p, t, m, ob, s0, b0, a)
+        return float((w_st * s).sum() + (w_ob * o).sum())
+
+    h = 1e-6
+    for idx in [(0, 0, 0, 0), (2, 0, 0, 1), (4, 0, 0, 3), (5, 0, 0, 2)]:
+        ap, am = acts.copy(), acts.copy()
+        ap[idx] += h
+        am[idx] -= h
+        fd = (loss(ap) - loss(am)) / (2 * h)
+        assert ga[idx] == pytest.approx(fd, rel=2e-6, abs=1e-9)
