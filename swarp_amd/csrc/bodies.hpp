@@ -38,6 +38,7 @@ template <typename T> struct ObTab {
     const SWARP_RO T *bprm;
     T lin_damp, ang_damp;
     int N;
+    int cache;   // backward: 1 keeps each substep's body cos / sin and contact sums in LDS
 };
 
 // Obstacle-state inputs / outputs of a rollout.
@@ -269,30 +270,64 @@ template <int PA> __device__ __forceinline__ typename MaskT<PA>::type env_ballot
 // bodies_env (the oracle's restatement of obstacle_dynamics_kernel).
 template <typename T> struct BodyNew {
     T qx, qy, th, tvx, tvy, om, ca, sa;   // input pose (with its sin / cos)
-    T fx, fy, tau, ext;                   // contact sum
+    T fx, fy, tau, ext;                   // contact sum; static extent of the body
     T nx, ny, nth, nvx, nvy, nom, nca, nsa;
     bool clx, cly;
 };
 
-// The body pass of one env for movable body root o: every lane of the env computes the
-// same values (agent contributions reach all of them by readlane, env_ordered_sums).  Agent state of
-// the lane in `st`; `od` = the env's obstacle state at the substep input.
-template <typename T, int PA>
-__device__ __forceinline__ void body_step(const Cst<T> &C, const ObTab<T> &tb,
-                                          const Lane<T, PA> &L, const BodyRow<T> &br,
-                                          const St<T> &st, const T *od, int o, BodyNew<T> &B)
+// Farthest point of body root o's shapes from the body origin (circles: |offset| +
+// radius; bodies.py:449-459): it depends on the installed tables only, so the kernels
+// evaluate it once per launch.
+template <typename T> __device__ __forceinline__ T body_ext(const ObTab<T> &tb, int o)
 {
-    typedef typename MaskT<PA>::type M;
-    const int N = tb.N;
-    const T *b = od + 6 * N + 6 * o;
+    T ext = T(0);
+    for (int s = 0; s < tb.N; ++s) {
+        if (tb.body[s] != o) continue;
+        const T ax = m_abs(tb.off[2 * s]), ay = m_abs(tb.off[2 * s + 1]);
+        ext = wmax(ext, m_sqrt(ax * ax + ay * ay) + tb.rad[s]);
+    }
+    return ext;
+}
+
+// Per-launch / per-step LDS of the body pass of one env slot:
+//   ext[o]                    static extent of body root o (body_ext)
+//   cs[2o], cs[2o+1]          cos, sin of body o's angle in the obstacle state they
+//                             accompany (one array per obstacle-state buffer)
+//   sums[3o .. 3o+2]          fx, fy, tau of body o's contact sum (backward only, per substep)
+// The sin / cos of a substep's output angle are those of the next substep's input angle,
+// so each angle is evaluated once.
+
+// Input pose of body root o from the env's obstacle state `od`, with its cos / sin (from
+// `cs`, or evaluated when cs is NULL).
+template <typename T>
+__device__ __forceinline__ void body_load(const ObTab<T> &tb, const T *od, const T *cs, int o,
+                                          BodyNew<T> &B)
+{
+    const T *b = od + 6 * tb.N + 6 * o;
     B.qx = b[0];
     B.qy = b[1];
     B.th = b[2];
     B.tvx = b[3];
     B.tvy = b[4];
     B.om = b[5];
-    psincos(B.th, B.sa, B.ca);
-    T fx = T(0), fy = T(0), tau = T(0), ext = T(0);
+    if (cs) {
+        B.ca = cs[2 * o];
+        B.sa = cs[2 * o + 1];
+    } else {
+        psincos(B.th, B.sa, B.ca);
+    }
+}
+
+// Contact sum of movable body root o: every lane of the env computes the same values
+// (agent contributions reach all of them by readlane, env_ordered_sums).  Agent state of
+// the lane in `st`; `od` = the env's obstacle state at the substep input.
+template <typename T, int PA>
+__device__ __forceinline__ void body_sum(const Cst<T> &C, const ObTab<T> &tb,
+                                         const Lane<T, PA> &L, const BodyRow<T> &br,
+                                         const St<T> &st, const T *od, int o, BodyNew<T> &B)
+{
+    const int N = tb.N;
+    T fx = T(0), fy = T(0), tau = T(0);
     const T mo = tb.mass[o];
     const T denom_self = T(1) + C.c * C.sub_dt / mo;
     for (int s = 0; s < N; ++s) {
@@ -303,9 +338,6 @@ __device__ __forceinline__ void body_step(const Cst<T> &C, const ObTab<T> &tb,
         const T csx = B.qx + owx, csy = B.qy + owy;
         const T vsx = B.tvx - B.om * owy, vsy = B.tvy + B.om * owx;
         const T ro = tb.rad[s];
-        const T ax = m_abs(offx), ay = m_abs(offy);
-        const T reach = m_sqrt(ax * ax + ay * ay) + ro;
-        ext = wmax(ext, reach);
         // the agents' reactions, in agent order
         T f0 = T(0), f1 = T(0), tq = T(0);
         if (L.active && !b_apart(st.px - csx, st.py - csy, br.r + ro + C.margin)) {
@@ -343,14 +375,21 @@ __device__ __forceinline__ void body_step(const Cst<T> &C, const ObTab<T> &tb,
     B.fx = fx;
     B.fy = fy;
     B.tau = tau;
-    B.ext = ext;
+}
+
+// Integration of body root o from its contact sum (B.fx, fy, tau, ext and the input pose
+// set): the new pose and velocity, with the clamp; not the new angle's sin / cos.
+template <typename T>
+__device__ __forceinline__ void body_advance(const Cst<T> &C, const ObTab<T> &tb, int o,
+                                             BodyNew<T> &B)
+{
     const T sdt = C.sub_dt, one = T(1);
     const T lin_decay = one - tb.lin_damp * sdt;
     const T ang_decay = one - tb.ang_damp * sdt;
-    const T I = tb.inertia[o];
-    T nvx = (B.tvx + fx / mo * sdt) * lin_decay;
-    T nvy = (B.tvy + fy / mo * sdt) * lin_decay;
-    const T nom = (B.om + tau / I * sdt) * ang_decay;
+    const T mo = tb.mass[o], I = tb.inertia[o], ext = B.ext;
+    T nvx = (B.tvx + B.fx / mo * sdt) * lin_decay;
+    T nvy = (B.tvy + B.fy / mo * sdt) * lin_decay;
+    const T nom = (B.om + B.tau / I * sdt) * ang_decay;
     T nx = B.qx + nvx * sdt;
     T ny = B.qy + nvy * sdt;
     B.clx = B.cly = false;
@@ -376,22 +415,43 @@ __device__ __forceinline__ void body_step(const Cst<T> &C, const ObTab<T> &tb,
     B.nvy = nvy;
     B.nom = nom;
     B.nth = B.th + nom * sdt;
-    psincos(B.nth, B.nsa, B.nca);
+}
+
+// cos / sin of the angle of every movable body root in the obstacle state `od`.  Lane
+// `agent` of the env fills roots agent, agent + PA, ...
+template <typename T, int PA>
+__device__ __forceinline__ void body_trig(const ObTab<T> &tb, const Lane<T, PA> &L, const T *od,
+                                          T *cs)
+{
+    for (int o = L.agent; o < tb.N; o += PA) {
+        if (tb.body[o] != o || tb.kind[o] != 1) continue;
+        T s, c;
+        psincos(od[6 * tb.N + 6 * o + 2], s, c);
+        cs[2 * o] = c;
+        cs[2 * o + 1] = s;
+    }
 }
 
 // The body pass of one env: obn = obc with every movable body advanced and its shapes
-// re-installed at the new pose.  Lane `agent` of the env copies entries agent, agent+PA...
+// re-installed at the new pose; cs_out = the new angles' cos / sin (cs_in: the input
+// angles'; both NULL when not kept); sums (nullable) receives each body's contact sum.
+// Lane `agent` of the env copies entries agent, agent+PA...
 template <typename T, int PA>
 __device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
                                           const Lane<T, PA> &L, const BodyRow<T> &br,
-                                          const St<T> &st, const T *obc, T *obn)
+                                          const St<T> &st, const T *obc, T *obn, const T *ext,
+                                          const T *cs_in, T *cs_out, T *sums)
 {
     const int N = tb.N;
     for (int q = L.agent; q < OB_W * N; q += PA) obn[q] = obc[q];
     for (int o = 0; o < N; ++o) {
         if (tb.body[o] != o || tb.kind[o] != 1) continue;
         BodyNew<T> B;
-        body_step<T, PA>(C, tb, L, br, st, obc, o, B);
+        body_load(tb, obc, cs_in, o, B);
+        B.ext = ext[o];
+        body_sum<T, PA>(C, tb, L, br, st, obc, o, B);
+        body_advance(C, tb, o, B);
+        psincos(B.nth, B.nsa, B.nca);
         if (L.agent == 0) {
             T *bo = obn + 6 * N + 6 * o;
             bo[0] = B.nx;
@@ -400,6 +460,15 @@ __device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
             bo[3] = B.nvx;
             bo[4] = B.nvy;
             bo[5] = B.nom;
+            if (cs_out) {
+                cs_out[2 * o] = B.nca;
+                cs_out[2 * o + 1] = B.nsa;
+            }
+            if (sums) {
+                sums[3 * o] = B.fx;
+                sums[3 * o + 1] = B.fy;
+                sums[3 * o + 2] = B.tau;
+            }
             for (int s = 0; s < N; ++s) {
                 if (tb.body[s] != o) continue;
                 const T offx = tb.off[2 * s], offy = tb.off[2 * s + 1];
@@ -443,6 +512,8 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
     __shared__ T sl[4 * 64];                         // px py vx vy of the substep
     __shared__ T lr[64];                             // agent radius per lane
     __shared__ T lob[2][EPW][OB_W * NOB_MAX];        // obstacle state: in / out of a substep
+    __shared__ T lcs[2][EPW][2 * NOB_MAX];           // its bodies' cos / sin (body_pass)
+    __shared__ T lext[NOB_MAX];                      // static extent per body root
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
     fold_prm<F>(L.pr);
@@ -453,6 +524,9 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
     const bool env_ok = L.env < C.E;
     const size_t eo = (size_t)(env_ok ? L.env : 0) * NW;
     for (int q = L.agent; q < NW; q += PA) lob[0][ew][q] = io.ob0[eo + q];
+    for (int o = L.lane; o < tb.N; o += 64) lext[o] = body_ext(tb, o);
+    __syncthreads();
+    body_trig<T, PA>(tb, L, lob[0][ew], lcs[0][ew]);
     St<T> st;
     load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
     if (!L.active) st.px = st.py = __builtin_nan("");
@@ -474,7 +548,8 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
             const T *obc = lob[cur][ew];
             T Fx, Fy;
             forces_b<T, PA>(C, tb, L, sl, lr, obc, st, s, s == 0 || !ok, cand, Fx, Fy);
-            body_pass<T, PA>(C, tb, L, br, st, obc, lob[cur ^ 1][ew]);
+            body_pass<T, PA>(C, tb, L, br, st, obc, lob[cur ^ 1][ew], lext, lcs[cur][ew],
+                             lcs[cur ^ 1][ew], nullptr);
             St<T> nx;
             integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
             if (C.use_skin) {
@@ -500,25 +575,31 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
 
 // Dynamic LDS of k_body_bwd (host and device agree on this layout).
 template <typename T, int PA, bool DRONE>
-__host__ __device__ constexpr size_t body_bwd_lds(int S, int N)
+__host__ __device__ constexpr size_t body_bwd_lds(int S, int N, bool cache)
 {
     typedef typename MaskT<PA>::type M;
     return 2 * 64 * sizeof(T)                               // radius, damping divisor
            + (size_t)S * (DRONE ? NF_DRONE : NF_2D) * 64 * sizeof(T)  // substep agent slots
            + (size_t)S * 64 * sizeof(M)                     // inclusion masks
            + (size_t)(S + 1) * (64 / PA) * OB_W * N * sizeof(T)  // obstacle state per substep
-           + 2 * (size_t)(64 / PA) * OB_W * N * sizeof(T);       // obstacle adjoint in / out
+           + 2 * (size_t)(64 / PA) * OB_W * N * sizeof(T)        // obstacle adjoint in / out
+           + (cache ? (size_t)(S + 1) * (64 / PA) * 2 * N * sizeof(T)   // body cos / sin
+                          + (size_t)S * (64 / PA) * 3 * N * sizeof(T)   // body contact sums
+                    : 0);
 }
 
 // Reverse of body_pass for one env.  gout = adjoint of the pass's output (the env's
 // obstacle state after the substep), gin receives the adjoint of its input (overwritten);
-// the lane's agent adjoint is accumulated into `ga`.  Same order of terms as the oracle's
-// bodies_env_adj.
+// the lane's agent adjoint is accumulated into `ga`.  ext / cs_in / cs_out / sums are what
+// the forward body_pass of this substep read and wrote: each body's new state is rebuilt
+// from its recorded contact sum, not summed again (NULL cs / sums: recomputed).  Same
+// order of terms as the oracle's bodies_env_adj.
 template <typename T, int PA>
 __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &tb,
                                               const Lane<T, PA> &L, const BodyRow<T> &br,
                                               const St<T> &st, const T *obc, const T *gout,
-                                              T *gin, St<T> &ga)
+                                              T *gin, St<T> &ga, const T *ext, const T *cs_in,
+                                              const T *cs_out, const T *sums)
 {
     typedef typename MaskT<PA>::type M;
     const int N = tb.N;
@@ -531,7 +612,22 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
     for (int o = 0; o < N; ++o) {
         if (tb.body[o] != o || tb.kind[o] != 1) continue;
         BodyNew<T> B;
-        body_step<T, PA>(C, tb, L, br, st, obc, o, B);
+        body_load(tb, obc, cs_in, o, B);
+        B.ext = ext[o];
+        if (sums) {
+            B.fx = sums[3 * o];
+            B.fy = sums[3 * o + 1];
+            B.tau = sums[3 * o + 2];
+        } else {
+            body_sum<T, PA>(C, tb, L, br, st, obc, o, B);
+        }
+        body_advance(C, tb, o, B);
+        if (cs_out) {
+            B.nca = cs_out[2 * o];
+            B.nsa = cs_out[2 * o + 1];
+        } else {
+            psincos(B.nth, B.nsa, B.nca);
+        }
         const T sdt = C.sub_dt, one = T(1);
         const T lin_decay = one - tb.lin_damp * sdt;
         const T ang_decay = one - tb.ang_damp * sdt;
@@ -667,6 +763,11 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
     M *lmask = (M *)(slots + (size_t)C.S * NF * 64);     // S inclusion masks
     T *lobs = (T *)(lmask + (size_t)C.S * 64);           // [S+1][EPW][NW] obstacle states
     T *lgob = lobs + (size_t)(C.S + 1) * EPW * NW;       // [2][EPW][NW] obstacle adjoints
+    // with tb.cache: [S+1][EPW][2N] body cos / sin, [S][EPW][3N] body contact sums
+    T *lcs = tb.cache ? lgob + (size_t)2 * EPW * NW : nullptr;
+    T *lsum = tb.cache ? lcs + (size_t)(C.S + 1) * EPW * 2 * N : nullptr;
+    __shared__ T lext[NOB_MAX];                          // static extent per body root
+    for (int o = threadIdx.x; o < N; o += 64) lext[o] = body_ext(tb, o);
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
     fold_prm<F>(L.pr);
@@ -700,6 +801,8 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             const T *src = t == 0 ? io.ob0 + eo : io.traj + (size_t)(t - 1) * ENW + eo;
             T *dst = lobs + (size_t)ew * NW;
             for (int q = L.agent; q < NW; q += PA) dst[q] = src[q];
+            __syncthreads();
+            if (lcs) body_trig<T, PA>(tb, L, dst, lcs + (size_t)ew * 2 * N);
         }
         T a[4];
         load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
@@ -719,7 +822,10 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             sl[F_FX * 64 + L.lane] = Fx;
             sl[F_FY * 64 + L.lane] = Fy;
             lmask[s * 64 + L.lane] = incl;
-            body_pass<T, PA>(C, tb, L, br, st, obc, lobs + ((size_t)(s + 1) * EPW + ew) * NW);
+            body_pass<T, PA>(C, tb, L, br, st, obc, lobs + ((size_t)(s + 1) * EPW + ew) * NW, lext,
+                             lcs ? lcs + ((size_t)s * EPW + ew) * 2 * N : nullptr,
+                             lcs ? lcs + ((size_t)(s + 1) * EPW + ew) * 2 * N : nullptr,
+                             lsum ? lsum + ((size_t)s * EPW + ew) * 3 * N : nullptr);
             St<T> nx;
             integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
             if (C.use_skin) {
@@ -742,7 +848,10 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             T gFx, gFy;
             integrate_adj<T, DRONE>(C, L.pr, in, a, Fx, Fy, gs, gi, ga, gFx, gFy);
             // the body pass: adjoint of its input obstacle state into gprev
-            body_pass_adj<T, PA>(C, tb, L, br, in, obc, gob, gprev, gi);
+            body_pass_adj<T, PA>(C, tb, L, br, in, obc, gob, gprev, gi, lext,
+                                 lcs ? lcs + ((size_t)s * EPW + ew) * 2 * N : nullptr,
+                                 lcs ? lcs + ((size_t)(s + 1) * EPW + ew) * 2 * N : nullptr,
+                                 lsum ? lsum + ((size_t)s * EPW + ew) * 3 * N : nullptr);
             if (C.needs_forces) {
                 const T wFx = gFx * L.inv_dd, wFy = gFy * L.inv_dd;
                 __syncthreads();
@@ -776,15 +885,14 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
                         ob_force_adj(C, tb, obc, o, in.px, in.py, in.vx, in.vy, L.pr.radius,
                                      L.dd, gFx, gFy, gi, opx, opy, ovx, ovy);
                     if (!shape_moves(tb, o)) continue;
+                    const bool fl = opx != T(0) || opy != T(0) || ovx != T(0) || ovy != T(0);
+                    if (__ballot(fl) == 0) continue;  // no agent of the wave touches it
                     // the env's agent-0 lane keeps the shape's adjoint; the other lanes'
                     // copies of the sums are not used
                     T *g2 = gprev + 6 * o;
                     T acc[4] = {g2[0], g2[1], g2[3], g2[4]};
                     const T val[4] = {opx, opy, ovx, ovy};
-                    env_ordered_sums<PA, 4>(acc, val,
-                                            opx != T(0) || opy != T(0) || ovx != T(0) ||
-                                                ovy != T(0),
-                                            L.lane);
+                    env_ordered_sums<PA, 4>(acc, val, fl, L.lane);
                     if (L.agent == 0) {
                         g2[0] = acc[0];
                         g2[1] = acc[1];
@@ -814,20 +922,21 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
 
 // ---------------------------------------------------------------------- launchers
 
-template <typename T, bool DRONE> size_t body_bwd_lds_pa(int PA, int S, int N)
+template <typename T, bool DRONE> size_t body_bwd_lds_pa(int PA, int S, int N, bool cache)
 {
     switch (PA) {
-    case 4: return body_bwd_lds<T, 4, DRONE>(S, N);
-    case 8: return body_bwd_lds<T, 8, DRONE>(S, N);
-    case 16: return body_bwd_lds<T, 16, DRONE>(S, N);
-    case 32: return body_bwd_lds<T, 32, DRONE>(S, N);
-    default: return body_bwd_lds<T, 64, DRONE>(S, N);
+    case 4: return body_bwd_lds<T, 4, DRONE>(S, N, cache);
+    case 8: return body_bwd_lds<T, 8, DRONE>(S, N, cache);
+    case 16: return body_bwd_lds<T, 16, DRONE>(S, N, cache);
+    case 32: return body_bwd_lds<T, 32, DRONE>(S, N, cache);
+    default: return body_bwd_lds<T, 64, DRONE>(S, N, cache);
     }
 }
 
-template <typename T> size_t body_bwd_lds_of(int PA, int S, int N, bool drone)
+template <typename T> size_t body_bwd_lds_of(int PA, int S, int N, bool drone, bool cache)
 {
-    return drone ? body_bwd_lds_pa<T, true>(PA, S, N) : body_bwd_lds_pa<T, false>(PA, S, N);
+    return drone ? body_bwd_lds_pa<T, true>(PA, S, N, cache)
+                 : body_bwd_lds_pa<T, false>(PA, S, N, cache);
 }
 
 #define SWARP_BODY_DISPATCH(KERNEL, DR, FP, SHM)                                       \

@@ -35,7 +35,7 @@
     extern template void launch_body_bwd<T>(int, const Cst<T> &, const Args<T> &,            \
                                             const ObTab<T> &, const ObIO<T> &, unsigned,     \
                                             bool, size_t, hipStream_t);                      \
-    extern template size_t body_bwd_lds_of<T>(int, int, int, bool);                          \
+    extern template size_t body_bwd_lds_of<T>(int, int, int, bool, bool);                    \
     extern template void launch_nav<T>(int, const Cst<T> &, const NavArgs<T> &, unsigned,    \
                                        hipStream_t);                                         \
     extern template void launch_neighbors<T>(int, const Cst<T> &, const T *, int32_t *,      \

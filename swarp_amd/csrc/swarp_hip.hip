@@ -432,6 +432,7 @@ template <typename T> static int fill_obtab(const swarp_desc_t *d, ObTab<T> &tb)
     tb.lin_damp = (T)d->lin_damping;
     tb.ang_damp = (T)d->ang_damping;
     tb.N = d->n_obstacles;
+    tb.cache = 0;
     return 0;
 }
 
@@ -491,7 +492,11 @@ static int rollout_bwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     a.nsteps = nT;
     ObIO<T> io = {(const T *)ob0, (T *)ob_traj, (const T *)aob_traj, (T *)aob0};
     const int PA = pad_agents(d->n_agents);
-    const size_t shm = body_bwd_lds_of<T>(PA, d->substeps, d->n_obstacles, d->has_drone != 0);
+    // the per-substep body caches (cos / sin, contact sums) when they fit
+    const bool dr = d->has_drone != 0;
+    size_t shm = body_bwd_lds_of<T>(PA, d->substeps, d->n_obstacles, dr, true);
+    tb.cache = shm <= 65536 ? 1 : 0;
+    if (!tb.cache) shm = body_bwd_lds_of<T>(PA, d->substeps, d->n_obstacles, dr, false);
     if (shm > 65536) return fail("substeps too large for the body backward's LDS staging (limit 64 KiB per wave)");
     launch_body_bwd<T>(PA, C, a, tb, io, world_features(d, true), d->has_drone != 0, shm, st);
     hipError_t e = hipGetLastError();
