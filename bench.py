@@ -250,6 +250,18 @@ def _c5(seed=0):
     return st, state, acts, goals, fwd, bwd, desc, "body"
 
 
+def event_pool(n):
+    """n timing events, each recorded once so that the device event exists before the
+    timed loop records into it (creating it there would add host time to every launch)."""
+    import torch
+
+    pool = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    for ev in pool:
+        ev.record()
+    torch.cuda.synchronize()
+    return pool
+
+
 def run_other(args):
     """Time one BPTT iteration of BASELINE configs[2..4] through the public API and print
     the same JSON line as the headline run (no CPU baseline, no Environment leg)."""
@@ -286,6 +298,7 @@ def run_other(args):
 
     for _ in range(args.warmup):
         step()
+    ag.EVENT_POOL = event_pool(2 * 2 * args.steps)
     torch.cuda.synchronize()
     gc.collect()  # the set-up's garbage: a full collection would land in the timed steps
     ag.KERNEL_EVENTS = []
@@ -294,7 +307,7 @@ def run_other(args):
         step()
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
-    events, ag.KERNEL_EVENTS = ag.KERNEL_EVENTS, None
+    events, ag.KERNEL_EVENTS, ag.EVENT_POOL = ag.KERNEL_EVENTS, None, None
     dur = {"fwd": [], "bwd": []}
     for k, e0, e1 in events:
         dur[k].append(e0.elapsed_time(e1) * 1e-3)
@@ -351,6 +364,7 @@ def main():
 
     for _ in range(args.warmup):
         bptt_step()
+    ag.EVENT_POOL = event_pool(2 * 2 * args.steps)
     torch.cuda.synchronize()
     gc.collect()  # the set-up's garbage: a full collection would land in the timed steps
     ag.KERNEL_EVENTS = []
@@ -360,7 +374,7 @@ def main():
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     events = ag.KERNEL_EVENTS
-    ag.KERNEL_EVENTS = None
+    ag.KERNEL_EVENTS = ag.EVENT_POOL = None
     dur = {"fwd": [], "bwd": []}
     for kind, e0, e1 in events:
         dur[kind].append(e0.elapsed_time(e1) * 1e-3)

@@ -40,8 +40,15 @@ FIELDS = ("pos", "theta", "vel", "speed", "ang_vel", "z", "vz", "attitude", "bod
 KERNEL_EVENTS: list | None = None
 
 
+#: timing events to record into instead of creating one per launch (a caller that times
+#: kernels fills it with events already created on the device; creating an event on the
+#: hot path costs host time that shows up in the timed loop)
+EVENT_POOL: list | None = None
+
+
 def _event(stream_tensor: torch.Tensor):
-    ev = torch.cuda.Event(enable_timing=True)
+    pool = EVENT_POOL
+    ev = pool.pop() if pool else torch.cuda.Event(enable_timing=True)
     ev.record(torch.cuda.current_stream(stream_tensor.device))
     return ev
 
