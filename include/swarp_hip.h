@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 12
+#define SWARP_ABI_VERSION 13
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -114,6 +114,10 @@ typedef struct swarp_desc {
        (swarp/core/stepper.py:961-964); the agents' own forces and integration read
        `params`.  Ignored when params_per_env = 0. */
     const void *body_params;
+    /* The obstacle shape types present as a bit set (bit t set when some obstacle's type
+       is t: 0 circle, 1 box, 2 segment); 0 reads as "any".  Lets the movable-body kernels
+       run an instance compiled without box and segment terms, so it must be truthful. */
+    int32_t obstacle_types;
 } swarp_desc_t;
 
 #define SWARP_LISTS_BRUTE 0
@@ -192,8 +196,8 @@ int swarp_rollout_bwd_tape(const swarp_desc_t *desc, int32_t T, const swarp_stat
 
 /* Rollout of a world whose obstacle state evolves: movable compound bodies integrated
  * from the agents' contact reactions inside every substep (the body pass of
- * obstacle_dynamics_kernel, swarp/core/bodies.py:367-568, disc variant: the shapes of a
- * movable body are circles; the reference runs it on untaped steps,
+ * obstacle_dynamics_kernel, swarp/core/bodies.py:367-568, disc variant: disc agents,
+ * body shapes of any type; the reference runs it on untaped steps,
  * swarp/core/stepper.py:952-991).  Replaces T calls of Stepper.launch_substeps with the
  * body pass enabled.  Fleets of any dynamics models including drones, shared or per-env
  * parameter rows (then desc->body_params), disc agents, at most 64 agents per env,

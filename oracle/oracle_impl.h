@@ -391,8 +391,11 @@ static inline void FN(obstacle_force)(const FN(ctx_t) *C, const REAL *od, int o,
     }
 }
 
-/* Reverse of obstacle_force.  `god` (nullable) receives the adjoint of a MOVABLE (circle)
-   shape's state; static obstacles are constants of the step. */
+/* Reverse of obstacle_force.  `god` (nullable) receives the adjoint of a MOVABLE shape's
+   state; static obstacles are constants of the step. */
+static void FN(obstacle_shape_adj)(const FN(ctx_t) *C, const REAL *sh, int st, REAL ro, REAL hx,
+                                   REAL hy, REAL px, REAL py, REAL vx, REAL vy, REAL ra, REAL dd,
+                                   REAL gfx, REAL gfy, REAL *g);
 static inline void FN(obstacle_force_adj)(const FN(ctx_t) *C, const REAL *od, int o, REAL px,
                                           REAL py, REAL vx, REAL vy, REAL ra, REAL dd, REAL gfx,
                                           REAL gfy, REAL *apx, REAL *apy, REAL *avx, REAL *avy,
@@ -407,6 +410,8 @@ static inline void FN(obstacle_force_adj)(const FN(ctx_t) *C, const REAL *od, in
     REAL vox = sh[3], voy = sh[4];
     REAL om = sh[5];
     REAL ang = sh[2];
+    if (st != 0 && god && FN(shape_moves)(C, o))
+        FN(obstacle_shape_adj)(C, sh, st, ro, hx, hy, px, py, vx, vy, ra, dd, gfx, gfy, god + 6 * o);
     if (st == 1) {
         FN(box_force_adj)(C, px, py, vx, vy, cx, cy, ang, hx, hy, ra + C->margin, dd, vox, voy,
                           om, gfx, gfy, apx, apy, avx, avy);
@@ -1446,18 +1451,181 @@ static void FN(integrate_agent_adj)(const FN(ctx_t) *C, const FN(prm_t) *P,
     }
 }
 
+/* ------------------------------------------------- body-pass terms of any shape type */
+
+#define D FN(dn)
+
+/* pair_force on duals (the same operations as FN(pair_force)) */
+static void FN(d_pair_force)(const FN(ctx_t) *C, D dx, D dy, D rvx, D rvy, REAL md, REAL dd,
+                             D *fx, D *fy)
+{
+    D d2 = FN(dadd)(FN(dmul)(dx, dx), FN(dmul)(dy, dy));
+    D dist = FN(dsqrt)(FN(dmax)(d2, FN(dk)(C->eps2)));
+    D ov = FN(dsub)(FN(dk)(md), dist);
+    *fx = FN(dk)((REAL)0);
+    *fy = FN(dk)((REAL)0);
+    if (ov.v > (REAL)0) {
+        D nx = FN(ddiv)(dx, dist), ny = FN(ddiv)(dy, dist);
+        D coef = FN(d_normal_coeff)(C, ov, FN(ddot)(rvx, rvy, nx, ny), dd);
+        *fx = FN(dmul)(coef, nx);
+        *fy = FN(dmul)(coef, ny);
+    }
+}
+
+/* closest_on_segment (swarp/core/collisions.py:157-171) on duals: the point of the core
+   (centre c, direction (ux, uy), half length hl) closest to p */
+static void FN(d_closest_on_segment)(D px, D py, D cx, D cy, D ux, D uy, REAL hl, D *qx, D *qy)
+{
+    D t = FN(dclamp)(FN(dadd)(FN(dmul)(FN(dsub)(px, cx), ux), FN(dmul)(FN(dsub)(py, cy), uy)),
+                     FN(dk)(-hl), FN(dk)(hl));
+    *qx = FN(dadd)(cx, FN(dmul)(t, ux));
+    *qy = FN(dadd)(cy, FN(dmul)(t, uy));
+}
+
+/* _reaction (swarp/core/bodies.py:80-127): force on the body from one disc agent (p, v,
+   radius ra, damping denominator dd) touching shape `ty` (radius ro, half extents hx, hy)
+   centred at c, oriented by (ca, sa) = cos / sin of the body angle, its centre moving
+   with vs and spinning with om; and the lever from the shape centre (r0, r1). */
+static void FN(d_body_reaction)(const FN(ctx_t) *C, int ty, REAL ro, REAL hx, REAL hy, REAL ra,
+                                REAL dd, D px, D py, D vx, D vy, D cx, D cy, D th, D vsx, D vsy,
+                                D om, D *f0, D *f1, D *r0, D *r1)
+{
+    D fx, fy;
+    if (ty == 1) {
+        FN(d_box_force)(C, px, py, vx, vy, cx, cy, th, hx, hy, ra + C->margin, dd, vsx, vsy, om,
+                        &fx, &fy);
+        *r0 = FN(dsub)(px, cx);
+        *r1 = FN(dsub)(py, cy);
+    } else if (ty == 2) {
+        D ux = FN(dcos)(th), uy = FN(dsin)(th), qx, qy;
+        FN(d_closest_on_segment)(px, py, cx, cy, ux, uy, hx, &qx, &qy);
+        D rrx = FN(dsub)(qx, cx), rry = FN(dsub)(qy, cy);
+        D sx = FN(dadd)(vsx, FN(dmul)(FN(dneg)(om), rry)), sy = FN(dadd)(vsy, FN(dmul)(om, rrx));
+        FN(d_pair_force)(C, FN(dsub)(px, qx), FN(dsub)(py, qy), FN(dsub)(vx, sx),
+                         FN(dsub)(vy, sy), ra + ro + C->margin, dd, &fx, &fy);
+        *r0 = rrx;
+        *r1 = rry;
+    } else {
+        FN(d_pair_force)(C, FN(dsub)(px, cx), FN(dsub)(py, cy), FN(dsub)(vx, vsx),
+                         FN(dsub)(vy, vsy), ra + ro + C->margin, dd, &fx, &fy);
+        *r0 = FN(dk)((REAL)0);
+        *r1 = FN(dk)((REAL)0);
+    }
+    *f0 = FN(dneg)(fx);
+    *f1 = FN(dneg)(fy);
+}
+
+/* _body_body (swarp/core/bodies.py:183-253): force on shape `ty` of a body (radius rs,
+   half extents hs, centre q moving with tv, angle th, spin om) from shape `ty2` of another
+   body or of the scenery (q2, tv2, th2, om2), and its lever from the shape centre.  A
+   box against a box exerts nothing (the reference models no box-box obstacle contact). */
+static void FN(d_body_body)(const FN(ctx_t) *C, int ty, REAL rs, REAL hsx, REAL hsy, int ty2,
+                            REAL r2, REAL h2x, REAL h2y, REAL dd, D qx, D qy, D tvx, D tvy, D th,
+                            D om, D q2x, D q2y, D tv2x, D tv2y, D th2, D om2, D *f0, D *f1,
+                            D *r0, D *r1)
+{
+    *f0 = *f1 = *r0 = *r1 = FN(dk)((REAL)0);
+    if (ty == 1) {
+        if (ty2 == 1) return;
+        D c2x = q2x, c2y = q2y, v2x = tv2x, v2y = tv2y;
+        if (ty2 == 2) {
+            FN(d_closest_on_segment)(qx, qy, q2x, q2y, FN(dcos)(th2), FN(dsin)(th2), h2x, &c2x,
+                                     &c2y);
+            D rrx = FN(dsub)(c2x, q2x), rry = FN(dsub)(c2y, q2y);
+            v2x = FN(dadd)(tv2x, FN(dmul)(FN(dneg)(om2), rry));
+            v2y = FN(dadd)(tv2y, FN(dmul)(om2, rrx));
+        }
+        D fox, foy;
+        FN(d_box_force)(C, c2x, c2y, v2x, v2y, qx, qy, th, hsx, hsy, r2 + C->margin, dd, tvx, tvy,
+                        om, &fox, &foy);
+        *f0 = FN(dneg)(fox);
+        *f1 = FN(dneg)(foy);
+        /* _closest_in_box (:168-180): c2 - q clamped onto this box, in world axes */
+        D ca = FN(dcos)(th), sa = FN(dsin)(th);
+        D dx = FN(dsub)(c2x, qx), dy = FN(dsub)(c2y, qy);
+        D lx = FN(dadd)(FN(dmul)(ca, dx), FN(dmul)(sa, dy));
+        D ly = FN(dadd)(FN(dmul)(FN(dneg)(sa), dx), FN(dmul)(ca, dy));
+        D kx = FN(dclamp)(lx, FN(dk)(-hsx), FN(dk)(hsx));
+        D ky = FN(dclamp)(ly, FN(dk)(-hsy), FN(dk)(hsy));
+        *r0 = FN(dsub)(FN(dmul)(ca, kx), FN(dmul)(sa, ky));
+        *r1 = FN(dadd)(FN(dmul)(sa, kx), FN(dmul)(ca, ky));
+    } else if (ty2 == 1) {
+        FN(d_box_force)(C, qx, qy, tvx, tvy, q2x, q2y, th2, h2x, h2y, rs + C->margin, dd, tv2x,
+                        tv2y, om2, f0, f1);
+    } else if (ty2 == 2) {
+        D cpx, cpy;
+        FN(d_closest_on_segment)(qx, qy, q2x, q2y, FN(dcos)(th2), FN(dsin)(th2), h2x, &cpx, &cpy);
+        D rrx = FN(dsub)(cpx, q2x), rry = FN(dsub)(cpy, q2y);
+        D s2x = FN(dadd)(tv2x, FN(dmul)(FN(dneg)(om2), rry));
+        D s2y = FN(dadd)(tv2y, FN(dmul)(om2, rrx));
+        FN(d_pair_force)(C, FN(dsub)(qx, cpx), FN(dsub)(qy, cpy), FN(dsub)(tvx, s2x),
+                         FN(dsub)(tvy, s2y), rs + r2 + C->margin, dd, f0, f1);
+    } else {
+        FN(d_pair_force)(C, FN(dsub)(qx, q2x), FN(dsub)(qy, q2y), FN(dsub)(tvx, tv2x),
+                         FN(dsub)(tvy, tv2y), rs + r2 + C->margin, dd, f0, f1);
+    }
+}
+
+/* Farthest point of shape s from its body's origin, the shape axis-aligned in the body
+   frame (swarp/core/bodies.py:449-459) */
+static inline REAL FN(shape_reach)(const FN(ctx_t) *C, int s)
+{
+    REAL ax = FABS(C->o_off[2 * s]), ay = FABS(C->o_off[2 * s + 1]);
+    REAL ro = C->o_rad[s], hx = C->o_half[2 * s], hy = C->o_half[2 * s + 1];
+    int ty = C->o_type[s];
+    if (ty == 1) return SQRT((ax + hx) * (ax + hx) + (ay + hy) * (ay + hy));
+    if (ty == 2) return SQRT((ax + hx) * (ax + hx) + ay * ay) + ro;
+    return SQRT(ax * ax + ay * ay) + ro;
+}
+
+static inline D FN(dseed)(REAL v, int k, int seed)
+{
+    D r = {v, k == seed ? (REAL)1 : (REAL)0};
+    return r;
+}
+
+/* The adjoint, added into g[0..5], of a moving box or segment shape's state sh (pos,
+   angle, vel, ang_vel) through its force on one disc agent (obstacle_force), the force
+   adjoint being (gfx, gfy): one Jacobian column per state entry. */
+static void FN(obstacle_shape_adj)(const FN(ctx_t) *C, const REAL *sh, int st, REAL ro, REAL hx,
+                                   REAL hy, REAL px, REAL py, REAL vx, REAL vy, REAL ra, REAL dd,
+                                   REAL gfx, REAL gfy, REAL *g)
+{
+    for (int k = 0; k < 6; ++k) {
+        D c0 = FN(dseed)(sh[0], 0, k), c1 = FN(dseed)(sh[1], 1, k), an = FN(dseed)(sh[2], 2, k);
+        D v0 = FN(dseed)(sh[3], 3, k), v1 = FN(dseed)(sh[4], 4, k), om = FN(dseed)(sh[5], 5, k);
+        D fx, fy;
+        if (st == 1) {
+            FN(d_box_force)(C, FN(dk)(px), FN(dk)(py), FN(dk)(vx), FN(dk)(vy), c0, c1, an, hx, hy,
+                            ra + C->margin, dd, v0, v1, om, &fx, &fy);
+        } else {
+            D qx, qy;
+            FN(d_closest_on_segment)(FN(dk)(px), FN(dk)(py), c0, c1, FN(dcos)(an), FN(dsin)(an),
+                                     hx, &qx, &qy);
+            D rx = FN(dsub)(qx, c0), ry = FN(dsub)(qy, c1);
+            D sx = FN(dadd)(v0, FN(dmul)(FN(dneg)(om), ry)), sy = FN(dadd)(v1, FN(dmul)(om, rx));
+            FN(d_pair_force)(C, FN(dsub)(FN(dk)(px), qx), FN(dsub)(FN(dk)(py), qy),
+                             FN(dsub)(FN(dk)(vx), sx), FN(dsub)(FN(dk)(vy), sy),
+                             ra + ro + C->margin, dd, &fx, &fy);
+        }
+        g[k] += gfx * fx.d + gfy * fy.d;
+    }
+}
+
+#undef D
+
 /* ------------------------------------------------------------- movable bodies */
 
 /* One movable body's contact sum, for the forward pass and its reverse.  Body rooted at
-   o; every shape of it is a circle (the build's scope).  Per shape s of the body (index
-   order) the reaction of every agent not bounds_apart from it, in agent order, then the
-   contacts with the circles of other bodies and of the scenery (index order), exactly
-   the loops of obstacle_dynamics_kernel (swarp/core/bodies.py:423-501). */
+   o.  Per shape s of the body (index order) the reaction of every agent not bounds_apart
+   from it, in agent order, then the contacts with the shapes of other bodies and of the
+   scenery (index order), exactly the loops of obstacle_dynamics_kernel
+   (swarp/core/bodies.py:423-501).  Circles take the plain contact law; boxes and
+   segments the dual-number terms above, evaluated without a tangent. */
 typedef struct {
     REAL qx, qy, th, tvx, tvy, om, ca, sa;
     REAL fx, fy, tau, ext;
 } FN(bodysum_t);
-
 
 static void FN(body_sum)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_t) *st,
                          const REAL *od, const REAL *bd, int o, FN(bodysum_t) *B)
@@ -1475,20 +1643,30 @@ static void FN(body_sum)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_
         REAL owy = B->sa * offx + B->ca * offy;
         REAL csx = B->qx + owx, csy = B->qy + owy;
         REAL vsx = B->tvx - B->om * owy, vsy = B->tvy + B->om * owx;
-        REAL ro = C->o_rad[s];
-        REAL ax = FABS(offx), ay = FABS(offy);
-        REAL reach = SQRT(ax * ax + ay * ay) + ro;
-        ext = FN(rmax)(ext, reach);
-        REAL bound = ro;
+        int ty = C->o_type[s];
+        REAL ro = C->o_rad[s], hx = C->o_half[2 * s], hy = C->o_half[2 * s + 1];
+        ext = FN(rmax)(ext, FN(shape_reach)(C, s));
+        REAL bound = FN(shape_bound)(ty, ro, hx, hy);
         for (int a = 0; a < A; ++a) {
             REAL ra = P[a].radius;
             if (FN(bounds_apart)(st[a].px - csx, st[a].py - csy, ra + bound + C->margin)) continue;
             REAL dd = (REAL)1 + C->c * C->sub_dt / P[a].mass;
-            REAL gx, gy;
-            FN(pair_force)(C, st[a].px - csx, st[a].py - csy, st[a].vx - vsx, st[a].vy - vsy,
-                           ra + ro + C->margin, dd, &gx, &gy);
-            REAL f0 = -gx, f1 = -gy;
-            REAL lx = owx + (REAL)0, ly = owy + (REAL)0;
+            REAL f0, f1, r0 = 0, r1 = 0;
+            if (ty == 0) {
+                REAL gx, gy;
+                FN(pair_force)(C, st[a].px - csx, st[a].py - csy, st[a].vx - vsx,
+                               st[a].vy - vsy, ra + ro + C->margin, dd, &gx, &gy);
+                f0 = -gx;
+                f1 = -gy;
+            } else {
+                FN(dn) g0, g1, l0, l1;
+                FN(d_body_reaction)(C, ty, ro, hx, hy, ra, dd, FN(dk)(st[a].px), FN(dk)(st[a].py),
+                                    FN(dk)(st[a].vx), FN(dk)(st[a].vy), FN(dk)(csx), FN(dk)(csy),
+                                    FN(dk)(B->th), FN(dk)(vsx), FN(dk)(vsy), FN(dk)(B->om), &g0,
+                                    &g1, &l0, &l1);
+                f0 = g0.v; f1 = g1.v; r0 = l0.v; r1 = l1.v;
+            }
+            REAL lx = owx + r0, ly = owy + r1;
             fx += f0;
             fy += f1;
             tau += lx * f1 - ly * f0;
@@ -1496,12 +1674,24 @@ static void FN(body_sum)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_
         for (int o2 = 0; o2 < N; ++o2) {
             if (C->o_body[o2] == o) continue;
             const REAL *d2 = od + 6 * o2;
-            REAL r2 = C->o_rad[o2];
-            if (FN(bounds_apart)(d2[0] - csx, d2[1] - csy, bound + r2 + C->margin)) continue;
-            REAL gx, gy;
-            FN(pair_force)(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4],
-                           ro + r2 + C->margin, denom_self, &gx, &gy);
-            REAL lx = owx + (REAL)0, ly = owy + (REAL)0;
+            int ty2 = C->o_type[o2];
+            REAL r2 = C->o_rad[o2], h2x = C->o_half[2 * o2], h2y = C->o_half[2 * o2 + 1];
+            if (FN(bounds_apart)(d2[0] - csx, d2[1] - csy,
+                                 bound + FN(shape_bound)(ty2, r2, h2x, h2y) + C->margin))
+                continue;
+            REAL gx, gy, r0 = 0, r1 = 0;
+            if (ty == 0 && ty2 == 0) {
+                FN(pair_force)(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4],
+                               ro + r2 + C->margin, denom_self, &gx, &gy);
+            } else {
+                FN(dn) g0, g1, l0, l1;
+                FN(d_body_body)(C, ty, ro, hx, hy, ty2, r2, h2x, h2y, denom_self, FN(dk)(csx),
+                                FN(dk)(csy), FN(dk)(vsx), FN(dk)(vsy), FN(dk)(B->th),
+                                FN(dk)(B->om), FN(dk)(d2[0]), FN(dk)(d2[1]), FN(dk)(d2[3]),
+                                FN(dk)(d2[4]), FN(dk)(d2[2]), FN(dk)(d2[5]), &g0, &g1, &l0, &l1);
+                gx = g0.v; gy = g1.v; r0 = l0.v; r1 = l1.v;
+            }
+            REAL lx = owx + r0, ly = owy + r1;
             fx += gx;
             fy += gy;
             tau += lx * gy - ly * gx;
@@ -1644,12 +1834,53 @@ static void FN(bodies_env_adj)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(
             REAL owy = B.sa * offx + B.ca * offy;
             REAL csx = B.qx + owx, csy = B.qy + owy;
             REAL vsx = B.tvx - B.om * owy, vsy = B.tvy + B.om * owx;
-            REAL ro = C->o_rad[s];
+            int ty = C->o_type[s];
+            REAL ro = C->o_rad[s], hx = C->o_half[2 * s], hy = C->o_half[2 * s + 1];
+            REAL bound = FN(shape_bound)(ty, ro, hx, hy);
             REAL g_owx = 0, g_owy = 0, g_csx = 0, g_csy = 0, g_vsx = 0, g_vsy = 0;
+            REAL g_thd = 0, g_omd = 0;  /* through the shape's own angle and spin */
             for (int a = 0; a < A; ++a) {
                 REAL ra = P[a].radius;
-                if (FN(bounds_apart)(st[a].px - csx, st[a].py - csy, ra + ro + C->margin)) continue;
+                if (FN(bounds_apart)(st[a].px - csx, st[a].py - csy, ra + bound + C->margin)) continue;
                 REAL dd = (REAL)1 + C->c * C->sub_dt / P[a].mass;
+                if (ty != 0) {
+                    /* a box or segment: the term's Jacobian column by column */
+                    const REAL in[10] = {st[a].px, st[a].py, st[a].vx, st[a].vy, csx, csy, B.th,
+                                         vsx, vsy, B.om};
+                    REAL f0 = 0, f1 = 0, r0 = 0, r1 = 0, g_f0 = 0, g_f1 = 0, g_r0 = 0, g_r1 = 0;
+                    for (int k = -1; k < 10; ++k) {
+                        FN(dn) x[10], o0, o1, l0, l1;
+                        for (int q = 0; q < 10; ++q) x[q] = FN(dseed)(in[q], q, k);
+                        FN(d_body_reaction)(C, ty, ro, hx, hy, ra, dd, x[0], x[1], x[2], x[3],
+                                            x[4], x[5], x[6], x[7], x[8], x[9], &o0, &o1, &l0,
+                                            &l1);
+                        if (k < 0) {
+                            f0 = o0.v; f1 = o1.v; r0 = l0.v; r1 = l1.v;
+                            REAL L0 = owx + r0, L1 = owy + r1;
+                            g_f0 = g_fx - g_tau * L1;
+                            g_f1 = g_fy + g_tau * L0;
+                            g_r0 = g_tau * f1;
+                            g_r1 = -(g_tau * f0);
+                            g_owx += g_tau * f1;
+                            g_owy -= g_tau * f0;
+                            continue;
+                        }
+                        REAL adj = g_f0 * o0.d + g_f1 * o1.d + g_r0 * l0.d + g_r1 * l1.d;
+                        switch (k) {
+                        case 0: gst[a].px += adj; break;
+                        case 1: gst[a].py += adj; break;
+                        case 2: gst[a].vx += adj; break;
+                        case 3: gst[a].vy += adj; break;
+                        case 4: g_csx += adj; break;
+                        case 5: g_csy += adj; break;
+                        case 6: g_thd += adj; break;
+                        case 7: g_vsx += adj; break;
+                        case 8: g_vsy += adj; break;
+                        default: g_omd += adj; break;
+                        }
+                    }
+                    continue;
+                }
                 REAL gx, gy;
                 FN(pair_force)(C, st[a].px - csx, st[a].py - csy, st[a].vx - vsx, st[a].vy - vsy,
                                ra + ro + C->margin, dd, &gx, &gy);
@@ -1674,8 +1905,44 @@ static void FN(bodies_env_adj)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(
             for (int o2 = 0; o2 < N; ++o2) {
                 if (C->o_body[o2] == o) continue;
                 const REAL *d2 = ob + 6 * o2;
-                REAL r2 = C->o_rad[o2];
-                if (FN(bounds_apart)(d2[0] - csx, d2[1] - csy, ro + r2 + C->margin)) continue;
+                int ty2 = C->o_type[o2];
+                REAL r2 = C->o_rad[o2], h2x = C->o_half[2 * o2], h2y = C->o_half[2 * o2 + 1];
+                if (FN(bounds_apart)(d2[0] - csx, d2[1] - csy,
+                                     bound + FN(shape_bound)(ty2, r2, h2x, h2y) + C->margin))
+                    continue;
+                if (ty != 0 || ty2 != 0) {
+                    const REAL in[12] = {csx, csy, vsx, vsy, B.th, B.om,
+                                         d2[0], d2[1], d2[3], d2[4], d2[2], d2[5]};
+                    static const int to_state[6] = {0, 1, 3, 4, 2, 5};
+                    REAL f0 = 0, f1 = 0, g_f0 = 0, g_f1 = 0, g_r0 = 0, g_r1 = 0;
+                    for (int k = -1; k < 12; ++k) {
+                        FN(dn) x[12], o0, o1, l0, l1;
+                        for (int q = 0; q < 12; ++q) x[q] = FN(dseed)(in[q], q, k);
+                        FN(d_body_body)(C, ty, ro, hx, hy, ty2, r2, h2x, h2y, denom_self, x[0],
+                                        x[1], x[2], x[3], x[4], x[5], x[6], x[7], x[8], x[9],
+                                        x[10], x[11], &o0, &o1, &l0, &l1);
+                        if (k < 0) {
+                            f0 = o0.v; f1 = o1.v;
+                            REAL L0 = owx + l0.v, L1 = owy + l1.v;
+                            g_f0 = g_fx - g_tau * L1;
+                            g_f1 = g_fy + g_tau * L0;
+                            g_r0 = g_tau * f1;
+                            g_r1 = -(g_tau * f0);
+                            g_owx += g_tau * f1;
+                            g_owy -= g_tau * f0;
+                            continue;
+                        }
+                        REAL adj = g_f0 * o0.d + g_f1 * o1.d + g_r0 * l0.d + g_r1 * l1.d;
+                        if (k == 0) g_csx += adj;
+                        else if (k == 1) g_csy += adj;
+                        else if (k == 2) g_vsx += adj;
+                        else if (k == 3) g_vsy += adj;
+                        else if (k == 4) g_thd += adj;
+                        else if (k == 5) g_omd += adj;
+                        else if (FN(shape_moves)(C, o2)) gob[6 * o2 + to_state[k - 6]] += adj;
+                    }
+                    continue;
+                }
                 REAL gx, gy;
                 FN(pair_force)(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4],
                                ro + r2 + C->margin, denom_self, &gx, &gy);
@@ -1705,8 +1972,8 @@ static void FN(bodies_env_adj)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(
             g_owy += g_csy - g_vsx * B.om;
             g_tvx += g_vsx;
             g_tvy += g_vsy;
-            g_om += -g_vsx * owy + g_vsy * owx;
-            g_th += -g_owx * owy + g_owy * owx;
+            g_om += -g_vsx * owy + g_vsy * owx + g_omd;
+            g_th += -g_owx * owy + g_owy * owx + g_thd;
         }
         REAL *gi = gob + 6 * N + 6 * o;
         gi[0] = g_qx; gi[1] = g_qy; gi[2] = g_th; gi[3] = g_tvx; gi[4] = g_tvy; gi[5] = g_om;

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 F32, F64 = 0, 1
 EULER, RK4 = 0, 1
 LISTS_BRUTE, LISTS_GRID = 0, 1
@@ -81,6 +81,7 @@ class SwarpDesc(ctypes.Structure):
         ("grid_cell", ctypes.c_double),
         ("grid_frame", ctypes.c_void_p),
         ("body_params", ctypes.c_void_p),
+        ("obstacle_types", ctypes.c_int32),
     ]
 
 

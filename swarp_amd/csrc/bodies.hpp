@@ -1,6 +1,6 @@
 // bodies.hpp -- rollout kernels for worlds with movable compound bodies: the body pass of
-// obstacle_dynamics_kernel (swarp/core/bodies.py:367-568, disc variant: every shape of a
-// movable body is a circle) inside the fused substep chain, and this build's own adjoint
+// obstacle_dynamics_kernel (swarp/core/bodies.py:367-568, disc variant: disc agents, body
+// shapes of any type) inside the fused substep chain, and this build's own adjoint
 // of it (the reference never tapes the body pass, swarp/core/stepper.py:952).
 // Instantiated by k_bodies.hip.
 //
@@ -88,6 +88,137 @@ template <typename T> __device__ __forceinline__ bool shape_moves(const ObTab<T>
     return tb.body[r] == r && tb.kind[r] == 1;
 }
 
+// ------------------------------------------------ body-pass terms of any shape type
+//
+// Written once over the value type V: plain T in the forward pass, a one-tangent Dual in
+// the reverse pass, which evaluates them once per seeded input (a column of the term's
+// Jacobian) for the boxes and segments.  Circles keep the plain contact law and its
+// hand-written reverse.
+
+// pair_force over V (the same operations)
+template <typename T, typename V>
+__device__ __forceinline__ void pair_force_v(const Cst<T> &C, V dx, V dy, V rvx, V rvy, T md, T dd,
+                                             V &fx, V &fy)
+{
+    const V dist = m_sqrt(wmax(dx * dx + dy * dy, V(C.eps2)));
+    const V ov = V(md) - dist;
+    fx = V(T(0));
+    fy = V(T(0));
+    if (val(ov) > T(0)) {
+        const V nx = dx / dist, ny = dy / dist;
+        const V coef = normal_coeff_v(C, ov, rvx * nx + rvy * ny, dd);
+        fx = coef * nx;
+        fy = coef * ny;
+    }
+}
+
+// closest_on_segment (swarp/core/collisions.py:157-171): the point of the core (centre c,
+// direction (ux, uy), half length hl) closest to p
+template <typename T, typename V>
+__device__ __forceinline__ void closest_seg_v(V px, V py, V cx, V cy, V ux, V uy, T hl, V &qx,
+                                              V &qy)
+{
+    const V t = wclamp((px - cx) * ux + (py - cy) * uy, V(-hl), V(hl));
+    qx = cx + t * ux;
+    qy = cy + t * uy;
+}
+
+// _reaction (swarp/core/bodies.py:80-127): force on the body from one disc agent (p, v,
+// radius ra, damping denominator dd) touching shape `ty` (radius ro, half extents hx, hy)
+// centred at c, oriented by (ca, sa) = cos / sin of the body angle, its centre moving
+// with vs, spinning with om; and the lever from the shape centre (r0, r1).
+template <typename T, typename V>
+__device__ __forceinline__ void body_reaction_v(const Cst<T> &C, int ty, T ro, T hx, T hy, T ra,
+                                                T dd, V px, V py, V vx, V vy, V cx, V cy, V ca,
+                                                V sa, V vsx, V vsy, V om, V &f0, V &f1, V &r0,
+                                                V &r1)
+{
+    V fx, fy;
+    if (ty == 1) {
+        box_force_v<T, V>(C, px, py, vx, vy, cx, cy, ca, sa, hx, hy, ra + C.margin, dd, vsx, vsy,
+                          om, fx, fy);
+        r0 = px - cx;
+        r1 = py - cy;
+    } else if (ty == 2) {
+        V qx, qy;
+        closest_seg_v<T, V>(px, py, cx, cy, ca, sa, hx, qx, qy);
+        const V rrx = qx - cx, rry = qy - cy;
+        const V sx = vsx + (-om) * rry, sy = vsy + om * rrx;
+        pair_force_v<T, V>(C, px - qx, py - qy, vx - sx, vy - sy, ra + ro + C.margin, dd, fx, fy);
+        r0 = rrx;
+        r1 = rry;
+    } else {
+        pair_force_v<T, V>(C, px - cx, py - cy, vx - vsx, vy - vsy, ra + ro + C.margin, dd, fx, fy);
+        r0 = V(T(0));
+        r1 = V(T(0));
+    }
+    f0 = -fx;
+    f1 = -fy;
+}
+
+// _body_body (swarp/core/bodies.py:183-253): force on shape `ty` of a body (radius rs,
+// half extents hs, centre q moving with tv, orientation (ca, sa), spin om) from shape ty2
+// of another body or of the scenery (q2, tv2, (ca2, sa2), om2), and its lever from the
+// shape centre.  A box against a box exerts nothing (the reference models no box-box
+// obstacle contact); a round body meets a box as a disc of its radius at its centre.
+template <typename T, typename V>
+__device__ __forceinline__ void body_body_v(const Cst<T> &C, int ty, T rs, T hsx, T hsy, int ty2,
+                                            T r2, T h2x, T h2y, T dd, V qx, V qy, V tvx, V tvy,
+                                            V ca, V sa, V om, V q2x, V q2y, V tv2x, V tv2y, V ca2,
+                                            V sa2, V om2, V &f0, V &f1, V &r0, V &r1)
+{
+    f0 = f1 = r0 = r1 = V(T(0));
+    if (ty == 1) {
+        if (ty2 == 1) return;
+        V c2x = q2x, c2y = q2y, v2x = tv2x, v2y = tv2y;
+        if (ty2 == 2) {
+            closest_seg_v<T, V>(qx, qy, q2x, q2y, ca2, sa2, h2x, c2x, c2y);
+            const V rrx = c2x - q2x, rry = c2y - q2y;
+            v2x = tv2x + (-om2) * rry;
+            v2y = tv2y + om2 * rrx;
+        }
+        V fox, foy;
+        box_force_v<T, V>(C, c2x, c2y, v2x, v2y, qx, qy, ca, sa, hsx, hsy, r2 + C.margin, dd, tvx,
+                          tvy, om, fox, foy);
+        f0 = -fox;
+        f1 = -foy;
+        // _closest_in_box (:168-180): c2 - q clamped onto this box, in world axes
+        const V dx = c2x - qx, dy = c2y - qy;
+        const V lx = ca * dx + sa * dy, ly = (-sa) * dx + ca * dy;
+        const V kx = wclamp(lx, V(-hsx), V(hsx)), ky = wclamp(ly, V(-hsy), V(hsy));
+        r0 = ca * kx - sa * ky;
+        r1 = sa * kx + ca * ky;
+    } else if (ty2 == 1) {
+        box_force_v<T, V>(C, qx, qy, tvx, tvy, q2x, q2y, ca2, sa2, h2x, h2y, rs + C.margin, dd,
+                          tv2x, tv2y, om2, f0, f1);
+    } else if (ty2 == 2) {
+        V cpx, cpy;
+        closest_seg_v<T, V>(qx, qy, q2x, q2y, ca2, sa2, h2x, cpx, cpy);
+        const V rrx = cpx - q2x, rry = cpy - q2y;
+        const V s2x = tv2x + (-om2) * rry, s2y = tv2y + om2 * rrx;
+        pair_force_v<T, V>(C, qx - cpx, qy - cpy, tvx - s2x, tvy - s2y, rs + r2 + C.margin, dd, f0,
+                           f1);
+    } else {
+        pair_force_v<T, V>(C, qx - q2x, qy - q2y, tvx - tv2x, tvy - tv2y, rs + r2 + C.margin, dd,
+                           f0, f1);
+    }
+}
+
+// shape_bound (swarp/core/collisions.py:61-70): radius of the disc about a shape's centre
+// that holds it
+template <typename T> __device__ __forceinline__ T shape_bound(int ty, T r, T hx, T hy)
+{
+    return ty == 1 ? m_sqrt(hx * hx + hy * hy) : (ty == 2 ? hx + r : r);
+}
+
+// A one-tangent dual of x, seeded when k == seed.
+template <typename T> __device__ __forceinline__ Dual<T, 1> dseed(T x, int k, int seed)
+{
+    Dual<T, 1> r(x);
+    r.d[0] = k == seed ? T(1) : T(0);
+    return r;
+}
+
 // One obstacle's force on an agent, the obstacle's pose read from the env's state `od`
 // (_obstacle_forces body, swarp/core/collisions.py:690-743).
 template <typename T>
@@ -98,7 +229,7 @@ __device__ __forceinline__ void ob_force(const Cst<T> &C, const ObTab<T> &tb, co
     fy = T(0);
     const T *sh = od + 6 * o;
     const T cx = sh[0], cy = sh[1];
-    const int st = tb.type[o];
+    const int st = (C.round_only ? 0 : tb.type[o]);
     const T ro = tb.rad[o], hx = tb.half[2 * o], hy = tb.half[2 * o + 1];
     const T bound = st == 1 ? m_sqrt(hx * hx + hy * hy) : (st == 2 ? hx + ro : ro);
     if (b_apart(px - cx, py - cy, ra + C.margin + bound)) return;
@@ -118,21 +249,44 @@ __device__ __forceinline__ void ob_force(const Cst<T> &C, const ObTab<T> &tb, co
     }
 }
 
-// Reverse of ob_force: the agent's adjoint into `a`; for a circle the adjoint of the
-// obstacle's position and velocity is returned in (opx, opy, ovx, ovy) (zero otherwise).
+// Reverse of ob_force: the agent's adjoint into `a`; with `shape` set (a moving shape) the
+// adjoint of the shape's state (pos x, pos y, angle, vel x, vel y, ang_vel) is returned in
+// op[0..5] (zero otherwise).
 template <typename T>
 __device__ __forceinline__ void ob_force_adj(const Cst<T> &C, const ObTab<T> &tb, const T *od,
                                              int o, T px, T py, T vx, T vy, T ra, T dd, T gx,
-                                             T gy, St<T> &a, T &opx, T &opy, T &ovx, T &ovy)
+                                             T gy, St<T> &a, bool shape, T (&op)[6])
 {
-    opx = opy = ovx = ovy = T(0);
+#pragma unroll
+    for (int q = 0; q < 6; ++q) op[q] = T(0);
     const T *sh = od + 6 * o;
     const T cx = sh[0], cy = sh[1];
-    const int st = tb.type[o];
+    const int st = (C.round_only ? 0 : tb.type[o]);
     const T ro = tb.rad[o], hx = tb.half[2 * o], hy = tb.half[2 * o + 1];
     const T bound = st == 1 ? m_sqrt(hx * hx + hy * hy) : (st == 2 ? hx + ro : ro);
     if (b_apart(px - cx, py - cy, ra + C.margin + bound)) return;
     const T vox = sh[3], voy = sh[4], om = sh[5], ang = sh[2];
+    if (st != 0 && shape) {
+        // a moving box or segment: its state's adjoint, one seeded entry at a time
+        for (int k = 0; k < 6; ++k) {
+            const Dual<T, 1> c0 = dseed(sh[0], 0, k), c1 = dseed(sh[1], 1, k);
+            const Dual<T, 1> an = dseed(sh[2], 2, k), v0 = dseed(sh[3], 3, k);
+            const Dual<T, 1> v1 = dseed(sh[4], 4, k), w = dseed(sh[5], 5, k);
+            const Dual<T, 1> P0(px), P1(py), U0(vx), U1(vy);
+            Dual<T, 1> fx, fy;
+            if (st == 1) {
+                box_force_v<T, Dual<T, 1>>(C, P0, P1, U0, U1, c0, c1, m_cos(an), m_sin(an), hx,
+                                           hy, ra + C.margin, dd, v0, v1, w, fx, fy);
+            } else {
+                Dual<T, 1> qx, qy;
+                closest_seg_v<T, Dual<T, 1>>(P0, P1, c0, c1, m_cos(an), m_sin(an), hx, qx, qy);
+                const Dual<T, 1> rx = qx - c0, ry = qy - c1;
+                pair_force_v<T, Dual<T, 1>>(C, P0 - qx, P1 - qy, U0 - (v0 + (-w) * ry),
+                                            U1 - (v1 + w * rx), ra + ro + C.margin, dd, fx, fy);
+            }
+            op[k] = gx * fx.d[0] + gy * fy.d[0];
+        }
+    }
     if (st == 1) {
         box_force_adj(C, px, py, vx, vy, cx, cy, ang, hx, hy, ra + C.margin, dd, vox, voy, om,
                       gx, gy, a);
@@ -162,10 +316,12 @@ __device__ __forceinline__ void ob_force_adj(const Cst<T> &C, const ObTab<T> &tb
         a.py += ady;
         a.vx += arx;
         a.vy += ary;
-        opx = -adx;
-        opy = -ady;
-        ovx = -arx;
-        ovy = -ary;
+        if (shape) {
+            op[0] = -adx;
+            op[1] = -ady;
+            op[3] = -arx;
+            op[4] = -ary;
+        }
     }
 }
 
@@ -275,16 +431,21 @@ template <typename T> struct BodyNew {
     bool clx, cly;
 };
 
-// Farthest point of body root o's shapes from the body origin (circles: |offset| +
-// radius; bodies.py:449-459): it depends on the installed tables only, so the kernels
-// evaluate it once per launch.
+// Farthest point of body root o's shapes from the body origin, each shape axis-aligned in
+// the body frame (bodies.py:449-459): it depends on the installed tables only, so the
+// kernels evaluate it once per launch.
 template <typename T> __device__ __forceinline__ T body_ext(const ObTab<T> &tb, int o)
 {
     T ext = T(0);
     for (int s = 0; s < tb.N; ++s) {
         if (tb.body[s] != o) continue;
         const T ax = m_abs(tb.off[2 * s]), ay = m_abs(tb.off[2 * s + 1]);
-        ext = wmax(ext, m_sqrt(ax * ax + ay * ay) + tb.rad[s]);
+        const T ro = tb.rad[s], hx = tb.half[2 * s], hy = tb.half[2 * s + 1];
+        const int ty = tb.type[s];
+        const T reach = ty == 1 ? m_sqrt((ax + hx) * (ax + hx) + (ay + hy) * (ay + hy))
+                      : ty == 2 ? m_sqrt((ax + hx) * (ax + hx) + ay * ay) + ro
+                                : m_sqrt(ax * ax + ay * ay) + ro;
+        ext = wmax(ext, reach);
     }
     return ext;
 }
@@ -320,7 +481,10 @@ __device__ __forceinline__ void body_load(const ObTab<T> &tb, const T *od, const
 
 // Contact sum of movable body root o: every lane of the env computes the same values
 // (agent contributions reach all of them by readlane, env_ordered_sums).  Agent state of
-// the lane in `st`; `od` = the env's obstacle state at the substep input.
+// the lane in `st`; `od` = the env's obstacle state at the substep input.  Per shape of
+// the body (index order): the agents' reactions in agent order, then the contacts with
+// the shapes of other bodies and of the scenery in index order (swarp/core/bodies.py:
+// 423-501).
 template <typename T, int PA>
 __device__ __forceinline__ void body_sum(const Cst<T> &C, const ObTab<T> &tb,
                                          const Lane<T, PA> &L, const BodyRow<T> &br,
@@ -337,16 +501,24 @@ __device__ __forceinline__ void body_sum(const Cst<T> &C, const ObTab<T> &tb,
         const T owy = B.sa * offx + B.ca * offy;
         const T csx = B.qx + owx, csy = B.qy + owy;
         const T vsx = B.tvx - B.om * owy, vsy = B.tvy + B.om * owx;
-        const T ro = tb.rad[s];
+        const int ty = (C.round_only ? 0 : tb.type[s]);
+        const T ro = tb.rad[s], hx = tb.half[2 * s], hy = tb.half[2 * s + 1];
+        const T bound = shape_bound(ty, ro, hx, hy);
         // the agents' reactions, in agent order
         T f0 = T(0), f1 = T(0), tq = T(0);
-        if (L.active && !b_apart(st.px - csx, st.py - csy, br.r + ro + C.margin)) {
-            T gx, gy;
-            pair_force(C, st.px - csx, st.py - csy, st.vx - vsx, st.vy - vsy,
-                       br.r + ro + C.margin, br.dd, gx, gy);
-            f0 = -gx;
-            f1 = -gy;
-            const T lx = owx + T(0), ly = owy + T(0);
+        if (L.active && !b_apart(st.px - csx, st.py - csy, br.r + bound + C.margin)) {
+            T r0 = T(0), r1 = T(0);
+            if (ty == 0) {
+                T gx, gy;
+                pair_force(C, st.px - csx, st.py - csy, st.vx - vsx, st.vy - vsy,
+                           br.r + ro + C.margin, br.dd, gx, gy);
+                f0 = -gx;
+                f1 = -gy;
+            } else {
+                body_reaction_v<T, T>(C, ty, ro, hx, hy, br.r, br.dd, st.px, st.py, st.vx, st.vy,
+                                      csx, csy, B.ca, B.sa, vsx, vsy, B.om, f0, f1, r0, r1);
+            }
+            const T lx = owx + r0, ly = owy + r1;
             tq = lx * f1 - ly * f0;
         }
         {
@@ -357,16 +529,25 @@ __device__ __forceinline__ void body_sum(const Cst<T> &C, const ObTab<T> &tb,
             fy = acc[1];
             tau = acc[2];
         }
-        // contacts with the circles of other bodies and of the scenery, in index order
+        // contacts with the shapes of other bodies and of the scenery, in index order
         for (int o2 = 0; o2 < N; ++o2) {
             if (tb.body[o2] == o) continue;
             const T *d2 = od + 6 * o2;
-            const T r2 = tb.rad[o2];
-            if (b_apart(d2[0] - csx, d2[1] - csy, ro + r2 + C.margin)) continue;
-            T gx, gy;
-            pair_force(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4], ro + r2 + C.margin,
-                       denom_self, gx, gy);
-            const T lx = owx + T(0), ly = owy + T(0);
+            const int ty2 = (C.round_only ? 0 : tb.type[o2]);
+            const T r2 = tb.rad[o2], h2x = tb.half[2 * o2], h2y = tb.half[2 * o2 + 1];
+            if (b_apart(d2[0] - csx, d2[1] - csy, bound + shape_bound(ty2, r2, h2x, h2y) + C.margin))
+                continue;
+            T gx, gy, r0 = T(0), r1 = T(0);
+            if (ty == 0 && ty2 == 0) {
+                pair_force(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4],
+                           ro + r2 + C.margin, denom_self, gx, gy);
+            } else {
+                const T ca2 = ty2 == 0 ? T(1) : m_cos(d2[2]), sa2 = ty2 == 0 ? T(0) : m_sin(d2[2]);
+                body_body_v<T, T>(C, ty, ro, hx, hy, ty2, r2, h2x, h2y, denom_self, csx, csy, vsx,
+                                  vsy, B.ca, B.sa, B.om, d2[0], d2[1], d2[3], d2[4], ca2, sa2,
+                                  d2[5], gx, gy, r0, r1);
+            }
+            const T lx = owx + r0, ly = owy + r1;
             fx += gx;
             fy += gy;
             tau += lx * gy - ly * gx;
@@ -667,44 +848,126 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
             const T owy = B.sa * offx + B.ca * offy;
             const T csx = B.qx + owx, csy = B.qy + owy;
             const T vsx = B.tvx - B.om * owy, vsy = B.tvy + B.om * owx;
-            const T ro = tb.rad[s];
+            const int ty = (C.round_only ? 0 : tb.type[s]);
+            const T ro = tb.rad[s], hx = tb.half[2 * s], hy = tb.half[2 * s + 1];
+            const T bound = shape_bound(ty, ro, hx, hy);
             const T g_f0 = g_fx - g_tau * owy, g_f1 = g_fy + g_tau * owx;
-            // the agents' terms, in agent order
-            T c0 = T(0), c1 = T(0), c2 = T(0), c3 = T(0), c4 = T(0), c5 = T(0);
-            if (L.active && !b_apart(st.px - csx, st.py - csy, br.r + ro + C.margin)) {
-                const T dx = st.px - csx, dy = st.py - csy, rvx = st.vx - vsx, rvy = st.vy - vsy;
-                const T md = br.r + ro + C.margin;
-                T gx, gy;
-                pair_force(C, dx, dy, rvx, rvy, md, br.dd, gx, gy);
-                const T f0 = -gx, f1 = -gy;
-                T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
-                pair_force_adj(C, dx, dy, rvx, rvy, md, br.dd, -g_f0, -g_f1, adx, ady, arx, ary);
-                ga.px += adx;
-                ga.py += ady;
-                ga.vx += arx;
-                ga.vy += ary;
-                c0 = g_tau * f1;   // onto g_owx
-                c1 = -(g_tau * f0);  // onto g_owy (g_owy -= g_tau * f0)
-                c2 = -adx;         // onto g_csx
-                c3 = -ady;
-                c4 = -arx;         // onto g_vsx
-                c5 = -ary;
+            // the agents' terms, in agent order: contributions to the adjoints of ow, the
+            // shape centre cs, its velocity vs, and (boxes, segments) the shape's own angle
+            // and spin
+            T cv[8] = {T(0), T(0), T(0), T(0), T(0), T(0), T(0), T(0)};
+            if (L.active && !b_apart(st.px - csx, st.py - csy, br.r + bound + C.margin)) {
+                if (ty == 0) {
+                    const T dx = st.px - csx, dy = st.py - csy, rvx = st.vx - vsx,
+                            rvy = st.vy - vsy;
+                    const T md = br.r + ro + C.margin;
+                    T gx, gy;
+                    pair_force(C, dx, dy, rvx, rvy, md, br.dd, gx, gy);
+                    const T f0 = -gx, f1 = -gy;
+                    T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
+                    pair_force_adj(C, dx, dy, rvx, rvy, md, br.dd, -g_f0, -g_f1, adx, ady, arx,
+                                   ary);
+                    ga.px += adx;
+                    ga.py += ady;
+                    ga.vx += arx;
+                    ga.vy += ary;
+                    cv[0] = g_tau * f1;    // onto g_owx
+                    cv[1] = -(g_tau * f0); // onto g_owy (g_owy -= g_tau * f0)
+                    cv[2] = -adx;          // onto g_csx
+                    cv[3] = -ady;
+                    cv[4] = -arx;          // onto g_vsx
+                    cv[5] = -ary;
+                } else {
+                    // a box or segment: the term's Jacobian, one seeded input at a time
+                    T f0, f1, r0, r1;
+                    body_reaction_v<T, T>(C, ty, ro, hx, hy, br.r, br.dd, st.px, st.py, st.vx,
+                                          st.vy, csx, csy, B.ca, B.sa, vsx, vsy, B.om, f0, f1,
+                                          r0, r1);
+                    const T L0 = owx + r0, L1 = owy + r1;
+                    const T h0 = g_fx - g_tau * L1, h1 = g_fy + g_tau * L0;
+                    const T hr0 = g_tau * f1, hr1 = -(g_tau * f0);
+                    cv[0] = g_tau * f1;
+                    cv[1] = -(g_tau * f0);
+                    const T in[10] = {st.px, st.py, st.vx, st.vy, csx, csy, B.th, vsx, vsy, B.om};
+                    for (int k = 0; k < 10; ++k) {
+                        Dual<T, 1> x[10], o0, o1, l0, l1;
+#pragma unroll
+                        for (int q = 0; q < 10; ++q) x[q] = dseed(in[q], q, k);
+                        body_reaction_v<T, Dual<T, 1>>(C, ty, ro, hx, hy, br.r, br.dd, x[0], x[1],
+                                                       x[2], x[3], x[4], x[5], m_cos(x[6]),
+                                                       m_sin(x[6]), x[7], x[8], x[9], o0, o1, l0,
+                                                       l1);
+                        const T adj = h0 * o0.d[0] + h1 * o1.d[0] + hr0 * l0.d[0] + hr1 * l1.d[0];
+                        if (k == 0) ga.px += adj;
+                        else if (k == 1) ga.py += adj;
+                        else if (k == 2) ga.vx += adj;
+                        else if (k == 3) ga.vy += adj;
+                        else if (k == 4) cv[2] += adj;
+                        else if (k == 5) cv[3] += adj;
+                        else if (k == 6) cv[6] += adj;
+                        else if (k == 7) cv[4] += adj;
+                        else if (k == 8) cv[5] += adj;
+                        else cv[7] += adj;
+                    }
+                }
             }
-            T acc[6] = {T(0), T(0), T(0), T(0), T(0), T(0)};
+            T acc[8] = {T(0), T(0), T(0), T(0), T(0), T(0), T(0), T(0)};
             {
-                const T val[6] = {c0, c1, c2, c3, c4, c5};
-                env_ordered_sums<PA, 6>(acc, val,
-                                        c0 != T(0) || c1 != T(0) || c2 != T(0) || c3 != T(0) ||
-                                            c4 != T(0) || c5 != T(0),
-                                        L.lane);
+                bool fl = false;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) fl = fl || cv[q] != T(0);
+                env_ordered_sums<PA, 8>(acc, cv, fl, L.lane);
             }
             T g_owx = acc[0], g_owy = acc[1], g_csx = acc[2], g_csy = acc[3], g_vsx = acc[4],
-              g_vsy = acc[5];
+              g_vsy = acc[5], g_thd = acc[6], g_omd = acc[7];
             for (int o2 = 0; o2 < N; ++o2) {
                 if (tb.body[o2] == o) continue;
                 const T *d2 = obc + 6 * o2;
-                const T r2 = tb.rad[o2];
-                if (b_apart(d2[0] - csx, d2[1] - csy, ro + r2 + C.margin)) continue;
+                const int ty2 = (C.round_only ? 0 : tb.type[o2]);
+                const T r2 = tb.rad[o2], h2x = tb.half[2 * o2], h2y = tb.half[2 * o2 + 1];
+                if (b_apart(d2[0] - csx, d2[1] - csy, bound + shape_bound(ty2, r2, h2x, h2y) + C.margin))
+                    continue;
+                if (ty != 0 || ty2 != 0) {
+                    // the term's Jacobian over both shapes' states, one input at a time
+                    const T ca2 = ty2 == 0 ? T(1) : m_cos(d2[2]);
+                    const T sa2 = ty2 == 0 ? T(0) : m_sin(d2[2]);
+                    T f0, f1, r0, r1;
+                    body_body_v<T, T>(C, ty, ro, hx, hy, ty2, r2, h2x, h2y, denom_self, csx, csy,
+                                      vsx, vsy, B.ca, B.sa, B.om, d2[0], d2[1], d2[3], d2[4], ca2,
+                                      sa2, d2[5], f0, f1, r0, r1);
+                    const T L0 = owx + r0, L1 = owy + r1;
+                    const T h0 = g_fx - g_tau * L1, h1 = g_fy + g_tau * L0;
+                    const T hr0 = g_tau * f1, hr1 = -(g_tau * f0);
+                    g_owx += g_tau * f1;
+                    g_owy -= g_tau * f0;
+                    const T in[12] = {csx, csy, vsx, vsy, B.th, B.om,
+                                      d2[0], d2[1], d2[3], d2[4], d2[2], d2[5]};
+                    const bool mv = shape_moves(tb, o2) && L.agent == 0;
+                    for (int k = 0; k < 12; ++k) {
+                        Dual<T, 1> x[12], o0, o1, l0, l1;
+#pragma unroll
+                        for (int q = 0; q < 12; ++q) x[q] = dseed(in[q], q, k);
+                        body_body_v<T, Dual<T, 1>>(C, ty, ro, hx, hy, ty2, r2, h2x, h2y,
+                                                   denom_self, x[0], x[1], x[2], x[3],
+                                                   m_cos(x[4]), m_sin(x[4]), x[5], x[6], x[7],
+                                                   x[8], x[9], m_cos(x[10]), m_sin(x[10]), x[11],
+                                                   o0, o1, l0, l1);
+                        const T adj = h0 * o0.d[0] + h1 * o1.d[0] + hr0 * l0.d[0] + hr1 * l1.d[0];
+                        if (k == 0) g_csx += adj;
+                        else if (k == 1) g_csy += adj;
+                        else if (k == 2) g_vsx += adj;
+                        else if (k == 3) g_vsy += adj;
+                        else if (k == 4) g_thd += adj;
+                        else if (k == 5) g_omd += adj;
+                        else if (mv) {
+                            // the other shape's state: pos x, pos y, vel x, vel y, angle, spin
+                            const int slot = k == 6 ? 0 : k == 7 ? 1 : k == 8 ? 3 : k == 9 ? 4
+                                           : k == 10 ? 2 : 5;
+                            gin[6 * o2 + slot] += adj;
+                        }
+                    }
+                    continue;
+                }
                 T gx, gy;
                 pair_force(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4],
                            ro + r2 + C.margin, denom_self, gx, gy);
@@ -731,8 +994,8 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
             g_owy += g_csy - g_vsx * B.om;
             g_tvx += g_vsx;
             g_tvy += g_vsy;
-            g_om += -g_vsx * owy + g_vsy * owx;
-            g_th += -g_owx * owy + g_owy * owx;
+            g_om += -g_vsx * owy + g_vsy * owx + g_omd;
+            g_th += -g_owx * owy + g_owy * owx + g_thd;
         }
         if (L.agent == 0) {
             T *gi = gin + 6 * N + 6 * o;
@@ -878,26 +1141,30 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
                                           gi.px, gi.py, gi.vx, gi.vy);
                     }
                 }
-                // obstacles: the agent's adjoint, and the moving circles' in agent order
+                // obstacles: the agent's adjoint, and the moving shapes' in agent order
                 for (int o = 0; o < N; ++o) {
-                    T opx = T(0), opy = T(0), ovx = T(0), ovy = T(0);
-                    if (L.active)
+                    const bool mv = shape_moves(tb, o);
+                    T op[6];
+                    if (L.active) {
                         ob_force_adj(C, tb, obc, o, in.px, in.py, in.vx, in.vy, L.pr.radius,
-                                     L.dd, gFx, gFy, gi, opx, opy, ovx, ovy);
-                    if (!shape_moves(tb, o)) continue;
-                    const bool fl = opx != T(0) || opy != T(0) || ovx != T(0) || ovy != T(0);
+                                     L.dd, gFx, gFy, gi, mv, op);
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 6; ++q) op[q] = T(0);
+                    }
+                    if (!mv) continue;
+                    bool fl = false;
+#pragma unroll
+                    for (int q = 0; q < 6; ++q) fl = fl || op[q] != T(0);
                     if (__ballot(fl) == 0) continue;  // no agent of the wave touches it
                     // the env's agent-0 lane keeps the shape's adjoint; the other lanes'
                     // copies of the sums are not used
                     T *g2 = gprev + 6 * o;
-                    T acc[4] = {g2[0], g2[1], g2[3], g2[4]};
-                    const T val[4] = {opx, opy, ovx, ovy};
-                    env_ordered_sums<PA, 4>(acc, val, fl, L.lane);
+                    T acc[6] = {g2[0], g2[1], g2[2], g2[3], g2[4], g2[5]};
+                    env_ordered_sums<PA, 6>(acc, op, fl, L.lane);
                     if (L.agent == 0) {
-                        g2[0] = acc[0];
-                        g2[1] = acc[1];
-                        g2[3] = acc[2];
-                        g2[4] = acc[3];
+#pragma unroll
+                        for (int q = 0; q < 6; ++q) g2[q] = acc[q];
                     }
                 }
                 if (C.soft_walls)

@@ -234,7 +234,8 @@ enum : unsigned {
     FT_DIFF = 1u << 7,
     FT_BICY = 1u << 8,
     FT_DRONE = 1u << 9,
-    FT_ALL = 0x3ffu,
+    FT_SHAPES = 1u << 10,  // box or segment obstacles in a body world (body kernels only)
+    FT_ALL = 0x7ffu,
 };
 // Profiles compiled besides FT_ALL (float32): 2-D fleets with obstacles and walls under
 // Euler, drone fleets (config 4), holonomic fleets with movable bodies
@@ -250,6 +251,7 @@ template <unsigned F, typename T> __device__ __forceinline__ Cst<T> fold_cst(Cst
     if (!(F & FT_OBST)) C.N = 0;
     if (!(F & FT_WALL)) C.soft_walls = 0;
     if (!(F & FT_CLAMP)) C.clamp = 0;
+    if (!(F & FT_SHAPES)) C.round_only = 1;
     return C;
 }
 

@@ -77,6 +77,7 @@ template <typename T> struct Cst {
     int boxes;     // some agent is a box: the box-aware contact pass
     int wheel;     // WorldConfig.wheel_contacts: contact torques + wheel_contact (no grad)
     int per_env;   // parameter rows per (env, agent) instead of per agent
+    int round_only;  // every obstacle is a circle (the body pass takes no box / segment terms)
     T lat_grip, turn_cap;
     int fast_div;  // neighbour radius <= 2^20: contact distances are short-division divisors
     int rk4;       // Integrator.RK4 instead of semi-implicit Euler

@@ -103,6 +103,7 @@ template <typename T> static int fill_cst(const swarp_desc_t *d, double skin, Cs
     C.clamp = d->clamp_bounds;
     C.boxes = d->has_boxes ? 1 : 0;
     C.per_env = d->params_per_env ? 1 : 0;
+    C.round_only = d->obstacle_types == 1 ? 1 : 0;
     C.wheel = d->wheel_contacts ? 1 : 0;
     C.lat_grip = (T)d->lat_grip;
     C.turn_cap = (T)d->turn_cap;
@@ -209,6 +210,8 @@ static unsigned world_features(const swarp_desc_t *d, bool body)
     if (d->integrator == SWARP_RK4) f |= FT_RK4;
     if (d->max_overlap > 0.0) f |= FT_SAT;
     if (!body && d->n_obstacles > 0) f |= FT_OBST;
+    // box or segment shapes among the obstacles of a body world (0: not known)
+    if (body && d->obstacle_types != 1) f |= FT_SHAPES;
     if (d->soft_walls) f |= FT_WALL;
     if (d->clamp_bounds) f |= FT_CLAMP;
     const unsigned models = d->fleet_models ? (unsigned)d->fleet_models : ~0u;

@@ -152,6 +152,7 @@ class Stepper:
             self._bounds = (0.0, 0.0, 0.0, 0.0)
 
         self.n_obstacles = 0
+        self._obstacle_types = 0  # bit set of the obstacle shape types present
         self.obstacles: Obstacles | None = None
         self._obs: dict[str, torch.Tensor] = {}
         self.any_movable = False
@@ -275,25 +276,18 @@ class Stepper:
                 raise NotImplementedError(
                     "movable bodies: this build steps them with at most 64 agents per env and "
                     "index-ordered lists")
-            moving = self._moving_shapes(self._obs["kind"], self._obs["body"])
-            if bool(((self._obs["type"] != 0) & moving).any()):
-                raise NotImplementedError(
-                    "movable bodies: only circle shapes (the disc variant of the body pass)")
         self.obstacles = obstacles
         self.n_obstacles = n
         self._obs_envs = n_envs
         self.any_movable = movable
+        # shape types present (bit t: type t), for the kernel instance without box / segment
+        # terms when every obstacle is a circle
+        self._obstacle_types = sum(1 << int(t) for t in torch.unique(self._obs["type"].cpu())) if n else 0
         self.ob_state = self._body_seed() if movable else None
         self.ob_trajectory = None
         self._descs.clear()
         self._tape_sizes.clear()
         self.mutation_version += 1
-
-    @staticmethod
-    def _moving_shapes(kind: torch.Tensor, body: torch.Tensor) -> torch.Tensor:
-        """Bool [N]: the shape belongs to a movable body (its root is MOVABLE)."""
-        root = body.long()
-        return (body[root] == body) & (kind[root] == 1)
 
     def _body_seed(self) -> torch.Tensor:
         """Obstacle state [n_envs, 12 N]: per shape its installed pose and velocity, then
@@ -388,6 +382,7 @@ class Stepper:
             d.obs_mass = o["mass"].data_ptr()
             d.obs_inertia = o["inertia"].data_ptr()
             d.obs_body_off = o["off"].data_ptr()
+        d.obstacle_types = self._obstacle_types
         d.lin_damping = float(self.world.obstacle_linear_damping)
         d.ang_damping = float(self.world.obstacle_angular_damping)
         d.integrator = _lib.RK4 if self.world.integrator == Integrator.RK4 else _lib.EULER

@@ -50,6 +50,7 @@ struct Case {
     bool drone, boxes, walls, bodies, rk4, grid;
     int models;  // 0 holonomic, 1 diff/bicycle mix, 3 drone
     bool per_env = false;  // per-env parameter rows (the body pass then reads the shared)
+    bool shaped = false;   // movable bodies of box and segment shapes too
 };
 
 template <typename T>
@@ -130,8 +131,8 @@ int run_case(const Case &c)
         for (int o = 0; o < N; ++o) {
             orad[o] = T(0.1);
             ohalf[2 * o] = T(0.15);
-            ohalf[2 * o + 1] = T(c.bodies ? 0 : 0.08);
-            otype[o] = c.bodies ? 0 : o % 3;
+            ohalf[2 * o + 1] = T(c.bodies && !c.shaped ? 0 : 0.08);
+            otype[o] = c.bodies && !c.shaped ? 0 : o % 3;
         }
         d.obs_pos = opos;
         d.obs_radius = orad;
@@ -239,6 +240,7 @@ int main(int argc, char **argv)
         {"bodies f32 A=64",      2, 64, 3, 2, 16, 2, 5, false, false, true,  true,  false, false, 0},
         {"bodies drones f32 A=8", 9, 8, 3, 2, 8, 4, 5, true,  false, true,  true,  false, false, 3},
         {"bodies per-env f32",   6, 12, 3, 2, 8, 2, 5, false, false, true,  true,  false, false, 0, true},
+        {"bodies shaped f32",    6, 12, 3, 2, 8, 2, 5, false, false, true,  true,  false, false, 0, false, true},
         {"drones f32 64x8",     16, 8, 6, 2, 8, 4, 0, true,  false, false, false, false, false, 3},
         {"drones f64 A=3",       4, 3, 5, 1, 4, 4, 0, true,  false, false, false, false, false, 3},
         {"mixed f32 obstacles",  9, 32, 4, 2, 16, 2, 6, false, false, true,  false, false, false, 1},

@@ -222,10 +222,18 @@ def test_stepper_reach_check_and_unsupported_features():
     for idx in (0, 1):  # every index carries the state of its body (rooted at 0)
         assert torch.allclose(ob[0, 1, idx, 0:3], torch.tensor([*origin, 0.5], dtype=torch.float64))
         assert torch.allclose(ob[0, 1, idx, 3:5], torch.tensor([0.1, 0.2], dtype=torch.float64))
-    with pytest.raises(NotImplementedError, match="circle"):
-        st.set_obstacles(Obstacles(pos=torch.zeros(1, 1, 2), radius=torch.ones(1),
-                                   shape=torch.ones(1, dtype=torch.int32),
-                                   kind=torch.ones(1, dtype=torch.int32)))
+    # box and segment shapes move with their bodies too (the body pass of any shape)
+    st.set_obstacles(Obstacles(pos=torch.zeros(1, 1, 2), radius=torch.ones(1),
+                               shape=torch.ones(1, dtype=torch.int32),
+                               kind=torch.ones(1, dtype=torch.int32)))
+    assert st.any_movable
+    # the descriptor names the shape types present (bit t: type t), which picks the body
+    # kernel instance: circles only run the one compiled without box / segment terms
+    assert st.desc(1, 2).obstacle_types == 0b10
+    st.set_obstacles(Obstacles(pos=torch.zeros(1, 2, 2), radius=torch.ones(2),
+                               shape=torch.tensor([0, 2], dtype=torch.int32),
+                               kind=torch.ones(2, dtype=torch.int32)))
+    assert st.desc(1, 2).obstacle_types == 0b101
     # drone fleets push bodies by their planar state (the body kernels' DRONE instances)
     dr = Stepper([drone_config()], device="cpu")
     dr.set_obstacles(Obstacles(pos=torch.zeros(1, 1, 2), radius=torch.ones(1),

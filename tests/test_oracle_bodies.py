@@ -306,3 +306,89 @@ def test_drone_fleet_pushes_a_body():
         am[idx] -= h
         fd = (loss(ap) - loss(am)) / (2 * h)
         assert ga[idx] == pytest.approx(fd, rel=2e-6, abs=1e-9)
+
+
+def _shapes(E, centers, radius, types, half, kind, body, off, mass, inertia, angle=None):
+    """Obstacles of any shape type (0 circle, 1 box, 2 segment) with body fields."""
+    n = len(centers)
+    d = {"pos": np.broadcast_to(np.asarray(centers, dtype=np.float64), (E, n, 2)).copy(),
+         "radius": np.asarray(radius, dtype=np.float64), "type": np.asarray(types, np.int32),
+         "half": np.asarray(half, dtype=np.float64), "kind": np.asarray(kind, np.int32),
+         "body": np.asarray(body, np.int32), "body_off": np.asarray(off, dtype=np.float64),
+         "mass": np.asarray(mass, dtype=np.float64),
+         "inertia": np.asarray(inertia, dtype=np.float64)}
+    if angle is not None:
+        d["angle"] = np.broadcast_to(np.asarray(angle, dtype=np.float64), (E, n)).copy()
+    return obstacles_np(d, E)
+
+
+def test_box_body_off_centre_push_closed_form():
+    """One substep of a disc agent pressing on a box body's face off its centre line
+    (swarp/core/bodies.py:80-127): the force on the body is minus box_force, the lever
+    runs from the body origin to the agent's centre (r = p - c), so the body spins."""
+    world = _world(collision_k=100.0, collision_c=1.0, collision_margin=0.02)
+    cfgs = _agents(1, radius=0.1)
+    ob = _shapes(1, [[0.2, 0.0]], [0.0], [1], [[0.1, 0.05]], [MOVABLE], [0], [[0.0, 0.0]],
+                 [2.0], [0.3])
+    s0 = pack_state({"pos": [[[0.0, 0.03]]], "vel": [[[0.3, 0.0]]]})
+    acts = np.array([[[[0.3, 0.0]]]])
+    dt = 0.01
+    _, obo = _run(cfgs, world, dt, 1, s0, acts, ob)
+    dd = 1.0 + 1.0 * dt / 1.0
+    # face x = -0.1 of the box: normal (-1, 0), overlap = reach - 0.1 = 0.02, vn = -0.3
+    coef = (100.0 * 0.02 - 1.0 * (-0.3)) / dd
+    R = np.array([coef, 0.0])                      # minus the agent's force coef * (-1, 0)
+    lever = np.array([0.0 - 0.2, 0.03 - 0.0])      # r = p - c, the root's offset is 0
+    tau = lever[0] * R[1] - lever[1] * R[0]
+    decay, adecay = 1.0 - 10.0 * dt, 1.0 - 10.0 * dt
+    body = obo[0, 0, 6:12]
+    assert body[3] == pytest.approx(R[0] / 2.0 * dt * decay, rel=1e-13) and body[4] == 0.0
+    assert body[5] == pytest.approx(tau / 0.3 * dt * adecay, rel=1e-13) and body[5] < 0.0
+    assert body[2] == pytest.approx(body[5] * dt, rel=1e-13)
+
+
+def test_segment_body_and_box_scenery():
+    """A capsule body pushed along its axis into static box scenery: the agent's push
+    moves it, and the box stops it.  The reference's body-body term takes a round body as
+    a disc of its radius at its centre against a box (swarp/core/bodies.py:238-242), so
+    the capsule's centre, not its end, is what the box holds back."""
+    world = _world(collision_k=200.0, collision_c=2.0, collision_margin=0.01, bounds=None)
+    cfgs = _agents(1, radius=0.06)
+    s0 = pack_state({"pos": [[[-0.35, 0.0]]]})
+    acts = np.broadcast_to(np.array([1.0, 0.0]), (60, 1, 1, 2)).copy()
+    x = {}
+    for box_x in (0.7, 5.0):
+        ob = _shapes(1, [[0.0, 0.0], [box_x, 0.0]], [0.05, 0.0], [2, 1],
+                     [[0.2, 0.0], [0.05, 0.4]], [MOVABLE, 0], [0, 1], [[0.0, 0.0], [0.0, 0.0]],
+                     [1.0, 1.0], [0.05, 1.0])
+        _, obo = _run(cfgs, world, 0.05, 4, s0, acts, ob)
+        x[box_x] = obo[:, 0, 0]
+        np.testing.assert_array_equal(obo[:, 0, 6:12], np.broadcast_to(obo[0, 0, 6:12], (60, 6)))
+    assert x[5.0][-1] > 2.0, "the capsule was not pushed"
+    assert x[0.7].max() < 0.7 and x[0.7][-1] < 0.6, "the box did not stop the capsule"
+
+
+def test_box_and_segment_body_adjoint_matches_finite_differences():
+    """Every adjoint path of box and segment shapes in the body pass: agent reactions on a
+    box + capsule compound body (lever p - c on the box, the closest core point on the
+    capsule), the body-body terms box vs circle, box vs capsule, capsule vs box, circle vs
+    box, and the agents' own forces from the moving box and capsule shapes."""
+    world = _world(collision_k=60.0, collision_c=0.8, collision_margin=0.02, bounds=None,
+                   obstacle_linear_damping=3.0, obstacle_angular_damping=2.0)
+    cfgs = _agents(3, mode=ControlMode.ACCELERATION, radius=0.07, big=True)
+    th = 0.3
+    off1 = np.array([0.05, 0.21])
+    c1 = np.array([np.cos(th) * off1[0] - np.sin(th) * off1[1],
+                   np.sin(th) * off1[0] + np.cos(th) * off1[1]])
+    centers = [[0.0, 0.0], list(c1), [c1[0] + 0.01, c1[1] + 0.1], [0.0, -0.2], [0.2, -0.1]]
+    ob = _shapes(1, centers, [0.0, 0.04, 0.0, 0.08, 0.06], [1, 2, 1, 0, 0],
+                 [[0.12, 0.07], [0.15, 0.0], [0.06, 0.05], [0.0, 0.0], [0.0, 0.0]],
+                 [MOVABLE, MOVABLE, MOVABLE, 0, MOVABLE], [0, 0, 2, 3, 4],
+                 [[0.0, 0.0], list(off1), [0.0, 0.0], [0.0, 0.0], [0.0, 0.0]],
+                 [0.8, 0.8, 0.5, 1.0, 0.4], [0.04, 0.04, 0.02, 1.0, 0.01],
+                 angle=[th, th, -0.4, 0.0, 0.0])
+    s0 = pack_state({"pos": [[[-0.24, 0.05], [-0.1, 0.36], [0.2, -0.26]]],
+                     "vel": [[[0.5, 0.0], [0.1, -0.4], [0.0, 0.3]]]})
+    acts = np.random.default_rng(8).normal(size=(5, 1, 3, 2)) * 0.5
+    st, obo = _fd_bodies(cfgs, world, 0.05, 2, s0, acts, ob, tol=5e-7, seed=3)
+    assert np.abs(obo[-1, 0, 6 * 5 + 5]).max() > 1e-4, "the compound body never turned"
