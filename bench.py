@@ -7,9 +7,10 @@ uniform in the 4x4 arena (walls at +-2), zero initial velocity, actions uniform 
 
 One benchmark step = one BPTT iteration through the public API:
 ``rollout(stepper, state0, actions)`` (32 env steps, one HIP launch), the loss, and
-``loss.backward()`` (one HIP launch).  ``value`` = n_envs * T * steps / elapsed, with
-inputs already resident in HBM.  The per-kernel durations for the roofline come from
-HIP events recorded around each launch on its own stream during the timed steps.
+``loss.backward()`` (one HIP launch).  ``value`` = n_envs * T * steps / elapsed over a
+timed loop with inputs already resident in HBM; the per-kernel durations for the
+roofline come from HIP events recorded around each launch, on the stream it goes to, in
+a second timed loop of the same steps (the events' markers stay out of the first).
 
 ``cpu_baseline`` times the CPU oracle (oracle/swarp_oracle.c, OpenMP over envs) on a
 bounded sample of the same workload on this host's cores.
@@ -262,12 +263,41 @@ def event_pool(n):
     return pool
 
 
+def timed_loops(step, steps):
+    """Two timed loops of `steps` iterations, each bracketed by synchronisations: the
+    first gives the wall time (no timing events on the stream: recording them adds
+    device-side markers between the kernels), the second records a HIP event pair around
+    every fwd / bwd launch, on the stream it goes to, for the kernel durations.
+    Returns (seconds of the first loop, {"fwd": [s, ...], "bwd": [s, ...]})."""
+    import torch
+
+    import swarp_amd.autograd as ag
+
+    torch.cuda.synchronize()
+    gc.collect()  # the set-up's garbage: a full collection would land in the timed steps
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    ag.EVENT_POOL = event_pool(2 * 2 * steps)
+    gc.collect()
+    ag.KERNEL_EVENTS = []
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    events, ag.KERNEL_EVENTS, ag.EVENT_POOL = ag.KERNEL_EVENTS, None, None
+    dur = {"fwd": [], "bwd": []}
+    for k, e0, e1 in events:
+        dur[k].append(e0.elapsed_time(e1) * 1e-3)
+    return el, dur
+
+
 def run_other(args):
     """Time one BPTT iteration of BASELINE configs[2..4] through the public API and print
     the same JSON line as the headline run (no CPU baseline, no Environment leg)."""
     import torch
 
-    import swarp_amd.autograd as ag
     from swarp_amd import TorchState, rollout
 
     st, state, acts, goals, fwd_b, bwd_b, desc, kind = {
@@ -298,19 +328,7 @@ def run_other(args):
 
     for _ in range(args.warmup):
         step()
-    ag.EVENT_POOL = event_pool(2 * 2 * args.steps)
-    torch.cuda.synchronize()
-    gc.collect()  # the set-up's garbage: a full collection would land in the timed steps
-    ag.KERNEL_EVENTS = []
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    el = time.perf_counter() - t0
-    events, ag.KERNEL_EVENTS, ag.EVENT_POOL = ag.KERNEL_EVENTS, None, None
-    dur = {"fwd": [], "bwd": []}
-    for k, e0, e1 in events:
-        dur[k].append(e0.elapsed_time(e1) * 1e-3)
+    el, dur = timed_loops(step, args.steps)
     kernels = {}
     for k, per in (("fwd", fwd_b), ("bwd", bwd_b)):
         d = sum(dur[k]) / max(len(dur[k]), 1)
@@ -347,7 +365,6 @@ def main():
         return
     import torch
 
-    import swarp_amd.autograd as ag
     from swarp_amd import rollout
 
     E, A, T, S = args.envs, args.agents, args.horizon, args.substeps
@@ -364,20 +381,7 @@ def main():
 
     for _ in range(args.warmup):
         bptt_step()
-    ag.EVENT_POOL = event_pool(2 * 2 * args.steps)
-    torch.cuda.synchronize()
-    gc.collect()  # the set-up's garbage: a full collection would land in the timed steps
-    ag.KERNEL_EVENTS = []
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        bptt_step()
-    torch.cuda.synchronize()
-    el = time.perf_counter() - t0
-    events = ag.KERNEL_EVENTS
-    ag.KERNEL_EVENTS = ag.EVENT_POOL = None
-    dur = {"fwd": [], "bwd": []}
-    for kind, e0, e1 in events:
-        dur[kind].append(e0.elapsed_time(e1) * 1e-3)
+    el, dur = timed_loops(bptt_step, args.steps)
     ms_per_step = el / args.steps * 1e3
     value = E * T * args.steps / el
 

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 13
+#define SWARP_ABI_VERSION 14
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -299,6 +299,13 @@ int swarp_edge_index(int32_t n_envs, int32_t n_agents, int32_t max_neighbors,
 int swarp_edge_index_noalloc(int32_t n_envs, int32_t n_agents, int32_t max_neighbors,
                              const int32_t *idx, const int32_t *cnt, int64_t capacity,
                              int64_t *edge_index, int64_t *n_edges, void *stream);
+
+/* Default values of the four drone fields of n agents, written in one pass into one
+ * contiguous buffer of 9 n elements of `dtype` (SWARP_F32 or SWARP_F64) laid out as
+ * [z (n), vz (n), attitude (4 n, x y z w), body_rates (3 n)]: zeros, with the identity
+ * quaternion (0, 0, 0, 1) per agent.  Replaces the zero and identity tensors of
+ * fill_state_defaults (swarp/interop/autograd.py:48-68). */
+int swarp_state_defaults(int32_t dtype, int64_t n, void *buf, void *stream);
 
 #ifdef __cplusplus
 }

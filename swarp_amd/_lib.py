@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 F32, F64 = 0, 1
 EULER, RK4 = 0, 1
 LISTS_BRUTE, LISTS_GRID = 0, 1
@@ -177,6 +177,10 @@ SIGNATURES = {
     "swarp_edge_index_noalloc": (
         [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
          ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "swarp_state_defaults": (
+        [ctypes.c_int32, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p],
         ctypes.c_int,
     ),
 }

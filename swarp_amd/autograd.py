@@ -77,16 +77,20 @@ def fill_state_defaults(state: TorchState) -> TorchState:
         return state
     ref = state.pos
     e, a = ref.shape[0], ref.shape[1]
-    # the missing fields are disjoint views of one zeroed allocation (one fill, not four)
-    buf = torch.zeros(9 * e * a, device=ref.device, dtype=ref.dtype)
     n = e * a
+    # the missing fields are disjoint views of one allocation [z | vz | attitude |
+    # body_rates], written by one library launch on a GPU (zeros and identity
+    # quaternions), by torch elsewhere
+    if ref.is_cuda and ref.dtype in (torch.float32, torch.float64):
+        buf = torch.empty(9 * n, device=ref.device, dtype=ref.dtype)
+        _lib.check(_lib.load().swarp_state_defaults(
+            0 if ref.dtype == torch.float32 else 1, n, buf.data_ptr(), _stream(ref)))
+    else:
+        buf = torch.zeros(9 * n, device=ref.device, dtype=ref.dtype)
+        buf[2 * n:6 * n].view(n, 4)[:, 3] = 1.0
     z = state.z if state.z is not None else buf[:n].view(e, a)
     vz = state.vz if state.vz is not None else buf[n:2 * n].view(e, a)
-    if state.attitude is not None:
-        att = state.attitude
-    else:
-        att = buf[2 * n:6 * n].view(e, a, 4)
-        att[..., 3] = 1.0
+    att = state.attitude if state.attitude is not None else buf[2 * n:6 * n].view(e, a, 4)
     br = state.body_rates if state.body_rates is not None else buf[6 * n:].view(e, a, 3)
     return state._replace(z=z, vz=vz, attitude=att, body_rates=br)
 

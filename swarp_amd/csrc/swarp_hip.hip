@@ -555,6 +555,19 @@ template <typename T> static int nav_obs(const swarp_desc_t *d, const swarp_nav_
     return 0;
 }
 
+// Default drone fields [z n | vz n | attitude 4n | body_rates 3n]: every element 0 except
+// the w component of each quaternion.  Four consecutive elements per lane.
+template <typename T> __global__ void k_state_defaults(int64_t n, T *buf)
+{
+    const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    const int64_t end = 9 * n;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int64_t i = i0 + k;
+        if (i < end) buf[i] = (i >= 2 * n && i < 6 * n && ((i - 2 * n) & 3) == 3) ? T(1) : T(0);
+    }
+}
+
 extern "C" {
 
 int swarp_abi_version(void) { return SWARP_ABI_VERSION; }
@@ -736,6 +749,26 @@ int swarp_nav_obs(const swarp_desc_t *desc, const swarp_nav_t *nav, void *stream
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32) return nav_obs<float>(desc, nav, st);
     return nav_obs<double>(desc, nav, st);
+}
+
+int swarp_state_defaults(int32_t dtype, int64_t n, void *buf, void *stream)
+{
+    g_err[0] = 0;
+    if (dtype != SWARP_F32 && dtype != SWARP_F64) return fail("dtype must be SWARP_F32 or SWARP_F64");
+    if (n < 0 || n > (int64_t)1 << 40) return fail("n out of range");
+    if (n == 0) return 0;
+    if (!buf) return fail("buf must be set");
+    const int64_t items = (9 * n + 3) / 4;
+    const unsigned blocks = (unsigned)((items + 255) / 256);
+    if (dtype == SWARP_F32)
+        hipLaunchKernelGGL(k_state_defaults<float>, dim3(blocks), dim3(256), 0, (hipStream_t)stream,
+                           n, (float *)buf);
+    else
+        hipLaunchKernelGGL(k_state_defaults<double>, dim3(blocks), dim3(256), 0,
+                           (hipStream_t)stream, n, (double *)buf);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(hipGetErrorString(e));
+    return 0;
 }
 
 int swarp_edge_index(int32_t n_envs, int32_t n_agents, int32_t max_neighbors, const int32_t *idx,

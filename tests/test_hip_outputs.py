@@ -79,3 +79,28 @@ def test_trajectory_matches_final_and_defaults():
     for s in traj:
         assert torch.equal(s.attitude, ident) and torch.equal(s.z, torch.zeros(E, A, device="cuda"))
     assert torch.equal(traj[-1].pos, final.pos)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
+@pytest.mark.parametrize("E,A", [(3, 5), (1, 1), (16000, 16)])
+def test_fill_state_defaults_on_device_equals_the_host_defaults(E, A, dtype):
+    """swarp_state_defaults (one launch) writes what the host path builds with torch:
+    zeros and the identity quaternion, for sizes whose 9 E A elements are not a multiple
+    of the four elements a lane writes; fields the caller gave are kept."""
+    from swarp_amd.autograd import fill_state_defaults
+
+    def defaults(dev):
+        pos = torch.zeros(E, A, 2, device=dev, dtype=dtype)
+        z = torch.zeros(E, A, device=dev, dtype=dtype)
+        return fill_state_defaults(TorchState(pos, z, torch.zeros(E, A, 2, device=dev, dtype=dtype),
+                                              z, z))
+
+    got, want = defaults("cuda"), defaults("cpu")
+    for name in TAIL:
+        g, w = getattr(got, name), getattr(want, name)
+        assert g.dtype == dtype and g.shape == w.shape and torch.equal(g.cpu(), w)
+    assert torch.equal(want.attitude[..., 3], torch.ones(E, A, dtype=dtype))
+    vz = torch.full((E, A), 7.0, device="cuda", dtype=dtype)
+    pos = torch.zeros(E, A, 2, device="cuda", dtype=dtype)
+    s = fill_state_defaults(TorchState(pos, pos[..., 0], pos, pos[..., 0], pos[..., 0], vz=vz))
+    assert s.vz is vz and torch.equal(s.z.cpu(), torch.zeros(E, A, dtype=dtype))

@@ -38,6 +38,18 @@ def test_library_exports_every_declared_function():
     assert lib.swarp_last_error() == b""
 
 
+def test_state_defaults_rejects_bad_arguments_without_gpu():
+    """swarp_state_defaults checks its arguments on the host; n = 0 launches nothing."""
+    lib = _lib.load()
+    assert lib.swarp_state_defaults(2, 4, None, None) != 0
+    assert b"dtype" in lib.swarp_last_error()
+    assert lib.swarp_state_defaults(0, -1, None, None) != 0
+    assert lib.swarp_state_defaults(0, 4, None, None) != 0
+    assert b"buf" in lib.swarp_last_error()
+    assert lib.swarp_state_defaults(1, 0, None, None) == 0
+    assert lib.swarp_last_error() == b""
+
+
 def test_struct_layout_matches_header(tmp_path):
     prog = tmp_path / "layout.c"
     desc_fields = [f for f, _ in _lib.SwarpDesc._fields_]
