@@ -303,8 +303,8 @@ int swarp_edge_index_noalloc(int32_t n_envs, int32_t n_agents, int32_t max_neigh
 /* Default values of the four drone fields of n agents, written in one pass into one
  * contiguous buffer of 9 n elements of `dtype` (SWARP_F32 or SWARP_F64) laid out as
  * [z (n), vz (n), attitude (4 n, x y z w), body_rates (3 n)]: zeros, with the identity
- * quaternion (0, 0, 0, 1) per agent.  Replaces the zero and identity tensors of
- * fill_state_defaults (swarp/interop/autograd.py:48-68). */
+ * quaternion (0, 0, 0, 1) per agent.  `buf` must be 16-byte aligned.  Replaces the zero
+ * and identity tensors of fill_state_defaults (swarp/interop/autograd.py:48-68). */
 int swarp_state_defaults(int32_t dtype, int64_t n, void *buf, void *stream);
 
 #ifdef __cplusplus

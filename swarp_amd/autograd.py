@@ -18,8 +18,9 @@ and ``warp_step`` writes into the stepper's two recycled output slots
 (``swarp/core/stepper.py:688-710``).
 
 For a fleet without drones the four drone fields (``z, vz, attitude, body_rates``) are
-not stepped: every output state carries the input's drone tensors, whose values the
-reference would have copied unchanged (``swarp/dynamics/kernels.py:1856-1864``).
+not stepped: every output state carries its own copies of the input's drone tensors,
+whose values the reference copies unchanged (``swarp/dynamics/kernels.py:1856-1864``),
+with their gradient passed through.
 """
 
 from __future__ import annotations
@@ -459,9 +460,13 @@ def _assemble(stepper: Stepper, state: TorchState, outs, T: int, given=(True,) *
     final = TorchState(*final_f, *final_tail)
 
     def build():
-        # one unbind per field (a single autograd node) instead of T - 1 selects per field
+        # one unbind per field (a single autograd node) instead of T - 1 selects per field;
+        # the passed-through fields of the T - 1 states as one broadcast copy per field
+        # (each state owns its own slice) instead of T - 1 copies
         per_step = [f.unbind(0) for f in traj_f] if T > 1 else []
-        steps = [TorchState(*(u[t] for u in per_step), *(x.clone() for x in tail))
+        tails = ([x.unsqueeze(0).expand(T - 1, *x.shape).clone().unbind(0) for x in tail]
+                 if T > 1 else [])
+        steps = [TorchState(*(u[t] for u in per_step), *(v[t] for v in tails))
                  for t in range(T - 1)]
         steps.append(final)
         return steps

@@ -53,16 +53,18 @@ template <typename T> struct ObIO {
 // 1 + c sub_dt / m of its parameter row in the table the pass reads.
 template <typename T> struct BodyRow {
     T r, dd;
+    Dv<T> ddv;  // dd as a prepared divisor
 };
 
 template <typename T, int PA>
 __device__ __forceinline__ BodyRow<T> body_row(const Cst<T> &C, const ObTab<T> &tb,
                                                const Lane<T, PA> &L)
 {
-    if (!tb.bprm) return BodyRow<T>{L.pr.radius, L.dd};
+    if (!tb.bprm) return BodyRow<T>{L.pr.radius, L.dd, L.ddv};
     const int ag = L.real ? L.agent : 0;
     const T m = tb.bprm[(size_t)ag * 22 + 1];
-    return BodyRow<T>{tb.bprm[(size_t)ag * 22], T(1) + C.c * C.sub_dt / m};
+    const T dd = T(1) + C.c * C.sub_dt / m;
+    return BodyRow<T>{tb.bprm[(size_t)ag * 22], dd, divisor(dd, true)};
 }
 
 // sin and cos of a body angle (the portable evaluation of swarp_pmath.h, as the oracle's)
@@ -220,10 +222,12 @@ template <typename T> __device__ __forceinline__ Dual<T, 1> dseed(T x, int k, in
 }
 
 // One obstacle's force on an agent, the obstacle's pose read from the env's state `od`
-// (_obstacle_forces body, swarp/core/collisions.py:690-743).
-template <typename T>
+// (_obstacle_forces body, swarp/core/collisions.py:690-743).  DD: the damping denominator
+// as a value or a prepared divisor (the same bits).
+template <typename T, typename DD>
 __device__ __forceinline__ void ob_force(const Cst<T> &C, const ObTab<T> &tb, const T *od, int o,
-                                         T px, T py, T vx, T vy, T ra, T dd, T &fx, T &fy)
+                                         T px, T py, T vx, T vy, T ra, const DD &dd, T &fx,
+                                         T &fy)
 {
     fx = T(0);
     fy = T(0);
@@ -352,7 +356,7 @@ __device__ __forceinline__ typename MaskT<PA>::type forces_b(
             const int j = L.base + b;
             T gx, gy;
             pair_force(C, st.px - lx[j], st.py - ly[j], st.vx - lvx[j], st.vy - lvy[j],
-                       ra + lr[j] + C.margin, L.dd, gx, gy);
+                       ra + lr[j] + C.margin, L.ddv, gx, gy);
             fx += gx;
             fy += gy;
         }
@@ -360,7 +364,7 @@ __device__ __forceinline__ typename MaskT<PA>::type forces_b(
     T sx = T(0), sy = T(0);
     for (int o = 0; o < tb.N; ++o) {
         T gx, gy;
-        ob_force(C, tb, od, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.dd, gx, gy);
+        ob_force(C, tb, od, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv, gx, gy);
         sx += gx;
         sy += gy;
     }
@@ -511,7 +515,7 @@ __device__ __forceinline__ void body_sum(const Cst<T> &C, const ObTab<T> &tb,
             if (ty == 0) {
                 T gx, gy;
                 pair_force(C, st.px - csx, st.py - csy, st.vx - vsx, st.vy - vsy,
-                           br.r + ro + C.margin, br.dd, gx, gy);
+                           br.r + ro + C.margin, br.ddv, gx, gy);
                 f0 = -gx;
                 f1 = -gy;
             } else {
@@ -862,7 +866,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
                             rvy = st.vy - vsy;
                     const T md = br.r + ro + C.margin;
                     T gx, gy;
-                    pair_force(C, dx, dy, rvx, rvy, md, br.dd, gx, gy);
+                    pair_force(C, dx, dy, rvx, rvy, md, br.ddv, gx, gy);
                     const T f0 = -gx, f1 = -gy;
                     T adx = T(0), ady = T(0), arx = T(0), ary = T(0);
                     pair_force_adj(C, dx, dy, rvx, rvy, md, br.dd, -g_f0, -g_f1, adx, ady, arx,

@@ -301,6 +301,17 @@ __device__ __forceinline__ void lane_init(const Cst<T> &C, const Args<T> &g, Lan
     L.ddv = divisor(L.dd, true);
 }
 
+// Orders one wave's LDS stores before its later LDS loads across lanes, for kernels whose
+// workgroup is that one wave: the LDS executes a wave's instructions in the order they
+// are issued, so the exchange needs only a wavefront-scope fence that keeps the compiler
+// from moving accesses across it -- no s_barrier and no wait for the stores to complete.
+__device__ __forceinline__ void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Whether every real agent of this lane's env stayed within the skin budget.
 template <int PA> __device__ __forceinline__ bool env_all(bool ok, int base)
 {
@@ -388,7 +399,7 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
                                        gx, gy);
             } else {
                 pair_force(C, st.px - lx[j], st.py - ly[j], st.vx - lvx[j], st.vy - lvy[j],
-                           ra + lr[j] + C.margin, L.dd, gx, gy);
+                           ra + lr[j] + C.margin, L.ddv, gx, gy);
             }
             fx += gx;
             fy += gy;
@@ -406,8 +417,8 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
         for (int o = 0; o < C.N; ++o) {
             T gx, gy;
-            obstacle_force(C, g.obs, eN, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.dd, gx, gy,
-                           ocs);
+            obstacle_force(C, g.obs, eN, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv, gx,
+                           gy, ocs);
             sx += gx;
             sy += gy;
         }

@@ -1,6 +1,7 @@
 // lean.hpp -- specialised rollout kernels for fleets of holonomic agents in velocity
 // mode without obstacles (the reference's NavigationScenario default, BASELINE config 1/2).
-// Instantiated by k_holo.hip; the host side sizes the tape with TapeRec.
+// Instantiated by k_holo.hip; the host side sizes the tape with TapeRec.  A workgroup is one
+// wave, so lanes exchange values through LDS with wave_lds_sync instead of a barrier.
 //
 // Same arithmetic, in the same order, as the generic kernels (so the results are
 // bit-identical), with what this fleet does not need removed:
@@ -331,10 +332,10 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
             T Fx = T(0), Fy = T(0);
             if (C.needs_forces) {
                 if (C.collisions) {
-                    __syncthreads();
+                    wave_lds_sync();
                     lp[lane] = p;
                     lv[lane] = v;
-                    __syncthreads();
+                    wave_lds_sync();
                 }
                 lean_forces<T, PA, SAT>(C, lp, lv, lr, base, me, ra, ddv, p.x, p.y, v.x, v.y,
                                         s == 0 || !ok, s == 0, cand, incl, act, wb, Fx, Fy);
@@ -510,7 +511,7 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
 
         // ---- the substeps of step t into LDS: from the tape, or recomputed
         if (TAPE) {
-            __syncthreads();  // the previous step's reverse pass is done with the slots
+            wave_lds_sync();  // the previous step's reverse pass is done with the slots
             P2<T> pp = p, vv = v;
 #pragma unroll
             for (int s = 0; s < TAPE_MAX_S; ++s) {
@@ -536,7 +537,7 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
                     }
                 }
             }
-            __syncthreads();
+            wave_lds_sync();
             v = vout;
         }
         M cand = 0, incl, act;
@@ -545,10 +546,10 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
         bool ok = false;
         for (int s = 0; s < (TAPE ? 0 : S); ++s) {
             P2<T> *sp = slot + s * 128;
-            __syncthreads();
+            wave_lds_sync();
             sp[lane] = p;
             sp[64 + lane] = v;
-            __syncthreads();
+            wave_lds_sync();
             T Fx = T(0), Fy = T(0);
             if (C.needs_forces) {
                 lean_forces<T, PA, SAT>(C, sp, sp + 64, lr, base, me, ra, ddv, p.x, p.y, v.x,
@@ -596,12 +597,12 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
                 const P2<T> q0 = sp[lane], w0 = sp[64 + lane];
                 if (C.collisions) {
                     // publish the force adjoint pre-divided by the damping denominator
-                    __syncthreads();
+                    wave_lds_sync();
                     P2<T> gg;
                     gg.x = gFx * inv_dd;
                     gg.y = gFy * inv_dd;
                     lg[lane] = gg;
-                    __syncthreads();
+                    wave_lds_sync();
                     const M mact = la[s * 64 + lane];
                     M m = lm[s * 64 + lane];
                     while (m) {

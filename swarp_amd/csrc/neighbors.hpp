@@ -6,15 +6,24 @@ namespace swarp {
 
 // --------------------------------------------------------------- neighbour lists
 
-template <typename T, int PA>
+// Padded lists of one state (NeighborGrid.query_into's brute-force order).  Each lane
+// builds the K slots of its row; with STAGE the rows are staged in LDS in (env, agent)
+// order -- the order of the output -- and the wave stores its envs' rows, one contiguous
+// block of idx, with coalesced 16-byte stores (4-byte ones when the block is not 16-byte
+// aligned) instead of K scattered 4-byte stores per lane.  STAGE = false (rows too long
+// for the LDS) writes each row directly.
+template <typename T, int PA, bool STAGE>
 __global__ __launch_bounds__(64) void k_neighbors(const Cst<T> C, const T *pos, int32_t *idx,
                                                   int32_t *cnt, int32_t *tru)
 {
     typedef typename MaskT<PA>::type M;
     constexpr int EPW = 64 / PA;
     __shared__ T lx[64], ly[64];
+    extern __shared__ __align__(16) unsigned char smem[];
+    int32_t *const srows = (int32_t *)smem;  // [EPW * A][K] (STAGE)
     const int lane = threadIdx.x, agent = lane % PA, base = lane - agent;
-    const int env = blockIdx.x * EPW + lane / PA;
+    const int e0 = blockIdx.x * EPW;
+    const int env = e0 + lane / PA;
     const bool active = agent < C.A && env < C.E;
     const size_t i = active ? (size_t)env * C.A + agent : 0;
     const bool real = agent < C.A;
@@ -24,35 +33,62 @@ __global__ __launch_bounds__(64) void k_neighbors(const Cst<T> C, const T *pos, 
     __syncthreads();
     M cd;
     const M incl = scan_all<T, PA>(lx, ly, base, C.A, agent, px, py, C.t_nbr, C.t_nbr, cd);
-    if (!active) return;
     M m = cap_list(incl, C.K);
     const int n = m_popc(m);
-    int32_t *row = idx + i * C.K;
-    for (int k = 0; k < C.K; ++k) {
-        int v = 0;
-        if (k < n) {
-            v = m_ctz(m);
-            m &= m - 1;
+    int32_t *row = STAGE ? srows + ((size_t)(lane / PA) * C.A + agent) * C.K : idx + i * C.K;
+    if (active) {
+        for (int k = 0; k < C.K; ++k) {
+            int v = 0;
+            if (k < n) {
+                v = m_ctz(m);
+                m &= m - 1;
+            }
+            row[k] = v;
         }
-        row[k] = v;
+        cnt[i] = n;
+        if (tru) tru[i] = m_popc(incl);
     }
-    cnt[i] = n;
-    if (tru) tru[i] = m_popc(incl);
+    if (STAGE) {
+        wave_lds_sync();  // the workgroup is this one wave
+        const int ne = C.E - e0 < EPW ? C.E - e0 : EPW;
+        const size_t nb = (size_t)ne * C.A * C.K;  // rows of the wave's active envs
+        int32_t *dst = idx + (size_t)e0 * C.A * C.K;
+        if (((uintptr_t)dst & 15u) == 0u && (nb & 3u) == 0u) {
+            const int4 *s4 = (const int4 *)srows;
+            int4 *d4 = (int4 *)dst;
+            for (size_t q = lane; q < nb / 4; q += 64) d4[q] = s4[q];
+        } else {
+            for (size_t q = lane; q < nb; q += 64) dst[q] = srows[q];
+        }
+    }
 }
 
+// LDS bytes of the staged rows of one wave (0: rows too long to stage).
+inline size_t neighbors_stage_bytes(int PA, int A, int K)
+{
+    const size_t b = (size_t)(64 / PA) * A * K * sizeof(int32_t);
+    return b <= 65536 ? b : 0;
+}
 
 template <typename T>
 void launch_neighbors(int PA, const Cst<T> &C, const T *p, int32_t *idx, int32_t *cnt,
                       int32_t *tru, hipStream_t st)
 {
     const dim3 grid((C.E + (64 / PA) - 1) / (64 / PA));
+    const size_t shm = neighbors_stage_bytes(PA, C.A, C.K);
+#define SWARP_NBR(PA_)                                                                             \
+    if (shm)                                                                                       \
+        hipLaunchKernelGGL((k_neighbors<T, PA_, true>), grid, dim3(64), shm, st, C, p, idx, cnt, tru); \
+    else                                                                                           \
+        hipLaunchKernelGGL((k_neighbors<T, PA_, false>), grid, dim3(64), 0, st, C, p, idx, cnt, tru);
     switch (PA) {
-    case 4: hipLaunchKernelGGL((k_neighbors<T, 4>), grid, dim3(64), 0, st, C, p, idx, cnt, tru); break;
-    case 8: hipLaunchKernelGGL((k_neighbors<T, 8>), grid, dim3(64), 0, st, C, p, idx, cnt, tru); break;
-    case 16: hipLaunchKernelGGL((k_neighbors<T, 16>), grid, dim3(64), 0, st, C, p, idx, cnt, tru); break;
-    case 32: hipLaunchKernelGGL((k_neighbors<T, 32>), grid, dim3(64), 0, st, C, p, idx, cnt, tru); break;
-    default: hipLaunchKernelGGL((k_neighbors<T, 64>), grid, dim3(64), 0, st, C, p, idx, cnt, tru); break;
+    case 4: SWARP_NBR(4) break;
+    case 8: SWARP_NBR(8) break;
+    case 16: SWARP_NBR(16) break;
+    case 32: SWARP_NBR(32) break;
+    default: SWARP_NBR(64) break;
     }
+#undef SWARP_NBR
 }
 
 void launch_edge_index(int E, int A, int K, const int32_t *idx, const int32_t *cnt,

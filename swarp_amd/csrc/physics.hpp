@@ -213,6 +213,13 @@ __device__ __forceinline__ T normal_coeff_r(const Cst<T> &C, T ov, T vn, const D
     return wmax(div_rn(C.k * o - C.c * vn, dd), T(0));
 }
 
+// normal_coeff given the damping denominator as a prepared divisor (same result)
+template <typename T, bool SAT = true>
+__device__ __forceinline__ T normal_coeff(const Cst<T> &C, T ov, T vn, const Dv<T> &dd)
+{
+    return normal_coeff_r<T, SAT>(C, ov, vn, dd);
+}
+
 template <typename T, bool SAT = true>
 __device__ __forceinline__ void normal_coeff_adj(const Cst<T> &C, T ov, T vn, T dd, T g,
                                                  T &a_ov, T &a_vn)
@@ -242,6 +249,27 @@ __device__ __forceinline__ void pair_force(const Cst<T> &C, T dx, T dy, T rvx, T
     if (ov > T(0)) {
         T nx = dx / dist, ny = dy / dist;
         T coef = normal_coeff(C, ov, rvx * nx + rvy * ny, dd);
+        fx = coef * nx;
+        fy = coef * ny;
+    }
+}
+
+// pair_force with the damping denominator as a prepared divisor, in the exact fast
+// arithmetic: the distance (at least sqrt(eps2)) through sqrt_rn_big, the normal through
+// one prepared divisor (a distance outside [2^-60, 2^20] takes the general division).
+// Same bits as pair_force.
+template <typename T>
+__device__ __forceinline__ void pair_force(const Cst<T> &C, T dx, T dy, T rvx, T rvy, T md,
+                                           const Dv<T> &dd, T &fx, T &fy)
+{
+    T dist = sqrt_rn_big(wmax(dx * dx + dy * dy, C.eps2));
+    T ov = md - dist;
+    fx = T(0);
+    fy = T(0);
+    if (ov > T(0)) {
+        const Dv<T> ds = divisor(dist, true);
+        T nx = div_rn(dx, ds), ny = div_rn(dy, ds);
+        T coef = normal_coeff_r(C, ov, rvx * nx + rvy * ny, dd);
         fx = coef * nx;
         fy = coef * ny;
     }
@@ -590,10 +618,52 @@ __device__ __forceinline__ void box_force_cs(const Cst<T> &C, T px, T py, T vx, 
     }
 }
 
+// box_force_cs with the damping denominator as a prepared divisor, in the exact fast
+// arithmetic of pair_force's overload (same bits).
 template <typename T>
+__device__ __forceinline__ void box_force_cs(const Cst<T> &C, T px, T py, T vx, T vy, T cx0,
+                                             T cy0, T ca, T sa, T hx, T hy, T reach,
+                                             const Dv<T> &dd, T vox, T voy, T om, T &fx, T &fy)
+{
+    T dx = px - cx0, dy = py - cy0;
+    T lx = ca * dx + sa * dy;
+    T ly = -sa * dx + ca * dy;
+    T qx = m_abs(lx) - hx, qy = m_abs(ly) - hy;
+    T ox = lx - wclamp(lx, -hx, hx), oy = ly - wclamp(ly, -hy, hy);
+    T od2 = ox * ox + oy * oy;
+    T s, nlx, nly;
+    if (od2 > C.eps2) {
+        s = sqrt_rn_big(od2);
+        const Dv<T> ds = divisor(s, true);
+        nlx = div_rn(ox, ds);
+        nly = div_rn(oy, ds);
+    } else if (qx > qy) {
+        s = qx;
+        nlx = lx >= T(0) ? T(1) : T(-1);
+        nly = T(0);
+    } else {
+        s = qy;
+        nlx = T(0);
+        nly = ly >= T(0) ? T(1) : T(-1);
+    }
+    fx = T(0);
+    fy = T(0);
+    T ov = reach - s;
+    if (ov > T(0)) {
+        T nx = ca * nlx - sa * nly, ny = sa * nlx + ca * nly;
+        T spx = lx - s * nlx, spy = ly - s * nly;
+        T rx = ca * spx - sa * spy, ry = sa * spx + ca * spy;
+        T rvx = vx - (vox + -om * ry), rvy = vy - (voy + om * rx);
+        T coef = normal_coeff_r(C, ov, rvx * nx + rvy * ny, dd);
+        fx = coef * nx;
+        fy = coef * ny;
+    }
+}
+
+template <typename T, typename DD>
 __device__ __forceinline__ void box_force(const Cst<T> &C, T px, T py, T vx, T vy, T cx0, T cy0,
-                                          T ang, T hx, T hy, T reach, T dd, T vox, T voy, T om,
-                                          T &fx, T &fy)
+                                          T ang, T hx, T hy, T reach, const DD &dd, T vox, T voy,
+                                          T om, T &fx, T &fy)
 {
     box_force_cs(C, px, py, vx, vy, cx0, cy0, m_cos(ang), m_sin(ang), hx, hy, reach, dd, vox,
                  voy, om, fx, fy);
@@ -692,10 +762,12 @@ __device__ __forceinline__ void ob_trig(const Obs<T> &O, size_t j, int o, const 
 // One obstacle on one agent (_obstacle_forces body, swarp/core/collisions.py:690-743).
 // `cs`: this env's obstacle angles as (cos, sin) pairs [N][2], computed once per launch
 // (the angles do not change within one), or NULL to evaluate them here.
-template <typename T>
+// DD: the damping denominator as a plain value or as a prepared divisor (Dv<T>, the
+// exact fast arithmetic of the force overloads that take one); the same bits either way.
+template <typename T, typename DD>
 __device__ __forceinline__ void obstacle_force(const Cst<T> &C, const Obs<T> &O, size_t eN, int o,
-                                               T px, T py, T vx, T vy, T ra, T dd, T &fx, T &fy,
-                                               const T *cs = nullptr)
+                                               T px, T py, T vx, T vy, T ra, const DD &dd, T &fx,
+                                               T &fy, const T *cs = nullptr)
 {
     fx = T(0);
     fy = T(0);

@@ -556,15 +556,28 @@ template <typename T> static int nav_obs(const swarp_desc_t *d, const swarp_nav_
 }
 
 // Default drone fields [z n | vz n | attitude 4n | body_rates 3n]: every element 0 except
-// the w component of each quaternion.  Four consecutive elements per lane.
+// the w component of each quaternion.  Each lane writes one 16-byte piece (16 / sizeof(T)
+// consecutive elements) with one vector store; the piece at the end of a buffer whose
+// length is not a multiple of it is written element by element.  `buf` is 16-byte aligned
+// (the caller's allocation).
 template <typename T> __global__ void k_state_defaults(int64_t n, T *buf)
 {
-    const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    constexpr int V = 16 / sizeof(T);
+    const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V;
     const int64_t end = 9 * n;
+    if (i0 >= end) return;
+    T v[V];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < V; ++k) {
         const int64_t i = i0 + k;
-        if (i < end) buf[i] = (i >= 2 * n && i < 6 * n && ((i - 2 * n) & 3) == 3) ? T(1) : T(0);
+        v[k] = (i >= 2 * n && i < 6 * n && ((i - 2 * n) & 3) == 3) ? T(1) : T(0);
+    }
+    if (i0 + V <= end) {
+        uint4 w;
+        __builtin_memcpy(&w, v, 16);
+        *(uint4 *)(buf + i0) = w;
+    } else {
+        for (int k = 0; k < V && i0 + k < end; ++k) buf[i0 + k] = v[k];
     }
 }
 
@@ -758,7 +771,9 @@ int swarp_state_defaults(int32_t dtype, int64_t n, void *buf, void *stream)
     if (n < 0 || n > (int64_t)1 << 40) return fail("n out of range");
     if (n == 0) return 0;
     if (!buf) return fail("buf must be set");
-    const int64_t items = (9 * n + 3) / 4;
+    if (((uintptr_t)buf & 15u) != 0u) return fail("buf must be 16-byte aligned");
+    const int64_t per = dtype == SWARP_F32 ? 4 : 2;  // elements per 16-byte piece
+    const int64_t items = (9 * n + per - 1) / per;
     const unsigned blocks = (unsigned)((items + 255) / 256);
     if (dtype == SWARP_F32)
         hipLaunchKernelGGL(k_state_defaults<float>, dim3(blocks), dim3(256), 0, (hipStream_t)stream,

@@ -359,7 +359,7 @@ __device__ __forceinline__ void wide_forces(const Cst<T> &C, const Args<T> &g,
                             [&](int j, int32_t key) {
                                 T gx, gy;
                                 pair_force(C, st.px - W.px[j], st.py - W.py[j], st.vx - W.vx[j],
-                                           st.vy - W.vy[j], ra + W.rad[j] + C.margin, L.dd, gx, gy);
+                                           st.vy - W.vy[j], ra + W.rad[j] + C.margin, L.ddv, gx, gy);
                                 fx += gx;
                                 fy += gy;
                                 last = key;
@@ -372,7 +372,7 @@ __device__ __forceinline__ void wide_forces(const Cst<T> &C, const Args<T> &g,
         const size_t eN = (size_t)L.env * C.N;
         for (int o = 0; o < C.N; ++o) {
             T gx, gy;
-            obstacle_force(C, g.obs, eN, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.dd, gx, gy);
+            obstacle_force(C, g.obs, eN, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv, gx, gy);
             sx += gx;
             sy += gy;
         }

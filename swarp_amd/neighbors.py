@@ -132,6 +132,9 @@ class NeighborGrid:
         self.neighbor_idx = torch.zeros(n_envs, n_agents, max_neighbors, **z)
         self.neighbor_count = torch.zeros(n_envs, n_agents, **z)
         self.neighbor_true_count = torch.zeros(n_envs, n_agents, **z)
+        # edge_index's running sums of the counts: [0, c0, c0 + c1, ...] (the leading
+        # zero is written once, so [:-1] are the exclusive offsets and [-1] the edge count)
+        self._csum = torch.zeros(n_envs * n_agents + 1, device=self.device, dtype=torch.int64)
         self.build_count = 0
         self.built_version = -1
         # the batch-reduced grid frame (origin x, y, cell size) of the last build
@@ -221,13 +224,15 @@ class NeighborGrid:
     def edge_index(self) -> torch.Tensor:
         """COO ``[2, n_edges]`` int64 (sender, receiver), global ids ``e * A + a``, in
         (env, agent, slot) order.  Reads the edge count back to the host (one sync)."""
-        cnt = self.neighbor_count.reshape(-1).to(torch.int64)
-        incl = torch.cumsum(cnt, 0)
-        n_edges = int(incl[-1].item()) if cnt.numel() else 0
+        cnt = self.neighbor_count.reshape(-1)
+        if cnt.numel() == 0:
+            return torch.empty(2, 0, device=self.device, dtype=torch.int64)
+        torch.cumsum(cnt, 0, dtype=torch.int64, out=self._csum[1:])
+        n_edges = int(self._csum[-1].item())
         out = torch.empty(2, n_edges, device=self.device, dtype=torch.int64)
         if n_edges == 0:
             return out
-        offsets = (incl - cnt).contiguous()
+        offsets = self._csum[:-1]
         lib = _lib.load()
         stream = _lib.stream_of(out.device)
         _lib.check(lib.swarp_edge_index(

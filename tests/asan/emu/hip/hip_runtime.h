@@ -180,6 +180,14 @@ template <typename T> inline T __shfl(T x, int src, int width = 64)
     const int l = (int)(::emu::tIdx.x % 64), base = l - l % width;
     return emu_from<T>(v[base + ((src % width) + width) % width]);
 }
+template <typename T> inline T __shfl_xor(T x, int mask, int width = 64)
+{
+    uint64_t v[64];
+    ::emu::exchange(emu_bits(x), v);
+    const int l = (int)(::emu::tIdx.x % 64), base = l - l % width;
+    const int src = l ^ mask;
+    return (src >= base && src < base + width) ? emu_from<T>(v[src]) : x;
+}
 template <typename T> inline T __shfl_up(T x, unsigned d, int width = 64)
 {
     uint64_t v[64];
@@ -232,7 +240,18 @@ inline int __builtin_amdgcn_mov_dpp(int, int, int, int, bool) { emu_not_emulated
 inline unsigned __builtin_amdgcn_ubfe(unsigned, unsigned, unsigned) { emu_not_emulated("ubfe"); }
 inline void __builtin_amdgcn_s_waitcnt(int) {}
 inline void __builtin_amdgcn_s_barrier() { emu_not_emulated("s_barrier"); }
+// The hardware executes one wave's LDS instructions in issue order, so kernels whose
+// workgroup is one wave exchange values through LDS behind a wavefront-scope fence (a
+// compiler fence only).  The emulated work-items run as concurrent threads, so here the
+// fence is a barrier of the workgroup (one wave wherever the kernels use it).
 inline void __builtin_amdgcn_wave_barrier() {}
+inline void __builtin_amdgcn_fence(int, const char *scope)
+{
+    if (scope && strcmp(scope, "wavefront") == 0) ::emu::block->bar.wait("wave fence");
+}
+struct alignas(16) int4 {
+    int x, y, z, w;
+};
 inline uint64_t __builtin_amdgcn_read_exec() { emu_not_emulated("read_exec"); }
 inline int __builtin_amdgcn_readfirstlane(int x) { return __builtin_amdgcn_readlane(x, 0); }
 inline unsigned __builtin_amdgcn_mbcnt_lo(unsigned, unsigned) { emu_not_emulated("mbcnt"); }

@@ -248,3 +248,29 @@ def test_padded_agent_slots():
             hip = hip_run(st, s0, acts, w, np.float32)
             orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float32)
             _check(f"pad A={A} spec={spec}", hip, orc, state_exact=True)
+
+
+def test_listed_neighbours_beyond_contact_reach():
+    """Lists wider than any contact (neighbour radius 0.35) in dense envs with per-agent
+    radii from 0.02 to 0.12 and truncated lists: the forward visits only the listed
+    neighbours within the env's contact bound (the largest radius of the env sets it), so
+    this case has listed pairs on both sides of every agent's reach, and agents whose
+    largest-radius neighbour decides the bound.  States bit-exact with the oracle,
+    gradients 1e-5, generic kernels in velocity and acceleration mode."""
+    E, A, T, S = 160, 12, 8, 3
+    rng = np.random.default_rng(11)
+    radii = np.linspace(0.02, 0.12, A)[rng.permutation(A)]
+    for mode in (ControlMode.VELOCITY, ControlMode.ACCELERATION):
+        cfgs = [AgentConfig(model=DynamicsModel.HOLONOMIC, ctrl_mode=mode, radius=float(r),
+                            max_speed=1.0, max_accel=2.0) for r in radii]
+        world = WorldConfig(collision_k=80.0, collision_c=1.5, collision_margin=0.03,
+                            max_neighbors=5, neighbor_radius=0.35, bounds=(-0.6, 0.6, -0.6, 0.6))
+        s0 = pack_state({"pos": rng.uniform(-0.5, 0.5, size=(E, A, 2)),
+                         "vel": 0.2 * rng.normal(size=(E, A, 2))}).astype(np.float32)
+        acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
+        w = _cotangent(T, E, A, 13)
+        st = make_stepper(cfgs, world, 0.05, S, torch.float32)
+        st.use_specialised = False
+        hip = hip_run(st, s0, acts, w, np.float32)
+        orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float32)
+        _check(f"wide lists {mode.name}", hip, orc, state_exact=True)

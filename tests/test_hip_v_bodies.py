@@ -18,7 +18,7 @@ from cases import body_seed_np, nav_agents, obstacles_np, oracle_cfg, params_of
 from hip_helpers import make_stepper, rel, state_to16, to_torch_state
 from oracle.oracle import Oracle, pack_state
 from swarp_amd import rollout
-from swarp_amd.config import Integrator, WorldConfig
+from swarp_amd.config import AgentConfig, Integrator, WorldConfig
 
 pytestmark = pytest.mark.gpu
 MOVABLE = 1
@@ -391,3 +391,17 @@ def test_box_and_segment_bodies_match_oracle(np_dtype):
     _check_fields("shapes", hip, orc, cols, exact=True,
                   g_tol=1e-5 if np_dtype == np.float32 else 1e-12)
     assert np.abs(orc[1][-1, :, 6 * 5 + 5]).max() > 1e-4, "the compound body never turned"
+
+
+def test_bodies_heterogeneous_radii_wide_lists():
+    """Per-agent radii from 0.02 to 0.1 under radius-0.3 lists (K = 6, truncated): the
+    agent-pair pass visits only listed neighbours within the env's contact bound, set by
+    its largest radius.  Agent and body states bit-exact, gradients 1e-5."""
+    E, A = 24, 16
+    s0, acts = _pushers(E, A, 5, spread=0.7)
+    rng = np.random.default_rng(6)
+    radii = np.linspace(0.02, 0.1, A)[rng.permutation(A)]
+    cfgs = [AgentConfig(radius=float(r), max_speed=1.0, max_accel=2.0) for r in radii]
+    obs = cross_obs(E, (0.0, 0.0))
+    hip, orc = run_pair(cfgs, _world(max_neighbors=6), 0.05, 4, s0, acts, obs, np.float32)
+    check("hetero radii", hip, orc)

@@ -46,6 +46,8 @@ def test_state_defaults_rejects_bad_arguments_without_gpu():
     assert lib.swarp_state_defaults(0, -1, None, None) != 0
     assert lib.swarp_state_defaults(0, 4, None, None) != 0
     assert b"buf" in lib.swarp_last_error()
+    assert lib.swarp_state_defaults(0, 4, 8, None) != 0  # misaligned: rejected before launch
+    assert b"aligned" in lib.swarp_last_error()
     assert lib.swarp_state_defaults(1, 0, None, None) == 0
     assert lib.swarp_last_error() == b""
 
