@@ -281,11 +281,15 @@ template <typename T, int PA> struct Lane {
     Dv<T> ddv;     // dd as a prepared divisor (exact fp32 division by dd)
 };
 
+// `lane`: the work-item's lane within its wave's env slots (the thread index of a
+// one-wave workgroup; split kernels pass threadIdx.x % 64, so both waves of a workgroup
+// hold the same envs).
 template <typename T, int PA>
-__device__ __forceinline__ void lane_init(const Cst<T> &C, const Args<T> &g, Lane<T, PA> &L)
+__device__ __forceinline__ void lane_init(const Cst<T> &C, const Args<T> &g, Lane<T, PA> &L,
+                                          int lane = -1)
 {
     constexpr int EPW = 64 / PA;
-    L.lane = threadIdx.x;
+    L.lane = lane < 0 ? (int)threadIdx.x : lane;
     L.agent = L.lane % PA;
     L.base = L.lane - L.agent;
     L.env = blockIdx.x * EPW + L.lane / PA;

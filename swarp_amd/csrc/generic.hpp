@@ -90,6 +90,121 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> Cin, const Args
 }
 
 
+// Forward rollout of 2-D fleets among static obstacles (feature profile F with FT_OBST,
+// no box agents, no drones), two waves per workgroup holding the same envs: wave 0 (the
+// agent wave) publishes each substep's state, scans, sums the listed pairs' forces and the
+// walls', integrates and stores; wave 1 (the obstacle wave) sums each agent's obstacle
+// forces in index order from the published state.  The force is fx + (so + w): the pair
+// sum plus the static sum, obstacles then walls, the reference's order
+// (swarp/core/collisions.py:852-880, 781-815), so the bits are k_rollout_fwd's.  The
+// obstacle pass is about half of such a step; on its own wave it overlaps the agent wave's
+// work and doubles the resident waves of a launch that is latency-bound with two.
+template <typename T, int PA, unsigned F>
+__global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, const Args<T> g)
+{
+    typedef typename MaskT<PA>::type M;
+    const Cst<T> C = fold_cst<F>(Cin);
+    __shared__ T sl[7 * 64];  // px py vx vy of the current substep (F_* rows)
+    __shared__ T lr[64];      // agent radius per lane
+    __shared__ T lso[2 * 64]; // the obstacle wave's sums: x row, y row
+    __shared__ T ocs_lds[2 * OCS_MAX];
+    const bool agent_wave = threadIdx.x < 64;
+    Lane<T, PA> L;
+    lane_init<T, PA>(C, g, L, (int)(threadIdx.x & 63));
+    fold_prm<F>(L.pr);
+    if (agent_wave) lr[L.lane] = L.pr.radius;
+    const T *ocs = ob_trig_table<T, PA>(C, g, L, ocs_lds);
+    const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
+    St<T> st;
+    load_state<T, false>(g.s0.f, L.idx, 0, st);
+    if (!L.real) st.px = st.py = __builtin_nan("");
+    const size_t EA = (size_t)C.E * C.A;
+    for (int t = 0; t < g.nsteps; ++t) {
+        T a[4];
+        if (agent_wave) load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
+        M cand = 0;
+        T D = T(0);
+        bool ok = false;
+        for (int s = 0; s < C.S; ++s) {
+            __syncthreads();  // the previous substep's readers are done with sl / lso
+            if (agent_wave) {
+                sl[F_PX * 64 + L.lane] = st.px;
+                sl[F_PY * 64 + L.lane] = st.py;
+                sl[F_VX * 64 + L.lane] = st.vx;
+                sl[F_VY * 64 + L.lane] = st.vy;
+            }
+            __syncthreads();
+            if (!agent_wave) {
+                const T px = sl[F_PX * 64 + L.lane], py = sl[F_PY * 64 + L.lane];
+                const T vx = sl[F_VX * 64 + L.lane], vy = sl[F_VY * 64 + L.lane];
+                T sx = T(0), sy = T(0);
+                for (int o = 0; o < C.N; ++o) {
+                    T gx, gy;
+                    obstacle_force(C, g.obs, eN, o, px, py, vx, vy, L.pr.radius, L.ddv, gx, gy,
+                                   ocs);
+                    sx += gx;
+                    sy += gy;
+                }
+                lso[L.lane] = sx;
+                lso[64 + L.lane] = sy;
+            }
+            T fx = T(0), fy = T(0), wx = T(0), wy = T(0);
+            M incl = 0;
+            if (agent_wave) {
+                if (C.collisions) {
+                    const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64;
+                    const T *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
+                    if (s == 0 || !ok) {
+                        M cd;
+                        incl = scan_all<T, PA>(lx, ly, L.base, C.A, L.agent, st.px, st.py, C.t_nbr,
+                                               C.t_skin, cd);
+                        if (s == 0) cand = cd;
+                    } else {
+                        incl = scan_cand<T, PA>(lx, ly, L.base, st.px, st.py, C.t_nbr, cand);
+                    }
+                    M m = cap_list(incl, C.K);
+                    const T ra = L.pr.radius;
+                    while (m) {
+                        const int b = m_ctz(m);
+                        m &= m - 1;
+                        const int j = L.base + b;
+                        T gx, gy;
+                        pair_force(C, st.px - lx[j], st.py - ly[j], st.vx - lvx[j], st.vy - lvy[j],
+                                   ra + lr[j] + C.margin, L.ddv, gx, gy);
+                        fx += gx;
+                        fy += gy;
+                    }
+                }
+                if (C.soft_walls) {
+                    unsigned wb;
+                    wall_force_axes(C, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv, wx, wy, wb);
+                }
+            }
+            __syncthreads();  // the obstacle sums are in lso
+            if (agent_wave) {
+                T sx = lso[L.lane], sy = lso[64 + L.lane];
+                if (C.soft_walls) {
+                    sx += wx;
+                    sy += wy;
+                }
+                St<T> nx;
+                integrate<T, false>(C, L.pr, st, a, fx + sx, fy + sy, nx);
+                if (C.use_skin) {
+                    D += (m_abs(nx.px - st.px) + m_abs(nx.py - st.py)) * T(1.0001);
+                    ok = env_all<PA>(!L.real || D <= C.half_margin, L.base);
+                }
+                st = nx;
+            }
+        }
+        if (agent_wave && L.active) {
+            if (t + 1 < g.nsteps)
+                store_state<T, false>(g.traj.f, (size_t)t * EA + L.idx, st);
+            else
+                store_state<T, false>(g.fin.f, L.idx, st);
+        }
+    }
+}
+
 // Reverse pass of one substep's box contacts, as one wave-wide work list.  Lane a's items
 // are its force-exerting box pairs (ascending neighbour), then for a box agent its
 // force-exerting obstacles (ascending index) and walls -- or, when an obstacle past the
@@ -396,6 +511,18 @@ void launch_fwd(int PA, const Cst<T> &C, const Args<T> &a, unsigned feat, hipStr
     const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
         grid32((C.E + 1) / 2), grid64(C.E);
     constexpr unsigned P = family_profile<T, DRONE, BOXES>();
+    if (!DRONE && !BOXES && P != 0u && (feat & ~P) == 0u && (feat & FT_OBST) && C.N > 0) {
+        // static obstacles: the obstacle pass on a wave of its own
+        constexpr unsigned PS = P ? P : FT_ALL;
+        switch (PA) {
+        case 4: hipLaunchKernelGGL((k_rollout_fwd_split<T, 4, PS>), grid4, dim3(128), 0, st, C, a); break;
+        case 8: hipLaunchKernelGGL((k_rollout_fwd_split<T, 8, PS>), grid8, dim3(128), 0, st, C, a); break;
+        case 16: hipLaunchKernelGGL((k_rollout_fwd_split<T, 16, PS>), grid16, dim3(128), 0, st, C, a); break;
+        case 32: hipLaunchKernelGGL((k_rollout_fwd_split<T, 32, PS>), grid32, dim3(128), 0, st, C, a); break;
+        default: hipLaunchKernelGGL((k_rollout_fwd_split<T, 64, PS>), grid64, dim3(128), 0, st, C, a); break;
+        }
+        return;
+    }
     if (P != 0u && (feat & ~P) == 0u) {
         SWARP_DISPATCH_PA(PA, k_rollout_fwd, DRONE, BOXES, P ? P : FT_ALL)
     } else {
