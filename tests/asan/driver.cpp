@@ -51,6 +51,8 @@ struct Case {
     int models;  // 0 holonomic, 1 diff/bicycle mix, 3 drone
     bool per_env = false;  // per-env parameter rows (the body pass then reads the shared)
     bool shaped = false;   // movable bodies of box and segment shapes too
+    bool fleet = false;    // fleet model / mode bit sets filled in (the profile instances,
+                           // and for 2-D fleets among obstacles the two-wave forward)
 };
 
 template <typename T>
@@ -117,6 +119,12 @@ int run_case(const Case &c)
     }
     d.model_tag = tag;
     d.ctrl_mode = mode;
+    if (c.fleet) {
+        int mb = 0;
+        for (int a = 0; a < A; ++a) mb |= 1 << tag[a];
+        d.fleet_models = mb;
+        d.fleet_modes = 1;  // every agent in VELOCITY mode
+    }
     const int N = c.nobs;
     d.n_obstacles = N;
     if (N > 0) {
@@ -244,6 +252,8 @@ int main(int argc, char **argv)
         {"drones f32 64x8",     16, 8, 6, 2, 8, 4, 0, true,  false, false, false, false, false, 3},
         {"drones f64 A=3",       4, 3, 5, 1, 4, 4, 0, true,  false, false, false, false, false, 3},
         {"mixed f32 obstacles",  9, 32, 4, 2, 16, 2, 6, false, false, true,  false, false, false, 1},
+        {"mixed f32 obstacles profile", 9, 32, 4, 2, 16, 2, 6, false, false, true, false, false, false, 1,
+         false, false, true},
         {"mixed f32 rk4",        5, 20, 3, 2, 8, 2, 3, false, false, true,  false, true,  false, 1},
         {"boxes f32",            7, 16, 3, 2, 8, 2, 3, false, true,  true,  false, false, false, 1},
         {"holonomic f64 A=5",   11, 5, 4, 3, 4, 2, 0, false, false, true,  false, false, false, 0},

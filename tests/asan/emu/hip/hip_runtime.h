@@ -240,14 +240,14 @@ inline int __builtin_amdgcn_mov_dpp(int, int, int, int, bool) { emu_not_emulated
 inline unsigned __builtin_amdgcn_ubfe(unsigned, unsigned, unsigned) { emu_not_emulated("ubfe"); }
 inline void __builtin_amdgcn_s_waitcnt(int) {}
 inline void __builtin_amdgcn_s_barrier() { emu_not_emulated("s_barrier"); }
-// The hardware executes one wave's LDS instructions in issue order, so kernels whose
-// workgroup is one wave exchange values through LDS behind a wavefront-scope fence (a
-// compiler fence only).  The emulated work-items run as concurrent threads, so here the
-// fence is a barrier of the workgroup (one wave wherever the kernels use it).
+// The hardware executes one wave's LDS instructions in issue order, so the lanes of a
+// wave exchange values through LDS behind a wavefront-scope fence (a compiler fence
+// only).  The emulated work-items run as concurrent threads, so here the fence is a
+// barrier of the calling thread's wave.
 inline void __builtin_amdgcn_wave_barrier() {}
 inline void __builtin_amdgcn_fence(int, const char *scope)
 {
-    if (scope && strcmp(scope, "wavefront") == 0) ::emu::block->bar.wait("wave fence");
+    if (scope && strcmp(scope, "wavefront") == 0) ::emu::my_wave().bar.wait("wave fence");
 }
 struct alignas(16) int4 {
     int x, y, z, w;
