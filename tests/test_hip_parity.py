@@ -274,3 +274,32 @@ def test_listed_neighbours_beyond_contact_reach():
         hip = hip_run(st, s0, acts, w, np.float32)
         orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float32)
         _check(f"wide lists {mode.name}", hip, orc, state_exact=True)
+
+
+@pytest.mark.parametrize("E,A", [(13, 5), (40, 16), (9, 64)])
+def test_obstacle_worlds_across_env_widths(E, A):
+    """2-D fleets among static obstacles at every env width the two-wave forward serves
+    (pad lanes and a partial last workgroup at A = 5, four envs per wave at A = 16, one
+    at A = 64): diff-drive, bicycle and holonomic agents, circles, boxes and segments,
+    soft walls.  States bit-exact with the float32 oracle, gradients 1e-5."""
+    T, S = 6, 3
+    rng = np.random.default_rng(E * 7 + A)
+    models = (DynamicsModel.DIFF_DRIVE, DynamicsModel.KINEMATIC_BICYCLE, DynamicsModel.HOLONOMIC)
+    cfgs = [AgentConfig(model=models[a % 3], radius=0.05) for a in range(A)]
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.025,
+                        bounds=(-1.0, 1.0, -1.0, 1.0), max_neighbors=min(16, A))
+    n = 6
+    obs = {"pos": rng.uniform(-1, 1, size=(E, n, 2)),
+           "radius": np.r_[rng.uniform(0.05, 0.2, 2), np.zeros(2), np.full(2, 0.05)],
+           "type": np.r_[np.zeros(2), np.ones(2), np.full(2, 2)].astype(np.int32),
+           "angle": rng.uniform(-np.pi, np.pi, size=(E, n)),
+           "half": np.r_[np.zeros((2, 2)), rng.uniform(0.05, 0.3, size=(2, 2)),
+                         np.c_[rng.uniform(0.1, 0.4, 2), np.zeros(2)]]}
+    s0 = pack_state({"pos": rng.uniform(-1, 1, size=(E, A, 2)),
+                     "theta": rng.uniform(-np.pi, np.pi, size=(E, A))}).astype(np.float32)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
+    w = _cotangent(T, E, A, 5, scale=0.1)
+    st = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
+    hip = hip_run(st, s0, acts, w, np.float32)
+    orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float32, obs=obs)
+    _check(f"obstacles E={E} A={A}", hip, orc, state_exact=True)
