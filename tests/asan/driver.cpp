@@ -249,6 +249,10 @@ int main(int argc, char **argv)
         {"bodies drones f32 A=8", 9, 8, 3, 2, 8, 4, 5, true,  false, true,  true,  false, false, 3},
         {"bodies per-env f32",   6, 12, 3, 2, 8, 2, 5, false, false, true,  true,  false, false, 0, true},
         {"bodies shaped f32",    6, 12, 3, 2, 8, 2, 5, false, false, true,  true,  false, false, 0, false, true},
+        {"bodies f32 A=64 profile", 2, 64, 3, 2, 16, 2, 5, false, false, true, true, false, false, 0,
+         false, false, true},
+        {"bodies f32 A=12 profile", 5, 12, 4, 2, 8, 2, 5, false, false, true, true, false, false, 0,
+         false, false, true},
         {"drones f32 64x8",     16, 8, 6, 2, 8, 4, 0, true,  false, false, false, false, false, 3},
         {"drones f64 A=3",       4, 3, 5, 1, 4, 4, 0, true,  false, false, false, false, false, 3},
         {"mixed f32 obstacles",  9, 32, 4, 2, 16, 2, 6, false, false, true,  false, false, false, 1},
