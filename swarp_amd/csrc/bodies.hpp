@@ -717,9 +717,13 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
     if (!L.active) st.px = st.py = __builtin_nan("");
     const size_t EA = (size_t)C.E * C.A, ENW = (size_t)C.E * NW;
     int cur = 0;
+    // each step's action is loaded one step ahead and taken into registers before the
+    // step's stores (memory operations complete in order)
+    T a[4];
+    load_act(g.act, L.idx, C.ad, a);
     for (int t = 0; t < g.nsteps; ++t) {
-        T a[4];
-        load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
+        T an[4] = {a[0], a[1], a[2], a[3]};
+        if (t + 1 < g.nsteps) load_act(g.act, (size_t)(t + 1) * EA + L.idx, C.ad, an);
         M cand = 0;
         T D = T(0);
         bool ok = false;
@@ -744,6 +748,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
             st = nx;
             cur ^= 1;
         }
+        asm volatile("" ::"v"(an[0]), "v"(an[1]), "v"(an[2]), "v"(an[3]));
         __syncthreads();
         if (L.active) {
             if (t + 1 < g.nsteps)
@@ -753,6 +758,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
         }
         if (env_ok)
             for (int q = L.agent; q < NW; q += PA) io.traj[(size_t)t * ENW + eo + q] = lob[cur][ew][q];
+        for (int k = 0; k < 4; ++k) a[k] = an[k];
     }
 }
 

@@ -32,9 +32,14 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> Cin, const Args
     load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
     if (!L.real) st.px = st.py = __builtin_nan("");
     const size_t EA = (size_t)C.E * C.A;
+    // each step's action is loaded one step ahead and taken into registers before the
+    // step's state stores: memory operations complete in order, so a load issued after
+    // the stores would also wait for them
+    T a[4];
+    load_act(g.act, L.idx, C.ad, a);
     for (int t = 0; t < g.nsteps; ++t) {
-        T a[4];
-        load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
+        T an[4] = {a[0], a[1], a[2], a[3]};
+        if (t + 1 < g.nsteps) load_act(g.act, (size_t)(t + 1) * EA + L.idx, C.ad, an);
         M cand = 0;
         T D = T(0);
         bool ok = false;
@@ -80,12 +85,14 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> Cin, const Args
             }
             st = nx;
         }
+        asm volatile("" ::"v"(an[0]), "v"(an[1]), "v"(an[2]), "v"(an[3]));
         if (L.active) {
             if (t + 1 < g.nsteps)
                 store_state<T, DRONE>(g.traj.f, (size_t)t * EA + L.idx, st);
             else
                 store_state<T, DRONE>(g.fin.f, L.idx, st);
         }
+        for (int k = 0; k < 4; ++k) a[k] = an[k];
     }
 }
 
@@ -119,9 +126,11 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
     load_state<T, false>(g.s0.f, L.idx, 0, st);
     if (!L.real) st.px = st.py = __builtin_nan("");
     const size_t EA = (size_t)C.E * C.A;
+    T a[4] = {T(0), T(0), T(0), T(0)};  // the step's action, loaded one step ahead
+    if (agent_wave) load_act(g.act, L.idx, C.ad, a);
     for (int t = 0; t < g.nsteps; ++t) {
-        T a[4];
-        if (agent_wave) load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
+        T an[4] = {a[0], a[1], a[2], a[3]};
+        if (agent_wave && t + 1 < g.nsteps) load_act(g.act, (size_t)(t + 1) * EA + L.idx, C.ad, an);
         M cand = 0;
         T D = T(0);
         bool ok = false;
@@ -196,12 +205,14 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
                 st = nx;
             }
         }
+        asm volatile("" ::"v"(an[0]), "v"(an[1]), "v"(an[2]), "v"(an[3]));
         if (agent_wave && L.active) {
             if (t + 1 < g.nsteps)
                 store_state<T, false>(g.traj.f, (size_t)t * EA + L.idx, st);
             else
                 store_state<T, false>(g.fin.f, L.idx, st);
         }
+        for (int k = 0; k < 4; ++k) a[k] = an[k];
     }
 }
 
