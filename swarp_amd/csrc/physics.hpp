@@ -759,6 +759,24 @@ __device__ __forceinline__ void ob_trig(const Obs<T> &O, size_t j, int o, const 
     }
 }
 
+// The broad phase of _obstacle_forces (swarp/core/collisions.py:717-720, with shape_bound
+// :62-70 and bounds_apart :74-84): whether obstacle o's bounding disc comes within reach
+// of an agent of radius ra at (px, py).  A NaN position is in reach (the comparison that
+// would cull it fails), so a NaN state still propagates through the contact code.
+template <typename T>
+__device__ __forceinline__ bool obstacle_in_reach(const Cst<T> &C, const Obs<T> &O, size_t eN,
+                                                  int o, T px, T py, T ra)
+{
+    const size_t j = eN + o;
+    const T cx = O.pos[2 * j], cy = O.pos[2 * j + 1];
+    const int st = O.type[o];
+    const T ro = O.rad[o], hx = O.half[2 * o], hy = O.half[2 * o + 1];
+    T bound = st == 1 ? m_sqrt(hx * hx + hy * hy) : (st == 2 ? hx + ro : ro);
+    T lim = (ra + C.margin + bound) * T(1.0001) + T(1.0e-6);
+    T ddx = px - cx, ddy = py - cy;
+    return !(ddx * ddx + ddy * ddy > lim * lim);
+}
+
 // One obstacle on one agent (_obstacle_forces body, swarp/core/collisions.py:690-743).
 // `cs`: this env's obstacle angles as (cos, sin) pairs [N][2], computed once per launch
 // (the angles do not change within one), or NULL to evaluate them here.
@@ -771,14 +789,11 @@ __device__ __forceinline__ void obstacle_force(const Cst<T> &C, const Obs<T> &O,
 {
     fx = T(0);
     fy = T(0);
+    if (!obstacle_in_reach(C, O, eN, o, px, py, ra)) return;
     const size_t j = eN + o;
     const T cx = O.pos[2 * j], cy = O.pos[2 * j + 1];
     const int st = O.type[o];
     const T ro = O.rad[o], hx = O.half[2 * o], hy = O.half[2 * o + 1];
-    T bound = st == 1 ? m_sqrt(hx * hx + hy * hy) : (st == 2 ? hx + ro : ro);
-    T lim = (ra + C.margin + bound) * T(1.0001) + T(1.0e-6);
-    T ddx = px - cx, ddy = py - cy;
-    if (ddx * ddx + ddy * ddy > lim * lim) return;
     const T vox = O.vel[2 * j], voy = O.vel[2 * j + 1], om = O.om[j];
     if (st == 1) {
         T ca, sa;
@@ -803,14 +818,11 @@ __device__ __forceinline__ void obstacle_force_adj(const Cst<T> &C, const Obs<T>
                                                    int o, T px, T py, T vx, T vy, T ra, T dd,
                                                    T gx, T gy, St<T> &a, const T *cs = nullptr)
 {
+    if (!obstacle_in_reach(C, O, eN, o, px, py, ra)) return;
     const size_t j = eN + o;
     const T cx = O.pos[2 * j], cy = O.pos[2 * j + 1];
     const int st = O.type[o];
     const T ro = O.rad[o], hx = O.half[2 * o], hy = O.half[2 * o + 1];
-    T bound = st == 1 ? m_sqrt(hx * hx + hy * hy) : (st == 2 ? hx + ro : ro);
-    T lim = (ra + C.margin + bound) * T(1.0001) + T(1.0e-6);
-    T ddx = px - cx, ddy = py - cy;
-    if (ddx * ddx + ddy * ddy > lim * lim) return;
     const T vox = O.vel[2 * j], voy = O.vel[2 * j + 1], om = O.om[j];
     if (st == 1) {
         T ca, sa;

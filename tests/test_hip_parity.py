@@ -303,3 +303,33 @@ def test_obstacle_worlds_across_env_widths(E, A):
     hip = hip_run(st, s0, acts, w, np.float32)
     orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float32, obs=obs)
     _check(f"obstacles E={E} A={A}", hip, orc, state_exact=True)
+
+
+@pytest.mark.parametrize("n", [3, 7, 40])
+def test_obstacle_counts_across_forward_layouts(n):
+    """Obstacle counts from a few to more than a wave's agents: 3, 7 (an odd count) and 40
+    obstacles per env, circles, boxes and segments in turn, soft walls, 12 agents of the
+    three 2-D models.  States bit-exact with the float32 oracle, gradients 1e-5."""
+    E, A, T, S = 9, 12, 5, 2
+    rng = np.random.default_rng(100 + n)
+    models = (DynamicsModel.DIFF_DRIVE, DynamicsModel.KINEMATIC_BICYCLE, DynamicsModel.HOLONOMIC)
+    cfgs = [AgentConfig(model=models[a % 3], radius=0.05) for a in range(A)]
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.025,
+                        bounds=(-1.0, 1.0, -1.0, 1.0), max_neighbors=8)
+    kind = np.arange(n) % 3
+    half = np.zeros((n, 2))
+    half[kind == 1] = rng.uniform(0.05, 0.3, size=(int((kind == 1).sum()), 2))
+    half[kind == 2, 0] = rng.uniform(0.1, 0.4, size=int((kind == 2).sum()))
+    obs = {"pos": rng.uniform(-1, 1, size=(E, n, 2)),
+           "radius": np.where(kind == 0, rng.uniform(0.05, 0.2, n), np.where(kind == 2, 0.05, 0.0)),
+           "type": kind.astype(np.int32),
+           "angle": rng.uniform(-np.pi, np.pi, size=(E, n)),
+           "half": half}
+    s0 = pack_state({"pos": rng.uniform(-1, 1, size=(E, A, 2)),
+                     "theta": rng.uniform(-np.pi, np.pi, size=(E, A))}).astype(np.float32)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
+    w = _cotangent(T, E, A, 6, scale=0.1)
+    st = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
+    hip = hip_run(st, s0, acts, w, np.float32)
+    orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float32, obs=obs)
+    _check(f"obstacles n={n}", hip, orc, state_exact=True)
