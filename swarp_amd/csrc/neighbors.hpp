@@ -37,7 +37,24 @@ __global__ __launch_bounds__(64) void k_neighbors(const Cst<T> C, const T *pos, 
     const int n = m_popc(m);
     int32_t *row = STAGE ? srows + ((size_t)(lane / PA) * C.A + agent) * C.K : idx + i * C.K;
     if (active) {
-        for (int k = 0; k < C.K; ++k) {
+        int k = 0;
+        if (STAGE && (C.K & 3) == 0) {
+            // 16-byte LDS writes: a row of K words at a stride of K words per lane puts
+            // every lane's k-th word in the same few banks, and one 16-byte write per four
+            // slots quarters the conflicting writes
+            for (; k < C.K; k += 4) {
+                int w[4];
+                for (int u = 0; u < 4; ++u) {
+                    w[u] = 0;
+                    if (k + u < n) {
+                        w[u] = m_ctz(m);
+                        m &= m - 1;
+                    }
+                }
+                *(int4 *)(row + k) = make_int4(w[0], w[1], w[2], w[3]);
+            }
+        }
+        for (; k < C.K; ++k) {
             int v = 0;
             if (k < n) {
                 v = m_ctz(m);

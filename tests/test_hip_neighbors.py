@@ -22,7 +22,8 @@ def _hip_lists(pos_np, radius, K, dtype=torch.float32):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float64])
 @pytest.mark.parametrize("E,A,radius,K", [(64, 4, 0.125, 4), (500, 16, 0.3, 16), (40, 32, 0.5, 8),
-                                          (30, 64, 0.3, 16), (7, 5, 0.2, 2), (3, 1, 0.5, 4)])
+                                          (30, 64, 0.3, 16), (7, 5, 0.2, 2), (3, 1, 0.5, 4),
+                                          (33, 12, 0.4, 7), (9, 24, 0.35, 12)])
 def test_lists_bitexact(dtype, E, A, radius, K):
     rng = np.random.default_rng(E * 131 + A)
     npdt = np.float32 if dtype == torch.float32 else np.float64
