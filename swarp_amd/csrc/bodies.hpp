@@ -26,7 +26,6 @@
 namespace swarp {
 
 constexpr int OB_W = 12;       // scalars per obstacle index in the per-env state
-constexpr int NOB_MAX = 16;    // obstacles per env on this path
 
 // Static obstacle tables of the body path.
 template <typename T> struct ObTab {
@@ -696,22 +695,28 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
     constexpr int EPW = 64 / PA;
     __shared__ T sl[4 * 64];                         // px py vx vy of the substep
     __shared__ T lr[64];                             // agent radius per lane
-    __shared__ T lob[2][EPW][OB_W * NOB_MAX];        // obstacle state: in / out of a substep
-    __shared__ T lcs[2][EPW][2 * NOB_MAX];           // its bodies' cos / sin (body_pass)
-    __shared__ T lext[NOB_MAX];                      // static extent per body root
+    // dynamic LDS (body_fwd_lds): [2][EPW][NW] obstacle state in / out of a substep,
+    // [2][EPW][2N] its bodies' cos / sin (body_pass), [N] static extent per body root
+    extern __shared__ __align__(16) unsigned char smem[];
+    const int NW = OB_W * tb.N;
+    T *const lob = (T *)smem;
+    T *const lcs = lob + (size_t)2 * EPW * NW;
+    T *const lext = lcs + (size_t)2 * EPW * 2 * tb.N;
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
     fold_prm<F>(L.pr);
     const BodyRow<T> br = body_row<T, PA>(C, tb, L);
     lr[L.lane] = L.pr.radius;
     const int ew = L.lane / PA;
-    const int NW = OB_W * tb.N;
+    // this env's obstacle state and body cos / sin in buffer c (0 / 1)
+    const auto obs = [&](int c) { return lob + ((size_t)c * EPW + ew) * NW; };
+    const auto ocs = [&](int c) { return lcs + ((size_t)c * EPW + ew) * 2 * tb.N; };
     const bool env_ok = L.env < C.E;
     const size_t eo = (size_t)(env_ok ? L.env : 0) * NW;
-    for (int q = L.agent; q < NW; q += PA) lob[0][ew][q] = io.ob0[eo + q];
+    for (int q = L.agent; q < NW; q += PA) obs(0)[q] = io.ob0[eo + q];
     for (int o = L.lane; o < tb.N; o += 64) lext[o] = body_ext(tb, o);
     __syncthreads();
-    body_trig<T, PA>(tb, L, lob[0][ew], lcs[0][ew]);
+    body_trig<T, PA>(tb, L, obs(0), ocs(0));
     St<T> st;
     load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
     if (!L.active) st.px = st.py = __builtin_nan("");
@@ -734,11 +739,11 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
             sl[F_VX * 64 + L.lane] = st.vx;
             sl[F_VY * 64 + L.lane] = st.vy;
             __syncthreads();
-            const T *obc = lob[cur][ew];
+            const T *obc = obs(cur);
             T Fx, Fy;
             forces_b<T, PA>(C, tb, L, sl, lr, obc, st, s, s == 0 || !ok, cand, Fx, Fy);
-            body_pass<T, PA>(C, tb, L, br, st, obc, lob[cur ^ 1][ew], lext, lcs[cur][ew],
-                             lcs[cur ^ 1][ew], nullptr);
+            body_pass<T, PA>(C, tb, L, br, st, obc, obs(cur ^ 1), lext, ocs(cur), ocs(cur ^ 1),
+                             nullptr);
             St<T> nx;
             integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
             if (C.use_skin) {
@@ -757,7 +762,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
                 store_state<T, DRONE>(g.fin.f, L.idx, st);
         }
         if (env_ok)
-            for (int q = L.agent; q < NW; q += PA) io.traj[(size_t)t * ENW + eo + q] = lob[cur][ew][q];
+            for (int q = L.agent; q < NW; q += PA) io.traj[(size_t)t * ENW + eo + q] = obs(cur)[q];
         for (int k = 0; k < 4; ++k) a[k] = an[k];
     }
 }
@@ -776,7 +781,15 @@ __host__ __device__ constexpr size_t body_bwd_lds(int S, int N, bool cache)
            + 2 * (size_t)(64 / PA) * OB_W * N * sizeof(T)        // obstacle adjoint in / out
            + (cache ? (size_t)(S + 1) * (64 / PA) * 2 * N * sizeof(T)   // body cos / sin
                           + (size_t)S * (64 / PA) * 3 * N * sizeof(T)   // body contact sums
-                    : 0);
+                    : 0)
+           + (size_t)N * sizeof(T);                         // static extent per body root
+}
+
+// Dynamic LDS of k_body_fwd: two obstacle states and two cos / sin tables per env slot of
+// the wave, and the extent table.
+__host__ __device__ constexpr size_t body_fwd_lds(int PA, int N, size_t tsize)
+{
+    return ((size_t)2 * (64 / PA) * (OB_W + 2) * N + N) * tsize;
 }
 
 // Reverse of body_pass for one env.  gout = adjoint of the pass's output (the env's
@@ -1039,7 +1052,8 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
     // with tb.cache: [S+1][EPW][2N] body cos / sin, [S][EPW][3N] body contact sums
     T *lcs = tb.cache ? lgob + (size_t)2 * EPW * NW : nullptr;
     T *lsum = tb.cache ? lcs + (size_t)(C.S + 1) * EPW * 2 * N : nullptr;
-    __shared__ T lext[NOB_MAX];                          // static extent per body root
+    // [N] static extent per body root, after the caches (or the adjoints without them)
+    T *lext = tb.cache ? lsum + (size_t)C.S * EPW * 3 * N : lgob + (size_t)2 * EPW * NW;
     for (int o = threadIdx.x; o < N; o += 64) lext[o] = body_ext(tb, o);
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
@@ -1239,12 +1253,13 @@ void launch_body_fwd(int PA, const Cst<T> &C, const Args<T> &a, const ObTab<T> &
 {
     const dim3 grid((C.E + 64 / PA - 1) / (64 / PA));
     constexpr unsigned P = body_profile<T>();
+    const size_t shm = body_fwd_lds(PA, tb.N, sizeof(T));
     if (drone) {
-        SWARP_BODY_DISPATCH(k_body_fwd, true, FT_ALL, 0)
+        SWARP_BODY_DISPATCH(k_body_fwd, true, FT_ALL, shm)
     } else if (P != 0u && (feat & ~P) == 0u) {
-        SWARP_BODY_DISPATCH(k_body_fwd, false, (P ? P : FT_ALL), 0)
+        SWARP_BODY_DISPATCH(k_body_fwd, false, (P ? P : FT_ALL), shm)
     } else {
-        SWARP_BODY_DISPATCH(k_body_fwd, false, FT_ALL, 0)
+        SWARP_BODY_DISPATCH(k_body_fwd, false, FT_ALL, shm)
     }
 }
 

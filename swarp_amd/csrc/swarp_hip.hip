@@ -414,8 +414,10 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
 
 template <typename T> static int fill_obtab(const swarp_desc_t *d, ObTab<T> &tb)
 {
-    if (d->n_obstacles < 1 || d->n_obstacles > NOB_MAX)
-        return fail("the body path takes 1 to 16 obstacles per env");
+    if (d->n_obstacles < 1) return fail("the body path takes at least one obstacle per env");
+    if (body_fwd_lds(pad_agents(d->n_agents), d->n_obstacles, sizeof(T)) > 65536)
+        return fail("too many obstacles per env for the body forward's LDS staging (limit "
+                    "64 KiB per wave)");
     if (!d->obs_kind || !d->obs_body || !d->obs_mass || !d->obs_inertia || !d->obs_body_off)
         return fail("obs_kind/obs_body/obs_mass/obs_inertia/obs_body_off must be set");
     if (wide_path(d))

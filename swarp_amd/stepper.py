@@ -268,8 +268,6 @@ class Stepper:
             raise ValueError(f"obstacle body indices must lie in [0, {n})")
         movable = obs.any_movable
         if movable:
-            if n > 16:
-                raise NotImplementedError("movable bodies: this build steps at most 16 obstacles per env")
             if self.has_boxes:
                 raise NotImplementedError("movable bodies with box agents are not implemented")
             if self.wide:

@@ -140,6 +140,36 @@ def test_bodies_match_oracle_config5_shape():
     check("config5", hip, orc)
 
 
+
+def _ring_extra(n, radius=1.0, r=0.07):
+    """n circles on a ring around the cross, every third one static."""
+    ang = np.linspace(0.0, 2 * np.pi, n, endpoint=False)
+    return tuple(((radius * np.cos(a), radius * np.sin(a)), r, k % 3 != 2)
+                 for k, a in enumerate(ang))
+
+
+@pytest.mark.parametrize("A,n_extra", [(64, 35), (16, 19)])
+def test_bodies_beyond_sixteen_obstacles(A, n_extra):
+    """More than 16 obstacles per env (each env's obstacle state staged in LDS sized by the
+    obstacle count): the cross body and a ring of movable and static circles, one env per
+    wave at 64 agents and four per wave at 16."""
+    E = 6 if A == 64 else 9
+    s0, acts = _pushers(E, A, 3, spread=1.2)
+    obs = cross_obs(E, (0.0, 0.0), extra=_ring_extra(n_extra))
+    hip, orc = run_pair(nav_agents(A), _world(bounds=2.0), 0.05, 4, s0, acts, obs, np.float32)
+    check(f"{5 + n_extra} obstacles", hip, orc)
+    assert np.abs(orc[1][-1] - orc[1][0]).max() > 1e-3, "no body moved"
+
+
+def test_bodies_obstacle_count_beyond_lds_is_rejected():
+    """An obstacle count whose per-env staging exceeds 64 KiB of LDS (float64, 4 agents per
+    env: 16 env slots per wave) is refused by the host before any launch."""
+    E, A = 3, 4
+    s0, acts = _pushers(E, A, 4)
+    obs = cross_obs(E, (0.0, 0.0), extra=_ring_extra(20))
+    with pytest.raises(RuntimeError, match="LDS"):
+        run_pair(nav_agents(A), _world(), 0.05, 4, s0, acts, obs, np.float64)
+
 def test_bodies_clamp_bounds():
     E, A = 8, 8
     s0, acts = _pushers(E, A, 3, spread=0.4)
