@@ -412,10 +412,23 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     return 0;
 }
 
+// Env slot width of the body kernels: the padded agent count, doubled (fewer env slots per
+// wave, more pad lanes) until the obstacle staging of both passes fits 64 KiB of LDS; 64
+// when nothing fits (the callers then refuse).
+template <typename T> static int body_pa(const swarp_desc_t *d)
+{
+    const bool dr = d->has_drone != 0;
+    int PA = pad_agents(d->n_agents);
+    while (PA < 64 && (body_fwd_lds(PA, d->n_obstacles, sizeof(T)) > 65536 ||
+                       body_bwd_lds_of<T>(PA, d->substeps, d->n_obstacles, dr, false) > 65536))
+        PA *= 2;
+    return PA;
+}
+
 template <typename T> static int fill_obtab(const swarp_desc_t *d, ObTab<T> &tb)
 {
     if (d->n_obstacles < 1) return fail("the body path takes at least one obstacle per env");
-    if (body_fwd_lds(pad_agents(d->n_agents), d->n_obstacles, sizeof(T)) > 65536)
+    if (body_fwd_lds(body_pa<T>(d), d->n_obstacles, sizeof(T)) > 65536)
         return fail("too many obstacles per env for the body forward's LDS staging (limit "
                     "64 KiB per wave)");
     if (!d->obs_kind || !d->obs_body || !d->obs_mass || !d->obs_inertia || !d->obs_body_off)
@@ -463,7 +476,7 @@ static int rollout_fwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     a.act = (const T *)act;
     a.nsteps = nT;
     ObIO<T> io = {(const T *)ob0, (T *)ob_traj, nullptr, nullptr};
-    const int PA = pad_agents(d->n_agents);
+    const int PA = body_pa<T>(d);
     launch_body_fwd<T>(PA, C, a, tb, io, world_features(d, true), d->has_drone != 0, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
@@ -496,13 +509,15 @@ static int rollout_bwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     a.aact = (T *)aact;
     a.nsteps = nT;
     ObIO<T> io = {(const T *)ob0, (T *)ob_traj, (const T *)aob_traj, (T *)aob0};
-    const int PA = pad_agents(d->n_agents);
+    const int PA = body_pa<T>(d);
     // the per-substep body caches (cos / sin, contact sums) when they fit
     const bool dr = d->has_drone != 0;
     size_t shm = body_bwd_lds_of<T>(PA, d->substeps, d->n_obstacles, dr, true);
     tb.cache = shm <= 65536 ? 1 : 0;
     if (!tb.cache) shm = body_bwd_lds_of<T>(PA, d->substeps, d->n_obstacles, dr, false);
-    if (shm > 65536) return fail("substeps too large for the body backward's LDS staging (limit 64 KiB per wave)");
+    if (shm > 65536)
+        return fail("obstacle count or substeps too large for the body backward's LDS staging "
+                    "(limit 64 KiB per wave)");
     launch_body_bwd<T>(PA, C, a, tb, io, world_features(d, true), d->has_drone != 0, shm, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));

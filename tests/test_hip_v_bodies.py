@@ -161,12 +161,23 @@ def test_bodies_beyond_sixteen_obstacles(A, n_extra):
     assert np.abs(orc[1][-1] - orc[1][0]).max() > 1e-3, "no body moved"
 
 
+def test_bodies_few_agents_many_obstacles():
+    """4 agents per env with 13 obstacles: at 16 env slots per wave the backward's obstacle
+    staging would exceed 64 KiB of LDS, so the body kernels run wider env slots (pad lanes)."""
+    E, A = 10, 4
+    s0, acts = _pushers(E, A, 5)
+    obs = cross_obs(E, (0.0, 0.0), extra=_ring_extra(8, radius=0.5))
+    hip, orc = run_pair(nav_agents(A), _world(), 0.05, 4, s0, acts, obs, np.float32)
+    check("4 agents, 13 obstacles", hip, orc)
+    assert np.abs(orc[1][-1] - orc[1][0]).max() > 1e-3, "no body moved"
+
+
 def test_bodies_obstacle_count_beyond_lds_is_rejected():
-    """An obstacle count whose per-env staging exceeds 64 KiB of LDS (float64, 4 agents per
-    env: 16 env slots per wave) is refused by the host before any launch."""
+    """An obstacle count whose backward staging exceeds 64 KiB of LDS even at one env per
+    wave (float64, 100 obstacles) is refused by the host before the backward launches."""
     E, A = 3, 4
     s0, acts = _pushers(E, A, 4)
-    obs = cross_obs(E, (0.0, 0.0), extra=_ring_extra(20))
+    obs = cross_obs(E, (0.0, 0.0), extra=_ring_extra(95))
     with pytest.raises(RuntimeError, match="LDS"):
         run_pair(nav_agents(A), _world(), 0.05, 4, s0, acts, obs, np.float64)
 
