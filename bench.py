@@ -13,7 +13,11 @@ roofline come from HIP events recorded around each launch, on the stream it goes
 a second timed loop of the same steps (the events' markers stay out of the first).
 
 ``cpu_baseline`` times the CPU oracle (oracle/swarp_oracle.c, OpenMP over envs) on a
-bounded sample of the same workload on this host's cores.
+bounded sample of the same workload on this host's cores.  Its first oracle run takes
+the timed workload's own inputs for 256 envs, and ``self_check`` records how the GPU's
+outputs for those envs (one more iteration after the timed loops) compare with it:
+states bit-exact, gradients within the parity tests' bars; bench.py exits non-zero
+after printing its line when they do not.
 """
 
 from __future__ import annotations
@@ -90,8 +94,32 @@ def make_problem(E, A, T, S, seed=0):
     return stepper, state, goals, acts, cfgs, world
 
 
-def cpu_baseline(E_full, A, T, S, seconds, cfgs, world):
-    """Oracle fwd+bwd on a bounded env sample, OpenMP over every host core."""
+def gpu_sample(stepper, state, goals, acts, n):
+    """The timed BPTT iteration once more, outside the timed loops, keeping what the
+    benchmark discards: the inputs and outputs of its first n envs (every step's state,
+    d loss / d actions, d loss / d initial positions), as float32 numpy arrays.  Envs are
+    independent, so these are the outputs of an n-env run on the same inputs."""
+    import torch
+
+    from swarp_amd import rollout
+
+    a = acts.clone().requires_grad_(True)
+    s0 = type(state)(state.pos.clone().requires_grad_(True), *state[1:])
+    final, traj = rollout(stepper, s0, a)
+    ((final.pos - goals) ** 2).sum().backward()
+    host = lambda x: x[:n].detach().float().cpu().numpy()  # noqa: E731
+    st = [torch.cat([x.pos, x.theta[..., None], x.vel, x.speed[..., None],
+                     x.ang_vel[..., None]], -1) for x in traj]
+    return {"pos0": host(state.pos), "acts": acts[:, :n].float().cpu().numpy(),
+            "goals": host(goals), "states": torch.stack([s[:n] for s in st]).detach().cpu().numpy(),
+            "g_acts": a.grad[:, :n].float().cpu().numpy(), "g_pos0": host(s0.pos.grad)}
+
+
+def cpu_baseline(E_full, A, T, S, seconds, cfgs, world, sample=None):
+    """Oracle fwd+bwd on a bounded env sample, OpenMP over every host core.  With
+    `sample` (gpu_sample's arrays) the oracle's first run takes the GPU's own inputs for
+    those envs and its outputs are compared with the GPU's: states bit-exact, gradients
+    by max-norm and element-wise relative error (the parity tests' bars)."""
     import numpy as np
 
     from oracle.oracle import Oracle, cores, pack_state
@@ -102,12 +130,17 @@ def cpu_baseline(E_full, A, T, S, seconds, cfgs, world):
     tags = np.zeros(A, np.int32)
     modes = np.zeros(A, np.int32)
     b = world.bounds
+    check = {}
 
-    def run(E):
-        rng = np.random.default_rng(0)
-        s0 = pack_state({"pos": rng.uniform(-2, 2, size=(E, A, 2))}, dtype=np.float32)
-        acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
-        goals = rng.uniform(-2, 2, size=(E, A, 2)).astype(np.float32)
+    def run(E, inputs=None):
+        if inputs is None:
+            rng = np.random.default_rng(0)
+            pos = rng.uniform(-2, 2, size=(E, A, 2))
+            acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
+            goals = rng.uniform(-2, 2, size=(E, A, 2)).astype(np.float32)
+        else:
+            pos, acts, goals = inputs["pos0"], inputs["acts"], inputs["goals"]
+        s0 = pack_state({"pos": pos}, dtype=np.float32)
         cfg = dict(n_envs=E, n_agents=A, act_dim=2, substeps=S, max_neighbors=world.max_neighbors,
                    collisions=1, soft_walls=1, clamp_bounds=0, n_threads=n, dt=0.05,
                    k=world.collision_k, c=world.collision_c, margin=world.collision_margin,
@@ -117,9 +150,31 @@ def cpu_baseline(E_full, A, T, S, seconds, cfgs, world):
         states = O.rollout(cfg, rows, tags, modes, None, s0, acts)
         afin = np.zeros_like(s0)
         afin[..., 0:2] = 2 * (states[-1][..., 0:2] - goals)
-        O.rollout_adj(cfg, rows, tags, modes, None, s0, acts, states, None, afin)
-        return time.perf_counter() - t0
+        g0, ga = O.rollout_adj(cfg, rows, tags, modes, None, s0, acts, states, None, afin)
+        el = time.perf_counter() - t0
+        if inputs is not None:
+            def rel(h, o, floor=None):
+                h, o = h.astype(np.float64), o.astype(np.float64)
+                top = max(np.abs(o).max(), 1e-30)
+                if floor is None:
+                    return float(np.abs(h - o).max() / top)
+                return float((np.abs(h - o) / (np.abs(o) + floor * top)).max())
 
+            ra, rp = rel(inputs["g_acts"], ga), rel(inputs["g_pos0"], g0[..., 0:2])
+            ea, ep = rel(inputs["g_acts"], ga, 1e-3), rel(inputs["g_pos0"], g0[..., 0:2], 1e-3)
+            exact = bool(np.array_equal(inputs["states"], states[..., 0:7]))
+            check.update({
+                "envs": E, "of": E_full, "states_bitexact": exact,
+                "d_actions_rel_maxnorm": ra, "d_actions_rel_elementwise": ea,
+                "d_pos0_rel_maxnorm": rp, "d_pos0_rel_elementwise": ep,
+                "bars": "states bit-exact; gradients max-norm <= 1e-5 and element-wise <= 1e-4 "
+                        "(|diff| / (|oracle| + 1e-3 max|oracle|))",
+                "ok": exact and max(ra, rp) <= 1e-5 and max(ea, ep) <= 1e-4,
+            })
+        return el
+
+    if sample is not None:
+        run(sample["pos0"].shape[0], sample)
     probe = max(n * 8, 64)
     dt_probe = run(probe)
     E = int(min(E_full, max(probe, probe * seconds / max(dt_probe, 1e-6))))
@@ -128,7 +183,7 @@ def cpu_baseline(E_full, A, T, S, seconds, cfgs, world):
     while total < seconds and reps < 50:
         total += run(E)
         reps += 1
-    return {
+    return check, {
         "value": E * T * reps / total,
         "unit": "env-steps/s",
         "cores": n,
@@ -482,7 +537,12 @@ def main():
             }
         out["env_step_nograd_16000x16"] = rows
     if args.cpu_seconds > 0:
-        out["cpu_baseline"] = cpu_baseline(E, A, T, S, args.cpu_seconds, cfgs, world)
+        # the oracle also replays the timed workload's first 256 envs from their inputs and
+        # the result is compared with the GPU's outputs for them (outside the timed loops)
+        sample = gpu_sample(stepper, state, goals, acts, min(256, E))
+        check, out["cpu_baseline"] = cpu_baseline(E, A, T, S, args.cpu_seconds, cfgs, world,
+                                                  sample)
+        out["self_check"] = check
     if args.copy_mb > 0:
         n = args.copy_mb * (1 << 20) // 4
         src = torch.ones(n, device="cuda")
@@ -492,6 +552,10 @@ def main():
         torch.cuda.synchronize()
         out["copy_calibration_bytes"] = {"read": 4 * n, "write": 4 * n}
     print(json.dumps(out), flush=True)
+    if "self_check" in out and not out["self_check"].get("ok", False):
+        print("bench.py: the timed kernels' outputs disagree with the CPU oracle "
+              "(self_check); the throughput above is not valid", file=sys.stderr)
+        sys.exit(1)
 
 
 if __name__ == "__main__":

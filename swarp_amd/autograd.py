@@ -458,14 +458,20 @@ def _assemble(stepper: Stepper, state: TorchState, outs, T: int, given=(True,) *
     tail = tuple(state[nf:]) if nf == 5 else ()
     final_tail = tuple(t.clone() if given[nf + k] else t for k, t in enumerate(tail))
     final = TorchState(*final_f, *final_tail)
+    # the per-step views are built later, possibly under another grad mode (a no_grad
+    # logging read, inference mode): they are built under the modes of this call, so that
+    # they carry the same autograd history as states built eagerly here would
+    grad_on = torch.is_grad_enabled()
+    inference_on = torch.is_inference_mode_enabled()
 
     def build():
         # one unbind per field (a single autograd node) instead of T - 1 selects per field;
         # the passed-through fields of the T - 1 states as one broadcast copy per field
         # (each state owns its own slice) instead of T - 1 copies
-        per_step = [f.unbind(0) for f in traj_f] if T > 1 else []
-        tails = ([x.unsqueeze(0).expand(T - 1, *x.shape).clone().unbind(0) for x in tail]
-                 if T > 1 else [])
+        with torch.inference_mode(inference_on), torch.set_grad_enabled(grad_on):
+            per_step = [f.unbind(0) for f in traj_f] if T > 1 else []
+            tails = ([x.unsqueeze(0).expand(T - 1, *x.shape).clone().unbind(0) for x in tail]
+                     if T > 1 else [])
         steps = [TorchState(*(u[t] for u in per_step), *(v[t] for v in tails))
                  for t in range(T - 1)]
         steps.append(final)

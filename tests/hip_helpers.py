@@ -108,6 +108,37 @@ def oracle_run(configs, world, dt, substeps, s0_16, acts_np, w_traj, np_dtype, o
 
 
 def rel(a, b):
+    """Max-norm relative error: max |a - b| / max |b|."""
     a = np.asarray(a, dtype=np.float64)
     b = np.asarray(b, dtype=np.float64)
     return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+# Element-wise bar of the gradient parity tests: every element within ELEM_FACTOR times
+# the max-norm tolerance of the reference value, relative to its magnitude plus an
+# absolute floor of ELEM_FLOOR times the tensor's largest magnitude.  (An adjoint element
+# that cancels to a small value carries the rounding of the terms it was summed from,
+# and the summation order of the reverse pass is not the oracle's everywhere, so an
+# element-wise bar needs the floor; fp32 runs measure up to 7e-5 with floor 1e-3, fp64
+# runs 2e-13.)  With the fp32 tolerance 1e-5: each element within 1e-4 relative, or
+# within 1e-7 of the largest element absolutely.
+ELEM_FACTOR, ELEM_FLOOR = 10.0, 1e-3
+
+
+def rel_elem(a, b, floor=ELEM_FLOOR):
+    """Element-wise relative error with an absolute floor:
+    max_i |a_i - b_i| / (|b_i| + floor * max |b|)."""
+    a = np.asarray(a, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    den = np.abs(b) + floor * max(np.abs(b).max(), 1e-30)
+    return float((np.abs(a - b) / den).max())
+
+
+def check_grad(name, h, o, tol=1e-5, rtol=None, floor=ELEM_FLOOR):
+    """Gradient parity: max-norm relative error <= tol and element-wise relative error
+    (with the absolute floor) <= rtol (default ELEM_FACTOR * tol); both are printed."""
+    rtol = ELEM_FACTOR * tol if rtol is None else rtol
+    mn, el = rel(h, o), rel_elem(h, o, floor)
+    print(f"{name}: max-norm rel {mn:.3e}, element-wise rel (floor {floor:g}) {el:.3e}")
+    assert mn <= tol, f"{name}: max-norm rel {mn:.3e} > {tol:g}"
+    assert el <= rtol, f"{name}: element-wise rel {el:.3e} > {rtol:g}"

@@ -21,7 +21,7 @@ import pytest
 import torch
 
 from cases import nav_agents, nav_inputs, nav_world
-from hip_helpers import hip_run, make_stepper, oracle_run, rel
+from hip_helpers import check_grad, hip_run, make_stepper, oracle_run, rel
 from oracle.oracle import pack_state
 from swarp_amd.config import AgentConfig, ControlMode, DynamicsModel, ObstacleShape, WorldConfig
 
@@ -64,8 +64,8 @@ def _check(name, hip, orc, state_exact, g_tol=1e-5, nf=5, o64=None):
             f"{name}: states not bit-exact, max rel {rel(hs[..., cols], os_[..., cols]):.3e}")
     else:
         assert rel(hs[..., cols], os_[..., cols]) <= 1e-5, f"{name}: states rel {rel(hs[..., cols], os_[..., cols]):.3e}"
-    assert rel(hga, oga) <= g_tol, f"{name}: d/d actions rel {rel(hga, oga):.3e}"
-    assert rel(hg0[..., cols], og0[..., cols]) <= g_tol, f"{name}: d/d state0 rel {rel(hg0[..., cols], og0[..., cols]):.3e}"
+    check_grad(f"{name}: d/d actions", hga, oga, tol=g_tol)
+    check_grad(f"{name}: d/d state0", hg0[..., cols], og0[..., cols], tol=g_tol)
 
 
 def test_config1_navigation_bitexact():

@@ -15,7 +15,7 @@ import pytest
 import torch
 
 from cases import body_seed_np, nav_agents, obstacles_np, oracle_cfg, params_of
-from hip_helpers import make_stepper, rel, state_to16, to_torch_state
+from hip_helpers import check_grad, make_stepper, rel, state_to16, to_torch_state
 from oracle.oracle import Oracle, pack_state
 from swarp_amd import rollout
 from swarp_amd.config import AgentConfig, Integrator, WorldConfig
@@ -96,9 +96,9 @@ def check(name, hip, orc, exact=True, g_tol=1e-5):
         assert np.array_equal(hob, oob), f"{name}: obstacle states not bit-exact (rel {rel(hob, oob):.2e})"
     else:
         assert rel(hs[..., :7], os_[..., :7]) <= 1e-12 and rel(hob, oob) <= 1e-12, name
-    assert rel(hga, oga) <= g_tol, f"{name}: d/d actions rel {rel(hga, oga):.3e}"
-    assert rel(hg0, og0) <= g_tol, f"{name}: d/d pos0 rel {rel(hg0, og0):.3e}"
-    assert rel(hgob, ogob) <= g_tol, f"{name}: d/d ob0 rel {rel(hgob, ogob):.3e}"
+    check_grad(f"{name}: d/d actions", hga, oga, tol=g_tol)
+    check_grad(f"{name}: d/d pos0", hg0, og0, tol=g_tol)
+    check_grad(f"{name}: d/d ob0", hgob, ogob, tol=g_tol)
 
 
 def _world(bounds=1.5, mode="soft", **kw):
@@ -138,6 +138,88 @@ def test_bodies_match_oracle_config5_shape():
     obs = cross_obs(E, (0.0, 0.0))
     hip, orc = run_pair(nav_agents(A), _world(bounds=3.0), 0.05, 4, s0, acts, obs, np.float32)
     check("config5", hip, orc)
+
+
+def _coo(idx, cnt):
+    """COO [2, n] (row 0 sender e*A + idx, row 1 receiver e*A + a, (e, a, slot) order) of
+    padded lists, as NeighborGrid.edge_index (swarp/core/neighbors.py:716-733)."""
+    E, A = cnt.shape
+    snd, rcv = [], []
+    for e in range(E):
+        for a in range(A):
+            for k in range(cnt[e, a]):
+                snd.append(e * A + idx[e, a, k])
+                rcv.append(e * A + a)
+    return np.array([snd, rcv], dtype=np.int64).reshape(2, -1)
+
+
+def test_bodies_config5_spec_against_oracle():
+    """Config 5 at its specification, on 64 of its 16000 envs: 64 agents per env with
+    positions U[-3, 3]^2 and actions U[-1, 1]^2 around the cross (5 circles r 0.1, mass 1,
+    inertia from the geometry) in soft walls at +-3, 16 steps of 4 substeps, lists of
+    radius 0.3 capped at K = 16, loss = squared distance of the body to a goal U[-2, 2]^2.
+    Agent and body states bit-exact; every step's lists, counts, overflow flags and COO
+    radius graph equal to the oracle's; gradients to the actions, the initial positions
+    and the initial obstacle state within 1e-5 (max-norm and element-wise)."""
+    E, A, T, S = 64, 64, 16, 4
+    rng = np.random.default_rng(55)
+    pos = rng.uniform(-3.0, 3.0, size=(E, A, 2))
+    acts = rng.uniform(-1.0, 1.0, size=(T, E, A, 2)).astype(np.float32)
+    goals = rng.uniform(-2.0, 2.0, size=(E, 2)).astype(np.float32)
+    s0 = pack_state({"pos": pos}).astype(np.float32)
+    cfgs = [AgentConfig(radius=0.05, max_speed=1.0, max_accel=2.0) for _ in range(A)]
+    world = _world(bounds=3.0)
+    obs = cross_obs(E, (0.0, 0.0))
+    st = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
+    ob0 = st.ob_state.detach().clone().requires_grad_(True)
+    st.ob_state = ob0
+    s0t = to_torch_state(s0, torch.float32, True, 5)
+    a = torch.tensor(acts, device="cuda", requires_grad=True)
+    final, traj = rollout(st, s0t, a)
+    body = st.ob_trajectory[-1][:, 30:32]  # the body rooted at shape 0: its position
+    loss = ((body - torch.tensor(goals, device="cuda")) ** 2).sum()
+    loss.backward()
+    hs = np.stack([state_to16(x) for x in traj])
+    hob = st.ob_trajectory.detach().double().cpu().numpy()
+    grid = st.grid(E)
+    h_lists = []
+    for x in traj:
+        grid.build(x.pos.detach())
+        idx, cnt = grid.neighbor_idx.cpu().numpy(), grid.neighbor_count.cpu().numpy()
+        h_lists.append((idx, cnt, grid.overflow_view().cpu().numpy(),
+                        grid.edge_index().cpu().numpy()))
+
+    O = Oracle(np.float32)
+    cfg = oracle_cfg(cfgs, world, 0.05, S, E, 2, n_threads=8)
+    p, t_, m = params_of(cfgs)
+    ob = obstacles_np(obs, E)
+    ob0n = ob0.detach().cpu().numpy()
+    ost, oob = O.rollout_ob(cfg, p, t_, m, ob, s0, ob0n, acts)
+    w_ob = np.zeros(oob.shape)
+    w_ob[-1, :, 30:32] = 2.0 * (oob[-1, :, 30:32].astype(np.float64) - goals)
+    g0, gob0, ga = O.rollout_adj_ob(cfg, p, t_, m, ob, s0, ob0n, acts, ost, oob, None, None,
+                                    w_ob, None)
+
+    assert np.array_equal(hs[..., :7], ost[..., :7].astype(np.float64)), (
+        f"agent states not bit-exact (rel {rel(hs[..., :7], ost[..., :7]):.2e})")
+    assert np.array_equal(hob, oob.astype(np.float64)), "body states not bit-exact"
+    n_over = n_edges = 0
+    for k, (idx, cnt, over, coo) in enumerate(h_lists):
+        oi, oc, ot = O.neighbors(ost[k, ..., 0:2], 0.3, 16)
+        assert np.array_equal(cnt, oc), f"step {k}: counts differ"
+        for e in range(E):
+            for i in range(A):
+                assert np.array_equal(idx[e, i, :cnt[e, i]], oi[e, i, :oc[e, i]]), f"step {k}: lists differ"
+        assert np.array_equal(over, ot > oc), f"step {k}: overflow flags differ"
+        assert np.array_equal(coo, _coo(oi, oc)), f"step {k}: COO differs"
+        n_over += int(over.sum())
+        n_edges += coo.shape[1]
+    print(f"\nconfig5 spec: {n_edges} edges and {n_over} overflowing lists over {T} steps")
+    assert n_edges > 0
+    check_grad("config5 spec d/d actions", a.grad.double().cpu().numpy(), ga)
+    check_grad("config5 spec d/d pos0", s0t.pos.grad.double().cpu().numpy(), g0[..., 0:2])
+    check_grad("config5 spec d/d ob0", ob0.grad.double().cpu().numpy(), gob0)
+    assert np.abs(ga).max() > 0, "no gradient reached the actions"
 
 
 

@@ -505,3 +505,39 @@ def test_trajectory_is_a_list_built_on_first_use():
     assert len(t) == 4 and t.index("s3") == 3 and built == [1]
     e = Trajectory(0, list)
     assert len(e) == 0 and not e and list(e) == []
+
+
+def test_trajectory_built_under_no_grad_keeps_the_rollout_grad_mode():
+    """A trajectory first read under no_grad (or inference mode) must still give the
+    gradients an eager build would: the per-step views are built under the grad mode of
+    the rollout call, not of the first read."""
+    from swarp_amd.autograd import _assemble
+
+    class St:
+        has_drone = False
+
+    T, E, A = 4, 3, 2
+    torch.manual_seed(0)
+    src = [torch.randn(T, E, A, 2, requires_grad=True), torch.randn(T, E, A, requires_grad=True),
+           torch.randn(T, E, A, 2, requires_grad=True), torch.randn(T, E, A, requires_grad=True),
+           torch.randn(T, E, A, requires_grad=True)]
+    tail = [torch.zeros(E, A, requires_grad=True), torch.zeros(E, A, requires_grad=True),
+            torch.zeros(E, A, 4, requires_grad=True), torch.zeros(E, A, 3, requires_grad=True)]
+
+    def run(read_first):
+        outs = [f[T - 1] * 2.0 for f in src] + [f[:T - 1] * 2.0 for f in src]
+        state = [None] * 5 + tail
+        final, traj = _assemble(St(), state, outs, T)
+        if read_first is not None:
+            with read_first():
+                _ = traj[0].pos.sum().item()
+        loss = sum((s.pos ** 2).sum() + s.theta.sum() + s.vel.sum() + s.speed.sum()
+                   + s.ang_vel.sum() + s.z.sum() for s in traj[:T - 1])
+        grads = torch.autograd.grad(loss, src + tail[:1])
+        return [g.clone() for g in grads]
+
+    eager = run(None)
+    for mode in (torch.no_grad, torch.inference_mode):
+        lazy = run(mode)
+        assert all(torch.equal(a, b) for a, b in zip(eager, lazy)), mode
+    assert eager[0].abs().sum() > 0 and eager[-1].abs().sum() > 0
