@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 14
+#define SWARP_ABI_VERSION 15
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -200,8 +200,12 @@ int swarp_rollout_bwd_tape(const swarp_desc_t *desc, int32_t T, const swarp_stat
  * body shapes of any type; the reference runs it on untaped steps,
  * swarp/core/stepper.py:952-991).  Replaces T calls of Stepper.launch_substeps with the
  * body pass enabled.  Fleets of any dynamics models including drones, shared or per-env
- * parameter rows (then desc->body_params), disc agents, at most 64 agents per env,
- * 1 <= n_obstacles <= 16.
+ * parameter rows (then desc->body_params), disc agents, at most 64 agents per env, and
+ * n_obstacles >= 1 up to what the per-env obstacle staging allows: the forward's and the
+ * backward's LDS of one workgroup (dynamic and static) stay within 64 KiB, the env slots
+ * widened (fewer envs per wave) as far as one env per wave when needed; at 64 agents, 4
+ * substeps and float32 that is 553 obstacles forward and 164 backward.  Beyond it the call
+ * fails before any launch (swarp_rollout_bwd_ob_check asks the backward's limit).
  * ob0 [E, 12N]: per env and obstacle index o, the shape state (pos x, pos y, angle,
  * vel x, vel y, ang_vel) at [6o..6o+5] and the state of the body rooted at o at
  * [6N+6o..6N+6o+5] (the reference's obs_* and body_* arrays, stepper.py:418-431).
@@ -221,6 +225,15 @@ int swarp_rollout_bwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
                          const swarp_state_t *adj_final, const void *adj_ob_traj,
                          const swarp_state_t *adj_state0, void *adj_ob0, void *adj_actions,
                          void *stream);
+
+/* 0 when swarp_rollout_bwd_ob can run a configuration (descriptor valid for the body path,
+ * obstacle staging within the backward's LDS), else -1 with the reason in
+ * swarp_last_error.  Replaces no reference function: a caller whose forward will be
+ * differentiated asks it before swarp_rollout_fwd_ob, so that a configuration the
+ * backward refuses is refused before the forward advances any state (the reference's
+ * taped forward and its backward accept the same configurations,
+ * swarp/interop/autograd.py:229-296). */
+int swarp_rollout_bwd_ob_check(const swarp_desc_t *desc);
 
 /* Padded radius-neighbour lists of one state: replaces NeighborGrid.query_into's
  * brute-force kernel (swarp/core/neighbors.py:76-97, 465-492).  pos [E,A,2] of

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 F32, F64 = 0, 1
 EULER, RK4 = 0, 1
 LISTS_BRUTE, LISTS_GRID = 0, 1
@@ -160,6 +160,7 @@ SIGNATURES = {
          ctypes.c_void_p, ctypes.c_void_p],
         ctypes.c_int,
     ),
+    "swarp_rollout_bwd_ob_check": ([ctypes.POINTER(SwarpDesc)], ctypes.c_int),
     "swarp_neighbors": (
         [ctypes.POINTER(SwarpDesc), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
          ctypes.c_void_p, ctypes.c_void_p],

@@ -372,6 +372,11 @@ def _rollout_bodies(stepper: Stepper, state: TorchState, actions_seq: torch.Tens
         or any(t is not None and t.requires_grad for t in state))
     nf = _nfields(stepper)
     if grad:
+        # a configuration the body backward refuses is refused before the forward runs,
+        # so that stepper.ob_state / ob_trajectory are not advanced by a forward whose
+        # backward could not follow
+        _lib.check(_lib.load().swarp_rollout_bwd_ob_check(
+            ctypes.byref(stepper.desc(E, actions_seq.shape[3]))))
         outs = _RolloutObFn.apply(stepper, actions_seq, ob0, *state[:nf])
         ob_traj = outs[2 * nf]
         outs = outs[:2 * nf]

@@ -792,6 +792,13 @@ __host__ __device__ constexpr size_t body_fwd_lds(int PA, int N, size_t tsize)
     return ((size_t)2 * (64 / PA) * (OB_W + 2) * N + N) * tsize;
 }
 
+// All LDS of one k_body_fwd workgroup: the dynamic part above and the kernel's static
+// arrays (sl[4 * 64] and lr[64] scalars).  The 64 KiB limits are checked on this total.
+__host__ __device__ constexpr size_t body_fwd_lds_total(int PA, int N, size_t tsize)
+{
+    return body_fwd_lds(PA, N, tsize) + (size_t)5 * 64 * tsize;
+}
+
 // Reverse of body_pass for one env.  gout = adjoint of the pass's output (the env's
 // obstacle state after the substep), gin receives the adjoint of its input (overwritten);
 // the lane's agent adjoint is accumulated into `ga`.  ext / cs_in / cs_out / sums are what

@@ -136,8 +136,14 @@ int scratch_ptr(void **ptr)
     if (dev < 0 || dev >= MAX_DEVICES) return fail("device ordinal out of range");
     std::lock_guard<std::mutex> lk(g_mu);
     if (!g_ptr[dev]) {
+        // The lookup is not a stream operation, but a caller may be capturing a graph in
+        // the global capture mode, which refuses calls of this kind from any thread: this
+        // thread's mode is relaxed around the lookup and restored after it.
+        hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+        const bool swapped = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
         void *p = nullptr;
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (swapped) (void)hipThreadExchangeStreamCaptureMode(&mode);
         if (e != hipSuccess || !p) {
             char m[160];
             snprintf(m, sizeof m, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));

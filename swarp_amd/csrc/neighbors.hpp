@@ -80,11 +80,12 @@ __global__ __launch_bounds__(64) void k_neighbors(const Cst<T> C, const T *pos, 
     }
 }
 
-// LDS bytes of the staged rows of one wave (0: rows too long to stage).
-inline size_t neighbors_stage_bytes(int PA, int A, int K)
+// LDS bytes of the staged rows of one wave (0: rows too long to stage: with the kernel's
+// static position arrays lx / ly, a workgroup's LDS stays within 64 KiB).
+inline size_t neighbors_stage_bytes(int PA, int A, int K, size_t tsize)
 {
     const size_t b = (size_t)(64 / PA) * A * K * sizeof(int32_t);
-    return b <= 65536 ? b : 0;
+    return b + 2 * 64 * tsize <= 65536 ? b : 0;
 }
 
 template <typename T>
@@ -92,7 +93,7 @@ void launch_neighbors(int PA, const Cst<T> &C, const T *p, int32_t *idx, int32_t
                       int32_t *tru, hipStream_t st)
 {
     const dim3 grid((C.E + (64 / PA) - 1) / (64 / PA));
-    const size_t shm = neighbors_stage_bytes(PA, C.A, C.K);
+    const size_t shm = neighbors_stage_bytes(PA, C.A, C.K, sizeof(T));
 #define SWARP_NBR(PA_)                                                                             \
     if (shm)                                                                                       \
         hipLaunchKernelGGL((k_neighbors<T, PA_, true>), grid, dim3(64), shm, st, C, p, idx, cnt, tru); \

@@ -247,7 +247,8 @@ static const char *wide_unsupported(const swarp_desc_t *d)
 template <typename T> static int wide_lds_check(const swarp_desc_t *d)
 {
     const int NC = d->neighbor_method == SWARP_LISTS_GRID ? d->grid_bins * d->grid_bins : 0;
-    if (wide_lds_bytes<T>(((d->n_agents + 63) / 64) * 64, NC) > 65536)
+    // dynamic staging + k_wide_lists' static wsum[16]: the workgroup's whole LDS
+    if (wide_lds_bytes<T>(((d->n_agents + 63) / 64) * 64, NC) + 16 * sizeof(int32_t) > 65536)
         return fail("n_agents too large for the wide-env LDS staging at this dtype (limit 64 KiB)");
     return 0;
 }
@@ -400,7 +401,9 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
                  (size_t)d->substeps * 64 * msz;
     if (d->has_boxes)  // contact masks, heading cos / sin, static-contact flags per substep
         shm += (size_t)d->substeps * 64 * (msz + 2 * sizeof(T) + 8 + 1);
-    if (shm > 65536) return fail("substeps too large for the backward LDS staging (limit 64 KiB per wave)");
+    // with k_rollout_bwd's static arrays (ocs_lds[2 OCS_MAX], lbx[3 * 64]): the whole LDS
+    if (shm + (2 * OCS_MAX + 3 * 64) * sizeof(T) > 65536)
+        return fail("substeps too large for the backward LDS staging (limit 64 KiB per wave)");
     if (d->has_drone)
         launch_bwd<T, true, false>(PA, C, a, world_features(d, false), shm, st);
     else if (d->has_boxes)
@@ -419,7 +422,7 @@ template <typename T> static int body_pa(const swarp_desc_t *d)
 {
     const bool dr = d->has_drone != 0;
     int PA = pad_agents(d->n_agents);
-    while (PA < 64 && (body_fwd_lds(PA, d->n_obstacles, sizeof(T)) > 65536 ||
+    while (PA < 64 && (body_fwd_lds_total(PA, d->n_obstacles, sizeof(T)) > 65536 ||
                        body_bwd_lds_of<T>(PA, d->substeps, d->n_obstacles, dr, false) > 65536))
         PA *= 2;
     return PA;
@@ -428,7 +431,7 @@ template <typename T> static int body_pa(const swarp_desc_t *d)
 template <typename T> static int fill_obtab(const swarp_desc_t *d, ObTab<T> &tb)
 {
     if (d->n_obstacles < 1) return fail("the body path takes at least one obstacle per env");
-    if (body_fwd_lds(body_pa<T>(d), d->n_obstacles, sizeof(T)) > 65536)
+    if (body_fwd_lds_total(body_pa<T>(d), d->n_obstacles, sizeof(T)) > 65536)
         return fail("too many obstacles per env for the body forward's LDS staging (limit "
                     "64 KiB per wave)");
     if (!d->obs_kind || !d->obs_body || !d->obs_mass || !d->obs_inertia || !d->obs_body_off)
@@ -521,6 +524,18 @@ static int rollout_bwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     launch_body_bwd<T>(PA, C, a, tb, io, world_features(d, true), d->has_drone != 0, shm, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
+    return 0;
+}
+
+// Whether rollout_bwd_ob can run this configuration (the checks it makes before its launch).
+template <typename T> static int bwd_ob_fits(const swarp_desc_t *d)
+{
+    ObTab<T> tb;
+    if (fill_obtab<T>(d, tb)) return -1;
+    if (body_bwd_lds_of<T>(body_pa<T>(d), d->substeps, d->n_obstacles, d->has_drone != 0, false) >
+        65536)
+        return fail("obstacle count or substeps too large for the body backward's LDS staging "
+                    "(limit 64 KiB per wave)");
     return 0;
 }
 
@@ -637,6 +652,16 @@ int swarp_rollout_bwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
                                      adj_final, adj_ob_traj, adj_state0, adj_ob0, adj_actions, st);
     return rollout_bwd_ob<double>(desc, T, state0, ob0, actions, traj, ob_traj, adj_traj,
                                   adj_final, adj_ob_traj, adj_state0, adj_ob0, adj_actions, st);
+}
+
+int swarp_rollout_bwd_ob_check(const swarp_desc_t *desc)
+{
+    g_err[0] = 0;
+    if (check_desc(desc)) return -1;
+    if (desc->has_boxes || desc->wheel_contacts)
+        return fail("box agents and wheel contacts with movable bodies are not supported in "
+                    "this build");
+    return desc->dtype == SWARP_F32 ? bwd_ob_fits<float>(desc) : bwd_ob_fits<double>(desc);
 }
 
 const char *swarp_last_error(void) { return g_err; }

@@ -256,12 +256,24 @@ def test_bodies_few_agents_many_obstacles():
 
 def test_bodies_obstacle_count_beyond_lds_is_rejected():
     """An obstacle count whose backward staging exceeds 64 KiB of LDS even at one env per
-    wave (float64, 100 obstacles) is refused by the host before the backward launches."""
+    wave (float64, 100 obstacles) is refused by the host -- when a gradient is required,
+    before the forward runs, so the stepper's obstacle state is not advanced; a no-grad
+    rollout of the same world still runs."""
     E, A = 3, 4
     s0, acts = _pushers(E, A, 4)
     obs = cross_obs(E, (0.0, 0.0), extra=_ring_extra(95))
     with pytest.raises(RuntimeError, match="LDS"):
         run_pair(nav_agents(A), _world(), 0.05, 4, s0, acts, obs, np.float64)
+    st = make_stepper(nav_agents(A), _world(), 0.05, 4, torch.float64, obs=obs, n_envs=E)
+    before = st.ob_state.detach().clone()
+    s0t = to_torch_state(s0, torch.float64, True, 5)
+    a = torch.tensor(acts, dtype=torch.float64, device="cuda", requires_grad=True)
+    with pytest.raises(RuntimeError, match="LDS"):
+        rollout(st, s0t, a)
+    assert torch.equal(st.ob_state.detach(), before) and st.ob_trajectory is None
+    with torch.no_grad():
+        rollout(st, s0t, a)
+    assert st.ob_trajectory is not None and st.ob_trajectory.shape[0] == acts.shape[0]
 
 def test_bodies_clamp_bounds():
     E, A = 8, 8

@@ -77,6 +77,49 @@ def test_rejects_sizes_beyond_the_limit():
     assert b"allocation-free limit" in lib.swarp_last_error()
 
 
+_FIRST_CALL_IN_CAPTURE = r"""
+import sys
+sys.path.insert(0, sys.argv[1])
+import numpy as np, torch
+from swarp_amd import NeighborGrid, _lib
+E, A, K = 300, 64, 16
+g = NeighborGrid(E, A, radius=0.3, max_neighbors=K, device="cuda:0", dtype=torch.float32)
+rng = np.random.default_rng(21)
+g.build(torch.tensor(rng.uniform(-3, 3, size=(E, A, 2)), dtype=torch.float32, device="cuda"))
+ref = g.edge_index()
+cap = E * A * K
+out = torch.full((2, cap), -7, dtype=torch.int64, device="cuda")
+n = torch.zeros(1, dtype=torch.int64, device="cuda")
+lib = _lib.load()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):  # the process's first call of the entry point
+    _lib.check(lib.swarp_edge_index_noalloc(E, A, K, g.neighbor_idx.data_ptr(),
+                                            g.neighbor_count.data_ptr(), cap, out.data_ptr(),
+                                            n.data_ptr(), _lib.stream_of(out.device)))
+for _ in range(2):
+    out.fill_(-7)
+    graph.replay()
+    torch.cuda.synchronize()
+    m = ref.shape[1]
+    assert int(n.item()) == m and torch.equal(out[:, :m], ref)
+print("ok", m)
+"""
+
+
+def test_first_call_inside_graph_capture():
+    """The scratch array's address is looked up on the first call on a device; a first
+    call made while torch captures a graph (global capture mode) must work too.  Run in a
+    fresh process, so that this call is the process's first."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = str(Path(__file__).resolve().parents[1])
+    r = subprocess.run([sys.executable, "-c", _FIRST_CALL_IN_CAPTURE, root],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and r.stdout.startswith("ok"), r.stdout + r.stderr
+
+
 def test_replays_from_a_captured_graph():
     E, A, K = 1000, 64, 16
     g = _lists(E, A, 0.3, K, 3.0, seed=5)
