@@ -299,7 +299,10 @@ def _c5(seed=0):
                        c(torch.zeros(E, A, 2)), c(z), c(z))
     acts = c(torch.rand(T, E, A, 2, generator=g) * 2 - 1)
     goals = c((torch.rand(E, 2, generator=g) * 2 - 1) * 2.0)
-    fwd = 4 * A * (2 * 7 + 2) + 48 + 4 * A * (16 + 2)
+    # the body forward moves states, actions and the body (48 B); each step's lists
+    # (4 A (K + 2) B) and COO edges (16 B each) are written by k_neighbors / k_edge_index,
+    # separate launches whose bytes are not the forward's
+    fwd = 4 * A * (2 * 7 + 2) + 48
     bwd = 4 * A * (3 * 7 + 2 * 2) + 72
     desc = ("movable cross body, 16000 envs x 64 agents, r_nbr 0.3 / K 16 lists + overflow "
             "+ COO every step, 4 substeps, 16-step BPTT (BASELINE configs[4])")
