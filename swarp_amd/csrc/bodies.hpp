@@ -20,6 +20,10 @@
 // are formed in agent order by one loop over the contributing lanes of the env, which
 // keeps them in the reference's summation order; a contribution that is exactly zero is
 // skipped, which does not change a sum that starts at +0.
+//
+// Both kernels run one wave per workgroup: lanes exchange values through LDS behind
+// wave_lds_sync (a wavefront-scope fence), not a workgroup barrier, whose fence would
+// also wait for every outstanding global load and store.
 #pragma once
 #include "common.hpp"
 
@@ -715,7 +719,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
     const size_t eo = (size_t)(env_ok ? L.env : 0) * NW;
     for (int q = L.agent; q < NW; q += PA) obs(0)[q] = io.ob0[eo + q];
     for (int o = L.lane; o < tb.N; o += 64) lext[o] = body_ext(tb, o);
-    __syncthreads();
+    wave_lds_sync();
     body_trig<T, PA>(tb, L, obs(0), ocs(0));
     St<T> st;
     load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
@@ -733,12 +737,12 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
         T D = T(0);
         bool ok = false;
         for (int s = 0; s < C.S; ++s) {
-            __syncthreads();
+            wave_lds_sync();
             sl[F_PX * 64 + L.lane] = st.px;
             sl[F_PY * 64 + L.lane] = st.py;
             sl[F_VX * 64 + L.lane] = st.vx;
             sl[F_VY * 64 + L.lane] = st.vy;
-            __syncthreads();
+            wave_lds_sync();
             const T *obc = obs(cur);
             T Fx, Fy;
             forces_b<T, PA>(C, tb, L, sl, lr, obc, st, s, s == 0 || !ok, cand, Fx, Fy);
@@ -754,7 +758,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
             cur ^= 1;
         }
         asm volatile("" ::"v"(an[0]), "v"(an[1]), "v"(an[2]), "v"(an[3]));
-        __syncthreads();
+        wave_lds_sync();
         if (L.active) {
             if (t + 1 < g.nsteps)
                 store_state<T, DRONE>(g.traj.f, (size_t)t * EA + L.idx, st);
@@ -819,7 +823,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
         const int s = q / 6;
         gin[q] = (q < 6 * N && shape_moves(tb, s)) ? T(0) : gout[q];
     }
-    __syncthreads();
+    wave_lds_sync();
     for (int o = 0; o < N; ++o) {
         if (tb.body[o] != o || tb.kind[o] != 1) continue;
         BodyNew<T> B;
@@ -1036,7 +1040,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
             gi[4] = g_tvy;
             gi[5] = g_om;
         }
-        __syncthreads();
+        wave_lds_sync();
     }
 }
 
@@ -1082,7 +1086,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             add_adj<T, DRONE>(g.afin.f, L.idx, gs);
         else
             add_adj<T, DRONE>(g.atraj.f, (size_t)t * EA + L.idx, gs);
-        __syncthreads();
+        wave_lds_sync();
         if (io.atraj && env_ok)
             for (int q = L.agent; q < NW; q += PA) gob[q] += io.atraj[(size_t)t * ENW + eo + q];
         St<T> st;
@@ -1095,7 +1099,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             const T *src = t == 0 ? io.ob0 + eo : io.traj + (size_t)(t - 1) * ENW + eo;
             T *dst = lobs + (size_t)ew * NW;
             for (int q = L.agent; q < NW; q += PA) dst[q] = src[q];
-            __syncthreads();
+            wave_lds_sync();
             if (lcs) body_trig<T, PA>(tb, L, dst, lcs + (size_t)ew * 2 * N);
         }
         T a[4];
@@ -1107,9 +1111,9 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
         bool ok = false;
         for (int s = 0; s < C.S; ++s) {
             T *sl = slots + (size_t)s * NF * 64;
-            __syncthreads();
+            wave_lds_sync();
             slot_put<T, DRONE>(sl, L.lane, st);
-            __syncthreads();
+            wave_lds_sync();
             const T *obc = lobs + ((size_t)s * EPW + ew) * NW;
             T Fx, Fy;
             const M incl = forces_b<T, PA>(C, tb, L, sl, lr, obc, st, s, s == 0 || !ok, cand, Fx, Fy);
@@ -1120,13 +1124,16 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
                              lcs ? lcs + ((size_t)s * EPW + ew) * 2 * N : nullptr,
                              lcs ? lcs + ((size_t)(s + 1) * EPW + ew) * 2 * N : nullptr,
                              lsum ? lsum + ((size_t)s * EPW + ew) * 3 * N : nullptr);
-            St<T> nx;
-            integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
-            if (C.use_skin) {
-                D += (m_abs(nx.px - st.px) + m_abs(nx.py - st.py)) * T(1.0001);
-                ok = env_all<PA>(!L.active || D <= C.half_margin, L.base);
+            // the last substep's agent output is the step's checkpoint: not needed here
+            if (s + 1 < C.S) {
+                St<T> nx;
+                integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
+                if (C.use_skin) {
+                    D += (m_abs(nx.px - st.px) + m_abs(nx.py - st.py)) * T(1.0001);
+                    ok = env_all<PA>(!L.active || D <= C.half_margin, L.base);
+                }
+                st = nx;
             }
-            st = nx;
         }
 
         // ---- reverse pass
@@ -1134,7 +1141,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
         for (int s = C.S - 1; s >= 0; --s) {
             T *sl = slots + (size_t)s * NF * 64;
             const T *obc = lobs + ((size_t)s * EPW + ew) * NW;
-            __syncthreads();
+            wave_lds_sync();
             St<T> in;
             slot_get<T, DRONE>(sl, L.lane, in);
             const T Fx = sl[F_FX * 64 + L.lane], Fy = sl[F_FY * 64 + L.lane];
@@ -1148,10 +1155,10 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
                                  lsum ? lsum + ((size_t)s * EPW + ew) * 3 * N : nullptr);
             if (C.needs_forces) {
                 const T wFx = gFx * L.inv_dd, wFy = gFy * L.inv_dd;
-                __syncthreads();
+                wave_lds_sync();
                 sl[F_FX * 64 + L.lane] = wFx;
                 sl[F_FY * 64 + L.lane] = wFy;
-                __syncthreads();
+                wave_lds_sync();
                 if (C.collisions) {
                     const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64;
                     const T *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
@@ -1202,7 +1209,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
                     wall_force_adj(C, in.px, in.py, in.vx, in.vy, L.pr.radius, L.dd, gFx, gFy, gi);
             }
             gs = gi;
-            __syncthreads();
+            wave_lds_sync();
             T *tmp = gob;
             gob = gprev;
             gprev = tmp;
@@ -1213,7 +1220,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
         }
     }
     if (L.active) store_adj<T, DRONE>(g.a0.f, L.idx, gs);
-    __syncthreads();
+    wave_lds_sync();
     if (io.a0 && env_ok)
         for (int q = L.agent; q < NW; q += PA) io.a0[eo + q] = gob[q];
 }

@@ -1,6 +1,12 @@
 // generic.hpp -- the generic rollout kernels (every fleet the specialised holonomic kernels
 // do not cover: diff-drive, bicycle, drones, obstacles, clamps, box agents, RK4) and their
 // launchers.  Instantiated per (dtype, DRONE, BOXES) by the k_generic*.hip units.
+//
+// k_rollout_fwd and k_rollout_bwd run one wave per workgroup, so their lanes exchange
+// values through LDS behind wave_lds_sync (a wavefront-scope fence) instead of a
+// workgroup barrier, whose fence would also wait for every outstanding global load and
+// store.
+// k_rollout_fwd_split runs two waves per workgroup and synchronises them with barriers.
 #pragma once
 #include "common.hpp"
 
@@ -47,7 +53,7 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> Cin, const Args
             T Fx = T(0), Fy = T(0), Tq = T(0);
             if (C.needs_forces) {
                 if (C.collisions) {
-                    __syncthreads();
+                    wave_lds_sync();
                     sl[F_PX * 64 + L.lane] = st.px;
                     sl[F_PY * 64 + L.lane] = st.py;
                     sl[F_VX * 64 + L.lane] = st.vx;
@@ -58,11 +64,11 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> Cin, const Args
                     }
                 }
                 if (BOXES) {
-                    if (!C.collisions) __syncthreads();
+                    if (!C.collisions) wave_lds_sync();
                     lcs[L.lane] = m_cos(st.th);
                     lcs[64 + L.lane] = m_sin(st.th);
                 }
-                if (C.collisions || BOXES) __syncthreads();
+                if (C.collisions || BOXES) wave_lds_sync();
                 forces<T, PA, BOXES>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy, ocs, lbx,
                                      lcs, nullptr, nullptr, nullptr, nullptr,
                                      BOXES && C.wheel ? &Tq : nullptr);
@@ -260,7 +266,7 @@ __device__ __forceinline__ void box_rounds(const Cst<T> &C, const Args<T> &g,
     iwf[lane] = (unsigned char)wf;
     gfr[lane] = gFx;
     gfr[64 + lane] = gFy;
-    __syncthreads();
+    wave_lds_sync();
     for (int r = 0; r < total; r += 64) {
         const int q = r + lane;
         if (q < total) {
@@ -320,7 +326,7 @@ __device__ __forceinline__ void box_rounds(const Cst<T> &C, const Args<T> &g,
             res[256 + lane] = acc.vy;
             res[320 + lane] = acc.w;
         }
-        __syncthreads();
+        wave_lds_sync();
         const int q0 = start > r ? start : r, q1 = min(start + n, r + 64);
         for (int c = q0 - r; c < q1 - r; ++c) {
             gi.px += res[c];
@@ -330,7 +336,7 @@ __device__ __forceinline__ void box_rounds(const Cst<T> &C, const Args<T> &g,
             gi.vy += res[256 + c];
             gi.w += res[320 + c];
         }
-        __syncthreads();
+        wave_lds_sync();
     }
 }
 
@@ -386,13 +392,13 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> Cin, const Args
         bool ok = false;
         for (int s = 0; s < C.S; ++s) {
             T *sl = slots + (size_t)s * NF * 64;
-            __syncthreads();
+            wave_lds_sync();
             slot_put<T, DRONE>(sl, L.lane, st);
             if (BOXES) {
                 lcsb[s * 128 + L.lane] = m_cos(st.th);
                 lcsb[s * 128 + 64 + L.lane] = m_sin(st.th);
             }
-            __syncthreads();
+            wave_lds_sync();
             T Fx = T(0), Fy = T(0);
             M incl = 0;
             if (C.needs_forces) {
@@ -410,20 +416,24 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> Cin, const Args
             sl[F_FX * 64 + L.lane] = Fx;
             sl[F_FY * 64 + L.lane] = Fy;
             lmask[s * 64 + L.lane] = incl;
-            St<T> nx;
-            integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
-            if (C.use_skin) {
-                D += (m_abs(nx.px - st.px) + m_abs(nx.py - st.py)) * T(1.0001);
-                ok = env_all<PA>(!L.real || D <= C.half_margin, L.base);
+            // the reverse pass reads each substep's input and force; the last substep's
+            // output is the step's checkpoint and is not needed here
+            if (s + 1 < C.S) {
+                St<T> nx;
+                integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
+                if (C.use_skin) {
+                    D += (m_abs(nx.px - st.px) + m_abs(nx.py - st.py)) * T(1.0001);
+                    ok = env_all<PA>(!L.real || D <= C.half_margin, L.base);
+                }
+                st = nx;
             }
-            st = nx;
         }
 
         // ---- reverse pass
         T ga[4] = {T(0), T(0), T(0), T(0)};
         for (int s = C.S - 1; s >= 0; --s) {
             T *sl = slots + (size_t)s * NF * 64;
-            __syncthreads();
+            wave_lds_sync();
             St<T> in;
             slot_get<T, DRONE>(sl, L.lane, in);
             const T Fx = sl[F_FX * 64 + L.lane], Fy = sl[F_FY * 64 + L.lane];
@@ -433,10 +443,10 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> Cin, const Args
             if (C.needs_forces) {
                 // the slot now carries the force adjoint divided by the damping denominator
                 const T wFx = gFx * L.inv_dd, wFy = gFy * L.inv_dd;
-                __syncthreads();
+                wave_lds_sync();
                 sl[F_FX * 64 + L.lane] = wFx;
                 sl[F_FY * 64 + L.lane] = wFy;
-                __syncthreads();
+                wave_lds_sync();
                 M imask = 0;  // force-exerting box pairs, reversed in box_rounds
                 if (C.collisions) {
                     const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64;

@@ -192,6 +192,35 @@ __device__ __forceinline__ float div_rn(float n, const Dv<float> &v)
     return q;
 }
 
+// Division policies of the drone branches, which divide by the same few values many
+// times (mass, the inertias, the quaternion norm): ArithIEEE divides and takes square
+// roots with the correctly rounded IEEE operations (any T); ArithPrep computes the same
+// float results through prepared divisors (rcp_d once per divisor, then three short
+// operations per quotient) and sqrt_rn_big, without branches -- a numerator or radicand
+// outside the range where those are exact only raises `bad`, after which the caller
+// recomputes with ArithIEEE (zero numerators are exact for every divisor).
+template <typename T> struct ArithIEEE {
+    typedef T D;
+    __device__ __forceinline__ D prep(T d) const { return d; }
+    __device__ __forceinline__ T div(T n, const D &d) const { return n / d; }
+    __device__ __forceinline__ T sqrt(T x) const { return m_sqrt(x); }
+};
+struct ArithPrep {
+    bool bad = false;
+    typedef Dv<float> D;
+    __device__ __forceinline__ D prep(float d) const { return divisor(d, true); }
+    __device__ __forceinline__ float div(float n, const D &d)
+    {
+        bad |= !(fabsf(n) >= d.lo) && n != 0.0f;
+        return (float)((double)n * d.y);
+    }
+    __device__ __forceinline__ float sqrt(float x)
+    {
+        bad |= !(x >= 0x1p-96f && x < __builtin_inff());
+        return sqrt_rn_big(x);
+    }
+};
+
 // ------------------------------------------------------------- contact law
 
 // _normal_coeff (swarp/core/collisions.py:87-105).  SAT = false compiles the tanh
@@ -1344,6 +1373,55 @@ __device__ __forceinline__ void integrate_rk4_adj(const Cst<T> &C, const Prm<T> 
     }
 }
 
+// The drone branch of the Euler substep (_integrate_agent TAG_DRONE,
+// swarp/dynamics/kernels.py:349-369): "+" quadrotor, rotor clamp, body rates, vz, planar
+// velocity (+ contact dv), attitude q = normalize(q + qdot(br_new) dt), position, z.
+// Writes the fields it steps into o (and the new planar position into pnx / pny).
+template <typename T, typename Ar>
+__device__ __forceinline__ void drone_euler(const Prm<T> &P, const St<T> &in, const T (&a)[4],
+                                            T dt, T dvx, T dvy, Ar &&A, St<T> &o, T &pnx,
+                                            T &pny)
+{
+    const T z0 = T(0);
+    T f0 = wclamp(a[0], z0, P.thrust_max), f1 = wclamp(a[1], z0, P.thrust_max);
+    T f2 = wclamp(a[2], z0, P.thrust_max), f3 = wclamp(a[3], z0, P.thrust_max);
+    T thr = f0 + f1 + f2 + f3;
+    const auto dm = A.prep(P.mass), dix = A.prep(P.ixx), diy = A.prep(P.iyy), diz = A.prep(P.izz);
+    // _quat_rotate_vec(q, (0,0,thrust)) written generically (kernels.py:108-114)
+    T vx3 = T(0), vy3 = T(0), vz3 = thr;
+    T c1x = in.qy * vz3 - in.qz * vy3, c1y = in.qz * vx3 - in.qx * vz3;
+    T c1z = in.qx * vy3 - in.qy * vx3;
+    T tx = T(2) * c1x, ty = T(2) * c1y, tz = T(2) * c1z;
+    T c2x = in.qy * tz - in.qz * ty, c2y = in.qz * tx - in.qx * tz, c2z = in.qx * ty - in.qy * tx;
+    T fwx = vx3 + in.qw * tx + c2x, fwy = vy3 + in.qw * ty + c2y, fwz = vz3 + in.qw * tz + c2z;
+    T accx = A.div(fwx, dm) - z0, accy = A.div(fwy, dm) - z0, accz = A.div(fwz, dm) - P.gravity;
+    T tqx = P.arm * (f1 - f3), tqy = P.arm * (f2 - f0), tqz = P.kappa * (f0 - f1 + f2 - f3);
+    T nbx = in.bx + A.div(tqx - (P.izz - P.iyy) * in.by * in.bz, dix) * dt;
+    T nby = in.by + A.div(tqy - (P.ixx - P.izz) * in.bz * in.bx, diy) * dt;
+    T nbz = in.bz + A.div(tqz - (P.iyy - P.ixx) * in.bx * in.by, diz) * dt;
+    T nvz = in.vz + accz * dt;
+    T vxx = in.vx + accx * dt + dvx, vxy = in.vy + accy * dt + dvy;
+    const T h = T(0.5);
+    T dqx = h * (in.qw * nbx + in.qy * nbz - in.qz * nby);
+    T dqy = h * (in.qw * nby - in.qx * nbz + in.qz * nbx);
+    T dqz = h * (in.qw * nbz + in.qx * nby - in.qy * nbx);
+    T dqw = h * (-in.qx * nbx - in.qy * nby - in.qz * nbz);
+    T ux = in.qx + dqx * dt, uy = in.qy + dqy * dt, uz = in.qz + dqz * dt, uw = in.qw + dqw * dt;
+    T l = A.sqrt(ux * ux + uy * uy + uz * uz + uw * uw);
+    if (l > T(0)) {
+        const auto dl = A.prep(l);
+        o.qx = A.div(ux, dl); o.qy = A.div(uy, dl); o.qz = A.div(uz, dl); o.qw = A.div(uw, dl);
+    } else {
+        o.qx = T(0); o.qy = T(0); o.qz = T(0); o.qw = T(1);
+    }
+    pnx = in.px + vxx * dt;
+    pny = in.py + vxy * dt;
+    o.z = in.z + nvz * dt;
+    o.vz = nvz;
+    o.bx = nbx; o.by = nby; o.bz = nbz;
+    o.vx = vxx; o.vy = vxy;
+}
+
 // Semi-implicit Euler substep of one agent: _integrate_agent + _step_2d
 // (swarp/dynamics/kernels.py:194-413).  `o` receives the new state.
 template <typename T, bool DRONE>
@@ -1360,42 +1438,13 @@ __device__ __forceinline__ void integrate_core(const Cst<T> &C, const Prm<T> &P,
     o = in;
     T pnx = in.px, pny = in.py;
     if (DRONE && P.tag == 3) {
-        const T z0 = T(0);
-        T f0 = wclamp(a[0], z0, P.thrust_max), f1 = wclamp(a[1], z0, P.thrust_max);
-        T f2 = wclamp(a[2], z0, P.thrust_max), f3 = wclamp(a[3], z0, P.thrust_max);
-        T thr = f0 + f1 + f2 + f3;
-        // _quat_rotate_vec(q, (0,0,thrust)) written generically (kernels.py:108-114)
-        T vx3 = T(0), vy3 = T(0), vz3 = thr;
-        T c1x = in.qy * vz3 - in.qz * vy3, c1y = in.qz * vx3 - in.qx * vz3;
-        T c1z = in.qx * vy3 - in.qy * vx3;
-        T tx = T(2) * c1x, ty = T(2) * c1y, tz = T(2) * c1z;
-        T c2x = in.qy * tz - in.qz * ty, c2y = in.qz * tx - in.qx * tz, c2z = in.qx * ty - in.qy * tx;
-        T fwx = vx3 + in.qw * tx + c2x, fwy = vy3 + in.qw * ty + c2y, fwz = vz3 + in.qw * tz + c2z;
-        T accx = fwx / P.mass - z0, accy = fwy / P.mass - z0, accz = fwz / P.mass - P.gravity;
-        T tqx = P.arm * (f1 - f3), tqy = P.arm * (f2 - f0), tqz = P.kappa * (f0 - f1 + f2 - f3);
-        T nbx = in.bx + (tqx - (P.izz - P.iyy) * in.by * in.bz) / P.ixx * dt;
-        T nby = in.by + (tqy - (P.ixx - P.izz) * in.bz * in.bx) / P.iyy * dt;
-        T nbz = in.bz + (tqz - (P.iyy - P.ixx) * in.bx * in.by) / P.izz * dt;
-        T nvz = in.vz + accz * dt;
-        T vxx = in.vx + accx * dt + dvx, vxy = in.vy + accy * dt + dvy;
-        const T h = T(0.5);
-        T dqx = h * (in.qw * nbx + in.qy * nbz - in.qz * nby);
-        T dqy = h * (in.qw * nby - in.qx * nbz + in.qz * nbx);
-        T dqz = h * (in.qw * nbz + in.qx * nby - in.qy * nbx);
-        T dqw = h * (-in.qx * nbx - in.qy * nby - in.qz * nbz);
-        T ux = in.qx + dqx * dt, uy = in.qy + dqy * dt, uz = in.qz + dqz * dt, uw = in.qw + dqw * dt;
-        T l = m_sqrt(ux * ux + uy * uy + uz * uz + uw * uw);
-        if (l > T(0)) {
-            o.qx = ux / l; o.qy = uy / l; o.qz = uz / l; o.qw = uw / l;
+        if constexpr (sizeof(T) == 4) {
+            ArithPrep A;
+            drone_euler(P, in, a, dt, dvx, dvy, A, o, pnx, pny);
+            if (__builtin_expect(A.bad, 0)) drone_euler(P, in, a, dt, dvx, dvy, ArithIEEE<T>(), o, pnx, pny);
         } else {
-            o.qx = T(0); o.qy = T(0); o.qz = T(0); o.qw = T(1);
+            drone_euler(P, in, a, dt, dvx, dvy, ArithIEEE<T>(), o, pnx, pny);
         }
-        pnx = in.px + vxx * dt;
-        pny = in.py + vxy * dt;
-        o.z = in.z + nvz * dt;
-        o.vz = nvz;
-        o.bx = nbx; o.by = nby; o.bz = nbz;
-        o.vx = vxx; o.vy = vxy;
     } else if (P.tag == 0) {
         T vnx, vny;
         if (P.mode == 0) {
@@ -1482,6 +1531,97 @@ __device__ __forceinline__ void integrate(const Cst<T> &C, const Prm<T> &P, cons
     integrate_core<T, DRONE>(C, Pv, in, as, Fx, Fy, o);
 }
 
+// Reverse of drone_euler (gi = g on entry: the fields the drone does not step pass
+// through).  g = adjoint of the substep output; writes the adjoints of the fields it
+// steps into gi, the force adjoint into gFx / gFy and each rotor's action adjoint into
+// gact (to be added to the action adjoint).
+template <typename T, typename Ar>
+__device__ __forceinline__ void drone_euler_adj(const Prm<T> &P, const St<T> &in, const T (&a)[4],
+                                                T dt, T dtm, const St<T> &g, Ar &&A, St<T> &gi,
+                                                T &gFx, T &gFy, T (&gact)[4])
+{
+    const T gpx = g.px, gpy = g.py;
+    const T z0 = T(0);
+    T f0 = wclamp(a[0], z0, P.thrust_max), f1 = wclamp(a[1], z0, P.thrust_max);
+    T f2 = wclamp(a[2], z0, P.thrust_max), f3 = wclamp(a[3], z0, P.thrust_max);
+    T thr = f0 + f1 + f2 + f3;
+    const auto dm = A.prep(P.mass), dix = A.prep(P.ixx), diy = A.prep(P.iyy), diz = A.prep(P.izz);
+    T vx3 = T(0), vy3 = T(0), vz3 = thr;
+    T qx = in.qx, qy = in.qy, qz = in.qz, qw = in.qw;
+    T c1x = qy * vz3 - qz * vy3, c1y = qz * vx3 - qx * vz3, c1z = qx * vy3 - qy * vx3;
+    T tx = T(2) * c1x, ty = T(2) * c1y, tz = T(2) * c1z;
+    T nbx = in.bx + A.div(P.arm * (f1 - f3) - (P.izz - P.iyy) * in.by * in.bz, dix) * dt;
+    T nby = in.by + A.div(P.arm * (f2 - f0) - (P.ixx - P.izz) * in.bz * in.bx, diy) * dt;
+    T nbz = in.bz + A.div(P.kappa * (f0 - f1 + f2 - f3) - (P.iyy - P.ixx) * in.bx * in.by, diz) * dt;
+    const T h = T(0.5);
+    T ux = qx + h * (qw * nbx + qy * nbz - qz * nby) * dt;
+    T uy = qy + h * (qw * nby - qx * nbz + qz * nbx) * dt;
+    T uz = qz + h * (qw * nbz + qx * nby - qy * nbx) * dt;
+    T uw = qw + h * (-qx * nbx - qy * nby - qz * nbz) * dt;
+    T l = A.sqrt(ux * ux + uy * uy + uz * uz + uw * uw);
+    gi.px = gpx;
+    gi.py = gpy;
+    T gvx = g.vx + gpx * dt, gvy = g.vy + gpy * dt;
+    gi.z = g.z;
+    T gnvz = g.vz + g.z * dt;
+    T gux = T(0), guy = T(0), guz = T(0), guw = T(0);
+    if (l > T(0)) {
+        const auto dl = A.prep(l);
+        T nx = A.div(ux, dl), ny = A.div(uy, dl), nz = A.div(uz, dl), nw = A.div(uw, dl);
+        T dq = g.qx * nx + g.qy * ny + g.qz * nz + g.qw * nw;
+        gux = A.div(g.qx - nx * dq, dl);
+        guy = A.div(g.qy - ny * dq, dl);
+        guz = A.div(g.qz - nz * dq, dl);
+        guw = A.div(g.qw - nw * dq, dl);
+    }
+    T gqx = gux, gqy = guy, gqz = guz, gqw = guw;
+    T Dx = h * gux * dt, Dy = h * guy * dt, Dz = h * guz * dt, Dw = h * guw * dt;
+    gqw += Dx * nbx + Dy * nby + Dz * nbz;
+    gqx += -Dy * nbz + Dz * nby - Dw * nbx;
+    gqy += Dx * nbz - Dz * nbx - Dw * nby;
+    gqz += -Dx * nby + Dy * nbx - Dw * nbz;
+    T gnbx = g.bx + Dx * qw + Dy * qz - Dz * qy - Dw * qx;
+    T gnby = g.by - Dx * qz + Dy * qw + Dz * qx - Dw * qy;
+    T gnbz = g.bz + Dx * qy - Dy * qx + Dz * qw - Dw * qz;
+    T gbx = gnbx, gby = gnby, gbz = gnbz;
+    T gtx = A.div(gnbx * dt, dix), gty = A.div(gnby * dt, diy), gtz = A.div(gnbz * dt, diz);
+    gby -= (P.izz - P.iyy) * in.bz * gtx;
+    gbz -= (P.izz - P.iyy) * in.by * gtx;
+    gbz -= (P.ixx - P.izz) * in.bx * gty;
+    gbx -= (P.ixx - P.izz) * in.bz * gty;
+    gbx -= (P.iyy - P.ixx) * in.by * gtz;
+    gby -= (P.iyy - P.ixx) * in.bx * gtz;
+    T gf0 = -P.arm * gty + P.kappa * gtz;
+    T gf1 = P.arm * gtx - P.kappa * gtz;
+    T gf2 = P.arm * gty + P.kappa * gtz;
+    T gf3 = -P.arm * gtx - P.kappa * gtz;
+    gi.vz = gnvz;
+    gi.vx = gvx;
+    gi.vy = gvy;
+    gFx = gvx * dtm;
+    gFy = gvy * dtm;
+    T gfx = A.div(gvx * dt, dm), gfy = A.div(gvy * dt, dm), gfz = A.div(gnvz * dt, dm);
+    gqw += gfx * tx + gfy * ty + gfz * tz;
+    T gtx2 = qw * gfx + (gfy * qz - gfz * qy);
+    T gty2 = qw * gfy + (gfz * qx - gfx * qz);
+    T gtz2 = qw * gfz + (gfx * qy - gfy * qx);
+    gqx += ty * gfz - tz * gfy;
+    gqy += tz * gfx - tx * gfz;
+    gqz += tx * gfy - ty * gfx;
+    T g1x = T(2) * gtx2, g1y = T(2) * gty2, g1z = T(2) * gtz2;
+    gqx += vy3 * g1z - vz3 * g1y;
+    gqy += vz3 * g1x - vx3 * g1z;
+    gqz += vx3 * g1y - vy3 * g1x;
+    T gthr = gfz + (g1x * qy - g1y * qx);
+    gf0 += gthr; gf1 += gthr; gf2 += gthr; gf3 += gthr;
+    gact[0] = wclamp_g(a[0], z0, P.thrust_max, gf0);
+    gact[1] = wclamp_g(a[1], z0, P.thrust_max, gf1);
+    gact[2] = wclamp_g(a[2], z0, P.thrust_max, gf2);
+    gact[3] = wclamp_g(a[3], z0, P.thrust_max, gf3);
+    gi.qx = gqx; gi.qy = gqy; gi.qz = gqz; gi.qw = gqw;
+    gi.bx = gbx; gi.by = gby; gi.bz = gbz;
+}
+
 // Reverse of integrate without its position clamp (integrate_adj reverses that first).
 // g = adjoint of the substep output.  Overwrites gi with the adjoint of the substep
 // input, accumulates ga (actions) and returns gF (force).
@@ -1503,87 +1643,19 @@ __device__ __forceinline__ void integrate_adj_core(const Cst<T> &C, const Prm<T>
     gFx = T(0);
     gFy = T(0);
     if (DRONE && P.tag == 3) {
-        const T z0 = T(0);
-        T f0 = wclamp(a[0], z0, P.thrust_max), f1 = wclamp(a[1], z0, P.thrust_max);
-        T f2 = wclamp(a[2], z0, P.thrust_max), f3 = wclamp(a[3], z0, P.thrust_max);
-        T thr = f0 + f1 + f2 + f3;
-        T vx3 = T(0), vy3 = T(0), vz3 = thr;
-        T qx = in.qx, qy = in.qy, qz = in.qz, qw = in.qw;
-        T c1x = qy * vz3 - qz * vy3, c1y = qz * vx3 - qx * vz3, c1z = qx * vy3 - qy * vx3;
-        T tx = T(2) * c1x, ty = T(2) * c1y, tz = T(2) * c1z;
-        T accx = (vx3 + qw * tx + (qy * tz - qz * ty)) / P.mass;
-        T accy = (vy3 + qw * ty + (qz * tx - qx * tz)) / P.mass;
-        T accz = (vz3 + qw * tz + (qx * ty - qy * tx)) / P.mass - P.gravity;
-        T nbx = in.bx + (P.arm * (f1 - f3) - (P.izz - P.iyy) * in.by * in.bz) / P.ixx * dt;
-        T nby = in.by + (P.arm * (f2 - f0) - (P.ixx - P.izz) * in.bz * in.bx) / P.iyy * dt;
-        T nbz = in.bz + (P.kappa * (f0 - f1 + f2 - f3) - (P.iyy - P.ixx) * in.bx * in.by) / P.izz * dt;
-        const T h = T(0.5);
-        T ux = qx + h * (qw * nbx + qy * nbz - qz * nby) * dt;
-        T uy = qy + h * (qw * nby - qx * nbz + qz * nbx) * dt;
-        T uz = qz + h * (qw * nbz + qx * nby - qy * nbx) * dt;
-        T uw = qw + h * (-qx * nbx - qy * nby - qz * nbz) * dt;
-        T l = m_sqrt(ux * ux + uy * uy + uz * uz + uw * uw);
-        (void)accx; (void)accy; (void)accz;
-        gi.px = gpx;
-        gi.py = gpy;
-        T gvx = g.vx + gpx * dt, gvy = g.vy + gpy * dt;
-        gi.z = g.z;
-        T gnvz = g.vz + g.z * dt;
-        T gux = T(0), guy = T(0), guz = T(0), guw = T(0);
-        if (l > T(0)) {
-            T nx = ux / l, ny = uy / l, nz = uz / l, nw = uw / l;
-            T dq = g.qx * nx + g.qy * ny + g.qz * nz + g.qw * nw;
-            gux = (g.qx - nx * dq) / l;
-            guy = (g.qy - ny * dq) / l;
-            guz = (g.qz - nz * dq) / l;
-            guw = (g.qw - nw * dq) / l;
+        T gact[4];
+        if constexpr (sizeof(T) == 4) {
+            ArithPrep A;
+            drone_euler_adj(P, in, a, dt, dtm, g, A, gi, gFx, gFy, gact);
+            if (__builtin_expect(A.bad, 0))
+                drone_euler_adj(P, in, a, dt, dtm, g, ArithIEEE<T>(), gi, gFx, gFy, gact);
+        } else {
+            drone_euler_adj(P, in, a, dt, dtm, g, ArithIEEE<T>(), gi, gFx, gFy, gact);
         }
-        T gqx = gux, gqy = guy, gqz = guz, gqw = guw;
-        T Dx = h * gux * dt, Dy = h * guy * dt, Dz = h * guz * dt, Dw = h * guw * dt;
-        gqw += Dx * nbx + Dy * nby + Dz * nbz;
-        gqx += -Dy * nbz + Dz * nby - Dw * nbx;
-        gqy += Dx * nbz - Dz * nbx - Dw * nby;
-        gqz += -Dx * nby + Dy * nbx - Dw * nbz;
-        T gnbx = g.bx + Dx * qw + Dy * qz - Dz * qy - Dw * qx;
-        T gnby = g.by - Dx * qz + Dy * qw + Dz * qx - Dw * qy;
-        T gnbz = g.bz + Dx * qy - Dy * qx + Dz * qw - Dw * qz;
-        T gbx = gnbx, gby = gnby, gbz = gnbz;
-        T gtx = gnbx * dt / P.ixx, gty = gnby * dt / P.iyy, gtz = gnbz * dt / P.izz;
-        gby -= (P.izz - P.iyy) * in.bz * gtx;
-        gbz -= (P.izz - P.iyy) * in.by * gtx;
-        gbz -= (P.ixx - P.izz) * in.bx * gty;
-        gbx -= (P.ixx - P.izz) * in.bz * gty;
-        gbx -= (P.iyy - P.ixx) * in.by * gtz;
-        gby -= (P.iyy - P.ixx) * in.bx * gtz;
-        T gf0 = -P.arm * gty + P.kappa * gtz;
-        T gf1 = P.arm * gtx - P.kappa * gtz;
-        T gf2 = P.arm * gty + P.kappa * gtz;
-        T gf3 = -P.arm * gtx - P.kappa * gtz;
-        gi.vz = gnvz;
-        gi.vx = gvx;
-        gi.vy = gvy;
-        gFx = gvx * dtm;
-        gFy = gvy * dtm;
-        T gfx = gvx * dt / P.mass, gfy = gvy * dt / P.mass, gfz = gnvz * dt / P.mass;
-        gqw += gfx * tx + gfy * ty + gfz * tz;
-        T gtx2 = qw * gfx + (gfy * qz - gfz * qy);
-        T gty2 = qw * gfy + (gfz * qx - gfx * qz);
-        T gtz2 = qw * gfz + (gfx * qy - gfy * qx);
-        gqx += ty * gfz - tz * gfy;
-        gqy += tz * gfx - tx * gfz;
-        gqz += tx * gfy - ty * gfx;
-        T g1x = T(2) * gtx2, g1y = T(2) * gty2, g1z = T(2) * gtz2;
-        gqx += vy3 * g1z - vz3 * g1y;
-        gqy += vz3 * g1x - vx3 * g1z;
-        gqz += vx3 * g1y - vy3 * g1x;
-        T gthr = gfz + (g1x * qy - g1y * qx);
-        gf0 += gthr; gf1 += gthr; gf2 += gthr; gf3 += gthr;
-        ga[0] += wclamp_g(a[0], z0, P.thrust_max, gf0);
-        ga[1] += wclamp_g(a[1], z0, P.thrust_max, gf1);
-        ga[2] += wclamp_g(a[2], z0, P.thrust_max, gf2);
-        ga[3] += wclamp_g(a[3], z0, P.thrust_max, gf3);
-        gi.qx = gqx; gi.qy = gqy; gi.qz = gqz; gi.qw = gqw;
-        gi.bx = gbx; gi.by = gby; gi.bz = gbz;
+        ga[0] += gact[0];
+        ga[1] += gact[1];
+        ga[2] += gact[2];
+        ga[3] += gact[3];
         return;
     }
     if (P.tag == 0) {
