@@ -68,8 +68,9 @@ __device__ __forceinline__ int fstride(int k)
     return k == 0 || k == 2 ? 2 : (k == 7 ? 4 : (k == 8 ? 3 : 1));
 }
 
-template <typename T, bool DRONE>
-__device__ __forceinline__ void load_state(const T *const *f, size_t i, size_t off, St<T> &s)
+// The field-pointer arrays below may hold generic pointers or global ones (see vgpr_ptr).
+template <typename T, bool DRONE, typename P>
+__device__ __forceinline__ void load_state(const P *f, size_t i, size_t off, St<T> &s)
 {
     // `off` = element offset of the state in the trajectory (step * E * A)
     const size_t j = i + off;
@@ -104,8 +105,8 @@ __device__ __forceinline__ void store_state(T *const *f, size_t j, const St<T> &
 }
 
 // Adds a nullable adjoint state (fields may be NULL) at element j.
-template <typename T, bool DRONE>
-__device__ __forceinline__ void add_adj(const T *const *f, size_t j, St<T> &g)
+template <typename T, bool DRONE, typename P>
+__device__ __forceinline__ void add_adj(const P *f, size_t j, St<T> &g)
 {
     if (f[0]) { g.px += f[0][2 * j]; g.py += f[0][2 * j + 1]; }
     if (f[1]) g.th += f[1][j];
@@ -303,6 +304,22 @@ __device__ __forceinline__ void lane_init(const Cst<T> &C, const Args<T> &g, Lan
     L.dd = T(1) + C.c * C.sub_dt / L.pr.mass;
     L.inv_dd = T(1) / L.dd;
     L.ddv = divisor(L.dd, true);
+}
+
+// A wave-uniform global-memory pointer held in vector registers: the value is unchanged,
+// but the compiler no longer treats it as uniform, so it does not occupy scalar registers.
+// Used for the many state-field pointers a step loop reads: kept in scalar registers they
+// overflow the scalar file and are spilled, and every use then re-reads them lane by lane.
+// The result is typed as a global (address space 1) pointer: laundered through integers
+// a generic pointer would be read with flat loads, which also count as LDS operations, so
+// every wait for an LDS result would wait for them too.
+#define SWARP_GLOBAL __attribute__((address_space(1)))
+template <typename T> __device__ __forceinline__ const SWARP_GLOBAL T *vgpr_ptr(const T *p)
+{
+    const uint64_t u = (uint64_t)p;
+    uint32_t lo = (uint32_t)u, hi = (uint32_t)(u >> 32);
+    asm volatile("" : "+v"(lo), "+v"(hi));
+    return (const SWARP_GLOBAL T *)(((uint64_t)hi << 32) | lo);
 }
 
 // Orders one wave's LDS stores before its later LDS loads across lanes, for kernels whose

@@ -372,19 +372,27 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> Cin, const Args
     const size_t EA = (size_t)C.E * C.A;
     St<T> gs;  // adjoint of the current step's output
     st_zero(gs);
+    // the trajectory and trajectory-adjoint field pointers the step loop reads, in vector
+    // registers (see vgpr_ptr)
+    const SWARP_GLOBAL T *trf[9], *atf[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) {
+        trf[k] = vgpr_ptr(g.traj.f[k]);
+        atf[k] = vgpr_ptr(g.atraj.f[k]);
+    }
     for (int t = g.nsteps - 1; t >= 0; --t) {
         if (t == g.nsteps - 1)
             add_adj<T, DRONE>(g.afin.f, L.idx, gs);
         else
-            add_adj<T, DRONE>(g.atraj.f, (size_t)t * EA + L.idx, gs);
+            add_adj<T, DRONE>(atf, (size_t)t * EA + L.idx, gs);
         St<T> st;
         if (t == 0)
             load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
         else
-            load_state<T, DRONE>(g.traj.f, L.idx, (size_t)(t - 1) * EA, st);
-        if (!L.real) st.px = st.py = __builtin_nan("");
+            load_state<T, DRONE>(trf, L.idx, (size_t)(t - 1) * EA, st);
         T a[4];
         load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
+        if (!L.real) st.px = st.py = __builtin_nan("");
 
         // ---- recompute the substep chain of this step into LDS
         M cand = 0;
