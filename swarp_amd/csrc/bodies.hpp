@@ -93,6 +93,85 @@ template <typename T> __device__ __forceinline__ bool shape_moves(const ObTab<T>
     return tb.body[r] == r && tb.kind[r] == 1;
 }
 
+// The env's shapes as index sets, for the loops of the body pass.  Instances compiled
+// without FT_MANYSH (SM) hold at most 64 shapes: lane s of the wave keeps shape s's body
+// root, a set is a 64-bit mask -- body o's shapes one ballot, the movable roots and the
+// moving shapes masks formed once per launch -- and a loop visits the set bits in
+// ascending order, the index order of a loop over all shapes, with no table reads on
+// its way.  Otherwise the loops test the shapes one by one from the tables.
+template <typename T, bool SM> struct ShapeSets {
+    int32_t root = -1;    // SM: the body root of this lane's shape (-1: no shape)
+    uint64_t roots = 0;   // SM: movable body roots
+    uint64_t moving = 0;  // SM: shapes of movable bodies
+    uint64_t all = 0;     // SM: every shape
+
+    // with the whole wave active
+    __device__ __forceinline__ void init(const ObTab<T> &tb, int lane)
+    {
+        if constexpr (SM) {
+            const bool has = lane < tb.N;
+            root = has ? tb.body[lane] : -1;
+            roots = __ballot(has && root == lane && tb.kind[lane] == 1);
+            moving = __ballot(has && ((roots >> ((uint32_t)root & 63u)) & 1ull) != 0);
+            all = __ballot(has);
+        }
+    }
+    // the shapes of body root o; SM: with the whole wave active
+    __device__ __forceinline__ uint64_t of(int o) const
+    {
+        if constexpr (SM) return __ballot(root == o);
+        return 0;
+    }
+    __device__ __forceinline__ bool moves(const ObTab<T> &tb, int s) const
+    {
+        if constexpr (SM) return ((moving >> s) & 1ull) != 0;
+        return shape_moves(tb, s);
+    }
+    __device__ __forceinline__ bool is_root(const ObTab<T> &tb, int o) const
+    {
+        if constexpr (SM) return ((roots >> o) & 1ull) != 0;
+        return tb.body[o] == o && tb.kind[o] == 1;
+    }
+    // whether shape s belongs to body root o (bm = of(o))
+    __device__ __forceinline__ bool in_body(const ObTab<T> &tb, int o, uint64_t bm, int s) const
+    {
+        if constexpr (SM) return ((bm >> s) & 1ull) != 0;
+        return tb.body[s] == o;
+    }
+    // f(o) for every movable body root o, in index order
+    template <typename Fn> __device__ __forceinline__ void each_root(const ObTab<T> &tb, Fn &&f) const
+    {
+        if constexpr (SM) {
+            for (uint64_t m = roots; m; m &= m - 1) f(__builtin_ctzll(m));
+        } else {
+            for (int o = 0; o < tb.N; ++o)
+                if (tb.body[o] == o && tb.kind[o] == 1) f(o);
+        }
+    }
+    // f(s) for every shape of body root o (bm = of(o)), in index order
+    template <typename Fn>
+    __device__ __forceinline__ void each_of(const ObTab<T> &tb, int o, uint64_t bm, Fn &&f) const
+    {
+        if constexpr (SM) {
+            for (uint64_t m = bm; m; m &= m - 1) f(__builtin_ctzll(m));
+        } else {
+            for (int s = 0; s < tb.N; ++s)
+                if (tb.body[s] == o) f(s);
+        }
+    }
+    // f(s) for every shape not of body root o (bm = of(o)), in index order
+    template <typename Fn>
+    __device__ __forceinline__ void each_other(const ObTab<T> &tb, int o, uint64_t bm, Fn &&f) const
+    {
+        if constexpr (SM) {
+            for (uint64_t m = all & ~bm; m; m &= m - 1) f(__builtin_ctzll(m));
+        } else {
+            for (int s = 0; s < tb.N; ++s)
+                if (tb.body[s] != o) f(s);
+        }
+    }
+};
+
 // ------------------------------------------------ body-pass terms of any shape type
 //
 // Written once over the value type V: plain T in the forward pass, a one-tangent Dual in
@@ -491,18 +570,17 @@ __device__ __forceinline__ void body_load(const ObTab<T> &tb, const T *od, const
 // the lane in `st`; `od` = the env's obstacle state at the substep input.  Per shape of
 // the body (index order): the agents' reactions in agent order, then the contacts with
 // the shapes of other bodies and of the scenery in index order (swarp/core/bodies.py:
-// 423-501).
-template <typename T, int PA>
+// 423-501).  bm = SS.of(o).
+template <typename T, int PA, bool SM>
 __device__ __forceinline__ void body_sum(const Cst<T> &C, const ObTab<T> &tb,
-                                         const Lane<T, PA> &L, const BodyRow<T> &br,
-                                         const St<T> &st, const T *od, int o, BodyNew<T> &B)
+                                         const ShapeSets<T, SM> &SS, const Lane<T, PA> &L,
+                                         const BodyRow<T> &br, const St<T> &st, const T *od,
+                                         int o, uint64_t bm, BodyNew<T> &B)
 {
-    const int N = tb.N;
     T fx = T(0), fy = T(0), tau = T(0);
     const T mo = tb.mass[o];
     const T denom_self = T(1) + C.c * C.sub_dt / mo;
-    for (int s = 0; s < N; ++s) {
-        if (tb.body[s] != o) continue;
+    SS.each_of(tb, o, bm, [&](int s) {
         const T offx = tb.off[2 * s], offy = tb.off[2 * s + 1];
         const T owx = B.ca * offx - B.sa * offy;
         const T owy = B.sa * offx + B.ca * offy;
@@ -537,13 +615,12 @@ __device__ __forceinline__ void body_sum(const Cst<T> &C, const ObTab<T> &tb,
             tau = acc[2];
         }
         // contacts with the shapes of other bodies and of the scenery, in index order
-        for (int o2 = 0; o2 < N; ++o2) {
-            if (tb.body[o2] == o) continue;
+        SS.each_other(tb, o, bm, [&](int o2) {
             const T *d2 = od + 6 * o2;
             const int ty2 = (C.round_only ? 0 : tb.type[o2]);
             const T r2 = tb.rad[o2], h2x = tb.half[2 * o2], h2y = tb.half[2 * o2 + 1];
             if (b_apart(d2[0] - csx, d2[1] - csy, bound + shape_bound(ty2, r2, h2x, h2y) + C.margin))
-                continue;
+                return;
             T gx, gy, r0 = T(0), r1 = T(0);
             if (ty == 0 && ty2 == 0) {
                 pair_force(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4],
@@ -558,8 +635,8 @@ __device__ __forceinline__ void body_sum(const Cst<T> &C, const ObTab<T> &tb,
             fx += gx;
             fy += gy;
             tau += lx * gy - ly * gx;
-        }
-    }
+        });
+    });
     B.fx = fx;
     B.fy = fy;
     B.tau = tau;
@@ -607,12 +684,12 @@ __device__ __forceinline__ void body_advance(const Cst<T> &C, const ObTab<T> &tb
 
 // cos / sin of the angle of every movable body root in the obstacle state `od`.  Lane
 // `agent` of the env fills roots agent, agent + PA, ...
-template <typename T, int PA>
-__device__ __forceinline__ void body_trig(const ObTab<T> &tb, const Lane<T, PA> &L, const T *od,
-                                          T *cs)
+template <typename T, int PA, bool SM>
+__device__ __forceinline__ void body_trig(const ObTab<T> &tb, const ShapeSets<T, SM> &SS,
+                                          const Lane<T, PA> &L, const T *od, T *cs)
 {
     for (int o = L.agent; o < tb.N; o += PA) {
-        if (tb.body[o] != o || tb.kind[o] != 1) continue;
+        if (!SS.is_root(tb, o)) continue;
         T s, c;
         psincos(od[6 * tb.N + 6 * o + 2], s, c);
         cs[2 * o] = c;
@@ -623,21 +700,23 @@ __device__ __forceinline__ void body_trig(const ObTab<T> &tb, const Lane<T, PA> 
 // The body pass of one env: obn = obc with every movable body advanced and its shapes
 // re-installed at the new pose; cs_out = the new angles' cos / sin (cs_in: the input
 // angles'; both NULL when not kept); sums (nullable) receives each body's contact sum.
-// Lane `agent` of the env copies entries agent, agent+PA...
-template <typename T, int PA>
+// Lane `agent` of the env copies entries agent, agent+PA..., and re-installs the moved
+// body's shapes agent, agent+PA...  With the whole wave active.
+template <typename T, int PA, bool SM>
 __device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
-                                          const Lane<T, PA> &L, const BodyRow<T> &br,
-                                          const St<T> &st, const T *obc, T *obn, const T *ext,
-                                          const T *cs_in, T *cs_out, T *sums)
+                                          const ShapeSets<T, SM> &SS, const Lane<T, PA> &L,
+                                          const BodyRow<T> &br, const St<T> &st, const T *obc,
+                                          T *obn, const T *ext, const T *cs_in, T *cs_out,
+                                          T *sums)
 {
     const int N = tb.N;
     for (int q = L.agent; q < OB_W * N; q += PA) obn[q] = obc[q];
-    for (int o = 0; o < N; ++o) {
-        if (tb.body[o] != o || tb.kind[o] != 1) continue;
+    SS.each_root(tb, [&](int o) {
+        const uint64_t bm = SS.of(o);
         BodyNew<T> B;
         body_load(tb, obc, cs_in, o, B);
         B.ext = ext[o];
-        body_sum<T, PA>(C, tb, L, br, st, obc, o, B);
+        body_sum<T, PA>(C, tb, SS, L, br, st, obc, o, bm, B);
         body_advance(C, tb, o, B);
         psincos(B.nth, B.nsa, B.nca);
         if (L.agent == 0) {
@@ -657,21 +736,21 @@ __device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
                 sums[3 * o + 1] = B.fy;
                 sums[3 * o + 2] = B.tau;
             }
-            for (int s = 0; s < N; ++s) {
-                if (tb.body[s] != o) continue;
-                const T offx = tb.off[2 * s], offy = tb.off[2 * s + 1];
-                const T owx = B.nca * offx - B.nsa * offy;
-                const T owy = B.nsa * offx + B.nca * offy;
-                T *so = obn + 6 * s;
-                so[0] = B.nx + owx;
-                so[1] = B.ny + owy;
-                so[2] = B.nth;
-                so[3] = B.nvx - B.nom * owy;
-                so[4] = B.nvy + B.nom * owx;
-                so[5] = B.nom;
-            }
         }
-    }
+        for (int s = L.agent; s < N; s += PA) {
+            if (!SS.in_body(tb, o, bm, s)) continue;
+            const T offx = tb.off[2 * s], offy = tb.off[2 * s + 1];
+            const T owx = B.nca * offx - B.nsa * offy;
+            const T owy = B.nsa * offx + B.nca * offy;
+            T *so = obn + 6 * s;
+            so[0] = B.nx + owx;
+            so[1] = B.ny + owy;
+            so[2] = B.nth;
+            so[3] = B.nvx - B.nom * owy;
+            so[4] = B.nvy + B.nom * owx;
+            so[5] = B.nom;
+        }
+    });
 }
 
 // Waves per SIMD the float32 profile instances of the body kernels are compiled for
@@ -708,6 +787,8 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
     T *const lext = lcs + (size_t)2 * EPW * 2 * tb.N;
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
+    ShapeSets<T, !(F & FT_MANYSH)> SS;
+    SS.init(tb, L.lane);
     fold_prm<F>(L.pr);
     const BodyRow<T> br = body_row<T, PA>(C, tb, L);
     lr[L.lane] = L.pr.radius;
@@ -720,7 +801,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
     for (int q = L.agent; q < NW; q += PA) obs(0)[q] = io.ob0[eo + q];
     for (int o = L.lane; o < tb.N; o += 64) lext[o] = body_ext(tb, o);
     wave_lds_sync();
-    body_trig<T, PA>(tb, L, obs(0), ocs(0));
+    body_trig<T, PA>(tb, SS, L, obs(0), ocs(0));
     St<T> st;
     load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
     if (!L.active) st.px = st.py = __builtin_nan("");
@@ -746,7 +827,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
             const T *obc = obs(cur);
             T Fx, Fy;
             forces_b<T, PA>(C, tb, L, sl, lr, obc, st, s, s == 0 || !ok, cand, Fx, Fy);
-            body_pass<T, PA>(C, tb, L, br, st, obc, obs(cur ^ 1), lext, ocs(cur), ocs(cur ^ 1),
+            body_pass<T, PA>(C, tb, SS, L, br, st, obc, obs(cur ^ 1), lext, ocs(cur), ocs(cur ^ 1),
                              nullptr);
             St<T> nx;
             integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
@@ -809,8 +890,9 @@ __host__ __device__ constexpr size_t body_fwd_lds_total(int PA, int N, size_t ts
 // the forward body_pass of this substep read and wrote: each body's new state is rebuilt
 // from its recorded contact sum, not summed again (NULL cs / sums: recomputed).  Same
 // order of terms as the oracle's bodies_env_adj.
-template <typename T, int PA>
+template <typename T, int PA, bool SM>
 __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &tb,
+                                              const ShapeSets<T, SM> &SS,
                                               const Lane<T, PA> &L, const BodyRow<T> &br,
                                               const St<T> &st, const T *obc, const T *gout,
                                               T *gin, St<T> &ga, const T *ext, const T *cs_in,
@@ -821,11 +903,11 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
     // pass-through of everything the pass does not rewrite
     for (int q = L.agent; q < OB_W * N; q += PA) {
         const int s = q / 6;
-        gin[q] = (q < 6 * N && shape_moves(tb, s)) ? T(0) : gout[q];
+        gin[q] = (q < 6 * N && SS.moves(tb, s)) ? T(0) : gout[q];
     }
     wave_lds_sync();
-    for (int o = 0; o < N; ++o) {
-        if (tb.body[o] != o || tb.kind[o] != 1) continue;
+    SS.each_root(tb, [&](int o) {
+        const uint64_t bm = SS.of(o);
         BodyNew<T> B;
         body_load(tb, obc, cs_in, o, B);
         B.ext = ext[o];
@@ -834,7 +916,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
             B.fy = sums[3 * o + 1];
             B.tau = sums[3 * o + 2];
         } else {
-            body_sum<T, PA>(C, tb, L, br, st, obc, o, B);
+            body_sum<T, PA>(C, tb, SS, L, br, st, obc, o, bm, B);
         }
         body_advance(C, tb, o, B);
         if (cs_out) {
@@ -850,8 +932,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
         // adjoint of the new body state: its own entry plus every re-installed shape
         const T *gb = gout + 6 * N + 6 * o;
         T g_nx = gb[0], g_ny = gb[1], g_nth = gb[2], g_nvx = gb[3], g_nvy = gb[4], g_nom = gb[5];
-        for (int s = 0; s < N; ++s) {
-            if (tb.body[s] != o) continue;
+        SS.each_of(tb, o, bm, [&](int s) {
             const T offx = tb.off[2 * s], offy = tb.off[2 * s + 1];
             const T owx = B.nca * offx - B.nsa * offy;
             const T owy = B.nsa * offx + B.nca * offy;
@@ -864,7 +945,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
             g_nom += gs[5] - gs[3] * owy + gs[4] * owx;
             const T g_owx = gs[0] + gs[4] * B.nom, g_owy = gs[1] - gs[3] * B.nom;
             g_nth += -g_owx * owy + g_owy * owx;
-        }
+        });
         T g_th = g_nth;
         g_nom += g_nth * sdt;
         T g_qx = B.clx ? T(0) : g_nx, g_qy = B.cly ? T(0) : g_ny;
@@ -875,8 +956,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
         T g_om = g_nom * ang_decay;
         const T g_tau = g_nom * ang_decay * sdt / I;
         const T denom_self = T(1) + C.c * C.sub_dt / m;
-        for (int s = 0; s < N; ++s) {
-            if (tb.body[s] != o) continue;
+        SS.each_of(tb, o, bm, [&](int s) {
             const T offx = tb.off[2 * s], offy = tb.off[2 * s + 1];
             const T owx = B.ca * offx - B.sa * offy;
             const T owy = B.sa * offx + B.ca * offy;
@@ -954,13 +1034,12 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
             }
             T g_owx = acc[0], g_owy = acc[1], g_csx = acc[2], g_csy = acc[3], g_vsx = acc[4],
               g_vsy = acc[5], g_thd = acc[6], g_omd = acc[7];
-            for (int o2 = 0; o2 < N; ++o2) {
-                if (tb.body[o2] == o) continue;
+            SS.each_other(tb, o, bm, [&](int o2) {
                 const T *d2 = obc + 6 * o2;
                 const int ty2 = (C.round_only ? 0 : tb.type[o2]);
                 const T r2 = tb.rad[o2], h2x = tb.half[2 * o2], h2y = tb.half[2 * o2 + 1];
                 if (b_apart(d2[0] - csx, d2[1] - csy, bound + shape_bound(ty2, r2, h2x, h2y) + C.margin))
-                    continue;
+                    return;
                 if (ty != 0 || ty2 != 0) {
                     // the term's Jacobian over both shapes' states, one input at a time
                     const T ca2 = ty2 == 0 ? T(1) : m_cos(d2[2]);
@@ -976,7 +1055,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
                     g_owy -= g_tau * f0;
                     const T in[12] = {csx, csy, vsx, vsy, B.th, B.om,
                                       d2[0], d2[1], d2[3], d2[4], d2[2], d2[5]};
-                    const bool mv = shape_moves(tb, o2) && L.agent == 0;
+                    const bool mv = SS.moves(tb, o2) && L.agent == 0;
                     for (int k = 0; k < 12; ++k) {
                         Dual<T, 1> x[12], o0, o1, l0, l1;
 #pragma unroll
@@ -1000,7 +1079,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
                             gin[6 * o2 + slot] += adj;
                         }
                     }
-                    continue;
+                    return;
                 }
                 T gx, gy;
                 pair_force(C, csx - d2[0], csy - d2[1], vsx - d2[3], vsy - d2[4],
@@ -1014,14 +1093,14 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
                 g_csy += ady;
                 g_vsx += arx;
                 g_vsy += ary;
-                if (shape_moves(tb, o2) && L.agent == 0) {
+                if (SS.moves(tb, o2) && L.agent == 0) {
                     T *g2 = gin + 6 * o2;
                     g2[0] -= adx;
                     g2[1] -= ady;
                     g2[3] -= arx;
                     g2[4] -= ary;
                 }
-            }
+            });
             g_qx += g_csx;
             g_qy += g_csy;
             g_owx += g_csx + g_vsy * B.om;
@@ -1030,7 +1109,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
             g_tvy += g_vsy;
             g_om += -g_vsx * owy + g_vsy * owx + g_omd;
             g_th += -g_owx * owy + g_owy * owx + g_thd;
-        }
+        });
         if (L.agent == 0) {
             T *gi = gin + 6 * N + 6 * o;
             gi[0] = g_qx;
@@ -1041,7 +1120,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
             gi[5] = g_om;
         }
         wave_lds_sync();
-    }
+    });
 }
 
 template <typename T, int PA, bool DRONE, unsigned F>
@@ -1068,6 +1147,8 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
     for (int o = threadIdx.x; o < N; o += 64) lext[o] = body_ext(tb, o);
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L);
+    ShapeSets<T, !(F & FT_MANYSH)> SS;
+    SS.init(tb, L.lane);
     fold_prm<F>(L.pr);
     const BodyRow<T> br = body_row<T, PA>(C, tb, L);
     lr[L.lane] = L.pr.radius;
@@ -1100,7 +1181,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             T *dst = lobs + (size_t)ew * NW;
             for (int q = L.agent; q < NW; q += PA) dst[q] = src[q];
             wave_lds_sync();
-            if (lcs) body_trig<T, PA>(tb, L, dst, lcs + (size_t)ew * 2 * N);
+            if (lcs) body_trig<T, PA>(tb, SS, L, dst, lcs + (size_t)ew * 2 * N);
         }
         T a[4];
         load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
@@ -1120,7 +1201,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             sl[F_FX * 64 + L.lane] = Fx;
             sl[F_FY * 64 + L.lane] = Fy;
             lmask[s * 64 + L.lane] = incl;
-            body_pass<T, PA>(C, tb, L, br, st, obc, lobs + ((size_t)(s + 1) * EPW + ew) * NW, lext,
+            body_pass<T, PA>(C, tb, SS, L, br, st, obc, lobs + ((size_t)(s + 1) * EPW + ew) * NW, lext,
                              lcs ? lcs + ((size_t)s * EPW + ew) * 2 * N : nullptr,
                              lcs ? lcs + ((size_t)(s + 1) * EPW + ew) * 2 * N : nullptr,
                              lsum ? lsum + ((size_t)s * EPW + ew) * 3 * N : nullptr);
@@ -1149,7 +1230,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             T gFx, gFy;
             integrate_adj<T, DRONE>(C, L.pr, in, a, Fx, Fy, gs, gi, ga, gFx, gFy);
             // the body pass: adjoint of its input obstacle state into gprev
-            body_pass_adj<T, PA>(C, tb, L, br, in, obc, gob, gprev, gi, lext,
+            body_pass_adj<T, PA>(C, tb, SS, L, br, in, obc, gob, gprev, gi, lext,
                                  lcs ? lcs + ((size_t)s * EPW + ew) * 2 * N : nullptr,
                                  lcs ? lcs + ((size_t)(s + 1) * EPW + ew) * 2 * N : nullptr,
                                  lsum ? lsum + ((size_t)s * EPW + ew) * 3 * N : nullptr);
@@ -1181,7 +1262,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
                 }
                 // obstacles: the agent's adjoint, and the moving shapes' in agent order
                 for (int o = 0; o < N; ++o) {
-                    const bool mv = shape_moves(tb, o);
+                    const bool mv = SS.moves(tb, o);
                     T op[6];
                     if (L.active) {
                         ob_force_adj(C, tb, obc, o, in.px, in.py, in.vx, in.vy, L.pr.radius,

@@ -236,7 +236,8 @@ enum : unsigned {
     FT_BICY = 1u << 8,
     FT_DRONE = 1u << 9,
     FT_SHAPES = 1u << 10,  // box or segment obstacles in a body world (body kernels only)
-    FT_ALL = 0x7ffu,
+    FT_MANYSH = 1u << 11,  // more than 64 obstacle shapes in a body world (body kernels only)
+    FT_ALL = 0xfffu,
 };
 // Profiles compiled besides FT_ALL (float32): 2-D fleets with obstacles and walls under
 // Euler, drone fleets (config 4), holonomic fleets with movable bodies
@@ -313,7 +314,11 @@ __device__ __forceinline__ void lane_init(const Cst<T> &C, const Args<T> &g, Lan
 // The result is typed as a global (address space 1) pointer: laundered through integers
 // a generic pointer would be read with flat loads, which also count as LDS operations, so
 // every wait for an LDS result would wait for them too.
+#if defined(__HIP_DEVICE_COMPILE__)
 #define SWARP_GLOBAL __attribute__((address_space(1)))
+#else
+#define SWARP_GLOBAL
+#endif
 template <typename T> __device__ __forceinline__ const SWARP_GLOBAL T *vgpr_ptr(const T *p)
 {
     const uint64_t u = (uint64_t)p;

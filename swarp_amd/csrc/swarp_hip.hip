@@ -212,6 +212,7 @@ static unsigned world_features(const swarp_desc_t *d, bool body)
     if (!body && d->n_obstacles > 0) f |= FT_OBST;
     // box or segment shapes among the obstacles of a body world (0: not known)
     if (body && d->obstacle_types != 1) f |= FT_SHAPES;
+    if (body && d->n_obstacles > 64) f |= FT_MANYSH;
     if (d->soft_walls) f |= FT_WALL;
     if (d->clamp_bounds) f |= FT_CLAMP;
     const unsigned models = d->fleet_models ? (unsigned)d->fleet_models : ~0u;

@@ -230,11 +230,13 @@ def _ring_extra(n, radius=1.0, r=0.07):
                  for k, a in enumerate(ang))
 
 
-@pytest.mark.parametrize("A,n_extra", [(64, 35), (16, 19)])
+@pytest.mark.parametrize("A,n_extra", [(64, 35), (16, 19), (16, 59), (16, 75)])
 def test_bodies_beyond_sixteen_obstacles(A, n_extra):
     """More than 16 obstacles per env (each env's obstacle state staged in LDS sized by the
     obstacle count): the cross body and a ring of movable and static circles, one env per
-    wave at 64 agents and four per wave at 16."""
+    wave at 64 agents and four per wave at 16.  64 shapes is the most the instances that
+    keep the shape sets as wave masks take; 80 runs the instances that test the shapes
+    one by one."""
     E = 6 if A == 64 else 9
     s0, acts = _pushers(E, A, 3, spread=1.2)
     obs = cross_obs(E, (0.0, 0.0), extra=_ring_extra(n_extra))
