@@ -168,6 +168,39 @@ constexpr int F_PX = 0, F_PY = 1, F_VX = 2, F_VY = 3, F_TH = 4, F_S = 5, F_W = 6
 
 // Neighbour lists of one agent as a bitmask over the env's agents, ascending bit =
 // ascending list order (neighbors.py:90-96).  Full scan over every pair of the env.
+// A wave-uniform 32-bit value written into lane L of a per-lane value (v_writelane_b32;
+// the lane is an inline constant: a second scalar operand would exceed the instruction's
+// one scalar read); the other lanes keep theirs.  The compiler's hazard checks do not see
+// into the asm: when v is VCC just written by a compare, the read as a scalar operand
+// needs one wait state, which the s_nop provides.
+template <int L> __device__ __forceinline__ uint32_t set_lane(uint32_t v, uint32_t old)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    asm("s_nop 0\n\tv_writelane_b32 %0, %1, %2" : "+v"(old) : "s"(v), "i"(L));
+    return old;
+#else
+    return (int)(threadIdx.x % 64) == L ? v : old;
+#endif
+}
+template <int L> __device__ __forceinline__ uint64_t set_lane64(uint64_t v, uint64_t old)
+{
+    const uint32_t lo = set_lane<L>((uint32_t)v, (uint32_t)old);
+    const uint32_t hi = set_lane<L>((uint32_t)(v >> 32), (uint32_t)(old >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// f(IntC<B>{}), f(IntC<B + 1>{}), ..., f(IntC<E - 1>{}): a loop whose index is a constant.
+template <int V> struct IntC {
+    static constexpr int value = V;
+};
+template <int B, int E, typename Fn> __device__ __forceinline__ void static_for(Fn &&f)
+{
+    if constexpr (B < E) {
+        f(IntC<B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
 template <typename T, int PA>
 __device__ __forceinline__ typename MaskT<PA>::type scan_all(const T *lx, const T *ly, int base,
                                                              int A, int me, T px, T py, T t_nbr,
@@ -177,12 +210,27 @@ __device__ __forceinline__ typename MaskT<PA>::type scan_all(const T *lx, const 
     typedef typename MaskT<PA>::type M;
     M incl = 0, cd = 0;
     (void)A;  // pad slots (b >= A) hold NaN positions and never pass the test
+    if constexpr (PA == 64) {
+        // One env per wave, and the env's lanes all run this scan together.  A pair's
+        // squared distance has the same bits from either end (x_b - x_a = -(x_a - x_b)
+        // exactly), so the wave's ballot over agent b's column is agent b's row: it goes
+        // to lane b as a scalar, with no per-lane bit assembly.
+        static_for<0, 64>([&](auto bc) {
+            constexpr int b = decltype(bc)::value;
+            const T dx = lx[base + b] - px, dy = ly[base + b] - py;
+            const T d2 = dx * dx + dy * dy;
+            const uint64_t ci = __ballot(d2 <= t_nbr), cs = __ballot(d2 <= t_skin);
+            incl = (M)set_lane64<b>(ci, (uint64_t)incl);
+            cd = (M)set_lane64<b>(cs, (uint64_t)cd);
+        });
+    } else {
 #pragma unroll
-    for (int b = 0; b < PA; ++b) {
-        T dx = lx[base + b] - px, dy = ly[base + b] - py;
-        T d2 = dx * dx + dy * dy;
-        incl |= d2 <= t_nbr ? (M(1) << b) : M(0);
-        cd |= d2 <= t_skin ? (M(1) << b) : M(0);
+        for (int b = 0; b < PA; ++b) {
+            T dx = lx[base + b] - px, dy = ly[base + b] - py;
+            T d2 = dx * dx + dy * dy;
+            incl |= d2 <= t_nbr ? (M(1) << b) : M(0);
+            cd |= d2 <= t_skin ? (M(1) << b) : M(0);
+        }
     }
     const M self = ~(M(1) << me);
     cand = cd & self;
