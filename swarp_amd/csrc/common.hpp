@@ -215,13 +215,23 @@ __device__ __forceinline__ typename MaskT<PA>::type scan_all(const T *lx, const 
         // squared distance has the same bits from either end (x_b - x_a = -(x_a - x_b)
         // exactly), so the wave's ballot over agent b's column is agent b's row: it goes
         // to lane b as a scalar, with no per-lane bit assembly.
-        static_for<0, 64>([&](auto bc) {
-            constexpr int b = decltype(bc)::value;
-            const T dx = lx[base + b] - px, dy = ly[base + b] - py;
-            const T d2 = dx * dx + dy * dy;
-            const uint64_t ci = __ballot(d2 <= t_nbr), cs = __ballot(d2 <= t_skin);
-            incl = (M)set_lane64<b>(ci, (uint64_t)incl);
-            cd = (M)set_lane64<b>(cs, (uint64_t)cd);
+        // (positions read eight at a time, so that one wait covers eight LDS reads)
+        static_for<0, 8>([&](auto cc) {
+            constexpr int b0 = decltype(cc)::value * 8;
+            T qx[8], qy[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                qx[k] = lx[base + b0 + k];
+                qy[k] = ly[base + b0 + k];
+            }
+            static_for<0, 8>([&](auto kc) {
+                constexpr int k = decltype(kc)::value, b = b0 + k;
+                const T dx = qx[k] - px, dy = qy[k] - py;
+                const T d2 = dx * dx + dy * dy;
+                const uint64_t ci = __ballot(d2 <= t_nbr), cs = __ballot(d2 <= t_skin);
+                incl = (M)set_lane64<b>(ci, (uint64_t)incl);
+                cd = (M)set_lane64<b>(cs, (uint64_t)cd);
+            });
         });
     } else {
 #pragma unroll
