@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define SWARP_ABI_VERSION 15
+#define SWARP_ABI_VERSION 16
 
 #define SWARP_F32 0
 #define SWARP_F64 1
@@ -234,6 +234,34 @@ int swarp_rollout_bwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
  * taped forward and its backward accept the same configurations,
  * swarp/interop/autograd.py:229-296). */
 int swarp_rollout_bwd_ob_check(const swarp_desc_t *desc);
+
+/* Body tape: per substep and movable body, the body pass's result -- the body's new pose
+ * and velocity, the new angle's cos / sin, its contact force and torque -- written by the
+ * forward so that the backward's recompute of each step reads it instead of evaluating
+ * the pass again (the agents' forces are still recomputed from the checkpoints).  Bodies
+ * are counted in root order (the obstacle indices o with body[o] = o and kind[o] = 1);
+ * a tape may hold the first n_bodies of them, and the backward evaluates the others.
+ * No counterpart in the reference: its body pass runs on untaped steps and is not
+ * differentiated (swarp/core/stepper.py:952-991).
+ * Writes in *bytes the size of the tape of a T-step rollout holding n_bodies bodies
+ * (1 <= n_bodies <= n_obstacles): T * substeps * n_envs * n_bodies * 12 scalars. */
+int swarp_ob_tape_bytes(const swarp_desc_t *desc, int32_t T, int32_t n_bodies, uint64_t *bytes);
+
+/* swarp_rollout_fwd_ob that also writes the body tape (device memory owned by the caller;
+ * tape_bytes = swarp_ob_tape_bytes(desc, T, n_bodies) for some n_bodies). */
+int swarp_rollout_fwd_ob_tape(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                              const void *ob0, const void *actions, const swarp_state_t *traj,
+                              const swarp_state_t *final_state, void *ob_traj, void *tape,
+                              uint64_t tape_bytes, void *stream);
+
+/* swarp_rollout_bwd_ob reading the body pass of the tape written by
+ * swarp_rollout_fwd_ob_tape on the same inputs (same results, bit for bit). */
+int swarp_rollout_bwd_ob_tape(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                              const void *ob0, const void *actions, const swarp_state_t *traj,
+                              const void *ob_traj, const swarp_state_t *adj_traj,
+                              const swarp_state_t *adj_final, const void *adj_ob_traj,
+                              const swarp_state_t *adj_state0, void *adj_ob0, void *adj_actions,
+                              const void *tape, uint64_t tape_bytes, void *stream);
 
 /* Padded radius-neighbour lists of one state: replaces NeighborGrid.query_into's
  * brute-force kernel (swarp/core/neighbors.py:76-97, 465-492).  pos [E,A,2] of

@@ -13,7 +13,7 @@ from pathlib import Path
 
 import torch
 
-ABI_VERSION = 15
+ABI_VERSION = 16
 F32, F64 = 0, 1
 EULER, RK4 = 0, 1
 LISTS_BRUTE, LISTS_GRID = 0, 1
@@ -161,6 +161,23 @@ SIGNATURES = {
         ctypes.c_int,
     ),
     "swarp_rollout_bwd_ob_check": ([ctypes.POINTER(SwarpDesc)], ctypes.c_int),
+    "swarp_ob_tape_bytes": (
+        [ctypes.POINTER(SwarpDesc), ctypes.c_int32, ctypes.c_int32, ctypes.POINTER(ctypes.c_uint64)],
+        ctypes.c_int,
+    ),
+    "swarp_rollout_fwd_ob_tape": (
+        [ctypes.POINTER(SwarpDesc), ctypes.c_int32, ctypes.POINTER(SwarpState), ctypes.c_void_p,
+         ctypes.c_void_p, ctypes.POINTER(SwarpState), ctypes.POINTER(SwarpState), ctypes.c_void_p,
+         ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p],
+        ctypes.c_int,
+    ),
+    "swarp_rollout_bwd_ob_tape": (
+        [ctypes.POINTER(SwarpDesc), ctypes.c_int32, ctypes.POINTER(SwarpState), ctypes.c_void_p,
+         ctypes.c_void_p, ctypes.POINTER(SwarpState), ctypes.c_void_p, ctypes.POINTER(SwarpState),
+         ctypes.POINTER(SwarpState), ctypes.c_void_p, ctypes.POINTER(SwarpState), ctypes.c_void_p,
+         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p],
+        ctypes.c_int,
+    ),
     "swarp_neighbors": (
         [ctypes.POINTER(SwarpDesc), ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
          ctypes.c_void_p, ctypes.c_void_p],

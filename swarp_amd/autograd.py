@@ -258,9 +258,9 @@ class _RolloutFn(torch.autograd.Function):
 
 
 def _launch_fwd_ob(stepper: Stepper, state0, ob0: torch.Tensor, actions_seq: torch.Tensor,
-                   traj, final, ob_traj: torch.Tensor) -> None:
+                   traj, final, ob_traj: torch.Tensor, tape: torch.Tensor | None = None) -> None:
     """One forward launch of a world with movable bodies (five state fields, nine with
-    drones)."""
+    drones); ``tape`` (uint8, ``Stepper.ob_tape_bytes`` long) also receives the body tape."""
     T, E, _, ad = actions_seq.shape
     nf = _nfields(stepper)
     lib = _lib.load()
@@ -272,10 +272,18 @@ def _launch_fwd_ob(stepper: Stepper, state0, ob0: torch.Tensor, actions_seq: tor
     s0 = state_struct(list(state0)[:nf], EA, dt, "state0")
     fin = state_struct(list(final)[:nf], EA, dt, "final")
     tr = state_struct(list(traj)[:nf], (T - 1) * EA, dt, "traj") if traj is not None and T > 1 else None
-    _lib.check(lib.swarp_rollout_fwd_ob(
+    if tape is None:
+        _lib.check(lib.swarp_rollout_fwd_ob(
+            ctypes.byref(desc), T, ctypes.byref(s0), ob0.data_ptr(), actions_seq.data_ptr(),
+            ctypes.byref(tr) if tr is not None else None, ctypes.byref(fin), ob_traj.data_ptr(),
+            _stream(actions_seq),
+        ))
+        return
+    check_extent(tape, stepper.ob_tape_bytes(E, ad, T), "ob_tape", torch.uint8)
+    _lib.check(lib.swarp_rollout_fwd_ob_tape(
         ctypes.byref(desc), T, ctypes.byref(s0), ob0.data_ptr(), actions_seq.data_ptr(),
         ctypes.byref(tr) if tr is not None else None, ctypes.byref(fin), ob_traj.data_ptr(),
-        _stream(actions_seq),
+        tape.data_ptr(), tape.numel(), _stream(actions_seq),
     ))
 
 
@@ -297,13 +305,17 @@ class _RolloutObFn(torch.autograd.Function):
         final = _empty_like_fields(stepper, (), E, dev)
         traj = _empty_like_fields(stepper, (max(T - 1, 0),), E, dev)
         ob_traj = torch.empty((T,) + tuple(ob0.shape), device=dev, dtype=ob0.dtype)
+        # the body tape lets the backward skip evaluating the body pass again
+        nb = stepper.ob_tape_bytes(E, actions_seq.shape[3], T)
+        tape = torch.empty(nb, device=dev, dtype=torch.uint8) if nb else None
         sink = KERNEL_EVENTS
         if sink is not None:
             e0 = _event(actions_seq)
-        _launch_fwd_ob(stepper, state0, ob0, actions_seq, traj, final, ob_traj)
+        _launch_fwd_ob(stepper, state0, ob0, actions_seq, traj, final, ob_traj, tape)
         if sink is not None:
             sink.append(("fwd", e0, _event(actions_seq)))
         ctx.stepper = stepper
+        ctx.tape = tape
         ctx.T = T
         ctx.nf = len(state0)
         ctx.save_for_backward(actions_seq, ob0, ob_traj, *state0, *traj)
@@ -344,15 +356,21 @@ class _RolloutObFn(torch.autograd.Function):
         sink = KERNEL_EVENTS
         if sink is not None:
             e0 = _event(actions_seq)
-        _lib.check(lib.swarp_rollout_bwd_ob(
+        args = (
             ctypes.byref(desc), T, ctypes.byref(s0), ob0.data_ptr(), actions_seq.data_ptr(),
             ctypes.byref(tr) if tr is not None else None, ob_traj.data_ptr(),
             ctypes.byref(gtr) if gtr is not None else None,
             ctypes.byref(gfin) if gfin is not None else None,
             g_ob.data_ptr() if g_ob is not None else None, ctypes.byref(a0),
             adj_ob0.data_ptr() if adj_ob0 is not None else None, adj_act.data_ptr(),
-            _stream(actions_seq),
-        ))
+        )
+        tape = ctx.tape
+        if tape is None:
+            _lib.check(lib.swarp_rollout_bwd_ob(*args, _stream(actions_seq)))
+        else:
+            check_extent(tape, stepper.ob_tape_bytes(E, ad, T), "ob_tape", torch.uint8)
+            _lib.check(lib.swarp_rollout_bwd_ob_tape(*args, tape.data_ptr(), tape.numel(),
+                                                     _stream(actions_seq)))
         if sink is not None:
             sink.append(("bwd", e0, _event(actions_seq)))
         return (None, adj_act if need[1] else None, adj_ob0, *adj0)

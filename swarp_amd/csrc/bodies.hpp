@@ -50,7 +50,17 @@ template <typename T> struct ObIO {
     T *traj;            // [T, E, 12N] state after each step
     const T *atraj;     // [T, E, 12N] adjoint arriving at each step's output (nullable)
     T *a0;              // [E, 12N] adjoint of ob0 (nullable)
+    // Body tape (nullable): [T][S][tape_roots][E][BODY_REC] records of the body pass, one
+    // per substep and movable body (in root order, the first tape_roots of them): written
+    // by the forward, read by the backward in place of evaluating the pass again.
+    T *tape;
+    int tape_roots;
 };
+
+// Body-tape record of one body and substep: its new pose and velocity (x, y, angle,
+// vel x, vel y, ang_vel), the new angle's cos and sin, its contact sum (fx, fy, tau); one
+// pad entry keeps records 16-byte aligned.
+constexpr int BODY_REC = 12;
 
 // An agent as the body pass sees it: the radius and the implicit damping denominator
 // 1 + c sub_dt / m of its parameter row in the table the pass reads.
@@ -701,24 +711,60 @@ __device__ __forceinline__ void body_trig(const ObTab<T> &tb, const ShapeSets<T,
 // re-installed at the new pose; cs_out = the new angles' cos / sin (cs_in: the input
 // angles'; both NULL when not kept); sums (nullable) receives each body's contact sum.
 // Lane `agent` of the env copies entries agent, agent+PA..., and re-installs the moved
-// body's shapes agent, agent+PA...  With the whole wave active.
+// body's shapes agent, agent+PA...  With the whole wave active.  Body-tape records of
+// this env and substep (BODY_REC entries per body, rstride entries from one body's to
+// the next's, the first `rroots` bodies): `rout` receives them (nullable); with `rin`
+// they are read instead of evaluating those bodies' contact sums and integration.
 template <typename T, int PA, bool SM>
 __device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
                                           const ShapeSets<T, SM> &SS, const Lane<T, PA> &L,
                                           const BodyRow<T> &br, const St<T> &st, const T *obc,
                                           T *obn, const T *ext, const T *cs_in, T *cs_out,
-                                          T *sums)
+                                          T *sums, const T *rin = nullptr, T *rout = nullptr,
+                                          size_t rstride = 0, int rroots = 0)
 {
     const int N = tb.N;
     for (int q = L.agent; q < OB_W * N; q += PA) obn[q] = obc[q];
+    int r = 0;  // the body's place in root order
     SS.each_root(tb, [&](int o) {
         const uint64_t bm = SS.of(o);
         BodyNew<T> B;
-        body_load(tb, obc, cs_in, o, B);
-        B.ext = ext[o];
-        body_sum<T, PA>(C, tb, SS, L, br, st, obc, o, bm, B);
-        body_advance(C, tb, o, B);
-        psincos(B.nth, B.nsa, B.nca);
+        if (rin && r < rroots) {
+            const T *rec = rin + (size_t)r * rstride;
+            B.nx = rec[0];
+            B.ny = rec[1];
+            B.nth = rec[2];
+            B.nvx = rec[3];
+            B.nvy = rec[4];
+            B.nom = rec[5];
+            B.nca = rec[6];
+            B.nsa = rec[7];
+            B.fx = rec[8];
+            B.fy = rec[9];
+            B.tau = rec[10];
+        } else {
+            body_load(tb, obc, cs_in, o, B);
+            B.ext = ext[o];
+            body_sum<T, PA>(C, tb, SS, L, br, st, obc, o, bm, B);
+            body_advance(C, tb, o, B);
+            psincos(B.nth, B.nsa, B.nca);
+        }
+        if (rout && r < rroots && L.agent == 0) {
+            T *rec = rout + (size_t)r * rstride;
+            rec[0] = B.nx;
+            rec[1] = B.ny;
+            rec[2] = B.nth;
+            rec[3] = B.nvx;
+            rec[4] = B.nvy;
+            rec[5] = B.nom;
+            rec[6] = B.nca;
+            rec[7] = B.nsa;
+            rec[8] = B.fx;
+            rec[9] = B.fy;
+            rec[10] = B.tau;
+            rec[11] = T(0);
+        }
+        ++r;
         if (L.agent == 0) {
             T *bo = obn + 6 * N + 6 * o;
             bo[0] = B.nx;
@@ -827,8 +873,11 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
             const T *obc = obs(cur);
             T Fx, Fy;
             forces_b<T, PA>(C, tb, L, sl, lr, obc, st, s, s == 0 || !ok, cand, Fx, Fy);
+            T *rout = io.tape && env_ok ? io.tape + (((size_t)t * C.S + s) * io.tape_roots * C.E +
+                                                     L.env) * BODY_REC
+                                        : nullptr;
             body_pass<T, PA>(C, tb, SS, L, br, st, obc, obs(cur ^ 1), lext, ocs(cur), ocs(cur ^ 1),
-                             nullptr);
+                             nullptr, nullptr, rout, (size_t)C.E * BODY_REC, io.tape_roots);
             St<T> nx;
             integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
             if (C.use_skin) {
@@ -1201,10 +1250,14 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             sl[F_FX * 64 + L.lane] = Fx;
             sl[F_FY * 64 + L.lane] = Fy;
             lmask[s * 64 + L.lane] = incl;
+            const T *rin = io.tape ? io.tape + (((size_t)t * C.S + s) * io.tape_roots * C.E +
+                                                (env_ok ? L.env : 0)) * BODY_REC
+                                   : nullptr;
             body_pass<T, PA>(C, tb, SS, L, br, st, obc, lobs + ((size_t)(s + 1) * EPW + ew) * NW, lext,
                              lcs ? lcs + ((size_t)s * EPW + ew) * 2 * N : nullptr,
                              lcs ? lcs + ((size_t)(s + 1) * EPW + ew) * 2 * N : nullptr,
-                             lsum ? lsum + ((size_t)s * EPW + ew) * 3 * N : nullptr);
+                             lsum ? lsum + ((size_t)s * EPW + ew) * 3 * N : nullptr, rin, nullptr,
+                             (size_t)C.E * BODY_REC, io.tape_roots);
             // the last substep's agent output is the step's checkpoint: not needed here
             if (s + 1 < C.S) {
                 St<T> nx;

@@ -458,10 +458,20 @@ template <typename T> static int fill_obtab(const swarp_desc_t *d, ObTab<T> &tb)
     return 0;
 }
 
+// Bodies a body tape of `bytes` holds for a T-step rollout of d (0: not a whole number of
+// per-body slices, or none).
+template <typename T> static int64_t ob_tape_roots(const swarp_desc_t *d, int32_t nT, uint64_t bytes)
+{
+    const uint64_t per = (uint64_t)nT * d->substeps * d->n_envs * BODY_REC * sizeof(T);
+    if (per == 0 || bytes % per != 0) return 0;
+    return (int64_t)(bytes / per);
+}
+
 template <typename T>
 static int rollout_fwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s0,
                           const void *ob0, const void *act, const swarp_state_t *traj,
-                          const swarp_state_t *fin, void *ob_traj, hipStream_t st)
+                          const swarp_state_t *fin, void *ob_traj, void *tape, uint64_t tape_bytes,
+                          hipStream_t st)
 {
     Cst<T> C;
     fill_cst<T>(d, skin_of(d), C);
@@ -479,7 +489,14 @@ static int rollout_fwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     if (nT > 1) copy_fields<T>(traj, a.traj.f);
     a.act = (const T *)act;
     a.nsteps = nT;
-    ObIO<T> io = {(const T *)ob0, (T *)ob_traj, nullptr, nullptr};
+    ObIO<T> io = {(const T *)ob0, (T *)ob_traj, nullptr, nullptr, nullptr, 0};
+    if (tape) {
+        const int64_t r = ob_tape_roots<T>(d, nT, tape_bytes);
+        if (r < 1 || r > d->n_obstacles)
+            return fail("tape_bytes is not swarp_ob_tape_bytes of 1..n_obstacles bodies");
+        io.tape = (T *)tape;
+        io.tape_roots = (int)r;
+    }
     const int PA = body_pa<T>(d);
     launch_body_fwd<T>(PA, C, a, tb, io, world_features(d, true), d->has_drone != 0, st);
     hipError_t e = hipGetLastError();
@@ -492,7 +509,8 @@ static int rollout_bwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
                           const void *ob0, const void *act, const swarp_state_t *traj,
                           const void *ob_traj, const swarp_state_t *atraj,
                           const swarp_state_t *afin, const void *aob_traj,
-                          const swarp_state_t *a0, void *aob0, void *aact, hipStream_t st)
+                          const swarp_state_t *a0, void *aob0, void *aact, const void *tape,
+                          uint64_t tape_bytes, hipStream_t st)
 {
     Cst<T> C;
     fill_cst<T>(d, skin_of(d), C);
@@ -512,7 +530,14 @@ static int rollout_bwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     a.act = (const T *)act;
     a.aact = (T *)aact;
     a.nsteps = nT;
-    ObIO<T> io = {(const T *)ob0, (T *)ob_traj, (const T *)aob_traj, (T *)aob0};
+    ObIO<T> io = {(const T *)ob0, (T *)ob_traj, (const T *)aob_traj, (T *)aob0, nullptr, 0};
+    if (tape) {
+        const int64_t r = ob_tape_roots<T>(d, nT, tape_bytes);
+        if (r < 1 || r > d->n_obstacles)
+            return fail("tape_bytes is not swarp_ob_tape_bytes of 1..n_obstacles bodies");
+        io.tape = (T *)tape;
+        io.tape_roots = (int)r;
+    }
     const int PA = body_pa<T>(d);
     // the per-substep body caches (cos / sin, contact sums) when they fit
     const bool dr = d->has_drone != 0;
@@ -630,8 +655,43 @@ int swarp_rollout_fwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
                     "this build");
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
-        return rollout_fwd_ob<float>(desc, T, state0, ob0, actions, traj, final_state, ob_traj, st);
-    return rollout_fwd_ob<double>(desc, T, state0, ob0, actions, traj, final_state, ob_traj, st);
+        return rollout_fwd_ob<float>(desc, T, state0, ob0, actions, traj, final_state, ob_traj,
+                                     nullptr, 0, st);
+    return rollout_fwd_ob<double>(desc, T, state0, ob0, actions, traj, final_state, ob_traj,
+                                  nullptr, 0, st);
+}
+
+int swarp_ob_tape_bytes(const swarp_desc_t *desc, int32_t T, int32_t n_bodies, uint64_t *bytes)
+{
+    g_err[0] = 0;
+    if (check_desc(desc)) return -1;
+    if (!bytes) return fail("bytes is NULL");
+    if (T < 1) return fail("T must be >= 1");
+    if (n_bodies < 1 || n_bodies > desc->n_obstacles)
+        return fail("n_bodies must lie in [1, n_obstacles]");
+    const uint64_t ts = desc->dtype == SWARP_F32 ? 4 : 8;
+    *bytes = (uint64_t)T * desc->substeps * desc->n_envs * n_bodies * BODY_REC * ts;
+    return 0;
+}
+
+int swarp_rollout_fwd_ob_tape(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                              const void *ob0, const void *actions, const swarp_state_t *traj,
+                              const swarp_state_t *final_state, void *ob_traj, void *tape,
+                              uint64_t tape_bytes, void *stream)
+{
+    g_err[0] = 0;
+    if (check_desc(desc)) return -1;
+    if (T < 1) return fail("T must be >= 1");
+    if (!tape) return fail("tape is NULL");
+    if (desc->has_boxes || desc->wheel_contacts)
+        return fail("box agents and wheel contacts with movable bodies are not supported in "
+                    "this build");
+    hipStream_t st = (hipStream_t)stream;
+    if (desc->dtype == SWARP_F32)
+        return rollout_fwd_ob<float>(desc, T, state0, ob0, actions, traj, final_state, ob_traj,
+                                     tape, tape_bytes, st);
+    return rollout_fwd_ob<double>(desc, T, state0, ob0, actions, traj, final_state, ob_traj,
+                                  tape, tape_bytes, st);
 }
 
 int swarp_rollout_bwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
@@ -650,9 +710,35 @@ int swarp_rollout_bwd_ob(const swarp_desc_t *desc, int32_t T, const swarp_state_
     hipStream_t st = (hipStream_t)stream;
     if (desc->dtype == SWARP_F32)
         return rollout_bwd_ob<float>(desc, T, state0, ob0, actions, traj, ob_traj, adj_traj,
-                                     adj_final, adj_ob_traj, adj_state0, adj_ob0, adj_actions, st);
+                                     adj_final, adj_ob_traj, adj_state0, adj_ob0, adj_actions,
+                                     nullptr, 0, st);
     return rollout_bwd_ob<double>(desc, T, state0, ob0, actions, traj, ob_traj, adj_traj,
-                                  adj_final, adj_ob_traj, adj_state0, adj_ob0, adj_actions, st);
+                                  adj_final, adj_ob_traj, adj_state0, adj_ob0, adj_actions,
+                                  nullptr, 0, st);
+}
+
+int swarp_rollout_bwd_ob_tape(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
+                              const void *ob0, const void *actions, const swarp_state_t *traj,
+                              const void *ob_traj, const swarp_state_t *adj_traj,
+                              const swarp_state_t *adj_final, const void *adj_ob_traj,
+                              const swarp_state_t *adj_state0, void *adj_ob0, void *adj_actions,
+                              const void *tape, uint64_t tape_bytes, void *stream)
+{
+    g_err[0] = 0;
+    if (check_desc(desc)) return -1;
+    if (T < 1) return fail("T must be >= 1");
+    if (!tape) return fail("tape is NULL");
+    if (desc->has_boxes || desc->wheel_contacts)
+        return fail("box agents and wheel contacts with movable bodies are not supported in "
+                    "this build");
+    hipStream_t st = (hipStream_t)stream;
+    if (desc->dtype == SWARP_F32)
+        return rollout_bwd_ob<float>(desc, T, state0, ob0, actions, traj, ob_traj, adj_traj,
+                                     adj_final, adj_ob_traj, adj_state0, adj_ob0, adj_actions,
+                                     tape, tape_bytes, st);
+    return rollout_bwd_ob<double>(desc, T, state0, ob0, actions, traj, ob_traj, adj_traj,
+                                  adj_final, adj_ob_traj, adj_state0, adj_ob0, adj_actions,
+                                  tape, tape_bytes, st);
 }
 
 int swarp_rollout_bwd_ob_check(const swarp_desc_t *desc)

@@ -123,8 +123,9 @@ class Stepper:
         #: generic ones; both give bit-identical results)
         self.use_specialised = True
         #: grad rollouts on the specialised kernels keep a tape of the substep
-        #: intermediates so that the backward does not recompute them (set False to
-        #: recompute; both give bit-identical results)
+        #: intermediates, grad rollouts with movable bodies one of the body pass, so that
+        #: the backward does not recompute them (set False to recompute; both give
+        #: bit-identical results)
         self.use_tape = True
         #: route fleets whose features a compiled profile covers (2-D fleets with
         #: obstacles and walls under Euler, drone fleets, holonomic fleets pushing movable
@@ -152,6 +153,7 @@ class Stepper:
             self._bounds = (0.0, 0.0, 0.0, 0.0)
 
         self.n_obstacles = 0
+        self.n_body_roots = 0
         self._obstacle_types = 0  # bit set of the obstacle shape types present
         self.obstacles: Obstacles | None = None
         self._obs: dict[str, torch.Tensor] = {}
@@ -281,6 +283,12 @@ class Stepper:
         # shape types present (bit t: type t), for the kernel instance without box / segment
         # terms when every obstacle is a circle
         self._obstacle_types = sum(1 << int(t) for t in torch.unique(self._obs["type"].cpu())) if n else 0
+        # movable bodies (roots: body[o] = o and kind[o] = 1), the records of a body tape
+        if n:
+            b, k = body.cpu(), self._obs["kind"].cpu()
+            self.n_body_roots = int(((b == torch.arange(n, dtype=b.dtype)) & (k == 1)).sum())
+        else:
+            self.n_body_roots = 0
         self.ob_state = self._body_seed() if movable else None
         self.ob_trajectory = None
         self._descs.clear()
@@ -412,6 +420,21 @@ class Stepper:
         if n is None:
             c = ctypes.c_uint64(0)
             _lib.check(_lib.load().swarp_tape_bytes(ctypes.byref(d), T, ctypes.byref(c)))
+            n = self._tape_sizes[key] = int(c.value)
+        return n
+
+    def ob_tape_bytes(self, n_envs: int, act_dim: int, T: int) -> int:
+        """Size of the body tape of a T-step grad rollout of a world with movable bodies,
+        holding every movable body (0: no tape is kept)."""
+        if not self.use_tape or not self.any_movable or self.n_body_roots < 1:
+            return 0
+        d = self.desc(n_envs, act_dim)
+        key = (ctypes.addressof(d), T, "ob")
+        n = self._tape_sizes.get(key)
+        if n is None:
+            c = ctypes.c_uint64(0)
+            _lib.check(_lib.load().swarp_ob_tape_bytes(ctypes.byref(d), T, self.n_body_roots,
+                                                       ctypes.byref(c)))
             n = self._tape_sizes[key] = int(c.value)
         return n
 

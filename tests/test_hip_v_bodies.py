@@ -47,13 +47,11 @@ def cross_obs(E, center, d=0.2, r=0.1, mass=1.0, extra=()):
             "mass": np.asarray(m), "inertia": np.asarray(inert)}
 
 
-def run_pair(cfgs, world, dt, S, s0, acts, obs, np_dtype, seed=0):
-    """HIP and oracle rollouts + backward of a random linear loss on the agent trajectory
-    and the obstacle-state trajectory; returns both (states, ob, g_state0, g_ob0, g_act)."""
+def hip_body_run(st, s0, acts, td, seed=0):
+    """HIP rollout + backward of a random linear loss on the agent trajectory and the
+    obstacle-state trajectory: (states, ob, g_state0, g_ob0, g_act), and the loss weights."""
     E, A = s0.shape[:2]
     T = acts.shape[0]
-    td = TDT[np_dtype]
-    st = make_stepper(cfgs, world, dt, S, td, obs=obs, n_envs=E)
     ob0 = st.ob_state.detach().clone().requires_grad_(True)
     st.ob_state = ob0
     rng = np.random.default_rng(seed)
@@ -73,6 +71,16 @@ def run_pair(cfgs, world, dt, S, s0, acts, obs, np_dtype, seed=0):
     hip = (np.stack([state_to16(x) for x in traj]), obtr.detach().double().cpu().numpy(),
            s0t.pos.grad.double().cpu().numpy(), ob0.grad.double().cpu().numpy(),
            a.grad.double().cpu().numpy())
+    return hip, ob0, w_st, w_ob
+
+
+def run_pair(cfgs, world, dt, S, s0, acts, obs, np_dtype, seed=0):
+    """HIP and oracle rollouts + backward of a random linear loss on the agent trajectory
+    and the obstacle-state trajectory; returns both (states, ob, g_state0, g_ob0, g_act)."""
+    E = s0.shape[0]
+    td = TDT[np_dtype]
+    st = make_stepper(cfgs, world, dt, S, td, obs=obs, n_envs=E)
+    hip, ob0, w_st, w_ob = hip_body_run(st, s0, acts, td, seed)
     O = Oracle(np_dtype)
     cfg = oracle_cfg(cfgs, world, dt, S, E, acts.shape[-1], n_threads=8)
     p, t_, m = params_of(cfgs)
@@ -243,6 +251,36 @@ def test_bodies_beyond_sixteen_obstacles(A, n_extra):
     hip, orc = run_pair(nav_agents(A), _world(bounds=2.0), 0.05, 4, s0, acts, obs, np.float32)
     check(f"{5 + n_extra} obstacles", hip, orc)
     assert np.abs(orc[1][-1] - orc[1][0]).max() > 1e-3, "no body moved"
+
+
+@pytest.mark.parametrize("A,n_extra,roots,np_dtype", [
+    (64, 0, None, np.float32),   # config 5's body
+    (16, 19, None, np.float32),  # several movable bodies, four envs per wave
+    (16, 19, 2, np.float32),     # a tape of the first two bodies: the others evaluated
+    (8, 6, None, np.float64),
+])
+def test_body_tape_matches_recompute(A, n_extra, roots, np_dtype):
+    """The backward reading each substep's body pass from the forward's body tape against
+    the backward evaluating it again: the same values reach the same arithmetic in the
+    same order, so states and every gradient are equal bit for bit.  With `roots` the
+    tape holds only the first bodies in root order and the backward evaluates the rest."""
+    E, S = 7, 4
+    s0, acts = _pushers(E, A, 11, spread=1.0)
+    obs = cross_obs(E, (0.0, 0.0), extra=_ring_extra(n_extra, radius=0.6) if n_extra else ())
+    td = TDT[np_dtype]
+    runs = []
+    for tape in (True, False):
+        st = make_stepper(nav_agents(A), _world(), 0.05, S, td, obs=obs, n_envs=E)
+        st.use_tape = tape
+        if tape and roots is not None:
+            assert st.n_body_roots > roots
+            st.n_body_roots = roots
+        assert (st.ob_tape_bytes(E, 2, acts.shape[0]) > 0) == tape
+        runs.append(hip_body_run(st, s0, acts, td, seed=3)[0])
+    names = ("agent states", "obstacle states", "d/d pos0", "d/d ob0", "d/d actions")
+    for name, x, y in zip(names, runs[0], runs[1]):
+        assert np.array_equal(x, y), f"{name} differ between the taped and recomputed backward"
+    assert np.abs(runs[0][4]).max() > 0 and np.abs(runs[0][1][-1] - runs[0][1][0]).max() > 1e-4
 
 
 def test_bodies_few_agents_many_obstacles():
