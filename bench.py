@@ -18,6 +18,11 @@ the timed workload's own inputs for 256 envs, and ``self_check`` records how the
 outputs for those envs (one more iteration after the timed loops) compare with it:
 states bit-exact, gradients within the parity tests' bars; bench.py exits non-zero
 after printing its line when they do not.
+
+``valu_issue`` states the VALU-issue side of the roofline next to the HBM one: the
+dominant kernel's VALU instructions per launch (from the committed counter profile of the
+workload, ``profiles/valu_counts.json``) at one wave64 instruction per CU per cycle, as a
+fraction of its measured duration.
 """
 
 from __future__ import annotations
@@ -48,6 +53,34 @@ def fwd_bytes(A):
 
 def bwd_bytes(A):
     return 4 * A * (3 * S_F + 2 * ACT)
+
+
+def valu_issue(workload, kernels):
+    """VALU-issue fraction of each timed kernel: the VALU instructions one launch issues
+    (SQ_INSTS_VALU of the committed counter profile of this workload, not measured in this
+    run) at one wave64 instruction per CU per cycle, over the kernel's measured duration.
+    Adds `valu_issue_us` / `valu_issue_frac` to each kernel entry; returns the summary
+    object for the dominant kernel (None without a profile)."""
+    prof = ROOT / "profiles" / "valu_counts.json"
+    if not prof.exists():
+        return None
+    vc = json.loads(prof.read_text())
+    w = vc["workloads"].get(workload)
+    if w is None:
+        return None
+    rate = vc["cus"] * vc["clock_ghz"] * 1e9  # wave64 VALU instructions per second
+    for k, kd in kernels.items():
+        if k in w and kd.get("avg_ms"):
+            issue = w[k]["valu_insts"] / rate
+            kd["valu_issue_us"] = issue * 1e6
+            kd["valu_issue_frac"] = issue / (kd["avg_ms"] * 1e-3)
+    dom = max(kernels, key=lambda k: kernels[k]["avg_ms"])
+    if "valu_issue_frac" not in kernels[dom]:
+        return None
+    return {"bound": "valu", "kernel": w[dom]["kernel"], "frac": kernels[dom]["valu_issue_frac"],
+            "achieved_us": kernels[dom]["valu_issue_us"], "measured_us": kernels[dom]["avg_ms"] * 1e3,
+            "source": f"{w['source']}: SQ_INSTS_VALU per launch at {vc['cus']} CUs x "
+                      f"{vc['clock_ghz']} GHz (committed profile, not measured in this run)"}
 
 
 def parse():
@@ -406,6 +439,7 @@ def run_other(args):
                      "traffic": None},
         "fwd_bwd_kernel_roofline_frac": (fwd_b + bwd_b) * E * T / (
             (kernels["fwd"]["avg_ms"] + kernels["bwd"]["avg_ms"]) * 1e-3) / HBM_PEAK,
+        "valu_issue": valu_issue(args.workload, kernels),
         "kernels": kernels,
     }
     print(json.dumps(out), flush=True)
@@ -524,6 +558,7 @@ def main():
         },
         "fwd_bwd_kernel_roofline_frac": fused_frac,
         "fwd_only_env_steps_per_s": fwd_only,
+        "valu_issue": valu_issue("c2", kernels) if (E, A, T, S) == (16000, 16, 32, 4) else None,
         "kernels": kernels,
     }
     if args.env_steps > 0:
