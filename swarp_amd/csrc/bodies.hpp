@@ -518,6 +518,29 @@ template <int PA> __device__ __forceinline__ typename MaskT<PA>::type env_ballot
     return (M)((bal >> base) & full);
 }
 
+// How the body pass reaches the agents of its env.  The narrow kernels put an env on PA
+// lanes of one wave (NarrowEnv); the wide kernels on a workgroup of waves (WideEnv,
+// wide_bodies.hpp).  Every thread of the env calls the pass together:
+//   me()      this thread's agent slot in the env; stride() the env's slots
+//   active()  the slot holds a real agent
+//   ordered<NV>(acc, v, flag)  acc[q] += v[q] of every flagged agent of the env, in
+//             ascending agent order; every thread of the env gets the sums
+//   any(flag) whether a thread of the env (narrow: of the wave) has the flag
+//   sync()    orders the env's LDS writes before its later LDS reads
+template <typename T, int PA> struct NarrowEnv {
+    const Lane<T, PA> &L;
+    __device__ __forceinline__ int me() const { return L.agent; }
+    __device__ __forceinline__ int stride() const { return PA; }
+    __device__ __forceinline__ bool active() const { return L.active; }
+    template <int NV>
+    __device__ __forceinline__ void ordered(T (&acc)[NV], const T (&v)[NV], bool flag) const
+    {
+        env_ordered_sums<PA, NV>(acc, v, flag, L.lane);
+    }
+    __device__ __forceinline__ bool any(bool f) const { return __ballot(f) != 0; }
+    __device__ __forceinline__ void sync() const { wave_lds_sync(); }
+};
+
 // New state of one movable body: the contact sum of body_sum, then the integration of
 // bodies_env (the oracle's restatement of obstacle_dynamics_kernel).
 template <typename T> struct BodyNew {
@@ -581,9 +604,9 @@ __device__ __forceinline__ void body_load(const ObTab<T> &tb, const T *od, const
 // the body (index order): the agents' reactions in agent order, then the contacts with
 // the shapes of other bodies and of the scenery in index order (swarp/core/bodies.py:
 // 423-501).  bm = SS.of(o).
-template <typename T, int PA, bool SM>
+template <typename T, typename X, bool SM>
 __device__ __forceinline__ void body_sum(const Cst<T> &C, const ObTab<T> &tb,
-                                         const ShapeSets<T, SM> &SS, const Lane<T, PA> &L,
+                                         const ShapeSets<T, SM> &SS, const X &L,
                                          const BodyRow<T> &br, const St<T> &st, const T *od,
                                          int o, uint64_t bm, BodyNew<T> &B)
 {
@@ -601,7 +624,7 @@ __device__ __forceinline__ void body_sum(const Cst<T> &C, const ObTab<T> &tb,
         const T bound = shape_bound(ty, ro, hx, hy);
         // the agents' reactions, in agent order
         T f0 = T(0), f1 = T(0), tq = T(0);
-        if (L.active && !b_apart(st.px - csx, st.py - csy, br.r + bound + C.margin)) {
+        if (L.active() && !b_apart(st.px - csx, st.py - csy, br.r + bound + C.margin)) {
             T r0 = T(0), r1 = T(0);
             if (ty == 0) {
                 T gx, gy;
@@ -619,7 +642,7 @@ __device__ __forceinline__ void body_sum(const Cst<T> &C, const ObTab<T> &tb,
         {
             T acc[3] = {fx, fy, tau};
             const T val[3] = {f0, f1, tq};
-            env_ordered_sums<PA, 3>(acc, val, f0 != T(0) || f1 != T(0), L.lane);
+            L.template ordered<3>(acc, val, f0 != T(0) || f1 != T(0));
             fx = acc[0];
             fy = acc[1];
             tau = acc[2];
@@ -694,11 +717,11 @@ __device__ __forceinline__ void body_advance(const Cst<T> &C, const ObTab<T> &tb
 
 // cos / sin of the angle of every movable body root in the obstacle state `od`.  Lane
 // `agent` of the env fills roots agent, agent + PA, ...
-template <typename T, int PA, bool SM>
+template <typename T, typename X, bool SM>
 __device__ __forceinline__ void body_trig(const ObTab<T> &tb, const ShapeSets<T, SM> &SS,
-                                          const Lane<T, PA> &L, const T *od, T *cs)
+                                          const X &L, const T *od, T *cs)
 {
-    for (int o = L.agent; o < tb.N; o += PA) {
+    for (int o = L.me(); o < tb.N; o += L.stride()) {
         if (!SS.is_root(tb, o)) continue;
         T s, c;
         psincos(od[6 * tb.N + 6 * o + 2], s, c);
@@ -710,21 +733,24 @@ __device__ __forceinline__ void body_trig(const ObTab<T> &tb, const ShapeSets<T,
 // The body pass of one env: obn = obc with every movable body advanced and its shapes
 // re-installed at the new pose; cs_out = the new angles' cos / sin (cs_in: the input
 // angles'; both NULL when not kept); sums (nullable) receives each body's contact sum.
-// Lane `agent` of the env copies entries agent, agent+PA..., and re-installs the moved
-// body's shapes agent, agent+PA...  With the whole wave active.  Body-tape records of
+// Slot `me` of the env copies the entries me, me + stride, ... that the pass does not
+// rewrite, and re-installs the moved body's shapes me, me + stride, ...  Body-tape records of
 // this env and substep (BODY_REC entries per body, rstride entries from one body's to
 // the next's, the first `rroots` bodies): `rout` receives them (nullable); with `rin`
 // they are read instead of evaluating those bodies' contact sums and integration.
-template <typename T, int PA, bool SM>
+template <typename T, typename X, bool SM>
 __device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
-                                          const ShapeSets<T, SM> &SS, const Lane<T, PA> &L,
+                                          const ShapeSets<T, SM> &SS, const X &L,
                                           const BodyRow<T> &br, const St<T> &st, const T *obc,
                                           T *obn, const T *ext, const T *cs_in, T *cs_out,
                                           T *sums, const T *rin = nullptr, T *rout = nullptr,
                                           size_t rstride = 0, int rroots = 0)
 {
     const int N = tb.N;
-    for (int q = L.agent; q < OB_W * N; q += PA) obn[q] = obc[q];
+    for (int q = L.me(); q < OB_W * N; q += L.stride()) {
+        const bool rewritten = q < 6 * N ? SS.moves(tb, q / 6) : SS.is_root(tb, (q - 6 * N) / 6);
+        if (!rewritten) obn[q] = obc[q];
+    }
     int r = 0;  // the body's place in root order
     SS.each_root(tb, [&](int o) {
         const uint64_t bm = SS.of(o);
@@ -745,11 +771,11 @@ __device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
         } else {
             body_load(tb, obc, cs_in, o, B);
             B.ext = ext[o];
-            body_sum<T, PA>(C, tb, SS, L, br, st, obc, o, bm, B);
+            body_sum<T>(C, tb, SS, L, br, st, obc, o, bm, B);
             body_advance(C, tb, o, B);
             psincos(B.nth, B.nsa, B.nca);
         }
-        if (rout && r < rroots && L.agent == 0) {
+        if (rout && r < rroots && L.me() == 0) {
             T *rec = rout + (size_t)r * rstride;
             rec[0] = B.nx;
             rec[1] = B.ny;
@@ -765,7 +791,7 @@ __device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
             rec[11] = T(0);
         }
         ++r;
-        if (L.agent == 0) {
+        if (L.me() == 0) {
             T *bo = obn + 6 * N + 6 * o;
             bo[0] = B.nx;
             bo[1] = B.ny;
@@ -783,7 +809,7 @@ __device__ __forceinline__ void body_pass(const Cst<T> &C, const ObTab<T> &tb,
                 sums[3 * o + 2] = B.tau;
             }
         }
-        for (int s = L.agent; s < N; s += PA) {
+        for (int s = L.me(); s < N; s += L.stride()) {
             if (!SS.in_body(tb, o, bm, s)) continue;
             const T offx = tb.off[2 * s], offy = tb.off[2 * s + 1];
             const T owx = B.nca * offx - B.nsa * offy;
@@ -835,6 +861,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
     lane_init<T, PA>(C, g, L);
     ShapeSets<T, !(F & FT_MANYSH)> SS;
     SS.init(tb, L.lane);
+    const NarrowEnv<T, PA> X{L};
     fold_prm<F>(L.pr);
     const BodyRow<T> br = body_row<T, PA>(C, tb, L);
     lr[L.lane] = L.pr.radius;
@@ -847,7 +874,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
     for (int q = L.agent; q < NW; q += PA) obs(0)[q] = io.ob0[eo + q];
     for (int o = L.lane; o < tb.N; o += 64) lext[o] = body_ext(tb, o);
     wave_lds_sync();
-    body_trig<T, PA>(tb, SS, L, obs(0), ocs(0));
+    body_trig<T>(tb, SS, X, obs(0), ocs(0));
     St<T> st;
     load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
     if (!L.active) st.px = st.py = __builtin_nan("");
@@ -876,7 +903,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
             T *rout = io.tape && env_ok ? io.tape + (((size_t)t * C.S + s) * io.tape_roots * C.E +
                                                      L.env) * BODY_REC
                                         : nullptr;
-            body_pass<T, PA>(C, tb, SS, L, br, st, obc, obs(cur ^ 1), lext, ocs(cur), ocs(cur ^ 1),
+            body_pass<T>(C, tb, SS, X, br, st, obc, obs(cur ^ 1), lext, ocs(cur), ocs(cur ^ 1),
                              nullptr, nullptr, rout, (size_t)C.E * BODY_REC, io.tape_roots);
             St<T> nx;
             integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
@@ -939,22 +966,21 @@ __host__ __device__ constexpr size_t body_fwd_lds_total(int PA, int N, size_t ts
 // the forward body_pass of this substep read and wrote: each body's new state is rebuilt
 // from its recorded contact sum, not summed again (NULL cs / sums: recomputed).  Same
 // order of terms as the oracle's bodies_env_adj.
-template <typename T, int PA, bool SM>
+template <typename T, typename X, bool SM>
 __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &tb,
                                               const ShapeSets<T, SM> &SS,
-                                              const Lane<T, PA> &L, const BodyRow<T> &br,
+                                              const X &L, const BodyRow<T> &br,
                                               const St<T> &st, const T *obc, const T *gout,
                                               T *gin, St<T> &ga, const T *ext, const T *cs_in,
                                               const T *cs_out, const T *sums)
 {
-    typedef typename MaskT<PA>::type M;
     const int N = tb.N;
     // pass-through of everything the pass does not rewrite
-    for (int q = L.agent; q < OB_W * N; q += PA) {
+    for (int q = L.me(); q < OB_W * N; q += L.stride()) {
         const int s = q / 6;
         gin[q] = (q < 6 * N && SS.moves(tb, s)) ? T(0) : gout[q];
     }
-    wave_lds_sync();
+    L.sync();
     SS.each_root(tb, [&](int o) {
         const uint64_t bm = SS.of(o);
         BodyNew<T> B;
@@ -965,7 +991,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
             B.fy = sums[3 * o + 1];
             B.tau = sums[3 * o + 2];
         } else {
-            body_sum<T, PA>(C, tb, SS, L, br, st, obc, o, bm, B);
+            body_sum<T>(C, tb, SS, L, br, st, obc, o, bm, B);
         }
         body_advance(C, tb, o, B);
         if (cs_out) {
@@ -1019,7 +1045,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
             // shape centre cs, its velocity vs, and (boxes, segments) the shape's own angle
             // and spin
             T cv[8] = {T(0), T(0), T(0), T(0), T(0), T(0), T(0), T(0)};
-            if (L.active && !b_apart(st.px - csx, st.py - csy, br.r + bound + C.margin)) {
+            if (L.active() && !b_apart(st.px - csx, st.py - csy, br.r + bound + C.margin)) {
                 if (ty == 0) {
                     const T dx = st.px - csx, dy = st.py - csy, rvx = st.vx - vsx,
                             rvy = st.vy - vsy;
@@ -1079,7 +1105,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
                 bool fl = false;
 #pragma unroll
                 for (int q = 0; q < 8; ++q) fl = fl || cv[q] != T(0);
-                env_ordered_sums<PA, 8>(acc, cv, fl, L.lane);
+                L.template ordered<8>(acc, cv, fl);
             }
             T g_owx = acc[0], g_owy = acc[1], g_csx = acc[2], g_csy = acc[3], g_vsx = acc[4],
               g_vsy = acc[5], g_thd = acc[6], g_omd = acc[7];
@@ -1104,7 +1130,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
                     g_owy -= g_tau * f0;
                     const T in[12] = {csx, csy, vsx, vsy, B.th, B.om,
                                       d2[0], d2[1], d2[3], d2[4], d2[2], d2[5]};
-                    const bool mv = SS.moves(tb, o2) && L.agent == 0;
+                    const bool mv = SS.moves(tb, o2) && L.me() == 0;
                     for (int k = 0; k < 12; ++k) {
                         Dual<T, 1> x[12], o0, o1, l0, l1;
 #pragma unroll
@@ -1142,7 +1168,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
                 g_csy += ady;
                 g_vsx += arx;
                 g_vsy += ary;
-                if (SS.moves(tb, o2) && L.agent == 0) {
+                if (SS.moves(tb, o2) && L.me() == 0) {
                     T *g2 = gin + 6 * o2;
                     g2[0] -= adx;
                     g2[1] -= ady;
@@ -1159,7 +1185,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
             g_om += -g_vsx * owy + g_vsy * owx + g_omd;
             g_th += -g_owx * owy + g_owy * owx + g_thd;
         });
-        if (L.agent == 0) {
+        if (L.me() == 0) {
             T *gi = gin + 6 * N + 6 * o;
             gi[0] = g_qx;
             gi[1] = g_qy;
@@ -1168,7 +1194,7 @@ __device__ __forceinline__ void body_pass_adj(const Cst<T> &C, const ObTab<T> &t
             gi[4] = g_tvy;
             gi[5] = g_om;
         }
-        wave_lds_sync();
+        L.sync();
     });
 }
 
@@ -1198,6 +1224,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
     lane_init<T, PA>(C, g, L);
     ShapeSets<T, !(F & FT_MANYSH)> SS;
     SS.init(tb, L.lane);
+    const NarrowEnv<T, PA> X{L};
     fold_prm<F>(L.pr);
     const BodyRow<T> br = body_row<T, PA>(C, tb, L);
     lr[L.lane] = L.pr.radius;
@@ -1230,7 +1257,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             T *dst = lobs + (size_t)ew * NW;
             for (int q = L.agent; q < NW; q += PA) dst[q] = src[q];
             wave_lds_sync();
-            if (lcs) body_trig<T, PA>(tb, SS, L, dst, lcs + (size_t)ew * 2 * N);
+            if (lcs) body_trig<T>(tb, SS, X, dst, lcs + (size_t)ew * 2 * N);
         }
         T a[4];
         load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
@@ -1253,7 +1280,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             const T *rin = io.tape ? io.tape + (((size_t)t * C.S + s) * io.tape_roots * C.E +
                                                 (env_ok ? L.env : 0)) * BODY_REC
                                    : nullptr;
-            body_pass<T, PA>(C, tb, SS, L, br, st, obc, lobs + ((size_t)(s + 1) * EPW + ew) * NW, lext,
+            body_pass<T>(C, tb, SS, X, br, st, obc, lobs + ((size_t)(s + 1) * EPW + ew) * NW, lext,
                              lcs ? lcs + ((size_t)s * EPW + ew) * 2 * N : nullptr,
                              lcs ? lcs + ((size_t)(s + 1) * EPW + ew) * 2 * N : nullptr,
                              lsum ? lsum + ((size_t)s * EPW + ew) * 3 * N : nullptr, rin, nullptr,
@@ -1283,7 +1310,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             T gFx, gFy;
             integrate_adj<T, DRONE>(C, L.pr, in, a, Fx, Fy, gs, gi, ga, gFx, gFy);
             // the body pass: adjoint of its input obstacle state into gprev
-            body_pass_adj<T, PA>(C, tb, SS, L, br, in, obc, gob, gprev, gi, lext,
+            body_pass_adj<T>(C, tb, SS, X, br, in, obc, gob, gprev, gi, lext,
                                  lcs ? lcs + ((size_t)s * EPW + ew) * 2 * N : nullptr,
                                  lcs ? lcs + ((size_t)(s + 1) * EPW + ew) * 2 * N : nullptr,
                                  lsum ? lsum + ((size_t)s * EPW + ew) * 3 * N : nullptr);
