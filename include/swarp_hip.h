@@ -200,12 +200,17 @@ int swarp_rollout_bwd_tape(const swarp_desc_t *desc, int32_t T, const swarp_stat
  * body shapes of any type; the reference runs it on untaped steps,
  * swarp/core/stepper.py:952-991).  Replaces T calls of Stepper.launch_substeps with the
  * body pass enabled.  Fleets of any dynamics models including drones, shared or per-env
- * parameter rows (then desc->body_params), disc agents, at most 64 agents per env, and
- * n_obstacles >= 1 up to what the per-env obstacle staging allows: the forward's and the
- * backward's LDS of one workgroup (dynamic and static) stay within 64 KiB, the env slots
- * widened (fewer envs per wave) as far as one env per wave when needed; at 64 agents, 4
- * substeps and float32 that is 553 obstacles forward and 164 backward.  Beyond it the call
- * fails before any launch (swarp_rollout_bwd_ob_check asks the backward's limit).
+ * parameter rows (then desc->body_params), disc agents, up to 1024 agents per env with
+ * index-ordered or (pinned-frame) uniform-grid lists, and n_obstacles >= 1 up to what the
+ * per-env obstacle staging allows: the forward's and the backward's LDS of one workgroup
+ * (dynamic and static) stay within 64 KiB.  Up to 64 agents per env with index-ordered
+ * lists an env takes a slot of one wave, widened (fewer envs per wave) as far as one env
+ * per wave when needed -- at 64 agents, 4 substeps and float32 that is 553 obstacles
+ * forward and 164 backward; wider envs and grid-ordered lists take a workgroup of
+ * ceil(n_agents / 64) waves, whose agent staging shares the 64 KiB (brute lists, float32:
+ * 346 / 142 obstacles forward / backward at 512 agents, 38 / 15 at 1024).  Beyond it the call fails before any launch
+ * (swarp_rollout_bwd_ob_check asks the backward's limit).  The _tape entry points keep
+ * no body tape on the workgroup-per-env kernels (they accept one and leave it unused).
  * ob0 [E, 12N]: per env and obstacle index o, the shape state (pos x, pos y, angle,
  * vel x, vel y, ang_vel) at [6o..6o+5] and the state of the body rooted at o at
  * [6N+6o..6N+6o+5] (the reference's obs_* and body_* arrays, stepper.py:418-431).

@@ -7,6 +7,7 @@
 #include "nav.hpp"
 #include "neighbors.hpp"
 #include "wide.hpp"
+#include "wide_bodies.hpp"
 
 #define SWARP_EXTERN_LAUNCHERS(T)                                                            \
     extern template void launch_fwd<T, false, false>(int, const Cst<T> &, const Args<T> &,   \
@@ -46,7 +47,11 @@
     extern template void launch_wide_fwd<T>(bool, const Cst<T> &, const Args<T> &,            \
                                             hipStream_t);                                    \
     extern template void launch_wide_bwd<T>(bool, const Cst<T> &, const Args<T> &,            \
-                                            hipStream_t);
+                                            hipStream_t);                                    \
+    extern template void launch_wbody_fwd<T>(bool, const Cst<T> &, const Args<T> &,           \
+                                             const ObTab<T> &, const ObIO<T> &, hipStream_t); \
+    extern template void launch_wbody_bwd<T>(bool, const Cst<T> &, const Args<T> &,           \
+                                             const ObTab<T> &, const ObIO<T> &, hipStream_t);
 
 namespace swarp {
 SWARP_EXTERN_LAUNCHERS(float)

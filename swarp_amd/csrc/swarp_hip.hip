@@ -429,16 +429,32 @@ template <typename T> static int body_pa(const swarp_desc_t *d)
     return PA;
 }
 
+// LDS of the wide body kernels' workgroup (dynamic staging + the static wsum[16]) within
+// 64 KiB; bwd: the backward's (three obstacle states and two adjoints instead of two).
+template <typename T> static int wbody_lds_check(const swarp_desc_t *d, bool bwd)
+{
+    const int NC = d->neighbor_method == SWARP_LISTS_GRID ? d->grid_bins * d->grid_bins : 0;
+    const int AP = ((d->n_agents + 63) / 64) * 64;
+    if (wbody_lds_bytes<T>(AP, NC, d->n_obstacles, bwd) + 16 * sizeof(int32_t) > 65536)
+        return fail(bwd ? "agents and obstacles per env too many for the wide body backward's "
+                          "LDS staging (limit 64 KiB per workgroup)"
+                        : "agents and obstacles per env too many for the wide body forward's "
+                          "LDS staging (limit 64 KiB per workgroup)");
+    return 0;
+}
+
 template <typename T> static int fill_obtab(const swarp_desc_t *d, ObTab<T> &tb)
 {
     if (d->n_obstacles < 1) return fail("the body path takes at least one obstacle per env");
-    if (body_fwd_lds_total(body_pa<T>(d), d->n_obstacles, sizeof(T)) > 65536)
+    if (wide_path(d)) {
+        if (const char *why = wide_unsupported(d)) return fail(why);
+        if (wbody_lds_check<T>(d, false)) return -1;
+    } else if (body_fwd_lds_total(body_pa<T>(d), d->n_obstacles, sizeof(T)) > 65536) {
         return fail("too many obstacles per env for the body forward's LDS staging (limit "
                     "64 KiB per wave)");
+    }
     if (!d->obs_kind || !d->obs_body || !d->obs_mass || !d->obs_inertia || !d->obs_body_off)
         return fail("obs_kind/obs_body/obs_mass/obs_inertia/obs_body_off must be set");
-    if (wide_path(d))
-        return fail("the body path steps at most 64 agents per env with index-ordered lists");
     tb.rad = (decltype(tb.rad))d->obs_radius;
     tb.half = (decltype(tb.half))d->obs_half;
     tb.mass = (decltype(tb.mass))d->obs_mass;
@@ -497,8 +513,15 @@ static int rollout_fwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
         io.tape = (T *)tape;
         io.tape_roots = (int)r;
     }
-    const int PA = body_pa<T>(d);
-    launch_body_fwd<T>(PA, C, a, tb, io, world_features(d, true), d->has_drone != 0, st);
+    if (wide_path(d)) {
+        // the wide kernels keep no body tape (their backward evaluates the pass again)
+        io.tape = nullptr;
+        io.tape_roots = 0;
+        launch_wbody_fwd<T>(d->has_drone != 0, C, a, tb, io, st);
+    } else {
+        launch_body_fwd<T>(body_pa<T>(d), C, a, tb, io, world_features(d, true),
+                           d->has_drone != 0, st);
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
     return 0;
@@ -538,6 +561,15 @@ static int rollout_bwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
         io.tape = (T *)tape;
         io.tape_roots = (int)r;
     }
+    if (wide_path(d)) {
+        if (wbody_lds_check<T>(d, true)) return -1;
+        io.tape = nullptr;
+        io.tape_roots = 0;
+        launch_wbody_bwd<T>(d->has_drone != 0, C, a, tb, io, st);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return fail(hipGetErrorString(e));
+        return 0;
+    }
     const int PA = body_pa<T>(d);
     // the per-substep body caches (cos / sin, contact sums) when they fit
     const bool dr = d->has_drone != 0;
@@ -558,6 +590,7 @@ template <typename T> static int bwd_ob_fits(const swarp_desc_t *d)
 {
     ObTab<T> tb;
     if (fill_obtab<T>(d, tb)) return -1;
+    if (wide_path(d)) return wbody_lds_check<T>(d, true);
     if (body_bwd_lds_of<T>(body_pa<T>(d), d->substeps, d->n_obstacles, d->has_drone != 0, false) >
         65536)
         return fail("obstacle count or substeps too large for the body backward's LDS staging "

@@ -343,11 +343,13 @@ __device__ __forceinline__ void wide_publish(const Cst<T> &C, const WideLds<T> &
 // Contact and static forces of the lane's agent (collision_forces_kernel, swarp/core/
 // collisions.py:818-881: listed pairs in list order, then obstacles, then walls); `cut`
 // receives the key of the K-th listed neighbour (CUT_ALL when the list is not full).
-template <typename T, bool GRID>
-__device__ __forceinline__ void wide_forces(const Cst<T> &C, const Args<T> &g,
-                                            const WideLds<T> &W, const GridFrame<T> &G,
-                                            const WLane<T> &L, const St<T> &st, T &Fx, T &Fy,
-                                            int32_t &cut)
+// `obst(sx, sy)` adds the obstacle forces of an active lane (the static obstacles of
+// `g.obs` in wide_forces; the env's obstacle state in the movable-body kernels).
+template <typename T, bool GRID, typename ObF>
+__device__ __forceinline__ void wide_forces_with(const Cst<T> &C, const WideLds<T> &W,
+                                                 const GridFrame<T> &G, const WLane<T> &L,
+                                                 const St<T> &st, T &Fx, T &Fy, int32_t &cut,
+                                                 ObF &&obst)
 {
     T fx = T(0), fy = T(0);
     cut = CUT_ALL;
@@ -368,15 +370,7 @@ __device__ __forceinline__ void wide_forces(const Cst<T> &C, const Args<T> &g,
         if (n >= C.K) cut = last;
     }
     T sx = T(0), sy = T(0);
-    if (C.N > 0 && L.active) {
-        const size_t eN = (size_t)L.env * C.N;
-        for (int o = 0; o < C.N; ++o) {
-            T gx, gy;
-            obstacle_force(C, g.obs, eN, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv, gx, gy);
-            sx += gx;
-            sy += gy;
-        }
-    }
+    if (L.active) obst(sx, sy);
     if (C.soft_walls) {
         T gx, gy;
         unsigned wb;
@@ -386,6 +380,23 @@ __device__ __forceinline__ void wide_forces(const Cst<T> &C, const Args<T> &g,
     }
     Fx = fx + sx;
     Fy = fy + sy;
+}
+
+template <typename T, bool GRID>
+__device__ __forceinline__ void wide_forces(const Cst<T> &C, const Args<T> &g,
+                                            const WideLds<T> &W, const GridFrame<T> &G,
+                                            const WLane<T> &L, const St<T> &st, T &Fx, T &Fy,
+                                            int32_t &cut)
+{
+    wide_forces_with<T, GRID>(C, W, G, L, st, Fx, Fy, cut, [&](T &sx, T &sy) {
+        const size_t eN = (size_t)L.env * C.N;
+        for (int o = 0; o < C.N; ++o) {
+            T gx, gy;
+            obstacle_force(C, g.obs, eN, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv, gx, gy);
+            sx += gx;
+            sy += gy;
+        }
+    });
 }
 
 template <typename T, bool DRONE, bool GRID>

@@ -269,13 +269,8 @@ class Stepper:
         if n > 0 and bool(((body < 0) | (body >= n)).any()):
             raise ValueError(f"obstacle body indices must lie in [0, {n})")
         movable = obs.any_movable
-        if movable:
-            if self.has_boxes:
-                raise NotImplementedError("movable bodies with box agents are not implemented")
-            if self.wide:
-                raise NotImplementedError(
-                    "movable bodies: this build steps them with at most 64 agents per env and "
-                    "index-ordered lists")
+        if movable and self.has_boxes:
+            raise NotImplementedError("movable bodies with box agents are not implemented")
         self.obstacles = obstacles
         self.n_obstacles = n
         self._obs_envs = n_envs
@@ -426,8 +421,8 @@ class Stepper:
     def ob_tape_bytes(self, n_envs: int, act_dim: int, T: int) -> int:
         """Size of the body tape of a T-step grad rollout of a world with movable bodies,
         holding every movable body (0: no tape is kept)."""
-        if not self.use_tape or not self.any_movable or self.n_body_roots < 1:
-            return 0
+        if not self.use_tape or not self.any_movable or self.n_body_roots < 1 or self.wide:
+            return 0  # (the wide kernels keep no body tape)
         d = self.desc(n_envs, act_dim)
         key = (ctypes.addressof(d), T, "ob")
         n = self._tape_sizes.get(key)

@@ -263,6 +263,10 @@ int main(int argc, char **argv)
         {"holonomic f64 A=5",   11, 5, 4, 3, 4, 2, 0, false, false, true,  false, false, false, 0},
         {"wide f32 A=100",       2, 100, 3, 2, 12, 2, 3, false, false, true,  false, false, false, 1},
         {"wide grid f32 A=70",   2, 70, 3, 2, 8, 2, 0, false, false, true,  false, false, true,  0},
+        {"wide bodies f32 A=100", 2, 100, 3, 2, 12, 2, 5, false, false, true, true, false, false, 0},
+        {"wide bodies grid f32 A=70", 2, 70, 3, 2, 8, 2, 5, false, false, true, true, false, true, 0},
+        {"wide bodies drones f32 A=72", 2, 72, 3, 2, 8, 4, 5, true, false, true, true, false, false, 3},
+        {"wide bodies f64 A=65",  2, 65, 2, 2, 8, 2, 6, false, false, true, true, false, false, 0},
     };
     int bad = 0;
     for (const Case &c : cases) {

@@ -283,6 +283,26 @@ def test_body_tape_matches_recompute(A, n_extra, roots, np_dtype):
     assert np.abs(runs[0][4]).max() > 0 and np.abs(runs[0][1][-1] - runs[0][1][0]).max() > 1e-4
 
 
+@pytest.mark.parametrize("A,E,method,np_dtype", [
+    (128, 4, "brute", np.float32),
+    (512, 2, "brute", np.float32),
+    (100, 3, "uniform_grid", np.float32),
+    (72, 2, "brute", np.float64),
+])
+def test_bodies_wide_envs_match_oracle(A, E, method, np_dtype):
+    """Movable bodies in envs of more than 64 agents, and with grid-ordered lists: the wide
+    kernels (one workgroup of ceil(A / 64) waves per env, the body pass's sums over the
+    env's waves in agent order).  Agent and obstacle states bit-exact with the oracle,
+    gradients within the bars."""
+    s0, acts = _pushers(E, A, 17, spread=1.4)
+    obs = cross_obs(E, (0.0, 0.0), extra=_ring_extra(4, radius=0.7))
+    world = _world(bounds=2.0, neighbor_method=method)
+    hip, orc = run_pair(nav_agents(A), world, 0.05, 4, s0, acts, obs, np_dtype)
+    check(f"{A} agents per env, {method} lists", hip, orc, exact=True,
+          g_tol=1e-5 if np_dtype == np.float32 else 1e-12)
+    assert np.abs(orc[1][-1] - orc[1][0]).max() > 1e-3, "no body moved"
+
+
 def test_bodies_few_agents_many_obstacles():
     """4 agents per env with 13 obstacles: at 16 env slots per wave the backward's obstacle
     staging would exceed 64 KiB of LDS, so the body kernels run wider env slots (pad lanes)."""
