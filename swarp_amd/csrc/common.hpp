@@ -201,52 +201,6 @@ template <int B, int E, typename Fn> __device__ __forceinline__ void static_for(
     }
 }
 
-template <typename T, int PA>
-__device__ __forceinline__ typename MaskT<PA>::type scan_all(const T *lx, const T *ly, int base,
-                                                             int A, int me, T px, T py, T t_nbr,
-                                                             T t_skin,
-                                                             typename MaskT<PA>::type &cand)
-{
-    typedef typename MaskT<PA>::type M;
-    M incl = 0, cd = 0;
-    (void)A;  // pad slots (b >= A) hold NaN positions and never pass the test
-    if constexpr (PA == 64) {
-        // One env per wave, and the env's lanes all run this scan together.  A pair's
-        // squared distance has the same bits from either end (x_b - x_a = -(x_a - x_b)
-        // exactly), so the wave's ballot over agent b's column is agent b's row: it goes
-        // to lane b as a scalar, with no per-lane bit assembly.
-        // (positions read eight at a time, so that one wait covers eight LDS reads)
-        static_for<0, 8>([&](auto cc) {
-            constexpr int b0 = decltype(cc)::value * 8;
-            T qx[8], qy[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                qx[k] = lx[base + b0 + k];
-                qy[k] = ly[base + b0 + k];
-            }
-            static_for<0, 8>([&](auto kc) {
-                constexpr int k = decltype(kc)::value, b = b0 + k;
-                const T dx = qx[k] - px, dy = qy[k] - py;
-                const T d2 = dx * dx + dy * dy;
-                const uint64_t ci = __ballot(d2 <= t_nbr), cs = __ballot(d2 <= t_skin);
-                incl = (M)set_lane64<b>(ci, (uint64_t)incl);
-                cd = (M)set_lane64<b>(cs, (uint64_t)cd);
-            });
-        });
-    } else {
-#pragma unroll
-        for (int b = 0; b < PA; ++b) {
-            T dx = lx[base + b] - px, dy = ly[base + b] - py;
-            T d2 = dx * dx + dy * dy;
-            incl |= d2 <= t_nbr ? (M(1) << b) : M(0);
-            cd |= d2 <= t_skin ? (M(1) << b) : M(0);
-        }
-    }
-    const M self = ~(M(1) << me);
-    cand = cd & self;
-    return incl & self;
-}
-
 // Same membership, evaluated only on the skin candidates.
 template <typename T, int PA>
 __device__ __forceinline__ typename MaskT<PA>::type scan_cand(const T *lx, const T *ly, int base,
@@ -263,6 +217,54 @@ __device__ __forceinline__ typename MaskT<PA>::type scan_cand(const T *lx, const
         incl |= d2 <= t_nbr ? (M(1) << b) : M(0);
     }
     return incl;
+}
+
+template <typename T, int PA>
+__device__ __forceinline__ typename MaskT<PA>::type scan_all(const T *lx, const T *ly, int base,
+                                                             int A, int me, T px, T py, T t_nbr,
+                                                             T t_skin,
+                                                             typename MaskT<PA>::type &cand)
+{
+    typedef typename MaskT<PA>::type M;
+    M incl = 0, cd = 0;
+    (void)A;  // pad slots (b >= A) hold NaN positions and never pass the test
+    if constexpr (PA == 64) {
+        // One env per wave, and the env's lanes all run this scan together.  A pair's
+        // squared distance has the same bits from either end (x_b - x_a = -(x_a - x_b)
+        // exactly), so the wave's ballot over agent b's column is agent b's row: it goes
+        // to lane b as a scalar, with no per-lane bit assembly.  Only the skin mask is
+        // built so; the inclusion mask is the candidates' test (a subset: t_nbr <= t_skin).
+        // (positions read eight at a time, so that one wait covers eight LDS reads)
+        static_for<0, 8>([&](auto cc) {
+            constexpr int b0 = decltype(cc)::value * 8;
+            T qx[8], qy[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                qx[k] = lx[base + b0 + k];
+                qy[k] = ly[base + b0 + k];
+            }
+            static_for<0, 8>([&](auto kc) {
+                constexpr int k = decltype(kc)::value, b = b0 + k;
+                const T dx = qx[k] - px, dy = qy[k] - py;
+                const T d2 = dx * dx + dy * dy;
+                cd = (M)set_lane64<b>(__ballot(d2 <= t_skin), (uint64_t)cd);
+            });
+        });
+        const M self = ~(M(1) << me);
+        cand = cd & self;
+        return t_nbr == t_skin ? cand : scan_cand<T, PA>(lx, ly, base, px, py, t_nbr, cand);
+    } else {
+#pragma unroll
+        for (int b = 0; b < PA; ++b) {
+            T dx = lx[base + b] - px, dy = ly[base + b] - py;
+            T d2 = dx * dx + dy * dy;
+            incl |= d2 <= t_nbr ? (M(1) << b) : M(0);
+            cd |= d2 <= t_skin ? (M(1) << b) : M(0);
+        }
+    }
+    const M self = ~(M(1) << me);
+    cand = cd & self;
+    return incl & self;
 }
 
 // First K members of an inclusion mask (the padded list of length K).
