@@ -428,6 +428,29 @@ __device__ __forceinline__ const T *ob_trig_table(const Cst<T> &C, const Args<T>
     return ocs + 2 * ew * C.N;
 }
 
+// This env's obstacle poses and bounding radii (OPOSE_W scalars per obstacle, see
+// obstacle_in_reach) staged once per launch under ob_trig_table's condition, and before
+// it: its barrier publishes both.  NULL when they do not fit.
+template <typename T, int PA>
+__device__ __forceinline__ const T *ob_pose_table(const Cst<T> &C, const Args<T> &g,
+                                                  const Lane<T, PA> &L, T *opos)
+{
+    if (C.N <= 0 || (64 / PA) * C.N > OCS_MAX) return nullptr;
+    const int ew = L.lane / PA;
+    const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
+    T *dst = opos + OPOSE_W * ew * C.N;
+    for (int q = L.agent; q < C.N; q += PA) {
+        const size_t j = eN + q;
+        dst[OPOSE_W * q] = g.obs.pos[2 * j];
+        dst[OPOSE_W * q + 1] = g.obs.pos[2 * j + 1];
+        dst[OPOSE_W * q + 2] = g.obs.vel[2 * j];
+        dst[OPOSE_W * q + 3] = g.obs.vel[2 * j + 1];
+        dst[OPOSE_W * q + 4] = g.obs.om[j];
+        dst[OPOSE_W * q + 5] = ob_bound(g.obs, q);
+    }
+    return dst;
+}
+
 // Box worlds (BOXES; false compiles the box paths out): `lbx` holds per lane the
 // footprint (shape, hx, hy rows of 64), `lcs` the cos and sin of every lane's heading
 // (rows of 64), and the slot `sl` also carries the headings and spins (F_TH, F_W rows).

@@ -121,11 +121,15 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
     __shared__ T lr[64];      // agent radius per lane
     __shared__ T lso[2 * 64]; // the obstacle wave's sums: x row, y row
     __shared__ T ocs_lds[2 * OCS_MAX];
+    // the env slots' obstacle poses and bounds (the launcher runs this kernel only when
+    // the per-launch obstacle tables fit)
+    __shared__ T opos_lds[OPOSE_W * OCS_MAX];
     const bool agent_wave = threadIdx.x < 64;
     Lane<T, PA> L;
     lane_init<T, PA>(C, g, L, (int)(threadIdx.x & 63));
     fold_prm<F>(L.pr);
     if (agent_wave) lr[L.lane] = L.pr.radius;
+    const T *opos = ob_pose_table<T, PA>(C, g, L, opos_lds);
     const T *ocs = ob_trig_table<T, PA>(C, g, L, ocs_lds);
     const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
     St<T> st;
@@ -155,8 +159,8 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
                 T sx = T(0), sy = T(0);
                 for (int o = 0; o < C.N; ++o) {
                     T gx, gy;
-                    obstacle_force(C, g.obs, eN, o, px, py, vx, vy, L.pr.radius, L.ddv, gx, gy,
-                                   ocs);
+                    obstacle_force<T, Dv<T>, true>(C, g.obs, eN, o, px, py, vx, vy, L.pr.radius,
+                                                   L.ddv, gx, gy, ocs, opos);
                     sx += gx;
                     sy += gy;
                 }
@@ -540,8 +544,9 @@ void launch_fwd(int PA, const Cst<T> &C, const Args<T> &a, unsigned feat, hipStr
     const dim3 grid4((C.E + 15) / 16), grid8((C.E + 7) / 8), grid16((C.E + 3) / 4),
         grid32((C.E + 1) / 2), grid64(C.E);
     constexpr unsigned P = family_profile<T, DRONE, BOXES>();
-    if (!DRONE && !BOXES && P != 0u && (feat & ~P) == 0u && (feat & FT_OBST) && C.N > 0) {
-        // static obstacles: the obstacle pass on a wave of its own
+    if (!DRONE && !BOXES && P != 0u && (feat & ~P) == 0u && (feat & FT_OBST) && C.N > 0 &&
+        (64 / PA) * C.N <= OCS_MAX) {
+        // static obstacles (whose per-launch tables fit): the obstacle pass on a wave of its own
         constexpr unsigned PS = P ? P : FT_ALL;
         switch (PA) {
         case 4: hipLaunchKernelGGL((k_rollout_fwd_split<T, 4, PS>), grid4, dim3(128), 0, st, C, a); break;

@@ -792,15 +792,26 @@ __device__ __forceinline__ void ob_trig(const Obs<T> &O, size_t j, int o, const 
 // :62-70 and bounds_apart :74-84): whether obstacle o's bounding disc comes within reach
 // of an agent of radius ra at (px, py).  A NaN position is in reach (the comparison that
 // would cull it fails), so a NaN state still propagates through the contact code.
-template <typename T>
-__device__ __forceinline__ bool obstacle_in_reach(const Cst<T> &C, const Obs<T> &O, size_t eN,
-                                                  int o, T px, T py, T ra)
+// PT: the env's obstacle poses and bounding radii come from a per-launch table `pose`
+// (OPOSE_W scalars per obstacle index: pos x, pos y, vel x, vel y, ang_vel, the bound
+// below), the same values read once per launch.
+constexpr int OPOSE_W = 8;
+
+template <typename T> __device__ __forceinline__ T ob_bound(const Obs<T> &O, int o)
 {
-    const size_t j = eN + o;
-    const T cx = O.pos[2 * j], cy = O.pos[2 * j + 1];
     const int st = O.type[o];
     const T ro = O.rad[o], hx = O.half[2 * o], hy = O.half[2 * o + 1];
-    T bound = st == 1 ? m_sqrt(hx * hx + hy * hy) : (st == 2 ? hx + ro : ro);
+    return st == 1 ? m_sqrt(hx * hx + hy * hy) : (st == 2 ? hx + ro : ro);
+}
+
+template <typename T, bool PT = false>
+__device__ __forceinline__ bool obstacle_in_reach(const Cst<T> &C, const Obs<T> &O, size_t eN,
+                                                  int o, T px, T py, T ra, const T *pose = nullptr)
+{
+    const size_t j = eN + o;
+    const T cx = PT ? pose[OPOSE_W * o] : O.pos[2 * j];
+    const T cy = PT ? pose[OPOSE_W * o + 1] : O.pos[2 * j + 1];
+    T bound = PT ? pose[OPOSE_W * o + 5] : ob_bound(O, o);
     T lim = (ra + C.margin + bound) * T(1.0001) + T(1.0e-6);
     T ddx = px - cx, ddy = py - cy;
     return !(ddx * ddx + ddy * ddy > lim * lim);
@@ -811,19 +822,22 @@ __device__ __forceinline__ bool obstacle_in_reach(const Cst<T> &C, const Obs<T> 
 // (the angles do not change within one), or NULL to evaluate them here.
 // DD: the damping denominator as a plain value or as a prepared divisor (Dv<T>, the
 // exact fast arithmetic of the force overloads that take one); the same bits either way.
-template <typename T, typename DD>
+template <typename T, typename DD, bool PT = false>
 __device__ __forceinline__ void obstacle_force(const Cst<T> &C, const Obs<T> &O, size_t eN, int o,
                                                T px, T py, T vx, T vy, T ra, const DD &dd, T &fx,
-                                               T &fy, const T *cs = nullptr)
+                                               T &fy, const T *cs = nullptr,
+                                               const T *pose = nullptr)
 {
     fx = T(0);
     fy = T(0);
-    if (!obstacle_in_reach(C, O, eN, o, px, py, ra)) return;
+    if (!obstacle_in_reach<T, PT>(C, O, eN, o, px, py, ra, pose)) return;
     const size_t j = eN + o;
-    const T cx = O.pos[2 * j], cy = O.pos[2 * j + 1];
+    const T *pp = pose + OPOSE_W * o;
+    const T cx = PT ? pp[0] : O.pos[2 * j], cy = PT ? pp[1] : O.pos[2 * j + 1];
     const int st = O.type[o];
     const T ro = O.rad[o], hx = O.half[2 * o], hy = O.half[2 * o + 1];
-    const T vox = O.vel[2 * j], voy = O.vel[2 * j + 1], om = O.om[j];
+    const T vox = PT ? pp[2] : O.vel[2 * j], voy = PT ? pp[3] : O.vel[2 * j + 1];
+    const T om = PT ? pp[4] : O.om[j];
     if (st == 1) {
         T ca, sa;
         ob_trig(O, j, o, cs, ca, sa);
