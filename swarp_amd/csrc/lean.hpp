@@ -128,6 +128,18 @@ __device__ __forceinline__ uint32_t skin_dpp16(float px, float py, float t, uint
     return __builtin_amdgcn_ubfe(r | (r << 16), rot, 16u);
 }
 
+// Issue priority of a wave from the number of its lanes with contact or wall work in a
+// step: a launch ends with its slowest waves, the ones whose envs are crowded, so such a
+// wave issues ahead of the lighter waves sharing its SIMD (which have time to spare).
+// s_setprio orders instruction issue between waves only; no result depends on it.
+__device__ __forceinline__ void busy_priority(int busy_lanes)
+{
+    if (busy_lanes >= 24) __builtin_amdgcn_s_setprio(3);
+    else if (busy_lanes >= 16) __builtin_amdgcn_s_setprio(2);
+    else if (busy_lanes >= 8) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+}
+
 // One substep of the force pass: neighbour lists (into `incl`) and the total force.
 // Also records which listed contacts are active (`act`) and the wall contact bits, the
 // branches the reverse pass follows.  SAT: contact_max_overlap > 0 (the tanh law).
@@ -339,6 +351,8 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
                 }
                 lean_forces<T, PA, SAT>(C, lp, lv, lr, base, me, ra, ddv, p.x, p.y, v.x, v.y,
                                         s == 0 || !ok, s == 0, cand, incl, act, wb, Fx, Fy);
+                // this step's work: the lanes with skin candidates or a wall contact
+                if (s == 0) busy_priority(__builtin_popcountll(__ballot(cand != 0 || wb != 0u)));
             }
             const T vnx = cnx + Fx * dtm, vny = cny + Fy * dtm;
             const T pnx = p.x + vnx * dt, pny = p.y + vny * dt;
@@ -508,6 +522,15 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
         T cnx, cny;
         clamp_norm(a.x, a.y, vmax, cnx, cny);
         const P2<T> vin = v;
+        if (TAPE) {
+            // this step's work: the lanes on which a contact or wall force acted
+            bool busy = false;
+#pragma unroll
+            for (int s = 0; s < TAPE_MAX_S; ++s)
+                if (s < S)
+                    busy = busy || vel_stored<PA>(rec_get<W>(tc.c, TR::OM + s * (int)sizeof(W)), me);
+            busy_priority(__builtin_popcountll(__ballot(busy)));
+        }
 
         // ---- the substeps of step t into LDS: from the tape, or recomputed
         if (TAPE) {

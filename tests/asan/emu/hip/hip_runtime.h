@@ -255,6 +255,8 @@ struct alignas(16) int4 {
 inline int4 make_int4(int x, int y, int z, int w) { return int4{x, y, z, w}; }
 inline uint64_t __builtin_amdgcn_read_exec() { emu_not_emulated("read_exec"); }
 inline int __builtin_amdgcn_readfirstlane(int x) { return __builtin_amdgcn_readlane(x, 0); }
+// issue priority between waves: nothing to order on the host
+inline void __builtin_amdgcn_s_setprio(int) {}
 
 inline unsigned __builtin_amdgcn_mbcnt_lo(unsigned, unsigned) { emu_not_emulated("mbcnt"); }
 inline unsigned __builtin_amdgcn_mbcnt_hi(unsigned, unsigned) { emu_not_emulated("mbcnt"); }
