@@ -174,9 +174,13 @@ int swarp_rollout_bwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *
  * the taped substep buffers the reference keeps alive for wp.Tape.backward
  * (StepBuffers / make_buffers, swarp/core/stepper.py:55-63, 642-678).
  * Writes in *bytes the tape size of a T-step rollout of this configuration; 0 when the
- * configuration keeps no tape (only fleets on the specialised holonomic-velocity kernels
- * with substeps <= 4 and contacts or walls do), in which case the _tape entry points
- * behave as the plain ones. */
+ * configuration keeps no tape, in which case the _tape entry points behave as the plain
+ * ones.  Two kinds of configuration keep one: fleets on the specialised holonomic-velocity
+ * kernels with substeps <= 4 and contacts or walls (the records above), and float32 2-D
+ * fleets among static obstacles whose forward runs the obstacle pass on a wave of its own
+ * (at most 256 / (envs per 64 lanes) obstacles, no box agents, wheel contacts or drones):
+ * there the tape holds each substep's per-agent obstacle force sum, 8 T S E A bytes
+ * (rounded up to 256), which the backward reads instead of evaluating the obstacles. */
 int swarp_tape_bytes(const swarp_desc_t *desc, int32_t T, uint64_t *bytes);
 
 /* swarp_rollout_fwd that also writes the tape (`tape_bytes` must be

@@ -60,6 +60,10 @@ template <typename T> struct Args {
     Fields<T> a0;        // adjoint of s0 (nullable per field)
     T *aact;             // adjoint of actions
     int nsteps;
+    // Obstacle-sum tape (nullable): per step, substep and agent the sum of the static
+    // obstacles' forces, [T][S][E A] pairs -- written by the two-wave forward, read by the
+    // backward's recompute in place of evaluating the obstacles again.
+    T *osum;
 };
 
 __device__ __forceinline__ int fstride(int k)
@@ -463,7 +467,7 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
     const St<T> &st, int s, bool full, typename MaskT<PA>::type &cand, T &Fx, T &Fy,
     const T *ocs = nullptr, const T *lbx = nullptr, const T *lcs = nullptr,
     typename MaskT<PA>::type *act = nullptr, uint64_t *om = nullptr, bool *wall = nullptr,
-    bool *beyond = nullptr, T *tq = nullptr)
+    bool *beyond = nullptr, T *tq = nullptr, const T *osum = nullptr)
 {
     const bool box_me = BOXES && L.pr.shape > T(0.5);
     T me[6] = {st.px, st.py, st.th, st.vx, st.vy, st.w};
@@ -522,6 +526,10 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
                                 om, wall, beyond);
         if (wheel)
             tau = tau + box_static_torque(C, g.obs, eN, ocs, L.pr.hx, L.pr.hy, me, cme, sme, L.dd);
+    } else if (osum) {
+        // the obstacles' sum as the forward recorded it (the same bits)
+        sx = osum[0];
+        sy = osum[1];
     } else if (C.N > 0) {
         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
         for (int o = 0; o < C.N; ++o) {

@@ -166,6 +166,11 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
                 }
                 lso[L.lane] = sx;
                 lso[64 + L.lane] = sy;
+                if (g.osum && L.active) {
+                    T *const o2 = g.osum + 2 * (((size_t)t * C.S + s) * EA + L.idx);
+                    o2[0] = sx;
+                    o2[1] = sy;
+                }
             }
             T fx = T(0), fy = T(0), wx = T(0), wy = T(0);
             M incl = 0;
@@ -417,8 +422,11 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> Cin, const Args
                 M am = 0;
                 uint64_t om = 0;
                 bool wl = false, far = false;
+                const T *osum =
+                    !BOXES && g.osum ? g.osum + 2 * (((size_t)t * C.S + s) * EA + L.idx) : nullptr;
                 incl = forces<T, PA, BOXES>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy,
-                                            ocs, lbx, lcsb + s * 128, &am, &om, &wl, &far);
+                                            ocs, lbx, lcsb + s * 128, &am, &om, &wl, &far, nullptr,
+                                            osum);
                 if (BOXES) {
                     lact[s * 64 + L.lane] = am;
                     lom[s * 64 + L.lane] = om;

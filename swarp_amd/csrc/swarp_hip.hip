@@ -261,9 +261,12 @@ static bool lean_ok(const swarp_desc_t *d)
            !d->params_per_env;
 }
 
-// Byte offsets of the tape regions (see lean.hpp); total == 0: no tape.
+// Byte offsets of the tape regions (see lean.hpp); total == 0: no tape.  The specialised
+// holonomic kernels keep records (rec) and last velocities (vl); the two-wave forward of
+// 2-D fleets among static obstacles keeps each substep's obstacle force sums (osum, read
+// by the backward's recompute), alone.
 struct TapeLayout {
-    uint64_t rec, vl, total;
+    uint64_t rec, vl, osum, total;
 };
 
 static uint64_t align256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
@@ -279,9 +282,25 @@ template <typename T> static uint64_t tape_rec_bytes(int PA)
     }
 }
 
+// Whether rollout_fwd runs the two-wave forward (launch_fwd's condition for it).
+static bool split_ok(const swarp_desc_t *d)
+{
+    if (wide_path(d) || lean_ok(d) || d->has_drone || d->has_boxes || d->wheel_contacts)
+        return false;
+    if (d->dtype != SWARP_F32 || d->n_obstacles <= 0) return false;
+    const unsigned feat = world_features(d, false);
+    if ((feat & ~FT_PROF_2D) != 0u || !(feat & FT_OBST)) return false;
+    return (64 / pad_agents(d->n_agents)) * d->n_obstacles <= OCS_MAX;
+}
+
 static TapeLayout tape_layout(const swarp_desc_t *d, int32_t nT)
 {
-    TapeLayout L = {0, 0, 0};
+    TapeLayout L = {0, 0, 0, 0};
+    if (nT >= 1 && split_ok(d)) {
+        L.osum = 0;
+        L.total = align256((uint64_t)nT * d->substeps * d->n_envs * d->n_agents * 2 * sizeof(float));
+        return L;
+    }
     const bool forces = d->collisions || d->soft_walls;
     if (!lean_ok(d) || !forces || d->substeps > TAPE_MAX_S || nT < 1) return L;
     const bool f32 = d->dtype == SWARP_F32;
@@ -326,6 +345,7 @@ static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     if (nT > 1) copy_fields<T>(traj, a.traj.f);
     a.act = (const T *)act;
     a.nsteps = nT;
+    if (tape && TL.total && split_ok(d)) a.osum = (T *)((unsigned char *)tape + TL.osum);
     const int PA = pad_agents(d->n_agents);
     const unsigned feat = world_features(d, false);
     if (wide_path(d)) {
@@ -373,6 +393,7 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     a.act = (const T *)act;
     a.aact = (T *)aact;
     a.nsteps = nT;
+    if (tape && TL.total && split_ok(d)) a.osum = (T *)((unsigned char *)tape + TL.osum);
     const int PA = pad_agents(d->n_agents);
     if (wide_path(d)) {
         if (const char *why = wide_unsupported(d)) return fail(why);

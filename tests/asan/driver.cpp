@@ -226,6 +226,19 @@ int run_case(const Case &c)
         rc = swarp_rollout_bwd(&d, nT, &s0, act, nT > 1 ? &traj : nullptr, nullptr, &afin2, &a0,
                                aact, nullptr);
         if (rc) return fprintf(stderr, "%s bwd (sparse adjoints): %s\n", c.name, swarp_last_error()), 1;
+        // the taped pair, where the configuration keeps a tape
+        uint64_t tb = 0;
+        rc = swarp_tape_bytes(&d, nT, &tb);
+        if (rc) return fprintf(stderr, "%s tape_bytes: %s\n", c.name, swarp_last_error()), 1;
+        if (tb) {
+            void *tape = make<unsigned char>(tb, own);
+            rc = swarp_rollout_fwd_tape(&d, nT, &s0, act, nT > 1 ? &traj : nullptr, &fin, tape, tb,
+                                        nullptr);
+            if (rc) return fprintf(stderr, "%s fwd_tape: %s\n", c.name, swarp_last_error()), 1;
+            rc = swarp_rollout_bwd_tape(&d, nT, &s0, act, nT > 1 ? &traj : nullptr,
+                                        nT > 1 ? &atr : nullptr, &afin, &a0, aact, tape, tb, nullptr);
+            if (rc) return fprintf(stderr, "%s bwd_tape: %s\n", c.name, swarp_last_error()), 1;
+        }
     }
     // neighbour lists of the initial state
     int32_t *idx = make<int32_t>(EA * c.K, own), *cnt = make<int32_t>(EA, own), *tru = make<int32_t>(EA, own);

@@ -101,3 +101,63 @@ def test_no_tape_beyond_four_substeps():
     assert st.tape_bytes(E, 2, T) == 0
     states, g0, ga = hip_run(st, s0, acts, w, np.float32)
     assert np.isfinite(ga).all() and np.isfinite(g0).all()
+
+
+def _obstacle_world(E, A, n, seed):
+    """A mixed 2-D fleet (diff-drive + bicycle) among n static obstacles of every shape."""
+    from swarp_amd.config import AgentConfig, DynamicsModel
+    rng = np.random.default_rng(seed)
+    cfgs = [AgentConfig(model=DynamicsModel.DIFF_DRIVE, radius=0.05) for _ in range(A // 2)] + [
+        AgentConfig(model=DynamicsModel.KINEMATIC_BICYCLE, radius=0.05)
+        for _ in range(A - A // 2)]
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.025,
+                        bounds=(-1.0, 1.0, -1.0, 1.0), max_neighbors=32)
+    ty = np.arange(n) % 3
+    obs = {"pos": rng.uniform(-1, 1, size=(E, n, 2)),
+           "radius": np.where(ty == 0, rng.uniform(0.05, 0.2, n), np.where(ty == 2, 0.05, 0.0)),
+           "type": ty.astype(np.int32),
+           "angle": rng.uniform(-np.pi, np.pi, size=(E, n)),
+           "half": np.where((ty == 1)[:, None], rng.uniform(0.05, 0.3, size=(n, 2)),
+                            np.where((ty == 2)[:, None],
+                                     np.c_[rng.uniform(0.1, 0.4, n), np.zeros(n)], 0.0))}
+    s0 = pack_state({"pos": rng.uniform(-1, 1, size=(E, A, 2)),
+                     "theta": rng.uniform(-np.pi, np.pi, size=(E, A))}).astype(np.float32)
+    return cfgs, world, obs, s0, rng
+
+
+@pytest.mark.parametrize("E,A,T,S,n", [
+    (300, 32, 8, 4, 8),     # config-3 shape: two envs per workgroup
+    (41, 8, 6, 3, 12),      # eight envs per workgroup, partial last one, S = 3
+    (17, 64, 5, 2, 30),     # one env per workgroup, many obstacles
+    (23, 4, 4, 1, 16),      # sixteen envs per workgroup at the table's limit, S = 1
+])
+def test_obstacle_sum_tape_matches_recompute(E, A, T, S, n):
+    """Static obstacles: the forward keeps each substep's obstacle force sums and the
+    backward reads them instead of evaluating the obstacles again -- bit-identical."""
+    cfgs, world, obs, s0, rng = _obstacle_world(E, A, n, seed=E + n)
+    on = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
+    off = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
+    off.use_tape = False
+    assert on.tape_bytes(E, 2, T) == 2 * 4 * T * S * E * A + (-(2 * 4 * T * S * E * A) % 256)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
+    w = rng.normal(size=(T, E, A, 16)) * 0.1
+    w[..., 7:] = 0.0
+    a = hip_run(on, s0, acts, w, np.float32)
+    b = hip_run(off, s0, acts, w, np.float32)
+    assert np.array_equal(a[0][..., :7], b[0][..., :7]), "forward states differ"
+    assert np.array_equal(a[2], b[2]), "d/d actions differ"
+    assert np.array_equal(a[1][..., :7], b[1][..., :7]), "d/d state0 differ"
+
+
+def test_no_obstacle_tape_beyond_the_pose_table():
+    """Seventeen obstacles at four agents per env overflow the forward's per-launch
+    obstacle table (16 envs x 17 > 256 entries): no tape, and the rollout still runs."""
+    E, A, T, S, n = 20, 4, 3, 2, 17
+    cfgs, world, obs, s0, rng = _obstacle_world(E, A, n, seed=1)
+    st = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
+    assert st.tape_bytes(E, 2, T) == 0
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
+    w = rng.normal(size=(T, E, A, 16)) * 0.1
+    w[..., 7:] = 0.0
+    states, g0, ga = hip_run(st, s0, acts, w, np.float32)
+    assert np.isfinite(ga).all() and np.isfinite(g0).all()
