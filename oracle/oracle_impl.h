@@ -2022,7 +2022,7 @@ static void FN(step_env)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_
             memcpy(obn, obc, sizeof(REAL) * nob);
         if (C->wheel) {
             /* contact torques, the unclamped step, wheel_contact, then the clamp */
-            REAL tq[64];
+            REAL *tq = (REAL *)malloc(sizeof(REAL) * (size_t)A);
             FN(ctx_t) C2 = *C;
             C2.clamp_bounds = 0;
             if (C->needs_forces && C->collisions + C->n_obs + C->soft_walls > 0)
@@ -2034,6 +2034,7 @@ static void FN(step_env)(const FN(ctx_t) *C, const FN(prm_t) *P, const FN(agent_
                 FN(wheel_contact)(C, P + a, cur + a, F[a * 2], F[a * 2 + 1], tq[a], nxt + a);
                 if (C->clamp_bounds) FN(clamp_position)(C, P + a, nxt[a].th, &nxt[a].px, &nxt[a].py);
             }
+            free(tq);
         } else {
             for (int a = 0; a < A; ++a)
                 FN(integrate_agent)(C, P + a, cur + a, act + a * ad, F[a * 2], F[a * 2 + 1], nxt + a);

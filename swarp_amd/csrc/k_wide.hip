@@ -7,8 +7,8 @@ template void launch_wide_lists<SWARP_T>(const Cst<SWARP_T> &, const SWARP_T *, 
                                          int32_t *, int32_t *, int32_t *, hipStream_t);
 template void launch_grid_frame<SWARP_T>(const SWARP_T *, int64_t, SWARP_T, int, SWARP_T *,
                                          hipStream_t);
-template void launch_wide_fwd<SWARP_T>(bool, const Cst<SWARP_T> &, const Args<SWARP_T> &,
+template void launch_wide_fwd<SWARP_T>(bool, bool, const Cst<SWARP_T> &, const Args<SWARP_T> &,
                                        hipStream_t);
-template void launch_wide_bwd<SWARP_T>(bool, const Cst<SWARP_T> &, const Args<SWARP_T> &,
+template void launch_wide_bwd<SWARP_T>(bool, bool, const Cst<SWARP_T> &, const Args<SWARP_T> &,
                                        hipStream_t);
 }  // namespace swarp

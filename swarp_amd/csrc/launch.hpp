@@ -44,9 +44,9 @@
     extern template void launch_wide_lists<T>(const Cst<T> &, const T *, const T *, int32_t *,\
                                               int32_t *, int32_t *, hipStream_t);            \
     extern template void launch_grid_frame<T>(const T *, int64_t, T, int, T *, hipStream_t);  \
-    extern template void launch_wide_fwd<T>(bool, const Cst<T> &, const Args<T> &,            \
+    extern template void launch_wide_fwd<T>(bool, bool, const Cst<T> &, const Args<T> &,      \
                                             hipStream_t);                                    \
-    extern template void launch_wide_bwd<T>(bool, const Cst<T> &, const Args<T> &,            \
+    extern template void launch_wide_bwd<T>(bool, bool, const Cst<T> &, const Args<T> &,      \
                                             hipStream_t);                                    \
     extern template void launch_wbody_fwd<T>(bool, const Cst<T> &, const Args<T> &,           \
                                              const ObTab<T> &, const ObIO<T> &, hipStream_t); \

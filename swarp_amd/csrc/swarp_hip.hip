@@ -237,20 +237,26 @@ static bool wide_path(const swarp_desc_t *d)
 // What the wide-env kernels do not step, as an error message (NULL: they step it).
 static const char *wide_unsupported(const swarp_desc_t *d)
 {
-    if (d->has_boxes) return "box agents step with at most 64 agents per env and index-ordered lists";
-    if (d->wheel_contacts) return "wheel contacts step with at most 64 agents per env and index-ordered lists";
     if (d->neighbor_method == SWARP_LISTS_GRID && d->collisions && !d->grid_pinned)
         return "stepping with uniform-grid lists needs the grid frame pinned by the world bounds "
                "(an adaptive frame reduces over every env at every substep)";
     return nullptr;
 }
 
-template <typename T> static int wide_lds_check(const swarp_desc_t *d)
+// lists_only: the list builder's staging (no box fields).
+template <typename T> static int wide_lds_check(const swarp_desc_t *d, bool lists_only = false)
 {
     const int NC = d->neighbor_method == SWARP_LISTS_GRID ? d->grid_bins * d->grid_bins : 0;
-    // dynamic staging + k_wide_lists' static wsum[16]: the workgroup's whole LDS
-    if (wide_lds_bytes<T>(((d->n_agents + 63) / 64) * 64, NC) + 16 * sizeof(int32_t) > 65536)
+    const int AP = ((d->n_agents + 63) / 64) * 64;
+    // dynamic staging + the kernels' static wsum[16]: the workgroup's whole LDS; box worlds
+    // also stage headings, spins and footprints
+    if (!lists_only && (d->has_boxes || d->wheel_contacts)) {
+        if (wide_box_lds_bytes<T>(AP, NC) + 16 * sizeof(int32_t) > 65536)
+            return fail("n_agents too large for the wide-env LDS staging of a box world at this "
+                        "dtype (limit 64 KiB)");
+    } else if (wide_lds_bytes<T>(AP, NC) + 16 * sizeof(int32_t) > 65536) {
         return fail("n_agents too large for the wide-env LDS staging at this dtype (limit 64 KiB)");
+    }
     return 0;
 }
 
@@ -351,7 +357,7 @@ static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     if (wide_path(d)) {
         if (const char *why = wide_unsupported(d)) return fail(why);
         if (wide_lds_check<T>(d)) return -1;
-        launch_wide_fwd<T>(d->has_drone != 0, C, a, st);
+        launch_wide_fwd<T>(d->has_drone != 0, d->has_boxes || d->wheel_contacts, C, a, st);
     } else if (lean_ok(d)) {
         if (tape && TL.total)
             launch_holo_fwd<T, true>(PA, C, a, tape_ptrs<T>(TL, tape), st);
@@ -398,7 +404,7 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     if (wide_path(d)) {
         if (const char *why = wide_unsupported(d)) return fail(why);
         if (wide_lds_check<T>(d)) return -1;
-        launch_wide_bwd<T>(d->has_drone != 0, C, a, st);
+        launch_wide_bwd<T>(d->has_drone != 0, d->has_boxes != 0, C, a, st);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return fail(hipGetErrorString(e));
         return 0;
@@ -895,7 +901,7 @@ int swarp_neighbors(const swarp_desc_t *desc, const void *pos, int32_t *idx, int
     const bool adaptive = desc->neighbor_method == SWARP_LISTS_GRID && !desc->grid_pinned;
     if (adaptive && !desc->grid_frame) return fail("grid_frame must be set for an adaptive grid frame");
     if (desc->dtype == SWARP_F32) {
-        if (wide_path(desc) && wide_lds_check<float>(desc)) return -1;
+        if (wide_path(desc) && wide_lds_check<float>(desc, true)) return -1;
         Cst<float> C;
         fill_cst<float>(desc, 0.0, C);
         if (wide_path(desc)) {
@@ -908,7 +914,7 @@ int swarp_neighbors(const swarp_desc_t *desc, const void *pos, int32_t *idx, int
             launch_neighbors<float>(PA, C, (const float *)pos, idx, cnt, true_cnt, st);
         }
     } else {
-        if (wide_path(desc) && wide_lds_check<double>(desc)) return -1;
+        if (wide_path(desc) && wide_lds_check<double>(desc, true)) return -1;
         Cst<double> C;
         fill_cst<double>(desc, 0.0, C);
         if (wide_path(desc)) {

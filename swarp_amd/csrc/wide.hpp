@@ -26,6 +26,13 @@
 // The backward recomputes, for each substep in reverse, the substeps before it from the
 // step's checkpoint (S (S + 1) / 2 forward substeps per step): no per-substep state of
 // the env has to fit in LDS.
+//
+// Box worlds (BOXES: some agent is a box, or wheel contacts) also stage each agent's
+// heading, spin and heading cos / sin per substep and its footprint per launch (WBoxLds):
+// a pair with a box takes the box law, a box agent its obstacles and walls through the
+// box statics, as the one-wave kernels do; their reverse evaluates each listed box pair
+// (both sides, as for discs) and a box agent's statics with the forward-mode tangents of
+// box_item_adj / box_static_adj.
 #pragma once
 #include "common.hpp"
 
@@ -81,6 +88,37 @@ template <typename T> __device__ __forceinline__ WideLds<T> wide_lds(unsigned ch
     W.sorted = q + 3 * AP;
     W.cstart = q + 4 * AP;
     return W;
+}
+
+// Box worlds: each agent's heading, spin and heading cos / sin this substep and its
+// footprint (shape, half-extents), after the staging above (16-byte aligned).
+template <typename T> struct WBoxLds {
+    T *th, *w, *cs, *sn, *shp, *hx, *hy;
+};
+
+template <typename T> __host__ __device__ inline size_t wide_box_offset(int AP, int NC)
+{
+    return (wide_lds_bytes<T>(AP, NC) + 15) / 16 * 16;
+}
+
+template <typename T> __host__ __device__ inline size_t wide_box_lds_bytes(int AP, int NC)
+{
+    return wide_box_offset<T>(AP, NC) + (size_t)7 * AP * sizeof(T);
+}
+
+template <typename T>
+__device__ __forceinline__ WBoxLds<T> wide_box_lds(unsigned char *smem, int AP, int NC)
+{
+    T *b = (T *)(smem + wide_box_offset<T>(AP, NC));
+    WBoxLds<T> B;
+    B.th = b;
+    B.w = b + AP;
+    B.cs = b + 2 * AP;
+    B.sn = b + 3 * AP;
+    B.shp = b + 4 * AP;
+    B.hx = b + 5 * AP;
+    B.hy = b + 6 * AP;
+    return B;
 }
 
 // Exclusive prefix sum of v[0 .. n) in place over the workgroup; v[n] = the total.
@@ -325,17 +363,25 @@ __device__ __forceinline__ void wide_init(const Cst<T> &C, const Args<T> &g, WLa
     L.ddv = divisor(L.dd, true);
 }
 
-// Publishes the substep's positions and velocities (and the grid) -- every thread.
+// Publishes the substep's positions and velocities (and the grid) -- every thread.  `B`
+// (box worlds, else NULL): also the headings, spins and heading cos / sin.
 template <typename T, bool GRID>
 __device__ __forceinline__ void wide_publish(const Cst<T> &C, const WideLds<T> &W,
                                              const GridFrame<T> &G, const WLane<T> &L,
-                                             const St<T> &st, int32_t *wsum)
+                                             const St<T> &st, int32_t *wsum,
+                                             const WBoxLds<T> *B = nullptr)
 {
     __syncthreads();
     W.px[L.i] = st.px;
     W.py[L.i] = st.py;
     W.vx[L.i] = st.vx;
     W.vy[L.i] = st.vy;
+    if (B) {
+        B->th[L.i] = st.th;
+        B->w[L.i] = st.w;
+        B->cs[L.i] = m_cos(st.th);
+        B->sn[L.i] = m_sin(st.th);
+    }
     __syncthreads();
     if (GRID && C.collisions) grid_build(W, C.A, G, wsum);
 }
@@ -399,41 +445,151 @@ __device__ __forceinline__ void wide_forces(const Cst<T> &C, const Args<T> &g,
     });
 }
 
-template <typename T, bool DRONE, bool GRID>
-__device__ __forceinline__ void wide_substep(const Cst<T> &C, const Args<T> &g,
-                                             const WideLds<T> &W, const GridFrame<T> &G,
-                                             const WLane<T> &L, const T (&a)[4], St<T> &st,
-                                             int32_t *wsum)
+// The forces of a box world (collision_forces_box_kernel, swarp/core/collisions.py:
+// 999-1059; the order of forces(): listed pairs, then a box agent's statics -- obstacles
+// then walls, _static_forces_shaped :950-996 -- or a disc's obstacles and walls).  A pair
+// with a box takes the box law with the lower index as box A.  `tq` (nullable): the
+// contact torque about the agent's centre (wheel contacts, :1128-1403).
+template <typename T, bool GRID>
+__device__ __forceinline__ void wide_forces_box(const Cst<T> &C, const Args<T> &g,
+                                                const WideLds<T> &W, const WBoxLds<T> &B,
+                                                const GridFrame<T> &G, const WLane<T> &L,
+                                                const St<T> &st, T &Fx, T &Fy, int32_t &cut,
+                                                T *tq)
 {
-    T Fx = T(0), Fy = T(0);
+    const bool box_me = L.pr.shape > T(0.5);
+    const T cme = m_cos(st.th), sme = m_sin(st.th);
+    const T me[6] = {st.px, st.py, st.th, st.vx, st.vy, st.w};
+    const Foot<T> fa = {L.pr.shape, L.pr.radius, L.pr.hx, L.pr.hy};
+    T fx = T(0), fy = T(0), tau = T(0);
+    cut = CUT_ALL;
+    if (C.collisions && L.active) {
+        int n = 0;
+        int32_t last = CUT_ALL;
+        visit_list<T, GRID>(W, C.A, G, L.i, st.px, st.py, C.t_nbr, C.K, false,
+                            [&](int j, int32_t key) {
+                                T gx, gy;
+                                if (box_me || B.shp[j] > T(0.5)) {
+                                    const Foot<T> fb = {B.shp[j], W.rad[j], B.hx[j], B.hy[j]};
+                                    const T ob[6] = {W.px[j], W.py[j], B.th[j],
+                                                     W.vx[j], W.vy[j], B.w[j]};
+                                    agent_pair_force_box<T, T>(C, L.i, j, fa, me, cme, sme, fb,
+                                                               ob, B.cs[j], B.sn[j], L.dd, gx,
+                                                               gy);
+                                    if (tq)
+                                        tau += pair_torque(C, L.i, j, fa, me, cme, sme, fb, ob,
+                                                           B.cs[j], B.sn[j], gx, gy);
+                                } else {
+                                    pair_force(C, st.px - W.px[j], st.py - W.py[j],
+                                               st.vx - W.vx[j], st.vy - W.vy[j],
+                                               L.pr.radius + W.rad[j] + C.margin, L.ddv, gx, gy);
+                                }
+                                fx += gx;
+                                fy += gy;
+                                last = key;
+                                ++n;
+                            });
+        if (n >= C.K) cut = last;
+    }
+    T sx = T(0), sy = T(0);
+    if (L.active) {
+        const size_t eN = (size_t)L.env * C.N;
+        if (box_me) {
+            box_static_forces<T, T>(C, g.obs, eN, nullptr, L.pr.hx, L.pr.hy, me, cme, sme, L.dd,
+                                    sx, sy);
+            if (tq)
+                tau = tau + box_static_torque(C, g.obs, eN, (const T *)nullptr, L.pr.hx, L.pr.hy,
+                                              me, cme, sme, L.dd);
+        } else {
+            for (int o = 0; o < C.N; ++o) {
+                T gx, gy;
+                obstacle_force(C, g.obs, eN, o, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv,
+                               gx, gy);
+                sx += gx;
+                sy += gy;
+            }
+        }
+    }
+    if (C.soft_walls && !box_me) {
+        T gx, gy;
+        unsigned wb;
+        wall_force_axes(C, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv, gx, gy, wb);
+        sx += gx;
+        sy += gy;
+    }
+    Fx = fx + sx;
+    Fy = fy + sy;
+    if (tq) *tq = tau;
+}
+
+// One substep.  Box worlds with wheel contacts integrate unclamped, rework the step with
+// wheel_contact, then clamp (integrate2d_wheel_kernel, swarp/dynamics/kernels.py:1389-1478).
+template <typename T, bool DRONE, bool GRID, bool BOXES>
+__device__ __forceinline__ void wide_substep(const Cst<T> &C, const Args<T> &g,
+                                             const WideLds<T> &W, const WBoxLds<T> &B,
+                                             const GridFrame<T> &G, const WLane<T> &L,
+                                             const T (&a)[4], St<T> &st, int32_t *wsum)
+{
+    T Fx = T(0), Fy = T(0), Tq = T(0);
     if (C.needs_forces) {
-        if (C.collisions) wide_publish<T, GRID>(C, W, G, L, st, wsum);
+        if (C.collisions) wide_publish<T, GRID>(C, W, G, L, st, wsum, BOXES ? &B : nullptr);
         int32_t cut;
-        wide_forces<T, GRID>(C, g, W, G, L, st, Fx, Fy, cut);
+        if constexpr (BOXES)
+            wide_forces_box<T, GRID>(C, g, W, B, G, L, st, Fx, Fy, cut, C.wheel ? &Tq : nullptr);
+        else
+            wide_forces<T, GRID>(C, g, W, G, L, st, Fx, Fy, cut);
     }
     St<T> nx;
+    if constexpr (BOXES) {
+        if (C.wheel) {
+            Cst<T> C0 = C;
+            C0.clamp = 0;
+            integrate<T, DRONE>(C0, L.pr, st, a, Fx, Fy, nx);
+            wheel_contact(C, L.pr, st, Fx, Fy, Tq, nx);
+            if (C.clamp) clamp_position(C, L.pr, nx.th, nx.px, nx.py);
+            st = nx;
+            return;
+        }
+    }
     integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
     st = nx;
 }
 
-template <typename T, bool DRONE, bool GRID, unsigned F>
+// Footprints of a box world's agents, once per launch.
+template <typename T>
+__device__ __forceinline__ void wide_box_init(const WBoxLds<T> &B, const WLane<T> &L)
+{
+    B.shp[L.i] = L.pr.shape;
+    B.hx[L.i] = L.pr.hx;
+    B.hy[L.i] = L.pr.hy;
+}
+
+template <typename T> __device__ __forceinline__ int wide_cells(const Cst<T> &C)
+{
+    return C.grid_bins > 0 ? C.grid_bins * C.grid_bins : 0;
+}
+
+template <typename T, bool DRONE, bool GRID, bool BOXES, unsigned F>
 __global__ __launch_bounds__(1024) void k_wide_fwd(const Cst<T> Cin, const Args<T> g)
 {
     const Cst<T> C = fold_cst<F>(Cin);
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int32_t wsum[16];
     const WideLds<T> W = wide_lds<T>(smem, blockDim.x);
+    const WBoxLds<T> B = wide_box_lds<T>(smem, blockDim.x, wide_cells(C));
     const GridFrame<T> G = grid_frame(C, (const T *)nullptr);
     WLane<T> L;
     wide_init<T, F>(C, g, L);
     W.rad[L.i] = L.pr.radius;
+    if (BOXES) wide_box_init(B, L);
     St<T> st;
     load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
     const size_t EA = (size_t)C.E * C.A;
     for (int t = 0; t < g.nsteps; ++t) {
         T a[4];
         load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
-        for (int s = 0; s < C.S; ++s) wide_substep<T, DRONE, GRID>(C, g, W, G, L, a, st, wsum);
+        for (int s = 0; s < C.S; ++s)
+            wide_substep<T, DRONE, GRID, BOXES>(C, g, W, B, G, L, a, st, wsum);
         if (L.active) {
             if (t + 1 < g.nsteps)
                 store_state<T, DRONE>(g.traj.f, (size_t)t * EA + L.idx, st);
@@ -443,17 +599,21 @@ __global__ __launch_bounds__(1024) void k_wide_fwd(const Cst<T> Cin, const Args<
     }
 }
 
-template <typename T, bool DRONE, bool GRID, unsigned F>
+template <typename T, bool DRONE, bool GRID, bool BOXES, unsigned F>
 __global__ __launch_bounds__(1024) void k_wide_bwd(const Cst<T> Cin, const Args<T> g)
 {
     const Cst<T> C = fold_cst<F>(Cin);
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int32_t wsum[16];
     const WideLds<T> W = wide_lds<T>(smem, blockDim.x);
+    const WBoxLds<T> B = wide_box_lds<T>(smem, blockDim.x, wide_cells(C));
     const GridFrame<T> G = grid_frame(C, (const T *)nullptr);
     WLane<T> L;
     wide_init<T, F>(C, g, L);
     W.rad[L.i] = L.pr.radius;
+    if (BOXES) wide_box_init(B, L);
+    const bool box_me = BOXES && L.pr.shape > T(0.5);
+    const Foot<T> fa = {L.pr.shape, L.pr.radius, L.pr.hx, L.pr.hy};
     const size_t EA = (size_t)C.E * C.A;
     St<T> gs;
     st_zero(gs);
@@ -475,12 +635,16 @@ __global__ __launch_bounds__(1024) void k_wide_bwd(const Cst<T> Cin, const Args<
         for (int s = C.S - 1; s >= 0; --s) {
             // the substep's input, recomputed from the step's checkpoint
             St<T> in = st0;
-            for (int q = 0; q < s; ++q) wide_substep<T, DRONE, GRID>(C, g, W, G, L, a, in, wsum);
+            for (int q = 0; q < s; ++q)
+                wide_substep<T, DRONE, GRID, BOXES>(C, g, W, B, G, L, a, in, wsum);
             T Fx = T(0), Fy = T(0);
             int32_t cut = CUT_ALL;
             if (C.needs_forces) {
-                if (C.collisions) wide_publish<T, GRID>(C, W, G, L, in, wsum);
-                wide_forces<T, GRID>(C, g, W, G, L, in, Fx, Fy, cut);
+                if (C.collisions) wide_publish<T, GRID>(C, W, G, L, in, wsum, BOXES ? &B : nullptr);
+                if constexpr (BOXES)
+                    wide_forces_box<T, GRID>(C, g, W, B, G, L, in, Fx, Fy, cut, nullptr);
+                else
+                    wide_forces<T, GRID>(C, g, W, G, L, in, Fx, Fy, cut);
             }
             St<T> gi;
             T gFx, gFy;
@@ -503,6 +667,19 @@ __global__ __launch_bounds__(1024) void k_wide_bwd(const Cst<T> Cin, const Args<
                                 if (!own && !rev) return;
                                 const T wx = (own ? wFx : T(0)) - (rev ? W.wfx[j] : T(0));
                                 const T wy = (own ? wFy : T(0)) - (rev ? W.wfy[j] : T(0));
+                                if constexpr (BOXES) {
+                                    if (box_me || B.shp[j] > T(0.5)) {
+                                        // one box contact seen from both sides; a contact
+                                        // that exerts no force has zero derivatives
+                                        const Foot<T> fb = {B.shp[j], W.rad[j], B.hx[j], B.hy[j]};
+                                        const T ob[6] = {W.px[j], W.py[j], B.th[j],
+                                                         W.vx[j], W.vy[j], B.w[j]};
+                                        box_item_adj(C, g.obs, (size_t)0, (const T *)nullptr,
+                                                     BI_PAIR, L.i, fa, in, j, fb, ob, B.cs[j],
+                                                     B.sn[j], 0, T(1), wx, wy, gi);
+                                        return;
+                                    }
+                                }
                                 pair_adj_combined(C, in.px - W.px[j], in.py - W.py[j],
                                                   in.vx - W.vx[j], in.vy - W.vy[j],
                                                   L.pr.radius + W.rad[j] + C.margin, wx, wy,
@@ -510,7 +687,16 @@ __global__ __launch_bounds__(1024) void k_wide_bwd(const Cst<T> Cin, const Args<
                             });
                     }
                 }
-                if (L.active) {
+                bool statics_done = false;
+                if constexpr (BOXES) {
+                    if (L.active && box_me) {
+                        // a box agent's obstacles and walls
+                        box_static_adj(C, g.obs, (size_t)L.env * C.N, (const T *)nullptr, fa,
+                                       in, L.dd, gFx, gFy, gi);
+                        statics_done = true;
+                    }
+                }
+                if (L.active && !statics_done) {
                     if (C.N > 0) {
                         const size_t eN = (size_t)L.env * C.N;
                         for (int o = 0; o < C.N; ++o)
@@ -536,9 +722,10 @@ __global__ __launch_bounds__(1024) void k_wide_bwd(const Cst<T> Cin, const Args<
 
 template <typename T> inline int wide_threads(int A) { return ((A + 63) / 64) * 64; }
 
-template <typename T> size_t wide_shm(const Cst<T> &C)
+template <typename T> size_t wide_shm(const Cst<T> &C, bool boxes = false)
 {
-    return wide_lds_bytes<T>(wide_threads<T>(C.A), C.grid_bins > 0 ? C.grid_bins * C.grid_bins : 0);
+    const int AP = wide_threads<T>(C.A), NC = C.grid_bins > 0 ? C.grid_bins * C.grid_bins : 0;
+    return boxes ? wide_box_lds_bytes<T>(AP, NC) : wide_lds_bytes<T>(AP, NC);
 }
 
 template <typename T>
@@ -559,27 +746,33 @@ void launch_grid_frame(const T *pos, int64_t n, T radius, int bins, T *frame, hi
     hipLaunchKernelGGL((k_grid_frame<T>), dim3(1), dim3(1024), 0, st, pos, n, radius, bins, frame);
 }
 
-#define SWARP_WIDE_DISPATCH(KERNEL)                                                            \
-    if (drone) {                                                                               \
-        if (grid) hipLaunchKernelGGL((KERNEL<T, true, true, FT_ALL>), g, b, shm, st, C, a);    \
-        else hipLaunchKernelGGL((KERNEL<T, true, false, FT_ALL>), g, b, shm, st, C, a);        \
-    } else {                                                                                   \
-        if (grid) hipLaunchKernelGGL((KERNEL<T, false, true, FT_ALL>), g, b, shm, st, C, a);   \
-        else hipLaunchKernelGGL((KERNEL<T, false, false, FT_ALL>), g, b, shm, st, C, a);       \
+// boxes: a box world (box agents or wheel contacts; never with drones).
+#define SWARP_WIDE_DISPATCH(KERNEL)                                                                   \
+    if (drone) {                                                                                      \
+        if (grid) hipLaunchKernelGGL((KERNEL<T, true, true, false, FT_ALL>), g, b, shm, st, C, a);    \
+        else hipLaunchKernelGGL((KERNEL<T, true, false, false, FT_ALL>), g, b, shm, st, C, a);        \
+    } else if (boxes) {                                                                               \
+        if (grid) hipLaunchKernelGGL((KERNEL<T, false, true, true, FT_ALL>), g, b, shm, st, C, a);    \
+        else hipLaunchKernelGGL((KERNEL<T, false, false, true, FT_ALL>), g, b, shm, st, C, a);        \
+    } else {                                                                                          \
+        if (grid) hipLaunchKernelGGL((KERNEL<T, false, true, false, FT_ALL>), g, b, shm, st, C, a);   \
+        else hipLaunchKernelGGL((KERNEL<T, false, false, false, FT_ALL>), g, b, shm, st, C, a);       \
     }
 
-template <typename T> void launch_wide_fwd(bool drone, const Cst<T> &C, const Args<T> &a, hipStream_t st)
+template <typename T>
+void launch_wide_fwd(bool drone, bool boxes, const Cst<T> &C, const Args<T> &a, hipStream_t st)
 {
     const dim3 g(C.E), b(wide_threads<T>(C.A));
-    const size_t shm = wide_shm<T>(C);
+    const size_t shm = wide_shm<T>(C, boxes);
     const bool grid = C.grid_bins > 0;
     SWARP_WIDE_DISPATCH(k_wide_fwd)
 }
 
-template <typename T> void launch_wide_bwd(bool drone, const Cst<T> &C, const Args<T> &a, hipStream_t st)
+template <typename T>
+void launch_wide_bwd(bool drone, bool boxes, const Cst<T> &C, const Args<T> &a, hipStream_t st)
 {
     const dim3 g(C.E), b(wide_threads<T>(C.A));
-    const size_t shm = wide_shm<T>(C);
+    const size_t shm = wide_shm<T>(C, boxes);
     const bool grid = C.grid_bins > 0;
     SWARP_WIDE_DISPATCH(k_wide_bwd)
 }

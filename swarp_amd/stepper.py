@@ -179,12 +179,6 @@ class Stepper:
         # envs over 64 agents, or grid-ordered lists, step on the wide-env kernels
         self.wide = self.n_agents > 64 or self.list_method == "uniform_grid"
         if self.wide:
-            if any(c.shape == AgentShape.BOX for c in self.configs):
-                raise NotImplementedError(
-                    "box agents step with at most 64 agents per env and index-ordered lists")
-            if w.wheel_contacts:
-                raise NotImplementedError(
-                    "wheel contacts step with at most 64 agents per env and index-ordered lists")
             if self.list_method == "uniform_grid" and w.collisions and w.bounds is None:
                 raise NotImplementedError(
                     "stepping with uniform-grid lists needs WorldConfig.bounds: the adaptive "

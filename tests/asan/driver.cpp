@@ -53,6 +53,7 @@ struct Case {
     bool shaped = false;   // movable bodies of box and segment shapes too
     bool fleet = false;    // fleet model / mode bit sets filled in (the profile instances,
                            // and for 2-D fleets among obstacles the two-wave forward)
+    bool wheel = false;    // wheel contacts (forward only)
 };
 
 template <typename T>
@@ -74,6 +75,11 @@ int run_case(const Case &c)
     d.soft_walls = c.walls ? 1 : 0;
     d.has_drone = c.drone ? 1 : 0;
     d.has_boxes = c.boxes ? 1 : 0;
+    if (c.wheel) {
+        d.wheel_contacts = 1;
+        d.lat_grip = 2.94;
+        d.turn_cap = 0.02;
+    }
     d.dt = 0.05;
     d.k = 100.0;
     d.c = 1.0;
@@ -211,6 +217,9 @@ int run_case(const Case &c)
         rc = swarp_rollout_bwd_ob(&d, nT, &s0, ob0, act, nT > 1 ? &traj : nullptr, obt,
                                   nT > 1 ? &atr : nullptr, &afin, aobt, &a0, aob0, aact, nullptr);
         if (rc) return fprintf(stderr, "%s bwd_ob: %s\n", c.name, swarp_last_error()), 1;
+    } else if (c.wheel) {
+        rc = swarp_rollout_fwd(&d, nT, &s0, act, nT > 1 ? &traj : nullptr, &fin, nullptr);
+        if (rc) return fprintf(stderr, "%s fwd: %s\n", c.name, swarp_last_error()), 1;
     } else {
         rc = swarp_rollout_fwd(&d, nT, &s0, act, nT > 1 ? &traj : nullptr, &fin, nullptr);
         if (rc) return fprintf(stderr, "%s fwd: %s\n", c.name, swarp_last_error()), 1;
@@ -280,6 +289,11 @@ int main(int argc, char **argv)
         {"wide bodies grid f32 A=70", 2, 70, 3, 2, 8, 2, 5, false, false, true, true, false, true, 0},
         {"wide bodies drones f32 A=72", 2, 72, 3, 2, 8, 4, 5, true, false, true, true, false, false, 3},
         {"wide bodies f64 A=65",  2, 65, 2, 2, 8, 2, 6, false, false, true, true, false, false, 0},
+        {"wide boxes f32 A=100",  2, 100, 3, 2, 12, 2, 3, false, true, true, false, false, false, 1},
+        {"wide boxes grid f32 A=70", 2, 70, 3, 2, 8, 2, 3, false, true, true, false, false, true, 1},
+        {"wide boxes f64 A=66",   2, 66, 2, 2, 8, 2, 2, false, true, true, false, false, false, 1},
+        {"wide wheel f32 A=72",   2, 72, 3, 2, 8, 2, 3, false, true, true, false, false, false, 1,
+         false, false, false, true},
     };
     int bad = 0;
     for (const Case &c : cases) {

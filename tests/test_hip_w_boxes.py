@@ -144,6 +144,37 @@ def test_sixty_four_box_agents():
     _check_box("64 boxes", cfgs, world, S, s0, acts, w)
 
 
+
+def test_wide_env_box_fleet():
+    """80 agents per env (the wide-env kernels: one workgroup per env): discs, diff-drive
+    boxes and bicycle boxes among circle, box and capsule obstacles inside soft walls."""
+    E, A, T, S = 5, 80, 5, 2
+    rng = np.random.default_rng(36)
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02,
+                        bounds=(-0.9, 0.9, -0.9, 0.9), max_neighbors=10)
+    s0 = _state(E, A, rng, 0.8, np.float64)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2))
+    w = _cotangent(T, E, A, 7, scale=0.1)
+    obs = _obstacles(E, rng)
+    obs["pos"] = obs["pos"] * 1.6
+    _check_box("wide boxes A=80", _fleet(A), world, S, s0, acts, w, obs=obs, E=E)
+
+
+def test_grid_ordered_box_fleet():
+    """Box agents with uniform-grid lists (pinned frame), capped at 4 neighbours so the
+    grid's traversal order decides which contacts act; footprint clamp."""
+    E, A, T, S = 6, 36, 5, 2
+    rng = np.random.default_rng(37)
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02,
+                        bounds=(-0.5, 0.5, -0.5, 0.5), bounds_mode="clamp", max_neighbors=4,
+                        neighbor_method="uniform_grid", uniform_bins=6)
+    s0 = _state(E, A, rng, 0.45, np.float64)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2))
+    w = _cotangent(T, E, A, 8, scale=0.1)
+    st = make_stepper(_fleet(A), world, 0.05, S, torch.float64)
+    assert st.wide and st.list_method == "uniform_grid"
+    _check_box("grid boxes A=36", _fleet(A), world, S, s0, acts, w)
+
 def test_wheel_contacts_forward_and_no_reverse():
     """WorldConfig.wheel_contacts: contact torques (pair torques at the manifold point or
     the disc's nearest point, obstacle and wall torques) and wheel_contact's rework of the
@@ -190,6 +221,40 @@ def test_wheel_contacts_forward_and_no_reverse():
     with pytest.raises(ValueError, match="wheel_contacts"):
         rollout(st, state, torch.zeros(T, E, A, 2, device="cuda", requires_grad=True))
 
+
+
+def test_wheel_contacts_wide_env():
+    """Wheel contacts (forward only) in envs of 72 agents on the wide-env kernels: states
+    within 1e-10 of the fp64 oracle and 1e-5 of the fp32 one."""
+    from hip_helpers import state_to16, to_torch_state
+    from oracle.oracle import Oracle
+    from cases import obstacles_np, oracle_cfg, params_of
+    from swarp_amd import rollout
+
+    E, A, T, S = 4, 72, 5, 2
+    rng = np.random.default_rng(38)
+    cfgs = ([AgentConfig(radius=0.05, max_speed=2.0, max_accel=4.0) for _ in range(24)]
+            + [_box(0.07, 0.04, DynamicsModel.DIFF_DRIVE, ctrl_mode=ControlMode.ACCELERATION)
+               for _ in range(48)])
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02,
+                        bounds=(-0.8, 0.8, -0.8, 0.8), max_neighbors=8, wheel_contacts=True,
+                        wheel_lateral_friction=0.3, wheel_turn_torque=0.02)
+    obs = _obstacles(E, rng)
+    s0 = _state(E, A, rng, 0.7, np.float64)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2))
+    for dt_np, td, tol in ((np.float64, torch.float64, 1e-10), (np.float32, torch.float32, 1e-5)):
+        st = make_stepper(cfgs, world, 0.05, S, td, obs=obs, n_envs=E)
+        assert st.wide
+        state = to_torch_state(s0.astype(dt_np), td, False, 5)
+        with torch.no_grad():
+            _, traj = rollout(st, state, torch.tensor(acts.astype(dt_np), dtype=td, device="cuda"))
+        hs = np.stack([state_to16(x) for x in traj])
+        cfg = oracle_cfg(cfgs, world, 0.05, S, E, 2)
+        p, t, m = params_of(cfgs)
+        os_ = Oracle(dt_np).rollout(cfg, p, t, m, obstacles_np(obs, E), s0.astype(dt_np),
+                                    acts.astype(dt_np))
+        assert np.isfinite(hs).all()
+        assert rel(hs[..., :7], os_[..., :7]) <= tol, f"{np.dtype(dt_np).name} states"
 
 def test_wheel_contacts_disc_diff_drive():
     """Disc diff-drive agents (velocity and servo control) under wheel_contacts: no

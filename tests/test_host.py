@@ -313,8 +313,9 @@ def test_list_method_resolution_and_grid_frame():
     assert Stepper([AgentConfig() for _ in range(100)], device="cpu").desc(2, 2).neighbor_method == 0
     with pytest.raises(NotImplementedError, match="bounds"):
         Stepper([AgentConfig(radius=0.02) for _ in range(600)], device="cpu", world=WorldConfig())
-    with pytest.raises(NotImplementedError, match="box agents"):
-        Stepper([AgentConfig(shape="box", half_extents=(0.02, 0.02)) for _ in range(70)], device="cpu")
+    # box worlds too (box agents, wheel contacts): the wide kernels' box pass
+    wb = Stepper([AgentConfig(shape="box", half_extents=(0.02, 0.02)) for _ in range(70)], device="cpu")
+    assert wb.wide and wb.desc(2, 2).has_boxes == 1
 
 
 def test_step_refuses_cpu_tensors():
