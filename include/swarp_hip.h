@@ -99,8 +99,8 @@ typedef struct swarp_desc {
     int32_t fleet_models, fleet_modes;
     /* Neighbour-list order (NeighborGrid's method, swarp/core/neighbors.py:387-389):
        SWARP_LISTS_BRUTE ascending agent index (_brute_force, :76-97); SWARP_LISTS_GRID the
-       uniform grid's (_query_uniform, :214-251) over grid_bins x grid_bins cells (at most
-       64 x 64).  grid_pinned = 1: the frame is grid_origin / grid_cell (the world
+       uniform grid's (_query_uniform, :214-251) over grid_bins x grid_bins cells (their
+       table in LDS beside the env's agents, see below).  grid_pinned = 1: the frame is grid_origin / grid_cell (the world
        rectangle's, NeighborGrid._fill_static_grid :476-490, as the reference computes
        them in float64; rounded to dtype here); 0: swarp_neighbors reduces it over the
        batch (:149-181) into grid_frame, a caller-owned device buffer of 3 scalars of
@@ -124,10 +124,11 @@ typedef struct swarp_desc {
 #define SWARP_LISTS_GRID 1
 /* Agents per env: up to 64 on every path; up to SWARP_WIDE_MAX_AGENTS on the wide-env
    path (one workgroup per env), which steps 2-D and drone fleets with any model,
-   control mode, obstacles, walls, clamp and integrator, box agents and wheel contacts
-   (up to 896 agents per env in float32, 448 in float64, with brute lists: the LDS
-   staging of their headings and footprints) and movable bodies (within their staging
-   limits), and serves every fleet with grid-ordered lists. */
+   control mode, obstacles, walls, clamp and integrator, box agents and wheel contacts,
+   and movable bodies (within their staging limits), and serves every fleet with
+   grid-ordered lists.  An env's staging (agents, the grid's bins^2 cells, box fields)
+   stays within the 160 KiB of LDS of one workgroup: at 1024 agents up to 172 bins per
+   axis in float32 (150 in float64; box worlds 150 / 90). */
 #define SWARP_WIDE_MAX_AGENTS 1024
 
 /* The nine state fields.  A NULL field means "not provided": an input adjoint that
@@ -209,12 +210,14 @@ int swarp_rollout_bwd_tape(const swarp_desc_t *desc, int32_t T, const swarp_stat
  * parameter rows (then desc->body_params), disc agents, up to 1024 agents per env with
  * index-ordered or (pinned-frame) uniform-grid lists, and n_obstacles >= 1 up to what the
  * per-env obstacle staging allows: the forward's and the backward's LDS of one workgroup
- * (dynamic and static) stay within 64 KiB.  Up to 64 agents per env with index-ordered
- * lists an env takes a slot of one wave, widened (fewer envs per wave) as far as one env
- * per wave when needed -- at 64 agents, 4 substeps and float32 that is 553 obstacles
- * forward and 164 backward; wider envs and grid-ordered lists take a workgroup of
- * ceil(n_agents / 64) waves, whose agent staging shares the 64 KiB (brute lists, float32:
- * 346 / 142 obstacles forward / backward at 512 agents, 38 / 15 at 1024).  Beyond it the call fails before any launch
+ * (dynamic and static) stay within the 160 KiB a gfx950 workgroup may hold.  Up to 64
+ * agents per env with index-ordered lists an env takes a slot of one wave, widened (fewer
+ * envs per wave) while the staging exceeds 64 KiB, as far as one env per wave -- at 64
+ * agents, 4 substeps and float32 that is 1401 obstacles forward and 447 backward (float64:
+ * 695 / 209); wider envs and grid-ordered lists take a workgroup of ceil(n_agents / 64)
+ * waves, whose agent staging shares the 160 KiB (brute lists, float32: 1329 / 544
+ * obstacles forward / backward at 512 agents, 1021 / 418 at 1024).  Beyond it the call
+ * fails before any launch
  * (swarp_rollout_bwd_ob_check asks the backward's limit).  The _tape entry points keep
  * no body tape on the workgroup-per-env kernels (they accept one and leave it unused).
  * ob0 [E, 12N]: per env and obstacle index o, the shape state (pos x, pos y, angle,

@@ -954,7 +954,7 @@ __host__ __device__ constexpr size_t body_fwd_lds(int PA, int N, size_t tsize)
 }
 
 // All LDS of one k_body_fwd workgroup: the dynamic part above and the kernel's static
-// arrays (sl[4 * 64] and lr[64] scalars).  The 64 KiB limits are checked on this total.
+// arrays (sl[4 * 64] and lr[64] scalars).  The LDS limits are checked on this total.
 __host__ __device__ constexpr size_t body_fwd_lds_total(int PA, int N, size_t tsize)
 {
     return body_fwd_lds(PA, N, tsize) + (size_t)5 * 64 * tsize;

@@ -416,6 +416,10 @@ template <int PA> __device__ __forceinline__ bool env_all(bool ok, int base)
 // 64/PA envs x N obstacles fit (OCS_MAX pairs); NULL table otherwise.
 constexpr int OCS_MAX = 256;
 
+// LDS one gfx950 workgroup may allocate, static and dynamic together (160 KiB); a launch
+// of more than 64 KiB needs no opt-in on this runtime.
+constexpr size_t LDS_MAX = 163840;
+
 template <typename T, int PA>
 __device__ __forceinline__ const T *ob_trig_table(const Cst<T> &C, const Args<T> &g,
                                                   const Lane<T, PA> &L, T *ocs)

@@ -131,7 +131,8 @@ static int check_desc(const swarp_desc_t *d, bool need_params = true)
     if (d->neighbor_method != SWARP_LISTS_BRUTE && d->neighbor_method != SWARP_LISTS_GRID)
         return fail("desc->neighbor_method must be SWARP_LISTS_BRUTE or SWARP_LISTS_GRID");
     if (d->neighbor_method == SWARP_LISTS_GRID) {
-        if (d->grid_bins < 1 || d->grid_bins > 64) return fail("grid_bins must lie in [1, 64]");
+        // the cell table's LDS bounds the bins (wide_lds_check); 1024 bounds bins^2's range
+        if (d->grid_bins < 1 || d->grid_bins > 1024) return fail("grid_bins must lie in [1, 1024]");
         if (d->grid_pinned && !(d->grid_cell > 0.0)) return fail("grid_cell must be positive");
     }
     if (d->act_dim < 1) return fail("act_dim must be >= 1");
@@ -251,11 +252,12 @@ template <typename T> static int wide_lds_check(const swarp_desc_t *d, bool list
     // dynamic staging + the kernels' static wsum[16]: the workgroup's whole LDS; box worlds
     // also stage headings, spins and footprints
     if (!lists_only && (d->has_boxes || d->wheel_contacts)) {
-        if (wide_box_lds_bytes<T>(AP, NC) + 16 * sizeof(int32_t) > 65536)
-            return fail("n_agents too large for the wide-env LDS staging of a box world at this "
-                        "dtype (limit 64 KiB)");
-    } else if (wide_lds_bytes<T>(AP, NC) + 16 * sizeof(int32_t) > 65536) {
-        return fail("n_agents too large for the wide-env LDS staging at this dtype (limit 64 KiB)");
+        if (wide_box_lds_bytes<T>(AP, NC) + 16 * sizeof(int32_t) > LDS_MAX)
+            return fail("n_agents / grid_bins too large for the wide-env LDS staging of a box "
+                        "world at this dtype (limit 160 KiB)");
+    } else if (wide_lds_bytes<T>(AP, NC) + 16 * sizeof(int32_t) > LDS_MAX) {
+        return fail("n_agents / grid_bins too large for the wide-env LDS staging at this dtype "
+                    "(limit 160 KiB)");
     }
     return 0;
 }
@@ -414,7 +416,7 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
         const size_t lshm = (size_t)d->substeps * 128 * 2 * sizeof(T) +
                             (size_t)d->substeps * 64 * msz * 2 + 64 * 2 * sizeof(T) +
                             2 * 64 * sizeof(T) + (size_t)d->substeps * 64;
-        if (lshm > 65536) return fail("substeps too large for the backward LDS staging (limit 64 KiB per wave)");
+        if (lshm > LDS_MAX) return fail("substeps too large for the backward LDS staging (limit 160 KiB per wave)");
         if (tape && TL.total)
             launch_holo_bwd<T, true>(PA, C, a, tape_ptrs<T>(TL, (void *)tape), lshm, st);
         else
@@ -430,8 +432,8 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     if (d->has_boxes)  // contact masks, heading cos / sin, static-contact flags per substep
         shm += (size_t)d->substeps * 64 * (msz + 2 * sizeof(T) + 8 + 1);
     // with k_rollout_bwd's static arrays (ocs_lds[2 OCS_MAX], lbx[3 * 64]): the whole LDS
-    if (shm + (2 * OCS_MAX + 3 * 64) * sizeof(T) > 65536)
-        return fail("substeps too large for the backward LDS staging (limit 64 KiB per wave)");
+    if (shm + (2 * OCS_MAX + 3 * 64) * sizeof(T) > LDS_MAX)
+        return fail("substeps too large for the backward LDS staging (limit 160 KiB per wave)");
     if (d->has_drone)
         launch_bwd<T, true, false>(PA, C, a, world_features(d, false), shm, st);
     else if (d->has_boxes)
@@ -444,8 +446,9 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
 }
 
 // Env slot width of the body kernels: the padded agent count, doubled (fewer env slots per
-// wave, more pad lanes) until the obstacle staging of both passes fits 64 KiB of LDS; 64
-// when nothing fits (the callers then refuse).
+// wave, more pad lanes) until the obstacle staging of both passes fits 64 KiB of LDS, which
+// leaves room for more resident workgroups than a larger staging; 64 when nothing fits (the
+// callers then check the 160 KiB a workgroup may hold).
 template <typename T> static int body_pa(const swarp_desc_t *d)
 {
     const bool dr = d->has_drone != 0;
@@ -457,16 +460,16 @@ template <typename T> static int body_pa(const swarp_desc_t *d)
 }
 
 // LDS of the wide body kernels' workgroup (dynamic staging + the static wsum[16]) within
-// 64 KiB; bwd: the backward's (three obstacle states and two adjoints instead of two).
+// 160 KiB; bwd: the backward's (three obstacle states and two adjoints instead of two).
 template <typename T> static int wbody_lds_check(const swarp_desc_t *d, bool bwd)
 {
     const int NC = d->neighbor_method == SWARP_LISTS_GRID ? d->grid_bins * d->grid_bins : 0;
     const int AP = ((d->n_agents + 63) / 64) * 64;
-    if (wbody_lds_bytes<T>(AP, NC, d->n_obstacles, bwd) + 16 * sizeof(int32_t) > 65536)
+    if (wbody_lds_bytes<T>(AP, NC, d->n_obstacles, bwd) + 16 * sizeof(int32_t) > LDS_MAX)
         return fail(bwd ? "agents and obstacles per env too many for the wide body backward's "
-                          "LDS staging (limit 64 KiB per workgroup)"
+                          "LDS staging (limit 160 KiB per workgroup)"
                         : "agents and obstacles per env too many for the wide body forward's "
-                          "LDS staging (limit 64 KiB per workgroup)");
+                          "LDS staging (limit 160 KiB per workgroup)");
     return 0;
 }
 
@@ -476,9 +479,9 @@ template <typename T> static int fill_obtab(const swarp_desc_t *d, ObTab<T> &tb)
     if (wide_path(d)) {
         if (const char *why = wide_unsupported(d)) return fail(why);
         if (wbody_lds_check<T>(d, false)) return -1;
-    } else if (body_fwd_lds_total(body_pa<T>(d), d->n_obstacles, sizeof(T)) > 65536) {
+    } else if (body_fwd_lds_total(body_pa<T>(d), d->n_obstacles, sizeof(T)) > LDS_MAX) {
         return fail("too many obstacles per env for the body forward's LDS staging (limit "
-                    "64 KiB per wave)");
+                    "160 KiB per wave)");
     }
     if (!d->obs_kind || !d->obs_body || !d->obs_mass || !d->obs_inertia || !d->obs_body_off)
         return fail("obs_kind/obs_body/obs_mass/obs_inertia/obs_body_off must be set");
@@ -601,11 +604,12 @@ static int rollout_bwd_ob(const swarp_desc_t *d, int32_t nT, const swarp_state_t
     // the per-substep body caches (cos / sin, contact sums) when they fit
     const bool dr = d->has_drone != 0;
     size_t shm = body_bwd_lds_of<T>(PA, d->substeps, d->n_obstacles, dr, true);
+    // (the caches only where they keep the workgroup within 64 KiB: more resident waves)
     tb.cache = shm <= 65536 ? 1 : 0;
     if (!tb.cache) shm = body_bwd_lds_of<T>(PA, d->substeps, d->n_obstacles, dr, false);
-    if (shm > 65536)
+    if (shm > LDS_MAX)
         return fail("obstacle count or substeps too large for the body backward's LDS staging "
-                    "(limit 64 KiB per wave)");
+                    "(limit 160 KiB per wave)");
     launch_body_bwd<T>(PA, C, a, tb, io, world_features(d, true), d->has_drone != 0, shm, st);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail(hipGetErrorString(e));
@@ -619,9 +623,9 @@ template <typename T> static int bwd_ob_fits(const swarp_desc_t *d)
     if (fill_obtab<T>(d, tb)) return -1;
     if (wide_path(d)) return wbody_lds_check<T>(d, true);
     if (body_bwd_lds_of<T>(body_pa<T>(d), d->substeps, d->n_obstacles, d->has_drone != 0, false) >
-        65536)
+        LDS_MAX)
         return fail("obstacle count or substeps too large for the body backward's LDS staging "
-                    "(limit 64 KiB per wave)");
+                    "(limit 160 KiB per wave)");
     return 0;
 }
 

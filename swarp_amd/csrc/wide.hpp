@@ -39,7 +39,6 @@
 namespace swarp {
 
 constexpr int WIDE_MAX_AGENTS = 1024;
-constexpr int GRID_MAX_CELLS = 4096;   // bins^2 cell offsets in LDS
 constexpr int32_t CUT_ALL = 0x7fffffff;
 
 // Uniform-grid frame of one launch: origin and cell size (from Cst for a pinned frame,

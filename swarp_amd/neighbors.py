@@ -61,10 +61,15 @@ def fill_list_order(d, method: str, n_agents: int, uniform_bins: int | None, bou
         d.neighbor_method = _lib.LISTS_BRUTE
 
 
-def _check_bins(bins: int) -> None:
-    if bins > 64:
+def _check_bins(bins: int, n_agents: int) -> None:
+    """The cell table (bins^2 + 1 offsets) and the env's float32 agent staging (44 B per
+    agent slot) share one workgroup's 160 KiB of LDS (``wide_lds_bytes``); float64 and box
+    worlds stage more, which the library checks at the call."""
+    slots = -(-n_agents // 64) * 64
+    if slots * 44 + (bins * bins + 1) * 4 + 64 > 163840:
         raise NotImplementedError(
-            f"uniform_bins={bins}: this build keeps at most 64 x 64 cells per env in LDS")
+            f"uniform_bins={bins}: {bins * bins} cells per env with {n_agents} agents exceed "
+            "the 160 KiB of LDS of the workgroup that holds an env")
 
 
 def check_list_method(method: str, n_agents: int, uniform_bins: int | None,
@@ -88,7 +93,7 @@ def check_list_method(method: str, n_agents: int, uniform_bins: int | None,
     if m == "uniform_grid":
         bins = grid_bins(n_agents, uniform_bins)
         if stepping:
-            _check_bins(bins)
+            _check_bins(bins, n_agents)
         if bins * bins > 16 * max(1, n_agents):
             warnings.warn(
                 f"uniform_bins={bins} gives {bins * bins} cells per env for {n_agents} agents; "
@@ -185,7 +190,7 @@ class NeighborGrid:
 
     def _query(self, pos, neighbor_idx, neighbor_count, method: str) -> None:
         if method == "uniform_grid":
-            _check_bins(self.uniform_bins)
+            _check_bins(self.uniform_bins, self.n_agents)
         if pos.shape != (self.n_envs, self.n_agents, 2):
             raise ValueError(
                 f"pos must be [{self.n_envs}, {self.n_agents}, 2]; got {tuple(pos.shape)}"

@@ -238,13 +238,13 @@ def _ring_extra(n, radius=1.0, r=0.07):
                  for k, a in enumerate(ang))
 
 
-@pytest.mark.parametrize("A,n_extra", [(64, 35), (16, 19), (16, 59), (16, 75)])
+@pytest.mark.parametrize("A,n_extra", [(64, 35), (16, 19), (16, 59), (16, 75), (64, 195)])
 def test_bodies_beyond_sixteen_obstacles(A, n_extra):
     """More than 16 obstacles per env (each env's obstacle state staged in LDS sized by the
     obstacle count): the cross body and a ring of movable and static circles, one env per
     wave at 64 agents and four per wave at 16.  64 shapes is the most the instances that
     keep the shape sets as wave masks take; 80 runs the instances that test the shapes
-    one by one."""
+    one by one; 200 needs a backward workgroup of more than 64 KiB of LDS."""
     E = 6 if A == 64 else 9
     s0, acts = _pushers(E, A, 3, spread=1.2)
     obs = cross_obs(E, (0.0, 0.0), extra=_ring_extra(n_extra))
@@ -315,13 +315,13 @@ def test_bodies_few_agents_many_obstacles():
 
 
 def test_bodies_obstacle_count_beyond_lds_is_rejected():
-    """An obstacle count whose backward staging exceeds 64 KiB of LDS even at one env per
-    wave (float64, 100 obstacles) is refused by the host -- when a gradient is required,
-    before the forward runs, so the stepper's obstacle state is not advanced; a no-grad
-    rollout of the same world still runs."""
+    """An obstacle count whose backward staging exceeds the 160 KiB of LDS of a workgroup
+    even at one env per wave (float64, 250 obstacles) is refused by the host -- when a
+    gradient is required, before the forward runs, so the stepper's obstacle state is not
+    advanced; a no-grad rollout of the same world still runs."""
     E, A = 3, 4
     s0, acts = _pushers(E, A, 4)
-    obs = cross_obs(E, (0.0, 0.0), extra=_ring_extra(95))
+    obs = cross_obs(E, (0.0, 0.0), extra=_ring_extra(245, radius=1.5, r=0.01))
     with pytest.raises(RuntimeError, match="LDS"):
         run_pair(nav_agents(A), _world(), 0.05, 4, s0, acts, obs, np.float64)
     st = make_stepper(nav_agents(A), _world(), 0.05, 4, torch.float64, obs=obs, n_envs=E)
@@ -334,6 +334,16 @@ def test_bodies_obstacle_count_beyond_lds_is_rejected():
     with torch.no_grad():
         rollout(st, s0t, a)
     assert st.ob_trajectory is not None and st.ob_trajectory.shape[0] == acts.shape[0]
+
+
+def test_bodies_wide_env_many_obstacles():
+    """1024 agents per env with 40 obstacles: the wide body backward's staging (agents,
+    five obstacle states) needs more than 64 KiB of LDS."""
+    E, A = 1, 1024
+    s0, acts = _pushers(E, A, 5, spread=1.4)
+    obs = cross_obs(E, (0.0, 0.0), extra=_ring_extra(35, radius=0.9, r=0.04))
+    hip, orc = run_pair(nav_agents(A), _world(bounds=2.0), 0.05, 4, s0, acts, obs, np.float32)
+    check("1024 agents, 40 obstacles", hip, orc, exact=True)
 
 def test_bodies_clamp_bounds():
     E, A = 8, 8

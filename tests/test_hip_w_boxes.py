@@ -160,6 +160,19 @@ def test_wide_env_box_fleet():
     _check_box("wide boxes A=80", _fleet(A), world, S, s0, acts, w, obs=obs, E=E)
 
 
+
+def test_box_fleet_1024_agents_per_env():
+    """1024 agents per env, a third of them discs: the box world's staging (headings, spins,
+    footprints) takes the workgroup beyond 64 KiB of LDS."""
+    E, A, T, S = 1, 1024, 3, 2
+    rng = np.random.default_rng(39)
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.02,
+                        bounds=(-2.5, 2.5, -2.5, 2.5), max_neighbors=8)
+    s0 = _state(E, A, rng, 2.4, np.float64)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2))
+    w = _cotangent(T, E, A, 9, scale=0.1)
+    _check_box("wide boxes A=1024", _fleet(A), world, S, s0, acts, w)
+
 def test_grid_ordered_box_fleet():
     """Box agents with uniform-grid lists (pinned frame), capped at 4 neighbours so the
     grid's traversal order decides which contacts act; footprint clamp."""

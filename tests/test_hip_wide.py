@@ -151,6 +151,33 @@ def test_wide_step_grid_pinned_600():
     _check("wide grid A=600", hip, orc)
 
 
+
+def test_wide_step_grid_100_bins():
+    """uniform_bins = 100 (10000 cells per env): the cell table and 600 agents' staging take
+    the workgroup beyond 64 KiB of LDS.  Lists bit-exact, states bit-exact with the oracle
+    stepping in the same grid order."""
+    E, A, T, S = 2, 600, 3, 2
+    rng = np.random.default_rng(25)
+    cfgs = ([AgentConfig(radius=0.03) for _ in range(300)]
+            + [AgentConfig(model=DynamicsModel.DIFF_DRIVE, radius=0.03) for _ in range(300)])
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.015,
+                        bounds=(-1.5, 1.5, -1.5, 1.5), max_neighbors=4, neighbor_radius=0.12,
+                        neighbor_method="uniform_grid", uniform_bins=100)
+    pos = rng.uniform(-1.0, 1.0, size=(E, A, 2))
+    g = NeighborGrid(E, A, radius=0.05, max_neighbors=6, device="cuda:0", method="uniform_grid",
+                     uniform_bins=100)
+    gi, gc, gt = _lists(g, pos.astype(np.float32))
+    oi, oc, ot, _ = Oracle(np.float32).neighbors_grid(pos.astype(np.float32), 0.05, 6, 100)
+    assert np.array_equal(gc, oc) and np.array_equal(gt, ot) and np.array_equal(gi, oi)
+    s0 = pack_state({"pos": pos, "theta": rng.uniform(-np.pi, np.pi, size=(E, A))}).astype(np.float32)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
+    w = _cot(T, E, A, 26)
+    st = make_stepper(cfgs, world, 0.05, S, torch.float32)
+    assert st.wide and st.list_method == "uniform_grid"
+    hip = hip_run(st, s0, acts, w, np.float32)
+    orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float32)
+    _check("grid A=600 bins=100", hip, orc)
+
 def test_grid_step_small_env():
     """A 32-agent env with uniform_grid lists asked for explicitly (the wide kernels serve
     every grid-ordered world)."""
