@@ -123,13 +123,14 @@ typedef struct swarp_desc {
 #define SWARP_LISTS_BRUTE 0
 #define SWARP_LISTS_GRID 1
 /* Agents per env: up to 64 on every path; up to SWARP_WIDE_MAX_AGENTS on the wide-env
-   path (one workgroup per env), which steps 2-D and drone fleets with any model,
+   path (one workgroup per env, 1, 2 or 4 agents per thread; movable bodies up to 1024
+   agents, one per thread), which steps 2-D and drone fleets with any model,
    control mode, obstacles, walls, clamp and integrator, box agents and wheel contacts,
    and movable bodies (within their staging limits), and serves every fleet with
    grid-ordered lists.  An env's staging (agents, the grid's bins^2 cells, box fields)
    stays within the 160 KiB of LDS of one workgroup: at 1024 agents up to 172 bins per
    axis in float32 (150 in float64; box worlds 150 / 90). */
-#define SWARP_WIDE_MAX_AGENTS 1024
+#define SWARP_WIDE_MAX_AGENTS 4096
 
 /* The nine state fields.  A NULL field means "not provided": an input adjoint that
  * is NULL reads as zero, an output adjoint that is NULL is not written.  For a fleet

@@ -17,7 +17,7 @@ ABI_VERSION = 16
 F32, F64 = 0, 1
 EULER, RK4 = 0, 1
 LISTS_BRUTE, LISTS_GRID = 0, 1
-WIDE_MAX_AGENTS = 1024
+WIDE_MAX_AGENTS = 4096
 
 _PKG = Path(__file__).resolve().parent
 LIB_PATH = Path(os.environ.get("SWARP_HIP_LIB", _PKG / "libswarp_hip.so"))

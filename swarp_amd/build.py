@@ -34,7 +34,7 @@ ARCH = os.environ.get("SWARP_OFFLOAD_ARCH", "gfx950")
 
 # (object stem, source, extra defines)
 FAMILIES = ("k_generic", "k_drone", "k_boxes", "k_holo", "k_bodies", "k_nav", "k_wide",
-            "k_wbodies")
+            "k_wide2", "k_wide4", "k_wbodies")
 DTYPES = (("f32", "float", "1"), ("f64", "double", "0"))
 
 

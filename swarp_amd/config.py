@@ -15,7 +15,7 @@ types so a caller's configuration code carries over unchanged:
 What the MI355X build does not run is rejected loudly rather than silently
 approximated, with ``NotImplementedError`` when a ``Stepper`` is built with it (or the
 bodies installed): movable bodies together with box agents or wheel contacts; more than
-1024 agents per env; the hash-grid list order; and stepping with grid-ordered lists
+4096 agents per env (1024 with movable bodies); the hash-grid list order; and stepping with grid-ordered lists
 without world bounds.  Configurations whose per-env staging exceeds a workgroup's LDS
 fail at the library call with a message that says so.
 """

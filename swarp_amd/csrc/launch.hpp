@@ -44,10 +44,18 @@
     extern template void launch_wide_lists<T>(const Cst<T> &, const T *, const T *, int32_t *,\
                                               int32_t *, int32_t *, hipStream_t);            \
     extern template void launch_grid_frame<T>(const T *, int64_t, T, int, T *, hipStream_t);  \
-    extern template void launch_wide_fwd<T>(bool, bool, const Cst<T> &, const Args<T> &,      \
-                                            hipStream_t);                                    \
-    extern template void launch_wide_bwd<T>(bool, bool, const Cst<T> &, const Args<T> &,      \
-                                            hipStream_t);                                    \
+    extern template void launch_wide_fwd_apt<T, 1>(bool, bool, const Cst<T> &, const Args<T> &, \
+                                                   hipStream_t);                             \
+    extern template void launch_wide_fwd_apt<T, 2>(bool, bool, const Cst<T> &, const Args<T> &, \
+                                                   hipStream_t);                             \
+    extern template void launch_wide_fwd_apt<T, 4>(bool, bool, const Cst<T> &, const Args<T> &, \
+                                                   hipStream_t);                             \
+    extern template void launch_wide_bwd_apt<T, 1>(bool, bool, const Cst<T> &, const Args<T> &, \
+                                                   hipStream_t);                             \
+    extern template void launch_wide_bwd_apt<T, 2>(bool, bool, const Cst<T> &, const Args<T> &, \
+                                                   hipStream_t);                             \
+    extern template void launch_wide_bwd_apt<T, 4>(bool, bool, const Cst<T> &, const Args<T> &, \
+                                                   hipStream_t);                             \
     extern template void launch_wbody_fwd<T>(bool, const Cst<T> &, const Args<T> &,           \
                                              const ObTab<T> &, const ObIO<T> &, hipStream_t); \
     extern template void launch_wbody_bwd<T>(bool, const Cst<T> &, const Args<T> &,           \

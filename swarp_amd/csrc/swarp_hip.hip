@@ -127,7 +127,7 @@ static int check_desc(const swarp_desc_t *d, bool need_params = true)
     if (d->dtype != SWARP_F32 && d->dtype != SWARP_F64) return fail("desc->dtype must be SWARP_F32 or SWARP_F64");
     if (d->n_envs < 1) return fail("n_envs must be >= 1");
     if (d->n_agents < 1 || d->n_agents > SWARP_WIDE_MAX_AGENTS)
-        return fail("n_agents must lie in [1, 1024]");
+        return fail("n_agents must lie in [1, 4096]");
     if (d->neighbor_method != SWARP_LISTS_BRUTE && d->neighbor_method != SWARP_LISTS_GRID)
         return fail("desc->neighbor_method must be SWARP_LISTS_BRUTE or SWARP_LISTS_GRID");
     if (d->neighbor_method == SWARP_LISTS_GRID) {
@@ -248,7 +248,7 @@ static const char *wide_unsupported(const swarp_desc_t *d)
 template <typename T> static int wide_lds_check(const swarp_desc_t *d, bool lists_only = false)
 {
     const int NC = d->neighbor_method == SWARP_LISTS_GRID ? d->grid_bins * d->grid_bins : 0;
-    const int AP = ((d->n_agents + 63) / 64) * 64;
+    const int AP = wide_geom(d->n_agents).slots;
     // dynamic staging + the kernels' static wsum[16]: the workgroup's whole LDS; box worlds
     // also stage headings, spins and footprints
     if (!lists_only && (d->has_boxes || d->wheel_contacts)) {
@@ -476,6 +476,9 @@ template <typename T> static int wbody_lds_check(const swarp_desc_t *d, bool bwd
 template <typename T> static int fill_obtab(const swarp_desc_t *d, ObTab<T> &tb)
 {
     if (d->n_obstacles < 1) return fail("the body path takes at least one obstacle per env");
+    if (d->n_agents > 1024)
+        return fail("movable bodies step at most 1024 agents per env (one thread per agent in "
+                    "the env's workgroup)");
     if (wide_path(d)) {
         if (const char *why = wide_unsupported(d)) return fail(why);
         if (wbody_lds_check<T>(d, false)) return -1;

@@ -1,11 +1,13 @@
-// wide.hpp -- envs of up to 1024 agents, and the uniform-grid list order.
+// wide.hpp -- envs of up to 4096 agents, and the uniform-grid list order.
 //
 // The generic and specialised kernels put a whole env into one wave (at most 64 agents,
-// the lists as 64-bit masks).  These kernels give each env one workgroup of ceil(A/64)
-// waves, one lane per agent, with the env's positions, velocities and radii in LDS.  They
-// serve every 2-D or drone fleet (any model, control mode, obstacles, walls, clamp,
-// integrator) of more than 64 agents per env, and every fleet whose lists follow the
-// uniform grid.
+// the lists as 64-bit masks).  These kernels give each env one workgroup of up to 16
+// waves, one lane per agent up to 1024 agents and 2 or 4 agents per lane beyond
+// (wide_geom: agent i = thread + k * threads), with the env's positions, velocities and
+// radii in LDS.  They serve every 2-D or drone fleet (any model, control mode, obstacles,
+// walls, clamp, integrator, box agents, wheel contacts) of more than 64 agents per env,
+// and every fleet whose lists follow the uniform grid, as far as the env's staging fits
+// the 160 KiB of LDS of a workgroup.
 //
 // List order (which K in-radius neighbours a capped list keeps, and the order the pair
 // forces are summed in):
@@ -16,7 +18,7 @@
 //          :184-211, 663-666).  A cell is (int)((p - origin) / cell_size) per axis,
 //          clamped to [0, bins); the frame (origin, cell size) is pinned by the world
 //          bounds or, for list builds, reduced over the batch (:149-181).
-// Every list position has a traversal key -- the agent index (brute), or slot * 1024 +
+// Every list position has a traversal key -- the agent index (brute), or slot * 4096 +
 // rank in its cell with slot = 3 (dy + 1) + (dx + 1) (grid) -- increasing along the
 // traversal, so "j is in i's capped list" is "j within radius of i and key_i(j) <=
 // cut_i", where cut_i is the key of i's K-th listed neighbour (INT_MAX when fewer).  The
@@ -38,7 +40,7 @@
 
 namespace swarp {
 
-constexpr int WIDE_MAX_AGENTS = 1024;
+constexpr int WIDE_MAX_AGENTS = 4096;
 constexpr int32_t CUT_ALL = 0x7fffffff;
 
 // Uniform-grid frame of one launch: origin and cell size (from Cst for a pinned frame,
@@ -159,21 +161,21 @@ __device__ inline void grid_build(const WideLds<T> &W, int A, const GridFrame<T>
     const int tid = threadIdx.x, nt = blockDim.x, NC = G.bins * G.bins;
     for (int c = tid; c < NC; c += nt) W.cstart[c] = 0;
     __syncthreads();
-    int k = 0;
-    if (tid < A) {
-        const int cx = grid_axis(W.px[tid], G.ox, G.cs, G.bins);
-        const int cy = grid_axis(W.py[tid], G.oy, G.cs, G.bins);
-        k = cy * G.bins + cx;
-        W.key[tid] = k;
+    for (int i = tid; i < A; i += nt) {
+        const int cx = grid_axis(W.px[i], G.ox, G.cs, G.bins);
+        const int cy = grid_axis(W.py[i], G.oy, G.cs, G.bins);
+        const int k = cy * G.bins + cx;
+        W.key[i] = k;
         atomicAdd(&W.cstart[k], 1);
     }
     __syncthreads();
     block_exclusive_scan(W.cstart, NC, wsum);
-    if (tid < A) {
+    for (int i = tid; i < A; i += nt) {
+        const int k = W.key[i];
         int r = 0;  // agents of the same cell with a smaller index
-        for (int j = 0; j < tid; ++j) r += W.key[j] == k ? 1 : 0;
-        W.rank[tid] = r;
-        W.sorted[W.cstart[k] + r] = tid;
+        for (int j = 0; j < i; ++j) r += W.key[j] == k ? 1 : 0;
+        W.rank[i] = r;
+        W.sorted[W.cstart[k] + r] = i;
     }
     __syncthreads();
 }
@@ -221,7 +223,7 @@ __device__ __forceinline__ int visit_list(const WideLds<T> &W, int A, const Grid
                 const T dx = W.px[j] - px, dy = W.py[j] - py;
                 const T d2 = dx * dx + dy * dy;
                 if (!(d2 <= t_nbr) || j == i) continue;
-                if (n < limit) f(j, (3 * sy + sx) * 1024 + (si - c0));
+                if (n < limit) f(j, (3 * sy + sx) * WIDE_MAX_AGENTS + (si - c0));
                 ++n;
                 if (!count_all && n >= limit) return n;
             }
@@ -237,7 +239,7 @@ __device__ __forceinline__ int32_t grid_key_in(const WideLds<T> &W, int bins, in
 {
     const int ki = W.key[i], kj = W.key[j];
     const int sx = ki % bins - kj % bins + 1, sy = ki / bins - kj / bins + 1;
-    return (3 * sy + sx) * 1024 + W.rank[i];
+    return (3 * sy + sx) * WIDE_MAX_AGENTS + W.rank[i];
 }
 
 // Frame of this launch.
@@ -310,6 +312,22 @@ __global__ __launch_bounds__(1024) void k_grid_frame(const T *pos, int64_t n, T 
 
 // ------------------------------------------------------------------ neighbour lists
 
+// Launch geometry of the workgroup of an env of A agents: `apt` agents per thread (1, 2
+// or 4; agent i = thread + k * threads), `threads` a multiple of 64 up to 1024, `slots` =
+// threads * apt >= A staging entries per array.
+struct WideGeom {
+    int apt, threads, slots;
+};
+
+__host__ __device__ inline WideGeom wide_geom(int A)
+{
+    const int ap = (A + 63) / 64 * 64;
+    int apt = (ap + 1023) / 1024;
+    if (apt == 3) apt = 4;
+    const int th = ((ap + apt - 1) / apt + 63) / 64 * 64;
+    return {apt, th, th * apt};
+}
+
 // Padded lists, counts and true counts of one env per workgroup (brute or grid order).
 template <typename T, bool GRID>
 __global__ __launch_bounds__(1024) void k_wide_lists(const Cst<T> C, const T *pos, const T *frame,
@@ -317,23 +335,27 @@ __global__ __launch_bounds__(1024) void k_wide_lists(const Cst<T> C, const T *po
 {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int32_t wsum[16];
-    const int AP = blockDim.x, i = threadIdx.x, A = C.A, env = blockIdx.x;
+    const int nt = blockDim.x, A = C.A, env = blockIdx.x;
+    const int AP = nt * wide_geom(A).apt;
     const WideLds<T> W = wide_lds<T>(smem, AP);
     const GridFrame<T> G = grid_frame(C, frame);
-    const size_t row = (size_t)env * A + (i < A ? i : 0);
-    const T px = i < A ? pos[2 * row] : T(0), py = i < A ? pos[2 * row + 1] : T(0);
-    W.px[i] = px;
-    W.py[i] = py;
+    for (int i = threadIdx.x; i < AP; i += nt) {
+        const size_t row = (size_t)env * A + (i < A ? i : 0);
+        W.px[i] = i < A ? pos[2 * row] : T(0);
+        W.py[i] = i < A ? pos[2 * row + 1] : T(0);
+    }
     __syncthreads();
     if (GRID) grid_build(W, A, G, wsum);
-    if (i >= A) return;
-    int32_t *out = idx + row * C.K;
-    const int n = visit_list<T, GRID>(W, A, G, i, px, py, C.t_nbr, C.K, true,
-                                      [&](int j, int32_t) { *out++ = j; });
-    const int c = n < C.K ? n : C.K;
-    for (int q = c; q < C.K; ++q) idx[row * C.K + q] = 0;
-    cnt[row] = c;
-    if (tru) tru[row] = n;
+    for (int i = threadIdx.x; i < A; i += nt) {
+        const size_t row = (size_t)env * A + i;
+        int32_t *out = idx + row * C.K;
+        const int n = visit_list<T, GRID>(W, A, G, i, W.px[i], W.py[i], C.t_nbr, C.K, true,
+                                          [&](int j, int32_t) { *out++ = j; });
+        const int c = n < C.K ? n : C.K;
+        for (int q = c; q < C.K; ++q) idx[row * C.K + q] = 0;
+        cnt[row] = c;
+        if (tru) tru[row] = n;
+    }
 }
 
 // ------------------------------------------------------------------ rollout kernels
@@ -348,9 +370,10 @@ template <typename T> struct WLane {
 };
 
 template <typename T, unsigned F>
-__device__ __forceinline__ void wide_init(const Cst<T> &C, const Args<T> &g, WLane<T> &L)
+__device__ __forceinline__ void wide_init(const Cst<T> &C, const Args<T> &g, WLane<T> &L,
+                                          int i = (int)threadIdx.x)
 {
-    L.i = threadIdx.x;
+    L.i = i;
     L.env = blockIdx.x;
     L.active = L.i < C.A;
     const int ag = L.active ? L.i : 0;
@@ -371,16 +394,7 @@ __device__ __forceinline__ void wide_publish(const Cst<T> &C, const WideLds<T> &
                                              const WBoxLds<T> *B = nullptr)
 {
     __syncthreads();
-    W.px[L.i] = st.px;
-    W.py[L.i] = st.py;
-    W.vx[L.i] = st.vx;
-    W.vy[L.i] = st.vy;
-    if (B) {
-        B->th[L.i] = st.th;
-        B->w[L.i] = st.w;
-        B->cs[L.i] = m_cos(st.th);
-        B->sn[L.i] = m_sin(st.th);
-    }
+    wide_put(W, L, st, B);
     __syncthreads();
     if (GRID && C.collisions) grid_build(W, C.A, G, wsum);
 }
@@ -521,37 +535,83 @@ __device__ __forceinline__ void wide_forces_box(const Cst<T> &C, const Args<T> &
     if (tq) *tq = tau;
 }
 
-// One substep.  Box worlds with wheel contacts integrate unclamped, rework the step with
-// wheel_contact, then clamp (integrate2d_wheel_kernel, swarp/dynamics/kernels.py:1389-1478).
-template <typename T, bool DRONE, bool GRID, bool BOXES>
+// Stores one agent's state of this substep in the env's staging (box worlds: also its
+// heading, spin and heading cos / sin).
+template <typename T>
+__device__ __forceinline__ void wide_put(const WideLds<T> &W, const WLane<T> &L, const St<T> &st,
+                                         const WBoxLds<T> *B)
+{
+    W.px[L.i] = st.px;
+    W.py[L.i] = st.py;
+    W.vx[L.i] = st.vx;
+    W.vy[L.i] = st.vy;
+    if (B) {
+        B->th[L.i] = st.th;
+        B->w[L.i] = st.w;
+        B->cs[L.i] = m_cos(st.th);
+        B->sn[L.i] = m_sin(st.th);
+    }
+}
+
+// One agent's forces of a substep whose state is published.
+template <typename T, bool GRID, bool BOXES>
+__device__ __forceinline__ void wide_agent_forces(const Cst<T> &C, const Args<T> &g,
+                                                  const WideLds<T> &W, const WBoxLds<T> &B,
+                                                  const GridFrame<T> &G, const WLane<T> &L,
+                                                  const St<T> &st, T &Fx, T &Fy, int32_t &cut,
+                                                  T *tq)
+{
+    if constexpr (BOXES)
+        wide_forces_box<T, GRID>(C, g, W, B, G, L, st, Fx, Fy, cut, tq);
+    else
+        wide_forces<T, GRID>(C, g, W, G, L, st, Fx, Fy, cut);
+}
+
+// One substep of the APT agents of each thread (agent i = thread + k * threads).  Box
+// worlds with wheel contacts integrate unclamped, rework the step with wheel_contact, then
+// clamp (integrate2d_wheel_kernel, swarp/dynamics/kernels.py:1389-1478).
+template <typename T, bool DRONE, bool GRID, bool BOXES, int APT>
 __device__ __forceinline__ void wide_substep(const Cst<T> &C, const Args<T> &g,
                                              const WideLds<T> &W, const WBoxLds<T> &B,
-                                             const GridFrame<T> &G, const WLane<T> &L,
-                                             const T (&a)[4], St<T> &st, int32_t *wsum)
+                                             const GridFrame<T> &G, const WLane<T> (&L)[APT],
+                                             const T (&a)[APT][4], St<T> (&st)[APT],
+                                             int32_t *wsum)
 {
-    T Fx = T(0), Fy = T(0), Tq = T(0);
+    T Fx[APT], Fy[APT], Tq[APT];
+#pragma unroll
+    for (int k = 0; k < APT; ++k) Fx[k] = Fy[k] = Tq[k] = T(0);
     if (C.needs_forces) {
-        if (C.collisions) wide_publish<T, GRID>(C, W, G, L, st, wsum, BOXES ? &B : nullptr);
-        int32_t cut;
-        if constexpr (BOXES)
-            wide_forces_box<T, GRID>(C, g, W, B, G, L, st, Fx, Fy, cut, C.wheel ? &Tq : nullptr);
-        else
-            wide_forces<T, GRID>(C, g, W, G, L, st, Fx, Fy, cut);
-    }
-    St<T> nx;
-    if constexpr (BOXES) {
-        if (C.wheel) {
-            Cst<T> C0 = C;
-            C0.clamp = 0;
-            integrate<T, DRONE>(C0, L.pr, st, a, Fx, Fy, nx);
-            wheel_contact(C, L.pr, st, Fx, Fy, Tq, nx);
-            if (C.clamp) clamp_position(C, L.pr, nx.th, nx.px, nx.py);
-            st = nx;
-            return;
+        if (C.collisions) {
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < APT; ++k) wide_put(W, L[k], st[k], BOXES ? &B : nullptr);
+            __syncthreads();
+            if (GRID) grid_build(W, C.A, G, wsum);
+        }
+#pragma unroll
+        for (int k = 0; k < APT; ++k) {
+            int32_t cut;
+            wide_agent_forces<T, GRID, BOXES>(C, g, W, B, G, L[k], st[k], Fx[k], Fy[k], cut,
+                                              BOXES && C.wheel ? &Tq[k] : nullptr);
         }
     }
-    integrate<T, DRONE>(C, L.pr, st, a, Fx, Fy, nx);
-    st = nx;
+#pragma unroll
+    for (int k = 0; k < APT; ++k) {
+        St<T> nx;
+        if constexpr (BOXES) {
+            if (C.wheel) {
+                Cst<T> C0 = C;
+                C0.clamp = 0;
+                integrate<T, DRONE>(C0, L[k].pr, st[k], a[k], Fx[k], Fy[k], nx);
+                wheel_contact(C, L[k].pr, st[k], Fx[k], Fy[k], Tq[k], nx);
+                if (C.clamp) clamp_position(C, L[k].pr, nx.th, nx.px, nx.py);
+                st[k] = nx;
+                continue;
+            }
+        }
+        integrate<T, DRONE>(C, L[k].pr, st[k], a[k], Fx[k], Fy[k], nx);
+        st[k] = nx;
+    }
 }
 
 // Footprints of a box world's agents, once per launch.
@@ -568,162 +628,215 @@ template <typename T> __device__ __forceinline__ int wide_cells(const Cst<T> &C)
     return C.grid_bins > 0 ? C.grid_bins * C.grid_bins : 0;
 }
 
-template <typename T, bool DRONE, bool GRID, bool BOXES, unsigned F>
+// The lanes of the launch: APT agents per thread, thread + k * threads.
+template <typename T, bool BOXES, int APT, unsigned F>
+__device__ __forceinline__ void wide_lanes(const Cst<T> &C, const Args<T> &g, const WideLds<T> &W,
+                                           const WBoxLds<T> &B, WLane<T> (&L)[APT])
+{
+#pragma unroll
+    for (int k = 0; k < APT; ++k) {
+        wide_init<T, F>(C, g, L[k], (int)(threadIdx.x + k * blockDim.x));
+        W.rad[L[k].i] = L[k].pr.radius;
+        if (BOXES) wide_box_init(B, L[k]);
+    }
+}
+
+template <typename T, bool DRONE, bool GRID, bool BOXES, int APT, unsigned F>
 __global__ __launch_bounds__(1024) void k_wide_fwd(const Cst<T> Cin, const Args<T> g)
 {
     const Cst<T> C = fold_cst<F>(Cin);
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int32_t wsum[16];
-    const WideLds<T> W = wide_lds<T>(smem, blockDim.x);
-    const WBoxLds<T> B = wide_box_lds<T>(smem, blockDim.x, wide_cells(C));
+    const int AP = (int)blockDim.x * APT;
+    const WideLds<T> W = wide_lds<T>(smem, AP);
+    const WBoxLds<T> B = wide_box_lds<T>(smem, AP, wide_cells(C));
     const GridFrame<T> G = grid_frame(C, (const T *)nullptr);
-    WLane<T> L;
-    wide_init<T, F>(C, g, L);
-    W.rad[L.i] = L.pr.radius;
-    if (BOXES) wide_box_init(B, L);
-    St<T> st;
-    load_state<T, DRONE>(g.s0.f, L.idx, 0, st);
+    WLane<T> L[APT];
+    wide_lanes<T, BOXES, APT, F>(C, g, W, B, L);
+    St<T> st[APT];
+#pragma unroll
+    for (int k = 0; k < APT; ++k) load_state<T, DRONE>(g.s0.f, L[k].idx, 0, st[k]);
     const size_t EA = (size_t)C.E * C.A;
     for (int t = 0; t < g.nsteps; ++t) {
-        T a[4];
-        load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
+        T a[APT][4];
+#pragma unroll
+        for (int k = 0; k < APT; ++k) load_act(g.act, (size_t)t * EA + L[k].idx, C.ad, a[k]);
         for (int s = 0; s < C.S; ++s)
-            wide_substep<T, DRONE, GRID, BOXES>(C, g, W, B, G, L, a, st, wsum);
-        if (L.active) {
+            wide_substep<T, DRONE, GRID, BOXES, APT>(C, g, W, B, G, L, a, st, wsum);
+#pragma unroll
+        for (int k = 0; k < APT; ++k) {
+            if (!L[k].active) continue;
             if (t + 1 < g.nsteps)
-                store_state<T, DRONE>(g.traj.f, (size_t)t * EA + L.idx, st);
+                store_state<T, DRONE>(g.traj.f, (size_t)t * EA + L[k].idx, st[k]);
             else
-                store_state<T, DRONE>(g.fin.f, L.idx, st);
+                store_state<T, DRONE>(g.fin.f, L[k].idx, st[k]);
         }
     }
 }
 
-template <typename T, bool DRONE, bool GRID, bool BOXES, unsigned F>
+// Reverse of one agent's forces of a substep (published state and force adjoints /
+// damping denominators `wF`, cut keys): every in-radius pair, both sides -- own (j in
+// i's list), rev (i in j's) -- then the obstacles and walls.
+template <typename T, bool GRID, bool BOXES>
+__device__ __forceinline__ void wide_agent_adj(const Cst<T> &C, const Args<T> &g,
+                                               const WideLds<T> &W, const WBoxLds<T> &B,
+                                               const GridFrame<T> &G, const WLane<T> &L,
+                                               const St<T> &in, T gFx, T gFy, int32_t cut,
+                                               St<T> &gi)
+{
+    if (!L.active) return;
+    const bool box_me = BOXES && L.pr.shape > T(0.5);
+    const Foot<T> fa = {L.pr.shape, L.pr.radius, L.pr.hx, L.pr.hy};
+    if (C.collisions) {
+        const T wFx = W.wfx[L.i], wFy = W.wfy[L.i];
+        visit_list<T, GRID>(
+            W, C.A, G, L.i, in.px, in.py, C.t_nbr, C.A, false, [&](int j, int32_t key) {
+                const bool own = key <= cut;
+                const int32_t kin = GRID ? grid_key_in(W, G.bins, L.i, j) : L.i;
+                const bool rev = kin <= W.cut[j];
+                if (!own && !rev) return;
+                const T wx = (own ? wFx : T(0)) - (rev ? W.wfx[j] : T(0));
+                const T wy = (own ? wFy : T(0)) - (rev ? W.wfy[j] : T(0));
+                if constexpr (BOXES) {
+                    if (box_me || B.shp[j] > T(0.5)) {
+                        // one box contact seen from both sides; a contact that exerts no
+                        // force has zero derivatives
+                        const Foot<T> fb = {B.shp[j], W.rad[j], B.hx[j], B.hy[j]};
+                        const T ob[6] = {W.px[j], W.py[j], B.th[j], W.vx[j], W.vy[j], B.w[j]};
+                        box_item_adj(C, g.obs, (size_t)0, (const T *)nullptr, BI_PAIR, L.i, fa, in,
+                                     j, fb, ob, B.cs[j], B.sn[j], 0, T(1), wx, wy, gi);
+                        return;
+                    }
+                }
+                pair_adj_combined(C, in.px - W.px[j], in.py - W.py[j], in.vx - W.vx[j],
+                                  in.vy - W.vy[j], L.pr.radius + W.rad[j] + C.margin, wx, wy,
+                                  gi.px, gi.py, gi.vx, gi.vy);
+            });
+    }
+    if constexpr (BOXES) {
+        if (box_me) {
+            // a box agent's obstacles and walls
+            box_static_adj(C, g.obs, (size_t)L.env * C.N, (const T *)nullptr, fa, in, L.dd, gFx,
+                           gFy, gi);
+            return;
+        }
+    }
+    if (C.N > 0) {
+        const size_t eN = (size_t)L.env * C.N;
+        for (int o = 0; o < C.N; ++o)
+            obstacle_force_adj(C, g.obs, eN, o, in.px, in.py, in.vx, in.vy, L.pr.radius, L.dd,
+                               gFx, gFy, gi);
+    }
+    if (C.soft_walls)
+        wall_force_adj(C, in.px, in.py, in.vx, in.vy, L.pr.radius, L.dd, gFx, gFy, gi);
+}
+
+template <typename T, bool DRONE, bool GRID, bool BOXES, int APT, unsigned F>
 __global__ __launch_bounds__(1024) void k_wide_bwd(const Cst<T> Cin, const Args<T> g)
 {
     const Cst<T> C = fold_cst<F>(Cin);
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ int32_t wsum[16];
-    const WideLds<T> W = wide_lds<T>(smem, blockDim.x);
-    const WBoxLds<T> B = wide_box_lds<T>(smem, blockDim.x, wide_cells(C));
+    const int AP = (int)blockDim.x * APT;
+    const WideLds<T> W = wide_lds<T>(smem, AP);
+    const WBoxLds<T> B = wide_box_lds<T>(smem, AP, wide_cells(C));
     const GridFrame<T> G = grid_frame(C, (const T *)nullptr);
-    WLane<T> L;
-    wide_init<T, F>(C, g, L);
-    W.rad[L.i] = L.pr.radius;
-    if (BOXES) wide_box_init(B, L);
-    const bool box_me = BOXES && L.pr.shape > T(0.5);
-    const Foot<T> fa = {L.pr.shape, L.pr.radius, L.pr.hx, L.pr.hy};
+    WLane<T> L[APT];
+    wide_lanes<T, BOXES, APT, F>(C, g, W, B, L);
     const size_t EA = (size_t)C.E * C.A;
-    St<T> gs;
-    st_zero(gs);
+    St<T> gs[APT];
+#pragma unroll
+    for (int k = 0; k < APT; ++k) st_zero(gs[k]);
     for (int t = g.nsteps - 1; t >= 0; --t) {
-        if (L.active) {
-            if (t == g.nsteps - 1)
-                add_adj<T, DRONE>(g.afin.f, L.idx, gs);
+        St<T> st0[APT];
+        T a[APT][4], ga[APT][4];
+#pragma unroll
+        for (int k = 0; k < APT; ++k) {
+            if (L[k].active) {
+                if (t == g.nsteps - 1)
+                    add_adj<T, DRONE>(g.afin.f, L[k].idx, gs[k]);
+                else
+                    add_adj<T, DRONE>(g.atraj.f, (size_t)t * EA + L[k].idx, gs[k]);
+            }
+            if (t == 0)
+                load_state<T, DRONE>(g.s0.f, L[k].idx, 0, st0[k]);
             else
-                add_adj<T, DRONE>(g.atraj.f, (size_t)t * EA + L.idx, gs);
+                load_state<T, DRONE>(g.traj.f, L[k].idx, (size_t)(t - 1) * EA, st0[k]);
+            load_act(g.act, (size_t)t * EA + L[k].idx, C.ad, a[k]);
+            for (int q = 0; q < 4; ++q) ga[k][q] = T(0);
         }
-        St<T> st0;
-        if (t == 0)
-            load_state<T, DRONE>(g.s0.f, L.idx, 0, st0);
-        else
-            load_state<T, DRONE>(g.traj.f, L.idx, (size_t)(t - 1) * EA, st0);
-        T a[4];
-        load_act(g.act, (size_t)t * EA + L.idx, C.ad, a);
-        T ga[4] = {T(0), T(0), T(0), T(0)};
         for (int s = C.S - 1; s >= 0; --s) {
             // the substep's input, recomputed from the step's checkpoint
-            St<T> in = st0;
+            St<T> in[APT];
+#pragma unroll
+            for (int k = 0; k < APT; ++k) in[k] = st0[k];
             for (int q = 0; q < s; ++q)
-                wide_substep<T, DRONE, GRID, BOXES>(C, g, W, B, G, L, a, in, wsum);
-            T Fx = T(0), Fy = T(0);
-            int32_t cut = CUT_ALL;
-            if (C.needs_forces) {
-                if (C.collisions) wide_publish<T, GRID>(C, W, G, L, in, wsum, BOXES ? &B : nullptr);
-                if constexpr (BOXES)
-                    wide_forces_box<T, GRID>(C, g, W, B, G, L, in, Fx, Fy, cut, nullptr);
-                else
-                    wide_forces<T, GRID>(C, g, W, G, L, in, Fx, Fy, cut);
+                wide_substep<T, DRONE, GRID, BOXES, APT>(C, g, W, B, G, L, a, in, wsum);
+            T Fx[APT], Fy[APT];
+            int32_t cut[APT];
+#pragma unroll
+            for (int k = 0; k < APT; ++k) {
+                Fx[k] = Fy[k] = T(0);
+                cut[k] = CUT_ALL;
             }
-            St<T> gi;
-            T gFx, gFy;
-            integrate_adj<T, DRONE>(C, L.pr, in, a, Fx, Fy, gs, gi, ga, gFx, gFy);
             if (C.needs_forces) {
                 if (C.collisions) {
-                    const T wFx = gFx * L.inv_dd, wFy = gFy * L.inv_dd;
-                    W.wfx[L.i] = wFx;
-                    W.wfy[L.i] = wFy;
-                    W.cut[L.i] = cut;
                     __syncthreads();
-                    if (L.active) {
-                        // every in-radius pair, both sides: own (j in i's list), rev (i in j's)
-                        visit_list<T, GRID>(
-                            W, C.A, G, L.i, in.px, in.py, C.t_nbr, C.A, false,
-                            [&](int j, int32_t key) {
-                                const bool own = key <= cut;
-                                const int32_t kin = GRID ? grid_key_in(W, G.bins, L.i, j) : L.i;
-                                const bool rev = kin <= W.cut[j];
-                                if (!own && !rev) return;
-                                const T wx = (own ? wFx : T(0)) - (rev ? W.wfx[j] : T(0));
-                                const T wy = (own ? wFy : T(0)) - (rev ? W.wfy[j] : T(0));
-                                if constexpr (BOXES) {
-                                    if (box_me || B.shp[j] > T(0.5)) {
-                                        // one box contact seen from both sides; a contact
-                                        // that exerts no force has zero derivatives
-                                        const Foot<T> fb = {B.shp[j], W.rad[j], B.hx[j], B.hy[j]};
-                                        const T ob[6] = {W.px[j], W.py[j], B.th[j],
-                                                         W.vx[j], W.vy[j], B.w[j]};
-                                        box_item_adj(C, g.obs, (size_t)0, (const T *)nullptr,
-                                                     BI_PAIR, L.i, fa, in, j, fb, ob, B.cs[j],
-                                                     B.sn[j], 0, T(1), wx, wy, gi);
-                                        return;
-                                    }
-                                }
-                                pair_adj_combined(C, in.px - W.px[j], in.py - W.py[j],
-                                                  in.vx - W.vx[j], in.vy - W.vy[j],
-                                                  L.pr.radius + W.rad[j] + C.margin, wx, wy,
-                                                  gi.px, gi.py, gi.vx, gi.vy);
-                            });
-                    }
+#pragma unroll
+                    for (int k = 0; k < APT; ++k) wide_put(W, L[k], in[k], BOXES ? &B : nullptr);
+                    __syncthreads();
+                    if (GRID) grid_build(W, C.A, G, wsum);
                 }
-                bool statics_done = false;
-                if constexpr (BOXES) {
-                    if (L.active && box_me) {
-                        // a box agent's obstacles and walls
-                        box_static_adj(C, g.obs, (size_t)L.env * C.N, (const T *)nullptr, fa,
-                                       in, L.dd, gFx, gFy, gi);
-                        statics_done = true;
-                    }
-                }
-                if (L.active && !statics_done) {
-                    if (C.N > 0) {
-                        const size_t eN = (size_t)L.env * C.N;
-                        for (int o = 0; o < C.N; ++o)
-                            obstacle_force_adj(C, g.obs, eN, o, in.px, in.py, in.vx, in.vy,
-                                               L.pr.radius, L.dd, gFx, gFy, gi);
-                    }
-                    if (C.soft_walls)
-                        wall_force_adj(C, in.px, in.py, in.vx, in.vy, L.pr.radius, L.dd, gFx,
-                                       gFy, gi);
-                }
+#pragma unroll
+                for (int k = 0; k < APT; ++k)
+                    wide_agent_forces<T, GRID, BOXES>(C, g, W, B, G, L[k], in[k], Fx[k], Fy[k],
+                                                      cut[k], nullptr);
             }
-            gs = gi;
+            St<T> gi[APT];
+            T gFx[APT], gFy[APT];
+#pragma unroll
+            for (int k = 0; k < APT; ++k)
+                integrate_adj<T, DRONE>(C, L[k].pr, in[k], a[k], Fx[k], Fy[k], gs[k], gi[k], ga[k],
+                                        gFx[k], gFy[k]);
+            if (C.needs_forces) {
+                if (C.collisions) {
+#pragma unroll
+                    for (int k = 0; k < APT; ++k) {
+                        // the force adjoint divided by the damping denominator
+                        W.wfx[L[k].i] = gFx[k] * L[k].inv_dd;
+                        W.wfy[L[k].i] = gFy[k] * L[k].inv_dd;
+                        W.cut[L[k].i] = cut[k];
+                    }
+                    __syncthreads();
+                }
+#pragma unroll
+                for (int k = 0; k < APT; ++k)
+                    wide_agent_adj<T, GRID, BOXES>(C, g, W, B, G, L[k], in[k], gFx[k], gFy[k],
+                                                   cut[k], gi[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < APT; ++k) gs[k] = gi[k];
         }
-        if (L.active) {
-            T *pa = g.aact + ((size_t)t * EA + L.idx) * C.ad;
-            for (int k = 0; k < C.ad; ++k) pa[k] = k < 4 ? ga[k] : T(0);
+#pragma unroll
+        for (int k = 0; k < APT; ++k) {
+            if (!L[k].active) continue;
+            T *pa = g.aact + ((size_t)t * EA + L[k].idx) * C.ad;
+            for (int q = 0; q < C.ad; ++q) pa[q] = q < 4 ? ga[k][q] : T(0);
         }
     }
-    if (L.active) store_adj<T, DRONE>(g.a0.f, L.idx, gs);
+#pragma unroll
+    for (int k = 0; k < APT; ++k)
+        if (L[k].active) store_adj<T, DRONE>(g.a0.f, L[k].idx, gs[k]);
 }
 
 // ---------------------------------------------------------------------- launchers
 
+// Threads of the movable-body kernels' workgroup (one per agent slot, at most 1024 agents).
 template <typename T> inline int wide_threads(int A) { return ((A + 63) / 64) * 64; }
 
 template <typename T> size_t wide_shm(const Cst<T> &C, bool boxes = false)
 {
-    const int AP = wide_threads<T>(C.A), NC = C.grid_bins > 0 ? C.grid_bins * C.grid_bins : 0;
+    const int AP = wide_geom(C.A).slots, NC = C.grid_bins > 0 ? C.grid_bins * C.grid_bins : 0;
     return boxes ? wide_box_lds_bytes<T>(AP, NC) : wide_lds_bytes<T>(AP, NC);
 }
 
@@ -731,7 +844,7 @@ template <typename T>
 void launch_wide_lists(const Cst<T> &C, const T *pos, const T *frame, int32_t *idx, int32_t *cnt,
                        int32_t *tru, hipStream_t st)
 {
-    const dim3 grid(C.E), block(wide_threads<T>(C.A));
+    const dim3 grid(C.E), block(wide_geom(C.A).threads);
     const size_t shm = wide_shm<T>(C);
     if (C.grid_bins > 0)
         hipLaunchKernelGGL((k_wide_lists<T, true>), grid, block, shm, st, C, pos, frame, idx, cnt, tru);
@@ -746,35 +859,59 @@ void launch_grid_frame(const T *pos, int64_t n, T radius, int bins, T *frame, hi
 }
 
 // boxes: a box world (box agents or wheel contacts; never with drones).
-#define SWARP_WIDE_DISPATCH(KERNEL)                                                                   \
-    if (drone) {                                                                                      \
-        if (grid) hipLaunchKernelGGL((KERNEL<T, true, true, false, FT_ALL>), g, b, shm, st, C, a);    \
-        else hipLaunchKernelGGL((KERNEL<T, true, false, false, FT_ALL>), g, b, shm, st, C, a);        \
-    } else if (boxes) {                                                                               \
-        if (grid) hipLaunchKernelGGL((KERNEL<T, false, true, true, FT_ALL>), g, b, shm, st, C, a);    \
-        else hipLaunchKernelGGL((KERNEL<T, false, false, true, FT_ALL>), g, b, shm, st, C, a);        \
-    } else {                                                                                          \
-        if (grid) hipLaunchKernelGGL((KERNEL<T, false, true, false, FT_ALL>), g, b, shm, st, C, a);   \
-        else hipLaunchKernelGGL((KERNEL<T, false, false, false, FT_ALL>), g, b, shm, st, C, a);       \
+#define SWARP_WIDE_DISPATCH_APT(KERNEL, APT)                                                           \
+    if (drone) {                                                                                       \
+        if (grid) hipLaunchKernelGGL((KERNEL<T, true, true, false, APT, FT_ALL>), g, b, shm, st, C, a);  \
+        else hipLaunchKernelGGL((KERNEL<T, true, false, false, APT, FT_ALL>), g, b, shm, st, C, a);      \
+    } else if (boxes) {                                                                                \
+        if (grid) hipLaunchKernelGGL((KERNEL<T, false, true, true, APT, FT_ALL>), g, b, shm, st, C, a);  \
+        else hipLaunchKernelGGL((KERNEL<T, false, false, true, APT, FT_ALL>), g, b, shm, st, C, a);      \
+    } else {                                                                                           \
+        if (grid) hipLaunchKernelGGL((KERNEL<T, false, true, false, APT, FT_ALL>), g, b, shm, st, C, a); \
+        else hipLaunchKernelGGL((KERNEL<T, false, false, false, APT, FT_ALL>), g, b, shm, st, C, a);     \
     }
-
-template <typename T>
-void launch_wide_fwd(bool drone, bool boxes, const Cst<T> &C, const Args<T> &a, hipStream_t st)
+// The launchers of one agents-per-thread count (each count its own compilation unit).
+template <typename T, int APT>
+void launch_wide_fwd_apt(bool drone, bool boxes, const Cst<T> &C, const Args<T> &a,
+                         hipStream_t st)
 {
-    const dim3 g(C.E), b(wide_threads<T>(C.A));
+    const dim3 g(C.E), b(wide_geom(C.A).threads);
     const size_t shm = wide_shm<T>(C, boxes);
     const bool grid = C.grid_bins > 0;
-    SWARP_WIDE_DISPATCH(k_wide_fwd)
+    SWARP_WIDE_DISPATCH_APT(k_wide_fwd, APT)
+}
+
+template <typename T, int APT>
+void launch_wide_bwd_apt(bool drone, bool boxes, const Cst<T> &C, const Args<T> &a,
+                         hipStream_t st)
+{
+    const dim3 g(C.E), b(wide_geom(C.A).threads);
+    const size_t shm = wide_shm<T>(C, boxes);
+    const bool grid = C.grid_bins > 0;
+    SWARP_WIDE_DISPATCH_APT(k_wide_bwd, APT)
+}
+#undef SWARP_WIDE_DISPATCH_APT
+
+template <typename T>
+inline void launch_wide_fwd(bool drone, bool boxes, const Cst<T> &C, const Args<T> &a,
+                            hipStream_t st)
+{
+    switch (wide_geom(C.A).apt) {
+    case 1: launch_wide_fwd_apt<T, 1>(drone, boxes, C, a, st); break;
+    case 2: launch_wide_fwd_apt<T, 2>(drone, boxes, C, a, st); break;
+    default: launch_wide_fwd_apt<T, 4>(drone, boxes, C, a, st); break;
+    }
 }
 
 template <typename T>
-void launch_wide_bwd(bool drone, bool boxes, const Cst<T> &C, const Args<T> &a, hipStream_t st)
+inline void launch_wide_bwd(bool drone, bool boxes, const Cst<T> &C, const Args<T> &a,
+                            hipStream_t st)
 {
-    const dim3 g(C.E), b(wide_threads<T>(C.A));
-    const size_t shm = wide_shm<T>(C, boxes);
-    const bool grid = C.grid_bins > 0;
-    SWARP_WIDE_DISPATCH(k_wide_bwd)
+    switch (wide_geom(C.A).apt) {
+    case 1: launch_wide_bwd_apt<T, 1>(drone, boxes, C, a, st); break;
+    case 2: launch_wide_bwd_apt<T, 2>(drone, boxes, C, a, st); break;
+    default: launch_wide_bwd_apt<T, 4>(drone, boxes, C, a, st); break;
+    }
 }
-#undef SWARP_WIDE_DISPATCH
 
 }  // namespace swarp

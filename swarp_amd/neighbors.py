@@ -61,12 +61,20 @@ def fill_list_order(d, method: str, n_agents: int, uniform_bins: int | None, bou
         d.neighbor_method = _lib.LISTS_BRUTE
 
 
+def wide_slots(n_agents: int) -> int:
+    """Agent slots of an env's workgroup (``wide_geom``): 64-agent granules spread over at
+    most 1024 threads, 1, 2 or 4 agents per thread."""
+    ap = -(-n_agents // 64) * 64
+    apt = -(-ap // 1024)
+    apt = 4 if apt == 3 else apt
+    return -(-(-(-ap // apt)) // 64) * 64 * apt
+
+
 def _check_bins(bins: int, n_agents: int) -> None:
     """The cell table (bins^2 + 1 offsets) and the env's float32 agent staging (44 B per
     agent slot) share one workgroup's 160 KiB of LDS (``wide_lds_bytes``); float64 and box
     worlds stage more, which the library checks at the call."""
-    slots = -(-n_agents // 64) * 64
-    if slots * 44 + (bins * bins + 1) * 4 + 64 > 163840:
+    if wide_slots(n_agents) * 44 + (bins * bins + 1) * 4 + 64 > 163840:
         raise NotImplementedError(
             f"uniform_bins={bins}: {bins * bins} cells per env with {n_agents} agents exceed "
             "the 160 KiB of LDS of the workgroup that holds an env")

@@ -265,6 +265,10 @@ class Stepper:
         movable = obs.any_movable
         if movable and self.has_boxes:
             raise NotImplementedError("movable bodies with box agents are not implemented")
+        if movable and self.n_agents > 1024:
+            raise NotImplementedError(
+                "movable bodies step at most 1024 agents per env (one thread per agent in the "
+                "env's workgroup)")
         self.obstacles = obstacles
         self.n_obstacles = n
         self._obs_envs = n_envs

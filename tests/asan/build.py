@@ -29,7 +29,7 @@ FLAGS = ["-std=c++17", "-O1", "-g", "-fno-omit-frame-pointer", "-fsanitize=addre
          "-Wno-unused-result", "-Wno-ignored-attributes", "-Wno-attributes"]
 UNITS = [("swarp_hip", "swarp_hip.hip", [])]
 for fam in ("k_generic", "k_drone", "k_boxes", "k_holo", "k_bodies", "k_nav", "k_wide",
-            "k_wbodies"):
+            "k_wide2", "k_wide4", "k_wbodies"):
     for tag, ctype, is32 in (("f32", "float", "1"), ("f64", "double", "0")):
         UNITS.append((f"{fam}.{tag}", f"{fam}.hip", [f"-DSWARP_T={ctype}", f"-DSWARP_T_IS_F32={is32}"]))
 

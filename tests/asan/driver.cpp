@@ -294,6 +294,8 @@ int main(int argc, char **argv)
         {"wide boxes f64 A=66",   2, 66, 2, 2, 8, 2, 2, false, true, true, false, false, false, 1},
         {"wide wheel f32 A=72",   2, 72, 3, 2, 8, 2, 3, false, true, true, false, false, false, 1,
          false, false, false, true},
+        {"wide 2 per lane f32 A=1100", 1, 1100, 2, 2, 8, 2, 2, false, false, true, false, false, false, 1},
+        {"wide 4 per lane grid f32 A=2100", 1, 2100, 2, 1, 8, 2, 0, false, false, true, false, false, true, 0},
     };
     int bad = 0;
     for (const Case &c : cases) {

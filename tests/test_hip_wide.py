@@ -32,7 +32,8 @@ def _lists(g, pos):
             g.neighbor_true_count.cpu().numpy())
 
 
-@pytest.mark.parametrize("A,K,r", [(100, 16, 0.3), (256, 8, 0.5), (1024, 32, 0.15)])
+@pytest.mark.parametrize("A,K,r", [(100, 16, 0.3), (256, 8, 0.5), (1024, 32, 0.15),
+                                   (1500, 16, 0.1), (3000, 12, 0.08)])
 def test_wide_brute_lists_bitexact(A, K, r):
     E = 5
     rng = np.random.default_rng(A)
@@ -46,7 +47,8 @@ def test_wide_brute_lists_bitexact(A, K, r):
 
 @pytest.mark.parametrize("A,pinned,extent,K", [(600, False, 2.2, 16), (600, True, 2.2, 16),
                                                (40, False, 2.2, 16), (1000, True, 2.2, 16),
-                                               (600, True, 1.0, 6)])
+                                               (600, True, 1.0, 6), (2500, True, 2.2, 8),
+                                               (1200, False, 1.0, 6)])
 def test_grid_lists_bitexact(A, pinned, extent, K):
     """extent 1.0 with K = 6: most lists are capped, so the order decides the members."""
     E, r = 3, 0.15
@@ -177,6 +179,36 @@ def test_wide_step_grid_100_bins():
     hip = hip_run(st, s0, acts, w, np.float32)
     orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np.float32)
     _check("grid A=600 bins=100", hip, orc)
+
+
+@pytest.mark.parametrize("A,method,np_dtype", [(1500, "brute", np.float32),
+                                               (3000, "uniform_grid", np.float32),
+                                               (1100, "uniform_grid", np.float64)])
+def test_wide_step_beyond_1024_agents(A, method, np_dtype):
+    """Envs of more than 1024 agents: 2 or 4 agents per thread of the env's workgroup
+    (1100 and 1500: 2 per thread; 3000: 4).  A mixed fleet among obstacles inside soft
+    walls, lists capped at K = 6; states bit-exact with the oracle, gradients within the
+    bars."""
+    E, T, S = 1, 3, 2
+    rng = np.random.default_rng(A)
+    h = A // 2
+    cfgs = ([AgentConfig(radius=0.02) for _ in range(h)]
+            + [AgentConfig(model=DynamicsModel.DIFF_DRIVE, radius=0.02) for _ in range(A - h)])
+    world = WorldConfig(collision_k=100.0, collision_c=1.0, collision_margin=0.01,
+                        bounds=(-1.6, 1.6, -1.6, 1.6), max_neighbors=6, neighbor_radius=0.08,
+                        neighbor_method=method)
+    s0 = pack_state({"pos": rng.uniform(-1.5, 1.5, size=(E, A, 2)),
+                     "theta": rng.uniform(-np.pi, np.pi, size=(E, A))}).astype(np_dtype)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np_dtype)
+    w = _cot(T, E, A, A + 1)
+    obs = _obstacles(E, rng)
+    td = torch.float32 if np_dtype == np.float32 else torch.float64
+    st = make_stepper(cfgs, world, 0.05, S, td, obs=obs, n_envs=E)
+    assert st.wide
+    hip = hip_run(st, s0, acts, w, np_dtype)
+    orc = oracle_run(cfgs, world, 0.05, S, s0, acts, w, np_dtype, obs=obs)
+    f32 = np_dtype == np.float32
+    _check(f"wide A={A} {method}", hip, orc, g_tol=1e-5 if f32 else 1e-12, exact=f32)
 
 def test_grid_step_small_env():
     """A 32-agent env with uniform_grid lists asked for explicitly (the wide kernels serve

@@ -82,7 +82,7 @@ def test_library_rejects_bad_descriptor_without_gpu():
     assert rc != 0 and b"abi_version" in lib.swarp_last_error()
     d.abi_version = _lib.ABI_VERSION
     d.dtype = 0
-    d.n_envs, d.n_agents, d.act_dim, d.substeps = 1, 1025, 2, 1
+    d.n_envs, d.n_agents, d.act_dim, d.substeps = 1, 4097, 2, 1
     rc = lib.swarp_rollout_fwd(ctypes.byref(d), 1, ctypes.byref(s), None, None, ctypes.byref(s), None)
     assert rc != 0 and b"n_agents" in lib.swarp_last_error()
     # per-env agent rows with moving bodies need the shared table for the body pass
@@ -302,8 +302,14 @@ def test_list_method_resolution_and_grid_frame():
         NeighborGrid(2, 8, radius=0.5, device="cpu", method="uniform_grid", uniform_bins=0)
     with pytest.raises(NotImplementedError, match="HashGrid"):
         NeighborGrid(2, 8, radius=0.5, device="cpu", method="grid")
-    with pytest.raises(NotImplementedError, match="1024"):
-        NeighborGrid(2, 1025, radius=0.5, device="cpu")
+    with pytest.raises(NotImplementedError, match="4096"):
+        NeighborGrid(2, 4097, radius=0.5, device="cpu")
+    NeighborGrid(2, 3000, radius=0.5, device="cpu")  # 4 agents per thread
+    with pytest.raises(NotImplementedError, match="1024 agents"):
+        big_bodies = Stepper([AgentConfig(radius=0.01) for _ in range(1100)], device="cpu",
+                             world=WorldConfig(bounds=(-5.0, 5.0, -5.0, 5.0)))
+        big_bodies.set_obstacles(Obstacles(pos=torch.zeros(1, 1, 2), radius=torch.ones(1),
+                                           kind=torch.ones(1, dtype=torch.int32)))
     # stepping: more than 64 agents or grid lists take the wide-env kernels
     big = Stepper([AgentConfig(radius=0.02) for _ in range(600)], device="cpu",
                   world=WorldConfig(bounds=(-2.0, 2.0, -2.0, 2.0)))
