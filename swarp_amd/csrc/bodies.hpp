@@ -446,9 +446,10 @@ __device__ __forceinline__ typename MaskT<PA>::type forces_b(
             const int b = m_ctz(m);
             m &= m - 1;
             const int j = L.base + b;
+            const T dx = st.px - lx[j], dy = st.py - ly[j], md = ra + lr[j] + C.margin;
+            if (pair_apart(dx, dy, md)) continue;  // adds exactly +0 (fx is never -0)
             T gx, gy;
-            pair_force(C, st.px - lx[j], st.py - ly[j], st.vx - lvx[j], st.vy - lvy[j],
-                       ra + lr[j] + C.margin, L.ddv, gx, gy);
+            pair_force(C, dx, dy, st.vx - lvx[j], st.vy - lvy[j], md, L.ddv, gx, gy);
             fx += gx;
             fy += gy;
         }
@@ -1330,13 +1331,15 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
                         const int b = m_ctz(m);
                         m &= m - 1;
                         const int j = L.base + b;
+                        const T dx = in.px - lx[j], dy = in.py - ly[j];
+                        const T md = L.pr.radius + lr[j] + C.margin;
+                        if (pair_apart(dx, dy, md)) continue;  // no contact: nothing to add
                         const bool own = in_list(mine, b, C.K);
                         const bool rev = in_list(lmask[s * 64 + j], L.agent, C.K);
                         if (!own && !rev) continue;
                         const T wx = (own ? wFx : T(0)) - (rev ? lgx[j] : T(0));
                         const T wy = (own ? wFy : T(0)) - (rev ? lgy[j] : T(0));
-                        pair_adj_combined(C, in.px - lx[j], in.py - ly[j], in.vx - lvx[j],
-                                          in.vy - lvy[j], L.pr.radius + lr[j] + C.margin, wx, wy,
+                        pair_adj_combined(C, dx, dy, in.vx - lvx[j], in.vy - lvy[j], md, wx, wy,
                                           gi.px, gi.py, gi.vx, gi.vy);
                     }
                 }

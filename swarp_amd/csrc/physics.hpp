@@ -266,6 +266,16 @@ __device__ __forceinline__ void normal_coeff_adj(const Cst<T> &C, T ov, T vn, T 
     }
 }
 
+// Whether a pair at offset (dx, dy) is certainly apart at contact distance md: its
+// squared distance, computed as pair_force computes it, exceeds md^2 by more than the
+// roundings of md * md, so the correctly rounded distance is at least md and neither
+// pair_force nor its reverses take their contact branch.  Lets a list wider than the
+// contact reach skip its far members before their square root.
+template <typename T> __device__ __forceinline__ bool pair_apart(T dx, T dy, T md)
+{
+    return dx * dx + dy * dy > md * md * T(1.000001);
+}
+
 // pair_force (swarp/core/collisions.py:108-143): force on self, d = self - other
 template <typename T>
 __device__ __forceinline__ void pair_force(const Cst<T> &C, T dx, T dy, T rvx, T rvy, T md,
