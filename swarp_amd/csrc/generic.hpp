@@ -112,6 +112,8 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> Cin, const Args
 // (swarp/core/collisions.py:852-880, 781-815), so the bits are k_rollout_fwd's.  The
 // obstacle pass is about half of such a step; on its own wave it overlaps the agent wave's
 // work and doubles the resident waves of a launch that is latency-bound with two.
+constexpr int SPLIT_TAIL_MAX = 2;  // obstacles the two-wave forward's agent wave may take
+
 template <typename T, int PA, unsigned F>
 __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, const Args<T> g)
 {
@@ -132,6 +134,9 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
     const T *opos = ob_pose_table<T, PA>(C, g, L, opos_lds);
     const T *ocs = ob_trig_table<T, PA>(C, g, L, ocs_lds);
     const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
+    // the last NT obstacles go to the agent wave, which adds their forces to the obstacle
+    // wave's sum in index order (the same sum): it balances the two waves' work
+    const int NT = C.N / 4 < SPLIT_TAIL_MAX ? C.N / 4 : SPLIT_TAIL_MAX;
     St<T> st;
     load_state<T, false>(g.s0.f, L.idx, 0, st);
     if (!L.real) st.px = st.py = __builtin_nan("");
@@ -157,7 +162,7 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
                 const T px = sl[F_PX * 64 + L.lane], py = sl[F_PY * 64 + L.lane];
                 const T vx = sl[F_VX * 64 + L.lane], vy = sl[F_VY * 64 + L.lane];
                 T sx = T(0), sy = T(0);
-                for (int o = 0; o < C.N; ++o) {
+                for (int o = 0; o < C.N - NT; ++o) {
                     T gx, gy;
                     obstacle_force<T, Dv<T>, true>(C, g.obs, eN, o, px, py, vx, vy, L.pr.radius,
                                                    L.ddv, gx, gy, ocs, opos);
@@ -166,15 +171,19 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
                 }
                 lso[L.lane] = sx;
                 lso[64 + L.lane] = sy;
-                if (g.osum && L.active) {
-                    T *const o2 = g.osum + 2 * (((size_t)t * C.S + s) * EA + L.idx);
-                    o2[0] = sx;
-                    o2[1] = sy;
-                }
             }
             T fx = T(0), fy = T(0), wx = T(0), wy = T(0);
+            T tfx[SPLIT_TAIL_MAX], tfy[SPLIT_TAIL_MAX];  // the tail obstacles' forces
             M incl = 0;
             if (agent_wave) {
+#pragma unroll
+                for (int k = 0; k < SPLIT_TAIL_MAX; ++k) {
+                    tfx[k] = tfy[k] = T(0);
+                    if (k < NT)
+                        obstacle_force<T, Dv<T>, true>(C, g.obs, eN, C.N - NT + k, st.px, st.py,
+                                                       st.vx, st.vy, L.pr.radius, L.ddv, tfx[k],
+                                                       tfy[k], ocs, opos);
+                }
                 if (C.collisions) {
                     const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64;
                     const T *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
@@ -207,6 +216,17 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
             __syncthreads();  // the obstacle sums are in lso
             if (agent_wave) {
                 T sx = lso[L.lane], sy = lso[64 + L.lane];
+#pragma unroll
+                for (int k = 0; k < SPLIT_TAIL_MAX; ++k)
+                    if (k < NT) {
+                        sx += tfx[k];
+                        sy += tfy[k];
+                    }
+                if (g.osum && L.active) {
+                    T *const o2 = g.osum + 2 * (((size_t)t * C.S + s) * EA + L.idx);
+                    o2[0] = sx;
+                    o2[1] = sy;
+                }
                 if (C.soft_walls) {
                     sx += wx;
                     sy += wy;
