@@ -128,15 +128,22 @@ __device__ __forceinline__ uint32_t skin_dpp16(float px, float py, float t, uint
     return __builtin_amdgcn_ubfe(r | (r << 16), rot, 16u);
 }
 
-// Issue priority of a wave from the number of its lanes with contact or wall work in a
-// step: a launch ends with its slowest waves, the ones whose envs are crowded, so such a
-// wave issues ahead of the lighter waves sharing its SIMD (which have time to spare).
-// s_setprio orders instruction issue between waves only; no result depends on it.
-__device__ __forceinline__ void busy_priority(int busy_lanes)
+// Issue priority of a wave from its progress through the rollout (`done` of `total`
+// steps).  The waves of these launches all start together, several share each SIMD, and
+// the launch ends with its slowest wave: per-wave timing copies of the config-2 forward
+// show wave durations spread from 0.65x to 1.0x of the launch, barely correlated with the
+// waves' own contact work (r = 0.26) -- the spread comes from the waves a wave shares its
+// SIMD with.  A wave that has fallen behind its neighbours therefore issues ahead of them,
+// so the waves of a SIMD finish together instead of leaving one to run alone.  Levels by
+// the fraction done: [0, 1/2) 3, [1/2, 3/4) 2, [3/4, 7/8) 1, then 0 (measured against even
+// quarters, against later bands and against a priority from the step's own contact count).
+// s_setprio orders instruction issue between the waves of one SIMD; no result depends on it.
+__device__ __forceinline__ void progress_priority(int done, int total)
 {
-    if (busy_lanes >= 24) __builtin_amdgcn_s_setprio(3);
-    else if (busy_lanes >= 16) __builtin_amdgcn_s_setprio(2);
-    else if (busy_lanes >= 8) __builtin_amdgcn_s_setprio(1);
+    const int q8 = (8 * done) / total;
+    if (q8 < 4) __builtin_amdgcn_s_setprio(3);
+    else if (q8 < 6) __builtin_amdgcn_s_setprio(2);
+    else if (q8 < 7) __builtin_amdgcn_s_setprio(1);
     else __builtin_amdgcn_s_setprio(0);
 }
 
@@ -351,8 +358,7 @@ __global__ __launch_bounds__(64) void k_holo_fwd(const Cst<T> C, const Args<T> g
                 }
                 lean_forces<T, PA, SAT>(C, lp, lv, lr, base, me, ra, ddv, p.x, p.y, v.x, v.y,
                                         s == 0 || !ok, s == 0, cand, incl, act, wb, Fx, Fy);
-                // this step's work: the lanes with skin candidates or a wall contact
-                if (s == 0) busy_priority(__builtin_popcountll(__ballot(cand != 0 || wb != 0u)));
+                if (s == 0) progress_priority(t, g.nsteps);
             }
             const T vnx = cnx + Fx * dtm, vny = cny + Fy * dtm;
             const T pnx = p.x + vnx * dt, pny = p.y + vny * dt;
@@ -522,15 +528,7 @@ __global__ __launch_bounds__(64) void k_holo_bwd(const Cst<T> C, const Args<T> g
         T cnx, cny;
         clamp_norm(a.x, a.y, vmax, cnx, cny);
         const P2<T> vin = v;
-        if (TAPE) {
-            // this step's work: the lanes on which a contact or wall force acted
-            bool busy = false;
-#pragma unroll
-            for (int s = 0; s < TAPE_MAX_S; ++s)
-                if (s < S)
-                    busy = busy || vel_stored<PA>(rec_get<W>(tc.c, TR::OM + s * (int)sizeof(W)), me);
-            busy_priority(__builtin_popcountll(__ballot(busy)));
-        }
+        progress_priority(g.nsteps - 1 - t, g.nsteps);
 
         // ---- the substeps of step t into LDS: from the tape, or recomputed
         if (TAPE) {
