@@ -888,6 +888,7 @@ __global__ __launch_bounds__(64, body_fwd_waves(PA, sizeof(T), F)) void k_body_f
     for (int t = 0; t < g.nsteps; ++t) {
         T an[4] = {a[0], a[1], a[2], a[3]};
         if (t + 1 < g.nsteps) load_act(g.act, (size_t)(t + 1) * EA + L.idx, C.ad, an);
+        progress_priority(t, g.nsteps);
         M cand = 0;
         T D = T(0);
         bool ok = false;
@@ -1244,6 +1245,7 @@ __global__ __launch_bounds__(64, body_bwd_waves(PA, sizeof(T), F)) void k_body_b
             add_adj<T, DRONE>(g.afin.f, L.idx, gs);
         else
             add_adj<T, DRONE>(g.atraj.f, (size_t)t * EA + L.idx, gs);
+        progress_priority(g.nsteps - 1 - t, g.nsteps);
         wave_lds_sync();
         if (io.atraj && env_ok)
             for (int q = L.agent; q < NW; q += PA) gob[q] += io.atraj[(size_t)t * ENW + eo + q];

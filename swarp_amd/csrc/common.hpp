@@ -39,6 +39,26 @@ __device__ __forceinline__ int m_ctz(uint64_t m) { return __builtin_ctzll(m); }
 __device__ __forceinline__ int m_popc(uint32_t m) { return __builtin_popcount(m); }
 __device__ __forceinline__ int m_popc(uint64_t m) { return __builtin_popcountll(m); }
 
+// Issue priority of a wave from its progress through the rollout (`done` of `total`
+// steps), for the rollout kernels that keep several waves per SIMD.  Their waves start
+// together and the launch ends with its slowest wave: per-wave timing copies of the
+// config-2 forward show wave durations spread from 0.65x to 1.0x of the launch, barely
+// correlated with the waves' own contact work (r = 0.26) -- the spread comes from the
+// waves a wave shares its SIMD with.  A wave that has fallen behind its neighbours
+// therefore issues ahead of them, so the waves of a SIMD finish together instead of
+// leaving one to run alone.  Levels by the fraction done: [0, 1/2) 3, [1/2, 3/4) 2,
+// [3/4, 7/8) 1, then 0 (measured against even quarters, against later bands and against
+// a priority from the step's own contact count).  s_setprio orders instruction issue
+// between the waves of one SIMD; no result depends on it.
+__device__ __forceinline__ void progress_priority(int done, int total)
+{
+    const int d8 = 8 * done;  // d8 < k * total <=> the fraction done is below k / 8
+    if (d8 < 4 * total) __builtin_amdgcn_s_setprio(3);
+    else if (d8 < 6 * total) __builtin_amdgcn_s_setprio(2);
+    else if (d8 < 7 * total) __builtin_amdgcn_s_setprio(1);
+    else __builtin_amdgcn_s_setprio(0);
+}
+
 // Field pointers of one state; strides (in scalars) 2,1,2,1,1,1,1,4,3.
 template <typename T> struct Fields {
     T *f[9];

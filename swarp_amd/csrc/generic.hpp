@@ -44,6 +44,8 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> Cin, const Args
     T a[4];
     load_act(g.act, L.idx, C.ad, a);
     for (int t = 0; t < g.nsteps; ++t) {
+        // no progress_priority: this kernel's main user, the quadrotor fleet, runs one wave
+        // per SIMD, and the priority switches cost it 3 % there
         T an[4] = {a[0], a[1], a[2], a[3]};
         if (t + 1 < g.nsteps) load_act(g.act, (size_t)(t + 1) * EA + L.idx, C.ad, an);
         M cand = 0;
@@ -144,6 +146,7 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
     T a[4] = {T(0), T(0), T(0), T(0)};  // the step's action, loaded one step ahead
     if (agent_wave) load_act(g.act, L.idx, C.ad, a);
     for (int t = 0; t < g.nsteps; ++t) {
+        progress_priority(t, g.nsteps);
         T an[4] = {a[0], a[1], a[2], a[3]};
         if (agent_wave && t + 1 < g.nsteps) load_act(g.act, (size_t)(t + 1) * EA + L.idx, C.ad, an);
         M cand = 0;
@@ -410,6 +413,7 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> Cin, const Args
         atf[k] = vgpr_ptr(g.atraj.f[k]);
     }
     for (int t = g.nsteps - 1; t >= 0; --t) {
+        progress_priority(g.nsteps - 1 - t, g.nsteps);
         if (t == g.nsteps - 1)
             add_adj<T, DRONE>(g.afin.f, L.idx, gs);
         else

@@ -128,25 +128,6 @@ __device__ __forceinline__ uint32_t skin_dpp16(float px, float py, float t, uint
     return __builtin_amdgcn_ubfe(r | (r << 16), rot, 16u);
 }
 
-// Issue priority of a wave from its progress through the rollout (`done` of `total`
-// steps).  The waves of these launches all start together, several share each SIMD, and
-// the launch ends with its slowest wave: per-wave timing copies of the config-2 forward
-// show wave durations spread from 0.65x to 1.0x of the launch, barely correlated with the
-// waves' own contact work (r = 0.26) -- the spread comes from the waves a wave shares its
-// SIMD with.  A wave that has fallen behind its neighbours therefore issues ahead of them,
-// so the waves of a SIMD finish together instead of leaving one to run alone.  Levels by
-// the fraction done: [0, 1/2) 3, [1/2, 3/4) 2, [3/4, 7/8) 1, then 0 (measured against even
-// quarters, against later bands and against a priority from the step's own contact count).
-// s_setprio orders instruction issue between the waves of one SIMD; no result depends on it.
-__device__ __forceinline__ void progress_priority(int done, int total)
-{
-    const int q8 = (8 * done) / total;
-    if (q8 < 4) __builtin_amdgcn_s_setprio(3);
-    else if (q8 < 6) __builtin_amdgcn_s_setprio(2);
-    else if (q8 < 7) __builtin_amdgcn_s_setprio(1);
-    else __builtin_amdgcn_s_setprio(0);
-}
-
 // One substep of the force pass: neighbour lists (into `incl`) and the total force.
 // Also records which listed contacts are active (`act`) and the wall contact bits, the
 // branches the reverse pass follows.  SAT: contact_max_overlap > 0 (the tanh law).
