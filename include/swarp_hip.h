@@ -184,7 +184,11 @@ int swarp_rollout_bwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *
  * fleets among static obstacles whose forward runs the obstacle pass on a wave of its own
  * (at most 256 / (envs per 64 lanes) obstacles, no box agents, wheel contacts or drones):
  * there the tape holds each substep's per-agent obstacle force sum, 8 T S E A bytes
- * (rounded up to 256), which the backward reads instead of evaluating the obstacles. */
+ * (rounded up to 256), which the backward reads instead of evaluating the obstacles, and
+ * for at most 32 obstacles each substep's per-agent mask of the obstacles in contact,
+ * w T S E A bytes more (w = 1, 2 or 4 for up to 8, 16 or 32 obstacles; each part rounded
+ * up to 256), so that the backward reverses only those.  The taped backward gives the
+ * untaped one's values; a gradient that is zero may differ in the sign of that zero. */
 int swarp_tape_bytes(const swarp_desc_t *desc, int32_t T, uint64_t *bytes);
 
 /* swarp_rollout_fwd that also writes the tape (`tape_bytes` must be
@@ -195,7 +199,8 @@ int swarp_rollout_fwd_tape(const swarp_desc_t *desc, int32_t T, const swarp_stat
                            void *stream);
 
 /* swarp_rollout_bwd reading the substep intermediates from the tape written by
- * swarp_rollout_fwd_tape on the same inputs (same results, bit for bit). */
+ * swarp_rollout_fwd_tape on the same inputs (same results; see swarp_tape_bytes for the
+ * sign of zero gradients under the obstacle tape). */
 int swarp_rollout_bwd_tape(const swarp_desc_t *desc, int32_t T, const swarp_state_t *state0,
                            const void *actions, const swarp_state_t *traj,
                            const swarp_state_t *adj_traj, const swarp_state_t *adj_final,

@@ -84,7 +84,36 @@ template <typename T> struct Args {
     // obstacles' forces, [T][S][E A] pairs -- written by the two-wave forward, read by the
     // backward's recompute in place of evaluating the obstacles again.
     T *osum;
+    // Obstacle-contact tape (nullable, with osum, at most 32 obstacles): per step, substep
+    // and agent a mask of the obstacles whose narrow phase took its contact branch, bit o
+    // for obstacle o, [T][S][E A] words of omask_bytes(N) bytes, written by the two-wave
+    // forward's obstacle wave for the obstacles it evaluates (all but the last few, which
+    // its agent wave takes) -- the backward reverses only those and the last few (the
+    // others' reverses add zeros at most).
+    void *omask;
 };
+
+// Width of one obstacle-contact mask word for N obstacles (0: no mask above 32).
+__host__ __device__ constexpr int omask_bytes(int N)
+{
+    return N <= 8 ? 1 : (N <= 16 ? 2 : (N <= 32 ? 4 : 0));
+}
+
+__device__ __forceinline__ void omask_put(void *base, int N, size_t k, uint32_t m)
+{
+    const int w = omask_bytes(N);
+    if (w == 1) ((uint8_t *)base)[k] = (uint8_t)m;
+    else if (w == 2) ((uint16_t *)base)[k] = (uint16_t)m;
+    else ((uint32_t *)base)[k] = m;
+}
+
+__device__ __forceinline__ uint32_t omask_get(const void *base, int N, size_t k)
+{
+    const int w = omask_bytes(N);
+    if (w == 1) return ((const uint8_t *)base)[k];
+    if (w == 2) return ((const uint16_t *)base)[k];
+    return ((const uint32_t *)base)[k];
+}
 
 __device__ __forceinline__ int fstride(int k)
 {

@@ -115,6 +115,11 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> Cin, const Args
 // obstacle pass is about half of such a step; on its own wave it overlaps the agent wave's
 // work and doubles the resident waves of a launch that is latency-bound with two.
 constexpr int SPLIT_TAIL_MAX = 2;  // obstacles the two-wave forward's agent wave may take
+// How many of N obstacles (the last ones) the agent wave takes.
+__device__ __forceinline__ int split_tail(int N)
+{
+    return N / 4 < SPLIT_TAIL_MAX ? N / 4 : SPLIT_TAIL_MAX;
+}
 
 template <typename T, int PA, unsigned F>
 __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, const Args<T> g)
@@ -124,6 +129,7 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
     __shared__ T sl[7 * 64];  // px py vx vy of the current substep (F_* rows)
     __shared__ T lr[64];      // agent radius per lane
     __shared__ T lso[2 * 64]; // the obstacle wave's sums: x row, y row
+    __shared__ uint32_t lom[2 * 64];  // obstacles in contact: obstacle wave's, agent wave's
     __shared__ T ocs_lds[2 * OCS_MAX];
     // the env slots' obstacle poses and bounds (the launcher runs this kernel only when
     // the per-launch obstacle tables fit)
@@ -138,7 +144,7 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
     const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
     // the last NT obstacles go to the agent wave, which adds their forces to the obstacle
     // wave's sum in index order (the same sum): it balances the two waves' work
-    const int NT = C.N / 4 < SPLIT_TAIL_MAX ? C.N / 4 : SPLIT_TAIL_MAX;
+    const int NT = split_tail(C.N);
     St<T> st;
     load_state<T, false>(g.s0.f, L.idx, 0, st);
     if (!L.real) st.px = st.py = __builtin_nan("");
@@ -165,28 +171,34 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
                 const T px = sl[F_PX * 64 + L.lane], py = sl[F_PY * 64 + L.lane];
                 const T vx = sl[F_VX * 64 + L.lane], vy = sl[F_VY * 64 + L.lane];
                 T sx = T(0), sy = T(0);
+                uint32_t om = 0u;  // obstacles in contact (kept for at most 32)
                 for (int o = 0; o < C.N - NT; ++o) {
                     T gx, gy;
-                    obstacle_force<T, Dv<T>, true>(C, g.obs, eN, o, px, py, vx, vy, L.pr.radius,
-                                                   L.ddv, gx, gy, ocs, opos);
+                    if (obstacle_force<T, Dv<T>, true>(C, g.obs, eN, o, px, py, vx, vy,
+                                                       L.pr.radius, L.ddv, gx, gy, ocs, opos))
+                        om |= 1u << (o & 31);
                     sx += gx;
                     sy += gy;
                 }
                 lso[L.lane] = sx;
                 lso[64 + L.lane] = sy;
+                lom[L.lane] = om;
             }
             T fx = T(0), fy = T(0), wx = T(0), wy = T(0);
             T tfx[SPLIT_TAIL_MAX], tfy[SPLIT_TAIL_MAX];  // the tail obstacles' forces
             M incl = 0;
             if (agent_wave) {
+                uint32_t omt = 0u;
 #pragma unroll
                 for (int k = 0; k < SPLIT_TAIL_MAX; ++k) {
                     tfx[k] = tfy[k] = T(0);
-                    if (k < NT)
+                    if (k < NT &&
                         obstacle_force<T, Dv<T>, true>(C, g.obs, eN, C.N - NT + k, st.px, st.py,
                                                        st.vx, st.vy, L.pr.radius, L.ddv, tfx[k],
-                                                       tfy[k], ocs, opos);
+                                                       tfy[k], ocs, opos))
+                        omt |= 1u << ((C.N - NT + k) & 31);
                 }
+                lom[64 + L.lane] = omt;
                 if (C.collisions) {
                     const T *lx = sl + F_PX * 64, *ly = sl + F_PY * 64;
                     const T *lvx = sl + F_VX * 64, *lvy = sl + F_VY * 64;
@@ -216,7 +228,10 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
                     wall_force_axes(C, st.px, st.py, st.vx, st.vy, L.pr.radius, L.ddv, wx, wy, wb);
                 }
             }
-            __syncthreads();  // the obstacle sums are in lso
+            __syncthreads();  // the obstacle sums are in lso, the contact masks in lom
+            if (!agent_wave && g.omask && L.active)
+                omask_put(g.omask, C.N, ((size_t)t * C.S + s) * EA + L.idx,
+                          lom[L.lane] | lom[64 + L.lane]);
             if (agent_wave) {
                 T sx = lso[L.lane], sy = lso[64 + L.lane];
 #pragma unroll
@@ -383,6 +398,8 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> Cin, const Args
     T *ldd = lr + 64;           // damping denominator per lane
     T *slots = ldd + 64;        // S slots of NF fields
     M *lmask = (M *)(slots + (size_t)C.S * NF * 64);  // S inclusion masks per lane
+    // worlds without box agents, with the obstacle-contact tape: S contact masks per lane
+    uint32_t *lomk = (uint32_t *)(lmask + (size_t)C.S * 64);
     // box worlds, per substep: the masks of force-exerting box pairs, the cos / sin of
     // every lane's heading, a box agent's force-exerting obstacles (first 64) and flags
     // (1: a wall exerts a force, 2: a later obstacle does)
@@ -448,6 +465,9 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> Cin, const Args
                 bool wl = false, far = false;
                 const T *osum =
                     !BOXES && g.osum ? g.osum + 2 * (((size_t)t * C.S + s) * EA + L.idx) : nullptr;
+                if (!BOXES && g.omask)
+                    lomk[s * 64 + L.lane] =
+                        L.active ? omask_get(g.omask, C.N, ((size_t)t * C.S + s) * EA + L.idx) : 0u;
                 incl = forces<T, PA, BOXES>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy,
                                             ocs, lbx, lcsb + s * 128, &am, &om, &wl, &far, nullptr,
                                             osum);
@@ -532,9 +552,20 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> Cin, const Args
                 } else {
                     if (C.N > 0) {
                         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
-                        for (int o = 0; o < C.N; ++o)
-                            obstacle_force_adj(C, g.obs, eN, o, in.px, in.py, in.vx, in.vy,
-                                               L.pr.radius, L.dd, gFx, gFy, gi, ocs);
+                        if (!BOXES && g.omask) {
+                            // the obstacles in contact at this substep, in index order
+                            uint32_t m = lomk[s * 64 + L.lane];
+                            while (m) {
+                                const int o = __builtin_ctz(m);
+                                m &= m - 1;
+                                obstacle_force_adj(C, g.obs, eN, o, in.px, in.py, in.vx, in.vy,
+                                                   L.pr.radius, L.dd, gFx, gFy, gi, ocs);
+                            }
+                        } else {
+                            for (int o = 0; o < C.N; ++o)
+                                obstacle_force_adj(C, g.obs, eN, o, in.px, in.py, in.vx, in.vy,
+                                                   L.pr.radius, L.dd, gFx, gFy, gi, ocs);
+                        }
                     }
                     if (C.soft_walls)
                         wall_force_adj(C, in.px, in.py, in.vx, in.vy, L.pr.radius, L.dd, gFx,

@@ -276,9 +276,11 @@ template <typename T> __device__ __forceinline__ bool pair_apart(T dx, T dy, T m
     return dx * dx + dy * dy > md * md * T(1.000001);
 }
 
-// pair_force (swarp/core/collisions.py:108-143): force on self, d = self - other
+// pair_force (swarp/core/collisions.py:108-143): force on self, d = self - other.
+// Returns whether the contact branch ran (overlap > 0), the test pair_force_adj repeats
+// on the same operands: it contributes only then.
 template <typename T>
-__device__ __forceinline__ void pair_force(const Cst<T> &C, T dx, T dy, T rvx, T rvy, T md,
+__device__ __forceinline__ bool pair_force(const Cst<T> &C, T dx, T dy, T rvx, T rvy, T md,
                                            T dd, T &fx, T &fy)
 {
     T dist = m_sqrt(wmax(dx * dx + dy * dy, C.eps2));
@@ -291,6 +293,7 @@ __device__ __forceinline__ void pair_force(const Cst<T> &C, T dx, T dy, T rvx, T
         fx = coef * nx;
         fy = coef * ny;
     }
+    return ov > T(0);
 }
 
 // pair_force with the damping denominator as a prepared divisor, in the exact fast
@@ -298,7 +301,7 @@ __device__ __forceinline__ void pair_force(const Cst<T> &C, T dx, T dy, T rvx, T
 // one prepared divisor (a distance outside [2^-60, 2^20] takes the general division).
 // Same bits as pair_force.
 template <typename T>
-__device__ __forceinline__ void pair_force(const Cst<T> &C, T dx, T dy, T rvx, T rvy, T md,
+__device__ __forceinline__ bool pair_force(const Cst<T> &C, T dx, T dy, T rvx, T rvy, T md,
                                            const Dv<T> &dd, T &fx, T &fy)
 {
     T dist = sqrt_rn_big(wmax(dx * dx + dy * dy, C.eps2));
@@ -312,6 +315,7 @@ __device__ __forceinline__ void pair_force(const Cst<T> &C, T dx, T dy, T rvx, T
         fx = coef * nx;
         fy = coef * ny;
     }
+    return ov > T(0);
 }
 
 // pair_force that also reports whether the contact is active (overlap and a positive
@@ -617,9 +621,10 @@ __device__ __forceinline__ void wall_force_adj(const Cst<T> &C, T px, T py, T vx
 // --------------------------------------------------------------- obstacles
 
 // box_force (swarp/core/collisions.py:174-260); reach = agent radius + margin
-// (ca, sa) = cos / sin of the box angle
+// (ca, sa) = cos / sin of the box angle.  Returns whether the contact branch ran, the
+// test box_force_adj_cs repeats on the same operands.
 template <typename T>
-__device__ __forceinline__ void box_force_cs(const Cst<T> &C, T px, T py, T vx, T vy, T cx0,
+__device__ __forceinline__ bool box_force_cs(const Cst<T> &C, T px, T py, T vx, T vy, T cx0,
                                              T cy0, T ca, T sa, T hx, T hy, T reach, T dd,
                                              T vox, T voy, T om, T &fx, T &fy)
 {
@@ -655,12 +660,13 @@ __device__ __forceinline__ void box_force_cs(const Cst<T> &C, T px, T py, T vx, 
         fx = coef * nx;
         fy = coef * ny;
     }
+    return ov > T(0);
 }
 
 // box_force_cs with the damping denominator as a prepared divisor, in the exact fast
 // arithmetic of pair_force's overload (same bits).
 template <typename T>
-__device__ __forceinline__ void box_force_cs(const Cst<T> &C, T px, T py, T vx, T vy, T cx0,
+__device__ __forceinline__ bool box_force_cs(const Cst<T> &C, T px, T py, T vx, T vy, T cx0,
                                              T cy0, T ca, T sa, T hx, T hy, T reach,
                                              const Dv<T> &dd, T vox, T voy, T om, T &fx, T &fy)
 {
@@ -697,6 +703,7 @@ __device__ __forceinline__ void box_force_cs(const Cst<T> &C, T px, T py, T vx, 
         fx = coef * nx;
         fy = coef * ny;
     }
+    return ov > T(0);
 }
 
 template <typename T, typename DD>
@@ -828,19 +835,21 @@ __device__ __forceinline__ bool obstacle_in_reach(const Cst<T> &C, const Obs<T> 
 }
 
 // One obstacle on one agent (_obstacle_forces body, swarp/core/collisions.py:690-743).
+// Returns whether its narrow phase took the contact branch: obstacle_force_adj on the
+// same state contributes only then (elsewhere it adds zeros at most).
 // `cs`: this env's obstacle angles as (cos, sin) pairs [N][2], computed once per launch
 // (the angles do not change within one), or NULL to evaluate them here.
 // DD: the damping denominator as a plain value or as a prepared divisor (Dv<T>, the
 // exact fast arithmetic of the force overloads that take one); the same bits either way.
 template <typename T, typename DD, bool PT = false>
-__device__ __forceinline__ void obstacle_force(const Cst<T> &C, const Obs<T> &O, size_t eN, int o,
+__device__ __forceinline__ bool obstacle_force(const Cst<T> &C, const Obs<T> &O, size_t eN, int o,
                                                T px, T py, T vx, T vy, T ra, const DD &dd, T &fx,
                                                T &fy, const T *cs = nullptr,
                                                const T *pose = nullptr)
 {
     fx = T(0);
     fy = T(0);
-    if (!obstacle_in_reach<T, PT>(C, O, eN, o, px, py, ra, pose)) return;
+    if (!obstacle_in_reach<T, PT>(C, O, eN, o, px, py, ra, pose)) return false;
     const size_t j = eN + o;
     const T *pp = pose + OPOSE_W * o;
     const T cx = PT ? pp[0] : O.pos[2 * j], cy = PT ? pp[1] : O.pos[2 * j + 1];
@@ -851,18 +860,19 @@ __device__ __forceinline__ void obstacle_force(const Cst<T> &C, const Obs<T> &O,
     if (st == 1) {
         T ca, sa;
         ob_trig(O, j, o, cs, ca, sa);
-        box_force_cs(C, px, py, vx, vy, cx, cy, ca, sa, hx, hy, ra + C.margin, dd, vox, voy, om,
-                     fx, fy);
+        return box_force_cs(C, px, py, vx, vy, cx, cy, ca, sa, hx, hy, ra + C.margin, dd, vox,
+                            voy, om, fx, fy);
     } else if (st == 2) {
         T ux, uy;
         ob_trig(O, j, o, cs, ux, uy);
         T t = wclamp((px - cx) * ux + (py - cy) * uy, -hx, hx);
         T qx = cx + t * ux, qy = cy + t * uy;
         T rx = qx - cx, ry = qy - cy;
-        pair_force(C, px - qx, py - qy, vx - (vox + -om * ry), vy - (voy + om * rx),
-                   ra + ro + C.margin, dd, fx, fy);
+        return pair_force(C, px - qx, py - qy, vx - (vox + -om * ry), vy - (voy + om * rx),
+                          ra + ro + C.margin, dd, fx, fy);
     } else {
-        pair_force(C, px - cx, py - cy, vx - vox, vy - voy, ra + ro + C.margin, dd, fx, fy);
+        return pair_force(C, px - cx, py - cy, vx - vox, vy - voy, ra + ro + C.margin, dd, fx,
+                          fy);
     }
 }
 

@@ -272,9 +272,10 @@ static bool lean_ok(const swarp_desc_t *d)
 // Byte offsets of the tape regions (see lean.hpp); total == 0: no tape.  The specialised
 // holonomic kernels keep records (rec) and last velocities (vl); the two-wave forward of
 // 2-D fleets among static obstacles keeps each substep's obstacle force sums (osum, read
-// by the backward's recompute), alone.
+// by the backward's recompute) and, for at most 32 obstacles, each substep's obstacle
+// contact masks (omask, read by its reverse pass).
 struct TapeLayout {
-    uint64_t rec, vl, osum, total;
+    uint64_t rec, vl, osum, omask, total;
 };
 
 static uint64_t align256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
@@ -303,10 +304,12 @@ static bool split_ok(const swarp_desc_t *d)
 
 static TapeLayout tape_layout(const swarp_desc_t *d, int32_t nT)
 {
-    TapeLayout L = {0, 0, 0, 0};
+    TapeLayout L = {0, 0, 0, 0, 0};
     if (nT >= 1 && split_ok(d)) {
+        const uint64_t n = (uint64_t)nT * d->substeps * d->n_envs * d->n_agents;
         L.osum = 0;
-        L.total = align256((uint64_t)nT * d->substeps * d->n_envs * d->n_agents * 2 * sizeof(float));
+        L.omask = align256(n * 2 * sizeof(float));
+        L.total = align256(L.omask + n * omask_bytes(d->n_obstacles));
         return L;
     }
     const bool forces = d->collisions || d->soft_walls;
@@ -353,7 +356,10 @@ static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     if (nT > 1) copy_fields<T>(traj, a.traj.f);
     a.act = (const T *)act;
     a.nsteps = nT;
-    if (tape && TL.total && split_ok(d)) a.osum = (T *)((unsigned char *)tape + TL.osum);
+    if (tape && TL.total && split_ok(d)) {
+        a.osum = (T *)((unsigned char *)tape + TL.osum);
+        if (omask_bytes(d->n_obstacles)) a.omask = (unsigned char *)tape + TL.omask;
+    }
     const int PA = pad_agents(d->n_agents);
     const unsigned feat = world_features(d, false);
     if (wide_path(d)) {
@@ -401,7 +407,10 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     a.act = (const T *)act;
     a.aact = (T *)aact;
     a.nsteps = nT;
-    if (tape && TL.total && split_ok(d)) a.osum = (T *)((unsigned char *)tape + TL.osum);
+    if (tape && TL.total && split_ok(d)) {
+        a.osum = (T *)((unsigned char *)tape + TL.osum);
+        if (omask_bytes(d->n_obstacles)) a.omask = (unsigned char *)tape + TL.omask;
+    }
     const int PA = pad_agents(d->n_agents);
     if (wide_path(d)) {
         if (const char *why = wide_unsupported(d)) return fail(why);
@@ -431,6 +440,8 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
                  (size_t)d->substeps * 64 * msz;
     if (d->has_boxes)  // contact masks, heading cos / sin, static-contact flags per substep
         shm += (size_t)d->substeps * 64 * (msz + 2 * sizeof(T) + 8 + 1);
+    else if (split_ok(d) && omask_bytes(d->n_obstacles))  // obstacle-contact masks per substep
+        shm += (size_t)d->substeps * 64 * sizeof(uint32_t);
     // with k_rollout_bwd's static arrays (ocs_lds[2 OCS_MAX], lbx[3 * 64]): the whole LDS
     if (shm + (2 * OCS_MAX + 3 * 64) * sizeof(T) > LDS_MAX)
         return fail("substeps too large for the backward LDS staging (limit 160 KiB per wave)");

@@ -130,15 +130,19 @@ def _obstacle_world(E, A, n, seed):
     (41, 8, 6, 3, 12),      # eight envs per workgroup, partial last one, S = 3
     (17, 64, 5, 2, 30),     # one env per workgroup, many obstacles
     (23, 4, 4, 1, 16),      # sixteen envs per workgroup at the table's limit, S = 1
+    (9, 40, 4, 2, 40),      # more than 32 obstacles: sums only, no contact masks
 ])
 def test_obstacle_sum_tape_matches_recompute(E, A, T, S, n):
-    """Static obstacles: the forward keeps each substep's obstacle force sums and the
-    backward reads them instead of evaluating the obstacles again -- bit-identical."""
+    """Static obstacles: the forward keeps each substep's obstacle force sums and contact
+    masks, and the backward reads them instead of evaluating the obstacles again and
+    reverses only the obstacles in contact -- the same values."""
     cfgs, world, obs, s0, rng = _obstacle_world(E, A, n, seed=E + n)
     on = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
     off = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
     off.use_tape = False
-    assert on.tape_bytes(E, 2, T) == 2 * 4 * T * S * E * A + (-(2 * 4 * T * S * E * A) % 256)
+    al = lambda x: x + (-x % 256)  # noqa: E731
+    mw = 1 if n <= 8 else (2 if n <= 16 else (4 if n <= 32 else 0))  # contact-mask word
+    assert on.tape_bytes(E, 2, T) == al(al(2 * 4 * T * S * E * A) + mw * T * S * E * A)
     acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
     w = rng.normal(size=(T, E, A, 16)) * 0.1
     w[..., 7:] = 0.0
