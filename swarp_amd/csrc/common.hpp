@@ -80,16 +80,16 @@ template <typename T> struct Args {
     Fields<T> a0;        // adjoint of s0 (nullable per field)
     T *aact;             // adjoint of actions
     int nsteps;
-    // Obstacle-sum tape (nullable): per step, substep and agent the sum of the static
-    // obstacles' forces, [T][S][E A] pairs -- written by the two-wave forward, read by the
-    // backward's recompute in place of evaluating the obstacles again.
-    T *osum;
-    // Obstacle-contact tape (nullable, with osum, at most 32 obstacles): per step, substep
+    // Force tape (nullable): per step, substep and agent the total force the forward
+    // integrated (listed pairs, static obstacles, walls), [T][S][E A] pairs -- written by
+    // the two-wave forward, read by the backward's recompute in place of evaluating the
+    // forces again (it still scans for the neighbour lists its reverse pass walks).
+    T *fsum;
+    // Obstacle-contact tape (nullable, with fsum, at most 32 obstacles): per step, substep
     // and agent a mask of the obstacles whose narrow phase took its contact branch, bit o
     // for obstacle o, [T][S][E A] words of omask_bytes(N) bytes, written by the two-wave
-    // forward's obstacle wave for the obstacles it evaluates (all but the last few, which
-    // its agent wave takes) -- the backward reverses only those and the last few (the
-    // others' reverses add zeros at most).
+    // forward -- the backward reverses only those obstacles (the others' reverses add
+    // zeros at most).
     void *omask;
 };
 
@@ -514,13 +514,15 @@ __device__ __forceinline__ const T *ob_pose_table(const Cst<T> &C, const Args<T>
 // `act` (nullable) receives the mask of listed neighbours whose box contact exerts a
 // force; for a box agent `om` / `wall` / `beyond` which of its first 64 obstacles, its
 // walls, and any later obstacle do: the contacts without force have zero derivatives.
+// `fsum` (nullable, worlds without box agents): the substep's total force as a forward
+// recorded it -- then only the neighbour lists are built.
 template <typename T, int PA, bool BOXES>
 __device__ __forceinline__ typename MaskT<PA>::type forces(
     const Cst<T> &C, const Args<T> &g, const Lane<T, PA> &L, const T *sl, const T *lr,
     const St<T> &st, int s, bool full, typename MaskT<PA>::type &cand, T &Fx, T &Fy,
     const T *ocs = nullptr, const T *lbx = nullptr, const T *lcs = nullptr,
     typename MaskT<PA>::type *act = nullptr, uint64_t *om = nullptr, bool *wall = nullptr,
-    bool *beyond = nullptr, T *tq = nullptr, const T *osum = nullptr)
+    bool *beyond = nullptr, T *tq = nullptr, const T *fsum = nullptr)
 {
     const bool box_me = BOXES && L.pr.shape > T(0.5);
     T me[6] = {st.px, st.py, st.th, st.vx, st.vy, st.w};
@@ -544,6 +546,14 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
         } else {
             incl = scan_cand<T, PA>(lx, ly, L.base, st.px, st.py, C.t_nbr, cand);
         }
+    }
+    if (!BOXES && fsum) {
+        // the total force as the forward recorded it (the same bits): only the lists
+        Fx = fsum[0];
+        Fy = fsum[1];
+        return incl;
+    }
+    if (C.collisions) {
         M m = cap_list(incl, C.K);
         const T ra = L.pr.radius;
         const Foot<T> fa = {L.pr.shape, ra, L.pr.hx, L.pr.hy};
@@ -579,10 +589,6 @@ __device__ __forceinline__ typename MaskT<PA>::type forces(
                                 om, wall, beyond);
         if (wheel)
             tau = tau + box_static_torque(C, g.obs, eN, ocs, L.pr.hx, L.pr.hy, me, cme, sme, L.dd);
-    } else if (osum) {
-        // the obstacles' sum as the forward recorded it (the same bits)
-        sx = osum[0];
-        sy = osum[1];
     } else if (C.N > 0) {
         const size_t eN = (size_t)(L.env < C.E ? L.env : 0) * C.N;
         for (int o = 0; o < C.N; ++o) {

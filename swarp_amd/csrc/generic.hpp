@@ -240,17 +240,18 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
                         sx += tfx[k];
                         sy += tfy[k];
                     }
-                if (g.osum && L.active) {
-                    T *const o2 = g.osum + 2 * (((size_t)t * C.S + s) * EA + L.idx);
-                    o2[0] = sx;
-                    o2[1] = sy;
-                }
                 if (C.soft_walls) {
                     sx += wx;
                     sy += wy;
                 }
+                const T Fx = fx + sx, Fy = fy + sy;
+                if (g.fsum && L.active) {
+                    T *const o2 = g.fsum + 2 * (((size_t)t * C.S + s) * EA + L.idx);
+                    o2[0] = Fx;
+                    o2[1] = Fy;
+                }
                 St<T> nx;
-                integrate<T, false>(C, L.pr, st, a, fx + sx, fy + sy, nx);
+                integrate<T, false>(C, L.pr, st, a, Fx, Fy, nx);
                 if (C.use_skin) {
                     D += (m_abs(nx.px - st.px) + m_abs(nx.py - st.py)) * T(1.0001);
                     ok = env_all<PA>(!L.real || D <= C.half_margin, L.base);
@@ -463,14 +464,14 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> Cin, const Args
                 M am = 0;
                 uint64_t om = 0;
                 bool wl = false, far = false;
-                const T *osum =
-                    !BOXES && g.osum ? g.osum + 2 * (((size_t)t * C.S + s) * EA + L.idx) : nullptr;
+                const T *fsum =
+                    !BOXES && g.fsum ? g.fsum + 2 * (((size_t)t * C.S + s) * EA + L.idx) : nullptr;
                 if (!BOXES && g.omask)
                     lomk[s * 64 + L.lane] =
                         L.active ? omask_get(g.omask, C.N, ((size_t)t * C.S + s) * EA + L.idx) : 0u;
                 incl = forces<T, PA, BOXES>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy,
                                             ocs, lbx, lcsb + s * 128, &am, &om, &wl, &far, nullptr,
-                                            osum);
+                                            fsum);
                 if (BOXES) {
                     lact[s * 64 + L.lane] = am;
                     lom[s * 64 + L.lane] = om;

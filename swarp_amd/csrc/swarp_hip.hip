@@ -271,11 +271,11 @@ static bool lean_ok(const swarp_desc_t *d)
 
 // Byte offsets of the tape regions (see lean.hpp); total == 0: no tape.  The specialised
 // holonomic kernels keep records (rec) and last velocities (vl); the two-wave forward of
-// 2-D fleets among static obstacles keeps each substep's obstacle force sums (osum, read
-// by the backward's recompute) and, for at most 32 obstacles, each substep's obstacle
-// contact masks (omask, read by its reverse pass).
+// 2-D fleets among static obstacles keeps each substep's total forces (fsum, read by the
+// backward's recompute) and, for at most 32 obstacles, each substep's obstacle contact
+// masks (omask, read by its reverse pass).
 struct TapeLayout {
-    uint64_t rec, vl, osum, omask, total;
+    uint64_t rec, vl, fsum, omask, total;
 };
 
 static uint64_t align256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
@@ -307,7 +307,7 @@ static TapeLayout tape_layout(const swarp_desc_t *d, int32_t nT)
     TapeLayout L = {0, 0, 0, 0, 0};
     if (nT >= 1 && split_ok(d)) {
         const uint64_t n = (uint64_t)nT * d->substeps * d->n_envs * d->n_agents;
-        L.osum = 0;
+        L.fsum = 0;
         L.omask = align256(n * 2 * sizeof(float));
         L.total = align256(L.omask + n * omask_bytes(d->n_obstacles));
         return L;
@@ -357,7 +357,7 @@ static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     a.act = (const T *)act;
     a.nsteps = nT;
     if (tape && TL.total && split_ok(d)) {
-        a.osum = (T *)((unsigned char *)tape + TL.osum);
+        a.fsum = (T *)((unsigned char *)tape + TL.fsum);
         if (omask_bytes(d->n_obstacles)) a.omask = (unsigned char *)tape + TL.omask;
     }
     const int PA = pad_agents(d->n_agents);
@@ -408,7 +408,7 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     a.aact = (T *)aact;
     a.nsteps = nT;
     if (tape && TL.total && split_ok(d)) {
-        a.osum = (T *)((unsigned char *)tape + TL.osum);
+        a.fsum = (T *)((unsigned char *)tape + TL.fsum);
         if (omask_bytes(d->n_obstacles)) a.omask = (unsigned char *)tape + TL.omask;
     }
     const int PA = pad_agents(d->n_agents);
