@@ -184,8 +184,8 @@ int swarp_rollout_bwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *
  * fleets among static obstacles whose forward runs the obstacle pass on a wave of its own
  * (at most 256 / (envs per 64 lanes) obstacles, no box agents, wheel contacts or drones):
  * there the tape holds each substep's per-agent total force (listed pairs, obstacles,
- * walls), 8 T S E A bytes (rounded up to 256), which the backward reads instead of
- * evaluating the forces (it still builds the neighbour lists), and
+ * walls), 8 T S E A bytes, and neighbour-inclusion mask, 4 T S E A bytes (8 at more than
+ * 32 agents), which the backward reads instead of evaluating the forces and scanning, and
  * for at most 32 obstacles each substep's per-agent mask of the obstacles in contact,
  * w T S E A bytes more (w = 1, 2 or 4 for up to 8, 16 or 32 obstacles; each part rounded
  * up to 256), so that the backward reverses only those.  The taped backward gives the

@@ -91,6 +91,10 @@ template <typename T> struct Args {
     // forward -- the backward reverses only those obstacles (the others' reverses add
     // zeros at most).
     void *omask;
+    // Neighbour tape (nullable, with fsum): per step, substep and agent the uncapped
+    // inclusion mask of its neighbour lists (MaskT<PA> words, [T][S][E A]), written by the
+    // two-wave forward -- the backward's recompute reads it instead of scanning.
+    void *nmask;
 };
 
 // Width of one obstacle-contact mask word for N obstacles (0: no mask above 32).

@@ -210,6 +210,8 @@ __global__ __launch_bounds__(128, 4) void k_rollout_fwd_split(const Cst<T> Cin, 
                     } else {
                         incl = scan_cand<T, PA>(lx, ly, L.base, st.px, st.py, C.t_nbr, cand);
                     }
+                    if (g.nmask && L.active)
+                        ((M *)g.nmask)[((size_t)t * C.S + s) * EA + L.idx] = incl;
                     M m = cap_list(incl, C.K);
                     const T ra = L.pr.radius;
                     while (m) {
@@ -469,9 +471,18 @@ __global__ __launch_bounds__(64) void k_rollout_bwd(const Cst<T> Cin, const Args
                 if (!BOXES && g.omask)
                     lomk[s * 64 + L.lane] =
                         L.active ? omask_get(g.omask, C.N, ((size_t)t * C.S + s) * EA + L.idx) : 0u;
-                incl = forces<T, PA, BOXES>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy,
-                                            ocs, lbx, lcsb + s * 128, &am, &om, &wl, &far, nullptr,
-                                            fsum);
+                if (!BOXES && fsum && g.nmask) {
+                    // the forward's force and lists (the same bits): no force pass at all
+                    Fx = fsum[0];
+                    Fy = fsum[1];
+                    incl = L.active && C.collisions
+                               ? ((const M *)g.nmask)[((size_t)t * C.S + s) * EA + L.idx]
+                               : M(0);
+                } else {
+                    incl = forces<T, PA, BOXES>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx,
+                                                Fy, ocs, lbx, lcsb + s * 128, &am, &om, &wl, &far,
+                                                nullptr, fsum);
+                }
                 if (BOXES) {
                     lact[s * 64 + L.lane] = am;
                     lom[s * 64 + L.lane] = om;

@@ -272,10 +272,11 @@ static bool lean_ok(const swarp_desc_t *d)
 // Byte offsets of the tape regions (see lean.hpp); total == 0: no tape.  The specialised
 // holonomic kernels keep records (rec) and last velocities (vl); the two-wave forward of
 // 2-D fleets among static obstacles keeps each substep's total forces (fsum, read by the
-// backward's recompute) and, for at most 32 obstacles, each substep's obstacle contact
-// masks (omask, read by its reverse pass).
+// backward's recompute), each substep's neighbour-inclusion masks (nmask, read by the
+// recompute in place of its scan) and, for at most 32 obstacles, each substep's obstacle
+// contact masks (omask, read by its reverse pass).
 struct TapeLayout {
-    uint64_t rec, vl, fsum, omask, total;
+    uint64_t rec, vl, fsum, omask, nmask, total;
 };
 
 static uint64_t align256(uint64_t x) { return (x + 255) & ~(uint64_t)255; }
@@ -304,12 +305,13 @@ static bool split_ok(const swarp_desc_t *d)
 
 static TapeLayout tape_layout(const swarp_desc_t *d, int32_t nT)
 {
-    TapeLayout L = {0, 0, 0, 0, 0};
+    TapeLayout L = {0, 0, 0, 0, 0, 0};
     if (nT >= 1 && split_ok(d)) {
         const uint64_t n = (uint64_t)nT * d->substeps * d->n_envs * d->n_agents;
         L.fsum = 0;
         L.omask = align256(n * 2 * sizeof(float));
-        L.total = align256(L.omask + n * omask_bytes(d->n_obstacles));
+        L.nmask = align256(L.omask + n * omask_bytes(d->n_obstacles));
+        L.total = align256(L.nmask + n * (pad_agents(d->n_agents) == 64 ? 8 : 4));
         return L;
     }
     const bool forces = d->collisions || d->soft_walls;
@@ -359,6 +361,7 @@ static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     if (tape && TL.total && split_ok(d)) {
         a.fsum = (T *)((unsigned char *)tape + TL.fsum);
         if (omask_bytes(d->n_obstacles)) a.omask = (unsigned char *)tape + TL.omask;
+        a.nmask = (unsigned char *)tape + TL.nmask;
     }
     const int PA = pad_agents(d->n_agents);
     const unsigned feat = world_features(d, false);
@@ -410,6 +413,7 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     if (tape && TL.total && split_ok(d)) {
         a.fsum = (T *)((unsigned char *)tape + TL.fsum);
         if (omask_bytes(d->n_obstacles)) a.omask = (unsigned char *)tape + TL.omask;
+        a.nmask = (unsigned char *)tape + TL.nmask;
     }
     const int PA = pad_agents(d->n_agents);
     if (wide_path(d)) {

@@ -133,16 +133,40 @@ def _obstacle_world(E, A, n, seed):
     (9, 40, 4, 2, 40),      # more than 32 obstacles: sums only, no contact masks
 ])
 def test_obstacle_sum_tape_matches_recompute(E, A, T, S, n):
-    """Static obstacles: the forward keeps each substep's obstacle force sums and contact
-    masks, and the backward reads them instead of evaluating the obstacles again and
-    reverses only the obstacles in contact -- the same values."""
+    """Static obstacles: the forward keeps each substep's total force, neighbour lists and
+    obstacle contacts, and the backward reads them instead of evaluating the forces and
+    scanning again, and reverses only the obstacles in contact -- the same values."""
     cfgs, world, obs, s0, rng = _obstacle_world(E, A, n, seed=E + n)
     on = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
     off = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
     off.use_tape = False
     al = lambda x: x + (-x % 256)  # noqa: E731
+    n_ = T * S * E * A
     mw = 1 if n <= 8 else (2 if n <= 16 else (4 if n <= 32 else 0))  # contact-mask word
-    assert on.tape_bytes(E, 2, T) == al(al(2 * 4 * T * S * E * A) + mw * T * S * E * A)
+    nw = 8 if A > 32 else 4  # neighbour-mask word (64-lane envs: 64-bit masks)
+    assert on.tape_bytes(E, 2, T) == al(al(al(2 * 4 * n_) + mw * n_) + nw * n_)
+    acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
+    w = rng.normal(size=(T, E, A, 16)) * 0.1
+    w[..., 7:] = 0.0
+    a = hip_run(on, s0, acts, w, np.float32)
+    b = hip_run(off, s0, acts, w, np.float32)
+    assert np.array_equal(a[0][..., :7], b[0][..., :7]), "forward states differ"
+    assert np.array_equal(a[2], b[2]), "d/d actions differ"
+    assert np.array_equal(a[1][..., :7], b[1][..., :7]), "d/d state0 differ"
+
+
+def test_obstacle_tape_without_agent_collisions():
+    """Obstacles and walls but no agent-agent contacts: the forward keeps no neighbour
+    lists, and the taped backward must build none either -- the untaped values."""
+    E, A, T, S, n = 37, 16, 5, 3, 8
+    cfgs, _, obs, s0, rng = _obstacle_world(E, A, n, seed=5)
+    world = WorldConfig(collisions=False, collision_k=100.0, collision_c=1.0,
+                        collision_margin=0.025, bounds=(-1.0, 1.0, -1.0, 1.0),
+                        bounds_mode="soft")
+    on = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
+    off = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
+    off.use_tape = False
+    assert on.tape_bytes(E, 2, T) > 0
     acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
     w = rng.normal(size=(T, E, A, 16)) * 0.1
     w[..., 7:] = 0.0
