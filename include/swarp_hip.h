@@ -179,7 +179,7 @@ int swarp_rollout_bwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *
  * (StepBuffers / make_buffers, swarp/core/stepper.py:55-63, 642-678).
  * Writes in *bytes the tape size of a T-step rollout of this configuration; 0 when the
  * configuration keeps no tape, in which case the _tape entry points behave as the plain
- * ones.  Two kinds of configuration keep one: fleets on the specialised holonomic-velocity
+ * ones.  Three kinds of configuration keep one: fleets on the specialised holonomic-velocity
  * kernels with substeps <= 4 and contacts or walls (the records above), and float32 2-D
  * fleets among static obstacles whose forward runs the obstacle pass on a wave of its own
  * (at most 256 / (envs per 64 lanes) obstacles, no box agents, wheel contacts or drones):
@@ -188,7 +188,10 @@ int swarp_rollout_bwd(const swarp_desc_t *desc, int32_t T, const swarp_state_t *
  * 32 agents), which the backward reads instead of evaluating the forces and scanning, and
  * for at most 32 obstacles each substep's per-agent mask of the obstacles in contact,
  * w T S E A bytes more (w = 1, 2 or 4 for up to 8, 16 or 32 obstacles; each part rounded
- * up to 256), so that the backward reverses only those.  The taped backward gives the
+ * up to 256), so that the backward reverses only those; and the other fleets without box
+ * agents or wheel contacts that have contacts, walls or obstacles (drones among them):
+ * each substep's total force and neighbour mask as above, no contact masks.  The taped
+ * backward gives the
  * untaped one's values; a gradient that is zero may differ in the sign of that zero. */
 int swarp_tape_bytes(const swarp_desc_t *desc, int32_t T, uint64_t *bytes);
 

@@ -82,8 +82,8 @@ template <typename T> struct Args {
     int nsteps;
     // Force tape (nullable): per step, substep and agent the total force the forward
     // integrated (listed pairs, static obstacles, walls), [T][S][E A] pairs -- written by
-    // the two-wave forward, read by the backward's recompute in place of evaluating the
-    // forces again (it still scans for the neighbour lists its reverse pass walks).
+    // the generic forward kernels (worlds without box agents or wheel contacts), read by
+    // the backward's recompute in place of evaluating the forces again.
     T *fsum;
     // Obstacle-contact tape (nullable, with fsum, at most 32 obstacles): per step, substep
     // and agent a mask of the obstacles whose narrow phase took its contact branch, bit o
@@ -92,8 +92,9 @@ template <typename T> struct Args {
     // zeros at most).
     void *omask;
     // Neighbour tape (nullable, with fsum): per step, substep and agent the uncapped
-    // inclusion mask of its neighbour lists (MaskT<PA> words, [T][S][E A]), written by the
-    // two-wave forward -- the backward's recompute reads it instead of scanning.
+    // inclusion mask of its neighbour lists (MaskT<PA> words, [T][S][E A]; worlds with
+    // agent contacts), written with fsum -- the backward's recompute reads it instead of
+    // scanning.
     void *nmask;
 };
 

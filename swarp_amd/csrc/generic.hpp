@@ -71,9 +71,16 @@ __global__ __launch_bounds__(64) void k_rollout_fwd(const Cst<T> Cin, const Args
                     lcs[64 + L.lane] = m_sin(st.th);
                 }
                 if (C.collisions || BOXES) wave_lds_sync();
-                forces<T, PA, BOXES>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy, ocs, lbx,
-                                     lcs, nullptr, nullptr, nullptr, nullptr,
-                                     BOXES && C.wheel ? &Tq : nullptr);
+                const M incl =
+                    forces<T, PA, BOXES>(C, g, L, sl, lr, st, s, s == 0 || !ok, cand, Fx, Fy, ocs,
+                                         lbx, lcs, nullptr, nullptr, nullptr, nullptr,
+                                         BOXES && C.wheel ? &Tq : nullptr);
+                if (!BOXES && g.fsum && L.active) {
+                    const size_t k = ((size_t)t * C.S + s) * EA + L.idx;
+                    g.fsum[2 * k] = Fx;
+                    g.fsum[2 * k + 1] = Fy;
+                    if (C.collisions) ((M *)g.nmask)[k] = incl;
+                }
             }
             St<T> nx;
             if (BOXES && C.wheel) {

@@ -303,6 +303,14 @@ static bool split_ok(const swarp_desc_t *d)
     return (64 / pad_agents(d->n_agents)) * d->n_obstacles <= OCS_MAX;
 }
 
+// Whether the one-wave generic forward keeps a tape: each substep's total force (fsum) and
+// neighbour-inclusion masks (nmask), which its backward reads instead of a force pass.
+static bool gen_tape_ok(const swarp_desc_t *d)
+{
+    return !wide_path(d) && !lean_ok(d) && !split_ok(d) && !d->has_boxes && !d->wheel_contacts &&
+           (d->collisions || d->soft_walls || d->n_obstacles > 0);
+}
+
 static TapeLayout tape_layout(const swarp_desc_t *d, int32_t nT)
 {
     TapeLayout L = {0, 0, 0, 0, 0, 0};
@@ -311,6 +319,13 @@ static TapeLayout tape_layout(const swarp_desc_t *d, int32_t nT)
         L.fsum = 0;
         L.omask = align256(n * 2 * sizeof(float));
         L.nmask = align256(L.omask + n * omask_bytes(d->n_obstacles));
+        L.total = align256(L.nmask + n * (pad_agents(d->n_agents) == 64 ? 8 : 4));
+        return L;
+    }
+    if (nT >= 1 && gen_tape_ok(d)) {
+        const uint64_t n = (uint64_t)nT * d->substeps * d->n_envs * d->n_agents;
+        L.fsum = 0;
+        L.omask = L.nmask = align256(n * 2 * (d->dtype == SWARP_F32 ? 4 : 8));
         L.total = align256(L.nmask + n * (pad_agents(d->n_agents) == 64 ? 8 : 4));
         return L;
     }
@@ -358,9 +373,9 @@ static int rollout_fwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     if (nT > 1) copy_fields<T>(traj, a.traj.f);
     a.act = (const T *)act;
     a.nsteps = nT;
-    if (tape && TL.total && split_ok(d)) {
+    if (tape && TL.total && (split_ok(d) || gen_tape_ok(d))) {
         a.fsum = (T *)((unsigned char *)tape + TL.fsum);
-        if (omask_bytes(d->n_obstacles)) a.omask = (unsigned char *)tape + TL.omask;
+        if (split_ok(d) && omask_bytes(d->n_obstacles)) a.omask = (unsigned char *)tape + TL.omask;
         a.nmask = (unsigned char *)tape + TL.nmask;
     }
     const int PA = pad_agents(d->n_agents);
@@ -410,9 +425,9 @@ static int rollout_bwd(const swarp_desc_t *d, int32_t nT, const swarp_state_t *s
     a.act = (const T *)act;
     a.aact = (T *)aact;
     a.nsteps = nT;
-    if (tape && TL.total && split_ok(d)) {
+    if (tape && TL.total && (split_ok(d) || gen_tape_ok(d))) {
         a.fsum = (T *)((unsigned char *)tape + TL.fsum);
-        if (omask_bytes(d->n_obstacles)) a.omask = (unsigned char *)tape + TL.omask;
+        if (split_ok(d) && omask_bytes(d->n_obstacles)) a.omask = (unsigned char *)tape + TL.omask;
         a.nmask = (unsigned char *)tape + TL.nmask;
     }
     const int PA = pad_agents(d->n_agents);

@@ -178,14 +178,23 @@ def test_obstacle_tape_without_agent_collisions():
 
 
 def test_no_obstacle_tape_beyond_the_pose_table():
-    """Seventeen obstacles at four agents per env overflow the forward's per-launch
-    obstacle table (16 envs x 17 > 256 entries): no tape, and the rollout still runs."""
+    """Seventeen obstacles at four agents per env overflow the two-wave forward's
+    per-launch obstacle table (16 envs x 17 > 256 entries): the one-wave forward runs and
+    keeps the generic tape (forces and lists, no contact masks) -- the untaped values."""
     E, A, T, S, n = 20, 4, 3, 2, 17
     cfgs, world, obs, s0, rng = _obstacle_world(E, A, n, seed=1)
     st = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
-    assert st.tape_bytes(E, 2, T) == 0
+    off = make_stepper(cfgs, world, 0.05, S, torch.float32, obs=obs, n_envs=E)
+    off.use_tape = False
+    al = lambda x: x + (-x % 256)  # noqa: E731
+    n_ = T * S * E * A
+    assert st.tape_bytes(E, 2, T) == al(al(2 * 4 * n_) + 4 * n_)
     acts = rng.uniform(-1, 1, size=(T, E, A, 2)).astype(np.float32)
     w = rng.normal(size=(T, E, A, 16)) * 0.1
     w[..., 7:] = 0.0
-    states, g0, ga = hip_run(st, s0, acts, w, np.float32)
-    assert np.isfinite(ga).all() and np.isfinite(g0).all()
+    a = hip_run(st, s0, acts, w, np.float32)
+    b = hip_run(off, s0, acts, w, np.float32)
+    assert np.isfinite(a[2]).all() and np.isfinite(a[1]).all()
+    assert np.array_equal(a[0][..., :7], b[0][..., :7]), "forward states differ"
+    assert np.array_equal(a[2], b[2]), "d/d actions differ"
+    assert np.array_equal(a[1][..., :7], b[1][..., :7]), "d/d state0 differ"

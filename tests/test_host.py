@@ -137,7 +137,10 @@ def test_tape_size_without_gpu():
     assert st.tape_bytes(E, 2, T) == 0
     dd = Stepper(nav_agents(4, model=DynamicsModel.DIFF_DRIVE), dt=0.05, device="cpu",
                  world=nav_world(4))
-    assert dd.tape_bytes(E, 2, T) == 0
+    # the generic kernels' tape: per substep and agent the force pair and the 4-byte
+    # neighbour mask, each part rounded up to 256 bytes
+    n_ = T * dd.substeps * E * 4
+    assert dd.tape_bytes(E, 2, T) == al(al(8 * n_) + 4 * n_)
     free = Stepper(nav_agents(4), dt=0.05, device="cpu", world=WorldConfig(collisions=False))
     assert free.tape_bytes(E, 2, T) == 0
     lib = _lib.load()
